@@ -1,0 +1,22 @@
+"""isaac_net_amd: a MI355X-native backend for isaac-net's per-control-step NR uplink engine.
+
+make_engine("L2", E, R, "cuda", NRConfig(...), backend="hip") returns an engine with the reference contract API
+(reset / submit / step -> dict / clock / output_schema / counters / state_dict, isaac_net/core/engine.py:319-960)
+whose step runs the hand-written HIP kernels of csrc/ through the C ABI of include/inet_nr.h.
+"""
+from .config import NRConfig  # noqa: F401
+from .phy import PhyTables  # noqa: F401
+
+__version__ = "0.1.0"
+
+
+def make_engine(*args, **kwargs):
+    from .engine import make_engine as _mk
+    return _mk(*args, **kwargs)
+
+
+def __getattr__(name):
+    if name in ("HipNREngine", "Requests", "refusals", "HipUnsupported"):
+        from . import engine
+        return getattr(engine, name)
+    raise AttributeError(name)

@@ -1,0 +1,69 @@
+"""TR 38.901 (V17.0.0) large-scale parameters the engine's radio prologue needs (host side, Python floats).
+
+Restates the scenario table and formulas of isaac_net/core/channels/tr38901.py:54-255 for the deterministic-LOS
+case (tr38901_los "los" / "nlos") and the log-distance model of core/radio.py:265-273. The per-robot evaluation runs in
+the HIP step kernel; this module supplies the scenario constants and the plane-wave shadowing fields' parameters.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+C_LIGHT = 3.0e8
+
+
+@dataclass(frozen=True)
+class Scenario:
+    name: str
+    h_bs: float
+    los_corr_m: float
+    sf_corr_los_m: float
+    sf_corr_nlos_m: float
+
+
+SCENARIOS = {
+    "RMa": Scenario("RMa", 35.0, 60.0, 37.0, 120.0),
+    "UMa": Scenario("UMa", 25.0, 50.0, 37.0, 50.0),
+    "UMi": Scenario("UMi", 10.0, 50.0, 10.0, 13.0),
+    "InH": Scenario("InH", 3.0, 10.0, 10.0, 6.0),
+    "InF-SL": Scenario("InF-SL", 1.5, 5.0, 10.0, 10.0),
+    "InF-DL": Scenario("InF-DL", 1.5, 1.0, 10.0, 10.0),
+    "InF-SH": Scenario("InF-SH", 8.0, 5.0, 10.0, 10.0),
+    "InF-DH": Scenario("InF-DH", 8.0, 1.0, 10.0, 10.0),
+}
+ALIASES = {"rma": "RMa", "uma": "UMa", "umi": "UMi", "inh": "InH", "inh_office": "InH", "inf_sl": "InF-SL",
+           "inf_dl": "InF-DL", "inf_sh": "InF-SH", "inf_dh": "InF-DH"}
+UT_HEIGHT_RANGE = {"UMa": (1.5, 22.5), "UMi": (1.5, 22.5), "RMa": (1.0, 10.0)}
+# (sigma_SF LOS, sigma_SF NLOS) dB, Table 7.4.1-1 (RMa LOS depends on the breakpoint, handled by the caller)
+SIGMA_SF = {"UMa": (4.0, 6.0), "UMi": (4.0, 7.82), "InH": (3.0, 8.03), "InF-SL": (4.3, 5.7),
+            "InF-DL": (4.3, 7.2), "InF-SH": (4.3, 5.9), "InF-DH": (4.3, 4.0)}
+
+
+def scenario_name(s):
+    if s in SCENARIOS:
+        return s
+    key = s.lower().replace("-", "_")
+    if key in ALIASES:
+        return ALIASES[key]
+    raise ValueError(f"unknown TR 38.901 scenario {s!r}; one of {tuple(SCENARIOS)}")
+
+
+def check_heights(scn, h_bs, h_ut):
+    """Table 7.4.1-1 applicability of UMa / UMi / RMa heights (reference tr38901.py:120-141)."""
+    if scn in UT_HEIGHT_RANGE:
+        lo, hi = UT_HEIGHT_RANGE[scn]
+        if not lo - 1e-9 <= h_ut <= hi + 1e-9:
+            raise ValueError(f"TR 38.901 {scn} path loss is defined for {lo:g} m <= ue_height_m <= {hi:g} m")
+        if h_bs <= (1.0 if scn in ("UMa", "UMi") else 0.0):
+            raise ValueError(f"TR 38.901 {scn}: BS height too low for a positive breakpoint distance")
+
+
+def breakpoint_m(scn, fc_ghz, h_bs, h_ut):
+    """d'_BP with h_E = 1 m for UMa / UMi (Note 1), d_BP for RMa (Note 5), inf indoors."""
+    check_heights(scn, h_bs, h_ut)
+    fc = fc_ghz * 1e9
+    if scn == "RMa":
+        return 2 * math.pi * h_bs * h_ut * fc / C_LIGHT
+    if scn in ("UMa", "UMi"):
+        return 4 * (h_bs - 1.0) * (h_ut - 1.0) * fc / C_LIGHT
+    return math.inf

@@ -1,0 +1,322 @@
+"""NRConfig: the fields of isaac-net's NR configuration that the per-control-step uplink engine reads.
+
+Same field names, meanings and defaults as the reference dataclass (isaac_net/core/config.py:477-786), restricted
+to what the single-cell uplink step path uses, plus the derived numerology it needs (config.py:955-1127). Fields that
+exist only for features outside this engine (downlink, multi-cell, QoS, BSR pipeline, MIMO, ...) are kept with their
+reference defaults so that a config built for the reference can be passed unchanged; the HIP backend refuses every
+such feature that is switched on (engine.refusals), as the reference's triton backend refuses what it lacks
+(core/nr_fast.py:538-563).
+
+Sources of the tables: TS 38.101-1 Table 5.3.2-1 (N_RB), TS 38.214 Table 5.1.2.2.1-1 (RBG size).
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from dataclasses import dataclass
+
+# TS 38.101-1 Table 5.3.2-1, FR1 maximum transmission bandwidth: {SCS kHz: {bandwidth MHz: N_RB}}
+NRB_FR1 = {
+    15: {5: 25, 10: 52, 15: 79, 20: 106, 25: 133, 30: 160, 35: 188, 40: 216, 45: 242, 50: 270},
+    30: {5: 11, 10: 24, 15: 38, 20: 51, 25: 65, 30: 78, 35: 92, 40: 106, 45: 119, 50: 133,
+         60: 162, 70: 189, 80: 217, 90: 245, 100: 273},
+    60: {10: 11, 15: 18, 20: 24, 25: 31, 30: 38, 35: 44, 40: 51, 45: 58, 50: 65,
+         60: 79, 70: 93, 80: 107, 90: 121, 100: 135},
+}
+# TS 38.214 Table 5.1.2.2.1-1: (largest bandwidth-part size, P for configuration 1, P for configuration 2)
+RBG_ROWS = ((36, 2, 4), (72, 4, 8), (144, 8, 16), (275, 16, 16))
+
+
+def rbg_size_38214(n_prb, config=1):
+    """RBG size P (PRBs) of a bandwidth part of n_prb PRBs (reference config.py:36-41)."""
+    for hi, p1, p2 in RBG_ROWS:
+        if n_prb <= hi:
+            return p1 if config == 1 else p2
+    raise ValueError(f"no RBG size for {n_prb} PRBs")
+
+
+@dataclass
+class NRConfig:
+    # ---- numerology, carrier, frame structure (reference config.py:491-513)
+    mu: int = 1
+    bandwidth_mhz: int = 20
+    n_prb: int | None = None
+    rbg_size: int | None = None
+    rbg_config: int = 1
+    duplex: str = "tdd"
+    tdd_pattern: str = "DDDSU"
+    special_split: tuple = (10, 2, 2)
+    special_dl_data: bool = True
+    special_ul_data: bool = False
+    dl_ctrl_symbols: int = 1
+    ul_data_symbols: int = 12
+    ul_mini_slot_symbols: int | None = None
+    dmrs_re_per_prb: int = 12
+    overhead_re_per_prb: int = 0
+    # ---- MAC timing (config.py:515-524)
+    k1: int = 2
+    k2: int = 2
+    gnb_proc_slots: int = 1
+    sr_period_slots: int = 5
+    sr_grant_delay_slots: int | None = None
+    ul_harq_rtt_slots: int | None = None
+    cqi_period_slots: int = 10
+    proactive_grant: str = "off"
+    proc_offset_ms: float = 0.0
+    # ---- HARQ / RLC (config.py:526-535)
+    n_harq: int = 16
+    max_harq_tx: int = 4
+    harq_combining: str = "cc"
+    harq_fail: str = "rlc_am"
+    rlc_retx_slots: int = 50
+    discard: str = "purge"
+    # ---- PHY abstraction / link adaptation / scheduler (config.py:536-595)
+    mcs_table: int = 1
+    eff_sinr: str = "eesm"
+    bler_source: str = "pdsch"
+    tbs_mode: str = "38214"
+    bler_target: float = 0.1
+    ul_mcs_max: int | None = None
+    dl_mcs_max: int | None = None
+    olla: bool = True
+    olla_up_db: float = 0.05
+    scheduler: str = "pf"
+    pf_metric: str = "subband"
+    pf_window: float = 100.0
+    retx_priority: bool = True
+    n_layers_max: int = 1
+    pf_update: str = "slot"
+    pf_avg_idle: str = "decay"
+    ul_retx_sched: str = "ofdma"
+    ul_amc_alloc: str = "current"
+    ul_grant_model: str = "lumped"
+    # ---- link budget and fading (config.py:596-637)
+    snr_ref_prbs: int = 10
+    ul_power: str = "allocated"
+    phr_cap: bool = True
+    phr_min_db: float = 3.0
+    fading: bool = True
+    fading_rho_per_ms: float = 0.93 ** (1 / 2.5)
+    fading_doppler: str = "global"
+    carrier_ghz: float = 3.5
+    fading_rician: bool = False
+    rician_k_db: float | None = None
+    rician_k_from_los: bool = True
+    rician_k_ramp_slots: int = 4
+    fading_freq_corr: bool = False
+    dl_snr_offset_db: float = 10.0
+    noise_model: str = "fixed"
+    ni_fixed_dbm: float = -90.0
+    gnb_nf_db: float = 5.0
+    ue_nf_db: float = 9.0
+    ue_tx_dbm: float = 23.0
+    gnb_tx_dbm: float = 43.0
+    tb_overhead_bytes: int = 0
+    pkt_payload_bytes: int = 1400
+    pkt_overhead_bytes: int = 0
+    # ---- radio (config.py:638-676)
+    pl_const_db: float = 40.0
+    pathloss_exp: float = 3.5
+    shadow_sigma_db: float = 6.0
+    shadow_modes: int = 8
+    shadow_dcorr_m: float = 10.3
+    shadow_acf: str = "sos"
+    shadow_white_frac: float = 0.0
+    channel: str = "log_distance"
+    tr38901_scenario: str = "InF-SH"
+    tr38901_los: str = "stochastic"
+    gnb_height_m: float | None = None
+    ue_height_m: float = 1.5
+    o2i_indoor_frac: float = 0.0
+    blockage: bool = False
+    los_source: str = "stochastic"
+    los_soft: bool = False
+    gnb_antenna: str = "isotropic"
+    # ---- cells (config.py:682-700)
+    n_cells: int = 1
+    cell_layout: str = "custom"
+    cell_positions_m: tuple = ((0.0, 0.0),)
+    cell_isd_m: float = 100.0
+    cell_center_m: tuple = (75.0, 75.0)
+    cell_arena_m: float = 150.0
+    ul_pc: bool | None = None
+    ul_pc_p0_dbm: float = -88.0
+    ul_pc_alpha: float = 1.0
+    ul_tpc: bool = False
+    rlf: bool = False
+    rach: bool = False
+    drx: bool = False
+    # ---- application (config.py:755-786)
+    ul: bool = True
+    dl: bool = False
+    control_step_ms: float = 100.0
+    frame_buffer: int = 16
+    timeout_steps: int = 20
+    msg_sizes: tuple = (4000.0, 30000.0)
+    traffic: tuple | None = None
+    seed: int | None = None
+    rng: str = "engine"
+    qos_classes: int = 2
+    edge: object = None
+    background: object = None
+    energy: object = None
+
+    def __post_init__(self):
+        assert self.mu in (0, 1, 2), "mu must be 0, 1 or 2 (FR1)"
+        assert set(self.tdd_pattern) <= set("DSU") and self.tdd_pattern
+        assert self.harq_combining in ("cc", "ir_lena", "none") and self.harq_fail in ("rlc_am", "drop")
+        assert self.eff_sinr in ("eesm", "mean_db") and self.pf_metric in ("subband", "wideband")
+        assert self.scheduler in ("pf", "pf_wideband", "maxci", "rr", "qos")
+        assert self.discard in ("purge", "none", "pdcp_arrival") and self.tbs_mode in ("38214", "lena")
+        assert self.noise_model in ("fixed", "thermal") and self.ul_power in ("allocated", "whole_band")
+        assert self.proactive_grant in ("off", "every_ul_slot", "per_period")
+        assert self.mcs_table in (1, 2) and self.n_harq >= 1 and self.max_harq_tx >= 1
+        assert sum(self.special_split) == 14 and self.duplex in ("tdd", "fdd")
+        assert self.frame_buffer >= 1 and self.timeout_steps >= 1 and self.control_step_ms > 0
+        assert len(self.msg_sizes) >= 1 and 1 <= self.n_cells <= 7
+        self.msg_sizes = tuple(float(s) for s in self.msg_sizes)
+        self.cell_positions_m = tuple(tuple(float(v) for v in p) for p in self.cell_positions_m)
+        if self.channel.startswith("tr38901_"):           # shorthand, as config.py TR38901_SHORT
+            self.tr38901_scenario = self.channel[len("tr38901_"):].replace("_", "-")
+            self.channel = "tr38901"
+        if self.channel == "tr38901":
+            from .channels import scenario_name
+            self.tr38901_scenario = scenario_name(self.tr38901_scenario)
+
+    def with_(self, **changes):
+        return dataclasses.replace(self, **changes)
+
+    # ---------------- derived (reference config.py:955-1127) ----------------
+    @property
+    def scs_khz(self):
+        return 15 * 2 ** self.mu
+
+    @property
+    def slot_ms(self):
+        return 1.0 / 2 ** self.mu
+
+    @property
+    def nprb(self):
+        if self.n_prb is not None:
+            return self.n_prb
+        tab = NRB_FR1[self.scs_khz]
+        if self.bandwidth_mhz not in tab:
+            raise ValueError(f"{self.bandwidth_mhz} MHz not defined at {self.scs_khz} kHz")
+        return tab[self.bandwidth_mhz]
+
+    @property
+    def rbg(self):
+        return self.rbg_size if self.rbg_size is not None else rbg_size_38214(self.nprb, self.rbg_config)
+
+    @property
+    def n_subbands(self):
+        return math.ceil(self.nprb / self.rbg)
+
+    @property
+    def subband_prbs(self):
+        s = [self.rbg] * self.n_subbands
+        s[-1] = self.nprb - self.rbg * (self.n_subbands - 1)
+        return s
+
+    @property
+    def slots_per_step(self):
+        n = self.control_step_ms / self.slot_ms
+        assert abs(n - round(n)) < 1e-9, "control step must be a whole number of slots"
+        return int(round(n))
+
+    def slot_symbols(self, pos):
+        """(DL data symbols, UL data symbols) of the slot at pattern position pos (config.py:1034-1046)."""
+        if self.duplex == "fdd":
+            return 14 - self.dl_ctrl_symbols, self.ul_data_symbols
+        c = self.tdd_pattern[pos % len(self.tdd_pattern)]
+        if c == "D":
+            return 14 - self.dl_ctrl_symbols, 0
+        if c == "U":
+            return 0, self.ul_data_symbols
+        dl = self.special_split[0] - self.dl_ctrl_symbols if self.special_dl_data else 0
+        ul = self.special_split[2] if self.special_ul_data else 0
+        return max(dl, 0), ul
+
+    def ul_capable(self, pos):
+        if self.duplex == "fdd":
+            return True
+        c = self.tdd_pattern[pos % len(self.tdd_pattern)]
+        return c == "U" or (c == "S" and self.special_split[2] > 0)
+
+    def first_ul_in_window(self, g, period):
+        """SR / CQI opportunity: g is the first UL-capable slot of its window (config.py:1070-1074)."""
+        if not self.ul_capable(g):
+            return False
+        return not any(self.ul_capable(x) for x in range(period * (g // period), g))
+
+    def next_ul_capable(self, g):
+        P = len(self.tdd_pattern)
+        for d in range(P):
+            if self.ul_capable(g + d):
+                return g + d
+        raise ValueError("pattern has no UL-capable slot")
+
+    @property
+    def sr_delay(self):
+        return self.sr_grant_delay_slots if self.sr_grant_delay_slots is not None else self.gnb_proc_slots + self.k2
+
+    @property
+    def ul_rtt(self):
+        return self.ul_harq_rtt_slots if self.ul_harq_rtt_slots is not None else self.gnb_proc_slots + self.k2
+
+    @property
+    def ul_slots_per_step(self):
+        return sum(1 for g in range(self.slots_per_step) if self.slot_symbols(g)[1] > 0)
+
+    @property
+    def ul_pc_on(self):
+        return self.n_cells > 1 if self.ul_pc is None else bool(self.ul_pc)
+
+    @property
+    def rician_mode(self):
+        """None (Rayleigh), "fixed" (rician_k_db) or "los" (K from the LOS state), as config.py rician_mode."""
+        if not (self.fading and self.fading_rician):
+            return None
+        if self.rician_k_db is not None:
+            return "fixed"
+        return "los" if self.rician_k_from_los else None
+
+    def noise_dbm_per_prb(self, rx="gnb"):
+        if self.noise_model == "fixed":
+            return self.ni_fixed_dbm - 10 * math.log10(self.snr_ref_prbs)
+        nf = self.gnb_nf_db if rx == "gnb" else self.ue_nf_db
+        return -174.0 + 10 * math.log10(12 * self.scs_khz * 1e3) + nf
+
+    @property
+    def subband_noise_dbm(self):
+        return self.noise_dbm_per_prb("gnb") + 10 * math.log10(self.snr_ref_prbs)
+
+    def gnb_xy(self):
+        """gNB positions in env-local metres (config.py:1417-1433)."""
+        n = self.n_cells
+        if self.cell_layout == "custom":
+            return [tuple(map(float, p)) for p in self.cell_positions_m]
+        if self.cell_layout == "hex":
+            isd = self.cell_isd_m
+            pts = [(0.0, 0.0)] + [(isd * math.cos(math.pi / 3 * j), isd * math.sin(math.pi / 3 * j)) for j in range(6)]
+            pts = pts[:n]
+            cx, cy = sum(p[0] for p in pts) / n, sum(p[1] for p in pts) / n
+            return [(p[0] - cx + self.cell_center_m[0], p[1] - cy + self.cell_center_m[1]) for p in pts]
+        cols = math.ceil(math.sqrt(n))
+        rows = math.ceil(n / cols)
+        dx, dy = self.cell_arena_m / cols, self.cell_arena_m / rows
+        return [((i % cols + 0.5) * dx, (i // cols + 0.5) * dy) for i in range(n)]
+
+    def schedule(self, g0):
+        """Scheduled slots of the control step starting at slot g0 (reference nr_engine.py:506-523, uplink part):
+        [(rel, ul data symbols, SR opportunity)] for every slot with UL data or an SR opportunity."""
+        out = []
+        for rel in range(self.slots_per_step):
+            g = g0 + rel
+            uls = self.slot_symbols(g)[1] if self.ul else 0
+            sr = self.first_ul_in_window(g, self.sr_period_slots) and self.ul
+            dls = self.slot_symbols(g)[0] if self.dl else 0
+            cqi = self.first_ul_in_window(g, self.cqi_period_slots) and self.dl
+            if dls or uls or cqi or sr:
+                out.append((rel, uls, bool(sr)))
+        return out

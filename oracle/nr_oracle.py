@@ -1,0 +1,862 @@
+"""CPU oracle of the NR uplink per-control-step engine.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
+
+A from-scratch torch-CPU restatement of isaac-net's single-cell uplink NR engine, reference backend:
+  NREngine        core/engine.py:319-960   (clock, submit, step, partial reset)
+  NRNet           core/nr_engine.py:171-888 (reset, fading AR(1) + Rician, step_rx, step, _finish)
+  UlMac/MacLink   core/mac_ul.py:58-260, core/mac.py:65-616 (lumped SR/grants, PF/maxCI/RR scheduling, retx admission,
+                  RBG allocation, EESM / mean-dB link adaptation, HARQ cc/none/ir_lena, rlc_am/drop, OLLA, PF average,
+                  RLC in-order delivery, end_step, compact)
+  FrameQueue      core/queues.py:36-143
+  NRRng           core/nr_rng.py, core/proto/rng.py (counter hash, Box-Muller)
+  RadioMC         core/radio.py:59-277 (log_distance), core/channels/models.py:34-167 + tr38901.py (deterministic LOS
+                  state "los" / "nlos"), core/channels/fields.py:38-64 (plane-wave shadowing)
+The element-wise operations, the reduction calls and their order are those of the reference, so that on the same
+CPU the oracle is bitwise equal to the reference path (pinned by the golden trajectories under tests/golden/).
+The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
+
+Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state and outputs
+after every step of six scenarios) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF
+metric is not implemented here (refused), and `whole_band` UL power is not implemented (refused).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+BIG = 2 ** 62
+AVG_MIN = 1e-9
+M32 = 0xFFFFFFFF
+C1, C2 = 0x21F0AAAD, 0x735A2D97
+GOLD = 0x9E3779B9
+INV24 = 1.0 / 16777216.0
+SUBMIT, STEP, RESET = 1, 2, 3
+FADING, BLER_UL, BLER_DL, H0, KFAC, KPHI, DSPR = 1, 2, 3, 4, 5, 6, 7
+LOG_DISTANCE_STREAM = 10
+RADIO_STREAM = 0x52 << 16
+TR38901_STREAM = RADIO_STREAM + 16
+
+
+# ------------------------------------------------------------------------------------------ counter RNG
+def mix32(x):
+    """lowbias32 (proto/rng.py:42-48), Python int or int64 tensor in [0, 2^32)."""
+    x = x ^ (x >> 16)
+    x = (x * C1) & M32
+    x = x ^ (x >> 15)
+    x = (x * C2) & M32
+    return x ^ (x >> 15)
+
+
+def salt(v):
+    return (mix32(v & M32) + GOLD) & M32
+
+
+def seed_key(seed):
+    """proto/rng.py:60-62."""
+    return mix32(mix32(seed & M32) ^ salt((seed >> 32) & M32))
+
+
+def base_key(s0, env, ep, channel, ctr, stream):
+    """Key of (seed, env, episode, channel, counter, stream) (proto/rng.py:164-170)."""
+    h = mix32(s0 ^ salt(env & M32))
+    h = mix32(h ^ salt(ep & M32))
+    h = mix32(h ^ salt(channel))
+    h = mix32(h ^ salt(ctr & M32))
+    return mix32(h ^ salt(stream))
+
+
+def elem_hash(base, i):
+    """Element i under base: two lowbias32 rounds over base + i * GOLD (proto/rng.py:173-175)."""
+    w = (i * GOLD) & M32
+    return mix32(mix32((base + w) & M32) ^ base)
+
+
+def uniform_from(h):
+    return (h >> 8).to(torch.float32) * INV24
+
+
+def normal_from(h1, h2):
+    """Box-Muller, cosine branch (proto/rng.py:182-185)."""
+    u1 = ((h1 >> 8) + 1).to(torch.float32) * INV24
+    u2 = (h2 >> 8).to(torch.float32) * INV24
+    return torch.sqrt(-2.0 * torch.log(u1)) * torch.cos(2.0 * math.pi * u2)
+
+
+class CounterRNG:
+    """Per-env streams: episode [E] and call counters; draws are pure functions of the key (proto/rng.py:70-183)."""
+
+    def __init__(self, seed, E):
+        self.seed = int(seed)
+        self.E = E
+        self.s0 = seed_key(self.seed)
+        self.env = torch.arange(E, dtype=torch.long)
+        self.episode = torch.full((E,), -1, dtype=torch.long)
+        self.ctr = {SUBMIT: torch.zeros(E, dtype=torch.long), STEP: torch.zeros(E, dtype=torch.long)}
+
+    def reset_mask(self, mask=None):
+        """New episode for the envs of mask (None = all), counters to 0 (nr_rng.py:45-52, proto/rng.py:88-100)."""
+        if mask is None:
+            self.episode.add_(1)
+            for c in self.ctr.values():
+                c.zero_()
+            return
+        self.episode.add_(mask.long())
+        for c in self.ctr.values():
+            c.masked_fill_(mask, 0)
+
+    def _draw(self, ctr, channel, stream, n, normal):
+        base = base_key(self.s0, self.env, self.episode, channel, ctr, stream)[:, None]
+        if not normal:
+            return uniform_from(elem_hash(base, torch.arange(n, dtype=torch.long)))
+        idx = torch.arange(2 * n, dtype=torch.long).view(n, 2)
+        return normal_from(elem_hash(base, idx[:, 0]), elem_hash(base, idx[:, 1]))
+
+    def step_normal(self, site, slot, n):
+        return self._draw(self.ctr[STEP], STEP, (site << 16) | slot, n, True)
+
+    def step_uniform(self, site, slot, n):
+        return self._draw(self.ctr[STEP], STEP, (site << 16) | slot, n, False)
+
+    def reset_normal(self, stream, n):
+        return self._draw(torch.zeros(self.E, dtype=torch.long), RESET, stream, n, True)
+
+    def reset_uniform(self, stream, n):
+        return self._draw(torch.zeros(self.E, dtype=torch.long), RESET, stream, n, False)
+
+
+def onehot(idx, n):
+    return idx[..., None] == torch.arange(n)
+
+
+def where_env(mask_e, value, t):
+    m = mask_e.view(-1, *([1] * (t.dim() - 1)))
+    if torch.is_tensor(value):
+        return torch.where(m, value.expand_as(t), t)
+    return torch.where(m, torch.full_like(t, value), t)
+
+
+def sum_last(x):
+    return x.sum(-1)
+
+
+# ------------------------------------------------------------------------------------------ PHY on torch
+class Phy:
+    """Torch views of isaac_net_amd.phy.PhyTables with the lookups of core/phy.py:263-363."""
+
+    def __init__(self, tabs):
+        self.t = tabs
+        self.M = tabs.M
+        self.bler = torch.from_numpy(tabs.bler)
+        self.flat = self.bler.reshape(-1)
+        self.C, self.G = tabs.C, tabs.G
+        self.s0, self.ds, self.c0, self.dc = tabs.s0, tabs.ds, tabs.c0, tabs.dc
+        self.beta = torch.from_numpy(tabs.beta)
+        self.se = torch.from_numpy(tabs.se)
+        self.r = torch.from_numpy(tabs.r)
+        self.qm = torch.from_numpy(tabs.qm)
+        self.thr_ref = torch.from_numpy(tabs.thr_ref)
+        self.mcs_eq = torch.from_numpy(tabs.mcs_eq)
+        self.mcs_max = tabs.mcs_max
+        self.target = tabs.target
+
+    def tbs_all(self, n_prb, nsym, dmrs, oh):
+        """[..., M] int64 TBS of every MCS (phy.tbs_all / tbs_38214, float64 math)."""
+        from isaac_net_amd.phy import tbs_38214
+        n = n_prb.double().numpy()[..., None]
+        return torch.from_numpy(tbs_38214(self.t.qm.astype(np.float64), self.t.r.astype(np.float64), n,
+                                          float(nsym), dmrs, oh))
+
+    @staticmethod
+    def segment(tbs, r):
+        """phy.segment (38.212 5.2.2) in float64: (code-block size, number of code blocks)."""
+        t = tbs.double()
+        r = r.double()
+        bg2 = (t <= 292) | ((t <= 3824) & (r <= 0.67)) | (r <= 0.25)
+        kcb = torch.where(bg2, torch.full_like(t, 3840.0), torch.full_like(t, 8448.0))
+        b = t + torch.where(t > 3824, torch.full_like(t, 24.0), torch.full_like(t, 16.0))
+        c = torch.where(b <= kcb, torch.ones_like(b), torch.ceil(b / (kcb - 24)))
+        bp = torch.where(c > 1, b + 24 * c, b)
+        return bp / c, c
+
+    def cidx(self, cbs):
+        x = ((cbs - self.c0) / self.dc).clamp(0, self.C - 1)
+        i0 = x.floor().clamp(max=self.C - 2).long()
+        return i0, x - i0
+
+    def bler_lookup(self, mcs, sinr_db, cbs):
+        """Bilinear code-block BLER at (mcs, SINR dB, code-block size) (phy.py:271-285), base graph 0."""
+        i0, wi = self.cidx(cbs.float())
+        base0 = (mcs.long() * self.C + i0) * self.G
+        x = ((sinr_db.nan_to_num(-30.0) - self.s0) / self.ds).clamp(0, self.G - 1)
+        j0 = x.floor().clamp(max=self.G - 2).long()
+        wj = x - j0
+        f = self.flat
+        lo = f[base0 + j0] * (1 - wj) + f[base0 + j0 + 1] * wj
+        hi = f[base0 + self.G + j0] * (1 - wj) + f[base0 + self.G + j0 + 1] * wj
+        return lo * (1 - wi) + hi * wi
+
+    def mcs_at(self, sinr_db):
+        ok = (sinr_db[..., None] >= self.thr_ref) & (torch.arange(self.M) <= self.mcs_max)
+        return (ok.long() * torch.arange(1, self.M + 1)).max(-1).values.clamp(min=1) - 1
+
+    @staticmethod
+    def lw(mask, w):
+        lw = torch.log(w.float())
+        return torch.where(mask, lw.expand_as(mask), torch.full(mask.shape, -float("inf")))
+
+    @staticmethod
+    def db(lin):
+        return (10 * torch.log10(lin.clamp(min=1e-6))).nan_to_num(nan=-30.0, posinf=60.0, neginf=-30.0)
+
+    def eff_sinr_all(self, sinr_db, mask, mode, w):
+        """Effective SINR per MCS over the masked subbands (phy.py:311-321)."""
+        lw = self.lw(mask, w)
+        lnw = torch.logsumexp(lw, -1, keepdim=True)
+        if mode == "mean_db":
+            v = (sinr_db * torch.exp(lw - lnw)).nan_to_num(0).sum(-1, keepdim=True)
+            return v.expand(*v.shape[:-1], self.M)
+        lin = 10 ** (sinr_db.clamp(-30, 60) / 10)
+        x = -lin[..., None, :] / self.beta[:, None] + lw[..., None, :]
+        eff = -self.beta * (torch.logsumexp(x, -1) - lnw)
+        return self.db(eff)
+
+    def eesm_lse(self, sinr_db, mask, mcs, w):
+        lw = self.lw(mask, w)
+        beta = self.beta[mcs.long()][..., None]
+        lin = 10 ** (sinr_db.clamp(-30, 60) / 10)
+        return torch.logsumexp(-lin / beta + lw, -1), torch.logsumexp(lw, -1)
+
+    def eff_sinr(self, sinr_db, mask, mcs, mode, w):
+        if mode == "mean_db":
+            lw = self.lw(mask, w)
+            return (sinr_db * torch.exp(lw - torch.logsumexp(lw, -1, keepdim=True))).nan_to_num(0).sum(-1)
+        lse, lnw = self.eesm_lse(sinr_db, mask, mcs, w)
+        return self.db(-self.beta[mcs.long()] * (lse - lnw))
+
+    def select_mcs(self, est_db, mask, offset_db, n_prb, nsym, dmrs, oh, mode, w):
+        """Highest MCS meeting the BLER target at the offset effective SINR (phy.py:339-350)."""
+        eff = self.eff_sinr_all(est_db, mask, mode, w) + offset_db[..., None]
+        tbs = self.tbs_all(n_prb, nsym, dmrs, oh)
+        cbs, c = self.segment(tbs, self.r)
+        m_all = torch.arange(self.M).expand_as(tbs)
+        tbler = 1 - (1 - self.bler_lookup(m_all, eff, cbs.float())) ** c.float()
+        ok = (tbler <= self.target) & (tbs > 0) & (m_all <= self.mcs_max)
+        m = (ok.long() * torch.arange(1, self.M + 1)).max(-1).values.clamp(min=1) - 1
+        return m, tbs.gather(-1, m[..., None]).squeeze(-1)
+
+    def tb_error_prob(self, mcs, sinr_eff_db, tbs, mcs_eq=None):
+        cbs, c = self.segment(tbs, self.r[mcs.long()])
+        b = self.bler_lookup(mcs if mcs_eq is None else mcs_eq, sinr_eff_db, cbs.float())
+        return 1 - (1 - b) ** c.float()
+
+
+# ------------------------------------------------------------------------------------------ radio
+def plane_waves(rand, spectrum, dcorr):
+    """draw_plane_waves (channels/fields.py:38-58) from rand(i) -> U[0,1) [E,C,K]: k [C,E,K,2], phi [C,E,K]."""
+    ang = rand(0) * 2 * math.pi
+    if spectrum == "sos":
+        wl = 20 + 40 * rand(1)
+        if dcorr != 10.3:
+            wl = wl * (dcorr / 10.3)
+        k = torch.stack([torch.cos(ang), torch.sin(ang)], -1) * (2 * math.pi / wl)[..., None]
+    else:
+        u = rand(1).clamp(max=1 - 1e-6)
+        kmag = torch.sqrt((1 - u) ** -2 - 1) / dcorr
+        k = torch.stack([torch.cos(ang), torch.sin(ang)], -1) * kmag[..., None]
+    phi = rand(2) * 2 * math.pi
+    return k.permute(1, 0, 2, 3).contiguous(), phi.permute(1, 0, 2).contiguous()
+
+
+def eval_plane_waves(pos, k, phi, amp):
+    arg = torch.einsum("erx,cekx->cerk", pos, k) + phi[:, :, None, :]
+    return (amp * torch.cos(arg).sum(-1)).permute(1, 2, 0)
+
+
+class Radio:
+    """RadioMC at one cell for channel "log_distance" or "tr38901" with a deterministic LOS state."""
+
+    def __init__(self, cfg, E, rng):
+        from isaac_net_amd.channels import SCENARIOS, SIGMA_SF, breakpoint_m
+        self.cfg, self.E, self.rng = cfg, E, rng
+        self.gnb = torch.tensor(cfg.gnb_xy(), dtype=torch.float32)
+        K = cfg.shadow_modes
+        self.model = cfg.channel
+        assert cfg.n_cells == 1 and cfg.shadow_white_frac == 0 and not cfg.blockage
+        if self.model == "log_distance":
+            self.amp = cfg.shadow_sigma_db * math.sqrt(2 / K)
+        else:
+            assert cfg.tr38901_los in ("los", "nlos") and cfg.o2i_indoor_frac == 0
+            sc = SCENARIOS[cfg.tr38901_scenario]
+            self.scn = cfg.tr38901_scenario
+            self.h_bs = float(cfg.gnb_height_m) if cfg.gnb_height_m is not None else sc.h_bs
+            self.h_ut = float(cfg.ue_height_m)
+            self.fc = cfg.carrier_ghz if hasattr(cfg, "carrier_ghz") else 3.5
+            self.dbp = breakpoint_m(self.scn, self.fc, self.h_bs, self.h_ut)
+            self.sig = SIGMA_SF[self.scn]
+            self.amp = 1.0 * math.sqrt(2 / K)
+            self.dcorr = (sc.sf_corr_los_m, sc.sf_corr_nlos_m, sc.los_corr_m)
+        self.fields = self.draw()
+
+    def draw(self):
+        cfg, K = self.cfg, self.cfg.shadow_modes
+        rng = self.rng
+        if self.model == "log_distance":
+            return [plane_waves(lambda i: rng.reset_uniform(LOG_DISTANCE_STREAM + i, K).view(self.E, 1, K),
+                                cfg.shadow_acf, cfg.shadow_dcorr_m)]
+        out = []
+        for j, dc in enumerate(self.dcorr):          # sf_los, sf_nlos, los_field (models.py:78-80)
+            st = TR38901_STREAM + 3 * j
+            out.append(plane_waves(lambda i, st=st: rng.reset_uniform(st + i, K).view(self.E, 1, K), "exp", dc))
+        return out
+
+    def reset(self, m):
+        new = self.draw()
+        self.fields = [(torch.where(m.view(1, -1, 1, 1), k2, k1), torch.where(m.view(1, -1, 1), p2, p1))
+                       for (k1, p1), (k2, p2) in zip(self.fields, new)]
+
+    def pathgain(self, pos):
+        """Large-scale gain [E,R] dB of the poses (radio.py:238-277, models.py:137-167)."""
+        cfg = self.cfg
+        if self.model == "log_distance":
+            d = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
+            pl = cfg.pl_const_db + (10 * cfg.pathloss_exp) * torch.log10(d)
+            k, phi = self.fields[0]
+            sh = eval_plane_waves(pos, k, phi, self.amp)
+            rx = cfg.ue_tx_dbm - pl - sh
+            return (rx - cfg.ue_tx_dbm)[..., 0]
+        d2 = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
+        d3 = torch.sqrt(d2 * d2 + (self.h_bs - self.h_ut) ** 2)
+        los = cfg.tr38901_los == "los"
+        pl_l = self._pl_los(d2, d3)
+        pl = pl_l if los else self._pl_nlos(d3, pl_l)
+        k, phi = self.fields[0] if los else self.fields[1]
+        sf = (self.sig[0] if los else self.sig[1]) * eval_plane_waves(pos, k, phi, self.amp)
+        loss = pl + sf
+        rx = cfg.ue_tx_dbm + (-loss)
+        return (rx - cfg.ue_tx_dbm)[..., 0]
+
+    def _pl_los(self, d2, d3):
+        """tr38901.pl_los for UMa / UMi / InH / InF (tr38901.py:162-176)."""
+        scn, fc = self.scn, self.fc
+        lg = torch.log10(d3)
+        if scn in ("UMa", "UMi"):
+            a, n1, b = (28.0, 22.0, 9.0) if scn == "UMa" else (32.4, 21.0, 9.5)
+            pl1 = a + n1 * lg + 20 * math.log10(fc)
+            pl2 = a + 40 * lg + 20 * math.log10(fc) - b * math.log10(self.dbp ** 2 + (self.h_bs - self.h_ut) ** 2)
+            return torch.where(d2 <= self.dbp, pl1, pl2)
+        if scn == "InH":
+            return 32.4 + 17.3 * lg + 20 * math.log10(fc)
+        if scn.startswith("InF"):
+            return 31.84 + 21.50 * lg + 19.00 * math.log10(fc)
+        raise NotImplementedError(scn)
+
+    def _pl_nlos(self, d3, los):
+        scn, fc = self.scn, self.fc
+        lg = torch.log10(d3)
+        lf = 20 * math.log10(fc)
+        if scn == "UMa":
+            return torch.maximum(los, 13.54 + 39.08 * lg + lf - 0.6 * (self.h_ut - 1.5))
+        if scn == "UMi":
+            return torch.maximum(los, 35.3 * lg + 22.4 + 21.3 * math.log10(fc) - 0.3 * (self.h_ut - 1.5))
+        if scn == "InH":
+            return torch.maximum(los, 38.3 * lg + 17.30 + 24.9 * math.log10(fc))
+        raise NotImplementedError(scn)
+
+
+# ------------------------------------------------------------------------------------------ the engine
+class OracleEngine:
+    """NREngine + NRNet + UlMac restated for one cell, uplink, lumped grants (see the module docstring)."""
+
+    FIELDS_Q = ("cap", "start", "end", "lost", "fin", "cls", "det", "hid")
+
+    def __init__(self, E, R, cfg, seed=0, tabs=None):
+        from isaac_net_amd.phy import PhyTables
+        self.cfg, self.E, self.R = cfg, E, R
+        self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
+        assert cfg.n_cells == 1 and cfg.ul and not cfg.dl and cfg.ul_grant_model == "lumped"
+        assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
+        assert cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay" and cfg.ul_retx_sched == "ofdma"
+        assert cfg.ul_amc_alloc == "current" and not cfg.ul_pc_on and cfg.ul_power == "allocated"
+        assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
+        assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
+        self.tabs = tabs if tabs is not None else PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2),
+                                                            cfg.ul_mcs_max)
+        self.phy = Phy(self.tabs)
+        self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
+        self.w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
+        self.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
+        self.rng = CounterRNG(seed, E)
+        self.rician = cfg.rician_mode
+        self.radio = None
+        self.T = 0
+        self.epoch = torch.zeros(E, dtype=torch.long)
+        self.uniform_epoch = 0
+        self.last_snr = torch.zeros(E, R)
+        self.last_hid = torch.zeros(E, dtype=torch.long)
+        self.last_g = None
+        self.ctr = {}
+        E_, R_, S, P, F = E, R, self.S, self.P, self.F
+        z = lambda shape, v, dt: torch.full(shape, v, dtype=dt)  # noqa: E731
+        # MacLink.STATE (mac.py:67-81)
+        self.sent, self.floor = z((E_, R_), 0, torch.long), z((E_, R_), 0, torch.long)
+        self.olla, self.avg = z((E_, R_), 0.0, torch.float32), z((E_, R_), 100.0, torch.float32)
+        self.bsr, self.sr_t = z((E_, R_), 0, torch.long), z((E_, R_), -1, torch.long)
+        self.csi = z((E_, R_, S), 0.0, torch.float32)
+        for n in ("h_state", "h_lo", "h_hi", "h_ready", "h_ntx", "h_mcs", "h_tbs", "h_nsb"):
+            setattr(self, n, z((E_, R_, P), 0, torch.long))
+        self.h_comb, self.h_nrb = z((E_, R_, P), 0.0, torch.float32), z((E_, R_, P), 0.0, torch.float32)
+        self.h_lexp = z((E_, R_, P), -float("inf"), torch.float32)
+        self.last_tx = z((E_, R_), -1, torch.long)
+        # FrameQueue (queues.py:49-61) with the meta fields cls / det / hid of NRNet (nr_engine.py:191-193)
+        self.q_cap, self.q_start, self.q_end = z((E_, R_, F), -1, torch.long), z((E_, R_, F), 0, torch.long), \
+            z((E_, R_, F), 0, torch.long)
+        self.q_lost, self.q_fin = z((E_, R_, F), False, torch.bool), z((E_, R_, F), float("inf"), torch.float64)
+        self.q_cls, self.q_det, self.q_hid = z((E_, R_, F), 0, torch.long), z((E_, R_, F), False, torch.bool), \
+            z((E_, R_, F), 0, torch.long)
+        self.q_enq = z((E_, R_), 0, torch.long)
+        self.h = torch.zeros(E_, R_, S, 2)
+        self._reset_net(None)
+
+    # ---------------- queue helpers (queues.py) ----------------
+    def count(self):
+        return (self.q_cap >= 0).sum(-1)
+
+    def unsent(self):
+        return self.q_enq - self.sent
+
+    def ack_ptr(self):
+        """In-order pointer (mac.py:194-197)."""
+        own = (self.h_state == 1) & (self.h_hi > self.floor[..., None])
+        lo = torch.where(own, torch.maximum(self.h_lo, self.floor[..., None]), torch.full_like(self.h_lo, BIG))
+        return torch.minimum(self.sent, lo.min(-1).values)
+
+    # ---------------- reset (engine.py:763-794, nr_engine.py:250-320, mac.py:176-189, queues.py:70-78) ----------
+    def _reset_net(self, mask):
+        E, R, S = self.E, self.R, self.S
+        m = torch.ones(E, dtype=torch.bool) if mask is None else mask
+        init_q = {"cap": -1, "start": 0, "end": 0, "lost": False, "fin": float("inf"), "cls": 0, "det": False,
+                  "hid": 0}
+        for n, v in init_q.items():
+            setattr(self, "q_" + n, where_env(m, v, getattr(self, "q_" + n)))
+        self.q_enq = where_env(m, 0, self.q_enq)
+        init = {"sent": 0, "floor": 0, "olla": 0.0, "avg": 100.0, "bsr": 0, "sr_t": -1, "csi": 0.0, "h_state": 0,
+                "h_lo": 0, "h_hi": 0, "h_ready": 0, "h_ntx": 0, "h_mcs": 0, "h_tbs": 0, "h_nsb": 0, "h_comb": 0.0,
+                "h_lexp": -float("inf"), "h_nrb": 0.0, "last_tx": -1}
+        for n, v in init.items():
+            setattr(self, n, where_env(m, v, getattr(self, n)))
+        if mask is None:
+            self.ctr = {k: 0 for k in ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new",
+                                       "lost_frames", "new_while_pending", "prb_used", "prb_avail")}
+        self.rng.reset_mask(mask)
+        h0 = self.rng.reset_normal(H0 << 16, R * S * 2).view(E, R, S, 2) / math.sqrt(2)
+        if mask is None:
+            self.h = h0
+            self.last_g = None
+        else:
+            self.h = where_env(m, h0, self.h)
+        if self.rician:
+            u = self.rng.reset_uniform(KPHI << 16, R)
+            self.rng.reset_normal(KFAC << 16, R)
+            phi = (2 * math.pi) * u.view(E, R)
+            spec = torch.stack((torch.cos(phi), torch.sin(phi)), -1)
+            k_los = torch.full((E, R), 10 ** (self.cfg.rician_k_db / 10))
+            if mask is None:
+                self.spec, self.k_los = spec, k_los
+                self.k_in, self.k_lin, self.k_from = k_los.clone(), k_los.clone(), k_los.clone()
+                self.k_g0 = torch.zeros((E, R), dtype=torch.long)
+            else:
+                self.spec = where_env(m, spec, self.spec)
+                self.k_los = where_env(m, k_los, self.k_los)
+                for n in ("k_in", "k_lin", "k_from"):
+                    setattr(self, n, where_env(m, k_los, getattr(self, n)))
+                self.k_g0 = where_env(m, 0, self.k_g0)
+
+    def reset(self, env_ids=None):
+        if env_ids is None:
+            self._reset_net(None)
+            self.T = 0
+            self.epoch.zero_()
+            self.uniform_epoch = 0
+            self.last_snr = torch.zeros_like(self.last_snr)
+            self.last_hid = torch.zeros_like(self.last_hid)
+            if self.radio is not None:
+                self.radio.reset(torch.ones(self.E, dtype=torch.bool))
+            return
+        ids = torch.as_tensor(env_ids, dtype=torch.long).reshape(-1)
+        if ids.numel() == 0:
+            return
+        m = torch.zeros(self.E, dtype=torch.bool)
+        m[ids] = True
+        self._reset_net(m)
+        self.epoch.index_fill_(0, ids, self.T)
+        self.uniform_epoch = None
+        self.last_snr = self.last_snr.clone().index_fill_(0, ids, 0.0)
+        self.last_hid = self.last_hid.clone().index_fill_(0, ids, 0)
+        if self.radio is not None:
+            self.radio.reset(m)
+
+    @property
+    def clock(self):
+        return self.T - self.epoch
+
+    # ---------------- submit (engine.py:796-819, nr_engine.py:451-487, queues.py:87-103) ----------------
+    def submit(self, send, det=None, hid=None):
+        cfg, F, t = self.cfg, self.F, self.T
+        det = torch.zeros_like(send, dtype=torch.bool) if det is None else det
+        hid = torch.zeros(self.E, dtype=torch.long) if hid is None else hid
+        self.last_hid = hid.clone()
+        want = send > 0
+        adm = want
+        if cfg.discard == "pdcp_arrival":
+            stale = (self.q_cap[..., 0] >= 0) & ((t - self.q_cap[..., 0]) >= cfg.timeout_steps)
+            adm = want & ~stale
+        size = self.sizes[(send - 1).clamp(min=0)]
+        if cfg.pkt_overhead_bytes:
+            size = size + torch.ceil(size / cfg.pkt_payload_bytes) * cfg.pkt_overhead_bytes
+        cnt = self.count()
+        acc = adm & (cnt < F) & (size > 0)
+        i = cnt.clamp(max=F - 1)
+        oh = onehot(i, F) & acc[..., None]
+        nb = size.round().long()
+        self.q_cap = torch.where(oh, torch.full_like(self.q_cap, t), self.q_cap)
+        self.q_start = torch.where(oh, self.q_enq[..., None], self.q_start)
+        self.q_end = torch.where(oh, (self.q_enq + nb)[..., None], self.q_end)
+        self.q_lost = self.q_lost & ~oh
+        self.q_fin = torch.where(oh, torch.full_like(self.q_fin, float("inf")), self.q_fin)
+        self.q_enq = self.q_enq + nb * acc
+        self.q_cls = torch.where(oh, send[..., None], self.q_cls)
+        self.q_det = torch.where(oh, det[..., None], self.q_det)
+        self.q_hid = torch.where(oh, hid[:, None, None].expand(-1, self.R, 1), self.q_hid)
+        return acc
+
+    # ---------------- step (engine.py:867-960, nr_engine.py:613-668) ----------------
+    def step(self, x=None, snr_db=None):
+        cfg = self.cfg
+        T = self.T
+        hid = self.last_hid
+        if snr_db is None and x is not None and x.dim() == 3:
+            if self.radio is None:
+                self.radio = Radio(cfg, self.E, self.rng)
+            pg = self.radio.pathgain(x)
+            pgs = pg[..., None].expand(-1, -1, self.S)
+            n_ul = torch.full_like(pgs, cfg.noise_dbm_per_prb("gnb"))
+            ul_ref = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs) + pgs - n_ul
+            snr = pg + cfg.ue_tx_dbm - cfg.subband_noise_dbm
+        else:
+            xs = x if snr_db is None else snr_db
+            ul_ref = xs if xs.dim() == 3 else xs[..., None].expand(-1, -1, self.S)
+            snr = xs if xs.dim() == 2 else xs.mean(-1)
+        out = self._net_step(T, ul_ref, hid)
+        self.last_snr = snr.clone()
+        out["newest"] = self._rel(out["newest"])
+        self.T = T + 1
+        out["cap"] = self._rel(out["cap"])
+        out["sinr_db"] = snr
+        out["serving_cell"] = torch.zeros(self.E, self.R, dtype=torch.long)
+        out["t"] = (T - self.epoch).clone()
+        return out
+
+    def _rel(self, x):
+        shape = (-1,) + (1,) * (x.dim() - 1)
+        return torch.where(x >= 0, x - self.epoch.view(shape), torch.full_like(x, -1))
+
+    def schedule(self, g0):
+        return self.cfg.schedule(g0)
+
+    def _net_step(self, t, ul_ref, hid):
+        cfg = self.cfg
+        N = cfg.slots_per_step
+        g0 = t * N
+        if self.rician:
+            self.k_lin = self.k_in                       # _rician_update with no ramp (nr_engine.py:410-415)
+        for rel, uls, sr in self.schedule(g0):
+            g = g0 + rel
+            self._evolve(g, rel)
+            gain = self._gain()
+            if sr:
+                self._sr_step(g)
+            if uls:
+                self._slot(g, t + (rel + 1) / N, uls, ul_ref, gain, rel)
+        return self._finish(t, hid)
+
+    def _evolve(self, g, rel):
+        """AR(1) fading step (nr_engine.py:570-590)."""
+        if not self.cfg.fading:
+            return
+        dt = 1 if self.last_g is None else g - self.last_g
+        if dt > 0:
+            z = self.rng.step_normal(FADING, rel, self.h[0].numel()).view(self.h.shape)
+            rho = self.cfg.fading_rho_per_ms ** (dt * self.cfg.slot_ms)
+            self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
+        self.last_g = g
+
+    def _gain(self):
+        """Fading gain dB [E,R,S] (nr_engine.py:602-611)."""
+        if not self.cfg.fading:
+            return torch.zeros(self.h.shape[:-1])
+        if not self.rician:
+            return 10 * torch.log10((self.h ** 2).sum(-1).clamp(min=1e-6))
+        k = self.k_lin[..., None, None]
+        inv = 1 / (k + 1)
+        x = torch.sqrt(k * inv) * self.spec[..., None, :] + torch.sqrt(inv) * self.h
+        return 10 * torch.log10((x ** 2).sum(-1).clamp(min=1e-6))
+
+    def _sr_step(self, g):
+        """UlMac.sr_step, lumped (mac_ul.py:66-71)."""
+        need_sr = (self.unsent() > 0) & (self.bsr <= 0) & (self.sr_t < 0)
+        self.sr_t = torch.where(need_sr, torch.full_like(self.sr_t, g), self.sr_t)
+
+    def _split(self, n_prb):
+        return 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
+
+    def _slot(self, g, frac, nsym, sinr_ref, gain_now, rel):
+        """MacLink.slot for the UL (mac.py:228-508 with the UlMac hooks of mac_ul.py)."""
+        cfg, E, R, S, P, phy = self.cfg, self.E, self.R, self.S, self.P, self.phy
+        w = self.w
+        unsent = self.unsent()
+        self.h_state = torch.where((self.h_state == 2) & (self.h_ready <= g), torch.zeros_like(self.h_state),
+                                   self.h_state)
+        # UlMac._pre_slot_lumped (mac_ul.py:140-147)
+        P_ = len(cfg.tdd_pattern)
+        pg_pos = next(p for p in range(P_) if cfg.slot_symbols(p)[1] > 0)
+        if cfg.proactive_grant == "every_ul_slot" or (cfg.proactive_grant == "per_period" and g % P_ == pg_pos):
+            self.bsr = self.bsr.clamp(min=1)
+        granted = (self.sr_t >= 0) & (g - self.sr_t >= cfg.sr_delay)
+        self.bsr = torch.where(granted, self.bsr.clamp(min=1), self.bsr)
+        self.sr_t = torch.where(granted, torch.full_like(self.sr_t, -1), self.sr_t)
+        # candidates
+        rx_el = (self.h_state == 1) & (self.h_ready <= g)
+        rx_p = torch.where(rx_el, self.h_ready, torch.full_like(self.h_ready, BIG)).argmin(-1)
+        has_rx = rx_el.any(-1)
+        free = self.h_state == 0
+        p_new = free.long().argmax(-1)
+        need = torch.minimum(self.bsr, unsent)
+        new_el = free.any(-1) & (need > 0) & ~has_rx
+        pending = (self.h_state == 1).any(-1)
+        rx_nsb = self.h_nsb.gather(-1, rx_p[..., None]).squeeze(-1)
+        # UlMac._sched_estimate (mac_ul.py:154-171)
+        est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + self.csi
+        if cfg.phr_cap:
+            ref = sinr_ref.mean(-1)
+            n_max_prb = cfg.snr_ref_prbs * 10 ** ((ref - cfg.phr_min_db) / 10)
+            n_max = torch.floor(n_max_prb / w[0]).clamp(1, S).long()
+        else:
+            n_max = torch.full((E, R), S, dtype=torch.long)
+        est_o = est + (self.olla[..., None] if cfg.olla else 0.0)
+        re_prb = float(min(12 * nsym - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156))
+        rate_sb = phy.se[phy.mcs_at(est_o)] * re_prb * w / 8
+        if cfg.scheduler == "maxci":
+            metric_sb = rate_sb
+        elif cfg.scheduler == "rr":
+            metric_sb = (g - self.last_tx).float()[..., None].expand_as(rate_sb)
+        else:
+            metric_sb = rate_sb / self.avg.clamp(min=AVG_MIN)[..., None]
+        # retransmission admission (mac.py:300-304)
+        rkey = torch.where(has_rx, metric_sb.sum(-1), torch.full_like(metric_sb[..., 0], -1.0))
+        order = rkey.argsort(-1, descending=True)
+        cum = (rx_nsb * has_rx).gather(-1, order).cumsum(-1)
+        adm_sorted = has_rx.gather(-1, order) & (cum <= S)
+        has_rx = torch.zeros_like(has_rx).scatter(-1, order, adm_sorted)
+        want_cnt = torch.where(has_rx, rx_nsb, torch.where(new_el, n_max, torch.zeros_like(n_max)))
+        lex = cfg.retx_priority
+        prio = (1e9 if lex else 0.0) * has_rx.float()
+        # RBG-by-RBG allocation (mac.py:322-352)
+        cnt = torch.zeros(E, R, dtype=torch.long)
+        left = need.float()
+        cols = []
+        for s in range(S):
+            want = (cnt < want_cnt) & (has_rx | (left > 0))
+            m = torch.where(want, metric_sb[..., s] + prio, torch.full_like(left, -1.0))
+            if lex:
+                wr = want & has_rx
+                m = torch.where(wr.any(-1, keepdim=True) & ~wr, torch.full_like(m, -1.0), m)
+            best, wi = m.max(-1)
+            oh = onehot(wi, R) & (best >= 0)[:, None]
+            cols.append(oh)
+            cnt = cnt + oh.long()
+            left = left - rate_sb[..., s] * oh * ~has_rx
+        won = torch.stack(cols, -1)
+        if not lex:                                      # release short retransmissions (mac.py:353-379)
+            short = has_rx & (won.sum(-1) != rx_nsb)
+            rel_rs = won & short[..., None]
+            won = won & ~short[..., None]
+            cnt = won.sum(-1)
+            cols = []
+            for s in range(S):
+                want = (cnt < want_cnt) & new_el & (left > 0)
+                m = torch.where(want, metric_sb[..., s], torch.full_like(left, -1.0))
+                best, wi = m.max(-1)
+                oh = onehot(wi, R) & ((best >= 0) & rel_rs[..., s].any(-1))[:, None]
+                cols.append(oh)
+                cnt = cnt + oh.long()
+                left = left - rate_sb[..., s] * oh
+            won = won | torch.stack(cols, -1)
+        n_sb = won.sum(-1)
+        n_prb = (won * w).sum(-1)
+        tx_rx = has_rx & (n_sb == rx_nsb) & (n_sb > 0)
+        tx_new = new_el & (n_sb > 0)
+        tx = tx_rx | tx_new
+        # link adaptation (mac.py:386-405, mac_ul.py:182-183)
+        est_tx = sinr_ref - self._split(n_prb)[..., None] + self.csi
+        off = self.olla if cfg.olla else torch.zeros_like(self.olla)
+        mcs_new, tbs_new = phy.select_mcs(est_tx, won, off, n_prb, nsym, cfg.dmrs_re_per_prb,
+                                          cfg.overhead_re_per_prb, cfg.eff_sinr, w)
+        cap_b = (tbs_new // 8 - cfg.tb_overhead_bytes).clamp(min=1)
+        byt_new = torch.minimum(cap_b, unsent)
+        # bind TBs to processes (mac.py:407-426)
+        p_tx = torch.where(tx_rx, rx_p, p_new)
+        ohp = onehot(p_tx, P) & tx[..., None]
+        ohn = ohp & tx_new[..., None]
+        self.h_lo = torch.where(ohn, self.sent[..., None], self.h_lo)
+        self.h_hi = torch.where(ohn, (self.sent + byt_new)[..., None], self.h_hi)
+        self.h_mcs = torch.where(ohn, mcs_new[..., None], self.h_mcs)
+        self.h_tbs = torch.where(ohn, tbs_new[..., None], self.h_tbs)
+        self.h_nsb = torch.where(ohn, n_sb[..., None], self.h_nsb)
+        self.h_ntx = torch.where(ohn, torch.zeros_like(self.h_ntx), self.h_ntx)
+        self.h_comb = torch.where(ohn, torch.zeros_like(self.h_comb), self.h_comb)
+        self.h_lexp = torch.where(ohn, torch.full_like(self.h_lexp, -float("inf")), self.h_lexp)
+        self.h_nrb = torch.where(ohn, torch.zeros_like(self.h_nrb), self.h_nrb)
+        self.h_state = torch.where(ohn, torch.ones_like(self.h_state), self.h_state)
+        self.sent = self.sent + byt_new * tx_new
+        g1 = lambda x: x.gather(-1, p_tx[..., None]).squeeze(-1)  # noqa: E731
+        mcs, tbs = g1(self.h_mcs), g1(self.h_tbs)
+        ntx = g1(self.h_ntx) + 1
+        # decoding (mac.py:428-454, mac_ul.py:185-192)
+        act = sinr_ref - self._split(n_prb)[..., None] + gain_now
+        mcs_eq = None
+        if cfg.harq_combining == "ir_lena":
+            lse, _ = phy.eesm_lse(act, won, mcs, w)
+            lexp = torch.logaddexp(g1(self.h_lexp), lse)
+            nrb = g1(self.h_nrb) + n_prb
+            eff_used = 10 * torch.log10((-phy.beta[mcs] * (lexp - torch.log(nrb.clamp(min=1)))).clamp(min=1e-6))
+            eff_used = eff_used.nan_to_num(nan=-30.0, posinf=60.0, neginf=-30.0)
+            mcs_eq = phy.mcs_eq[mcs, ntx.clamp(max=phy.mcs_eq.shape[1] - 1)]
+            self.h_lexp = torch.where(ohp, lexp[..., None], self.h_lexp)
+            self.h_nrb = torch.where(ohp, nrb[..., None], self.h_nrb)
+            comb = g1(self.h_comb)
+        else:
+            eff = phy.eff_sinr(act, won, mcs, cfg.eff_sinr, w)
+            comb = g1(self.h_comb) + 10 ** (eff / 10) if cfg.harq_combining == "cc" else 10 ** (eff / 10)
+            eff_used = 10 * torch.log10(comb.clamp(min=1e-9))
+        p_err = phy.tb_error_prob(mcs, eff_used, tbs, mcs_eq)
+        u = self.rng.step_uniform(BLER_UL, rel, R)
+        ok = tx & (u >= p_err)
+        fail = tx & ~ok
+        exh = fail & (ntx >= cfg.max_harq_tx)
+        # HARQ update (mac.py:456-477, UL timing mac_ul.py:218-219)
+        ohp_ok, ohp_fail, ohp_exh = ohp & ok[..., None], ohp & fail[..., None], ohp & exh[..., None]
+        self.h_state = torch.where(ohp_ok, torch.zeros_like(self.h_state), self.h_state)
+        self.h_ready = torch.where(ohp_ok, torch.full_like(self.h_ready, g), self.h_ready)
+        self.h_ntx = torch.where(ohp, ntx[..., None], self.h_ntx)
+        self.h_comb = torch.where(ohp, comb[..., None], self.h_comb)
+        self.h_ready = torch.where(ohp_fail, torch.full_like(self.h_ready, g + cfg.ul_rtt), self.h_ready)
+        lo_tx, hi_tx = g1(self.h_lo), g1(self.h_hi)
+        lost_new = 0
+        if cfg.harq_fail == "rlc_am":
+            self.h_ntx = torch.where(ohp_exh, torch.zeros_like(self.h_ntx), self.h_ntx)
+            self.h_comb = torch.where(ohp_exh, torch.zeros_like(self.h_comb), self.h_comb)
+            self.h_lexp = torch.where(ohp_exh, torch.full_like(self.h_lexp, -float("inf")), self.h_lexp)
+            self.h_nrb = torch.where(ohp_exh, torch.zeros_like(self.h_nrb), self.h_nrb)
+            self.h_ready = torch.where(ohp_exh, torch.full_like(self.h_ready, g + cfg.rlc_retx_slots), self.h_ready)
+        else:
+            self.h_state = torch.where(ohp_exh, torch.zeros_like(self.h_state), self.h_state)
+            ov = exh[..., None] & (self.q_start < hi_tx[..., None]) & (self.q_end > lo_tx[..., None]) & \
+                (self.q_cap >= 0)
+            lost_new = int((ov & ~self.q_lost).sum())
+            self.q_lost = self.q_lost | ov
+        # OLLA, BSR / CSI, PF (mac.py:479-485, mac_ul.py:221-236, mac.py:534-554)
+        if cfg.olla:
+            self.olla = (self.olla + cfg.olla_up_db * ok - self.olla_dn * fail).clamp(-10, 10)
+        served = (hi_tx - lo_tx) * ok
+        self.bsr = torch.where(tx, self.unsent(), self.bsr)
+        self.csi = gain_now
+        self.avg = ((1 - 1 / cfg.pf_window) * self.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
+        if cfg.scheduler == "rr":
+            self.last_tx = torch.where(tx, torch.full_like(self.last_tx, g), self.last_tx)
+        c = self.ctr
+        c["tb_new"] += int(tx_new.sum()); c["tb_retx"] += int(tx_rx.sum()); c["tb_ok"] += int(ok.sum())
+        c["tb_fail"] += int(fail.sum()); c["exhaust"] += int(exh.sum()); c["bytes_ok"] += int(served.sum())
+        c["bytes_new"] += int((byt_new * tx_new).sum()); c["new_while_pending"] += int((tx_new & pending).sum())
+        c["prb_used"] += float((n_prb * tx).sum()); c["prb_avail"] += float(self.w.sum()) * E
+        c["lost_frames"] += lost_new
+        # RLC in-order delivery (mac.py:500-503)
+        ack = self.ack_ptr()
+        done = (self.q_cap >= 0) & (self.q_end <= ack[..., None]) & ~self.q_lost & torch.isinf(self.q_fin)
+        self.q_fin = torch.where(done, torch.full_like(self.q_fin, frac + cfg.proc_offset_ms / cfg.control_step_ms),
+                                 self.q_fin)
+
+    # ---------------- end of step (nr_engine.py:843-888, mac.py:585-616, mac_ul.py:255-257) ----------------
+    def _finish(self, t, cur_hid):
+        cfg, F = self.cfg, self.F
+        self.rng.ctr[STEP].add_(1)
+        valid = self.q_cap >= 0
+        delivered = valid & (self.q_fin <= t + 1 + 1e-9)
+        if cfg.discard == "purge":
+            timed = valid & torch.isinf(self.q_fin) & ((t + 1 - self.q_cap) >= cfg.timeout_steps)
+        else:
+            timed = torch.zeros_like(valid)
+        dropped = valid & self.q_lost & (self.q_end <= self.ack_ptr()[..., None]) & ~timed
+        capd = torch.where(delivered, self.q_cap, torch.full_like(self.q_cap, -1))
+        newest = capd.max(-1).values
+        det_env = (delivered & self.q_det & (self.q_hid == cur_hid[:, None, None])).flatten(1).any(-1)
+        out = {"newest": newest, "det_env": det_env, "delivered": delivered, "timed_out": timed, "dropped": dropped,
+               "cap": self.q_cap.clone(), "cls": torch.where(valid, self.q_cls, torch.zeros_like(self.q_cls)),
+               "delay": torch.where(delivered, (self.q_fin - self.q_cap.double()).float(),
+                                    torch.full(self.q_cap.shape, float("nan")))}
+        gone = delivered | timed | dropped
+        self.q_cap = torch.where(gone, torch.full_like(self.q_cap, -1), self.q_cap)
+        key = (self.q_cap < 0).long() * F + torch.arange(F)
+        order = key.argsort(-1)
+        for n in self.FIELDS_Q:
+            setattr(self, "q_" + n, getattr(self, "q_" + n).gather(-1, order))
+        head = self.q_cap[..., 0] >= 0
+        self.floor = torch.where(head, self.q_start[..., 0], self.q_enq)
+        self.sent = torch.maximum(self.sent, self.floor)
+        dead = (self.h_state == 1) & (self.h_hi <= self.floor[..., None]) & (self.h_hi > self.h_lo)
+        for n, v in (("h_state", 0), ("h_ready", 0), ("h_ntx", 0), ("h_comb", 0.0), ("h_lexp", -float("inf")),
+                     ("h_nrb", 0.0)):
+            x = getattr(self, n)
+            setattr(self, n, torch.where(dead, torch.full_like(x, v), x))
+        self.bsr = torch.minimum(self.bsr, self.unsent())
+        out["queue_len"] = self.count()
+        out["queue_bytes"] = (self.q_enq - self.ack_ptr()).clamp(min=0).float()
+        return out
+
+    # ---------------- state in the reference's state_dict names (core/nr_fast.py:41-75) ----------------
+    STATE_MAP = {"ul.sent": "sent", "ul.floor": "floor", "ul.olla": "olla", "ul.avg": "avg", "ul.bsr": "bsr",
+                 "ul.sr_t": "sr_t", "ul.csi": "csi", "ul.h_state": "h_state", "ul.h_lo": "h_lo", "ul.h_hi": "h_hi",
+                 "ul.h_ready": "h_ready", "ul.h_ntx": "h_ntx", "ul.h_mcs": "h_mcs", "ul.h_tbs": "h_tbs",
+                 "ul.h_nsb": "h_nsb", "ul.h_comb": "h_comb", "ul.h_lexp": "h_lexp", "ul.h_nrb": "h_nrb",
+                 "ul.last_tx": "last_tx", "ul.q.cap": "q_cap", "ul.q.start": "q_start", "ul.q.end": "q_end",
+                 "ul.q.lost": "q_lost", "ul.q.fin": "q_fin", "ul.q.cls": "q_cls", "ul.q.det": "q_det",
+                 "ul.q.hid": "q_hid", "ul.q.enq": "q_enq", "net.h": "h", "eng.epoch": "epoch",
+                 "eng._last_snr": "last_snr", "eng._last_hid": "last_hid"}
+    RICIAN_MAP = {"net.spec": "spec", "net.k_los": "k_los", "net.k_in": "k_in", "net.k_lin": "k_lin",
+                  "net.k_from": "k_from", "net.k_g0": "k_g0"}
+
+    def state(self):
+        out = {k: getattr(self, v) for k, v in self.STATE_MAP.items()}
+        if self.rician:
+            out.update({k: getattr(self, v) for k, v in self.RICIAN_MAP.items()})
+        out["rng.episode"] = self.rng.episode
+        out["rng.ctr[1]"] = self.rng.ctr[SUBMIT]
+        out["rng.ctr[2]"] = self.rng.ctr[STEP]
+        return out
+
+    def load_state(self, sd, T, last_g):
+        """Teacher forcing: overwrite every state tensor (copies) and the host clock / last fading slot."""
+        for k, v in self.STATE_MAP.items():
+            if k in sd:
+                setattr(self, v, torch.as_tensor(sd[k]).clone())
+        if self.rician:
+            for k, v in self.RICIAN_MAP.items():
+                if k in sd:
+                    setattr(self, v, torch.as_tensor(sd[k]).clone())
+        self.rng.episode = torch.as_tensor(sd["rng.episode"]).clone()
+        self.rng.ctr[SUBMIT] = torch.as_tensor(sd["rng.ctr[1]"]).clone()
+        self.rng.ctr[STEP] = torch.as_tensor(sd["rng.ctr[2]"]).clone()
+        self.T, self.last_g = int(T), last_g

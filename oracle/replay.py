@@ -1,0 +1,44 @@
+"""Replay a golden trajectory (tests/golden/traj_*.npz) on an engine: same inputs, resets and submit order.
+Test infrastructure only (see oracle/__init__.py)."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import torch
+
+
+def load_case(path):
+    d = np.load(path, allow_pickle=False)
+    cfg = json.loads(bytes(d["cfg_json"]).decode())
+    for k in ("msg_sizes", "cell_positions_m"):
+        if k in cfg:
+            cfg[k] = tuple(tuple(v) if isinstance(v, list) else v for v in cfg[k])
+    return d, cfg, bytes(d["kind"]).decode()
+
+
+def submits(counts_s):
+    """The harness's submit calls of one step: class 1 first, one call per message index. counts_s [E,R,NC]."""
+    out = []
+    for ci in range(counts_s.shape[-1]):
+        n = counts_s[..., ci]
+        for i in range(int(n.max()) if n.size else 0):
+            out.append(np.where(n > i, ci + 1, 0).astype(np.int64))
+    return out
+
+
+def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)):
+    """Drive eng (oracle or HIP engine) through the case; on_step(s, out, accepted_list) after every step."""
+    T = int(d["steps"]) if steps is None else steps
+    for s in range(T):
+        ids = np.nonzero(d["reset_mask"][s])[0]
+        if len(ids):
+            eng.reset(ids.tolist())
+        acc = [eng.submit(to(send)) for send in submits(d["counts"][s])]
+        x = to(d["x"][s])
+        if kind == "snr3":
+            o = eng.step(snr_db=x)
+        else:
+            o = eng.step(x)
+        if on_step is not None:
+            on_step(s, o, acc)

@@ -1,0 +1,238 @@
+"""Write the golden vectors that pin the oracle (run in the build container only; needs the reference checkout).
+
+The reference package (isaac-net, pure Python + PyTorch) is imported from /root/reference and its CPU
+`backend="reference"` NR engine is run on small scenarios. What is written is data only: per-step inputs,
+the step output dicts, the engine state after every step, and the processed PHY tables. Nothing from the
+reference is copied. The vectors pin what no closed form or known answer pins:
+
+  * multi-slot trajectories of NRNet.step / step_rx (scheduler, link adaptation, HARQ, RLC interplay, CPU argsort
+    tie order), isaac_net/core/nr_engine.py:613-668, core/mac.py:228-508;
+  * the processed BLER table and thr_ref (core/phy.py:234-243, 405-482);
+  * the plane-wave shadowing draws of the radio (core/radio.py:185-189, core/channels/fields.py:38-64);
+  * the eager _finish / compaction output layout (core/nr_engine.py:843-888, core/queues.py:105-110).
+
+Usage:  python tests/golden/make_fixtures.py            (writes tests/golden/*.npz)
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+
+REF = "/root/reference"
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _ref():
+    sys.path.insert(0, REF)
+    from isaac_net.core.config import NRConfig
+    from isaac_net.core.engine import make_engine
+    from isaac_net.core.nr_fast import state_dict
+    from isaac_net.core.traffic import Requests
+    return NRConfig, make_engine, state_dict, Requests
+
+
+# ---------------------------------------------------------------------------------------------- scenarios
+# Each case: config overrides, E, R, steps, input kind, pose / traffic generator parameters, resets.
+CASES = {
+    # the CPU-runnable NR plumbing scenario, shrunk: RR, K=4 UL slots, 1500 B, Poisson 0.5
+    "c1": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=4,
+                        max_harq_tx=4, frame_buffer=16, msg_sizes=(1500.0,), fading_rho_per_ms=0.0,
+                        channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                        cell_positions_m=((50.0, 50.0),), gnb_height_m=10.0),
+               E=4, R=8, steps=40, kind="pose", arena=100.0, walk=0.0, rates=(0.5,), resets={25: [2]}),
+    # the RL-scale scenario, shrunk: PF alpha 0.01, Rician K 3 dB, two classes, random walk
+    "c2": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", pf_window=100.0,
+                        n_harq=8, max_harq_tx=5, frame_buffer=32, msg_sizes=(200.0, 4000.0), fading_rho_per_ms=0.0,
+                        fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi",
+                        tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+               E=4, R=8, steps=40, kind="pose", arena=200.0, walk=0.025, rates=(0.8, 0.1), resets={20: [1]}),
+    # heavy load on the config-2 MAC: contention, retransmissions, exhaustion, purge timeouts
+    "c2heavy": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf",
+                             n_harq=8, max_harq_tx=3, frame_buffer=12, msg_sizes=(2000.0, 9000.0),
+                             fading_rho_per_ms=0.0, fading_rician=True, rician_k_db=3.0, timeout_steps=3,
+                             channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                             cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                    E=4, R=16, steps=30, kind="pose", arena=400.0, walk=0.5, rates=(2.0, 0.7), resets={12: [0, 3]}),
+    # SNR input, correlated AR(1) Rayleigh fading, RLC UM drop, small FIFO (overflow), max C/I
+    "snr_drop": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=2,
+                              harq_fail="drop", frame_buffer=6, msg_sizes=(3000.0, 500.0), timeout_steps=6),
+                     E=3, R=8, steps=30, kind="snr", snr=(-4.0, 14.0), rates=(1.2, 0.6), resets={17: [1]}),
+    # per-subband SNR input, IR combining, no retransmission priority, no PHR cap, stack processing offset
+    "snr3_ir": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="pf", n_harq=4, max_harq_tx=3,
+                             harq_combining="ir_lena", retx_priority=False, phr_cap=False, frame_buffer=8,
+                             msg_sizes=(2500.0,), proc_offset_ms=4.0, discard="none"),
+                    E=3, R=8, steps=30, kind="snr3", snr=(-2.0, 16.0), rates=(1.0,), resets={}),
+    # log-distance radio, mean-dB effective SINR without combining, round robin, PDCP discard on arrival
+    "logd_meandb": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=5.0, scheduler="rr", n_harq=2, max_harq_tx=4,
+                                 harq_combining="none", eff_sinr="mean_db", frame_buffer=10, msg_sizes=(1200.0,),
+                                 discard="pdcp_arrival", timeout_steps=4, cell_positions_m=((20.0, 30.0),)),
+                        E=3, R=8, steps=30, kind="pose", arena=120.0, walk=1.0, rates=(1.3,), resets={9: [0, 2]}),
+}
+
+
+def _inputs(name, c):
+    """Per-step inputs of a case: poses or SNR, and per-class arrival counts (numpy, seeded by the case name)."""
+    rs = np.random.default_rng(int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little"))
+    E, R, T = c["E"], c["R"], c["steps"]
+    n_cls = len(c["rates"])
+    counts = np.stack([rs.poisson(lam, size=(T, E, R)) for lam in c["rates"]], -1).astype(np.int64)
+    if c["kind"] == "pose":
+        a = c["arena"]
+        p = rs.uniform(0.0, a, size=(E, R, 2))
+        xs = []
+        for _ in range(T):
+            xs.append(p.copy())
+            ang = rs.uniform(0.0, 2 * math.pi, size=(E, R))
+            p = np.clip(p + c["walk"] * np.stack([np.cos(ang), np.sin(ang)], -1), 0.0, a)
+        x = np.stack(xs).astype(np.float32)
+    elif c["kind"] == "snr":
+        lo, hi = c["snr"]
+        x = rs.uniform(lo, hi, size=(T, E, R)).astype(np.float32)
+    else:
+        lo, hi = c["snr"]
+        x = rs.uniform(lo, hi, size=(T, E, R, 1)) + rs.normal(0.0, 2.0, size=(T, E, R, 13))
+        x = x.astype(np.float32)
+    assert counts.shape == (T, E, R, n_cls)
+    return x, counts
+
+
+def _np(v):
+    """A copy (the reference updates some state tensors in place: rng counters, episode, epoch)."""
+    return np.array(v.detach().cpu().numpy(), copy=True)
+
+
+def run_case(name, c):
+    NRConfig, make_engine, state_dict, Requests = _ref()
+    cfg = NRConfig(**c["cfg"], seed=0)
+    E, R, T = c["E"], c["R"], c["steps"]
+    eng = make_engine("L2", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
+    x, counts = _inputs(name, c)
+    out = {"x": x, "counts": counts, "E": np.int64(E), "R": np.int64(R), "steps": np.int64(T),
+           "cfg_json": np.frombuffer(json.dumps(c["cfg"]).encode(), dtype=np.uint8),
+           "kind": np.frombuffer(c["kind"].encode(), dtype=np.uint8)}
+    reset_mask = np.zeros((T, E), dtype=np.bool_)
+    for s, ids in c["resets"].items():
+        reset_mask[s, ids] = True
+    out["reset_mask"] = reset_mask
+    keys_seen = set()
+
+    def snap(prefix):
+        sd = state_dict(eng)
+        for k, v in sd.items():
+            if torch.is_tensor(v):
+                out[f"{prefix}/{k}"] = _np(v)
+                keys_seen.add(k)
+        rad = eng.radio
+        if rad is not None:
+            if rad.k is not None:
+                out[f"{prefix}/radio.k"] = _np(rad.k)
+                out[f"{prefix}/radio.phi"] = _np(rad.phi)
+            if rad.ch is not None:
+                for fname in ("sf_los", "sf_nlos", "los_field"):
+                    f = getattr(rad.ch, fname)
+                    out[f"{prefix}/radio.{fname}.k"] = _np(f.k)
+                    out[f"{prefix}/radio.{fname}.phi"] = _np(f.phi)
+
+    snap("init")
+    for s in range(T):
+        ids = np.nonzero(reset_mask[s])[0]
+        if len(ids):
+            eng.reset(torch.tensor(ids, dtype=torch.long))
+            snap(f"reset{s:03d}")
+        # arrivals: for each class in order, one submit per message index (harness order, class 1 first)
+        acc_all = []
+        for ci in range(counts.shape[-1]):
+            n = torch.from_numpy(counts[s, :, :, ci])
+            for i in range(int(n.max())):
+                send = torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n))
+                acc_all.append(_np(eng.submit(None, Requests(send=send))))
+        out[f"s{s:03d}/n_submit"] = np.int64(len(acc_all))
+        if acc_all:
+            out[f"s{s:03d}/accepted"] = np.stack(acc_all)
+        xs = torch.from_numpy(x[s])
+        if c["kind"] == "pose":
+            o = eng.step(None, xs)
+        elif c["kind"] == "snr":
+            o = eng.step(None, xs)
+        else:
+            o = eng.step(None, snr_db=xs)
+        for k, v in o.items():
+            out[f"s{s:03d}/out.{k}"] = _np(v)
+        snap(f"s{s:03d}")
+    out["counters_json"] = np.frombuffer(json.dumps(eng.counters()).encode(), dtype=np.uint8)
+    np.savez_compressed(os.path.join(HERE, f"traj_{name}.npz"), **out)
+    print(name, "state keys:", len(keys_seen), "arrays:", len(out))
+
+
+def phy_tables():
+    """Processed PHY tables of both MCS tables (core/phy.py PHY): BLER table, grids, betas, thresholds, TBS."""
+    NRConfig, make_engine, state_dict, Requests = _ref()
+    from isaac_net.core.phy import PHY, tbs_38214, segment
+    out = {}
+    for mt in (1, 2):
+        ph = PHY("ul", mt, "cpu")
+        b = ph.bler.numpy()
+        out[f"t{mt}/bler_sha256"] = np.frombuffer(hashlib.sha256(np.ascontiguousarray(b).tobytes()).digest(),
+                                                  dtype=np.uint8)
+        out[f"t{mt}/bler_shape"] = np.array(b.shape, dtype=np.int64)
+        rs = np.random.default_rng(mt)
+        idx = np.stack([rs.integers(0, s, size=4000) for s in b.shape[1:]], -1)
+        out[f"t{mt}/sample_idx"] = idx
+        out[f"t{mt}/sample_val"] = b[0, idx[:, 0], idx[:, 1], idx[:, 2]]
+        out[f"t{mt}/snr_grid"] = ph.snr_grid.numpy()
+        out[f"t{mt}/cbs_axis"] = ph.cbs_axis.numpy()
+        out[f"t{mt}/beta"] = ph.beta.numpy()
+        out[f"t{mt}/thr_ref"] = ph.thr_ref.numpy()
+        out[f"t{mt}/thr"] = ph.thr.numpy()
+        out[f"t{mt}/mcs_eq"] = ph.mcs_eq.numpy()
+        out[f"t{mt}/se"] = ph.se.numpy()
+        for ns in (2, 4, 12, 13):
+            n = torch.arange(0, 274, dtype=torch.float32)
+            tbs = ph.tbs_all(n, ns, 12, 0)
+            out[f"t{mt}/tbs_ns{ns}"] = tbs.numpy()
+            cbs, c, bg = ph.cb(tbs, ph.r)
+            out[f"t{mt}/cbs_ns{ns}"] = cbs.numpy()
+            out[f"t{mt}/ncb_ns{ns}"] = c.numpy()
+    # a few TBS values at other dmrs / overhead and two layers
+    n = torch.arange(0, 274, dtype=torch.float32)[:, None]
+    out["tbs_oh6_l2"] = tbs_38214(torch.tensor([2.0, 4.0, 6.0, 8.0]), torch.tensor([0.2, 0.5, 0.7, 0.93]), n, 12,
+                                  12, 6, 2).numpy()
+    np.savez_compressed(os.path.join(HERE, "phy_tables.npz"), **out)
+    print("phy tables written")
+
+
+def rng_vectors():
+    """Counter-RNG draws (core/proto/rng.py) for a few keys: uniforms and normals, step and reset channels."""
+    sys.path.insert(0, REF)
+    from isaac_net.core.proto import rng as R_
+    out = {}
+    r = R_.CounterRNG(0xC0FFEE1234, 6, "cpu")
+    r.reset(None)
+    r.reset(torch.tensor([1, 4]))
+    r.tick(R_.STEP)
+    r.tick(R_.STEP)
+    out["seed"] = np.int64(0xC0FFEE1234)
+    out["episode"] = r.episode.numpy()
+    out["ctr_step"] = r.ctr[R_.STEP].numpy()
+    out["u_step_s5"] = r.uniform(R_.STEP, (2 << 16) | 5, 37).numpy()
+    out["n_step_s3"] = r.normal(R_.STEP, (1 << 16) | 3, 52).numpy()
+    out["u_reset_s0"] = r.reset_uniform(None, 6 << 16, 9).numpy()
+    out["n_reset_s0"] = r.reset_normal(None, 4 << 16, 20).numpy()
+    out["s0"] = np.int64(r.s0)
+    np.savez_compressed(os.path.join(HERE, "rng_vectors.npz"), **out)
+    print("rng vectors written")
+
+
+if __name__ == "__main__":
+    torch.set_num_threads(1)
+    names = sys.argv[1:] or list(CASES)
+    rng_vectors()
+    phy_tables()
+    for n in names:
+        run_case(n, CASES[n])
