@@ -1,0 +1,171 @@
+/*
+ * inet_nr.h -- C ABI of the MI355X-native NR uplink engine (libinet_nr.so, HIP kernels for gfx950).
+ *
+ * Drop-in boundary for isaac-net's per-control-step NR engine hot path (level "L2", one cell, uplink). The
+ * reference launches its fused Triton kernel through
+ *     nr_triton.launch_step(eng, uref, dref, pc, itab, ftab, K, gate, dgate)      isaac_net/core/nr_triton.py:1104-1167
+ * from NRTritonEngine._triton_step (isaac_net/core/nr_fast.py:702-752), and runs the enqueue (NRNet.add_frames,
+ * isaac_net/core/nr_engine.py:466-487) and partial reset (NREngine.reset, isaac_net/core/engine.py:763-794) as eager
+ * torch code. This library replaces all three with plain-pointer entry points:
+ *
+ *   inet_nr_step    one control step: radio prologue, every scheduled slot (fading, SR, UL MAC), the RLC
+ *                   epilogue (delivered / timed-out / dropped, compaction) and the step outputs.
+ *                   Replaces launch_step + the torch prologue/epilogue of _triton_step (nr_fast.py:702-752,
+ *                   nr_engine.py:843-888) and the radio of NREngine._pathgain (engine.py:853-865).
+ *   inet_nr_submit  enqueue one message per robot (FrameQueue.add / NRNet.add_frames, queues.py:87-103,
+ *                   nr_engine.py:466-487), or several per robot in class order (counts form).
+ *   inet_nr_reset   partial or full reset of an env mask (NRNet.reset, MacLink.reset, FrameQueue.reset,
+ *                   NRRng.reset_mask, RadioMC.reset: nr_engine.py:250-320, mac.py:176-189, queues.py:70-78,
+ *                   nr_rng.py:45-52, radio.py:200-219).
+ *
+ * Conventions
+ *   Ownership  The caller allocates and owns every buffer (device memory); the library never allocates or frees
+ *              and updates state in place, so a call can be captured in a HIP graph.
+ *   Layout     Robot-minor SoA: per-robot scalars [E][R]; per-subband [E][S][R]; per-HARQ-process [E][P][R];
+ *              per-frame state [E][F][R]. Step outputs use the reference's [E][R][F] layout and dtypes.
+ *   Errors     Every entry point returns 0 on success or a negative INET_NR_E* code, checked before any launch.
+ *   Threading  Call from one host thread; work is enqueued on `stream` (a hipStream_t), with no host sync and no
+ *              host read of device data.
+ */
+#ifndef INET_NR_H
+#define INET_NR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INET_NR_ABI_VERSION 1
+#define INET_NR_MAX_S 32          /* subbands (RBGs) */
+#define INET_NR_MAX_P 16          /* HARQ processes */
+#define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
+#define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
+#define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
+
+#define INET_NR_OK 0
+#define INET_NR_EINVAL (-1)       /* a size or pointer argument is out of range or missing */
+#define INET_NR_EUNSUPPORTED (-2) /* a feature flag this build does not implement */
+#define INET_NR_ELAUNCH (-3)      /* the HIP runtime refused a launch */
+
+/* Per-env engine state (all device pointers). */
+typedef struct InetNrState {
+    /* MAC per robot [E][R] (mac.py:67-81, mac_ul.py) */
+    int32_t *sent, *floor_, *bsr, *sr_t, *last_tx;
+    float *olla, *avg;
+    /* queue per robot [E][R]: stream length and number of queued frames (frames are a prefix) */
+    int32_t *enq, *qlen;
+    /* per subband [E][S][R]: CSI (last PUSCH gain, dB) and the AR(1) fading state h = re + j im */
+    float *csi, *h_re, *h_im;
+    /* HARQ [E][P][R]: meta = state | ntx << 8 | mcs << 16 | nsb << 24; byte ranges, ready slot, TBS (bits),
+       chase-combined linear SINR, IR log-sum and PRB count */
+    uint32_t *h_meta;
+    int32_t *h_lo, *h_hi, *h_ready, *h_tbs;
+    float *h_comb, *h_lexp, *h_nrb;
+    /* frames [E][F][R]: capture step, byte range, completion slot (INT32_MAX = not completed),
+       meta = lost | det << 1 | cls << 8, hazard id */
+    int32_t *q_cap, *q_start, *q_end, *q_fin;
+    uint32_t *q_meta;
+    int32_t *q_hid;
+    /* Rician specular phasor and K (linear) per robot [E][R] (rician_k_db mode) */
+    float *spec_re, *spec_im, *k_lin;
+    /* counter RNG per env [E]: env id (global), episode, step and submit call counters */
+    int32_t *env_id, *episode, *ctr_step, *ctr_submit;
+    /* engine clock epoch per env [E] */
+    int32_t *epoch;
+    /* shadowing plane waves per env [E][NF][KF][3] = (kx, ky, phi), NF = 3 (tr38901) or 1 (log_distance) */
+    float *field;
+    /* per-env counters [E][INET_NR_NCTR] int64: tb_new, tb_retx, tb_ok, tb_fail, exhaust, bytes_ok, bytes_new,
+       lost_frames, new_while_pending, prb_used, reserved, reserved; and per-env HARQ histograms
+       [E][3][max_tx + 1] int64: decoded TBs by transmissions, TBs sent as transmission k, failed as transmission k */
+    int64_t *ctr, *hist;
+} InetNrState;
+
+/* Device tables (PHY) and the host constants that go with them. */
+typedef struct InetNrTables {
+    const float *bler;        /* [M][C][G] code-block BLER */
+    const float *thr_ref;     /* [M] target-BLER SINR of one 10-PRB RBG */
+    const float *se;          /* [M] spectral efficiency Qm R */
+    const float *beta;        /* [M] EESM beta */
+    const float *rate;        /* [M] code rate R */
+    const int32_t *mcs_eq;    /* [M][EQW] HARQ-IR equivalent MCS */
+    const int32_t *la_tbs;    /* [NSYM][NPRB + 1][M] TBS bits */
+    const int32_t *la_ci0;    /* [NSYM][NPRB + 1][M] code-block-size index */
+    const float *la_cwi;      /* [NSYM][NPRB + 1][M] its interpolation weight */
+    const float *la_ncb;      /* [NSYM][NPRB + 1][M] number of code blocks */
+    const float *w;           /* [S] PRBs per subband */
+    const float *logw;        /* [S] log(w) */
+    const float *wdb;         /* [S] 10 log10(w / snr_ref_prbs) */
+    float s0, ds, c0, dc;     /* SNR grid origin / step, code-block axis origin / step */
+    int32_t M, C, G, NPRB, EQW, mcs_max, thr_monotone, pad;
+} InetNrTables;
+
+/* Config constants of the step (derived on the host from NRConfig). */
+typedef struct InetNrParams {
+    int32_t E, R, S, P, F, N;         /* envs, robots, subbands, HARQ processes, frame buffer, slots per step */
+    int32_t sched;                    /* 0 pf, 1 maxci, 2 rr */
+    int32_t comb;                     /* 0 none, 1 cc, 2 ir_lena */
+    int32_t eesm;                     /* 1 eesm, 0 mean_db */
+    int32_t harq_drop, olla, phr_cap, retx_prio, rician, fading, purge, input_kind, radio_model, out_ref;
+    int32_t max_tx, sr_delay, ul_rtt, rlc_retx, timeout, tb_oh, n_fields, n_modes, seed_key, pad0;
+    float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
+    float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
+    /* radio constants (float32 values of the reference's Python doubles) */
+    float gnb_x, gnb_y, hh2, dbp, pl_a, pl_n1, pl_c20, pl_c2, nl_b1, nl_b0, nl_c, nl_d, sig, amp, pl_const, pl_exp10;
+    float proc_off_hi, proc_off_lo;   /* proc_offset_ms / control_step_ms as a double split in two floats */
+} InetNrParams;
+
+/* One scheduled slot of the control step (host-built per TDD key, device resident). */
+typedef struct InetNrRow {
+    int32_t rel;          /* slot index inside the control step */
+    int32_t nsym_idx;     /* index into the LA tables (-1: no UL data symbols) */
+    int32_t flags;        /* 1 SR opportunity, 2 UL data, 4 fading evolves, 8 fading state needed, 16 proactive grant */
+    float re_prb;         /* data REs per PRB of the UL slot */
+    float rho, c1;        /* AR(1) coefficients rho^(dt slot_ms) and sqrt(1 - rho^2), as float32 */
+    uint32_t salt_fade;   /* salt((FADING << 16) | rel) */
+    uint32_t salt_bler;   /* salt((BLER_UL << 16) | rel) */
+} InetNrRow;
+
+/* Step outputs. out_ref = 1: reference dtypes and layout; 0: compact form (flags/delay/cap/cls of every frame). */
+typedef struct InetNrOutputs {
+    uint8_t *delivered, *timed_out, *dropped;   /* [E][R][F] bool (out_ref = 1); flags bit 0/1/2 in delivered (0) */
+    int64_t *cap, *cls;                          /* [E][R][F] int64 (out_ref = 1) */
+    int32_t *cap32;                              /* [E][R][F] int32 (out_ref = 0) */
+    uint8_t *cls8;                               /* [E][R][F] uint8 (out_ref = 0) */
+    float *delay;                                /* [E][R][F] float32 */
+    int64_t *newest, *queue_len, *serving_cell;  /* [E][R] int64 */
+    float *queue_bytes, *sinr_db;                /* [E][R] float32 */
+    uint8_t *det_env;                            /* [E] bool */
+    int64_t *t;                                  /* [E] int64 */
+} InetNrOutputs;
+
+/* Library version (INET_NR_ABI_VERSION) and a short build string. */
+int32_t inet_nr_abi_version(void);
+const char *inet_nr_build_info(void);
+
+/* One control step T (the engine's global control-step counter) over rows[0..n_rows) (device buffer).
+   x: poses [E][R][2] (input_kind 0), SNR [E][R] (1) or per-subband SNR [E][R][S] (2), float32, device.
+   cur_hid: [E] int64 hazard ids for det_env (device). first_evolve_dt is folded into rows[0] by the host. */
+int32_t inet_nr_step(const InetNrState *st, const InetNrTables *tab, const InetNrParams *prm, const InetNrRow *rows,
+                     int32_t n_rows, int64_t T, const float *x, const int64_t *cur_hid, const InetNrOutputs *out,
+                     void *stream);
+
+/* Enqueue at control step T. Single form (counts == NULL): send [E][R] int64 class index (0 = none), det [E][R]
+   uint8 or NULL, hid [E] int64 or NULL; accepted [E][R] uint8. Counts form (send == NULL): counts [E][R][NC]
+   uint8 messages per class, enqueued class by class; accepted [E][R] int32 = messages accepted.
+   sizes [NC] float32 message bytes; discard_pdcp: 1 = refuse while the head frame is stale (timeout_steps). */
+int32_t inet_nr_submit(const InetNrState *st, const InetNrParams *prm, int64_t T, const int64_t *send,
+                       const uint8_t *det, const int64_t *hid, const uint8_t *counts, int32_t n_cls,
+                       const float *sizes, int32_t discard_pdcp, int32_t pkt_payload, int32_t pkt_overhead,
+                       void *accepted, void *stream);
+
+/* Reset the envs of mask [E] uint8 (device; NULL = every env, full reset). T: control step of the reset (the
+   epoch of the reset envs). k_lin0: Rician K (linear) of a reset link. dcorr[3]: correlation distances of the
+   shadowing fields (tr38901: sf LOS, sf NLOS, LOS state; log_distance: shadow_dcorr_m), spectrum: 0 sos, 1 exp. */
+int32_t inet_nr_reset(const InetNrState *st, const InetNrParams *prm, const uint8_t *mask, int64_t T, float k_lin0,
+                      const float *dcorr, int32_t spectrum, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INET_NR_H */

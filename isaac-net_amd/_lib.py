@@ -1,0 +1,79 @@
+"""ctypes binding of libinet_nr.so (include/inet_nr.h). No torch types cross the ABI: only pointers and sizes."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libinet_nr.so")
+
+P = C.c_void_p
+i32, i64, f32, u32 = C.c_int32, C.c_int64, C.c_float, C.c_uint32
+
+
+class InetNrState(C.Structure):
+    _fields_ = [(n, P) for n in (
+        "sent", "floor_", "bsr", "sr_t", "last_tx", "olla", "avg", "enq", "qlen", "csi", "h_re", "h_im",
+        "h_meta", "h_lo", "h_hi", "h_ready", "h_tbs", "h_comb", "h_lexp", "h_nrb",
+        "q_cap", "q_start", "q_end", "q_fin", "q_meta", "q_hid", "spec_re", "spec_im", "k_lin",
+        "env_id", "episode", "ctr_step", "ctr_submit", "epoch", "field", "ctr", "hist")]
+
+
+class InetNrTables(C.Structure):
+    _fields_ = [(n, P) for n in ("bler", "thr_ref", "se", "beta", "rate", "mcs_eq", "la_tbs", "la_ci0", "la_cwi",
+                                 "la_ncb", "w", "logw", "wdb")] + \
+               [(n, f32) for n in ("s0", "ds", "c0", "dc")] + \
+               [(n, i32) for n in ("M", "C", "G", "NPRB", "EQW", "mcs_max", "thr_monotone", "pad")]
+
+
+class InetNrParams(C.Structure):
+    _fields_ = [(n, i32) for n in (
+        "E", "R", "S", "P", "F", "N", "sched", "comb", "eesm", "harq_drop", "olla", "phr_cap", "retx_prio", "rician",
+        "fading", "purge", "input_kind", "radio_model", "out_ref", "max_tx", "sr_delay", "ul_rtt", "rlc_retx",
+        "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "pad0")] + \
+               [(n, f32) for n in (
+        "olla_up", "olla_dn", "pf_a", "pf_b", "target", "phr_min", "snr_ref_prbs", "w0", "ref_off", "noise_prb",
+        "ue_tx", "subband_noise", "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1",
+        "nl_b0", "nl_c", "nl_d", "sig", "amp", "pl_const", "pl_exp10", "proc_off_hi", "proc_off_lo")]
+
+
+class InetNrOutputs(C.Structure):
+    _fields_ = [(n, P) for n in ("delivered", "timed_out", "dropped", "cap", "cls", "cap32", "cls8", "delay",
+                                 "newest", "queue_len", "serving_cell", "queue_bytes", "sinr_db", "det_env", "t")]
+
+
+ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fade", "salt_bler")   # 8 x 4 bytes
+ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
+          -3: "HIP launch failed"}
+
+_LIB = None
+
+
+def load(path=LIB_PATH):
+    """Load the library (built in-tree by build.py); raises if it is missing: there is no CPU fallback."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with `python isaac-net_amd/build.py` (hipcc, gfx950)")
+    lib = C.CDLL(path)
+    lib.inet_nr_abi_version.restype = i32
+    lib.inet_nr_build_info.restype = C.c_char_p
+    lib.inet_nr_step.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrTables), C.POINTER(InetNrParams), P, i32,
+                                 i64, P, P, C.POINTER(InetNrOutputs), P]
+    lib.inet_nr_step.restype = i32
+    lib.inet_nr_submit.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), i64, P, P, P, P, i32, P, i32, i32,
+                                   i32, P, P]
+    lib.inet_nr_submit.restype = i32
+    lib.inet_nr_reset.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), P, i64, f32, C.POINTER(f32), i32,
+                                  P]
+    lib.inet_nr_reset.restype = i32
+    if lib.inet_nr_abi_version() != 1:
+        raise RuntimeError("libinet_nr.so ABI version mismatch; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: {ERRORS.get(rc, rc)}")

@@ -1,0 +1,621 @@
+"""make_engine / HipNREngine: the contract API of isaac-net's NR engine over the HIP kernels of libinet_nr.so.
+
+Mirrors isaac_net/core/engine.py (make_engine :230-316, NREngine :319-960) for level "L2" with backend="hip":
+reset(env_ids) / submit(t, requests) / step(t, poses_or_snr) -> dict / clock / output_schema / counters, with the same
+inputs, output keys, dtypes and shapes, the same per-env clock rules (t=None uses the engine clock; an explicit t must
+equal it) and the same error behaviour for inputs the engine cannot take. What the kernels do not implement is refused
+at construction with HipUnsupported (a NotImplementedError and a ValueError, like the reference's TritonUnsupported,
+nr_fast.py:104-111, 538-563).
+
+All per-env state lives in device tensors that torch allocates; every call hands the library plain pointers. The host
+keeps only the control-step counter T, the per-env epoch used by `clock`, and the slot of the last fading update.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from .config import NRConfig
+from .phy import PhyTables
+
+BIG_SLOT = 0x7FFFFFFF
+FADING, BLER_UL = 1, 2
+NCTR = 12
+CTR_NAMES = ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
+             "new_while_pending", "prb_used")
+
+
+class HipUnsupported(NotImplementedError, ValueError):
+    """A config feature the HIP backend does not implement (refused before anything is built)."""
+
+
+@dataclass
+class Requests:
+    """Messages each robot enqueues in one control step (isaac_net/core/proto/netsim.py:163-172).
+    send [E,R] long (0 = none, c >= 1 = one message of class c), det [E,R] bool, hid [E] long (optional)."""
+    send: torch.Tensor
+    det: Optional[torch.Tensor] = None
+    hid: Optional[torch.Tensor] = None
+
+
+# ---------------------------------------------------------------------------------------------- counter hash (host)
+M32 = 0xFFFFFFFF
+
+
+def mix32(x):
+    x ^= x >> 16
+    x = (x * 0x21F0AAAD) & M32
+    x ^= x >> 15
+    x = (x * 0x735A2D97) & M32
+    return x ^ (x >> 15)
+
+
+def salt(v):
+    return (mix32(v & M32) + 0x9E3779B9) & M32
+
+
+def seed_key(seed):
+    return mix32(mix32(seed & M32) ^ salt((seed >> 32) & M32))
+
+
+def refusals(cfg: NRConfig):
+    """[(feature, why)] of the config's features the HIP step kernel does not implement (empty: it runs)."""
+    out = []
+
+    def no(cond, what, why):
+        if cond:
+            out.append((what, why))
+    no(cfg.n_cells != 1, "several cells (n_cells > 1)", "one cell's scheduler and HARQ per env")
+    no(cfg.dl or not cfg.ul, "the downlink (dl=True) or ul=False", "uplink engine")
+    no(cfg.ul_grant_model != "lumped", "ul_grant_model='bsr'", "lumped SR grants only")
+    no(cfg.n_layers_max != 1, "rank-2 MIMO", "single-layer TBs")
+    no(cfg.ul_mini_slot_symbols is not None, "mini-slot grants", "one scheduling occasion per slot")
+    no(cfg.scheduler not in ("pf", "maxci", "rr"), f"scheduler={cfg.scheduler!r}", "pf, maxci and rr")
+    no(cfg.pf_metric != "subband", "pf_metric='wideband'", "per-RBG PF metric")
+    no(cfg.pf_update != "slot" or cfg.pf_avg_idle != "decay", "pf_update / pf_avg_idle switches", "slot EWMA")
+    no(cfg.ul_retx_sched != "ofdma" or cfg.ul_amc_alloc != "current", "ul_retx_sched / ul_amc_alloc switches",
+       "OFDMA retransmissions, current-allocation AMC")
+    no(cfg.ul_pc_on or cfg.ul_tpc, "UL power control (ul_pc / ul_tpc)", "full-power PSD split")
+    no(cfg.ul_power != "allocated", "ul_power='whole_band'", "allocated power split")
+    no(cfg.rician_mode == "los", "Rician K from the LOS state", "fixed rician_k_db or Rayleigh")
+    no(cfg.fading_freq_corr or cfg.fading_doppler != "global", "frequency-correlated / per-robot Doppler fading",
+       "i.i.d. subbands, one rho")
+    no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
+    no(cfg.rach or cfg.drx, "RACH / DRX access", "always connected")
+    no(cfg.tbs_mode != "38214" or cfg.bler_source != "pdsch", "tbs_mode / bler_source", "38.214 TBS, Sionna PDSCH")
+    no(cfg.rng != "engine", "rng='global'", "counter-based engine RNG")
+    no(cfg.edge is not None or cfg.background is not None or cfg.energy is not None, "edge / background / energy",
+       "no wrapper stages")
+    no(cfg.blockage or cfg.los_source != "stochastic" or cfg.gnb_antenna != "isotropic" or cfg.o2i_indoor_frac > 0
+       or cfg.shadow_white_frac > 0, "obstacle stack, sector antennas, O2I or white shadowing",
+       "plain path loss + plane-wave shadowing")
+    no(cfg.channel not in ("log_distance", "tr38901"), f"channel={cfg.channel!r}", "log_distance and tr38901")
+    if cfg.channel == "tr38901":
+        no(cfg.tr38901_los not in ("los", "nlos"), "tr38901_los='stochastic'", "a fixed LOS state (los / nlos)")
+        no(cfg.tr38901_scenario == "RMa", "the RMa scenario", "UMa, UMi, InH, InF")
+        no(cfg.tr38901_scenario.startswith("InF") and cfg.tr38901_los == "nlos", "InF NLOS", "InF LOS")
+    no(cfg.n_subbands not in (8, 13), f"{cfg.n_subbands} subbands", "8 or 13 RBGs in this build")
+    no(cfg.n_harq not in (2, 4, 8, 16), f"n_harq={cfg.n_harq}", "2, 4, 8 or 16 HARQ processes in this build")
+    no(cfg.max_harq_tx > 16, "max_harq_tx > 16", "up to 16 transmissions")
+    no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
+    no(cfg.frame_buffer > 255, "frame_buffer > 255", "8-bit class field, int32 offsets")
+    no(len(cfg.msg_sizes) > 255, "more than 255 message classes", "8-bit class field")
+    return out
+
+
+class HipNREngine:
+    """NR engine (level "L2", one cell, uplink) on MI355X. API of isaac_net.core.engine.NREngine."""
+
+    level = "L2"
+    backend = "hip"
+
+    def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, out_format="reference"):
+        cfg = cfg if cfg is not None else NRConfig()
+        no = refusals(cfg)
+        if no:
+            raise HipUnsupported("the hip backend of the NR engine does not implement "
+                                 + "; ".join(f"{f} ({why})" for f, why in no))
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("the hip backend needs a GPU device (cuda:N on ROCm)")
+        if not 1 <= R <= 64:
+            raise HipUnsupported(f"R={R}: the hip backend holds one env's robots in one 64-lane wavefront segment "
+                                 "(1 <= R <= 64)")
+        self._lib = _lib.load()
+        self.E, self.R, self.dev, self.config = E, R, dev, cfg
+        if seed is None:
+            seed = cfg.seed if cfg.seed is not None else int(torch.randint(0, 2 ** 62, ()).item())
+        self.seed = int(seed)
+        self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
+        self.N = cfg.slots_per_step
+        self.out_format = out_format
+        self.tabs = PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2), cfg.ul_mcs_max)
+        self._alloc_state()
+        self._upload_tables()
+        self._build_params()
+        self.T = 0
+        self._uniform_epoch = 0
+        self.last_g = None
+        self._last_hid = torch.zeros(E, dtype=torch.long, device=dev)
+        self._rows = {}
+        self.reset(None)
+
+    # ------------------------------------------------------------------ buffers
+    def _alloc_state(self):
+        E, R, S, P, F, d = self.E, self.R, self.S, self.P, self.F, self.dev
+        i32, f32 = torch.int32, torch.float32
+        z = lambda *shape, dt=i32, v=0: torch.full(shape, v, dtype=dt, device=d)  # noqa: E731
+        cfg = self.config
+        nf = 0 if cfg.channel not in ("log_distance", "tr38901") else (3 if cfg.channel == "tr38901" else 1)
+        self.st = {
+            "sent": z(E, R), "floor_": z(E, R), "bsr": z(E, R), "sr_t": z(E, R, v=-1), "last_tx": z(E, R, v=-1),
+            "olla": z(E, R, dt=f32), "avg": z(E, R, dt=f32, v=100.0), "enq": z(E, R), "qlen": z(E, R),
+            "csi": z(E, S, R, dt=f32), "h_re": z(E, S, R, dt=f32), "h_im": z(E, S, R, dt=f32),
+            "h_meta": z(E, P, R), "h_lo": z(E, P, R), "h_hi": z(E, P, R), "h_ready": z(E, P, R), "h_tbs": z(E, P, R),
+            "h_comb": z(E, P, R, dt=f32), "h_lexp": z(E, P, R, dt=f32, v=-math.inf), "h_nrb": z(E, P, R, dt=f32),
+            "q_cap": z(E, F, R, v=-1), "q_start": z(E, F, R), "q_end": z(E, F, R), "q_fin": z(E, F, R, v=BIG_SLOT),
+            "q_meta": z(E, F, R), "q_hid": z(E, F, R),
+            "spec_re": z(E, R, dt=f32), "spec_im": z(E, R, dt=f32), "k_lin": z(E, R, dt=f32),
+            "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
+            "ctr_submit": z(E), "epoch": z(E),
+            "field": z(E, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
+            "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
+        }
+        self._n_fields = nf
+        self._last_snr = torch.zeros(E, R, device=d)
+        s = _lib.InetNrState()
+        for name, _ in _lib.InetNrState._fields_:
+            setattr(s, name, self.st[name].data_ptr())
+        self._cstate = s
+
+    def _upload_tables(self):
+        cfg, t, d = self.config, self.tabs, self.dev
+        nsyms = sorted({cfg.slot_symbols(p)[1] for p in range(len(cfg.tdd_pattern))} - {0}) or [cfg.ul_data_symbols]
+        self._nsym_idx = {ns: i for i, ns in enumerate(nsyms)}
+        la = [t.la_tables(cfg.nprb, ns, cfg.dmrs_re_per_prb, cfg.overhead_re_per_prb) for ns in nsyms]
+        w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
+        host = {
+            "bler": torch.from_numpy(t.bler.reshape(-1)), "thr_ref": torch.from_numpy(t.thr_ref),
+            "se": torch.from_numpy(t.se), "beta": torch.from_numpy(t.beta), "rate": torch.from_numpy(t.r),
+            "mcs_eq": torch.from_numpy(t.mcs_eq.astype(np.int32)).reshape(-1),
+            "la_tbs": torch.from_numpy(np.stack([x[0] for x in la])).reshape(-1),
+            "la_ci0": torch.from_numpy(np.stack([x[1] for x in la]).astype(np.int32)).reshape(-1),
+            "la_cwi": torch.from_numpy(np.stack([x[2] for x in la])).reshape(-1),
+            "la_ncb": torch.from_numpy(np.stack([x[3] for x in la])).reshape(-1),
+            "w": w, "logw": torch.log(w.float()), "wdb": 10 * torch.log10(w / cfg.snr_ref_prbs),
+        }
+        self.tab = {k: v.contiguous().to(d) for k, v in host.items()}
+        c = _lib.InetNrTables()
+        for k, v in self.tab.items():
+            setattr(c, k, v.data_ptr())
+        c.s0, c.ds, c.c0, c.dc = t.s0, t.ds, t.c0, t.dc
+        c.M, c.C, c.G, c.NPRB, c.EQW, c.mcs_max = t.M, t.C, t.G, cfg.nprb, t.mcs_eq.shape[1], t.mcs_max
+        c.thr_monotone = int(bool(np.all(np.diff(t.thr_ref[:t.mcs_max + 1]) >= 0)))
+        self._ctab = c
+        self._sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32, device=d)
+
+    def _build_params(self):
+        from .channels import SCENARIOS, SIGMA_SF, breakpoint_m
+        cfg = self.config
+        p = _lib.InetNrParams()
+        p.E, p.R, p.S, p.P, p.F, p.N = self.E, self.R, self.S, self.P, self.F, self.N
+        p.sched = {"pf": 0, "maxci": 1, "rr": 2}[cfg.scheduler]
+        p.comb = {"none": 0, "cc": 1, "ir_lena": 2}[cfg.harq_combining]
+        p.eesm = int(cfg.eff_sinr == "eesm")
+        p.harq_drop = int(cfg.harq_fail == "drop")
+        p.olla, p.phr_cap, p.retx_prio = int(cfg.olla), int(cfg.phr_cap), int(cfg.retx_priority)
+        p.rician, p.fading = int(cfg.rician_mode == "fixed"), int(cfg.fading)
+        p.purge = int(cfg.discard == "purge")
+        p.out_ref = int(self.out_format == "reference")
+        p.max_tx, p.sr_delay, p.ul_rtt, p.rlc_retx = cfg.max_harq_tx, cfg.sr_delay, cfg.ul_rtt, cfg.rlc_retx_slots
+        p.timeout, p.tb_oh = cfg.timeout_steps, cfg.tb_overhead_bytes
+        p.n_fields, p.n_modes = self._n_fields, cfg.shadow_modes
+        p.seed_key = C.c_int32(seed_key(self.seed) - (1 << 32) if seed_key(self.seed) >= 1 << 31
+                               else seed_key(self.seed)).value
+        p.olla_up = cfg.olla_up_db
+        p.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
+        p.pf_a, p.pf_b = 1 - 1 / cfg.pf_window, 1 / cfg.pf_window
+        p.target, p.phr_min, p.snr_ref_prbs = cfg.bler_target, cfg.phr_min_db, float(cfg.snr_ref_prbs)
+        p.w0 = float(cfg.subband_prbs[0])
+        p.ref_off = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs)
+        p.noise_prb, p.ue_tx, p.subband_noise = cfg.noise_dbm_per_prb("gnb"), cfg.ue_tx_dbm, cfg.subband_noise_dbm
+        gx, gy = cfg.gnb_xy()[0]
+        p.gnb_x, p.gnb_y = gx, gy
+        po = cfg.proc_offset_ms / cfg.control_step_ms
+        p.proc_off_hi = po
+        p.proc_off_lo = po - float(np.float32(po))
+        K = cfg.shadow_modes
+        self._spectrum, self._dcorr = 0, (cfg.shadow_dcorr_m, 0.0, 0.0)
+        if cfg.channel == "tr38901":
+            sc = SCENARIOS[cfg.tr38901_scenario]
+            scn = cfg.tr38901_scenario
+            h_bs = float(cfg.gnb_height_m) if cfg.gnb_height_m is not None else sc.h_bs
+            h_ut, fc = float(cfg.ue_height_m), cfg.carrier_ghz
+            dbp = breakpoint_m(scn, fc, h_bs, h_ut)
+            p.radio_model = 1
+            p.hh2 = (h_bs - h_ut) ** 2
+            p.dbp = dbp if math.isfinite(dbp) else float("inf")
+            if scn in ("UMa", "UMi"):
+                a, n1, b = (28.0, 22.0, 9.0) if scn == "UMa" else (32.4, 21.0, 9.5)
+                p.pl_a, p.pl_n1, p.pl_c20 = a, n1, 20 * math.log10(fc)
+                p.pl_c2 = b * math.log10(dbp ** 2 + (h_bs - h_ut) ** 2)
+            elif scn == "InH":
+                p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 32.4, 17.3, 20 * math.log10(fc), 0.0
+            else:                                                   # InF (LOS)
+                p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 31.84, 21.50, 19.00 * math.log10(fc), 0.0
+            los = cfg.tr38901_los == "los"
+            if not los:
+                if scn == "UMi":
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 35.3, 22.4, 21.3 * math.log10(fc), 0.3 * (h_ut - 1.5)
+                elif scn == "UMa":
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 39.08, 13.54, 20 * math.log10(fc), 0.6 * (h_ut - 1.5)
+                else:                                               # InH
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 38.3, 17.30, 24.9 * math.log10(fc), 0.0
+            p.sig = SIGMA_SF[scn][0 if los else 1]
+            p.amp = 1.0 * math.sqrt(2 / K)
+            self._spectrum, self._dcorr = 1, (sc.sf_corr_los_m, sc.sf_corr_nlos_m, sc.los_corr_m)
+        else:
+            p.radio_model = 0
+            p.amp = cfg.shadow_sigma_db * math.sqrt(2 / K)
+            p.pl_const, p.pl_exp10 = cfg.pl_const_db, 10 * cfg.pathloss_exp
+            self._spectrum = 0 if cfg.shadow_acf == "sos" else 1
+        self._cparams = p
+        self._dcorr_c = (C.c_float * 3)(*self._dcorr)
+
+    # ------------------------------------------------------------------ schedule rows (nr_engine.py:506-523)
+    def _rows_for(self, g0, dt0):
+        cfg = self.config
+        P_ = len(cfg.tdd_pattern)
+        key = (g0 % math.lcm(P_, cfg.sr_period_slots, cfg.cqi_period_slots), dt0)
+        hit = self._rows.get(key)
+        if hit is not None:
+            return hit
+        sched = cfg.schedule(g0)
+        pg_pos = next(p for p in range(P_) if cfg.slot_symbols(p)[1] > 0)
+        rows, prev = [], None
+        evol, rhos = [], []
+        for rel, uls, sr in sched:
+            dt = dt0 if prev is None else rel - prev
+            prev = rel
+            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
+            evol.append(cfg.fading and dt > 0)
+            rhos.append(float(np.float32(rho)))
+        n = len(sched)
+        for k, (rel, uls, sr) in enumerate(sched):
+            dt = dt0 if k == 0 else rel - sched[k - 1][0]
+            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
+            c1 = math.sqrt(1 - rho ** 2)
+            need_h = evol[k] and (uls > 0 or k == n - 1 or not (evol[k + 1] and rhos[k + 1] == 0.0))
+            pg = cfg.proactive_grant == "every_ul_slot" or (cfg.proactive_grant == "per_period"
+                                                            and (g0 + rel) % P_ == pg_pos)
+            flags = (1 if sr else 0) | (2 if uls else 0) | (4 if evol[k] else 0) | (8 if need_h else 0) | \
+                (16 if pg else 0)
+            re = float(min(12 * uls - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156)) if uls else 0.0
+            rows.append((rel, self._nsym_idx.get(uls, -1), flags, re, rho, c1, salt((FADING << 16) | rel),
+                         salt((BLER_UL << 16) | rel)))
+        if sum(1 for r in rows if r[2] & 2) > 64:
+            raise HipUnsupported("more than 64 UL data slots per control step")
+        buf = np.zeros((max(n, 1), 8), dtype=np.int32)
+        for k, r in enumerate(rows):
+            buf[k, 0:3] = r[0:3]
+            buf[k, 3:6] = np.array(r[3:6], dtype=np.float32).view(np.int32)
+            buf[k, 6:8] = np.array(r[6:8], dtype=np.uint32).view(np.int32)
+        dev_rows = torch.from_numpy(buf).to(self.dev)
+        res = (dev_rows, n, sched[-1][0] if sched else None, sum(1 for r in rows if r[2] & 2))
+        self._rows[key] = res
+        return res
+
+    # ------------------------------------------------------------------ contract API
+    @property
+    def clock(self):
+        return self.T - self.st["epoch"].long()
+
+    def output_schema(self):
+        keys = [("newest", "[E,R]", "int64"), ("det_env", "[E]", "bool"), ("delivered", "[E,R,F]", "bool"),
+                ("timed_out", "[E,R,F]", "bool"), ("dropped", "[E,R,F]", "bool"), ("cap", "[E,R,F]", "int64"),
+                ("cls", "[E,R,F]", "int64"), ("delay", "[E,R,F]", "float32"), ("queue_len", "[E,R]", "int64"),
+                ("queue_bytes", "[E,R]", "float32"), ("sinr_db", "[E,R]", "float32"),
+                ("serving_cell", "[E,R]", "int64"), ("t", "[E]", "int64")]
+        return {k: {"shape": s, "dtype": dt, "when": "always"} for k, s, dt in keys}
+
+    def _now(self, t):
+        """engine.py:738-755."""
+        if t is None:
+            return self.T
+        if isinstance(t, torch.Tensor):
+            if t.dim() == 0:
+                t = int(t)
+            else:
+                if not torch.equal(t.to(self.dev, torch.long), self.clock):
+                    raise ValueError("t must equal the engine clock (the NR engine cannot jump in time); pass t=None")
+                return self.T
+        t = int(t)
+        if self._uniform_epoch is None:
+            raise ValueError("after a partial reset the envs have different clocks: pass t=None")
+        if t + self._uniform_epoch != self.T:
+            raise ValueError(f"t={t} but the engine clock is {self.T - self._uniform_epoch}: the NR engine cannot "
+                             "jump in time; pass t=None")
+        return self.T
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.dev).cuda_stream
+
+    def reset(self, env_ids=None):
+        """Re-initialize env_ids (None = all; index tensor, list or bool mask [E])."""
+        if env_ids is not None and isinstance(env_ids, slice) and env_ids == slice(None):
+            env_ids = None
+        lib = self._lib
+        if env_ids is None:
+            self.T = 0
+            self._ul_slots_run = 0
+            self._uniform_epoch = 0
+            self.last_g = None
+            self._last_snr = torch.zeros_like(self._last_snr)
+            self._last_hid = torch.zeros_like(self._last_hid)
+            _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), None, 0,
+                                         self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+            return
+        if isinstance(env_ids, torch.Tensor) and env_ids.dtype == torch.bool:
+            mask = env_ids.to(self.dev)
+        else:
+            ids = torch.as_tensor(env_ids if isinstance(env_ids, torch.Tensor) else list(env_ids), dtype=torch.long,
+                                  device=self.dev).reshape(-1)
+            if ids.numel() == 0:
+                return
+            mask = torch.zeros(self.E, dtype=torch.bool, device=self.dev)
+            mask[ids] = True
+        if not bool(mask.any()):
+            return
+        m8 = mask.to(torch.uint8).contiguous()
+        _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), m8.data_ptr(), self.T,
+                                     self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+        self._uniform_epoch = None
+        mk = mask[:, None]
+        self._last_snr = torch.where(mk, torch.zeros_like(self._last_snr), self._last_snr)
+        self._last_hid = torch.where(mask, torch.zeros_like(self._last_hid), self._last_hid)
+
+    def _k_lin0(self):
+        cfg = self.config
+        return float(10 ** (cfg.rician_k_db / 10)) if cfg.rician_mode == "fixed" else 0.0
+
+    def submit(self, t, requests, snr_db=None, *, tag=None, priority=None, deadline_ms=None):
+        """Enqueue one message per robot (Requests or send [E,R]); returns accepted [E,R] bool (engine.py:796-819)."""
+        if tag is not None or priority is not None or deadline_ms is not None:
+            raise HipUnsupported("per-message extras (tag / priority / deadline_ms) are not implemented")
+        T = self._now(t)
+        req = requests if isinstance(requests, Requests) or hasattr(requests, "send") else Requests(send=requests)
+        send = req.send.to(self.dev, torch.long).contiguous()
+        if tuple(send.shape) != (self.E, self.R):
+            raise ValueError(f"send must be [E,R] = [{self.E},{self.R}], got {tuple(send.shape)}")
+        det = None if req.det is None else req.det.to(self.dev, torch.uint8).contiguous()
+        hid = torch.zeros(self.E, dtype=torch.long, device=self.dev) if req.hid is None else \
+            req.hid.to(self.dev, torch.long).contiguous()
+        self._last_hid = hid.clone()
+        acc = torch.empty(self.E, self.R, dtype=torch.bool, device=self.dev)
+        cfg = self.config
+        _lib.check(self._lib.inet_nr_submit(
+            C.byref(self._cstate), C.byref(self._cparams), T, send.data_ptr(), None if det is None else det.data_ptr(),
+            hid.data_ptr(), None, 0, self._sizes.data_ptr(), int(cfg.discard == "pdcp_arrival"),
+            cfg.pkt_payload_bytes, cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "submit")
+        return acc
+
+    def submit_counts(self, counts, t=None):
+        """Enqueue counts [E,R,NC] messages per class in one launch: equivalent to the submit() calls of class 1
+        first, one call per message index. Returns accepted messages [E,R] int32."""
+        T = self._now(t)
+        cnt = counts.to(self.dev, torch.uint8).contiguous()
+        nc = cnt.shape[-1]
+        if tuple(cnt.shape[:2]) != (self.E, self.R) or nc > len(self.config.msg_sizes):
+            raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        self._last_hid = torch.zeros_like(self._last_hid)
+        acc = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
+        cfg = self.config
+        _lib.check(self._lib.inet_nr_submit(
+            C.byref(self._cstate), C.byref(self._cparams), T, None, None, None, cnt.data_ptr(), nc,
+            self._sizes.data_ptr(), int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
+            cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "submit")
+        return acc
+
+    def add_frames(self, t, send, det, hid, snr_db=None):
+        """Legacy wrapper (NetSlot API)."""
+        self.submit(t, Requests(send, det, hid), snr_db)
+
+    def _alloc_out(self):
+        E, R, F, d = self.E, self.R, self.F, self.dev
+        e = lambda *s, dt: torch.empty(*s, dtype=dt, device=d)  # noqa: E731
+        if self.out_format == "reference":
+            o = {"newest": e(E, R, dt=torch.int64), "det_env": e(E, dt=torch.bool),
+                 "delivered": e(E, R, F, dt=torch.bool), "timed_out": e(E, R, F, dt=torch.bool),
+                 "dropped": e(E, R, F, dt=torch.bool), "cap": e(E, R, F, dt=torch.int64),
+                 "cls": e(E, R, F, dt=torch.int64), "delay": e(E, R, F, dt=torch.float32),
+                 "queue_len": e(E, R, dt=torch.int64), "queue_bytes": e(E, R, dt=torch.float32),
+                 "sinr_db": e(E, R, dt=torch.float32), "serving_cell": e(E, R, dt=torch.int64),
+                 "t": e(E, dt=torch.int64)}
+        else:
+            o = {"newest": e(E, R, dt=torch.int64), "det_env": e(E, dt=torch.bool), "flags": e(E, R, F, dt=torch.uint8),
+                 "cap32": e(E, R, F, dt=torch.int32), "cls8": e(E, R, F, dt=torch.uint8),
+                 "delay": e(E, R, F, dt=torch.float32), "queue_len": e(E, R, dt=torch.int64),
+                 "queue_bytes": e(E, R, dt=torch.float32), "sinr_db": e(E, R, dt=torch.float32),
+                 "t": e(E, dt=torch.int64)}
+        c = _lib.InetNrOutputs()
+        ptr = lambda k: o[k].data_ptr() if k in o else None  # noqa: E731
+        c.delivered = ptr("delivered") or ptr("flags")
+        c.timed_out, c.dropped, c.cap, c.cls = ptr("timed_out"), ptr("dropped"), ptr("cap"), ptr("cls")
+        c.cap32, c.cls8, c.delay = ptr("cap32"), ptr("cls8"), ptr("delay")
+        c.newest, c.queue_len, c.serving_cell = ptr("newest"), ptr("queue_len"), ptr("serving_cell")
+        c.queue_bytes, c.sinr_db, c.det_env, c.t = ptr("queue_bytes"), ptr("sinr_db"), ptr("det_env"), ptr("t")
+        return o, c
+
+    def step(self, t=None, x=None, cur_hid=None, *, snr_db=None, dl_snr_db=None, pathgain_db=None, vel=None,
+             triggers=None, blockers=None):
+        """Advance [t, t+1). x: poses [E,R,2|3] (through the radio) or SNR [E,R] dB; snr_db=: [E,R,S] or [E,R].
+        Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env)."""
+        if dl_snr_db is not None or pathgain_db is not None or vel is not None or triggers is not None or \
+                blockers is not None:
+            raise HipUnsupported("dl_snr_db / pathgain_db / vel / triggers / blockers need features the hip backend "
+                                 "does not implement (downlink, several cells, per-robot Doppler, traffic models, "
+                                 "blockage)")
+        T = self._now(t)
+        legacy = cur_hid is not None
+        hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
+        cfg, E, R, S = self.config, self.E, self.R, self.S
+        if snr_db is None:
+            if x is None:
+                raise ValueError("step needs poses [E,R,2|3] or an SNR [E,R]")
+            if x.dim() == 3:
+                kind, xin = 0, x[..., :2].to(self.dev, torch.float32).contiguous()
+            else:
+                kind, xin = 1, x.to(self.dev, torch.float32).contiguous()
+        else:
+            xin = snr_db.to(self.dev, torch.float32).contiguous()
+            kind = 2 if xin.dim() == 3 else 1
+        want = {0: (E, R, 2), 1: (E, R), 2: (E, R, S)}[kind]
+        if tuple(xin.shape) != want:
+            raise ValueError(f"input must have shape {want}, got {tuple(xin.shape)}")
+        self._cparams.input_kind = kind
+        N = self.N
+        g0 = T * N
+        sched = cfg.schedule(g0)
+        fad = cfg.fading and len(sched) > 0
+        dt0 = (1 if self.last_g is None else g0 + sched[0][0] - self.last_g) if fad else 0
+        rows, n_rows, last_rel, n_ul = self._rows_for(g0, dt0)
+        o, co = self._alloc_out()
+        _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
+                                          rows.data_ptr(), n_rows, T, xin.data_ptr(), hid.data_ptr(), C.byref(co),
+                                          self._stream()), "step")
+        if fad:
+            self.last_g = g0 + last_rel
+        self._ul_slots_run += n_ul
+        self.T = T + 1
+        self._last_snr = o["sinr_db"]
+        if legacy:
+            return o["newest"], o["det_env"]
+        return o
+
+    # ------------------------------------------------------------------ statistics
+    def counters(self):
+        """{"ul": {counter: value, ntx_hist, rv_tx, rv_fail}} since the last full reset (NRNet.counters)."""
+        c = self.st["ctr"].sum(0).tolist()
+        h = self.st["hist"]
+        cfg = self.config
+        res = {k: float(c[i]) for i, k in enumerate(CTR_NAMES)}
+        res["ntx_hist"] = h[:, 0].sum(0).double().tolist()
+        res["rv_tx"] = h[:, 1].sum(0).double().tolist()
+        res["rv_fail"] = h[:, 2].sum(0).double().tolist()
+        res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * self._ul_slots_run
+        return {"ul": res}
+
+    _ul_slots_run = 0
+
+    # ------------------------------------------------------------------ state in the reference's layout
+    def state_dict(self):
+        """Every state tensor in the reference's names, shapes and dtypes (isaac_net/core/nr_fast.py:41-75), on the
+        engine's device. Frame fields of empty queue slots are unspecified (the reference leaves stale values)."""
+        st, cfg, N = self.st, self.config, self.N
+        L = lambda x: x.long()  # noqa: E731
+        rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
+        meta = st["h_meta"]
+        po = cfg.proc_offset_ms / cfg.control_step_ms
+        fin_slot = st["q_fin"].long()
+        tf = torch.div(fin_slot, N, rounding_mode="floor")
+        fin = (tf.double() + (fin_slot - tf * N + 1).double() / N) + po
+        fin = torch.where(fin_slot == BIG_SLOT, torch.full_like(fin, math.inf), fin)
+        qm = st["q_meta"]
+        out = {
+            "ul.sent": L(st["sent"]), "ul.floor": L(st["floor_"]), "ul.olla": st["olla"], "ul.avg": st["avg"],
+            "ul.bsr": L(st["bsr"]), "ul.sr_t": L(st["sr_t"]), "ul.csi": rs(st["csi"]),
+            "ul.h_state": rs(L(meta & 0xFF)), "ul.h_ntx": rs(L((meta >> 8) & 0xFF)),
+            "ul.h_mcs": rs(L((meta >> 16) & 0xFF)), "ul.h_nsb": rs(L((meta >> 24) & 0xFF)),
+            "ul.h_lo": rs(L(st["h_lo"])), "ul.h_hi": rs(L(st["h_hi"])), "ul.h_ready": rs(L(st["h_ready"])),
+            "ul.h_tbs": rs(L(st["h_tbs"])), "ul.h_comb": rs(st["h_comb"]), "ul.h_lexp": rs(st["h_lexp"]),
+            "ul.h_nrb": rs(st["h_nrb"]), "ul.last_tx": L(st["last_tx"]),
+            "ul.q.cap": rs(L(st["q_cap"])), "ul.q.start": rs(L(st["q_start"])), "ul.q.end": rs(L(st["q_end"])),
+            "ul.q.lost": rs((qm & 1) != 0), "ul.q.fin": rs(fin), "ul.q.cls": rs(L((qm >> 8) & 0xFF)),
+            "ul.q.det": rs((qm & 2) != 0), "ul.q.hid": rs(L(st["q_hid"])), "ul.q.enq": L(st["enq"]),
+            "net.h": torch.stack([rs(st["h_re"]), rs(st["h_im"])], -1), "eng.epoch": L(st["epoch"]),
+            "eng._last_snr": self._last_snr, "eng._last_hid": self._last_hid,
+            "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"]),
+        }
+        if cfg.rician_mode == "fixed":
+            k = st["k_lin"]
+            out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1), "net.k_los": k, "net.k_in": k,
+                        "net.k_lin": k, "net.k_from": k, "net.k_g0": torch.zeros_like(L(st["epoch"]))[:, None]
+                        .expand(-1, self.R)})
+        return out
+
+    def load_state_dict(self, sd, T=None, last_g=None):
+        """Load reference-layout state (the keys of state_dict(); tensors on any device) into the device buffers;
+        T / last_g set the host clock and the last fading slot (teacher forcing)."""
+        st, cfg, N, d = self.st, self.config, self.N, self.dev
+        g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+        rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
+        I = lambda x: x.to(torch.int32)  # noqa: E731
+        for a, b in (("sent", "ul.sent"), ("floor_", "ul.floor"), ("bsr", "ul.bsr"), ("sr_t", "ul.sr_t"),
+                     ("last_tx", "ul.last_tx"), ("enq", "ul.q.enq")):
+            st[a].copy_(I(g(b)))
+        st["olla"].copy_(g("ul.olla"))
+        st["avg"].copy_(g("ul.avg"))
+        st["csi"].copy_(rs(g("ul.csi")))
+        meta = (g("ul.h_state") | (g("ul.h_ntx") << 8) | (g("ul.h_mcs") << 16) | (g("ul.h_nsb") << 24))
+        st["h_meta"].copy_(rs(I(meta)))
+        for a in ("h_lo", "h_hi", "h_ready", "h_tbs"):
+            st[a].copy_(rs(I(g("ul." + a))))
+        for a in ("h_comb", "h_lexp", "h_nrb"):
+            st[a].copy_(rs(g("ul." + a).float()))
+        cap = g("ul.q.cap")
+        valid = cap >= 0
+        st["qlen"].copy_(I(valid.sum(-1)))
+        st["q_cap"].copy_(rs(I(torch.where(valid, cap, torch.full_like(cap, -1)))))
+        st["q_start"].copy_(rs(I(g("ul.q.start"))))
+        st["q_end"].copy_(rs(I(g("ul.q.end"))))
+        po = cfg.proc_offset_ms / cfg.control_step_ms
+        fin = g("ul.q.fin").double()
+        slot = torch.round((fin - po) * N).long() - 1
+        slot = torch.where(torch.isinf(fin) | ~valid, torch.full_like(slot, BIG_SLOT), slot)
+        st["q_fin"].copy_(rs(I(slot)))
+        qm = g("ul.q.lost").long() | (g("ul.q.det").long() << 1) | (g("ul.q.cls").long() << 8)
+        st["q_meta"].copy_(rs(I(qm)))
+        st["q_hid"].copy_(rs(I(g("ul.q.hid"))))
+        h = g("net.h")
+        st["h_re"].copy_(rs(h[..., 0]))
+        st["h_im"].copy_(rs(h[..., 1]))
+        st["epoch"].copy_(I(g("eng.epoch")))
+        st["episode"].copy_(I(g("rng.episode")))
+        st["ctr_submit"].copy_(I(g("rng.ctr[1]")))
+        st["ctr_step"].copy_(I(g("rng.ctr[2]")))
+        if cfg.rician_mode == "fixed":
+            sp = g("net.spec")
+            st["spec_re"].copy_(sp[..., 0])
+            st["spec_im"].copy_(sp[..., 1])
+            st["k_lin"].copy_(g("net.k_lin"))
+        self._last_snr = g("eng._last_snr").float().clone()
+        self._last_hid = g("eng._last_hid").long().clone()
+        if T is not None:
+            self.T = int(T)
+            ep = st["epoch"]
+            self._uniform_epoch = int(ep[0]) if bool((ep == ep[0]).all()) else None
+        self.last_g = last_g
+
+
+def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, backend="hip", *, sizes=None,
+                params=None, seed=None, inject=False, strict=False, out_format="reference"):
+    """Factory with the signature of isaac_net.core.engine.make_engine (engine.py:230-255) for level "L2" and
+    backend "hip" (also "auto", which resolves to "hip" on a GPU device)."""
+    if level != "L2":
+        raise HipUnsupported(f"level {level!r}: the hip backend implements the NR engine (level 'L2') only")
+    if backend not in ("hip", "auto"):
+        raise ValueError(f"unknown backend {backend!r} for this package; use 'hip'")
+    if inject:
+        raise HipUnsupported("inject=True (externally fed draws) is not implemented; the engine RNG is used")
+    cfg = config if config is not None else NRConfig()
+    if sizes is not None:
+        cfg = cfg.with_(msg_sizes=tuple(float(s) for s in sizes))
+    if seed is None:
+        seed = cfg.seed
+    return HipNREngine(E, R, device, cfg, seed=seed, out_format=out_format)

@@ -504,8 +504,16 @@ class OracleEngine:
         return self.T - self.epoch
 
     # ---------------- submit (engine.py:796-819, nr_engine.py:451-487, queues.py:87-103) ----------------
-    def submit(self, send, det=None, hid=None):
-        cfg, F, t = self.cfg, self.F, self.T
+    def submit(self, t, requests, det=None, hid=None):
+        """t: None (engine clock) or the clock value; requests: send [E,R] or an object with send / det / hid."""
+        cfg, F = self.cfg, self.F
+        if t is not None and int(t) + (self.uniform_epoch or 0) != self.T:
+            raise ValueError("t must equal the engine clock")
+        t = self.T
+        send = requests.send if hasattr(requests, "send") else requests
+        if hasattr(requests, "send"):
+            det = requests.det if requests.det is not None else det
+            hid = requests.hid if requests.hid is not None else hid
         det = torch.zeros_like(send, dtype=torch.bool) if det is None else det
         hid = torch.zeros(self.E, dtype=torch.long) if hid is None else hid
         self.last_hid = hid.clone()
@@ -534,7 +542,7 @@ class OracleEngine:
         return acc
 
     # ---------------- step (engine.py:867-960, nr_engine.py:613-668) ----------------
-    def step(self, x=None, snr_db=None):
+    def step(self, t=None, x=None, snr_db=None):
         cfg = self.cfg
         T = self.T
         hid = self.last_hid

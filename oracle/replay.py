@@ -34,11 +34,11 @@ def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)
         ids = np.nonzero(d["reset_mask"][s])[0]
         if len(ids):
             eng.reset(ids.tolist())
-        acc = [eng.submit(to(send)) for send in submits(d["counts"][s])]
+        acc = [eng.submit(None, to(send)) for send in submits(d["counts"][s])]
         x = to(d["x"][s])
         if kind == "snr3":
-            o = eng.step(snr_db=x)
+            o = eng.step(None, snr_db=x)
         else:
-            o = eng.step(x)
+            o = eng.step(None, x)
         if on_step is not None:
             on_step(s, o, acc)
