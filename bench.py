@@ -1,0 +1,174 @@
+"""Benchmark of the NR uplink engine hot path on one MI355X: robot-slots/s of the RL-scale workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--out-format reference|compact] [--no-cpu]
+
+A step is one control step of every env: submit_counts (this step's message arrivals, one launch) and step (poses in,
+the reference's output dict out: one launch of the fused step kernel). Inputs (poses and arrival counts of every
+step) are generated before the timed region and are resident in HBM. The timed region is K steps bracketed by
+torch.cuda.synchronize(); value = E * R * K_ul * K / seconds (robot-slots/s, K_ul = 10 UL slots per step).
+The step kernel's average duration is measured live with HIP events on the engine's stream; roofline.achieved is the
+kernel's algorithmic HBM bytes per launch (from the state layout and the measured queue occupancy) over that
+duration. The CPU baseline times the oracle (a torch-CPU restatement of the reference path) on the first envs of the
+same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "robot-slots/sec @4096 envs×32 robots K=10; achieved HBM GB/s vs peak"
+PEAK_GBS = 8000.0
+
+
+def load_package():
+    if "isaac_net_amd" in sys.modules:
+        return sys.modules["isaac_net_amd"]
+    d = os.path.join(ROOT, "isaac-net_amd")
+    spec = importlib.util.spec_from_file_location("isaac_net_amd", os.path.join(d, "__init__.py"),
+                                                  submodule_search_locations=[d])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["isaac_net_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def step_kernel_bytes(eng, qlen_mean, kept_mean):
+    """Algorithmic HBM bytes of one step-kernel launch for the engine's layout: every per-robot state word the
+    kernel must read and write, the queued frames it touches (qlen_mean read, kept_mean rewritten), inputs, outputs,
+    and the per-env words (RNG counters, epoch, shadowing field, counters) spread over the env's robots."""
+    cfg, E, R, S, P, F = eng.config, eng.E, eng.R, eng.S, eng.P, eng.F
+    p = eng._cparams
+    rd = 9 * 4 + S * 4 + P * 6 * 4 + 8                     # scalars, CSI, HARQ (meta lo hi ready tbs comb), pose
+    wr = 8 * 4 + S * 4 + P * 6 * 4
+    if cfg.fading:
+        wr += 2 * S * 4                                     # fading state written
+        if cfg.fading_rho_per_ms != 0.0:
+            rd += 2 * S * 4                                 # and read when it is correlated
+    if p.comb == 2:
+        rd += P * 8
+        wr += P * 8
+    if p.rician:
+        rd += 3 * 4
+    rd += qlen_mean * 20                                    # cap, start, end, fin, meta of queued frames
+    wr += kept_mean * 8 + max(qlen_mean - kept_mean, 0.0) * 4
+    if p.out_ref:
+        wr += F * (3 + 8 + 8 + 4) + 8 + 8 + 4 + 4 + 8       # reference dtypes
+    else:
+        wr += F * (1 + 4 + 1 + 4) + 8 + 8 + 4 + 4
+    per_env = 4 * 4 + 4 + p.n_fields * p.n_modes * 3 * 4 + 2 * 8 * 12 + 2 * 8 * 3 * (cfg.max_harq_tx + 1) + 9
+    return E * R * (rd + wr) + E * per_env
+
+
+def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
+    import torch
+
+    from oracle import nr_oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    R = wl.R
+    ora = O.OracleEngine(E_cpu, R, cfg, seed=0)
+    poses = wl.poses[:, :E_cpu].cpu()
+    counts = wl.counts[:, :E_cpu].cpu().numpy()
+
+    def one(s):
+        c = counts[s]
+        for ci in range(c.shape[-1]):
+            for i in range(int(c[..., ci].max())):
+                ora.submit(None, torch.from_numpy((c[..., ci] > i).astype("int64") * (ci + 1)))
+        ora.step(None, poses[s])
+    for s in range(warmup):
+        one(s)
+    t0 = time.perf_counter()
+    for s in range(warmup, warmup + steps):
+        one(s)
+    dt = time.perf_counter() - t0
+    k_ul = sum(1 for x in cfg.schedule(0) if x[1])
+    return {"value": E_cpu * R * k_ul * steps / dt, "unit": "robot-slots/s", "cores": threads, "kind": "port",
+            "sample": f"oracle (torch CPU restatement of the reference path) on the first {E_cpu} of the 4096 envs "
+                      f"x {R} robots, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
+            "ms_per_step": 1e3 * dt / steps}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--envs", type=int, default=4096)
+    ap.add_argument("--robots", type=int, default=32)
+    ap.add_argument("--out-format", default="reference", choices=("reference", "compact"))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-envs", type=int, default=1024)
+    ap.add_argument("--cpu-steps", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this engine runs on one GPU (envs are independent; sharding is a design note); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    P = load_package()
+    from isaac_net_amd import scenarios as S
+    dev = "cuda:0"
+    E, R = args.envs, args.robots
+    total = args.warmup + args.steps
+    print(f"# workload rl_scale {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev)
+    cfg = wl.cfg
+    eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
+    k_ul = sum(1 for x in cfg.schedule(0) if x[1])
+    q_pre, q_post = [], []
+    for s in range(args.warmup):
+        eng.submit_counts(wl.counts[s])
+        q_pre.append(float(eng.st["qlen"].float().mean()))
+        eng.step(None, wl.poses[s])
+        q_post.append(float(eng.st["qlen"].float().mean()))
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        s = args.warmup + i
+        eng.submit_counts(wl.counts[s])
+        ev[i][0].record(stream)
+        eng.step(None, wl.poses[s])
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    k_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    k_avg = sum(k_ms) / len(k_ms)
+    qlen_mean = sum(q_pre) / max(len(q_pre), 1)
+    kept_mean = sum(q_post) / max(len(q_post), 1)
+    nbytes = step_kernel_bytes(eng, qlen_mean, kept_mean)
+    achieved = nbytes / (k_avg * 1e-3) / 1e9
+    value = E * R * k_ul * args.steps / dt
+    traffic = None
+    tp = os.path.join(ROOT, "profiles", f"step_kernel_traffic_{args.out_format}.json")
+    if os.path.exists(tp):
+        traffic = json.load(open(tp)).get("bytes_per_launch")
+    res = {"metric": METRIC, "value": value, "unit": "robot-slots/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"rl_scale: {E} envs x {R} robots, K={k_ul} UL slots/step (DDDSU, 25 ms), 52 PRB "
+                                  "(13 RBGs), PF alpha 0.01, 8 HARQ x 5 tx, Rician K 3 dB, 200 B @0.8 + 4000 B @0.1 "
+                                  "per robot-step, FIFO 32, UMi LOS",
+                      "envs": E, "robots": R, "ul_slots_per_step": k_ul, "global_batch": E * R,
+                      "parallelism": "single GPU", "out_format": args.out_format},
+           "env_steps_per_s": E * args.steps / dt,
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / PEAK_GBS, "traffic": traffic,
+                        "kernel": "nr_step_kernel", "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
+                        "algorithmic_bytes_per_launch": nbytes, "queue_frames_per_robot": qlen_mean}}
+    if not args.no_cpu:
+        print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

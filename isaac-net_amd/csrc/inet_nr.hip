@@ -150,11 +150,13 @@ __global__ __launch_bounds__(BLOCK) void nr_step_kernel(InetNrState st, InetNrTa
         if (act) { px = xin[ir * 2]; py = xin[ir * 2 + 1]; }
         float dx = px - pm.gnb_x, dy = py - pm.gnb_y;
         float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
+        // once per robot and step: the transcendental functions of the radio are evaluated in double precision and
+        // rounded once (correctly rounded float results; the field arguments k . x reach 1e4 rad)
         int fi = 0;
         float pl;
         if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203), deterministic LOS state
             float d3 = sqrtf(d2 * d2 + pm.hh2);
-            float lg = log10f(d3);
+            float lg = (float)log10((double)d3);
             float pl1 = (pm.pl_a + pm.pl_n1 * lg) + pm.pl_c20;
             float pl2 = ((pm.pl_a + 40.0f * lg) + pm.pl_c20) - pm.pl_c2;
             pl = d2 <= pm.dbp ? pl1 : pl2;
@@ -164,13 +166,13 @@ __global__ __launch_bounds__(BLOCK) void nr_step_kernel(InetNrState st, InetNrTa
                 fi = 1;
             }
         } else {
-            pl = pm.pl_const + pm.pl_exp10 * log10f(d2);
+            pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
         }
         const float* fld = st.field + ((size_t)ee * pm.n_fields + fi) * pm.n_modes * 3;
         float cs[INET_NR_MAX_KF];
         for (int k = 0; k < pm.n_modes; ++k) {
             float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
-            cs[k] = cosf(arg);
+            cs[k] = (float)cos((double)arg);
         }
         float field = pm.amp * aten_sum_rt(cs, pm.n_modes);
         float pg;
@@ -752,7 +754,9 @@ __global__ void nr_submit_kernel(InetNrState st, int E, int R, int F, int T, con
 
 // ======================================================================================= reset kernel
 // One block per env. NRNet.reset / MacLink.reset / FrameQueue.reset / NRRng.reset_mask and the reset draws: H0 of
-// the fading state, the Rician phase (KPHI), the radio's plane-wave fields (radio.py:185-219).
+// the fading state, the Rician phase (KPHI) and the radio's plane-wave fields (channels/fields.py:38-58,
+// radio.py:185-219); the fields' cos / sin / sqrt are evaluated in double precision and rounded once (correctly rounded
+// float32), since the step multiplies each wave vector by positions of hundreds of metres.
 __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* __restrict__ mask, int T, float k_lin0,
                                 float dc0, float dc1, float dc2, int spectrum, int full) {
     const int e = blockIdx.x;
@@ -794,7 +798,7 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             st.k_lin[ir] = k_lin0;
         }
     }
-    // env-level: radio fields (draw_plane_waves, channels/fields.py:38-58) and the clock epoch
+    // env-level: radio fields (draw_plane_waves) of the new episode
     const int K = pm.n_modes;
     const float dcs[3] = {dc0, dc1, dc2};
     for (int q = threadIdx.x; q < pm.n_fields * K; q += blockDim.x) {
@@ -803,20 +807,20 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
         float u0 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 0u), (uint32_t)kk));
         float u1 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 1u), (uint32_t)kk));
         float u2 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 2u), (uint32_t)kk));
-        float ang = (u0 * 2.0f) * (float)3.141592653589793;
+        float ang = (u0 * 2.0f) * (float)3.141592653589793;          // rand * 2 * pi, in that order
         float kmag;
-        if (spectrum == 0) {
+        if (spectrum == 0) {                                          // "sos": wavelengths 20..60 m
             float wl = 20.0f + 40.0f * u1;
             if (dcs[fi] != 10.3f) wl = wl * (float)((double)dcs[fi] / 10.3);
-            kmag = (1.0f / wl) * (float)6.283185307179586;
-        } else {
+            kmag = (1.0f / wl) * (float)6.283185307179586;            // 2 pi / wl = reciprocal(wl) * 2 pi
+        } else {                                                      // "exp": inverse CDF of the radial spectrum
             float u = clamp_max(u1, (float)(1.0 - 1e-6));
             float a = 1.0f - u;
             kmag = sqrtf(1.0f / (a * a) - 1.0f) / dcs[fi];
         }
         float* fp = st.field + (((size_t)e * pm.n_fields + fi) * K + kk) * 3;
-        fp[0] = cosf(ang) * kmag;
-        fp[1] = sinf(ang) * kmag;
+        fp[0] = (float)cos((double)ang) * kmag;
+        fp[1] = (float)sin((double)ang) * kmag;
         fp[2] = (u2 * 2.0f) * (float)3.141592653589793;
     }
     __syncthreads();

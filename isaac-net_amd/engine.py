@@ -370,11 +370,13 @@ class HipNREngine:
                 return
             mask = torch.zeros(self.E, dtype=torch.bool, device=self.dev)
             mask[ids] = True
-        if not bool(mask.any()):
+        rows = mask.nonzero(as_tuple=True)[0].cpu()
+        if rows.numel() == 0:
             return
         m8 = mask.to(torch.uint8).contiguous()
         _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), m8.data_ptr(), self.T,
                                      self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+
         self._uniform_epoch = None
         mk = mask[:, None]
         self._last_snr = torch.where(mk, torch.zeros_like(self._last_snr), self._last_snr)

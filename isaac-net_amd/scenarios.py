@@ -1,0 +1,65 @@
+"""Synthetic workloads of the NR uplink engine: the configurations it is benchmarked and tested on, as NRConfig
+objects, and their per-step inputs (robot poses and message arrivals).
+
+Mapping to NRConfig (TDD "DDDSU" at mu = 1: one UL data slot and one SR opportunity per 2.5 ms, so K UL slots per
+control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 38.101 value at 30 kHz is 51):
+  plumbing    64 envs x 8 robots, K = 4, round robin, 4 HARQ x 4 transmissions, 1500 B at Poisson 0.5, FIFO 16,
+              UMi LOS around a gNB at the centre of a 100 m square, i.i.d. Rayleigh block fading per slot.
+  rl_scale    4096 envs x 32 robots, K = 10, PF with EWMA 0.01, 8 HARQ x 5 transmissions, Rician K = 3 dB, 200 B at
+              Poisson 0.8 + 4000 B at Poisson 0.1, FIFO 32, random walk at 1 m/s in a 200 m square, UMi LOS.
+Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
+the square; arrival counts per class), identical for the GPU engine and the CPU oracle.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from .config import NRConfig
+
+
+def plumbing_config(**kw):
+    base = dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=4,
+                frame_buffer=16, msg_sizes=(1500.0,), fading_rho_per_ms=0.0, channel="tr38901",
+                tr38901_scenario="UMi", tr38901_los="los", cell_positions_m=((50.0, 50.0),), gnb_height_m=10.0,
+                seed=0)
+    base.update(kw)
+    return NRConfig(**base)
+
+
+def rl_scale_config(**kw):
+    base = dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", pf_window=100.0,
+                n_harq=8, max_harq_tx=5, frame_buffer=32, msg_sizes=(200.0, 4000.0), fading_rho_per_ms=0.0,
+                fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0, seed=0)
+    base.update(kw)
+    return NRConfig(**base)
+
+
+WORKLOADS = {
+    "plumbing": dict(cfg=plumbing_config, E=64, R=8, arena=100.0, speed=0.0, rates=(0.5,), steps=1000),
+    "rl_scale": dict(cfg=rl_scale_config, E=4096, R=32, arena=200.0, speed=1.0, rates=(0.8, 0.1), steps=500),
+}
+
+
+class Workload:
+    """Per-step inputs of a workload: poses [steps, E, R, 2] float32 and arrival counts [steps, E, R, NC] uint8,
+    generated on the host and moved to `device` (resident before any timed region)."""
+
+    def __init__(self, E, R, steps, seed=0, device="cpu", name="rl_scale"):
+        w = WORKLOADS[name]
+        self.cfg = w["cfg"]()
+        rs = np.random.default_rng(seed)
+        a, step_m = w["arena"], w["speed"] * self.cfg.control_step_ms * 1e-3
+        p = rs.uniform(0.0, a, size=(E, R, 2))
+        poses = np.empty((steps, E, R, 2), np.float32)
+        for s in range(steps):
+            poses[s] = p
+            ang = rs.uniform(0.0, 2 * math.pi, size=(E, R))
+            p = np.clip(p + step_m * np.stack([np.cos(ang), np.sin(ang)], -1), 0.0, a)
+        counts = np.stack([rs.poisson(lam, size=(steps, E, R)) for lam in w["rates"]], -1)
+        self.poses = torch.from_numpy(poses).to(device)
+        self.counts = torch.from_numpy(np.minimum(counts, 255).astype(np.uint8)).to(device)
+        self.E, self.R, self.steps = E, R, steps

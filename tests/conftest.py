@@ -1,0 +1,48 @@
+"""pytest setup: the `gpu` marker, and the product package loaded from its directory (isaac-net_amd/)."""
+import importlib.util
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def load_package():
+    if "isaac_net_amd" in sys.modules:
+        return sys.modules["isaac_net_amd"]
+    d = os.path.join(ROOT, "isaac-net_amd")
+    spec = importlib.util.spec_from_file_location("isaac_net_amd", os.path.join(d, "__init__.py"),
+                                                  submodule_search_locations=[d])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["isaac_net_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+load_package()
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an AMD GPU (MI355X) and the built libinet_nr.so")
+    config.addinivalue_line("markers", "slow: longer CPU runs")
+
+
+def pytest_collection_modifyitems(config, items):
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:  # pragma: no cover
+        has_gpu = False
+    if has_gpu:
+        return
+    skip = pytest.mark.skip(reason="no GPU in this environment")
+    for it in items:
+        if "gpu" in it.keywords:
+            it.add_marker(skip)
+
+
+CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb"]

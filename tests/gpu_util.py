@@ -1,0 +1,128 @@
+"""Shared helpers of the GPU parity tests (comparison rules and teacher forcing on the golden trajectories)."""
+import os
+
+import numpy as np
+import torch
+
+from conftest import GOLDEN
+from oracle import replay
+
+# float state: csi / h / spec carry transcendental rounding (1e-5 relative, 1 dB / unit floor); h_comb / lexp are the
+# EESM log-sum over subbands, ill-conditioned at low SINR (difference of two nearly equal logs), 1e-3 relative; the
+# OLLA offset and PF average are pure arithmetic on the decisions and must be bitwise equal.
+FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1e-5, "ul.h_comb": 1e-3,
+             "ul.h_lexp": 1e-3, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0, "net.k_los": 0.0,
+             "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0}
+OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
+# The reported SINR is (pg + ue_tx) - noise with |pg| ~ 100-150 dB: one float32 ulp there is 7.6e-6 .. 1.5e-5 dB,
+# so near 0 dB a relative bound is meaningless; the absolute floor is 4 ulp of that magnitude.
+ABS_FLOOR = {"sinr_db": 6.1e-5, "eng._last_snr": 6.1e-5}
+MAX_DEV = {}
+BOUND = {}     # key -> per-element absolute bound (numpy) for the current comparison, from oracle.tolerance
+
+
+def close(m, r, tol, floor=0.0, key=None):
+    m = np.asarray(m, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    same = (m == r) | (np.isnan(m) & np.isnan(r))
+    if tol == 0.0:
+        return same
+    dev = np.where(same, 0.0, np.abs(m - r))
+    if key is not None and dev.size:
+        MAX_DEV[key] = max(MAX_DEV.get(key, 0.0), float(np.nanmax(dev)))
+    lim = np.maximum(tol * np.maximum(np.maximum(np.abs(m), np.abs(r)), 1.0), floor)
+    if key in BOUND:
+        lim = np.maximum(lim, BOUND[key])
+    return same | (dev <= lim)
+
+
+def compare(ref, s, out, sd, E, R):
+    """(integer keys that differ, float keys out of tolerance, bool [E,R] robots with an integer difference)."""
+    pre = f"s{s:03d}/"
+    valid = ref[pre + "ul.q.cap"] >= 0
+    bad_i, bad_f = {}, {}
+    robots = np.zeros((E, R), bool)
+    for k, v in out.items():
+        if pre + "out." + k not in ref:
+            continue
+        r, m = ref[pre + "out." + k], v.detach().cpu().numpy()
+        ok = close(m, r, OUT_TOL[k], ABS_FLOOR.get(k, 0.0), "out." + k) if k in OUT_TOL else (m == r)
+        if not ok.all():
+            (bad_f if k in OUT_TOL else bad_i)["out." + k] = int((~ok).sum())
+            if k not in OUT_TOL and ok.shape[:2] == (E, R):
+                robots |= ~ok.reshape(E, R, -1).all(-1)
+    for k, v in sd.items():
+        if pre + k not in ref:
+            continue
+        r, m = ref[pre + k], v.detach().cpu().numpy()
+        if k.startswith("ul.q.") and k != "ul.q.enq":
+            vv = valid if m.shape == valid.shape else valid[..., None]
+            m, r = np.where(vv, m, 0), np.where(vv, r, 0)
+        ok = close(m, r, FLOAT_TOL[k], ABS_FLOOR.get(k, 0.0), k) if k in FLOAT_TOL else (m == r)
+        if not ok.all():
+            (bad_f if k in FLOAT_TOL else bad_i)[k] = int((~ok).sum())
+            if k not in FLOAT_TOL and ok.ndim >= 2 and ok.shape[:2] == (E, R):
+                robots |= ~ok.reshape(E, R, -1).all(-1)
+    return bad_i, bad_f, robots
+
+
+def load(name):
+    return replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
+
+
+def snapshot(ref, pre):
+    skip = ("radio", "out.", "accepted", "n_submit")
+    return {k.split("/", 1)[1]: ref[k] for k in ref.files
+            if k.startswith(pre + "/") and not k.split("/", 1)[1].startswith(skip)}
+
+
+def set_radio_bound(ref, s, cfg, eng, kind):
+    """sinr_db / _last_snr bound of step s (oracle.tolerance.sinr_bound) from the reference's fields and poses."""
+    from oracle.tolerance import engine_radio, sinr_bound
+    BOUND.clear()
+    if kind != "pose":
+        return
+    fi, sig, amp = engine_radio(eng)
+    key = next((k for k in (f"s{s:03d}/radio.k", f"s{s:03d}/radio.sf_los.k") if k in ref), None)
+    if key is None:
+        return
+    if key.endswith("radio.k"):
+        k3 = np.concatenate([ref[f"s{s:03d}/radio.k"][0], ref[f"s{s:03d}/radio.phi"][0][..., None]], -1)
+    else:
+        n = ("sf_los", "sf_nlos")[fi]
+        k3 = np.concatenate([ref[f"s{s:03d}/radio.{n}.k"][0], ref[f"s{s:03d}/radio.{n}.phi"][0][..., None]], -1)
+    b = sinr_bound(ref["x"][s], k3, sig, amp, ref[f"s{s:03d}/out.sinr_db"])
+    BOUND["out.sinr_db"] = b
+    BOUND["eng._last_snr"] = b
+
+
+def teacher_forced(P, name, dev="cuda:0"):
+    """Load the reference state before every step, run one step on the GPU, compare with the reference's next
+    state and outputs. Returns (robot-steps with an integer difference, robot-steps, int keys, float keys)."""
+    ref, cfgd, kind = load(name)
+    cfg = P.NRConfig(**cfgd, seed=0)
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    N = cfg.slots_per_step
+    last = cfg.schedule(0)[-1][0]
+    to = lambda a: torch.from_numpy(np.asarray(a)).to(dev)  # noqa: E731
+    eng = P.make_engine("L2", E, R, dev, cfg, seed=0)
+    n_bad, keys_i, keys_f = 0, {}, {}
+    for s in range(T):
+        lg = None if s == 0 else (s - 1) * N + last
+        eng.load_state_dict(snapshot(ref, f"s{s - 1:03d}" if s > 0 else "init"), T=s, last_g=lg)
+        ids = np.nonzero(ref["reset_mask"][s])[0]
+        if len(ids):
+            eng.reset(ids.tolist())
+            eng.load_state_dict(snapshot(ref, f"reset{s:03d}"), T=s, last_g=lg)
+        for send in replay.submits(ref["counts"][s]):
+            eng.submit(None, to(send))
+        x = to(ref["x"][s])
+        o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x)
+        set_radio_bound(ref, s, cfg, eng, kind)
+        bi, bf, robots = compare(ref, s, o, eng.state_dict(), E, R)
+        n_bad += int(robots.sum())
+        for k, v in bi.items():
+            keys_i[k] = keys_i.get(k, 0) + v
+        for k, v in bf.items():
+            keys_f[k] = keys_f.get(k, 0) + v
+    return n_bad, E * R * T, keys_i, keys_f

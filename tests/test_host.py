@@ -1,0 +1,62 @@
+"""Host logic of the engine that needs no GPU: refusals, the per-step slot schedule rows, config validation."""
+import math
+
+import numpy as np
+import pytest
+
+import isaac_net_amd as P
+from isaac_net_amd import engine as EN
+
+
+def test_refusals_name_each_unimplemented_feature():
+    assert EN.refusals(P.NRConfig(n_prb=52)) == []
+    bad = P.NRConfig(n_prb=52, dl=True, scheduler="qos", n_cells=3, cell_layout="hex", ul_grant_model="bsr")
+    names = " ".join(f for f, _ in EN.refusals(bad))
+    for word in ("several cells", "downlink", "bsr", "qos"):
+        assert word in names
+
+
+def test_make_engine_refuses_before_building():
+    with pytest.raises(EN.HipUnsupported):
+        P.make_engine("L2", 2, 2, "cuda", P.NRConfig(n_prb=52, dl=True))
+    with pytest.raises(NotImplementedError):
+        P.make_engine("L1", 2, 2, "cuda", P.NRConfig(n_prb=52))
+    with pytest.raises(ValueError):
+        EN.HipNREngine(2, 2, "cpu", P.NRConfig(n_prb=52))
+
+
+def test_schedule_rows_of_the_rl_workload():
+    """DDDSU at 25 ms: 20 scheduled slots (10 S with an SR opportunity, 10 U with data); with i.i.d. fading
+    (rho 0) the S-slot fading draws are skipped (the next slot overwrites the state) and the U slots keep theirs."""
+    cfg = P.NRConfig(mu=1, n_prb=52, control_step_ms=25.0, fading_rho_per_ms=0.0)
+    eng = EN.HipNREngine.__new__(EN.HipNREngine)
+    eng.config, eng.dev, eng._rows, eng._nsym_idx = cfg, "cpu", {}, {12: 0}
+    rows, n, last_rel, n_ul = eng._rows_for(0, 1)
+    r = rows.numpy()
+    assert n == 20 and n_ul == 10 and last_rel == 49
+    flags = r[:, 2]
+    assert np.all((flags[0::2] & 1) == 1) and np.all((flags[1::2] & 2) == 2)
+    assert np.all((flags & 4) == 4)                        # every scheduled slot evolves the fading
+    assert np.all((flags[0::2] & 8) == 0) and np.all((flags[1::2] & 8) == 8)
+    rho = r[:, 4].view(np.float32)
+    assert np.all(rho == 0.0)
+    assert r[1, 0] == 4 and r[0, 0] == 3
+    assert r[1, 6] == EN.salt((1 << 16) | 4) - (1 << 32) if EN.salt((1 << 16) | 4) >= 1 << 31 else True
+
+
+def test_schedule_rows_correlated_fading_keep_every_draw():
+    cfg = P.NRConfig(mu=1, n_prb=52, control_step_ms=10.0)
+    eng = EN.HipNREngine.__new__(EN.HipNREngine)
+    eng.config, eng.dev, eng._rows, eng._nsym_idx = cfg, "cpu", {}, {12: 0}
+    rows, n, _, _ = eng._rows_for(20, 4)
+    r = rows.numpy()
+    assert np.all((r[:n, 2] & 8) == 8)
+    rho = r[:n, 4].view(np.float32)
+    assert abs(float(rho[0]) - cfg.fading_rho_per_ms ** (4 * 0.5)) < 1e-6
+    assert abs(float(rho[1]) - cfg.fading_rho_per_ms ** (1 * 0.5)) < 1e-6
+
+
+def test_hash_helpers_agree():
+    for v in (0, 5, (2 << 16) | 7, 0xFFFFFFFF):
+        assert EN.salt(v) == (EN.mix32(v) + 0x9E3779B9) & 0xFFFFFFFF
+    assert EN.seed_key(0) == EN.mix32(EN.mix32(0) ^ EN.salt(0))
