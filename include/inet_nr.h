@@ -42,6 +42,7 @@ extern "C" {
 #define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
 #define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
 #define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
+#define INET_NR_MAX_ROWS 64       /* scheduled slots (InetNrRow) per control step */
 
 #define INET_NR_OK 0
 #define INET_NR_EINVAL (-1)       /* a size or pointer argument is out of range or missing */

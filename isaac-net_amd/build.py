@@ -2,26 +2,42 @@
 
     python isaac-net_amd/build.py            # or __graft_entry__.build()
 
-Flags: -ffp-contract=off keeps every float multiply and add separately rounded (the op order mirrors the
-reference's torch expressions), and packed FP32 instructions are disabled for this target.
+The step-kernel instantiations are split over translation units (one per subband count) that compile in parallel
+and link into one shared library. Flags: -ffp-contract=off keeps every float multiply and add separately rounded
+(the op order mirrors the reference's torch expressions), and packed FP32 instructions are disabled for this target.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import os
 import subprocess
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libinet_nr.so")
-SRC = [os.path.join(HERE, "csrc", "inet_nr.hip")]
+UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
 
 
-def build(verbose=False):
+def build(verbose=False, out_dir=None):
+    obj_dir = out_dir or os.path.join(HERE, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+
+    def compile_unit(u):
+        obj = os.path.join(obj_dir, u.replace(".hip", ".o"))
+        cmd = [HIPCC, *FLAGS, "-c", "-o", obj, os.path.join(CSRC, u)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        return obj
+
+    with cf.ThreadPoolExecutor(len(UNITS)) as ex:
+        objs = list(ex.map(compile_unit, UNITS))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-o", tmp, *SRC]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

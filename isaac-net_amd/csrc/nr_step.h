@@ -1,0 +1,891 @@
+// The control-step kernel of the NR uplink engine (gfx950, wave64), instantiated per (subbands S, HARQ processes P,
+// IR combining, per-subband SNR input) by nr_step_s*.hip.
+//
+// nr_step_kernel runs one whole control step per env: the radio prologue (TR 38.901 / log-distance path gain of the
+// pose, isaac_net/core/radio.py:238-277), every scheduled slot of the step (AR(1) Rician / Rayleigh fading,
+// nr_engine.py:570-611; SR opportunities, mac_ul.py:66-71; UL data slots, mac.py:228-508 with the UlMac hooks of
+// mac_ul.py:140-236) and the end of step (nr_engine.py:843-888, mac.py:585-616, queues.py:105-110), reading and
+// writing HBM once per step.
+//
+// Work decomposition: one workgroup is one wavefront; one robot per lane; the RB = next_pow2(R) lanes of an env form
+// one aligned segment of the wavefront, so every cross-robot step of the scheduler (retransmission admission,
+// RBG-by-RBG argmax, lexicographic masking) is a DPP / swizzle butterfly or a ballot inside the segment, with no
+// barrier. Per-robot state (HARQ processes, subband CSI and fading, MAC scalars) stays in VGPRs across the slots;
+// the per-MCS tables live in LDS; the in-order RLC pointer after every UL slot is recorded in LDS and replayed over
+// the queued frames in the epilogue, so the slot loop never reads the frame FIFO.
+//
+// Float arithmetic follows the reference's torch op order (no contraction, ATen reduction order) so that only the
+// transcendental functions (logf, expf, powf, log10f, cosf) differ from the CPU path by rounding. Sums over the RBGs
+// a robot holds skip the RBGs it does not hold: their terms are exact zeros of the ATen-order sum, so visiting the
+// held RBGs in that order gives the same bits (aten_rot).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/inet_nr.h"
+#include "inet_nr_dev.h"
+
+namespace inet {
+
+constexpr int STEP_WAVE = 64;          // one wavefront per workgroup
+constexpr int MAX_UL_ROWS = 64;        // UL data slots per control step
+constexpr int MAX_M = 32;              // MCS table rows
+constexpr int MAX_EQW = INET_NR_MAX_P + 1;
+constexpr uint32_t CH_STEP = 2;
+
+// Loads and stores at a uniform base plus a 32-bit per-lane byte offset (global_load ... v_off, s[base]): every
+// per-lane address is one 32-bit VGPR, and the row strides of the [E][X][R] arrays stay in scalar registers.
+template <class T>
+DEV T ldo(const T* base, uint32_t off) { return *(const T*)((const char*)base + off); }
+template <class T>
+DEV void sto(T* base, uint32_t off, T v) { *(T*)((char*)base + off) = v; }
+
+DEV int hm_state(uint32_t m) { return (int)(m & 0xffu); }
+DEV int hm_ntx(uint32_t m) { return (int)((m >> 8) & 0xffu); }
+DEV int hm_mcs(uint32_t m) { return (int)((m >> 16) & 0xffu); }
+DEV int hm_nsb(uint32_t m) { return (int)((m >> 24) & 0xffu); }
+DEV uint32_t hm_pack(int st, int ntx, int mcs, int nsb) {
+    return (uint32_t)st | ((uint32_t)ntx << 8) | ((uint32_t)mcs << 16) | ((uint32_t)nsb << 24);
+}
+
+// ---------------------------------------------------------------- butterflies inside a power-of-two segment
+// Level L pairs every lane with a lane of the other half of its 2^(L+1) group: quad_perm [1,0,3,2] and [2,3,0,1],
+// row_half_mirror, row_mirror (DPP), a swizzle with xor 16 and a permute with xor 32. Used only for reductions whose
+// operands are already uniform inside each 2^L group, where any such pairing gives the group result.
+template <int L>
+DEV int bfly(int v) {
+    if constexpr (L == 0) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (L == 1) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (L == 2) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+    else if constexpr (L == 3) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
+    else if constexpr (L == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+    else return __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), v);
+}
+
+DEV int bsum(int v, int rb) {
+    if (rb > 1) v += bfly<0>(v);
+    if (rb > 2) v += bfly<1>(v);
+    if (rb > 4) v += bfly<2>(v);
+    if (rb > 8) v += bfly<3>(v);
+    if (rb > 16) v += bfly<4>(v);
+    if (rb > 32) v += bfly<5>(v);
+    return v;
+}
+
+template <int L>
+DEV void amax_lvl(float& v, int& i) {
+    float v2 = __int_as_float(bfly<L>(__float_as_int(v)));
+    int i2 = bfly<L>(i);
+    bool take = (v2 > v) || (v2 == v && i2 < i);
+    v = take ? v2 : v;
+    i = take ? i2 : i;
+}
+// argmax over the segment with the first index on ties (torch max / argmax)
+DEV void bargmax(float& v, int& i, int rb) {
+    if (rb > 1) amax_lvl<0>(v, i);
+    if (rb > 2) amax_lvl<1>(v, i);
+    if (rb > 4) amax_lvl<2>(v, i);
+    if (rb > 8) amax_lvl<3>(v, i);
+    if (rb > 16) amax_lvl<4>(v, i);
+    if (rb > 32) amax_lvl<5>(v, i);
+}
+
+// ---------------------------------------------------------------- ATen-order sums over the RBGs a robot holds
+// torch's CPU sum of a row of N (N = 8 or 13 here) adds, from 0, the elements past the last full 8-vector first and
+// then the 8 vector lanes in order: for N = 13 the order is 8, 9, ..., 12, 0, 1, ..., 7; for N = 8 it is 0, ..., 7.
+// With every other element an exact zero (+0 or -0), adding only the held elements in that order gives the same sum.
+template <int S>
+DEV uint32_t aten_rot(uint32_t won) {
+    if constexpr (S > 8) return (won >> 8) | ((won & 0xffu) << (S - 8));
+    else return won;
+}
+template <int S>
+DEV int aten_unrot(int b) {
+    if constexpr (S > 8) return b < S - 8 ? b + 8 : b - (S - 8);
+    else return b;
+}
+// torch.logsumexp over a row that is -inf outside the held RBGs, visiting the held RBGs in ATen order: the max is
+// taken over the held RBGs (the others are -inf) and exp(-inf - max) = 0 is skipped.
+// lse_logw: the row log w_s (the log of the held PRB count, as torch computes it).
+template <int S>
+DEV float lse_logw(const float* s_logw, uint32_t won) {
+    uint32_t rot = aten_rot<S>(won);
+    float mx = -INFINITY;
+    for (uint32_t m = rot; m; m &= m - 1) {
+        float x = s_logw[aten_unrot<S>(__builtin_ctz(m))];
+        mx = x > mx ? x : mx;
+    }
+    if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
+    float sum = 0.f;
+    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
+    return logf(sum) + mx;
+}
+// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s, with lin_s in LDS at s_lin[s * 64 + lane]. `nan` says
+// that some lin_s of the full row (held or not) is NaN, which makes torch's result NaN.
+template <int S>
+DEV float lse_eesm(const float* s_lin, int lane, const float* s_logw, uint32_t won, float beta, bool nan) {
+    uint32_t rot = aten_rot<S>(won);
+    float mx = -INFINITY;
+    for (uint32_t m = rot; m; m &= m - 1) {
+        int s = aten_unrot<S>(__builtin_ctz(m));
+        float x = (-s_lin[s * STEP_WAVE + lane]) / beta + s_logw[s];
+        mx = x > mx ? x : mx;
+    }
+    if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
+    float sum = 0.f;
+    for (uint32_t m = rot; m; m &= m - 1) {
+        int s = aten_unrot<S>(__builtin_ctz(m));
+        float x = (-s_lin[s * STEP_WAVE + lane]) / beta + s_logw[s];
+        sum += expf(x - mx);
+    }
+    float r = logf(sum) + mx;
+    return nan ? NAN : r;
+}
+// PRB-weighted mean of the per-RBG dB values x_s (s_x[s * 64 + lane]) over the held RBGs (mean_db): the ATen-order
+// sum of nan_to_num(x_s * exp(log w_s - lnw)); the RBGs not held contribute exact zeros.
+template <int S>
+DEV float mean_db_held(const float* s_x, int lane, const float* s_logw, uint32_t won, float lnw) {
+    float acc = 0.f;
+    for (uint32_t m = aten_rot<S>(won); m; m &= m - 1) {
+        int s = aten_unrot<S>(__builtin_ctz(m));
+        float t = s_x[s * STEP_WAVE + lane] * expf(s_logw[s] - lnw);
+        acc += nan_to_num(t, 0.0f, 3.4028234663852886e38f, -3.4028234663852886e38f);
+    }
+    return acc;
+}
+
+// Bilinear BLER at (table row base, SINR dB) with the code-block interpolation weight wi (phy.bler_lookup)
+DEV float bler_at(const float* __restrict__ tab, int base0, int G, float s0, float ds, float sinr, float wi) {
+    float xs = sinr != sinr ? -30.0f : sinr;
+    float xg = clampf((xs - s0) / ds, 0.0f, (float)(G - 1));
+    float j0f = clamp_max(floorf(xg), (float)(G - 2));
+    int j0 = (int)j0f;
+    float wj = xg - j0f;
+    const float* p = tab + base0 + j0;
+    float lo = p[0] * (1.0f - wj) + p[1] * wj;
+    float hi = p[G] * (1.0f - wj) + p[G + 1] * wj;
+    return lo * (1.0f - wi) + hi * wi;
+}
+
+// code-block segmentation (phy.segment) of TBS tbs at code rate r (float32 rate, float64 math) -> (cbs f32, ncb f32)
+DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
+    double t = (double)tbs, r = (double)r32;
+    bool bg2 = (t <= 292.0) || ((t <= 3824.0) && (r <= 0.67)) || (r <= 0.25);
+    double kcb = bg2 ? 3840.0 : 8448.0;
+    double b = t + (t > 3824.0 ? 24.0 : 16.0);
+    double c = b <= kcb ? 1.0 : ceil(b / (kcb - 24.0));
+    double bp = c > 1.0 ? b + 24.0 * c : b;
+    cbs = (float)(bp / c);
+    ncb = (float)c;
+}
+
+// runtime-length ATen row sum for the shadowing modes (n <= 16)
+DEV float aten_sum_rt(const float* x, int n) {
+    if (n >= 8) {
+        float fin = 0.f;
+        for (int k = 8; k < n; ++k) fin += x[k];
+        for (int l = 0; l < 8; ++l) fin += x[l];
+        return fin;
+    }
+    float q[4] = {0.f, 0.f, 0.f, 0.f};
+    int si = n / 4;
+    for (int i = 0; i < si; ++i)
+        for (int k = 0; k < 4; ++k) q[k] += x[i * 4 + k];
+    for (int i = si * 4; i < n; ++i) q[0] += x[i];
+    return ((q[0] + q[1]) + q[2]) + q[3];
+}
+
+// Dynamic LDS of the step kernel, in ints: the in-order pointer after every UL slot [n_ul][64], with RLC drop the
+// byte range of a TB that exhausted its HARQ [n_ul][64] x 2, then the per-env HARQ histograms [64 / RB][3][max_tx + 1].
+inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
+    return sizeof(int) * ((size_t)n_ul * STEP_WAVE * (harq_drop ? 3 : 1) +
+                          (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1));
+}
+
+template <int S, int P, bool IR, bool VREF>
+__global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
+    InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T,
+    const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb, int n_ul_max) {
+    extern __shared__ int dyn[];
+    __shared__ float s_thr[MAX_M], s_se[MAX_M], s_beta[MAX_M], s_rate[MAX_M];
+    __shared__ float s_w[S], s_logw[S], s_wdb[S];
+    __shared__ int s_eq[MAX_M * MAX_EQW];
+    __shared__ int s_ulrel[MAX_UL_ROWS];
+    __shared__ float s_x[2 * S * STEP_WAVE];                     // per-lane rows: fading normals, RBG SINR (dB)
+    __shared__ float s_lin[S * STEP_WAVE];                       // per-lane rows: linear RBG SINR
+
+    const int lane = threadIdx.x;
+    const int envs_pw = STEP_WAVE / rb;
+    const int eloc = lane / rb;
+    const int e = blockIdx.x * envs_pw + eloc;
+    const int r = lane & (rb - 1);
+    const int R = pm.R, E = pm.E, F = pm.F, N = pm.N;
+    const bool act = (e < E) && (r < R);
+    const int ee = e < E ? e : E - 1;
+    const int rr0 = r < R ? r : 0;
+    const uint32_t o_r0 = (uint32_t)(ee * R + rr0) * 4u;           // [E][R] element of this robot
+    const uint32_t o_sr0 = (uint32_t)(ee * S * R + rr0) * 4u;      // [E][S][R] at s = 0 (row stride R)
+    const uint32_t o_pr0 = (uint32_t)(ee * P * R + rr0) * 4u;      // [E][P][R] at p = 0
+    const uint32_t o_fr0 = (uint32_t)(ee * F * R + rr0) * 4u;      // [E][F][R] at f = 0
+    const uint32_t o_r = o_r0, o_sr = o_sr0, o_pr = o_pr0;
+    const int HB = pm.max_tx + 1;
+    int* const ack_l = dyn;
+    int* const exlo_l = dyn + n_ul_max * STEP_WAVE;
+    int* const exhi_l = dyn + 2 * n_ul_max * STEP_WAVE;
+    int* const hist_l = dyn + (pm.harq_drop ? 3 : 1) * n_ul_max * STEP_WAVE;
+    int* const my_hist = hist_l + eloc * 3 * HB;
+
+    // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
+    if (lane < tb.M) {
+        s_thr[lane] = tb.thr_ref[lane]; s_se[lane] = tb.se[lane]; s_beta[lane] = tb.beta[lane];
+        s_rate[lane] = tb.rate[lane];
+    }
+    if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
+    for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
+    for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
+    if (lane == 0) {
+        int j = 0;
+        for (int k = 0; k < n_rows && j < MAX_UL_ROWS; ++k)
+            if (rows[k].flags & 2) s_ulrel[j++] = rows[k].rel;
+    }
+    __syncthreads();
+
+    // ---------------- load per-robot state ----------------
+    int sent = 0, floor_ = 0, bsr = 0, sr_t = -1, last_tx = -1, enq = 0, qlen = 0;
+    float olla = 0.f, avg = 100.f;
+    float csi[S], hr[S], hi[S];
+    uint32_t hmeta[P];
+    int hlo[P], hhi[P], hrdy[P], htbs[P];
+    float hcomb[P], hlexp[IR ? P : 1], hnrb[IR ? P : 1];
+    const bool read_h = pm.fading && !(n_rows > 0 && (rows[0].flags & 4) && rows[0].rho == 0.0f);
+    // (lanes without a robot read a clamped, valid address and discard the value: the loads are branch-free)
+    sent = ldo(st.sent, o_r); floor_ = ldo(st.floor_, o_r); bsr = ldo(st.bsr, o_r); sr_t = ldo(st.sr_t, o_r);
+    last_tx = ldo(st.last_tx, o_r); enq = ldo(st.enq, o_r); qlen = ldo(st.qlen, o_r);
+    olla = ldo(st.olla, o_r); avg = ldo(st.avg, o_r);
+    qlen = qlen < 0 ? 0 : (qlen > F ? F : qlen);
+    if (!act) { sent = 0; floor_ = 0; bsr = 0; sr_t = -1; last_tx = -1; enq = 0; qlen = 0; olla = 0.f; avg = 100.f; }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        csi[s] = ldo(st.csi + s * R, o_sr);
+        hr[s] = 0.f; hi[s] = 0.f;
+        if (read_h) { hr[s] = ldo(st.h_re + s * R, o_sr); hi[s] = ldo(st.h_im + s * R, o_sr); }
+        if (!act) { csi[s] = 0.f; hr[s] = 0.f; hi[s] = 0.f; }
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int pr = p * R;
+        hmeta[p] = ldo(st.h_meta + pr, o_pr); hlo[p] = ldo(st.h_lo + pr, o_pr); hhi[p] = ldo(st.h_hi + pr, o_pr);
+        hrdy[p] = ldo(st.h_ready + pr, o_pr); htbs[p] = ldo(st.h_tbs + pr, o_pr); hcomb[p] = ldo(st.h_comb + pr, o_pr);
+        if constexpr (IR) { hlexp[p] = ldo(st.h_lexp + pr, o_pr); hnrb[p] = ldo(st.h_nrb + pr, o_pr); }
+        if (!act) {
+            hmeta[p] = 0u; hlo[p] = 0; hhi[p] = 0; hrdy[p] = 0; htbs[p] = 0; hcomb[p] = 0.f;
+            if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+        }
+    }
+    float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
+    if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
+    // rician gain coefficients (nr_engine.py:608-611): inv = 1 / (K + 1), sqrt(K inv), sqrt(inv)
+    const float kinv = 1.0f / (kk + 1.0f);
+    const float ka = sqrtf(kk * kinv), kb = sqrtf(kinv);
+
+    // ---------------- inputs: SINR reference per subband and the reported SNR ----------------
+    float ref[VREF ? S : 1];
+    float snr_out = 0.f;
+    if constexpr (VREF) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) ref[s] = act ? ldo(xin + s, o_r * S) : 0.f;
+        snr_out = aten_sum<S>(ref) / (float)S;
+    } else if (pm.input_kind == 1) {
+        ref[0] = act ? ldo(xin, o_r) : 0.f;
+        snr_out = ref[0];
+    } else {                                       // poses -> path gain (radio prologue)
+        float px = 0.f, py = 0.f;
+        if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
+        float dx = px - pm.gnb_x, dy = py - pm.gnb_y;
+        float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
+        // once per robot and step: the transcendental functions of the radio are evaluated in double precision and
+        // rounded once (correctly rounded float results; the field arguments k . x reach 1e4 rad)
+        int fi = 0;
+        float pl;
+        if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203), deterministic LOS state
+            float d3 = sqrtf(d2 * d2 + pm.hh2);
+            float lg = (float)log10((double)d3);
+            float pl1 = (pm.pl_a + pm.pl_n1 * lg) + pm.pl_c20;
+            float pl2 = ((pm.pl_a + 40.0f * lg) + pm.pl_c20) - pm.pl_c2;
+            pl = d2 <= pm.dbp ? pl1 : pl2;
+            if (pm.nl_b1 != 0.0f) {                // NLOS: max(PL_LOS, PL'_NLOS)
+                float pn = ((pm.nl_b1 * lg + pm.nl_b0) + pm.nl_c) - pm.nl_d;
+                pl = pn > pl ? pn : pl;
+                fi = 1;
+            }
+        } else {
+            pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
+        }
+        const float* fld = st.field + ((size_t)ee * pm.n_fields + fi) * pm.n_modes * 3;
+        float cs[INET_NR_MAX_KF];
+        for (int k = 0; k < pm.n_modes; ++k) {
+            float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
+            cs[k] = (float)cos((double)arg);
+        }
+        float field = pm.amp * aten_sum_rt(cs, pm.n_modes);
+        float pg;
+        if (pm.radio_model == 1) {
+            float loss = pl + pm.sig * field;
+            pg = (pm.ue_tx + (-loss)) - pm.ue_tx;
+        } else {
+            pg = ((pm.ue_tx - pl) - field) - pm.ue_tx;
+        }
+        ref[0] = (pg + pm.ref_off) - pm.noise_prb;
+        snr_out = (pg + pm.ue_tx) - pm.subband_noise;
+    }
+    auto REF = [&](int s) -> float { return VREF ? ref[s] : ref[0]; };
+    // PHR cap n_max (mac_ul.py:165-168): ref.mean(-1) -> snr_ref_prbs 10^((ref - phr_min) / 10) / w0
+    int n_max = S;
+    if (pm.phr_cap) {
+        float rr[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) rr[s] = REF(s);
+        float mref = aten_sum<S>(rr) / (float)S;
+        float nmp = pm.snr_ref_prbs * from_db(mref - pm.phr_min);
+        float f = floorf(nmp / pm.w0);
+        f = clampf(f, 1.0f, (float)S);
+        n_max = (int)f;
+    }
+
+    // ---------------- counter RNG key of this env and step ----------------
+    uint32_t base0 = 0;
+    if (e < E) {
+        uint32_t h = mix32((uint32_t)pm.seed_key ^ salt32((uint32_t)st.env_id[e]));
+        h = mix32(h ^ salt32((uint32_t)st.episode[e]));
+        h = mix32(h ^ salt32(CH_STEP));
+        base0 = mix32(h ^ salt32((uint32_t)st.ctr_step[e]));
+    }
+
+    // per-robot counters of this step (summed over the segment at the end)
+    int c_new = 0, c_retx = 0, c_ok = 0, c_fail = 0, c_exh = 0, c_new_pend = 0;
+    int c_bytes_ok = 0, c_bytes_new = 0, c_prb = 0;
+
+    auto ack_ptr = [&]() {
+        int a = sent;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            bool own = hm_state(hmeta[p]) == 1 && hhi[p] > floor_;
+            int lo = hlo[p] > floor_ ? hlo[p] : floor_;
+            if (own && lo < a) a = lo;
+        }
+        return a;
+    };
+
+    int n_ul = 0;
+    const int g0 = (int)(T * (int64_t)N);
+    // ================================================================ slot loop
+    for (int k = 0; k < n_rows; ++k) {
+        const InetNrRow row = rows[k];
+        const int g = g0 + row.rel;
+        if ((row.flags & 4) && (row.flags & 8)) {  // AR(1) fading innovation of this slot (nr_engine.py:575-589)
+            // the 2 S normals of this robot go through LDS (s_x, s_lin are free here): drawing them in a rolled loop
+            // keeps one Box-Muller evaluation in flight instead of 2 S
+            const uint32_t bf = mix32(base0 ^ row.salt_fade);
+            float* const s_z = s_x;
+#pragma unroll 1
+            for (int q = 0; q < 2 * S; ++q) s_z[q * STEP_WAVE + lane] = normal_at(bf, (uint32_t)(r * S * 2 + q));
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                float zr = s_z[(2 * s) * STEP_WAVE + lane], zi = s_z[(2 * s + 1) * STEP_WAVE + lane];
+                hr[s] = row.rho * hr[s] + (row.c1 * zr) / (float)1.4142135623730951;
+                hi[s] = row.rho * hi[s] + (row.c1 * zi) / (float)1.4142135623730951;
+            }
+        }
+        if (row.flags & 1) {                       // SR opportunity (UlMac.sr_step, lumped)
+            if ((enq - sent) > 0 && bsr <= 0 && sr_t < 0) sr_t = g;
+        }
+        if (!(row.flags & 2)) continue;
+        // ============================ UL data slot (MacLink.slot) ============================
+        const int unsent = enq - sent;
+        // grants (UlMac._pre_slot_lumped)
+        if (row.flags & 16) bsr = bsr > 1 ? bsr : 1;
+        if (sr_t >= 0 && g - sr_t >= pm.sr_delay) { bsr = bsr > 1 ? bsr : 1; sr_t = -1; }
+        // candidates: the retransmission ready first (lowest ready slot, then lowest process), the lowest free process
+        int rx_p = 0, p_new = 0;
+        int best_rdy = 0x7fffffff;
+        bool has_rx = false, any_free = false, pending = false;
+#pragma unroll
+        for (int p = P - 1; p >= 0; --p) {
+            int stp = hm_state(hmeta[p]);
+            if (stp == 1 && hrdy[p] <= g && hrdy[p] <= best_rdy) { best_rdy = hrdy[p]; rx_p = p; has_rx = true; }
+            if (stp == 0) { any_free = true; p_new = p; }
+            if (stp == 1) pending = true;
+        }
+        const int need = bsr < unsent ? bsr : unsent;
+        bool new_el = any_free && need > 0 && !has_rx && act;
+        has_rx = has_rx && act;
+        int rx_nsb = 0;
+#pragma unroll
+        for (int p = 0; p < P; ++p) rx_nsb = p == rx_p ? hm_nsb(hmeta[p]) : rx_nsb;
+        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275)
+        float rate[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            float est = (REF(s) - s_wdb[s]) + csi[s];
+            float eo = pm.olla ? est + olla : est;
+            int mi = 0;
+            if (tb.thr_monotone) {
+                if (eo >= s_thr[0]) {                 // highest m <= mcs_max with eo >= thr[m]
+                    int lo = 0, hi_ = tb.mcs_max;
+                    while (lo < hi_) { int mid = (lo + hi_ + 1) >> 1; if (eo >= s_thr[mid]) lo = mid; else hi_ = mid - 1; }
+                    mi = lo;
+                }
+            } else {
+                for (int m = 0; m <= tb.mcs_max; ++m) if (eo >= s_thr[m]) mi = m;
+            }
+            rate[s] = ((s_se[mi] * row.re_prb) * s_w[s]) / 8.0f;
+        }
+        const float avg_c = clamp_min(avg, 1e-9f);
+        auto metric_of = [&](int s) -> float {
+            if (pm.sched == 0) return rate[s] / avg_c;
+            if (pm.sched == 1) return rate[s];
+            return (float)(g - last_tx);
+        };
+        // retransmission admission (mac.py:300-304): rank by the metric sum, admit while the RBG counts fit
+        if (seg_any(has_rx, rb, lane)) {
+            int val = has_rx ? rx_nsb : 0;
+            int tot = bsum(val, rb);
+            if (tot > S) {
+                float mt[S];
+#pragma unroll
+                for (int s = 0; s < S; ++s) mt[s] = metric_of(s);
+                float rkey = has_rx ? aten_sum<S>(mt) : -1.0f;
+                int cum = 0;
+                const int sb = lane & ~(rb - 1);
+                for (int j = 0; j < rb; ++j) {
+                    float kj = __shfl(rkey, sb + j, 64);
+                    int vj = __shfl(val, sb + j, 64);
+                    bool before = (kj > rkey) || (kj == rkey && j <= r);
+                    cum += before ? vj : 0;
+                }
+                has_rx = has_rx && cum <= S;
+            }
+        }
+        const int want_cnt = has_rx ? rx_nsb : (new_el ? n_max : 0);
+        const float prio = pm.retx_prio ? (has_rx ? 1e9f : 0.0f) : 0.0f;
+        // RBG-by-RBG allocation (mac.py:322-352)
+        int cnt = 0;
+        float left = (float)need;
+        uint32_t won = 0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
+            float m = want ? metric_of(s) + prio : -1.0f;
+            if (pm.retx_prio) {
+                bool wr = want && has_rx;
+                if (seg_any(wr, rb, lane) && !wr) m = -1.0f;
+            }
+            float bv = m;
+            int bi = r;
+            bargmax(bv, bi, rb);
+            bool sel = (bi == r) && bv >= 0.0f;
+            if (sel) { won |= 1u << s; ++cnt; }
+            left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
+        }
+        if (!pm.retx_prio) {                          // release short retransmissions (mac.py:353-379)
+            bool short_ = has_rx && (__popc(won) != rx_nsb);
+            uint32_t rel_rs = short_ ? won : 0u;
+            if (short_) won = 0u;
+            cnt = __popc(won);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                bool avs = seg_any((rel_rs >> s) & 1u, rb, lane);
+                bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
+                float m = want ? metric_of(s) : -1.0f;
+                float bv = m;
+                int bi = r;
+                bargmax(bv, bi, rb);
+                bool sel = (bi == r) && bv >= 0.0f && avs;
+                if (sel) { won |= 1u << s; ++cnt; }
+                left = left - (sel ? rate[s] : 0.0f);
+            }
+        }
+        const int n_sb = __popc(won);
+        float n_prb = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) n_prb += ((won >> s) & 1u) ? s_w[s] : 0.0f;
+        const bool tx_rx = has_rx && n_sb == rx_nsb && n_sb > 0;
+        const bool tx_new = new_el && n_sb > 0;
+        const bool tx = tx_rx || tx_new;
+        // power split (mac_ul.py:173-180): PUSCH power spread over n_prb PRBs
+        const float sp = 10.0f * log10f(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
+        // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
+        const float lnw = lse_logw<S>(s_logw, won);
+        // ---- link adaptation for new TBs (phy.select_mcs): the highest MCS meeting the BLER target ----
+        int mcs_new = 0, tbs_new = 0;
+        if (__ballot(tx_new) != 0ull) {
+            // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on the held RBGs
+            bool nan = false;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                float x = (REF(s) - sp) + csi[s];
+                nan |= x != x;
+                s_x[s * STEP_WAVE + lane] = x;
+            }
+            for (uint32_t mm = tx_new ? won : 0u; mm; mm &= mm - 1) {
+                int s = __builtin_ctz(mm);
+                s_lin[s * STEP_WAVE + lane] = from_db(clampf(s_x[s * STEP_WAVE + lane], -30.0f, 60.0f));
+            }
+            const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S>(s_x, lane, s_logw, won, lnw) : 0.f;
+            const int np = (int)n_prb;
+            const int toff = (row.nsym_idx * (tb.NPRB + 1) + np) * tb.M;
+            bool found = !tx_new;
+            for (int m = tb.mcs_max; m >= 0 && !found; --m) {
+                int tbs_m = tb.la_tbs[toff + m];
+                if (tbs_m <= 0) continue;
+                float eff;
+                if (pm.eesm) {
+                    const float beta = s_beta[m];
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan) - lnw));
+                } else {
+                    eff = eff_md;
+                }
+                eff = eff + (pm.olla ? olla : 0.0f);
+                const int base0m = (m * tb.C + tb.la_ci0[toff + m]) * tb.G;
+                float b = bler_at(tb.bler, base0m, tb.G, tb.s0, tb.ds, eff, tb.la_cwi[toff + m]);
+                float tbler = 1.0f - powf(1.0f - b, tb.la_ncb[toff + m]);
+                if (tbler <= pm.target) { mcs_new = m; tbs_new = tbs_m; found = true; }
+            }
+            if (!found) { mcs_new = 0; tbs_new = tb.la_tbs[toff]; }
+            if (!tx_new) { mcs_new = 0; tbs_new = 0; }
+        }
+        int cap_b = tbs_new / 8 - pm.tb_oh;
+        cap_b = cap_b > 1 ? cap_b : 1;
+        const int byt_new = cap_b < unsent ? cap_b : unsent;
+        // ---- bind TBs to HARQ processes (mac.py:407-426) ----
+        const int p_tx = tx_rx ? rx_p : p_new;
+        int mcs = 0, tbs = 0, ntx = 1, lo_tx = 0, hi_tx = 0;
+        float comb_p = 0.f, lexp_p = -INFINITY, nrb_p = 0.f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (p == p_tx) {
+                if (tx_new) {
+                    hlo[p] = sent; hhi[p] = sent + byt_new; htbs[p] = tbs_new;
+                    hmeta[p] = hm_pack(1, 0, mcs_new, n_sb);
+                    hcomb[p] = 0.f;
+                    if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+                }
+                mcs = hm_mcs(hmeta[p]); tbs = htbs[p]; ntx = hm_ntx(hmeta[p]) + 1;
+                comb_p = hcomb[p]; lo_tx = hlo[p]; hi_tx = hhi[p];
+                if constexpr (IR) { lexp_p = hlexp[p]; nrb_p = hnrb[p]; }
+            }
+        }
+        mcs = mcs < tb.M ? mcs : tb.M - 1;
+        if (tx_new) sent = sent + byt_new;
+        // ---- actual channel of this slot: fading gain per subband -> CSI (mac_ul.py:229-236) ----
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            float gs = 0.f;
+            if (pm.fading) {
+                float p;
+                if (pm.rician) {
+                    float xr = ka * sp_re + kb * hr[s];
+                    float xi = ka * sp_im + kb * hi[s];
+                    p = xr * xr + xi * xi;
+                } else {
+                    p = hr[s] * hr[s] + hi[s] * hi[s];
+                }
+                gs = 10.0f * log10f(clamp_min(p, 1e-6f));
+            }
+            csi[s] = gs;
+        }
+        // ---- decoding on the actual channel (mac.py:428-454, mac_ul.py:185-192) ----
+        bool ok = false, fail = false, exh = false;
+        float comb = comb_p, lexp = lexp_p, nrb = nrb_p;
+        if (__ballot(tx) != 0ull) {
+            const float beta = s_beta[mcs];
+            bool nan = false;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                float x = (REF(s) - sp) + csi[s];
+                nan |= x != x;
+                s_x[s * STEP_WAVE + lane] = x;
+            }
+            for (uint32_t mm = tx ? won : 0u; mm; mm &= mm - 1) {
+                int s = __builtin_ctz(mm);
+                s_lin[s * STEP_WAVE + lane] = from_db(clampf(s_x[s * STEP_WAVE + lane], -30.0f, 60.0f));
+            }
+            float eff_used;
+            int m_look = mcs;
+            if constexpr (IR) {
+                float lse = lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan);
+                // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
+                if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
+                else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
+                nrb = nrb_p + n_prb;
+                float v = (-beta) * (lexp - logf(clamp_min(nrb, 1.0f)));
+                eff_used = nan_to_num(10.0f * log10f(clamp_min(v, 1e-6f)), -30.0f, 60.0f, -30.0f);
+                int nt = ntx < tb.EQW - 1 ? ntx : tb.EQW - 1;
+                m_look = s_eq[mcs * tb.EQW + nt];
+                comb = comb_p;
+            } else {
+                float eff;
+                if (pm.eesm) {
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan) - lnw));
+                } else {
+                    eff = mean_db_held<S>(s_x, lane, s_logw, won, lnw);
+                }
+                float lin_e = from_db(eff);
+                comb = pm.comb == 1 ? comb_p + lin_e : lin_e;
+                eff_used = 10.0f * log10f(clamp_min(comb, 1e-9f));
+            }
+            float cbs, ncb;
+            segment_f(tbs, s_rate[mcs], cbs, ncb);
+            float xc = clampf((cbs - tb.c0) / tb.dc, 0.0f, (float)(tb.C - 1));
+            float i0f = clamp_max(floorf(xc), (float)(tb.C - 2));
+            float wi = xc - i0f;
+            float b = bler_at(tb.bler, (m_look * tb.C + (int)i0f) * tb.G, tb.G, tb.s0, tb.ds, eff_used, wi);
+            float p_err = 1.0f - powf(1.0f - b, ncb);
+            float u = uniform_bits(elem_hash(mix32(base0 ^ row.salt_bler), (uint32_t)r));
+            ok = tx && u >= p_err;
+            fail = tx && !ok;
+            exh = fail && ntx >= pm.max_tx;
+        }
+        // ---- HARQ state update (mac.py:456-477, mac_ul.py:218-219) ----
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (p == p_tx && tx) {
+                int stp = hm_state(hmeta[p]);
+                int ntxp = ntx;
+                if (ok) { stp = 0; hrdy[p] = g; }
+                hcomb[p] = comb;
+                if constexpr (IR) { hlexp[p] = lexp; hnrb[p] = nrb; }
+                if (fail) hrdy[p] = g + pm.ul_rtt;
+                if (exh) {
+                    if (pm.harq_drop) stp = 0;
+                    else {
+                        ntxp = 0; hcomb[p] = 0.f;
+                        if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+                        hrdy[p] = g + pm.rlc_retx;
+                    }
+                }
+                hmeta[p] = hm_pack(stp, ntxp, hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
+            }
+        }
+        // ---- OLLA, BSR, PF average, RR (mac.py:479-485, mac_ul.py:229-236, mac.py:534-554) ----
+        if (pm.olla) olla = clampf((olla + pm.olla_up * (ok ? 1.0f : 0.0f)) - pm.olla_dn * (fail ? 1.0f : 0.0f),
+                                   -10.0f, 10.0f);
+        const int served = ok ? hi_tx - lo_tx : 0;
+        if (tx) bsr = enq - sent;
+        avg = clamp_min(pm.pf_a * avg + pm.pf_b * (float)served, 1e-9f);
+        if (pm.sched == 2 && tx) last_tx = g;
+        // ---- counters ----
+        c_new += tx_new; c_retx += tx_rx; c_ok += ok; c_fail += fail; c_exh += exh;
+        c_bytes_ok += served; c_bytes_new += tx_new ? byt_new : 0; c_new_pend += (tx_new && pending);
+        c_prb += tx ? (int)n_prb : 0;
+        if (tx) {
+            int kh = ntx < pm.max_tx ? ntx : pm.max_tx;
+            atomicAdd(&my_hist[HB + kh], 1);
+            atomicAdd(&my_hist[(ok ? 0 : 2 * HB) + kh], 1);
+        }
+        // ---- RLC in-order pointer of this slot (completion replayed in the epilogue) ----
+        if (n_ul < n_ul_max) {
+            ack_l[n_ul * STEP_WAVE + lane] = ack_ptr();
+            if (pm.harq_drop) {
+                exlo_l[n_ul * STEP_WAVE + lane] = exh ? lo_tx : 0;
+                exhi_l[n_ul * STEP_WAVE + lane] = exh ? hi_tx : 0;
+            }
+        }
+        ++n_ul;
+    }
+    const int n_hist = n_ul < n_ul_max ? n_ul : n_ul_max;
+
+    // ================================================================ end of step (NRNet._finish)
+    const int t = (int)T;
+    const int ack_end = ack_ptr();
+    const int ep0 = act ? st.epoch[ee] : 0;
+    int newest = -1, kept = 0, lost_new = 0;
+    bool det_hit = false;
+    int new_floor = enq;
+    const int64_t hid_cur = (act && cur_hid) ? cur_hid[ee] : 0;
+    const double po = (double)pm.proc_off_hi + (double)pm.proc_off_lo;
+    const uint32_t ob = (uint32_t)(ee * R + rr0) * (uint32_t)F;   // output row of this robot [E][R][F], elements
+    uint32_t o_fr = o_fr0;
+    asm volatile("" : "+v"(o_fr));
+    for (int f = 0; f < F; ++f) {
+        bool valid = act && f < qlen;
+        int cap = -1, qs = 0, qe = 0, fin = FIN_NONE;
+        uint32_t meta = 0;
+        const int fr = f * R;
+        if (valid) {
+            cap = ldo(st.q_cap + fr, o_fr); qs = ldo(st.q_start + fr, o_fr); qe = ldo(st.q_end + fr, o_fr);
+            fin = ldo(st.q_fin + fr, o_fr); meta = ldo(st.q_meta + fr, o_fr);
+        }
+        bool lost = meta & 1u;
+        if (valid) {
+            // replay the slots: lost marking (RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
+            for (int j = 0; j < n_hist; ++j) {
+                if (pm.harq_drop) {
+                    int xl = exlo_l[j * STEP_WAVE + lane], xh = exhi_l[j * STEP_WAVE + lane];
+                    if (xh > xl && qs < xh && qe > xl) {
+                        if (!lost) ++lost_new;
+                        lost = true;
+                    }
+                }
+                if (fin == FIN_NONE && !lost && qe <= ack_l[j * STEP_WAVE + lane]) fin = g0 + s_ulrel[j];
+            }
+        }
+        bool delivered = false, timed = false, dropped = false;
+        float delay = NAN;
+        if (valid) {
+            double fin_d = INFINITY;
+            if (fin != FIN_NONE) {
+                int tf = fin / N, rel = fin - tf * N;
+                fin_d = ((double)tf + (double)(rel + 1) / (double)N) + po;
+            }
+            delivered = fin_d <= ((double)t + 1.0) + 1e-9;
+            timed = pm.purge && fin == FIN_NONE && (t + 1 - cap) >= pm.timeout;
+            dropped = lost && qe <= ack_end && !timed;
+            if (delivered) {
+                delay = (float)(fin_d - (double)cap);
+                newest = cap > newest ? cap : newest;
+                if ((meta & 2u) && ldo(st.q_hid + fr, o_fr) == (int32_t)hid_cur) det_hit = true;
+            }
+        }
+        if (act) {
+            int cap_rel = cap >= 0 ? cap - ep0 : -1;
+            int cls = valid ? (int)((meta >> 8) & 0xffu) : 0;
+            if (pm.out_ref) {
+                sto(out.delivered + f, ob, (uint8_t)delivered);
+                sto(out.timed_out + f, ob, (uint8_t)timed);
+                sto(out.dropped + f, ob, (uint8_t)dropped);
+                sto(out.cap + f, ob * 8u, (int64_t)cap_rel);
+                sto(out.cls + f, ob * 8u, (int64_t)cls);
+            } else {
+                sto(out.delivered + f, ob, (uint8_t)(delivered | (timed << 1) | (dropped << 2)));
+                sto(out.cap32 + f, ob * 4u, (int32_t)cap_rel);
+                sto(out.cls8 + f, ob, (uint8_t)cls);
+            }
+            sto(out.delay + f, ob * 4u, delay);
+        }
+        // compaction: the frames that stay move to the front, in order (queues.py:105-110)
+        if (valid && !(delivered || timed || dropped)) {
+            if (kept == 0) new_floor = qs;
+            if (kept != f) {
+                const int kr = kept * R;
+                sto(st.q_cap + kr, o_fr, cap); sto(st.q_start + kr, o_fr, qs); sto(st.q_end + kr, o_fr, qe);
+                sto(st.q_meta + kr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
+                sto(st.q_hid + kr, o_fr, ldo(st.q_hid + fr, o_fr));
+                sto(st.q_fin + kr, o_fr, fin);
+            } else {
+                sto(st.q_meta + fr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
+                sto(st.q_fin + fr, o_fr, fin);
+            }
+            ++kept;
+        }
+    }
+    if (act) {
+        for (int f = kept; f < qlen; ++f) sto(st.q_cap + f * R, o_fr, -1);
+    }
+    // compact(): floor, sent, dead processes, BSR (mac.py:610-616, mac_ul.py:255-257)
+    floor_ = new_floor;
+    sent = sent > floor_ ? sent : floor_;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        if (hm_state(hmeta[p]) == 1 && hhi[p] <= floor_ && hhi[p] > hlo[p]) {
+            hmeta[p] = hm_pack(0, 0, hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
+            hrdy[p] = 0; hcomb[p] = 0.f;
+            if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+        }
+    }
+    {
+        int un = enq - sent;
+        bsr = bsr < un ? bsr : un;
+    }
+    const int ack_new = ack_ptr();
+    // ---------------- store state and per-robot outputs ----------------
+    {
+        // fresh copies of the per-lane offsets: the store addresses are recomputed here instead of being kept live
+        // from the loads at the top of the kernel
+        uint32_t o_r = o_r0, o_sr = o_sr0, o_pr = o_pr0;
+        asm volatile("" : "+v"(o_r), "+v"(o_sr), "+v"(o_pr));
+    if (act) {
+        sto(st.sent, o_r, sent); sto(st.floor_, o_r, floor_); sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
+        sto(st.last_tx, o_r, last_tx); sto(st.qlen, o_r, kept); sto(st.olla, o_r, olla); sto(st.avg, o_r, avg);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            sto(st.csi + s * R, o_sr, csi[s]);
+            if (pm.fading) { sto(st.h_re + s * R, o_sr, hr[s]); sto(st.h_im + s * R, o_sr, hi[s]); }
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int pr = p * R;
+            sto(st.h_meta + pr, o_pr, hmeta[p]); sto(st.h_lo + pr, o_pr, hlo[p]); sto(st.h_hi + pr, o_pr, hhi[p]);
+            sto(st.h_ready + pr, o_pr, hrdy[p]); sto(st.h_tbs + pr, o_pr, htbs[p]); sto(st.h_comb + pr, o_pr, hcomb[p]);
+            if constexpr (IR) { sto(st.h_lexp + pr, o_pr, hlexp[p]); sto(st.h_nrb + pr, o_pr, hnrb[p]); }
+        }
+        sto(out.newest, o_r * 2u, (int64_t)(newest >= 0 ? newest - ep0 : -1));
+        sto(out.queue_len, o_r * 2u, (int64_t)kept);
+        int qb = enq - ack_new;
+        sto(out.queue_bytes, o_r, (float)(qb > 0 ? qb : 0));
+        sto(out.sinr_db, o_r, snr_out);
+        if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)0);
+    }
+    }
+    // per-env outputs and counters (segment reductions, written by robot 0)
+    const bool det_any = seg_any(det_hit, rb, lane);
+    const int v_new = bsum(act ? c_new : 0, rb), v_retx = bsum(act ? c_retx : 0, rb);
+    const int v_ok = bsum(act ? c_ok : 0, rb), v_fail = bsum(act ? c_fail : 0, rb);
+    const int v_exh = bsum(act ? c_exh : 0, rb), v_lost = bsum(act ? lost_new : 0, rb);
+    const int v_pend = bsum(act ? c_new_pend : 0, rb), v_bok = bsum(act ? c_bytes_ok : 0, rb);
+    const int v_bnew = bsum(act ? c_bytes_new : 0, rb), v_prb = bsum(act ? c_prb : 0, rb);
+    __syncthreads();                                  // histogram atomics of every lane are done
+    if (r == 0 && e < E) {
+        out.det_env[e] = det_any;
+        out.t[e] = (int64_t)t - (int64_t)st.epoch[e];
+        st.ctr_step[e] = st.ctr_step[e] + 1;          // rng.tick_step (nr_engine.py:847-848)
+        int64_t* c = st.ctr + (size_t)e * INET_NR_NCTR;
+        c[0] += v_new; c[1] += v_retx; c[2] += v_ok; c[3] += v_fail; c[4] += v_exh;
+        c[5] += v_bok; c[6] += v_bnew; c[7] += v_lost; c[8] += v_pend; c[9] += v_prb;
+    }
+    if (e < E && r < 3 * HB) st.hist[(size_t)e * 3 * HB + r] += my_hist[r];
+    if (e < E && rb < 3 * HB) {                       // segments narrower than the histogram: robot 0 adds the rest
+        if (r == 0)
+            for (int q = rb; q < 3 * HB; ++q) st.hist[(size_t)e * 3 * HB + q] += my_hist[q];
+    }
+}
+
+// ---------------------------------------------------------------- launch plumbing
+struct StepArgs {
+    InetNrState st;
+    InetNrTables tb;
+    InetNrParams pm;
+    const InetNrRow* rows;
+    int n_rows;
+    int64_t T;
+    const float* x;
+    const int64_t* hid;
+    InetNrOutputs out;
+    int rb;
+    unsigned grid;
+    size_t lds;
+    hipStream_t stream;
+};
+typedef void (*StepFn)(const StepArgs&);
+
+template <int S, int P, bool IR, bool VREF>
+void launch_step(const StepArgs& a) {
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF>), dim3(a.grid), dim3(STEP_WAVE), a.lds, a.stream, a.st, a.tb,
+                       a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
+}
+
+template <int S>
+StepFn pick_step_s(int P, bool ir, bool vref) {
+#define INET_PICK(PP)                                                                                 \
+    if (P == PP)                                                                                      \
+        return ir ? (vref ? &launch_step<S, PP, true, true> : &launch_step<S, PP, true, false>)      \
+                  : (vref ? &launch_step<S, PP, false, true> : &launch_step<S, PP, false, false>);
+    INET_PICK(2) INET_PICK(4) INET_PICK(8) INET_PICK(16)
+#undef INET_PICK
+    return nullptr;
+}
+
+StepFn pick_step_s13(int P, bool ir, bool vref);   // nr_step_s13.hip
+StepFn pick_step_s8(int P, bool ir, bool vref);    // nr_step_s8.hip
+
+}  // namespace inet

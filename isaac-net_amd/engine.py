@@ -299,8 +299,8 @@ class HipNREngine:
             re = float(min(12 * uls - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156)) if uls else 0.0
             rows.append((rel, self._nsym_idx.get(uls, -1), flags, re, rho, c1, salt((FADING << 16) | rel),
                          salt((BLER_UL << 16) | rel)))
-        if sum(1 for r in rows if r[2] & 2) > 64:
-            raise HipUnsupported("more than 64 UL data slots per control step")
+        if n > 64:
+            raise HipUnsupported("more than 64 scheduled slots (SR / UL / fading) per control step")
         buf = np.zeros((max(n, 1), 8), dtype=np.int32)
         for k, r in enumerate(rows):
             buf[k, 0:3] = r[0:3]
