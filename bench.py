@@ -105,6 +105,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-envs", type=int, default=1024)
     ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB three times (a plain copy kernel of known "
+                         "size, the calibration of the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (envs are independent; sharding is a design note); "
@@ -164,6 +167,13 @@ def main():
                         "frac": achieved / PEAK_GBS, "traffic": traffic,
                         "kernel": "nr_step_kernel", "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "queue_frames_per_robot": qlen_mean}}
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_calibration_bytes"] = 2 * src.numel()
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)

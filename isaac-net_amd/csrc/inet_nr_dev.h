@@ -58,8 +58,22 @@ DEV float nan_to_num(float x, float nan, float pinf, float ninf) {
 }
 // phy._db: 10 log10(max(x, 1e-6)) with NaN -> -30, +inf -> 60, -inf -> -30
 DEV float db_of(float lin) { return nan_to_num(10.0f * log10f(clamp_min(lin, 1e-6f)), -30.0f, 60.0f, -30.0f); }
-// 10 ** (x / 10) as torch evaluates it (x / 10 in float32, then pow(10, .))
-DEV float from_db(float x) { return powf(10.0f, x / 10.0f); }
+// 10 ** (x / 10) as torch evaluates it: x / 10 in float32, then 10 to that power (exp10, within an ulp)
+DEV float from_db(float x) { return exp10f(x / 10.0f); }
+// x ** n for the integer-valued float n >= 0 of a code-block count (torch pow(float, float)): binary powering in
+// double precision, rounded once to float (correctly rounded unless the exact power lies within ~1e-15 relative of a
+// rounding boundary); other exponents take powf
+DEV float pow_count(float x, float nf) {
+    int n = (int)nf;
+    if (!(nf >= 0.0f && nf <= 4096.0f) || (float)n != nf) return powf(x, nf);
+    double r = 1.0, b = (double)x;
+    while (n) {
+        if (n & 1) r *= b;
+        b *= b;
+        n >>= 1;
+    }
+    return (float)r;
+}
 
 // torch CPU float sum of a contiguous row of N elements (SumKernel.cpp vectorized_inner_sum / row_sum order)
 template <int N>

@@ -120,24 +120,23 @@ DEV float lse_logw(const float* s_logw, uint32_t won) {
     for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
     return logf(sum) + mx;
 }
-// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s, with lin_s in LDS at s_lin[s * 64 + lane]. `nan` says
-// that some lin_s of the full row (held or not) is NaN, which makes torch's result NaN.
+// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s, with lin_s in LDS at s_lin[s * 64 + lane] (x_s is kept in
+// s_tmp between the max and the sum). `nan` says that some lin_s of the full row (held or not) is NaN, which makes
+// torch's result NaN.
 template <int S>
-DEV float lse_eesm(const float* s_lin, int lane, const float* s_logw, uint32_t won, float beta, bool nan) {
+DEV float lse_eesm(const float* s_lin, float* s_tmp, int lane, const float* s_logw, uint32_t won, float beta,
+                   bool nan) {
     uint32_t rot = aten_rot<S>(won);
     float mx = -INFINITY;
     for (uint32_t m = rot; m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
         float x = (-s_lin[s * STEP_WAVE + lane]) / beta + s_logw[s];
+        s_tmp[s * STEP_WAVE + lane] = x;
         mx = x > mx ? x : mx;
     }
     if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
     float sum = 0.f;
-    for (uint32_t m = rot; m; m &= m - 1) {
-        int s = aten_unrot<S>(__builtin_ctz(m));
-        float x = (-s_lin[s * STEP_WAVE + lane]) / beta + s_logw[s];
-        sum += expf(x - mx);
-    }
+    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * STEP_WAVE + lane] - mx);
     float r = logf(sum) + mx;
     return nan ? NAN : r;
 }
@@ -236,10 +235,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     int* const my_hist = hist_l + eloc * 3 * HB;
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
-    if (lane < tb.M) {
-        s_thr[lane] = tb.thr_ref[lane]; s_se[lane] = tb.se[lane]; s_beta[lane] = tb.beta[lane];
-        s_rate[lane] = tb.rate[lane];
-    }
+    if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
+    if (lane < tb.M) { s_se[lane] = tb.se[lane]; s_beta[lane] = tb.beta[lane]; s_rate[lane] = tb.rate[lane]; }
     if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
     for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
     for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
@@ -429,11 +426,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             float est = (REF(s) - s_wdb[s]) + csi[s];
             float eo = pm.olla ? est + olla : est;
             int mi = 0;
-            if (tb.thr_monotone) {
-                if (eo >= s_thr[0]) {                 // highest m <= mcs_max with eo >= thr[m]
-                    int lo = 0, hi_ = tb.mcs_max;
-                    while (lo < hi_) { int mid = (lo + hi_ + 1) >> 1; if (eo >= s_thr[mid]) lo = mid; else hi_ = mid - 1; }
-                    mi = lo;
+            if (tb.thr_monotone) {                    // highest m <= mcs_max with eo >= thr[m] (s_thr is +inf past it)
+                if (eo >= s_thr[0]) {
+#pragma unroll
+                    for (int step = MAX_M / 2; step > 0; step >>= 1) mi += (eo >= s_thr[mi + step]) ? step : 0;
                 }
             } else {
                 for (int m = 0; m <= tb.mcs_max; ++m) if (eo >= s_thr[m]) mi = m;
@@ -541,14 +537,14 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 float eff;
                 if (pm.eesm) {
                     const float beta = s_beta[m];
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan) - lnw));
                 } else {
                     eff = eff_md;
                 }
                 eff = eff + (pm.olla ? olla : 0.0f);
                 const int base0m = (m * tb.C + tb.la_ci0[toff + m]) * tb.G;
                 float b = bler_at(tb.bler, base0m, tb.G, tb.s0, tb.ds, eff, tb.la_cwi[toff + m]);
-                float tbler = 1.0f - powf(1.0f - b, tb.la_ncb[toff + m]);
+                float tbler = 1.0f - pow_count(1.0f - b, tb.la_ncb[toff + m]);
                 if (tbler <= pm.target) { mcs_new = m; tbs_new = tbs_m; found = true; }
             }
             if (!found) { mcs_new = 0; tbs_new = tb.la_tbs[toff]; }
@@ -613,7 +609,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan);
+                float lse = lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan);
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -626,7 +622,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_logw, won, beta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan) - lnw));
                 } else {
                     eff = mean_db_held<S>(s_x, lane, s_logw, won, lnw);
                 }
@@ -640,7 +636,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             float i0f = clamp_max(floorf(xc), (float)(tb.C - 2));
             float wi = xc - i0f;
             float b = bler_at(tb.bler, (m_look * tb.C + (int)i0f) * tb.G, tb.G, tb.s0, tb.ds, eff_used, wi);
-            float p_err = 1.0f - powf(1.0f - b, ncb);
+            float p_err = 1.0f - pow_count(1.0f - b, ncb);
             float u = uniform_bits(elem_hash(mix32(base0 ^ row.salt_bler), (uint32_t)r));
             ok = tx && u >= p_err;
             fail = tx && !ok;
