@@ -6,7 +6,8 @@ A step is one control step of every env: submit_counts (this step's message arri
 the reference's output dict out: one launch of the fused step kernel). Inputs (poses and arrival counts of every
 step) are generated before the timed region and are resident in HBM. The timed region is K steps bracketed by
 torch.cuda.synchronize(); value = E * R * K_ul * K / seconds (robot-slots/s, K_ul = 10 UL slots per step).
-The step kernel's average duration is measured live with HIP events on the engine's stream; roofline.achieved is the
+The step kernel's average duration is measured live with HIP events recorded around each launch on the launch
+stream (the engine's kernel_events hook); roofline.achieved is the
 kernel's algorithmic HBM bytes per launch (from the state layout and the measured queue occupancy) over that
 duration. The CPU baseline times the oracle (a torch-CPU restatement of the reference path) on the first envs of the
 same workload.
@@ -37,31 +38,36 @@ def load_package():
     return mod
 
 
-def step_kernel_bytes(eng, qlen_mean, kept_mean):
-    """Algorithmic HBM bytes of one step-kernel launch for the engine's layout: every per-robot state word the
-    kernel must read and write, the queued frames it touches (qlen_mean read, kept_mean rewritten), inputs, outputs,
-    and the per-env words (RNG counters, epoch, shadowing field, counters) spread over the env's robots."""
+def step_kernel_bytes(eng):
+    """Algorithmic HBM bytes of one step-kernel launch: per robot-step 2 B_rw + B_ro + B_in + B_out over this
+    engine's state layout (every per-robot state word read and written once, the whole frame FIFO included),
+    plus the per-env words (RNG key and counters, epoch, shadowing field, per-env counters and histograms)."""
     cfg, E, R, S, P, F = eng.config, eng.E, eng.R, eng.S, eng.P, eng.F
     p = eng._cparams
-    rd = 9 * 4 + S * 4 + P * 6 * 4 + 8                     # scalars, CSI, HARQ (meta lo hi ready tbs comb), pose
-    wr = 8 * 4 + S * 4 + P * 6 * 4
+    b_rw = 9 * 4 + S * 4 + P * 6 * 4 + F * 6 * 4           # MAC scalars, CSI, HARQ processes, FIFO frames
     if cfg.fading:
-        wr += 2 * S * 4                                     # fading state written
-        if cfg.fading_rho_per_ms != 0.0:
-            rd += 2 * S * 4                                 # and read when it is correlated
+        b_rw += 2 * S * 4                                   # fading state
     if p.comb == 2:
-        rd += P * 8
-        wr += P * 8
-    if p.rician:
-        rd += 3 * 4
-    rd += qlen_mean * 20                                    # cap, start, end, fin, meta of queued frames
-    wr += kept_mean * 8 + max(qlen_mean - kept_mean, 0.0) * 4
+        b_rw += 2 * P * 4                                   # IR log-sum and PRB count
+    b_ro = 3 * 4 if p.rician else 0                         # Rician phasor and K
+    b_in = 8                                                # pose
     if p.out_ref:
-        wr += F * (3 + 8 + 8 + 4) + 8 + 8 + 4 + 4 + 8       # reference dtypes
+        b_out = F * (3 + 8 + 8 + 4) + 8 + 8 + 8 + 4 + 4     # delivered/timed/dropped, cap, cls, delay; per robot
     else:
-        wr += F * (1 + 4 + 1 + 4) + 8 + 8 + 4 + 4
-    per_env = 4 * 4 + 4 + p.n_fields * p.n_modes * 3 * 4 + 2 * 8 * 12 + 2 * 8 * 3 * (cfg.max_harq_tx + 1) + 9
-    return E * R * (rd + wr) + E * per_env
+        b_out = F * (1 + 4 + 1 + 4) + 8 + 8 + 4 + 4
+    per_env = 5 * 4 + p.n_fields * p.n_modes * 3 * 4 + 2 * 8 * 10 + 2 * 8 * 3 * (cfg.max_harq_tx + 1) + 9
+    per_robot = 2 * b_rw + b_ro + b_in + b_out
+    return E * R * per_robot + E * per_env, per_robot
+
+
+def step_kernel_touched_bytes(eng, qlen_mean, kept_mean):
+    """HBM bytes the kernel actually moves for the measured queue occupancy: the frame FIFO is touched only up to
+    each robot's queue length (qlen_mean frames read, kept_mean rewritten), everything else as in step_kernel_bytes."""
+    total, per_robot = step_kernel_bytes(eng)
+    F = eng.F
+    fifo_full = 2 * F * 6 * 4
+    fifo_touched = qlen_mean * 6 * 4 + kept_mean * 6 * 4
+    return total - eng.E * eng.R * (fifo_full - fifo_touched)
 
 
 def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
@@ -131,23 +137,22 @@ def main():
         eng.step(None, wl.poses[s])
         q_post.append(float(eng.st["qlen"].float().mean()))
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    eng.kernel_events = ev = []                              # HIP events around each step-kernel launch
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         s = args.warmup + i
         eng.submit_counts(wl.counts[s])
-        ev[i][0].record(stream)
         eng.step(None, wl.poses[s])
-        ev[i][1].record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    eng.kernel_events = None
     k_ms = sorted(a.elapsed_time(b) for a, b in ev)
     k_avg = sum(k_ms) / len(k_ms)
     qlen_mean = sum(q_pre) / max(len(q_pre), 1)
     kept_mean = sum(q_post) / max(len(q_post), 1)
-    nbytes = step_kernel_bytes(eng, qlen_mean, kept_mean)
+    nbytes, per_robot = step_kernel_bytes(eng)
+    touched = step_kernel_touched_bytes(eng, qlen_mean, kept_mean)
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     value = E * R * k_ul * args.steps / dt
     traffic = None
@@ -166,7 +171,8 @@ def main():
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                         "frac": achieved / PEAK_GBS, "traffic": traffic,
                         "kernel": "nr_step_kernel", "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
-                        "algorithmic_bytes_per_launch": nbytes, "queue_frames_per_robot": qlen_mean}}
+                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
+                        "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean}}
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -90,6 +90,25 @@ DEV void bargmax(float& v, int& i, int rb) {
     if (rb > 32) amax_lvl<5>(v, i);
 }
 
+template <int L>
+DEV float fmax_lvl(float v) { return fmaxf(v, __int_as_float(bfly<L>(__float_as_int(v)))); }
+// maximum over the segment (values without NaN), at every lane of the segment
+DEV float bmax(float v, int rb) {
+    if (rb > 1) v = fmax_lvl<0>(v);
+    if (rb > 2) v = fmax_lvl<1>(v);
+    if (rb > 4) v = fmax_lvl<2>(v);
+    if (rb > 8) v = fmax_lvl<3>(v);
+    if (rb > 16) v = fmax_lvl<4>(v);
+    if (rb > 32) v = fmax_lvl<5>(v);
+    return v;
+}
+// index (inside the segment) of the first lane of this lane's segment whose predicate holds; rb if none
+DEV int seg_first(bool p, int rb, int lane) {
+    unsigned long long b = __ballot(p) >> (lane & ~(rb - 1));
+    if (rb < 64) b &= (1ull << rb) - 1ull;
+    return b ? (int)__builtin_ctzll(b) : rb;
+}
+
 // ---------------------------------------------------------------- ATen-order sums over the RBGs a robot holds
 // torch's CPU sum of a row of N (N = 8 or 13 here) adds, from 0, the elements past the last full 8-vector first and
 // then the 8 vector lanes in order: for N = 13 the order is 8, 9, ..., 12, 0, 1, ..., 7; for N = 8 it is 0, ..., 7.
@@ -120,23 +139,23 @@ DEV float lse_logw(const float* s_logw, uint32_t won) {
     for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
     return logf(sum) + mx;
 }
-// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s, with lin_s in LDS at s_lin[s * 64 + lane] (x_s is kept in
-// s_tmp between the max and the sum). `nan` says that some lin_s of the full row (held or not) is NaN, which makes
-// torch's result NaN.
+// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of the robot whose linear SINR row is column `col` of s_lin
+// (s_lin[s * 64 + col]); x_s is kept in column `tmp` of s_tmp between the max and the sum. `nan` says that some
+// lin_s of the full row (held or not) is NaN, which makes torch's result NaN.
 template <int S>
-DEV float lse_eesm(const float* s_lin, float* s_tmp, int lane, const float* s_logw, uint32_t won, float beta,
+DEV float lse_eesm(const float* s_lin, int col, float* s_tmp, int tmp, const float* s_logw, uint32_t won, float beta,
                    bool nan) {
     uint32_t rot = aten_rot<S>(won);
     float mx = -INFINITY;
     for (uint32_t m = rot; m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
-        float x = (-s_lin[s * STEP_WAVE + lane]) / beta + s_logw[s];
-        s_tmp[s * STEP_WAVE + lane] = x;
+        float x = (-s_lin[s * STEP_WAVE + col]) / beta + s_logw[s];
+        s_tmp[s * STEP_WAVE + tmp] = x;
         mx = x > mx ? x : mx;
     }
     if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
     float sum = 0.f;
-    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * STEP_WAVE + lane] - mx);
+    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * STEP_WAVE + tmp] - mx);
     float r = logf(sum) + mx;
     return nan ? NAN : r;
 }
@@ -206,12 +225,15 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T,
     const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb, int n_ul_max) {
     extern __shared__ int dyn[];
-    __shared__ float s_thr[MAX_M], s_se[MAX_M], s_beta[MAX_M], s_rate[MAX_M];
+    __shared__ __align__(16) float s_thr[MAX_M];
+    __shared__ float s_se[MAX_M], s_beta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
     __shared__ int s_eq[MAX_M * MAX_EQW];
     __shared__ int s_ulrel[MAX_UL_ROWS];
     __shared__ float s_x[2 * S * STEP_WAVE];                     // per-lane rows: fading normals, RBG SINR (dB)
     __shared__ float s_lin[S * STEP_WAVE];                       // per-lane rows: linear RBG SINR
+    __shared__ int s_la_i[2 * STEP_WAVE], s_la_slot[STEP_WAVE], s_la_top[STEP_WAVE];   // link adaptation work list
+    __shared__ float s_la_f[3 * STEP_WAVE];
 
     const int lane = threadIdx.x;
     const int envs_pw = STEP_WAVE / rb;
@@ -419,29 +441,55 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         int rx_nsb = 0;
 #pragma unroll
         for (int p = 0; p < P; ++p) rx_nsb = p == rx_p ? hm_nsb(hmeta[p]) : rx_nsb;
-        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275)
+        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275), and the scheduler
+        // metric per RBG into LDS (rows 0..S-1 of s_x) for the allocation loop
         float rate[S];
+        {
+            float eo[S];
+            int mi[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            float est = (REF(s) - s_wdb[s]) + csi[s];
-            float eo = pm.olla ? est + olla : est;
-            int mi = 0;
-            if (tb.thr_monotone) {                    // highest m <= mcs_max with eo >= thr[m] (s_thr is +inf past it)
-                if (eo >= s_thr[0]) {
+            for (int s = 0; s < S; ++s) {
+                float est = (REF(s) - s_wdb[s]) + csi[s];
+                eo[s] = pm.olla ? est + olla : est;
+                mi[s] = 0;
+            }
+            if (tb.thr_monotone) {
+                // highest m <= mcs_max with eo >= thr[m] (0 when eo < thr[0] or NaN), thr non-decreasing and +inf
+                // past mcs_max: a binary search whose first three levels compare with the same seven thresholds in
+                // every lane (broadcast LDS reads), then one 16-byte LDS read of the last block of four and a count
+                // of the thresholds passed in it (the S reads are independent of each other)
+                const float t16 = s_thr[16], t8 = s_thr[8], t24 = s_thr[24];
+                const float t4 = s_thr[4], t12 = s_thr[12], t20 = s_thr[20], t28 = s_thr[28];
 #pragma unroll
-                    for (int step = MAX_M / 2; step > 0; step >>= 1) mi += (eo >= s_thr[mi + step]) ? step : 0;
+                for (int s = 0; s < S; ++s) {
+                    const float e = eo[s];
+                    int m = e >= t16 ? 16 : 0;
+                    m += e >= (m ? t24 : t8) ? 8 : 0;
+                    m += e >= (m < 16 ? (m < 8 ? t4 : t12) : (m < 24 ? t20 : t28)) ? 4 : 0;
+                    mi[s] = m;
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float4 q = *reinterpret_cast<const float4*>(&s_thr[mi[s]]);
+                    const float e = eo[s];
+                    mi[s] += (e >= q.y ? 1 : 0) + (e >= q.z ? 1 : 0) + (e >= q.w ? 1 : 0);
                 }
             } else {
-                for (int m = 0; m <= tb.mcs_max; ++m) if (eo >= s_thr[m]) mi = m;
+                for (int m = 0; m <= tb.mcs_max; ++m) {
+                    const float th = s_thr[m];
+#pragma unroll
+                    for (int s = 0; s < S; ++s) mi[s] = eo[s] >= th ? m : mi[s];
+                }
             }
-            rate[s] = ((s_se[mi] * row.re_prb) * s_w[s]) / 8.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) rate[s] = ((s_se[mi[s]] * row.re_prb) * s_w[s]) / 8.0f;
         }
         const float avg_c = clamp_min(avg, 1e-9f);
-        auto metric_of = [&](int s) -> float {
-            if (pm.sched == 0) return rate[s] / avg_c;
-            if (pm.sched == 1) return rate[s];
-            return (float)(g - last_tx);
-        };
+        float* const s_met = s_x;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            s_met[s * STEP_WAVE + lane] = pm.sched == 0 ? rate[s] / avg_c : (pm.sched == 1 ? rate[s] : (float)(g - last_tx));
+        auto metric_of = [&](int s) -> float { return s_met[s * STEP_WAVE + lane]; };
         // retransmission admission (mac.py:300-304): rank by the metric sum, admit while the RBG counts fit
         if (seg_any(has_rx, rb, lane)) {
             int val = has_rx ? rx_nsb : 0;
@@ -476,10 +524,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 bool wr = want && has_rx;
                 if (seg_any(wr, rb, lane) && !wr) m = -1.0f;
             }
-            float bv = m;
-            int bi = r;
-            bargmax(bv, bi, rb);
-            bool sel = (bi == r) && bv >= 0.0f;
+            // argmax over the robots, first robot on ties (torch argmax); -1 marks robots that do not bid
+            const float mx = bmax(m, rb);
+            const bool sel = m >= 0.0f && seg_first(m == mx, rb, lane) == r;
             if (sel) { won |= 1u << s; ++cnt; }
             left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
         }
@@ -493,10 +540,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 bool avs = seg_any((rel_rs >> s) & 1u, rb, lane);
                 bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
                 float m = want ? metric_of(s) : -1.0f;
-                float bv = m;
-                int bi = r;
-                bargmax(bv, bi, rb);
-                bool sel = (bi == r) && bv >= 0.0f && avs;
+                const float mx = bmax(m, rb);
+                const bool sel = m >= 0.0f && seg_first(m == mx, rb, lane) == r && avs;
                 if (sel) { won |= 1u << s; ++cnt; }
                 left = left - (sel ? rate[s] : 0.0f);
             }
@@ -530,25 +575,64 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S>(s_x, lane, s_logw, won, lnw) : 0.f;
             const int np = (int)n_prb;
             const int toff = (row.nsym_idx * (tb.NPRB + 1) + np) * tb.M;
-            bool found = !tx_new;
-            for (int m = tb.mcs_max; m >= 0 && !found; --m) {
-                int tbs_m = tb.la_tbs[toff + m];
-                if (tbs_m <= 0) continue;
-                float eff;
-                if (pm.eesm) {
-                    const float beta = s_beta[m];
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan) - lnw));
-                } else {
-                    eff = eff_md;
+            // The search for the highest MCS that meets the target is shared by the whole wavefront: every round,
+            // each robot still searching gets 64 / n_searching lanes, which evaluate its next MCS candidates in
+            // parallel (top, top - 1, ...); the robot takes the highest candidate that passes or moves its top down.
+            // The result is the top-down scan's (phy.select_mcs takes the highest passing MCS), without its
+            // divergent tail. A robot's inputs (table row, held RBGs, lnw, OLLA offset, mean_db value) and its
+            // linear SINR row are read from LDS by its helpers.
+            s_la_i[lane] = toff;
+            s_la_i[STEP_WAVE + lane] = (int)(won | (nan ? 0x80000000u : 0u));
+            s_la_f[lane] = lnw;
+            s_la_f[STEP_WAVE + lane] = pm.olla ? olla : 0.0f;
+            s_la_f[2 * STEP_WAVE + lane] = eff_md;
+            int top = tb.mcs_max, found_m = -1;
+            bool mine = tx_new;
+            unsigned long long searching = __ballot(mine);
+            while (searching) {
+                const int n_s = __popcll(searching);
+                const int chunk = STEP_WAVE / n_s;
+                const int rank = __popcll(searching & ((1ull << lane) - 1ull));
+                if (mine) { s_la_slot[rank] = lane; s_la_top[lane] = top; }
+                __syncthreads();
+                const int slot = lane / chunk, j = lane - slot * chunk;
+                bool pass = false;
+                if (slot < n_s) {
+                    const int rl = s_la_slot[slot];
+                    const int m = s_la_top[rl] - j;
+                    const int toff_r = s_la_i[rl];
+                    const int tbs_m = m >= 0 ? tb.la_tbs[toff_r + m] : 0;
+                    if (tbs_m > 0) {
+                        float eff;
+                        if (pm.eesm) {
+                            const uint32_t wr = (uint32_t)s_la_i[STEP_WAVE + rl];
+                            const float beta = s_beta[m];
+                            eff = db_of((-beta) * (lse_eesm<S>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
+                                                               (wr >> 31) != 0u) - s_la_f[rl]));
+                        } else {
+                            eff = s_la_f[2 * STEP_WAVE + rl];
+                        }
+                        eff = eff + s_la_f[STEP_WAVE + rl];
+                        const int base0m = (m * tb.C + tb.la_ci0[toff_r + m]) * tb.G;
+                        float b = bler_at(tb.bler, base0m, tb.G, tb.s0, tb.ds, eff, tb.la_cwi[toff_r + m]);
+                        float tbler = 1.0f - pow_count(1.0f - b, tb.la_ncb[toff_r + m]);
+                        pass = tbler <= pm.target;
+                    }
                 }
-                eff = eff + (pm.olla ? olla : 0.0f);
-                const int base0m = (m * tb.C + tb.la_ci0[toff + m]) * tb.G;
-                float b = bler_at(tb.bler, base0m, tb.G, tb.s0, tb.ds, eff, tb.la_cwi[toff + m]);
-                float tbler = 1.0f - pow_count(1.0f - b, tb.la_ncb[toff + m]);
-                if (tbler <= pm.target) { mcs_new = m; tbs_new = tbs_m; found = true; }
+                const unsigned long long pb = __ballot(pass);
+                if (mine) {
+                    const unsigned long long cm =
+                        (pb >> (rank * chunk)) & (chunk >= STEP_WAVE ? ~0ull : ((1ull << chunk) - 1ull));
+                    if (cm) { found_m = top - (int)__builtin_ctzll(cm); mine = false; }
+                    else { top -= chunk; mine = top >= 0; }
+                }
+                searching = __ballot(mine);
+                __syncthreads();
             }
-            if (!found) { mcs_new = 0; tbs_new = tb.la_tbs[toff]; }
-            if (!tx_new) { mcs_new = 0; tbs_new = 0; }
+            if (tx_new) {
+                mcs_new = found_m >= 0 ? found_m : 0;
+                tbs_new = tb.la_tbs[toff + mcs_new];
+            }
         }
         int cap_b = tbs_new / 8 - pm.tb_oh;
         cap_b = cap_b > 1 ? cap_b : 1;
@@ -609,7 +693,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan);
+                float lse = lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, nan);
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -622,7 +706,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, s_x, lane, s_logw, won, beta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, nan) - lnw));
                 } else {
                     eff = mean_db_held<S>(s_x, lane, s_logw, won, lnw);
                 }

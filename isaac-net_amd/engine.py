@@ -488,9 +488,16 @@ class HipNREngine:
         dt0 = (1 if self.last_g is None else g0 + sched[0][0] - self.last_g) if fad else 0
         rows, n_rows, last_rel, n_ul = self._rows_for(g0, dt0)
         o, co = self._alloc_out()
+        ev = self.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream(self.dev))
         _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
                                           rows.data_ptr(), n_rows, T, xin.data_ptr(), hid.data_ptr(), C.byref(co),
                                           self._stream()), "step")
+        if ev is not None:
+            e1.record(torch.cuda.current_stream(self.dev))
+            ev.append((e0, e1))
         if fad:
             self.last_g = g0 + last_rel
         self._ul_slots_run += n_ul
@@ -514,6 +521,8 @@ class HipNREngine:
         return {"ul": res}
 
     _ul_slots_run = 0
+    # set to a list to record (start, end) HIP events around every step-kernel launch, on the launch stream
+    kernel_events = None
 
     # ------------------------------------------------------------------ state in the reference's layout
     def state_dict(self):
