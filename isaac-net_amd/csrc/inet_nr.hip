@@ -106,8 +106,8 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
         for (int s = 0; s < S; ++s) {
             uint32_t j = (uint32_t)((r * S + s) * 2);
             size_t is = ((size_t)e * S + s) * R + r;
-            st.h_re[is] = normal_at(bh, j) / (float)1.4142135623730951;
-            st.h_im[is] = normal_at(bh, j + 1u) / (float)1.4142135623730951;
+            st.h_re[is] = div_const(normal_at(bh, j), SQRT2_F, INV_SQRT2_F);
+            st.h_im[is] = div_const(normal_at(bh, j + 1u), SQRT2_F, INV_SQRT2_F);
         }
         if (pm.rician) {                                   // phi = 2 pi u (KPHI), nr_engine.py:293-299
             const uint32_t bk = base_key(s0, env, ep, CH_RESET, 0u, SITE_KPHI << 16);

@@ -33,13 +33,27 @@ DEV uint32_t mix32(uint32_t x) {
 DEV uint32_t salt32(uint32_t v) { return mix32(v) + GOLD; }
 DEV uint32_t elem_hash(uint32_t base, uint32_t i) { return mix32(mix32(base + i * GOLD) ^ base); }
 DEV float uniform_bits(uint32_t h) { return (float)(h >> 8) * INV24; }
-// element j of a normal draw uses hash elements 2j and 2j + 1 (Box-Muller, cosine branch)
-DEV float normal_at(uint32_t base, uint32_t j) {
-    uint32_t h1 = elem_hash(base, 2u * j), h2 = elem_hash(base, 2u * j + 1u);
+// Box-Muller, cosine branch, from the hashes of elements 2j and 2j + 1
+DEV float normal_of(uint32_t h1, uint32_t h2) {
     float u1 = (float)((h1 >> 8) + 1u) * INV24;
     float u2 = (float)(h2 >> 8) * INV24;
     return sqrtf(-2.0f * logf(u1)) * cosf((float)6.283185307179586 * u2);
 }
+// element j of a normal draw uses hash elements 2j and 2j + 1
+DEV float normal_at(uint32_t base, uint32_t j) { return normal_of(elem_hash(base, 2u * j), elem_hash(base, 2u * j + 1u)); }
+
+// x / y rounded to nearest for a constant y with r = RN(1 / y): q = RN(x r), then one fma correction of the residual
+// (Markstein). For the constants below this equals IEEE division for every float32 x; the check runs over every
+// significand in tests/test_numerics.py.
+DEV float div_const(float x, float y, float r) {
+    float q = x * r;
+    float e = fmaf(-q, y, x);
+    return fmaf(e, r, q);
+}
+constexpr float SQRT2_F = (float)1.4142135623730951;
+constexpr float INV_SQRT2_F = (float)(1.0 / (double)SQRT2_F);
+constexpr float TEN_F = 10.0f;
+constexpr float INV_TEN_F = (float)(1.0 / 10.0);
 // base key of (seed key, env, episode, channel, counter, stream), proto/rng.py key_torch
 DEV uint32_t base_key(uint32_t s0, uint32_t env, uint32_t ep, uint32_t channel, uint32_t ctr, uint32_t stream) {
     uint32_t h = mix32(s0 ^ salt32(env));
@@ -59,7 +73,7 @@ DEV float nan_to_num(float x, float nan, float pinf, float ninf) {
 // phy._db: 10 log10(max(x, 1e-6)) with NaN -> -30, +inf -> 60, -inf -> -30
 DEV float db_of(float lin) { return nan_to_num(10.0f * log10f(clamp_min(lin, 1e-6f)), -30.0f, 60.0f, -30.0f); }
 // 10 ** (x / 10) as torch evaluates it: x / 10 in float32, then 10 to that power (exp10, within an ulp)
-DEV float from_db(float x) { return exp10f(x / 10.0f); }
+DEV float from_db(float x) { return exp10f(div_const(x, TEN_F, INV_TEN_F)); }
 // x ** n for the integer-valued float n >= 0 of a code-block count (torch pow(float, float)): binary powering in
 // double precision, rounded once to float (correctly rounded unless the exact power lies within ~1e-15 relative of a
 // rounding boundary); other exponents take powf

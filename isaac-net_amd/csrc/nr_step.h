@@ -404,15 +404,22 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         if ((row.flags & 4) && (row.flags & 8)) {  // AR(1) fading innovation of this slot (nr_engine.py:575-589)
             // the 2 S normals of this robot go through LDS (s_x, s_lin are free here): drawing them in a rolled loop
             // keeps one Box-Muller evaluation in flight instead of 2 S
+            // normal j = 2 S r + q uses hash elements 2j, 2j + 1: the element's hash input base + e * GOLD advances
+            // by 2 GOLD per normal
             const uint32_t bf = mix32(base0 ^ row.salt_fade);
             float* const s_z = s_x;
+            uint32_t hin = bf + (uint32_t)(4 * r * S) * GOLD;
 #pragma unroll 1
-            for (int q = 0; q < 2 * S; ++q) s_z[q * STEP_WAVE + lane] = normal_at(bf, (uint32_t)(r * S * 2 + q));
+            for (int q = 0; q < 2 * S; ++q) {
+                const uint32_t h1 = mix32(mix32(hin) ^ bf), h2 = mix32(mix32(hin + GOLD) ^ bf);
+                s_z[q * STEP_WAVE + lane] = normal_of(h1, h2);
+                hin += 2u * GOLD;
+            }
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 float zr = s_z[(2 * s) * STEP_WAVE + lane], zi = s_z[(2 * s + 1) * STEP_WAVE + lane];
-                hr[s] = row.rho * hr[s] + (row.c1 * zr) / (float)1.4142135623730951;
-                hi[s] = row.rho * hi[s] + (row.c1 * zi) / (float)1.4142135623730951;
+                hr[s] = row.rho * hr[s] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                hi[s] = row.rho * hi[s] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
             }
         }
         if (row.flags & 1) {                       // SR opportunity (UlMac.sr_step, lumped)
@@ -787,64 +794,54 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const uint32_t ob = (uint32_t)(ee * R + rr0) * (uint32_t)F;   // output row of this robot [E][R][F], elements
     uint32_t o_fr = o_fr0;
     asm volatile("" : "+v"(o_fr));
-    for (int f = 0; f < F; ++f) {
-        bool valid = act && f < qlen;
-        int cap = -1, qs = 0, qe = 0, fin = FIN_NONE;
-        uint32_t meta = 0;
+    const int qv = act ? qlen : 0;                     // queued frames of this robot (a prefix of the FIFO)
+    for (int f = 0; f < qv; ++f) {
         const int fr = f * R;
-        if (valid) {
-            cap = ldo(st.q_cap + fr, o_fr); qs = ldo(st.q_start + fr, o_fr); qe = ldo(st.q_end + fr, o_fr);
-            fin = ldo(st.q_fin + fr, o_fr); meta = ldo(st.q_meta + fr, o_fr);
-        }
+        const int cap = ldo(st.q_cap + fr, o_fr), qs = ldo(st.q_start + fr, o_fr), qe = ldo(st.q_end + fr, o_fr);
+        int fin = ldo(st.q_fin + fr, o_fr);
+        const uint32_t meta = ldo(st.q_meta + fr, o_fr);
         bool lost = meta & 1u;
-        if (valid) {
-            // replay the slots: lost marking (RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
-            for (int j = 0; j < n_hist; ++j) {
-                if (pm.harq_drop) {
-                    int xl = exlo_l[j * STEP_WAVE + lane], xh = exhi_l[j * STEP_WAVE + lane];
-                    if (xh > xl && qs < xh && qe > xl) {
-                        if (!lost) ++lost_new;
-                        lost = true;
-                    }
+        // replay the slots: lost marking (RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
+        for (int j = 0; j < n_hist; ++j) {
+            if (pm.harq_drop) {
+                int xl = exlo_l[j * STEP_WAVE + lane], xh = exhi_l[j * STEP_WAVE + lane];
+                if (xh > xl && qs < xh && qe > xl) {
+                    if (!lost) ++lost_new;
+                    lost = true;
                 }
-                if (fin == FIN_NONE && !lost && qe <= ack_l[j * STEP_WAVE + lane]) fin = g0 + s_ulrel[j];
             }
+            if (fin == FIN_NONE && !lost && qe <= ack_l[j * STEP_WAVE + lane]) fin = g0 + s_ulrel[j];
         }
-        bool delivered = false, timed = false, dropped = false;
+        double fin_d = INFINITY;
+        if (fin != FIN_NONE) {
+            int tf = fin / N, rel = fin - tf * N;
+            fin_d = ((double)tf + (double)(rel + 1) / (double)N) + po;
+        }
+        const bool delivered = fin_d <= ((double)t + 1.0) + 1e-9;
+        const bool timed = pm.purge && fin == FIN_NONE && (t + 1 - cap) >= pm.timeout;
+        const bool dropped = lost && qe <= ack_end && !timed;
         float delay = NAN;
-        if (valid) {
-            double fin_d = INFINITY;
-            if (fin != FIN_NONE) {
-                int tf = fin / N, rel = fin - tf * N;
-                fin_d = ((double)tf + (double)(rel + 1) / (double)N) + po;
-            }
-            delivered = fin_d <= ((double)t + 1.0) + 1e-9;
-            timed = pm.purge && fin == FIN_NONE && (t + 1 - cap) >= pm.timeout;
-            dropped = lost && qe <= ack_end && !timed;
-            if (delivered) {
-                delay = (float)(fin_d - (double)cap);
-                newest = cap > newest ? cap : newest;
-                if ((meta & 2u) && ldo(st.q_hid + fr, o_fr) == (int32_t)hid_cur) det_hit = true;
-            }
+        if (delivered) {
+            delay = (float)(fin_d - (double)cap);
+            newest = cap > newest ? cap : newest;
+            if ((meta & 2u) && ldo(st.q_hid + fr, o_fr) == (int32_t)hid_cur) det_hit = true;
         }
-        if (act) {
-            int cap_rel = cap >= 0 ? cap - ep0 : -1;
-            int cls = valid ? (int)((meta >> 8) & 0xffu) : 0;
-            if (pm.out_ref) {
-                sto(out.delivered + f, ob, (uint8_t)delivered);
-                sto(out.timed_out + f, ob, (uint8_t)timed);
-                sto(out.dropped + f, ob, (uint8_t)dropped);
-                sto(out.cap + f, ob * 8u, (int64_t)cap_rel);
-                sto(out.cls + f, ob * 8u, (int64_t)cls);
-            } else {
-                sto(out.delivered + f, ob, (uint8_t)(delivered | (timed << 1) | (dropped << 2)));
-                sto(out.cap32 + f, ob * 4u, (int32_t)cap_rel);
-                sto(out.cls8 + f, ob, (uint8_t)cls);
-            }
-            sto(out.delay + f, ob * 4u, delay);
+        const int cap_rel = cap >= 0 ? cap - ep0 : -1;
+        const int cls = (int)((meta >> 8) & 0xffu);
+        if (pm.out_ref) {
+            sto(out.delivered + f, ob, (uint8_t)delivered);
+            sto(out.timed_out + f, ob, (uint8_t)timed);
+            sto(out.dropped + f, ob, (uint8_t)dropped);
+            sto(out.cap + f, ob * 8u, (int64_t)cap_rel);
+            sto(out.cls + f, ob * 8u, (int64_t)cls);
+        } else {
+            sto(out.delivered + f, ob, (uint8_t)(delivered | (timed << 1) | (dropped << 2)));
+            sto(out.cap32 + f, ob * 4u, (int32_t)cap_rel);
+            sto(out.cls8 + f, ob, (uint8_t)cls);
         }
+        sto(out.delay + f, ob * 4u, delay);
         // compaction: the frames that stay move to the front, in order (queues.py:105-110)
-        if (valid && !(delivered || timed || dropped)) {
+        if (!(delivered || timed || dropped)) {
             if (kept == 0) new_floor = qs;
             if (kept != f) {
                 const int kr = kept * R;
@@ -857,6 +854,40 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 sto(st.q_fin + fr, o_fr, fin);
             }
             ++kept;
+        }
+    }
+    // the slots past the queue get the outputs of an empty slot (not delivered / timed out / dropped, cap -1,
+    // class 0, delay NaN): one frame at a time up to a multiple of 4, then 16-byte stores of 4 frames per array
+    if (act) {
+        const bool vec = (F & 3) == 0;
+        const int fa = vec ? ((qv + 3) & ~3) : F;
+        const uint32_t qnan = 0x7fc00000u;
+        for (int f = qv; f < fa; ++f) {
+            if (pm.out_ref) {
+                sto(out.delivered + f, ob, (uint8_t)0); sto(out.timed_out + f, ob, (uint8_t)0);
+                sto(out.dropped + f, ob, (uint8_t)0);
+                sto(out.cap + f, ob * 8u, (int64_t)-1); sto(out.cls + f, ob * 8u, (int64_t)0);
+            } else {
+                sto(out.delivered + f, ob, (uint8_t)0); sto(out.cap32 + f, ob * 4u, (int32_t)-1);
+                sto(out.cls8 + f, ob, (uint8_t)0);
+            }
+            sto(out.delay + f, ob * 4u, __uint_as_float(qnan));
+        }
+        const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u), zeros = make_uint4(0u, 0u, 0u, 0u);
+        const uint4 nans = make_uint4(qnan, qnan, qnan, qnan);
+        for (int f = fa; f < F; f += 4) {
+            if (pm.out_ref) {
+                sto((uint32_t*)(out.delivered + f), ob, 0u);
+                sto((uint32_t*)(out.timed_out + f), ob, 0u);
+                sto((uint32_t*)(out.dropped + f), ob, 0u);
+                sto((uint4*)(out.cap + f), ob * 8u, ones); sto((uint4*)(out.cap + f + 2), ob * 8u, ones);
+                sto((uint4*)(out.cls + f), ob * 8u, zeros); sto((uint4*)(out.cls + f + 2), ob * 8u, zeros);
+            } else {
+                sto((uint32_t*)(out.delivered + f), ob, 0u);
+                sto((uint4*)(out.cap32 + f), ob * 4u, ones);
+                sto((uint32_t*)(out.cls8 + f), ob, 0u);
+            }
+            sto((uint4*)(out.delay + f), ob * 4u, nans);
         }
     }
     if (act) {
