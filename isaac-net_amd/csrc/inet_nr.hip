@@ -186,10 +186,10 @@ int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetN
     if (p.input_kind < 0 || p.input_kind > 2) return INET_NR_EINVAL;
     if (T < 0 || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
-    inet::StepFn fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref)
-                    : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref) : nullptr;
-    if (!fn) return INET_NR_EUNSUPPORTED;
     const int rb = next_pow2(p.R);
+    inet::StepFn fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
+                    : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
+    if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = inet::STEP_WAVE / rb;
     inet::StepArgs a{*st, t, p, rows, n_rows, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),

@@ -91,15 +91,16 @@ DEV void bargmax(float& v, int& i, int rb) {
 }
 
 template <int L>
-DEV float fmax_lvl(float v) { return fmaxf(v, __int_as_float(bfly<L>(__float_as_int(v)))); }
-// maximum over the segment (values without NaN), at every lane of the segment
-DEV float bmax(float v, int rb) {
-    if (rb > 1) v = fmax_lvl<0>(v);
-    if (rb > 2) v = fmax_lvl<1>(v);
-    if (rb > 4) v = fmax_lvl<2>(v);
-    if (rb > 8) v = fmax_lvl<3>(v);
-    if (rb > 16) v = fmax_lvl<4>(v);
-    if (rb > 32) v = fmax_lvl<5>(v);
+DEV int imax_lvl(int v) { return max(v, bfly<L>(v)); }
+// maximum over the segment, at every lane of the segment. The scheduler's bids are non-negative floats, whose bit
+// patterns order like the values, or -1 for no bid, so the argmax runs on integers.
+DEV int bmax_i(int v, int rb) {
+    if (rb > 1) v = imax_lvl<0>(v);
+    if (rb > 2) v = imax_lvl<1>(v);
+    if (rb > 4) v = imax_lvl<2>(v);
+    if (rb > 8) v = imax_lvl<3>(v);
+    if (rb > 16) v = imax_lvl<4>(v);
+    if (rb > 32) v = imax_lvl<5>(v);
     return v;
 }
 // index (inside the segment) of the first lane of this lane's segment whose predicate holds; rb if none
@@ -220,10 +221,13 @@ inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
                           (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1));
 }
 
-template <int S, int P, bool IR, bool VREF>
+// RBT: the segment width when it is fixed at compile time (0: the runtime argument rb)
+template <int S, int P, bool IR, bool VREF, int RBT>
 __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T,
-    const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb, int n_ul_max) {
+    const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
+    int n_ul_max) {
+    const int rb = RBT ? RBT : rb_arg;
     extern __shared__ int dyn[];
     __shared__ __align__(16) float s_thr[MAX_M];
     __shared__ float s_se[MAX_M], s_beta[MAX_M], s_rate[MAX_M];
@@ -526,14 +530,16 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
-            float m = want ? metric_of(s) + prio : -1.0f;
+            // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
+            int m = want ? __float_as_int(metric_of(s) + prio) : -1;
             if (pm.retx_prio) {
                 bool wr = want && has_rx;
-                if (seg_any(wr, rb, lane) && !wr) m = -1.0f;
+                if (seg_any(wr, rb, lane) && !wr) m = -1;
             }
             // argmax over the robots, first robot on ties (torch argmax); -1 marks robots that do not bid
-            const float mx = bmax(m, rb);
-            const bool sel = m >= 0.0f && seg_first(m == mx, rb, lane) == r;
+            const int mx = bmax_i(m, rb);
+            const int first = seg_first(m == mx, rb, lane);
+            const bool sel = m >= 0 && first == r;
             if (sel) { won |= 1u << s; ++cnt; }
             left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
         }
@@ -546,9 +552,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             for (int s = 0; s < S; ++s) {
                 bool avs = seg_any((rel_rs >> s) & 1u, rb, lane);
                 bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
-                float m = want ? metric_of(s) : -1.0f;
-                const float mx = bmax(m, rb);
-                const bool sel = m >= 0.0f && seg_first(m == mx, rb, lane) == r && avs;
+                const int m = want ? __float_as_int(metric_of(s)) : -1;
+                const int mx = bmax_i(m, rb);
+                const int first = seg_first(m == mx, rb, lane);
+                const bool sel = m >= 0 && first == r && avs;
                 if (sel) { won |= 1u << s; ++cnt; }
                 left = left - (sel ? rate[s] : 0.0f);
             }
@@ -604,25 +611,26 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 __syncthreads();
                 const int slot = lane / chunk, j = lane - slot * chunk;
                 bool pass = false;
-                if (slot < n_s) {
-                    const int rl = s_la_slot[slot];
-                    const int m = s_la_top[rl] - j;
-                    const int toff_r = s_la_i[rl];
-                    const int tbs_m = m >= 0 ? tb.la_tbs[toff_r + m] : 0;
+                const int rl = slot < n_s ? s_la_slot[slot] : 0;
+                const int m = slot < n_s ? s_la_top[rl] - j : -1;
+                if (m >= 0) {
+                    // the four table words are loaded first; the EESM (LDS and ALU only) runs while they arrive
+                    const int ti = s_la_i[rl] + m;
+                    const int tbs_m = tb.la_tbs[ti], ci0 = tb.la_ci0[ti];
+                    const float cwi = tb.la_cwi[ti], ncb = tb.la_ncb[ti];
+                    float eff;
+                    if (pm.eesm) {
+                        const uint32_t wr = (uint32_t)s_la_i[STEP_WAVE + rl];
+                        const float beta = s_beta[m];
+                        eff = db_of((-beta) * (lse_eesm<S>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
+                                                           (wr >> 31) != 0u) - s_la_f[rl]));
+                    } else {
+                        eff = s_la_f[2 * STEP_WAVE + rl];
+                    }
+                    eff = eff + s_la_f[STEP_WAVE + rl];
                     if (tbs_m > 0) {
-                        float eff;
-                        if (pm.eesm) {
-                            const uint32_t wr = (uint32_t)s_la_i[STEP_WAVE + rl];
-                            const float beta = s_beta[m];
-                            eff = db_of((-beta) * (lse_eesm<S>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
-                                                               (wr >> 31) != 0u) - s_la_f[rl]));
-                        } else {
-                            eff = s_la_f[2 * STEP_WAVE + rl];
-                        }
-                        eff = eff + s_la_f[STEP_WAVE + rl];
-                        const int base0m = (m * tb.C + tb.la_ci0[toff_r + m]) * tb.G;
-                        float b = bler_at(tb.bler, base0m, tb.G, tb.s0, tb.ds, eff, tb.la_cwi[toff_r + m]);
-                        float tbler = 1.0f - pow_count(1.0f - b, tb.la_ncb[toff_r + m]);
+                        float b = bler_at(tb.bler, (m * tb.C + ci0) * tb.G, tb.G, tb.s0, tb.ds, eff, cwi);
+                        float tbler = 1.0f - pow_count(1.0f - b, ncb);
                         pass = tbler <= pm.target;
                     }
                 }
@@ -979,24 +987,28 @@ struct StepArgs {
 };
 typedef void (*StepFn)(const StepArgs&);
 
-template <int S, int P, bool IR, bool VREF>
+template <int S, int P, bool IR, bool VREF, int RBT>
 void launch_step(const StepArgs& a) {
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF>), dim3(a.grid), dim3(STEP_WAVE), a.lds, a.stream, a.st, a.tb,
-                       a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT>), dim3(a.grid), dim3(STEP_WAVE), a.lds, a.stream, a.st,
+                       a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
 }
 
+// every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband
+// input, a build with the width fixed at compile time
 template <int S>
-StepFn pick_step_s(int P, bool ir, bool vref) {
+StepFn pick_step_s(int P, bool ir, bool vref, int rb) {
 #define INET_PICK(PP)                                                                                 \
-    if (P == PP)                                                                                      \
-        return ir ? (vref ? &launch_step<S, PP, true, true> : &launch_step<S, PP, true, false>)      \
-                  : (vref ? &launch_step<S, PP, false, true> : &launch_step<S, PP, false, false>);
+    if (P == PP) {                                                                                    \
+        if (!ir && !vref && rb == 32) return &launch_step<S, PP, false, false, 32>;                  \
+        return ir ? (vref ? &launch_step<S, PP, true, true, 0> : &launch_step<S, PP, true, false, 0>) \
+                  : (vref ? &launch_step<S, PP, false, true, 0> : &launch_step<S, PP, false, false, 0>); \
+    }
     INET_PICK(2) INET_PICK(4) INET_PICK(8) INET_PICK(16)
 #undef INET_PICK
     return nullptr;
 }
 
-StepFn pick_step_s13(int P, bool ir, bool vref);   // nr_step_s13.hip
-StepFn pick_step_s8(int P, bool ir, bool vref);    // nr_step_s8.hip
+StepFn pick_step_s13(int P, bool ir, bool vref, int rb);   // nr_step_s13.hip
+StepFn pick_step_s8(int P, bool ir, bool vref, int rb);    // nr_step_s8.hip
 
 }  // namespace inet
