@@ -3,7 +3,8 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--out-format reference|compact] [--no-cpu]
 
 A step is one control step of every env: submit_counts (this step's message arrivals, one launch) and step (poses in,
-the reference's output dict out: one launch of the fused step kernel). Inputs (poses and arrival counts of every
+the reference's output dict out: one launch of the fused step kernel), launched from Python every step (--graph:
+replayed from HIP graphs recorded after the warm-up). Inputs (poses and arrival counts of every
 step) are generated before the timed region and are resident in HBM. The timed region is K steps bracketed by
 torch.cuda.synchronize(); value = E * R * K_ul * K / seconds (robot-slots/s, K_ul = 10 UL slots per step).
 The step kernel's average duration is measured live with HIP events recorded around each launch on the launch
@@ -109,6 +110,9 @@ def main():
     ap.add_argument("--robots", type=int, default=32)
     ap.add_argument("--out-format", default="reference", choices=("reference", "compact"))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay submit and step from HIP graphs recorded after the warm-up instead of launching them "
+                         "from Python every step (on this stack the eager launches are the faster of the two)")
     ap.add_argument("--cpu-envs", type=int, default=2048)
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -137,13 +141,17 @@ def main():
         eng.step(None, wl.poses[s])
         q_post.append(float(eng.st["qlen"].float().mean()))
     torch.cuda.synchronize()
+    graph = eng.graph_step() if args.graph else None        # submit + step recorded once, replayed every step
     eng.kernel_events = ev = []                              # HIP events around each step-kernel launch
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         s = args.warmup + i
-        eng.submit_counts(wl.counts[s])
-        eng.step(None, wl.poses[s])
+        if graph is not None:
+            graph(wl.poses[s], wl.counts[s])
+        else:
+            eng.submit_counts(wl.counts[s])
+            eng.step(None, wl.poses[s])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
@@ -168,7 +176,8 @@ def main():
                                   "(13 RBGs), PF alpha 0.01, 8 HARQ x 5 tx, Rician K 3 dB, 200 B @0.8 + 4000 B @0.1 "
                                   "per robot-step, FIFO 32, UMi LOS",
                       "envs": E, "robots": R, "ul_slots_per_step": k_ul, "global_batch": E * R,
-                      "parallelism": "single GPU", "out_format": args.out_format},
+                      "parallelism": "single GPU", "out_format": args.out_format,
+                      "launch": "hip graph replay" if args.graph else "eager"},
            "env_steps_per_s": E * args.steps / dt,
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                         "frac": achieved / PEAK_GBS, "traffic": traffic,

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 1
+#define INET_NR_ABI_VERSION 2
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
@@ -80,6 +80,9 @@ typedef struct InetNrState {
        lost_frames, new_while_pending, prb_used, reserved, reserved; and per-env HARQ histograms
        [E][3][max_tx + 1] int64: decoded TBs by transmissions, TBs sent as transmission k, failed as transmission k */
     int64_t *ctr, *hist;
+    /* the engine's control-step counter T on the device [1] int64: read by inet_nr_step / inet_nr_submit when
+       they are called with T < 0 (a launch recorded once in a HIP graph and replayed at every step) */
+    int64_t *clock;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -144,14 +147,15 @@ typedef struct InetNrOutputs {
 int32_t inet_nr_abi_version(void);
 const char *inet_nr_build_info(void);
 
-/* One control step T (the engine's global control-step counter) over rows[0..n_rows) (device buffer).
+/* One control step T (the engine's global control-step counter; T < 0: *st->clock, read on the device) over
+   rows[0..n_rows) (device buffer).
    x: poses [E][R][2] (input_kind 0), SNR [E][R] (1) or per-subband SNR [E][R][S] (2), float32, device.
    cur_hid: [E] int64 hazard ids for det_env (device). first_evolve_dt is folded into rows[0] by the host. */
 int32_t inet_nr_step(const InetNrState *st, const InetNrTables *tab, const InetNrParams *prm, const InetNrRow *rows,
                      int32_t n_rows, int64_t T, const float *x, const int64_t *cur_hid, const InetNrOutputs *out,
                      void *stream);
 
-/* Enqueue at control step T. Single form (counts == NULL): send [E][R] int64 class index (0 = none), det [E][R]
+/* Enqueue at control step T (T < 0: *st->clock on the device). Single form (counts == NULL): send [E][R] int64 class index (0 = none), det [E][R]
    uint8 or NULL, hid [E] int64 or NULL; accepted [E][R] uint8. Counts form (send == NULL): counts [E][R][NC]
    uint8 messages per class, enqueued class by class; accepted [E][R] int32 = messages accepted.
    sizes [NC] float32 message bytes; discard_pdcp: 1 = refuse while the head frame is stale (timeout_steps). */

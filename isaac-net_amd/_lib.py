@@ -16,7 +16,7 @@ class InetNrState(C.Structure):
         "sent", "floor_", "bsr", "sr_t", "last_tx", "olla", "avg", "enq", "qlen", "csi", "h_re", "h_im",
         "h_meta", "h_lo", "h_hi", "h_ready", "h_tbs", "h_comb", "h_lexp", "h_nrb",
         "q_cap", "q_start", "q_end", "q_fin", "q_meta", "q_hid", "spec_re", "spec_im", "k_lin",
-        "env_id", "episode", "ctr_step", "ctr_submit", "epoch", "field", "ctr", "hist")]
+        "env_id", "episode", "ctr_step", "ctr_submit", "epoch", "field", "ctr", "hist", "clock")]
 
 
 class InetNrTables(C.Structure):
@@ -46,6 +46,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
+ABI_VERSION = 2
 _LIB = None
 
 
@@ -68,7 +69,7 @@ def load(path=LIB_PATH):
     lib.inet_nr_reset.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), P, i64, f32, C.POINTER(f32), i32,
                                   P]
     lib.inet_nr_reset.restype = i32
-    if lib.inet_nr_abi_version() != 1:
+    if lib.inet_nr_abi_version() != ABI_VERSION:
         raise RuntimeError("libinet_nr.so ABI version mismatch; rebuild it")
     _LIB = lib
     return lib

@@ -23,12 +23,13 @@ constexpr uint32_t TR38901_STREAM = (0x52u << 16) + 16u;
 
 // ======================================================================================= submit kernel
 // FrameQueue.add + NRNet.add_frames (queues.py:87-103, nr_engine.py:451-487): one frame per message at the tail.
-__global__ void nr_submit_kernel(InetNrState st, int E, int R, int F, int T, const int64_t* __restrict__ send,
+__global__ void nr_submit_kernel(InetNrState st, int E, int R, int F, int64_t T_arg, const int64_t* __restrict__ send,
                                  const uint8_t* __restrict__ det, const int64_t* __restrict__ hid,
                                  const uint8_t* __restrict__ counts, int n_cls, const float* __restrict__ sizes,
                                  int discard_pdcp, int timeout, int pkt_payload, int pkt_overhead, void* accepted) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= E * R) return;
+    const int T = (int)(T_arg >= 0 ? T_arg : st.clock[0]);
     int e = i / R, r = i - e * R;
     int qlen = st.qlen[i], enq = st.enq[i];
     int n_acc = 0;
@@ -184,7 +185,7 @@ int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetN
         return INET_NR_EINVAL;
     if (t.M <= 0 || t.M > inet::MAX_M || t.EQW <= 0 || t.EQW > inet::MAX_EQW || t.mcs_max >= t.M) return INET_NR_EINVAL;
     if (p.input_kind < 0 || p.input_kind > 2) return INET_NR_EINVAL;
-    if (T < 0 || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
+    if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);
     inet::StepFn fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
@@ -205,11 +206,11 @@ int32_t inet_nr_submit(const InetNrState* st, const InetNrParams* prm, int64_t T
     if (!st || !prm || !sizes || (!send && !counts) || (send && counts)) return INET_NR_EINVAL;
     if (!counts && !accepted) return INET_NR_EINVAL;
     if (counts && n_cls <= 0) return INET_NR_EINVAL;
-    if (T < 0 || T > 0x7fffffff || (pkt_overhead && pkt_payload <= 0)) return INET_NR_EINVAL;
+    if ((T < 0 && !st->clock) || T > 0x7fffffff || (pkt_overhead && pkt_payload <= 0)) return INET_NR_EINVAL;
     const InetNrParams& p = *prm;
     int n = p.E * p.R;
     hipLaunchKernelGGL(nr_submit_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, *st, p.E, p.R,
-                       p.F, (int)T, send, det, hid, counts, n_cls, sizes, discard_pdcp, p.timeout, pkt_payload,
+                       p.F, T, send, det, hid, counts, n_cls, sizes, discard_pdcp, p.timeout, pkt_payload,
                        pkt_overhead, accepted);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }

@@ -186,15 +186,16 @@ DEV float bler_at(const float* __restrict__ tab, int base0, int G, float s0, flo
     return lo * (1.0f - wi) + hi * wi;
 }
 
-// code-block segmentation (phy.segment) of TBS tbs at code rate r (float32 rate, float64 math) -> (cbs f32, ncb f32)
+// code-block segmentation (phy.segment) of TBS tbs at code rate r (float32 rate; the reference's float64 math) ->
+// (cbs f32, ncb f32). The block count ceil(B / (Kcb - 24)) is an integer ceiling division: B < 2^31 and the divisor
+// is 3816 or 8424, so the float64 quotient never crosses an integer the exact one does not.
 DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
-    double t = (double)tbs, r = (double)r32;
-    bool bg2 = (t <= 292.0) || ((t <= 3824.0) && (r <= 0.67)) || (r <= 0.25);
-    double kcb = bg2 ? 3840.0 : 8448.0;
-    double b = t + (t > 3824.0 ? 24.0 : 16.0);
-    double c = b <= kcb ? 1.0 : ceil(b / (kcb - 24.0));
-    double bp = c > 1.0 ? b + 24.0 * c : b;
-    cbs = (float)(bp / c);
+    const double r = (double)r32;
+    const bool bg2 = (tbs <= 292) || ((tbs <= 3824) && (r <= 0.67)) || (r <= 0.25);
+    const int kcb = bg2 ? 3840 : 8448;
+    const int b = tbs + (tbs > 3824 ? 24 : 16);
+    const int c = b <= kcb ? 1 : (b + (kcb - 24) - 1) / (kcb - 24);
+    cbs = c > 1 ? (float)((double)(b + 24 * c) / (double)c) : (float)b;
     ncb = (float)c;
 }
 
@@ -224,13 +225,15 @@ inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
 // RBT: the segment width when it is fixed at compile time (0: the runtime argument rb)
 template <int S, int P, bool IR, bool VREF, int RBT>
 __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
-    InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T,
+    InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T_arg,
     const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max) {
     const int rb = RBT ? RBT : rb_arg;
+    const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
     extern __shared__ int dyn[];
     __shared__ __align__(16) float s_thr[MAX_M];
-    __shared__ float s_se[MAX_M], s_beta[MAX_M], s_rate[MAX_M];
+    __shared__ __align__(16) float s_se[MAX_M];
+    __shared__ float s_beta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
     __shared__ int s_eq[MAX_M * MAX_EQW];
     __shared__ int s_ulrel[MAX_UL_ROWS];
@@ -262,7 +265,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
-    if (lane < tb.M) { s_se[lane] = tb.se[lane]; s_beta[lane] = tb.beta[lane]; s_rate[lane] = tb.rate[lane]; }
+    if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
+    if (lane < tb.M) { s_beta[lane] = tb.beta[lane]; s_rate[lane] = tb.rate[lane]; }
     if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
     for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
     for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
@@ -481,9 +485,13 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
+                    // thresholds and spectral efficiencies of the block are read together
                     const float4 q = *reinterpret_cast<const float4*>(&s_thr[mi[s]]);
+                    const float4 g = *reinterpret_cast<const float4*>(&s_se[mi[s]]);
                     const float e = eo[s];
-                    mi[s] += (e >= q.y ? 1 : 0) + (e >= q.z ? 1 : 0) + (e >= q.w ? 1 : 0);
+                    const int k = (e >= q.y ? 1 : 0) + (e >= q.z ? 1 : 0) + (e >= q.w ? 1 : 0);
+                    const float se = k == 0 ? g.x : (k == 1 ? g.y : (k == 2 ? g.z : g.w));
+                    rate[s] = ((se * row.re_prb) * s_w[s]) / 8.0f;
                 }
             } else {
                 for (int m = 0; m <= tb.mcs_max; ++m) {
@@ -491,9 +499,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 #pragma unroll
                     for (int s = 0; s < S; ++s) mi[s] = eo[s] >= th ? m : mi[s];
                 }
-            }
 #pragma unroll
-            for (int s = 0; s < S; ++s) rate[s] = ((s_se[mi[s]] * row.re_prb) * s_w[s]) / 8.0f;
+                for (int s = 0; s < S; ++s) rate[s] = ((s_se[mi[s]] * row.re_prb) * s_w[s]) / 8.0f;
+            }
         }
         const float avg_c = clamp_min(avg, 1e-9f);
         float* const s_met = s_x;

@@ -166,6 +166,7 @@ class HipNREngine:
             "ctr_submit": z(E), "epoch": z(E),
             "field": z(E, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
             "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
+            "clock": z(1, dt=torch.int64),
         }
         self._n_fields = nf
         self._last_snr = torch.zeros(E, R, device=d)
@@ -415,11 +416,14 @@ class HipNREngine:
         nc = cnt.shape[-1]
         if tuple(cnt.shape[:2]) != (self.E, self.R) or nc > len(self.config.msg_sizes):
             raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        return self._launch_submit_counts(T, cnt)
+
+    def _launch_submit_counts(self, T, cnt):
         self._last_hid = torch.zeros_like(self._last_hid)
         acc = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
         cfg = self.config
         _lib.check(self._lib.inet_nr_submit(
-            C.byref(self._cstate), C.byref(self._cparams), T, None, None, None, cnt.data_ptr(), nc,
+            C.byref(self._cstate), C.byref(self._cparams), T, None, None, None, cnt.data_ptr(), cnt.shape[-1],
             self._sizes.data_ptr(), int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
             cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "submit")
         return acc
@@ -466,7 +470,16 @@ class HipNREngine:
         T = self._now(t)
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
-        cfg, E, R, S = self.config, self.E, self.R, self.S
+        kind, xin = self._input(x, snr_db)
+        plan = self._plan(T, kind)
+        o = self._launch_step(T, plan, xin, hid)
+        self._commit(T, plan, o)
+        if legacy:
+            return o["newest"], o["det_env"]
+        return o
+
+    def _input(self, x, snr_db):
+        E, R, S = self.E, self.R, self.S
         if snr_db is None:
             if x is None:
                 raise ValueError("step needs poses [E,R,2|3] or an SNR [E,R]")
@@ -480,32 +493,58 @@ class HipNREngine:
         want = {0: (E, R, 2), 1: (E, R), 2: (E, R, S)}[kind]
         if tuple(xin.shape) != want:
             raise ValueError(f"input must have shape {want}, got {tuple(xin.shape)}")
-        self._cparams.input_kind = kind
-        N = self.N
-        g0 = T * N
-        sched = cfg.schedule(g0)
+        return kind, xin
+
+    def _schedule(self, g0):
+        """cfg.schedule(g0), cached by g0 modulo the period of the TDD pattern, SR and CQI occasions."""
+        cfg = self.config
+        k = g0 % math.lcm(len(cfg.tdd_pattern), cfg.sr_period_slots, cfg.cqi_period_slots)
+        sc = self.__dict__.setdefault("_sched_cache", {})
+        if k not in sc:
+            sc[k] = cfg.schedule(g0)
+        return sc[k]
+
+    def _plan(self, T, kind):
+        """The host side of step T: its slot rows (device), their count, the last fading slot and the UL slots."""
+        cfg = self.config
+        g0 = T * self.N
+        sched = self._schedule(g0)
         fad = cfg.fading and len(sched) > 0
         dt0 = (1 if self.last_g is None else g0 + sched[0][0] - self.last_g) if fad else 0
         rows, n_rows, last_rel, n_ul = self._rows_for(g0, dt0)
+        key = (g0 % math.lcm(len(cfg.tdd_pattern), cfg.sr_period_slots, cfg.cqi_period_slots), dt0, kind)
+        return dict(rows=rows, n_rows=n_rows, last_rel=last_rel, n_ul=n_ul, fad=fad, kind=kind, key=key)
+
+    def _launch_step(self, T, plan, xin, hid):
+        """Launch the step kernel (T < 0: the kernel reads the device clock) and return the output dict."""
+        self._cparams.input_kind = plan["kind"]
         o, co = self._alloc_out()
         ev = self.kernel_events
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(torch.cuda.current_stream(self.dev))
         _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
-                                          rows.data_ptr(), n_rows, T, xin.data_ptr(), hid.data_ptr(), C.byref(co),
-                                          self._stream()), "step")
+                                          plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(),
+                                          hid.data_ptr(), C.byref(co), self._stream()), "step")
         if ev is not None:
             e1.record(torch.cuda.current_stream(self.dev))
             ev.append((e0, e1))
-        if fad:
-            self.last_g = g0 + last_rel
-        self._ul_slots_run += n_ul
+        return o
+
+    def _commit(self, T, plan, o):
+        """Host bookkeeping after step T: fading slot, UL slot count, clock, last SINR."""
+        if plan["fad"]:
+            self.last_g = T * self.N + plan["last_rel"]
+        self._ul_slots_run += plan["n_ul"]
         self.T = T + 1
         self._last_snr = o["sinr_db"]
-        if legacy:
-            return o["newest"], o["det_env"]
-        return o
+
+    def graph_step(self, n_cls=None):
+        """Record one control step (submit_counts of per-class arrival counts, then step on poses) in a HIP graph.
+        Returns a GraphStep; calling it with (poses [E,R,2|3], counts [E,R,NC]) replays the step. The schedule of
+        every replayed step must match the recorded one (the same TDD / SR / CQI phase and fading slot spacing),
+        which holds when the control step spans whole periods."""
+        return GraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     # ------------------------------------------------------------------ statistics
     def counters(self):
@@ -612,6 +651,59 @@ class HipNREngine:
             ep = st["epoch"]
             self._uniform_epoch = int(ep[0]) if bool((ep == ep[0]).all()) else None
         self.last_g = last_g
+
+
+class GraphStep:
+    """submit_counts + step of a HipNREngine, recorded once as two HIP graphs (torch.cuda.CUDAGraph: the enqueue,
+    then the step kernel) and replayed every control step.
+
+    The recorded launches read the control step from the engine's device clock (InetNrState.clock), which the
+    replay sets to the engine's T; the inputs are copied into the graphs' static buffers; the returned dict is the
+    static output buffers, overwritten by the next replay. The graphs hold kernel nodes only (no memset node)."""
+
+    def __init__(self, eng, n_cls):
+        E, R, dev = eng.E, eng.R, eng.dev
+        self.eng = eng
+        self.counts = torch.zeros(E, R, n_cls, dtype=torch.uint8, device=dev)
+        self.x = torch.zeros(E, R, 2, dtype=torch.float32, device=dev)
+        self.plan = eng._plan(eng.T, 0)
+        eng.st["clock"].fill_(eng.T)
+        torch.cuda.synchronize(dev)
+        self.g_submit, self.g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        ev, eng.kernel_events = eng.kernel_events, None
+        try:
+            with torch.cuda.graph(self.g_submit):
+                eng._launch_submit_counts(-1, self.counts)
+            self.hid = eng._last_hid
+            with torch.cuda.graph(self.g_step):
+                self.out = eng._launch_step(-1, self.plan, self.x, self.hid)
+        finally:
+            eng.kernel_events = ev
+        torch.cuda.synchronize(dev)
+
+    def __call__(self, x, counts):
+        eng = self.eng
+        T = eng.T
+        plan = eng._plan(T, 0)
+        if plan["key"] != self.plan["key"]:
+            raise HipUnsupported(f"step {T} has another slot schedule than the recorded step; use step()")
+        if tuple(counts.shape) != tuple(self.counts.shape):
+            raise ValueError(f"counts must be {tuple(self.counts.shape)}")
+        self.x.copy_(x[..., :2])
+        self.counts.copy_(counts)
+        eng.st["clock"].fill_(T)
+        self.g_submit.replay()
+        eng._last_hid = self.hid
+        ev = eng.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream(eng.dev))
+        self.g_step.replay()
+        if ev is not None:
+            e1.record(torch.cuda.current_stream(eng.dev))
+            ev.append((e0, e1))
+        eng._commit(T, self.plan, self.out)
+        return self.out
 
 
 def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, backend="hip", *, sizes=None,
