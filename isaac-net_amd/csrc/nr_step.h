@@ -141,16 +141,17 @@ DEV float lse_logw(const float* s_logw, uint32_t won) {
     return logf(sum) + mx;
 }
 // lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of the robot whose linear SINR row is column `col` of s_lin
-// (s_lin[s * 64 + col]); x_s is kept in column `tmp` of s_tmp between the max and the sum. `nan` says that some
-// lin_s of the full row (held or not) is NaN, which makes torch's result NaN.
+// (s_lin[s * 64 + col]); x_s is kept in column `tmp` of s_tmp between the max and the sum. rbeta = RN(1 / beta): the
+// division is div_const, exact for every beta of the MCS tables. `nan` says that some lin_s of the full row (held or
+// not) is NaN, which makes torch's result NaN.
 template <int S>
 DEV float lse_eesm(const float* s_lin, int col, float* s_tmp, int tmp, const float* s_logw, uint32_t won, float beta,
-                   bool nan) {
+                   float rbeta, bool nan) {
     uint32_t rot = aten_rot<S>(won);
     float mx = -INFINITY;
     for (uint32_t m = rot; m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
-        float x = (-s_lin[s * STEP_WAVE + col]) / beta + s_logw[s];
+        float x = div_const(-s_lin[s * STEP_WAVE + col], beta, rbeta) + s_logw[s];
         s_tmp[s * STEP_WAVE + tmp] = x;
         mx = x > mx ? x : mx;
     }
@@ -173,10 +174,11 @@ DEV float mean_db_held(const float* s_x, int lane, const float* s_logw, uint32_t
     return acc;
 }
 
-// Bilinear BLER at (table row base, SINR dB) with the code-block interpolation weight wi (phy.bler_lookup)
-DEV float bler_at(const float* __restrict__ tab, int base0, int G, float s0, float ds, float sinr, float wi) {
+// Bilinear BLER at (table row base, SINR dB) with the code-block interpolation weight wi (phy.bler_lookup); rds =
+// RN(1 / ds), the division by the SINR grid step being div_const
+DEV float bler_at(const float* __restrict__ tab, int base0, int G, float s0, float ds, float rds, float sinr, float wi) {
     float xs = sinr != sinr ? -30.0f : sinr;
-    float xg = clampf((xs - s0) / ds, 0.0f, (float)(G - 1));
+    float xg = clampf(div_const(xs - s0, ds, rds), 0.0f, (float)(G - 1));
     float j0f = clamp_max(floorf(xg), (float)(G - 2));
     int j0 = (int)j0f;
     float wj = xg - j0f;
@@ -233,7 +235,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     extern __shared__ int dyn[];
     __shared__ __align__(16) float s_thr[MAX_M];
     __shared__ __align__(16) float s_se[MAX_M];
-    __shared__ float s_beta[MAX_M], s_rate[MAX_M];
+    __shared__ float s_beta[MAX_M], s_rbeta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
     __shared__ int s_eq[MAX_M * MAX_EQW];
     __shared__ int s_ulrel[MAX_UL_ROWS];
@@ -266,7 +268,13 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
     if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
-    if (lane < tb.M) { s_beta[lane] = tb.beta[lane]; s_rate[lane] = tb.rate[lane]; }
+    if (lane < tb.M) {
+        s_beta[lane] = tb.beta[lane];
+        s_rbeta[lane] = 1.0f / tb.beta[lane];
+        s_rate[lane] = tb.rate[lane];
+    }
+    // reciprocals of the BLER table's grid steps (div_const)
+    const float rds = 1.0f / tb.ds, rdc = 1.0f / tb.dc;
     if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
     for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
     for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
@@ -631,13 +639,13 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                         const uint32_t wr = (uint32_t)s_la_i[STEP_WAVE + rl];
                         const float beta = s_beta[m];
                         eff = db_of((-beta) * (lse_eesm<S>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
-                                                           (wr >> 31) != 0u) - s_la_f[rl]));
+                                                           s_rbeta[m], (wr >> 31) != 0u) - s_la_f[rl]));
                     } else {
                         eff = s_la_f[2 * STEP_WAVE + rl];
                     }
                     eff = eff + s_la_f[STEP_WAVE + rl];
                     if (tbs_m > 0) {
-                        float b = bler_at(tb.bler, (m * tb.C + ci0) * tb.G, tb.G, tb.s0, tb.ds, eff, cwi);
+                        float b = bler_at(tb.bler, (m * tb.C + ci0) * tb.G, tb.G, tb.s0, tb.ds, rds, eff, cwi);
                         float tbler = 1.0f - pow_count(1.0f - b, ncb);
                         pass = tbler <= pm.target;
                     }
@@ -701,7 +709,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         bool ok = false, fail = false, exh = false;
         float comb = comb_p, lexp = lexp_p, nrb = nrb_p;
         if (__ballot(tx) != 0ull) {
-            const float beta = s_beta[mcs];
+            const float beta = s_beta[mcs], rbeta = s_rbeta[mcs];
             bool nan = false;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
@@ -716,7 +724,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, nan);
+                float lse = lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan);
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -729,7 +737,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan) - lnw));
                 } else {
                     eff = mean_db_held<S>(s_x, lane, s_logw, won, lnw);
                 }
@@ -739,10 +747,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             }
             float cbs, ncb;
             segment_f(tbs, s_rate[mcs], cbs, ncb);
-            float xc = clampf((cbs - tb.c0) / tb.dc, 0.0f, (float)(tb.C - 1));
+            float xc = clampf(div_const(cbs - tb.c0, tb.dc, rdc), 0.0f, (float)(tb.C - 1));
             float i0f = clamp_max(floorf(xc), (float)(tb.C - 2));
             float wi = xc - i0f;
-            float b = bler_at(tb.bler, (m_look * tb.C + (int)i0f) * tb.G, tb.G, tb.s0, tb.ds, eff_used, wi);
+            float b = bler_at(tb.bler, (m_look * tb.C + (int)i0f) * tb.G, tb.G, tb.s0, tb.ds, rds, eff_used, wi);
             float p_err = 1.0f - pow_count(1.0f - b, ncb);
             float u = uniform_bits(elem_hash(mix32(base0 ^ row.salt_bler), (uint32_t)r));
             ok = tx && u >= p_err;
