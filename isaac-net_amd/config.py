@@ -160,6 +160,7 @@ class NRConfig:
     edge: object = None
     background: object = None
     energy: object = None
+    wifi: object = None               # WifiConfig of level "WIFI" (isaac_net_amd.wifi_config); None = defaults
 
     def __post_init__(self):
         assert self.mu in (0, 1, 2), "mu must be 0, 1 or 2 (FR1)"

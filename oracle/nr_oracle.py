@@ -319,15 +319,18 @@ class Radio:
                        for (k1, p1), (k2, p2) in zip(self.fields, new)]
 
     def pathgain(self, pos):
-        """Large-scale gain [E,R] dB of the poses (radio.py:238-277, models.py:137-167)."""
+        """Large-scale gain [E,R] dB of the poses (radio.py:275-277): rx_dbm - ue_tx_dbm."""
+        return (self.rx_dbm(pos) - self.cfg.ue_tx_dbm)[..., 0]
+
+    def rx_dbm(self, pos):
+        """Received power [E,R,1] dBm of the poses (radio.py:238-272, models.py:137-167)."""
         cfg = self.cfg
         if self.model == "log_distance":
             d = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
             pl = cfg.pl_const_db + (10 * cfg.pathloss_exp) * torch.log10(d)
             k, phi = self.fields[0]
             sh = eval_plane_waves(pos, k, phi, self.amp)
-            rx = cfg.ue_tx_dbm - pl - sh
-            return (rx - cfg.ue_tx_dbm)[..., 0]
+            return cfg.ue_tx_dbm - pl - sh
         d2 = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
         d3 = torch.sqrt(d2 * d2 + (self.h_bs - self.h_ut) ** 2)
         los = cfg.tr38901_los == "los"
@@ -336,8 +339,7 @@ class Radio:
         k, phi = self.fields[0] if los else self.fields[1]
         sf = (self.sig[0] if los else self.sig[1]) * eval_plane_waves(pos, k, phi, self.amp)
         loss = pl + sf
-        rx = cfg.ue_tx_dbm + (-loss)
-        return (rx - cfg.ue_tx_dbm)[..., 0]
+        return cfg.ue_tx_dbm + (-loss)
 
     def _pl_los(self, d2, d3):
         """tr38901.pl_los for UMa / UMi / InH / InF (tr38901.py:162-176)."""

@@ -42,3 +42,17 @@ def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)
             o = eng.step(None, x)
         if on_step is not None:
             on_step(s, o, acc)
+
+
+def load_wifi_case(path, NRConfig, WifiConfig):
+    """(arrays, NRConfig with its WifiConfig, input kind "snr" | "pose") of a level WIFI trajectory."""
+    d = np.load(path, allow_pickle=False)
+    cfg = json.loads(bytes(d["cfg_json"]).decode())
+    wc = json.loads(bytes(d["wifi_json"]).decode())
+    for k in ("msg_sizes", "cell_positions_m"):
+        if k in cfg:
+            cfg[k] = tuple(tuple(v) if isinstance(v, list) else v for v in cfg[k])
+    for k in ("class_ac", "ap_positions_m", "ap_channels"):
+        if wc.get(k) is not None:
+            wc[k] = tuple(tuple(v) if isinstance(v, list) else v for v in wc[k])
+    return d, NRConfig(**cfg, wifi=WifiConfig(**wc), seed=0), bytes(d["kind"]).decode()

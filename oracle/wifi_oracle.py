@@ -1,0 +1,407 @@
+"""CPU oracle of level WIFI (the mean-field 802.11 uplink).  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
+
+A from-scratch torch-CPU restatement of isaac-net's WifiNet with one access point, for the configs the HIP backend
+implements (one AP, so one collision domain; no hidden nodes; one AIFS zone):
+  LevelNet         core/levels/base.py:43-360 (clock, reset, submit, step, the regions' order)
+  add_body         core/proto/netsim_fast.py:136-160 (enqueue into FIFO slot count)
+  finish_body      core/proto/netsim_fast.py:185-206 (delivered / timed out, newest, det_env, stable compaction)
+  serve_fifo       core/proto/netsim.py:86-92
+  WifiNet          core/wifi/engine.py:100-403 (association, _serve: K sub-steps of mean-field solve, Poisson or
+                   renewal access counts, FIFO service, finish times, retry-limit loss, the extra outputs)
+  poisson_icdf     core/wifi/engine.py:57-63
+  meanfield.solve  core/wifi/meanfield.py:48-62 (stage factors, tau(p)), :65-73 (one domain), :106-209 (Z = 1)
+  AccessTiming     core/wifi/phy.py:107-155 (cap_bytes, times)
+  CounterRNG       core/proto/rng.py (STEP draws uniform(STEP, 0, K, R) and uniform(STEP, 1, R, F))
+  RadioMC          through oracle.nr_oracle.Radio on the APs' NRConfig (core/wifi/engine.py:82-97, 189-197)
+The element-wise operations, the reduction calls and their order are those of the reference, so that on the same CPU
+the oracle is bitwise equal to the reference (pinned by tests/golden/traj_w_*.npz, every state tensor and output
+after every step). The constants come from isaac_net_amd.wifi_config (pinned by the same fixtures' static tensors).
+
+Parity status: every function here is pinned by the five golden Wi-Fi trajectories, including both access-noise
+modes, RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background
+stations, both radio models and partial resets. Not implemented (refused, as by the HIP backend): several APs,
+hidden nodes, AIFS zones (Z > 1), roaming interruptions with several APs.
+"""
+from __future__ import annotations
+
+import torch
+
+from .nr_oracle import STEP, SUBMIT, CounterRNG, Radio
+
+INF = float("inf")
+PPDU_MAX_US = 5484.0
+
+
+class WifiOracle:
+    FIELDS = ("cap", "cls", "det", "hid", "rem", "dlv", "f_nact", "f_snr", "f_own")
+    INIT = {"cap": -1, "cls": 0, "det": False, "hid": -1, "rem": 0.0, "dlv": INF, "f_nact": 0, "f_snr": 0.0,
+            "f_own": 0}
+    DTYPE = {"cap": torch.long, "cls": torch.long, "det": torch.bool, "hid": torch.long, "rem": torch.float32,
+             "dlv": torch.float32, "f_nact": torch.long, "f_snr": torch.float32, "f_own": torch.long}
+
+    def __init__(self, E, R, cfg, seed=0):
+        from isaac_net_amd.wifi_config import WifiConfig, derive, radio_config
+        wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
+        assert len(wc.ap_xy(cfg)) == 1 and not wc.hidden_nodes, "one AP, no hidden nodes"
+        d = derive(cfg, wc)
+        assert d.Z == 1, "one AIFS zone"
+        self.cfg, self.wc, self.d, self.E, self.R = cfg, wc, d, E, R
+        self.K, self.F, self.timeout = d.K, cfg.frame_buffer, cfg.timeout_steps
+        self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
+        f = torch.float32
+        self.rates, self.thr = torch.from_numpy(d.rates), torch.from_numpy(d.thr)
+        self.mcs_ids = torch.from_numpy(d.mcs_ids)
+        self.ac_W0, self.ac_Wmax = torch.from_numpy(d.ac_W0), torch.from_numpy(d.ac_Wmax)
+        self.ac_aifsn, self.ac_txop = torch.from_numpy(d.ac_aifsn), torch.from_numpy(d.ac_txop)
+        self.cls_ac = torch.from_numpy(d.cls_ac)
+        self.bg_w = torch.full((E, 1), float(wc.bg_stations))
+        self.bg_rate = torch.full((E, 1), d.bg_rate, dtype=f)
+        self.bg_B = torch.full((E, 1), float(wc.bg_frame_bytes))
+        self.bg_ac = torch.full((E, 1), d.bg_ac, dtype=torch.long)
+        self.lgamma = torch.from_numpy(d.lgamma)
+        self.rng = CounterRNG(seed, E)
+        self.radio_cfg = radio_config(cfg, wc)
+        self.radio = None
+        self.roam_sub = int(round(wc.roam_ms / wc.substep_ms))
+        z = lambda shape, v, dt: torch.full(shape, v, dtype=dt)  # noqa: E731
+        for n in self.FIELDS:
+            setattr(self, n, z((E, R, self.F), self.INIT[n], self.DTYPE[n]))
+        self.clock = z((E,), 0, torch.long)
+        self.last_snr = z((E, R), 0.0, f)
+        self.last_hid = z((E,), 0, torch.long)
+        self.tau = z((E, R + 1), d.tau0, f)
+        self.roam_left = z((E, R), 0, torch.long)
+        self.att_n, self.att_logp, self.credit = z((E, R), 0.0, f), z((E, R), 0.0, f), z((E, R), 0.0, f)
+        self.serv = z((E, R), 0, torch.long)
+        self.pending = z((E,), True, torch.bool)
+        self.reset(None)
+
+    # ------------------------------------------------------------------ reset / clock (levels/base.py:142-157)
+    def reset(self, env_ids=None):
+        E = self.E
+        if env_ids is None:
+            m = torch.ones(E, dtype=torch.bool)
+            self.rng.reset_mask(None)
+        else:
+            m = torch.zeros(E, dtype=torch.bool)
+            m[torch.as_tensor(env_ids, dtype=torch.long)] = True
+            self.rng.reset_mask(m)
+        for n in self.FIELDS:
+            x = getattr(self, n)
+            x[m] = self.INIT[n]
+        self.clock[m] = 0
+        self.last_snr[m] = 0.0
+        self.last_hid[m] = 0
+        self.tau[m] = self.d.tau0
+        self.roam_left[m] = 0
+        self.att_n[m] = 0.0
+        self.att_logp[m] = 0.0
+        self.credit[m] = 0.0
+        self.serv[m] = 0
+        self.pending[m] = True
+        if self.radio is not None:
+            self.radio.reset(m)
+
+    def _tvec(self, t):
+        if t is None:
+            return self.clock.clone()
+        if torch.is_tensor(t):
+            t = t.to(torch.long)
+            return t.expand(self.E).clone() if t.dim() == 0 else t
+        return torch.full((self.E,), int(t), dtype=torch.long)
+
+    # ------------------------------------------------------------------ submit (base.py:223-246, add_body)
+    def submit(self, t, send, det=None, hid=None):
+        t = self._tvec(t)
+        send = send.to(torch.long)
+        det_in = torch.zeros_like(send, dtype=torch.bool) if det is None else det.to(torch.bool)
+        hid_in = torch.zeros(self.E, dtype=torch.long) if hid is None else hid.to(torch.long)
+        self.last_hid = hid_in.clone()
+        snr_in = self.last_snr.clone()
+        self.rng.ctr[SUBMIT] += 1
+        F = self.F
+        count = (self.cap >= 0).sum(-1)
+        new = (send > 0) & (count < F)
+        idx = count.clamp(max=F - 1)[..., None]
+        nact = ((count + new.long()) > 0).sum(-1)
+
+        def put(x, v):
+            cur = x.gather(-1, idx).squeeze(-1)
+            x.scatter_(-1, idx, torch.where(new, v.to(x.dtype), cur)[..., None])
+        put(self.cap, t[:, None].expand_as(send))
+        put(self.cls, send)
+        put(self.det, det_in)
+        put(self.hid, hid_in[:, None].expand_as(send))
+        put(self.rem, self.sizes[(send - 1).clamp(min=0)])
+        put(self.f_nact, nact[:, None].expand_as(send))
+        put(self.f_snr, snr_in)
+        put(self.f_own, count)
+        return new
+
+    # ------------------------------------------------------------------ association (wifi/engine.py:227-259)
+    def _snr_from(self, x):
+        E, R = self.E, self.R
+        if x.dim() == 3:
+            if self.radio is None:
+                self.radio = Radio(self.radio_cfg, E, self.rng)
+            rx = self.radio.rx_dbm(x[..., :2].to(torch.float32))
+        else:
+            rx = (x.to(torch.float32) + self.d.noise_dbm)[..., None]
+        best = rx.argmax(-1)
+        cur = rx.gather(-1, self.serv[..., None])[..., 0]
+        better = rx.max(-1).values > cur + self.wc.roam_hyst_db
+        pend = self.pending[:, None].expand(E, R)
+        roam = better & ~pend & (best != self.serv)
+        new = torch.where(pend | roam, best, self.serv)
+        self.serv = new.clone()
+        self.pending = torch.zeros_like(self.pending)
+        if self.roam_sub > 0:
+            self.roam_left = torch.where(roam, torch.full_like(self.roam_left, self.roam_sub), self.roam_left)
+        self.serv_out = new.clone()
+        return rx.gather(-1, new[..., None])[..., 0] - self.d.noise_dbm
+
+    # ------------------------------------------------------------------ PHY timing (wifi/phy.py:130-155)
+    def _cap_bytes(self, rate, txop):
+        wc, d = self.wc, self.d
+        if wc.max_ampdu_bytes == 0:
+            return torch.full_like(rate, float(wc.msdu_payload_bytes))
+        tmax = torch.where(txop > 0, torch.clamp(txop, max=PPDU_MAX_US), torch.full_like(txop, PPDU_MAX_US))
+        by_time = (tmax - d.pre) * rate / 8.0 / d.ovh1
+        return torch.clamp(by_time, max=d.ampdu_lim).clamp(min=float(wc.msdu_payload_bytes))
+
+    def _times(self, B, rate, aifsn):
+        wc, d = self.wc, self.d
+        aifs = wc.sifs_us + aifsn * wc.slot_us
+        nsym = torch.ceil((22.0 + 8.0 * (B * d.ovh1)) / (rate * d.tsym))
+        tdata = d.pre + d.tsym * nsym
+        if wc.rts_cts:
+            hs = d.t_rts + wc.sifs_us + d.t_cts + wc.sifs_us
+            ts = aifs + hs + tdata + wc.sifs_us + d.t_ack
+            tc = aifs + d.t_rts + wc.sifs_us + d.t_cts
+        else:
+            ts = aifs + tdata + wc.sifs_us + d.t_ack
+            tc = ts if wc.collision_time == "ack" else aifs + tdata
+        return ts, tc
+
+    # ------------------------------------------------------------------ mean field, one domain, Z = 1
+    @staticmethod
+    def _dom_sum(x):
+        """Sum over the stations of the env (one collision domain), broadcast back."""
+        return x.sum(-1, keepdim=True).expand_as(x)
+
+    @staticmethod
+    def _stage_factors(W0, Wm, L):
+        k = torch.arange(int(L), dtype=W0.dtype)
+        Wk = torch.minimum(W0[..., None] * torch.exp2(k.clamp(max=60)), Wm[..., None])
+        return (Wk + 1.0) * 0.5
+
+    def _fail(self, w, tau, active):
+        """(p, success probability, S = sum_j w_j log(1 - tau_j)) of every station."""
+        lt = torch.log1p(-tau)
+        S = self._dom_sum(w * lt)
+        own = torch.where(active, lt, torch.zeros_like(lt))
+        ok = torch.exp(S - own) * 1.0 * (1.0 - self.wc.frame_error_rate)
+        num = torch.zeros_like(tau) + torch.ones_like(tau) * ok
+        O = torch.zeros_like(tau) + torch.ones_like(tau)
+        return 1.0 - num / O.clamp(min=1e-12), num, S
+
+    def _solve(self, w, Ts, Tc, tau, Wfac):
+        wc = self.wc
+        active = w > 0
+        k = torch.arange(Wfac.shape[-1], dtype=torch.float32)
+        for _ in range(int(wc.fp_iters)):
+            tau = tau.clamp(1e-7, 0.999)
+            p, _, _ = self._fail(w, tau, active)
+            pk = p[..., None] ** k
+            tau = tau + wc.fp_damping * (pk.sum(-1) / (pk * Wfac).sum(-1) - tau)
+        tau = tau.clamp(1e-7, 0.999)
+        p, succ, S = self._fail(w, tau, active)
+        r = w * tau / (1.0 - tau)
+        wt = w * tau
+        idle = torch.exp(S)
+        a0, a1 = self._dom_sum(r), self._dom_sum(r * Ts)
+        gd, g = self._dom_sum(wt), self._dom_sum(wt * Tc)
+        p_coll = (1.0 - idle - idle * a0).clamp(min=0.0)
+        tc = g / gd.clamp(min=1e-12)
+        tslot = torch.zeros_like(tau) + torch.ones_like(tau) * (wc.slot_us * idle + idle * a1 + p_coll * tc)
+        p_idle = torch.zeros_like(tau) + torch.ones_like(tau) * idle
+        mu = torch.where(active, tau * succ / tslot, torch.zeros_like(tau))
+        return tau, p, mu, p_idle
+
+    def _poisson(self, lam, u):
+        """poisson_icdf (wifi/engine.py:57-63) with the lgamma(k + 1) table of the derived constants."""
+        k = torch.arange(self.d.n_acc_max, dtype=lam.dtype)
+        logpmf = k * torch.log(lam.clamp(min=1e-30))[..., None] - lam[..., None] - self.lgamma
+        cdf = torch.exp(logpmf).cumsum(-1)
+        return (u[..., None] > cdf).sum(-1).to(lam.dtype)
+
+    @staticmethod
+    def _serve_fifo(rem, b):
+        cum = rem.cumsum(-1)
+        newcum = (cum - b[..., None]).clamp(min=0)
+        new = torch.diff(newcum, dim=-1, prepend=torch.zeros_like(newcum[..., :1]))
+        fin = (rem > 0) & (new <= 1e-3)
+        return torch.where(fin, torch.zeros_like(new), new), fin
+
+    # ------------------------------------------------------------------ the control step
+    def _serve(self, t, snr):
+        """WifiNet._serve (wifi/engine.py:292-403) for one domain and Z = 1: finish times [E,R,F]."""
+        wc, d, E, R, K, F = self.wc, self.d, self.E, self.R, self.K, self.F
+        u_acc = self.rng._draw(self.rng.ctr[STEP], STEP, 0, K * R, False).view(E, K, R)
+        u_loss = self.rng._draw(self.rng.ctr[STEP], STEP, 1, R * F, False).view(E, R, F)
+        nm = (snr[..., None] >= self.thr).sum(-1)
+        link = nm > 0
+        mcs = (nm - 1).clamp(min=0)
+        rate = self.rates[mcs]
+        rem, cls, tau, roam = self.rem, self.cls, self.tau, self.roam_left
+        att_n, att_logp, credit = self.att_n, self.att_logp, self.credit
+        fin_t = torch.full_like(rem, INF)
+        tf = t.to(torch.float32)[:, None, None]
+        size = self.sizes[(cls - 1).clamp(min=0)]
+        zero = torch.zeros(E, R)
+        acc_sum, acc_n, p_sum, busy_sum = zero.clone(), zero.clone(), zero.clone(), zero.clone()
+        rateN = torch.cat([rate, self.bg_rate], -1)
+        L = wc.max_tx
+
+        def ac_params(ac):
+            W0, Wm = self.ac_W0[ac], self.ac_Wmax[ac]
+            return W0, Wm, self.ac_aifsn[ac], self._cap_bytes(rate, self.ac_txop[ac][:, :R]), \
+                self._stage_factors(W0, Wm, L)
+
+        if not d.per_class_ac:
+            ac0 = torch.cat([self.cls_ac[torch.ones_like(snr, dtype=torch.long)], self.bg_ac], -1)
+            W0, Wm, aifsn, cap, Wfac = ac_params(ac0)
+        for k in range(K):
+            q = rem.sum(-1)
+            act = (q > 0) & link & (roam <= 0)
+            if d.per_class_ac:
+                hol = (rem > 0).to(torch.float32).argmax(-1)
+                ac = torch.cat([self.cls_ac[cls.gather(-1, hol[..., None])[..., 0]], self.bg_ac], -1)
+                W0, Wm, aifsn, cap, Wfac = ac_params(ac)
+            B = torch.where(act, torch.minimum(q, cap), cap)
+            BN = torch.cat([B, self.bg_B], -1)
+            w = torch.cat([act.to(torch.float32), self.bg_w], -1)
+            Ts, Tc = self._times(BN, rateN, aifsn)
+            tau, p, mu, p_idle = self._solve(w, Ts, Tc, tau, Wfac)
+            mu, p = mu[:, :R], p[:, :R]
+            lam = mu * d.dt_us
+            if wc.access_noise == "poisson":
+                n_acc = self._poisson(lam, u_acc[:, k])
+            else:
+                c1 = credit + lam * act
+                n_acc = torch.floor(c1)
+            served = torch.minimum(q, n_acc * B) * act
+            cum = rem.cumsum(-1)
+            rem_new, fin = self._serve_fifo(rem, served)
+            j = torch.ceil(cum / B[..., None] - 1e-6).clamp(min=1.0)
+            if wc.access_noise == "poisson":
+                frac = j / (n_acc[..., None] + 1.0)
+            else:
+                frac = (j - credit[..., None]) / lam[..., None].clamp(min=1e-9)
+                credit = torch.where(act, torch.where(rem_new.sum(-1) > 0, c1 - n_acc, torch.zeros_like(c1)), credit)
+            frac = frac.clamp(0.0, 1.0)
+            tfin = torch.minimum(tf + (k + frac) / K, tf + 1 - 1e-6)
+            back = q > 0
+            att_n = torch.where(back, att_n + act.to(torch.float32), torch.zeros_like(att_n))
+            lp = torch.where(act, torch.log(p.clamp(min=1e-12)), torch.zeros_like(p))
+            att_logp = torch.where(back, att_logp + lp, torch.zeros_like(att_logp))
+            p_bar = torch.where(att_n > 0, torch.exp(att_logp / att_n.clamp(min=1e-12)), p)
+            n_frame = torch.ceil(size / B[..., None]).clamp(min=1.0)
+            p_lost = 1.0 - (1.0 - p_bar[..., None] ** L) ** n_frame
+            ok = fin & ~(u_loss < p_lost)
+            fin_t = torch.where(ok, tfin, fin_t)
+            rem = rem_new
+            roam = (roam - 1).clamp(min=0)
+            actf = act.to(torch.float32)
+            acc_sum = acc_sum + torch.where(act, 1.0 / mu.clamp(min=1e-12), torch.zeros_like(mu))
+            acc_n = acc_n + actf
+            p_sum = p_sum + p * actf
+            busy_sum = busy_sum + (1.0 - p_idle[:, :R])
+        self.rem = rem
+        self.tau = tau
+        self.roam_left = roam
+        keep = rem.sum(-1) > 0
+        self.credit = torch.where(keep, credit, torch.zeros_like(credit))
+        self.att_n = torch.where(keep, att_n, torch.zeros_like(att_n))
+        self.att_logp = torch.where(keep, att_logp, torch.zeros_like(att_logp))
+        nan = torch.full_like(acc_sum, float("nan"))
+        self.o_access = torch.where(acc_n > 0, acc_sum / acc_n.clamp(min=1) / 1000.0, nan)
+        self.o_pfail = torch.where(acc_n > 0, p_sum / acc_n.clamp(min=1), nan)
+        self.o_busy = busy_sum / K
+        self.o_mcs = torch.where(link, self.mcs_ids[mcs], torch.full_like(mcs, -1))
+        self.o_rate = torch.where(link, rate, torch.zeros_like(rate))
+        return fin_t
+
+    def _finish(self, fin, t, cur_hid):
+        """finish_body (netsim_fast.py:185-206)."""
+        cap, cls, det, hid = self.cap, self.cls, self.det, self.hid
+        delivered = (cap >= 0) & torch.isfinite(fin)
+        newest = torch.where(delivered, cap, torch.full_like(cap, -1)).max(-1).values
+        det_env = (delivered & det & (hid == cur_hid[:, None, None])).flatten(1).any(-1)
+        timed = (cap >= 0) & ~delivered & ((t[:, None, None] + 1 - cap) >= self.timeout)
+        delay = torch.where(delivered, fin - cap.float(), torch.full_like(fin, float("nan")))
+        cap_out, cls_out = cap.clone(), cls.clone()
+        gone = delivered | timed
+        vals = {"cap": torch.where(gone, torch.full_like(cap, -1), cap), "cls": cls, "det": det & ~gone, "hid": hid,
+                "rem": torch.where(gone, torch.zeros_like(self.rem), self.rem),
+                "dlv": torch.where(gone, torch.full_like(self.dlv, INF), self.dlv),
+                "f_nact": self.f_nact, "f_snr": self.f_snr, "f_own": self.f_own}
+        vi = (vals["cap"] >= 0).long()
+        dest = torch.where(vi > 0, vi.cumsum(-1) - 1, vi.sum(-1, keepdim=True) + (1 - vi).cumsum(-1) - 1)
+        for n in self.FIELDS:
+            setattr(self, n, torch.empty_like(vals[n]).scatter_(-1, dest, vals[n]))
+        return newest, det_env, delivered, timed, delay, cap_out, cls_out
+
+    def step(self, t, x):
+        """Advance [t, t+1): x = SNR [E,R] dB (one AP) or poses [E,R,2|3]. The reference's step dict."""
+        t = self._tvec(t)
+        snr = self._snr_from(x)
+        self.last_snr = snr.clone()
+        cur_hid = self.last_hid.clone()
+        self.rng.ctr[STEP] += 1
+        fin = self._serve(t, snr)
+        newest, det_env, delivered, timed, delay, cap_out, cls_out = self._finish(fin, t, cur_hid)
+        out = {"newest": newest, "det_env": det_env, "delivered": delivered, "timed_out": timed, "cap": cap_out,
+               "cls": cls_out, "delay": delay, "queue_len": (self.cap >= 0).sum(-1), "queue_bytes": self.rem.sum(-1),
+               "sinr_db": snr.clone(), "t": t.clone(), "serving_cell": self.serv_out.clone(),
+               "wifi_mcs": self.o_mcs, "wifi_rate_mbps": self.o_rate, "wifi_access_ms": self.o_access,
+               "wifi_p_fail": self.o_pfail, "wifi_busy": self.o_busy}
+        self.clock = t + 1
+        return out
+
+    # ------------------------------------------------------------------ state under the reference's state_dict names
+    STATE = ("clock", "_last_snr", "_last_hid", "tau", "roam_left", "att_n", "att_logp", "credit", "serv", "pending")
+    _ATTR = {"_last_snr": "last_snr", "_last_hid": "last_hid"}
+
+    def state(self):
+        sd = {n: getattr(self, n).clone() for n in self.FIELDS}
+        for n in self.STATE:
+            sd[n] = getattr(self, self._ATTR.get(n, n)).clone()
+        sd["rng.episode"] = self.rng.episode.clone()
+        sd["rng.ctr[1]"] = self.rng.ctr[SUBMIT].clone()
+        sd["rng.ctr[2]"] = self.rng.ctr[STEP].clone()
+        if self.radio is not None:
+            for key, val in self._radio_keys().items():
+                sd[key] = val.clone()
+        return sd
+
+    def _radio_keys(self):
+        f = self.radio.fields
+        if self.radio.model == "log_distance":
+            return {"radio.k": f[0][0], "radio.phi": f[0][1]}
+        out = {}
+        for j, n in enumerate(("sf_los", "sf_nlos", "los_field")):
+            out[f"radio.ch.{n}.k"], out[f"radio.ch.{n}.phi"] = f[j]
+        return out
+
+    def load_state(self, sd):
+        for n in self.FIELDS + self.STATE:
+            if n in sd:
+                v = torch.as_tensor(sd[n])
+                setattr(self, self._ATTR.get(n, n), v.clone().to(getattr(self, self._ATTR.get(n, n)).dtype))
+        self.rng.episode = torch.as_tensor(sd["rng.episode"]).clone()
+        self.rng.ctr[SUBMIT] = torch.as_tensor(sd["rng.ctr[1]"]).clone()
+        self.rng.ctr[STEP] = torch.as_tensor(sd["rng.ctr[2]"]).clone()

@@ -9,7 +9,10 @@ reference is copied. The vectors pin what no closed form or known answer pins:
     tie order), isaac_net/core/nr_engine.py:613-668, core/mac.py:228-508;
   * the processed BLER table and thr_ref (core/phy.py:234-243, 405-482);
   * the plane-wave shadowing draws of the radio (core/radio.py:185-189, core/channels/fields.py:38-64);
-  * the eager _finish / compaction output layout (core/nr_engine.py:843-888, core/queues.py:105-110).
+  * the eager _finish / compaction output layout (core/nr_engine.py:843-888, core/queues.py:105-110);
+  * level WIFI trajectories (core/wifi/engine.py:100-403 WifiNet on the levels/base.py:43-360 FIFO): the mean-field
+    solve per sub-step (core/wifi/meanfield.py:187-209), the Poisson / renewal access counts, the FIFO service and the
+    retry-limit loss, with SNR inputs and with poses through the APs' radio.
 
 Usage:  python tests/golden/make_fixtures.py            (writes tests/golden/*.npz)
 """
@@ -76,13 +79,56 @@ CASES = {
 }
 
 
+# Level WIFI cases (make_engine("WIFI", ...)): NRConfig fields, WifiConfig fields, sizes, inputs and resets.
+WIFI_CASES = {
+    # defaults (802.11ax 20 MHz, BE, A-MPDU, Poisson accesses), SNR input over the whole MCS range and below MCS 0
+    "w_snr": dict(cfg=dict(control_step_ms=10.0, frame_buffer=8, msg_sizes=(1500.0,), timeout_steps=5),
+                  wifi=dict(), E=3, R=8, steps=30, kind="snr", snr=(-2.0, 42.0), rates=(2.5,), resets={12: [1]}),
+    # renewal ("mean") accesses, RTS/CTS, ACK collision time, no aggregation, VI (TXOP limit), residual FER, few
+    # attempts, VHT 40 MHz, two classes, short FIFO and timeout
+    "w_mean": dict(cfg=dict(control_step_ms=5.0, frame_buffer=6, msg_sizes=(200.0, 3000.0), timeout_steps=3),
+                   wifi=dict(access_noise="mean", rts_cts=True, collision_time="ack", max_ampdu_bytes=0,
+                             access_category="VI", frame_error_rate=0.1, max_tx=3, standard="ac", bandwidth_mhz=40),
+                   E=3, R=8, steps=30, kind="snr", snr=(4.0, 40.0), rates=(2.0, 0.8), resets={9: [0, 2]}),
+    # poses through the log-distance radio of one AP, non-HT 802.11a, rate margin, background stations, undamped
+    # solve with 3 iterations, 16 robots
+    "w_logd": dict(cfg=dict(control_step_ms=10.0, frame_buffer=12, msg_sizes=(1500.0,), timeout_steps=6,
+                            cell_positions_m=((40.0, 40.0),)),
+                   wifi=dict(standard="a", ra_margin_db=2.0, bg_stations=2, fp_iters=3, fp_damping=1.0, max_tx=4),
+                   E=2, R=16, steps=25, kind="pose", arena=80.0, walk=1.0, rates=(1.0,), resets={10: [1]}),
+    # poses through TR 38.901 UMi LOS, one AC per message class (VO / VI: same AIFSN), HE 80 MHz 2 streams, 2 ms
+    # sub-steps
+    "w_tr": dict(cfg=dict(control_step_ms=8.0, frame_buffer=10, msg_sizes=(400.0, 2500.0), timeout_steps=4,
+                          channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                          cell_positions_m=((75.0, 75.0),)),
+                 wifi=dict(class_ac=("VO", "VI"), bandwidth_mhz=80, n_ss=2, gi_us=1.6, substep_ms=2.0,
+                           ap_height_m=6.0),
+                 E=3, R=8, steps=25, kind="pose", arena=150.0, walk=2.0, rates=(1.5, 0.5), resets={15: [2]}),
+    # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
+    # AP, 1500 B messages, 20 sub-steps per control step
+    "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),
+                           cell_positions_m=((0.0, 0.0),)),
+                  wifi=dict(access_category="DCF"),
+                  E=4, R=16, steps=20, kind="disc", radius=50.0, walk=0.5, rates=(2.0,), resets={8: [3]}),
+}
+
+
 def _inputs(name, c):
     """Per-step inputs of a case: poses or SNR, and per-class arrival counts (numpy, seeded by the case name)."""
     rs = np.random.default_rng(int.from_bytes(hashlib.sha256(name.encode()).digest()[:4], "little"))
     E, R, T = c["E"], c["R"], c["steps"]
     n_cls = len(c["rates"])
     counts = np.stack([rs.poisson(lam, size=(T, E, R)) for lam in c["rates"]], -1).astype(np.int64)
-    if c["kind"] == "pose":
+    if c["kind"] == "disc":
+        rad, ang0 = c["radius"] * np.sqrt(rs.uniform(size=(E, R))), rs.uniform(0.0, 2 * math.pi, size=(E, R))
+        p = np.stack([rad * np.cos(ang0), rad * np.sin(ang0)], -1)
+        xs = []
+        for _ in range(T):
+            xs.append(p.copy())
+            ang = rs.uniform(0.0, 2 * math.pi, size=(E, R))
+            p = p + c["walk"] * np.stack([np.cos(ang), np.sin(ang)], -1)
+        x = np.stack(xs).astype(np.float32)
+    elif c["kind"] == "pose":
         a = c["arena"]
         p = rs.uniform(0.0, a, size=(E, R, 2))
         xs = []
@@ -170,6 +216,63 @@ def run_case(name, c):
     print(name, "state keys:", len(keys_seen), "arrays:", len(out))
 
 
+def run_wifi_case(name, c):
+    """A level WIFI trajectory: per step the submits (one call per class and message index), the step dict and the
+    engine's state_dict() after the step (FIFO, clock, mean-field state, counter RNG, radio)."""
+    sys.path.insert(0, REF)
+    from isaac_net.core.config import NRConfig
+    from isaac_net.core.engine import make_engine
+    from isaac_net.core.wifi import WifiConfig
+    cfg = NRConfig(**c["cfg"], wifi=WifiConfig(**c["wifi"]), seed=0)
+    E, R, T = c["E"], c["R"], c["steps"]
+    eng = make_engine("WIFI", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
+    x, counts = _inputs(name, c)
+    out = {"x": x, "counts": counts, "E": np.int64(E), "R": np.int64(R), "steps": np.int64(T),
+           "cfg_json": np.frombuffer(json.dumps(c["cfg"]).encode(), dtype=np.uint8),
+           "wifi_json": np.frombuffer(json.dumps(c["wifi"]).encode(), dtype=np.uint8),
+           "kind": np.frombuffer(("snr" if c["kind"] == "snr" else "pose").encode(), dtype=np.uint8),
+           "K": np.int64(eng.Ksub), "n_acc_max": np.int64(eng.n_acc_max)}
+    reset_mask = np.zeros((T, E), dtype=np.bool_)
+    for s, ids in c["resets"].items():
+        reset_mask[s, ids] = True
+    out["reset_mask"] = reset_mask
+
+    dynamic = ("cap", "cls", "det", "hid", "rem", "dlv", "f_nact", "f_snr", "f_own", "clock", "_last_snr",
+               "_last_hid", "tau", "roam_left", "att_n", "att_logp", "credit", "serv", "pending", "rng.episode",
+               "rng.ctr[1]", "rng.ctr[2]")
+
+    def snap(prefix, full=False):
+        """full: every tensor of state_dict() but generator states; else the state that a step or reset changes
+        (and the radio's plane waves)."""
+        for k, v in eng.state_dict().items():
+            if not torch.is_tensor(v) or k.endswith("gen"):
+                continue
+            if full or k in dynamic or (k.startswith("radio.") and k.endswith((".k", ".phi"))):
+                out[f"{prefix}/{k}"] = _np(v)
+
+    snap("init", full=True)
+    for s in range(T):
+        ids = np.nonzero(reset_mask[s])[0]
+        if len(ids):
+            eng.reset(torch.tensor(ids, dtype=torch.long))
+            snap(f"reset{s:03d}")
+        acc_all = []
+        for ci in range(counts.shape[-1]):
+            n = torch.from_numpy(counts[s, :, :, ci])
+            for i in range(int(n.max())):
+                send = torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n))
+                acc_all.append(_np(eng.submit(None, send)))
+        out[f"s{s:03d}/n_submit"] = np.int64(len(acc_all))
+        if acc_all:
+            out[f"s{s:03d}/accepted"] = np.stack(acc_all)
+        o = eng.step(None, torch.from_numpy(x[s]))
+        for k, v in o.items():
+            out[f"s{s:03d}/out.{k}"] = _np(v)
+        snap(f"s{s:03d}")
+    np.savez_compressed(os.path.join(HERE, f"traj_{name}.npz"), **out)
+    print(name, "arrays:", len(out))
+
+
 def phy_tables():
     """Processed PHY tables of both MCS tables (core/phy.py PHY): BLER table, grids, betas, thresholds, TBS."""
     NRConfig, make_engine, state_dict, Requests = _ref()
@@ -231,8 +334,12 @@ def rng_vectors():
 
 if __name__ == "__main__":
     torch.set_num_threads(1)
-    names = sys.argv[1:] or list(CASES)
-    rng_vectors()
-    phy_tables()
+    names = sys.argv[1:] or list(CASES) + list(WIFI_CASES)
+    if not sys.argv[1:]:
+        rng_vectors()
+        phy_tables()
     for n in names:
-        run_case(n, CASES[n])
+        if n in WIFI_CASES:
+            run_wifi_case(n, WIFI_CASES[n])
+        else:
+            run_case(n, CASES[n])
