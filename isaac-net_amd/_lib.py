@@ -1,4 +1,5 @@
-"""ctypes binding of libinet_nr.so (include/inet_nr.h). No torch types cross the ABI: only pointers and sizes."""
+"""ctypes binding of libinet_nr.so (include/inet_nr.h, include/inet_wifi.h). No torch types cross the ABI: only
+pointers and sizes."""
 from __future__ import annotations
 
 import ctypes as C
@@ -42,11 +43,45 @@ class InetNrOutputs(C.Structure):
                                  "newest", "queue_len", "serving_cell", "queue_bytes", "sinr_db", "det_env", "t")]
 
 
+class InetWifiState(C.Structure):
+    _fields_ = [(n, P) for n in (
+        "cap", "cls", "det", "hid", "rem", "f_nact", "f_snr", "f_own", "qlen", "last_snr", "roam_left", "serv",
+        "att_n", "att_logp", "credit", "tau", "clock", "last_hid", "pending", "env_id", "episode", "ctr_step",
+        "ctr_submit", "field")]
+
+
+WIFI_MAX_M, WIFI_MAX_CLS, WIFI_MAX_NACC = 16, 16, 128
+
+
+class InetWifiParams(C.Structure):
+    _fields_ = [(n, i32) for n in (
+        "E", "R", "F", "K", "M", "L", "n_cls", "n_acc_max", "fp_iters", "timeout", "access_noise", "rts_cts",
+        "coll_ack", "per_class_ac", "no_aggr", "radio_model", "n_fields", "n_modes", "seed_key", "roam_sub", "bg_ac",
+        "envs_per_wave", "spectrum", "pad0")] + \
+               [(n, f32) for n in (
+        "noise_dbm", "roam_hyst", "damp", "fer1", "dt_us", "tau0", "slot_us", "sifs_us", "pre", "tsym", "ovh1",
+        "t_ack", "t_rts", "t_cts", "hs", "ampdu_lim", "msdu_payload", "ppdu_max", "bg_w", "bg_rate", "bg_B")] + \
+               [("dcorr", f32 * 3), ("rates", f32 * WIFI_MAX_M), ("thr", f32 * WIFI_MAX_M),
+                ("mcs_ids", i32 * WIFI_MAX_M), ("ac_W0", f32 * 5), ("ac_Wmax", f32 * 5), ("ac_aifsn", f32 * 5),
+                ("ac_txop", f32 * 5), ("cls_ac", i32 * (WIFI_MAX_CLS + 1)), ("sizes", f32 * WIFI_MAX_CLS),
+                ("lgamma", f32 * WIFI_MAX_NACC)] + \
+               [(n, f32) for n in (
+        "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1", "nl_b0", "nl_c", "nl_d", "sig",
+        "amp", "pl_const", "pl_exp10", "ue_tx")] + [("pad1", i32)]
+
+
+class InetWifiOutputs(C.Structure):
+    _fields_ = [(n, P) for n in ("delivered", "timed_out", "cap", "cls", "delay", "newest", "queue_len",
+                                 "serving_cell", "mcs", "queue_bytes", "sinr_db", "rate_mbps", "access_ms", "p_fail",
+                                 "busy", "det_env", "t")]
+
+
 ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fade", "salt_bler")   # 8 x 4 bytes
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
 ABI_VERSION = 2
+WIFI_ABI_VERSION = 1
 _LIB = None
 
 
@@ -69,7 +104,15 @@ def load(path=LIB_PATH):
     lib.inet_nr_reset.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), P, i64, f32, C.POINTER(f32), i32,
                                   P]
     lib.inet_nr_reset.restype = i32
-    if lib.inet_nr_abi_version() != ABI_VERSION:
+    lib.inet_wifi_abi_version.restype = i32
+    lib.inet_wifi_step.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, i32, P, P,
+                                   C.POINTER(InetWifiOutputs), P]
+    lib.inet_wifi_step.restype = i32
+    lib.inet_wifi_submit.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, P, P, P, P, P, i32, P, P]
+    lib.inet_wifi_submit.restype = i32
+    lib.inet_wifi_reset.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, P]
+    lib.inet_wifi_reset.restype = i32
+    if lib.inet_nr_abi_version() != ABI_VERSION or lib.inet_wifi_abi_version() != WIFI_ABI_VERSION:
         raise RuntimeError("libinet_nr.so ABI version mismatch; rebuild it")
     _LIB = lib
     return lib

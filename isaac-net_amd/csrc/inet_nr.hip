@@ -16,8 +16,6 @@ namespace {
 
 constexpr uint32_t CH_RESET = 3;
 constexpr uint32_t SITE_H0 = 4, SITE_KPHI = 6;
-constexpr uint32_t LOG_DISTANCE_STREAM = 10;
-constexpr uint32_t TR38901_STREAM = (0x52u << 16) + 16u;
 
 }  // namespace
 
@@ -123,25 +121,8 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
     const float dcs[3] = {dc0, dc1, dc2};
     for (int q = threadIdx.x; q < pm.n_fields * K; q += blockDim.x) {
         int fi = q / K, kk = q - fi * K;
-        uint32_t st0 = pm.radio_model == 1 ? TR38901_STREAM + 3u * fi : LOG_DISTANCE_STREAM;
-        float u0 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 0u), (uint32_t)kk));
-        float u1 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 1u), (uint32_t)kk));
-        float u2 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET, 0u, st0 + 2u), (uint32_t)kk));
-        float ang = (u0 * 2.0f) * (float)3.141592653589793;          // rand * 2 * pi, in that order
-        float kmag;
-        if (spectrum == 0) {                                          // "sos": wavelengths 20..60 m
-            float wl = 20.0f + 40.0f * u1;
-            if (dcs[fi] != 10.3f) wl = wl * (float)((double)dcs[fi] / 10.3);
-            kmag = (1.0f / wl) * (float)6.283185307179586;            // 2 pi / wl = reciprocal(wl) * 2 pi
-        } else {                                                      // "exp": inverse CDF of the radial spectrum
-            float u = clamp_max(u1, (float)(1.0 - 1e-6));
-            float a = 1.0f - u;
-            kmag = sqrtf(1.0f / (a * a) - 1.0f) / dcs[fi];
-        }
-        float* fp = st.field + (((size_t)e * pm.n_fields + fi) * K + kk) * 3;
-        fp[0] = (float)cos((double)ang) * kmag;
-        fp[1] = (float)sin((double)ang) * kmag;
-        fp[2] = (u2 * 2.0f) * (float)3.141592653589793;
+        draw_plane_wave(s0, env, ep, pm.radio_model, fi, kk, dcs[fi], spectrum,
+                        st.field + (((size_t)e * pm.n_fields + fi) * K + kk) * 3);
     }
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -149,6 +149,115 @@ DEV float aten_lse(const float* x) {
     return logf(aten_sum<N>(e)) + mx;
 }
 
+// torch CPU float sum of a contiguous row of n < 512 elements x(0..n-1), n known at run time (same order as
+// aten_sum<N>: rows of 8 or more are 8-lane vectors accumulated in four interleaved partial vectors, the tail elements
+// summed first, then the vector lanes in order; shorter rows use four interleaved scalar partial sums)
+template <class X>
+DEV float aten_row_sum(int n, X x) {
+    if (n < 8) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        const int si = n >> 2;
+        for (int i = 0; i < si; ++i) { a0 += x(i * 4); a1 += x(i * 4 + 1); a2 += x(i * 4 + 2); a3 += x(i * 4 + 3); }
+        for (int i = si * 4; i < n; ++i) a0 += x(i);
+        return ((a0 + a1) + a2) + a3;
+    }
+    const int nv = n >> 3, ni = nv >> 2;
+    float fin = 0.f;
+    for (int i = nv * 8; i < n; ++i) fin += x(i);
+    for (int l = 0; l < 8; ++l) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        for (int i = 0; i < ni; ++i) {
+            a0 += x((i * 4) * 8 + l); a1 += x((i * 4 + 1) * 8 + l);
+            a2 += x((i * 4 + 2) * 8 + l); a3 += x((i * 4 + 3) * 8 + l);
+        }
+        for (int i = ni * 4; i < nv; ++i) a0 += x(i * 8 + l);
+        fin += ((a0 + a1) + a2) + a3;
+    }
+    return fin;
+}
+
+// ---------------------------------------------------------------- radio (RadioMC.rx_dbm at one cell / AP)
+// Received power (dBm) of a robot at (px, py) from the cell's path loss and plane-wave shadowing
+// (isaac_net/core/radio.py:238-272, channels/models.py:137-167, channels/tr38901.py:162-203 with a fixed LOS state).
+// PM: a parameter struct with the radio fields of InetNrParams (gnb_x ... pl_exp10, ue_tx, radio_model, n_modes);
+// fld_env: the env's fields [n_fields][n_modes][3] (kx, ky, phase). The transcendental functions are evaluated in
+// double precision and rounded once (the field arguments k . x reach 1e4 rad).
+template <class PM>
+DEV float radio_rx_dbm(const PM& pm, float px, float py, const float* fld_env) {
+    float dx = px - pm.gnb_x, dy = py - pm.gnb_y;
+    float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
+    int fi = 0;
+    float pl;
+    if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203), deterministic LOS state
+        float d3 = sqrtf(d2 * d2 + pm.hh2);
+        float lg = (float)log10((double)d3);
+        float pl1 = (pm.pl_a + pm.pl_n1 * lg) + pm.pl_c20;
+        float pl2 = ((pm.pl_a + 40.0f * lg) + pm.pl_c20) - pm.pl_c2;
+        pl = d2 <= pm.dbp ? pl1 : pl2;
+        if (pm.nl_b1 != 0.0f) {                // NLOS: max(PL_LOS, PL'_NLOS)
+            float pn = ((pm.nl_b1 * lg + pm.nl_b0) + pm.nl_c) - pm.nl_d;
+            pl = pn > pl ? pn : pl;
+            fi = 1;
+        }
+    } else {
+        pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
+    }
+    const float* fld = fld_env + fi * pm.n_modes * 3;
+    float cs[16];
+    for (int k = 0; k < pm.n_modes; ++k) {
+        float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
+        cs[k] = (float)cos((double)arg);
+    }
+    // runtime-length ATen row sum (n_modes <= 16)
+    float field;
+    if (pm.n_modes >= 8) {
+        field = 0.f;
+        for (int k = 8; k < pm.n_modes; ++k) field += cs[k];
+        for (int l = 0; l < 8; ++l) field += cs[l];
+    } else {
+        float q[4] = {0.f, 0.f, 0.f, 0.f};
+        const int si = pm.n_modes / 4;
+        for (int i = 0; i < si; ++i)
+            for (int k = 0; k < 4; ++k) q[k] += cs[i * 4 + k];
+        for (int i = si * 4; i < pm.n_modes; ++i) q[0] += cs[i];
+        field = ((q[0] + q[1]) + q[2]) + q[3];
+    }
+    field = pm.amp * field;
+    if (pm.radio_model == 1) {
+        float loss = pl + pm.sig * field;
+        return pm.ue_tx + (-loss);
+    }
+    return (pm.ue_tx - pl) - field;
+}
+
+// One plane wave kk of shadowing field fi drawn for (seed key, env, episode) (channels/fields.py:38-58,
+// radio.py:185-189): stream LOG_DISTANCE (10) for the log-distance field, TR38901 + 3 fi for the TR 38.901 fields;
+// spectrum 0 "sos" (wavelengths 20..60 m scaled by dcorr / 10.3), 1 "exp" (inverse CDF of the radial spectrum).
+// Writes (kx, ky, phase) to fp; cos / sin / the phase product are evaluated as the reference's float32 torch ops,
+// cos / sin in double precision rounded once.
+DEV void draw_plane_wave(uint32_t s0, uint32_t env, uint32_t ep, int radio_model, int fi, int kk, float dc,
+                         int spectrum, float* fp) {
+    constexpr uint32_t CH_RESET_ = 3, LOG_DISTANCE_STREAM = 10, TR38901_STREAM = (0x52u << 16) + 16u;
+    uint32_t st0 = radio_model == 1 ? TR38901_STREAM + 3u * fi : LOG_DISTANCE_STREAM;
+    float u0 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET_, 0u, st0 + 0u), (uint32_t)kk));
+    float u1 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET_, 0u, st0 + 1u), (uint32_t)kk));
+    float u2 = uniform_bits(elem_hash(base_key(s0, env, ep, CH_RESET_, 0u, st0 + 2u), (uint32_t)kk));
+    float ang = (u0 * 2.0f) * (float)3.141592653589793;          // rand * 2 * pi, in that order
+    float kmag;
+    if (spectrum == 0) {                                          // "sos": wavelengths 20..60 m
+        float wl = 20.0f + 40.0f * u1;
+        if (dc != 10.3f) wl = wl * (float)((double)dc / 10.3);
+        kmag = (1.0f / wl) * (float)6.283185307179586;            // 2 pi / wl = reciprocal(wl) * 2 pi
+    } else {                                                      // "exp": inverse CDF of the radial spectrum
+        float u = clamp_max(u1, (float)(1.0 - 1e-6));
+        float a = 1.0f - u;
+        kmag = sqrtf(1.0f / (a * a) - 1.0f) / dc;
+    }
+    fp[0] = (float)cos((double)ang) * kmag;
+    fp[1] = (float)sin((double)ang) * kmag;
+    fp[2] = (u2 * 2.0f) * (float)3.141592653589793;
+}
+
 // ---------------------------------------------------------------- segment collectives (RB lanes, power of two)
 DEV unsigned long long seg_bits(int rb, int lane) {
     unsigned long long m = rb >= 64 ? ~0ull : ((1ull << rb) - 1ull);

@@ -201,22 +201,6 @@ DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
     ncb = (float)c;
 }
 
-// runtime-length ATen row sum for the shadowing modes (n <= 16)
-DEV float aten_sum_rt(const float* x, int n) {
-    if (n >= 8) {
-        float fin = 0.f;
-        for (int k = 8; k < n; ++k) fin += x[k];
-        for (int l = 0; l < 8; ++l) fin += x[l];
-        return fin;
-    }
-    float q[4] = {0.f, 0.f, 0.f, 0.f};
-    int si = n / 4;
-    for (int i = 0; i < si; ++i)
-        for (int k = 0; k < 4; ++k) q[k] += x[i * 4 + k];
-    for (int i = si * 4; i < n; ++i) q[0] += x[i];
-    return ((q[0] + q[1]) + q[2]) + q[3];
-}
-
 // Dynamic LDS of the step kernel, in ints: the in-order pointer after every UL slot [n_ul][64], with RLC drop the
 // byte range of a TB that exhausted its HARQ [n_ul][64] x 2, then the per-env HARQ histograms [64 / RB][3][max_tx + 1].
 inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
@@ -336,40 +320,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     } else {                                       // poses -> path gain (radio prologue)
         float px = 0.f, py = 0.f;
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
-        float dx = px - pm.gnb_x, dy = py - pm.gnb_y;
-        float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
-        // once per robot and step: the transcendental functions of the radio are evaluated in double precision and
-        // rounded once (correctly rounded float results; the field arguments k . x reach 1e4 rad)
-        int fi = 0;
-        float pl;
-        if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203), deterministic LOS state
-            float d3 = sqrtf(d2 * d2 + pm.hh2);
-            float lg = (float)log10((double)d3);
-            float pl1 = (pm.pl_a + pm.pl_n1 * lg) + pm.pl_c20;
-            float pl2 = ((pm.pl_a + 40.0f * lg) + pm.pl_c20) - pm.pl_c2;
-            pl = d2 <= pm.dbp ? pl1 : pl2;
-            if (pm.nl_b1 != 0.0f) {                // NLOS: max(PL_LOS, PL'_NLOS)
-                float pn = ((pm.nl_b1 * lg + pm.nl_b0) + pm.nl_c) - pm.nl_d;
-                pl = pn > pl ? pn : pl;
-                fi = 1;
-            }
-        } else {
-            pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
-        }
-        const float* fld = st.field + ((size_t)ee * pm.n_fields + fi) * pm.n_modes * 3;
-        float cs[INET_NR_MAX_KF];
-        for (int k = 0; k < pm.n_modes; ++k) {
-            float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
-            cs[k] = (float)cos((double)arg);
-        }
-        float field = pm.amp * aten_sum_rt(cs, pm.n_modes);
-        float pg;
-        if (pm.radio_model == 1) {
-            float loss = pl + pm.sig * field;
-            pg = (pm.ue_tx + (-loss)) - pm.ue_tx;
-        } else {
-            pg = ((pm.ue_tx - pl) - field) - pm.ue_tx;
-        }
+        const float rx = radio_rx_dbm(pm, px, py, st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3);
+        const float pg = rx - pm.ue_tx;
         ref[0] = (pg + pm.ref_off) - pm.noise_prb;
         snr_out = (pg + pm.ue_tx) - pm.subband_noise;
     }

@@ -1,0 +1,562 @@
+// MI355X (gfx950) kernels of isaac-net's level "WIFI" (the mean-field 802.11 uplink at one access point) and the C
+// ABI of include/inet_wifi.h.
+//
+// wifi_step_kernel runs one whole control step per env: the SNR of each robot (poses through the AP's radio, or the
+// SNR / received power given), its MCS, the K sub-steps of WifiNet._serve (isaac_net/core/wifi/engine.py:292-403) and
+// the end of step of finish_body (proto/netsim_fast.py:185-206), reading and writing each env's state once.
+//
+// Work decomposition: one workgroup is one wavefront; one robot per lane; the RB = next_pow2(R) lanes of an env form
+// an aligned segment, and a wave holds G envs (G RB <= 64; a launch parameter: fewer envs per wave give more waves,
+// which hides the latency of the serial sub-step chain). The AP's background station is segment-uniform: every lane
+// of the env computes it. The mean-field sums over the stations of the domain (meanfield.SingleView.sum) run over
+// an LDS row in torch's CPU summation order (aten_row_sum), so that only the transcendental functions differ from
+// the CPU path; those are evaluated in double precision and rounded once. The FIFO of each robot lives in LDS
+// columns during the step ([F][64] floats).
+//
+// Per sub-step and lane: q = sum of the FIFO bytes; contention flag; AC parameters and the access's bytes B; the
+// channel times Ts, Tc (wifi/phy.py:141-155); fp_iters + 1 evaluations of the failure probability (one LDS row sum
+// each) and the damped update of tau (tau(p) of meanfield.py:55-62 over the max_tx backoff stages); the slot time
+// (four row sums); the access count (Poisson inverse CDF over a double-precision running sum, or the renewal credit);
+// the FIFO service with each frame's finish time and retry-limit loss draw.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/inet_wifi.h"
+#include "inet_nr_dev.h"
+
+using namespace inet;
+
+namespace {
+
+constexpr int WAVE = 64;
+constexpr uint32_t CH_STEP = 2;
+
+// transcendental functions evaluated in double precision and rounded once to float32
+DEV float exp_r(float x) { return (float)exp((double)x); }
+DEV float log_r(float x) { return (float)log((double)x); }
+DEV float log1p_r(float x) { return (float)log1p((double)x); }
+DEV float pow_r(float x, float y) { return (float)pow((double)x, (double)y); }
+// x ** n for a Python int exponent n (torch pow with a scalar: 1 copies, 2 and 3 multiply, others pow)
+DEV float pow_int_torch(float x, int n) {
+    if (n == 1) return x;
+    if (n == 2) return x * x;
+    if (n == 3) return (x * x) * x;
+    return pow_r(x, (float)n);
+}
+// p ** k of tau(p) (torch pow of two float tensors): 1 at k = 0, p at k = 1
+DEV float pow_k(float p, int k) { return k == 0 ? 1.0f : (k == 1 ? p : pow_r(p, (float)k)); }
+DEV float fminn(float a, float b) { return a != a ? a : (b != b ? b : (a < b ? a : b)); }   // torch.minimum
+
+// AccessTiming.cap_bytes (wifi/phy.py:130-139): application bytes one access carries
+DEV float cap_bytes(const InetWifiParams& pm, float rate, float txop) {
+    if (pm.no_aggr) return pm.msdu_payload;
+    float tmax = txop > 0.f ? clamp_max(txop, pm.ppdu_max) : pm.ppdu_max;
+    float by_time = (((tmax - pm.pre) * rate) / 8.0f) / pm.ovh1;
+    return clamp_min(clamp_max(by_time, pm.ampdu_lim), pm.msdu_payload);
+}
+// AccessTiming.times (wifi/phy.py:141-155): (Ts, Tc) in us of an access of B bytes at rate after AIFSN aifsn
+DEV void access_times(const InetWifiParams& pm, float B, float rate, float aifsn, float& ts, float& tc) {
+    float aifs = aifsn * pm.slot_us + pm.sifs_us;
+    float nsym = ceilf(((B * pm.ovh1) * 8.0f + 22.0f) / (rate * pm.tsym));
+    float tdata = pm.tsym * nsym + pm.pre;
+    if (pm.rts_cts) {
+        ts = (((aifs + pm.hs) + tdata) + pm.sifs_us) + pm.t_ack;
+        tc = ((aifs + pm.t_rts) + pm.sifs_us) + pm.t_cts;
+    } else {
+        ts = ((aifs + tdata) + pm.sifs_us) + pm.t_ack;
+        tc = pm.coll_ack ? ts : aifs + tdata;
+    }
+}
+// tau(p) of meanfield.tau_from_p: sum_k p^k / sum_k p^k (W_k + 1) / 2 over the L stages, W_k = min(2^k W0, Wmax),
+// both sums in torch's CPU order
+DEV float tau_of_p(float p, float W0, float Wm, int L) {
+    float num = aten_row_sum(L, [&](int k) { return pow_k(p, k); });
+    float den = aten_row_sum(L, [&](int k) {
+        float wk = fminn(W0 * exp2f((float)k), Wm);
+        return pow_k(p, k) * ((wk + 1.0f) * 0.5f);
+    });
+    return num / den;
+}
+
+}  // namespace
+
+// ======================================================================================= step kernel
+__global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetWifiParams pm,
+                                                         const int64_t* __restrict__ tin, int input_kind,
+                                                         const float* __restrict__ xin,
+                                                         const int64_t* __restrict__ hid_in, InetWifiOutputs out,
+                                                         int rb) {
+    extern __shared__ float dyn[];
+    __shared__ float s_red[WAVE];
+    const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
+    float* s_rem = dyn;                                   // [F][64] bytes left of every frame slot
+    float* s_fin = dyn + F * WAVE;                        // [F][64] finish time, then the compaction staging row
+    uint8_t* s_cls = (uint8_t*)(dyn + 2 * F * WAVE);      // [F][64] class of every frame slot
+    uint8_t* s_src = s_cls + F * WAVE;                    // [F][64] source slot of every compacted slot
+    int32_t* s_stage = (int32_t*)s_fin;
+
+    const int lane = threadIdx.x;
+    const int g = lane / rb, r = lane - g * rb;
+    const int e = blockIdx.x * G + g;
+    const bool env_ok = g < G && e < pm.E;
+    const bool rob = env_ok && r < R;
+    const int ec = env_ok ? e : 0, rc = rob ? r : 0;
+    const int gseg = g < G ? g : 0;
+    const size_t ir = (size_t)ec * R + rc;                 // [E][R]
+    const size_t fo = (size_t)ec * F * R + rc;             // [E][F][R] slot f at fo + f R
+
+    // ---------------- inputs, association, MCS (wifi/engine.py:227-259, 295-299) ----------------
+    const int64_t t = env_ok ? (tin ? tin[ec] : st.clock[ec]) : 0;
+    float rx = 0.f;
+    if (rob) {
+        if (input_kind == 0) {
+            float px = xin[ir * 2], py = xin[ir * 2 + 1];
+            rx = radio_rx_dbm(pm, px, py, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3);
+        } else if (input_kind == 1) {
+            rx = xin[ir] + pm.noise_dbm;
+        } else {
+            rx = xin[ir];
+        }
+    }
+    const float snr = rx - pm.noise_dbm;     // one AP: the association keeps AP 0 (no roaming between APs)
+    int nm = 0;
+    for (int m = 0; m < pm.M; ++m) nm += snr >= pm.thr[m] ? 1 : 0;
+    const bool link = nm > 0;
+    const int mcs = nm > 0 ? nm - 1 : 0;
+    const float rate = pm.rates[mcs];
+
+    // ---------------- state ----------------
+    int qlen = rob ? st.qlen[ir] : 0;
+    for (int f = 0; f < F; ++f) {
+        const int o = f * WAVE + lane;
+        s_rem[o] = rob && f < qlen ? st.rem[fo + (size_t)f * R] : 0.f;
+        s_cls[o] = rob ? (uint8_t)st.cls[fo + (size_t)f * R] : 0;
+        s_fin[o] = INFINITY;
+    }
+    float tau = rob ? st.tau[(size_t)ec * (R + 1) + rc] : pm.tau0;
+    float tau_b = env_ok ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0;
+    int roam = rob ? st.roam_left[ir] : 0;
+    float att_n = rob ? st.att_n[ir] : 0.f, att_logp = rob ? st.att_logp[ir] : 0.f;
+    float credit = rob ? st.credit[ir] : 0.f;
+
+    // counter-RNG keys of this step: the step counter advances before the draws (LevelNet._advance)
+    const int ctr = env_ok ? st.ctr_step[ec] + 1 : 0;
+    uint32_t key_acc = 0, key_loss = 0;
+    if (env_ok) {
+        uint32_t h = mix32((uint32_t)pm.seed_key ^ salt32((uint32_t)st.env_id[ec]));
+        h = mix32(h ^ salt32((uint32_t)st.episode[ec]));
+        h = mix32(h ^ salt32(CH_STEP));
+        h = mix32(h ^ salt32((uint32_t)ctr));
+        key_acc = mix32(h ^ salt32(0u));
+        key_loss = mix32(h ^ salt32(1u));
+    }
+
+    // EDCA parameters: the class-1 AC for every robot, or the head-of-line message's AC per sub-step
+    int ac = pm.cls_ac[1];
+    float W0 = pm.ac_W0[ac], Wm = pm.ac_Wmax[ac], aifsn = pm.ac_aifsn[ac];
+    float capB = cap_bytes(pm, rate, pm.ac_txop[ac]);
+    // the background station (segment-uniform)
+    const float W0b = pm.ac_W0[pm.bg_ac], Wmb = pm.ac_Wmax[pm.bg_ac];
+    float tsb, tcb;
+    access_times(pm, pm.bg_B, pm.bg_rate, pm.ac_aifsn[pm.bg_ac], tsb, tcb);
+    const float wb = pm.bg_w;
+    const bool act_b = wb > 0.f;
+
+    // sum over the stations of the env (robots in lane order, then the background station), torch's CPU order
+    auto dom_sum = [&](float v, float vb) -> float {
+        __syncthreads();
+        s_red[lane] = v;
+        __syncthreads();
+        const float* row = s_red + gseg * rb;
+        return aten_row_sum(R + 1, [&](int i) { return i < R ? row[i] : vb; });
+    };
+    auto fifo_sum = [&]() -> float {
+        return aten_row_sum(F, [&](int f) { return s_rem[f * WAVE + lane]; });
+    };
+
+    float acc_sum = 0.f, acc_n = 0.f, p_sum = 0.f, busy_sum = 0.f;
+    const float tf = (float)t;
+    for (int k = 0; k < K; ++k) {
+        const float q = fifo_sum();
+        const bool act = rob && q > 0.f && link && roam <= 0;
+        if (pm.per_class_ac) {
+            int hol = 0;
+            for (int f = qlen - 1; f >= 0; --f) hol = s_rem[f * WAVE + lane] > 0.f ? f : hol;
+            const int ch = s_cls[hol * WAVE + lane];
+            ac = pm.cls_ac[ch < pm.n_cls ? ch : pm.n_cls];
+            W0 = pm.ac_W0[ac]; Wm = pm.ac_Wmax[ac]; aifsn = pm.ac_aifsn[ac];
+            capB = cap_bytes(pm, rate, pm.ac_txop[ac]);
+        }
+        const float B = act ? fminn(q, capB) : capB;
+        const float w = act ? 1.0f : 0.0f;
+        float ts, tc;
+        access_times(pm, B, rate, aifsn, ts, tc);
+
+        // ---- mean-field fixed point (meanfield.solve, one domain, one AIFS zone)
+        float p = 0.f, ok = 0.f, pb = 0.f, S = 0.f;
+        auto fail = [&]() {
+            const float lt = log1p_r(-tau), ltb = log1p_r(-tau_b);
+            S = dom_sum(w * lt, wb * ltb);
+            const float own = act ? lt : 0.0f, ownb = act_b ? ltb : 0.0f;
+            ok = exp_r(S - own) * pm.fer1;
+            const float okb = exp_r(S - ownb) * pm.fer1;
+            p = 1.0f - ok;
+            pb = 1.0f - okb;
+        };
+        for (int it = 0; it < pm.fp_iters; ++it) {
+            tau = clampf(tau, 1e-7f, 0.999f);
+            tau_b = clampf(tau_b, 1e-7f, 0.999f);
+            fail();
+            tau = tau + pm.damp * (tau_of_p(p, W0, Wm, L) - tau);
+            tau_b = tau_b + pm.damp * (tau_of_p(pb, W0b, Wmb, L) - tau_b);
+        }
+        tau = clampf(tau, 1e-7f, 0.999f);
+        tau_b = clampf(tau_b, 1e-7f, 0.999f);
+        fail();
+        const float r_o = (w * tau) / (1.0f - tau), r_b = (wb * tau_b) / (1.0f - tau_b);
+        const float wt_o = w * tau, wt_b = wb * tau_b;
+        const float idle = exp_r(S);
+        const float a0 = dom_sum(r_o, r_b);
+        const float a1 = dom_sum(r_o * ts, r_b * tsb);
+        const float gd = dom_sum(wt_o, wt_b);
+        const float gg = dom_sum(wt_o * tc, wt_b * tcb);
+        const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
+        const float tcav = gg / clamp_min(gd, 1e-12f);
+        const float tslot = 0.0f + ((pm.slot_us * idle + idle * a1) + p_coll * tcav);
+        const float p_idle = 0.0f + idle;
+        const float mu = act ? (tau * ok) / tslot : 0.0f;
+
+        // ---- access count (wifi/engine.py:355-360)
+        const float lam = mu * pm.dt_us;
+        float n_acc, c1 = 0.f;
+        if (pm.access_noise == 0) {
+            const float u = uniform_bits(elem_hash(key_acc, (uint32_t)(k * R + rc)));
+            const float ll = log_r(clamp_min(lam, 1e-30f));
+            double cum = 0.0;
+            int n = 0;
+            for (int kk = 0; kk < pm.n_acc_max; ++kk) {
+                const float lp = ((float)kk * ll - lam) - pm.lgamma[kk];
+                cum += (double)exp_r(lp);
+                if (!(u > (float)cum)) break;      // the CDF never decreases: the count is the first k with u <= CDF
+                ++n;
+            }
+            n_acc = (float)n;
+        } else {
+            c1 = credit + lam * w;
+            n_acc = floorf(c1);
+        }
+        const float served = fminn(q, n_acc * B) * w;
+
+        // ---- retry-limit loss inputs (wifi/engine.py:375-381)
+        const bool back = q > 0.f;
+        att_n = back ? att_n + w : 0.0f;
+        const float lp = act ? log_r(clamp_min(p, 1e-12f)) : 0.0f;
+        att_logp = back ? att_logp + lp : 0.0f;
+        const float p_bar = att_n > 0.f ? exp_r(att_logp / clamp_min(att_n, 1e-12f)) : p;
+        const float pbl = pow_int_torch(p_bar, L);
+
+        // ---- FIFO service, finish times, loss (serve_fifo, wifi/engine.py:361-383)
+        double cacc = 0.0;
+        float prev_nc = 0.0f;
+        for (int f = 0; f < qlen; ++f) {
+            const int o = f * WAVE + lane;
+            const float rm = s_rem[o];
+            cacc += (double)rm;
+            const float cum = (float)cacc;
+            const float nc = clamp_min(cum - served, 0.0f);
+            const float nw = nc - prev_nc;
+            prev_nc = nc;
+            const bool fin = rm > 0.0f && nw <= 1e-3f;
+            s_rem[o] = fin ? 0.0f : nw;
+            if (fin) {
+                const float j = clamp_min(ceilf(cum / B - 1e-6f), 1.0f);
+                float frac = pm.access_noise == 0 ? j / (n_acc + 1.0f) : (j - credit) / clamp_min(lam, 1e-9f);
+                frac = clampf(frac, 0.0f, 1.0f);
+                const float tfin = fminn(tf + ((float)k + frac) / (float)K, (tf + 1.0f) - 1e-6f);
+                const int c = s_cls[o];
+                const float size = pm.sizes[(c > 1 ? (c < pm.n_cls ? c : pm.n_cls) : 1) - 1];
+                const float n_frame = clamp_min(ceilf(size / B), 1.0f);
+                const float p_lost = 1.0f - pow_r(1.0f - pbl, n_frame);
+                const float u = uniform_bits(elem_hash(key_loss, (uint32_t)(rc * F + f)));
+                if (!(u < p_lost)) s_fin[o] = tfin;
+            }
+        }
+        if (pm.access_noise == 1 && act) credit = fifo_sum() > 0.f ? c1 - n_acc : 0.0f;
+        roam = roam - 1 > 0 ? roam - 1 : 0;
+        acc_sum = acc_sum + (act ? 1.0f / clamp_min(mu, 1e-12f) : 0.0f);
+        acc_n = acc_n + w;
+        p_sum = p_sum + p * w;
+        busy_sum = busy_sum + (1.0f - p_idle);
+    }
+
+    // ---------------- per-robot state and outputs of _serve ----------------
+    const bool keep = fifo_sum() > 0.f;
+    if (rob) {
+        st.tau[(size_t)ec * (R + 1) + rc] = tau;
+        if (r == 0) st.tau[(size_t)ec * (R + 1) + R] = tau_b;
+        st.roam_left[ir] = roam;
+        st.credit[ir] = keep ? credit : 0.0f;
+        st.att_n[ir] = keep ? att_n : 0.0f;
+        st.att_logp[ir] = keep ? att_logp : 0.0f;
+        st.serv[ir] = 0;
+        st.last_snr[ir] = snr;
+        out.access_ms[ir] = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
+        out.p_fail[ir] = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
+        out.busy[ir] = busy_sum / (float)K;
+        out.mcs[ir] = link ? pm.mcs_ids[mcs] : -1;
+        out.rate_mbps[ir] = link ? rate : 0.0f;
+        out.sinr_db[ir] = snr;
+        out.serving_cell[ir] = 0;
+    }
+
+    // ---------------- end of step: finish_body ----------------
+    const int64_t chid = env_ok ? (hid_in ? hid_in[ec] : st.last_hid[ec]) : 0;
+    int newest = -1;
+    bool det_hit = false;
+    uint64_t vmask = 0, dmask = 0;                         // slots still queued after the step; their det flags
+    const size_t oo = ir * F;                              // [E][R][F] outputs
+    for (int f = 0; f < F; ++f) {
+        const int o = f * WAVE + lane;
+        int cap = -1;
+        bool dt = false;
+        int hid = 0;
+        if (rob) { cap = st.cap[fo + (size_t)f * R]; dt = st.det[fo + (size_t)f * R] != 0; hid = st.hid[fo + (size_t)f * R]; }
+        const float fin = s_fin[o];
+        const bool dlv = cap >= 0 && fin != INFINITY && fin == fin;
+        const bool timed = cap >= 0 && !dlv && ((t + 1 - (int64_t)cap) >= pm.timeout);
+        newest = dlv && cap > newest ? cap : newest;
+        det_hit = det_hit || (dlv && dt && (int64_t)hid == chid);
+        if (rob) {
+            out.delivered[oo + f] = dlv;
+            out.timed_out[oo + f] = timed;
+            out.cap[oo + f] = cap;
+            out.cls[oo + f] = s_cls[o];
+            out.delay[oo + f] = dlv ? fin - (float)cap : NAN;
+        }
+        const bool gone = dlv || timed;
+        if (gone) s_rem[o] = 0.0f;
+        if (!gone && cap >= 0) vmask |= 1ull << f;
+        if (dt && !gone) dmask |= 1ull << f;
+        s_stage[o] = gone ? -1 : cap;                      // the new cap row, staged for the permutation
+    }
+    // stable partition (finish_body's cumsum scatter): the queued slots in order, then the others in order
+    const int nvalid = __builtin_popcountll(vmask);
+    {
+        int gv = 0, gi = nvalid;
+        for (int f = 0; f < F; ++f) {
+            const int dst = ((vmask >> f) & 1ull) ? gv++ : gi++;
+            s_src[dst * WAVE + lane] = (uint8_t)f;
+        }
+    }
+    if (rob) {
+        // cap (staged above), then every other field through the staging row
+        for (int gdst = 0; gdst < F; ++gdst) st.cap[fo + (size_t)gdst * R] = s_stage[s_src[gdst * WAVE + lane] * WAVE + lane];
+        for (int f = 0; f < F; ++f) {
+            const int o = f * WAVE + lane;
+            s_stage[o] = s_cls[o];
+        }
+        for (int gdst = 0; gdst < F; ++gdst) st.cls[fo + (size_t)gdst * R] = s_stage[s_src[gdst * WAVE + lane] * WAVE + lane];
+        for (int gdst = 0; gdst < F; ++gdst) {
+            const int sf = s_src[gdst * WAVE + lane];
+            st.det[fo + (size_t)gdst * R] = (uint8_t)((dmask >> sf) & 1ull);
+        }
+        for (int f = 0; f < F; ++f) s_stage[f * WAVE + lane] = st.hid[fo + (size_t)f * R];
+        for (int gdst = 0; gdst < F; ++gdst) st.hid[fo + (size_t)gdst * R] = s_stage[s_src[gdst * WAVE + lane] * WAVE + lane];
+        for (int f = 0; f < F; ++f) s_stage[f * WAVE + lane] = st.f_nact[fo + (size_t)f * R];
+        for (int gdst = 0; gdst < F; ++gdst) st.f_nact[fo + (size_t)gdst * R] = s_stage[s_src[gdst * WAVE + lane] * WAVE + lane];
+        for (int f = 0; f < F; ++f) s_stage[f * WAVE + lane] = st.f_own[fo + (size_t)f * R];
+        for (int gdst = 0; gdst < F; ++gdst) st.f_own[fo + (size_t)gdst * R] = s_stage[s_src[gdst * WAVE + lane] * WAVE + lane];
+        float* s_stf = (float*)s_stage;
+        for (int f = 0; f < F; ++f) s_stf[f * WAVE + lane] = st.f_snr[fo + (size_t)f * R];
+        for (int gdst = 0; gdst < F; ++gdst) st.f_snr[fo + (size_t)gdst * R] = s_stf[s_src[gdst * WAVE + lane] * WAVE + lane];
+        for (int f = 0; f < F; ++f) s_stf[f * WAVE + lane] = s_rem[f * WAVE + lane];
+        for (int gdst = 0; gdst < F; ++gdst) {
+            const float v = s_stf[s_src[gdst * WAVE + lane] * WAVE + lane];
+            st.rem[fo + (size_t)gdst * R] = v;
+            s_rem[gdst * WAVE + lane] = v;
+        }
+        st.qlen[ir] = nvalid;
+        out.newest[ir] = newest;
+        out.queue_len[ir] = nvalid;
+        out.queue_bytes[ir] = fifo_sum();
+    }
+    // det_env: any delivered detection of the env's current hazard
+    const bool any_det = seg_any(det_hit && rob, rb, lane);
+    if (env_ok && r == 0) {
+        out.det_env[ec] = any_det;
+        out.t[ec] = t;
+        st.clock[ec] = t + 1;
+        st.ctr_step[ec] = ctr;
+        st.pending[ec] = 0;
+    }
+}
+
+// ======================================================================================= submit kernel
+// add_body (proto/netsim_fast.py:136-160) for one LevelNet.submit call (send) or the harness's sequence of calls
+// (counts: class 1 first, one call per message index).
+__global__ __launch_bounds__(WAVE) void wifi_submit_kernel(InetWifiState st, InetWifiParams pm,
+                                                           const int64_t* __restrict__ tin,
+                                                           const int64_t* __restrict__ send,
+                                                           const uint8_t* __restrict__ det,
+                                                           const int64_t* __restrict__ hid,
+                                                           const float* __restrict__ snr,
+                                                           const uint8_t* __restrict__ counts, int n_cls,
+                                                           void* accepted, int rb) {
+    const int R = pm.R, F = pm.F, G = pm.envs_per_wave;
+    const int lane = threadIdx.x;
+    const int g = lane / rb, r = lane - g * rb;
+    const int e = blockIdx.x * G + g;
+    const bool env_ok = g < G && e < pm.E;
+    const bool rob = env_ok && r < R;
+    const int ec = env_ok ? e : 0, rc = rob ? r : 0;
+    const size_t ir = (size_t)ec * R + rc;
+    const size_t fo = (size_t)ec * F * R + rc;
+    const int64_t t = env_ok ? (tin ? tin[ec] : st.clock[ec]) : 0;
+    const int64_t hid_e = env_ok && hid ? hid[ec] : 0;
+    int qlen = rob ? st.qlen[ir] : 0;
+    const float snr_in = rob ? (snr ? snr[ir] : st.last_snr[ir]) : 0.f;
+    const bool dt = rob && det ? det[ir] != 0 : false;
+    int n_calls = 0, n_acc = 0;
+
+    auto call = [&](int cls) {     // one submit of class cls (0 = none) by this lane
+        const bool nw = rob && cls > 0 && qlen < F;
+        const int nact = __builtin_popcountll(__ballot(rob && (qlen + (nw ? 1 : 0)) > 0) & seg_bits(rb, lane));
+        if (nw) {
+            const size_t o = fo + (size_t)qlen * R;
+            const int c = cls < pm.n_cls ? cls : pm.n_cls;
+            st.cap[o] = (int32_t)t;
+            st.cls[o] = cls;
+            st.det[o] = dt;
+            st.hid[o] = (int32_t)hid_e;
+            st.rem[o] = pm.sizes[c - 1];
+            st.f_nact[o] = nact;
+            st.f_snr[o] = snr_in;
+            st.f_own[o] = qlen;
+            ++qlen;
+            ++n_acc;
+        }
+        return nw;
+    };
+    if (!counts) {
+        const bool nw = call(rob ? (int)send[ir] : 0);
+        if (rob) ((uint8_t*)accepted)[ir] = nw;
+        n_calls = 1;
+    } else {
+        for (int c = 0; c < n_cls; ++c) {
+            const int mine = rob ? counts[ir * n_cls + c] : 0;
+            const int most = seg_max_i(mine, rb);
+            for (int i = 0; i < most; ++i) call(mine > i ? c + 1 : 0);
+            n_calls += most;
+        }
+        if (rob) ((int32_t*)accepted)[ir] = n_acc;
+    }
+    if (rob) st.qlen[ir] = qlen;
+    if (env_ok && r == 0 && n_calls > 0) {
+        st.last_hid[ec] = hid_e;
+        st.ctr_submit[ec] += n_calls;
+    }
+}
+
+// ======================================================================================= reset kernel
+// LevelNet.reset (levels/base.py:142-157) + WifiNet._reset_rows (wifi/engine.py:179-186) + the radio's plane waves
+// of the new episode (radio.py:200-219; the reference draws them when it makes the radio and at every reset, keyed by
+// the env's current episode, so drawing them at every reset gives the same fields). One block per env.
+__global__ void wifi_reset_kernel(InetWifiState st, InetWifiParams pm, const uint8_t* __restrict__ mask) {
+    const int e = blockIdx.x;
+    if (e >= pm.E || (mask && !mask[e])) return;
+    const int R = pm.R, F = pm.F;
+    const int ep_new = st.episode[e] + 1;
+    for (int i = threadIdx.x; i < F * R; i += blockDim.x) {
+        const size_t o = (size_t)e * F * R + i;
+        st.cap[o] = -1; st.cls[o] = 0; st.det[o] = 0; st.hid[o] = -1; st.rem[o] = 0.f;
+        st.f_nact[o] = 0; st.f_snr[o] = 0.f; st.f_own[o] = 0;
+    }
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        const size_t ir = (size_t)e * R + r;
+        st.qlen[ir] = 0; st.last_snr[ir] = 0.f; st.roam_left[ir] = 0; st.serv[ir] = 0;
+        st.att_n[ir] = 0.f; st.att_logp[ir] = 0.f; st.credit[ir] = 0.f;
+    }
+    for (int r = threadIdx.x; r <= R; r += blockDim.x) st.tau[(size_t)e * (R + 1) + r] = pm.tau0;
+    const int Kf = pm.n_modes;
+    for (int q = threadIdx.x; q < pm.n_fields * Kf; q += blockDim.x) {
+        const int fi = q / Kf, kk = q - fi * Kf;
+        draw_plane_wave((uint32_t)pm.seed_key, (uint32_t)st.env_id[e], (uint32_t)ep_new, pm.radio_model, fi, kk,
+                        pm.dcorr[fi], pm.spectrum, st.field + (((size_t)e * pm.n_fields + fi) * Kf + kk) * 3);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st.episode[e] = ep_new;
+        st.ctr_step[e] = 0;
+        st.ctr_submit[e] = 0;
+        st.clock[e] = 0;
+        st.last_hid[e] = 0;
+        st.pending[e] = 1;
+    }
+}
+
+// ======================================================================================= C ABI
+namespace {
+
+int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
+
+int check_params(const InetWifiParams& p) {
+    if (p.E <= 0 || p.R <= 0 || p.R > INET_WIFI_MAX_R || p.F <= 0 || p.F > INET_WIFI_MAX_F || p.K <= 0)
+        return INET_WIFI_EINVAL;
+    if (p.M <= 0 || p.M > INET_WIFI_MAX_M || p.L <= 0 || p.L > INET_WIFI_MAX_L || p.n_cls <= 0 ||
+        p.n_cls > INET_WIFI_MAX_CLS || p.n_acc_max <= 0 || p.n_acc_max > INET_WIFI_MAX_NACC || p.fp_iters < 1)
+        return INET_WIFI_EINVAL;
+    if (p.n_fields < 0 || p.n_fields > 3 || p.n_modes < 0 || p.n_modes > INET_WIFI_MAX_KF) return INET_WIFI_EINVAL;
+    if (p.bg_ac < 0 || p.bg_ac > 4) return INET_WIFI_EINVAL;
+    for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
+    const int rb = next_pow2(p.R);
+    if (p.envs_per_wave < 1 || p.envs_per_wave * rb > WAVE) return INET_WIFI_EINVAL;
+    return INET_WIFI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t inet_wifi_abi_version(void) { return INET_WIFI_ABI_VERSION; }
+
+int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const int64_t* t, int32_t input_kind,
+                       const float* x, const int64_t* cur_hid, const InetWifiOutputs* out, void* stream) {
+    if (!st || !prm || !x || !out) return INET_WIFI_EINVAL;
+    const InetWifiParams& p = *prm;
+    int rc = check_params(p);
+    if (rc) return rc;
+    if (input_kind < 0 || input_kind > 2) return INET_WIFI_EINVAL;
+    if (input_kind == 0 && p.n_fields < 1) return INET_WIFI_EINVAL;
+    const int rb = next_pow2(p.R);
+    const int G = p.envs_per_wave;
+    const unsigned grid = (unsigned)((p.E + G - 1) / G);
+    const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
+    hipLaunchKernelGGL(wifi_step_kernel, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t, input_kind, x,
+                       cur_hid, *out, rb);
+    return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
+}
+
+int32_t inet_wifi_submit(const InetWifiState* st, const InetWifiParams* prm, const int64_t* t, const int64_t* send,
+                         const uint8_t* det, const int64_t* hid, const float* snr, const uint8_t* counts,
+                         int32_t n_cls, void* accepted, void* stream) {
+    if (!st || !prm || !accepted || (!send && !counts) || (send && counts)) return INET_WIFI_EINVAL;
+    const InetWifiParams& p = *prm;
+    int rc = check_params(p);
+    if (rc) return rc;
+    if (counts && (n_cls <= 0 || n_cls > p.n_cls)) return INET_WIFI_EINVAL;
+    const int rb = next_pow2(p.R);
+    const int G = p.envs_per_wave;
+    hipLaunchKernelGGL(wifi_submit_kernel, dim3((p.E + G - 1) / G), dim3(WAVE), 0, (hipStream_t)stream, *st, p, t,
+                       send, det, hid, snr, counts, n_cls, accepted, rb);
+    return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
+}
+
+int32_t inet_wifi_reset(const InetWifiState* st, const InetWifiParams* prm, const uint8_t* mask, void* stream) {
+    if (!st || !prm) return INET_WIFI_EINVAL;
+    int rc = check_params(*prm);
+    if (rc) return rc;
+    hipLaunchKernelGGL(wifi_reset_kernel, dim3(prm->E), dim3(WAVE), 0, (hipStream_t)stream, *st, *prm, mask);
+    return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
+}
+
+}  // extern "C"

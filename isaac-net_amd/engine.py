@@ -708,10 +708,11 @@ class GraphStep:
 
 def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, backend="hip", *, sizes=None,
                 params=None, seed=None, inject=False, strict=False, out_format="reference"):
-    """Factory with the signature of isaac_net.core.engine.make_engine (engine.py:230-255) for level "L2" and
-    backend "hip" (also "auto", which resolves to "hip" on a GPU device)."""
-    if level != "L2":
-        raise HipUnsupported(f"level {level!r}: the hip backend implements the NR engine (level 'L2') only")
+    """Factory with the signature of isaac_net.core.engine.make_engine (engine.py:230-255) for level "L2" (the NR
+    engine) and level "WIFI" (isaac_net/core/wifi/engine.py:436-444), backend "hip" (also "auto", which resolves to
+    "hip" on a GPU device)."""
+    if level not in ("L2", "WIFI"):
+        raise HipUnsupported(f"level {level!r}: the hip backend implements levels 'L2' (NR) and 'WIFI'")
     if backend not in ("hip", "auto"):
         raise ValueError(f"unknown backend {backend!r} for this package; use 'hip'")
     if inject:
@@ -721,4 +722,7 @@ def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, back
         cfg = cfg.with_(msg_sizes=tuple(float(s) for s in sizes))
     if seed is None:
         seed = cfg.seed
+    if level == "WIFI":
+        from .wifi_engine import HipWifiEngine
+        return HipWifiEngine(E, R, device, cfg, seed=seed)
     return HipNREngine(E, R, device, cfg, seed=seed, out_format=out_format)

@@ -1,0 +1,400 @@
+"""HipWifiEngine: level "WIFI" (the mean-field 802.11 uplink at one access point) over the HIP kernels of
+libinet_nr.so (include/inet_wifi.h).
+
+Mirrors isaac_net/core/wifi/engine.py (WifiNet, :100-403) on the LevelNet contract (isaac_net/core/levels/base.py:43-360):
+reset(env_ids) / submit(t, requests, snr_db) / step(t, poses_or_snr, cur_hid, *, rx_dbm) -> dict / clock /
+state_dict, with the same inputs, output keys, dtypes and shapes and the same per-env clock rules (t=None uses the
+engine clock; an int or an [E] tensor sets each env's step). What the kernels do not implement is refused at
+construction with HipUnsupported: several access points (and with them roaming and several channels), hidden nodes,
+AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio features the NR engine
+refuses.
+
+All state lives in device tensors that torch allocates; every call hands the library plain pointers.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+from .config import NRConfig
+from .engine import HipUnsupported, Requests, seed_key
+from .wifi_config import PPDU_MAX_US, WifiConfig, derive, radio_config
+
+OUT_KEYS = ("newest", "det_env", "delivered", "timed_out", "cap", "cls", "delay", "queue_len", "queue_bytes",
+            "sinr_db", "t", "serving_cell", "wifi_mcs", "wifi_rate_mbps", "wifi_access_ms", "wifi_p_fail",
+            "wifi_busy")
+
+
+def wifi_refusals(cfg: NRConfig):
+    """[(feature, why)] of the config's features the HIP Wi-Fi kernels do not implement (empty: it runs)."""
+    wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
+    out = []
+
+    def no(cond, what, why):
+        if cond:
+            out.append((what, why))
+    n_ap = len(wc.ap_xy(cfg))
+    no(n_ap != 1, f"{n_ap} access points", "one AP per env (one collision domain, no roaming)")
+    no(wc.hidden_nodes, "hidden_nodes=True", "every robot senses every other one")
+    d = derive(cfg, wc)
+    no(d.Z > 1, "access categories with different AIFSN in one env (AIFS zones)", "one AIFS zone")
+    no(cfg.rng != "engine", "rng='global'", "counter-based engine RNG")
+    no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
+    no(cfg.frame_buffer > 64, "frame_buffer > 64", "FIFO columns of up to 64 slots in LDS")
+    no(wc.max_tx > 16, "max_tx > 16", "up to 16 backoff stages")
+    no(len(cfg.msg_sizes) > 16, "more than 16 message classes", "16 classes")
+    no(d.n_acc_max > 128, "a Poisson support above 128 accesses per sub-step", "substep_ms too long for the table")
+    no(len(d.rates) > 16, "more than 16 MCS", "16 table entries")
+    no(cfg.blockage or cfg.los_source != "stochastic" or cfg.gnb_antenna != "isotropic" or cfg.o2i_indoor_frac > 0
+       or cfg.shadow_white_frac > 0, "obstacle stack, sector antennas, O2I or white shadowing",
+       "plain path loss + plane-wave shadowing")
+    no(cfg.channel not in ("log_distance", "tr38901"), f"channel={cfg.channel!r}", "log_distance and tr38901")
+    if cfg.channel == "tr38901":
+        no(cfg.tr38901_los not in ("los", "nlos"), "tr38901_los='stochastic'", "a fixed LOS state (los / nlos)")
+        no(cfg.tr38901_scenario == "RMa", "the RMa scenario", "UMa, UMi, InH, InF")
+        no(cfg.tr38901_scenario.startswith("InF") and cfg.tr38901_los == "nlos", "InF NLOS", "InF LOS")
+    no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
+    return out
+
+
+class HipWifiEngine:
+    """Level WIFI on MI355X. API of isaac_net.core.wifi.engine.WifiNet (levels/base.LevelNet)."""
+
+    level = "WIFI"
+    backend = "hip"
+
+    def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, envs_per_wave=None):
+        cfg = cfg if cfg is not None else NRConfig()
+        if cfg.wifi is not None and not isinstance(cfg.wifi, WifiConfig):
+            raise TypeError("NRConfig.wifi must be a WifiConfig")
+        no = wifi_refusals(cfg)
+        if no:
+            raise HipUnsupported("the hip backend of level WIFI does not implement "
+                                 + "; ".join(f"{f} ({why})" for f, why in no))
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("the hip backend needs a GPU device (cuda:N on ROCm)")
+        if not 1 <= R <= 64:
+            raise HipUnsupported(f"R={R}: one env's robots share one 64-lane wavefront segment (1 <= R <= 64)")
+        self._lib = _lib.load()
+        self.E, self.R, self.dev, self.config = E, R, dev, cfg
+        self.wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
+        if seed is None:
+            seed = cfg.seed if cfg.seed is not None else int(torch.randint(0, 2 ** 62, ()).item())
+        self.seed = int(seed)
+        self.F, self.TIMEOUT = cfg.frame_buffer, cfg.timeout_steps
+        self.d = derive(cfg, self.wc)
+        self.K = self.Ksub = self.d.K
+        self.n_acc_max = self.d.n_acc_max
+        rb = 1 << max(0, (R - 1).bit_length())
+        self.envs_per_wave = int(envs_per_wave) if envs_per_wave is not None else 1
+        if self.envs_per_wave < 1 or self.envs_per_wave * rb > 64:
+            raise ValueError(f"envs_per_wave must be in 1..{64 // rb} for R={R}")
+        self._alloc_state()
+        self._build_params()
+        self.reset(None)
+
+    # ------------------------------------------------------------------ buffers and constants
+    def _alloc_state(self):
+        E, R, F, d = self.E, self.R, self.F, self.dev
+        i32, f32 = torch.int32, torch.float32
+        z = lambda *shape, dt=i32, v=0: torch.full(shape, v, dtype=dt, device=d)  # noqa: E731
+        cfg = self.config
+        nf = 3 if cfg.channel == "tr38901" else 1
+        self._n_fields = nf
+        self.st = {
+            "cap": z(E, F, R, v=-1), "cls": z(E, F, R), "det": z(E, F, R, dt=torch.uint8), "hid": z(E, F, R, v=-1),
+            "rem": z(E, F, R, dt=f32), "f_nact": z(E, F, R), "f_snr": z(E, F, R, dt=f32), "f_own": z(E, F, R),
+            "qlen": z(E, R), "last_snr": z(E, R, dt=f32), "roam_left": z(E, R), "serv": z(E, R),
+            "att_n": z(E, R, dt=f32), "att_logp": z(E, R, dt=f32), "credit": z(E, R, dt=f32),
+            "tau": z(E, R + 1, dt=f32), "clock": z(E, dt=torch.int64), "last_hid": z(E, dt=torch.int64),
+            "pending": z(E, dt=torch.uint8, v=1), "env_id": torch.arange(E, dtype=i32, device=d),
+            "episode": z(E, v=-1), "ctr_step": z(E), "ctr_submit": z(E),
+            "field": z(E, nf, max(cfg.shadow_modes, 1), 3, dt=f32),
+        }
+        s = _lib.InetWifiState()
+        for name, _ in _lib.InetWifiState._fields_:
+            setattr(s, name, self.st[name].data_ptr())
+        self._cstate = s
+
+    def _build_params(self):
+        from .channels import SCENARIOS, SIGMA_SF, breakpoint_m
+        cfg, wc, dd = self.config, self.wc, self.d
+        p = _lib.InetWifiParams()
+        p.E, p.R, p.F, p.K, p.M, p.L = self.E, self.R, self.F, dd.K, len(dd.rates), wc.max_tx
+        p.n_cls, p.n_acc_max, p.fp_iters, p.timeout = len(cfg.msg_sizes), dd.n_acc_max, wc.fp_iters, self.TIMEOUT
+        p.access_noise = 0 if wc.access_noise == "poisson" else 1
+        p.rts_cts, p.coll_ack = int(wc.rts_cts), int(wc.collision_time == "ack")
+        p.per_class_ac, p.no_aggr = int(dd.per_class_ac), int(wc.max_ampdu_bytes == 0)
+        p.seed_key = C.c_int32(seed_key(self.seed) - (1 << 32) if seed_key(self.seed) >= 1 << 31
+                               else seed_key(self.seed)).value
+        p.roam_sub = int(round(wc.roam_ms / wc.substep_ms))
+        p.bg_ac, p.envs_per_wave = dd.bg_ac, self.envs_per_wave
+        f = np.float32
+        p.noise_dbm, p.roam_hyst, p.damp = dd.noise_dbm, wc.roam_hyst_db, wc.fp_damping
+        p.fer1 = float(f(1.0 - wc.frame_error_rate))
+        p.dt_us, p.tau0, p.slot_us, p.sifs_us = dd.dt_us, dd.tau0, wc.slot_us, wc.sifs_us
+        p.pre, p.tsym, p.ovh1, p.t_ack, p.t_rts, p.t_cts = dd.pre, dd.tsym, dd.ovh1, dd.t_ack, dd.t_rts, dd.t_cts
+        p.hs = dd.t_rts + wc.sifs_us + dd.t_cts + wc.sifs_us
+        p.ampdu_lim, p.msdu_payload, p.ppdu_max = dd.ampdu_lim, float(wc.msdu_payload_bytes), PPDU_MAX_US
+        p.bg_w, p.bg_rate, p.bg_B = float(wc.bg_stations), dd.bg_rate, float(wc.bg_frame_bytes)
+        for i, v in enumerate(dd.rates):
+            p.rates[i], p.thr[i], p.mcs_ids[i] = float(v), float(dd.thr[i]), int(dd.mcs_ids[i])
+        for a in range(5):
+            p.ac_W0[a], p.ac_Wmax[a] = float(dd.ac_W0[a]), float(dd.ac_Wmax[a])
+            p.ac_aifsn[a], p.ac_txop[a] = float(dd.ac_aifsn[a]), float(dd.ac_txop[a])
+        for c, a in enumerate(dd.cls_ac):
+            p.cls_ac[c] = int(a)
+        for c, v in enumerate(cfg.msg_sizes):
+            p.sizes[c] = float(v)
+        for k, v in enumerate(dd.lgamma):
+            p.lgamma[k] = float(v)
+        # the AP's radio: the NRConfig of RadioMC for the APs (wifi/engine.py:82-97)
+        rc = radio_config(cfg, wc)
+        K = rc.shadow_modes
+        p.n_fields, p.n_modes = self._n_fields, K
+        gx, gy = rc.gnb_xy()[0]
+        p.gnb_x, p.gnb_y, p.ue_tx = gx, gy, rc.ue_tx_dbm
+        dc = (rc.shadow_dcorr_m, 0.0, 0.0)
+        p.spectrum = 0 if rc.shadow_acf == "sos" else 1
+        if rc.channel == "tr38901":
+            sc = SCENARIOS[rc.tr38901_scenario]
+            scn = rc.tr38901_scenario
+            h_bs = float(rc.gnb_height_m) if rc.gnb_height_m is not None else sc.h_bs
+            h_ut, fc = float(rc.ue_height_m), rc.carrier_ghz
+            dbp = breakpoint_m(scn, fc, h_bs, h_ut)
+            p.radio_model = 1
+            p.hh2 = (h_bs - h_ut) ** 2
+            p.dbp = dbp if math.isfinite(dbp) else float("inf")
+            if scn in ("UMa", "UMi"):
+                a, n1, b = (28.0, 22.0, 9.0) if scn == "UMa" else (32.4, 21.0, 9.5)
+                p.pl_a, p.pl_n1, p.pl_c20 = a, n1, 20 * math.log10(fc)
+                p.pl_c2 = b * math.log10(dbp ** 2 + (h_bs - h_ut) ** 2)
+            elif scn == "InH":
+                p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 32.4, 17.3, 20 * math.log10(fc), 0.0
+            else:
+                p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 31.84, 21.50, 19.00 * math.log10(fc), 0.0
+            if rc.tr38901_los != "los":
+                if scn == "UMi":
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 35.3, 22.4, 21.3 * math.log10(fc), 0.3 * (h_ut - 1.5)
+                elif scn == "UMa":
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 39.08, 13.54, 20 * math.log10(fc), 0.6 * (h_ut - 1.5)
+                else:
+                    p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 38.3, 17.30, 24.9 * math.log10(fc), 0.0
+            p.sig = SIGMA_SF[scn][0 if rc.tr38901_los == "los" else 1]
+            p.amp = 1.0 * math.sqrt(2 / K)
+            p.spectrum = 1
+            dc = (sc.sf_corr_los_m, sc.sf_corr_nlos_m, sc.los_corr_m)
+        else:
+            p.radio_model = 0
+            p.amp = rc.shadow_sigma_db * math.sqrt(2 / K)
+            p.pl_const, p.pl_exp10 = rc.pl_const_db, 10 * rc.pathloss_exp
+        for i in range(3):
+            p.dcorr[i] = dc[i]
+        self._cparams = p
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.dev).cuda_stream
+
+    # ------------------------------------------------------------------ API
+    @property
+    def clock(self):
+        return self.st["clock"].clone()
+
+    def output_schema(self):
+        E, R, F = "E", "R", "F"
+        shapes = {"newest": ("[E,R]", "int64"), "det_env": ("[E]", "bool"), "delivered": ("[E,R,F]", "bool"),
+                  "timed_out": ("[E,R,F]", "bool"), "cap": ("[E,R,F]", "int64"), "cls": ("[E,R,F]", "int64"),
+                  "delay": ("[E,R,F]", "float32"), "queue_len": ("[E,R]", "int64"),
+                  "queue_bytes": ("[E,R]", "float32"), "sinr_db": ("[E,R]", "float32"), "t": ("[E]", "int64"),
+                  "serving_cell": ("[E,R]", "int64"), "wifi_mcs": ("[E,R]", "int64"),
+                  "wifi_rate_mbps": ("[E,R]", "float32"), "wifi_access_ms": ("[E,R]", "float32"),
+                  "wifi_p_fail": ("[E,R]", "float32"), "wifi_busy": ("[E,R]", "float32")}
+        del E, R, F
+        return {k: {"shape": s, "dtype": dt, "when": "always"} for k, (s, dt) in shapes.items()}
+
+    def _tvec(self, t):
+        """Per-env step [E] int64 on the device (None: the engine clock)."""
+        if t is None:
+            return None
+        if isinstance(t, torch.Tensor):
+            t = t.to(self.dev, torch.long)
+            return t.expand(self.E).contiguous() if t.dim() == 0 else t.contiguous()
+        return torch.full((self.E,), int(t), dtype=torch.long, device=self.dev)
+
+    def reset(self, env_ids=None):
+        """Re-initialize env_ids (None = all; index tensor, list or bool mask [E]) (levels/base.py:142-157)."""
+        if isinstance(env_ids, slice) and env_ids == slice(None):
+            env_ids = None
+        m8 = None
+        if env_ids is not None:
+            if isinstance(env_ids, torch.Tensor) and env_ids.dtype == torch.bool:
+                mask = env_ids.to(self.dev)
+            else:
+                ids = torch.as_tensor(env_ids if isinstance(env_ids, torch.Tensor) else list(env_ids),
+                                      dtype=torch.long, device=self.dev).reshape(-1)
+                if ids.numel() == 0:
+                    return
+                mask = torch.zeros(self.E, dtype=torch.bool, device=self.dev)
+                mask[ids] = True
+            m8 = mask.to(torch.uint8).contiguous()
+        _lib.check(self._lib.inet_wifi_reset(C.byref(self._cstate), C.byref(self._cparams),
+                                             None if m8 is None else m8.data_ptr(), self._stream()), "wifi reset")
+
+    def submit(self, t, requests, snr_db=None):
+        """Enqueue one message per robot (Requests or send [E,R]); returns accepted [E,R] bool
+        (levels/base.py:223-246)."""
+        tv = self._tvec(t)
+        req = requests if isinstance(requests, Requests) or hasattr(requests, "send") else Requests(send=requests)
+        send = req.send.to(self.dev, torch.long).contiguous()
+        if tuple(send.shape) != (self.E, self.R):
+            raise ValueError(f"send must be [E,R] = [{self.E},{self.R}], got {tuple(send.shape)}")
+        det = None if req.det is None else req.det.to(self.dev, torch.uint8).contiguous()
+        hid = None if req.hid is None else req.hid.to(self.dev, torch.long).contiguous()
+        snr = None if snr_db is None else snr_db.to(self.dev, torch.float32).contiguous()
+        acc = torch.empty(self.E, self.R, dtype=torch.bool, device=self.dev)
+        ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+        _lib.check(self._lib.inet_wifi_submit(
+            C.byref(self._cstate), C.byref(self._cparams), ptr(tv), send.data_ptr(), ptr(det), ptr(hid), ptr(snr),
+            None, 0, acc.data_ptr(), self._stream()), "wifi submit")
+        return acc
+
+    def submit_counts(self, counts, t=None):
+        """Enqueue counts [E,R,NC] messages per class in one launch: the submit() calls of class 1 first, one call per
+        message index. Returns accepted messages [E,R] int32."""
+        tv = self._tvec(t)
+        cnt = counts.to(self.dev, torch.uint8).contiguous()
+        if tuple(cnt.shape[:2]) != (self.E, self.R) or cnt.shape[-1] > len(self.config.msg_sizes):
+            raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        acc = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
+        _lib.check(self._lib.inet_wifi_submit(
+            C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), None, None, None,
+            None, cnt.data_ptr(), cnt.shape[-1], acc.data_ptr(), self._stream()), "wifi submit")
+        return acc
+
+    def add_frames(self, t, send, det, hid, snr_db=None):
+        """Legacy wrapper (NetSlot API)."""
+        self.submit(t, Requests(send, det, hid), snr_db)
+
+    def _alloc_out(self):
+        E, R, F, d = self.E, self.R, self.F, self.dev
+        e = lambda *s, dt: torch.empty(*s, dtype=dt, device=d)  # noqa: E731
+        o = {"newest": e(E, R, dt=torch.int64), "det_env": e(E, dt=torch.bool),
+             "delivered": e(E, R, F, dt=torch.bool), "timed_out": e(E, R, F, dt=torch.bool),
+             "cap": e(E, R, F, dt=torch.int64), "cls": e(E, R, F, dt=torch.int64), "delay": e(E, R, F, dt=torch.float32),
+             "queue_len": e(E, R, dt=torch.int64), "queue_bytes": e(E, R, dt=torch.float32),
+             "sinr_db": e(E, R, dt=torch.float32), "t": e(E, dt=torch.int64), "serving_cell": e(E, R, dt=torch.int64),
+             "wifi_mcs": e(E, R, dt=torch.int64), "wifi_rate_mbps": e(E, R, dt=torch.float32),
+             "wifi_access_ms": e(E, R, dt=torch.float32), "wifi_p_fail": e(E, R, dt=torch.float32),
+             "wifi_busy": e(E, R, dt=torch.float32)}
+        c = _lib.InetWifiOutputs()
+        for a, k in (("delivered", "delivered"), ("timed_out", "timed_out"), ("cap", "cap"), ("cls", "cls"),
+                     ("delay", "delay"), ("newest", "newest"), ("queue_len", "queue_len"),
+                     ("serving_cell", "serving_cell"), ("mcs", "wifi_mcs"), ("queue_bytes", "queue_bytes"),
+                     ("sinr_db", "sinr_db"), ("rate_mbps", "wifi_rate_mbps"), ("access_ms", "wifi_access_ms"),
+                     ("p_fail", "wifi_p_fail"), ("busy", "wifi_busy"), ("det_env", "det_env"), ("t", "t")):
+            setattr(c, a, o[k].data_ptr())
+        return o, c
+
+    def step(self, t=None, x=None, cur_hid=None, *, rx_dbm=None, sense=None):
+        """Advance [t, t+1). x: poses [E,R,2|3] (through the AP's radio) or the SNR [E,R] in dB; rx_dbm= [E,R,1]
+        gives the received power (dBm) instead (wifi/engine.py:207-225). Returns the reference's dict, or
+        (newest, det_env) in the legacy form with cur_hid."""
+        if sense is not None:
+            raise ValueError("sense= needs WifiConfig(hidden_nodes=True)")
+        if x is None and rx_dbm is None:
+            raise ValueError("pass poses, an SNR [E,R] or rx_dbm=[E,R,A]")
+        E, R = self.E, self.R
+        if rx_dbm is not None:
+            xin = rx_dbm.to(self.dev, torch.float32)
+            if tuple(xin.shape) != (E, R, 1):
+                raise ValueError(f"rx_dbm must be [E,R,A] = {(E, R, 1)}")
+            xin, kind = xin[..., 0].contiguous(), 2
+        elif x.dim() == 3:
+            xin, kind = x[..., :2].to(self.dev, torch.float32).contiguous(), 0
+        else:
+            xin, kind = x.to(self.dev, torch.float32).contiguous(), 1
+            if tuple(xin.shape) != (E, R):
+                raise ValueError(f"SNR must be [E,R] = {(E, R)}")
+        tv = self._tvec(t)
+        hid = None if cur_hid is None else torch.as_tensor(cur_hid).to(self.dev, torch.long).contiguous()
+        o, c = self._alloc_out()
+        ev = self.kernel_events
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream(self.dev))
+        _lib.check(self._lib.inet_wifi_step(
+            C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), kind,
+            xin.data_ptr(), None if hid is None else hid.data_ptr(), C.byref(c), self._stream()), "wifi step")
+        if ev is not None:
+            e1.record(torch.cuda.current_stream(self.dev))
+            ev.append((e0, e1))
+        if cur_hid is not None:
+            return o["newest"], o["det_env"]
+        return o
+
+    # set to a list to record (start, end) events around every step-kernel launch, on the launch stream
+    kernel_events = None
+
+    # ------------------------------------------------------------------ state in the reference's names
+    def state_dict(self):
+        """The state tensors of the reference's WifiNet.state_dict() (FIFO fields [E,R,F], clock, mean-field state,
+        counter RNG, radio plane waves), on the engine's device."""
+        st = self.st
+        rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
+        L = lambda x: x.long()  # noqa: E731
+        out = {"cap": rs(L(st["cap"])), "cls": rs(L(st["cls"])), "det": rs(st["det"] != 0), "hid": rs(L(st["hid"])),
+               "rem": rs(st["rem"]), "dlv": torch.full_like(rs(st["rem"]), math.inf), "f_nact": rs(L(st["f_nact"])),
+               "f_snr": rs(st["f_snr"]), "f_own": rs(L(st["f_own"])), "clock": st["clock"].clone(),
+               "_last_snr": st["last_snr"], "_last_hid": st["last_hid"], "tau": st["tau"],
+               "roam_left": L(st["roam_left"]), "att_n": st["att_n"], "att_logp": st["att_logp"],
+               "credit": st["credit"], "serv": L(st["serv"]), "pending": st["pending"] != 0,
+               "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"])}
+        f = st["field"]
+        if self.config.channel == "tr38901":
+            for j, n in enumerate(("sf_los", "sf_nlos", "los_field")):
+                out[f"radio.ch.{n}.k"] = f[None, :, j, :, :2]
+                out[f"radio.ch.{n}.phi"] = f[None, :, j, :, 2]
+        else:
+            out["radio.k"] = f[None, :, 0, :, :2]
+            out["radio.phi"] = f[None, :, 0, :, 2]
+        return out
+
+    def load_state_dict(self, sd):
+        """Load reference-named state (the keys of state_dict(); tensors on any device) into the device buffers."""
+        st, d = self.st, self.dev
+        g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+        rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
+        I = lambda x: x.to(torch.int32)  # noqa: E731
+        cap = g("cap")
+        st["qlen"].copy_(I((cap >= 0).sum(-1)))
+        for k in ("cap", "cls", "hid", "f_nact", "f_own"):
+            st[k].copy_(rs(I(g(k))))
+        st["det"].copy_(rs(g("det").to(torch.uint8)))
+        st["rem"].copy_(rs(g("rem").float()))
+        st["f_snr"].copy_(rs(g("f_snr").float()))
+        st["clock"].copy_(g("clock").long())
+        st["last_snr"].copy_(g("_last_snr").float())
+        st["last_hid"].copy_(g("_last_hid").long())
+        st["tau"].copy_(g("tau").float())
+        for k in ("roam_left", "serv"):
+            st[k].copy_(I(g(k)))
+        for k in ("att_n", "att_logp", "credit"):
+            st[k].copy_(g(k).float())
+        st["pending"].copy_(g("pending").to(torch.uint8))
+        st["episode"].copy_(I(g("rng.episode")))
+        st["ctr_submit"].copy_(I(g("rng.ctr[1]")))
+        st["ctr_step"].copy_(I(g("rng.ctr[2]")))
+        names = (("sf_los", 0), ("sf_nlos", 1), ("los_field", 2)) if self.config.channel == "tr38901" else ()
+        if names:
+            for n, j in names:
+                if f"radio.ch.{n}.k" in sd:
+                    st["field"][:, j, :, :2].copy_(g(f"radio.ch.{n}.k")[0])
+                    st["field"][:, j, :, 2].copy_(g(f"radio.ch.{n}.phi")[0])
+        elif "radio.k" in sd:
+            st["field"][:, 0, :, :2].copy_(g("radio.k")[0])
+            st["field"][:, 0, :, 2].copy_(g("radio.phi")[0])

@@ -1,6 +1,6 @@
-"""The C ABI: libinet_nr.so loads (no GPU needed), exports every function include/inet_nr.h declares, and the
-ctypes mirrors of the structs have the C layout (checked against sizeof / offsetof from the header compiled by gcc).
-No compute entry point is called here."""
+"""The C ABI: libinet_nr.so loads (no GPU needed), exports every function include/inet_nr.h and include/inet_wifi.h
+declare, and the ctypes mirrors of the structs have the C layout (checked against sizeof / offsetof from the headers
+compiled by gcc). No compute entry point is called here."""
 import ctypes
 import os
 import re
@@ -13,6 +13,7 @@ from conftest import ROOT
 from isaac_net_amd import _lib
 
 HEADER = os.path.join(ROOT, "include", "inet_nr.h")
+WIFI_HEADER = os.path.join(ROOT, "include", "inet_wifi.h")
 
 
 def _lib_path():
@@ -22,9 +23,9 @@ def _lib_path():
     return _lib.LIB_PATH
 
 
-def declared_functions():
-    src = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int32_t|const char \*)\s*(inet_nr_\w+)\s*\(", src, re.M)))
+def declared_functions(header=HEADER, prefix="inet_nr_"):
+    src = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|const char \*)\s*(" + prefix + r"\w+)\s*\(", src, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -38,14 +39,22 @@ def test_library_exports_every_declared_symbol():
     assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 2
     lib.inet_nr_build_info.restype = ctypes.c_char_p
     assert b"gfx950" in lib.inet_nr_build_info()
+    wifi = declared_functions(WIFI_HEADER, "inet_wifi_")
+    assert wifi == sorted(["inet_wifi_abi_version", "inet_wifi_step", "inet_wifi_submit", "inet_wifi_reset"])
+    for n in wifi:
+        assert hasattr(lib, n), n
+    lib.inet_wifi_abi_version.restype = ctypes.c_int32
+    assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 1
 
 
-STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow")
+STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetWifiState",
+           "InetWifiParams", "InetWifiOutputs")
 
 
 def test_ctypes_layout_matches_header():
     py = {n: getattr(_lib, n) for n in STRUCTS if hasattr(_lib, n)}
-    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', f'#include "{WIFI_HEADER}"',
+             "int main(void) {"]
     for n, cls in py.items():
         lines.append(f'printf("{n} %zu\\n", sizeof({n}));')
         for f, _ in cls._fields_:

@@ -1,0 +1,190 @@
+"""Level WIFI on the GPU: the HIP engine against the reference's golden trajectories (tests/golden/traj_w_*.npz,
+bitwise equal to the oracle by test_wifi_oracle), teacher-forced (the reference state is loaded before every step)
+and free running from the same seed, plus the counts form of submit and a larger free run against the oracle.
+
+Bar: integer state and integer / boolean outputs bit-exact (FIFO fields, queue lengths, deliveries, timeouts,
+newest, det_env, MCS, counters, clock, contention counts att_n); bytes left (rem), queue bytes and, with Poisson
+accesses, the finish times and delays bit-exact too (they are exact arithmetic on the integer access counts). Floats
+that pass through transcendental functions (the mean-field tau, log failure sums, renewal credit, access time,
+failure and busy averages, SNR from poses) within 2e-5 relative (the solve's log1p / exp / pow are evaluated in double
+precision and rounded once on the GPU, while the CPU uses its own vectorized float routines; a fixed-point iteration
+carries those last-bit differences), with absolute floors stated below."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import replay
+from oracle.wifi_oracle import WifiOracle
+import isaac_net_amd as P
+from isaac_net_amd.wifi_config import WifiConfig
+
+pytestmark = pytest.mark.gpu
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_dcf"]
+
+# relative tolerance, absolute floor
+FLOAT_TOL = {"tau": (2e-5, 1e-9), "att_logp": (2e-5, 1e-6), "credit": (2e-5, 1e-5), "_last_snr": (1e-5, 6.1e-5),
+             "f_snr": (1e-5, 6.1e-5), "out.sinr_db": (1e-5, 6.1e-5), "out.wifi_access_ms": (2e-5, 0.0),
+             "out.wifi_p_fail": (2e-5, 1e-7), "out.wifi_busy": (2e-5, 1e-7), "out.delay": (2e-5, 2e-6)}
+# the plane waves: phases bitwise, wave vectors within two float32 ulp (cos / sin rounding)
+FIELD_KEYS = ("radio.k", "radio.ch.sf_los.k", "radio.ch.sf_nlos.k", "radio.ch.los_field.k")
+MAX_DEV = {}
+
+
+def load(name):
+    return replay.load_wifi_case(os.path.join(GOLDEN, f"traj_{name}.npz"), P.NRConfig, WifiConfig)
+
+
+def close(key, m, r):
+    m = np.asarray(m)
+    r = np.asarray(r)
+    if m.shape != r.shape:
+        return np.zeros(r.shape, bool)
+    if key in FIELD_KEYS:
+        return np.abs(m.astype(np.float64) - r) <= 2 * np.spacing(np.abs(r).astype(np.float32)) + 1e-30
+    same = (m == r) | ((m != m) & (r != r))
+    tol = FLOAT_TOL.get(key)
+    if tol is None:
+        return same
+    m64, r64 = m.astype(np.float64), r.astype(np.float64)
+    dev = np.where(same, 0.0, np.abs(m64 - r64))
+    if dev.size:
+        MAX_DEV[key] = max(MAX_DEV.get(key, 0.0), float(np.nanmax(dev)))
+    lim = np.maximum(tol[0] * np.maximum(np.abs(m64), np.abs(r64)), tol[1])
+    return same | (dev <= lim)
+
+
+def compare(ref, pre, vals):
+    """{key: elements out of tolerance} for the keys of vals that the reference holds under pre/."""
+    bad = {}
+    for k, v in vals.items():
+        rk = f"{pre}/{k}"
+        if rk not in ref.files:
+            continue
+        ok = close(k, v.detach().cpu().numpy() if torch.is_tensor(v) else v, ref[rk])
+        if not ok.all():
+            bad[k] = int((~ok).sum())
+    return bad
+
+
+def snapshot(ref, pre):
+    return {k.split("/", 1)[1]: ref[k] for k in ref.files if k.startswith(pre + "/")
+            and not k.split("/", 1)[1].startswith(("out.", "accepted", "n_submit"))}
+
+
+@pytest.mark.parametrize("name", WIFI_CASES)
+def test_wifi_teacher_forced(name):
+    print(f"wifi case {name} teacher-forced", flush=True)
+    ref, cfg, kind = load(name)
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    eng = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    to = lambda a: torch.from_numpy(np.asarray(a)).to("cuda:0")  # noqa: E731
+    bad = []
+    for s in range(T):
+        eng.load_state_dict(snapshot(ref, f"s{s - 1:03d}" if s > 0 else "init"))
+        ids = np.nonzero(ref["reset_mask"][s])[0]
+        if len(ids):
+            eng.reset(ids.tolist())
+            b = compare(ref, f"reset{s:03d}", eng.state_dict())
+            if b:
+                bad.append((s, "reset", b))
+            eng.load_state_dict(snapshot(ref, f"reset{s:03d}"))
+        acc = [eng.submit(None, to(send)).cpu().numpy() for send in replay.submits(ref["counts"][s])]
+        if acc and not np.array_equal(np.stack(acc), ref[f"s{s:03d}/accepted"]):
+            bad.append((s, "accepted"))
+        o = eng.step(None, to(ref["x"][s]))
+        b = compare(ref, f"s{s:03d}", {"out." + k: v for k, v in o.items()})
+        b.update(compare(ref, f"s{s:03d}", eng.state_dict()))
+        if b:
+            bad.append((s, b))
+    print(f"{name}: max |deviation| { {k: f'{v:.2e}' for k, v in MAX_DEV.items()} }", flush=True)
+    MAX_DEV.clear()
+    assert not bad, bad[:5]
+
+
+@pytest.mark.parametrize("name", WIFI_CASES)
+def test_wifi_free_running(name):
+    print(f"wifi case {name} free running", flush=True)
+    ref, cfg, kind = load(name)
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    eng = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    to = lambda a: torch.from_numpy(np.asarray(a)).to("cuda:0")  # noqa: E731
+    bad = []
+    b = compare(ref, "init", eng.state_dict())
+    if b:
+        bad.append(("init", b))
+    for s in range(T):
+        ids = np.nonzero(ref["reset_mask"][s])[0]
+        if len(ids):
+            eng.reset(ids.tolist())
+        acc = [eng.submit(None, to(send)).cpu().numpy() for send in replay.submits(ref["counts"][s])]
+        if acc and not np.array_equal(np.stack(acc), ref[f"s{s:03d}/accepted"]):
+            bad.append((s, "accepted"))
+        o = eng.step(None, to(ref["x"][s]))
+        b = compare(ref, f"s{s:03d}", {"out." + k: v for k, v in o.items()})
+        b.update(compare(ref, f"s{s:03d}", eng.state_dict()))
+        if b:
+            bad.append((s, b))
+    print(f"{name}: free running; max |deviation| { {k: f'{v:.2e}' for k, v in MAX_DEV.items()} }", flush=True)
+    MAX_DEV.clear()
+    assert not bad, bad[:5]
+
+
+def test_wifi_submit_counts_equals_per_class_calls():
+    """The counts form (one launch) leaves the FIFO exactly as the per-class, per-message-index submit calls."""
+    ref, cfg, kind = load("w_mean")
+    E, R = int(ref["E"]), int(ref["R"])
+    a = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    b = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    to = lambda x: torch.from_numpy(np.asarray(x)).to("cuda:0")  # noqa: E731
+    for s in range(6):
+        cnt = ref["counts"][s]
+        n_a = sum(a.submit(None, to(send)).long() for send in replay.submits(cnt))
+        n_b = b.submit_counts(to(cnt.astype(np.uint8)))
+        assert torch.equal(n_b.long(), torch.as_tensor(n_a, device="cuda:0").long().expand(E, R))
+        x = to(ref["x"][s])
+        a.step(None, x)
+        b.step(None, x)
+    sa, sb = a.state_dict(), b.state_dict()
+    for k in ("cap", "cls", "det", "hid", "rem", "f_nact", "f_snr", "f_own", "tau", "credit"):
+        assert torch.equal(sa[k], sb[k]), k
+
+
+def test_wifi_larger_free_run_vs_oracle():
+    """E = 64 envs x 16 robots of the DCF workload for 12 steps, free running against the oracle: integer state and
+    outputs bit-exact, every float within the tolerances above."""
+    _, cfg, _ = load("w_dcf")
+    E, R, T = 64, 16, 12
+    rs = np.random.default_rng(11)
+    eng = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=3)
+    orc = WifiOracle(E, R, cfg, seed=3)
+    rad = 50.0 * np.sqrt(rs.uniform(size=(E, R)))
+    ang = rs.uniform(0, 2 * np.pi, size=(E, R))
+    pos = np.stack([rad * np.cos(ang), rad * np.sin(ang)], -1).astype(np.float32)
+    bad = []
+    for s in range(T):
+        counts = rs.poisson(1.5, size=(E, R))
+        for i in range(int(counts.max())):
+            send = np.where(counts > i, 1, 0).astype(np.int64)
+            acc_g = eng.submit(None, torch.from_numpy(send).to("cuda:0")).cpu().numpy()
+            acc_o = orc.submit(None, torch.from_numpy(send)).numpy()
+            if not np.array_equal(acc_g, acc_o):
+                bad.append((s, "accepted"))
+        og = eng.step(None, torch.from_numpy(pos).to("cuda:0"))
+        oo = orc.step(None, torch.from_numpy(pos))
+        ref = {f"s/out.{k}": v.numpy() for k, v in oo.items()}
+        ref.update({f"s/{k}": v.numpy() for k, v in orc.state().items()})
+
+        class D(dict):
+            files = property(lambda self: list(self.keys()))
+        d = D(ref)
+        b = compare(d, "s", {"out." + k: v for k, v in og.items()})
+        b.update(compare(d, "s", eng.state_dict()))
+        if b:
+            bad.append((s, b))
+        pos = pos + rs.normal(0, 0.5, size=pos.shape).astype(np.float32)
+    print(f"64x16 free run: max |deviation| { {k: f'{v:.2e}' for k, v in MAX_DEV.items()} }", flush=True)
+    MAX_DEV.clear()
+    assert not bad, bad[:5]
