@@ -1,6 +1,7 @@
 """Benchmark of the NR uplink engine hot path on one MI355X: robot-slots/s of the RL-scale workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--out-format reference|compact] [--no-cpu]
+    python bench.py --workload wifi_dcf [--envs-per-wave G]     (level WIFI: station-substeps/s)
 
 A step is one control step of every env: submit_counts (this step's message arrivals, one launch) and step (poses in,
 the reference's output dict out: one launch of the fused step kernel), launched from Python every step (--graph:
@@ -71,6 +72,99 @@ def step_kernel_touched_bytes(eng, qlen_mean, kept_mean):
     return total - eng.E * eng.R * (fifo_full - fifo_touched)
 
 
+def wifi_step_bytes(eng):
+    """Algorithmic HBM bytes of one Wi-Fi step-kernel launch: per station-step the frame FIFO (F slots of cap, cls,
+    det, hid, rem, f_nact, f_snr, f_own = 29 B) and the per-station words (queue length, last SNR, roaming, serving AP,
+    contention count, log-failure sum, credit, tau = 32 B) read and written once, the pose (8 B), the [E,R,F] outputs
+    (delivered, timed out, cap, cls, delay = 22 B per slot) and the per-station outputs (4 int64 + 6 float32 = 56 B);
+    per env the background station's tau, clock, hazard id, RNG key and counters and the shadowing field."""
+    p = eng._cparams
+    F = eng.F
+    per_robot = 2 * (F * 29 + 32) + 8 + F * 22 + 56
+    per_env = 2 * (4 + 8 + 8 + 1 + 4 * 4) + p.n_fields * p.n_modes * 3 * 4
+    return eng.E * eng.R * per_robot + eng.E * per_env, per_robot
+
+
+def wifi_cpu_baseline(wl, cfg, E_cpu, steps, warmup):
+    import torch
+
+    from oracle.wifi_oracle import WifiOracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    R = wl.R
+    ora = WifiOracle(E_cpu, R, cfg, seed=0)
+    poses = wl.poses[:, :E_cpu].cpu()
+    counts = wl.counts[:, :E_cpu].cpu().numpy()
+
+    def one(s):
+        c = counts[s]
+        for ci in range(c.shape[-1]):
+            for i in range(int(c[..., ci].max())):
+                ora.submit(None, torch.from_numpy((c[..., ci] > i).astype("int64") * (ci + 1)))
+        ora.step(None, poses[s])
+    for s in range(warmup):
+        one(s)
+    t0 = time.perf_counter()
+    for s in range(warmup, warmup + steps):
+        one(s)
+    dt = time.perf_counter() - t0
+    return {"value": E_cpu * R * ora.K * steps / dt, "unit": "station-substeps/s", "cores": threads, "kind": "port",
+            "sample": f"oracle (torch CPU restatement of the reference WifiNet) on the first {E_cpu} of the "
+                      f"{wl.E} envs x {R} stations, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
+            "ms_per_step": 1e3 * dt / steps}
+
+
+def run_wifi(args, P, torch):
+    """The level WIFI workload: one line with station-substeps/s and the step kernel's roofline fields."""
+    from isaac_net_amd import scenarios as S
+    dev = "cuda:0"
+    E = args.envs if args.envs_set else 2048
+    R = args.robots if args.robots_set else 16
+    total = args.warmup + args.steps
+    print(f"# workload wifi_dcf {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev, name="wifi_dcf")
+    cfg = wl.cfg
+    from isaac_net_amd.wifi_engine import HipWifiEngine
+    eng = HipWifiEngine(E, R, dev, cfg, seed=0, envs_per_wave=args.envs_per_wave)
+    K = eng.K
+    for s in range(args.warmup):
+        eng.submit_counts(wl.counts[s])
+        eng.step(None, wl.poses[s])
+    torch.cuda.synchronize()
+    eng.kernel_events = ev = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        s = args.warmup + i
+        eng.submit_counts(wl.counts[s])
+        eng.step(None, wl.poses[s])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.kernel_events = None
+    k_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    k_avg = sum(k_ms) / len(k_ms)
+    nbytes, per_robot = wifi_step_bytes(eng)
+    achieved = nbytes / (k_avg * 1e-3) / 1e9
+    res = {"metric": f"station-substeps/sec @{E} envs×{R} stations K={K} (level WIFI, DCF)",
+           "value": E * R * K * args.steps / dt, "unit": "station-substeps/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"wifi_dcf: {E} envs x {R} stations at one AP, DCF (CWmin 15, CWmax 1023, 7 "
+                                  f"attempts), 802.11ax 20 MHz 12 MCS, K={K} sub-steps of 1 ms, 1500 B @0.4 per "
+                                  "station-step, FIFO 16, 50 m disc, log-distance + shadowing",
+                      "envs": E, "stations": R, "substeps_per_step": K, "envs_per_wave": args.envs_per_wave,
+                      "parallelism": "single GPU", "launch": "eager"},
+           "env_steps_per_s": E * args.steps / dt,
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "wifi_step_kernel",
+                        "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
+                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_station_step": per_robot}}
+    if not args.no_cpu:
+        print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = wifi_cpu_baseline(wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)
+    print(json.dumps(res), flush=True)
+
+
 def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
     import torch
 
@@ -106,8 +200,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--envs", type=int, default=4096)
-    ap.add_argument("--robots", type=int, default=32)
+    ap.add_argument("--workload", default="rl_scale", choices=("rl_scale", "wifi_dcf"),
+                    help="rl_scale: the NR engine's RL-scale workload (the headline metric); wifi_dcf: level WIFI")
+    ap.add_argument("--envs", type=int, default=None)
+    ap.add_argument("--robots", type=int, default=None)
+    ap.add_argument("--envs-per-wave", type=int, default=1, help="level WIFI: envs per 64-lane wavefront")
     ap.add_argument("--out-format", default="reference", choices=("reference", "compact"))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--graph", action="store_true",
@@ -125,9 +222,13 @@ def main():
         sys.exit(2)
     import torch
     P = load_package()
+    args.envs_set, args.robots_set = args.envs is not None, args.robots is not None
+    if args.workload == "wifi_dcf":
+        return run_wifi(args, P, torch)
     from isaac_net_amd import scenarios as S
     dev = "cuda:0"
-    E, R = args.envs, args.robots
+    E = args.envs if args.envs_set else 4096
+    R = args.robots if args.robots_set else 32
     total = args.warmup + args.steps
     print(f"# workload rl_scale {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
     wl = S.Workload(E, R, total, seed=0, device=dev)

@@ -43,8 +43,9 @@ DEV float pow_int_torch(float x, int n) {
     if (n == 3) return (x * x) * x;
     return pow_r(x, (float)n);
 }
-// p ** k of tau(p) (torch pow of two float tensors): 1 at k = 0, p at k = 1
-DEV float pow_k(float p, int k) { return k == 0 ? 1.0f : (k == 1 ? p : pow_r(p, (float)k)); }
+// p ** k of tau(p) (torch pow of two float tensors) for an integer k >= 0: double-precision binary powering,
+// rounded once
+DEV float pow_k(float p, int k) { return pow_count(p, (float)k); }
 DEV float fminn(float a, float b) { return a != a ? a : (b != b ? b : (a < b ? a : b)); }   // torch.minimum
 
 // AccessTiming.cap_bytes (wifi/phy.py:130-139): application bytes one access carries
@@ -68,8 +69,28 @@ DEV void access_times(const InetWifiParams& pm, float B, float rate, float aifsn
     }
 }
 // tau(p) of meanfield.tau_from_p: sum_k p^k / sum_k p^k (W_k + 1) / 2 over the L stages, W_k = min(2^k W0, Wmax),
-// both sums in torch's CPU order
+// both sums in torch's CPU order. p^k is the double-precision running product rounded once (the correctly rounded
+// power unless p^k lies within ~k 2^-53 relative of a float rounding boundary). Under 8 stages the CPU order adds
+// stages 0..3 into four partial sums and the later stages into the first, so one pass over k in order suffices.
 DEV float tau_of_p(float p, float W0, float Wm, int L) {
+    if (L < 8) {
+        float n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f, d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+        const double pd = (double)p;
+        double pw = 1.0;
+        float wk = W0;
+        for (int k = 0; k < L; ++k) {
+            const float pk = (float)pw;
+            pw *= pd;
+            const float t = pk * ((fminn(wk, Wm) + 1.0f) * 0.5f);
+            wk = wk * 2.0f;
+            const int slot = L >= 4 && k < 4 ? k : 0;
+            if (slot == 0) { n0 += pk; d0 += t; }
+            else if (slot == 1) { n1 += pk; d1 += t; }
+            else if (slot == 2) { n2 += pk; d2 += t; }
+            else { n3 += pk; d3 += t; }
+        }
+        return (((n0 + n1) + n2) + n3) / (((d0 + d1) + d2) + d3);
+    }
     float num = aten_row_sum(L, [&](int k) { return pow_k(p, k); });
     float den = aten_row_sum(L, [&](int k) {
         float wk = fminn(W0 * exp2f((float)k), Wm);

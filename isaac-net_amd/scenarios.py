@@ -7,8 +7,12 @@ control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 
               UMi LOS around a gNB at the centre of a 100 m square, i.i.d. Rayleigh block fading per slot.
   rl_scale    4096 envs x 32 robots, K = 10, PF with EWMA 0.01, 8 HARQ x 5 transmissions, Rician K = 3 dB, 200 B at
               Poisson 0.8 + 4000 B at Poisson 0.1, FIFO 32, random walk at 1 m/s in a 200 m square, UMi LOS.
+  wifi_dcf    level WIFI: 2048 envs x 16 stations at one AP, legacy DCF parameters (CWmin 15, CWmax 1023, binary
+              exponential backoff over 7 attempts), 802.11ax 20 MHz with its 12-entry MCS table, 20 sub-steps of 1 ms
+              per control step, 1500 B at Poisson 0.4, FIFO 16, stations uniform in a 50 m disc around the AP with a
+              1 m/s random walk kept inside the disc, log-distance path loss with plane-wave shadowing.
 Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
-the square; arrival counts per class), identical for the GPU engine and the CPU oracle.
+the square or disc; arrival counts per class), identical for the GPU engine and the CPU oracle.
 """
 from __future__ import annotations
 
@@ -38,9 +42,19 @@ def rl_scale_config(**kw):
     return NRConfig(**base)
 
 
+def wifi_dcf_config(**kw):
+    from .wifi_config import WifiConfig
+    base = dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,), cell_positions_m=((0.0, 0.0),),
+                wifi=WifiConfig(access_category="DCF", standard="ax", bandwidth_mhz=20), seed=0)
+    base.update(kw)
+    return NRConfig(**base)
+
+
 WORKLOADS = {
     "plumbing": dict(cfg=plumbing_config, E=64, R=8, arena=100.0, speed=0.0, rates=(0.5,), steps=1000),
     "rl_scale": dict(cfg=rl_scale_config, E=4096, R=32, arena=200.0, speed=1.0, rates=(0.8, 0.1), steps=500),
+    "wifi_dcf": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
+                     level="WIFI"),
 }
 
 
@@ -51,14 +65,26 @@ class Workload:
     def __init__(self, E, R, steps, seed=0, device="cpu", name="rl_scale"):
         w = WORKLOADS[name]
         self.cfg = w["cfg"]()
+        self.level = w.get("level", "L2")
         rs = np.random.default_rng(seed)
-        a, step_m = w["arena"], w["speed"] * self.cfg.control_step_ms * 1e-3
-        p = rs.uniform(0.0, a, size=(E, R, 2))
+        step_m = w["speed"] * self.cfg.control_step_ms * 1e-3
         poses = np.empty((steps, E, R, 2), np.float32)
+        if "radius" in w:                                   # uniform in a disc around the AP at the origin
+            rad = w["radius"]
+            r0, a0 = rad * np.sqrt(rs.uniform(size=(E, R))), rs.uniform(0.0, 2 * math.pi, size=(E, R))
+            p = np.stack([r0 * np.cos(a0), r0 * np.sin(a0)], -1)
+        else:
+            a = w["arena"]
+            p = rs.uniform(0.0, a, size=(E, R, 2))
         for s in range(steps):
             poses[s] = p
             ang = rs.uniform(0.0, 2 * math.pi, size=(E, R))
-            p = np.clip(p + step_m * np.stack([np.cos(ang), np.sin(ang)], -1), 0.0, a)
+            p = p + step_m * np.stack([np.cos(ang), np.sin(ang)], -1)
+            if "radius" in w:
+                n = np.linalg.norm(p, axis=-1, keepdims=True)
+                p = np.where(n > rad, p * (rad / np.maximum(n, 1e-9)), p)
+            else:
+                p = np.clip(p, 0.0, a)
         counts = np.stack([rs.poisson(lam, size=(steps, E, R)) for lam in w["rates"]], -1)
         self.poses = torch.from_numpy(poses).to(device)
         self.counts = torch.from_numpy(np.minimum(counts, 255).astype(np.uint8)).to(device)
