@@ -221,12 +221,14 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     __shared__ __align__(16) float s_se[MAX_M];
     __shared__ float s_beta[MAX_M], s_rbeta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
-    __shared__ int s_eq[MAX_M * MAX_EQW];
+    __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
     __shared__ int s_ulrel[MAX_UL_ROWS];
     __shared__ float s_x[2 * S * STEP_WAVE];                     // per-lane rows: fading normals, RBG SINR (dB)
     __shared__ float s_lin[S * STEP_WAVE];                       // per-lane rows: linear RBG SINR
     __shared__ int s_la_i[2 * STEP_WAVE], s_la_slot[STEP_WAVE], s_la_top[STEP_WAVE];   // link adaptation work list
     __shared__ float s_la_f[3 * STEP_WAVE];
+    __shared__ uint8_t s_list[STEP_WAVE];                        // lanes that draw fading innovations this slot
+    __shared__ uint32_t s_bfe[STEP_WAVE];                        // per env of the wave: its fading key this slot
 
     const int lane = threadIdx.x;
     const int envs_pw = STEP_WAVE / rb;
@@ -260,7 +262,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     // reciprocals of the BLER table's grid steps (div_const)
     const float rds = 1.0f / tb.ds, rdc = 1.0f / tb.dc;
     if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
-    for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
+    if constexpr (IR)
+        for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
     for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
     if (lane == 0) {
         int j = 0;
@@ -365,29 +368,61 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 
     int n_ul = 0;
     const int g0 = (int)(T * (int64_t)N);
+    // i.i.d. fading (rho = 0 at every evolving row): a robot's fading state and CSI are then pure functions of the
+    // latest draw, so a robot with nothing to send and no HARQ process pending (it takes part in no decision for the
+    // rest of the step) skips the draws until the last row that fixes the stored state (the last UL slot for the CSI,
+    // the last row needing the state for h)
+    int last_ul_row = -1, last_h_row = -1;
+    bool iid = true;
+    for (int k = 0; k < n_rows; ++k) {
+        const int fl = rows[k].flags;
+        if (fl & 2) last_ul_row = k;
+        if ((fl & 4) && (fl & 8)) last_h_row = k;
+        if ((fl & 4) && rows[k].rho != 0.0f) iid = false;
+    }
     // ================================================================ slot loop
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
         const int g = g0 + row.rel;
         if ((row.flags & 4) && (row.flags & 8)) {  // AR(1) fading innovation of this slot (nr_engine.py:575-589)
-            // the 2 S normals of this robot go through LDS (s_x, s_lin are free here): drawing them in a rolled loop
-            // keeps one Box-Muller evaluation in flight instead of 2 S
-            // normal j = 2 S r + q uses hash elements 2j, 2j + 1: the element's hash input base + e * GOLD advances
-            // by 2 GOLD per normal
-            const uint32_t bf = mix32(base0 ^ row.salt_fade);
-            float* const s_z = s_x;
-            uint32_t hin = bf + (uint32_t)(4 * r * S) * GOLD;
-#pragma unroll 1
-            for (int q = 0; q < 2 * S; ++q) {
-                const uint32_t h1 = mix32(mix32(hin) ^ bf), h2 = mix32(mix32(hin + GOLD) ^ bf);
-                s_z[q * STEP_WAVE + lane] = normal_of(h1, h2);
-                hin += 2u * GOLD;
-            }
+            // The 2 S normals of every robot that needs them are drawn cooperatively by the whole wavefront: the
+            // (robot, subband) pairs are dealt round-robin over the 64 lanes, each pair's two normals land in the
+            // robot's LDS column (s_x), and the robot then updates its own state. Normal j = 2 S r + q (q = 2 s for
+            // the real part, 2 s + 1 for the imaginary one) uses hash elements 2j, 2j + 1.
+            bool busy = false;
 #pragma unroll
-            for (int s = 0; s < S; ++s) {
-                float zr = s_z[(2 * s) * STEP_WAVE + lane], zi = s_z[(2 * s + 1) * STEP_WAVE + lane];
-                hr[s] = row.rho * hr[s] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
-                hi[s] = row.rho * hi[s] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+            for (int p = 0; p < P; ++p) busy |= hm_state(hmeta[p]) == 1;
+            busy |= (enq - sent) > 0;
+            const bool full = !iid || k == last_ul_row || k == last_h_row;
+            const bool draw = act && (full || busy);
+            const unsigned long long need = __ballot(draw);
+            float* const s_z = s_x;
+            if (r == 0) s_bfe[eloc] = mix32(base0 ^ row.salt_fade);
+            if (draw) s_list[__builtin_popcountll(need & ((1ull << lane) - 1ull))] = (uint8_t)lane;
+            __syncthreads();
+            // pairs in subband-major order: the lanes of one pass write different robots' columns (no LDS bank
+            // conflicts between the pairs of one robot)
+            const int n_need = __builtin_popcountll(need);
+            const int items = n_need * S;
+#pragma unroll 1
+            for (int it = lane; it < items; it += STEP_WAVE) {
+                const int s = it / n_need, ri = it - s * n_need;
+                const int L = s_list[ri];
+                const uint32_t bf = s_bfe[L / rb];
+                const uint32_t hin = bf + (uint32_t)(4 * (L & (rb - 1)) * S + 4 * s) * GOLD;
+                const float zr = normal_of(mix32(mix32(hin) ^ bf), mix32(mix32(hin + GOLD) ^ bf));
+                const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bf), mix32(mix32(hin + 3u * GOLD) ^ bf));
+                s_z[(2 * s) * STEP_WAVE + L] = zr;
+                s_z[(2 * s + 1) * STEP_WAVE + L] = zi;
+            }
+            __syncthreads();
+            if (draw) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    float zr = s_z[(2 * s) * STEP_WAVE + lane], zi = s_z[(2 * s + 1) * STEP_WAVE + lane];
+                    hr[s] = row.rho * hr[s] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                    hi[s] = row.rho * hi[s] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+                }
             }
         }
         if (row.flags & 1) {                       // SR opportunity (UlMac.sr_step, lumped)
