@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 1
+#define INET_WIFI_ABI_VERSION 2
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -109,6 +109,26 @@ typedef struct InetWifiOutputs {
     int64_t *t;                                          /* [E] */
 } InetWifiOutputs;
 
+/* Level WIFI_DCF (this build's per-slot CSMA/CA access with integer backoff counters, following the semantics of
+   the reference's validation simulator isaac_net/core/wifi/eventsim.py:56-186, behind the same LevelNet API):
+   the per-station counter state and the per-env end of the last busy period. */
+typedef struct InetDcfState {
+    int32_t *b;          /* [E][R] backoff counter (slots) */
+    int32_t *stage;      /* [E][R] retry stage of the current access */
+    uint8_t *had;        /* [E][R] contending (bytes queued, usable MCS) at the end of the last step */
+    int32_t *t_idle;     /* [E] end of the last busy period, ns relative to the start of the next step (<= 0) */
+} InetDcfState;
+
+/* Integer timing of the DCF level (ns) and its EDCA set. */
+typedef struct InetDcfParams {
+    int32_t ndbps[INET_WIFI_MAX_M];   /* data bits per OFDM symbol of each MCS entry */
+    int32_t T;                        /* control step, ns (<= 2^30) */
+    int32_t tsym, pre, sifs, slot, t_ack, t_rts, t_cts;
+    int32_t W0, Wmax, aifsn;          /* CWmin + 1, CWmax + 1, AIFSN of the access category */
+    int32_t ovh, payload;             /* per-MSDU overhead bytes and MSDU payload bytes */
+    float fer;                        /* residual frame error rate (float32) */
+} InetDcfParams;
+
 int32_t inet_wifi_abi_version(void);
 
 /* One control step. t: [E] int64 step of each env (device) or NULL for st->clock. input_kind: 0 poses [E][R][2],
@@ -130,6 +150,20 @@ int32_t inet_wifi_submit(const InetWifiState *st, const InetWifiParams *prm, con
 
 /* Reset the envs of mask [E] uint8 (device; NULL = every env) (LevelNet.reset, levels/base.py:142-157). */
 int32_t inet_wifi_reset(const InetWifiState *st, const InetWifiParams *prm, const uint8_t *mask, void *stream);
+
+/* Level WIFI_DCF: one control step with the per-slot CSMA/CA access in place of the mean-field sub-steps (same
+   arguments and outputs as inet_wifi_step; wifi_access_ms, wifi_p_fail and wifi_busy are the step's measured access
+   time, failure share and busy share). No counterpart in the reference's engines: its integer-backoff semantics
+   exist only in the validation simulator (wifi/eventsim.py:56-186). Refused (INET_WIFI_EUNSUPPORTED): per-class
+   access categories and background stations; refused (INET_WIFI_EINVAL): message sizes above 2^24 bytes, T above
+   2^30 ns, non-positive symbol, slot, RTS or CTS times. */
+int32_t inet_wifi_dcf_step(const InetWifiState *st, const InetDcfState *ds, const InetWifiParams *prm,
+                           const InetDcfParams *dp, const int64_t *t, int32_t input_kind, const float *x,
+                           const int64_t *cur_hid, const InetWifiOutputs *out, void *stream);
+
+/* Level WIFI_DCF reset: inet_wifi_reset plus the initial backoff counters of the new episode. */
+int32_t inet_wifi_dcf_reset(const InetWifiState *st, const InetDcfState *ds, const InetWifiParams *prm,
+                            const InetDcfParams *dp, const uint8_t *mask, void *stream);
 
 #ifdef __cplusplus
 }

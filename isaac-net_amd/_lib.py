@@ -76,12 +76,22 @@ class InetWifiOutputs(C.Structure):
                                  "busy", "det_env", "t")]
 
 
+class InetDcfState(C.Structure):
+    _fields_ = [(n, P) for n in ("b", "stage", "had", "t_idle")]
+
+
+class InetDcfParams(C.Structure):
+    _fields_ = [("ndbps", i32 * WIFI_MAX_M)] + [(n, i32) for n in (
+        "T", "tsym", "pre", "sifs", "slot", "t_ack", "t_rts", "t_cts", "W0", "Wmax", "aifsn", "ovh", "payload")] + \
+               [("fer", f32)]
+
+
 ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fade", "salt_bler")   # 8 x 4 bytes
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
 ABI_VERSION = 2
-WIFI_ABI_VERSION = 1
+WIFI_ABI_VERSION = 2
 _LIB = None
 
 
@@ -112,6 +122,12 @@ def load(path=LIB_PATH):
     lib.inet_wifi_submit.restype = i32
     lib.inet_wifi_reset.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, P]
     lib.inet_wifi_reset.restype = i32
+    lib.inet_wifi_dcf_step.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetDcfState), C.POINTER(InetWifiParams),
+                                       C.POINTER(InetDcfParams), P, i32, P, P, C.POINTER(InetWifiOutputs), P]
+    lib.inet_wifi_dcf_step.restype = i32
+    lib.inet_wifi_dcf_reset.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetDcfState), C.POINTER(InetWifiParams),
+                                        C.POINTER(InetDcfParams), P, P]
+    lib.inet_wifi_dcf_reset.restype = i32
     if lib.inet_nr_abi_version() != ABI_VERSION or lib.inet_wifi_abi_version() != WIFI_ABI_VERSION:
         raise RuntimeError("libinet_nr.so ABI version mismatch; rebuild it")
     _LIB = lib

@@ -99,14 +99,33 @@ DEV float tau_of_p(float p, float W0, float Wm, int L) {
     return num / den;
 }
 
+// U{0..W-1} from an element hash: ((h >> 8) W) >> 24
+DEV int draw_int(uint32_t h, int W) { return (int)(((uint64_t)(h >> 8) * (uint64_t)W) >> 24); }
+// channel time (ns) of an access of B bytes: the busy period of a lone transmission (success or FER loss) and of a
+// collision (wifi/eventsim.py:140-152 with the AccessTiming exchange of wifi/phy.py:141-155, integer nanoseconds)
+DEV void dcf_busy(const InetWifiParams& pm, const InetDcfParams& dp, int B, int nd, int& succ, int& coll) {
+    const int nmsdu = (B + dp.payload - 1) / dp.payload;
+    const int bits = 22 + 8 * B + 8 * dp.ovh * nmsdu;
+    const int tdata = dp.pre + dp.tsym * ((bits + nd - 1) / nd);
+    if (pm.rts_cts) {
+        succ = dp.t_rts + dp.sifs + dp.t_cts + dp.sifs + tdata + dp.sifs + dp.t_ack;
+        coll = dp.t_rts + dp.sifs + dp.t_cts;
+    } else {
+        succ = tdata + dp.sifs + dp.t_ack;
+        coll = pm.coll_ack ? succ : tdata;
+    }
+}
+
 }  // namespace
 
 // ======================================================================================= step kernel
+// DCF = false: the mean-field level (WifiNet._serve); true: the per-slot CSMA/CA level (integer backoff counters)
+template <bool DCF>
 __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetWifiParams pm,
                                                          const int64_t* __restrict__ tin, int input_kind,
                                                          const float* __restrict__ xin,
                                                          const int64_t* __restrict__ hid_in, InetWifiOutputs out,
-                                                         int rb) {
+                                                         int rb, InetDcfState ds, InetDcfParams dp) {
     extern __shared__ float dyn[];
     __shared__ float s_red[WAVE];
     const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
@@ -154,28 +173,31 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         s_cls[o] = rob ? (uint8_t)st.cls[fo + (size_t)f * R] : 0;
         s_fin[o] = INFINITY;
     }
+    // counter-RNG keys of this step: the step counter advances before the draws (LevelNet._advance)
+    const int ctr = env_ok ? st.ctr_step[ec] + 1 : 0;
+    uint32_t hkey = 0;
+    if (env_ok) {
+        uint32_t h = mix32((uint32_t)pm.seed_key ^ salt32((uint32_t)st.env_id[ec]));
+        h = mix32(h ^ salt32((uint32_t)st.episode[ec]));
+        h = mix32(h ^ salt32(CH_STEP));
+        hkey = mix32(h ^ salt32((uint32_t)ctr));
+    }
+    const uint32_t key_acc = mix32(hkey ^ salt32(0u)), key_loss = mix32(hkey ^ salt32(1u));
+    // EDCA parameters: the class-1 AC for every robot, or the head-of-line message's AC per sub-step
+    int ac = pm.cls_ac[1];
+    float capB = cap_bytes(pm, rate, pm.ac_txop[ac]);
+    float o_acc = NAN, o_pf = NAN, o_busy = 0.0f;       // wifi_access_ms, wifi_p_fail, wifi_busy
+    auto fifo_sum = [&]() -> float {
+        return aten_row_sum(F, [&](int f) { return s_rem[f * WAVE + lane]; });
+    };
+    if constexpr (!DCF) {
     float tau = rob ? st.tau[(size_t)ec * (R + 1) + rc] : pm.tau0;
     float tau_b = env_ok ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
     float att_n = rob ? st.att_n[ir] : 0.f, att_logp = rob ? st.att_logp[ir] : 0.f;
     float credit = rob ? st.credit[ir] : 0.f;
 
-    // counter-RNG keys of this step: the step counter advances before the draws (LevelNet._advance)
-    const int ctr = env_ok ? st.ctr_step[ec] + 1 : 0;
-    uint32_t key_acc = 0, key_loss = 0;
-    if (env_ok) {
-        uint32_t h = mix32((uint32_t)pm.seed_key ^ salt32((uint32_t)st.env_id[ec]));
-        h = mix32(h ^ salt32((uint32_t)st.episode[ec]));
-        h = mix32(h ^ salt32(CH_STEP));
-        h = mix32(h ^ salt32((uint32_t)ctr));
-        key_acc = mix32(h ^ salt32(0u));
-        key_loss = mix32(h ^ salt32(1u));
-    }
-
-    // EDCA parameters: the class-1 AC for every robot, or the head-of-line message's AC per sub-step
-    int ac = pm.cls_ac[1];
     float W0 = pm.ac_W0[ac], Wm = pm.ac_Wmax[ac], aifsn = pm.ac_aifsn[ac];
-    float capB = cap_bytes(pm, rate, pm.ac_txop[ac]);
     // the background station (segment-uniform)
     const float W0b = pm.ac_W0[pm.bg_ac], Wmb = pm.ac_Wmax[pm.bg_ac];
     float tsb, tcb;
@@ -190,9 +212,6 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         __syncthreads();
         const float* row = s_red + gseg * rb;
         return aten_row_sum(R + 1, [&](int i) { return i < R ? row[i] : vb; });
-    };
-    auto fifo_sum = [&]() -> float {
-        return aten_row_sum(F, [&](int f) { return s_rem[f * WAVE + lane]; });
     };
 
     float acc_sum = 0.f, acc_n = 0.f, p_sum = 0.f, busy_sum = 0.f;
@@ -319,11 +338,123 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         st.credit[ir] = keep ? credit : 0.0f;
         st.att_n[ir] = keep ? att_n : 0.0f;
         st.att_logp[ir] = keep ? att_logp : 0.0f;
+    }
+    o_acc = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
+    o_pf = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
+    o_busy = busy_sum / (float)K;
+    } else {
+    // ---------------- per-slot CSMA/CA: the next transmission slot, its transmitters, the outcome ----------------
+    const int aif = dp.aifsn, slot = dp.slot, sifs = dp.sifs, Tn = dp.T;
+    int b = rob ? ds.b[ir] : 0, stage = rob ? ds.stage[ir] : 0;
+    const bool had = rob && ds.had[ir] != 0;
+    int ti = env_ok ? ds.t_idle[ec] : 0;                  // end of the last busy period, ns from the step start
+    const uint32_t kpost = mix32(hkey ^ salt32(2u)), karr = mix32(hkey ^ salt32(3u)), kfer = mix32(hkey ^ salt32(4u));
+    const int capi = (int)floorf(capB);
+    const int nd = dp.ndbps[mcs];
+    int64_t q = 0;                                         // whole bytes queued (sizes rounded up)
+    for (int f = 0; f < qlen; ++f) {
+        const int o = f * WAVE + lane;
+        s_rem[o] = ceilf(s_rem[o]);
+        q += (int64_t)s_rem[o];
+    }
+    // a station that was not contending (empty queue or no usable MCS): it sends at the next slot boundary when its
+    // counter has run out during an idle period of at least its AIFS, else it draws a counter first
+    // (eventsim.py:113-123)
+    if (rob && q > 0 && link && !had) {
+        const int el = -ti - sifs;
+        const int ka = el >= 0 ? el / slot : -1;
+        const int spent = ka - aif > 0 ? ka - aif : 0;
+        if (b - spent <= 0) b = ka >= aif ? ka + 1 - aif : draw_int(elem_hash(karr, (uint32_t)rc), dp.W0);
+    }
+    // serve (lost = false) or drop (lost = true) Bc bytes from the head of this station's FIFO; a message with a
+    // dropped byte is discarded whole
+    auto consume = [&](int Bc, bool lost, int t_end) {
+        const float tfin = (float)((double)t + (double)t_end / (double)Tn);
+        for (int f = 0; f < qlen && Bc > 0; ++f) {
+            const int o = f * WAVE + lane;
+            const int rm = (int)s_rem[o];
+            if (rm <= 0) continue;
+            const int take = Bc < rm ? Bc : rm;
+            Bc -= take;
+            if (lost) {
+                s_rem[o] = 0.0f;
+                q -= rm;
+            } else {
+                s_rem[o] = (float)(rm - take);
+                q -= take;
+                if (rm == take) s_fin[o] = tfin;
+            }
+        }
+    };
+    int n_ev = 0, n_att = 0, n_fail = 0, n_succ = 0, prev_end = 0, busy_ns = 0;
+    double acc_ms = 0.0;
+    bool done = !env_ok, idle_end = false;
+    while (__ballot(!done) != 0ull) {
+        const bool cand = rob && !done && q > 0 && link;
+        const int key = cand ? aif + b : 0x3fffffff;
+        const int Kc = -seg_max_i(-key, rb);
+        const bool tx = cand && key == Kc;
+        const int Bv = q < (int64_t)capi ? (int)q : capi;
+        int d_succ, d_coll;
+        dcf_busy(pm, dp, Bv, nd, d_succ, d_coll);
+        const int n_tx = __builtin_popcountll(__ballot(tx) & seg_bits(rb, lane));
+        const int dur = n_tx == 1 ? seg_sum_i(tx ? d_succ : 0, rb) : seg_max_i(tx ? d_coll : 0, rb);
+        const bool none = Kc >= 0x3fffffff;
+        const int t_end = none ? 0 : ti + sifs + Kc * slot + dur;
+        const bool stop = none || t_end > Tn;      // the exchange must end within the step
+        if (!done && !stop) {
+            const int dec = Kc - aif > 0 ? Kc - aif : 0;
+            b = b - dec > 0 ? b - dec : 0;
+            bool ok = false;
+            if (n_tx == 1) ok = !(uniform_bits(elem_hash(kfer, (uint32_t)n_ev)) < dp.fer);
+            busy_ns += dur;
+            if (tx) {
+                ++n_att;
+                int W;
+                if (ok) {
+                    consume(Bv, false, t_end);
+                    acc_ms += (double)(t_end - prev_end) * 1e-6;
+                    ++n_succ;
+                    stage = 0;
+                    W = dp.W0;
+                } else {
+                    ++n_fail;
+                    ++stage;
+                    if (stage >= L) { consume(Bv, true, t_end); stage = 0; }
+                    W = dp.W0 << stage;
+                    W = W < dp.Wmax ? W : dp.Wmax;
+                }
+                b = draw_int(elem_hash(kpost, (uint32_t)(n_ev * R + rc)), W);
+                prev_end = t_end;
+            }
+            ti = t_end;
+            ++n_ev;
+        }
+        if (!done && stop) idle_end = none;
+        done = done || stop;
+    }
+    ti -= Tn;
+    if (idle_end && -ti - sifs >= 0) {
+        // nobody contends: re-base the idle anchor to AIFS slots before the step end and count the extra idle slots
+        // off every counter (the later transmission times and counters are unchanged; the integers stay bounded)
+        const int m = (-ti - sifs) / slot - aif;
+        if (m > 0) {
+            ti += m * slot;
+            b = b - m > 0 ? b - m : 0;
+        }
+    }
+    if (rob) { ds.b[ir] = b; ds.stage[ir] = stage; ds.had[ir] = q > 0 && link ? 1 : 0; }
+    if (env_ok && r == 0) ds.t_idle[ec] = ti;
+    o_acc = n_succ > 0 ? (float)(acc_ms / (double)n_succ) : NAN;
+    o_pf = n_att > 0 ? (float)((double)n_fail / (double)n_att) : NAN;
+    o_busy = (float)((double)busy_ns / (double)Tn);
+    }
+    if (rob) {
         st.serv[ir] = 0;
         st.last_snr[ir] = snr;
-        out.access_ms[ir] = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
-        out.p_fail[ir] = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
-        out.busy[ir] = busy_sum / (float)K;
+        out.access_ms[ir] = o_acc;
+        out.p_fail[ir] = o_pf;
+        out.busy[ir] = o_busy;
         out.mcs[ir] = link ? pm.mcs_ids[mcs] : -1;
         out.rate_mbps[ir] = link ? rate : 0.0f;
         out.sinr_db[ir] = snr;
@@ -515,6 +646,22 @@ __global__ void wifi_reset_kernel(InetWifiState st, InetWifiParams pm, const uin
     }
 }
 
+// ======================================================================================= DCF reset kernel
+// the initial backoff counters of the new episode (channel RESET, stream 5, element r), stage 0, idle medium
+__global__ void dcf_reset_kernel(InetWifiState st, InetDcfState ds, InetWifiParams pm, InetDcfParams dp,
+                                 const uint8_t* __restrict__ mask) {
+    const int e = blockIdx.x;
+    if (e >= pm.E || (mask && !mask[e])) return;
+    const uint32_t key = base_key((uint32_t)pm.seed_key, (uint32_t)st.env_id[e], (uint32_t)st.episode[e], 3u, 0u, 5u);
+    for (int r = threadIdx.x; r < pm.R; r += blockDim.x) {
+        const size_t ir = (size_t)e * pm.R + r;
+        ds.b[ir] = draw_int(elem_hash(key, (uint32_t)r), dp.W0);
+        ds.stage[ir] = 0;
+        ds.had[ir] = 0;
+    }
+    if (threadIdx.x == 0) ds.t_idle[e] = 0;
+}
+
 // ======================================================================================= C ABI
 namespace {
 
@@ -552,8 +699,8 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     const int G = p.envs_per_wave;
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    hipLaunchKernelGGL(wifi_step_kernel, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t, input_kind, x,
-                       cur_hid, *out, rb);
+    hipLaunchKernelGGL(wifi_step_kernel<false>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t,
+                       input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 
@@ -569,6 +716,52 @@ int32_t inet_wifi_submit(const InetWifiState* st, const InetWifiParams* prm, con
     const int G = p.envs_per_wave;
     hipLaunchKernelGGL(wifi_submit_kernel, dim3((p.E + G - 1) / G), dim3(WAVE), 0, (hipStream_t)stream, *st, p, t,
                        send, det, hid, snr, counts, n_cls, accepted, rb);
+    return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
+}
+
+namespace {
+int check_dcf(const InetWifiParams& p, const InetDcfParams& d) {
+    // every exchange lasts at least one symbol or one control frame, so the event loop ends within the step
+    if (d.T <= 0 || d.T > (1 << 30) || d.slot <= 0 || d.sifs < 0 || d.tsym <= 0 || d.pre < 0 || d.t_ack < 0 ||
+        d.t_rts <= 0 || d.t_cts <= 0 || d.W0 < 1 || d.Wmax < d.W0 || d.Wmax > 65536 || d.aifsn < 0 ||
+        d.aifsn > 64 || d.payload <= 0 || d.ovh < 0)
+        return INET_WIFI_EINVAL;
+    for (int m = 0; m < p.M; ++m) if (d.ndbps[m] <= 0) return INET_WIFI_EINVAL;
+    // whole-byte sizes stay exact in the float32 FIFO
+    for (int c = 0; c < p.n_cls; ++c) if (!(p.sizes[c] >= 0.0f && p.sizes[c] <= 16777216.0f)) return INET_WIFI_EINVAL;
+    if (p.per_class_ac || p.bg_w != 0.0f) return INET_WIFI_EUNSUPPORTED;
+    return INET_WIFI_OK;
+}
+}  // namespace
+
+int32_t inet_wifi_dcf_step(const InetWifiState* st, const InetDcfState* ds, const InetWifiParams* prm,
+                           const InetDcfParams* dp, const int64_t* t, int32_t input_kind, const float* x,
+                           const int64_t* cur_hid, const InetWifiOutputs* out, void* stream) {
+    if (!st || !ds || !prm || !dp || !x || !out) return INET_WIFI_EINVAL;
+    const InetWifiParams& p = *prm;
+    int rc = check_params(p);
+    if (!rc) rc = check_dcf(p, *dp);
+    if (rc) return rc;
+    if (input_kind < 0 || input_kind > 2) return INET_WIFI_EINVAL;
+    if (input_kind == 0 && p.n_fields < 1) return INET_WIFI_EINVAL;
+    const int rb = next_pow2(p.R);
+    const int G = p.envs_per_wave;
+    const unsigned grid = (unsigned)((p.E + G - 1) / G);
+    const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
+    hipLaunchKernelGGL(wifi_step_kernel<true>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t,
+                       input_kind, x, cur_hid, *out, rb, *ds, *dp);
+    return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
+}
+
+int32_t inet_wifi_dcf_reset(const InetWifiState* st, const InetDcfState* ds, const InetWifiParams* prm,
+                            const InetDcfParams* dp, const uint8_t* mask, void* stream) {
+    if (!st || !ds || !prm || !dp) return INET_WIFI_EINVAL;
+    int rc = check_params(*prm);
+    if (!rc) rc = check_dcf(*prm, *dp);
+    if (rc) return rc;
+    hipLaunchKernelGGL(wifi_reset_kernel, dim3(prm->E), dim3(WAVE), 0, (hipStream_t)stream, *st, *prm, mask);
+    if (hipGetLastError() != hipSuccess) return INET_WIFI_ELAUNCH;
+    hipLaunchKernelGGL(dcf_reset_kernel, dim3(prm->E), dim3(WAVE), 0, (hipStream_t)stream, *st, *ds, *prm, *dp, mask);
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 

@@ -711,8 +711,9 @@ def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, back
     """Factory with the signature of isaac_net.core.engine.make_engine (engine.py:230-255) for level "L2" (the NR
     engine) and level "WIFI" (isaac_net/core/wifi/engine.py:436-444), backend "hip" (also "auto", which resolves to
     "hip" on a GPU device)."""
-    if level not in ("L2", "WIFI"):
-        raise HipUnsupported(f"level {level!r}: the hip backend implements levels 'L2' (NR) and 'WIFI'")
+    if level not in ("L2", "WIFI", "WIFI_DCF"):
+        raise HipUnsupported(f"level {level!r}: the hip backend implements levels 'L2' (NR), 'WIFI' and "
+                             "'WIFI_DCF'")
     if backend not in ("hip", "auto"):
         raise ValueError(f"unknown backend {backend!r} for this package; use 'hip'")
     if inject:
@@ -725,4 +726,7 @@ def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, back
     if level == "WIFI":
         from .wifi_engine import HipWifiEngine
         return HipWifiEngine(E, R, device, cfg, seed=seed)
+    if level == "WIFI_DCF":
+        from .wifi_engine import HipWifiDcfEngine
+        return HipWifiDcfEngine(E, R, device, cfg, seed=seed)
     return HipNREngine(E, R, device, cfg, seed=seed, out_format=out_format)

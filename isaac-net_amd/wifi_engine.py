@@ -242,6 +242,9 @@ class HipWifiEngine:
                 mask = torch.zeros(self.E, dtype=torch.bool, device=self.dev)
                 mask[ids] = True
             m8 = mask.to(torch.uint8).contiguous()
+        self._reset_launch(m8)
+
+    def _reset_launch(self, m8):
         _lib.check(self._lib.inet_wifi_reset(C.byref(self._cstate), C.byref(self._cparams),
                                              None if m8 is None else m8.data_ptr(), self._stream()), "wifi reset")
 
@@ -327,15 +330,18 @@ class HipWifiEngine:
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(torch.cuda.current_stream(self.dev))
-        _lib.check(self._lib.inet_wifi_step(
-            C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), kind,
-            xin.data_ptr(), None if hid is None else hid.data_ptr(), C.byref(c), self._stream()), "wifi step")
+        _lib.check(self._launch(tv, kind, xin, hid, c), "wifi step")
         if ev is not None:
             e1.record(torch.cuda.current_stream(self.dev))
             ev.append((e0, e1))
         if cur_hid is not None:
             return o["newest"], o["det_env"]
         return o
+
+    def _launch(self, tv, kind, xin, hid, c):
+        return self._lib.inet_wifi_step(
+            C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), kind,
+            xin.data_ptr(), None if hid is None else hid.data_ptr(), C.byref(c), self._stream())
 
     # set to a list to record (start, end) events around every step-kernel launch, on the launch stream
     kernel_events = None
@@ -398,3 +404,88 @@ class HipWifiEngine:
         elif "radio.k" in sd:
             st["field"][:, 0, :, :2].copy_(g("radio.k")[0])
             st["field"][:, 0, :, 2].copy_(g("radio.phi")[0])
+
+
+class HipWifiDcfEngine(HipWifiEngine):
+    """Level WIFI_DCF on MI355X: the level WIFI API with per-slot CSMA/CA access (integer backoff counters, collisions,
+    binary exponential backoff, retry limit) in place of the mean-field sub-steps. The semantics follow the
+    reference's validation simulator (isaac_net/core/wifi/eventsim.py:56-186) on the engine's counter RNG; they are
+    stated in full in include/inet_wifi.h and oracle/dcf_oracle.py's module docstring."""
+
+    level = "WIFI_DCF"
+
+    def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, envs_per_wave=None):
+        cfg = cfg if cfg is not None else NRConfig()
+        wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
+        if wc.bg_stations > 0 or wc.class_ac is not None:
+            raise HipUnsupported("level WIFI_DCF: one access category for every robot and no background stations")
+        self._dcf_ready = False
+        super().__init__(E, R, device, cfg, seed=seed, envs_per_wave=envs_per_wave)
+        self._build_dcf()
+        self._dcf_ready = True
+        self.reset(None)
+
+    def _build_dcf(self):
+        from .wifi_config import AC_NAMES, ACK_BYTES, BLOCK_ACK_BYTES, CTS_BYTES, DATA_SUBCARRIERS, EDCA, \
+            MODULATION, NON_HT_RATES, RTS_BYTES, mcs_numbers, preamble_us, symbol_us
+        cfg, wc, E, R, d = self.config, self.wc, self.E, self.R, self.dev
+        self.dst = {"b": torch.zeros(E, R, dtype=torch.int32, device=d),
+                    "stage": torch.zeros(E, R, dtype=torch.int32, device=d),
+                    "had": torch.zeros(E, R, dtype=torch.uint8, device=d),
+                    "t_idle": torch.zeros(E, dtype=torch.int32, device=d)}
+        s = _lib.InetDcfState()
+        for n, _ in _lib.InetDcfState._fields_:
+            setattr(s, n, self.dst[n].data_ptr())
+        self._cdcf = s
+        ns = lambda us: int(round(us * 1000.0))  # noqa: E731
+        p = _lib.InetDcfParams()
+        if wc.standard == "a":
+            nd = [int(r * 4) for r in NON_HT_RATES]
+        else:
+            nsd = DATA_SUBCARRIERS[wc.standard][wc.bandwidth_mhz]
+            nd = [int(round(nsd * MODULATION[m][0] * MODULATION[m][1] * wc.n_ss))
+                  for m in mcs_numbers(wc.standard, wc.bandwidth_mhz, wc.n_ss)]
+        for i, v in enumerate(nd):
+            p.ndbps[i] = v
+        T = cfg.control_step_ms * 1e6
+        if abs(T - round(T)) > 1e-6 or round(T) > 1 << 30:
+            raise HipUnsupported("level WIFI_DCF: the control step must be a whole number of ns up to 1.07 s")
+        ctrl = lambda n: ns(20.0 + 4.0 * math.ceil((22 + 8 * n) / (wc.ctrl_rate_mbps * 4.0)))  # noqa: E731
+        cw = EDCA[wc.access_category]
+        p.T, p.tsym, p.pre = int(round(T)), ns(symbol_us(wc.standard, wc.gi_us)), ns(preamble_us(wc.standard, wc.n_ss))
+        p.sifs, p.slot = ns(wc.sifs_us), ns(wc.slot_us)
+        p.t_ack = ctrl(BLOCK_ACK_BYTES if wc.max_ampdu_bytes > 0 else ACK_BYTES)
+        p.t_rts, p.t_cts = ctrl(RTS_BYTES), ctrl(CTS_BYTES)
+        p.W0, p.Wmax, p.aifsn = cw[0] + 1, cw[1] + 1, int(cw[2])
+        p.ovh, p.payload = int(wc.msdu_overhead_bytes), int(wc.msdu_payload_bytes)
+        p.fer = float(np.float32(wc.frame_error_rate))
+        self._cdparams = p
+        self.dcf_ac = AC_NAMES.index(wc.access_category)
+
+    def _reset_launch(self, m8):
+        if not getattr(self, "_dcf_ready", False):
+            return                # the base constructor's reset: the full reset follows once the DCF state exists
+        _lib.check(self._lib.inet_wifi_dcf_reset(C.byref(self._cstate), C.byref(self._cdcf), C.byref(self._cparams),
+                                                 C.byref(self._cdparams), None if m8 is None else m8.data_ptr(),
+                                                 self._stream()), "wifi dcf reset")
+
+    def _launch(self, tv, kind, xin, hid, c):
+        return self._lib.inet_wifi_dcf_step(
+            C.byref(self._cstate), C.byref(self._cdcf), C.byref(self._cparams), C.byref(self._cdparams),
+            None if tv is None else tv.data_ptr(), kind, xin.data_ptr(), None if hid is None else hid.data_ptr(),
+            C.byref(c), self._stream())
+
+    def state_dict(self):
+        sd = super().state_dict()
+        sd.update({"dcf.b": self.dst["b"].long(), "dcf.stage": self.dst["stage"].long(),
+                   "dcf.had": self.dst["had"] != 0, "dcf.t_idle": self.dst["t_idle"].long()})
+        return sd
+
+    def load_state_dict(self, sd):
+        super().load_state_dict(sd)
+        g = lambda k: torch.as_tensor(sd[k]).to(self.dev)  # noqa: E731
+        if "dcf.b" in sd:
+            self.dst["b"].copy_(g("dcf.b").to(torch.int32))
+            self.dst["stage"].copy_(g("dcf.stage").to(torch.int32))
+            self.dst["had"].copy_(g("dcf.had").to(torch.uint8))
+            self.dst["t_idle"].copy_(g("dcf.t_idle").to(torch.int32))

@@ -273,6 +273,42 @@ def run_wifi_case(name, c):
     print(name, "arrays:", len(out))
 
 
+def eventsim_vectors():
+    """Saturation statistics of the reference's CSMA/CA event simulator (core/wifi/eventsim.py:56-186) for the
+    exchange times of the DCF level (802.11ax 20 MHz MCS 11, 1472-byte MSDUs without aggregation, legacy DCF
+    parameters): per n stations, attempts, successes and the busy share over 4 s. The DCF level's oracle is compared
+    with them statistically (its draws come from the engine's counter RNG, the simulator's from numpy PCG64)."""
+    sys.path.insert(0, REF)
+    sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+    from isaac_net.core.wifi import eventsim as ev
+    import importlib.util
+    d = os.path.join(os.path.dirname(os.path.dirname(HERE)), "isaac-net_amd")
+    spec = importlib.util.spec_from_file_location("isaac_net_amd", os.path.join(d, "__init__.py"),
+                                                  submodule_search_locations=[d])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["isaac_net_amd"] = mod
+    spec.loader.exec_module(mod)
+    from oracle.dcf_oracle import DcfOracle
+    from isaac_net_amd.wifi_config import WifiConfig
+    cfg = mod.NRConfig(control_step_ms=20.0, msg_sizes=(60000.0,), wifi=WifiConfig(access_category="DCF",
+                                                                                     max_ampdu_bytes=0))
+    o = DcfOracle(1, 2, cfg)
+    succ_ns, coll_ns = o.busy(1472, o.k["ndbps"][-1])
+    out = {"busy_succ_us": np.float64(succ_ns / 1000.0), "busy_coll_us": np.float64(coll_ns / 1000.0),
+           "n": np.array([5, 10, 20], np.int64), "sim_us": np.float64(4e6)}
+    att, succ, busy = [], [], []
+    for n in (5, 10, 20):
+        st = [ev.Station(16, 1024, 2, 1472.0, ev.Const(succ_ns / 1000.0), ev.Const(coll_ns / 1000.0), 7, 0.0)
+              for _ in range(n)]
+        r = ev.run(st, 4e6, 9.0, 16.0, arrivals=None, seed=0)
+        att.append(int(r["n_att"].sum()))
+        succ.append(int(r["n_succ"].sum()))
+        busy.append(float(r["busy_frac"]))
+    out.update(n_att=np.array(att, np.int64), n_succ=np.array(succ, np.int64), busy_frac=np.array(busy))
+    np.savez_compressed(os.path.join(HERE, "eventsim_sat.npz"), **out)
+    print("eventsim vectors written", att, succ, busy)
+
+
 def phy_tables():
     """Processed PHY tables of both MCS tables (core/phy.py PHY): BLER table, grids, betas, thresholds, TBS."""
     NRConfig, make_engine, state_dict, Requests = _ref()
@@ -334,12 +370,14 @@ def rng_vectors():
 
 if __name__ == "__main__":
     torch.set_num_threads(1)
-    names = sys.argv[1:] or list(CASES) + list(WIFI_CASES)
+    names = sys.argv[1:] or list(CASES) + list(WIFI_CASES) + ["eventsim"]
     if not sys.argv[1:]:
         rng_vectors()
         phy_tables()
     for n in names:
-        if n in WIFI_CASES:
+        if n == "eventsim":
+            eventsim_vectors()
+        elif n in WIFI_CASES:
             run_wifi_case(n, WIFI_CASES[n])
         else:
             run_case(n, CASES[n])

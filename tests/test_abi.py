@@ -40,15 +40,16 @@ def test_library_exports_every_declared_symbol():
     lib.inet_nr_build_info.restype = ctypes.c_char_p
     assert b"gfx950" in lib.inet_nr_build_info()
     wifi = declared_functions(WIFI_HEADER, "inet_wifi_")
-    assert wifi == sorted(["inet_wifi_abi_version", "inet_wifi_step", "inet_wifi_submit", "inet_wifi_reset"])
+    assert wifi == sorted(["inet_wifi_abi_version", "inet_wifi_step", "inet_wifi_submit", "inet_wifi_reset",
+                           "inet_wifi_dcf_step", "inet_wifi_dcf_reset"])
     for n in wifi:
         assert hasattr(lib, n), n
     lib.inet_wifi_abi_version.restype = ctypes.c_int32
-    assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 1
+    assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 2
 
 
 STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetWifiState",
-           "InetWifiParams", "InetWifiOutputs")
+           "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
 
 
 def test_ctypes_layout_matches_header():
