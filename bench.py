@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--out-format reference|compact] [--no-cpu]
     python bench.py --workload wifi_dcf [--envs-per-wave G]     (level WIFI: station-substeps/s)
+    python bench.py --workload wifi_dcf_slots [--envs-per-wave G]  (level WIFI_DCF: station-steps/s)
 
 A step is one control step of every env: submit_counts (this step's message arrivals, one launch) and step (poses in,
 the reference's output dict out: one launch of the fused step kernel), launched from Python every step (--graph:
@@ -72,6 +73,17 @@ def step_kernel_touched_bytes(eng, qlen_mean, kept_mean):
     return total - eng.E * eng.R * (fifo_full - fifo_touched)
 
 
+def copy_calibration(args, res, torch, dev):
+    """--copy-mib: copy a buffer of known size three times after the run (the byte counters' calibration kernel)."""
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        res["copy_calibration_bytes"] = 2 * src.numel()
+
+
 def wifi_step_bytes(eng):
     """Algorithmic HBM bytes of one Wi-Fi step-kernel launch: per station-step the frame FIFO (F slots of cap, cls,
     det, hid, rem, f_nact, f_snr, f_own = 29 B) and the per-station words (queue length, last SNR, roaming, serving AP,
@@ -85,14 +97,28 @@ def wifi_step_bytes(eng):
     return eng.E * eng.R * per_robot + eng.E * per_env, per_robot
 
 
-def wifi_cpu_baseline(wl, cfg, E_cpu, steps, warmup):
+def dcf_step_bytes(eng):
+    """Algorithmic HBM bytes of one WIFI_DCF step-kernel launch: per station-step the frame FIFO (29 B per slot) read
+    and written once, the queue length (read and written), last SNR and serving AP (written), the backoff counter,
+    retry stage and contention flag (9 B, read and written), the pose (8 B), the [E,R,F] outputs (22 B per slot) and
+    the per-station outputs (56 B); per env the clock, step counter and idle anchor (read and written), the hazard id,
+    RNG key, episode, pending flag, det_env and t, and the shadowing field."""
+    p = eng._cparams
+    F = eng.F
+    per_robot = 2 * F * 29 + 8 + 4 + 4 + 2 * 9 + 8 + F * 22 + 56
+    per_env = 2 * (8 + 4 + 4) + 8 + 4 + 4 + 1 + 1 + 8 + p.n_fields * p.n_modes * 3 * 4
+    return eng.E * eng.R * per_robot + eng.E * per_env, per_robot
+
+
+def wifi_cpu_baseline(wl, cfg, E_cpu, steps, warmup, slots=False):
     import torch
 
+    from oracle.dcf_oracle import DcfOracle
     from oracle.wifi_oracle import WifiOracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
     R = wl.R
-    ora = WifiOracle(E_cpu, R, cfg, seed=0)
+    ora = (DcfOracle if slots else WifiOracle)(E_cpu, R, cfg, seed=0)
     poses = wl.poses[:, :E_cpu].cpu()
     counts = wl.counts[:, :E_cpu].cpu().numpy()
 
@@ -108,6 +134,12 @@ def wifi_cpu_baseline(wl, cfg, E_cpu, steps, warmup):
     for s in range(warmup, warmup + steps):
         one(s)
     dt = time.perf_counter() - t0
+    if slots:
+        att = int(ora.tot["att"].sum())
+        return {"value": E_cpu * R * steps / dt, "unit": "station-steps/s", "cores": threads, "kind": "port",
+                "sample": f"oracle (per-env event loop in numpy) on the first {E_cpu} of the {wl.E} envs x {R} "
+                          f"stations, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
+                "ms_per_step": 1e3 * dt / steps, "attempts_per_env_step": att / (E_cpu * (steps + warmup))}
     return {"value": E_cpu * R * ora.K * steps / dt, "unit": "station-substeps/s", "cores": threads, "kind": "port",
             "sample": f"oracle (torch CPU restatement of the reference WifiNet) on the first {E_cpu} of the "
                       f"{wl.E} envs x {R} stations, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
@@ -115,23 +147,26 @@ def wifi_cpu_baseline(wl, cfg, E_cpu, steps, warmup):
 
 
 def run_wifi(args, P, torch):
-    """The level WIFI workload: one line with station-substeps/s and the step kernel's roofline fields."""
+    """The Wi-Fi workloads: level WIFI (station-substeps/s) or level WIFI_DCF (station-steps/s), one line with the
+    step kernel's roofline fields."""
     from isaac_net_amd import scenarios as S
+    slots = args.workload == "wifi_dcf_slots"
     dev = "cuda:0"
     E = args.envs if args.envs_set else 2048
     R = args.robots if args.robots_set else 16
     total = args.warmup + args.steps
-    print(f"# workload wifi_dcf {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
-    wl = S.Workload(E, R, total, seed=0, device=dev, name="wifi_dcf")
+    print(f"# workload {args.workload} {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev, name=args.workload)
     cfg = wl.cfg
-    from isaac_net_amd.wifi_engine import HipWifiEngine
-    eng = HipWifiEngine(E, R, dev, cfg, seed=0, envs_per_wave=args.envs_per_wave)
+    from isaac_net_amd.engine import KernelTimer
+    from isaac_net_amd.wifi_engine import HipWifiDcfEngine, HipWifiEngine
+    eng = (HipWifiDcfEngine if slots else HipWifiEngine)(E, R, dev, cfg, seed=0, envs_per_wave=args.envs_per_wave)
     K = eng.K
     for s in range(args.warmup):
         eng.submit_counts(wl.counts[s])
         eng.step(None, wl.poses[s])
     torch.cuda.synchronize()
-    eng.kernel_events = ev = []
+    eng.kernel_events = ev = KernelTimer(args.steps, dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -141,17 +176,23 @@ def run_wifi(args, P, torch):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
-    k_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
-    nbytes, per_robot = wifi_step_bytes(eng)
+    nbytes, per_robot = (dcf_step_bytes if slots else wifi_step_bytes)(eng)
     achieved = nbytes / (k_avg * 1e-3) / 1e9
-    res = {"metric": f"station-substeps/sec @{E} envs×{R} stations K={K} (level WIFI, DCF)",
-           "value": E * R * K * args.steps / dt, "unit": "station-substeps/s", "n_gpus": 1, "steps": args.steps,
+    if slots:
+        metric, value, unit = (f"station-steps/sec @{E} envs×{R} stations (level WIFI_DCF, per-slot CSMA/CA)",
+                               E * R * args.steps / dt, "station-steps/s")
+    else:
+        metric, value, unit = (f"station-substeps/sec @{E} envs×{R} stations K={K} (level WIFI, DCF)",
+                               E * R * K * args.steps / dt, "station-substeps/s")
+    res = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-           "config": {"workload": f"wifi_dcf: {E} envs x {R} stations at one AP, DCF (CWmin 15, CWmax 1023, 7 "
-                                  f"attempts), 802.11ax 20 MHz 12 MCS, K={K} sub-steps of 1 ms, 1500 B @0.4 per "
-                                  "station-step, FIFO 16, 50 m disc, log-distance + shadowing",
+           "config": {"workload": f"{args.workload}: {E} envs x {R} stations at one AP, DCF (CWmin 15, CWmax 1023, "
+                                  "7 attempts), 802.11ax 20 MHz 12 MCS, "
+                                  + ("per-slot CSMA/CA over the 20 ms step" if slots else f"K={K} sub-steps of 1 ms")
+                                  + ", 1500 B @0.4 per station-step, FIFO 16, 50 m disc, log-distance + shadowing",
                       "envs": E, "stations": R, "substeps_per_step": K, "envs_per_wave": args.envs_per_wave,
                       "parallelism": "single GPU", "launch": "eager"},
            "env_steps_per_s": E * args.steps / dt,
@@ -159,9 +200,10 @@ def run_wifi(args, P, torch):
                         "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "wifi_step_kernel",
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_station_step": per_robot}}
+    copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
-        res["cpu_baseline"] = wifi_cpu_baseline(wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)
+        res["cpu_baseline"] = wifi_cpu_baseline(wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1, slots=slots)
     print(json.dumps(res), flush=True)
 
 
@@ -200,8 +242,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="rl_scale", choices=("rl_scale", "wifi_dcf"),
-                    help="rl_scale: the NR engine's RL-scale workload (the headline metric); wifi_dcf: level WIFI")
+    ap.add_argument("--workload", default="rl_scale", choices=("rl_scale", "wifi_dcf", "wifi_dcf_slots"),
+                    help="rl_scale: the NR engine's RL-scale workload (the headline metric); wifi_dcf: level WIFI; "
+                         "wifi_dcf_slots: level WIFI_DCF on the same inputs")
     ap.add_argument("--envs", type=int, default=None)
     ap.add_argument("--robots", type=int, default=None)
     ap.add_argument("--envs-per-wave", type=int, default=1, help="level WIFI: envs per 64-lane wavefront")
@@ -223,9 +266,10 @@ def main():
     import torch
     P = load_package()
     args.envs_set, args.robots_set = args.envs is not None, args.robots is not None
-    if args.workload == "wifi_dcf":
+    if args.workload in ("wifi_dcf", "wifi_dcf_slots"):
         return run_wifi(args, P, torch)
     from isaac_net_amd import scenarios as S
+    from isaac_net_amd.engine import KernelTimer
     dev = "cuda:0"
     E = args.envs if args.envs_set else 4096
     R = args.robots if args.robots_set else 32
@@ -243,7 +287,7 @@ def main():
         q_post.append(float(eng.st["qlen"].float().mean()))
     torch.cuda.synchronize()
     graph = eng.graph_step() if args.graph else None        # submit + step recorded once, replayed every step
-    eng.kernel_events = ev = []                              # HIP events around each step-kernel launch
+    eng.kernel_events = ev = KernelTimer(args.steps, dev)    # HIP events around each step-kernel launch
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -256,7 +300,7 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
-    k_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
     qlen_mean = sum(q_pre) / max(len(q_pre), 1)
     kept_mean = sum(q_post) / max(len(q_post), 1)
@@ -285,13 +329,7 @@ def main():
                         "kernel": "nr_step_kernel", "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
                         "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean}}
-    if args.copy_mib > 0:
-        src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        res["copy_calibration_bytes"] = 2 * src.numel()
+    copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)

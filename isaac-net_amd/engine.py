@@ -521,14 +521,12 @@ class HipNREngine:
         o, co = self._alloc_out()
         ev = self.kernel_events
         if ev is not None:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(torch.cuda.current_stream(self.dev))
+            ev.begin(torch.cuda.current_stream(self.dev))
         _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
                                           plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(),
                                           hid.data_ptr(), C.byref(co), self._stream()), "step")
         if ev is not None:
-            e1.record(torch.cuda.current_stream(self.dev))
-            ev.append((e0, e1))
+            ev.end(torch.cuda.current_stream(self.dev))
         return o
 
     def _commit(self, T, plan, o):
@@ -560,7 +558,7 @@ class HipNREngine:
         return {"ul": res}
 
     _ul_slots_run = 0
-    # set to a list to record (start, end) HIP events around every step-kernel launch, on the launch stream
+    # set to a KernelTimer to record HIP events around every step-kernel launch, on the launch stream
     kernel_events = None
 
     # ------------------------------------------------------------------ state in the reference's layout
@@ -696,14 +694,40 @@ class GraphStep:
         eng._last_hid = self.hid
         ev = eng.kernel_events
         if ev is not None:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(torch.cuda.current_stream(eng.dev))
+            ev.begin(torch.cuda.current_stream(eng.dev))
         self.g_step.replay()
         if ev is not None:
-            e1.record(torch.cuda.current_stream(eng.dev))
-            ev.append((e0, e1))
+            ev.end(torch.cuda.current_stream(eng.dev))
         eng._commit(T, self.plan, self.out)
         return self.out
+
+
+class KernelTimer:
+    """Timing events recorded around each step-kernel launch on the launch stream (an engine's kernel_events hook).
+    The n event pairs are created and recorded once here: a HIP event is created on its first record, which can
+    cost more than the launch it brackets, so none is created inside a timed loop."""
+
+    def __init__(self, n, device="cuda"):
+        self.pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        stream = torch.cuda.current_stream(device)
+        for a, b in self.pairs:
+            a.record(stream)
+            b.record(stream)
+        torch.cuda.synchronize(device)
+        self.n = 0
+
+    def begin(self, stream):
+        if self.n >= len(self.pairs):
+            raise RuntimeError(f"KernelTimer: more than {len(self.pairs)} timed launches")
+        self.pairs[self.n][0].record(stream)
+
+    def end(self, stream):
+        self.pairs[self.n][1].record(stream)
+        self.n += 1
+
+    def ms(self):
+        """Duration of every timed launch in ms (after the stream has been synchronized)."""
+        return [a.elapsed_time(b) for a, b in self.pairs[:self.n]]
 
 
 def make_engine(level, E, R, device="cuda", config: NRConfig | None = None, backend="hip", *, sizes=None,

@@ -11,6 +11,7 @@ control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 
               exponential backoff over 7 attempts), 802.11ax 20 MHz with its 12-entry MCS table, 20 sub-steps of 1 ms
               per control step, 1500 B at Poisson 0.4, FIFO 16, stations uniform in a 50 m disc around the AP with a
               1 m/s random walk kept inside the disc, log-distance path loss with plane-wave shadowing.
+  wifi_dcf_slots  the same inputs on level WIFI_DCF (per-slot CSMA/CA with integer backoff counters).
 Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
 the square or disc; arrival counts per class), identical for the GPU engine and the CPU oracle.
 """
@@ -55,6 +56,8 @@ WORKLOADS = {
     "rl_scale": dict(cfg=rl_scale_config, E=4096, R=32, arena=200.0, speed=1.0, rates=(0.8, 0.1), steps=500),
     "wifi_dcf": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
                      level="WIFI"),
+    "wifi_dcf_slots": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
+                           level="WIFI_DCF"),
 }
 
 

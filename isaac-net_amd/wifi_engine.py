@@ -328,12 +328,10 @@ class HipWifiEngine:
         o, c = self._alloc_out()
         ev = self.kernel_events
         if ev is not None:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(torch.cuda.current_stream(self.dev))
+            ev.begin(torch.cuda.current_stream(self.dev))
         _lib.check(self._launch(tv, kind, xin, hid, c), "wifi step")
         if ev is not None:
-            e1.record(torch.cuda.current_stream(self.dev))
-            ev.append((e0, e1))
+            ev.end(torch.cuda.current_stream(self.dev))
         if cur_hid is not None:
             return o["newest"], o["det_env"]
         return o
@@ -343,7 +341,7 @@ class HipWifiEngine:
             C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), kind,
             xin.data_ptr(), None if hid is None else hid.data_ptr(), C.byref(c), self._stream())
 
-    # set to a list to record (start, end) events around every step-kernel launch, on the launch stream
+    # set to an engine.KernelTimer to record HIP events around every step-kernel launch, on the launch stream
     kernel_events = None
 
     # ------------------------------------------------------------------ state in the reference's names
