@@ -230,7 +230,7 @@ def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
     for s in range(warmup, warmup + steps):
         one(s)
     dt = time.perf_counter() - t0
-    k_ul = sum(1 for x in cfg.schedule(0) if x[1])
+    k_ul = sum(1 for x in cfg.schedule(0) if x[2])
     return {"value": E_cpu * R * k_ul * steps / dt, "unit": "robot-slots/s", "cores": threads, "kind": "port",
             "sample": f"oracle (torch CPU restatement of the reference path) on the first {E_cpu} of the 4096 envs "
                       f"x {R} robots, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
@@ -278,7 +278,7 @@ def main():
     wl = S.Workload(E, R, total, seed=0, device=dev)
     cfg = wl.cfg
     eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
-    k_ul = sum(1 for x in cfg.schedule(0) if x[1])
+    k_ul = sum(1 for x in cfg.schedule(0) if x[2])
     q_pre, q_post = [], []
     for s in range(args.warmup):
         eng.submit_counts(wl.counts[s])

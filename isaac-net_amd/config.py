@@ -78,6 +78,7 @@ class NRConfig:
     bler_target: float = 0.1
     ul_mcs_max: int | None = None
     dl_mcs_max: int | None = None
+    cqi_table: str = "mcs"                # DL CQI: "mcs" (best MCS per RBG) or "38214" (4-bit CQI of TS 38.214)
     olla: bool = True
     olla_up_db: float = 0.05
     scheduler: str = "pf"
@@ -309,15 +310,19 @@ class NRConfig:
         return [((i % cols + 0.5) * dx, (i // cols + 0.5) * dy) for i in range(n)]
 
     def schedule(self, g0):
-        """Scheduled slots of the control step starting at slot g0 (reference nr_engine.py:506-523, uplink part):
-        [(rel, ul data symbols, SR opportunity)] for every slot with UL data or an SR opportunity."""
+        """Scheduled slots of the control step starting at slot g0 (reference nr_engine.py:506-523):
+        [(rel, DL data symbols, UL data symbols, SR opportunity, CQI report, ack)] for every slot with DL or UL data,
+        an SR opportunity or a CQI report; ack = the first UL-capable slot >= g + k1, relative to g0 (the HARQ-ACK
+        slot of a DL transport block sent in that slot)."""
         out = []
         for rel in range(self.slots_per_step):
             g = g0 + rel
-            uls = self.slot_symbols(g)[1] if self.ul else 0
-            sr = self.first_ul_in_window(g, self.sr_period_slots) and self.ul
-            dls = self.slot_symbols(g)[0] if self.dl else 0
-            cqi = self.first_ul_in_window(g, self.cqi_period_slots) and self.dl
-            if dls or uls or cqi or sr:
-                out.append((rel, uls, bool(sr)))
+            dls, uls = self.slot_symbols(g)
+            sr = self.first_ul_in_window(g, self.sr_period_slots)
+            cqi = self.first_ul_in_window(g, self.cqi_period_slots)
+            ack = self.next_ul_capable(g + self.k1) - g0
+            dls = dls if self.dl else 0
+            uls = uls if self.ul else 0
+            if dls or uls or (cqi and self.dl) or (sr and self.ul):
+                out.append((rel, dls, uls, bool(sr and self.ul), bool(cqi and self.dl), ack))
         return out

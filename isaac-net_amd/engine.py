@@ -281,14 +281,14 @@ class HipNREngine:
         pg_pos = next(p for p in range(P_) if cfg.slot_symbols(p)[1] > 0)
         rows, prev = [], None
         evol, rhos = [], []
-        for rel, uls, sr in sched:
+        for rel, _dls, uls, sr, _cqi, _ack in sched:
             dt = dt0 if prev is None else rel - prev
             prev = rel
             rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
             evol.append(cfg.fading and dt > 0)
             rhos.append(float(np.float32(rho)))
         n = len(sched)
-        for k, (rel, uls, sr) in enumerate(sched):
+        for k, (rel, _dls, uls, sr, _cqi, _ack) in enumerate(sched):
             dt = dt0 if k == 0 else rel - sched[k - 1][0]
             rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
             c1 = math.sqrt(1 - rho ** 2)

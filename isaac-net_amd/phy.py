@@ -30,6 +30,13 @@ MCS_T2 = [(2, 120), (2, 193), (2, 308), (2, 449), (2, 602), (4, 378), (4, 434), 
           (6, 822), (6, 873), (8, 682.5), (8, 711), (8, 754), (8, 797), (8, 841), (8, 885),
           (8, 916.5), (8, 948)]
 MCS_TABLES = {1: MCS_T1, 2: MCS_T2}
+# TS 38.214 Table 5.2.2.1-2 (4-bit CQI table 1) and Table 5.2.2.1-3 (table 2, up to 256QAM): (Qm, code rate x 1024)
+# of CQI 1..15
+CQI_T1 = [(2, 78), (2, 120), (2, 193), (2, 308), (2, 449), (2, 602), (4, 378), (4, 490), (4, 616), (6, 466), (6, 567),
+          (6, 666), (6, 772), (6, 873), (6, 948)]
+CQI_T2 = [(2, 78), (2, 193), (2, 449), (4, 378), (4, 490), (4, 616), (6, 466), (6, 567), (6, 666), (6, 772), (6, 873),
+          (8, 711), (8, 797), (8, 885), (8, 948)]
+CQI_TABLES = {1: CQI_T1, 2: CQI_T2}
 # TS 38.214 Table 5.1.3.2-1: TBS for N_info <= 3824
 TBS_TABLE = np.array([24, 32, 40, 48, 56, 64, 72, 80, 88, 96, 104, 112, 120, 128, 136, 144, 152, 160, 168, 176,
                       184, 192, 208, 224, 240, 256, 272, 288, 304, 320, 336, 352, 368, 384, 408, 432, 456, 480,
@@ -207,3 +214,28 @@ class PhyTables:
         cbs, c = segment(tbs, self.r.astype(np.float64)[None, :])
         i0, wi = self.cidx(cbs.astype(_f32))
         return (tbs.astype(np.int32), i0.astype(np.int32), wi.astype(_f32), c.astype(_f32))
+
+
+def cqi_tables(tabs, mcs_table):
+    """The 38.214 CQI report of the DL (cqi_table="38214", reference core/phy.py:366-391) for PhyTables tabs:
+    (thr [15] float32, cqi_mcs [16] int64). thr[k - 1] is the SINR from which CQI k is reported: thr_ref of the MCS
+    with the CQI's spectral efficiency, or of the nearest one shifted by the Shannon-gap difference
+    10 log10((2^se - 1) / (2^se_mcs - 1)) (ties to the lower MCS), made non-decreasing. cqi_mcs[k] is the highest
+    MCS <= mcs_max whose spectral efficiency does not exceed CQI k's (0 for CQI 0 and below every MCS)."""
+    se_c = [q * r / 1024 for q, r in CQI_TABLES[mcs_table]]
+    se_m = [float(x) for x in tabs.se]
+    thr_m = [float(x) for x in tabs.thr_ref]
+
+    def gap(e):
+        return 10 * math.log10(2 ** e - 1)
+    thr = []
+    for e in se_c:
+        m = min(range(tabs.M), key=lambda k: (abs(se_m[k] - e), k))
+        thr.append(thr_m[m] + (0.0 if abs(se_m[m] - e) < 1e-6 else gap(e) - gap(se_m[m])))
+    for k in range(1, len(thr)):
+        thr[k] = max(thr[k], thr[k - 1])
+    cqi_mcs = [0]
+    for e in se_c:
+        ok = [m for m in range(tabs.mcs_max + 1) if se_m[m] <= e + 1e-6]
+        cqi_mcs.append(max(ok) if ok else 0)
+    return np.array(thr, dtype=_f32), np.array(cqi_mcs, dtype=np.int64)

@@ -1,14 +1,15 @@
-"""CPU oracle of the NR uplink per-control-step engine.  TEST INFRASTRUCTURE ONLY.
+"""CPU oracle of the NR per-control-step engine (uplink; downlink with dl=True).  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
 checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
 
-A from-scratch torch-CPU restatement of isaac-net's single-cell uplink NR engine, reference backend:
-  NREngine        core/engine.py:319-960   (clock, submit, step, partial reset)
+A from-scratch torch-CPU restatement of isaac-net's single-cell NR engine, reference backend:
+  NREngine        core/engine.py:319-960   (clock, submit, add_dl_frames, step, partial reset)
   NRNet           core/nr_engine.py:171-888 (reset, fading AR(1) + Rician, step_rx, step, _finish)
   UlMac/MacLink   core/mac_ul.py:58-260, core/mac.py:65-616 (lumped SR/grants, PF/maxCI/RR scheduling, retx admission,
                   RBG allocation, EESM / mean-dB link adaptation, HARQ cc/none/ir_lena, rlc_am/drop, OLLA, PF average,
                   RLC in-order delivery, end_step, compact)
+  DlMac           core/mac_dl.py:19-49 (CQI report "mcs" / "38214", estimate, decode SINR, HARQ-ACK timing via K1)
   FrameQueue      core/queues.py:36-143
   NRRng           core/nr_rng.py, core/proto/rng.py (counter hash, Box-Muller)
   RadioMC         core/radio.py:59-277 (log_distance), core/channels/models.py:34-167 + tr38901.py (deterministic LOS
@@ -18,7 +19,7 @@ CPU the oracle is bitwise equal to the reference path (pinned by the golden traj
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
 
 Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state and outputs
-after every step of six scenarios) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF
+after every step of six uplink and three downlink scenarios) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF
 metric is not implemented here (refused), and `whole_band` UL power is not implemented (refused).
 """
 from __future__ import annotations
@@ -370,23 +371,125 @@ class Radio:
 
 
 # ------------------------------------------------------------------------------------------ the engine
+class Link:
+    """MacLink state (mac.py:67-81) and FrameQueue (queues.py:49-61) of one direction, with the queue helpers.
+    The UL queue carries the meta fields cls / det / hid of NRNet (nr_engine.py:191-193); the DL queue cls only
+    (nr_engine.py:194)."""
+
+    INIT = {"sent": 0, "floor": 0, "olla": 0.0, "avg": 100.0, "bsr": 0, "sr_t": -1, "csi": 0.0, "h_state": 0,
+            "h_lo": 0, "h_hi": 0, "h_ready": 0, "h_ntx": 0, "h_mcs": 0, "h_tbs": 0, "h_nsb": 0, "h_comb": 0.0,
+            "h_lexp": -float("inf"), "h_nrb": 0.0, "last_tx": -1}
+    INIT_Q = {"cap": -1, "start": 0, "end": 0, "lost": False, "fin": float("inf"), "cls": 0, "det": False, "hid": 0}
+    CTR = ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
+           "new_while_pending", "prb_used", "prb_avail")
+
+    def __init__(self, d, E, R, S, P, F, phy):
+        self.dir, self.phy = d, phy
+        self.F = F
+        self.FIELDS_Q = ("cap", "start", "end", "lost", "fin", "cls", "det", "hid") if d == "ul" else \
+            ("cap", "start", "end", "lost", "fin", "cls")
+        z = lambda shape, v, dt: torch.full(shape, v, dtype=dt)  # noqa: E731
+        self.sent, self.floor = z((E, R), 0, torch.long), z((E, R), 0, torch.long)
+        self.olla, self.avg = z((E, R), 0.0, torch.float32), z((E, R), 100.0, torch.float32)
+        self.bsr, self.sr_t = z((E, R), 0, torch.long), z((E, R), -1, torch.long)
+        self.csi = z((E, R, S), 0.0, torch.float32)
+        for n in ("h_state", "h_lo", "h_hi", "h_ready", "h_ntx", "h_mcs", "h_tbs", "h_nsb"):
+            setattr(self, n, z((E, R, P), 0, torch.long))
+        self.h_comb, self.h_nrb = z((E, R, P), 0.0, torch.float32), z((E, R, P), 0.0, torch.float32)
+        self.h_lexp = z((E, R, P), -float("inf"), torch.float32)
+        self.last_tx = z((E, R), -1, torch.long)
+        self.q_cap, self.q_start, self.q_end = z((E, R, F), -1, torch.long), z((E, R, F), 0, torch.long), \
+            z((E, R, F), 0, torch.long)
+        self.q_lost, self.q_fin = z((E, R, F), False, torch.bool), z((E, R, F), float("inf"), torch.float64)
+        self.q_cls, self.q_det, self.q_hid = z((E, R, F), 0, torch.long), z((E, R, F), False, torch.bool), \
+            z((E, R, F), 0, torch.long)
+        self.q_enq = z((E, R), 0, torch.long)
+        self.ctr = {k: 0 for k in self.CTR}
+
+    def reset(self, m, full):
+        """MacLink.reset / FrameQueue.reset of the envs m (mac.py:176-189, queues.py:70-78); counters on a full
+        reset only."""
+        for n, v in self.INIT_Q.items():
+            setattr(self, "q_" + n, where_env(m, v, getattr(self, "q_" + n)))
+        self.q_enq = where_env(m, 0, self.q_enq)
+        for n, v in self.INIT.items():
+            setattr(self, n, where_env(m, v, getattr(self, n)))
+        if full:
+            self.ctr = {k: 0 for k in self.CTR}
+
+    def count(self):
+        return (self.q_cap >= 0).sum(-1)
+
+    def unsent(self):
+        return self.q_enq - self.sent
+
+    def ack_ptr(self):
+        """In-order pointer (mac.py:194-197)."""
+        own = (self.h_state == 1) & (self.h_hi > self.floor[..., None])
+        lo = torch.where(own, torch.maximum(self.h_lo, self.floor[..., None]), torch.full_like(self.h_lo, BIG))
+        return torch.minimum(self.sent, lo.min(-1).values)
+
+    def add(self, t, adm, size):
+        """FrameQueue.add (queues.py:87-103): append one frame of size bytes where adm; (accepted, index, one-hot)."""
+        F = self.F
+        cnt = self.count()
+        acc = adm & (cnt < F) & (size > 0)
+        i = cnt.clamp(max=F - 1)
+        oh = onehot(i, F) & acc[..., None]
+        nb = size.round().long()
+        self.q_cap = torch.where(oh, torch.full_like(self.q_cap, t), self.q_cap)
+        self.q_start = torch.where(oh, self.q_enq[..., None], self.q_start)
+        self.q_end = torch.where(oh, (self.q_enq + nb)[..., None], self.q_end)
+        self.q_lost = self.q_lost & ~oh
+        self.q_fin = torch.where(oh, torch.full_like(self.q_fin, float("inf")), self.q_fin)
+        self.q_enq = self.q_enq + nb * acc
+        return acc, i, oh
+
+    def end_step(self, t, timeout, purge):
+        """MacLink.end_step (mac.py:585-596): delivered, timed out (purge only) and resolved-lost frames."""
+        valid = self.q_cap >= 0
+        delivered = valid & (self.q_fin <= t + 1 + 1e-9)
+        if purge:
+            timed = valid & torch.isinf(self.q_fin) & ((t + 1 - self.q_cap) >= timeout)
+        else:
+            timed = torch.zeros_like(valid)
+        dropped = valid & self.q_lost & (self.q_end <= self.ack_ptr()[..., None]) & ~timed
+        return delivered, timed, dropped
+
+    def compact(self, gone):
+        """MacLink.compact (mac.py:598-616) with FrameQueue.remove / floor (queues.py:105-110, 140-143)."""
+        F = self.F
+        self.q_cap = torch.where(gone, torch.full_like(self.q_cap, -1), self.q_cap)
+        key = (self.q_cap < 0).long() * F + torch.arange(F)
+        order = key.argsort(-1)
+        for n in self.FIELDS_Q:
+            setattr(self, "q_" + n, getattr(self, "q_" + n).gather(-1, order))
+        head = self.q_cap[..., 0] >= 0
+        self.floor = torch.where(head, self.q_start[..., 0], self.q_enq)
+        self.sent = torch.maximum(self.sent, self.floor)
+        dead = (self.h_state == 1) & (self.h_hi <= self.floor[..., None]) & (self.h_hi > self.h_lo)
+        for n, v in (("h_state", 0), ("h_ready", 0), ("h_ntx", 0), ("h_comb", 0.0), ("h_lexp", -float("inf")),
+                     ("h_nrb", 0.0)):
+            x = getattr(self, n)
+            setattr(self, n, torch.where(dead, torch.full_like(x, v), x))
+
+
 class OracleEngine:
-    """NREngine + NRNet + UlMac restated for one cell, uplink, lumped grants (see the module docstring)."""
+    """NREngine + NRNet + UlMac / DlMac restated for one cell, lumped UL grants (see the module docstring)."""
 
-    FIELDS_Q = ("cap", "start", "end", "lost", "fin", "cls", "det", "hid")
-
-    def __init__(self, E, R, cfg, seed=0, tabs=None):
-        from isaac_net_amd.phy import PhyTables
+    def __init__(self, E, R, cfg, seed=0, tabs=None, tabs_dl=None):
+        from isaac_net_amd.phy import PhyTables, cqi_tables
         self.cfg, self.E, self.R = cfg, E, R
         self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
-        assert cfg.n_cells == 1 and cfg.ul and not cfg.dl and cfg.ul_grant_model == "lumped"
+        assert cfg.n_cells == 1 and cfg.ul and cfg.ul_grant_model == "lumped"
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay" and cfg.ul_retx_sched == "ofdma"
         assert cfg.ul_amc_alloc == "current" and not cfg.ul_pc_on and cfg.ul_power == "allocated"
         assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
-        self.tabs = tabs if tabs is not None else PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2),
-                                                            cfg.ul_mcs_max)
+        assert cfg.duplex == "tdd"
+        mt = max(cfg.max_harq_tx, 2)
+        self.tabs = tabs if tabs is not None else PhyTables(cfg.mcs_table, cfg.bler_target, mt, cfg.ul_mcs_max)
         self.phy = Phy(self.tabs)
         self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
         self.w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
@@ -400,59 +503,36 @@ class OracleEngine:
         self.last_snr = torch.zeros(E, R)
         self.last_hid = torch.zeros(E, dtype=torch.long)
         self.last_g = None
-        self.ctr = {}
-        E_, R_, S, P, F = E, R, self.S, self.P, self.F
-        z = lambda shape, v, dt: torch.full(shape, v, dtype=dt)  # noqa: E731
-        # MacLink.STATE (mac.py:67-81)
-        self.sent, self.floor = z((E_, R_), 0, torch.long), z((E_, R_), 0, torch.long)
-        self.olla, self.avg = z((E_, R_), 0.0, torch.float32), z((E_, R_), 100.0, torch.float32)
-        self.bsr, self.sr_t = z((E_, R_), 0, torch.long), z((E_, R_), -1, torch.long)
-        self.csi = z((E_, R_, S), 0.0, torch.float32)
-        for n in ("h_state", "h_lo", "h_hi", "h_ready", "h_ntx", "h_mcs", "h_tbs", "h_nsb"):
-            setattr(self, n, z((E_, R_, P), 0, torch.long))
-        self.h_comb, self.h_nrb = z((E_, R_, P), 0.0, torch.float32), z((E_, R_, P), 0.0, torch.float32)
-        self.h_lexp = z((E_, R_, P), -float("inf"), torch.float32)
-        self.last_tx = z((E_, R_), -1, torch.long)
-        # FrameQueue (queues.py:49-61) with the meta fields cls / det / hid of NRNet (nr_engine.py:191-193)
-        self.q_cap, self.q_start, self.q_end = z((E_, R_, F), -1, torch.long), z((E_, R_, F), 0, torch.long), \
-            z((E_, R_, F), 0, torch.long)
-        self.q_lost, self.q_fin = z((E_, R_, F), False, torch.bool), z((E_, R_, F), float("inf"), torch.float64)
-        self.q_cls, self.q_det, self.q_hid = z((E_, R_, F), 0, torch.long), z((E_, R_, F), False, torch.bool), \
-            z((E_, R_, F), 0, torch.long)
-        self.q_enq = z((E_, R_), 0, torch.long)
-        self.h = torch.zeros(E_, R_, S, 2)
+        S, P, F = self.S, self.P, self.F
+        self.ul = Link("ul", E, R, S, P, F, self.phy)
+        self.dl = None
+        if cfg.dl:
+            self.tabs_dl = tabs_dl if tabs_dl is not None else PhyTables(cfg.mcs_table, cfg.bler_target, mt,
+                                                                         cfg.dl_mcs_max)
+            self.dl = Link("dl", E, R, S, P, F, Phy(self.tabs_dl))
+            self.cqi = None
+            if cfg.cqi_table == "38214":
+                thr, cm = cqi_tables(self.tabs_dl, cfg.mcs_table)
+                self.cqi = (torch.from_numpy(thr), torch.from_numpy(cm))
+            self.dl_newest = torch.full((E, R), -1, dtype=torch.long)
+        self.h = torch.zeros(E, R, S, 2)
         self._reset_net(None)
 
-    # ---------------- queue helpers (queues.py) ----------------
-    def count(self):
-        return (self.q_cap >= 0).sum(-1)
+    @property
+    def ctr(self):
+        return self.ul.ctr
 
-    def unsent(self):
-        return self.q_enq - self.sent
-
-    def ack_ptr(self):
-        """In-order pointer (mac.py:194-197)."""
-        own = (self.h_state == 1) & (self.h_hi > self.floor[..., None])
-        lo = torch.where(own, torch.maximum(self.h_lo, self.floor[..., None]), torch.full_like(self.h_lo, BIG))
-        return torch.minimum(self.sent, lo.min(-1).values)
+    def links(self):
+        return [lk for lk in (self.ul, self.dl) if lk is not None]
 
     # ---------------- reset (engine.py:763-794, nr_engine.py:250-320, mac.py:176-189, queues.py:70-78) ----------
     def _reset_net(self, mask):
         E, R, S = self.E, self.R, self.S
         m = torch.ones(E, dtype=torch.bool) if mask is None else mask
-        init_q = {"cap": -1, "start": 0, "end": 0, "lost": False, "fin": float("inf"), "cls": 0, "det": False,
-                  "hid": 0}
-        for n, v in init_q.items():
-            setattr(self, "q_" + n, where_env(m, v, getattr(self, "q_" + n)))
-        self.q_enq = where_env(m, 0, self.q_enq)
-        init = {"sent": 0, "floor": 0, "olla": 0.0, "avg": 100.0, "bsr": 0, "sr_t": -1, "csi": 0.0, "h_state": 0,
-                "h_lo": 0, "h_hi": 0, "h_ready": 0, "h_ntx": 0, "h_mcs": 0, "h_tbs": 0, "h_nsb": 0, "h_comb": 0.0,
-                "h_lexp": -float("inf"), "h_nrb": 0.0, "last_tx": -1}
-        for n, v in init.items():
-            setattr(self, n, where_env(m, v, getattr(self, n)))
-        if mask is None:
-            self.ctr = {k: 0 for k in ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new",
-                                       "lost_frames", "new_while_pending", "prb_used", "prb_avail")}
+        for lk in self.links():
+            lk.reset(m, mask is None)
+        if self.dl is not None:
+            self.dl_newest = where_env(m, -1, self.dl_newest)
         self.rng.reset_mask(mask)
         h0 = self.rng.reset_normal(H0 << 16, R * S * 2).view(E, R, S, 2) / math.sqrt(2)
         if mask is None:
@@ -505,12 +585,26 @@ class OracleEngine:
     def clock(self):
         return self.T - self.epoch
 
-    # ---------------- submit (engine.py:796-819, nr_engine.py:451-487, queues.py:87-103) ----------------
-    def submit(self, t, requests, det=None, hid=None):
-        """t: None (engine clock) or the clock value; requests: send [E,R] or an object with send / det / hid."""
-        cfg, F = self.cfg, self.F
+    # ---------------- submit (engine.py:796-827, nr_engine.py:451-498, queues.py:87-103) ----------------
+    def _air_bytes(self, size):
+        cfg = self.cfg
+        if cfg.pkt_overhead_bytes:
+            size = size + torch.ceil(size / cfg.pkt_payload_bytes) * cfg.pkt_overhead_bytes
+        return size
+
+    def _admit(self, lk, t, want):
+        if self.cfg.discard != "pdcp_arrival":
+            return want
+        stale = (lk.q_cap[..., 0] >= 0) & ((t - lk.q_cap[..., 0]) >= self.cfg.timeout_steps)
+        return want & ~stale
+
+    def _check_t(self, t):
         if t is not None and int(t) + (self.uniform_epoch or 0) != self.T:
             raise ValueError("t must equal the engine clock")
+
+    def submit(self, t, requests, det=None, hid=None):
+        """t: None (engine clock) or the clock value; requests: send [E,R] or an object with send / det / hid."""
+        self._check_t(t)
         t = self.T
         send = requests.send if hasattr(requests, "send") else requests
         if hasattr(requests, "send"):
@@ -519,35 +613,33 @@ class OracleEngine:
         det = torch.zeros_like(send, dtype=torch.bool) if det is None else det
         hid = torch.zeros(self.E, dtype=torch.long) if hid is None else hid
         self.last_hid = hid.clone()
-        want = send > 0
-        adm = want
-        if cfg.discard == "pdcp_arrival":
-            stale = (self.q_cap[..., 0] >= 0) & ((t - self.q_cap[..., 0]) >= cfg.timeout_steps)
-            adm = want & ~stale
-        size = self.sizes[(send - 1).clamp(min=0)]
-        if cfg.pkt_overhead_bytes:
-            size = size + torch.ceil(size / cfg.pkt_payload_bytes) * cfg.pkt_overhead_bytes
-        cnt = self.count()
-        acc = adm & (cnt < F) & (size > 0)
-        i = cnt.clamp(max=F - 1)
-        oh = onehot(i, F) & acc[..., None]
-        nb = size.round().long()
-        self.q_cap = torch.where(oh, torch.full_like(self.q_cap, t), self.q_cap)
-        self.q_start = torch.where(oh, self.q_enq[..., None], self.q_start)
-        self.q_end = torch.where(oh, (self.q_enq + nb)[..., None], self.q_end)
-        self.q_lost = self.q_lost & ~oh
-        self.q_fin = torch.where(oh, torch.full_like(self.q_fin, float("inf")), self.q_fin)
-        self.q_enq = self.q_enq + nb * acc
-        self.q_cls = torch.where(oh, send[..., None], self.q_cls)
-        self.q_det = torch.where(oh, det[..., None], self.q_det)
-        self.q_hid = torch.where(oh, hid[:, None, None].expand(-1, self.R, 1), self.q_hid)
+        lk = self.ul
+        adm = self._admit(lk, t, send > 0)
+        size = self._air_bytes(self.sizes[(send - 1).clamp(min=0)])
+        acc, _, oh = lk.add(t, adm, size)
+        lk.q_cls = torch.where(oh, send[..., None], lk.q_cls)
+        lk.q_det = torch.where(oh, det[..., None], lk.q_det)
+        lk.q_hid = torch.where(oh, hid[:, None, None].expand(-1, self.R, 1), lk.q_hid)
+        return acc
+
+    def add_dl_frames(self, t, nbytes, cls=None):
+        """NRNet.add_dl_frames (nr_engine.py:489-497): one DL frame of nbytes [E,R] application bytes (0 = none)."""
+        assert self.dl is not None, "cfg.dl is False"
+        self._check_t(t)
+        t = self.T
+        lk = self.dl
+        adm = self._admit(lk, t, nbytes > 0)
+        acc, _, oh = lk.add(t, adm, self._air_bytes(nbytes.float()))
+        if cls is not None:                              # meta fields are not reset by add: a slot keeps its class
+            lk.q_cls = torch.where(oh, cls.long()[..., None], lk.q_cls)
         return acc
 
     # ---------------- step (engine.py:867-960, nr_engine.py:613-668) ----------------
-    def step(self, t=None, x=None, snr_db=None):
+    def step(self, t=None, x=None, snr_db=None, dl_snr_db=None):
         cfg = self.cfg
         T = self.T
         hid = self.last_hid
+        dl_ref = None
         if snr_db is None and x is not None and x.dim() == 3:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
@@ -555,16 +647,24 @@ class OracleEngine:
             pgs = pg[..., None].expand(-1, -1, self.S)
             n_ul = torch.full_like(pgs, cfg.noise_dbm_per_prb("gnb"))
             ul_ref = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs) + pgs - n_ul
+            if self.dl is not None:                      # NRNet.step_rx (nr_engine.py:624-631), reciprocal path gain
+                n_dl = torch.full_like(pgs, cfg.noise_dbm_per_prb("ue"))
+                dl_ref = cfg.gnb_tx_dbm - 10 * math.log10(cfg.nprb) + pgs - n_dl
             snr = pg + cfg.ue_tx_dbm - cfg.subband_noise_dbm
         else:
             xs = x if snr_db is None else snr_db
             ul_ref = xs if xs.dim() == 3 else xs[..., None].expand(-1, -1, self.S)
             snr = xs if xs.dim() == 2 else xs.mean(-1)
-        out = self._net_step(T, ul_ref, hid)
+            if self.dl is not None:                      # NRNet.step (nr_engine.py:651-653)
+                dref = dl_snr_db if dl_snr_db is not None else xs + cfg.dl_snr_offset_db
+                dl_ref = dref if dref.dim() == 3 else dref[..., None].expand(-1, -1, self.S)
+        out = self._net_step(T, ul_ref, dl_ref, hid)
         self.last_snr = snr.clone()
         out["newest"] = self._rel(out["newest"])
         self.T = T + 1
         out["cap"] = self._rel(out["cap"])
+        if "dl_newest" in out:
+            out["dl_newest"] = self._rel(out["dl_newest"])
         out["sinr_db"] = snr
         out["serving_cell"] = torch.zeros(self.E, self.R, dtype=torch.long)
         out["t"] = (T - self.epoch).clone()
@@ -577,20 +677,24 @@ class OracleEngine:
     def schedule(self, g0):
         return self.cfg.schedule(g0)
 
-    def _net_step(self, t, ul_ref, hid):
+    def _net_step(self, t, ul_ref, dl_ref, hid):
         cfg = self.cfg
         N = cfg.slots_per_step
         g0 = t * N
         if self.rician:
             self.k_lin = self.k_in                       # _rician_update with no ramp (nr_engine.py:410-415)
-        for rel, uls, sr in self.schedule(g0):
+        for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
             g = g0 + rel
             self._evolve(g, rel)
             gain = self._gain()
+            if cqi:
+                self._cqi_report(dl_ref, gain)
+            if dls:
+                self._slot(self.dl, g, t + (rel + 1) / N, dls, dl_ref, gain, rel, g0 + ack)
             if sr:
                 self._sr_step(g)
             if uls:
-                self._slot(g, t + (rel + 1) / N, uls, ul_ref, gain, rel)
+                self._slot(self.ul, g, t + (rel + 1) / N, uls, ul_ref, gain, rel, 0)
         return self._finish(t, hid)
 
     def _evolve(self, g, rel):
@@ -615,56 +719,73 @@ class OracleEngine:
         x = torch.sqrt(k * inv) * self.spec[..., None, :] + torch.sqrt(inv) * self.h
         return 10 * torch.log10((x ** 2).sum(-1).clamp(min=1e-6))
 
+    def _cqi_report(self, sinr_ref, gain_now):
+        """DlMac.cqi_report (mac_dl.py:30-40): the best MCS (or the 38.214 CQI mapped back to an MCS) per subband;
+        the gNB keeps that MCS's threshold SINR as its estimate until the next report."""
+        lk = self.dl
+        if self.cqi is None:
+            m = lk.phy.mcs_at(sinr_ref + gain_now)
+        else:
+            thr, cqi_mcs = self.cqi
+            cqi = ((sinr_ref + gain_now)[..., None] >= thr).sum(-1)
+            m = cqi_mcs[cqi]
+        lk.csi = lk.phy.thr_ref[m] - sinr_ref
+
     def _sr_step(self, g):
         """UlMac.sr_step, lumped (mac_ul.py:66-71)."""
-        need_sr = (self.unsent() > 0) & (self.bsr <= 0) & (self.sr_t < 0)
-        self.sr_t = torch.where(need_sr, torch.full_like(self.sr_t, g), self.sr_t)
+        u = self.ul
+        need_sr = (u.unsent() > 0) & (u.bsr <= 0) & (u.sr_t < 0)
+        u.sr_t = torch.where(need_sr, torch.full_like(u.sr_t, g), u.sr_t)
 
     def _split(self, n_prb):
         return 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
 
-    def _slot(self, g, frac, nsym, sinr_ref, gain_now, rel):
-        """MacLink.slot for the UL (mac.py:228-508 with the UlMac hooks of mac_ul.py)."""
-        cfg, E, R, S, P, phy = self.cfg, self.E, self.R, self.S, self.P, self.phy
+    def _slot(self, L, g, frac, nsym, sinr_ref, gain_now, rel, ack_slot):
+        """MacLink.slot (mac.py:228-508) with the UlMac hooks (mac_ul.py) for L.dir == "ul" and the DlMac hooks
+        (mac_dl.py:42-49) for "dl"."""
+        cfg, E, R, S, P, phy = self.cfg, self.E, self.R, self.S, self.P, L.phy
+        ul = L.dir == "ul"
         w = self.w
-        unsent = self.unsent()
-        self.h_state = torch.where((self.h_state == 2) & (self.h_ready <= g), torch.zeros_like(self.h_state),
-                                   self.h_state)
-        # UlMac._pre_slot_lumped (mac_ul.py:140-147)
-        P_ = len(cfg.tdd_pattern)
-        pg_pos = next(p for p in range(P_) if cfg.slot_symbols(p)[1] > 0)
-        if cfg.proactive_grant == "every_ul_slot" or (cfg.proactive_grant == "per_period" and g % P_ == pg_pos):
-            self.bsr = self.bsr.clamp(min=1)
-        granted = (self.sr_t >= 0) & (g - self.sr_t >= cfg.sr_delay)
-        self.bsr = torch.where(granted, self.bsr.clamp(min=1), self.bsr)
-        self.sr_t = torch.where(granted, torch.full_like(self.sr_t, -1), self.sr_t)
+        unsent = L.unsent()
+        L.h_state = torch.where((L.h_state == 2) & (L.h_ready <= g), torch.zeros_like(L.h_state), L.h_state)
+        if ul:                                           # UlMac._pre_slot_lumped (mac_ul.py:140-147)
+            P_ = len(cfg.tdd_pattern)
+            pg_pos = next(p for p in range(P_) if cfg.slot_symbols(p)[1] > 0)
+            if cfg.proactive_grant == "every_ul_slot" or (cfg.proactive_grant == "per_period" and g % P_ == pg_pos):
+                L.bsr = L.bsr.clamp(min=1)
+            granted = (L.sr_t >= 0) & (g - L.sr_t >= cfg.sr_delay)
+            L.bsr = torch.where(granted, L.bsr.clamp(min=1), L.bsr)
+            L.sr_t = torch.where(granted, torch.full_like(L.sr_t, -1), L.sr_t)
         # candidates
-        rx_el = (self.h_state == 1) & (self.h_ready <= g)
-        rx_p = torch.where(rx_el, self.h_ready, torch.full_like(self.h_ready, BIG)).argmin(-1)
+        rx_el = (L.h_state == 1) & (L.h_ready <= g)
+        rx_p = torch.where(rx_el, L.h_ready, torch.full_like(L.h_ready, BIG)).argmin(-1)
         has_rx = rx_el.any(-1)
-        free = self.h_state == 0
+        free = L.h_state == 0
         p_new = free.long().argmax(-1)
-        need = torch.minimum(self.bsr, unsent)
+        need = torch.minimum(L.bsr, unsent) if ul else unsent
         new_el = free.any(-1) & (need > 0) & ~has_rx
-        pending = (self.h_state == 1).any(-1)
-        rx_nsb = self.h_nsb.gather(-1, rx_p[..., None]).squeeze(-1)
-        # UlMac._sched_estimate (mac_ul.py:154-171)
-        est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + self.csi
-        if cfg.phr_cap:
-            ref = sinr_ref.mean(-1)
-            n_max_prb = cfg.snr_ref_prbs * 10 ** ((ref - cfg.phr_min_db) / 10)
-            n_max = torch.floor(n_max_prb / w[0]).clamp(1, S).long()
-        else:
+        pending = (L.h_state == 1).any(-1)
+        rx_nsb = L.h_nsb.gather(-1, rx_p[..., None]).squeeze(-1)
+        if ul:                                           # UlMac._sched_estimate (mac_ul.py:154-171)
+            est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + L.csi
+            if cfg.phr_cap:
+                ref = sinr_ref.mean(-1)
+                n_max_prb = cfg.snr_ref_prbs * 10 ** ((ref - cfg.phr_min_db) / 10)
+                n_max = torch.floor(n_max_prb / w[0]).clamp(1, S).long()
+            else:
+                n_max = torch.full((E, R), S, dtype=torch.long)
+        else:                                            # DlMac._sched_estimate (mac_dl.py:42-43)
+            est = sinr_ref + L.csi
             n_max = torch.full((E, R), S, dtype=torch.long)
-        est_o = est + (self.olla[..., None] if cfg.olla else 0.0)
+        est_o = est + (L.olla[..., None] if cfg.olla else 0.0)
         re_prb = float(min(12 * nsym - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156))
         rate_sb = phy.se[phy.mcs_at(est_o)] * re_prb * w / 8
         if cfg.scheduler == "maxci":
             metric_sb = rate_sb
         elif cfg.scheduler == "rr":
-            metric_sb = (g - self.last_tx).float()[..., None].expand_as(rate_sb)
+            metric_sb = (g - L.last_tx).float()[..., None].expand_as(rate_sb)
         else:
-            metric_sb = rate_sb / self.avg.clamp(min=AVG_MIN)[..., None]
+            metric_sb = rate_sb / L.avg.clamp(min=AVG_MIN)[..., None]
         # retransmission admission (mac.py:300-304)
         rkey = torch.where(has_rx, metric_sb.sum(-1), torch.full_like(metric_sb[..., 0], -1.0))
         order = rkey.argsort(-1, descending=True)
@@ -710,9 +831,9 @@ class OracleEngine:
         tx_rx = has_rx & (n_sb == rx_nsb) & (n_sb > 0)
         tx_new = new_el & (n_sb > 0)
         tx = tx_rx | tx_new
-        # link adaptation (mac.py:386-405, mac_ul.py:182-183)
-        est_tx = sinr_ref - self._split(n_prb)[..., None] + self.csi
-        off = self.olla if cfg.olla else torch.zeros_like(self.olla)
+        # link adaptation (mac.py:386-405; UL estimate mac_ul.py:182-183, DL the scheduler's)
+        est_tx = sinr_ref - self._split(n_prb)[..., None] + L.csi if ul else est
+        off = L.olla if cfg.olla else torch.zeros_like(L.olla)
         mcs_new, tbs_new = phy.select_mcs(est_tx, won, off, n_prb, nsym, cfg.dmrs_re_per_prb,
                                           cfg.overhead_re_per_prb, cfg.eff_sinr, w)
         cap_b = (tbs_new // 8 - cfg.tb_overhead_bytes).clamp(min=1)
@@ -721,137 +842,143 @@ class OracleEngine:
         p_tx = torch.where(tx_rx, rx_p, p_new)
         ohp = onehot(p_tx, P) & tx[..., None]
         ohn = ohp & tx_new[..., None]
-        self.h_lo = torch.where(ohn, self.sent[..., None], self.h_lo)
-        self.h_hi = torch.where(ohn, (self.sent + byt_new)[..., None], self.h_hi)
-        self.h_mcs = torch.where(ohn, mcs_new[..., None], self.h_mcs)
-        self.h_tbs = torch.where(ohn, tbs_new[..., None], self.h_tbs)
-        self.h_nsb = torch.where(ohn, n_sb[..., None], self.h_nsb)
-        self.h_ntx = torch.where(ohn, torch.zeros_like(self.h_ntx), self.h_ntx)
-        self.h_comb = torch.where(ohn, torch.zeros_like(self.h_comb), self.h_comb)
-        self.h_lexp = torch.where(ohn, torch.full_like(self.h_lexp, -float("inf")), self.h_lexp)
-        self.h_nrb = torch.where(ohn, torch.zeros_like(self.h_nrb), self.h_nrb)
-        self.h_state = torch.where(ohn, torch.ones_like(self.h_state), self.h_state)
-        self.sent = self.sent + byt_new * tx_new
+        L.h_lo = torch.where(ohn, L.sent[..., None], L.h_lo)
+        L.h_hi = torch.where(ohn, (L.sent + byt_new)[..., None], L.h_hi)
+        L.h_mcs = torch.where(ohn, mcs_new[..., None], L.h_mcs)
+        L.h_tbs = torch.where(ohn, tbs_new[..., None], L.h_tbs)
+        L.h_nsb = torch.where(ohn, n_sb[..., None], L.h_nsb)
+        L.h_ntx = torch.where(ohn, torch.zeros_like(L.h_ntx), L.h_ntx)
+        L.h_comb = torch.where(ohn, torch.zeros_like(L.h_comb), L.h_comb)
+        L.h_lexp = torch.where(ohn, torch.full_like(L.h_lexp, -float("inf")), L.h_lexp)
+        L.h_nrb = torch.where(ohn, torch.zeros_like(L.h_nrb), L.h_nrb)
+        L.h_state = torch.where(ohn, torch.ones_like(L.h_state), L.h_state)
+        L.sent = L.sent + byt_new * tx_new
         g1 = lambda x: x.gather(-1, p_tx[..., None]).squeeze(-1)  # noqa: E731
-        mcs, tbs = g1(self.h_mcs), g1(self.h_tbs)
-        ntx = g1(self.h_ntx) + 1
-        # decoding (mac.py:428-454, mac_ul.py:185-192)
-        act = sinr_ref - self._split(n_prb)[..., None] + gain_now
+        mcs, tbs = g1(L.h_mcs), g1(L.h_tbs)
+        ntx = g1(L.h_ntx) + 1
+        # decoding (mac.py:428-454; UL mac_ul.py:185-192, DL mac_dl.py:45-46)
+        act = sinr_ref - self._split(n_prb)[..., None] + gain_now if ul else sinr_ref + gain_now
         mcs_eq = None
         if cfg.harq_combining == "ir_lena":
             lse, _ = phy.eesm_lse(act, won, mcs, w)
-            lexp = torch.logaddexp(g1(self.h_lexp), lse)
-            nrb = g1(self.h_nrb) + n_prb
+            lexp = torch.logaddexp(g1(L.h_lexp), lse)
+            nrb = g1(L.h_nrb) + n_prb
             eff_used = 10 * torch.log10((-phy.beta[mcs] * (lexp - torch.log(nrb.clamp(min=1)))).clamp(min=1e-6))
             eff_used = eff_used.nan_to_num(nan=-30.0, posinf=60.0, neginf=-30.0)
             mcs_eq = phy.mcs_eq[mcs, ntx.clamp(max=phy.mcs_eq.shape[1] - 1)]
-            self.h_lexp = torch.where(ohp, lexp[..., None], self.h_lexp)
-            self.h_nrb = torch.where(ohp, nrb[..., None], self.h_nrb)
-            comb = g1(self.h_comb)
+            L.h_lexp = torch.where(ohp, lexp[..., None], L.h_lexp)
+            L.h_nrb = torch.where(ohp, nrb[..., None], L.h_nrb)
+            comb = g1(L.h_comb)
         else:
             eff = phy.eff_sinr(act, won, mcs, cfg.eff_sinr, w)
-            comb = g1(self.h_comb) + 10 ** (eff / 10) if cfg.harq_combining == "cc" else 10 ** (eff / 10)
+            comb = g1(L.h_comb) + 10 ** (eff / 10) if cfg.harq_combining == "cc" else 10 ** (eff / 10)
             eff_used = 10 * torch.log10(comb.clamp(min=1e-9))
         p_err = phy.tb_error_prob(mcs, eff_used, tbs, mcs_eq)
-        u = self.rng.step_uniform(BLER_UL, rel, R)
+        u = self.rng.step_uniform(BLER_UL if ul else BLER_DL, rel, R)
         ok = tx & (u >= p_err)
         fail = tx & ~ok
         exh = fail & (ntx >= cfg.max_harq_tx)
-        # HARQ update (mac.py:456-477, UL timing mac_ul.py:218-219)
+        # HARQ update (mac.py:456-477; UL timing mac_ul.py:218-219, DL mac_dl.py:47-49)
+        if ul:
+            st_ok, rdy_ok, rdy_fail = 0, g, g + cfg.ul_rtt
+        else:
+            r_ = ack_slot + cfg.gnb_proc_slots
+            st_ok, rdy_ok, rdy_fail = 2, r_, r_
         ohp_ok, ohp_fail, ohp_exh = ohp & ok[..., None], ohp & fail[..., None], ohp & exh[..., None]
-        self.h_state = torch.where(ohp_ok, torch.zeros_like(self.h_state), self.h_state)
-        self.h_ready = torch.where(ohp_ok, torch.full_like(self.h_ready, g), self.h_ready)
-        self.h_ntx = torch.where(ohp, ntx[..., None], self.h_ntx)
-        self.h_comb = torch.where(ohp, comb[..., None], self.h_comb)
-        self.h_ready = torch.where(ohp_fail, torch.full_like(self.h_ready, g + cfg.ul_rtt), self.h_ready)
-        lo_tx, hi_tx = g1(self.h_lo), g1(self.h_hi)
+        L.h_state = torch.where(ohp_ok, torch.full_like(L.h_state, st_ok), L.h_state)
+        L.h_ready = torch.where(ohp_ok, torch.full_like(L.h_ready, rdy_ok), L.h_ready)
+        L.h_ntx = torch.where(ohp, ntx[..., None], L.h_ntx)
+        L.h_comb = torch.where(ohp, comb[..., None], L.h_comb)
+        L.h_ready = torch.where(ohp_fail, torch.full_like(L.h_ready, rdy_fail), L.h_ready)
+        lo_tx, hi_tx = g1(L.h_lo), g1(L.h_hi)
         lost_new = 0
         if cfg.harq_fail == "rlc_am":
-            self.h_ntx = torch.where(ohp_exh, torch.zeros_like(self.h_ntx), self.h_ntx)
-            self.h_comb = torch.where(ohp_exh, torch.zeros_like(self.h_comb), self.h_comb)
-            self.h_lexp = torch.where(ohp_exh, torch.full_like(self.h_lexp, -float("inf")), self.h_lexp)
-            self.h_nrb = torch.where(ohp_exh, torch.zeros_like(self.h_nrb), self.h_nrb)
-            self.h_ready = torch.where(ohp_exh, torch.full_like(self.h_ready, g + cfg.rlc_retx_slots), self.h_ready)
+            L.h_ntx = torch.where(ohp_exh, torch.zeros_like(L.h_ntx), L.h_ntx)
+            L.h_comb = torch.where(ohp_exh, torch.zeros_like(L.h_comb), L.h_comb)
+            L.h_lexp = torch.where(ohp_exh, torch.full_like(L.h_lexp, -float("inf")), L.h_lexp)
+            L.h_nrb = torch.where(ohp_exh, torch.zeros_like(L.h_nrb), L.h_nrb)
+            L.h_ready = torch.where(ohp_exh, torch.full_like(L.h_ready, g + cfg.rlc_retx_slots), L.h_ready)
         else:
-            self.h_state = torch.where(ohp_exh, torch.zeros_like(self.h_state), self.h_state)
-            ov = exh[..., None] & (self.q_start < hi_tx[..., None]) & (self.q_end > lo_tx[..., None]) & \
-                (self.q_cap >= 0)
-            lost_new = int((ov & ~self.q_lost).sum())
-            self.q_lost = self.q_lost | ov
-        # OLLA, BSR / CSI, PF (mac.py:479-485, mac_ul.py:221-236, mac.py:534-554)
+            L.h_state = torch.where(ohp_exh, torch.zeros_like(L.h_state), L.h_state)
+            ov = exh[..., None] & (L.q_start < hi_tx[..., None]) & (L.q_end > lo_tx[..., None]) & (L.q_cap >= 0)
+            lost_new = int((ov & ~L.q_lost).sum())
+            L.q_lost = L.q_lost | ov
+        # OLLA, UL BSR / CSI, PF (mac.py:479-485, mac_ul.py:221-236, mac.py:534-554)
         if cfg.olla:
-            self.olla = (self.olla + cfg.olla_up_db * ok - self.olla_dn * fail).clamp(-10, 10)
+            L.olla = (L.olla + cfg.olla_up_db * ok - self.olla_dn * fail).clamp(-10, 10)
         served = (hi_tx - lo_tx) * ok
-        self.bsr = torch.where(tx, self.unsent(), self.bsr)
-        self.csi = gain_now
-        self.avg = ((1 - 1 / cfg.pf_window) * self.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
+        if ul:
+            L.bsr = torch.where(tx, L.unsent(), L.bsr)
+            L.csi = gain_now
+        L.avg = ((1 - 1 / cfg.pf_window) * L.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
         if cfg.scheduler == "rr":
-            self.last_tx = torch.where(tx, torch.full_like(self.last_tx, g), self.last_tx)
-        c = self.ctr
+            L.last_tx = torch.where(tx, torch.full_like(L.last_tx, g), L.last_tx)
+        c = L.ctr
         c["tb_new"] += int(tx_new.sum()); c["tb_retx"] += int(tx_rx.sum()); c["tb_ok"] += int(ok.sum())
         c["tb_fail"] += int(fail.sum()); c["exhaust"] += int(exh.sum()); c["bytes_ok"] += int(served.sum())
         c["bytes_new"] += int((byt_new * tx_new).sum()); c["new_while_pending"] += int((tx_new & pending).sum())
         c["prb_used"] += float((n_prb * tx).sum()); c["prb_avail"] += float(self.w.sum()) * E
         c["lost_frames"] += lost_new
         # RLC in-order delivery (mac.py:500-503)
-        ack = self.ack_ptr()
-        done = (self.q_cap >= 0) & (self.q_end <= ack[..., None]) & ~self.q_lost & torch.isinf(self.q_fin)
-        self.q_fin = torch.where(done, torch.full_like(self.q_fin, frac + cfg.proc_offset_ms / cfg.control_step_ms),
-                                 self.q_fin)
+        ack = L.ack_ptr()
+        done = (L.q_cap >= 0) & (L.q_end <= ack[..., None]) & ~L.q_lost & torch.isinf(L.q_fin)
+        L.q_fin = torch.where(done, torch.full_like(L.q_fin, frac + cfg.proc_offset_ms / cfg.control_step_ms),
+                              L.q_fin)
 
     # ---------------- end of step (nr_engine.py:843-888, mac.py:585-616, mac_ul.py:255-257) ----------------
     def _finish(self, t, cur_hid):
-        cfg, F = self.cfg, self.F
+        cfg = self.cfg
+        purge = cfg.discard == "purge"
         self.rng.ctr[STEP].add_(1)
-        valid = self.q_cap >= 0
-        delivered = valid & (self.q_fin <= t + 1 + 1e-9)
-        if cfg.discard == "purge":
-            timed = valid & torch.isinf(self.q_fin) & ((t + 1 - self.q_cap) >= cfg.timeout_steps)
-        else:
-            timed = torch.zeros_like(valid)
-        dropped = valid & self.q_lost & (self.q_end <= self.ack_ptr()[..., None]) & ~timed
-        capd = torch.where(delivered, self.q_cap, torch.full_like(self.q_cap, -1))
+        u = self.ul
+        delivered, timed, dropped = u.end_step(t, cfg.timeout_steps, purge)
+        valid = u.q_cap >= 0
+        capd = torch.where(delivered, u.q_cap, torch.full_like(u.q_cap, -1))
         newest = capd.max(-1).values
-        det_env = (delivered & self.q_det & (self.q_hid == cur_hid[:, None, None])).flatten(1).any(-1)
+        det_env = (delivered & u.q_det & (u.q_hid == cur_hid[:, None, None])).flatten(1).any(-1)
         out = {"newest": newest, "det_env": det_env, "delivered": delivered, "timed_out": timed, "dropped": dropped,
-               "cap": self.q_cap.clone(), "cls": torch.where(valid, self.q_cls, torch.zeros_like(self.q_cls)),
-               "delay": torch.where(delivered, (self.q_fin - self.q_cap.double()).float(),
-                                    torch.full(self.q_cap.shape, float("nan")))}
-        gone = delivered | timed | dropped
-        self.q_cap = torch.where(gone, torch.full_like(self.q_cap, -1), self.q_cap)
-        key = (self.q_cap < 0).long() * F + torch.arange(F)
-        order = key.argsort(-1)
-        for n in self.FIELDS_Q:
-            setattr(self, "q_" + n, getattr(self, "q_" + n).gather(-1, order))
-        head = self.q_cap[..., 0] >= 0
-        self.floor = torch.where(head, self.q_start[..., 0], self.q_enq)
-        self.sent = torch.maximum(self.sent, self.floor)
-        dead = (self.h_state == 1) & (self.h_hi <= self.floor[..., None]) & (self.h_hi > self.h_lo)
-        for n, v in (("h_state", 0), ("h_ready", 0), ("h_ntx", 0), ("h_comb", 0.0), ("h_lexp", -float("inf")),
-                     ("h_nrb", 0.0)):
-            x = getattr(self, n)
-            setattr(self, n, torch.where(dead, torch.full_like(x, v), x))
-        self.bsr = torch.minimum(self.bsr, self.unsent())
-        out["queue_len"] = self.count()
-        out["queue_bytes"] = (self.q_enq - self.ack_ptr()).clamp(min=0).float()
+               "cap": u.q_cap.clone(), "cls": torch.where(valid, u.q_cls, torch.zeros_like(u.q_cls)),
+               "delay": torch.where(delivered, (u.q_fin - u.q_cap.double()).float(),
+                                    torch.full(u.q_cap.shape, float("nan")))}
+        u.compact(delivered | timed | dropped)
+        u.bsr = torch.minimum(u.bsr, u.unsent())
+        if self.dl is not None:
+            d = self.dl
+            dd, dt_, dr = d.end_step(t, cfg.timeout_steps, purge)
+            self.dl_newest = torch.where(dd, d.q_cap, torch.full_like(d.q_cap, -1)).max(-1).values
+            d.compact(dd | dt_ | dr)
+        out["queue_len"] = u.count()
+        out["queue_bytes"] = (u.q_enq - u.ack_ptr()).clamp(min=0).float()
+        if self.dl is not None:
+            out["dl_newest"] = self.dl_newest.clone()
+            out["dl_queue_len"] = self.dl.count()
         return out
 
     # ---------------- state in the reference's state_dict names (core/nr_fast.py:41-75) ----------------
-    STATE_MAP = {"ul.sent": "sent", "ul.floor": "floor", "ul.olla": "olla", "ul.avg": "avg", "ul.bsr": "bsr",
-                 "ul.sr_t": "sr_t", "ul.csi": "csi", "ul.h_state": "h_state", "ul.h_lo": "h_lo", "ul.h_hi": "h_hi",
-                 "ul.h_ready": "h_ready", "ul.h_ntx": "h_ntx", "ul.h_mcs": "h_mcs", "ul.h_tbs": "h_tbs",
-                 "ul.h_nsb": "h_nsb", "ul.h_comb": "h_comb", "ul.h_lexp": "h_lexp", "ul.h_nrb": "h_nrb",
-                 "ul.last_tx": "last_tx", "ul.q.cap": "q_cap", "ul.q.start": "q_start", "ul.q.end": "q_end",
-                 "ul.q.lost": "q_lost", "ul.q.fin": "q_fin", "ul.q.cls": "q_cls", "ul.q.det": "q_det",
-                 "ul.q.hid": "q_hid", "ul.q.enq": "q_enq", "net.h": "h", "eng.epoch": "epoch",
-                 "eng._last_snr": "last_snr", "eng._last_hid": "last_hid"}
+    LINK_KEYS = {"sent": "sent", "floor": "floor", "olla": "olla", "avg": "avg", "bsr": "bsr", "sr_t": "sr_t",
+                 "csi": "csi", "h_state": "h_state", "h_lo": "h_lo", "h_hi": "h_hi", "h_ready": "h_ready",
+                 "h_ntx": "h_ntx", "h_mcs": "h_mcs", "h_tbs": "h_tbs", "h_nsb": "h_nsb", "h_comb": "h_comb",
+                 "h_lexp": "h_lexp", "h_nrb": "h_nrb", "last_tx": "last_tx", "q.cap": "q_cap", "q.start": "q_start",
+                 "q.end": "q_end", "q.lost": "q_lost", "q.fin": "q_fin", "q.cls": "q_cls", "q.enq": "q_enq"}
+    UL_ONLY = {"q.det": "q_det", "q.hid": "q_hid"}
+    NET_KEYS = {"net.h": "h", "eng.epoch": "epoch", "eng._last_snr": "last_snr", "eng._last_hid": "last_hid"}
     RICIAN_MAP = {"net.spec": "spec", "net.k_los": "k_los", "net.k_in": "k_in", "net.k_lin": "k_lin",
                   "net.k_from": "k_from", "net.k_g0": "k_g0"}
 
-    def state(self):
-        out = {k: getattr(self, v) for k, v in self.STATE_MAP.items()}
+    def _state_items(self):
+        """[(state_dict key, owner, attribute)] of every state tensor."""
+        items = [(k, self, v) for k, v in self.NET_KEYS.items()]
+        for lk in self.links():
+            keys = dict(self.LINK_KEYS, **(self.UL_ONLY if lk.dir == "ul" else {}))
+            items += [(f"{lk.dir}.{k}", lk, v) for k, v in keys.items()]
+        if self.dl is not None:
+            items.append(("net.dl_newest", self, "dl_newest"))
         if self.rician:
-            out.update({k: getattr(self, v) for k, v in self.RICIAN_MAP.items()})
+            items += [(k, self, v) for k, v in self.RICIAN_MAP.items()]
+        return items
+
+    def state(self):
+        out = {k: getattr(o, v) for k, o, v in self._state_items()}
         out["rng.episode"] = self.rng.episode
         out["rng.ctr[1]"] = self.rng.ctr[SUBMIT]
         out["rng.ctr[2]"] = self.rng.ctr[STEP]
@@ -859,13 +986,9 @@ class OracleEngine:
 
     def load_state(self, sd, T, last_g):
         """Teacher forcing: overwrite every state tensor (copies) and the host clock / last fading slot."""
-        for k, v in self.STATE_MAP.items():
+        for k, o, v in self._state_items():
             if k in sd:
-                setattr(self, v, torch.as_tensor(sd[k]).clone())
-        if self.rician:
-            for k, v in self.RICIAN_MAP.items():
-                if k in sd:
-                    setattr(self, v, torch.as_tensor(sd[k]).clone())
+                setattr(o, v, torch.as_tensor(sd[k]).clone())
         self.rng.episode = torch.as_tensor(sd["rng.episode"]).clone()
         self.rng.ctr[SUBMIT] = torch.as_tensor(sd["rng.ctr[1]"]).clone()
         self.rng.ctr[STEP] = torch.as_tensor(sd["rng.ctr[2]"]).clone()

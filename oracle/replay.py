@@ -27,6 +27,20 @@ def submits(counts_s):
     return out
 
 
+def dl_frames(d, s):
+    """The harness's add_dl_frames calls of step s: (bytes [E,R] float32, class [E,R] int64) per call, DL class 1
+    first, one call per message index (empty without a downlink)."""
+    if "dl_counts" not in d.files:
+        return []
+    out = []
+    cnt, sizes = d["dl_counts"][s], d["dl_sizes"]
+    for ci in range(cnt.shape[-1]):
+        n = cnt[..., ci]
+        for i in range(int(n.max()) if n.size else 0):
+            out.append((np.where(n > i, sizes[ci], 0.0).astype(np.float32), np.where(n > i, ci + 1, 0).astype(np.int64)))
+    return out
+
+
 def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)):
     """Drive eng (oracle or HIP engine) through the case; on_step(s, out, accepted_list) after every step."""
     T = int(d["steps"]) if steps is None else steps
@@ -35,6 +49,8 @@ def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)
         if len(ids):
             eng.reset(ids.tolist())
         acc = [eng.submit(None, to(send)) for send in submits(d["counts"][s])]
+        for nb, cls in dl_frames(d, s):
+            eng.add_dl_frames(None, to(nb), to(cls))
         x = to(d["x"][s])
         if kind == "snr3":
             o = eng.step(None, snr_db=x)

@@ -46,3 +46,4 @@ def pytest_collection_modifyitems(config, items):
 
 
 CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb"]
+DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr"]    # the downlink on (NRConfig(dl=True))

@@ -76,6 +76,28 @@ CASES = {
                                  harq_combining="none", eff_sinr="mean_db", frame_buffer=10, msg_sizes=(1200.0,),
                                  discard="pdcp_arrival", timeout_steps=4, cell_positions_m=((20.0, 30.0),)),
                         E=3, R=8, steps=30, kind="pose", arena=120.0, walk=1.0, rates=(1.3,), resets={9: [0, 2]}),
+    # downlink on (NRNet with DlMac): the RL-scale MAC with PF, Rician fading, CQI every 10 slots, two DL classes
+    "dl_c2": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", pf_window=100.0,
+                           n_harq=8, max_harq_tx=5, frame_buffer=16, msg_sizes=(200.0, 4000.0), fading_rho_per_ms=0.0,
+                           fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi",
+                           tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0, dl=True),
+                  E=4, R=8, steps=40, kind="pose", arena=200.0, walk=0.025, rates=(0.8, 0.1),
+                  dl_sizes=(6000.0, 30000.0), dl_rates=(0.6, 0.2), resets={20: [1]}),
+    # downlink with SNR input: correlated AR(1) fading, 38.214 CQI every 5 slots, K1 = 3, DL MCS cap, max C/I, RLC UM
+    # drop, small FIFOs (DL overflow), DL SNR offset
+    "dl_snr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                            harq_fail="drop", frame_buffer=6, msg_sizes=(3000.0,), timeout_steps=6,
+                            fading_rho_per_ms=0.9, dl=True, cqi_table="38214", cqi_period_slots=5, k1=3,
+                            dl_mcs_max=20, dl_snr_offset_db=6.0),
+                   E=3, R=8, steps=30, kind="snr", snr=(-4.0, 14.0), rates=(0.8,), dl_sizes=(9000.0, 1500.0),
+                   dl_rates=(0.9, 0.8), resets={17: [1]}),
+    # downlink with per-subband SNR: IR combining, no retransmission priority, round robin, PDCP discard, gNB
+    # processing 2 slots
+    "dl_ir_rr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,
+                              harq_combining="ir_lena", retx_priority=False, frame_buffer=8, msg_sizes=(2500.0,),
+                              discard="pdcp_arrival", timeout_steps=5, gnb_proc_slots=2, dl=True),
+                     E=3, R=8, steps=30, kind="snr3", snr=(-2.0, 16.0), rates=(0.7,), dl_sizes=(5000.0,),
+                     dl_rates=(1.1,), resets={11: [0, 2]}),
 }
 
 
@@ -145,6 +167,9 @@ def _inputs(name, c):
         x = rs.uniform(lo, hi, size=(T, E, R, 1)) + rs.normal(0.0, 2.0, size=(T, E, R, 13))
         x = x.astype(np.float32)
     assert counts.shape == (T, E, R, n_cls)
+    if "dl_rates" in c:
+        dl = np.stack([rs.poisson(lam, size=(T, E, R)) for lam in c["dl_rates"]], -1).astype(np.int64)
+        return x, counts, dl
     return x, counts
 
 
@@ -158,10 +183,14 @@ def run_case(name, c):
     cfg = NRConfig(**c["cfg"], seed=0)
     E, R, T = c["E"], c["R"], c["steps"]
     eng = make_engine("L2", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
-    x, counts = _inputs(name, c)
+    x, counts, *dl = _inputs(name, c)
+    dl_counts = dl[0] if dl else None
     out = {"x": x, "counts": counts, "E": np.int64(E), "R": np.int64(R), "steps": np.int64(T),
            "cfg_json": np.frombuffer(json.dumps(c["cfg"]).encode(), dtype=np.uint8),
            "kind": np.frombuffer(c["kind"].encode(), dtype=np.uint8)}
+    if dl_counts is not None:
+        out["dl_counts"] = dl_counts
+        out["dl_sizes"] = np.asarray(c["dl_sizes"], dtype=np.float32)
     reset_mask = np.zeros((T, E), dtype=np.bool_)
     for s, ids in c["resets"].items():
         reset_mask[s, ids] = True
@@ -201,6 +230,13 @@ def run_case(name, c):
         out[f"s{s:03d}/n_submit"] = np.int64(len(acc_all))
         if acc_all:
             out[f"s{s:03d}/accepted"] = np.stack(acc_all)
+        if dl_counts is not None:
+            # downlink arrivals: for each DL class in order, one add_dl_frames per message index (bytes, class)
+            for ci in range(dl_counts.shape[-1]):
+                n = torch.from_numpy(dl_counts[s, :, :, ci])
+                for i in range(int(n.max())):
+                    nb = torch.where(n > i, torch.full(n.shape, c["dl_sizes"][ci]), torch.zeros(n.shape))
+                    eng.add_dl_frames(None, nb, torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n)))
         xs = torch.from_numpy(x[s])
         if c["kind"] == "pose":
             o = eng.step(None, xs)

@@ -42,7 +42,7 @@ def test_numerology():
     # the RL-scale workload: 52 PRB -> 13 RBGs of 4, DDDSU at 25 ms -> 10 UL data slots and 10 SR opportunities
     c = P.NRConfig(mu=1, n_prb=52, control_step_ms=25.0)
     sched = c.schedule(0)
-    assert c.n_subbands == 13 and sum(1 for s in sched if s[1]) == 10 and sum(1 for s in sched if s[2]) == 10
+    assert c.n_subbands == 13 and sum(1 for s in sched if s[2]) == 10 and sum(1 for s in sched if s[3]) == 10
 
 
 def test_phy_tables_equal_reference_processing():
@@ -157,3 +157,24 @@ def test_breakpoint_distance():
     assert abs(CH.breakpoint_m("UMi", 3.5, 10.0, 1.5) - 210.0) < 1e-9
     with pytest.raises(ValueError):
         CH.breakpoint_m("UMi", 3.5, 10.0, 0.5)
+
+
+def test_cqi_tables_closed_form():
+    """38.214 CQI report (cqi_table="38214"): CQI -> MCS is the highest MCS of no larger spectral efficiency (CQI 1's
+    QPSK 78/1024 lies below MCS 0, CQI 7 = 16QAM 378 is MCS 11 of table 1, CQI 15 = 64QAM 948 is MCS 28, or the
+    cap); a CQI with an MCS of equal efficiency reports from that MCS's threshold, CQI 1 from MCS 0's shifted by the
+    Shannon-gap difference; the thresholds never decrease."""
+    import math
+    t = PH.PhyTables(1, max_tx=4)
+    thr, cm = PH.cqi_tables(t, 1)
+    assert cm.shape == (16,) and thr.shape == (15,)
+    assert cm[0] == 0 and cm[1] == 0 and cm[7] == 11 and cm[15] == 28
+    gap = lambda e: 10 * math.log10(2 ** e - 1)  # noqa: E731
+    assert abs(float(thr[0]) - (float(t.thr_ref[0]) + gap(2 * 78 / 1024) - gap(float(t.se[0])))) < 1e-5
+    assert float(thr[6]) == float(t.thr_ref[11])
+    assert (np.diff(thr) >= 0).all()
+    capped = PH.PhyTables(1, max_tx=4, mcs_cap=20)
+    assert PH.cqi_tables(capped, 1)[1][15] == 20
+    t2 = PH.PhyTables(2, max_tx=4)
+    thr2, cm2 = PH.cqi_tables(t2, 2)
+    assert cm2[15] == 27 and cm2[12] == 21      # 256QAM 948 is MCS 27 of table 2; 256QAM 711 is MCS 21

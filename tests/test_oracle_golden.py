@@ -7,13 +7,13 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import CASES, GOLDEN
+from conftest import CASES, DL_CASES, GOLDEN
 from oracle import nr_oracle as O
 from oracle import replay
 import isaac_net_amd as P
 
 
-@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES)
 def test_oracle_bitwise_vs_reference(name):
     torch.set_num_threads(1)
     d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
@@ -28,11 +28,11 @@ def test_oracle_bitwise_vs_reference(name):
         for k, v in o.items():
             if not np.array_equal(d[f"s{s:03d}/out.{k}"], v.numpy(), equal_nan=True):
                 bad.append((s, "out." + k))
-        valid = d[f"s{s:03d}/ul.q.cap"] >= 0
+        valid = {lk: d[f"s{s:03d}/{lk}.q.cap"] >= 0 for lk in ("ul", "dl") if f"s{s:03d}/{lk}.q.cap" in d.files}
         for k, v in eng.state().items():
             ref, mine = d[f"s{s:03d}/{k}"], v.numpy()
-            if k.startswith("ul.q.") and k != "ul.q.enq":
-                ref, mine = np.where(valid, ref, 0), np.where(valid, mine, 0)
+            if k[3:5] == "q." and k[5:] != "enq":
+                ref, mine = np.where(valid[k[:2]], ref, 0), np.where(valid[k[:2]], mine, 0)
             if not np.array_equal(ref, mine, equal_nan=True):
                 bad.append((s, k))
 
