@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 2
+#define INET_NR_ABI_VERSION 3
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
@@ -143,6 +143,32 @@ typedef struct InetNrOutputs {
     int64_t *t;                                  /* [E] int64 */
 } InetNrOutputs;
 
+/* The downlink of NRConfig(dl=True) (DlMac, isaac_net/core/mac_dl.py:19-49, on MacLink, mac.py:65-616): the DL
+   link's MAC state and frame queue (the same fields and layouts as the UL link's in InetNrState), its step outputs
+   and constants. The state both links share (fading h_re / h_im, Rician spectrum, RNG words, epoch, clock, radio
+   fields) stays in InetNrState: the DL step reads it and never writes it. */
+typedef struct InetNrDlState {
+    int32_t *sent, *floor_, *last_tx;   /* [E][R] */
+    float *olla, *avg;                  /* [E][R] */
+    int32_t *enq, *qlen;                /* [E][R] */
+    float *csi;                         /* [E][S][R] the gNB's estimate from the last CQI report (dB) */
+    uint32_t *h_meta;                   /* [E][P][R] state (0 free, 1 undecoded, 2 decoded awaiting HARQ-ACK) | ... */
+    int32_t *h_lo, *h_hi, *h_ready, *h_tbs;
+    float *h_comb, *h_lexp, *h_nrb;
+    int32_t *q_cap, *q_start, *q_end, *q_fin;   /* [E][F][R] */
+    uint32_t *q_meta;                   /* [E][F][R] lost | cls << 8 */
+    int32_t *newest;                    /* [E][R] capture step (engine clock, absolute) of the newest DL frame
+                                           delivered in the last step, -1 if none (NRNet.dl_newest) */
+    int64_t *ctr, *hist;                /* [E][INET_NR_NCTR], [E][3][max_tx + 1]: as InetNrState's, for the DL */
+    int64_t *out_newest, *out_queue_len;        /* [E][R] step outputs dl_newest (env clock) and dl_queue_len */
+    const float *cqi_thr;               /* [15] SINR from which CQI k + 1 is reported (cqi_table = "38214"), */
+    const int32_t *cqi_mcs;             /* [16] MCS of each CQI; both NULL for cqi_table = "mcs" */
+    int32_t gnb_proc;                   /* gNB processing slots after the HARQ-ACK */
+    int32_t snr_offset;                 /* 1: SNR input plus snr_off (dl_snr_offset_db); 0: the DL SNR as given */
+    float ref_off, noise_prb, snr_off;  /* pose input: dl_ref = (pg + ref_off) - noise_prb (gNB PSD, UE noise) */
+    int32_t pad;
+} InetNrDlState;
+
 /* Library version (INET_NR_ABI_VERSION) and a short build string. */
 int32_t inet_nr_abi_version(void);
 const char *inet_nr_build_info(void);
@@ -169,6 +195,30 @@ int32_t inet_nr_submit(const InetNrState *st, const InetNrParams *prm, int64_t T
    shadowing fields (tr38901: sf LOS, sf NLOS, LOS state; log_distance: shadow_dcorr_m), spectrum: 0 sos, 1 exp. */
 int32_t inet_nr_reset(const InetNrState *st, const InetNrParams *prm, const uint8_t *mask, int64_t T, float k_lin0,
                       const float *dcorr, int32_t spectrum, void *stream);
+
+/* The downlink part of control step T (NRNet.step / step_rx with dl=True, nr_engine.py:613-668: DlMac.cqi_report at
+   the CQI rows, MacLink.slot with the DlMac hooks at the DL data rows, and the DL half of _finish, nr_engine.py:866-
+   881). Launch it before inet_nr_step of the same step, on the same stream: both read the fading state and RNG words
+   of the step start, which inet_nr_step then advances. rows: the DL rows of the step (flags 1 CQI report, 2 DL data,
+   4 / 8 fading as for the UL rows, bits 8..23 the HARQ-ACK slot of the row relative to the step's first slot;
+   salt_bler = salt((BLER_DL << 16) | rel)). tab: the PHY tables with the DL MCS cap. x: as inet_nr_step's (poses,
+   SNR [E][R] or per-subband SNR [E][R][S]; with SNR, dl->snr_offset says whether dl_snr_offset_db is added).
+   No counterpart launch in the reference's triton backend: there the DL runs inside its one fused kernel
+   (nr_triton.py:938-989, the DL flag of _mac_slot). */
+int32_t inet_nr_dl_step(const InetNrState *st, const InetNrDlState *dl, const InetNrTables *tab,
+                        const InetNrParams *prm, const InetNrRow *rows, int32_t n_rows, int64_t T, const float *x,
+                        void *stream);
+
+/* Enqueue one DL frame per robot at control step T (T < 0: *st->clock): NRNet.add_dl_frames (nr_engine.py:489-497)
+   with FrameQueue.add (queues.py:87-103). nbytes [E][R] float32 application bytes (0 = none), cls [E][R] int64 or
+   NULL (the slot then keeps the class it held, as the reference's meta field); accepted [E][R] uint8. */
+int32_t inet_nr_dl_submit(const InetNrState *st, const InetNrDlState *dl, const InetNrParams *prm, int64_t T,
+                          const float *nbytes, const int64_t *cls, int32_t discard_pdcp, int32_t pkt_payload,
+                          int32_t pkt_overhead, uint8_t *accepted, void *stream);
+
+/* Reset the DL link of the envs of mask [E] uint8 (NULL = every env, which also clears the DL counters):
+   MacLink.reset / FrameQueue.reset of NRNet.dl and dl_newest (nr_engine.py:256-274). */
+int32_t inet_nr_dl_reset(const InetNrDlState *dl, const InetNrParams *prm, const uint8_t *mask, void *stream);
 
 #ifdef __cplusplus
 }

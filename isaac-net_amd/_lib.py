@@ -43,6 +43,15 @@ class InetNrOutputs(C.Structure):
                                  "newest", "queue_len", "serving_cell", "queue_bytes", "sinr_db", "det_env", "t")]
 
 
+class InetNrDlState(C.Structure):
+    _fields_ = [(n, P) for n in (
+        "sent", "floor_", "last_tx", "olla", "avg", "enq", "qlen", "csi", "h_meta", "h_lo", "h_hi", "h_ready", "h_tbs",
+        "h_comb", "h_lexp", "h_nrb", "q_cap", "q_start", "q_end", "q_fin", "q_meta", "newest", "ctr", "hist",
+        "out_newest", "out_queue_len", "cqi_thr", "cqi_mcs")] + \
+               [("gnb_proc", i32), ("snr_offset", i32), ("ref_off", f32), ("noise_prb", f32), ("snr_off", f32),
+                ("pad", i32)]
+
+
 class InetWifiState(C.Structure):
     _fields_ = [(n, P) for n in (
         "cap", "cls", "det", "hid", "rem", "f_nact", "f_snr", "f_own", "qlen", "last_snr", "roam_left", "serv",
@@ -90,7 +99,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 WIFI_ABI_VERSION = 2
 _LIB = None
 
@@ -114,6 +123,14 @@ def load(path=LIB_PATH):
     lib.inet_nr_reset.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), P, i64, f32, C.POINTER(f32), i32,
                                   P]
     lib.inet_nr_reset.restype = i32
+    lib.inet_nr_dl_step.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrDlState), C.POINTER(InetNrTables),
+                                    C.POINTER(InetNrParams), P, i32, i64, P, P]
+    lib.inet_nr_dl_step.restype = i32
+    lib.inet_nr_dl_submit.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrDlState), C.POINTER(InetNrParams), i64,
+                                      P, P, i32, i32, i32, P, P]
+    lib.inet_nr_dl_submit.restype = i32
+    lib.inet_nr_dl_reset.argtypes = [C.POINTER(InetNrDlState), C.POINTER(InetNrParams), P, P]
+    lib.inet_nr_dl_reset.restype = i32
     lib.inet_wifi_abi_version.restype = i32
     lib.inet_wifi_step.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, i32, P, P,
                                    C.POINTER(InetWifiOutputs), P]

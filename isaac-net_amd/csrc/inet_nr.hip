@@ -70,6 +70,68 @@ __global__ void nr_submit_kernel(InetNrState st, int E, int R, int F, int64_t T_
     st.enq[i] = enq;
 }
 
+// ======================================================================================= DL submit kernel
+// NRNet.add_dl_frames (nr_engine.py:489-497) with FrameQueue.add (queues.py:87-103): one DL frame of nbytes at the
+// tail. The class is a meta field that add does not reset: without cls the slot keeps the class it held.
+__global__ void nr_dl_submit_kernel(InetNrState st, InetNrDlState dl, int E, int R, int F, int64_t T_arg,
+                                    const float* __restrict__ nbytes, const int64_t* __restrict__ cls,
+                                    int discard_pdcp, int timeout, int pkt_payload, int pkt_overhead,
+                                    uint8_t* __restrict__ accepted) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= E * R) return;
+    const int T = (int)(T_arg >= 0 ? T_arg : st.clock[0]);
+    const int e = i / R, r = i - e * R;
+    int qlen = dl.qlen[i];
+    const int enq = dl.enq[i];
+    float size = nbytes[i];
+    bool adm = size > 0.0f;
+    if (discard_pdcp && qlen > 0) {
+        int cap0 = dl.q_cap[((size_t)e * F + 0) * R + r];
+        if (T - cap0 >= timeout) adm = false;
+    }
+    if (pkt_overhead) size = size + ceilf(size / (float)pkt_payload) * (float)pkt_overhead;
+    const bool acc = adm && qlen < F && size > 0.0f;
+    if (acc) {
+        const int nb = (int)rintf(size);
+        const size_t iq = ((size_t)e * F + qlen) * R + r;
+        dl.q_cap[iq] = T; dl.q_start[iq] = enq; dl.q_end[iq] = enq + nb; dl.q_fin[iq] = FIN_NONE;
+        const uint32_t c = cls ? ((uint32_t)cls[i] & 0xffu) << 8 : dl.q_meta[iq] & 0xff00u;
+        dl.q_meta[iq] = c;
+        dl.enq[i] = enq + nb;
+        dl.qlen[i] = qlen + 1;
+    }
+    accepted[i] = acc;
+}
+
+// ======================================================================================= DL reset kernel
+// MacLink.reset / FrameQueue.reset of NRNet.dl and dl_newest = -1 (nr_engine.py:256-274) for the envs of the mask;
+// a full reset (mask NULL) also clears the DL counters.
+__global__ void nr_dl_reset_kernel(InetNrDlState dl, InetNrParams pm, const uint8_t* __restrict__ mask, int full) {
+    const int e = blockIdx.x;
+    if (e >= pm.E) return;
+    if (!full && !mask[e]) return;
+    const int R = pm.R, S = pm.S, P = pm.P, F = pm.F;
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        size_t ir = (size_t)e * R + r;
+        dl.sent[ir] = 0; dl.floor_[ir] = 0; dl.last_tx[ir] = -1; dl.olla[ir] = 0.f; dl.avg[ir] = 100.f;
+        dl.enq[ir] = 0; dl.qlen[ir] = 0; dl.newest[ir] = -1;
+        for (int s = 0; s < S; ++s) dl.csi[((size_t)e * S + s) * R + r] = 0.f;
+        for (int p = 0; p < P; ++p) {
+            size_t ip = ((size_t)e * P + p) * R + r;
+            dl.h_meta[ip] = 0u; dl.h_lo[ip] = 0; dl.h_hi[ip] = 0; dl.h_ready[ip] = 0; dl.h_tbs[ip] = 0;
+            dl.h_comb[ip] = 0.f; dl.h_lexp[ip] = -INFINITY; dl.h_nrb[ip] = 0.f;
+        }
+        for (int f = 0; f < F; ++f) {
+            size_t iq = ((size_t)e * F + f) * R + r;
+            dl.q_cap[iq] = -1; dl.q_start[iq] = 0; dl.q_end[iq] = 0; dl.q_fin[iq] = FIN_NONE; dl.q_meta[iq] = 0u;
+        }
+    }
+    if (full && threadIdx.x == 0) {
+        for (int q = 0; q < INET_NR_NCTR; ++q) dl.ctr[(size_t)e * INET_NR_NCTR + q] = 0;
+        for (int q = 0; q < 3 * (pm.max_tx + 1); ++q) dl.hist[(size_t)e * 3 * (pm.max_tx + 1) + q] = 0;
+    }
+}
+
 // ======================================================================================= reset kernel
 // One block per env. NRNet.reset / MacLink.reset / FrameQueue.reset / NRRng.reset_mask and the reset draws: H0 of
 // the fading state, the Rician phase (KPHI) and the radio's plane-wave fields (channels/fields.py:38-58,
@@ -142,21 +204,10 @@ namespace {
 
 int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
 
-}  // namespace
-
-extern "C" {
-
-int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
-
-const char* inet_nr_build_info(void) {
-    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, one wave64 per workgroup, "
-           "DPP segment reductions, ATen-order sums";
-}
-
-int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,
-                     int32_t n_rows, int64_t T, const float* x, const int64_t* cur_hid, const InetNrOutputs* out,
-                     void* stream) {
-    if (!st || !tab || !prm || !out || !x) return INET_NR_EINVAL;
+// the argument checks and the launch of one step kernel (UL: dl NULL)
+int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
+                           const InetNrParams* prm, const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x,
+                           const int64_t* cur_hid, const InetNrOutputs* out, void* stream) {
     const InetNrParams& p = *prm;
     const InetNrTables& t = *tab;
     if (p.E <= 0 || p.R <= 0 || p.R > INET_NR_MAX_R || p.F <= 0 || p.N <= 0) return INET_NR_EINVAL;
@@ -173,10 +224,60 @@ int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetN
                     : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = inet::STEP_WAVE / rb;
-    inet::StepArgs a{*st, t, p, rows, n_rows, T, x, cur_hid, *out, rb,
+    inet::StepArgs a{*st, dl, t, p, rows, n_rows, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
                      inet::step_lds_bytes(n_rows, p.harq_drop, rb, p.max_tx), (hipStream_t)stream};
     fn(a);
+    return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
+
+const char* inet_nr_build_info(void) {
+    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, one wave64 per workgroup, "
+           "DPP segment reductions, ATen-order sums";
+}
+
+int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,
+                     int32_t n_rows, int64_t T, const float* x, const int64_t* cur_hid, const InetNrOutputs* out,
+                     void* stream) {
+    if (!st || !tab || !prm || !out || !x) return INET_NR_EINVAL;
+    return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, stream);
+}
+
+int32_t inet_nr_dl_step(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
+                        const InetNrParams* prm, const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x,
+                        void* stream) {
+    if (!st || !dl || !tab || !prm || !x) return INET_NR_EINVAL;
+    if (!dl->sent || !dl->q_cap || !dl->newest || !dl->out_newest || !dl->out_queue_len || !dl->ctr || !dl->hist)
+        return INET_NR_EINVAL;
+    if ((dl->cqi_thr == nullptr) != (dl->cqi_mcs == nullptr) || dl->gnb_proc < 0) return INET_NR_EINVAL;
+    InetNrOutputs none{};
+    return launch_step_kernel(st, dl, tab, prm, rows, n_rows, T, x, nullptr, &none, stream);
+}
+
+int32_t inet_nr_dl_submit(const InetNrState* st, const InetNrDlState* dl, const InetNrParams* prm, int64_t T,
+                          const float* nbytes, const int64_t* cls, int32_t discard_pdcp, int32_t pkt_payload,
+                          int32_t pkt_overhead, uint8_t* accepted, void* stream) {
+    if (!st || !dl || !prm || !nbytes || !accepted) return INET_NR_EINVAL;
+    if ((T < 0 && !st->clock) || T > 0x7fffffff || (pkt_overhead && pkt_payload <= 0)) return INET_NR_EINVAL;
+    const InetNrParams& p = *prm;
+    if (p.E <= 0 || p.R <= 0 || p.F <= 0) return INET_NR_EINVAL;
+    int n = p.E * p.R;
+    hipLaunchKernelGGL(nr_dl_submit_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, *st, *dl, p.E,
+                       p.R, p.F, T, nbytes, cls, discard_pdcp, p.timeout, pkt_payload, pkt_overhead, accepted);
+    return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
+}
+
+int32_t inet_nr_dl_reset(const InetNrDlState* dl, const InetNrParams* prm, const uint8_t* mask, void* stream) {
+    if (!dl || !prm) return INET_NR_EINVAL;
+    const InetNrParams& p = *prm;
+    if (p.E <= 0 || p.R <= 0 || p.S > INET_NR_MAX_S || p.P > INET_NR_MAX_P) return INET_NR_EINVAL;
+    hipLaunchKernelGGL(nr_dl_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *dl, p, mask, mask ? 0 : 1);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }
 

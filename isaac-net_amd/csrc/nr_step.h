@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/inet_nr.h"
 #include "inet_nr_dev.h"
 
@@ -208,12 +210,16 @@ inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
                           (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1));
 }
 
-// RBT: the segment width when it is fixed at compile time (0: the runtime argument rb)
-template <int S, int P, bool IR, bool VREF, int RBT>
+// RBT: the segment width when it is fixed at compile time (0: the runtime argument rb).
+// LS: the link whose MAC state and queue the kernel runs: InetNrState (the UL; lk is st) or InetNrDlState (the DL
+// of NRConfig(dl=True): CQI reports and DL data slots with the DlMac hooks; it reads the shared state of st and writes
+// only the DL link's).
+template <int S, int P, bool IR, bool VREF, int RBT, class LS>
 __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
-    InetNrState st, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows, int64_t T_arg,
-    const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
+    InetNrState st, LS lk, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows,
+    int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max) {
+    constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     const int rb = RBT ? RBT : rb_arg;
     const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
     extern __shared__ int dyn[];
@@ -281,14 +287,15 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     float hcomb[P], hlexp[IR ? P : 1], hnrb[IR ? P : 1];
     const bool read_h = pm.fading && !(n_rows > 0 && (rows[0].flags & 4) && rows[0].rho == 0.0f);
     // (lanes without a robot read a clamped, valid address and discard the value: the loads are branch-free)
-    sent = ldo(st.sent, o_r); floor_ = ldo(st.floor_, o_r); bsr = ldo(st.bsr, o_r); sr_t = ldo(st.sr_t, o_r);
-    last_tx = ldo(st.last_tx, o_r); enq = ldo(st.enq, o_r); qlen = ldo(st.qlen, o_r);
-    olla = ldo(st.olla, o_r); avg = ldo(st.avg, o_r);
+    sent = ldo(lk.sent, o_r); floor_ = ldo(lk.floor_, o_r);
+    if constexpr (!DL) { bsr = ldo(st.bsr, o_r); sr_t = ldo(st.sr_t, o_r); }
+    last_tx = ldo(lk.last_tx, o_r); enq = ldo(lk.enq, o_r); qlen = ldo(lk.qlen, o_r);
+    olla = ldo(lk.olla, o_r); avg = ldo(lk.avg, o_r);
     qlen = qlen < 0 ? 0 : (qlen > F ? F : qlen);
     if (!act) { sent = 0; floor_ = 0; bsr = 0; sr_t = -1; last_tx = -1; enq = 0; qlen = 0; olla = 0.f; avg = 100.f; }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        csi[s] = ldo(st.csi + s * R, o_sr);
+        csi[s] = ldo(lk.csi + s * R, o_sr);
         hr[s] = 0.f; hi[s] = 0.f;
         if (read_h) { hr[s] = ldo(st.h_re + s * R, o_sr); hi[s] = ldo(st.h_im + s * R, o_sr); }
         if (!act) { csi[s] = 0.f; hr[s] = 0.f; hi[s] = 0.f; }
@@ -296,9 +303,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const int pr = p * R;
-        hmeta[p] = ldo(st.h_meta + pr, o_pr); hlo[p] = ldo(st.h_lo + pr, o_pr); hhi[p] = ldo(st.h_hi + pr, o_pr);
-        hrdy[p] = ldo(st.h_ready + pr, o_pr); htbs[p] = ldo(st.h_tbs + pr, o_pr); hcomb[p] = ldo(st.h_comb + pr, o_pr);
-        if constexpr (IR) { hlexp[p] = ldo(st.h_lexp + pr, o_pr); hnrb[p] = ldo(st.h_nrb + pr, o_pr); }
+        hmeta[p] = ldo(lk.h_meta + pr, o_pr); hlo[p] = ldo(lk.h_lo + pr, o_pr); hhi[p] = ldo(lk.h_hi + pr, o_pr);
+        hrdy[p] = ldo(lk.h_ready + pr, o_pr); htbs[p] = ldo(lk.h_tbs + pr, o_pr); hcomb[p] = ldo(lk.h_comb + pr, o_pr);
+        if constexpr (IR) { hlexp[p] = ldo(lk.h_lexp + pr, o_pr); hnrb[p] = ldo(lk.h_nrb + pr, o_pr); }
         if (!act) {
             hmeta[p] = 0u; hlo[p] = 0; hhi[p] = 0; hrdy[p] = 0; htbs[p] = 0; hcomb[p] = 0.f;
             if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
@@ -311,27 +318,35 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const float ka = sqrtf(kk * kinv), kb = sqrtf(kinv);
 
     // ---------------- inputs: SINR reference per subband and the reported SNR ----------------
+    // the DL reference SINR per PRB (NRNet.step_rx / step, nr_engine.py:624-631, 651-653): with poses the gNB PSD
+    // over the reciprocal path gain against the UE noise; with SNR input the input plus dl_snr_offset_db (or the DL
+    // SNR as given)
     float ref[VREF ? S : 1];
     float snr_out = 0.f;
     if constexpr (VREF) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) ref[s] = act ? ldo(xin + s, o_r * S) : 0.f;
-        snr_out = aten_sum<S>(ref) / (float)S;
+        for (int s = 0; s < S; ++s) {
+            ref[s] = act ? ldo(xin + s, o_r * S) : 0.f;
+            if constexpr (DL) ref[s] = lk.snr_offset ? ref[s] + lk.snr_off : ref[s];
+        }
+        if constexpr (!DL) snr_out = aten_sum<S>(ref) / (float)S;
     } else if (pm.input_kind == 1) {
         ref[0] = act ? ldo(xin, o_r) : 0.f;
+        if constexpr (DL) ref[0] = lk.snr_offset ? ref[0] + lk.snr_off : ref[0];
         snr_out = ref[0];
     } else {                                       // poses -> path gain (radio prologue)
         float px = 0.f, py = 0.f;
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
         const float rx = radio_rx_dbm(pm, px, py, st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3);
         const float pg = rx - pm.ue_tx;
-        ref[0] = (pg + pm.ref_off) - pm.noise_prb;
+        if constexpr (DL) ref[0] = (pg + lk.ref_off) - lk.noise_prb;
+        else ref[0] = (pg + pm.ref_off) - pm.noise_prb;
         snr_out = (pg + pm.ue_tx) - pm.subband_noise;
     }
     auto REF = [&](int s) -> float { return VREF ? ref[s] : ref[0]; };
     // PHR cap n_max (mac_ul.py:165-168): ref.mean(-1) -> snr_ref_prbs 10^((ref - phr_min) / 10) / w0
     int n_max = S;
-    if (pm.phr_cap) {
+    if (!DL && pm.phr_cap) {
         float rr[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) rr[s] = REF(s);
@@ -393,7 +408,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 #pragma unroll
             for (int p = 0; p < P; ++p) busy |= hm_state(hmeta[p]) == 1;
             busy |= (enq - sent) > 0;
-            const bool full = !iid || k == last_ul_row || k == last_h_row;
+            // (the DL draws every robot's gain at its CQI rows, which set the CSI of every robot)
+            const bool full = !iid || (DL ? (row.flags & 1) != 0 : (k == last_ul_row || k == last_h_row));
             const bool draw = act && (full || busy);
             const unsigned long long need = __ballot(draw);
             float* const s_z = s_x;
@@ -425,15 +441,59 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 }
             }
         }
-        if (row.flags & 1) {                       // SR opportunity (UlMac.sr_step, lumped)
-            if ((enq - sent) > 0 && bsr <= 0 && sr_t < 0) sr_t = g;
+        // fading gain (dB) of subband s in this slot (nr_engine.py:602-611)
+        auto gain_of = [&](int s) -> float {
+            float gs = 0.f;
+            if (pm.fading) {
+                float p;
+                if (pm.rician) {
+                    float xr = ka * sp_re + kb * hr[s];
+                    float xi = ka * sp_im + kb * hi[s];
+                    p = xr * xr + xi * xi;
+                } else {
+                    p = hr[s] * hr[s] + hi[s] * hi[s];
+                }
+                gs = 10.0f * log10f(clamp_min(p, 1e-6f));
+            }
+            return gs;
+        };
+        if constexpr (DL) {
+            if (row.flags & 1) {                   // CQI report (DlMac.cqi_report, mac_dl.py:30-40)
+                // per subband the best MCS at ref + gain (mcs_at: the highest m <= mcs_max with x >= thr_ref[m], else
+                // 0), or the 38.214 CQI mapped back to an MCS; the gNB keeps that MCS's threshold as its estimate
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float x = REF(s) + gain_of(s);
+                    int m = 0;
+                    if (lk.cqi_thr) {
+                        int q = 0;
+                        for (int j = 0; j < 15; ++j) q += x >= lk.cqi_thr[j] ? 1 : 0;
+                        m = lk.cqi_mcs[q];
+                    } else {
+                        for (int j = 0; j <= tb.mcs_max; ++j) m = x >= s_thr[j] ? j : m;
+                    }
+                    csi[s] = s_thr[m] - REF(s);
+                }
+            }
+        } else {
+            if (row.flags & 1) {                   // SR opportunity (UlMac.sr_step, lumped)
+                if ((enq - sent) > 0 && bsr <= 0 && sr_t < 0) sr_t = g;
+            }
         }
         if (!(row.flags & 2)) continue;
-        // ============================ UL data slot (MacLink.slot) ============================
+        // ============================ data slot (MacLink.slot) ============================
         const int unsent = enq - sent;
-        // grants (UlMac._pre_slot_lumped)
-        if (row.flags & 16) bsr = bsr > 1 ? bsr : 1;
-        if (sr_t >= 0 && g - sr_t >= pm.sr_delay) { bsr = bsr > 1 ? bsr : 1; sr_t = -1; }
+        if constexpr (DL) {
+            // DL processes whose HARQ-ACK has reached the gNB become free (mac.py:243)
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                if (hm_state(hmeta[p]) == 2 && hrdy[p] <= g)
+                    hmeta[p] = hm_pack(0, hm_ntx(hmeta[p]), hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
+        } else {
+            // grants (UlMac._pre_slot_lumped)
+            if (row.flags & 16) bsr = bsr > 1 ? bsr : 1;
+            if (sr_t >= 0 && g - sr_t >= pm.sr_delay) { bsr = bsr > 1 ? bsr : 1; sr_t = -1; }
+        }
         // candidates: the retransmission ready first (lowest ready slot, then lowest process), the lowest free process
         int rx_p = 0, p_new = 0;
         int best_rdy = 0x7fffffff;
@@ -445,7 +505,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             if (stp == 0) { any_free = true; p_new = p; }
             if (stp == 1) pending = true;
         }
-        const int need = bsr < unsent ? bsr : unsent;
+        const int need = DL ? unsent : (bsr < unsent ? bsr : unsent);
         bool new_el = any_free && need > 0 && !has_rx && act;
         has_rx = has_rx && act;
         int rx_nsb = 0;
@@ -459,7 +519,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             int mi[S];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                float est = (REF(s) - s_wdb[s]) + csi[s];
+                // UL: the PSD over one RBG (mac_ul.py:154-171); DL: sinr_ref + csi (mac_dl.py:42-43)
+                float est = DL ? REF(s) + csi[s] : (REF(s) - s_wdb[s]) + csi[s];
                 eo[s] = pm.olla ? est + olla : est;
                 mi[s] = 0;
             }
@@ -581,7 +642,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             bool nan = false;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                float x = (REF(s) - sp) + csi[s];
+                float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
                 nan |= x != x;
                 s_x[s * STEP_WAVE + lane] = x;
             }
@@ -675,22 +736,12 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         }
         mcs = mcs < tb.M ? mcs : tb.M - 1;
         if (tx_new) sent = sent + byt_new;
-        // ---- actual channel of this slot: fading gain per subband -> CSI (mac_ul.py:229-236) ----
+        // ---- actual channel of this slot: fading gain per subband; in the UL it becomes the CSI (mac_ul.py:229-236)
+        float gn[DL ? S : 1];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            float gs = 0.f;
-            if (pm.fading) {
-                float p;
-                if (pm.rician) {
-                    float xr = ka * sp_re + kb * hr[s];
-                    float xi = ka * sp_im + kb * hi[s];
-                    p = xr * xr + xi * xi;
-                } else {
-                    p = hr[s] * hr[s] + hi[s] * hi[s];
-                }
-                gs = 10.0f * log10f(clamp_min(p, 1e-6f));
-            }
-            csi[s] = gs;
+            if constexpr (DL) gn[s] = gain_of(s);
+            else csi[s] = gain_of(s);
         }
         // ---- decoding on the actual channel (mac.py:428-454, mac_ul.py:185-192) ----
         bool ok = false, fail = false, exh = false;
@@ -700,7 +751,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             bool nan = false;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                float x = (REF(s) - sp) + csi[s];
+                float x;                          // UL: ref - split + gain (mac_ul.py:185-192); DL: ref + gain
+                if constexpr (DL) x = REF(s) + gn[s];
+                else x = (REF(s) - sp) + csi[s];
                 nan |= x != x;
                 s_x[s * STEP_WAVE + lane] = x;
             }
@@ -744,16 +797,23 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             fail = tx && !ok;
             exh = fail && ntx >= pm.max_tx;
         }
-        // ---- HARQ state update (mac.py:456-477, mac_ul.py:218-219) ----
+        // ---- HARQ state update (mac.py:456-477; UL timing mac_ul.py:218-219, DL mac_dl.py:47-49: decoded TBs wait
+        // for their HARQ-ACK at the row's ACK slot, and both outcomes are known gnb_proc slots after it) ----
+        int rdy_ok = g, rdy_fail = g + pm.ul_rtt, st_ok = 0;
+        if constexpr (DL) {
+            rdy_ok = g0 + ((row.flags >> 8) & 0xffff) + lk.gnb_proc;
+            rdy_fail = rdy_ok;
+            st_ok = 2;
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             if (p == p_tx && tx) {
                 int stp = hm_state(hmeta[p]);
                 int ntxp = ntx;
-                if (ok) { stp = 0; hrdy[p] = g; }
+                if (ok) { stp = st_ok; hrdy[p] = rdy_ok; }
                 hcomb[p] = comb;
                 if constexpr (IR) { hlexp[p] = lexp; hnrb[p] = nrb; }
-                if (fail) hrdy[p] = g + pm.ul_rtt;
+                if (fail) hrdy[p] = rdy_fail;
                 if (exh) {
                     if (pm.harq_drop) stp = 0;
                     else {
@@ -769,7 +829,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         if (pm.olla) olla = clampf((olla + pm.olla_up * (ok ? 1.0f : 0.0f)) - pm.olla_dn * (fail ? 1.0f : 0.0f),
                                    -10.0f, 10.0f);
         const int served = ok ? hi_tx - lo_tx : 0;
-        if (tx) bsr = enq - sent;
+        if (!DL && tx) bsr = enq - sent;
         avg = clamp_min(pm.pf_a * avg + pm.pf_b * (float)served, 1e-9f);
         if (pm.sched == 2 && tx) last_tx = g;
         // ---- counters ----
@@ -808,9 +868,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const int qv = act ? qlen : 0;                     // queued frames of this robot (a prefix of the FIFO)
     for (int f = 0; f < qv; ++f) {
         const int fr = f * R;
-        const int cap = ldo(st.q_cap + fr, o_fr), qs = ldo(st.q_start + fr, o_fr), qe = ldo(st.q_end + fr, o_fr);
-        int fin = ldo(st.q_fin + fr, o_fr);
-        const uint32_t meta = ldo(st.q_meta + fr, o_fr);
+        const int cap = ldo(lk.q_cap + fr, o_fr), qs = ldo(lk.q_start + fr, o_fr), qe = ldo(lk.q_end + fr, o_fr);
+        int fin = ldo(lk.q_fin + fr, o_fr);
+        const uint32_t meta = ldo(lk.q_meta + fr, o_fr);
         bool lost = meta & 1u;
         // replay the slots: lost marking (RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
         for (int j = 0; j < n_hist; ++j) {
@@ -835,11 +895,14 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         if (delivered) {
             delay = (float)(fin_d - (double)cap);
             newest = cap > newest ? cap : newest;
-            if ((meta & 2u) && ldo(st.q_hid + fr, o_fr) == (int32_t)hid_cur) det_hit = true;
+            if constexpr (!DL)
+                if ((meta & 2u) && ldo(st.q_hid + fr, o_fr) == (int32_t)hid_cur) det_hit = true;
         }
         const int cap_rel = cap >= 0 ? cap - ep0 : -1;
         const int cls = (int)((meta >> 8) & 0xffu);
-        if (pm.out_ref) {
+        if (DL) {
+            // the DL reports no per-frame outputs (nr_engine.py:866-881)
+        } else if (pm.out_ref) {
             sto(out.delivered + f, ob, (uint8_t)delivered);
             sto(out.timed_out + f, ob, (uint8_t)timed);
             sto(out.dropped + f, ob, (uint8_t)dropped);
@@ -850,26 +913,26 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             sto(out.cap32 + f, ob * 4u, (int32_t)cap_rel);
             sto(out.cls8 + f, ob, (uint8_t)cls);
         }
-        sto(out.delay + f, ob * 4u, delay);
+        if constexpr (!DL) sto(out.delay + f, ob * 4u, delay);
         // compaction: the frames that stay move to the front, in order (queues.py:105-110)
         if (!(delivered || timed || dropped)) {
             if (kept == 0) new_floor = qs;
             if (kept != f) {
                 const int kr = kept * R;
-                sto(st.q_cap + kr, o_fr, cap); sto(st.q_start + kr, o_fr, qs); sto(st.q_end + kr, o_fr, qe);
-                sto(st.q_meta + kr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
-                sto(st.q_hid + kr, o_fr, ldo(st.q_hid + fr, o_fr));
-                sto(st.q_fin + kr, o_fr, fin);
+                sto(lk.q_cap + kr, o_fr, cap); sto(lk.q_start + kr, o_fr, qs); sto(lk.q_end + kr, o_fr, qe);
+                sto(lk.q_meta + kr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
+                if constexpr (!DL) sto(st.q_hid + kr, o_fr, ldo(st.q_hid + fr, o_fr));
+                sto(lk.q_fin + kr, o_fr, fin);
             } else {
-                sto(st.q_meta + fr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
-                sto(st.q_fin + fr, o_fr, fin);
+                sto(lk.q_meta + fr, o_fr, (meta & ~1u) | (lost ? 1u : 0u));
+                sto(lk.q_fin + fr, o_fr, fin);
             }
             ++kept;
         }
     }
     // the slots past the queue get the outputs of an empty slot (not delivered / timed out / dropped, cap -1,
     // class 0, delay NaN): one frame at a time up to a multiple of 4, then 16-byte stores of 4 frames per array
-    if (act) {
+    if (!DL && act) {
         const bool vec = (F & 3) == 0;
         const int fa = vec ? ((qv + 3) & ~3) : F;
         const uint32_t qnan = 0x7fc00000u;
@@ -902,7 +965,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         }
     }
     if (act) {
-        for (int f = kept; f < qlen; ++f) sto(st.q_cap + f * R, o_fr, -1);
+        for (int f = kept; f < qlen; ++f) sto(lk.q_cap + f * R, o_fr, -1);
     }
     // compact(): floor, sent, dead processes, BSR (mac.py:610-616, mac_ul.py:255-257)
     floor_ = new_floor;
@@ -915,7 +978,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
         }
     }
-    {
+    if constexpr (!DL) {
         int un = enq - sent;
         bsr = bsr < un ? bsr : un;
     }
@@ -927,26 +990,35 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         uint32_t o_r = o_r0, o_sr = o_sr0, o_pr = o_pr0;
         asm volatile("" : "+v"(o_r), "+v"(o_sr), "+v"(o_pr));
     if (act) {
-        sto(st.sent, o_r, sent); sto(st.floor_, o_r, floor_); sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
-        sto(st.last_tx, o_r, last_tx); sto(st.qlen, o_r, kept); sto(st.olla, o_r, olla); sto(st.avg, o_r, avg);
+        sto(lk.sent, o_r, sent); sto(lk.floor_, o_r, floor_);
+        if constexpr (!DL) { sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t); }
+        sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            sto(st.csi + s * R, o_sr, csi[s]);
-            if (pm.fading) { sto(st.h_re + s * R, o_sr, hr[s]); sto(st.h_im + s * R, o_sr, hi[s]); }
+            sto(lk.csi + s * R, o_sr, csi[s]);
+            if constexpr (!DL)
+                if (pm.fading) { sto(st.h_re + s * R, o_sr, hr[s]); sto(st.h_im + s * R, o_sr, hi[s]); }
         }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int pr = p * R;
-            sto(st.h_meta + pr, o_pr, hmeta[p]); sto(st.h_lo + pr, o_pr, hlo[p]); sto(st.h_hi + pr, o_pr, hhi[p]);
-            sto(st.h_ready + pr, o_pr, hrdy[p]); sto(st.h_tbs + pr, o_pr, htbs[p]); sto(st.h_comb + pr, o_pr, hcomb[p]);
-            if constexpr (IR) { sto(st.h_lexp + pr, o_pr, hlexp[p]); sto(st.h_nrb + pr, o_pr, hnrb[p]); }
+            sto(lk.h_meta + pr, o_pr, hmeta[p]); sto(lk.h_lo + pr, o_pr, hlo[p]); sto(lk.h_hi + pr, o_pr, hhi[p]);
+            sto(lk.h_ready + pr, o_pr, hrdy[p]); sto(lk.h_tbs + pr, o_pr, htbs[p]); sto(lk.h_comb + pr, o_pr, hcomb[p]);
+            if constexpr (IR) { sto(lk.h_lexp + pr, o_pr, hlexp[p]); sto(lk.h_nrb + pr, o_pr, hnrb[p]); }
         }
-        sto(out.newest, o_r * 2u, (int64_t)(newest >= 0 ? newest - ep0 : -1));
-        sto(out.queue_len, o_r * 2u, (int64_t)kept);
-        int qb = enq - ack_new;
-        sto(out.queue_bytes, o_r, (float)(qb > 0 ? qb : 0));
-        sto(out.sinr_db, o_r, snr_out);
-        if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)0);
+        if constexpr (DL) {
+            // NRNet.dl_newest (absolute) and the step outputs dl_newest (env clock) and dl_queue_len
+            sto(lk.newest, o_r, newest);
+            sto(lk.out_newest, o_r * 2u, (int64_t)(newest >= 0 ? newest - ep0 : -1));
+            sto(lk.out_queue_len, o_r * 2u, (int64_t)kept);
+        } else {
+            sto(out.newest, o_r * 2u, (int64_t)(newest >= 0 ? newest - ep0 : -1));
+            sto(out.queue_len, o_r * 2u, (int64_t)kept);
+            int qb = enq - ack_new;
+            sto(out.queue_bytes, o_r, (float)(qb > 0 ? qb : 0));
+            sto(out.sinr_db, o_r, snr_out);
+            if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)0);
+        }
     }
     }
     // per-env outputs and counters (segment reductions, written by robot 0)
@@ -958,23 +1030,26 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const int v_bnew = bsum(act ? c_bytes_new : 0, rb), v_prb = bsum(act ? c_prb : 0, rb);
     __syncthreads();                                  // histogram atomics of every lane are done
     if (r == 0 && e < E) {
-        out.det_env[e] = det_any;
-        out.t[e] = (int64_t)t - (int64_t)st.epoch[e];
-        st.ctr_step[e] = st.ctr_step[e] + 1;          // rng.tick_step (nr_engine.py:847-848)
-        int64_t* c = st.ctr + (size_t)e * INET_NR_NCTR;
+        if constexpr (!DL) {
+            out.det_env[e] = det_any;
+            out.t[e] = (int64_t)t - (int64_t)st.epoch[e];
+            st.ctr_step[e] = st.ctr_step[e] + 1;      // rng.tick_step (nr_engine.py:847-848)
+        }
+        int64_t* c = lk.ctr + (size_t)e * INET_NR_NCTR;
         c[0] += v_new; c[1] += v_retx; c[2] += v_ok; c[3] += v_fail; c[4] += v_exh;
         c[5] += v_bok; c[6] += v_bnew; c[7] += v_lost; c[8] += v_pend; c[9] += v_prb;
     }
-    if (e < E && r < 3 * HB) st.hist[(size_t)e * 3 * HB + r] += my_hist[r];
+    if (e < E && r < 3 * HB) lk.hist[(size_t)e * 3 * HB + r] += my_hist[r];
     if (e < E && rb < 3 * HB) {                       // segments narrower than the histogram: robot 0 adds the rest
         if (r == 0)
-            for (int q = rb; q < 3 * HB; ++q) st.hist[(size_t)e * 3 * HB + q] += my_hist[q];
+            for (int q = rb; q < 3 * HB; ++q) lk.hist[(size_t)e * 3 * HB + q] += my_hist[q];
     }
 }
 
 // ---------------------------------------------------------------- launch plumbing
 struct StepArgs {
     InetNrState st;
+    const InetNrDlState* dl;          // NULL: the UL step; else the DL step of this link
     InetNrTables tb;
     InetNrParams pm;
     const InetNrRow* rows;
@@ -992,8 +1067,13 @@ typedef void (*StepFn)(const StepArgs&);
 
 template <int S, int P, bool IR, bool VREF, int RBT>
 void launch_step(const StepArgs& a) {
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT>), dim3(a.grid), dim3(STEP_WAVE), a.lds, a.stream, a.st,
-                       a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
+    if (a.dl)
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
+                           a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
+                           a.n_rows);
+    else
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
+                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
 }
 
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband

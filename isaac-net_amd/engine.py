@@ -22,10 +22,10 @@ import torch
 
 from . import _lib
 from .config import NRConfig
-from .phy import PhyTables
+from .phy import PhyTables, cqi_tables
 
 BIG_SLOT = 0x7FFFFFFF
-FADING, BLER_UL = 1, 2
+FADING, BLER_UL, BLER_DL = 1, 2, 3
 NCTR = 12
 CTR_NAMES = ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
              "new_while_pending", "prb_used")
@@ -72,7 +72,8 @@ def refusals(cfg: NRConfig):
         if cond:
             out.append((what, why))
     no(cfg.n_cells != 1, "several cells (n_cells > 1)", "one cell's scheduler and HARQ per env")
-    no(cfg.dl or not cfg.ul, "the downlink (dl=True) or ul=False", "uplink engine")
+    no(not cfg.ul, "ul=False (a downlink-only engine)", "the UL link runs every step")
+    no(cfg.dl and cfg.duplex != "tdd", "the FDD downlink carrier", "TDD (one carrier)")
     no(cfg.ul_grant_model != "lumped", "ul_grant_model='bsr'", "lumped SR grants only")
     no(cfg.n_layers_max != 1, "rank-2 MIMO", "single-layer TBs")
     no(cfg.ul_mini_slot_symbols is not None, "mini-slot grants", "one scheduling occasion per slot")
@@ -110,7 +111,8 @@ def refusals(cfg: NRConfig):
 
 
 class HipNREngine:
-    """NR engine (level "L2", one cell, uplink) on MI355X. API of isaac_net.core.engine.NREngine."""
+    """NR engine (level "L2", one cell; uplink, and the downlink with NRConfig(dl=True)) on MI355X. API of
+    isaac_net.core.engine.NREngine."""
 
     level = "L2"
     backend = "hip"
@@ -136,6 +138,10 @@ class HipNREngine:
         self.N = cfg.slots_per_step
         self.out_format = out_format
         self.tabs = PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2), cfg.ul_mcs_max)
+        self.dl = bool(cfg.dl)
+        # the DL PHY differs from the UL's only by its MCS cap (dl_mcs_max), mac.py:97-99
+        self.tabs_dl = PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2), cfg.dl_mcs_max) \
+            if self.dl else None
         self._alloc_state()
         self._upload_tables()
         self._build_params()
@@ -174,10 +180,34 @@ class HipNREngine:
         for name, _ in _lib.InetNrState._fields_:
             setattr(s, name, self.st[name].data_ptr())
         self._cstate = s
+        if self.dl:
+            self.dst = {
+                "sent": z(E, R), "floor_": z(E, R), "last_tx": z(E, R, v=-1), "olla": z(E, R, dt=f32),
+                "avg": z(E, R, dt=f32, v=100.0), "enq": z(E, R), "qlen": z(E, R), "csi": z(E, S, R, dt=f32),
+                "h_meta": z(E, P, R), "h_lo": z(E, P, R), "h_hi": z(E, P, R), "h_ready": z(E, P, R),
+                "h_tbs": z(E, P, R), "h_comb": z(E, P, R, dt=f32), "h_lexp": z(E, P, R, dt=f32, v=-math.inf),
+                "h_nrb": z(E, P, R, dt=f32), "q_cap": z(E, F, R, v=-1), "q_start": z(E, F, R), "q_end": z(E, F, R),
+                "q_fin": z(E, F, R, v=BIG_SLOT), "q_meta": z(E, F, R), "newest": z(E, R, v=-1),
+                "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
+            }
+            ds = _lib.InetNrDlState()
+            for name, t_ in self.dst.items():
+                setattr(ds, name, t_.data_ptr())
+            if cfg.cqi_table == "38214":
+                thr, cm = cqi_tables(self.tabs_dl, cfg.mcs_table)
+                self._cqi = (torch.from_numpy(thr).to(d), torch.from_numpy(cm.astype(np.int32)).to(d))
+                ds.cqi_thr, ds.cqi_mcs = self._cqi[0].data_ptr(), self._cqi[1].data_ptr()
+            ds.gnb_proc = cfg.gnb_proc_slots
+            ds.ref_off = cfg.gnb_tx_dbm - 10 * math.log10(cfg.nprb)
+            ds.noise_prb = cfg.noise_dbm_per_prb("ue")
+            ds.snr_off = cfg.dl_snr_offset_db
+            self._cdl = ds
 
     def _upload_tables(self):
         cfg, t, d = self.config, self.tabs, self.dev
         nsyms = sorted({cfg.slot_symbols(p)[1] for p in range(len(cfg.tdd_pattern))} - {0}) or [cfg.ul_data_symbols]
+        if self.dl:
+            nsyms = sorted(set(nsyms) | ({cfg.slot_symbols(p)[0] for p in range(len(cfg.tdd_pattern))} - {0}))
         self._nsym_idx = {ns: i for i, ns in enumerate(nsyms)}
         la = [t.la_tables(cfg.nprb, ns, cfg.dmrs_re_per_prb, cfg.overhead_re_per_prb) for ns in nsyms]
         w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
@@ -199,6 +229,13 @@ class HipNREngine:
         c.M, c.C, c.G, c.NPRB, c.EQW, c.mcs_max = t.M, t.C, t.G, cfg.nprb, t.mcs_eq.shape[1], t.mcs_max
         c.thr_monotone = int(bool(np.all(np.diff(t.thr_ref[:t.mcs_max + 1]) >= 0)))
         self._ctab = c
+        if self.dl:                                   # the same tables with the DL MCS cap
+            cd = _lib.InetNrTables()
+            C.memmove(C.addressof(cd), C.addressof(c), C.sizeof(c))
+            mx = self.tabs_dl.mcs_max
+            cd.mcs_max = mx
+            cd.thr_monotone = int(bool(np.all(np.diff(t.thr_ref[:mx + 1]) >= 0)))
+            self._ctab_dl = cd
         self._sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32, device=d)
 
     def _build_params(self):
@@ -302,15 +339,39 @@ class HipNREngine:
                          salt((BLER_UL << 16) | rel)))
         if n > 64:
             raise HipUnsupported("more than 64 scheduled slots (SR / UL / fading) per control step")
-        buf = np.zeros((max(n, 1), 8), dtype=np.int32)
+        res = (self._rows_to_device(rows), n, sched[-1][0] if sched else None, sum(1 for r in rows if r[2] & 2))
+        if self.dl:
+            res = res + (self._rows_to_device(self._dl_rows(sched, evol, rhos, dt0)),)
+        self._rows[key] = res
+        return res
+
+    def _dl_rows(self, sched, evol, rhos, dt0):
+        """The DL rows of a step (the rows of the UL kernel with the DL meaning): flags 1 CQI report, 2 DL data slot,
+        4 / 8 fading evolves / its gain is needed (at DL data and CQI rows, and wherever a later row's evolution
+        depends on it), bits 8..23 the HARQ-ACK slot relative to the step's first slot; the DL decode stream."""
+        cfg = self.config
+        n = len(sched)
+        rows = []
+        for k, (rel, dls, _uls, _sr, cqi, ack) in enumerate(sched):
+            dt = dt0 if k == 0 else rel - sched[k - 1][0]
+            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
+            c1 = math.sqrt(1 - rho ** 2)
+            need_h = evol[k] and (dls > 0 or cqi or (k < n - 1 and not (evol[k + 1] and rhos[k + 1] == 0.0)))
+            if not 0 <= ack < 1 << 16:
+                raise HipUnsupported("a HARQ-ACK slot more than 65535 slots after the step start")
+            flags = (1 if cqi else 0) | (2 if dls else 0) | (4 if evol[k] else 0) | (8 if need_h else 0) | (ack << 8)
+            re = float(min(12 * dls - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156)) if dls else 0.0
+            rows.append((rel, self._nsym_idx.get(dls, -1), flags, re, rho, c1, salt((FADING << 16) | rel),
+                         salt((BLER_DL << 16) | rel)))
+        return rows
+
+    def _rows_to_device(self, rows):
+        buf = np.zeros((max(len(rows), 1), 8), dtype=np.int32)
         for k, r in enumerate(rows):
             buf[k, 0:3] = r[0:3]
             buf[k, 3:6] = np.array(r[3:6], dtype=np.float32).view(np.int32)
             buf[k, 6:8] = np.array(r[6:8], dtype=np.uint32).view(np.int32)
-        dev_rows = torch.from_numpy(buf).to(self.dev)
-        res = (dev_rows, n, sched[-1][0] if sched else None, sum(1 for r in rows if r[2] & 2))
-        self._rows[key] = res
-        return res
+        return torch.from_numpy(buf).to(self.dev)
 
     # ------------------------------------------------------------------ contract API
     @property
@@ -323,7 +384,11 @@ class HipNREngine:
                 ("cls", "[E,R,F]", "int64"), ("delay", "[E,R,F]", "float32"), ("queue_len", "[E,R]", "int64"),
                 ("queue_bytes", "[E,R]", "float32"), ("sinr_db", "[E,R]", "float32"),
                 ("serving_cell", "[E,R]", "int64"), ("t", "[E]", "int64")]
-        return {k: {"shape": s, "dtype": dt, "when": "always"} for k, s, dt in keys}
+        out = {k: {"shape": s, "dtype": dt, "when": "always"} for k, s, dt in keys}
+        if self.dl:
+            for k in ("dl_newest", "dl_queue_len"):
+                out[k] = {"shape": "[E,R]", "dtype": "int64", "when": "dl"}
+        return out
 
     def _now(self, t):
         """engine.py:738-755."""
@@ -355,12 +420,16 @@ class HipNREngine:
         if env_ids is None:
             self.T = 0
             self._ul_slots_run = 0
+            self._dl_slots_run = 0
             self._uniform_epoch = 0
             self.last_g = None
             self._last_snr = torch.zeros_like(self._last_snr)
             self._last_hid = torch.zeros_like(self._last_hid)
             _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), None, 0,
                                          self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+            if self.dl:
+                _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), None, self._stream()),
+                           "dl reset")
             return
         if isinstance(env_ids, torch.Tensor) and env_ids.dtype == torch.bool:
             mask = env_ids.to(self.dev)
@@ -377,6 +446,9 @@ class HipNREngine:
         m8 = mask.to(torch.uint8).contiguous()
         _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), m8.data_ptr(), self.T,
                                      self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+        if self.dl:
+            _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), m8.data_ptr(),
+                                            self._stream()), "dl reset")
 
         self._uniform_epoch = None
         mk = mask[:, None]
@@ -432,6 +504,30 @@ class HipNREngine:
         """Legacy wrapper (NetSlot API)."""
         self.submit(t, Requests(send, det, hid), snr_db)
 
+    def add_dl_frames(self, t, nbytes, cls=None):
+        """Downlink messages of nbytes [E,R] application bytes (0 = none) at t, with classes cls [E,R] (0..255) or
+        None (NREngine.add_dl_frames, engine.py:825-827; needs config.dl). Returns accepted [E,R] bool."""
+        if not self.dl:
+            raise ValueError("add_dl_frames needs NRConfig(dl=True)")
+        T = self._now(t)
+        nb = torch.as_tensor(nbytes).to(self.dev, torch.float32).contiguous()
+        if tuple(nb.shape) != (self.E, self.R):
+            raise ValueError(f"nbytes must be [E,R] = [{self.E},{self.R}], got {tuple(nb.shape)}")
+        cl = None
+        if cls is not None:
+            cl = torch.as_tensor(cls).to(self.dev, torch.long).contiguous()
+            if tuple(cl.shape) != (self.E, self.R):
+                raise ValueError("cls must be [E,R]")
+            if bool(((cl < 0) | (cl > 255)).any()):
+                raise HipUnsupported("DL message classes outside 0..255 (8-bit class field)")
+        acc = torch.empty(self.E, self.R, dtype=torch.bool, device=self.dev)
+        cfg = self.config
+        _lib.check(self._lib.inet_nr_dl_submit(
+            C.byref(self._cstate), C.byref(self._cdl), C.byref(self._cparams), T, nb.data_ptr(),
+            None if cl is None else cl.data_ptr(), int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
+            cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "dl submit")
+        return acc
+
     def _alloc_out(self):
         E, R, F, d = self.E, self.R, self.F, self.dev
         e = lambda *s, dt: torch.empty(*s, dtype=dt, device=d)  # noqa: E731
@@ -462,17 +558,29 @@ class HipNREngine:
              triggers=None, blockers=None):
         """Advance [t, t+1). x: poses [E,R,2|3] (through the radio) or SNR [E,R] dB; snr_db=: [E,R,S] or [E,R].
         Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env)."""
-        if dl_snr_db is not None or pathgain_db is not None or vel is not None or triggers is not None or \
-                blockers is not None:
-            raise HipUnsupported("dl_snr_db / pathgain_db / vel / triggers / blockers need features the hip backend "
-                                 "does not implement (downlink, several cells, per-robot Doppler, traffic models, "
-                                 "blockage)")
+        if (dl_snr_db is not None and not self.dl) or pathgain_db is not None or vel is not None or \
+                triggers is not None or blockers is not None:
+            raise HipUnsupported("dl_snr_db (without dl=True) / pathgain_db / vel / triggers / blockers need features "
+                                 "the hip backend does not implement (several cells, per-robot Doppler, traffic "
+                                 "models, blockage)")
         T = self._now(t)
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
         plan = self._plan(T, kind)
-        o = self._launch_step(T, plan, xin, hid)
+        dl = None
+        if self.dl:
+            # DL reference (NREngine.step -> NRNet.step_rx / step, nr_engine.py:624-631, 651-653): from the poses'
+            # path gain; or the UL SNR plus dl_snr_offset_db; or dl_snr_db as given (SNR input only)
+            if kind != 0 and dl_snr_db is not None:
+                dxin = dl_snr_db.to(self.dev, torch.float32).contiguous()
+                dkind = 2 if dxin.dim() == 3 else 1
+                if tuple(dxin.shape) != {1: (self.E, self.R), 2: (self.E, self.R, self.S)}[dkind]:
+                    raise ValueError(f"dl_snr_db must be [E,R] or [E,R,S], got {tuple(dxin.shape)}")
+                dl = (dkind, dxin, 0)
+            else:
+                dl = (kind, xin, 1)
+        o = self._launch_step(T, plan, xin, hid, dl)
         self._commit(T, plan, o)
         if legacy:
             return o["newest"], o["det_env"]
@@ -511,14 +619,30 @@ class HipNREngine:
         sched = self._schedule(g0)
         fad = cfg.fading and len(sched) > 0
         dt0 = (1 if self.last_g is None else g0 + sched[0][0] - self.last_g) if fad else 0
-        rows, n_rows, last_rel, n_ul = self._rows_for(g0, dt0)
+        rows, n_rows, last_rel, n_ul, *dl_rows = self._rows_for(g0, dt0)
         key = (g0 % math.lcm(len(cfg.tdd_pattern), cfg.sr_period_slots, cfg.cqi_period_slots), dt0, kind)
-        return dict(rows=rows, n_rows=n_rows, last_rel=last_rel, n_ul=n_ul, fad=fad, kind=kind, key=key)
+        n_dl = sum(1 for r in sched if r[1]) if self.dl else 0
+        return dict(rows=rows, n_rows=n_rows, last_rel=last_rel, n_ul=n_ul, fad=fad, kind=kind, key=key,
+                    dl_rows=dl_rows[0] if dl_rows else None, n_dl=n_dl)
 
-    def _launch_step(self, T, plan, xin, hid):
-        """Launch the step kernel (T < 0: the kernel reads the device clock) and return the output dict."""
-        self._cparams.input_kind = plan["kind"]
+    def _launch_step(self, T, plan, xin, hid, dl=None):
+        """Launch the step kernel (T < 0: the kernel reads the device clock) and return the output dict. With the
+        downlink, dl = (input kind, input, add dl_snr_offset_db) of the DL step, launched first: it reads the fading
+        state and RNG words of the step start, which the UL step then advances."""
         o, co = self._alloc_out()
+        if self.dl:
+            dkind, dxin, add_off = dl
+            E, R, d = self.E, self.R, self.dev
+            o["dl_newest"] = torch.empty(E, R, dtype=torch.int64, device=d)
+            o["dl_queue_len"] = torch.empty(E, R, dtype=torch.int64, device=d)
+            cd = self._cdl
+            cd.out_newest, cd.out_queue_len = o["dl_newest"].data_ptr(), o["dl_queue_len"].data_ptr()
+            cd.snr_offset = add_off
+            self._cparams.input_kind = dkind
+            _lib.check(self._lib.inet_nr_dl_step(C.byref(self._cstate), C.byref(cd), C.byref(self._ctab_dl),
+                                                 C.byref(self._cparams), plan["dl_rows"].data_ptr(), plan["n_rows"], T,
+                                                 dxin.data_ptr(), self._stream()), "dl step")
+        self._cparams.input_kind = plan["kind"]
         ev = self.kernel_events
         if ev is not None:
             ev.begin(torch.cuda.current_stream(self.dev))
@@ -534,6 +658,8 @@ class HipNREngine:
         if plan["fad"]:
             self.last_g = T * self.N + plan["last_rel"]
         self._ul_slots_run += plan["n_ul"]
+        if self.dl:
+            self._dl_slots_run += plan["n_dl"]
         self.T = T + 1
         self._last_snr = o["sinr_db"]
 
@@ -542,30 +668,39 @@ class HipNREngine:
         Returns a GraphStep; calling it with (poses [E,R,2|3], counts [E,R,NC]) replays the step. The schedule of
         every replayed step must match the recorded one (the same TDD / SR / CQI phase and fading slot spacing),
         which holds when the control step spans whole periods."""
+        if self.dl:
+            raise HipUnsupported("graph_step with the downlink (dl=True): use step()")
         return GraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     # ------------------------------------------------------------------ statistics
     def counters(self):
-        """{"ul": {counter: value, ntx_hist, rv_tx, rv_fail}} since the last full reset (NRNet.counters)."""
-        c = self.st["ctr"].sum(0).tolist()
-        h = self.st["hist"]
+        """{"ul": {counter: value, ntx_hist, rv_tx, rv_fail}} (and "dl" with the downlink) since the last full reset
+        (NRNet.counters)."""
         cfg = self.config
-        res = {k: float(c[i]) for i, k in enumerate(CTR_NAMES)}
-        res["ntx_hist"] = h[:, 0].sum(0).double().tolist()
-        res["rv_tx"] = h[:, 1].sum(0).double().tolist()
-        res["rv_fail"] = h[:, 2].sum(0).double().tolist()
-        res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * self._ul_slots_run
-        return {"ul": res}
+
+        def link(st, n_slots):
+            c = st["ctr"].sum(0).tolist()
+            h = st["hist"]
+            res = {k: float(c[i]) for i, k in enumerate(CTR_NAMES)}
+            res["ntx_hist"] = h[:, 0].sum(0).double().tolist()
+            res["rv_tx"] = h[:, 1].sum(0).double().tolist()
+            res["rv_fail"] = h[:, 2].sum(0).double().tolist()
+            res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * n_slots
+            return res
+        out = {"ul": link(self.st, self._ul_slots_run)}
+        if self.dl:
+            out["dl"] = link(self.dst, self._dl_slots_run)
+        return out
 
     _ul_slots_run = 0
+    _dl_slots_run = 0
     # set to a KernelTimer to record HIP events around every step-kernel launch, on the launch stream
     kernel_events = None
 
     # ------------------------------------------------------------------ state in the reference's layout
-    def state_dict(self):
-        """Every state tensor in the reference's names, shapes and dtypes (isaac_net/core/nr_fast.py:41-75), on the
-        engine's device. Frame fields of empty queue slots are unspecified (the reference leaves stale values)."""
-        st, cfg, N = self.st, self.config, self.N
+    def _link_sd(self, pre, st):
+        """The MacLink / FrameQueue keys of one link ("ul" or "dl") in the reference's names and layouts."""
+        cfg, N = self.config, self.N
         L = lambda x: x.long()  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
         meta = st["h_meta"]
@@ -576,20 +711,36 @@ class HipNREngine:
         fin = torch.where(fin_slot == BIG_SLOT, torch.full_like(fin, math.inf), fin)
         qm = st["q_meta"]
         out = {
-            "ul.sent": L(st["sent"]), "ul.floor": L(st["floor_"]), "ul.olla": st["olla"], "ul.avg": st["avg"],
-            "ul.bsr": L(st["bsr"]), "ul.sr_t": L(st["sr_t"]), "ul.csi": rs(st["csi"]),
-            "ul.h_state": rs(L(meta & 0xFF)), "ul.h_ntx": rs(L((meta >> 8) & 0xFF)),
-            "ul.h_mcs": rs(L((meta >> 16) & 0xFF)), "ul.h_nsb": rs(L((meta >> 24) & 0xFF)),
-            "ul.h_lo": rs(L(st["h_lo"])), "ul.h_hi": rs(L(st["h_hi"])), "ul.h_ready": rs(L(st["h_ready"])),
-            "ul.h_tbs": rs(L(st["h_tbs"])), "ul.h_comb": rs(st["h_comb"]), "ul.h_lexp": rs(st["h_lexp"]),
-            "ul.h_nrb": rs(st["h_nrb"]), "ul.last_tx": L(st["last_tx"]),
-            "ul.q.cap": rs(L(st["q_cap"])), "ul.q.start": rs(L(st["q_start"])), "ul.q.end": rs(L(st["q_end"])),
-            "ul.q.lost": rs((qm & 1) != 0), "ul.q.fin": rs(fin), "ul.q.cls": rs(L((qm >> 8) & 0xFF)),
-            "ul.q.det": rs((qm & 2) != 0), "ul.q.hid": rs(L(st["q_hid"])), "ul.q.enq": L(st["enq"]),
+            "sent": L(st["sent"]), "floor": L(st["floor_"]), "olla": st["olla"], "avg": st["avg"], "csi": rs(st["csi"]),
+            "h_state": rs(L(meta & 0xFF)), "h_ntx": rs(L((meta >> 8) & 0xFF)), "h_mcs": rs(L((meta >> 16) & 0xFF)),
+            "h_nsb": rs(L((meta >> 24) & 0xFF)), "h_lo": rs(L(st["h_lo"])), "h_hi": rs(L(st["h_hi"])),
+            "h_ready": rs(L(st["h_ready"])), "h_tbs": rs(L(st["h_tbs"])), "h_comb": rs(st["h_comb"]),
+            "h_lexp": rs(st["h_lexp"]), "h_nrb": rs(st["h_nrb"]), "last_tx": L(st["last_tx"]),
+            "q.cap": rs(L(st["q_cap"])), "q.start": rs(L(st["q_start"])), "q.end": rs(L(st["q_end"])),
+            "q.lost": rs((qm & 1) != 0), "q.fin": rs(fin), "q.cls": rs(L((qm >> 8) & 0xFF)), "q.enq": L(st["enq"]),
+        }
+        if pre == "ul":
+            out.update({"bsr": L(st["bsr"]), "sr_t": L(st["sr_t"]), "q.det": rs((qm & 2) != 0),
+                        "q.hid": rs(L(st["q_hid"]))})
+        else:                                         # the DL link holds no BSR / SR state (constant initial values)
+            out.update({"bsr": torch.zeros_like(out["sent"]), "sr_t": torch.full_like(out["sent"], -1)})
+        return {f"{pre}.{k}": v for k, v in out.items()}
+
+    def state_dict(self):
+        """Every state tensor in the reference's names, shapes and dtypes (isaac_net/core/nr_fast.py:41-75), on the
+        engine's device. Frame fields of empty queue slots are unspecified (the reference leaves stale values)."""
+        st, cfg = self.st, self.config
+        L = lambda x: x.long()  # noqa: E731
+        rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
+        out = self._link_sd("ul", st)
+        out.update({
             "net.h": torch.stack([rs(st["h_re"]), rs(st["h_im"])], -1), "eng.epoch": L(st["epoch"]),
             "eng._last_snr": self._last_snr, "eng._last_hid": self._last_hid,
             "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"]),
-        }
+        })
+        if self.dl:
+            out.update(self._link_sd("dl", self.dst))
+            out["net.dl_newest"] = L(self.dst["newest"])
         if cfg.rician_mode == "fixed":
             k = st["k_lin"]
             out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1), "net.k_los": k, "net.k_in": k,
@@ -597,39 +748,54 @@ class HipNREngine:
                         .expand(-1, self.R)})
         return out
 
-    def load_state_dict(self, sd, T=None, last_g=None):
-        """Load reference-layout state (the keys of state_dict(); tensors on any device) into the device buffers;
-        T / last_g set the host clock and the last fading slot (teacher forcing)."""
-        st, cfg, N, d = self.st, self.config, self.N, self.dev
-        g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+    def _link_load(self, pre, st, sd):
+        """Load one link's keys of a reference-layout state dict into its device buffers."""
+        cfg, N, d = self.config, self.N, self.dev
+        g = lambda k: torch.as_tensor(sd[f"{pre}.{k}"]).to(d)  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
         I = lambda x: x.to(torch.int32)  # noqa: E731
-        for a, b in (("sent", "ul.sent"), ("floor_", "ul.floor"), ("bsr", "ul.bsr"), ("sr_t", "ul.sr_t"),
-                     ("last_tx", "ul.last_tx"), ("enq", "ul.q.enq")):
+        pairs = (("sent", "sent"), ("floor_", "floor"), ("last_tx", "last_tx"), ("enq", "q.enq"))
+        if pre == "ul":
+            pairs += (("bsr", "bsr"), ("sr_t", "sr_t"))
+        for a, b in pairs:
             st[a].copy_(I(g(b)))
-        st["olla"].copy_(g("ul.olla"))
-        st["avg"].copy_(g("ul.avg"))
-        st["csi"].copy_(rs(g("ul.csi")))
-        meta = (g("ul.h_state") | (g("ul.h_ntx") << 8) | (g("ul.h_mcs") << 16) | (g("ul.h_nsb") << 24))
+        st["olla"].copy_(g("olla"))
+        st["avg"].copy_(g("avg"))
+        st["csi"].copy_(rs(g("csi")))
+        meta = (g("h_state") | (g("h_ntx") << 8) | (g("h_mcs") << 16) | (g("h_nsb") << 24))
         st["h_meta"].copy_(rs(I(meta)))
         for a in ("h_lo", "h_hi", "h_ready", "h_tbs"):
-            st[a].copy_(rs(I(g("ul." + a))))
+            st[a].copy_(rs(I(g(a))))
         for a in ("h_comb", "h_lexp", "h_nrb"):
-            st[a].copy_(rs(g("ul." + a).float()))
-        cap = g("ul.q.cap")
+            st[a].copy_(rs(g(a).float()))
+        cap = g("q.cap")
         valid = cap >= 0
         st["qlen"].copy_(I(valid.sum(-1)))
         st["q_cap"].copy_(rs(I(torch.where(valid, cap, torch.full_like(cap, -1)))))
-        st["q_start"].copy_(rs(I(g("ul.q.start"))))
-        st["q_end"].copy_(rs(I(g("ul.q.end"))))
+        st["q_start"].copy_(rs(I(g("q.start"))))
+        st["q_end"].copy_(rs(I(g("q.end"))))
         po = cfg.proc_offset_ms / cfg.control_step_ms
-        fin = g("ul.q.fin").double()
+        fin = g("q.fin").double()
         slot = torch.round((fin - po) * N).long() - 1
         slot = torch.where(torch.isinf(fin) | ~valid, torch.full_like(slot, BIG_SLOT), slot)
         st["q_fin"].copy_(rs(I(slot)))
-        qm = g("ul.q.lost").long() | (g("ul.q.det").long() << 1) | (g("ul.q.cls").long() << 8)
+        qm = g("q.lost").long() | (g("q.cls").long() << 8)
+        if pre == "ul":
+            qm = qm | (g("q.det").long() << 1)
+            st["q_hid"].copy_(rs(I(g("q.hid"))))
         st["q_meta"].copy_(rs(I(qm)))
-        st["q_hid"].copy_(rs(I(g("ul.q.hid"))))
+
+    def load_state_dict(self, sd, T=None, last_g=None):
+        """Load reference-layout state (the keys of state_dict(); tensors on any device) into the device buffers;
+        T / last_g set the host clock and the last fading slot (teacher forcing)."""
+        st, cfg, d = self.st, self.config, self.dev
+        g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+        rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
+        I = lambda x: x.to(torch.int32)  # noqa: E731
+        self._link_load("ul", st, sd)
+        if self.dl:
+            self._link_load("dl", self.dst, sd)
+            self.dst["newest"].copy_(I(g("net.dl_newest")))
         h = g("net.h")
         st["h_re"].copy_(rs(h[..., 0]))
         st["h_im"].copy_(rs(h[..., 1]))

@@ -12,7 +12,10 @@ from oracle import replay
 # OLLA offset and PF average are pure arithmetic on the decisions and must be bitwise equal.
 FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1e-5, "ul.h_comb": 1e-3,
              "ul.h_lexp": 1e-3, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0, "net.k_los": 0.0,
-             "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0}
+             "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0,
+             # the DL link: its CSI is an MCS threshold minus the reference SINR (exact once the reported MCS agrees)
+             "dl.csi": 1e-5, "dl.h_comb": 1e-3, "dl.h_lexp": 1e-3, "dl.h_nrb": 0.0, "dl.olla": 0.0, "dl.avg": 0.0,
+             "dl.q.fin": 0.0}
 OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
 # The reported SINR is (pg + ue_tx) - noise with |pg| ~ 100-150 dB: one float32 ulp there is 7.6e-6 .. 1.5e-5 dB,
 # so near 0 dB a relative bound is meaningless; the absolute floor is 4 ulp of that magnitude.
@@ -39,7 +42,7 @@ def close(m, r, tol, floor=0.0, key=None):
 def compare(ref, s, out, sd, E, R):
     """(integer keys that differ, float keys out of tolerance, bool [E,R] robots with an integer difference)."""
     pre = f"s{s:03d}/"
-    valid = ref[pre + "ul.q.cap"] >= 0
+    valid = {lk: ref[pre + f"{lk}.q.cap"] >= 0 for lk in ("ul", "dl") if pre + f"{lk}.q.cap" in ref}
     bad_i, bad_f = {}, {}
     robots = np.zeros((E, R), bool)
     for k, v in out.items():
@@ -55,8 +58,9 @@ def compare(ref, s, out, sd, E, R):
         if pre + k not in ref:
             continue
         r, m = ref[pre + k], v.detach().cpu().numpy()
-        if k.startswith("ul.q.") and k != "ul.q.enq":
-            vv = valid if m.shape == valid.shape else valid[..., None]
+        if k[3:5] == "q." and k[5:] != "enq" and k[:2] in valid:
+            v_ = valid[k[:2]]
+            vv = v_ if m.shape == v_.shape else v_[..., None]
             m, r = np.where(vv, m, 0), np.where(vv, r, 0)
         ok = close(m, r, FLOAT_TOL[k], ABS_FLOOR.get(k, 0.0), k) if k in FLOAT_TOL else (m == r)
         if not ok.all():
@@ -116,6 +120,8 @@ def teacher_forced(P, name, dev="cuda:0"):
             eng.load_state_dict(snapshot(ref, f"reset{s:03d}"), T=s, last_g=lg)
         for send in replay.submits(ref["counts"][s]):
             eng.submit(None, to(send))
+        for nb, cls in replay.dl_frames(ref, s):
+            eng.add_dl_frames(None, to(nb), to(cls))
         x = to(ref["x"][s])
         o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x)
         set_radio_bound(ref, s, cfg, eng, kind)

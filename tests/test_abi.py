@@ -32,11 +32,11 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(_lib_path())
     names = declared_functions()
     assert names == sorted(["inet_nr_abi_version", "inet_nr_build_info", "inet_nr_step", "inet_nr_submit",
-                            "inet_nr_reset"])
+                            "inet_nr_reset", "inet_nr_dl_step", "inet_nr_dl_submit", "inet_nr_dl_reset"])
     for n in names:
         assert hasattr(lib, n), n
     lib.inet_nr_abi_version.restype = ctypes.c_int32
-    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 3
     lib.inet_nr_build_info.restype = ctypes.c_char_p
     assert b"gfx950" in lib.inet_nr_build_info()
     wifi = declared_functions(WIFI_HEADER, "inet_wifi_")
@@ -48,7 +48,7 @@ def test_library_exports_every_declared_symbol():
     assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 2
 
 
-STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetWifiState",
+STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetNrDlState", "InetWifiState",
            "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
 
 

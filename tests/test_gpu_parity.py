@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import CASES
+from conftest import CASES, DL_CASES
 import gpu_util
 from gpu_util import compare, load, set_radio_bound, teacher_forced
 from oracle import replay
@@ -14,7 +14,7 @@ import isaac_net_amd as P
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES)
 def test_teacher_forced_bit_exact(name):
     print(f"case {name} teacher-forced", flush=True)
     n_bad, n, keys_i, keys_f = teacher_forced(P, name)
@@ -25,7 +25,7 @@ def test_teacher_forced_bit_exact(name):
     assert not keys_f, keys_f
 
 
-@pytest.mark.parametrize("name", CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES)
 def test_free_running_bit_exact(name):
     print(f"case {name} free running", flush=True)
     ref, cfgd, kind = load(name)
@@ -51,13 +51,15 @@ def test_free_running_bit_exact(name):
     gpu_util.MAX_DEV.clear()
     # counters: integer accumulators on the device vs the reference's float sums
     import json
-    want = json.loads(bytes(ref["counters_json"]))["ul"]
-    got = eng.counters()["ul"]
-    for k in ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
-              "new_while_pending", "prb_used", "prb_avail"):
-        assert got[k] == pytest.approx(want[k], rel=1e-6), k
-    assert got["ntx_hist"] == pytest.approx(want["ntx_hist"])
-    assert got["rv_tx"] == pytest.approx(want["rv_tx"]) and got["rv_fail"] == pytest.approx(want["rv_fail"])
+    links = ("ul", "dl") if cfg.dl else ("ul",)
+    for lk in links:
+        want = json.loads(bytes(ref["counters_json"]))[lk]
+        got = eng.counters()[lk]
+        for k in ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
+                  "new_while_pending", "prb_used", "prb_avail"):
+            assert got[k] == pytest.approx(want[k], rel=1e-6), (lk, k)
+        assert got["ntx_hist"] == pytest.approx(want["ntx_hist"])
+        assert got["rv_tx"] == pytest.approx(want["rv_tx"]) and got["rv_fail"] == pytest.approx(want["rv_fail"])
 
 
 def test_reset_draws_match_reference_fields():

@@ -10,15 +10,18 @@ from isaac_net_amd import engine as EN
 
 def test_refusals_name_each_unimplemented_feature():
     assert EN.refusals(P.NRConfig(n_prb=52)) == []
-    bad = P.NRConfig(n_prb=52, dl=True, scheduler="qos", n_cells=3, cell_layout="hex", ul_grant_model="bsr")
+    assert EN.refusals(P.NRConfig(n_prb=52, dl=True)) == []
+    bad = P.NRConfig(n_prb=52, dl=True, duplex="fdd", scheduler="qos", n_cells=3, cell_layout="hex",
+                     ul_grant_model="bsr")
     names = " ".join(f for f, _ in EN.refusals(bad))
-    for word in ("several cells", "downlink", "bsr", "qos"):
+    for word in ("several cells", "FDD downlink", "bsr", "qos"):
         assert word in names
+    assert "ul=False" in " ".join(f for f, _ in EN.refusals(P.NRConfig(n_prb=52, ul=False, dl=True)))
 
 
 def test_make_engine_refuses_before_building():
     with pytest.raises(EN.HipUnsupported):
-        P.make_engine("L2", 2, 2, "cuda", P.NRConfig(n_prb=52, dl=True))
+        P.make_engine("L2", 2, 2, "cuda", P.NRConfig(n_prb=52, ul=False, dl=True))
     with pytest.raises(NotImplementedError):
         P.make_engine("L1", 2, 2, "cuda", P.NRConfig(n_prb=52))
     with pytest.raises(ValueError):
@@ -30,7 +33,7 @@ def test_schedule_rows_of_the_rl_workload():
     (rho 0) the S-slot fading draws are skipped (the next slot overwrites the state) and the U slots keep theirs."""
     cfg = P.NRConfig(mu=1, n_prb=52, control_step_ms=25.0, fading_rho_per_ms=0.0)
     eng = EN.HipNREngine.__new__(EN.HipNREngine)
-    eng.config, eng.dev, eng._rows, eng._nsym_idx = cfg, "cpu", {}, {12: 0}
+    eng.config, eng.dev, eng._rows, eng._nsym_idx, eng.dl = cfg, "cpu", {}, {12: 0}, False
     rows, n, last_rel, n_ul = eng._rows_for(0, 1)
     r = rows.numpy()
     assert n == 20 and n_ul == 10 and last_rel == 49
@@ -47,13 +50,41 @@ def test_schedule_rows_of_the_rl_workload():
 def test_schedule_rows_correlated_fading_keep_every_draw():
     cfg = P.NRConfig(mu=1, n_prb=52, control_step_ms=10.0)
     eng = EN.HipNREngine.__new__(EN.HipNREngine)
-    eng.config, eng.dev, eng._rows, eng._nsym_idx = cfg, "cpu", {}, {12: 0}
+    eng.config, eng.dev, eng._rows, eng._nsym_idx, eng.dl = cfg, "cpu", {}, {12: 0}, False
     rows, n, _, _ = eng._rows_for(20, 4)
     r = rows.numpy()
     assert np.all((r[:n, 2] & 8) == 8)
     rho = r[:n, 4].view(np.float32)
     assert abs(float(rho[0]) - cfg.fading_rho_per_ms ** (4 * 0.5)) < 1e-6
     assert abs(float(rho[1]) - cfg.fading_rho_per_ms ** (1 * 0.5)) < 1e-6
+
+
+def test_schedule_rows_with_the_downlink():
+    """dl=True, DDDSU at 10 ms (20 slots): every slot is scheduled (D and S carry DL data, U UL data); the DL
+    rows flag the CQI reports at the first UL-capable slot of each 10-slot window, the DL data slots with their
+    symbol-count index, the HARQ-ACK slot (the first UL-capable slot >= g + k1, relative to the step) in bits 8..23,
+    and the DL decode stream; the fading flags of both row lists agree where both need the gain."""
+    cfg = P.NRConfig(mu=1, n_prb=52, control_step_ms=10.0, fading_rho_per_ms=0.0, dl=True)
+    eng = EN.HipNREngine.__new__(EN.HipNREngine)
+    dls_syms = sorted({cfg.slot_symbols(p)[0] for p in range(5)} - {0})
+    nsyms = sorted(set(dls_syms) | {12})
+    eng.config, eng.dev, eng._rows, eng.dl = cfg, "cpu", {}, True
+    eng._nsym_idx = {ns: i for i, ns in enumerate(nsyms)}
+    rows, n, last_rel, n_ul, dl_rows = eng._rows_for(0, 1)
+    sched = cfg.schedule(0)
+    assert n == len(sched) == 20 and n_ul == 4
+    d = dl_rows.numpy()[:n]
+    fl = d[:, 2]
+    for k, (rel, dls, uls, sr, cqi, ack) in enumerate(sched):
+        assert d[k, 0] == rel
+        assert bool(fl[k] & 1) == cqi and bool(fl[k] & 2) == (dls > 0)
+        assert ((fl[k] >> 8) & 0xFFFF) == ack == cfg.next_ul_capable(rel + cfg.k1)
+        assert d[k, 1] == (eng._nsym_idx[dls] if dls else -1)
+        salt = EN.salt((EN.BLER_DL << 16) | rel)
+        assert d[k, 7] == (salt - (1 << 32) if salt >= 1 << 31 else salt)
+        # i.i.d. fading: the DL needs the gain at its data and CQI rows only
+        assert bool(fl[k] & 8) == (dls > 0 or cqi)
+    assert sorted(r[0] for r in sched if r[4]) == [3, 13]
 
 
 def test_hash_helpers_agree():
