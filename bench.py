@@ -63,6 +63,22 @@ def step_kernel_bytes(eng):
     return E * R * per_robot + E * per_env, per_robot
 
 
+def dl_step_kernel_bytes(eng):
+    """Algorithmic HBM bytes of one DL step-kernel launch: per robot-step the DL link's state read and written once
+    (MAC scalars, CSI, HARQ processes, the DL frame FIFO of 5 words per frame, dl_newest), the shared state it only
+    reads (fading state, Rician phasor and K), the pose, and the outputs dl_newest / dl_queue_len; plus the per-env
+    words (RNG key, epoch, shadowing field, DL counters and histograms)."""
+    cfg, E, R, S, P, F = eng.config, eng.E, eng.R, eng.S, eng.P, eng.F
+    p = eng._cparams
+    b_rw = 8 * 4 + S * 4 + P * 6 * 4 + F * 5 * 4          # MAC scalars + dl_newest, CSI, HARQ processes, frames
+    if p.comb == 2:
+        b_rw += 2 * P * 4
+    b_ro = (2 * S * 4 if cfg.fading else 0) + (3 * 4 if p.rician else 0)
+    per_robot = 2 * b_rw + b_ro + 8 + 2 * 8
+    per_env = 4 * 4 + p.n_fields * p.n_modes * 3 * 4 + 2 * 8 * 10 + 2 * 8 * 3 * (cfg.max_harq_tx + 1)
+    return E * R * per_robot + E * per_env, per_robot
+
+
 def step_kernel_touched_bytes(eng, qlen_mean, kept_mean):
     """HBM bytes the kernel actually moves for the measured queue occupancy: the frame FIFO is touched only up to
     each robot's queue length (qlen_mean frames read, kept_mean rewritten), everything else as in step_kernel_bytes."""
@@ -217,12 +233,16 @@ def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
     ora = O.OracleEngine(E_cpu, R, cfg, seed=0)
     poses = wl.poses[:, :E_cpu].cpu()
     counts = wl.counts[:, :E_cpu].cpu().numpy()
+    dl_bytes = None if wl.dl_bytes is None else wl.dl_bytes[:, :, :E_cpu].cpu()
 
     def one(s):
         c = counts[s]
         for ci in range(c.shape[-1]):
             for i in range(int(c[..., ci].max())):
                 ora.submit(None, torch.from_numpy((c[..., ci] > i).astype("int64") * (ci + 1)))
+        if dl_bytes is not None:
+            for i in range(dl_bytes.shape[1]):
+                ora.add_dl_frames(None, dl_bytes[s, i])
         ora.step(None, poses[s])
     for s in range(warmup):
         one(s)
@@ -230,11 +250,76 @@ def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
     for s in range(warmup, warmup + steps):
         one(s)
     dt = time.perf_counter() - t0
-    k_ul = sum(1 for x in cfg.schedule(0) if x[2])
+    k_ul = sum(1 for x in cfg.schedule(0) if x[2]) + sum(1 for x in cfg.schedule(0) if x[1])
     return {"value": E_cpu * R * k_ul * steps / dt, "unit": "robot-slots/s", "cores": threads, "kind": "port",
             "sample": f"oracle (torch CPU restatement of the reference path) on the first {E_cpu} of the 4096 envs "
                       f"x {R} robots, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
             "ms_per_step": 1e3 * dt / steps}
+
+
+def run_dl(args, P, torch):
+    """The RL-scale workload with the downlink on: one line with robot-slots/s over the UL and DL data slots and the
+    roofline fields of the slower of the two step kernels (both are reported)."""
+    from isaac_net_amd import scenarios as S
+    from isaac_net_amd.engine import KernelTimer
+    dev = "cuda:0"
+    E = args.envs if args.envs_set else 4096
+    R = args.robots if args.robots_set else 32
+    total = args.warmup + args.steps
+    print(f"# workload rl_scale_dl {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev, name="rl_scale_dl")
+    cfg = wl.cfg
+    eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
+    sched = cfg.schedule(0)
+    k_ul, k_dl = sum(1 for x in sched if x[2]), sum(1 for x in sched if x[1])
+
+    def one(s):
+        eng.submit_counts(wl.counts[s])
+        for i in range(wl.dl_bytes.shape[1]):
+            eng.add_dl_frames(None, wl.dl_bytes[s, i])
+        eng.step(None, wl.poses[s])
+    for s in range(args.warmup):
+        one(s)
+    torch.cuda.synchronize()
+    eng.kernel_events, eng.dl_kernel_events = KernelTimer(args.steps, dev), KernelTimer(args.steps, dev)
+    ev_ul, ev_dl = eng.kernel_events, eng.dl_kernel_events
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one(args.warmup + i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.kernel_events = eng.dl_kernel_events = None
+    ms = {}
+    for name, ev, fn in (("nr_step_kernel", ev_ul, step_kernel_bytes), ("nr_step_kernel<dl>", ev_dl,
+                                                                       dl_step_kernel_bytes)):
+        k = sorted(ev.ms())
+        avg = sum(k) / len(k)
+        nb, per_robot = fn(eng)
+        ach = nb / (avg * 1e-3) / 1e9
+        ms[name] = {"bound": "hbm", "achieved": ach, "peak": PEAK_GBS, "unit": "GB/s", "frac": ach / PEAK_GBS,
+                    "traffic": None, "kernel": name, "kernel_ms_avg": avg, "kernel_ms_median": k[len(k) // 2],
+                    "algorithmic_bytes_per_launch": nb, "algorithmic_bytes_per_robot_step": per_robot}
+    dom = max(ms.values(), key=lambda r: r["kernel_ms_avg"])
+    c = eng.counters()
+    res = {"metric": f"robot-slots/sec (UL + DL data slots) @{E} envs×{R} robots K_ul={k_ul} K_dl={k_dl}",
+           "value": E * R * (k_ul + k_dl) * args.steps / dt, "unit": "robot-slots/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"rl_scale_dl: rl_scale ({E} envs x {R} robots, DDDSU at 25 ms, 52 PRB, PF, 8 HARQ, "
+                                  f"Rician K 3 dB, UMi LOS) with the downlink: {k_dl} DL data slots and CQI every 10 "
+                                  "slots, 2000 B DL messages at Poisson 0.5 per robot-step",
+                      "envs": E, "robots": R, "ul_slots_per_step": k_ul, "dl_slots_per_step": k_dl,
+                      "parallelism": "single GPU", "out_format": args.out_format, "launch": "eager"},
+           "env_steps_per_s": E * args.steps / dt,
+           "roofline": dom, "kernels": ms,
+           "dl_tb_per_robot_step": c["dl"]["tb_new"] / (E * R * (args.warmup + args.steps))}
+    copy_calibration(args, res, torch, dev)
+    if not args.no_cpu:
+        print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
+        # the oracle runs 40 DL and 10 UL data slots per step: a smaller sample keeps it to about 15 s
+        res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, 256), min(args.cpu_steps, 4), 1)
+    print(json.dumps(res), flush=True)
 
 
 def main():
@@ -242,9 +327,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="rl_scale", choices=("rl_scale", "wifi_dcf", "wifi_dcf_slots"),
-                    help="rl_scale: the NR engine's RL-scale workload (the headline metric); wifi_dcf: level WIFI; "
-                         "wifi_dcf_slots: level WIFI_DCF on the same inputs")
+    ap.add_argument("--workload", default="rl_scale",
+                    choices=("rl_scale", "rl_scale_dl", "wifi_dcf", "wifi_dcf_slots"),
+                    help="rl_scale: the NR engine's RL-scale workload (the headline metric); rl_scale_dl: the same with "
+                         "the downlink on; wifi_dcf: level WIFI; wifi_dcf_slots: level WIFI_DCF on the same inputs")
     ap.add_argument("--envs", type=int, default=None)
     ap.add_argument("--robots", type=int, default=None)
     ap.add_argument("--envs-per-wave", type=int, default=1, help="level WIFI: envs per 64-lane wavefront")
@@ -268,6 +354,8 @@ def main():
     args.envs_set, args.robots_set = args.envs is not None, args.robots is not None
     if args.workload in ("wifi_dcf", "wifi_dcf_slots"):
         return run_wifi(args, P, torch)
+    if args.workload == "rl_scale_dl":
+        return run_dl(args, P, torch)
     from isaac_net_amd import scenarios as S
     from isaac_net_amd.engine import KernelTimer
     dev = "cuda:0"

@@ -111,7 +111,9 @@ typedef struct InetNrParams {
     int32_t comb;                     /* 0 none, 1 cc, 2 ir_lena */
     int32_t eesm;                     /* 1 eesm, 0 mean_db */
     int32_t harq_drop, olla, phr_cap, retx_prio, rician, fading, purge, input_kind, radio_model, out_ref;
-    int32_t max_tx, sr_delay, ul_rtt, rlc_retx, timeout, tb_oh, n_fields, n_modes, seed_key, pad0;
+    int32_t max_tx, sr_delay, ul_rtt, rlc_retx, timeout, tb_oh, n_fields, n_modes, seed_key;
+    int32_t n_data;                   /* data rows (flag 2) among the step's rows: sizes the kernel's per-slot LDS
+                                         history (0: n_rows); must not be smaller than the actual count */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */

@@ -31,7 +31,7 @@ class InetNrParams(C.Structure):
     _fields_ = [(n, i32) for n in (
         "E", "R", "S", "P", "F", "N", "sched", "comb", "eesm", "harq_drop", "olla", "phr_cap", "retx_prio", "rician",
         "fading", "purge", "input_kind", "radio_model", "out_ref", "max_tx", "sr_delay", "ul_rtt", "rlc_retx",
-        "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "pad0")] + \
+        "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "n_data")] + \
                [(n, f32) for n in (
         "olla_up", "olla_dn", "pf_a", "pf_b", "target", "phr_min", "snr_ref_prbs", "w0", "ref_off", "noise_prb",
         "ue_tx", "subband_noise", "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1",

@@ -218,15 +218,17 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (t.M <= 0 || t.M > inet::MAX_M || t.EQW <= 0 || t.EQW > inet::MAX_EQW || t.mcs_max >= t.M) return INET_NR_EINVAL;
     if (p.input_kind < 0 || p.input_kind > 2) return INET_NR_EINVAL;
     if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
+    if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
+    const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);
     inet::StepFn fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
                     : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = inet::STEP_WAVE / rb;
-    inet::StepArgs a{*st, dl, t, p, rows, n_rows, T, x, cur_hid, *out, rb,
+    inet::StepArgs a{*st, dl, t, p, rows, n_rows, n_data, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
-                     inet::step_lds_bytes(n_rows, p.harq_drop, rb, p.max_tx), (hipStream_t)stream};
+                     inet::step_lds_bytes(n_data, p.harq_drop, rb, p.max_tx), (hipStream_t)stream};
     fn(a);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }

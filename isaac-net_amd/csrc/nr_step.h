@@ -1053,7 +1053,7 @@ struct StepArgs {
     InetNrTables tb;
     InetNrParams pm;
     const InetNrRow* rows;
-    int n_rows;
+    int n_rows, n_data;
     int64_t T;
     const float* x;
     const int64_t* hid;
@@ -1070,10 +1070,10 @@ void launch_step(const StepArgs& a) {
     if (a.dl)
         hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
                            a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
-                           a.n_rows);
+                           a.n_data);
     else
         hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
-                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_rows);
+                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data);
 }
 
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband

@@ -639,10 +639,17 @@ class HipNREngine:
             cd.out_newest, cd.out_queue_len = o["dl_newest"].data_ptr(), o["dl_queue_len"].data_ptr()
             cd.snr_offset = add_off
             self._cparams.input_kind = dkind
+            self._cparams.n_data = plan["n_dl"]
+            dev_ = self.dl_kernel_events
+            if dev_ is not None:
+                dev_.begin(torch.cuda.current_stream(self.dev))
             _lib.check(self._lib.inet_nr_dl_step(C.byref(self._cstate), C.byref(cd), C.byref(self._ctab_dl),
                                                  C.byref(self._cparams), plan["dl_rows"].data_ptr(), plan["n_rows"], T,
                                                  dxin.data_ptr(), self._stream()), "dl step")
+            if dev_ is not None:
+                dev_.end(torch.cuda.current_stream(self.dev))
         self._cparams.input_kind = plan["kind"]
+        self._cparams.n_data = plan["n_ul"]
         ev = self.kernel_events
         if ev is not None:
             ev.begin(torch.cuda.current_stream(self.dev))
@@ -694,8 +701,9 @@ class HipNREngine:
 
     _ul_slots_run = 0
     _dl_slots_run = 0
-    # set to a KernelTimer to record HIP events around every step-kernel launch, on the launch stream
+    # set to a KernelTimer to record HIP events around every (UL / DL) step-kernel launch, on the launch stream
     kernel_events = None
+    dl_kernel_events = None
 
     # ------------------------------------------------------------------ state in the reference's layout
     def _link_sd(self, pre, st):

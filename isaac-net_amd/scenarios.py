@@ -12,6 +12,8 @@ control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 
               per control step, 1500 B at Poisson 0.4, FIFO 16, stations uniform in a 50 m disc around the AP with a
               1 m/s random walk kept inside the disc, log-distance path loss with plane-wave shadowing.
   wifi_dcf_slots  the same inputs on level WIFI_DCF (per-slot CSMA/CA with integer backoff counters).
+  rl_scale_dl  rl_scale with the downlink on (dl=True: 40 DL data slots and 5 CQI reports per step) and 2000 B DL
+              messages at Poisson 0.5 per robot-step (at most 2).
 Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
 the square or disc; arrival counts per class), identical for the GPU engine and the CPU oracle.
 """
@@ -54,6 +56,8 @@ def wifi_dcf_config(**kw):
 WORKLOADS = {
     "plumbing": dict(cfg=plumbing_config, E=64, R=8, arena=100.0, speed=0.0, rates=(0.5,), steps=1000),
     "rl_scale": dict(cfg=rl_scale_config, E=4096, R=32, arena=200.0, speed=1.0, rates=(0.8, 0.1), steps=500),
+    "rl_scale_dl": dict(cfg=lambda **kw: rl_scale_config(dl=True, **kw), E=4096, R=32, arena=200.0, speed=1.0,
+                        rates=(0.8, 0.1), steps=500, dl_rates=(0.5,), dl_size=2000.0),
     "wifi_dcf": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
                      level="WIFI"),
     "wifi_dcf_slots": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
@@ -91,4 +95,10 @@ class Workload:
         counts = np.stack([rs.poisson(lam, size=(steps, E, R)) for lam in w["rates"]], -1)
         self.poses = torch.from_numpy(poses).to(device)
         self.counts = torch.from_numpy(np.minimum(counts, 255).astype(np.uint8)).to(device)
+        self.dl_bytes = None
+        if "dl_rates" in w:
+            # DL messages per robot-step (Poisson, at most 2): the bytes of the add_dl_frames calls of each step
+            n = np.minimum(rs.poisson(w["dl_rates"][0], size=(steps, E, R)), 2)
+            self.dl_bytes = torch.from_numpy(np.stack([np.where(n > i, w["dl_size"], 0.0) for i in range(2)], 1)
+                                             .astype(np.float32)).to(device)             # [steps, 2, E, R]
         self.E, self.R, self.steps = E, R, steps

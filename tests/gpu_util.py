@@ -30,7 +30,8 @@ def close(m, r, tol, floor=0.0, key=None):
     same = (m == r) | (np.isnan(m) & np.isnan(r))
     if tol == 0.0:
         return same
-    dev = np.where(same, 0.0, np.abs(m - r))
+    with np.errstate(invalid="ignore"):                 # inf - inf where both hold the same infinity
+        dev = np.where(same, 0.0, np.abs(m - r))
     if key is not None and dev.size:
         MAX_DEV[key] = max(MAX_DEV.get(key, 0.0), float(np.nanmax(dev)))
     lim = np.maximum(tol * np.maximum(np.maximum(np.abs(m), np.abs(r)), 1.0), floor)
