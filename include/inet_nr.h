@@ -1,8 +1,8 @@
 /*
- * inet_nr.h -- C ABI of the MI355X-native NR uplink engine (libinet_nr.so, HIP kernels for gfx950).
+ * inet_nr.h -- C ABI of the MI355X-native NR engine (libinet_nr.so, HIP kernels for gfx950).
  *
- * Drop-in boundary for isaac-net's per-control-step NR engine hot path (level "L2", one cell, uplink). The
- * reference launches its fused Triton kernel through
+ * Drop-in boundary for isaac-net's per-control-step NR engine hot path (level "L2", one cell, uplink and
+ * downlink). The reference launches its fused Triton kernel through
  *     nr_triton.launch_step(eng, uref, dref, pc, itab, ftab, K, gate, dgate)      isaac_net/core/nr_triton.py:1104-1167
  * from NRTritonEngine._triton_step (isaac_net/core/nr_fast.py:702-752), and runs the enqueue (NRNet.add_frames,
  * isaac_net/core/nr_engine.py:466-487) and partial reset (NREngine.reset, isaac_net/core/engine.py:763-794) as eager
@@ -17,6 +17,8 @@
  *   inet_nr_reset   partial or full reset of an env mask (NRNet.reset, MacLink.reset, FrameQueue.reset,
  *                   NRRng.reset_mask, RadioMC.reset: nr_engine.py:250-320, mac.py:176-189, queues.py:70-78,
  *                   nr_rng.py:45-52, radio.py:200-219).
+ *   inet_nr_dl_step, inet_nr_dl_submit, inet_nr_dl_reset   the downlink of NRConfig(dl=True) (DlMac, mac_dl.py:19-49;
+ *                   NRNet.add_dl_frames, nr_engine.py:489-497), declared at the end of this header.
  *
  * Conventions
  *   Ownership  The caller allocates and owns every buffer (device memory); the library never allocates or frees
