@@ -4,9 +4,9 @@
     python bench.py --workload wifi_dcf [--envs-per-wave G]     (level WIFI: station-substeps/s)
     python bench.py --workload wifi_dcf_slots [--envs-per-wave G]  (level WIFI_DCF: station-steps/s)
 
-A step is one control step of every env: submit_counts (this step's message arrivals, one launch) and step (poses in,
-the reference's output dict out: one launch of the fused step kernel), launched from Python every step (--graph:
-replayed from HIP graphs recorded after the warm-up). Inputs (poses and arrival counts of every
+A step is one control step of every env: this step's message arrivals and step (poses in, the reference's output dict
+out), one launch of the fused step kernel that enqueues the arrivals first (--separate-submit: submit_counts and step,
+two launches; --graph: both replayed from HIP graphs recorded after the warm-up). Inputs (poses and arrival counts of every
 step) are generated before the timed region and are resident in HBM. The timed region is K steps bracketed by
 torch.cuda.synchronize(); value = E * R * K_ul * K / seconds (robot-slots/s, K_ul = 10 UL slots per step).
 The step kernel's average duration is measured live with HIP events recorded around each launch on the launch
@@ -274,10 +274,9 @@ def run_dl(args, P, torch):
     k_ul, k_dl = sum(1 for x in sched if x[2]), sum(1 for x in sched if x[1])
 
     def one(s):
-        eng.submit_counts(wl.counts[s])
         for i in range(wl.dl_bytes.shape[1]):
             eng.add_dl_frames(None, wl.dl_bytes[s, i])
-        eng.step(None, wl.poses[s])
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
     for s in range(args.warmup):
         one(s)
     torch.cuda.synchronize()
@@ -339,6 +338,8 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="replay submit and step from HIP graphs recorded after the warm-up instead of launching them "
                          "from Python every step (on this stack the eager launches are the faster of the two)")
+    ap.add_argument("--separate-submit", action="store_true",
+                    help="enqueue each step's arrivals with submit_counts (its own launch) instead of inside the step")
     ap.add_argument("--cpu-envs", type=int, default=2048)
     ap.add_argument("--cpu-steps", type=int, default=8)
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -382,9 +383,11 @@ def main():
         s = args.warmup + i
         if graph is not None:
             graph(wl.poses[s], wl.counts[s])
-        else:
+        elif args.separate_submit:
             eng.submit_counts(wl.counts[s])
             eng.step(None, wl.poses[s])
+        else:                                        # the arrivals enqueued inside the step's launch
+            eng.step(None, wl.poses[s], arrivals=wl.counts[s])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
@@ -410,7 +413,9 @@ def main():
                                   "per robot-step, FIFO 32, UMi LOS",
                       "envs": E, "robots": R, "ul_slots_per_step": k_ul, "global_batch": E * R,
                       "parallelism": "single GPU", "out_format": args.out_format,
-                      "launch": "hip graph replay" if args.graph else "eager"},
+                      "launch": "hip graph replay" if args.graph else
+                      ("eager: submit_counts + step" if args.separate_submit else "eager: one launch per step "
+                       "(arrivals enqueued inside the step kernel)")},
            "env_steps_per_s": E * args.steps / dt,
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                         "frac": achieved / PEAK_GBS, "traffic": traffic,

@@ -173,6 +173,14 @@ typedef struct InetNrDlState {
     int32_t pad;
 } InetNrDlState;
 
+/* The arrivals of one control step for inet_nr_submit_step: the counts form of inet_nr_submit. */
+typedef struct InetNrArrivals {
+    const uint8_t *counts;              /* [E][R][n_cls] messages per class, enqueued class by class (device) */
+    const float *sizes;                 /* [n_cls] message bytes (device) */
+    int32_t *accepted;                  /* [E][R] messages accepted, or NULL (device) */
+    int32_t n_cls, discard_pdcp, pkt_payload, pkt_overhead;
+} InetNrArrivals;
+
 /* Library version (INET_NR_ABI_VERSION) and a short build string. */
 int32_t inet_nr_abi_version(void);
 const char *inet_nr_build_info(void);
@@ -184,6 +192,13 @@ const char *inet_nr_build_info(void);
 int32_t inet_nr_step(const InetNrState *st, const InetNrTables *tab, const InetNrParams *prm, const InetNrRow *rows,
                      int32_t n_rows, int64_t T, const float *x, const int64_t *cur_hid, const InetNrOutputs *out,
                      void *stream);
+
+/* inet_nr_submit (counts form, arr) and inet_nr_step of the same control step in one launch: every lane enqueues its
+   robot's arrivals at the start of the step kernel (NRNet.add_frames, nr_engine.py:466-487, one message at a time in
+   class order), then runs the step. Same results as the two calls. */
+int32_t inet_nr_submit_step(const InetNrState *st, const InetNrTables *tab, const InetNrParams *prm,
+                            const InetNrRow *rows, int32_t n_rows, int64_t T, const float *x, const int64_t *cur_hid,
+                            const InetNrOutputs *out, const InetNrArrivals *arr, void *stream);
 
 /* Enqueue at control step T (T < 0: *st->clock on the device). Single form (counts == NULL): send [E][R] int64 class index (0 = none), det [E][R]
    uint8 or NULL, hid [E] int64 or NULL; accepted [E][R] uint8. Counts form (send == NULL): counts [E][R][NC]

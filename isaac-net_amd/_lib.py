@@ -52,6 +52,11 @@ class InetNrDlState(C.Structure):
                 ("pad", i32)]
 
 
+class InetNrArrivals(C.Structure):
+    _fields_ = [("counts", P), ("sizes", P), ("accepted", P), ("n_cls", i32), ("discard_pdcp", i32),
+                ("pkt_payload", i32), ("pkt_overhead", i32)]
+
+
 class InetWifiState(C.Structure):
     _fields_ = [(n, P) for n in (
         "cap", "cls", "det", "hid", "rem", "f_nact", "f_snr", "f_own", "qlen", "last_snr", "roam_left", "serv",
@@ -123,6 +128,9 @@ def load(path=LIB_PATH):
     lib.inet_nr_reset.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrParams), P, i64, f32, C.POINTER(f32), i32,
                                   P]
     lib.inet_nr_reset.restype = i32
+    lib.inet_nr_submit_step.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrTables), C.POINTER(InetNrParams), P,
+                                        i32, i64, P, P, C.POINTER(InetNrOutputs), C.POINTER(InetNrArrivals), P]
+    lib.inet_nr_submit_step.restype = i32
     lib.inet_nr_dl_step.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrDlState), C.POINTER(InetNrTables),
                                     C.POINTER(InetNrParams), P, i32, i64, P, P]
     lib.inet_nr_dl_step.restype = i32

@@ -207,7 +207,8 @@ int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
 // the argument checks and the launch of one step kernel (UL: dl NULL)
 int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
                            const InetNrParams* prm, const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x,
-                           const int64_t* cur_hid, const InetNrOutputs* out, void* stream) {
+                           const int64_t* cur_hid, const InetNrOutputs* out, const InetNrArrivals* arr,
+                           void* stream) {
     const InetNrParams& p = *prm;
     const InetNrTables& t = *tab;
     if (p.E <= 0 || p.R <= 0 || p.R > INET_NR_MAX_R || p.F <= 0 || p.N <= 0) return INET_NR_EINVAL;
@@ -226,7 +227,10 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
                     : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = inet::STEP_WAVE / rb;
-    inet::StepArgs a{*st, dl, t, p, rows, n_rows, n_data, T, x, cur_hid, *out, rb,
+    InetNrArrivals none{};
+    if (arr && (!arr->counts || !arr->sizes || arr->n_cls <= 0 || (arr->pkt_overhead && arr->pkt_payload <= 0)))
+        return INET_NR_EINVAL;
+    inet::StepArgs a{*st, dl, t, p, rows, n_rows, n_data, arr ? *arr : none, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
                      inet::step_lds_bytes(n_data, p.harq_drop, rb, p.max_tx), (hipStream_t)stream};
     fn(a);
@@ -248,7 +252,14 @@ int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetN
                      int32_t n_rows, int64_t T, const float* x, const int64_t* cur_hid, const InetNrOutputs* out,
                      void* stream) {
     if (!st || !tab || !prm || !out || !x) return INET_NR_EINVAL;
-    return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, stream);
+    return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, nullptr, stream);
+}
+
+int32_t inet_nr_submit_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm,
+                            const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x, const int64_t* cur_hid,
+                            const InetNrOutputs* out, const InetNrArrivals* arr, void* stream) {
+    if (!st || !tab || !prm || !out || !x || !arr) return INET_NR_EINVAL;
+    return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, arr, stream);
 }
 
 int32_t inet_nr_dl_step(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
@@ -259,7 +270,7 @@ int32_t inet_nr_dl_step(const InetNrState* st, const InetNrDlState* dl, const In
         return INET_NR_EINVAL;
     if ((dl->cqi_thr == nullptr) != (dl->cqi_mcs == nullptr) || dl->gnb_proc < 0) return INET_NR_EINVAL;
     InetNrOutputs none{};
-    return launch_step_kernel(st, dl, tab, prm, rows, n_rows, T, x, nullptr, &none, stream);
+    return launch_step_kernel(st, dl, tab, prm, rows, n_rows, T, x, nullptr, &none, nullptr, stream);
 }
 
 int32_t inet_nr_dl_submit(const InetNrState* st, const InetNrDlState* dl, const InetNrParams* prm, int64_t T,

@@ -218,7 +218,7 @@ template <int S, int P, bool IR, bool VREF, int RBT, class LS>
 __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     InetNrState st, LS lk, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
-    int n_ul_max) {
+    int n_ul_max, InetNrArrivals arr) {
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     const int rb = RBT ? RBT : rb_arg;
     const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
@@ -293,6 +293,34 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     olla = ldo(lk.olla, o_r); avg = ldo(lk.avg, o_r);
     qlen = qlen < 0 ? 0 : (qlen > F ? F : qlen);
     if (!act) { sent = 0; floor_ = 0; bsr = 0; sr_t = -1; last_tx = -1; enq = 0; qlen = 0; olla = 0.f; avg = 100.f; }
+    // the step's arrivals (inet_nr_submit_step): FrameQueue.add / NRNet.add_frames of every message, class by class
+    // (queues.py:87-103, nr_engine.py:466-487), at the tail of the FIFO, before the slots
+    if constexpr (!DL) {
+        if (arr.counts != nullptr && act) {
+            int n_acc = 0;
+            const size_t ci0 = ((size_t)ee * R + rr0) * (size_t)arr.n_cls;
+            for (int c = 0; c < arr.n_cls; ++c) {
+                const int nmsg = arr.counts[ci0 + c];
+                float size = arr.sizes[c];
+                if (arr.pkt_overhead) size = size + ceilf(size / (float)arr.pkt_payload) * (float)arr.pkt_overhead;
+                const int nb = (int)rintf(size);
+                for (int k = 0; k < nmsg; ++k) {
+                    bool adm = true;
+                    if (arr.discard_pdcp && qlen > 0 && (int)T - ldo(lk.q_cap, o_fr0) >= pm.timeout) adm = false;
+                    if (adm && qlen < F && size > 0.0f) {
+                        const int fr = qlen * R;
+                        sto(lk.q_cap + fr, o_fr0, (int)T); sto(lk.q_start + fr, o_fr0, enq);
+                        sto(lk.q_end + fr, o_fr0, enq + nb); sto(lk.q_fin + fr, o_fr0, (int)FIN_NONE);
+                        sto(lk.q_meta + fr, o_fr0, (uint32_t)(c + 1) << 8); sto(st.q_hid + fr, o_fr0, 0);
+                        enq += nb;
+                        ++qlen;
+                        ++n_acc;
+                    }
+                }
+            }
+            if (arr.accepted) sto(arr.accepted, o_r, n_acc);
+        }
+    }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         csi[s] = ldo(lk.csi + s * R, o_sr);
@@ -993,6 +1021,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         sto(lk.sent, o_r, sent); sto(lk.floor_, o_r, floor_);
         if constexpr (!DL) { sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t); }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
+        if (arr.counts) sto(lk.enq, o_r, enq);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             sto(lk.csi + s * R, o_sr, csi[s]);
@@ -1054,6 +1083,7 @@ struct StepArgs {
     InetNrParams pm;
     const InetNrRow* rows;
     int n_rows, n_data;
+    InetNrArrivals arr;               // counts == NULL: no arrivals in the launch
     int64_t T;
     const float* x;
     const int64_t* hid;
@@ -1070,10 +1100,11 @@ void launch_step(const StepArgs& a) {
     if (a.dl)
         hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
                            a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
-                           a.n_data);
+                           a.n_data, a.arr);
     else
         hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
-                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data);
+                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
+                           a.arr);
 }
 
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband

@@ -555,9 +555,11 @@ class HipNREngine:
         return o, c
 
     def step(self, t=None, x=None, cur_hid=None, *, snr_db=None, dl_snr_db=None, pathgain_db=None, vel=None,
-             triggers=None, blockers=None):
+             triggers=None, blockers=None, arrivals=None):
         """Advance [t, t+1). x: poses [E,R,2|3] (through the radio) or SNR [E,R] dB; snr_db=: [E,R,S] or [E,R].
-        Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env)."""
+        Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env).
+        arrivals= (extension): counts [E,R,NC] uint8 of this step's messages, enqueued inside the step's launch as
+        submit_counts(counts) would do before it; the dict then also holds arrivals_accepted [E,R] int32."""
         if (dl_snr_db is not None and not self.dl) or pathgain_db is not None or vel is not None or \
                 triggers is not None or blockers is not None:
             raise HipUnsupported("dl_snr_db (without dl=True) / pathgain_db / vel / triggers / blockers need features "
@@ -580,7 +582,16 @@ class HipNREngine:
                 dl = (dkind, dxin, 0)
             else:
                 dl = (kind, xin, 1)
-        o = self._launch_step(T, plan, xin, hid, dl)
+        arr = None
+        if arrivals is not None:
+            cnt = arrivals.to(self.dev, torch.uint8).contiguous()
+            if tuple(cnt.shape[:2]) != (self.E, self.R) or cnt.dim() != 3 or cnt.shape[-1] > len(self.config.msg_sizes):
+                raise ValueError("arrivals must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+            arr = cnt
+            if not legacy:
+                self._last_hid = torch.zeros_like(self._last_hid)
+                hid = self._last_hid
+        o = self._launch_step(T, plan, xin, hid, dl, arrivals=arr)
         self._commit(T, plan, o)
         if legacy:
             return o["newest"], o["det_env"]
@@ -625,7 +636,7 @@ class HipNREngine:
         return dict(rows=rows, n_rows=n_rows, last_rel=last_rel, n_ul=n_ul, fad=fad, kind=kind, key=key,
                     dl_rows=dl_rows[0] if dl_rows else None, n_dl=n_dl)
 
-    def _launch_step(self, T, plan, xin, hid, dl=None):
+    def _launch_step(self, T, plan, xin, hid, dl=None, arrivals=None):
         """Launch the step kernel (T < 0: the kernel reads the device clock) and return the output dict. With the
         downlink, dl = (input kind, input, add dl_snr_offset_db) of the DL step, launched first: it reads the fading
         state and RNG words of the step start, which the UL step then advances."""
@@ -653,9 +664,19 @@ class HipNREngine:
         ev = self.kernel_events
         if ev is not None:
             ev.begin(torch.cuda.current_stream(self.dev))
-        _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
-                                          plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(),
-                                          hid.data_ptr(), C.byref(co), self._stream()), "step")
+        if arrivals is None:
+            _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
+                                              plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(),
+                                              hid.data_ptr(), C.byref(co), self._stream()), "step")
+        else:
+            cfg = self.config
+            o["arrivals_accepted"] = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
+            a = _lib.InetNrArrivals(arrivals.data_ptr(), self._sizes.data_ptr(), o["arrivals_accepted"].data_ptr(),
+                                    arrivals.shape[-1], int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
+                                    cfg.pkt_overhead_bytes)
+            _lib.check(self._lib.inet_nr_submit_step(
+                C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams), plan["rows"].data_ptr(),
+                plan["n_rows"], T, xin.data_ptr(), hid.data_ptr(), C.byref(co), C.byref(a), self._stream()), "step")
         if ev is not None:
             ev.end(torch.cuda.current_stream(self.dev))
         return o

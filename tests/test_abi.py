@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(_lib_path())
     names = declared_functions()
     assert names == sorted(["inet_nr_abi_version", "inet_nr_build_info", "inet_nr_step", "inet_nr_submit",
-                            "inet_nr_reset", "inet_nr_dl_step", "inet_nr_dl_submit", "inet_nr_dl_reset"])
+                            "inet_nr_reset", "inet_nr_dl_step", "inet_nr_dl_submit", "inet_nr_dl_reset",
+                            "inet_nr_submit_step"])
     for n in names:
         assert hasattr(lib, n), n
     lib.inet_nr_abi_version.restype = ctypes.c_int32
@@ -48,8 +49,8 @@ def test_library_exports_every_declared_symbol():
     assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 2
 
 
-STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetNrDlState", "InetWifiState",
-           "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
+STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetNrDlState",
+           "InetNrArrivals", "InetWifiState", "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
 
 
 def test_ctypes_layout_matches_header():

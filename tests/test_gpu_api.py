@@ -143,3 +143,41 @@ def test_matches_oracle_with_submit_counts():
         fc.step(s, og, oo, tol)
     print(f"integer flips {fc.flips}; float issues {fc.float_bad}", flush=True)
     assert len(fc.flips) <= 1 and not fc.float_bad
+
+
+@pytest.mark.parametrize("variant", ["plain", "pdcp_overhead_small_fifo"])
+def test_fused_arrivals_equal_submit_counts_then_step(variant):
+    """step(arrivals=counts) (inet_nr_submit_step: the enqueue inside the step's launch) leaves every output and
+    every state tensor bitwise equal to submit_counts(counts) followed by step(), over steps with overflow,
+    PDCP discard and per-packet overhead, and a partial reset."""
+    kw = dict(control_step_ms=25.0, n_harq=8, frame_buffer=8, fading_rician=True, rician_k_db=3.0)
+    if variant != "plain":
+        kw.update(frame_buffer=3, discard="pdcp_arrival", timeout_steps=2, pkt_overhead_bytes=40,
+                  pkt_payload_bytes=600)
+    cfg = small_cfg(**kw)
+    E, R = 6, 32
+    a = P.make_engine("L2", E, R, DEV, cfg, seed=5)
+    b = P.make_engine("L2", E, R, DEV, cfg, seed=5)
+    rs = np.random.default_rng(3)
+    for s in range(12):
+        if s == 7:
+            a.reset([1, 4])
+            b.reset([1, 4])
+        counts = torch.from_numpy(np.stack([rs.poisson(1.2, (E, R)), rs.poisson(0.4, (E, R))], -1)
+                                  .astype(np.uint8)).to(DEV)
+        x = torch.from_numpy(rs.uniform(0, 100, (E, R, 2)).astype(np.float32)).to(DEV)
+        acc_a = a.submit_counts(counts)
+        oa = a.step(None, x)
+        ob = b.step(None, x, arrivals=counts)
+        assert torch.equal(acc_a, ob["arrivals_accepted"]), s
+        for k in oa:
+            assert torch.equal(oa[k], ob[k]) or (oa[k].is_floating_point() and
+                                                 torch.equal(oa[k].isnan(), ob[k].isnan()) and
+                                                 torch.equal(oa[k].nan_to_num(), ob[k].nan_to_num())), (s, k)
+        sa, sb = a.state_dict(), b.state_dict()
+        for k in sa:
+            va, vb = sa[k], sb[k]
+            if va.is_floating_point():
+                assert torch.equal(va.nan_to_num(), vb.nan_to_num()), (s, k)
+            else:
+                assert torch.equal(va, vb), (s, k)
