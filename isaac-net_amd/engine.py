@@ -755,9 +755,10 @@ class HipNREngine:
             out.update({"bsr": torch.zeros_like(out["sent"]), "sr_t": torch.full_like(out["sent"], -1)})
         return {f"{pre}.{k}": v for k, v in out.items()}
 
-    def state_dict(self):
-        """Every state tensor in the reference's names, shapes and dtypes (isaac_net/core/nr_fast.py:41-75), on the
-        engine's device. Frame fields of empty queue slots are unspecified (the reference leaves stale values)."""
+    def owner_state(self):
+        """Every state tensor under the reference's owner keys ("ul.sent", "net.h", "eng.epoch", "rng.ctr[2]": the
+        equivalence-test form of isaac_net/core/nr_fast.py:41-75, state_dict(eng)), reference shapes and dtypes, on
+        the engine's device. Frame fields of empty queue slots are unspecified (the reference leaves stale values)."""
         st, cfg = self.st, self.config
         L = lambda x: x.long()  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
@@ -814,9 +815,9 @@ class HipNREngine:
             st["q_hid"].copy_(rs(I(g("q.hid"))))
         st["q_meta"].copy_(rs(I(qm)))
 
-    def load_state_dict(self, sd, T=None, last_g=None):
-        """Load reference-layout state (the keys of state_dict(); tensors on any device) into the device buffers;
-        T / last_g set the host clock and the last fading slot (teacher forcing)."""
+    def load_owner_state(self, sd, T=None, last_g=None):
+        """Load owner-key state (the keys of owner_state(); tensors on any device) into the device buffers; T / last_g
+        set the host clock and the last fading slot (teacher forcing)."""
         st, cfg, d = self.st, self.config, self.dev
         g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
@@ -844,6 +845,129 @@ class HipNREngine:
             ep = st["epoch"]
             self._uniform_epoch = int(ep[0]) if bool((ep == ep[0]).all()) else None
         self.last_g = last_g
+
+
+    # ------------------------------------------------------------------ checkpoints (core/checkpoint.py:103-143)
+    _CK_ENG = {"eng.epoch": "epoch", "eng._last_snr": "_last_snr", "eng._last_hid": "_last_hid",
+               "rng.episode": "net.rng.episode", "rng.ctr[1]": "net.rng.ctr[1]", "rng.ctr[2]": "net.rng.ctr[2]"}
+
+    def _ck_key(self, k):
+        """Owner key -> the key of the reference's checkpoint (the attribute path from NREngine)."""
+        if k.startswith(("ul.", "dl.")):
+            return "net." + k
+        return self._CK_ENG.get(k, k)
+
+    def _field_keys(self):
+        """[(checkpoint key prefix, field index)] of the radio's shadowing fields (RadioMC / TR38901Channel)."""
+        if self._n_fields == 3:
+            return [("radio.ch.sf_los", 0), ("radio.ch.sf_nlos", 1), ("radio.ch.los_field", 2)]
+        return [("radio", 0)] if self._n_fields == 1 else []
+
+    def state_dict(self):
+        """The engine's checkpoint: a flat {key: tensor | host value} under the keys of the reference engine's
+        state_dict (core/checkpoint.py collect on NREngine: "net.ul.sent", "net.rng.ctr[2]", "radio.ch.sf_los.k",
+        "T", ...) for the state this engine keeps; counters as the reference keeps them (totals, per-env PRBs and
+        HARQ histograms). Tensors are snapshots (clones) on the engine's device."""
+        cfg, st, E = self.config, self.st, self.E
+        out = {self._ck_key(k): v.clone() for k, v in self.owner_state().items()}
+        out["net.rng.env"] = st["env_id"].long().clone()
+        for pre, fi in self._field_keys():
+            f = st["field"][:, fi]
+            out[pre + ".k"] = f[None, ..., :2].clone()
+            out[pre + ".phi"] = f[None, ..., 2].clone()
+        links = [("ul", st, self._ul_slots_run)] + ([("dl", self.dst, self._dl_slots_run)] if self.dl else [])
+        for name, ls, n_slots in links:
+            c = ls["ctr"]
+            for i, k in enumerate(CTR_NAMES):
+                out[f"net.{name}.ctr[{k}]"] = c[:, i].sum().float()
+            out[f"net.{name}.ctr[prb_avail]"] = torch.tensor(float(sum(cfg.subband_prbs)) * E * n_slots,
+                                                             device=self.dev)
+            h = ls["hist"].float()
+            out[f"net.{name}.ntx_hist"] = h[:, 0].sum(0)
+            out[f"net.{name}.rv_tx"] = h[:, 1].clone()
+            out[f"net.{name}.rv_fail"] = h[:, 2].clone()
+            out[f"net.{name}.prb_used_env"] = c[:, 9].float()
+        out.update({"T": int(self.T), "net.last_g": self.last_g, "_uniform_epoch": self._uniform_epoch,
+                    "E": E, "R": self.R, "F": self.F, "seed": self.seed,
+                    "net.rng.s0": int(self._cparams.seed_key) & M32})
+        return out
+
+    def load_state_dict(self, sd, strict=True, T=None, last_g=None):
+        """Restore a checkpoint in place: this engine's state_dict(), or the reference engine's (the same keys;
+        keys of the reference that hold no state here are skipped: torch generators, trace hooks, statistics, the
+        queue's f_nact / f_snr / f_own fields, host configuration values). Per-env counters come back as the
+        reference keeps them: totals (on env 0) and per-env PRBs and HARQ histograms. strict: raise if state this
+        engine keeps is missing or has another shape. The owner-key form of owner_state() is accepted too (with
+        T / last_g as in load_owner_state). Returns self."""
+        if "ul.sent" in sd and "net.ul.sent" not in sd:
+            self.load_owner_state(sd, T=T, last_g=last_g)
+            return self
+        cfg, st, d = self.config, self.st, self.dev
+        mine = self.owner_state()
+        owner, missing = {}, []
+        for k, v in mine.items():
+            ck = self._ck_key(k)
+            if ck in sd:
+                val = torch.as_tensor(sd[ck])
+                if strict and tuple(val.shape) != tuple(v.shape):
+                    raise KeyError(f"load_state_dict: {ck} has shape {tuple(val.shape)}, the engine {tuple(v.shape)}")
+                owner[k] = val
+            elif k.endswith((".bsr", ".sr_t")) and k.startswith("dl."):
+                owner[k] = v                                 # constant in the DL link
+            else:
+                missing.append(ck)
+        if missing:
+            if strict:
+                raise KeyError("load_state_dict: missing from the state dict: " + ", ".join(missing))
+            for k, v in mine.items():
+                owner.setdefault(k, v)
+        g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+        if "net.rng.env" in sd:
+            st["env_id"].copy_(g("net.rng.env").to(torch.int32))
+        for pre, fi in self._field_keys():
+            if pre + ".k" in sd:
+                st["field"][:, fi, :, :2].copy_(g(pre + ".k")[0])
+                st["field"][:, fi, :, 2].copy_(g(pre + ".phi")[0])
+            elif strict:
+                raise KeyError(f"load_state_dict: missing from the state dict: {pre}.k")
+        if "net.rng.s0" in sd:
+            s0 = int(sd["net.rng.s0"])
+            self._cparams.seed_key = C.c_int32(s0 - (1 << 32) if s0 >= 1 << 31 else s0).value
+        links = [("ul", st)] + ([("dl", self.dst)] if self.dl else [])
+        for name, ls in links:
+            if f"net.{name}.ctr[tb_new]" not in sd:
+                continue
+            c = torch.zeros_like(ls["ctr"])
+            for i, k in enumerate(CTR_NAMES):
+                c[0, i] = int(round(float(sd[f"net.{name}.ctr[{k}]"])))
+            if f"net.{name}.prb_used_env" in sd:
+                c[:, 9] = g(f"net.{name}.prb_used_env").round().long()
+            ls["ctr"].copy_(c)
+            h = torch.zeros_like(ls["hist"])
+            h[0, 0] = g(f"net.{name}.ntx_hist").round().long()
+            h[:, 1] = g(f"net.{name}.rv_tx").round().long()
+            h[:, 2] = g(f"net.{name}.rv_fail").round().long()
+            ls["hist"].copy_(h)
+            w = float(sum(cfg.subband_prbs)) * self.E
+            n_slots = int(round(float(sd[f"net.{name}.ctr[prb_avail]"]) / w))
+            if name == "ul":
+                self._ul_slots_run = n_slots
+            else:
+                self._dl_slots_run = n_slots
+        if "T" in sd:
+            T = int(sd["T"])
+        elif strict:
+            raise KeyError("load_state_dict: missing from the state dict: T")
+        self.load_owner_state(owner, T=T, last_g=sd.get("net.last_g", last_g))
+        if "_uniform_epoch" in sd:
+            self._uniform_epoch = sd["_uniform_epoch"]
+        return self
+
+
+def state_dict(eng):
+    """{owner key: tensor} of every state tensor of a hip NR engine: the form of the reference's
+    nr_fast.state_dict(eng) (isaac_net/core/nr_fast.py:61-67), used by the equivalence tests."""
+    return eng.owner_state()
 
 
 class GraphStep:

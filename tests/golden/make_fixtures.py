@@ -309,6 +309,42 @@ def run_wifi_case(name, c):
     print(name, "arrays:", len(out))
 
 
+def checkpoint_vectors(name, k_steps=10):
+    """The reference engine's checkpoint (core/checkpoint.py:103-143 collect: NREngine.state_dict()) of a golden
+    case after k_steps steps, with the case's own inputs: tensors under "ck/<key>", host values as JSON."""
+    NRConfig, make_engine, state_dict, Requests = _ref()
+    c = CASES[name]
+    cfg = NRConfig(**c["cfg"], seed=0)
+    E, R = c["E"], c["R"]
+    eng = make_engine("L2", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
+    x, counts, *dl = _inputs(name, c)
+    dl_counts = dl[0] if dl else None
+    for s in range(k_steps):
+        assert not any(s == r for r in c["resets"])
+        for ci in range(counts.shape[-1]):
+            n = torch.from_numpy(counts[s, :, :, ci])
+            for i in range(int(n.max())):
+                eng.submit(None, Requests(send=torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n))))
+        if dl_counts is not None:
+            for ci in range(dl_counts.shape[-1]):
+                n = torch.from_numpy(dl_counts[s, :, :, ci])
+                for i in range(int(n.max())):
+                    nb = torch.where(n > i, torch.full(n.shape, c["dl_sizes"][ci]), torch.zeros(n.shape))
+                    eng.add_dl_frames(None, nb, torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n)))
+        eng.step(None, torch.from_numpy(x[s]))
+    sd = eng.state_dict()
+    out, host = {}, {}
+    for k, v in sd.items():
+        if torch.is_tensor(v):
+            out["ck/" + k] = _np(v)
+        else:
+            host[k] = v if not isinstance(v, tuple) else list(v)
+    out["host_json"] = np.frombuffer(json.dumps(host).encode(), dtype=np.uint8)
+    out["k_steps"] = np.int64(k_steps)
+    np.savez_compressed(os.path.join(HERE, f"ckpt_{name}.npz"), **out)
+    print(name, "checkpoint:", len(sd), "entries,", len(host), "host values")
+
+
 def eventsim_vectors():
     """Saturation statistics of the reference's CSMA/CA event simulator (core/wifi/eventsim.py:56-186) for the
     exchange times of the DCF level (802.11ax 20 MHz MCS 11, 1472-byte MSDUs without aggregation, legacy DCF
@@ -413,6 +449,8 @@ if __name__ == "__main__":
     for n in names:
         if n == "eventsim":
             eventsim_vectors()
+        elif n.startswith("ckpt_"):
+            checkpoint_vectors(n[len("ckpt_"):])
         elif n in WIFI_CASES:
             run_wifi_case(n, WIFI_CASES[n])
         else:

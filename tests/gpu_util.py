@@ -126,7 +126,7 @@ def teacher_forced(P, name, dev="cuda:0"):
         x = to(ref["x"][s])
         o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x)
         set_radio_bound(ref, s, cfg, eng, kind)
-        bi, bf, robots = compare(ref, s, o, eng.state_dict(), E, R)
+        bi, bf, robots = compare(ref, s, o, eng.owner_state(), E, R)
         n_bad += int(robots.sum())
         for k, v in bi.items():
             keys_i[k] = keys_i.get(k, 0) + v

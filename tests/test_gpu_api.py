@@ -66,7 +66,7 @@ def test_submit_accepts_until_the_buffer_is_full():
     assert a1.tolist() == [[True, False, True], [True, True, False]]
     assert a2.tolist() == a1.tolist()
     assert not bool(a3.any())
-    st = eng.state_dict()
+    st = eng.owner_state()
     assert st["ul.q.enq"].tolist() == [[3000, 0, 600], [600, 600, 0]]
     assert st["ul.q.cls"][0, 0, :2].tolist() == [1, 1]
 
@@ -174,7 +174,7 @@ def test_fused_arrivals_equal_submit_counts_then_step(variant):
             assert torch.equal(oa[k], ob[k]) or (oa[k].is_floating_point() and
                                                  torch.equal(oa[k].isnan(), ob[k].isnan()) and
                                                  torch.equal(oa[k].nan_to_num(), ob[k].nan_to_num())), (s, k)
-        sa, sb = a.state_dict(), b.state_dict()
+        sa, sb = a.owner_state(), b.owner_state()
         for k in sa:
             va, vb = sa[k], sb[k]
             if va.is_floating_point():

@@ -42,7 +42,7 @@ def test_graph_replay_matches_eager():
         assert a.T == b.T
         for k in oa:
             assert _same(oa[k], ob[k]), (s, k)
-        sa, sb = a.state_dict(), b.state_dict()
+        sa, sb = a.owner_state(), b.owner_state()
         for k in sa:
             if torch.is_tensor(sa[k]):
                 assert _same(sa[k], sb[k]), (s, k)

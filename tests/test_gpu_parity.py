@@ -40,7 +40,7 @@ def test_free_running_bit_exact(name):
             if not np.array_equal(mine, ref[f"s{s:03d}/accepted"]):
                 bad.append((s, "accepted"))
         set_radio_bound(ref, s, cfg, eng, kind)
-        bi, bf, _ = compare(ref, s, o, eng.state_dict(), E, R)
+        bi, bf, _ = compare(ref, s, o, eng.owner_state(), E, R)
         if bi or bf:
             bad.append((s, bi, bf))
 

@@ -35,7 +35,7 @@ def test_rl_scale_invariants_and_prefix_parity():
         tol = sinr_bound(wl.poses[s][:E_chk].cpu().numpy(), eng.st["field"][:E_chk, fi].cpu().numpy(), sig, amp,
                          oo["sinr_db"].numpy())
         fc.step(s, {k: v[:E_chk] for k, v in og.items() if v.dim() >= 2}, oo, tol)
-        st = eng.state_dict()
+        st = eng.owner_state()
         qlen = eng.st["qlen"]
         assert int(qlen.max()) <= cfg.frame_buffer and int(qlen.min()) >= 0
         cap = st["ul.q.cap"]
