@@ -133,17 +133,26 @@ class NRConfig:
     los_source: str = "stochastic"
     los_soft: bool = False
     gnb_antenna: str = "isotropic"
-    # ---- cells (config.py:682-700)
+    # ---- cells, interference, power control and handover (config.py:682-717)
     n_cells: int = 1
     cell_layout: str = "custom"
     cell_positions_m: tuple = ((0.0, 0.0),)
     cell_isd_m: float = 100.0
     cell_center_m: tuple = (75.0, 75.0)
     cell_arena_m: float = 150.0
+    ul_interference: bool = True      # thermal noise only: same-slot other-cell UL interference
+    dl_interference: bool = True
+    li_alpha: float = 1.0             # link adaptation reads an EWMA of the measured N+I (1 = the previous slot's)
     ul_pc: bool | None = None
     ul_pc_p0_dbm: float = -88.0
     ul_pc_alpha: float = 1.0
     ul_tpc: bool = False
+    a3_offset_db: float = 0.0         # A3: neighbour > serving + offset + hysteresis, held for the time-to-trigger
+    a3_hyst_db: float = 3.0
+    a3_ttt_ms: float = 300.0
+    ho_interruption_ms: float = 40.0  # a robot is not scheduled for this long after its handover
+    ho_rlc: str = "carry"             # "carry": queued frames continue at the target; "flush": they are dropped
+    a3_min_target_rsrp_dbm: float | None = None
     rlf: bool = False
     rach: bool = False
     drx: bool = False
@@ -175,7 +184,7 @@ class NRConfig:
         assert self.mcs_table in (1, 2) and self.n_harq >= 1 and self.max_harq_tx >= 1
         assert sum(self.special_split) == 14 and self.duplex in ("tdd", "fdd")
         assert self.frame_buffer >= 1 and self.timeout_steps >= 1 and self.control_step_ms > 0
-        assert len(self.msg_sizes) >= 1 and 1 <= self.n_cells <= 7
+        assert len(self.msg_sizes) >= 1 and 1 <= self.n_cells <= 7 and self.ho_rlc in ("carry", "flush")
         self.msg_sizes = tuple(float(s) for s in self.msg_sizes)
         self.cell_positions_m = tuple(tuple(float(v) for v in p) for p in self.cell_positions_m)
         if self.channel.startswith("tr38901_"):           # shorthand, as config.py TR38901_SHORT

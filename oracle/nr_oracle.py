@@ -1,26 +1,31 @@
-"""CPU oracle of the NR per-control-step engine (uplink; downlink with dl=True).  TEST INFRASTRUCTURE ONLY.
+"""CPU oracle of the NR per-control-step engine (uplink; downlink with dl=True; several cells, uplink only).
+TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
 checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
 
-A from-scratch torch-CPU restatement of isaac-net's single-cell NR engine, reference backend:
+A from-scratch torch-CPU restatement of isaac-net's NR engine, reference backend:
   NREngine        core/engine.py:319-960   (clock, submit, add_dl_frames, step, partial reset)
-  NRNet           core/nr_engine.py:171-888 (reset, fading AR(1) + Rician, step_rx, step, _finish)
+  NRNet           core/nr_engine.py:171-888 (reset, fading AR(1) + Rician, step_rx, step, _finish; with several cells
+                  step_cells, _ul_ici, _handover, _pc_backoff, serving_sinr_db)
+  CellAssociation core/radio.py:303-437 (max-RSRP attach, A3 plan / switch, handover interruption; no RLF)
   UlMac/MacLink   core/mac_ul.py:58-260, core/mac.py:65-616 (lumped SR/grants, PF/maxCI/RR scheduling, retx admission,
                   RBG allocation, EESM / mean-dB link adaptation, HARQ cc/none/ir_lena, rlc_am/drop, OLLA, PF average,
                   RLC in-order delivery, end_step, compact)
   DlMac           core/mac_dl.py:19-49 (CQI report "mcs" / "38214", estimate, decode SINR, HARQ-ACK timing via K1)
   FrameQueue      core/queues.py:36-143
   NRRng           core/nr_rng.py, core/proto/rng.py (counter hash, Box-Muller)
-  RadioMC         core/radio.py:59-277 (log_distance), core/channels/models.py:34-167 + tr38901.py (deterministic LOS
+  RadioMC         core/radio.py:59-277 (log_distance, C cells), core/channels/models.py:34-167 + tr38901.py (deterministic LOS
                   state "los" / "nlos"), core/channels/fields.py:38-64 (plane-wave shadowing)
 The element-wise operations, the reduction calls and their order are those of the reference, so that on the same
 CPU the oracle is bitwise equal to the reference path (pinned by the golden trajectories under tests/golden/).
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
 
 Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state and outputs
-after every step of six uplink and three downlink scenarios) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF
-metric is not implemented here (refused), and `whole_band` UL power is not implemented (refused).
+after every step of six uplink, three downlink and two three-cell scenarios) except what those scenarios do not reach:
+the "pf_wideband" / "wideband" PF metric is not implemented here (refused), `whole_band` UL power is not implemented
+(refused), and of the multi-cell options the RSRP admission floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are
+restated but parity unpinned (no trajectory sets them).
 """
 from __future__ import annotations
 
@@ -278,15 +283,18 @@ def eval_plane_waves(pos, k, phi, amp):
 
 
 class Radio:
-    """RadioMC at one cell for channel "log_distance" or "tr38901" with a deterministic LOS state."""
+    """RadioMC (radio.py:59-277) for C = cfg.n_cells cells, channel "log_distance" or "tr38901" with a deterministic
+    LOS state. One plane-wave field per (cell, env): the RESET uniforms of a draw are [E, C*K], element c*K + k
+    (channels/fields.py:28-31)."""
 
     def __init__(self, cfg, E, rng):
         from isaac_net_amd.channels import SCENARIOS, SIGMA_SF, breakpoint_m
         self.cfg, self.E, self.rng = cfg, E, rng
         self.gnb = torch.tensor(cfg.gnb_xy(), dtype=torch.float32)
+        self.C = self.gnb.shape[0]
         K = cfg.shadow_modes
         self.model = cfg.channel
-        assert cfg.n_cells == 1 and cfg.shadow_white_frac == 0 and not cfg.blockage
+        assert cfg.shadow_white_frac == 0 and not cfg.blockage
         if self.model == "log_distance":
             self.amp = cfg.shadow_sigma_db * math.sqrt(2 / K)
         else:
@@ -303,15 +311,15 @@ class Radio:
         self.fields = self.draw()
 
     def draw(self):
-        cfg, K = self.cfg, self.cfg.shadow_modes
+        cfg, K, C = self.cfg, self.cfg.shadow_modes, self.C
         rng = self.rng
         if self.model == "log_distance":
-            return [plane_waves(lambda i: rng.reset_uniform(LOG_DISTANCE_STREAM + i, K).view(self.E, 1, K),
+            return [plane_waves(lambda i: rng.reset_uniform(LOG_DISTANCE_STREAM + i, C * K).view(self.E, C, K),
                                 cfg.shadow_acf, cfg.shadow_dcorr_m)]
         out = []
         for j, dc in enumerate(self.dcorr):          # sf_los, sf_nlos, los_field (models.py:78-80)
             st = TR38901_STREAM + 3 * j
-            out.append(plane_waves(lambda i, st=st: rng.reset_uniform(st + i, K).view(self.E, 1, K), "exp", dc))
+            out.append(plane_waves(lambda i, st=st: rng.reset_uniform(st + i, C * K).view(self.E, C, K), "exp", dc))
         return out
 
     def reset(self, m):
@@ -320,11 +328,13 @@ class Radio:
                        for (k1, p1), (k2, p2) in zip(self.fields, new)]
 
     def pathgain(self, pos):
-        """Large-scale gain [E,R] dB of the poses (radio.py:275-277): rx_dbm - ue_tx_dbm."""
-        return (self.rx_dbm(pos) - self.cfg.ue_tx_dbm)[..., 0]
+        """Large-scale gain dB of the poses (radio.py:275-277): rx_dbm - ue_tx_dbm, [E,R] at one cell, [E,R,C]
+        with several."""
+        pg = self.rx_dbm(pos) - self.cfg.ue_tx_dbm
+        return pg[..., 0] if self.C == 1 else pg
 
     def rx_dbm(self, pos):
-        """Received power [E,R,1] dBm of the poses (radio.py:238-272, models.py:137-167)."""
+        """Received power [E,R,C] dBm of the poses (radio.py:238-272, models.py:137-167)."""
         cfg = self.cfg
         if self.model == "log_distance":
             d = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
@@ -456,6 +466,34 @@ class Link:
         dropped = valid & self.q_lost & (self.q_end <= self.ack_ptr()[..., None]) & ~timed
         return delivered, timed, dropped
 
+    def handover(self, ho, flush, drop):
+        """MacLink.handover (mac.py:557-581) of the robots ho [E,R]: undecoded HARQ processes restart their combining
+        at the target, or (drop = RLC UM, or flush) their frames are lost; flush also drops every queued frame not
+        yet completed and skips the unsent bytes. OLLA, the PF average and the CSI start afresh. Returns the number
+        of frames newly marked lost."""
+        own = (self.h_state == 1) & ho[..., None]
+        lost = 0
+        if drop or flush:
+            valid = (self.q_cap >= 0) & torch.isinf(self.q_fin) & ~self.q_lost
+            ov = (own[..., None, :] & (self.q_start[..., None] < self.h_hi[..., None, :])
+                  & (self.q_end[..., None] > self.h_lo[..., None, :])).any(-1) & valid
+            if flush:
+                ov = ov | (valid & ho[..., None])
+                self.sent = torch.where(ho, self.q_enq, self.sent)
+            lost = int(ov.sum())
+            self.q_lost = self.q_lost | ov
+            self.h_state = torch.where(own, torch.zeros_like(self.h_state), self.h_state)
+        else:
+            self.h_ntx = torch.where(own, torch.zeros_like(self.h_ntx), self.h_ntx)
+            self.h_comb = torch.where(own, torch.zeros_like(self.h_comb), self.h_comb)
+            self.h_lexp = torch.where(own, torch.full_like(self.h_lexp, -float("inf")), self.h_lexp)
+            self.h_nrb = torch.where(own, torch.zeros_like(self.h_nrb), self.h_nrb)
+        for n in ("olla", "avg", "csi"):
+            x = getattr(self, n)
+            setattr(self, n, torch.where(ho.view(*ho.shape, *([1] * (x.dim() - 2))),
+                                         torch.full_like(x, self.INIT[n]), x))
+        return lost
+
     def compact(self, gone):
         """MacLink.compact (mac.py:598-616) with FrameQueue.remove / floor (queues.py:105-110, 140-143)."""
         F = self.F
@@ -474,17 +512,79 @@ class Link:
             setattr(self, n, torch.where(dead, torch.full_like(x, v), x))
 
 
+def pick(x, idx):
+    """x [E,R,C,...] at cell idx [E,R] -> [E,R,...] (radio.py:45-48)."""
+    ix = idx.view(*idx.shape, 1, *([1] * (x.dim() - 3))).expand(*idx.shape, 1, *x.shape[3:])
+    return x.gather(2, ix).squeeze(2)
+
+
+class Association:
+    """CellAssociation without radio link failure (radio.py:303-437): max-RSRP attach after a reset (associate), the
+    A3 condition evaluated once per control step with the exact slot at which the handover fires (plan), the switch
+    and the handover interruption (schedulable). RSRP here is rx = path gain + ue_tx_dbm [E,R,C]."""
+
+    INIT = {"serv": 0, "a3_cand": -1, "a3_cnt": 0, "ho_end": 0, "n_ho": 0}
+
+    def __init__(self, cfg, E, R, C):
+        self.cfg, self.C, self.K = cfg, C, cfg.slots_per_step
+        self.ttt = int(round(cfg.a3_ttt_ms / cfg.slot_ms))
+        self.ho_int = int(round(cfg.ho_interruption_ms / cfg.slot_ms))
+        floor = cfg.a3_min_target_rsrp_dbm
+        self.floor_rx = None if floor is None else floor - (cfg.gnb_tx_dbm - 10 * math.log10(12 * cfg.nprb)
+                                                            - cfg.ue_tx_dbm)
+        for n, v in self.INIT.items():
+            setattr(self, n, torch.full((E, R), v, dtype=torch.long))
+        self.pending = torch.ones(E, dtype=torch.bool)
+
+    def reset(self, m):
+        for n, v in self.INIT.items():
+            setattr(self, n, where_env(m, v, getattr(self, n)))
+        self.pending = torch.where(m, torch.ones_like(self.pending), self.pending)
+
+    def associate(self, rx):
+        self.serv = torch.where(self.pending[:, None], rx.argmax(-1), self.serv)
+        self.pending = torch.zeros_like(self.pending)
+
+    def plan(self, rx):
+        """(fire slot inside this control step [E,R] or -1, target cell [E,R]); at slot k the condition has held
+        cnt + k + 1 slots, so it fires at k = ttt - cnt - 1."""
+        cfg = self.cfg
+        rs = pick(rx, self.serv)
+        best, bc = rx.masked_fill(onehot(self.serv, self.C), -float("inf")).max(-1)
+        cond = best > rs + cfg.a3_offset_db + cfg.a3_hyst_db
+        if self.floor_rx is not None:
+            cond = cond & (best >= self.floor_rx)
+        cnt = torch.where(cond & (bc == self.a3_cand), self.a3_cnt, torch.zeros_like(self.a3_cnt))
+        k_fire = (self.ttt - cnt - 1).clamp(min=0)
+        fire = cond & (k_fire < self.K)
+        self.a3_cnt = torch.where(cond & ~fire, cnt + self.K, torch.zeros_like(cnt))
+        self.a3_cand = torch.where(cond & ~fire, bc, torch.full_like(bc, -1))
+        return torch.where(fire, k_fire, torch.full_like(k_fire, -1)), bc
+
+    def switch(self, ho, target, g):
+        self.serv = torch.where(ho, target, self.serv)
+        self.ho_end = torch.where(ho, g + self.ho_int, self.ho_end)
+        self.n_ho = self.n_ho + ho.long()
+
+    def schedulable(self, g):
+        return g >= self.ho_end
+
+
 class OracleEngine:
-    """NREngine + NRNet + UlMac / DlMac restated for one cell, lumped UL grants (see the module docstring)."""
+    """NREngine + NRNet + UlMac / DlMac restated (see the module docstring): one cell with uplink and optional
+    downlink, or several cells (NRNet.step_cells) with the uplink only, lumped UL grants."""
 
     def __init__(self, E, R, cfg, seed=0, tabs=None, tabs_dl=None):
         from isaac_net_amd.phy import PhyTables, cqi_tables
         self.cfg, self.E, self.R = cfg, E, R
         self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
-        assert cfg.n_cells == 1 and cfg.ul and cfg.ul_grant_model == "lumped"
+        self.C = C = cfg.n_cells
+        assert cfg.ul and cfg.ul_grant_model == "lumped"
+        assert C == 1 or not (cfg.dl or cfg.rlf), "several cells: uplink only, no radio link failure"
+        assert C > 1 or not cfg.ul_pc_on, "UL power control at one cell is not restated"
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay" and cfg.ul_retx_sched == "ofdma"
-        assert cfg.ul_amc_alloc == "current" and not cfg.ul_pc_on and cfg.ul_power == "allocated"
+        assert cfg.ul_amc_alloc == "current" and not cfg.ul_tpc and cfg.ul_power == "allocated"
         assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
@@ -515,7 +615,16 @@ class OracleEngine:
                 thr, cm = cqi_tables(self.tabs_dl, cfg.mcs_table)
                 self.cqi = (torch.from_numpy(thr), torch.from_numpy(cm))
             self.dl_newest = torch.full((E, R), -1, dtype=torch.long)
-        self.h = torch.zeros(E, R, S, 2)
+        self.pc_on = cfg.ul_pc_on
+        self.pc_backoff = self.phr_snr = None
+        if C > 1:                                        # NRNet._init_cells (nr_engine.py:216-230)
+            self.assoc = Association(cfg, E, R, C)
+            self.use_int = cfg.noise_model == "thermal" and cfg.ul_interference
+            self.noise_mw = 10 ** (cfg.noise_dbm_per_prb("gnb") / 10)
+            self.ref_db = 10 * math.log10(cfg.snr_ref_prbs)
+            self.member = self.sched_ok = self._gain_c = self._ni_la_ul = None
+        self.cdim = () if C == 1 else (C,)
+        self.h = torch.zeros(E, R, *self.cdim, S, 2)
         self._reset_net(None)
 
     @property
@@ -534,28 +643,39 @@ class OracleEngine:
         if self.dl is not None:
             self.dl_newest = where_env(m, -1, self.dl_newest)
         self.rng.reset_mask(mask)
-        h0 = self.rng.reset_normal(H0 << 16, R * S * 2).view(E, R, S, 2) / math.sqrt(2)
+        cd = self.cdim
+        h0 = self.rng.reset_normal(H0 << 16, R * math.prod(cd) * S * 2).view(E, R, *cd, S, 2) / math.sqrt(2)
         if mask is None:
             self.h = h0
             self.last_g = None
         else:
             self.h = where_env(m, h0, self.h)
         if self.rician:
-            u = self.rng.reset_uniform(KPHI << 16, R)
-            self.rng.reset_normal(KFAC << 16, R)
-            phi = (2 * math.pi) * u.view(E, R)
+            n = R * math.prod(cd)
+            u = self.rng.reset_uniform(KPHI << 16, n)
+            self.rng.reset_normal(KFAC << 16, n)
+            phi = (2 * math.pi) * u.view(E, R, *cd)
             spec = torch.stack((torch.cos(phi), torch.sin(phi)), -1)
-            k_los = torch.full((E, R), 10 ** (self.cfg.rician_k_db / 10))
+            k_los = torch.full((E, R, *cd), 10 ** (self.cfg.rician_k_db / 10))
             if mask is None:
                 self.spec, self.k_los = spec, k_los
                 self.k_in, self.k_lin, self.k_from = k_los.clone(), k_los.clone(), k_los.clone()
-                self.k_g0 = torch.zeros((E, R), dtype=torch.long)
+                self.k_g0 = torch.zeros((E, R, *cd), dtype=torch.long)
             else:
                 self.spec = where_env(m, spec, self.spec)
                 self.k_los = where_env(m, k_los, self.k_los)
                 for n in ("k_in", "k_lin", "k_from"):
                     setattr(self, n, where_env(m, k_los, getattr(self, n)))
                 self.k_g0 = where_env(m, 0, self.k_g0)
+        if self.C > 1:                                   # NRNet._reset_cells (nr_engine.py:424-438)
+            self.assoc.reset(m)
+            if mask is None:
+                self.ni_ul = torch.full((E, self.C, S), self.noise_mw)
+                self.ioN = torch.zeros(E)
+                self.ioN_n = 0
+                self._pg = torch.zeros(E, R, self.C)
+            else:
+                self.ni_ul = where_env(m, self.noise_mw, self.ni_ul)
 
     def reset(self, env_ids=None):
         if env_ids is None:
@@ -640,7 +760,13 @@ class OracleEngine:
         T = self.T
         hid = self.last_hid
         dl_ref = None
-        if snr_db is None and x is not None and x.dim() == 3:
+        if self.C > 1:                                   # engine.py:918-924 with NRNet.step_cells
+            assert snr_db is None and x is not None and x.dim() == 3, "several cells: pass poses [E,R,2]"
+            if self.radio is None:
+                self.radio = Radio(cfg, self.E, self.rng)
+            out = self._net_step_cells(T, self.radio.pathgain(x), hid)
+            snr = self.serving_sinr_db()
+        elif snr_db is None and x is not None and x.dim() == 3:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
@@ -658,7 +784,8 @@ class OracleEngine:
             if self.dl is not None:                      # NRNet.step (nr_engine.py:651-653)
                 dref = dl_snr_db if dl_snr_db is not None else xs + cfg.dl_snr_offset_db
                 dl_ref = dref if dref.dim() == 3 else dref[..., None].expand(-1, -1, self.S)
-        out = self._net_step(T, ul_ref, dl_ref, hid)
+        if self.C == 1:
+            out = self._net_step(T, ul_ref, dl_ref, hid)
         self.last_snr = snr.clone()
         out["newest"] = self._rel(out["newest"])
         self.T = T + 1
@@ -666,7 +793,8 @@ class OracleEngine:
         if "dl_newest" in out:
             out["dl_newest"] = self._rel(out["dl_newest"])
         out["sinr_db"] = snr
-        out["serving_cell"] = torch.zeros(self.E, self.R, dtype=torch.long)
+        if "serving_cell" not in out:
+            out["serving_cell"] = torch.zeros(self.E, self.R, dtype=torch.long)
         out["t"] = (T - self.epoch).clone()
         return out
 
@@ -696,6 +824,89 @@ class OracleEngine:
             if uls:
                 self._slot(self.ul, g, t + (rel + 1) / N, uls, ul_ref, gain, rel, 0)
         return self._finish(t, hid)
+
+    # ---------------- several cells (nr_engine.py:671-816) ----------------
+    def _net_step_cells(self, t, pg, hid):
+        """NRNet.step_cells (nr_engine.py:718-788) without the downlink and radio link failure: association, the A3
+        plan of the step, then per slot the handovers due by that slot, fading on every robot-cell link, one
+        scheduler per cell (member masks, handover interruption), the serving link's UL reference against the
+        serving gNB's N+I estimate, fractional power control, and the same-slot interference hook."""
+        cfg, C, S = self.cfg, self.C, self.S
+        N = cfg.slots_per_step
+        g0 = t * N
+        self._pg = pg
+        rx = pg + cfg.ue_tx_dbm
+        asc = self.assoc
+        asc.associate(rx)
+        k_ho, tgt = asc.plan(rx)
+        g_ho = g0 + k_ho
+        fired = torch.zeros(self.E, self.R, dtype=torch.bool)
+        if self.rician:
+            self.k_lin = self.k_in
+        for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
+            g = g0 + rel
+            ho = (k_ho >= 0) & (k_ho <= rel) & ~fired
+            self._handover(ho, tgt, g_ho)
+            fired = fired | ho
+            self._evolve(g, rel)
+            gain_c = self._gain()
+            self._gain_c = gain_c
+            serv = asc.serv
+            gain = pick(gain_c, serv)
+            self.member = onehot(serv, C).permute(0, 2, 1)
+            self.sched_ok = asc.schedulable(g)
+            pg_s = pick(pg, serv)[..., None]
+            if sr:
+                self._sr_step(g)
+            if uls:
+                self._ni_la_ul = 10 * torch.log10(self.ni_ul.gather(1, serv[..., None].expand(-1, -1, S)))
+                ul_ref = cfg.ue_tx_dbm - self.ref_db + pg_s - self._ni_la_ul
+                rx_s = pg_s[..., 0] + cfg.ue_tx_dbm
+                self.phr_snr = rx_s - cfg.subband_noise_dbm
+                if self.pc_on:
+                    self.pc_backoff = self._pc_backoff(rx_s)
+                self._slot(self.ul, g, t + (rel + 1) / N, uls, ul_ref, gain, rel, 0)
+        late = (k_ho >= 0) & ~fired                      # triggers after the last active slot of the step
+        self._handover(late, tgt, g_ho)
+        out = self._finish(t, hid)
+        out["serving_cell"] = asc.serv.clone()
+        return out
+
+    def _pc_backoff(self, rx_serv):
+        """Fractional UL power control (nr_engine.py:671-675): backoff from the full power over snr_ref_prbs PRBs
+        to the PSD P0 + alpha PL."""
+        c = self.cfg
+        return c.ue_tx_dbm - (c.ul_pc_p0_dbm + c.ul_pc_alpha * (c.ue_tx_dbm - rx_serv))
+
+    def _handover(self, ho, target, g):
+        """NRNet._handover (nr_engine.py:677-682): switch, then UlMac.handover (mac_ul.py:238-247)."""
+        self.assoc.switch(ho, target, g)
+        u = self.ul
+        u.ctr["lost_frames"] += u.handover(ho, self.cfg.ho_rlc == "flush", self.cfg.harq_fail == "drop")
+        u.sr_t = torch.where(ho, torch.full_like(u.sr_t, -1), u.sr_t)
+        u.bsr = torch.where(ho, u.unsent(), u.bsr)
+
+    def serving_sinr_db(self):
+        """nr_engine.py:709-713: full-power SINR over snr_ref_prbs PRBs against the serving gNB's N+I estimate."""
+        serv = self.assoc.serv
+        ni = self.ni_ul.gather(1, serv[..., None].expand(-1, -1, self.S)).mean(-1)
+        return pick(self._pg, serv) + self.cfg.ue_tx_dbm - self.ref_db - 10 * torch.log10(ni)
+
+    def _ul_ici(self, won, n_prb, act):
+        """NRNet._ul_ici (nr_engine.py:799-816): interference at every gNB from the robots of the other cells that
+        transmit on the RBG in this slot, the N+I estimate update and the decoding SINR."""
+        serv = self.assoc.serv
+        psd = (self._pg + self.cfg.ue_tx_dbm - self.ref_db)[..., None] - self._split(n_prb)[..., None, None]
+        p_rx = 10 ** ((psd + self._gain_c) / 10) * won[:, :, None, :]
+        other = ~onehot(serv, self.C)
+        interf = (p_rx * other[..., None]).sum(1)
+        ni_now = self.noise_mw + interf
+        ni_act = 10 * torch.log10(ni_now.gather(1, serv[..., None].expand(-1, -1, self.S)))
+        a = self.cfg.li_alpha
+        self.ni_ul = ni_now if a == 1.0 else a * ni_now + (1 - a) * self.ni_ul
+        self.ioN = self.ioN + (interf / self.noise_mw).sum((1, 2))
+        self.ioN_n += self.C * self.S
+        return act - (ni_act - self._ni_la_ul)
 
     def _evolve(self, g, rel):
         """AR(1) fading step (nr_engine.py:570-590)."""
@@ -738,7 +949,9 @@ class OracleEngine:
         u.sr_t = torch.where(need_sr, torch.full_like(u.sr_t, g), u.sr_t)
 
     def _split(self, n_prb):
-        return 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
+        """UlMac._split (mac_ul.py:173-180): per-PRB backoff from the full power, at least the power-control one."""
+        sp = 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
+        return sp if not self.pc_on else torch.maximum(sp, self.pc_backoff)
 
     def _slot(self, L, g, frac, nsym, sinr_ref, gain_now, rel, ack_slot):
         """MacLink.slot (mac.py:228-508) with the UlMac hooks (mac_ul.py) for L.dir == "ul" and the DlMac hooks
@@ -764,12 +977,20 @@ class OracleEngine:
         p_new = free.long().argmax(-1)
         need = torch.minimum(L.bsr, unsent) if ul else unsent
         new_el = free.any(-1) & (need > 0) & ~has_rx
+        M = self.member if self.C > 1 else None
+        if M is not None:                                # handover interruption (mac.py:249-251)
+            has_rx = has_rx & self.sched_ok
+            new_el = new_el & self.sched_ok
         pending = (L.h_state == 1).any(-1)
         rx_nsb = L.h_nsb.gather(-1, rx_p[..., None]).squeeze(-1)
         if ul:                                           # UlMac._sched_estimate (mac_ul.py:154-171)
-            est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + L.csi
+            if not self.pc_on:
+                est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + L.csi
+            else:
+                est = sinr_ref - torch.maximum(10 * torch.log10(w / cfg.snr_ref_prbs), self.pc_backoff[..., None]) \
+                    + L.csi
             if cfg.phr_cap:
-                ref = sinr_ref.mean(-1)
+                ref = sinr_ref.mean(-1) if self.phr_snr is None else self.phr_snr
                 n_max_prb = cfg.snr_ref_prbs * 10 ** ((ref - cfg.phr_min_db) / 10)
                 n_max = torch.floor(n_max_prb / w[0]).clamp(1, S).long()
             else:
@@ -786,12 +1007,20 @@ class OracleEngine:
             metric_sb = (g - L.last_tx).float()[..., None].expand_as(rate_sb)
         else:
             metric_sb = rate_sb / L.avg.clamp(min=AVG_MIN)[..., None]
-        # retransmission admission (mac.py:300-304)
+        # retransmission admission, ranked inside every cell (mac.py:300-313)
         rkey = torch.where(has_rx, metric_sb.sum(-1), torch.full_like(metric_sb[..., 0], -1.0))
-        order = rkey.argsort(-1, descending=True)
-        cum = (rx_nsb * has_rx).gather(-1, order).cumsum(-1)
-        adm_sorted = has_rx.gather(-1, order) & (cum <= S)
-        has_rx = torch.zeros_like(has_rx).scatter(-1, order, adm_sorted)
+        if M is None:
+            order = rkey.argsort(-1, descending=True)
+            cum = (rx_nsb * has_rx).gather(-1, order).cumsum(-1)
+            adm_sorted = has_rx.gather(-1, order) & (cum <= S)
+            has_rx = torch.zeros_like(has_rx).scatter(-1, order, adm_sorted)
+        else:
+            rx_c = has_rx[:, None, :] & M
+            order = torch.where(rx_c, rkey[:, None, :], torch.full_like(M, -1.0, dtype=rkey.dtype)).argsort(
+                -1, descending=True)
+            cum = (rx_nsb[:, None, :] * rx_c).gather(-1, order).cumsum(-1)
+            adm_sorted = rx_c.gather(-1, order) & (cum <= S)
+            has_rx = torch.zeros_like(rx_c).scatter(-1, order, adm_sorted).any(1)
         want_cnt = torch.where(has_rx, rx_nsb, torch.where(new_el, n_max, torch.zeros_like(n_max)))
         lex = cfg.retx_priority
         prio = (1e9 if lex else 0.0) * has_rx.float()
@@ -802,11 +1031,19 @@ class OracleEngine:
         for s in range(S):
             want = (cnt < want_cnt) & (has_rx | (left > 0))
             m = torch.where(want, metric_sb[..., s] + prio, torch.full_like(left, -1.0))
-            if lex:
-                wr = want & has_rx
-                m = torch.where(wr.any(-1, keepdim=True) & ~wr, torch.full_like(m, -1.0), m)
-            best, wi = m.max(-1)
-            oh = onehot(wi, R) & (best >= 0)[:, None]
+            wr = want & has_rx if lex else None
+            if M is None:
+                if lex:
+                    m = torch.where(wr.any(-1, keepdim=True) & ~wr, torch.full_like(m, -1.0), m)
+                best, wi = m.max(-1)
+                oh = onehot(wi, R) & (best >= 0)[:, None]
+            else:                                        # one scheduler per cell on RBG s
+                mc = torch.where(M, m[:, None, :], torch.full_like(m[:, None, :], -1.0))
+                if lex:
+                    wr_c = wr[:, None, :] & M
+                    mc = torch.where(wr_c.any(-1, keepdim=True) & ~wr_c, torch.full_like(mc, -1.0), mc)
+                best, wi = mc.max(-1)
+                oh = (onehot(wi, R) & (best >= 0)[..., None]).any(1)
             cols.append(oh)
             cnt = cnt + oh.long()
             left = left - rate_sb[..., s] * oh * ~has_rx
@@ -820,8 +1057,13 @@ class OracleEngine:
             for s in range(S):
                 want = (cnt < want_cnt) & new_el & (left > 0)
                 m = torch.where(want, metric_sb[..., s], torch.full_like(left, -1.0))
-                best, wi = m.max(-1)
-                oh = onehot(wi, R) & ((best >= 0) & rel_rs[..., s].any(-1))[:, None]
+                if M is None:
+                    best, wi = m.max(-1)
+                    oh = onehot(wi, R) & ((best >= 0) & rel_rs[..., s].any(-1))[:, None]
+                else:
+                    best, wi = torch.where(M, m[:, None, :], torch.full_like(m[:, None, :], -1.0)).max(-1)
+                    av = (rel_rs[..., s][:, None, :] & M).any(-1)
+                    oh = (onehot(wi, R) & ((best >= 0) & av)[..., None]).any(1)
                 cols.append(oh)
                 cnt = cnt + oh.long()
                 left = left - rate_sb[..., s] * oh
@@ -858,6 +1100,8 @@ class OracleEngine:
         ntx = g1(L.h_ntx) + 1
         # decoding (mac.py:428-454; UL mac_ul.py:185-192, DL mac_dl.py:45-46)
         act = sinr_ref - self._split(n_prb)[..., None] + gain_now if ul else sinr_ref + gain_now
+        if ul and self.C > 1 and self.use_int:          # the sinr_hook (mac.py:429-432)
+            act = self._ul_ici(won & tx[..., None], n_prb, act)
         mcs_eq = None
         if cfg.harq_combining == "ir_lena":
             lse, _ = phy.eesm_lse(act, won, mcs, w)
@@ -917,7 +1161,7 @@ class OracleEngine:
         c["tb_new"] += int(tx_new.sum()); c["tb_retx"] += int(tx_rx.sum()); c["tb_ok"] += int(ok.sum())
         c["tb_fail"] += int(fail.sum()); c["exhaust"] += int(exh.sum()); c["bytes_ok"] += int(served.sum())
         c["bytes_new"] += int((byt_new * tx_new).sum()); c["new_while_pending"] += int((tx_new & pending).sum())
-        c["prb_used"] += float((n_prb * tx).sum()); c["prb_avail"] += float(self.w.sum()) * E
+        c["prb_used"] += float((n_prb * tx).sum()); c["prb_avail"] += float(self.w.sum()) * E * self.C
         c["lost_frames"] += lost_new
         # RLC in-order delivery (mac.py:500-503)
         ack = L.ack_ptr()
@@ -965,6 +1209,10 @@ class OracleEngine:
     RICIAN_MAP = {"net.spec": "spec", "net.k_los": "k_los", "net.k_in": "k_in", "net.k_lin": "k_lin",
                   "net.k_from": "k_from", "net.k_g0": "k_g0"}
 
+    CELL_KEYS = {"net.ni_ul": "ni_ul", "net.ioN[ul]": "ioN", "net._pg": "_pg", "net._gain_c": "_gain_c",
+                 "net._ni_la_ul": "_ni_la_ul", "ul.pc_backoff": "pc_backoff", "ul.phr_snr": "phr_snr",
+                 "ul.member": "member", "ul.sched_ok": "sched_ok"}
+
     def _state_items(self):
         """[(state_dict key, owner, attribute)] of every state tensor."""
         items = [(k, self, v) for k, v in self.NET_KEYS.items()]
@@ -975,10 +1223,13 @@ class OracleEngine:
             items.append(("net.dl_newest", self, "dl_newest"))
         if self.rician:
             items += [(k, self, v) for k, v in self.RICIAN_MAP.items()]
+        if self.C > 1:
+            items += [(k, self, v) for k, v in self.CELL_KEYS.items()]
+            items += [("assoc." + n, self.assoc, n) for n in (*Association.INIT, "pending")]
         return items
 
     def state(self):
-        out = {k: getattr(o, v) for k, o, v in self._state_items()}
+        out = {k: getattr(o, v) for k, o, v in self._state_items() if getattr(o, v) is not None}
         out["rng.episode"] = self.rng.episode
         out["rng.ctr[1]"] = self.rng.ctr[SUBMIT]
         out["rng.ctr[2]"] = self.rng.ctr[STEP]

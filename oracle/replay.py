@@ -11,7 +11,7 @@ import torch
 def load_case(path):
     d = np.load(path, allow_pickle=False)
     cfg = json.loads(bytes(d["cfg_json"]).decode())
-    for k in ("msg_sizes", "cell_positions_m"):
+    for k in ("msg_sizes", "cell_positions_m", "cell_center_m"):
         if k in cfg:
             cfg[k] = tuple(tuple(v) if isinstance(v, list) else v for v in cfg[k])
     return d, cfg, bytes(d["kind"]).decode()

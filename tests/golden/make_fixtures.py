@@ -98,6 +98,21 @@ CASES = {
                               discard="pdcp_arrival", timeout_steps=5, gnb_proc_slots=2, dl=True),
                      E=3, R=8, steps=30, kind="snr3", snr=(-2.0, 16.0), rates=(0.7,), dl_sizes=(5000.0,),
                      dl_rates=(1.1,), resets={11: [0, 2]}),
+    # several cells (NRNet.step_cells): config 3 shrunk (3 hex cells 150 m apart, 106 PRB, PF, thermal noise with
+    # same-slot UL interference, fractional UL power control, correlated fading on every link, no handover)
+    "mc3": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=5, frame_buffer=12, msg_sizes=(1200.0,), n_cells=3, cell_layout="hex",
+                         cell_isd_m=150.0, noise_model="thermal", a3_offset_db=float("inf"), channel="tr38901",
+                         tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0),
+                E=2, R=16, steps=30, kind="pose", arena=260.0, walk=0.5, rates=(0.6,), resets={17: [1]}),
+    # several cells with A3 handovers (fast motion, short time-to-trigger and interruption), maxCI, RLC UM drop,
+    # i.i.d. fading, log-distance radio, an EWMA N+I estimate
+    "mc3_ho": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="maxci", n_harq=4,
+                            max_harq_tx=3, harq_fail="drop", frame_buffer=8, msg_sizes=(2500.0, 400.0), n_cells=3,
+                            cell_layout="hex", cell_isd_m=120.0, noise_model="thermal", a3_ttt_ms=20.0,
+                            ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
+                            cell_center_m=(60.0, 60.0)),
+                   E=3, R=8, steps=40, kind="pose", arena=200.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
 }
 
 

@@ -7,13 +7,13 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import CASES, DL_CASES, GOLDEN
+from conftest import CASES, DL_CASES, GOLDEN, MC_CASES
 from oracle import nr_oracle as O
 from oracle import replay
 import isaac_net_amd as P
 
 
-@pytest.mark.parametrize("name", CASES + DL_CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES + MC_CASES)
 def test_oracle_bitwise_vs_reference(name):
     torch.set_num_threads(1)
     d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
@@ -54,4 +54,29 @@ def test_oracle_catches_a_planted_error():
             diff.append(s)
 
     replay.run(eng, d, kind, steps=12, on_step=on_step)
+    assert diff
+
+
+@pytest.mark.parametrize("plant", ["ttt_off_by_one", "ewma_ignored"])
+def test_oracle_catches_planted_multicell_errors(plant):
+    """Plausible mistakes in the multi-cell restatement fail the golden comparison of the handover case: an A3
+    time-to-trigger one slot long (fire at ttt - cnt instead of ttt - cnt - 1), and an N+I estimate that ignores the
+    EWMA (li_alpha 0.5 read as 1)."""
+    import dataclasses
+    d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, "traj_mc3_ho.npz"))
+    cfg = P.NRConfig(**cfgd, seed=0)
+    eng = O.OracleEngine(int(d["E"]), int(d["R"]), cfg, seed=0)
+    if plant == "ttt_off_by_one":
+        eng.assoc.ttt += 1
+    else:
+        eng.cfg = dataclasses.replace(cfg, li_alpha=1.0)
+    diff = []
+
+    def on_step(s, o, acc):
+        st = eng.state()
+        for k in ("assoc.serv", "assoc.ho_end", "net.ni_ul", "ul.sent"):
+            if not np.array_equal(d[f"s{s:03d}/{k}"], st[k].numpy()):
+                diff.append((s, k))
+
+    replay.run(eng, d, kind, on_step=on_step)
     assert diff
