@@ -1,8 +1,8 @@
 /*
  * inet_nr.h -- C ABI of the MI355X-native NR engine (libinet_nr.so, HIP kernels for gfx950).
  *
- * Drop-in boundary for isaac-net's per-control-step NR engine hot path (level "L2", one cell, uplink and
- * downlink). The reference launches its fused Triton kernel through
+ * Drop-in boundary for isaac-net's per-control-step NR engine hot path (level "L2": one cell with uplink and
+ * downlink, or several cells with the uplink). The reference launches its fused Triton kernel through
  *     nr_triton.launch_step(eng, uref, dref, pc, itab, ftab, K, gate, dgate)      isaac_net/core/nr_triton.py:1104-1167
  * from NRTritonEngine._triton_step (isaac_net/core/nr_fast.py:702-752), and runs the enqueue (NRNet.add_frames,
  * isaac_net/core/nr_engine.py:466-487) and partial reset (NREngine.reset, isaac_net/core/engine.py:763-794) as eager
@@ -19,6 +19,9 @@
  *                   nr_rng.py:45-52, radio.py:200-219).
  *   inet_nr_dl_step, inet_nr_dl_submit, inet_nr_dl_reset   the downlink of NRConfig(dl=True) (DlMac, mac_dl.py:19-49;
  *                   NRNet.add_dl_frames, nr_engine.py:489-497), declared at the end of this header.
+ *   inet_nr_step_cells, inet_nr_cells_reset   several cells per env (NRNet.step_cells, nr_engine.py:718-788, with
+ *                   CellAssociation, radio.py:303-453): the step with association, A3 handover, one scheduler per
+ *                   cell and same-slot inter-cell interference, and the reset of the association state.
  *
  * Conventions
  *   Ownership  The caller allocates and owns every buffer (device memory); the library never allocates or frees
@@ -38,13 +41,14 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 3
+#define INET_NR_ABI_VERSION 4
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
 #define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
 #define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
 #define INET_NR_MAX_ROWS 64       /* scheduled slots (InetNrRow) per control step */
+#define INET_NR_MAX_C 7           /* cells per env */
 
 #define INET_NR_OK 0
 #define INET_NR_EINVAL (-1)       /* a size or pointer argument is out of range or missing */
@@ -58,7 +62,8 @@ typedef struct InetNrState {
     float *olla, *avg;
     /* queue per robot [E][R]: stream length and number of queued frames (frames are a prefix) */
     int32_t *enq, *qlen;
-    /* per subband [E][S][R]: CSI (last PUSCH gain, dB) and the AR(1) fading state h = re + j im */
+    /* per subband [E][S][R]: CSI (last PUSCH gain, dB); the AR(1) fading state h = re + j im of every robot-cell
+       link [E][C][S][R] (C = n_cells) */
     float *csi, *h_re, *h_im;
     /* HARQ [E][P][R]: meta = state | ntx << 8 | mcs << 16 | nsb << 24; byte ranges, ready slot, TBS (bits),
        chase-combined linear SINR, IR log-sum and PRB count */
@@ -76,7 +81,8 @@ typedef struct InetNrState {
     int32_t *env_id, *episode, *ctr_step, *ctr_submit;
     /* engine clock epoch per env [E] */
     int32_t *epoch;
-    /* shadowing plane waves per env [E][NF][KF][3] = (kx, ky, phi), NF = 3 (tr38901) or 1 (log_distance) */
+    /* shadowing plane waves per env and cell [E][C][NF][KF][3] = (kx, ky, phi), NF = 3 (tr38901) or 1
+       (log_distance) */
     float *field;
     /* per-env counters [E][INET_NR_NCTR] int64: tb_new, tb_retx, tb_ok, tb_fail, exhaust, bytes_ok, bytes_new,
        lost_frames, new_while_pending, prb_used, reserved, reserved; and per-env HARQ histograms
@@ -116,6 +122,7 @@ typedef struct InetNrParams {
     int32_t max_tx, sr_delay, ul_rtt, rlc_retx, timeout, tb_oh, n_fields, n_modes, seed_key;
     int32_t n_data;                   /* data rows (flag 2) among the step's rows: sizes the kernel's per-slot LDS
                                          history (0: n_rows); must not be smaller than the actual count */
+    int32_t n_cells;                  /* cells per env C (1: the single-cell engine; > 1: inet_nr_step_cells) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -181,6 +188,29 @@ typedef struct InetNrArrivals {
     int32_t n_cls, discard_pdcp, pkt_payload, pkt_overhead;
 } InetNrArrivals;
 
+/* Several cells per env (NRConfig(n_cells > 1), NRNet.step_cells, nr_engine.py:718-788): the association of every
+   robot (CellAssociation, radio.py:303-453, without radio link failure), each gNB's N+I estimate and the constants
+   of association, A3 handover, power control and interference. */
+typedef struct InetNrCells {
+    int32_t *serv, *a3_cand, *a3_cnt, *ho_end, *n_ho;   /* [E][R] serving cell, A3 candidate / count, end slot of
+                                                           the handover interruption, handovers */
+    int32_t *pending;                   /* [E] 1: associate to the max-RSRP cell at the next step (after a reset) */
+    float *ni_ul;                       /* [E][C][S] each gNB's N+I estimate per PRB (mW, EWMA of the measurements) */
+    float *ion;                         /* [E] sum of interference over thermal over gNB-RBG-slots */
+    float gnb_xy[2 * INET_NR_MAX_C];    /* gNB positions (x, y) */
+    int32_t C;                          /* cells (must equal the params' n_cells) */
+    int32_t ttt, ho_int;                /* A3 time-to-trigger and handover interruption, slots */
+    int32_t ho_flush;                   /* 1: ho_rlc = "flush" (queued frames are dropped at a handover) */
+    int32_t use_int;                    /* 1: same-slot UL interference (noise_model "thermal", ul_interference) */
+    int32_t pc_on;                      /* 1: fractional UL power control */
+    int32_t has_floor;                  /* 1: A3 target admission floor (a3_min_target_rsrp_dbm) */
+    float a3_off, a3_hyst, floor_rx;    /* A3: best > (serving + a3_off) + a3_hyst; floor on the rx scale */
+    float noise_mw;                     /* gNB noise per PRB (mW) */
+    float ref_db;                       /* 10 log10(snr_ref_prbs) */
+    float li_a, li_b;                   /* N+I EWMA: li_a * now + li_b * estimate (li_b = 0: the measurement) */
+    float pc_p0, pc_alpha;              /* power control: backoff = ue_tx - (p0 + alpha (ue_tx - rx_serving)) */
+} InetNrCells;
+
 /* Library version (INET_NR_ABI_VERSION) and a short build string. */
 int32_t inet_nr_abi_version(void);
 const char *inet_nr_build_info(void);
@@ -238,6 +268,28 @@ int32_t inet_nr_dl_submit(const InetNrState *st, const InetNrDlState *dl, const 
 /* Reset the DL link of the envs of mask [E] uint8 (NULL = every env, which also clears the DL counters):
    MacLink.reset / FrameQueue.reset of NRNet.dl and dl_newest (nr_engine.py:256-274). */
 int32_t inet_nr_dl_reset(const InetNrDlState *dl, const InetNrParams *prm, const uint8_t *mask, void *stream);
+
+/* One control step T with several cells (NRNet.step_cells, nr_engine.py:718-788, uplink): per robot the path gain to
+   every cell from its pose (x: poses [E][R][2]), the max-RSRP association of the envs flagged pending, the A3 plan of
+   the step (the slot at which a handover fires); per scheduled slot the handovers due by that slot (CellAssociation
+   switch, UlMac.handover: mac_ul.py:238-247, mac.py:557-581), AR(1) fading on every robot-cell link, one scheduler
+   per cell over the same RBGs (mac.py:278-379 with member masks), the robots in a handover interruption left out,
+   the UL reference against the serving gNB's N+I estimate, fractional power control (nr_engine.py:671-675,
+   mac_ul.py:154-180) and the same-slot interference of the other cells' transmissions (_ul_ici, nr_engine.py:799-816);
+   then the handovers due after the last slot and the end of step as inet_nr_step. sinr_db is the serving link's
+   full-power SINR against the serving gNB's estimate (serving_sinr_db, nr_engine.py:709-713); serving_cell the
+   serving cell. arr: this step's arrivals as inet_nr_submit_step, or NULL. Needs prm->n_cells == cells->C > 1,
+   poses input (input_kind 0), no Rician fading and F <= 64. No counterpart in the reference's triton backend, which
+   runs one cell (nr_fast.py:538-554 refuses n_cells > 1); the reference path is the eager NRNet.step_cells. */
+int32_t inet_nr_step_cells(const InetNrState *st, const InetNrCells *cells, const InetNrTables *tab,
+                           const InetNrParams *prm, const InetNrRow *rows, int32_t n_rows, int64_t T, const float *x,
+                           const int64_t *cur_hid, const InetNrOutputs *out, const InetNrArrivals *arr, void *stream);
+
+/* Reset the association and the N+I estimates of the envs of mask [E] uint8 (NULL = every env, which also clears
+   the interference statistic): CellAssociation.reset and NRNet._reset_cells (radio.py:402-408,
+   nr_engine.py:424-438). inet_nr_reset with prm->n_cells = C redraws the fading state of every link and the
+   shadowing fields of every cell. */
+int32_t inet_nr_cells_reset(const InetNrCells *cells, const InetNrParams *prm, const uint8_t *mask, void *stream);
 
 #ifdef __cplusplus
 }

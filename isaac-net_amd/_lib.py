@@ -31,7 +31,7 @@ class InetNrParams(C.Structure):
     _fields_ = [(n, i32) for n in (
         "E", "R", "S", "P", "F", "N", "sched", "comb", "eesm", "harq_drop", "olla", "phr_cap", "retx_prio", "rician",
         "fading", "purge", "input_kind", "radio_model", "out_ref", "max_tx", "sr_delay", "ul_rtt", "rlc_retx",
-        "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "n_data")] + \
+        "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "n_data", "n_cells")] + \
                [(n, f32) for n in (
         "olla_up", "olla_dn", "pf_a", "pf_b", "target", "phr_min", "snr_ref_prbs", "w0", "ref_off", "noise_prb",
         "ue_tx", "subband_noise", "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1",
@@ -50,6 +50,17 @@ class InetNrDlState(C.Structure):
         "out_newest", "out_queue_len", "cqi_thr", "cqi_mcs")] + \
                [("gnb_proc", i32), ("snr_offset", i32), ("ref_off", f32), ("noise_prb", f32), ("snr_off", f32),
                 ("pad", i32)]
+
+
+MAX_C = 7
+
+
+class InetNrCells(C.Structure):
+    _fields_ = [(n, P) for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho", "pending", "ni_ul", "ion")] + \
+               [("gnb_xy", f32 * (2 * MAX_C))] + \
+               [(n, i32) for n in ("C", "ttt", "ho_int", "ho_flush", "use_int", "pc_on", "has_floor")] + \
+               [(n, f32) for n in ("a3_off", "a3_hyst", "floor_rx", "noise_mw", "ref_db", "li_a", "li_b", "pc_p0",
+                                   "pc_alpha")]
 
 
 class InetNrArrivals(C.Structure):
@@ -104,7 +115,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 WIFI_ABI_VERSION = 2
 _LIB = None
 
@@ -139,6 +150,12 @@ def load(path=LIB_PATH):
     lib.inet_nr_dl_submit.restype = i32
     lib.inet_nr_dl_reset.argtypes = [C.POINTER(InetNrDlState), C.POINTER(InetNrParams), P, P]
     lib.inet_nr_dl_reset.restype = i32
+    lib.inet_nr_step_cells.argtypes = [C.POINTER(InetNrState), C.POINTER(InetNrCells), C.POINTER(InetNrTables),
+                                       C.POINTER(InetNrParams), P, i32, i64, P, P, C.POINTER(InetNrOutputs),
+                                       C.POINTER(InetNrArrivals), P]
+    lib.inet_nr_step_cells.restype = i32
+    lib.inet_nr_cells_reset.argtypes = [C.POINTER(InetNrCells), C.POINTER(InetNrParams), P, P]
+    lib.inet_nr_cells_reset.restype = i32
     lib.inet_wifi_abi_version.restype = i32
     lib.inet_wifi_step.argtypes = [C.POINTER(InetWifiState), C.POINTER(InetWifiParams), P, i32, P, P,
                                    C.POINTER(InetWifiOutputs), P]

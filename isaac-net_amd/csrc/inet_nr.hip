@@ -132,6 +132,25 @@ __global__ void nr_dl_reset_kernel(InetNrDlState dl, InetNrParams pm, const uint
     }
 }
 
+// ======================================================================================= cells reset kernel
+// CellAssociation.reset and NRNet._reset_cells (radio.py:402-408, nr_engine.py:424-438) of the envs of the mask: serving
+// cell 0 until the next step's association, no A3 candidate, no interruption, no handovers; every gNB's N+I estimate
+// back to the noise; a full reset (mask NULL) also clears the interference statistic.
+__global__ void nr_cells_reset_kernel(InetNrCells cl, int E, int R, int S, const uint8_t* __restrict__ mask, int full) {
+    const int e = blockIdx.x;
+    if (e >= E) return;
+    if (!full && !mask[e]) return;
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        size_t ir = (size_t)e * R + r;
+        cl.serv[ir] = 0; cl.a3_cand[ir] = -1; cl.a3_cnt[ir] = 0; cl.ho_end[ir] = 0; cl.n_ho[ir] = 0;
+    }
+    for (int q = threadIdx.x; q < cl.C * S; q += blockDim.x) cl.ni_ul[(size_t)e * cl.C * S + q] = cl.noise_mw;
+    if (threadIdx.x == 0) {
+        cl.pending[e] = 1;
+        if (full) cl.ion[e] = 0.f;
+    }
+}
+
 // ======================================================================================= reset kernel
 // One block per env. NRNet.reset / MacLink.reset / FrameQueue.reset / NRRng.reset_mask and the reset draws: H0 of
 // the fading state, the Rician phase (KPHI) and the radio's plane-wave fields (channels/fields.py:38-58,
@@ -143,6 +162,7 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
     if (e >= pm.E) return;
     if (!full && !mask[e]) return;
     const int R = pm.R, S = pm.S, P = pm.P, F = pm.F;
+    const int NC = pm.n_cells > 1 ? pm.n_cells : 1;
     __shared__ int ep_new;
     if (threadIdx.x == 0) ep_new = st.episode[e] + 1;
     __syncthreads();
@@ -162,11 +182,13 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             st.q_cap[iq] = -1; st.q_start[iq] = 0; st.q_end[iq] = 0; st.q_fin[iq] = FIN_NONE;
             st.q_meta[iq] = 0u; st.q_hid[iq] = 0;
         }
-        // H0: N(0, 1) / sqrt 2 per element (r, s, re/im) of the per-env draw (nr_engine.py:262-263)
+        // H0: N(0, 1) / sqrt 2 per element (r, c, s, re/im) of the per-env draw (nr_engine.py:262-263), for every
+        // robot-cell link q = c S + s
         const uint32_t bh = base_key(s0, env, ep, CH_RESET, 0u, SITE_H0 << 16);
-        for (int s = 0; s < S; ++s) {
-            uint32_t j = (uint32_t)((r * S + s) * 2);
-            size_t is = ((size_t)e * S + s) * R + r;
+        const int CS = NC * S;
+        for (int q = 0; q < CS; ++q) {
+            uint32_t j = (uint32_t)((r * CS + q) * 2);
+            size_t is = ((size_t)e * CS + q) * R + r;
             st.h_re[is] = div_const(normal_at(bh, j), SQRT2_F, INV_SQRT2_F);
             st.h_im[is] = div_const(normal_at(bh, j + 1u), SQRT2_F, INV_SQRT2_F);
         }
@@ -178,13 +200,15 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             st.k_lin[ir] = k_lin0;
         }
     }
-    // env-level: radio fields (draw_plane_waves) of the new episode
+    // env-level: radio fields (draw_plane_waves) of the new episode, one per cell: wave kk of cell c is element
+    // c K + kk of the field's draws
     const int K = pm.n_modes;
     const float dcs[3] = {dc0, dc1, dc2};
-    for (int q = threadIdx.x; q < pm.n_fields * K; q += blockDim.x) {
-        int fi = q / K, kk = q - fi * K;
-        draw_plane_wave(s0, env, ep, pm.radio_model, fi, kk, dcs[fi], spectrum,
-                        st.field + (((size_t)e * pm.n_fields + fi) * K + kk) * 3);
+    for (int q = threadIdx.x; q < NC * pm.n_fields * K; q += blockDim.x) {
+        int c = q / (pm.n_fields * K), rem = q - c * pm.n_fields * K;
+        int fi = rem / K, kk = rem - fi * K;
+        draw_plane_wave(s0, env, ep, pm.radio_model, fi, c * K + kk, dcs[fi], spectrum,
+                        st.field + ((((size_t)e * NC + c) * pm.n_fields + fi) * K + kk) * 3);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -208,7 +232,7 @@ int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
 int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
                            const InetNrParams* prm, const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x,
                            const int64_t* cur_hid, const InetNrOutputs* out, const InetNrArrivals* arr,
-                           void* stream) {
+                           void* stream, const InetNrCells* cells = nullptr) {
     const InetNrParams& p = *prm;
     const InetNrTables& t = *tab;
     if (p.E <= 0 || p.R <= 0 || p.R > INET_NR_MAX_R || p.F <= 0 || p.N <= 0) return INET_NR_EINVAL;
@@ -223,16 +247,30 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);
-    inet::StepFn fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
-                    : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
+    // the single-cell entry points run one cell; inet_nr_step_cells several
+    if ((cells != nullptr) != (p.n_cells > 1)) return INET_NR_EINVAL;
+    inet::StepFn fn;
+    if (cells) {
+        const InetNrCells& c = *cells;
+        if (c.C != p.n_cells || c.C > INET_NR_MAX_C || p.input_kind != 0 || p.rician || p.F > 64 || dl)
+            return INET_NR_EINVAL;
+        if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
+            return INET_NR_EINVAL;
+        if (c.ttt < 0 || c.ho_int < 0 || !(c.noise_mw > 0.0f)) return INET_NR_EINVAL;
+        fn = inet::pick_step_mc(p.S, c.C, p.P, ir);
+    } else {
+        fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
+           : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
+    }
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = inet::STEP_WAVE / rb;
     InetNrArrivals none{};
     if (arr && (!arr->counts || !arr->sizes || arr->n_cls <= 0 || (arr->pkt_overhead && arr->pkt_payload <= 0)))
         return INET_NR_EINVAL;
-    inet::StepArgs a{*st, dl, t, p, rows, n_rows, n_data, arr ? *arr : none, T, x, cur_hid, *out, rb,
+    inet::StepArgs a{*st, dl, cells, t, p, rows, n_rows, n_data, arr ? *arr : none, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
-                     inet::step_lds_bytes(n_data, p.harq_drop, rb, p.max_tx), (hipStream_t)stream};
+                     inet::step_lds_bytes(n_data, p.harq_drop, rb, p.max_tx, cells ? cells->C : 1, p.S),
+                     (hipStream_t)stream};
     fn(a);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }
@@ -244,8 +282,8 @@ extern "C" {
 int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
 
 const char* inet_nr_build_info(void) {
-    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, one wave64 per workgroup, "
-           "DPP segment reductions, ATen-order sums";
+    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, multi-cell step<C = 3, "
+           "S in {8,13,14}, P, IR>, one wave64 per workgroup, DPP segment reductions, ATen-order sums";
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,
@@ -260,6 +298,26 @@ int32_t inet_nr_submit_step(const InetNrState* st, const InetNrTables* tab, cons
                             const InetNrOutputs* out, const InetNrArrivals* arr, void* stream) {
     if (!st || !tab || !prm || !out || !x || !arr) return INET_NR_EINVAL;
     return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, arr, stream);
+}
+
+int32_t inet_nr_step_cells(const InetNrState* st, const InetNrCells* cells, const InetNrTables* tab,
+                           const InetNrParams* prm, const InetNrRow* rows, int32_t n_rows, int64_t T, const float* x,
+                           const int64_t* cur_hid, const InetNrOutputs* out, const InetNrArrivals* arr, void* stream) {
+    if (!st || !cells || !tab || !prm || !out || !x) return INET_NR_EINVAL;
+    return launch_step_kernel(st, nullptr, tab, prm, rows, n_rows, T, x, cur_hid, out, arr, stream, cells);
+}
+
+int32_t inet_nr_cells_reset(const InetNrCells* cells, const InetNrParams* prm, const uint8_t* mask, void* stream) {
+    if (!cells || !prm) return INET_NR_EINVAL;
+    const InetNrParams& p = *prm;
+    const InetNrCells& c = *cells;
+    if (p.E <= 0 || p.R <= 0 || p.S <= 0 || p.S > INET_NR_MAX_S || c.C < 2 || c.C > INET_NR_MAX_C || c.C != p.n_cells)
+        return INET_NR_EINVAL;
+    if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
+        return INET_NR_EINVAL;
+    hipLaunchKernelGGL(nr_cells_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, c, p.E, p.R, p.S, mask,
+                       mask ? 0 : 1);
+    return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }
 
 int32_t inet_nr_dl_step(const InetNrState* st, const InetNrDlState* dl, const InetNrTables* tab,
@@ -315,6 +373,7 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     if (!st || !prm || !dcorr) return INET_NR_EINVAL;
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
+    if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
     if (T < 0 || T > 0x7fffffff) return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,
                        dcorr[0], dcorr[1], dcorr[2], spectrum, mask ? 0 : 1);

@@ -136,6 +136,33 @@ DEV float aten_sum(const float* x) {
     }
 }
 
+// torch CPU float sum over the robots (dim 1) of an [E][R][C][S] tensor, column q = c S + s of the n_col = C S columns
+// (the outer reduction of SumKernel.cpp as this build's CPU runs it, pinned against torch in
+// tests/test_known_answers.py): the columns q < 32 floor(n_col / 32) add the rows in chunks of 16, each chunk from 0,
+// accumulate the chunk sums in order from 0 and add that to the sum of the rows past the last full chunk; the other
+// columns add row i into accumulator i mod 4 (the rows past the last group of four into accumulator 0) and return
+// ((a0 + a1) + a2) + a3. x(i): the value of row i.
+template <class X>
+DEV float aten_outer_sum(int n_rows, bool chunked, X x) {
+    if (chunked) {
+        float acc = 0.f;
+        int i = 0;
+        for (; i + 16 <= n_rows; i += 16) {
+            float c = 0.f;
+            for (int k = 0; k < 16; ++k) c += x(i + k);
+            acc += c;
+        }
+        float tail = 0.f;
+        for (; i < n_rows; ++i) tail += x(i);
+        return tail + acc;
+    }
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    const int g4 = n_rows >> 2;
+    for (int i = 0; i < g4; ++i) { a0 += x(4 * i); a1 += x(4 * i + 1); a2 += x(4 * i + 2); a3 += x(4 * i + 3); }
+    for (int i = 4 * g4; i < n_rows; ++i) a0 += x(i);
+    return ((a0 + a1) + a2) + a3;
+}
+
 // torch.logsumexp over a row of N
 template <int N>
 DEV float aten_lse(const float* x) {
@@ -177,14 +204,14 @@ DEV float aten_row_sum(int n, X x) {
 }
 
 // ---------------------------------------------------------------- radio (RadioMC.rx_dbm at one cell / AP)
-// Received power (dBm) of a robot at (px, py) from the cell's path loss and plane-wave shadowing
+// Received power (dBm) of a robot at (px, py) from the cell at (gx, gy): path loss and plane-wave shadowing
 // (isaac_net/core/radio.py:238-272, channels/models.py:137-167, channels/tr38901.py:162-203 with a fixed LOS state).
-// PM: a parameter struct with the radio fields of InetNrParams (gnb_x ... pl_exp10, ue_tx, radio_model, n_modes);
-// fld_env: the env's fields [n_fields][n_modes][3] (kx, ky, phase). The transcendental functions are evaluated in
+// PM: a parameter struct with the radio fields of InetNrParams (hh2 ... pl_exp10, ue_tx, radio_model, n_modes);
+// fld_env: the cell's fields of the env [n_fields][n_modes][3] (kx, ky, phase). The transcendental functions are evaluated in
 // double precision and rounded once (the field arguments k . x reach 1e4 rad).
 template <class PM>
-DEV float radio_rx_dbm(const PM& pm, float px, float py, const float* fld_env) {
-    float dx = px - pm.gnb_x, dy = py - pm.gnb_y;
+DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, const float* fld_env) {
+    float dx = px - gx, dy = py - gy;
     float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
     int fi = 0;
     float pl;
@@ -230,8 +257,9 @@ DEV float radio_rx_dbm(const PM& pm, float px, float py, const float* fld_env) {
     return (pm.ue_tx - pl) - field;
 }
 
-// One plane wave kk of shadowing field fi drawn for (seed key, env, episode) (channels/fields.py:38-58,
-// radio.py:185-189): stream LOG_DISTANCE (10) for the log-distance field, TR38901 + 3 fi for the TR 38.901 fields;
+// One plane wave of shadowing field fi drawn for (seed key, env, episode) (channels/fields.py:38-58,
+// radio.py:185-189): element kk = c K + k (cell c, wave k) of the RESET uniforms of stream LOG_DISTANCE (10) for the
+// log-distance field, TR38901 + 3 fi for the TR 38.901 fields;
 // spectrum 0 "sos" (wavelengths 20..60 m scaled by dcorr / 10.3), 1 "exp" (inverse CDF of the radial spectrum).
 // Writes (kx, ky, phase) to fp; cos / sin / the phase product are evaluated as the reference's float32 torch ops,
 // cos / sin in double precision rounded once.

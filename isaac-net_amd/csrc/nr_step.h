@@ -105,6 +105,22 @@ DEV int bmax_i(int v, int rb) {
     if (rb > 32) v = imax_lvl<5>(v);
     return v;
 }
+// bmax_i of N values at once (independent butterflies, interleaved)
+template <int N>
+DEV void bmax_n(int (&v)[N], int rb) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 1) v[i] = imax_lvl<0>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 2) v[i] = imax_lvl<1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 4) v[i] = imax_lvl<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 8) v[i] = imax_lvl<3>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 16) v[i] = imax_lvl<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (rb > 32) v[i] = imax_lvl<5>(v[i]);
+}
 // index (inside the segment) of the first lane of this lane's segment whose predicate holds; rb if none
 DEV int seg_first(bool p, int rb, int lane) {
     unsigned long long b = __ballot(p) >> (lane & ~(rb - 1));
@@ -204,22 +220,41 @@ DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
 }
 
 // Dynamic LDS of the step kernel, in ints: the in-order pointer after every UL slot [n_ul][64], with RLC drop the
-// byte range of a TB that exhausted its HARQ [n_ul][64] x 2, then the per-env HARQ histograms [64 / RB][3][max_tx + 1].
-inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx) {
+// byte range of a TB that exhausted its HARQ [n_ul][64] x 2, then the per-env HARQ histograms [64 / RB][3][max_tx + 1];
+// with several cells (nc > 1) then per env each gNB's N+I estimate and this slot's interference [64 / RB][2][nc S].
+inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx, int nc = 1, int S = 0) {
     return sizeof(int) * ((size_t)n_ul * STEP_WAVE * (harq_drop ? 3 : 1) +
-                          (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1));
+                          (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1) +
+                          (nc > 1 ? (size_t)(STEP_WAVE / rb) * 2 * nc * S : 0));
+}
+
+// v[idx] of a register array indexed by a runtime value (a chain of selects, no scratch memory)
+template <int N, class T>
+DEV T sel_of(const T (&v)[N], int idx) {
+    T r = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) r = idx == i ? v[i] : r;
+    return r;
 }
 
 // RBT: the segment width when it is fixed at compile time (0: the runtime argument rb).
 // LS: the link whose MAC state and queue the kernel runs: InetNrState (the UL; lk is st) or InetNrDlState (the DL
 // of NRConfig(dl=True): CQI reports and DL data slots with the DlMac hooks; it reads the shared state of st and writes
 // only the DL link's).
-template <int S, int P, bool IR, bool VREF, int RBT, class LS>
-__global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
+// NC: cells per env. NC > 1 runs NRNet.step_cells (nr_engine.py:718-788), UL with pose input: association and the A3
+// plan in the prologue, the handovers due at every row, fading on every robot-cell link, one scheduler per cell (the
+// segment's lanes of one serving cell: ballots masked to the cell, NC interleaved butterflies), fractional power
+// control, and the same-slot interference sum of every gNB and RBG over the other cells' robots (each lane's terms in
+// LDS, summed by one lane per (cell, RBG) in torch's CPU order); cl holds the association state and constants.
+template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC>
+__global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     InetNrState st, LS lk, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
-    int n_ul_max, InetNrArrivals arr) {
+    int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
+    constexpr bool MC = NC > 1;
+    static_assert(!(MC && (DL || VREF)), "several cells: the UL with pose input");
+    constexpr int NCS = NC * S;                        // fading links per robot (cell-major, subband-minor)
     const int rb = RBT ? RBT : rb_arg;
     const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
     extern __shared__ int dyn[];
@@ -229,7 +264,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
     __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
     __shared__ int s_ulrel[MAX_UL_ROWS];
-    __shared__ float s_x[2 * S * STEP_WAVE];                     // per-lane rows: fading normals, RBG SINR (dB)
+    // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
+    // interference terms at every (cell, RBG) during a UL slot
+    __shared__ float s_x[2 * NCS * STEP_WAVE];
     __shared__ float s_lin[S * STEP_WAVE];                       // per-lane rows: linear RBG SINR
     __shared__ int s_la_i[2 * STEP_WAVE], s_la_slot[STEP_WAVE], s_la_top[STEP_WAVE];   // link adaptation work list
     __shared__ float s_la_f[3 * STEP_WAVE];
@@ -256,6 +293,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     int* const exhi_l = dyn + 2 * n_ul_max * STEP_WAVE;
     int* const hist_l = dyn + (pm.harq_drop ? 3 : 1) * n_ul_max * STEP_WAVE;
     int* const my_hist = hist_l + eloc * 3 * HB;
+    // several cells: each gNB's N+I estimate [NC][S] and this slot's interference [NC][S] of this lane's env
+    float* const s_ni = reinterpret_cast<float*>(hist_l + envs_pw * 3 * HB) + eloc * 2 * NCS;
+    float* const s_if = s_ni + NCS;
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
@@ -281,7 +321,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     // ---------------- load per-robot state ----------------
     int sent = 0, floor_ = 0, bsr = 0, sr_t = -1, last_tx = -1, enq = 0, qlen = 0;
     float olla = 0.f, avg = 100.f;
-    float csi[S], hr[S], hi[S];
+    float csi[S], hr[NCS], hi[NCS];
     uint32_t hmeta[P];
     int hlo[P], hhi[P], hrdy[P], htbs[P];
     float hcomb[P], hlexp[IR ? P : 1], hnrb[IR ? P : 1];
@@ -321,12 +361,31 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             if (arr.accepted) sto(arr.accepted, o_r, n_acc);
         }
     }
+    const uint32_t o_hr0 = (uint32_t)(ee * NCS * R + rr0) * 4u;   // [E][NC S][R] at q = 0
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         csi[s] = ldo(lk.csi + s * R, o_sr);
-        hr[s] = 0.f; hi[s] = 0.f;
-        if (read_h) { hr[s] = ldo(st.h_re + s * R, o_sr); hi[s] = ldo(st.h_im + s * R, o_sr); }
-        if (!act) { csi[s] = 0.f; hr[s] = 0.f; hi[s] = 0.f; }
+        if (!act) csi[s] = 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < NCS; ++q) {
+        hr[q] = 0.f; hi[q] = 0.f;
+        if (read_h && act) { hr[q] = ldo(st.h_re + q * R, o_hr0); hi[q] = ldo(st.h_im + q * R, o_hr0); }
+    }
+    // several cells: association of this robot, the N+I estimates of its env (LDS), the env's interference statistic
+    int serv = 0, a3_cand = -1, a3_cnt = 0, ho_end = 0, n_ho = 0;
+    float ion = 0.f;
+    if constexpr (MC) {
+        if (act) {
+            serv = ldo(cl.serv, o_r); a3_cand = ldo(cl.a3_cand, o_r); a3_cnt = ldo(cl.a3_cnt, o_r);
+            ho_end = ldo(cl.ho_end, o_r); n_ho = ldo(cl.n_ho, o_r);
+            serv = serv < 0 ? 0 : (serv >= NC ? NC - 1 : serv);   // (indexes LDS rows: kept in range)
+        }
+        if (e < E) {
+            for (int q = r; q < NCS; q += rb) s_ni[q] = cl.ni_ul[(size_t)ee * NCS + q];
+            if (r == 0) ion = cl.ion[ee];
+        }
+        __syncthreads();
     }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -349,9 +408,21 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     // the DL reference SINR per PRB (NRNet.step_rx / step, nr_engine.py:624-631, 651-653): with poses the gNB PSD
     // over the reciprocal path gain against the UE noise; with SNR input the input plus dl_snr_offset_db (or the DL
     // SNR as given)
-    float ref[VREF ? S : 1];
+    float ref[(VREF || MC) ? S : 1];
     float snr_out = 0.f;
-    if constexpr (VREF) {
+    float pgc[NC];                                 // several cells: path gain to every cell (dB)
+    if constexpr (MC) {
+        // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
+        float px = 0.f, py = 0.f;
+        if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
+            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc) - pm.ue_tx;
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) ref[s] = 0.f;
+    } else if constexpr (VREF) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             ref[s] = act ? ldo(xin + s, o_r * S) : 0.f;
@@ -365,16 +436,18 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     } else {                                       // poses -> path gain (radio prologue)
         float px = 0.f, py = 0.f;
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
-        const float rx = radio_rx_dbm(pm, px, py, st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3);
+        const float rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y,
+                                      st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3);
         const float pg = rx - pm.ue_tx;
         if constexpr (DL) ref[0] = (pg + lk.ref_off) - lk.noise_prb;
         else ref[0] = (pg + pm.ref_off) - pm.noise_prb;
         snr_out = (pg + pm.ue_tx) - pm.subband_noise;
     }
-    auto REF = [&](int s) -> float { return VREF ? ref[s] : ref[0]; };
-    // PHR cap n_max (mac_ul.py:165-168): ref.mean(-1) -> snr_ref_prbs 10^((ref - phr_min) / 10) / w0
+    auto REF = [&](int s) -> float { return (VREF || MC) ? ref[s] : ref[0]; };
+    // PHR cap n_max (mac_ul.py:165-168): ref.mean(-1) -> snr_ref_prbs 10^((ref - phr_min) / 10) / w0 (several cells:
+    // from the serving link's noise-only SNR at every UL slot)
     int n_max = S;
-    if (!DL && pm.phr_cap) {
+    if (!DL && !MC && pm.phr_cap) {
         float rr[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) rr[s] = REF(s);
@@ -411,6 +484,92 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 
     int n_ul = 0;
     const int g0 = (int)(T * (int64_t)N);
+
+    // ---------------- several cells: association and the A3 plan of this step (CellAssociation, radio.py:410-437) ----
+    // rx = path gain + ue_tx (RSRP up to a constant); a pending env attaches every robot to its max-rx cell; the A3
+    // condition (best other cell > (serving + offset) + hysteresis, and above the admission floor) held toward the same
+    // target for ttt slots fires at slot k_ho = ttt - cnt - 1 of this step when that is inside the step
+    int k_ho = -1, tgt = 0, ho_j = -1;
+    bool fired = false;
+    unsigned long long ho_mask = 0ull;                 // frames a handover drops (replayed at UL slot ho_j)
+    if constexpr (MC) {
+        float rxc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) rxc[c] = pgc[c] + pm.ue_tx;
+        if (act && cl.pending[ee] != 0) {
+            int b = 0;
+            float bv = rxc[0];
+#pragma unroll
+            for (int c = 1; c < NC; ++c) if (rxc[c] > bv) { bv = rxc[c]; b = c; }
+            serv = b;
+        }
+        if (act) {
+            const float rs = sel_of(rxc, serv);
+            float best = 0.f;
+            int bc = 0;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float v = c == serv ? -INFINITY : rxc[c];
+                if (c == 0 || v > best) { best = v; bc = c; }
+            }
+            bool cond = best > ((rs + cl.a3_off) + cl.a3_hyst);
+            if (cl.has_floor) cond = cond && best >= cl.floor_rx;
+            const int cnt = (cond && bc == a3_cand) ? a3_cnt : 0;
+            int kf = cl.ttt - cnt - 1;
+            kf = kf > 0 ? kf : 0;
+            const bool fire = cond && kf < N;
+            a3_cnt = (cond && !fire) ? cnt + N : 0;
+            a3_cand = (cond && !fire) ? bc : -1;
+            k_ho = fire ? kf : -1;
+            tgt = bc;
+        }
+    }
+    // NRNet._handover at slot g_sw (nr_engine.py:677-682): the switch (radio.py:439-448), then UlMac.handover
+    // (mac_ul.py:238-247, mac.py:557-581): under RLC UM or ho_rlc "flush" the frames overlapping the undecoded HARQ
+    // bytes (flush: every queued frame) are lost, marked when the epilogue replays the UL slots (before UL slot ho_j)
+    // so that frames completed earlier keep their completion, and those processes are freed; otherwise they restart
+    // their combining at the target. OLLA, the PF average and the CSI start afresh; the BSR reaches the target, a
+    // pending SR is dropped.
+    auto handover = [&](int g_sw) {
+        serv = tgt;
+        ho_end = g_sw + cl.ho_int;
+        ++n_ho;
+        fired = true;
+        if (pm.harq_drop || cl.ho_flush) {
+            unsigned long long mk = 0ull;
+            if (cl.ho_flush) {
+                mk = qlen >= 64 ? ~0ull : ((1ull << qlen) - 1ull);
+            } else {
+                for (int f = 0; f < qlen; ++f) {
+                    const int qs = ldo(lk.q_start + f * R, o_fr0), qe = ldo(lk.q_end + f * R, o_fr0);
+                    bool ov = false;
+#pragma unroll
+                    for (int p = 0; p < P; ++p) ov |= hm_state(hmeta[p]) == 1 && qs < hhi[p] && qe > hlo[p];
+                    if (ov) mk |= 1ull << f;
+                }
+            }
+            ho_mask = mk;
+            ho_j = n_ul;
+            if (cl.ho_flush) sent = enq;
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                if (hm_state(hmeta[p]) == 1) hmeta[p] = hm_pack(0, hm_ntx(hmeta[p]), hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
+        } else {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                if (hm_state(hmeta[p]) == 1) {
+                    hmeta[p] = hm_pack(1, 0, hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
+                    hcomb[p] = 0.f;
+                    if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+                }
+            }
+        }
+        olla = 0.f;
+        avg = 100.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) csi[s] = 0.f;
+        if constexpr (!DL) { sr_t = -1; bsr = enq - sent; }
+    };
     // i.i.d. fading (rho = 0 at every evolving row): a robot's fading state and CSI are then pure functions of the
     // latest draw, so a robot with nothing to send and no HARQ process pending (it takes part in no decision for the
     // rest of the step) skips the draws until the last row that fixes the stored state (the last UL slot for the CSI,
@@ -427,11 +586,14 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
         const int g = g0 + row.rel;
+        if constexpr (MC) {                        // A3 handovers due by this slot (nr_engine.py:740-754)
+            if (act && !fired && k_ho >= 0 && k_ho <= row.rel) handover(g0 + k_ho);
+        }
         if ((row.flags & 4) && (row.flags & 8)) {  // AR(1) fading innovation of this slot (nr_engine.py:575-589)
-            // The 2 S normals of every robot that needs them are drawn cooperatively by the whole wavefront: the
-            // (robot, subband) pairs are dealt round-robin over the 64 lanes, each pair's two normals land in the
-            // robot's LDS column (s_x), and the robot then updates its own state. Normal j = 2 S r + q (q = 2 s for
-            // the real part, 2 s + 1 for the imaginary one) uses hash elements 2j, 2j + 1.
+            // The 2 NC S normals of every robot that needs them are drawn cooperatively by the whole wavefront: the
+            // (robot, link) pairs are dealt round-robin over the 64 lanes, each pair's two normals land in the
+            // robot's LDS column (s_x), and the robot then updates its own state. Normal j = 2 NC S r + 2 q + {0, 1}
+            // (link q = c S + s of cell c and subband s; real, imaginary part) uses hash elements 2j, 2j + 1.
             bool busy = false;
 #pragma unroll
             for (int p = 0; p < P; ++p) busy |= hm_state(hmeta[p]) == 1;
@@ -447,34 +609,42 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             // pairs in subband-major order: the lanes of one pass write different robots' columns (no LDS bank
             // conflicts between the pairs of one robot)
             const int n_need = __builtin_popcountll(need);
-            const int items = n_need * S;
+            const int items = n_need * NCS;
 #pragma unroll 1
             for (int it = lane; it < items; it += STEP_WAVE) {
-                const int s = it / n_need, ri = it - s * n_need;
+                const int q = it / n_need, ri = it - q * n_need;
                 const int L = s_list[ri];
                 const uint32_t bf = s_bfe[L / rb];
-                const uint32_t hin = bf + (uint32_t)(4 * (L & (rb - 1)) * S + 4 * s) * GOLD;
+                const uint32_t hin = bf + (uint32_t)(4 * (L & (rb - 1)) * NCS + 4 * q) * GOLD;
                 const float zr = normal_of(mix32(mix32(hin) ^ bf), mix32(mix32(hin + GOLD) ^ bf));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bf), mix32(mix32(hin + 3u * GOLD) ^ bf));
-                s_z[(2 * s) * STEP_WAVE + L] = zr;
-                s_z[(2 * s + 1) * STEP_WAVE + L] = zi;
+                s_z[(2 * q) * STEP_WAVE + L] = zr;
+                s_z[(2 * q + 1) * STEP_WAVE + L] = zi;
             }
             __syncthreads();
             if (draw) {
 #pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    float zr = s_z[(2 * s) * STEP_WAVE + lane], zi = s_z[(2 * s + 1) * STEP_WAVE + lane];
-                    hr[s] = row.rho * hr[s] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
-                    hi[s] = row.rho * hi[s] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+                for (int q = 0; q < NCS; ++q) {
+                    float zr = s_z[(2 * q) * STEP_WAVE + lane], zi = s_z[(2 * q + 1) * STEP_WAVE + lane];
+                    hr[q] = row.rho * hr[q] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                    hi[q] = row.rho * hi[q] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
                 }
             }
         }
-        // fading gain (dB) of subband s in this slot (nr_engine.py:602-611)
+        // fading gain (dB) of subband s of the serving link in this slot (nr_engine.py:602-611; several cells: the
+        // serving cell's, pick(gain_c, serv)), and of link (c, s) (gain_cs)
         auto gain_of = [&](int s) -> float {
             float gs = 0.f;
             if (pm.fading) {
                 float p;
-                if (pm.rician) {
+                if constexpr (MC) {
+                    p = hr[s] * hr[s] + hi[s] * hi[s];
+#pragma unroll
+                    for (int c = 1; c < NC; ++c) {
+                        const float pc_ = hr[c * S + s] * hr[c * S + s] + hi[c * S + s] * hi[c * S + s];
+                        p = serv == c ? pc_ : p;
+                    }
+                } else if (pm.rician) {
                     float xr = ka * sp_re + kb * hr[s];
                     float xi = ka * sp_im + kb * hi[s];
                     p = xr * xr + xi * xi;
@@ -484,6 +654,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 gs = 10.0f * log10f(clamp_min(p, 1e-6f));
             }
             return gs;
+        };
+        auto gain_cs = [&](int q) -> float {
+            return pm.fading ? 10.0f * log10f(clamp_min(hr[q] * hr[q] + hi[q] * hi[q], 1e-6f)) : 0.0f;
         };
         if constexpr (DL) {
             if (row.flags & 1) {                   // CQI report (DlMac.cqi_report, mac_dl.py:30-40)
@@ -510,6 +683,52 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         }
         if (!(row.flags & 2)) continue;
         // ============================ data slot (MacLink.slot) ============================
+        // several cells (nr_engine.py:757-766): the UL reference of the serving link per subband against the serving
+        // gNB's N+I estimate, the PHR cap from its noise-only SNR, the power-control backoff, this row's cells
+        float pc = -INFINITY;
+        float ni_la[MC ? S : 1];
+        unsigned long long mycell = 0ull;
+        if constexpr (MC) {
+            const float pg_s = sel_of(pgc, serv);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                ni_la[s] = 10.0f * log10f(s_ni[serv * S + s]);
+                ref[s] = (pm.ref_off + pg_s) - ni_la[s];
+            }
+            const float rx_s = pg_s + pm.ue_tx;
+            if (cl.pc_on) pc = pm.ue_tx - (cl.pc_p0 + cl.pc_alpha * (pm.ue_tx - rx_s));
+            n_max = S;
+            if (pm.phr_cap) {
+                const float phr = rx_s - pm.subband_noise;
+                float f = floorf((pm.snr_ref_prbs * from_db(phr - pm.phr_min)) / pm.w0);
+                n_max = (int)clampf(f, 1.0f, (float)S);
+            }
+            unsigned long long cm[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) cm[c] = __ballot(act && serv == c);
+            mycell = sel_of(cm, serv) & seg_bits(rb, lane);
+        }
+        // any lane of this lane's scheduler (its env's segment; several cells: the env's robots of its cell)
+        auto cell_any = [&](bool p) -> bool {
+            if constexpr (MC) return (__ballot(p) & mycell) != 0ull;
+            else return seg_any(p, rb, lane);
+        };
+        // true in the lane that wins the RBG with bid m (-1: no bid) in its scheduler: the highest bid, the first
+        // robot on ties (torch max)
+        auto winner = [&](int m) -> bool {
+            if constexpr (MC) {
+                int v[NC];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) v[c] = serv == c ? m : -1;
+                bmax_n<NC>(v, rb);
+                const int mx = sel_of(v, serv);
+                const unsigned long long b = (__ballot(m == mx) & mycell) >> (lane & ~(rb - 1));
+                return m >= 0 && b != 0ull && (int)__builtin_ctzll(b) == r;
+            } else {
+                const int mx = bmax_i(m, rb);
+                return m >= 0 && seg_first(m == mx, rb, lane) == r;
+            }
+        };
         const int unsent = enq - sent;
         if constexpr (DL) {
             // DL processes whose HARQ-ACK has reached the gNB become free (mac.py:243)
@@ -536,6 +755,11 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         const int need = DL ? unsent : (bsr < unsent ? bsr : unsent);
         bool new_el = any_free && need > 0 && !has_rx && act;
         has_rx = has_rx && act;
+        if constexpr (MC) {                        // handover interruption (mac.py:249-251, radio.py:450-453)
+            const bool ok_ = g >= ho_end;
+            has_rx = has_rx && ok_;
+            new_el = new_el && ok_;
+        }
         int rx_nsb = 0;
 #pragma unroll
         for (int p = 0; p < P; ++p) rx_nsb = p == rx_p ? hm_nsb(hmeta[p]) : rx_nsb;
@@ -547,8 +771,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             int mi[S];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                // UL: the PSD over one RBG (mac_ul.py:154-171); DL: sinr_ref + csi (mac_dl.py:42-43)
-                float est = DL ? REF(s) + csi[s] : (REF(s) - s_wdb[s]) + csi[s];
+                // UL: the PSD over one RBG, at most the power-control PSD (mac_ul.py:154-171); DL: sinr_ref + csi
+                // (mac_dl.py:42-43)
+                const float wd = MC ? (s_wdb[s] > pc ? s_wdb[s] : pc) : s_wdb[s];
+                float est = DL ? REF(s) + csi[s] : (REF(s) - wd) + csi[s];
                 eo[s] = pm.olla ? est + olla : est;
                 mi[s] = 0;
             }
@@ -593,7 +819,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         for (int s = 0; s < S; ++s)
             s_met[s * STEP_WAVE + lane] = pm.sched == 0 ? rate[s] / avg_c : (pm.sched == 1 ? rate[s] : (float)(g - last_tx));
         auto metric_of = [&](int s) -> float { return s_met[s * STEP_WAVE + lane]; };
-        // retransmission admission (mac.py:300-304): rank by the metric sum, admit while the RBG counts fit
+        // retransmission admission (mac.py:300-313): rank by the metric sum inside each scheduler, admit while the RBG
+        // counts fit (the segment's total fitting implies every cell's)
         if (seg_any(has_rx, rb, lane)) {
             int val = has_rx ? rx_nsb : 0;
             int tot = bsum(val, rb);
@@ -608,6 +835,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                     float kj = __shfl(rkey, sb + j, 64);
                     int vj = __shfl(val, sb + j, 64);
                     bool before = (kj > rkey) || (kj == rkey && j <= r);
+                    if constexpr (MC) before = before && __shfl(serv, sb + j, 64) == serv;
                     cum += before ? vj : 0;
                 }
                 has_rx = has_rx && cum <= S;
@@ -626,12 +854,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             int m = want ? __float_as_int(metric_of(s) + prio) : -1;
             if (pm.retx_prio) {
                 bool wr = want && has_rx;
-                if (seg_any(wr, rb, lane) && !wr) m = -1;
+                if (cell_any(wr) && !wr) m = -1;
             }
-            // argmax over the robots, first robot on ties (torch argmax); -1 marks robots that do not bid
-            const int mx = bmax_i(m, rb);
-            const int first = seg_first(m == mx, rb, lane);
-            const bool sel = m >= 0 && first == r;
+            // argmax over the robots of the scheduler, first robot on ties (torch argmax); -1: no bid
+            const bool sel = winner(m);
             if (sel) { won |= 1u << s; ++cnt; }
             left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
         }
@@ -642,12 +868,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             cnt = __popc(won);
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                bool avs = seg_any((rel_rs >> s) & 1u, rb, lane);
+                bool avs = cell_any((rel_rs >> s) & 1u);
                 bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
                 const int m = want ? __float_as_int(metric_of(s)) : -1;
-                const int mx = bmax_i(m, rb);
-                const int first = seg_first(m == mx, rb, lane);
-                const bool sel = m >= 0 && first == r && avs;
+                const bool sel = winner(m) && avs;
                 if (sel) { won |= 1u << s; ++cnt; }
                 left = left - (sel ? rate[s] : 0.0f);
             }
@@ -659,8 +883,9 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         const bool tx_rx = has_rx && n_sb == rx_nsb && n_sb > 0;
         const bool tx_new = new_el && n_sb > 0;
         const bool tx = tx_rx || tx_new;
-        // power split (mac_ul.py:173-180): PUSCH power spread over n_prb PRBs
-        const float sp = 10.0f * log10f(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
+        // power split (mac_ul.py:173-180): PUSCH power spread over n_prb PRBs, at least the power-control backoff
+        const float sp0 = 10.0f * log10f(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
+        const float sp = MC ? (sp0 > pc ? sp0 : pc) : sp0;
         // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
         const float lnw = lse_logw<S>(s_logw, won);
         // ---- link adaptation for new TBs (phy.select_mcs): the highest MCS meeting the BLER target ----
@@ -771,6 +996,40 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             if constexpr (DL) gn[s] = gain_of(s);
             else csi[s] = gain_of(s);
         }
+        // ---- several cells: same-slot UL interference (NRNet._ul_ici, nr_engine.py:799-816) ----
+        // Every robot that transmits adds, at each other cell c and RBG s it holds, its received power
+        // 10^((((pg_c + ue_tx) - ref_db) - split + gain_cs) / 10) (mW per PRB). Each lane writes its NC S terms (zeros
+        // elsewhere) to its LDS column; one lane per (cell, RBG) of the env sums its column over the robots in torch's
+        // order, and updates that gNB's N+I estimate (EWMA li_a now + li_b estimate) and the I/N statistic.
+        if constexpr (MC) {
+            if (cl.use_int) {
+                const bool txing = tx && act;
+                float* const s_t = s_x + S * STEP_WAVE;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const float psd = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        float v = 0.f;
+                        if (txing && c != serv && ((won >> s) & 1u)) v = from_db(psd + gain_cs(c * S + s));
+                        s_t[(c * S + s) * STEP_WAVE + lane] = v;
+                    }
+                }
+                __syncthreads();
+                if (e < E) {
+                    const int sb = lane & ~(rb - 1);
+                    for (int q = r; q < NCS; q += rb) {
+                        const float* col = s_t + q * STEP_WAVE + sb;
+                        const float itf = aten_outer_sum(R, q < 32 * (NCS / 32), [&](int i) { return col[i]; });
+                        s_if[q] = itf;
+                        const float now = cl.noise_mw + itf;
+                        s_ni[q] = cl.li_b == 0.0f ? now : cl.li_a * now + cl.li_b * s_ni[q];
+                    }
+                }
+                __syncthreads();
+                if (r == 0 && e < E) ion = ion + aten_row_sum(NCS, [&](int i) { return s_if[i] / cl.noise_mw; });
+            }
+        }
         // ---- decoding on the actual channel (mac.py:428-454, mac_ul.py:185-192) ----
         bool ok = false, fail = false, exh = false;
         float comb = comb_p, lexp = lexp_p, nrb = nrb_p;
@@ -782,6 +1041,8 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 float x;                          // UL: ref - split + gain (mac_ul.py:185-192); DL: ref + gain
                 if constexpr (DL) x = REF(s) + gn[s];
                 else x = (REF(s) - sp) + csi[s];
+                if constexpr (MC)                 // minus the measured N+I over the estimate (nr_engine.py:815)
+                    if (cl.use_int) x = x - ((10.0f * log10f(cl.noise_mw + s_if[serv * S + s])) - ni_la[s]);
                 nan |= x != x;
                 s_x[s * STEP_WAVE + lane] = x;
             }
@@ -882,6 +1143,15 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const int n_hist = n_ul < n_ul_max ? n_ul : n_ul_max;
 
     // ================================================================ end of step (NRNet._finish)
+    if constexpr (MC) {                            // A3 triggers after the step's last active slot (nr_engine.py:780)
+        if (act && !fired && k_ho >= 0) handover(g0 + k_ho);
+        // the reported SINR (serving_sinr_db, nr_engine.py:709-713): full power over snr_ref_prbs PRBs against the
+        // serving gNB's wideband N+I estimate, ((pg + ue_tx) - ref_db) - 10 log10(mean_s ni)
+        float nrow[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) nrow[s] = s_ni[serv * S + s];
+        snr_out = ((sel_of(pgc, serv) + pm.ue_tx) - cl.ref_db) - 10.0f * log10f(aten_sum<S>(nrow) / (float)S);
+    }
     const int t = (int)T;
     const int ack_end = ack_ptr();
     const int ep0 = act ? st.epoch[ee] : 0;
@@ -900,8 +1170,14 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         int fin = ldo(lk.q_fin + fr, o_fr);
         const uint32_t meta = ldo(lk.q_meta + fr, o_fr);
         bool lost = meta & 1u;
-        // replay the slots: lost marking (RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
+        // a handover's loss, at its place among the slots: frames not completed and not lost by then
+        const bool ho_hit = MC && ((ho_mask >> (f & 63)) & 1ull) != 0ull;
+        // replay the slots: lost marking (handover, RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
         for (int j = 0; j < n_hist; ++j) {
+            if (ho_hit && j == ho_j && fin == FIN_NONE) {
+                if (!lost) ++lost_new;
+                lost = true;
+            }
             if (pm.harq_drop) {
                 int xl = exlo_l[j * STEP_WAVE + lane], xh = exhi_l[j * STEP_WAVE + lane];
                 if (xh > xl && qs < xh && qe > xl) {
@@ -910,6 +1186,10 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
                 }
             }
             if (fin == FIN_NONE && !lost && qe <= ack_l[j * STEP_WAVE + lane]) fin = g0 + s_ulrel[j];
+        }
+        if (ho_hit && ho_j >= n_hist && fin == FIN_NONE) {
+            if (!lost) ++lost_new;
+            lost = true;
         }
         double fin_d = INFINITY;
         if (fin != FIN_NONE) {
@@ -1023,10 +1303,18 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
         if (arr.counts) sto(lk.enq, o_r, enq);
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            sto(lk.csi + s * R, o_sr, csi[s]);
-            if constexpr (!DL)
-                if (pm.fading) { sto(st.h_re + s * R, o_sr, hr[s]); sto(st.h_im + s * R, o_sr, hi[s]); }
+        for (int s = 0; s < S; ++s) sto(lk.csi + s * R, o_sr, csi[s]);
+        if constexpr (!DL) {
+            if (pm.fading) {
+                uint32_t o_hr = o_hr0;
+                asm volatile("" : "+v"(o_hr));
+#pragma unroll
+                for (int q = 0; q < NCS; ++q) { sto(st.h_re + q * R, o_hr, hr[q]); sto(st.h_im + q * R, o_hr, hi[q]); }
+            }
+        }
+        if constexpr (MC) {
+            sto(cl.serv, o_r, serv); sto(cl.a3_cand, o_r, a3_cand); sto(cl.a3_cnt, o_r, a3_cnt);
+            sto(cl.ho_end, o_r, ho_end); sto(cl.n_ho, o_r, n_ho);
         }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -1046,7 +1334,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
             int qb = enq - ack_new;
             sto(out.queue_bytes, o_r, (float)(qb > 0 ? qb : 0));
             sto(out.sinr_db, o_r, snr_out);
-            if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)0);
+            if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)serv);
         }
     }
     }
@@ -1058,6 +1346,12 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
     const int v_pend = bsum(act ? c_new_pend : 0, rb), v_bok = bsum(act ? c_bytes_ok : 0, rb);
     const int v_bnew = bsum(act ? c_bytes_new : 0, rb), v_prb = bsum(act ? c_prb : 0, rb);
     __syncthreads();                                  // histogram atomics of every lane are done
+    if constexpr (MC) {
+        if (e < E) {
+            for (int q = r; q < NCS; q += rb) cl.ni_ul[(size_t)e * NCS + q] = s_ni[q];
+            if (r == 0) { cl.pending[e] = 0; cl.ion[e] = ion; }
+        }
+    }
     if (r == 0 && e < E) {
         if constexpr (!DL) {
             out.det_env[e] = det_any;
@@ -1079,6 +1373,7 @@ __global__ __launch_bounds__(STEP_WAVE, 2) void nr_step_kernel(
 struct StepArgs {
     InetNrState st;
     const InetNrDlState* dl;          // NULL: the UL step; else the DL step of this link
+    const InetNrCells* cells;         // NULL: one cell; else the multi-cell step (NRNet.step_cells)
     InetNrTables tb;
     InetNrParams pm;
     const InetNrRow* rows;
@@ -1097,14 +1392,23 @@ typedef void (*StepFn)(const StepArgs&);
 
 template <int S, int P, bool IR, bool VREF, int RBT>
 void launch_step(const StepArgs& a) {
+    const InetNrCells none{};
     if (a.dl)
-        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
-                           a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
-                           a.n_data, a.arr);
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState, 1>), dim3(a.grid), dim3(STEP_WAVE),
+                           a.lds, a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
+                           a.n_data, a.arr, none);
     else
-        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
-                           a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
-                           a.arr);
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState, 1>), dim3(a.grid), dim3(STEP_WAVE),
+                           a.lds, a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
+                           a.n_data, a.arr, none);
+}
+
+// the multi-cell step: NC cells, pose input, runtime segment width
+template <int S, int P, bool IR, int NC>
+void launch_step_mc(const StepArgs& a) {
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 0, InetNrState, NC>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
+                       a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
+                       a.arr, *a.cells);
 }
 
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband
@@ -1124,5 +1428,16 @@ StepFn pick_step_s(int P, bool ir, bool vref, int rb) {
 
 StepFn pick_step_s13(int P, bool ir, bool vref, int rb);   // nr_step_s13.hip
 StepFn pick_step_s8(int P, bool ir, bool vref, int rb);    // nr_step_s8.hip
+
+// multi-cell builds (NC = 3): every (P, IR)
+template <int S>
+StepFn pick_step_mc_s(int P, bool ir) {
+#define INET_PICK_MC(PP) \
+    if (P == PP) return ir ? &launch_step_mc<S, PP, true, 3> : &launch_step_mc<S, PP, false, 3>;
+    INET_PICK_MC(2) INET_PICK_MC(4) INET_PICK_MC(8) INET_PICK_MC(16)
+#undef INET_PICK_MC
+    return nullptr;
+}
+StepFn pick_step_mc(int S, int C, int P, bool ir);         // nr_step_mc.hip
 
 }  // namespace inet

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     if (rob) {
         if (input_kind == 0) {
             float px = xin[ir * 2], py = xin[ir * 2 + 1];
-            rx = radio_rx_dbm(pm, px, py, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3);
+            rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3);
         } else if (input_kind == 1) {
             rx = xin[ir] + pm.noise_dbm;
         } else {

@@ -71,7 +71,12 @@ def refusals(cfg: NRConfig):
     def no(cond, what, why):
         if cond:
             out.append((what, why))
-    no(cfg.n_cells != 1, "several cells (n_cells > 1)", "one cell's scheduler and HARQ per env")
+    mc = cfg.n_cells > 1
+    no(mc and cfg.n_cells != 3, f"n_cells={cfg.n_cells}", "one or three cells per env in this build")
+    no(mc and cfg.dl, "the downlink with several cells", "the multi-cell step runs the uplink")
+    no(cfg.rlf, "radio link failure (rlf=True)", "A3 handover without RLF")
+    no(mc and cfg.rician_mode is not None, "Rician fading with several cells", "Rayleigh fading on every link")
+    no(mc and cfg.frame_buffer > 64, "frame_buffer > 64 with several cells", "a 64-bit handover loss mask")
     no(not cfg.ul, "ul=False (a downlink-only engine)", "the UL link runs every step")
     no(cfg.dl and cfg.duplex != "tdd", "the FDD downlink carrier", "TDD (one carrier)")
     no(cfg.ul_grant_model != "lumped", "ul_grant_model='bsr'", "lumped SR grants only")
@@ -82,7 +87,8 @@ def refusals(cfg: NRConfig):
     no(cfg.pf_update != "slot" or cfg.pf_avg_idle != "decay", "pf_update / pf_avg_idle switches", "slot EWMA")
     no(cfg.ul_retx_sched != "ofdma" or cfg.ul_amc_alloc != "current", "ul_retx_sched / ul_amc_alloc switches",
        "OFDMA retransmissions, current-allocation AMC")
-    no(cfg.ul_pc_on or cfg.ul_tpc, "UL power control (ul_pc / ul_tpc)", "full-power PSD split")
+    no((cfg.ul_pc_on and not mc) or cfg.ul_tpc, "UL power control at one cell / closed-loop TPC",
+       "full-power PSD split (open-loop fractional power control with several cells)")
     no(cfg.ul_power != "allocated", "ul_power='whole_band'", "allocated power split")
     no(cfg.rician_mode == "los", "Rician K from the LOS state", "fixed rician_k_db or Rayleigh")
     no(cfg.fading_freq_corr or cfg.fading_doppler != "global", "frequency-correlated / per-robot Doppler fading",
@@ -101,7 +107,8 @@ def refusals(cfg: NRConfig):
         no(cfg.tr38901_los not in ("los", "nlos"), "tr38901_los='stochastic'", "a fixed LOS state (los / nlos)")
         no(cfg.tr38901_scenario == "RMa", "the RMa scenario", "UMa, UMi, InH, InF")
         no(cfg.tr38901_scenario.startswith("InF") and cfg.tr38901_los == "nlos", "InF NLOS", "InF LOS")
-    no(cfg.n_subbands not in (8, 13), f"{cfg.n_subbands} subbands", "8 or 13 RBGs in this build")
+    no(cfg.n_subbands not in ((8, 13, 14) if mc else (8, 13)), f"{cfg.n_subbands} subbands",
+       "8 or 13 RBGs (several cells: 8, 13 or 14) in this build")
     no(cfg.n_harq not in (2, 4, 8, 16), f"n_harq={cfg.n_harq}", "2, 4, 8 or 16 HARQ processes in this build")
     no(cfg.max_harq_tx > 16, "max_harq_tx > 16", "up to 16 transmissions")
     no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
@@ -111,8 +118,8 @@ def refusals(cfg: NRConfig):
 
 
 class HipNREngine:
-    """NR engine (level "L2", one cell; uplink, and the downlink with NRConfig(dl=True)) on MI355X. API of
-    isaac_net.core.engine.NREngine."""
+    """NR engine (level "L2": one cell with the uplink, and the downlink with NRConfig(dl=True); or several cells
+    with the uplink, NRNet.step_cells) on MI355X. API of isaac_net.core.engine.NREngine."""
 
     level = "L2"
     backend = "hip"
@@ -135,6 +142,7 @@ class HipNREngine:
             seed = cfg.seed if cfg.seed is not None else int(torch.randint(0, 2 ** 62, ()).item())
         self.seed = int(seed)
         self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
+        self.C = cfg.n_cells
         self.N = cfg.slots_per_step
         self.out_format = out_format
         self.tabs = PhyTables(cfg.mcs_table, cfg.bler_target, max(cfg.max_harq_tx, 2), cfg.ul_mcs_max)
@@ -162,7 +170,7 @@ class HipNREngine:
         self.st = {
             "sent": z(E, R), "floor_": z(E, R), "bsr": z(E, R), "sr_t": z(E, R, v=-1), "last_tx": z(E, R, v=-1),
             "olla": z(E, R, dt=f32), "avg": z(E, R, dt=f32, v=100.0), "enq": z(E, R), "qlen": z(E, R),
-            "csi": z(E, S, R, dt=f32), "h_re": z(E, S, R, dt=f32), "h_im": z(E, S, R, dt=f32),
+            "csi": z(E, S, R, dt=f32), "h_re": z(E, self.C * S, R, dt=f32), "h_im": z(E, self.C * S, R, dt=f32),
             "h_meta": z(E, P, R), "h_lo": z(E, P, R), "h_hi": z(E, P, R), "h_ready": z(E, P, R), "h_tbs": z(E, P, R),
             "h_comb": z(E, P, R, dt=f32), "h_lexp": z(E, P, R, dt=f32, v=-math.inf), "h_nrb": z(E, P, R, dt=f32),
             "q_cap": z(E, F, R, v=-1), "q_start": z(E, F, R), "q_end": z(E, F, R), "q_fin": z(E, F, R, v=BIG_SLOT),
@@ -170,7 +178,7 @@ class HipNREngine:
             "spec_re": z(E, R, dt=f32), "spec_im": z(E, R, dt=f32), "k_lin": z(E, R, dt=f32),
             "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
             "ctr_submit": z(E), "epoch": z(E),
-            "field": z(E, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
+            "field": z(E, self.C, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
             "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
             "clock": z(1, dt=torch.int64),
         }
@@ -180,6 +188,32 @@ class HipNREngine:
         for name, _ in _lib.InetNrState._fields_:
             setattr(s, name, self.st[name].data_ptr())
         self._cstate = s
+        self._ccells = None
+        if self.C > 1:                       # association and N+I estimates (NRNet._init_cells, nr_engine.py:216-230)
+            C_ = self.C
+            self.cst = {"serv": z(E, R), "a3_cand": z(E, R, v=-1), "a3_cnt": z(E, R), "ho_end": z(E, R),
+                        "n_ho": z(E, R), "pending": z(E, v=1), "ni_ul": z(E, C_, S, dt=f32), "ion": z(E, dt=f32)}
+            c = _lib.InetNrCells()
+            for name, t_ in self.cst.items():
+                setattr(c, name, t_.data_ptr())
+            xy = [v for p_ in cfg.gnb_xy() for v in p_]
+            c.gnb_xy[:len(xy)] = xy
+            c.C = C_
+            c.ttt = int(round(cfg.a3_ttt_ms / cfg.slot_ms))
+            c.ho_int = int(round(cfg.ho_interruption_ms / cfg.slot_ms))
+            c.ho_flush = int(cfg.ho_rlc == "flush")
+            c.use_int = int(cfg.noise_model == "thermal" and cfg.ul_interference)
+            c.pc_on = int(cfg.ul_pc_on)
+            c.has_floor = int(cfg.a3_min_target_rsrp_dbm is not None)
+            c.a3_off, c.a3_hyst = cfg.a3_offset_db, cfg.a3_hyst_db
+            if c.has_floor:
+                c.floor_rx = cfg.a3_min_target_rsrp_dbm - (cfg.gnb_tx_dbm - 10 * math.log10(12 * cfg.nprb)
+                                                           - cfg.ue_tx_dbm)
+            c.noise_mw = 10 ** (cfg.noise_dbm_per_prb("gnb") / 10)
+            c.ref_db = 10 * math.log10(cfg.snr_ref_prbs)
+            c.li_a, c.li_b = cfg.li_alpha, 1 - cfg.li_alpha
+            c.pc_p0, c.pc_alpha = cfg.ul_pc_p0_dbm, cfg.ul_pc_alpha
+            self._ccells = c
         if self.dl:
             self.dst = {
                 "sent": z(E, R), "floor_": z(E, R), "last_tx": z(E, R, v=-1), "olla": z(E, R, dt=f32),
@@ -254,6 +288,7 @@ class HipNREngine:
         p.max_tx, p.sr_delay, p.ul_rtt, p.rlc_retx = cfg.max_harq_tx, cfg.sr_delay, cfg.ul_rtt, cfg.rlc_retx_slots
         p.timeout, p.tb_oh = cfg.timeout_steps, cfg.tb_overhead_bytes
         p.n_fields, p.n_modes = self._n_fields, cfg.shadow_modes
+        p.n_cells = self.C
         p.seed_key = C.c_int32(seed_key(self.seed) - (1 << 32) if seed_key(self.seed) >= 1 << 31
                                else seed_key(self.seed)).value
         p.olla_up = cfg.olla_up_db
@@ -427,6 +462,9 @@ class HipNREngine:
             self._last_hid = torch.zeros_like(self._last_hid)
             _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), None, 0,
                                          self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+            if self._ccells is not None:
+                _lib.check(lib.inet_nr_cells_reset(C.byref(self._ccells), C.byref(self._cparams), None,
+                                                   self._stream()), "cells reset")
             if self.dl:
                 _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), None, self._stream()),
                            "dl reset")
@@ -446,6 +484,9 @@ class HipNREngine:
         m8 = mask.to(torch.uint8).contiguous()
         _lib.check(lib.inet_nr_reset(C.byref(self._cstate), C.byref(self._cparams), m8.data_ptr(), self.T,
                                      self._k_lin0(), self._dcorr_c, self._spectrum, self._stream()), "reset")
+        if self._ccells is not None:
+            _lib.check(lib.inet_nr_cells_reset(C.byref(self._ccells), C.byref(self._cparams), m8.data_ptr(),
+                                               self._stream()), "cells reset")
         if self.dl:
             _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), m8.data_ptr(),
                                             self._stream()), "dl reset")
@@ -569,6 +610,9 @@ class HipNREngine:
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
+        if self.C > 1 and kind != 0:
+            raise ValueError("several cells: pass poses [E,R,2|3] (the path gain of every robot-cell link comes from "
+                             "the radio)")
         plan = self._plan(T, kind)
         dl = None
         if self.dl:
@@ -664,7 +708,19 @@ class HipNREngine:
         ev = self.kernel_events
         if ev is not None:
             ev.begin(torch.cuda.current_stream(self.dev))
-        if arrivals is None:
+        if self._ccells is not None:                  # NRNet.step_cells (inet_nr_step_cells), arrivals fused or not
+            a = None
+            if arrivals is not None:
+                cfg = self.config
+                o["arrivals_accepted"] = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
+                a = _lib.InetNrArrivals(arrivals.data_ptr(), self._sizes.data_ptr(), o["arrivals_accepted"].data_ptr(),
+                                        arrivals.shape[-1], int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
+                                        cfg.pkt_overhead_bytes)
+            _lib.check(self._lib.inet_nr_step_cells(
+                C.byref(self._cstate), C.byref(self._ccells), C.byref(self._ctab), C.byref(self._cparams),
+                plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(), hid.data_ptr(), C.byref(co),
+                None if a is None else C.byref(a), self._stream()), "step")
+        elif arrivals is None:
             _lib.check(self._lib.inet_nr_step(C.byref(self._cstate), C.byref(self._ctab), C.byref(self._cparams),
                                               plan["rows"].data_ptr(), plan["n_rows"], T, xin.data_ptr(),
                                               hid.data_ptr(), C.byref(co), self._stream()), "step")
@@ -696,8 +752,8 @@ class HipNREngine:
         Returns a GraphStep; calling it with (poses [E,R,2|3], counts [E,R,NC]) replays the step. The schedule of
         every replayed step must match the recorded one (the same TDD / SR / CQI phase and fading slot spacing),
         which holds when the control step spans whole periods."""
-        if self.dl:
-            raise HipUnsupported("graph_step with the downlink (dl=True): use step()")
+        if self.dl or self.C > 1:
+            raise HipUnsupported("graph_step with the downlink (dl=True) or several cells: use step()")
         return GraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     # ------------------------------------------------------------------ statistics
@@ -713,7 +769,7 @@ class HipNREngine:
             res["ntx_hist"] = h[:, 0].sum(0).double().tolist()
             res["rv_tx"] = h[:, 1].sum(0).double().tolist()
             res["rv_fail"] = h[:, 2].sum(0).double().tolist()
-            res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * n_slots
+            res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * self.C * n_slots
             return res
         out = {"ul": link(self.st, self._ul_slots_run)}
         if self.dl:
@@ -763,14 +819,22 @@ class HipNREngine:
         L = lambda x: x.long()  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1)  # noqa: E731
         out = self._link_sd("ul", st)
+        E, R, S = self.E, self.R, self.S
+        hh = lambda x: rs(x).reshape(E, R, self.C, S) if self.C > 1 else rs(x)  # noqa: E731
         out.update({
-            "net.h": torch.stack([rs(st["h_re"]), rs(st["h_im"])], -1), "eng.epoch": L(st["epoch"]),
+            "net.h": torch.stack([hh(st["h_re"]), hh(st["h_im"])], -1), "eng.epoch": L(st["epoch"]),
             "eng._last_snr": self._last_snr, "eng._last_hid": self._last_hid,
             "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"]),
         })
         if self.dl:
             out.update(self._link_sd("dl", self.dst))
             out["net.dl_newest"] = L(self.dst["newest"])
+        if self.C > 1:                                # CellAssociation and NRNet._reset_cells state
+            c = self.cst
+            out.update({"assoc." + n: L(c[n]) for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho")})
+            out["assoc.pending"] = c["pending"] != 0
+            out["net.ni_ul"] = c["ni_ul"]
+            out["net.ioN[ul]"] = c["ion"]
         if cfg.rician_mode == "fixed":
             k = st["k_lin"]
             out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1), "net.k_los": k, "net.k_in": k,
@@ -827,8 +891,17 @@ class HipNREngine:
             self._link_load("dl", self.dst, sd)
             self.dst["newest"].copy_(I(g("net.dl_newest")))
         h = g("net.h")
+        if self.C > 1:                                # [E,R,C,S,2] -> [E][C S][R]
+            h = h.reshape(self.E, self.R, self.C * self.S, 2)
         st["h_re"].copy_(rs(h[..., 0]))
         st["h_im"].copy_(rs(h[..., 1]))
+        if self.C > 1:
+            c = self.cst
+            for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho"):
+                c[n].copy_(I(g("assoc." + n)))
+            c["pending"].copy_(I(g("assoc.pending")))
+            c["ni_ul"].copy_(g("net.ni_ul").float())
+            c["ion"].copy_(g("net.ioN[ul]").float())
         st["epoch"].copy_(I(g("eng.epoch")))
         st["episode"].copy_(I(g("rng.episode")))
         st["ctr_submit"].copy_(I(g("rng.ctr[1]")))
@@ -853,7 +926,7 @@ class HipNREngine:
 
     def _ck_key(self, k):
         """Owner key -> the key of the reference's checkpoint (the attribute path from NREngine)."""
-        if k.startswith(("ul.", "dl.")):
+        if k.startswith(("ul.", "dl.", "assoc.")):
             return "net." + k
         return self._CK_ENG.get(k, k)
 
@@ -872,15 +945,15 @@ class HipNREngine:
         out = {self._ck_key(k): v.clone() for k, v in self.owner_state().items()}
         out["net.rng.env"] = st["env_id"].long().clone()
         for pre, fi in self._field_keys():
-            f = st["field"][:, fi]
-            out[pre + ".k"] = f[None, ..., :2].clone()
-            out[pre + ".phi"] = f[None, ..., 2].clone()
+            f = st["field"][:, :, fi].permute(1, 0, 2, 3)          # [C, E, K, 3]
+            out[pre + ".k"] = f[..., :2].clone()
+            out[pre + ".phi"] = f[..., 2].clone()
         links = [("ul", st, self._ul_slots_run)] + ([("dl", self.dst, self._dl_slots_run)] if self.dl else [])
         for name, ls, n_slots in links:
             c = ls["ctr"]
             for i, k in enumerate(CTR_NAMES):
                 out[f"net.{name}.ctr[{k}]"] = c[:, i].sum().float()
-            out[f"net.{name}.ctr[prb_avail]"] = torch.tensor(float(sum(cfg.subband_prbs)) * E * n_slots,
+            out[f"net.{name}.ctr[prb_avail]"] = torch.tensor(float(sum(cfg.subband_prbs)) * E * self.C * n_slots,
                                                              device=self.dev)
             h = ls["hist"].float()
             out[f"net.{name}.ntx_hist"] = h[:, 0].sum(0)
@@ -926,8 +999,8 @@ class HipNREngine:
             st["env_id"].copy_(g("net.rng.env").to(torch.int32))
         for pre, fi in self._field_keys():
             if pre + ".k" in sd:
-                st["field"][:, fi, :, :2].copy_(g(pre + ".k")[0])
-                st["field"][:, fi, :, 2].copy_(g(pre + ".phi")[0])
+                st["field"][:, :, fi, :, :2].copy_(g(pre + ".k").permute(1, 0, 2, 3))
+                st["field"][:, :, fi, :, 2].copy_(g(pre + ".phi").permute(1, 0, 2))
             elif strict:
                 raise KeyError(f"load_state_dict: missing from the state dict: {pre}.k")
         if "net.rng.s0" in sd:
@@ -948,7 +1021,7 @@ class HipNREngine:
             h[:, 1] = g(f"net.{name}.rv_tx").round().long()
             h[:, 2] = g(f"net.{name}.rv_fail").round().long()
             ls["hist"].copy_(h)
-            w = float(sum(cfg.subband_prbs)) * self.E
+            w = float(sum(cfg.subband_prbs)) * self.E * self.C
             n_slots = int(round(float(sd[f"net.{name}.ctr[prb_avail]"]) / w))
             if name == "ul":
                 self._ul_slots_run = n_slots

@@ -14,6 +14,11 @@ control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 
   wifi_dcf_slots  the same inputs on level WIFI_DCF (per-slot CSMA/CA with integer backoff counters).
   rl_scale_dl  rl_scale with the downlink on (dl=True: 40 DL data slots and 5 CQI reports per step) and 2000 B DL
               messages at Poisson 0.5 per robot-step (at most 2).
+  mc_interf   1024 envs x 64 robots, 3 cells on a hexagonal grid 150 m apart (centroid at the centre of a 200 m square),
+              max-RSRP association without handover (a3_offset_db = inf), thermal noise with the same-slot UL
+              interference of the other cells' scheduled robots, open-loop fractional power control (on by default
+              with several cells), PF over 106 PRBs (14 RBGs), K = 10, 1200 B at Poisson 0.3, UMi LOS, correlated
+              Rayleigh fading on every robot-cell link, 1 m/s random walk in the square.
 Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
 the square or disc; arrival counts per class), identical for the GPU engine and the CPU oracle.
 """
@@ -45,6 +50,15 @@ def rl_scale_config(**kw):
     return NRConfig(**base)
 
 
+def mc_interf_config(**kw):
+    base = dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", pf_window=100.0,
+                n_harq=8, max_harq_tx=5, frame_buffer=16, msg_sizes=(1200.0,), n_cells=3, cell_layout="hex",
+                cell_isd_m=150.0, cell_center_m=(100.0, 100.0), noise_model="thermal", a3_offset_db=float("inf"),
+                channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0, seed=0)
+    base.update(kw)
+    return NRConfig(**base)
+
+
 def wifi_dcf_config(**kw):
     from .wifi_config import WifiConfig
     base = dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,), cell_positions_m=((0.0, 0.0),),
@@ -58,6 +72,7 @@ WORKLOADS = {
     "rl_scale": dict(cfg=rl_scale_config, E=4096, R=32, arena=200.0, speed=1.0, rates=(0.8, 0.1), steps=500),
     "rl_scale_dl": dict(cfg=lambda **kw: rl_scale_config(dl=True, **kw), E=4096, R=32, arena=200.0, speed=1.0,
                         rates=(0.8, 0.1), steps=500, dl_rates=(0.5,), dl_size=2000.0),
+    "mc_interf": dict(cfg=mc_interf_config, E=1024, R=64, arena=200.0, speed=1.0, rates=(0.3,), steps=300),
     "wifi_dcf": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
                      level="WIFI"),
     "wifi_dcf_slots": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,

@@ -8,15 +8,15 @@ A from-scratch torch-CPU restatement of isaac-net's NR engine, reference backend
   NREngine        core/engine.py:319-960   (clock, submit, add_dl_frames, step, partial reset)
   NRNet           core/nr_engine.py:171-888 (reset, fading AR(1) + Rician, step_rx, step, _finish; with several cells
                   step_cells, _ul_ici, _handover, _pc_backoff, serving_sinr_db)
-  CellAssociation core/radio.py:303-437 (max-RSRP attach, A3 plan / switch, handover interruption; no RLF)
+  CellAssociation core/radio.py:303-453 (max-RSRP attach, A3 plan / switch, handover interruption; no RLF)
   UlMac/MacLink   core/mac_ul.py:58-260, core/mac.py:65-616 (lumped SR/grants, PF/maxCI/RR scheduling, retx admission,
                   RBG allocation, EESM / mean-dB link adaptation, HARQ cc/none/ir_lena, rlc_am/drop, OLLA, PF average,
                   RLC in-order delivery, end_step, compact)
   DlMac           core/mac_dl.py:19-49 (CQI report "mcs" / "38214", estimate, decode SINR, HARQ-ACK timing via K1)
   FrameQueue      core/queues.py:36-143
   NRRng           core/nr_rng.py, core/proto/rng.py (counter hash, Box-Muller)
-  RadioMC         core/radio.py:59-277 (log_distance, C cells), core/channels/models.py:34-167 + tr38901.py (deterministic LOS
-                  state "los" / "nlos"), core/channels/fields.py:38-64 (plane-wave shadowing)
+  RadioMC         core/radio.py:59-277 (log_distance, C cells), core/channels/models.py:34-167 + tr38901.py
+                  (deterministic LOS state "los" / "nlos"), core/channels/fields.py:38-64 (plane-wave shadowing)
 The element-wise operations, the reduction calls and their order are those of the reference, so that on the same
 CPU the oracle is bitwise equal to the reference path (pinned by the golden trajectories under tests/golden/).
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
@@ -519,7 +519,7 @@ def pick(x, idx):
 
 
 class Association:
-    """CellAssociation without radio link failure (radio.py:303-437): max-RSRP attach after a reset (associate), the
+    """CellAssociation without radio link failure (radio.py:303-453): max-RSRP attach after a reset (associate), the
     A3 condition evaluated once per control step with the exact slot at which the handover fires (plan), the switch
     and the handover interruption (schedulable). RSRP here is rx = path gain + ue_tx_dbm [E,R,C]."""
 

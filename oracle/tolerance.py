@@ -31,6 +31,29 @@ def sinr_bound(pos, field, sig, amp, sinr):
     return 1e-5 * np.maximum(np.abs(s), 1.0) + 4 * float(np.spacing(np.float32(128.0))) + 2 * sig * amp * d.sum(-1)
 
 
+def pg_bound(pos, field, sig, amp):
+    """Bound [E,R] (dB) on the path-gain difference of one cell's link between two evaluations of the radio whose
+    wave vectors differ by an ulp (the shadowing term of sinr_bound) plus 4 ulp of 128 dB for the rest of the link
+    budget. pos [E,R,2], field [E,K,3]."""
+    pos = np.asarray(pos, dtype=np.float64)
+    f = np.asarray(field, dtype=np.float64)
+    arg = pos[..., None, 0] * f[:, None, :, 0] + pos[..., None, 1] * f[:, None, :, 1] + f[:, None, :, 2]
+    d = np.abs(pos[..., None, 0]) * _ulp(f[:, None, :, 0]) + np.abs(pos[..., None, 1]) * _ulp(f[:, None, :, 1]) + \
+        _ulp(arg)
+    return 4 * float(np.spacing(np.float32(128.0))) + 2 * sig * amp * d.sum(-1)
+
+
+def ni_rel_bound(pos, fields, sig, amp):
+    """Relative bound [E,C] on each gNB's N+I estimate with several cells: every interference term is
+    10^(x / 10) of a dB sum x carrying its robot's path-gain difference to that cell (pg_bound) and, through the
+    power-control backoff (alpha <= 1 times the serving link's path gain), the difference of its serving link, so
+    its relative difference is at most ln(10) / 10 times their sum; the estimate is noise plus a sum of such terms.
+    5e-5 covers the float32 rounding of x (a few ulp of ~100 dB, 1.75e-6 relative each). fields: [C] of [E,K,3]."""
+    b = np.stack([pg_bound(pos, f, sig, amp) for f in fields], -1)               # [E,R,C]
+    serv = b.max(-1, keepdims=True)                                              # any serving cell
+    return 5e-5 + (np.log(10.0) / 10.0) * (b + serv).max(1)
+
+
 def engine_radio(eng):
     """(field index, sigma, amp) of a HIP engine's radio constants."""
     p = eng._cparams

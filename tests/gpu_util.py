@@ -15,7 +15,11 @@ FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1
              "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0,
              # the DL link: its CSI is an MCS threshold minus the reference SINR (exact once the reported MCS agrees)
              "dl.csi": 1e-5, "dl.h_comb": 1e-3, "dl.h_lexp": 1e-3, "dl.h_nrb": 0.0, "dl.olla": 0.0, "dl.avg": 0.0,
-             "dl.q.fin": 0.0}
+             "dl.q.fin": 0.0,
+             # several cells: each gNB's N+I estimate and its I/N statistic. The interference terms are
+             # 10^(x / 10) of dB sums x = psd + gain around -100 dB, where one float32 ulp of x (7.6e-6 dB) is
+             # 1.75e-6 relative in mW; x carries a few ulp from the path gain, the power split and the fading gain
+             "net.ni_ul": 5e-5, "net.ioN[ul]": 5e-5}
 OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
 # The reported SINR is (pg + ue_tx) - noise with |pg| ~ 100-150 dB: one float32 ulp there is 7.6e-6 .. 1.5e-5 dB,
 # so near 0 dB a relative bound is meaningless; the absolute floor is 4 ulp of that magnitude.
@@ -91,12 +95,13 @@ def set_radio_bound(ref, s, cfg, eng, kind):
     key = next((k for k in (f"s{s:03d}/radio.k", f"s{s:03d}/radio.sf_los.k") if k in ref), None)
     if key is None:
         return
-    if key.endswith("radio.k"):
-        k3 = np.concatenate([ref[f"s{s:03d}/radio.k"][0], ref[f"s{s:03d}/radio.phi"][0][..., None]], -1)
-    else:
-        n = ("sf_los", "sf_nlos")[fi]
-        k3 = np.concatenate([ref[f"s{s:03d}/radio.{n}.k"][0], ref[f"s{s:03d}/radio.{n}.phi"][0][..., None]], -1)
-    b = sinr_bound(ref["x"][s], k3, sig, amp, ref[f"s{s:03d}/out.sinr_db"])
+    n = "radio" if key.endswith("radio.k") else "radio." + ("sf_los", "sf_nlos")[fi]
+    k_, phi = ref[f"s{s:03d}/{n}.k"], ref[f"s{s:03d}/{n}.phi"]             # [C, E, K, 2], [C, E, K]
+    # the field of each robot's serving cell (cell 0 with one cell)
+    b = np.stack([sinr_bound(ref["x"][s], np.concatenate([k_[c], phi[c][..., None]], -1), sig, amp,
+                             ref[f"s{s:03d}/out.sinr_db"]) for c in range(k_.shape[0])], -1)
+    serv = ref[f"s{s:03d}/out.serving_cell"]
+    b = np.take_along_axis(b, serv[..., None], -1)[..., 0]
     BOUND["out.sinr_db"] = b
     BOUND["eng._last_snr"] = b
 

@@ -33,11 +33,11 @@ def test_library_exports_every_declared_symbol():
     names = declared_functions()
     assert names == sorted(["inet_nr_abi_version", "inet_nr_build_info", "inet_nr_step", "inet_nr_submit",
                             "inet_nr_reset", "inet_nr_dl_step", "inet_nr_dl_submit", "inet_nr_dl_reset",
-                            "inet_nr_submit_step"])
+                            "inet_nr_submit_step", "inet_nr_step_cells", "inet_nr_cells_reset"])
     for n in names:
         assert hasattr(lib, n), n
     lib.inet_nr_abi_version.restype = ctypes.c_int32
-    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 4
     lib.inet_nr_build_info.restype = ctypes.c_char_p
     assert b"gfx950" in lib.inet_nr_build_info()
     wifi = declared_functions(WIFI_HEADER, "inet_wifi_")
@@ -50,7 +50,7 @@ def test_library_exports_every_declared_symbol():
 
 
 STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetNrDlState",
-           "InetNrArrivals", "InetWifiState", "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
+           "InetNrArrivals", "InetNrCells", "InetWifiState", "InetWifiParams", "InetWifiOutputs", "InetDcfState", "InetDcfParams")
 
 
 def test_ctypes_layout_matches_header():

@@ -139,7 +139,7 @@ def test_matches_oracle_with_submit_counts():
         x = torch.from_numpy(rs.uniform(0, 100, (E, R, 2)).astype(np.float32))
         og, oo = eng.step(None, x.to(DEV)), ora.step(None, x)
         fi, sig, amp = engine_radio(eng)
-        tol = sinr_bound(x.numpy(), eng.st["field"][:, fi].cpu().numpy(), sig, amp, oo["sinr_db"].numpy())
+        tol = sinr_bound(x.numpy(), eng.st["field"][:, 0, fi].cpu().numpy(), sig, amp, oo["sinr_db"].numpy())
         fc.step(s, og, oo, tol)
     print(f"integer flips {fc.flips}; float issues {fc.float_bad}", flush=True)
     assert len(fc.flips) <= 1 and not fc.float_bad

@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import CASES, DL_CASES
+from conftest import CASES, DL_CASES, MC_CASES
 import gpu_util
 from gpu_util import compare, load, set_radio_bound, teacher_forced
 from oracle import replay
@@ -14,7 +14,7 @@ import isaac_net_amd as P
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name", CASES + DL_CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES + MC_CASES)
 def test_teacher_forced_bit_exact(name):
     print(f"case {name} teacher-forced", flush=True)
     n_bad, n, keys_i, keys_f = teacher_forced(P, name)
@@ -25,7 +25,7 @@ def test_teacher_forced_bit_exact(name):
     assert not keys_f, keys_f
 
 
-@pytest.mark.parametrize("name", CASES + DL_CASES)
+@pytest.mark.parametrize("name", CASES + DL_CASES + MC_CASES)
 def test_free_running_bit_exact(name):
     print(f"case {name} free running", flush=True)
     ref, cfgd, kind = load(name)
@@ -68,7 +68,7 @@ def test_reset_draws_match_reference_fields():
     ref, cfgd, kind = load("c2")
     cfg = P.NRConfig(**cfgd, seed=0)
     eng = P.make_engine("L2", int(ref["E"]), int(ref["R"]), "cuda:0", cfg, seed=0)
-    f = eng.st["field"].cpu().numpy()
+    f = eng.st["field"][:, 0].cpu().numpy()
     for j, n in enumerate(("sf_los", "sf_nlos", "los_field")):
         k, phi = ref[f"s000/radio.{n}.k"][0], ref[f"s000/radio.{n}.phi"][0]
         assert np.array_equal(f[:, j, :, 2], phi)

@@ -32,7 +32,7 @@ def test_rl_scale_invariants_and_prefix_parity():
                 ora.submit(None, torch.from_numpy(np.where(c[..., ci] > i, ci + 1, 0).astype(np.int64)))
         og = eng.step(None, wl.poses[s])
         oo = ora.step(None, wl.poses[s][:E_chk].cpu())
-        tol = sinr_bound(wl.poses[s][:E_chk].cpu().numpy(), eng.st["field"][:E_chk, fi].cpu().numpy(), sig, amp,
+        tol = sinr_bound(wl.poses[s][:E_chk].cpu().numpy(), eng.st["field"][:E_chk, 0, fi].cpu().numpy(), sig, amp,
                          oo["sinr_db"].numpy())
         fc.step(s, {k: v[:E_chk] for k, v in og.items() if v.dim() >= 2}, oo, tol)
         st = eng.owner_state()

@@ -17,6 +17,16 @@ def test_refusals_name_each_unimplemented_feature():
     for word in ("several cells", "FDD downlink", "bsr", "qos"):
         assert word in names
     assert "ul=False" in " ".join(f for f, _ in EN.refusals(P.NRConfig(n_prb=52, ul=False, dl=True)))
+    # three hex cells with thermal noise (interference), power control on by default, 106 PRB (14 RBGs): runs
+    mc = dict(mu=1, n_prb=106, n_cells=3, cell_layout="hex", cell_isd_m=150.0, noise_model="thermal")
+    assert EN.refusals(P.NRConfig(**mc)) == []
+    assert EN.refusals(P.NRConfig(**mc, a3_offset_db=float("inf"), harq_fail="drop", ho_rlc="flush")) == []
+    for extra, word in ((dict(n_cells=7), "n_cells=7"), (dict(dl=True), "downlink with several cells"),
+                        (dict(rlf=True), "radio link failure"), (dict(frame_buffer=65), "frame_buffer > 64"),
+                        (dict(fading_rician=True, rician_k_db=3.0), "Rician fading with several cells"),
+                        (dict(ul_tpc=True), "TPC")):
+        assert word in " ".join(f for f, _ in EN.refusals(P.NRConfig(**dict(mc, **extra)))), extra
+    assert "subbands" in " ".join(f for f, _ in EN.refusals(P.NRConfig(mu=1, n_prb=106)))   # one cell: 8 or 13
 
 
 def test_make_engine_refuses_before_building():
