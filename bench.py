@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--out-format reference|compact] [--no-cpu]
     python bench.py --workload wifi_dcf [--envs-per-wave G]     (level WIFI: station-substeps/s)
     python bench.py --workload wifi_dcf_slots [--envs-per-wave G]  (level WIFI_DCF: station-steps/s)
+    python bench.py --workload mc_interf     (three cells with UL interference, 1024 envs x 64 robots: robot-slots/s)
 
 A step is one control step of every env: this step's message arrivals and step (poses in, the reference's output dict
 out), one launch of the fused step kernel that enqueues the arrivals first (--separate-submit: submit_counts and step,
@@ -77,6 +78,19 @@ def dl_step_kernel_bytes(eng):
     per_robot = 2 * b_rw + b_ro + 8 + 2 * 8
     per_env = 4 * 4 + p.n_fields * p.n_modes * 3 * 4 + 2 * 8 * 10 + 2 * 8 * 3 * (cfg.max_harq_tx + 1)
     return E * R * per_robot + E * per_env, per_robot
+
+
+def mc_step_kernel_bytes(eng):
+    """Algorithmic HBM bytes of one multi-cell step-kernel launch (inet_nr_step_cells): step_kernel_bytes with the
+    fading state of every robot-cell link (2 C S floats instead of 2 S) and the association words (serving cell, A3
+    candidate and count, interruption end, handover count: 5 int32) read and written, the shadowing fields of every
+    cell; per env each gNB's N+I estimate (C S floats), the I/N statistic and the pending flag, read and written."""
+    total, per_robot = step_kernel_bytes(eng)
+    C, S, E, R = eng.C, eng.S, eng.E, eng.R
+    p = eng._cparams
+    extra_robot = 2 * (2 * (C - 1) * S * 4) + 2 * 5 * 4
+    extra_env = (C - 1) * p.n_fields * p.n_modes * 3 * 4 + 2 * (C * S * 4 + 4 + 4)
+    return total + E * R * extra_robot + E * extra_env, per_robot + extra_robot
 
 
 def step_kernel_touched_bytes(eng, qlen_mean, kept_mean):
@@ -252,7 +266,7 @@ def cpu_baseline(P, wl, cfg, E_cpu, steps, warmup):
     dt = time.perf_counter() - t0
     k_ul = sum(1 for x in cfg.schedule(0) if x[2]) + sum(1 for x in cfg.schedule(0) if x[1])
     return {"value": E_cpu * R * k_ul * steps / dt, "unit": "robot-slots/s", "cores": threads, "kind": "port",
-            "sample": f"oracle (torch CPU restatement of the reference path) on the first {E_cpu} of the 4096 envs "
+            "sample": f"oracle (torch CPU restatement of the reference path) on the first {E_cpu} of the {wl.E} envs "
                       f"x {R} robots, {steps} timed steps after {warmup} warm-up, {dt:.1f} s",
             "ms_per_step": 1e3 * dt / steps}
 
@@ -321,15 +335,75 @@ def run_dl(args, P, torch):
     print(json.dumps(res), flush=True)
 
 
+def run_mc(args, P, torch):
+    """Config 3: three cells per env with same-slot UL interference (NRNet.step_cells), one line with robot-slots/s
+    and the step kernel's measured duration against its algorithmic HBM bytes. The kernel is bound by its per-lane
+    arithmetic (the fading draws and gains of 3 links per robot, the per-cell schedulers and the interference sums),
+    not by HBM: roofline.frac says how far from the HBM bound it runs."""
+    from isaac_net_amd import scenarios as S
+    from isaac_net_amd.engine import KernelTimer
+    dev = "cuda:0"
+    E = args.envs if args.envs_set else 1024
+    R = args.robots if args.robots_set else 64
+    total = args.warmup + args.steps
+    print(f"# workload mc_interf {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev, name="mc_interf")
+    cfg = wl.cfg
+    eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
+    k_ul = sum(1 for x in cfg.schedule(0) if x[2])
+    for s in range(args.warmup):
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
+    torch.cuda.synchronize()
+    eng.kernel_events = ev = KernelTimer(args.steps, dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        s = args.warmup + i
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.kernel_events = None
+    k_ms = sorted(ev.ms())
+    k_avg = sum(k_ms) / len(k_ms)
+    nbytes, per_robot = mc_step_kernel_bytes(eng)
+    achieved = nbytes / (k_avg * 1e-3) / 1e9
+    st = eng.owner_state()
+    noise = 10 ** (cfg.noise_dbm_per_prb("gnb") / 10)
+    res = {"metric": f"robot-slots/sec @{E} envs×{R} robots K={k_ul}, 3 cells with UL interference",
+           "value": E * R * k_ul * args.steps / dt, "unit": "robot-slots/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"mc_interf: {E} envs x {R} robots, 3 hex cells 150 m apart, nearest-gNB "
+                                  "association, no handover, thermal noise + same-slot UL interference of the other "
+                                  f"cells' scheduled robots, fractional UL power control, PF over 106 PRB (14 RBGs), "
+                                  f"K={k_ul} UL slots/step (DDDSU, 25 ms), 1200 B at Poisson 0.3, FIFO 16, UMi LOS",
+                      "envs": E, "robots": R, "cells": 3, "ul_slots_per_step": k_ul, "parallelism": "single GPU",
+                      "out_format": args.out_format, "launch": "eager: one launch per step (arrivals enqueued "
+                                                               "inside the step kernel)"},
+           "env_steps_per_s": E * args.steps / dt,
+           "mean_interference_over_thermal_db": float(10 * torch.log10((st["net.ni_ul"] / noise).mean())),
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "nr_step_kernel<cells 3>",
+                        "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
+                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
+                        "note": "arithmetic-bound kernel: frac is the distance from the HBM bound"}}
+    copy_calibration(args, res, torch, dev)
+    if not args.no_cpu:
+        print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, 512), min(args.cpu_steps, 4), 1)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="rl_scale",
-                    choices=("rl_scale", "rl_scale_dl", "wifi_dcf", "wifi_dcf_slots"),
+                    choices=("rl_scale", "rl_scale_dl", "mc_interf", "wifi_dcf", "wifi_dcf_slots"),
                     help="rl_scale: the NR engine's RL-scale workload (the headline metric); rl_scale_dl: the same with "
-                         "the downlink on; wifi_dcf: level WIFI; wifi_dcf_slots: level WIFI_DCF on the same inputs")
+                         "the downlink on; mc_interf: three cells with UL interference (1024 x 64); wifi_dcf: level "
+                         "WIFI; wifi_dcf_slots: level WIFI_DCF on the same inputs")
     ap.add_argument("--envs", type=int, default=None)
     ap.add_argument("--robots", type=int, default=None)
     ap.add_argument("--envs-per-wave", type=int, default=1, help="level WIFI: envs per 64-lane wavefront")
@@ -357,6 +431,8 @@ def main():
         return run_wifi(args, P, torch)
     if args.workload == "rl_scale_dl":
         return run_dl(args, P, torch)
+    if args.workload == "mc_interf":
+        return run_mc(args, P, torch)
     from isaac_net_amd import scenarios as S
     from isaac_net_amd.engine import KernelTimer
     dev = "cuda:0"

@@ -178,3 +178,56 @@ def test_cqi_tables_closed_form():
     t2 = PH.PhyTables(2, max_tx=4)
     thr2, cm2 = PH.cqi_tables(t2, 2)
     assert cm2[15] == 27 and cm2[12] == 21      # 256QAM 948 is MCS 27 of table 2; 256QAM 711 is MCS 21
+
+
+def outer_sum_rule(x):
+    """The step kernel's order for torch's CPU sum over the robots (dim 1) of an [E,R,C,S] float32 tensor
+    (aten_outer_sum in inet_nr_dev.h): columns q = c S + s below 32 floor(C S / 32) add the rows in chunks of 16
+    (each chunk from 0, the chunk sums accumulated from 0, then added to the sum of the rows past the last chunk);
+    the other columns use four interleaved accumulators combined as ((a0 + a1) + a2) + a3."""
+    f = np.float32
+    E, R, C, S = x.shape
+    n = C * S
+    out = np.zeros((E, C, S), np.float32)
+    for e in range(E):
+        for q in range(n):
+            c, s = divmod(q, S)
+            v = x[e, :, c, s]
+            if q < 32 * (n // 32):
+                acc, i = f(0), 0
+                while i + 16 <= R:
+                    ch = f(0)
+                    for k in range(16):
+                        ch = f(ch + v[i + k])
+                    acc, i = f(acc + ch), i + 16
+                tail = f(0)
+                for k in range(i, R):
+                    tail = f(tail + v[k])
+                out[e, c, s] = f(tail + acc)
+            else:
+                a = [f(0)] * 4
+                for i in range(4 * (R // 4)):
+                    a[i % 4] = f(a[i % 4] + v[i])
+                for i in range(4 * (R // 4), R):
+                    a[0] = f(a[0] + v[i])
+                out[e, c, s] = f(f(f(a[0] + a[1]) + a[2]) + a[3])
+    return out
+
+
+@pytest.mark.skipif(torch.backends.cpu.get_cpu_capability() != "AVX512",
+                    reason="the pinned order is that of torch's AVX512 CPU kernels")
+@pytest.mark.parametrize("R,C,S", [(8, 3, 14), (16, 3, 13), (33, 3, 14), (64, 3, 14), (64, 3, 8), (40, 7, 14)])
+def test_interference_sum_order_is_torchs(R, C, S):
+    """The interference sum of the multi-cell step (_ul_ici: (p_rx * other).sum(1), nr_engine.py:799-816) in the
+    order the kernel replays equals torch's bit for bit, on terms spread over ten decades with exact zeros (robots
+    of the same cell, RBGs not held); a sequential sum differs (so the test pins the grouping)."""
+    g = torch.Generator().manual_seed(R * 100 + C * 10 + S)
+    x = (torch.rand(3, R, C, S, generator=g) * (torch.rand(3, R, C, S, generator=g) < 0.5) *
+         10 ** (torch.rand(3, R, C, S, generator=g) * 10 - 12)).float()
+    want = x.sum(1).numpy()
+    assert np.array_equal(outer_sum_rule(x.numpy()), want)
+    if R > 16:
+        seq = np.zeros_like(want)
+        for r in range(R):
+            seq = (seq + x.numpy()[:, r]).astype(np.float32)
+        assert not np.array_equal(seq, want)
