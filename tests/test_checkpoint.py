@@ -58,3 +58,15 @@ def test_reference_checkpoint_holds_the_restored_state():
               "net.rng.env", "net.dl_newest", "radio.ch.sf_los.k", "radio.ch.los_field.phi", "net.spec"):
         assert k in keys, k
     assert host["T"] == int(z["k_steps"]) and "net.last_g" in host and "net.rng.s0" in host
+
+
+def test_reference_multicell_checkpoint_holds_the_restored_state():
+    """With three cells the reference's checkpoint also holds the association, each gNB's N+I estimate, the
+    interference statistic, the fading of every link [E,R,C,S,2] and one shadowing field per cell [C,E,K,2]."""
+    z = np.load(os.path.join(GOLDEN, "ckpt_mc3_ho.npz"), allow_pickle=False)
+    keys = {k[3:] for k in z.files if k.startswith("ck/")}
+    for k in ("net.assoc.serv", "net.assoc.pending", "net.assoc.a3_cand", "net.assoc.a3_cnt", "net.assoc.ho_end",
+              "net.assoc.n_ho", "net.ni_ul", "net.ioN[ul]", "net.h", "radio.k", "radio.phi"):
+        assert k in keys, k
+    E, R = int(json.loads(bytes(z["host_json"]).decode())["E"]), int(json.loads(bytes(z["host_json"]).decode())["R"])
+    assert z["ck/net.h"].shape == (E, R, 3, 13, 2) and z["ck/radio.k"].shape[:2] == (3, E)

@@ -1,5 +1,6 @@
 """Checkpoints on the GPU (core/checkpoint.py:103-143 semantics): a checkpoint written by the reference's NR engine
-(tests/golden/ckpt_*.npz, its state_dict() after 10 steps of a golden case) loads into the hip engine, which then
+(tests/golden/ckpt_*.npz, its state_dict() after 10 steps of a golden case: one cell, the downlink, three cells with
+handovers) loads into the hip engine, which then
 continues bit for bit along the reference's trajectory (outputs, state and counters as in the free-running parity
 test); and checkpoint.save / load of the hip engine resumes exactly like the uninterrupted run."""
 import json
@@ -27,7 +28,7 @@ def reference_checkpoint(name):
     return sd, int(z["k_steps"])
 
 
-@pytest.mark.parametrize("name", ["c2", "dl_c2"])
+@pytest.mark.parametrize("name", ["c2", "dl_c2", "mc3_ho"])
 def test_reference_checkpoint_resumes_bit_exact(name):
     print(f"reference checkpoint of {name}", flush=True)
     ref, cfgd, kind = load(name)
