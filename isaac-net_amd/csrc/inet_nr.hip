@@ -267,9 +267,11 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     InetNrArrivals none{};
     if (arr && (!arr->counts || !arr->sizes || arr->n_cls <= 0 || (arr->pkt_overhead && arr->pkt_payload <= 0)))
         return INET_NR_EINVAL;
-    inet::StepArgs a{*st, dl, cells, t, p, rows, n_rows, n_data, arr ? *arr : none, T, x, cur_hid, *out, rb,
+    // the DL link resolves frame completion in the slot loop: no per-slot history in LDS
+    const int n_hist = dl ? 0 : n_data;
+    inet::StepArgs a{*st, dl, cells, t, p, rows, n_rows, n_hist, arr ? *arr : none, T, x, cur_hid, *out, rb,
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
-                     inet::step_lds_bytes(n_data, p.harq_drop, rb, p.max_tx, cells ? cells->C : 1, p.S),
+                     inet::step_lds_bytes(n_hist, p.harq_drop, rb, p.max_tx, cells ? cells->C : 1, p.S),
                      (hipStream_t)stream};
     fn(a);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;

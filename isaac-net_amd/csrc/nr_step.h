@@ -483,6 +483,7 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     };
 
     int n_ul = 0;
+    int nf = 0, lost_dl = 0;                      // DL: first frame not yet resolved, frames lost under RLC UM
     const int g0 = (int)(T * (int64_t)N);
 
     // ---------------- several cells: association and the A3 plan of this step (CellAssociation, radio.py:410-437) ----
@@ -1130,8 +1131,33 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             atomicAdd(&my_hist[HB + kh], 1);
             atomicAdd(&my_hist[(ok ? 0 : 2 * HB) + kh], 1);
         }
-        // ---- RLC in-order pointer of this slot (completion replayed in the epilogue) ----
-        if (n_ul < n_ul_max) {
+        // ---- RLC in-order pointer of this slot ----
+        if constexpr (DL) {
+            // the DL link resolves its frames as the pointer moves (no per-slot history in LDS): under RLC UM the
+            // frames an exhausted TB overlaps are lost (mac.py:474-477), then the frames the in-order pointer has
+            // passed complete at this slot (mac.py:500-503). Frames before nf are lost or completed, and no
+            // completed frame overlaps an undecoded TB, so both scans start at nf.
+            if (act) {
+                if (pm.harq_drop && exh) {
+                    for (int f = nf; f < qlen; ++f) {
+                        const int fr = f * R;
+                        if (ldo(lk.q_start + fr, o_fr0) >= hi_tx) break;
+                        if (ldo(lk.q_end + fr, o_fr0) > lo_tx) {
+                            const uint32_t m = ldo(lk.q_meta + fr, o_fr0);
+                            if (!(m & 1u)) { sto(lk.q_meta + fr, o_fr0, m | 1u); ++lost_dl; }
+                        }
+                    }
+                }
+                const int a = ack_ptr();
+                for (; nf < qlen; ++nf) {
+                    const int fr = nf * R;
+                    const uint32_t m = ldo(lk.q_meta + fr, o_fr0);
+                    if ((m & 1u) || ldo(lk.q_fin + fr, o_fr0) != FIN_NONE) continue;   // lost, or completed before
+                    if (ldo(lk.q_end + fr, o_fr0) > a) break;
+                    sto(lk.q_fin + fr, o_fr0, g);
+                }
+            }
+        } else if (n_ul < n_ul_max) {            // (UL: recorded, completion replayed in the epilogue)
             ack_l[n_ul * STEP_WAVE + lane] = ack_ptr();
             if (pm.harq_drop) {
                 exlo_l[n_ul * STEP_WAVE + lane] = exh ? lo_tx : 0;
@@ -1140,7 +1166,7 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
         }
         ++n_ul;
     }
-    const int n_hist = n_ul < n_ul_max ? n_ul : n_ul_max;
+    const int n_hist = DL ? 0 : (n_ul < n_ul_max ? n_ul : n_ul_max);
 
     // ================================================================ end of step (NRNet._finish)
     if constexpr (MC) {                            // A3 triggers after the step's last active slot (nr_engine.py:780)
@@ -1238,6 +1264,7 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             ++kept;
         }
     }
+    if constexpr (DL) lost_new += lost_dl;             // marked in the slot loop
     // the slots past the queue get the outputs of an empty slot (not delivered / timed out / dropped, cap -1,
     // class 0, delay NaN): one frame at a time up to a multiple of 4, then 16-byte stores of 4 frames per array
     if (!DL && act) {
@@ -1272,8 +1299,8 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             sto((uint4*)(out.delay + f), ob * 4u, nans);
         }
     }
-    if (act) {
-        for (int f = kept; f < qlen; ++f) sto(lk.q_cap + f * R, o_fr, -1);
+    if (act) {                                         // vacated slots: empty, not completed
+        for (int f = kept; f < qlen; ++f) { sto(lk.q_cap + f * R, o_fr, -1); sto(lk.q_fin + f * R, o_fr, (int)FIN_NONE); }
     }
     // compact(): floor, sent, dead processes, BSR (mac.py:610-616, mac_ul.py:255-257)
     floor_ = new_floor;
