@@ -44,7 +44,8 @@ extern "C" {
 #define INET_NR_ABI_VERSION 4
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
-#define INET_NR_MAX_R 64          /* robots per env (one segment of a 64-wide wavefront) */
+#define INET_NR_MAX_R 128         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two
+                                     wavefronts (65..128: the UL with pose or SNR [E][R] input, one cell) */
 #define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
 #define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
 #define INET_NR_MAX_ROWS 64       /* scheduled slots (InetNrRow) per control step */

@@ -16,7 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libinet_nr.so")
-UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip", "nr_step_mc.hip", "wifi.hip"]
+UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip", "nr_step_mc.hip", "nr_step_w2.hip", "wifi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]

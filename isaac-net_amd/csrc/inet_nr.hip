@@ -258,12 +258,15 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
             return INET_NR_EINVAL;
         if (c.ttt < 0 || c.ho_int < 0 || !(c.noise_mw > 0.0f)) return INET_NR_EINVAL;
         fn = inet::pick_step_mc(p.S, c.C, p.P, ir);
+    } else if (rb > inet::STEP_WAVE) {          // 65..128 robots: two wavefronts per env, UL
+        if (dl || vref) return INET_NR_EUNSUPPORTED;
+        fn = inet::pick_step_w2(p.S, p.P, ir);
     } else {
         fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
            : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
     }
     if (!fn) return INET_NR_EUNSUPPORTED;
-    const int envs_pw = inet::STEP_WAVE / rb;
+    const int envs_pw = rb > inet::STEP_WAVE ? 1 : inet::STEP_WAVE / rb;
     InetNrArrivals none{};
     if (arr && (!arr->counts || !arr->sizes || arr->n_cls <= 0 || (arr->pkt_overhead && arr->pkt_payload <= 0)))
         return INET_NR_EINVAL;
@@ -284,8 +287,8 @@ extern "C" {
 int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
 
 const char* inet_nr_build_info(void) {
-    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, multi-cell step<C = 3, "
-           "S in {8,13,14}, P, IR>, one wave64 per workgroup, DPP segment reductions, ATen-order sums";
+    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, two-wave step (R <= 128), "
+           "multi-cell step<C = 3, S in {8,13,14}, P, IR>, DPP segment reductions, ATen-order sums";
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,

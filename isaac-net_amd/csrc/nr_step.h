@@ -159,34 +159,34 @@ DEV float lse_logw(const float* s_logw, uint32_t won) {
     return logf(sum) + mx;
 }
 // lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of the robot whose linear SINR row is column `col` of s_lin
-// (s_lin[s * 64 + col]); x_s is kept in column `tmp` of s_tmp between the max and the sum. rbeta = RN(1 / beta): the
-// division is div_const, exact for every beta of the MCS tables. `nan` says that some lin_s of the full row (held or
-// not) is NaN, which makes torch's result NaN.
-template <int S>
+// (s_lin[s * CW + col], CW lanes per workgroup); x_s is kept in column `tmp` of s_tmp between the max and the sum.
+// rbeta = RN(1 / beta): the division is div_const, exact for every beta of the MCS tables. `nan` says that some lin_s
+// of the full row (held or not) is NaN, which makes torch's result NaN.
+template <int S, int CW = STEP_WAVE>
 DEV float lse_eesm(const float* s_lin, int col, float* s_tmp, int tmp, const float* s_logw, uint32_t won, float beta,
                    float rbeta, bool nan) {
     uint32_t rot = aten_rot<S>(won);
     float mx = -INFINITY;
     for (uint32_t m = rot; m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
-        float x = div_const(-s_lin[s * STEP_WAVE + col], beta, rbeta) + s_logw[s];
-        s_tmp[s * STEP_WAVE + tmp] = x;
+        float x = div_const(-s_lin[s * CW + col], beta, rbeta) + s_logw[s];
+        s_tmp[s * CW + tmp] = x;
         mx = x > mx ? x : mx;
     }
     if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
     float sum = 0.f;
-    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * STEP_WAVE + tmp] - mx);
+    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * CW + tmp] - mx);
     float r = logf(sum) + mx;
     return nan ? NAN : r;
 }
-// PRB-weighted mean of the per-RBG dB values x_s (s_x[s * 64 + lane]) over the held RBGs (mean_db): the ATen-order
+// PRB-weighted mean of the per-RBG dB values x_s (s_x[s * CW + lane]) over the held RBGs (mean_db): the ATen-order
 // sum of nan_to_num(x_s * exp(log w_s - lnw)); the RBGs not held contribute exact zeros.
-template <int S>
+template <int S, int CW = STEP_WAVE>
 DEV float mean_db_held(const float* s_x, int lane, const float* s_logw, uint32_t won, float lnw) {
     float acc = 0.f;
     for (uint32_t m = aten_rot<S>(won); m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
-        float t = s_x[s * STEP_WAVE + lane] * expf(s_logw[s] - lnw);
+        float t = s_x[s * CW + lane] * expf(s_logw[s] - lnw);
         acc += nan_to_num(t, 0.0f, 3.4028234663852886e38f, -3.4028234663852886e38f);
     }
     return acc;
@@ -223,9 +223,10 @@ DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
 // byte range of a TB that exhausted its HARQ [n_ul][64] x 2, then the per-env HARQ histograms [64 / RB][3][max_tx + 1];
 // with several cells (nc > 1) then per env each gNB's N+I estimate and this slot's interference [64 / RB][2][nc S].
 inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx, int nc = 1, int S = 0) {
-    return sizeof(int) * ((size_t)n_ul * STEP_WAVE * (harq_drop ? 3 : 1) +
-                          (size_t)(STEP_WAVE / rb) * 3 * (max_tx + 1) +
-                          (nc > 1 ? (size_t)(STEP_WAVE / rb) * 2 * nc * S : 0));
+    const size_t cw = rb > STEP_WAVE ? (size_t)rb : (size_t)STEP_WAVE;     // lanes per workgroup
+    return sizeof(int) * ((size_t)n_ul * cw * (harq_drop ? 3 : 1) +
+                          (cw / rb) * 3 * (max_tx + 1) +
+                          (nc > 1 ? (cw / rb) * 2 * nc * S : 0));
 }
 
 // v[idx] of a register array indexed by a runtime value (a chain of selects, no scratch memory)
@@ -246,14 +247,20 @@ DEV T sel_of(const T (&v)[N], int idx) {
 // segment's lanes of one serving cell: ballots masked to the cell, NC interleaved butterflies), fractional power
 // control, and the same-slot interference sum of every gNB and RBG over the other cells' robots (each lane's terms in
 // LDS, summed by one lane per (cell, RBG) in torch's CPU order); cl holds the association state and constants.
+// RBT = 128: envs of 65..128 robots, one env per workgroup of two wavefronts (W = 2); the env-wide collectives then
+// combine the two waves' ballots and butterflies through LDS (xchg), and every cooperative loop runs a number of
+// rounds that both waves agree on, so that every barrier is reached by both.
 template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC>
-__global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
+__global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
     InetNrState st, LS lk, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     constexpr bool MC = NC > 1;
     static_assert(!(MC && (DL || VREF)), "several cells: the UL with pose input");
+    constexpr int W = RBT > STEP_WAVE ? 2 : 1;         // wavefronts per env
+    constexpr int CW = STEP_WAVE * W;                   // lanes per workgroup (the LDS column stride)
+    static_assert(!(MC && W > 1), "several cells: one wavefront per env");
     constexpr int NCS = NC * S;                        // fading links per robot (cell-major, subband-minor)
     const int rb = RBT ? RBT : rb_arg;
     const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
@@ -266,15 +273,19 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     __shared__ int s_ulrel[MAX_UL_ROWS];
     // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
     // interference terms at every (cell, RBG) during a UL slot
-    __shared__ float s_x[2 * NCS * STEP_WAVE];
-    __shared__ float s_lin[S * STEP_WAVE];                       // per-lane rows: linear RBG SINR
-    __shared__ int s_la_i[2 * STEP_WAVE], s_la_slot[STEP_WAVE], s_la_top[STEP_WAVE];   // link adaptation work list
-    __shared__ float s_la_f[3 * STEP_WAVE];
-    __shared__ uint8_t s_list[STEP_WAVE];                        // lanes that draw fading innovations this slot
-    __shared__ uint32_t s_bfe[STEP_WAVE];                        // per env of the wave: its fading key this slot
+    __shared__ float s_x[2 * NCS * CW];
+    __shared__ float s_lin[S * CW];                              // per-lane rows: linear RBG SINR
+    __shared__ int s_la_i[2 * CW], s_la_slot[CW], s_la_top[CW];  // link adaptation work list
+    __shared__ float s_la_f[3 * CW];
+    __shared__ uint8_t s_list[CW];                               // lanes that draw fading innovations this slot
+    __shared__ uint32_t s_bfe[STEP_WAVE];                        // per env of the workgroup: its fading key this slot
+    __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
+    __shared__ int s_rval[W > 1 ? CW : 1];
+    __shared__ int s_xw[4];                                      // W = 2: the two waves' values of an env collective
 
     const int lane = threadIdx.x;
-    const int envs_pw = STEP_WAVE / rb;
+    const int wbase = lane & ~(STEP_WAVE - 1), wl = lane - wbase;   // this lane's wavefront (base lane) and lane in it
+    const int envs_pw = CW / rb;
     const int eloc = lane / rb;
     const int e = blockIdx.x * envs_pw + eloc;
     const int r = lane & (rb - 1);
@@ -289,13 +300,41 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     const uint32_t o_r = o_r0, o_sr = o_sr0, o_pr = o_pr0;
     const int HB = pm.max_tx + 1;
     int* const ack_l = dyn;
-    int* const exlo_l = dyn + n_ul_max * STEP_WAVE;
-    int* const exhi_l = dyn + 2 * n_ul_max * STEP_WAVE;
-    int* const hist_l = dyn + (pm.harq_drop ? 3 : 1) * n_ul_max * STEP_WAVE;
+    int* const exlo_l = dyn + n_ul_max * CW;
+    int* const exhi_l = dyn + 2 * n_ul_max * CW;
+    int* const hist_l = dyn + (pm.harq_drop ? 3 : 1) * n_ul_max * CW;
     int* const my_hist = hist_l + eloc * 3 * HB;
     // several cells: each gNB's N+I estimate [NC][S] and this slot's interference [NC][S] of this lane's env
     float* const s_ni = reinterpret_cast<float*>(hist_l + envs_pw * 3 * HB) + eloc * 2 * NCS;
     float* const s_if = s_ni + NCS;
+
+    // ---------------- env-wide collectives: inside the segment (W = 1), or over the two waves of the env (W = 2)
+    // through LDS, between two barriers that both waves reach
+    auto xchg2 = [&](int v, int& v0, int& v1) {        // v: uniform in each wave
+        if (wl == 0) s_xw[lane >> 6] = v;
+        __syncthreads();
+        v0 = s_xw[0];
+        v1 = s_xw[1];
+        __syncthreads();
+    };
+    auto env_any = [&](bool p) -> bool {
+        if constexpr (W == 1) {
+            return seg_any(p, rb, lane);
+        } else {
+            int a0, a1;
+            xchg2(__ballot(p) != 0ull ? 1 : 0, a0, a1);
+            return (a0 | a1) != 0;
+        }
+    };
+    auto env_sum = [&](int v) -> int {
+        if constexpr (W == 1) {
+            return bsum(v, rb);
+        } else {
+            int a0, a1;
+            xchg2(bsum(v, STEP_WAVE), a0, a1);
+            return a0 + a1;
+        }
+    };
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
@@ -309,8 +348,8 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     const float rds = 1.0f / tb.ds, rdc = 1.0f / tb.dc;
     if (lane < S) { s_w[lane] = tb.w[lane]; s_logw[lane] = tb.logw[lane]; s_wdb[lane] = tb.wdb[lane]; }
     if constexpr (IR)
-        for (int i = lane; i < tb.M * tb.EQW; i += STEP_WAVE) s_eq[i] = tb.mcs_eq[i];
-    for (int i = lane; i < envs_pw * 3 * HB; i += STEP_WAVE) hist_l[i] = 0;
+        for (int i = lane; i < tb.M * tb.EQW; i += CW) s_eq[i] = tb.mcs_eq[i];
+    for (int i = lane; i < envs_pw * 3 * HB; i += CW) hist_l[i] = 0;
     if (lane == 0) {
         int j = 0;
         for (int k = 0; k < n_rows && j < MAX_UL_ROWS; ++k)
@@ -602,31 +641,31 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             // (the DL draws every robot's gain at its CQI rows, which set the CSI of every robot)
             const bool full = !iid || (DL ? (row.flags & 1) != 0 : (k == last_ul_row || k == last_h_row));
             const bool draw = act && (full || busy);
-            const unsigned long long need = __ballot(draw);
+            const unsigned long long need = __ballot(draw);              // (per wave: each draws its own robots)
             float* const s_z = s_x;
             if (r == 0) s_bfe[eloc] = mix32(base0 ^ row.salt_fade);
-            if (draw) s_list[__builtin_popcountll(need & ((1ull << lane) - 1ull))] = (uint8_t)lane;
+            if (draw) s_list[wbase + __builtin_popcountll(need & ((1ull << wl) - 1ull))] = (uint8_t)lane;
             __syncthreads();
             // pairs in subband-major order: the lanes of one pass write different robots' columns (no LDS bank
             // conflicts between the pairs of one robot)
             const int n_need = __builtin_popcountll(need);
             const int items = n_need * NCS;
 #pragma unroll 1
-            for (int it = lane; it < items; it += STEP_WAVE) {
+            for (int it = wl; it < items; it += STEP_WAVE) {
                 const int q = it / n_need, ri = it - q * n_need;
-                const int L = s_list[ri];
+                const int L = s_list[wbase + ri];
                 const uint32_t bf = s_bfe[L / rb];
                 const uint32_t hin = bf + (uint32_t)(4 * (L & (rb - 1)) * NCS + 4 * q) * GOLD;
                 const float zr = normal_of(mix32(mix32(hin) ^ bf), mix32(mix32(hin + GOLD) ^ bf));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bf), mix32(mix32(hin + 3u * GOLD) ^ bf));
-                s_z[(2 * q) * STEP_WAVE + L] = zr;
-                s_z[(2 * q + 1) * STEP_WAVE + L] = zi;
+                s_z[(2 * q) * CW + L] = zr;
+                s_z[(2 * q + 1) * CW + L] = zi;
             }
             __syncthreads();
             if (draw) {
 #pragma unroll
                 for (int q = 0; q < NCS; ++q) {
-                    float zr = s_z[(2 * q) * STEP_WAVE + lane], zi = s_z[(2 * q + 1) * STEP_WAVE + lane];
+                    float zr = s_z[(2 * q) * CW + lane], zi = s_z[(2 * q + 1) * CW + lane];
                     hr[q] = row.rho * hr[q] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
                     hi[q] = row.rho * hi[q] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
                 }
@@ -712,7 +751,7 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
         // any lane of this lane's scheduler (its env's segment; several cells: the env's robots of its cell)
         auto cell_any = [&](bool p) -> bool {
             if constexpr (MC) return (__ballot(p) & mycell) != 0ull;
-            else return seg_any(p, rb, lane);
+            else return env_any(p);
         };
         // true in the lane that wins the RBG with bid m (-1: no bid) in its scheduler: the highest bid, the first
         // robot on ties (torch max)
@@ -725,6 +764,15 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                 const int mx = sel_of(v, serv);
                 const unsigned long long b = (__ballot(m == mx) & mycell) >> (lane & ~(rb - 1));
                 return m >= 0 && b != 0ull && (int)__builtin_ctzll(b) == r;
+            } else if constexpr (W > 1) {
+                // each wave's max and its first lane holding it; the env's winner is wave 0's on ties
+                const int mxw = bmax_i(m, STEP_WAVE);
+                const int fw = (int)__builtin_ctzll(__ballot(m == mxw));
+                if (wl == 0) { s_xw[2 * (lane >> 6)] = mxw; s_xw[2 * (lane >> 6) + 1] = fw; }
+                __syncthreads();
+                const int m0 = s_xw[0], f0 = s_xw[1], m1 = s_xw[2], f1 = s_xw[3];
+                __syncthreads();
+                return m >= 0 && lane == (m0 >= m1 ? f0 : STEP_WAVE + f1);
             } else {
                 const int mx = bmax_i(m, rb);
                 return m >= 0 && seg_first(m == mx, rb, lane) == r;
@@ -818,13 +866,13 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
         float* const s_met = s_x;
 #pragma unroll
         for (int s = 0; s < S; ++s)
-            s_met[s * STEP_WAVE + lane] = pm.sched == 0 ? rate[s] / avg_c : (pm.sched == 1 ? rate[s] : (float)(g - last_tx));
-        auto metric_of = [&](int s) -> float { return s_met[s * STEP_WAVE + lane]; };
+            s_met[s * CW + lane] = pm.sched == 0 ? rate[s] / avg_c : (pm.sched == 1 ? rate[s] : (float)(g - last_tx));
+        auto metric_of = [&](int s) -> float { return s_met[s * CW + lane]; };
         // retransmission admission (mac.py:300-313): rank by the metric sum inside each scheduler, admit while the RBG
         // counts fit (the segment's total fitting implies every cell's)
-        if (seg_any(has_rx, rb, lane)) {
+        if (env_any(has_rx)) {
             int val = has_rx ? rx_nsb : 0;
-            int tot = bsum(val, rb);
+            int tot = env_sum(val);
             if (tot > S) {
                 float mt[S];
 #pragma unroll
@@ -832,9 +880,16 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                 float rkey = has_rx ? aten_sum<S>(mt) : -1.0f;
                 int cum = 0;
                 const int sb = lane & ~(rb - 1);
+                if constexpr (W > 1) {             // the env's keys and counts through LDS
+                    s_rkey[lane] = rkey;
+                    s_rval[lane] = val;
+                    __syncthreads();
+                }
                 for (int j = 0; j < rb; ++j) {
-                    float kj = __shfl(rkey, sb + j, 64);
-                    int vj = __shfl(val, sb + j, 64);
+                    float kj;
+                    int vj;
+                    if constexpr (W > 1) { kj = s_rkey[j]; vj = s_rval[j]; }
+                    else { kj = __shfl(rkey, sb + j, 64); vj = __shfl(val, sb + j, 64); }
                     bool before = (kj > rkey) || (kj == rkey && j <= r);
                     if constexpr (MC) before = before && __shfl(serv, sb + j, 64) == serv;
                     cum += before ? vj : 0;
@@ -891,20 +946,23 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
         const float lnw = lse_logw<S>(s_logw, won);
         // ---- link adaptation for new TBs (phy.select_mcs): the highest MCS meeting the BLER target ----
         int mcs_new = 0, tbs_new = 0;
-        if (__ballot(tx_new) != 0ull) {
+        bool any_new;                                  // (W = 2: both waves enter, the search has barriers)
+        if constexpr (W == 1) any_new = __ballot(tx_new) != 0ull;
+        else any_new = env_any(tx_new);
+        if (any_new) {
             // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on the held RBGs
             bool nan = false;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
                 nan |= x != x;
-                s_x[s * STEP_WAVE + lane] = x;
+                s_x[s * CW + lane] = x;
             }
             for (uint32_t mm = tx_new ? won : 0u; mm; mm &= mm - 1) {
                 int s = __builtin_ctz(mm);
-                s_lin[s * STEP_WAVE + lane] = from_db(clampf(s_x[s * STEP_WAVE + lane], -30.0f, 60.0f));
+                s_lin[s * CW + lane] = from_db(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
             }
-            const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S>(s_x, lane, s_logw, won, lnw) : 0.f;
+            const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw) : 0.f;
             const int np = (int)n_prb;
             const int toff = (row.nsym_idx * (tb.NPRB + 1) + np) * tb.M;
             // The search for the highest MCS that meets the target is shared by the whole wavefront: every round,
@@ -913,23 +971,28 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             // The result is the top-down scan's (phy.select_mcs takes the highest passing MCS), without its
             // divergent tail. A robot's inputs (table row, held RBGs, lnw, OLLA offset, mean_db value) and its
             // linear SINR row are read from LDS by its helpers.
+            // (W = 2: each wave searches for its own robots; the rounds go on while either wave has robots left)
             s_la_i[lane] = toff;
-            s_la_i[STEP_WAVE + lane] = (int)(won | (nan ? 0x80000000u : 0u));
+            s_la_i[CW + lane] = (int)(won | (nan ? 0x80000000u : 0u));
             s_la_f[lane] = lnw;
-            s_la_f[STEP_WAVE + lane] = pm.olla ? olla : 0.0f;
-            s_la_f[2 * STEP_WAVE + lane] = eff_md;
+            s_la_f[CW + lane] = pm.olla ? olla : 0.0f;
+            s_la_f[2 * CW + lane] = eff_md;
             int top = tb.mcs_max, found_m = -1;
             bool mine = tx_new;
             unsigned long long searching = __ballot(mine);
-            while (searching) {
+            auto more = [&]() -> bool {
+                if constexpr (W == 1) return searching != 0ull;
+                else return env_any(searching != 0ull);
+            };
+            while (more()) {
                 const int n_s = __popcll(searching);
-                const int chunk = STEP_WAVE / n_s;
-                const int rank = __popcll(searching & ((1ull << lane) - 1ull));
-                if (mine) { s_la_slot[rank] = lane; s_la_top[lane] = top; }
+                const int chunk = n_s ? STEP_WAVE / n_s : STEP_WAVE;
+                const int rank = __popcll(searching & ((1ull << wl) - 1ull));
+                if (mine) { s_la_slot[wbase + rank] = lane; s_la_top[lane] = top; }
                 __syncthreads();
-                const int slot = lane / chunk, j = lane - slot * chunk;
+                const int slot = wl / chunk, j = wl - slot * chunk;
                 bool pass = false;
-                const int rl = slot < n_s ? s_la_slot[slot] : 0;
+                const int rl = slot < n_s ? s_la_slot[wbase + slot] : 0;
                 const int m = slot < n_s ? s_la_top[rl] - j : -1;
                 if (m >= 0) {
                     // the four table words are loaded first; the EESM (LDS and ALU only) runs while they arrive
@@ -938,14 +1001,14 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                     const float cwi = tb.la_cwi[ti], ncb = tb.la_ncb[ti];
                     float eff;
                     if (pm.eesm) {
-                        const uint32_t wr = (uint32_t)s_la_i[STEP_WAVE + rl];
+                        const uint32_t wr = (uint32_t)s_la_i[CW + rl];
                         const float beta = s_beta[m];
-                        eff = db_of((-beta) * (lse_eesm<S>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
-                                                           s_rbeta[m], (wr >> 31) != 0u) - s_la_f[rl]));
+                        eff = db_of((-beta) * (lse_eesm<S, CW>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
+                                                               s_rbeta[m], (wr >> 31) != 0u) - s_la_f[rl]));
                     } else {
-                        eff = s_la_f[2 * STEP_WAVE + rl];
+                        eff = s_la_f[2 * CW + rl];
                     }
-                    eff = eff + s_la_f[STEP_WAVE + rl];
+                    eff = eff + s_la_f[CW + rl];
                     if (tbs_m > 0) {
                         float b = bler_at(tb.bler, (m * tb.C + ci0) * tb.G, tb.G, tb.s0, tb.ds, rds, eff, cwi);
                         float tbler = 1.0f - pow_count(1.0f - b, ncb);
@@ -1045,16 +1108,16 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                 if constexpr (MC)                 // minus the measured N+I over the estimate (nr_engine.py:815)
                     if (cl.use_int) x = x - ((10.0f * log10f(cl.noise_mw + s_if[serv * S + s])) - ni_la[s]);
                 nan |= x != x;
-                s_x[s * STEP_WAVE + lane] = x;
+                s_x[s * CW + lane] = x;
             }
             for (uint32_t mm = tx ? won : 0u; mm; mm &= mm - 1) {
                 int s = __builtin_ctz(mm);
-                s_lin[s * STEP_WAVE + lane] = from_db(clampf(s_x[s * STEP_WAVE + lane], -30.0f, 60.0f));
+                s_lin[s * CW + lane] = from_db(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
             }
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan);
+                float lse = lse_eesm<S, CW>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan);
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -1067,9 +1130,9 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S, CW>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan) - lnw));
                 } else {
-                    eff = mean_db_held<S>(s_x, lane, s_logw, won, lnw);
+                    eff = mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw);
                 }
                 float lin_e = from_db(eff);
                 comb = pm.comb == 1 ? comb_p + lin_e : lin_e;
@@ -1158,10 +1221,10 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                 }
             }
         } else if (n_ul < n_ul_max) {            // (UL: recorded, completion replayed in the epilogue)
-            ack_l[n_ul * STEP_WAVE + lane] = ack_ptr();
+            ack_l[n_ul * CW + lane] = ack_ptr();
             if (pm.harq_drop) {
-                exlo_l[n_ul * STEP_WAVE + lane] = exh ? lo_tx : 0;
-                exhi_l[n_ul * STEP_WAVE + lane] = exh ? hi_tx : 0;
+                exlo_l[n_ul * CW + lane] = exh ? lo_tx : 0;
+                exhi_l[n_ul * CW + lane] = exh ? hi_tx : 0;
             }
         }
         ++n_ul;
@@ -1205,13 +1268,13 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
                 lost = true;
             }
             if (pm.harq_drop) {
-                int xl = exlo_l[j * STEP_WAVE + lane], xh = exhi_l[j * STEP_WAVE + lane];
+                int xl = exlo_l[j * CW + lane], xh = exhi_l[j * CW + lane];
                 if (xh > xl && qs < xh && qe > xl) {
                     if (!lost) ++lost_new;
                     lost = true;
                 }
             }
-            if (fin == FIN_NONE && !lost && qe <= ack_l[j * STEP_WAVE + lane]) fin = g0 + s_ulrel[j];
+            if (fin == FIN_NONE && !lost && qe <= ack_l[j * CW + lane]) fin = g0 + s_ulrel[j];
         }
         if (ho_hit && ho_j >= n_hist && fin == FIN_NONE) {
             if (!lost) ++lost_new;
@@ -1366,12 +1429,12 @@ __global__ __launch_bounds__(STEP_WAVE, NC > 1 ? 1 : 2) void nr_step_kernel(
     }
     }
     // per-env outputs and counters (segment reductions, written by robot 0)
-    const bool det_any = seg_any(det_hit, rb, lane);
-    const int v_new = bsum(act ? c_new : 0, rb), v_retx = bsum(act ? c_retx : 0, rb);
-    const int v_ok = bsum(act ? c_ok : 0, rb), v_fail = bsum(act ? c_fail : 0, rb);
-    const int v_exh = bsum(act ? c_exh : 0, rb), v_lost = bsum(act ? lost_new : 0, rb);
-    const int v_pend = bsum(act ? c_new_pend : 0, rb), v_bok = bsum(act ? c_bytes_ok : 0, rb);
-    const int v_bnew = bsum(act ? c_bytes_new : 0, rb), v_prb = bsum(act ? c_prb : 0, rb);
+    const bool det_any = env_any(det_hit);
+    const int v_new = env_sum(act ? c_new : 0), v_retx = env_sum(act ? c_retx : 0);
+    const int v_ok = env_sum(act ? c_ok : 0), v_fail = env_sum(act ? c_fail : 0);
+    const int v_exh = env_sum(act ? c_exh : 0), v_lost = env_sum(act ? lost_new : 0);
+    const int v_pend = env_sum(act ? c_new_pend : 0), v_bok = env_sum(act ? c_bytes_ok : 0);
+    const int v_bnew = env_sum(act ? c_bytes_new : 0), v_prb = env_sum(act ? c_prb : 0);
     __syncthreads();                                  // histogram atomics of every lane are done
     if constexpr (MC) {
         if (e < E) {
@@ -1430,6 +1493,15 @@ void launch_step(const StepArgs& a) {
                            a.n_data, a.arr, none);
 }
 
+// envs of 65..128 robots: one env per workgroup of two wavefronts (UL, pose or SNR input)
+template <int S, int P, bool IR>
+void launch_step_w2(const StepArgs& a) {
+    const InetNrCells none{};
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 128, InetNrState, 1>), dim3(a.grid), dim3(2 * STEP_WAVE),
+                       a.lds, a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
+                       a.n_data, a.arr, none);
+}
+
 // the multi-cell step: NC cells, pose input, runtime segment width
 template <int S, int P, bool IR, int NC>
 void launch_step_mc(const StepArgs& a) {
@@ -1466,5 +1538,16 @@ StepFn pick_step_mc_s(int P, bool ir) {
     return nullptr;
 }
 StepFn pick_step_mc(int S, int C, int P, bool ir);         // nr_step_mc.hip
+
+// two-wavefront builds (R = 65..128): every (P, IR)
+template <int S>
+StepFn pick_step_w2_s(int P, bool ir) {
+#define INET_PICK_W2(PP) \
+    if (P == PP) return ir ? &launch_step_w2<S, PP, true> : &launch_step_w2<S, PP, false>;
+    INET_PICK_W2(2) INET_PICK_W2(4) INET_PICK_W2(8) INET_PICK_W2(16)
+#undef INET_PICK_W2
+    return nullptr;
+}
+StepFn pick_step_w2(int S, int P, bool ir);                // nr_step_w2.hip
 
 }  // namespace inet

@@ -133,9 +133,12 @@ class HipNREngine:
         dev = torch.device(device)
         if dev.type != "cuda":
             raise ValueError("the hip backend needs a GPU device (cuda:N on ROCm)")
-        if not 1 <= R <= 64:
-            raise HipUnsupported(f"R={R}: the hip backend holds one env's robots in one 64-lane wavefront segment "
-                                 "(1 <= R <= 64)")
+        if not 1 <= R <= 128:
+            raise HipUnsupported(f"R={R}: the hip backend holds one env's robots in one 64-lane wavefront segment, "
+                                 "or in two wavefronts (1 <= R <= 128)")
+        if R > 64 and (cfg.dl or cfg.n_cells > 1):
+            raise HipUnsupported(f"R={R} with the downlink or several cells: envs of more than 64 robots (two "
+                                 "wavefronts) run the single-cell uplink")
         self._lib = _lib.load()
         self.E, self.R, self.dev, self.config = E, R, dev, cfg
         if seed is None:
@@ -610,6 +613,8 @@ class HipNREngine:
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
+        if self.R > 64 and kind == 2:
+            raise HipUnsupported("per-subband SNR input with more than 64 robots per env")
         if self.C > 1 and kind != 0:
             raise ValueError("several cells: pass poses [E,R,2|3] (the path gain of every robot-cell link comes from "
                              "the radio)")

@@ -45,6 +45,6 @@ def pytest_collection_modifyitems(config, items):
             it.add_marker(skip)
 
 
-CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb"]
+CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5"]
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr"]    # the downlink on (NRConfig(dl=True))
 MC_CASES = ["mc3", "mc3_ho"]                  # several cells (NRConfig(n_cells=3)), uplink

@@ -98,6 +98,13 @@ CASES = {
                               discard="pdcp_arrival", timeout_steps=5, gnb_proc_slots=2, dl=True),
                      E=3, R=8, steps=30, kind="snr3", snr=(-2.0, 16.0), rates=(0.7,), dl_sizes=(5000.0,),
                      dl_rates=(1.1,), resets={11: [0, 2]}),
+    # config 5 shrunk: 128 robots per env (two wavefronts per env on the GPU), 273 PRB in 8 RBGs of 35, i.i.d.
+    # Rayleigh fading per subband and slot, PF, K = 20 UL slots per step, 16 HARQ processes, 800 B, FIFO 16
+    "c5": dict(cfg=dict(mu=1, n_prb=273, rbg_size=35, tdd_pattern="DDDSU", control_step_ms=50.0, scheduler="pf",
+                        n_harq=16, max_harq_tx=4, frame_buffer=16, msg_sizes=(800.0,), fading_rho_per_ms=0.0,
+                        channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", cell_positions_m=((100.0, 100.0),),
+                        gnb_height_m=10.0),
+               E=2, R=128, steps=8, kind="pose", arena=200.0, walk=1.0, rates=(0.6,), resets={5: [1]}),
     # several cells (NRNet.step_cells): config 3 shrunk (3 hex cells 150 m apart, 106 PRB, PF, thermal noise with
     # same-slot UL interference, fractional UL power control, correlated fading on every link, no handover)
     "mc3": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", n_harq=8,
