@@ -4,6 +4,7 @@
     python bench.py --workload wifi_dcf [--envs-per-wave G]     (level WIFI: station-substeps/s)
     python bench.py --workload wifi_dcf_slots [--envs-per-wave G]  (level WIFI_DCF: station-steps/s)
     python bench.py --workload mc_interf     (three cells with UL interference, 1024 envs x 64 robots: robot-slots/s)
+    python bench.py --workload freq_sel      (16384 envs x 128 robots, 273 PRB in 8 RBGs, K = 20: robot-slots/s)
 
 A step is one control step of every env: this step's message arrivals and step (poses in, the reference's output dict
 out), one launch of the fused step kernel that enqueues the arrivals first (--separate-submit: submit_counts and step,
@@ -394,16 +395,70 @@ def run_mc(args, P, torch):
     print(json.dumps(res), flush=True)
 
 
+def run_freq_sel(args, P, torch):
+    """Config 5: 16384 envs x 128 robots (two wavefronts per env), 273 PRB in 8 RBGs, i.i.d. Rayleigh per subband,
+    PF, K = 20: one line with robot-slots/s and the step kernel's measured duration against its algorithmic bytes."""
+    from isaac_net_amd import scenarios as S
+    from isaac_net_amd.engine import KernelTimer
+    dev = "cuda:0"
+    E = args.envs if args.envs_set else 16384
+    R = args.robots if args.robots_set else 128
+    total = args.warmup + args.steps
+    print(f"# workload freq_sel {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
+    wl = S.Workload(E, R, total, seed=0, device=dev, name="freq_sel")
+    cfg = wl.cfg
+    eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
+    k_ul = sum(1 for x in cfg.schedule(0) if x[2])
+    for s in range(args.warmup):
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
+    torch.cuda.synchronize()
+    eng.kernel_events = ev = KernelTimer(args.steps, dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        s = args.warmup + i
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.kernel_events = None
+    k_ms = sorted(ev.ms())
+    k_avg = sum(k_ms) / len(k_ms)
+    nbytes, per_robot = step_kernel_bytes(eng)
+    achieved = nbytes / (k_avg * 1e-3) / 1e9
+    res = {"metric": f"robot-slots/sec @{E} envs×{R} robots K={k_ul}, 273 PRB in 8 RBGs",
+           "value": E * R * k_ul * args.steps / dt, "unit": "robot-slots/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": f"freq_sel: {E} envs x {R} robots (two wavefronts per env), one cell, 273 PRB "
+                                  f"(100 MHz at 30 kHz) in 8 RBGs of 35, i.i.d. Rayleigh per subband and slot, PF, "
+                                  f"K={k_ul} UL slots/step (DDDSU, 50 ms), 8 HARQ x 4 tx, 800 B at Poisson 0.2, "
+                                  "FIFO 16, UMi LOS",
+                      "envs": E, "robots": R, "ul_slots_per_step": k_ul, "parallelism": "single GPU",
+                      "out_format": args.out_format, "launch": "eager: one launch per step (arrivals enqueued "
+                                                               "inside the step kernel)"},
+           "env_steps_per_s": E * args.steps / dt,
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "nr_step_kernel<two waves>",
+                        "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
+                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot}}
+    copy_calibration(args, res, torch, dev)
+    if not args.no_cpu:
+        print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, 128), min(args.cpu_steps, 3), 1)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="rl_scale",
-                    choices=("rl_scale", "rl_scale_dl", "mc_interf", "wifi_dcf", "wifi_dcf_slots"),
+                    choices=("rl_scale", "rl_scale_dl", "mc_interf", "freq_sel", "wifi_dcf", "wifi_dcf_slots"),
                     help="rl_scale: the NR engine's RL-scale workload (the headline metric); rl_scale_dl: the same with "
-                         "the downlink on; mc_interf: three cells with UL interference (1024 x 64); wifi_dcf: level "
-                         "WIFI; wifi_dcf_slots: level WIFI_DCF on the same inputs")
+                         "the downlink on; mc_interf: three cells with UL interference (1024 x 64); freq_sel: 16384 x "
+                         "128, 273 PRB, K = 20; wifi_dcf: level WIFI; wifi_dcf_slots: level WIFI_DCF on the same "
+                         "inputs")
     ap.add_argument("--envs", type=int, default=None)
     ap.add_argument("--robots", type=int, default=None)
     ap.add_argument("--envs-per-wave", type=int, default=1, help="level WIFI: envs per 64-lane wavefront")
@@ -433,6 +488,8 @@ def main():
         return run_dl(args, P, torch)
     if args.workload == "mc_interf":
         return run_mc(args, P, torch)
+    if args.workload == "freq_sel":
+        return run_freq_sel(args, P, torch)
     from isaac_net_amd import scenarios as S
     from isaac_net_amd.engine import KernelTimer
     dev = "cuda:0"

@@ -19,6 +19,9 @@ control step need control_step_ms = 2.5 K; "52 PRBs" needs n_prb = 52 since the 
               interference of the other cells' scheduled robots, open-loop fractional power control (on by default
               with several cells), PF over 106 PRBs (14 RBGs), K = 10, 1200 B at Poisson 0.3, UMi LOS, correlated
               Rayleigh fading on every robot-cell link, 1 m/s random walk in the square.
+  freq_sel    16384 envs x 128 robots (two wavefronts per env), one cell, 273 PRBs (100 MHz at 30 kHz) in 8 RBGs of
+              35 PRBs, i.i.d. Rayleigh fading per subband and slot, PF, K = 20 (DDDSU at 50 ms), 8 HARQ x 4
+              transmissions, 800 B at Poisson 0.2, FIFO 16, UMi LOS around the centre of a 200 m square.
 Inputs come from numpy's PCG64 seeded by the workload seed (poses uniform at the start, then a random walk clamped to
 the square or disc; arrival counts per class), identical for the GPU engine and the CPU oracle.
 """
@@ -59,6 +62,15 @@ def mc_interf_config(**kw):
     return NRConfig(**base)
 
 
+def freq_sel_config(**kw):
+    base = dict(mu=1, n_prb=273, rbg_size=35, tdd_pattern="DDDSU", control_step_ms=50.0, scheduler="pf",
+                pf_window=100.0, n_harq=8, max_harq_tx=4, frame_buffer=16, msg_sizes=(800.0,), fading_rho_per_ms=0.0,
+                channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", cell_positions_m=((100.0, 100.0),),
+                gnb_height_m=10.0, seed=0)
+    base.update(kw)
+    return NRConfig(**base)
+
+
 def wifi_dcf_config(**kw):
     from .wifi_config import WifiConfig
     base = dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,), cell_positions_m=((0.0, 0.0),),
@@ -73,6 +85,7 @@ WORKLOADS = {
     "rl_scale_dl": dict(cfg=lambda **kw: rl_scale_config(dl=True, **kw), E=4096, R=32, arena=200.0, speed=1.0,
                         rates=(0.8, 0.1), steps=500, dl_rates=(0.5,), dl_size=2000.0),
     "mc_interf": dict(cfg=mc_interf_config, E=1024, R=64, arena=200.0, speed=1.0, rates=(0.3,), steps=300),
+    "freq_sel": dict(cfg=freq_sel_config, E=16384, R=128, arena=200.0, speed=1.0, rates=(0.2,), steps=100),
     "wifi_dcf": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
                      level="WIFI"),
     "wifi_dcf_slots": dict(cfg=wifi_dcf_config, E=2048, R=16, radius=50.0, speed=1.0, rates=(0.4,), steps=500,
