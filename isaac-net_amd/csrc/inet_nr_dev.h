@@ -7,8 +7,8 @@
 //   (max, masked to 0 when infinite, + log of the sum of exp(x - max)). Replaying the reference's summation order
 //   keeps the GPU bitwise equal to the CPU path wherever no transcendental function is involved;
 // * segment collectives: a 64-lane wavefront holds 64 / RB envs, one robot per lane in a power-of-two segment of
-//   RB lanes; reductions across the robots of one env are butterflies inside the segment (ds_bpermute) or
-//   ballots (SALU).
+//   RB lanes; reductions across the robots of one env are butterflies inside the segment (DPP and lane swaps)
+//   or ballots (SALU).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -33,11 +33,31 @@ DEV uint32_t mix32(uint32_t x) {
 DEV uint32_t salt32(uint32_t v) { return mix32(v) + GOLD; }
 DEV uint32_t elem_hash(uint32_t base, uint32_t i) { return mix32(mix32(base + i * GOLD) ^ base); }
 DEV float uniform_bits(uint32_t h) { return (float)(h >> 8) * INV24; }
-// Box-Muller, cosine branch, from the hashes of elements 2j and 2j + 1
+// natural log of u in [2^-24, 1] (a normal float): v_log_f32 (log2) scaled by ln 2 in two parts with the product's
+// rounding error recovered by an fma, the steps logf takes for such an argument (no denormal scaling and no
+// infinity or NaN fix-up is needed on this range)
+DEV float ln_unit(float u) {
+    const float l2 = __builtin_amdgcn_logf(u);
+    const float p = l2 * __int_as_float(0x3f317217);
+    const float e = fmaf(__int_as_float(0x3377d1cf), l2, fmaf(l2, __int_as_float(0x3f317217), -p));
+    return p + e;
+}
+// correctly rounded square root of x = +-0 or a normal positive float: the hardware estimate, then the neighbour one
+// ulp below or above it when the residual x - s s' shows that it is nearer (the steps sqrtf takes for such an
+// argument; no denormal scaling is needed on this range, and a zero returns itself)
+DEV float sqrt_pos(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float sd = __int_as_float(__float_as_int(s) - 1), su = __int_as_float(__float_as_int(s) + 1);
+    float r = fmaf(-sd, s, x) <= 0.0f ? sd : s;
+    r = fmaf(-su, s, x) > 0.0f ? su : r;
+    return x == 0.0f ? x : r;
+}
+// Box-Muller, cosine branch, from the hashes of elements 2j and 2j + 1 (u1 in [2^-24, 1], so -2 ln u1 is +-0 or a
+// normal float in [1.2e-7, 33.3])
 DEV float normal_of(uint32_t h1, uint32_t h2) {
     float u1 = (float)((h1 >> 8) + 1u) * INV24;
     float u2 = (float)(h2 >> 8) * INV24;
-    return sqrtf(-2.0f * logf(u1)) * cosf((float)6.283185307179586 * u2);
+    return sqrt_pos(-2.0f * ln_unit(u1)) * cosf((float)6.283185307179586 * u2);
 }
 // element j of a normal draw uses hash elements 2j and 2j + 1
 DEV float normal_at(uint32_t base, uint32_t j) { return normal_of(elem_hash(base, 2u * j), elem_hash(base, 2u * j + 1u)); }

@@ -9,7 +9,7 @@
 //
 // Work decomposition: one workgroup is one wavefront; one robot per lane; the RB = next_pow2(R) lanes of an env form
 // one aligned segment of the wavefront, so every cross-robot step of the scheduler (retransmission admission,
-// RBG-by-RBG argmax, lexicographic masking) is a DPP / swizzle butterfly or a ballot inside the segment, with no
+// RBG-by-RBG argmax, lexicographic masking) is a DPP / lane-swap butterfly or a ballot inside the segment, with no
 // barrier. Per-robot state (HARQ processes, subband CSI and fading, MAC scalars) stays in VGPRs across the slots;
 // the per-MCS tables live in LDS; the in-order RLC pointer after every UL slot is recorded in LDS and replayed over
 // the queued frames in the epilogue, so the slot loop never reads the frame FIFO.
@@ -51,49 +51,41 @@ DEV uint32_t hm_pack(int st, int ntx, int mcs, int nsb) {
 }
 
 // ---------------------------------------------------------------- butterflies inside a power-of-two segment
-// Level L pairs every lane with a lane of the other half of its 2^(L+1) group: quad_perm [1,0,3,2] and [2,3,0,1],
-// row_half_mirror, row_mirror (DPP), a swizzle with xor 16 and a permute with xor 32. Used only for reductions whose
-// operands are already uniform inside each 2^L group, where any such pairing gives the group result.
-template <int L>
-DEV int bfly(int v) {
-    if constexpr (L == 0) return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
-    else if constexpr (L == 1) return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
-    else if constexpr (L == 2) return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
-    else if constexpr (L == 3) return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
-    else if constexpr (L == 4) return __builtin_amdgcn_ds_swizzle(v, 0x401F);
-    else return __builtin_amdgcn_ds_bpermute((int)((__lane_id() ^ 32u) << 2), v);
+// Level L combines every lane with a lane of the other half of its 2^(L+1) group: quad_perm [1,0,3,2] and [2,3,0,1],
+// row_half_mirror, row_mirror (DPP moves with bound_ctrl, which the compiler folds into the consuming ALU op as a DPP
+// source operand), then v_permlane16_swap (16-lane rows 2j and 2j + 1) and v_permlane32_swap (the two 32-lane
+// halves): a swap of a value with itself leaves the first register holding the lower row's value and the second the
+// upper row's, at every lane of the pair. Used only for commutative reductions whose operands are already uniform
+// inside each 2^L group, where any such pairing gives the group result.
+template <int L, class Op>
+DEV int blevel(int v, Op op) {
+    if constexpr (L == 0) return op(v, __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true));
+    else if constexpr (L == 1) return op(v, __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true));
+    else if constexpr (L == 2) return op(v, __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true));
+    else if constexpr (L == 3) return op(v, __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true));
+    else if constexpr (L == 4) {
+        const auto s = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return op((int)s[0], (int)s[1]);
+    } else {
+        const auto s = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        return op((int)s[0], (int)s[1]);
+    }
 }
+struct OpAdd { DEV int operator()(int a, int b) const { return a + b; } };
+struct OpMax { DEV int operator()(int a, int b) const { return a > b ? a : b; } };
 
 DEV int bsum(int v, int rb) {
-    if (rb > 1) v += bfly<0>(v);
-    if (rb > 2) v += bfly<1>(v);
-    if (rb > 4) v += bfly<2>(v);
-    if (rb > 8) v += bfly<3>(v);
-    if (rb > 16) v += bfly<4>(v);
-    if (rb > 32) v += bfly<5>(v);
+    if (rb > 1) v = blevel<0>(v, OpAdd{});
+    if (rb > 2) v = blevel<1>(v, OpAdd{});
+    if (rb > 4) v = blevel<2>(v, OpAdd{});
+    if (rb > 8) v = blevel<3>(v, OpAdd{});
+    if (rb > 16) v = blevel<4>(v, OpAdd{});
+    if (rb > 32) v = blevel<5>(v, OpAdd{});
     return v;
 }
 
 template <int L>
-DEV void amax_lvl(float& v, int& i) {
-    float v2 = __int_as_float(bfly<L>(__float_as_int(v)));
-    int i2 = bfly<L>(i);
-    bool take = (v2 > v) || (v2 == v && i2 < i);
-    v = take ? v2 : v;
-    i = take ? i2 : i;
-}
-// argmax over the segment with the first index on ties (torch max / argmax)
-DEV void bargmax(float& v, int& i, int rb) {
-    if (rb > 1) amax_lvl<0>(v, i);
-    if (rb > 2) amax_lvl<1>(v, i);
-    if (rb > 4) amax_lvl<2>(v, i);
-    if (rb > 8) amax_lvl<3>(v, i);
-    if (rb > 16) amax_lvl<4>(v, i);
-    if (rb > 32) amax_lvl<5>(v, i);
-}
-
-template <int L>
-DEV int imax_lvl(int v) { return max(v, bfly<L>(v)); }
+DEV int imax_lvl(int v) { return blevel<L>(v, OpMax{}); }
 // maximum over the segment, at every lane of the segment. The scheduler's bids are non-negative floats, whose bit
 // patterns order like the values, or -1 for no bid, so the argmax runs on integers.
 DEV int bmax_i(int v, int rb) {
@@ -650,16 +642,33 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             // conflicts between the pairs of one robot)
             const int n_need = __builtin_popcountll(need);
             const int items = n_need * NCS;
+            // envs of 32 robots: the two keys of the wave from lanes 0 and 32; one env per wave or workgroup: its key
+            const uint32_t own_bf = mix32(base0 ^ row.salt_fade);
+            const uint32_t bf_lo = __builtin_amdgcn_readlane(own_bf, 0);
+            const uint32_t bf_hi = __builtin_amdgcn_readlane(own_bf, RBT == 32 ? 32 : 0);
+            // item it = q n_need + ri (subband q of the ri-th drawing robot); a lane's items are 64 apart, so (q, ri)
+            // advance by (dq, dr) with one carry, and the next item's robot is read from the list ahead of its use
+            int q = 0, ri = 0, dq = 0, dr = 0, L = 0;
+            if (n_need > 0) {
+                dq = STEP_WAVE / n_need;
+                dr = STEP_WAVE - dq * n_need;
+                q = wl / n_need;
+                ri = wl - q * n_need;
+                L = s_list[wbase + ri];
+            }
 #pragma unroll 1
             for (int it = wl; it < items; it += STEP_WAVE) {
-                const int q = it / n_need, ri = it - q * n_need;
-                const int L = s_list[wbase + ri];
-                const uint32_t bf = s_bfe[L / rb];
-                const uint32_t hin = bf + (uint32_t)(4 * (L & (rb - 1)) * NCS + 4 * q) * GOLD;
+                const int Lc = L, qc = q;
+                q += dq;
+                ri += dr;
+                if (ri >= n_need) { ri -= n_need; ++q; }
+                L = s_list[wbase + ri];                       // (ri < n_need: a valid entry, read for the next item)
+                const uint32_t bf = RBT >= 32 ? (Lc < 32 ? bf_lo : bf_hi) : s_bfe[Lc / rb];
+                const uint32_t hin = bf + (uint32_t)(4 * (Lc & (rb - 1)) * NCS + 4 * qc) * GOLD;
                 const float zr = normal_of(mix32(mix32(hin) ^ bf), mix32(mix32(hin + GOLD) ^ bf));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bf), mix32(mix32(hin + 3u * GOLD) ^ bf));
-                s_z[(2 * q) * CW + L] = zr;
-                s_z[(2 * q + 1) * CW + L] = zi;
+                s_z[(2 * qc) * CW + Lc] = zr;
+                s_z[(2 * qc + 1) * CW + Lc] = zi;
             }
             __syncthreads();
             if (draw) {
@@ -775,7 +784,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 return m >= 0 && lane == (m0 >= m1 ? f0 : STEP_WAVE + f1);
             } else {
                 const int mx = bmax_i(m, rb);
-                return m >= 0 && seg_first(m == mx, rb, lane) == r;
+                const int f = seg_first(m == mx, rb, lane);             // (every lane takes part in the ballot)
+                return m >= 0 && f == r;
             }
         };
         const int unsent = enq - sent;
@@ -812,8 +822,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         int rx_nsb = 0;
 #pragma unroll
         for (int p = 0; p < P; ++p) rx_nsb = p == rx_p ? hm_nsb(hmeta[p]) : rx_nsb;
-        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275), and the scheduler
-        // metric per RBG into LDS (rows 0..S-1 of s_x) for the allocation loop
+        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275)
         float rate[S];
         {
             float eo[S];
@@ -830,8 +839,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             if (tb.thr_monotone) {
                 // highest m <= mcs_max with eo >= thr[m] (0 when eo < thr[0] or NaN), thr non-decreasing and +inf
                 // past mcs_max: a binary search whose first three levels compare with the same seven thresholds in
-                // every lane (broadcast LDS reads), then one 16-byte LDS read of the last block of four and a count
-                // of the thresholds passed in it (the S reads are independent of each other)
+                // every lane (broadcast LDS reads), then a count of the thresholds passed in the last block of four
+                // and one read of the spectral efficiency at the result; no branch, and the S lookups are independent
+                // of each other
                 const float t16 = s_thr[16], t8 = s_thr[8], t24 = s_thr[24];
                 const float t4 = s_thr[4], t12 = s_thr[12], t20 = s_thr[20], t28 = s_thr[28];
 #pragma unroll
@@ -844,12 +854,17 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    // thresholds and spectral efficiencies of the block are read together
-                    const float4 q = *reinterpret_cast<const float4*>(&s_thr[mi[s]]);
-                    const float4 g = *reinterpret_cast<const float4*>(&s_se[mi[s]]);
+                    // the block's thresholds and spectral efficiencies, read together (the empty asm keeps the
+                    // values in registers, so that the selection below stays branch-free)
+                    float4 q = *reinterpret_cast<const float4*>(&s_thr[mi[s]]);
+                    float4 g = *reinterpret_cast<const float4*>(&s_se[mi[s]]);
+                    asm("" : "+v"(q.y), "+v"(q.z), "+v"(q.w), "+v"(g.x), "+v"(g.y), "+v"(g.z), "+v"(g.w));
                     const float e = eo[s];
                     const int k = (e >= q.y ? 1 : 0) + (e >= q.z ? 1 : 0) + (e >= q.w ? 1 : 0);
-                    const float se = k == 0 ? g.x : (k == 1 ? g.y : (k == 2 ? g.z : g.w));
+                    float se = g.x;
+                    se = k >= 1 ? g.y : se;
+                    se = k >= 2 ? g.z : se;
+                    se = k >= 3 ? g.w : se;
                     rate[s] = ((se * row.re_prb) * s_w[s]) / 8.0f;
                 }
             } else {
@@ -862,11 +877,21 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 for (int s = 0; s < S; ++s) rate[s] = ((s_se[mi[s]] * row.re_prb) * s_w[s]) / 8.0f;
             }
         }
-        const float avg_c = clamp_min(avg, 1e-9f);
+        // the scheduler metric per RBG (mac.py:267-275: PF, max C/I, RR) into LDS (rows 0..S-1 of s_x, this lane's
+        // column) for the allocation loop
         float* const s_met = s_x;
+        if (pm.sched == 0) {
+            const float avg_c = clamp_min(avg, 1e-9f);
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-            s_met[s * CW + lane] = pm.sched == 0 ? rate[s] / avg_c : (pm.sched == 1 ? rate[s] : (float)(g - last_tx));
+            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = rate[s] / avg_c;
+        } else if (pm.sched == 1) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = rate[s];
+        } else {
+            const float age = (float)(g - last_tx);
+#pragma unroll
+            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = age;
+        }
         auto metric_of = [&](int s) -> float { return s_met[s * CW + lane]; };
         // retransmission admission (mac.py:300-313): rank by the metric sum inside each scheduler, admit while the RBG
         // counts fit (the segment's total fitting implies every cell's)
@@ -907,7 +932,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         for (int s = 0; s < S; ++s) {
             bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
             // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
-            int m = want ? __float_as_int(metric_of(s) + prio) : -1;
+            const float ms = metric_of(s);              // (read by every lane, ahead of the bid)
+            int m = want ? __float_as_int(ms + prio) : -1;
             if (pm.retx_prio) {
                 bool wr = want && has_rx;
                 if (cell_any(wr) && !wr) m = -1;
@@ -926,7 +952,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             for (int s = 0; s < S; ++s) {
                 bool avs = cell_any((rel_rs >> s) & 1u);
                 bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
-                const int m = want ? __float_as_int(metric_of(s)) : -1;
+                const float ms = metric_of(s);
+                const int m = want ? __float_as_int(ms) : -1;
                 const bool sel = winner(m) && avs;
                 if (sel) { won |= 1u << s; ++cnt; }
                 left = left - (sel ? rate[s] : 0.0f);
