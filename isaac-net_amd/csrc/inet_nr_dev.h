@@ -42,6 +42,14 @@ DEV float ln_unit(float u) {
     const float e = fmaf(__int_as_float(0x3377d1cf), l2, fmaf(l2, __int_as_float(0x3f317217), -p));
     return p + e;
 }
+// log10 of a finite p >= 1e-6 (a normal float): v_log_f32 (log2) scaled by log10(2) in two parts with the product's
+// rounding error recovered by an fma, the steps log10f takes for such an argument
+DEV float log10_pos(float p) {
+    const float l2 = __builtin_amdgcn_logf(p);
+    const float a = l2 * __int_as_float(0x3e9a209a);
+    const float e = fmaf(__int_as_float(0x3284fbcf), l2, fmaf(l2, __int_as_float(0x3e9a209a), -a));
+    return a + e;
+}
 // correctly rounded square root of x = +-0 or a normal positive float: the hardware estimate, then the neighbour one
 // ulp below or above it when the residual x - s s' shows that it is nearer (the steps sqrtf takes for such an
 // argument; no denormal scaling is needed on this range, and a zero returns itself)

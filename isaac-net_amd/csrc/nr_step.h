@@ -682,30 +682,42 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         }
         // fading gain (dB) of subband s of the serving link in this slot (nr_engine.py:602-611; several cells: the
         // serving cell's, pick(gain_c, serv)), and of link (c, s) (gain_cs)
-        auto gain_of = [&](int s) -> float {
-            float gs = 0.f;
-            if (pm.fading) {
-                float p;
-                if constexpr (MC) {
-                    p = hr[s] * hr[s] + hi[s] * hi[s];
+        // (the powers are finite and clamped to at least 1e-6, where log10_pos is log10f)
+        auto power_of = [&](int s, bool rician) -> float {
+            if constexpr (MC) {
+                float p = hr[s] * hr[s] + hi[s] * hi[s];
 #pragma unroll
-                    for (int c = 1; c < NC; ++c) {
-                        const float pc_ = hr[c * S + s] * hr[c * S + s] + hi[c * S + s] * hi[c * S + s];
-                        p = serv == c ? pc_ : p;
-                    }
-                } else if (pm.rician) {
-                    float xr = ka * sp_re + kb * hr[s];
-                    float xi = ka * sp_im + kb * hi[s];
-                    p = xr * xr + xi * xi;
-                } else {
-                    p = hr[s] * hr[s] + hi[s] * hi[s];
+                for (int c = 1; c < NC; ++c) {
+                    const float pc_ = hr[c * S + s] * hr[c * S + s] + hi[c * S + s] * hi[c * S + s];
+                    p = serv == c ? pc_ : p;
                 }
-                gs = 10.0f * log10f(clamp_min(p, 1e-6f));
+                return p;
+            } else if (rician) {
+                const float xr = ka * sp_re + kb * hr[s];
+                const float xi = ka * sp_im + kb * hi[s];
+                return xr * xr + xi * xi;
+            } else {
+                return hr[s] * hr[s] + hi[s] * hi[s];
             }
-            return gs;
+        };
+        auto gain_of = [&](int s) -> float {
+            return pm.fading ? 10.0f * log10_pos(clamp_min(power_of(s, pm.rician), 1e-6f)) : 0.0f;
+        };
+        // every subband's gain into g[S], the mode tests hoisted out of the subband loop
+        auto gains_of = [&](float (&gv)[S]) {
+            if (!pm.fading) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) gv[s] = 0.0f;
+            } else if (!MC && pm.rician) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) gv[s] = 10.0f * log10_pos(clamp_min(power_of(s, true), 1e-6f));
+            } else {
+#pragma unroll
+                for (int s = 0; s < S; ++s) gv[s] = 10.0f * log10_pos(clamp_min(power_of(s, false), 1e-6f));
+            }
         };
         auto gain_cs = [&](int q) -> float {
-            return pm.fading ? 10.0f * log10f(clamp_min(hr[q] * hr[q] + hi[q] * hi[q], 1e-6f)) : 0.0f;
+            return pm.fading ? 10.0f * log10_pos(clamp_min(hr[q] * hr[q] + hi[q] * hi[q], 1e-6f)) : 0.0f;
         };
         if constexpr (DL) {
             if (row.flags & 1) {                   // CQI report (DlMac.cqi_report, mac_dl.py:30-40)
@@ -928,21 +940,27 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         int cnt = 0;
         float left = (float)need;
         uint32_t won = 0;
+        // (one copy of the loop per retx-priority setting, so that the test is not repeated per RBG)
+        auto allocate = [&](auto retx_prio) {
+            constexpr bool RP = decltype(retx_prio)::value;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
-            // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
-            const float ms = metric_of(s);              // (read by every lane, ahead of the bid)
-            int m = want ? __float_as_int(ms + prio) : -1;
-            if (pm.retx_prio) {
-                bool wr = want && has_rx;
-                if (cell_any(wr) && !wr) m = -1;
+            for (int s = 0; s < S; ++s) {
+                const bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
+                // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
+                const float ms = metric_of(s);          // (read by every lane, ahead of the bid)
+                int m = want ? __float_as_int(ms + prio) : -1;
+                if constexpr (RP) {
+                    const bool wr = want && has_rx;
+                    if (cell_any(wr) && !wr) m = -1;
+                }
+                // argmax over the robots of the scheduler, first robot on ties (torch argmax); -1: no bid
+                const bool sel = winner(m);
+                if (sel) { won |= 1u << s; ++cnt; }
+                left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
             }
-            // argmax over the robots of the scheduler, first robot on ties (torch argmax); -1: no bid
-            const bool sel = winner(m);
-            if (sel) { won |= 1u << s; ++cnt; }
-            left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
-        }
+        };
+        if (pm.retx_prio) allocate(std::true_type{});
+        else allocate(std::false_type{});
         if (!pm.retx_prio) {                          // release short retransmissions (mac.py:353-379)
             bool short_ = has_rx && (__popc(won) != rx_nsb);
             uint32_t rel_rs = short_ ? won : 0u;
@@ -1082,11 +1100,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         if (tx_new) sent = sent + byt_new;
         // ---- actual channel of this slot: fading gain per subband; in the UL it becomes the CSI (mac_ul.py:229-236)
         float gn[DL ? S : 1];
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            if constexpr (DL) gn[s] = gain_of(s);
-            else csi[s] = gain_of(s);
-        }
+        if constexpr (DL) gains_of(gn);
+        else gains_of(csi);
         // ---- several cells: same-slot UL interference (NRNet._ul_ici, nr_engine.py:799-816) ----
         // Every robot that transmits adds, at each other cell c and RBG s it holds, its received power
         // 10^((((pg_c + ue_tx) - ref_db) - split + gain_cs) / 10) (mW per PRB). Each lane writes its NC S terms (zeros
