@@ -110,7 +110,10 @@ typedef struct InetNrTables {
     const float *logw;        /* [S] log(w) */
     const float *wdb;         /* [S] 10 log10(w / snr_ref_prbs) */
     float s0, ds, c0, dc;     /* SNR grid origin / step, code-block axis origin / step */
-    int32_t M, C, G, NPRB, EQW, mcs_max, thr_monotone, pad;
+    int32_t M, C, G, NPRB, EQW, mcs_max;
+    int32_t thr_monotone;     /* informational: thr_ref[0..mcs_max] non-decreasing (the kernels search its suffix
+                                 minima, which give the highest passing MCS for any table) */
+    int32_t pad;
 } InetNrTables;
 
 /* Config constants of the step (derived on the host from NRConfig). */

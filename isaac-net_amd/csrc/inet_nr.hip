@@ -5,9 +5,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "../../include/inet_nr.h"
 #include "inet_nr_dev.h"
+
 #include "nr_step.h"
 
 using namespace inet;
@@ -262,8 +264,11 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
         if (dl || vref) return INET_NR_EUNSUPPORTED;
         fn = inet::pick_step_w2(p.S, p.P, ir);
     } else {
-        fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb)
-           : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb) : nullptr;
+        // (INET_NR_GENERIC=1 keeps the general build, for comparing the two)
+        const char* gen = getenv("INET_NR_GENERIC");
+        const bool fx = inet::fx_profile(p) && !(gen && gen[0] == '1');
+        fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb, fx)
+           : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb, fx) : nullptr;
     }
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = rb > inet::STEP_WAVE ? 1 : inet::STEP_WAVE / rb;
@@ -288,7 +293,8 @@ int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
 
 const char* inet_nr_build_info(void) {
     return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, two-wave step (R <= 128), "
-           "multi-cell step<C = 3, S in {8,13,14}, P, IR>, DPP segment reductions, ATen-order sums";
+           "multi-cell step<C = 3, S in {8,13,14}, P, IR>, common-configuration step<13, 8>, DPP segment reductions, "
+           "ATen-order sums";
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,

@@ -242,11 +242,21 @@ DEV T sel_of(const T (&v)[N], int idx) {
 // RBT = 128: envs of 65..128 robots, one env per workgroup of two wavefronts (W = 2); the env-wide collectives then
 // combine the two waves' ballots and butterflies through LDS (xchg), and every cooperative loop runs a number of
 // rounds that both waves agree on, so that every barrier is reached by both.
-template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC>
+//
+// FX = 1 builds the kernel for the common configuration (PF, chase combining, EESM, RLC AM, OLLA, PHR cap, retx
+// priority, a fixed Rician phasor, fading; fx_profile): those switches become
+// compile-time constants, which removes their tests from the slot loop and the scalar registers that hold them.
+template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC, int FX = 0>
 __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
-    InetNrState st, LS lk, InetNrTables tb, InetNrParams pm, const InetNrRow* __restrict__ rows, int n_rows,
+    InetNrState st, LS lk, InetNrTables tb_in, InetNrParams pm_in, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
+    InetNrParams pm = pm_in;
+    InetNrTables tb = tb_in;
+    if constexpr (FX == 1) {
+        pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
+        pm.rician = 1; pm.fading = 1;
+    }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     constexpr bool MC = NC > 1;
     static_assert(!(MC && (DL || VREF)), "several cells: the UL with pose input");
@@ -258,6 +268,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     const int64_t T = T_arg >= 0 ? T_arg : st.clock[0];
     extern __shared__ int dyn[];
     __shared__ __align__(16) float s_thr[MAX_M];
+    __shared__ __align__(16) float s_thrs[MAX_M];                // suffix minima of s_thr (the MCS search table)
     __shared__ __align__(16) float s_se[MAX_M];
     __shared__ float s_beta[MAX_M], s_rbeta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S];
@@ -330,6 +341,14 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
+    // "the highest m <= mcs_max with x >= thr[m]" is the highest m with x >= min(thr[m..mcs_max]): these suffix
+    // minima are non-decreasing, so a binary search over them gives the linear scan's result for any table. Past
+    // mcs_max the entries are NaN, which no comparison passes (not even x = +inf).
+    if (lane < MAX_M) {
+        float v = INFINITY;
+        for (int j = tb.mcs_max; j >= lane; --j) v = fminf(v, tb.thr_ref[j]);
+        s_thrs[lane] = lane <= tb.mcs_max ? v : __builtin_nanf("");
+    }
     if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
     if (lane < tb.M) {
         s_beta[lane] = tb.beta[lane];
@@ -848,14 +867,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 eo[s] = pm.olla ? est + olla : est;
                 mi[s] = 0;
             }
-            if (tb.thr_monotone) {
-                // highest m <= mcs_max with eo >= thr[m] (0 when eo < thr[0] or NaN), thr non-decreasing and +inf
-                // past mcs_max: a binary search whose first three levels compare with the same seven thresholds in
-                // every lane (broadcast LDS reads), then a count of the thresholds passed in the last block of four
-                // and one read of the spectral efficiency at the result; no branch, and the S lookups are independent
-                // of each other
-                const float t16 = s_thr[16], t8 = s_thr[8], t24 = s_thr[24];
-                const float t4 = s_thr[4], t12 = s_thr[12], t20 = s_thr[20], t28 = s_thr[28];
+            {
+                // highest m <= mcs_max with eo >= thr[m] (0 when none, or NaN): a binary search over the suffix
+                // minima, whose first three levels compare with the same seven values in every lane (broadcast
+                // LDS reads), then a count of the values passed in the last block of four and a branch-free
+                // selection of the spectral efficiency (the S lookups are independent of each other)
+                const float t16 = s_thrs[16], t8 = s_thrs[8], t24 = s_thrs[24];
+                const float t4 = s_thrs[4], t12 = s_thrs[12], t20 = s_thrs[20], t28 = s_thrs[28];
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     const float e = eo[s];
@@ -866,9 +884,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 }
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    // the block's thresholds and spectral efficiencies, read together (the empty asm keeps the
+                    // the block's search values and spectral efficiencies, read together (the empty asm keeps the
                     // values in registers, so that the selection below stays branch-free)
-                    float4 q = *reinterpret_cast<const float4*>(&s_thr[mi[s]]);
+                    float4 q = *reinterpret_cast<const float4*>(&s_thrs[mi[s]]);
                     float4 g = *reinterpret_cast<const float4*>(&s_se[mi[s]]);
                     asm("" : "+v"(q.y), "+v"(q.z), "+v"(q.w), "+v"(g.x), "+v"(g.y), "+v"(g.z), "+v"(g.w));
                     const float e = eo[s];
@@ -879,14 +897,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                     se = k >= 3 ? g.w : se;
                     rate[s] = ((se * row.re_prb) * s_w[s]) / 8.0f;
                 }
-            } else {
-                for (int m = 0; m <= tb.mcs_max; ++m) {
-                    const float th = s_thr[m];
-#pragma unroll
-                    for (int s = 0; s < S; ++s) mi[s] = eo[s] >= th ? m : mi[s];
-                }
-#pragma unroll
-                for (int s = 0; s < S; ++s) rate[s] = ((s_se[mi[s]] * row.re_prb) * s_w[s]) / 8.0f;
             }
         }
         // the scheduler metric per RBG (mac.py:267-275: PF, max C/I, RR) into LDS (rows 0..S-1 of s_x, this lane's
@@ -1522,17 +1532,23 @@ struct StepArgs {
 };
 typedef void (*StepFn)(const StepArgs&);
 
-template <int S, int P, bool IR, bool VREF, int RBT>
+template <int S, int P, bool IR, bool VREF, int RBT, int FX = 0>
 void launch_step(const StepArgs& a) {
     const InetNrCells none{};
     if (a.dl)
-        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState, 1>), dim3(a.grid), dim3(STEP_WAVE),
-                           a.lds, a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
-                           a.n_data, a.arr, none);
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrDlState, 1, FX>), dim3(a.grid),
+                           dim3(STEP_WAVE), a.lds, a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x,
+                           a.hid, a.out, a.rb, a.n_data, a.arr, none);
     else
-        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState, 1>), dim3(a.grid), dim3(STEP_WAVE),
+        hipLaunchKernelGGL((nr_step_kernel<S, P, IR, VREF, RBT, InetNrState, 1, FX>), dim3(a.grid), dim3(STEP_WAVE),
                            a.lds, a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
                            a.n_data, a.arr, none);
+}
+
+// true when the parameters are those the FX = 1 build fixes at compile time
+inline bool fx_profile(const InetNrParams& p) {
+    return p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 && p.phr_cap == 1 &&
+           p.retx_prio == 1 && p.rician == 1 && p.fading == 1;
 }
 
 // envs of 65..128 robots: one env per workgroup of two wavefronts (UL, pose or SNR input)
@@ -1555,7 +1571,9 @@ void launch_step_mc(const StepArgs& a) {
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband
 // input, a build with the width fixed at compile time
 template <int S>
-StepFn pick_step_s(int P, bool ir, bool vref, int rb) {
+StepFn pick_step_s(int P, bool ir, bool vref, int rb, bool fx) {
+    if constexpr (S == 13)                           // the common configuration at 13 RBGs, 8 HARQ, 32-robot envs
+        if (fx && P == 8 && !ir && !vref && rb == 32) return &launch_step<13, 8, false, false, 32, 1>;
 #define INET_PICK(PP)                                                                                 \
     if (P == PP) {                                                                                    \
         if (!ir && !vref && rb == 32) return &launch_step<S, PP, false, false, 32>;                  \
@@ -1567,8 +1585,8 @@ StepFn pick_step_s(int P, bool ir, bool vref, int rb) {
     return nullptr;
 }
 
-StepFn pick_step_s13(int P, bool ir, bool vref, int rb);   // nr_step_s13.hip
-StepFn pick_step_s8(int P, bool ir, bool vref, int rb);    // nr_step_s8.hip
+StepFn pick_step_s13(int P, bool ir, bool vref, int rb, bool fx);   // nr_step_s13.hip
+StepFn pick_step_s8(int P, bool ir, bool vref, int rb, bool fx);    // nr_step_s8.hip
 
 // multi-cell builds (NC = 3): every (P, IR)
 template <int S>

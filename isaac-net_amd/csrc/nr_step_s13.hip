@@ -1,8 +1,8 @@
 // Step-kernel instantiations for 13 subbands (RBGs): HARQ processes 2, 4, 8, 16 x (IR combining) x (per-subband
 // SNR input), with a runtime segment width; and the plain case (no IR, pose or SNR input) for 32-robot envs with the
-// segment width fixed at compile time.
+// segment width fixed at compile time; and that case with 8 processes built for the common configuration (FX = 1).
 #include "nr_step.h"
 
 namespace inet {
-StepFn pick_step_s13(int P, bool ir, bool vref, int rb) { return pick_step_s<13>(P, ir, vref, rb); }
+StepFn pick_step_s13(int P, bool ir, bool vref, int rb, bool fx) { return pick_step_s<13>(P, ir, vref, rb, fx); }
 }  // namespace inet

@@ -231,3 +231,32 @@ def test_interference_sum_order_is_torchs(R, C, S):
         for r in range(R):
             seq = (seq + x.numpy()[:, r]).astype(np.float32)
         assert not np.array_equal(seq, want)
+
+
+def _search_suffix_min(thr, mcs_max, e):
+    """The step kernel's MCS search: three binary levels, then a count inside the last block of four, over the
+    suffix minima of thr[0..mcs_max] (NaN past mcs_max, 32 entries)."""
+    t = np.full(32, np.nan, np.float32)
+    for m in range(mcs_max + 1):
+        t[m] = np.min(thr[m:mcs_max + 1])
+    m = 16 if e >= t[16] else 0
+    m += 8 if e >= (t[24] if m else t[8]) else 0
+    m += 4 if e >= (t[m + 4]) else 0
+    return m + int(e >= t[m + 1]) + int(e >= t[m + 2]) + int(e >= t[m + 3])
+
+
+def test_mcs_search_over_suffix_minima_is_the_linear_scan():
+    """phy.mcs_at (the highest m <= mcs_max with x >= thr_ref[m], else 0) equals the kernel's binary search over the
+    suffix minima for any table: non-monotone, with ties, and at NaN or infinite inputs."""
+    rs = np.random.default_rng(5)
+    for trial in range(300):
+        mcs_max = int(rs.integers(1, 32))
+        thr = np.sort(rs.uniform(-10, 25, mcs_max + 1)).astype(np.float32)
+        if trial % 3:
+            thr = thr + rs.normal(0, 2.0, thr.shape).astype(np.float32)        # non-monotone
+        if trial % 5 == 0:
+            thr[rs.integers(0, mcs_max + 1)] = thr[rs.integers(0, mcs_max + 1)]  # ties
+        xs = np.concatenate([rs.uniform(-15, 30, 40), thr, thr + np.float32(1e-6), [np.nan, -np.inf, np.inf]])
+        for e in xs.astype(np.float32):
+            lin = max([m for m in range(mcs_max + 1) if e >= thr[m]], default=0)
+            assert _search_suffix_min(thr, mcs_max, e) == lin, (trial, e)
