@@ -33,9 +33,9 @@ DEV uint32_t mix32(uint32_t x) {
 DEV uint32_t salt32(uint32_t v) { return mix32(v) + GOLD; }
 DEV uint32_t elem_hash(uint32_t base, uint32_t i) { return mix32(mix32(base + i * GOLD) ^ base); }
 DEV float uniform_bits(uint32_t h) { return (float)(h >> 8) * INV24; }
-// natural log of u in [2^-24, 1] (a normal float): v_log_f32 (log2) scaled by ln 2 in two parts with the product's
+// natural log of a normal, finite, positive u: v_log_f32 (log2) scaled by ln 2 in two parts with the product's
 // rounding error recovered by an fma, the steps logf takes for such an argument (no denormal scaling and no
-// infinity or NaN fix-up is needed on this range)
+// infinity or NaN fix-up is needed there)
 DEV float ln_unit(float u) {
     const float l2 = __builtin_amdgcn_logf(u);
     const float p = l2 * __int_as_float(0x3f317217);
@@ -100,6 +100,22 @@ DEV float nan_to_num(float x, float nan, float pinf, float ninf) {
 }
 // phy._db: 10 log10(max(x, 1e-6)) with NaN -> -30, +inf -> 60, -inf -> -30
 DEV float db_of(float lin) { return nan_to_num(10.0f * log10f(clamp_min(lin, 1e-6f)), -30.0f, 60.0f, -30.0f); }
+// 2^(y c) for the constant c = C1 + C2 (two parts) and y with y c well inside the float exponent range: the product
+// split into an integer and a fraction, v_exp_f32 of the fraction scaled by ldexp, the steps expf / exp10f take
+// for such an argument (their overflow and underflow fix-ups never fire there)
+template <uint32_t C1, uint32_t C2>
+DEV float exp2_scaled(float y) {
+    const float c1 = __int_as_float(C1);
+    const float t = y * c1;
+    const float e = fmaf(__int_as_float(C2), y, fmaf(y, c1, -t));
+    const float r = rintf(t);
+    return ldexpf(__builtin_amdgcn_exp2f((t - r) + e), (int)r);
+}
+// exp(x) for a finite x <= 0 inside a sum with a term 1 (the log-sum-exp after its max): below -103.97 expf returns
+// 0 where these steps can leave 2^-149, which the sum absorbs
+DEV float exp_nonpos(float x) { return exp2_scaled<0x3fb8aa3bu, 0x32a5705fu>(x); }
+// 10 ** (x / 10) for x in [-30, 60] (a clamped SINR in dB), as from_db below
+DEV float from_db_mid(float x) { return exp2_scaled<0x40549a78u, 0x33979a37u>(div_const(x, 10.0f, 0.1f)); }
 // 10 ** (x / 10) as torch evaluates it: x / 10 in float32, then 10 to that power (exp10, within an ulp)
 DEV float from_db(float x) { return exp10f(div_const(x, TEN_F, INV_TEN_F)); }
 // x ** n for the integer-valued float n >= 0 of a code-block count (torch pow(float, float)): binary powering in

@@ -147,8 +147,10 @@ DEV float lse_logw(const float* s_logw, uint32_t won) {
     }
     if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
     float sum = 0.f;
-    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
-    return logf(sum) + mx;
+    // (sum >= 1 when some RBG is held: the max term is exp(0); every term is exp of a finite x <= 0; none held: the
+    // log of 0)
+    for (uint32_t m = rot; m; m &= m - 1) sum += exp_nonpos(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
+    return (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
 }
 // lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of the robot whose linear SINR row is column `col` of s_lin
 // (s_lin[s * CW + col], CW lanes per workgroup); x_s is kept in column `tmp` of s_tmp between the max and the sum.
@@ -167,8 +169,10 @@ DEV float lse_eesm(const float* s_lin, int col, float* s_tmp, int tmp, const flo
     }
     if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
     float sum = 0.f;
-    for (uint32_t m = rot; m; m &= m - 1) sum += expf(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * CW + tmp] - mx);
-    float r = logf(sum) + mx;
+    // (sum >= 1 when some RBG is held: the max term is exp(0); every term is exp of a finite x <= 0; none held: the
+    // log of 0)
+    for (uint32_t m = rot; m; m &= m - 1) sum += exp_nonpos(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * CW + tmp] - mx);
+    float r = (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
     return nan ? NAN : r;
 }
 // PRB-weighted mean of the per-RBG dB values x_s (s_x[s * CW + lane]) over the held RBGs (mean_db): the ATen-order
@@ -178,7 +182,7 @@ DEV float mean_db_held(const float* s_x, int lane, const float* s_logw, uint32_t
     float acc = 0.f;
     for (uint32_t m = aten_rot<S>(won); m; m &= m - 1) {
         int s = aten_unrot<S>(__builtin_ctz(m));
-        float t = s_x[s * CW + lane] * expf(s_logw[s] - lnw);
+        float t = s_x[s * CW + lane] * exp_nonpos(s_logw[s] - lnw);        // (log w_s - log sum w in [-2.6, 0])
         acc += nan_to_num(t, 0.0f, 3.4028234663852886e38f, -3.4028234663852886e38f);
     }
     return acc;
@@ -1015,7 +1019,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             }
             for (uint32_t mm = tx_new ? won : 0u; mm; mm &= mm - 1) {
                 int s = __builtin_ctz(mm);
-                s_lin[s * CW + lane] = from_db(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
+                s_lin[s * CW + lane] = from_db_mid(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
             }
             const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw) : 0.f;
             const int np = (int)n_prb;
@@ -1164,7 +1168,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             }
             for (uint32_t mm = tx ? won : 0u; mm; mm &= mm - 1) {
                 int s = __builtin_ctz(mm);
-                s_lin[s * CW + lane] = from_db(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
+                s_lin[s * CW + lane] = from_db_mid(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
             }
             float eff_used;
             int m_look = mcs;
