@@ -70,6 +70,22 @@ DEV float normal_of(uint32_t h1, uint32_t h2) {
 // element j of a normal draw uses hash elements 2j and 2j + 1
 DEV float normal_at(uint32_t base, uint32_t j) { return normal_of(elem_hash(base, 2u * j), elem_hash(base, 2u * j + 1u)); }
 
+// x / y for many x over one y, with x in [0, 2^60] and y normal in [2^-60, 2^60]: the Newton-Raphson steps of the
+// IEEE division sequence (reciprocal, one refinement, then two residual corrections of the quotient), with the
+// refined reciprocal shared by every x. On such operands that sequence's scaling and special-value fix-up steps
+// change nothing, so the result is the IEEE quotient.
+struct DivBy {
+    float y, r;
+    DEV explicit DivBy(float y_) : y(y_) {
+        const float r0 = __builtin_amdgcn_rcpf(y_);
+        r = fmaf(fmaf(-y_, r0, 1.0f), r0, r0);
+    }
+    DEV float operator()(float x) const {
+        const float q0 = x * r;
+        const float q1 = fmaf(fmaf(-y, q0, x), r, q0);
+        return fmaf(fmaf(-y, q1, x), r, q1);
+    }
+};
 // x / y rounded to nearest for a constant y with r = RN(1 / y): q = RN(x r), then one fma correction of the residual
 // (Markstein). For the constants below this equals IEEE division for every float32 x; the check runs over every
 // significand in tests/test_numerics.py.
@@ -98,8 +114,14 @@ DEV float clampf(float x, float lo, float hi) { return x < lo ? lo : (x > hi ? h
 DEV float nan_to_num(float x, float nan, float pinf, float ninf) {
     return x != x ? nan : (x == INFINITY ? pinf : (x == -INFINITY ? ninf : x));
 }
+// log10 of x >= 1e-9 (after a clamp) that may also be +inf or NaN: log10_pos, with +inf kept (NaN stays NaN), as
+// log10f gives
+DEV float log10_clamped(float x) {
+    const float l = log10_pos(x);
+    return x == INFINITY ? x : l;
+}
 // phy._db: 10 log10(max(x, 1e-6)) with NaN -> -30, +inf -> 60, -inf -> -30
-DEV float db_of(float lin) { return nan_to_num(10.0f * log10f(clamp_min(lin, 1e-6f)), -30.0f, 60.0f, -30.0f); }
+DEV float db_of(float lin) { return nan_to_num(10.0f * log10_clamped(clamp_min(lin, 1e-6f)), -30.0f, 60.0f, -30.0f); }
 // 2^(y c) for the constant c = C1 + C2 (two parts) and y with y c well inside the float exponent range: the product
 // split into an integer and a fraction, v_exp_f32 of the fraction scaled by ldexp, the steps expf / exp10f take
 // for such an argument (their overflow and underflow fix-ups never fire there)

@@ -908,8 +908,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         float* const s_met = s_x;
         if (pm.sched == 0) {
             const float avg_c = clamp_min(avg, 1e-9f);
+            // (rates in [0, 2^20], the average in [1e-9, 2^40]: DivBy gives the IEEE quotient)
+            const DivBy div_avg(avg_c);
 #pragma unroll
-            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = rate[s] / avg_c;
+            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = div_avg(rate[s]);
         } else if (pm.sched == 1) {
 #pragma unroll
             for (int s = 0; s < S; ++s) s_met[s * CW + lane] = rate[s];
@@ -999,7 +1001,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         const bool tx_new = new_el && n_sb > 0;
         const bool tx = tx_rx || tx_new;
         // power split (mac_ul.py:173-180): PUSCH power spread over n_prb PRBs, at least the power-control backoff
-        const float sp0 = 10.0f * log10f(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
+        const float sp0 = 10.0f * log10_clamped(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
         const float sp = MC ? (sp0 > pc ? sp0 : pc) : sp0;
         // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
         const float lnw = lse_logw<S>(s_logw, won);
@@ -1179,7 +1181,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
                 nrb = nrb_p + n_prb;
                 float v = (-beta) * (lexp - logf(clamp_min(nrb, 1.0f)));
-                eff_used = nan_to_num(10.0f * log10f(clamp_min(v, 1e-6f)), -30.0f, 60.0f, -30.0f);
+                eff_used = nan_to_num(10.0f * log10_clamped(clamp_min(v, 1e-6f)), -30.0f, 60.0f, -30.0f);
                 int nt = ntx < tb.EQW - 1 ? ntx : tb.EQW - 1;
                 m_look = s_eq[mcs * tb.EQW + nt];
                 comb = comb_p;
@@ -1192,7 +1194,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 }
                 float lin_e = from_db(eff);
                 comb = pm.comb == 1 ? comb_p + lin_e : lin_e;
-                eff_used = 10.0f * log10f(clamp_min(comb, 1e-9f));
+                eff_used = 10.0f * log10_clamped(clamp_min(comb, 1e-9f));
             }
             float cbs, ncb;
             segment_f(tbs, s_rate[mcs], cbs, ncb);
