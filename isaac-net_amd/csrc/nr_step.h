@@ -210,7 +210,8 @@ DEV void segment_f(int tbs, float r32, float& cbs, float& ncb) {
     const bool bg2 = (tbs <= 292) || ((tbs <= 3824) && (r <= 0.67)) || (r <= 0.25);
     const int kcb = bg2 ? 3840 : 8448;
     const int b = tbs + (tbs > 3824 ? 24 : 16);
-    const int c = b <= kcb ? 1 : (b + (kcb - 24) - 1) / (kcb - 24);
+    // ceil(b / (kcb - 24)) with each constant divisor written out (a multiply by its reciprocal, not a division)
+    const int c = b <= kcb ? 1 : (bg2 ? (b + 3815) / 3816 : (b + 8423) / 8424);
     cbs = c > 1 ? (float)((double)(b + 24 * c) / (double)c) : (float)b;
     ncb = (float)c;
 }
