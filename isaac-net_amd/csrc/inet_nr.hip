@@ -252,6 +252,10 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     // the single-cell entry points run one cell; inet_nr_step_cells several
     if ((cells != nullptr) != (p.n_cells > 1)) return INET_NR_EINVAL;
     inet::StepFn fn;
+    // the builds with the common switches fixed at compile time (INET_NR_GENERIC=1 keeps the general build, for
+    // comparing the two)
+    const char* gen = getenv("INET_NR_GENERIC");
+    const int fx = (gen && gen[0] == '1') ? 0 : inet::fx_profile(p);
     if (cells) {
         const InetNrCells& c = *cells;
         if (c.C != p.n_cells || c.C > INET_NR_MAX_C || p.input_kind != 0 || p.rician || p.F > 64 || dl)
@@ -262,11 +266,8 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
         fn = inet::pick_step_mc(p.S, c.C, p.P, ir);
     } else if (rb > inet::STEP_WAVE) {          // 65..128 robots: two wavefronts per env, UL
         if (dl || vref) return INET_NR_EUNSUPPORTED;
-        fn = inet::pick_step_w2(p.S, p.P, ir);
+        fn = inet::pick_step_w2(p.S, p.P, ir, fx);
     } else {
-        // (INET_NR_GENERIC=1 keeps the general build, for comparing the two)
-        const char* gen = getenv("INET_NR_GENERIC");
-        const bool fx = inet::fx_profile(p) && !(gen && gen[0] == '1');
         fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb, fx)
            : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb, fx) : nullptr;
     }

@@ -249,7 +249,8 @@ DEV T sel_of(const T (&v)[N], int idx) {
 // rounds that both waves agree on, so that every barrier is reached by both.
 //
 // FX = 1 builds the kernel for the common configuration (PF, chase combining, EESM, RLC AM, OLLA, PHR cap, retx
-// priority, a fixed Rician phasor, fading; fx_profile): those switches become
+// priority, a fixed Rician phasor, fading; fx_profile), FX = 2 for the same without the Rician phasor: those
+// switches become
 // compile-time constants, which removes their tests from the slot loop and the scalar registers that hold them.
 template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC, int FX = 0>
 __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
@@ -258,9 +259,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
     InetNrParams pm = pm_in;
     InetNrTables tb = tb_in;
-    if constexpr (FX == 1) {
+    if constexpr (FX == 1 || FX == 2) {
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
-        pm.rician = 1; pm.fading = 1;
+        pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     constexpr bool MC = NC > 1;
@@ -1552,17 +1553,18 @@ void launch_step(const StepArgs& a) {
                            a.n_data, a.arr, none);
 }
 
-// true when the parameters are those the FX = 1 build fixes at compile time
-inline bool fx_profile(const InetNrParams& p) {
-    return p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 && p.phr_cap == 1 &&
-           p.retx_prio == 1 && p.rician == 1 && p.fading == 1;
+// the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
+inline int fx_profile(const InetNrParams& p) {
+    const bool common = p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
+                        p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
+    return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;
 }
 
 // envs of 65..128 robots: one env per workgroup of two wavefronts (UL, pose or SNR input)
-template <int S, int P, bool IR>
+template <int S, int P, bool IR, int FX = 0>
 void launch_step_w2(const StepArgs& a) {
     const InetNrCells none{};
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 128, InetNrState, 1>), dim3(a.grid), dim3(2 * STEP_WAVE),
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 128, InetNrState, 1, FX>), dim3(a.grid), dim3(2 * STEP_WAVE),
                        a.lds, a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
                        a.n_data, a.arr, none);
 }
@@ -1578,9 +1580,9 @@ void launch_step_mc(const StepArgs& a) {
 // every (P, IR, per-subband SNR) with a runtime segment width; plus, for 32-robot envs without IR or per-subband
 // input, a build with the width fixed at compile time
 template <int S>
-StepFn pick_step_s(int P, bool ir, bool vref, int rb, bool fx) {
+StepFn pick_step_s(int P, bool ir, bool vref, int rb, int fx) {
     if constexpr (S == 13)                           // the common configuration at 13 RBGs, 8 HARQ, 32-robot envs
-        if (fx && P == 8 && !ir && !vref && rb == 32) return &launch_step<13, 8, false, false, 32, 1>;
+        if (fx == 1 && P == 8 && !ir && !vref && rb == 32) return &launch_step<13, 8, false, false, 32, 1>;
 #define INET_PICK(PP)                                                                                 \
     if (P == PP) {                                                                                    \
         if (!ir && !vref && rb == 32) return &launch_step<S, PP, false, false, 32>;                  \
@@ -1592,8 +1594,8 @@ StepFn pick_step_s(int P, bool ir, bool vref, int rb, bool fx) {
     return nullptr;
 }
 
-StepFn pick_step_s13(int P, bool ir, bool vref, int rb, bool fx);   // nr_step_s13.hip
-StepFn pick_step_s8(int P, bool ir, bool vref, int rb, bool fx);    // nr_step_s8.hip
+StepFn pick_step_s13(int P, bool ir, bool vref, int rb, int fx);   // nr_step_s13.hip
+StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx);    // nr_step_s8.hip
 
 // multi-cell builds (NC = 3): every (P, IR)
 template <int S>
@@ -1608,13 +1610,15 @@ StepFn pick_step_mc(int S, int C, int P, bool ir);         // nr_step_mc.hip
 
 // two-wavefront builds (R = 65..128): every (P, IR)
 template <int S>
-StepFn pick_step_w2_s(int P, bool ir) {
+StepFn pick_step_w2_s(int P, bool ir, int fx) {
+    if constexpr (S == 8)                            // config 5's switches without the Rician phasor, 8 HARQ
+        if (fx == 2 && P == 8 && !ir) return &launch_step_w2<8, 8, false, 2>;
 #define INET_PICK_W2(PP) \
     if (P == PP) return ir ? &launch_step_w2<S, PP, true> : &launch_step_w2<S, PP, false>;
     INET_PICK_W2(2) INET_PICK_W2(4) INET_PICK_W2(8) INET_PICK_W2(16)
 #undef INET_PICK_W2
     return nullptr;
 }
-StepFn pick_step_w2(int S, int P, bool ir);                // nr_step_w2.hip
+StepFn pick_step_w2(int S, int P, bool ir, int fx);        // nr_step_w2.hip
 
 }  // namespace inet

@@ -4,5 +4,5 @@
 #include "nr_step.h"
 
 namespace inet {
-StepFn pick_step_s8(int P, bool ir, bool vref, int rb, bool fx) { return pick_step_s<8>(P, ir, vref, rb, fx); }
+StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx) { return pick_step_s<8>(P, ir, vref, rb, fx); }
 }  // namespace inet
