@@ -1570,9 +1570,9 @@ void launch_step_w2(const StepArgs& a) {
 }
 
 // the multi-cell step: NC cells, pose input, runtime segment width
-template <int S, int P, bool IR, int NC>
+template <int S, int P, bool IR, int NC, int FX = 0>
 void launch_step_mc(const StepArgs& a) {
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 0, InetNrState, NC>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 0, InetNrState, NC, FX>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
                        a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
                        a.arr, *a.cells);
 }
@@ -1599,14 +1599,16 @@ StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx);    // nr_step_s8
 
 // multi-cell builds (NC = 3): every (P, IR)
 template <int S>
-StepFn pick_step_mc_s(int P, bool ir) {
+StepFn pick_step_mc_s(int P, bool ir, int fx) {
+    if constexpr (S == 14)                           // config 3's switches (no Rician phasor), 8 HARQ
+        if (fx == 2 && P == 8 && !ir) return &launch_step_mc<14, 8, false, 3, 2>;
 #define INET_PICK_MC(PP) \
     if (P == PP) return ir ? &launch_step_mc<S, PP, true, 3> : &launch_step_mc<S, PP, false, 3>;
     INET_PICK_MC(2) INET_PICK_MC(4) INET_PICK_MC(8) INET_PICK_MC(16)
 #undef INET_PICK_MC
     return nullptr;
 }
-StepFn pick_step_mc(int S, int C, int P, bool ir);         // nr_step_mc.hip
+StepFn pick_step_mc(int S, int C, int P, bool ir, int fx); // nr_step_mc.hip
 
 // two-wavefront builds (R = 65..128): every (P, IR)
 template <int S>

@@ -1,6 +1,7 @@
 """The step kernels built for the common configurations (PF, chase combining, EESM, RLC AM, OLLA, PHR cap, retx
 priority, fading; with a fixed Rician phasor: the RL-scale configuration at 13 RBGs, 8 HARQ processes, 32-robot envs;
-without: config 5's two-wave kernel at 8 RBGs, 128-robot envs) equal the general builds bit for bit: outputs and every
+without: config 5's two-wave kernel at 8 RBGs, 128-robot envs, and config 3's three-cell kernel at 14 RBGs) equal the
+general builds bit for bit: outputs and every
 state tensor, UL and with the downlink, through a partial reset. INET_NR_GENERIC=1 makes the library launch the
 general build for the same call."""
 import os
@@ -43,9 +44,9 @@ def same(a, b):
     return torch.equal(a, b)
 
 
-@pytest.mark.parametrize("name", ["rl_scale", "rl_scale_dl", "freq_sel"])
+@pytest.mark.parametrize("name", ["rl_scale", "rl_scale_dl", "freq_sel", "mc_interf"])
 def test_common_configuration_build_equals_general_build(name):
-    E, R, steps = (64, 32, 8) if name != "freq_sel" else (16, 128, 4)
+    E, R, steps = {"freq_sel": (16, 128, 4), "mc_interf": (16, 64, 6)}.get(name, (64, 32, 8))
     print(f"{name} {E}x{R}, {steps} steps: common-configuration build vs general build", flush=True)
     o_fx, st_fx = run(name, E, R, steps, generic=False)
     o_gen, st_gen = run(name, E, R, steps, generic=True)
