@@ -142,8 +142,9 @@ int32_t inet_wifi_step(const InetWifiState *st, const InetWifiParams *prm, const
    (clock). snr: [E][R] float32 SNR recorded with the frames, or NULL for st->last_snr. Send form (counts == NULL):
    send [E][R] int64 class (0 = none; classes above n_cls take the last class's size), det [E][R] uint8 or NULL,
    hid [E] int64 or NULL; accepted [E][R] uint8. Counts form (send == NULL): counts [E][R][n_cls] uint8, the calls of
-   class 1 first, one call per message index up to the env's largest count; accepted [E][R] int32 = messages
-   accepted; the env's submit counter advances by its number of calls. */
+   class 1 first, one call per message index up to the class's largest count over every env (a call is global, as
+   LevelNet.submit is); accepted [E][R] int32 = messages accepted; every env's submit counter advances by the number
+   of calls and its last hazard id becomes 0 (a second, one-workgroup launch reduces the counts). */
 int32_t inet_wifi_submit(const InetWifiState *st, const InetWifiParams *prm, const int64_t *t, const int64_t *send,
                          const uint8_t *det, const int64_t *hid, const float *snr, const uint8_t *counts,
                          int32_t n_cls, void *accepted, void *stream);

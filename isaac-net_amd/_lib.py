@@ -172,6 +172,11 @@ def load(path=LIB_PATH):
     lib.inet_wifi_dcf_reset.restype = i32
     if lib.inet_nr_abi_version() != ABI_VERSION or lib.inet_wifi_abi_version() != WIFI_ABI_VERSION:
         raise RuntimeError("libinet_nr.so ABI version mismatch; rebuild it")
+    from .build import source_hash
+    built = lib.inet_nr_build_info().decode().rsplit("src=", 1)[-1]
+    if built != source_hash():
+        raise RuntimeError(f"{path} was built from other sources (src={built}, the tree's is {source_hash()}): "
+                           "rebuild it with `python isaac-net_amd/build.py`")
     _LIB = lib
     return lib
 

@@ -22,13 +22,28 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
 
 
+def source_hash():
+    """SHA-256 over the library's sources (csrc/*.h, csrc/*.hip, include/*.h, this file), in name order."""
+    import glob
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(CSRC, "*.hip")) +
+                   glob.glob(os.path.join(HERE, "..", "include", "*.h"))) + [os.path.abspath(__file__)]
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def build(verbose=False, out_dir=None):
     obj_dir = out_dir or os.path.join(HERE, "_build")
     os.makedirs(obj_dir, exist_ok=True)
+    src = source_hash()
 
     def compile_unit(u):
         obj = os.path.join(obj_dir, u.replace(".hip", ".o"))
-        cmd = [HIPCC, *FLAGS, "-c", "-o", obj, os.path.join(CSRC, u)]
+        cmd = [HIPCC, *FLAGS, f'-DINET_SRC_HASH="{src}"', "-c", "-o", obj, os.path.join(CSRC, u)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)

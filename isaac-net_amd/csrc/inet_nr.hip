@@ -292,10 +292,15 @@ extern "C" {
 
 int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
 
+#ifndef INET_SRC_HASH
+#define INET_SRC_HASH "unknown"
+#endif
+// "<description>; src=<sha256 of the sources the library was built from>" (build.py passes the hash; the loader
+// refuses a library whose hash is not the tree's)
 const char* inet_nr_build_info(void) {
     return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, two-wave step (R <= 128), "
            "multi-cell step<C = 3, S in {8,13,14}, P, IR>, common-configuration step<13, 8>, DPP segment reductions, "
-           "ATen-order sums";
+           "ATen-order sums; src=" INET_SRC_HASH;
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,

@@ -603,10 +603,36 @@ __global__ __launch_bounds__(WAVE) void wifi_submit_kernel(InetWifiState st, Ine
         if (rob) ((int32_t*)accepted)[ir] = n_acc;
     }
     if (rob) st.qlen[ir] = qlen;
-    if (env_ok && r == 0 && n_calls > 0) {
+    // (the counts form's calls are global: wifi_submit_calls_kernel advances every env's call counter)
+    if (!counts && env_ok && r == 0 && n_calls > 0) {
         st.last_hid[ec] = hid_e;
         st.ctr_submit[ec] += n_calls;
     }
+}
+
+// The counts form stands for a sequence of global submit calls (class 1 first, one call per message index up to the
+// largest count of the class over every env): each call advances every env's SUBMIT call counter and sets its last
+// hazard id (0: no hid in this form), including envs with nothing to send. One workgroup: the per-class maxima over
+// all [E][R] counts (LDS atomics), then the counters.
+__global__ __launch_bounds__(1024) void wifi_submit_calls_kernel(InetWifiState st, int E, int R,
+                                                                 const uint8_t* __restrict__ counts, int n_cls) {
+    __shared__ int s_max[INET_WIFI_MAX_CLS];
+    if ((int)threadIdx.x < n_cls) s_max[threadIdx.x] = 0;
+    __syncthreads();
+    const size_t n = (size_t)E * R;
+    for (int c = 0; c < n_cls; ++c) {
+        int m = 0;
+        for (size_t i = threadIdx.x; i < n; i += blockDim.x) m = max(m, (int)counts[i * n_cls + c]);
+        if (m > 0) atomicMax(&s_max[c], m);
+    }
+    __syncthreads();
+    int tot = 0;
+    for (int c = 0; c < n_cls; ++c) tot += s_max[c];
+    if (tot > 0)
+        for (int e = threadIdx.x; e < E; e += blockDim.x) {
+            st.ctr_submit[e] += tot;
+            st.last_hid[e] = 0;
+        }
 }
 
 // ======================================================================================= reset kernel
@@ -716,6 +742,9 @@ int32_t inet_wifi_submit(const InetWifiState* st, const InetWifiParams* prm, con
     const int G = p.envs_per_wave;
     hipLaunchKernelGGL(wifi_submit_kernel, dim3((p.E + G - 1) / G), dim3(WAVE), 0, (hipStream_t)stream, *st, p, t,
                        send, det, hid, snr, counts, n_cls, accepted, rb);
+    if (counts)
+        hipLaunchKernelGGL(wifi_submit_calls_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, *st, p.E, p.R,
+                           counts, n_cls);
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 

@@ -149,6 +149,45 @@ def sum_last(x):
     return x.sum(-1)
 
 
+# ------------------------------------------------------------------------------------------ threshold decisions
+class Decisions:
+    """The oracle's float threshold decisions, recorded and overridable, for tests that prove float-threshold flips.
+
+    Every comparison of a float quantity against a threshold whose outcome is integer state (the scheduler's MCS
+    lookup, the link adaptation's BLER target, the decode draw, the PHR cap's floor, the 38.214 CQI thresholds, the
+    A3 condition) goes through cmp(site, a, b, op). While recording, each call keeps (site, call index, a, b) so that
+    a test can rank the decisions of an env by their distance from the threshold; `force` maps (site, call index) to
+    a bool mask XORed into that call's outcome, which replays a step with chosen decisions flipped. Call indices count
+    the calls of a site since begin(); the sites are called for every env in the same order every step, so an index
+    names the same decision in a replay of the same step."""
+
+    def __init__(self):
+        self.record = False
+        self.rec = None
+        self.force = {}
+        self.n = {}
+
+    def begin(self):
+        self.n = {}
+        self.rec = [] if self.record else None
+
+    def cmp(self, site, a, b, op="ge"):
+        a, b = torch.broadcast_tensors(torch.as_tensor(a), torch.as_tensor(b))
+        ok = a >= b if op == "ge" else a > b
+        k = self.n.get(site, 0)
+        self.n[site] = k + 1
+        if self.rec is not None:
+            self.rec.append((site, k, a.clone(), b.clone()))
+        f = self.force.get((site, k))
+        if f is not None:
+            ok = ok ^ f
+        return ok
+
+
+def _ge(a, b, op="ge"):
+    return a >= b if op == "ge" else a > b
+
+
 # ------------------------------------------------------------------------------------------ PHY on torch
 class Phy:
     """Torch views of isaac_net_amd.phy.PhyTables with the lookups of core/phy.py:263-363."""
@@ -205,8 +244,9 @@ class Phy:
         hi = f[base0 + self.G + j0] * (1 - wj) + f[base0 + self.G + j0 + 1] * wj
         return lo * (1 - wi) + hi * wi
 
-    def mcs_at(self, sinr_db):
-        ok = (sinr_db[..., None] >= self.thr_ref) & (torch.arange(self.M) <= self.mcs_max)
+    def mcs_at(self, sinr_db, dec=None, site="mcs"):
+        ge = (lambda a, b: dec.cmp(site, a, b)) if dec is not None else _ge
+        ok = ge(sinr_db[..., None], self.thr_ref) & (torch.arange(self.M) <= self.mcs_max)
         return (ok.long() * torch.arange(1, self.M + 1)).max(-1).values.clamp(min=1) - 1
 
     @staticmethod
@@ -243,14 +283,16 @@ class Phy:
         lse, lnw = self.eesm_lse(sinr_db, mask, mcs, w)
         return self.db(-self.beta[mcs.long()] * (lse - lnw))
 
-    def select_mcs(self, est_db, mask, offset_db, n_prb, nsym, dmrs, oh, mode, w):
+    def select_mcs(self, est_db, mask, offset_db, n_prb, nsym, dmrs, oh, mode, w, dec=None):
         """Highest MCS meeting the BLER target at the offset effective SINR (phy.py:339-350)."""
         eff = self.eff_sinr_all(est_db, mask, mode, w) + offset_db[..., None]
         tbs = self.tbs_all(n_prb, nsym, dmrs, oh)
         cbs, c = self.segment(tbs, self.r)
         m_all = torch.arange(self.M).expand_as(tbs)
         tbler = 1 - (1 - self.bler_lookup(m_all, eff, cbs.float())) ** c.float()
-        ok = (tbler <= self.target) & (tbs > 0) & (m_all <= self.mcs_max)
+        pass_ = dec.cmp("la", torch.tensor(self.target, dtype=tbler.dtype), tbler) if dec is not None else \
+            tbler <= self.target
+        ok = pass_ & (tbs > 0) & (m_all <= self.mcs_max)
         m = (ok.long() * torch.arange(1, self.M + 1)).max(-1).values.clamp(min=1) - 1
         return m, tbs.gather(-1, m[..., None]).squeeze(-1)
 
@@ -545,15 +587,16 @@ class Association:
         self.serv = torch.where(self.pending[:, None], rx.argmax(-1), self.serv)
         self.pending = torch.zeros_like(self.pending)
 
-    def plan(self, rx):
+    def plan(self, rx, dec=None):
         """(fire slot inside this control step [E,R] or -1, target cell [E,R]); at slot k the condition has held
         cnt + k + 1 slots, so it fires at k = ttt - cnt - 1."""
         cfg = self.cfg
         rs = pick(rx, self.serv)
         best, bc = rx.masked_fill(onehot(self.serv, self.C), -float("inf")).max(-1)
-        cond = best > rs + cfg.a3_offset_db + cfg.a3_hyst_db
+        cmp = dec.cmp if dec is not None else (lambda _site, a, b, op="ge": _ge(a, b, op))
+        cond = cmp("a3", best, rs + cfg.a3_offset_db + cfg.a3_hyst_db, "gt")
         if self.floor_rx is not None:
-            cond = cond & (best >= self.floor_rx)
+            cond = cond & cmp("a3_floor", best, torch.tensor(self.floor_rx, dtype=best.dtype))
         cnt = torch.where(cond & (bc == self.a3_cand), self.a3_cnt, torch.zeros_like(self.a3_cnt))
         k_fire = (self.ttt - cnt - 1).clamp(min=0)
         fire = cond & (k_fire < self.K)
@@ -595,6 +638,7 @@ class OracleEngine:
         self.w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
         self.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
         self.rng = CounterRNG(seed, E)
+        self.dec = Decisions()
         self.rician = cfg.rician_mode
         self.radio = None
         self.T = 0
@@ -758,6 +802,7 @@ class OracleEngine:
     def step(self, t=None, x=None, snr_db=None, dl_snr_db=None):
         cfg = self.cfg
         T = self.T
+        self.dec.begin()
         hid = self.last_hid
         dl_ref = None
         if self.C > 1:                                   # engine.py:918-924 with NRNet.step_cells
@@ -838,7 +883,7 @@ class OracleEngine:
         rx = pg + cfg.ue_tx_dbm
         asc = self.assoc
         asc.associate(rx)
-        k_ho, tgt = asc.plan(rx)
+        k_ho, tgt = asc.plan(rx, self.dec)
         g_ho = g0 + k_ho
         fired = torch.zeros(self.E, self.R, dtype=torch.bool)
         if self.rician:
@@ -935,10 +980,10 @@ class OracleEngine:
         the gNB keeps that MCS's threshold SINR as its estimate until the next report."""
         lk = self.dl
         if self.cqi is None:
-            m = lk.phy.mcs_at(sinr_ref + gain_now)
+            m = lk.phy.mcs_at(sinr_ref + gain_now, self.dec, "cqi_mcs")
         else:
             thr, cqi_mcs = self.cqi
-            cqi = ((sinr_ref + gain_now)[..., None] >= thr).sum(-1)
+            cqi = self.dec.cmp("cqi", (sinr_ref + gain_now)[..., None], thr).sum(-1)
             m = cqi_mcs[cqi]
         lk.csi = lk.phy.thr_ref[m] - sinr_ref
 
@@ -992,7 +1037,16 @@ class OracleEngine:
             if cfg.phr_cap:
                 ref = sinr_ref.mean(-1) if self.phr_snr is None else self.phr_snr
                 n_max_prb = cfg.snr_ref_prbs * 10 ** ((ref - cfg.phr_min_db) / 10)
-                n_max = torch.floor(n_max_prb / w[0]).clamp(1, S).long()
+                x = n_max_prb / w[0]
+                fl = torch.floor(x)
+                # floor(x) inside the clamp range as two threshold decisions (x >= floor(x), x >= floor(x) + 1), so
+                # that a replay can move it; outside the range the floor does not matter (thresholds -inf / +inf)
+                in_rng = (fl >= 0) & (fl <= S)
+                inf = torch.full_like(fl, float("inf"))
+                up = self.dec.cmp("phr", x, torch.where(in_rng, fl, -inf)).to(fl.dtype)
+                up = up + self.dec.cmp("phr", x, torch.where(in_rng, fl + 1, inf)).to(fl.dtype)
+                fl = torch.where(in_rng, fl - 1 + up, fl)
+                n_max = fl.clamp(1, S).long()
             else:
                 n_max = torch.full((E, R), S, dtype=torch.long)
         else:                                            # DlMac._sched_estimate (mac_dl.py:42-43)
@@ -1000,7 +1054,7 @@ class OracleEngine:
             n_max = torch.full((E, R), S, dtype=torch.long)
         est_o = est + (L.olla[..., None] if cfg.olla else 0.0)
         re_prb = float(min(12 * nsym - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156))
-        rate_sb = phy.se[phy.mcs_at(est_o)] * re_prb * w / 8
+        rate_sb = phy.se[phy.mcs_at(est_o, self.dec)] * re_prb * w / 8
         if cfg.scheduler == "maxci":
             metric_sb = rate_sb
         elif cfg.scheduler == "rr":
@@ -1077,7 +1131,7 @@ class OracleEngine:
         est_tx = sinr_ref - self._split(n_prb)[..., None] + L.csi if ul else est
         off = L.olla if cfg.olla else torch.zeros_like(L.olla)
         mcs_new, tbs_new = phy.select_mcs(est_tx, won, off, n_prb, nsym, cfg.dmrs_re_per_prb,
-                                          cfg.overhead_re_per_prb, cfg.eff_sinr, w)
+                                          cfg.overhead_re_per_prb, cfg.eff_sinr, w, self.dec)
         cap_b = (tbs_new // 8 - cfg.tb_overhead_bytes).clamp(min=1)
         byt_new = torch.minimum(cap_b, unsent)
         # bind TBs to processes (mac.py:407-426)
@@ -1119,7 +1173,7 @@ class OracleEngine:
             eff_used = 10 * torch.log10(comb.clamp(min=1e-9))
         p_err = phy.tb_error_prob(mcs, eff_used, tbs, mcs_eq)
         u = self.rng.step_uniform(BLER_UL if ul else BLER_DL, rel, R)
-        ok = tx & (u >= p_err)
+        ok = tx & self.dec.cmp("dec", u, p_err)
         fail = tx & ~ok
         exh = fail & (ntx >= cfg.max_harq_tx)
         # HARQ update (mac.py:456-477; UL timing mac_ul.py:218-219, DL mac_dl.py:47-49)

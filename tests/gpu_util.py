@@ -7,14 +7,15 @@ import torch
 from conftest import GOLDEN
 from oracle import replay
 
-# float state: csi / h / spec carry transcendental rounding (1e-5 relative, 1 dB / unit floor); h_comb / lexp are the
-# EESM log-sum over subbands, ill-conditioned at low SINR (difference of two nearly equal logs), 1e-3 relative; the
-# OLLA offset and PF average are pure arithmetic on the decisions and must be bitwise equal.
-FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1e-5, "ul.h_comb": 1e-3,
-             "ul.h_lexp": 1e-3, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0, "net.k_los": 0.0,
+# float state: csi / h / spec carry transcendental rounding (1e-5 relative, 1 dB / unit floor); h_comb (chase
+# combining: the sum over a process's transmissions of the linear EESM SINR v = -beta (lse - lnw)) and h_lexp (the IR
+# log-sum) 1e-5 relative, h_comb with the derived bound comb_bound below plus, with poses, the radio's rounding of the
+# reference SINR; the OLLA offset and PF average are pure arithmetic on the decisions and must be bitwise equal.
+FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1e-5, "ul.h_comb": 1e-5,
+             "ul.h_lexp": 1e-5, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0, "net.k_los": 0.0,
              "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0,
              # the DL link: its CSI is an MCS threshold minus the reference SINR (exact once the reported MCS agrees)
-             "dl.csi": 1e-5, "dl.h_comb": 1e-3, "dl.h_lexp": 1e-3, "dl.h_nrb": 0.0, "dl.olla": 0.0, "dl.avg": 0.0,
+             "dl.csi": 1e-5, "dl.h_comb": 1e-5, "dl.h_lexp": 1e-5, "dl.h_nrb": 0.0, "dl.olla": 0.0, "dl.avg": 0.0,
              "dl.q.fin": 0.0,
              # several cells: each gNB's N+I estimate and its I/N statistic. The interference terms are
              # 10^(x / 10) of dB sums x = psd + gain around -100 dB, where one float32 ulp of x (7.6e-6 dB) is
@@ -26,6 +27,22 @@ OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
 ABS_FLOOR = {"sinr_db": 6.1e-5, "eng._last_snr": 6.1e-5}
 MAX_DEV = {}
 BOUND = {}     # key -> per-element absolute bound (numpy) for the current comparison, from oracle.tolerance
+
+
+def _beta_max():
+    from isaac_net_amd.phy import PhyTables
+    return max(float(PhyTables(t, 0.1, 2, 27).beta.max()) for t in (1, 2))
+
+
+BETA_MAX = _beta_max()
+
+
+def comb_bound(ntx):
+    """Absolute bound on a chase-combining sum of ntx EESM terms beyond its 1e-5 relative part: each term is
+    -beta (lse - lnw), the difference of two log-sum-exps over the held RBGs whose magnitudes at low SINR are below
+    8 (log of at most 273 PRBs, plus x / beta terms near 0), each within 8 float32 ulps (2^-21 each below 8) of the
+    CPU's, so a term is off by at most beta 16 2^-21 while its own value may be near 0."""
+    return np.maximum(np.asarray(ntx, dtype=np.float64), 1.0) * BETA_MAX * 16 * 2.0 ** -21
 
 
 def close(m, r, tol, floor=0.0, key=None):
@@ -67,6 +84,14 @@ def compare(ref, s, out, sd, E, R):
             v_ = valid[k[:2]]
             vv = v_ if m.shape == v_.shape else v_[..., None]
             m, r = np.where(vv, m, 0), np.where(vv, r, 0)
+        if k.endswith(".h_comb") and pre + k[:-6] + "h_ntx" in ref:
+            b = comb_bound(ref[pre + k[:-6] + "h_ntx"])
+            if "out.sinr_db" in BOUND:
+                # with poses the reference SINR of every term carries the radio's rounding (the sinr_db bound, dB):
+                # ln(10) / 10 of it relative on the linear sum
+                b = b + np.abs(np.asarray(r, dtype=np.float64)) * (np.log(10.0) / 10.0) * \
+                    np.asarray(BOUND["out.sinr_db"], dtype=np.float64)[..., None]
+            BOUND[k] = b
         ok = close(m, r, FLOAT_TOL[k], ABS_FLOOR.get(k, 0.0), k) if k in FLOAT_TOL else (m == r)
         if not ok.all():
             (bad_f if k in FLOAT_TOL else bad_i)[k] = int((~ok).sum())
@@ -138,3 +163,16 @@ def teacher_forced(P, name, dev="cuda:0"):
         for k, v in bf.items():
             keys_f[k] = keys_f.get(k, 0) + v
     return n_bad, E * R * T, keys_i, keys_f
+
+
+def head(sd, n):
+    """The first n envs of a state dict of device tensors, on the CPU (free-running prefix comparisons)."""
+    return {k: v[:n].cpu() for k, v in sd.items() if torch.is_tensor(v) and v.dim() >= 1 and v.shape[0] >= n}
+
+
+def submit_oracle(ora, c):
+    """The oracle's submit calls of per-class counts c [E,R,NC]: class 1 first, one call per message index."""
+    c = np.asarray(c)
+    for ci in range(c.shape[-1]):
+        for i in range(int(c[..., ci].max(initial=0))):
+            ora.submit(None, torch.from_numpy(np.where(c[..., ci] > i, ci + 1, 0).astype(np.int64)))

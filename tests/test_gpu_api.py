@@ -6,6 +6,7 @@ import pytest
 import torch
 
 import isaac_net_amd as P
+from gpu_util import head
 from oracle import nr_oracle as O
 from oracle.tolerance import FlipCounter, engine_radio, sinr_bound
 
@@ -125,7 +126,7 @@ def test_matches_oracle_with_submit_counts():
     E, R = 3, 8
     eng = P.make_engine("L2", E, R, DEV, cfg, seed=11)
     ora = O.OracleEngine(E, R, cfg, seed=11)
-    fc = FlipCounter(E)
+    fc = FlipCounter(E, ora)
     rs = np.random.default_rng(1)
     for s in range(10):
         counts = np.stack([rs.poisson(0.8, (E, R)), rs.poisson(0.3, (E, R))], -1).astype(np.uint8)
@@ -137,12 +138,14 @@ def test_matches_oracle_with_submit_counts():
                 n_acc += ora.submit(None, send).numpy()
         assert np.array_equal(acc.cpu().numpy(), n_acc)
         x = torch.from_numpy(rs.uniform(0, 100, (E, R, 2)).astype(np.float32))
-        og, oo = eng.step(None, x.to(DEV)), ora.step(None, x)
+        og = eng.step(None, x.to(DEV))
+        fc.before()
+        oo = ora.step(None, x)
         fi, sig, amp = engine_radio(eng)
         tol = sinr_bound(x.numpy(), eng.st["field"][:, 0, fi].cpu().numpy(), sig, amp, oo["sinr_db"].numpy())
-        fc.step(s, og, oo, tol)
-    print(f"integer flips {fc.flips}; float issues {fc.float_bad}", flush=True)
-    assert len(fc.flips) <= 1 and not fc.float_bad
+        fc.step(s, og, oo, tol, head(eng.owner_state(), E), lambda o, x=x: o.step(None, x))
+    print(fc.report(), flush=True)
+    assert fc.ok(E * R * 10), fc.report()
 
 
 @pytest.mark.parametrize("variant", ["plain", "pdcp_overhead_small_fifo"])

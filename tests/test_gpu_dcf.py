@@ -165,3 +165,61 @@ def test_dcf_refusals():
         P.make_engine("WIFI_DCF", 2, 4, DEV, P.NRConfig(wifi=WifiConfig(bg_stations=3)))
     with pytest.raises(P.HipUnsupported):
         P.make_engine("WIFI_DCF", 2, 4, DEV, P.NRConfig(wifi=WifiConfig(class_ac=("VO", "BE"))))
+
+
+def test_config4_workload_prefix_vs_oracle():
+    """The benchmarked WIFI_DCF workload itself (wifi_dcf_slots: 2048 envs x 16 stations at one AP, access category
+    DCF, 802.11ax 20 MHz, stations in a 50 m disc on a 1 m/s random walk, 1500 B at Poisson 0.4, FIFO 16, 20 ms
+    steps) for 60 control steps: its first 64 envs bit for bit against the oracle at every step (outputs and state,
+    SNR from poses within its float32 bound), and over all 2048 envs the counter invariants: each backoff counter
+    inside its retry stage's window, stages below the retry limit, queue lengths in [0, F]."""
+    from isaac_net_amd import scenarios as B
+    E, R, steps, E_chk = 2048, 16, 60, 64
+    print(f"wifi_dcf_slots {E}x{R}, {steps} steps, oracle on {E_chk} envs", flush=True)
+    wl = B.Workload(E, R, steps, seed=0, name="wifi_dcf_slots")
+    cfg = wl.cfg
+    eng = P.make_engine("WIFI_DCF", E, R, DEV, cfg, seed=0)
+    orc = DcfOracle(E_chk, R, cfg, seed=0)
+    p = eng._cdparams
+    max_tx = eng.wc.max_tx
+    F = cfg.frame_buffer
+
+    def head(v):
+        if not torch.is_tensor(v) or v.dim() == 0:
+            return v
+        if v.dim() >= 2 and v.shape[0] == 1 and v.shape[1] == E:          # radio fields [1, E, K, ...]
+            return v[:, :E_chk]
+        return v[:E_chk] if v.shape[0] == E else v
+
+    class _Prefix:                                     # the engine's outputs and state of the first E_chk envs
+        def __init__(self, e):
+            self.e = e
+
+        def state_dict(self):
+            return {k: head(v) for k, v in self.e.state_dict().items()}
+
+    n_del = n_att = 0
+    for s in range(steps):
+        c = wl.counts[s]
+        eng.submit_counts(c.to(DEV))
+        cn = c[:E_chk].numpy()
+        for ci in range(cn.shape[-1]):                 # the calls of the counts form are global: up to the largest
+            for i in range(int(c[..., ci].max())):     # count over every env
+                orc.submit(None, torch.from_numpy(np.where(cn[..., ci] > i, ci + 1, 0).astype(np.int64)))
+        x = wl.poses[s]
+        og = eng.step(None, x.to(DEV))
+        oo = orc.step(None, x[:E_chk])
+        bad = compare_all({k: head(v) for k, v in og.items()}, _Prefix(eng), oo, orc)
+        assert not bad, (s, bad)
+        b, st = eng.dst["b"].long(), eng.dst["stage"].long()
+        win = torch.clamp(p.W0 * torch.pow(2, st), max=p.Wmax)
+        assert bool((b >= 0).all()) and bool((b <= win - 1).all()), s
+        assert bool((st >= 0).all()) and bool((st < max_tx).all()), s
+        ql = og["queue_len"]
+        assert int(ql.min()) >= 0 and int(ql.max()) <= F, s
+        n_del += int(og["delivered"].sum())
+    n_att = int(orc.tot["att"].sum())
+    print(f"config 4: {n_del} deliveries over {E} envs, {n_att} attempts and {int(orc.tot['fail'].sum())} failures "
+          f"in the first {E_chk}; max |deviation| { {k: f'{v:.2e}' for k, v in MAX_DEV.items()} }", flush=True)
+    MAX_DEV.clear()
+    assert n_del > 0 and n_att > 0
