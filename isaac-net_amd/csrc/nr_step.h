@@ -134,45 +134,42 @@ DEV int aten_unrot(int b) {
     if constexpr (S > 8) return b < S - 8 ? b + 8 : b - (S - 8);
     else return b;
 }
-// torch.logsumexp over a row that is -inf outside the held RBGs, visiting the held RBGs in ATen order: the max is
-// taken over the held RBGs (the others are -inf) and exp(-inf - max) = 0 is skipped.
+// torch.logsumexp over a row that is -inf outside the held RBGs (won), as a dense sum over every RBG: the max over the
+// held RBGs, then the sum of exp(x_s - max) in ATen order with the RBGs not held adding exact zeros, which gives the
+// bits of a sum over the held RBGs only. The loops are unrolled, so the S reads of the row issue together.
+// xs(s): the row's value at RBG s (evaluated for every s, used where held).
+template <int S, class X>
+DEV float lse_held(X xs, uint32_t won) {
+    float x[S];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        x[s] = xs(s);
+        const float v = ((won >> s) & 1u) ? x[s] : -INFINITY;
+        mx = v > mx ? v : mx;
+    }
+    if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
+    float sum = 0.f;
+    // (sum >= 1 when some RBG is held: the max term is exp(0); every term is exp of a finite x <= 0; none held: the
+    // log of 0)
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const int s = aten_unrot<S>(i);
+        sum += ((won >> s) & 1u) ? exp_nonpos(x[s] - mx) : 0.0f;
+    }
+    return (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
+}
 // lse_logw: the row log w_s (the log of the held PRB count, as torch computes it).
 template <int S>
 DEV float lse_logw(const float* s_logw, uint32_t won) {
-    uint32_t rot = aten_rot<S>(won);
-    float mx = -INFINITY;
-    for (uint32_t m = rot; m; m &= m - 1) {
-        float x = s_logw[aten_unrot<S>(__builtin_ctz(m))];
-        mx = x > mx ? x : mx;
-    }
-    if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
-    float sum = 0.f;
-    // (sum >= 1 when some RBG is held: the max term is exp(0); every term is exp of a finite x <= 0; none held: the
-    // log of 0)
-    for (uint32_t m = rot; m; m &= m - 1) sum += exp_nonpos(s_logw[aten_unrot<S>(__builtin_ctz(m))] - mx);
-    return (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
+    return lse_held<S>([&](int s) { return s_logw[s]; }, won);
 }
-// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of the robot whose linear SINR row is column `col` of s_lin
-// (s_lin[s * CW + col], CW lanes per workgroup); x_s is kept in column `tmp` of s_tmp between the max and the sum.
-// rbeta = RN(1 / beta): the division is div_const, exact for every beta of the MCS tables. `nan` says that some lin_s
-// of the full row (held or not) is NaN, which makes torch's result NaN.
-template <int S, int CW = STEP_WAVE>
-DEV float lse_eesm(const float* s_lin, int col, float* s_tmp, int tmp, const float* s_logw, uint32_t won, float beta,
-                   float rbeta, bool nan) {
-    uint32_t rot = aten_rot<S>(won);
-    float mx = -INFINITY;
-    for (uint32_t m = rot; m; m &= m - 1) {
-        int s = aten_unrot<S>(__builtin_ctz(m));
-        float x = div_const(-s_lin[s * CW + col], beta, rbeta) + s_logw[s];
-        s_tmp[s * CW + tmp] = x;
-        mx = x > mx ? x : mx;
-    }
-    if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
-    float sum = 0.f;
-    // (sum >= 1 when some RBG is held: the max term is exp(0); every term is exp of a finite x <= 0; none held: the
-    // log of 0)
-    for (uint32_t m = rot; m; m &= m - 1) sum += exp_nonpos(s_tmp[aten_unrot<S>(__builtin_ctz(m)) * CW + tmp] - mx);
-    float r = (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
+// lse_eesm: the EESM row x_s = (-lin_s) / beta + log w_s of a robot whose linear SINR at RBG s is lin(s). rbeta =
+// RN(1 / beta): the division is div_const, exact for every beta of the MCS tables. `nan` says that some lin_s of the
+// full row (held or not) is NaN, which makes torch's result NaN.
+template <int S, class L>
+DEV float lse_eesm(L lin, const float* s_logw, uint32_t won, float beta, float rbeta, bool nan) {
+    const float r = lse_held<S>([&](int s) { return div_const(-lin(s), beta, rbeta) + s_logw[s]; }, won);
     return nan ? NAN : r;
 }
 // PRB-weighted mean of the per-RBG dB values x_s (s_x[s * CW + lane]) over the held RBGs (mean_db): the ATen-order
@@ -347,14 +344,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
 
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
-    // "the highest m <= mcs_max with x >= thr[m]" is the highest m with x >= min(thr[m..mcs_max]): these suffix
-    // minima are non-decreasing, so a binary search over them gives the linear scan's result for any table. Past
-    // mcs_max the entries are NaN, which no comparison passes (not even x = +inf).
-    if (lane < MAX_M) {
-        float v = INFINITY;
-        for (int j = tb.mcs_max; j >= lane; --j) v = fminf(v, tb.thr_ref[j]);
-        s_thrs[lane] = lane <= tb.mcs_max ? v : __builtin_nanf("");
-    }
     if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
     if (lane < tb.M) {
         s_beta[lane] = tb.beta[lane];
@@ -367,10 +356,28 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     if constexpr (IR)
         for (int i = lane; i < tb.M * tb.EQW; i += CW) s_eq[i] = tb.mcs_eq[i];
     for (int i = lane; i < envs_pw * 3 * HB; i += CW) hist_l[i] = 0;
-    if (lane == 0) {
-        int j = 0;
-        for (int k = 0; k < n_rows && j < MAX_UL_ROWS; ++k)
-            if (rows[k].flags & 2) s_ulrel[j++] = rows[k].rel;
+    // the step's rows, one per lane of each wavefront (n_rows <= 64), loaded together: the UL data rows' slots
+    // in order (a ballot prefix), the last UL row, the last row whose fading state is kept, and whether every
+    // evolving row is i.i.d. (rho = 0)
+    unsigned long long m_ul, m_h, m_corr;
+    {
+        const bool have = wl < n_rows;                 // (each wavefront of the workgroup reads the rows)
+        const int fl = have ? rows[wl].flags : 0;
+        const int rel_l = have ? rows[wl].rel : 0;
+        const float rho_l = have ? rows[wl].rho : 0.0f;
+        m_ul = __ballot((fl & 2) != 0);
+        m_h = __ballot((fl & 4) != 0 && (fl & 8) != 0);
+        m_corr = __ballot((fl & 4) != 0 && rho_l != 0.0f);
+        if (wbase == 0 && (fl & 2)) s_ulrel[__builtin_popcountll(m_ul & ((1ull << wl) - 1ull))] = rel_l;
+    }
+    __syncthreads();
+    // "the highest m <= mcs_max with x >= thr[m]" is the highest m with x >= min(thr[m..mcs_max]): these suffix
+    // minima are non-decreasing, so a binary search over them gives the linear scan's result for any table. Past
+    // mcs_max the entries are NaN, which no comparison passes (not even x = +inf).
+    if (lane < MAX_M) {
+        float v = INFINITY;
+        for (int j = tb.mcs_max; j >= lane; --j) v = fminf(v, s_thr[j]);
+        s_thrs[lane] = lane <= tb.mcs_max ? v : __builtin_nanf("");
     }
     __syncthreads();
 
@@ -631,14 +638,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     // latest draw, so a robot with nothing to send and no HARQ process pending (it takes part in no decision for the
     // rest of the step) skips the draws until the last row that fixes the stored state (the last UL slot for the CSI,
     // the last row needing the state for h)
-    int last_ul_row = -1, last_h_row = -1;
-    bool iid = true;
-    for (int k = 0; k < n_rows; ++k) {
-        const int fl = rows[k].flags;
-        if (fl & 2) last_ul_row = k;
-        if ((fl & 4) && (fl & 8)) last_h_row = k;
-        if ((fl & 4) && rows[k].rho != 0.0f) iid = false;
-    }
+    const int last_ul_row = m_ul ? 63 - __builtin_clzll(m_ul) : -1;
+    const int last_h_row = m_h ? 63 - __builtin_clzll(m_h) : -1;
+    const bool iid = m_corr == 0ull;
     // ================================================================ slot loop
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
@@ -1015,15 +1017,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         if (any_new) {
             // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on the held RBGs
             bool nan = false;
+            const uint32_t held = tx_new ? won : 0u;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
+                const float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
                 nan |= x != x;
-                s_x[s * CW + lane] = x;
-            }
-            for (uint32_t mm = tx_new ? won : 0u; mm; mm &= mm - 1) {
-                int s = __builtin_ctz(mm);
-                s_lin[s * CW + lane] = from_db_mid(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
+                if (!pm.eesm) s_x[s * CW + lane] = x;                    // (the mean-dB row)
+                if ((held >> s) & 1u) s_lin[s * CW + lane] = from_db_mid(clampf(x, -30.0f, 60.0f));
             }
             const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw) : 0.f;
             const int np = (int)n_prb;
@@ -1066,8 +1066,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                     if (pm.eesm) {
                         const uint32_t wr = (uint32_t)s_la_i[CW + rl];
                         const float beta = s_beta[m];
-                        eff = db_of((-beta) * (lse_eesm<S, CW>(s_lin, rl, s_x, lane, s_logw, wr & 0x7fffffffu, beta,
-                                                               s_rbeta[m], (wr >> 31) != 0u) - s_la_f[rl]));
+                        eff = db_of((-beta) * (lse_eesm<S>([&](int s) { return s_lin[s * CW + rl]; }, s_logw,
+                                                           wr & 0x7fffffffu, beta, s_rbeta[m], (wr >> 31) != 0u) -
+                                               s_la_f[rl]));
                     } else {
                         eff = s_la_f[2 * CW + rl];
                     }
@@ -1160,6 +1161,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         if (__ballot(tx) != 0ull) {
             const float beta = s_beta[mcs], rbeta = s_rbeta[mcs];
             bool nan = false;
+            float xs[S];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 float x;                          // UL: ref - split + gain (mac_ul.py:185-192); DL: ref + gain
@@ -1168,16 +1170,15 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 if constexpr (MC)                 // minus the measured N+I over the estimate (nr_engine.py:815)
                     if (cl.use_int) x = x - ((10.0f * log10f(cl.noise_mw + s_if[serv * S + s])) - ni_la[s]);
                 nan |= x != x;
-                s_x[s * CW + lane] = x;
+                xs[s] = x;
+                if (!pm.eesm) s_x[s * CW + lane] = x;                    // (the mean-dB row)
             }
-            for (uint32_t mm = tx ? won : 0u; mm; mm &= mm - 1) {
-                int s = __builtin_ctz(mm);
-                s_lin[s * CW + lane] = from_db_mid(clampf(s_x[s * CW + lane], -30.0f, 60.0f));
-            }
+            // the linear SINR of RBG s (used where held)
+            auto lin_of = [&](int s) { return from_db_mid(clampf(xs[s], -30.0f, 60.0f)); };
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S, CW>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan);
+                float lse = lse_eesm<S>(lin_of, s_logw, won, beta, rbeta, nan);
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -1190,7 +1191,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S, CW>(s_lin, lane, s_x, lane, s_logw, won, beta, rbeta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_eesm<S>(lin_of, s_logw, won, beta, rbeta, nan) - lnw));
                 } else {
                     eff = mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw);
                 }
