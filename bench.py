@@ -5,6 +5,7 @@
     python bench.py --workload wifi_dcf_slots [--envs-per-wave G]  (level WIFI_DCF: station-steps/s)
     python bench.py --workload mc_interf     (three cells with UL interference, 1024 envs x 64 robots: robot-slots/s)
     python bench.py --workload freq_sel      (16384 envs x 128 robots, 273 PRB in 8 RBGs, K = 20: robot-slots/s)
+    python bench.py --summarize-counters DIR KERNEL NAME   (rocprofv3 --pmc CSVs under DIR -> profiles/NAME.json)
 
 A step is one control step of every env: this step's message arrivals and step (poses in, the reference's output dict
 out), one launch of the fused step kernel that enqueues the arrivals first (--separate-submit: submit_counts and step,
@@ -12,9 +13,11 @@ two launches; --graph: both replayed from HIP graphs recorded after the warm-up)
 step) are generated before the timed region and are resident in HBM. The timed region is K steps bracketed by
 torch.cuda.synchronize(); value = E * R * K_ul * K / seconds (robot-slots/s, K_ul = 10 UL slots per step).
 The step kernel's average duration is measured live with HIP events recorded around each launch on the launch
-stream (the engine's kernel_events hook); roofline.achieved is the
-kernel's algorithmic HBM bytes per launch (from the state layout and the measured queue occupancy) over that
-duration. The CPU baseline times the oracle (a torch-CPU restatement of the reference path) on the first envs of the
+stream (the engine's kernel_events hook); roofline.achieved is the kernel's algorithmic HBM bytes per launch (the
+canonical compact layout's bytes per robot-step times the robots: 2,362 B at the RL-scale shape) over that duration.
+The bytes of this engine's own layout (reference output dtypes, the whole FIFO) and the bytes touched at the measured
+queue occupancy are reported beside it; roofline.traffic (rocprofv3 FETCH_SIZE + WRITE_SIZE) and valu_issue_util
+(SQ_INSTS_VALU) come from the counter summary under profiles/ recorded on the loaded library's sources, else null. The CPU baseline times the oracle (a torch-CPU restatement of the reference path) on the first envs of the
 same workload.
 """
 from __future__ import annotations
@@ -41,6 +44,27 @@ def load_package():
     sys.modules["isaac_net_amd"] = mod
     spec.loader.exec_module(mod)
     return mod
+
+
+def survey_bytes_per_robot_step(eng):
+    """The algorithmic bytes of one robot-step in the canonical compact layout (the survey's measurement section):
+    2 B_rw + B_ro + B_in + B_out with B_rw = 12 S + 32 + 32 P + 18 F (fading and CSI, MAC scalars, HARQ processes,
+    frame FIFO, read and written once), B_ro = 8 (Rician phasor), B_in = 10 (pose and arrivals) and B_out = 9 F + 16.
+    2,362 B at S = 13, P = 8, F = 32."""
+    S, P, F = eng.S, eng.P, eng.F
+    return 2 * (12 * S + 32 + 32 * P + 18 * F) + 8 + 10 + 9 * F + 16
+
+
+def counter_summary(name):
+    """The rocprofv3 counter summary profiles/<name>.json if it was recorded on this library's sources (its "src"
+    equals the hash the loaded library was built from), else None."""
+    from isaac_net_amd import _lib
+    path = os.path.join(ROOT, "profiles", name + ".json")
+    if not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    built = _lib.load().inet_nr_build_info().decode().rsplit("src=", 1)[-1]
+    return d if d.get("src") == built else None
 
 
 def step_kernel_bytes(eng):
@@ -423,7 +447,9 @@ def run_freq_sel(args, P, torch):
     eng.kernel_events = None
     k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
-    nbytes, per_robot = step_kernel_bytes(eng)
+    layout_bytes, layout_per_robot = step_kernel_bytes(eng)
+    per_robot = survey_bytes_per_robot_step(eng)
+    nbytes = E * R * per_robot
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     res = {"metric": f"robot-slots/sec @{E} envs×{R} robots K={k_ul}, 273 PRB in 8 RBGs",
            "value": E * R * k_ul * args.steps / dt, "unit": "robot-slots/s", "n_gpus": 1, "steps": args.steps,
@@ -440,7 +466,8 @@ def run_freq_sel(args, P, torch):
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                         "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "nr_step_kernel<two waves>",
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
-                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot}}
+                        "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
+                        "layout_bytes_per_launch": layout_bytes, "layout_bytes_per_robot_step": layout_per_robot}}
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
@@ -448,7 +475,58 @@ def run_freq_sel(args, P, torch):
     print(json.dumps(res), flush=True)
 
 
+def summarize_counters(d, kernel, name):
+    """Read the rocprofv3 --pmc CSV outputs under d (passes FETCH_SIZE, WRITE_SIZE and the SQ_* counters of bench runs
+    made with --copy-mib), scale the byte counters by what they read for the copy kernel of known size, and write
+    profiles/<name>.json tagged with the loaded library's source hash. Prints the summary."""
+    import csv
+    import glob
+    from isaac_net_amd import _lib
+    rows = []
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+
+    def per_dispatch(counter, match):
+        vals = {}
+        for r in rows:
+            if r["Counter_Name"] == counter and match(r["Kernel_Name"]):
+                vals[r.get("Dispatch_Id", len(vals))] = vals.get(r.get("Dispatch_Id", len(vals)), 0.0) + \
+                    float(r["Counter_Value"])
+        return [vals[k] for k in sorted(vals, key=lambda x: int(x))]
+    copy = lambda k: "copyBuffer" in k  # noqa: E731
+    mine = lambda k: kernel in k  # noqa: E731
+    res = {"kernel": kernel, "workload": name, "src": _lib.load().inet_nr_build_info().decode().rsplit("src=", 1)[-1]}
+    # the calibration copies: the three largest copy dispatches (the run's input copies are small)
+    cf, cw = sorted(per_dispatch("FETCH_SIZE", copy))[-3:], sorted(per_dispatch("WRITE_SIZE", copy))[-3:]
+    kf, kw = per_dispatch("FETCH_SIZE", mine)[2:], per_dispatch("WRITE_SIZE", mine)[2:]      # steady state
+    copy_kib = None
+    for a in sys.argv:
+        if a.startswith("--copy-mib="):
+            copy_kib = int(a.split("=")[1]) * 1024
+    copy_kib = copy_kib or 256 * 1024
+    if cf and kf:
+        fs = copy_kib / (sum(cf) / len(cf))
+        ws = copy_kib / (sum(cw) / len(cw))
+        res.update({"fetch_scale": fs, "write_scale": ws, "fetch_kib_per_dispatch": sum(kf) / len(kf),
+                    "write_kib_per_dispatch": sum(kw) / len(kw)})
+        res["fetch_bytes"] = res["fetch_kib_per_dispatch"] * fs * 1024
+        res["write_bytes"] = res["write_kib_per_dispatch"] * ws * 1024
+        res["bytes_per_launch"] = res["fetch_bytes"] + res["write_bytes"]
+    for c in ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR",
+              "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES"):
+        v = per_dispatch(c, mine)[2:]
+        if v:
+            res[c.lower() + "_per_dispatch"] = sum(v) / len(v)
+    if "sq_insts_valu_per_dispatch" in res:
+        res["valu_insts_per_dispatch"] = res["sq_insts_valu_per_dispatch"]
+    json.dump(res, open(os.path.join(ROOT, "profiles", name + ".json"), "w"), indent=1)
+    print(json.dumps(res, indent=1))
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize-counters":
+        load_package()
+        return summarize_counters(sys.argv[2], sys.argv[3], sys.argv[4])
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -528,16 +606,19 @@ def main():
     k_avg = sum(k_ms) / len(k_ms)
     qlen_mean = sum(q_pre) / max(len(q_pre), 1)
     kept_mean = sum(q_post) / max(len(q_post), 1)
-    nbytes, per_robot = step_kernel_bytes(eng)
+    layout_bytes, layout_per_robot = step_kernel_bytes(eng)
     touched = step_kernel_touched_bytes(eng, qlen_mean, kept_mean)
+    per_robot = survey_bytes_per_robot_step(eng)
+    nbytes = E * R * per_robot
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     value = E * R * k_ul * args.steps / dt
-    traffic = None
     # HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a copy-kernel
-    # calibration) for this workload and output format; null when no such summary is committed
-    tp = os.path.join(ROOT, "profiles", f"step_kernel_traffic_{args.out_format}.json")
-    if os.path.exists(tp) and (E, R) == (4096, 32):
-        traffic = json.load(open(tp)).get("bytes_per_launch")
+    # calibration) and VALU instructions (SQ_INSTS_VALU) of this workload, from the counter summary recorded on the
+    # loaded library's sources; null when there is none
+    cs = counter_summary(f"nr_step_kernel_counters_rl_scale_{args.out_format}") if (E, R) == (4096, 32) else None
+    traffic = cs.get("bytes_per_launch") if cs else None
+    # VALU issue utilisation: a wave64 VALU instruction occupies a 16-lane SIMD for 4 cycles; 1024 SIMDs at 2.4 GHz
+    valu_util = (cs["valu_insts_per_dispatch"] * 4 / (1024 * k_avg * 1e-3 * 2.4e9)) if cs else None
     res = {"metric": METRIC, "value": value, "unit": "robot-slots/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": 1e3 * dt / args.steps, "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
@@ -554,7 +635,10 @@ def main():
                         "frac": achieved / PEAK_GBS, "traffic": traffic,
                         "kernel": "nr_step_kernel", "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
-                        "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean}}
+                        "layout_bytes_per_launch": layout_bytes, "layout_bytes_per_robot_step": layout_per_robot,
+                        "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean,
+                        "valu_issue_util": valu_util,
+                        "counters_src": cs.get("src") if cs else None}}
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
