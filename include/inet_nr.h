@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 4
+#define INET_NR_ABI_VERSION 5
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 128         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two
@@ -92,6 +92,11 @@ typedef struct InetNrState {
     /* the engine's control-step counter T on the device [1] int64: read by inet_nr_step / inet_nr_submit when
        they are called with T < 0 (a launch recorded once in a HIP graph and replayed at every step) */
     int64_t *clock;
+    /* per robot [E][R] int64: the byte-stream base of the link. The reference's stream offsets (sent, floor, enq,
+       h_lo, h_hi, q_start, q_end: int64 in queues.py:52-60, mac.py:67-81) are base + the int32 values above. When a
+       robot's floor reaches params.rebase_at at the end of a step, the step moves its offsets down by the floor and
+       adds it to base, so the int32 values stay below 2^31 for any run length. */
+    int64_t *base;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -127,6 +132,8 @@ typedef struct InetNrParams {
     int32_t n_data;                   /* data rows (flag 2) among the step's rows: sizes the kernel's per-slot LDS
                                          history (0: n_rows); must not be smaller than the actual count */
     int32_t n_cells;                  /* cells per env C (1: the single-cell engine; > 1: inet_nr_step_cells) */
+    int32_t rebase_at;                /* floor (bytes) from which a step rebases a robot's byte offsets (InetNrState.base;
+                                         2^30; 0: never) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -178,6 +185,7 @@ typedef struct InetNrDlState {
     int64_t *out_newest, *out_queue_len;        /* [E][R] step outputs dl_newest (env clock) and dl_queue_len */
     const float *cqi_thr;               /* [15] SINR from which CQI k + 1 is reported (cqi_table = "38214"), */
     const int32_t *cqi_mcs;             /* [16] MCS of each CQI; both NULL for cqi_table = "mcs" */
+    int64_t *base;                      /* [E][R] the DL byte-stream base, as InetNrState.base for the UL */
     int32_t gnb_proc;                   /* gNB processing slots after the HARQ-ACK */
     int32_t snr_offset;                 /* 1: SNR input plus snr_off (dl_snr_offset_db); 0: the DL SNR as given */
     float ref_off, noise_prb, snr_off;  /* pose input: dl_ref = (pg + ref_off) - noise_prb (gNB PSD, UE noise) */
@@ -264,7 +272,8 @@ int32_t inet_nr_dl_step(const InetNrState *st, const InetNrDlState *dl, const In
 
 /* Enqueue one DL frame per robot at control step T (T < 0: *st->clock): NRNet.add_dl_frames (nr_engine.py:489-497)
    with FrameQueue.add (queues.py:87-103). nbytes [E][R] float32 application bytes (0 = none), cls [E][R] int64 or
-   NULL (the slot then keeps the class it held, as the reference's meta field); accepted [E][R] uint8. */
+   NULL (the slot then keeps the class it held, as the reference's meta field); accepted [E][R] uint8. Frames of more
+   than 2^22 bytes (after the packet overhead) are refused, which keeps a full queue inside the int32 offsets. */
 int32_t inet_nr_dl_submit(const InetNrState *st, const InetNrDlState *dl, const InetNrParams *prm, int64_t T,
                           const float *nbytes, const int64_t *cls, int32_t discard_pdcp, int32_t pkt_payload,
                           int32_t pkt_overhead, uint8_t *accepted, void *stream);

@@ -92,7 +92,8 @@ __global__ void nr_dl_submit_kernel(InetNrState st, InetNrDlState dl, int E, int
         if (T - cap0 >= timeout) adm = false;
     }
     if (pkt_overhead) size = size + ceilf(size / (float)pkt_payload) * (float)pkt_overhead;
-    const bool acc = adm && qlen < F && size > 0.0f;
+    // (frames above 2^22 bytes are refused: F of them stay inside the int32 offsets between two rebases)
+    const bool acc = adm && qlen < F && size > 0.0f && size <= 4194304.0f;
     if (acc) {
         const int nb = (int)rintf(size);
         const size_t iq = ((size_t)e * F + qlen) * R + r;
@@ -116,6 +117,7 @@ __global__ void nr_dl_reset_kernel(InetNrDlState dl, InetNrParams pm, const uint
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
         size_t ir = (size_t)e * R + r;
         dl.sent[ir] = 0; dl.floor_[ir] = 0; dl.last_tx[ir] = -1; dl.olla[ir] = 0.f; dl.avg[ir] = 100.f;
+        if (dl.base) dl.base[ir] = 0;
         dl.enq[ir] = 0; dl.qlen[ir] = 0; dl.newest[ir] = -1;
         for (int s = 0; s < S; ++s) dl.csi[((size_t)e * S + s) * R + r] = 0.f;
         for (int p = 0; p < P; ++p) {
@@ -172,6 +174,7 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
         size_t ir = (size_t)e * R + r;
         st.sent[ir] = 0; st.floor_[ir] = 0; st.bsr[ir] = 0; st.sr_t[ir] = -1; st.last_tx[ir] = -1;
+        if (st.base) st.base[ir] = 0;
         st.olla[ir] = 0.f; st.avg[ir] = 100.f; st.enq[ir] = 0; st.qlen[ir] = 0;
         for (int s = 0; s < S; ++s) st.csi[((size_t)e * S + s) * R + r] = 0.f;
         for (int p = 0; p < P; ++p) {

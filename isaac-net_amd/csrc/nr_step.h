@@ -1442,6 +1442,29 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         bsr = bsr < un ? bsr : un;
     }
     const int ack_new = ack_ptr();
+    const int qb_end = enq - ack_new;                  // (queue_bytes: a difference of offsets)
+    // The byte offsets stay in int32: once the floor reaches rebase_at, every offset of the robot moves down by the
+    // floor and the robot's 64-bit base takes it (the reference's int64 offsets are base + offset). The queued frames
+    // and the live HARQ processes lie at or within a TB of the floor; a free process's stale range is never read
+    // again and is kept at most 2^30 below the floor.
+    bool rebased = false;
+    if (lk.base != nullptr && pm.rebase_at > 0 && act && floor_ >= pm.rebase_at) {
+        const int b = floor_;
+        rebased = true;
+        sent -= b; enq -= b; floor_ = 0;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int64_t lo = (int64_t)hlo[p] - b, hi = (int64_t)hhi[p] - b;
+            hlo[p] = (int)(lo < -(1ll << 30) ? -(1ll << 30) : lo);
+            hhi[p] = (int)(hi < -(1ll << 30) ? -(1ll << 30) : hi);
+        }
+        for (int f = 0; f < kept; ++f) {
+            const int fr = f * R;
+            sto(lk.q_start + fr, o_fr, ldo(lk.q_start + fr, o_fr) - b);
+            sto(lk.q_end + fr, o_fr, ldo(lk.q_end + fr, o_fr) - b);
+        }
+        sto(lk.base, o_r0 * 2u, ldo(lk.base, o_r0 * 2u) + (int64_t)b);
+    }
     // ---------------- store state and per-robot outputs ----------------
     {
         // fresh copies of the per-lane offsets: the store addresses are recomputed here instead of being kept live
@@ -1452,7 +1475,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         sto(lk.sent, o_r, sent); sto(lk.floor_, o_r, floor_);
         if constexpr (!DL) { sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t); }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
-        if (arr.counts) sto(lk.enq, o_r, enq);
+        if (arr.counts || rebased) sto(lk.enq, o_r, enq);
 #pragma unroll
         for (int s = 0; s < S; ++s) sto(lk.csi + s * R, o_sr, csi[s]);
         if constexpr (!DL) {
@@ -1482,8 +1505,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         } else {
             sto(out.newest, o_r * 2u, (int64_t)(newest >= 0 ? newest - ep0 : -1));
             sto(out.queue_len, o_r * 2u, (int64_t)kept);
-            int qb = enq - ack_new;
-            sto(out.queue_bytes, o_r, (float)(qb > 0 ? qb : 0));
+            sto(out.queue_bytes, o_r, (float)(qb_end > 0 ? qb_end : 0));
             sto(out.sinr_db, o_r, snr_out);
             if (out.serving_cell) sto(out.serving_cell, o_r * 2u, (int64_t)serv);
         }

@@ -113,8 +113,24 @@ def refusals(cfg: NRConfig):
     no(cfg.max_harq_tx > 16, "max_harq_tx > 16", "up to 16 transmissions")
     no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
     no(cfg.frame_buffer > 255, "frame_buffer > 255", "8-bit class field, int32 offsets")
+    air = [m + (math.ceil(m / cfg.pkt_payload_bytes) * cfg.pkt_overhead_bytes if cfg.pkt_overhead_bytes else 0)
+           for m in cfg.msg_sizes]
+    no(max(air, default=0) > 1 << 22, "messages above 2^22 bytes", "a full queue inside the int32 byte offsets")
     no(len(cfg.msg_sizes) > 255, "more than 255 message classes", "8-bit class field")
     return out
+
+
+def split_offsets(floor, sent, enq, rebase_at):
+    """int64 byte offsets [E,R] -> (base [E,R] int64, rel(x) -> x - base as int32-range int64): the base is the
+    floor where the floor has reached rebase_at (else 0), as the step kernel rebases; raises if the queued bytes
+    (enq - floor) or the unsent ones do not fit in int32 above the base."""
+    base = torch.where(floor >= rebase_at, floor, torch.zeros_like(floor)) if rebase_at > 0 else \
+        torch.zeros_like(floor)
+    lim = (1 << 31) - 1
+    if bool(((enq - base) > lim).any()) or bool(((sent - base) < -(1 << 30)).any()) or \
+            bool(((floor - base) > lim).any()):
+        raise ValueError("byte offsets beyond 2^31 above the robot's floor: not representable")
+    return base, (lambda x: x.long() - base)
 
 
 class HipNREngine:
@@ -123,6 +139,8 @@ class HipNREngine:
 
     level = "L2"
     backend = "hip"
+    # the floor (bytes) from which a step moves a robot's int32 byte offsets down into its 64-bit base
+    REBASE_AT = 1 << 30
 
     def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, out_format="reference"):
         cfg = cfg if cfg is not None else NRConfig()
@@ -184,6 +202,7 @@ class HipNREngine:
             "field": z(E, self.C, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
             "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
             "clock": z(1, dt=torch.int64),
+            "base": z(E, R, dt=torch.int64),           # byte-stream base of every robot's UL offsets
         }
         self._n_fields = nf
         self._last_snr = torch.zeros(E, R, device=d)
@@ -226,6 +245,7 @@ class HipNREngine:
                 "h_nrb": z(E, P, R, dt=f32), "q_cap": z(E, F, R, v=-1), "q_start": z(E, F, R), "q_end": z(E, F, R),
                 "q_fin": z(E, F, R, v=BIG_SLOT), "q_meta": z(E, F, R), "newest": z(E, R, v=-1),
                 "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
+                "base": z(E, R, dt=torch.int64),
             }
             ds = _lib.InetNrDlState()
             for name, t_ in self.dst.items():
@@ -292,6 +312,7 @@ class HipNREngine:
         p.timeout, p.tb_oh = cfg.timeout_steps, cfg.tb_overhead_bytes
         p.n_fields, p.n_modes = self._n_fields, cfg.shadow_modes
         p.n_cells = self.C
+        p.rebase_at = self.REBASE_AT
         p.seed_key = C.c_int32(seed_key(self.seed) - (1 << 32) if seed_key(self.seed) >= 1 << 31
                                else seed_key(self.seed)).value
         p.olla_up = cfg.olla_up_db
@@ -800,14 +821,18 @@ class HipNREngine:
         fin = (tf.double() + (fin_slot - tf * N + 1).double() / N) + po
         fin = torch.where(fin_slot == BIG_SLOT, torch.full_like(fin, math.inf), fin)
         qm = st["q_meta"]
+        b = st["base"]                                # the int64 offsets are base + the int32 values
+        bq = b[:, :, None]
         out = {
-            "sent": L(st["sent"]), "floor": L(st["floor_"]), "olla": st["olla"], "avg": st["avg"], "csi": rs(st["csi"]),
+            "sent": L(st["sent"]) + b, "floor": L(st["floor_"]) + b, "olla": st["olla"], "avg": st["avg"],
+            "csi": rs(st["csi"]),
             "h_state": rs(L(meta & 0xFF)), "h_ntx": rs(L((meta >> 8) & 0xFF)), "h_mcs": rs(L((meta >> 16) & 0xFF)),
-            "h_nsb": rs(L((meta >> 24) & 0xFF)), "h_lo": rs(L(st["h_lo"])), "h_hi": rs(L(st["h_hi"])),
+            "h_nsb": rs(L((meta >> 24) & 0xFF)), "h_lo": rs(L(st["h_lo"])) + bq, "h_hi": rs(L(st["h_hi"])) + bq,
             "h_ready": rs(L(st["h_ready"])), "h_tbs": rs(L(st["h_tbs"])), "h_comb": rs(st["h_comb"]),
             "h_lexp": rs(st["h_lexp"]), "h_nrb": rs(st["h_nrb"]), "last_tx": L(st["last_tx"]),
-            "q.cap": rs(L(st["q_cap"])), "q.start": rs(L(st["q_start"])), "q.end": rs(L(st["q_end"])),
-            "q.lost": rs((qm & 1) != 0), "q.fin": rs(fin), "q.cls": rs(L((qm >> 8) & 0xFF)), "q.enq": L(st["enq"]),
+            "q.cap": rs(L(st["q_cap"])), "q.start": rs(L(st["q_start"])) + bq, "q.end": rs(L(st["q_end"])) + bq,
+            "q.lost": rs((qm & 1) != 0), "q.fin": rs(fin), "q.cls": rs(L((qm >> 8) & 0xFF)),
+            "q.enq": L(st["enq"]) + b,
         }
         if pre == "ul":
             out.update({"bsr": L(st["bsr"]), "sr_t": L(st["sr_t"]), "q.det": rs((qm & 2) != 0),
@@ -853,7 +878,14 @@ class HipNREngine:
         g = lambda k: torch.as_tensor(sd[f"{pre}.{k}"]).to(d)  # noqa: E731
         rs = lambda x: x.permute(0, 2, 1).contiguous()  # noqa: E731
         I = lambda x: x.to(torch.int32)  # noqa: E731
-        pairs = (("sent", "sent"), ("floor_", "floor"), ("last_tx", "last_tx"), ("enq", "q.enq"))
+        # the int64 byte offsets as base + int32 values: the base is the floor once that reaches REBASE_AT
+        base, rel = split_offsets(g("floor").long(), g("sent").long(), g("q.enq").long(), self.REBASE_AT)
+        st["base"].copy_(base)
+        bq = base[:, :, None]
+        st["floor_"].copy_(I(rel(g("floor"))))
+        st["sent"].copy_(I(rel(g("sent"))))
+        st["enq"].copy_(I(rel(g("q.enq"))))
+        pairs = (("last_tx", "last_tx"),)
         if pre == "ul":
             pairs += (("bsr", "bsr"), ("sr_t", "sr_t"))
         for a, b in pairs:
@@ -863,7 +895,9 @@ class HipNREngine:
         st["csi"].copy_(rs(g("csi")))
         meta = (g("h_state") | (g("h_ntx") << 8) | (g("h_mcs") << 16) | (g("h_nsb") << 24))
         st["h_meta"].copy_(rs(I(meta)))
-        for a in ("h_lo", "h_hi", "h_ready", "h_tbs"):
+        for a in ("h_lo", "h_hi"):                  # (a free process's stale range: at most 2^30 below the base)
+            st[a].copy_(rs(I((g(a).long() - bq).clamp(-(1 << 30), (1 << 31) - 1))))
+        for a in ("h_ready", "h_tbs"):
             st[a].copy_(rs(I(g(a))))
         for a in ("h_comb", "h_lexp", "h_nrb"):
             st[a].copy_(rs(g(a).float()))
@@ -871,8 +905,8 @@ class HipNREngine:
         valid = cap >= 0
         st["qlen"].copy_(I(valid.sum(-1)))
         st["q_cap"].copy_(rs(I(torch.where(valid, cap, torch.full_like(cap, -1)))))
-        st["q_start"].copy_(rs(I(g("q.start"))))
-        st["q_end"].copy_(rs(I(g("q.end"))))
+        for a, k in (("q_start", "q.start"), ("q_end", "q.end")):      # (empty slots keep their stale values)
+            st[a].copy_(rs(I((g(k).long() - bq).clamp(-(1 << 30), (1 << 31) - 1))))
         po = cfg.proc_offset_ms / cfg.control_step_ms
         fin = g("q.fin").double()
         slot = torch.round((fin - po) * N).long() - 1

@@ -101,3 +101,20 @@ def test_hash_helpers_agree():
     for v in (0, 5, (2 << 16) | 7, 0xFFFFFFFF):
         assert EN.salt(v) == (EN.mix32(v) + 0x9E3779B9) & 0xFFFFFFFF
     assert EN.seed_key(0) == EN.mix32(EN.mix32(0) ^ EN.salt(0))
+
+
+def test_split_offsets_rebases_at_the_floor():
+    """Byte offsets as base + int32 values (the step kernel's rebase): the base is the floor once it reaches the
+    threshold, offsets at or above the floor stay non-negative, and offsets that do not fit are refused."""
+    import torch
+    from isaac_net_amd.engine import split_offsets
+    big = 3 * (1 << 31) + 12345
+    floor = torch.tensor([[0, 1000, big, (1 << 30) - 1]])
+    sent = floor + torch.tensor([[5, 0, 70000, 3]])
+    enq = sent + torch.tensor([[9, 0, 1 << 20, 0]])
+    base, rel = split_offsets(floor, sent, enq, 1 << 30)
+    assert base.tolist() == [[0, 0, big, 0]]
+    assert rel(floor).tolist() == [[0, 1000, 0, (1 << 30) - 1]] and rel(enq)[0, 2] == 70000 + (1 << 20)
+    assert torch.equal(base + rel(enq), enq)
+    with pytest.raises(ValueError):
+        split_offsets(torch.tensor([[0]]), torch.tensor([[0]]), torch.tensor([[1 << 31]]), 1 << 30)
