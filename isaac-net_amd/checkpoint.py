@@ -90,8 +90,10 @@ def read(path, map_location="cpu"):
 
 
 def _config_diff(mine, theirs, path=""):
-    """Paths of the fields of this build's config whose values differ in the checkpoint's config (fields that only
-    one side has are not compared: the reference's NRConfig has fields this build refuses or does not model)."""
+    """Paths of the fields whose values differ between this build's config and the checkpoint's. At the top level a
+    field only the checkpoint has must be one of the reference's fields this build does not model, at its reference
+    default (config.REFERENCE_ONLY_DEFAULTS): otherwise the checkpoint ran a feature this engine does not, and the
+    field is reported too."""
     if isinstance(mine, dict) and isinstance(theirs, dict):
         out = []
         for k in mine:
@@ -99,6 +101,14 @@ def _config_diff(mine, theirs, path=""):
                 continue
             if k in theirs:
                 out += _config_diff(mine[k], theirs[k], f"{path}{k}.")
+        if path == "" and mine.get("__type__") == "NRConfig":
+            from .config import REFERENCE_ONLY_DEFAULTS
+            for k in theirs:
+                if k in mine or k == "__type__":
+                    continue
+                if k not in REFERENCE_ONLY_DEFAULTS or \
+                        _config_diff(_plain(REFERENCE_ONLY_DEFAULTS[k]), theirs[k], f"{k}."):
+                    out.append(f"{k} (not modelled by this engine; {theirs[k]!r})")
         return out
     if isinstance(mine, list) and isinstance(theirs, list):
         if len(mine) != len(theirs):

@@ -35,6 +35,98 @@ def rbg_size_38214(n_prb, config=1):
     raise ValueError(f"no RBG size for {n_prb} PRBs")
 
 
+# The reference NRConfig's fields that this build does not model, with their reference defaults (isaac_net/core/
+# config.py:477-786): FDD DL carrier, DL mini-slots, LENA TBS, rank / MIMO, QoS, the BSR grant pipeline, Doppler and
+# delay-spread fading, InF / O2I details, radio maps, blockage, sector antennas, closed-loop TPC, radio link failure,
+# RACH, DRX and the prototype levels. A reference config (a checkpoint's) that sets one of them to anything else
+# needs a feature this engine does not run (checkpoint.check refuses it).
+REFERENCE_ONLY_DEFAULTS = {
+    'dl_n_prb': None,
+    'dl_bandwidth_mhz': None,
+    'mini_slot_dl': False,
+    'lena_ref_sc_per_rb': 1,
+    'rank_rule': 'sinr_los',
+    'rank_sinr_min_db': 10.0,
+    'rank_k_max_db': 3.0,
+    'rank_layer_penalty_db': 3.0,
+    'ul_mimo': False,
+    'dl_mimo': True,
+    'qos_priority': (10, 70),
+    'qos_pdb_ms': (math.inf, math.inf),
+    'qos_gamma': 1.0,
+    'sr_boot_slots': 6,
+    'sr_boot_bytes': 17,
+    'bsr_delay_slots': 10,
+    'bsr_hdr_bytes': 8,
+    'bsr_est_hdr_bytes': 5,
+    'rlc_tail_bytes': 16,
+    'rlc_tail_timer_ms': 10.0,
+    'ue_speed_mps': None,
+    'doppler_min_speed_mps': 0.0,
+    'fading_delay_spread_ns': None,
+    'fading_ds_from_los': True,
+    'fading_pdp': 'exponential',
+    'fading_ds_grid': (3.0, 3000.0, 16),
+    'inf_hall_volume_m3': None,
+    'inf_hall_surface_m2': None,
+    'inf_lg_ds': None,
+    'shadow_white_dcorr_m': 1.0,
+    'o2i_model': 'low',
+    'inf_clutter_density': None,
+    'inf_clutter_size_m': None,
+    'inf_clutter_height_m': None,
+    'radio_map_path': None,
+    'blockage_radius_m': 0.3,
+    'blockage_loss_db': 20.0,
+    'los_raycast_samples': 32,
+    'los_diffraction': False,
+    'nlos_extra_loss_db': 0.0,
+    'blockage_model': 'sphere',
+    'blocker_size_m': ((0.6, 1.5), (0.3, 1.7), (4.8, 1.4)),
+    'blockage_max_db': 40.0,
+    'cell_azimuth_deg': None,
+    'cell_tilt_deg': 0.0,
+    'gnb_antenna_gain_dbi': 8.0,
+    'ul_tpc_mode': 'accumulate',
+    'ul_tpc_target_db': None,
+    'ul_tpc_steps_db': None,
+    'ul_tpc_delay_slots': None,
+    'ul_tpc_range_db': 20.0,
+    'rlf_qout_db': -8.0,
+    'rlf_qin_db': -6.0,
+    'n310': 1,
+    'n311': 1,
+    't310_ms': 1000.0,
+    't311_ms': 3000.0,
+    'reest_delay_ms': 40.0,
+    'rlf_rlc': None,
+    'rach_occasion_slots': 20,
+    'rach_preambles': 64,
+    'rach_rar_window_slots': 10,
+    'rach_msg3_slots': 10,
+    'rach_backoff_ms': 20.0,
+    'rach_max_attempts': 10,
+    'rach_initial': 'connected',
+    'rach_release_after_ms': None,
+    'drx_inactivity_ms': 100.0,
+    'drx_cycle_ms': 160.0,
+    'drx_on_ms': 10.0,
+    'drx_short_cycle_ms': None,
+    'drx_short_cycles': 2,
+    'drx_start_offset_ms': 0.0,
+    'drx_ul_wake': 'sr',
+    'l0_delay_median_steps': 0.05,
+    'l0_delay_log_sigma': 0.5,
+    'l0_loss': 0.0,
+    'dr_delay_median_steps': (0.05, 10.0),
+    'dr_delay_log_sigma': (0.2, 1.2),
+    'dr_loss': (0.0, 0.2),
+    'l1_eta': 0.9,
+    'proto_ul_slots_per_step': None,
+    'fidelity': None,
+}
+
+
 @dataclass
 class NRConfig:
     # ---- numerology, carrier, frame structure (reference config.py:491-513)

@@ -1004,6 +1004,39 @@ class HipNREngine:
                     "net.rng.s0": int(self._cparams.seed_key) & M32})
         return out
 
+    # Reference checkpoint keys that hold no state here: torch generators (the engine's draws are counter based),
+    # values derived from the config, the reference's per-step caches (recomputed every step) and statistics buffers.
+    _CK_SKIP = {"gen", "net.gen", "radio.gen", "net.rng._zero", "net.sizes", "radio._sizes", "radio.gnb", "radio.gnb3",
+                "radio.ch.gnb", "radio.ch.los", "radio.has_prev", "radio.prev_pos", "radio.speed", "net.refused_env",
+                "net._gain_c", "net._ni_la_ul", "net._pg", "net.ul.member", "net.ul.pc_backoff", "net.ul.phr_snr",
+                "net.ul.sched_ok", "net.ioN[dl]", "net.ni_dl", "net.ul.sb_prb", "net.dl.sb_prb", "net.ul.q.f_nact",
+                "net.ul.q.f_snr", "net.ul.q.f_own", "net.dl.q.f_nact", "net.dl.q.f_snr", "net.dl.q.f_own",
+                "net.dl.q.det", "net.dl.q.hid", "net.dl_newest"}
+    # Reference host values that switch on what this engine does not run (traffic models, access procedures, hooks
+    # and traces, frequency-correlated or per-robot fading, blockage, O2I, radio link failure, TPC, BSR grants,
+    # MIMO, QoS, the LENA MAC): a checkpoint holding another value was written with that feature on.
+    _CK_OFF = {"_gate": None, "_dl_gate": None, "_los_fn": None, "access": None, "_extras": False, "traffic": None,
+               "traffic_dl": None, "per_robot_doppler": False, "net.fc_mode": None, "net.trace_frames": None,
+               "net.trace_frames_dl": None, "net._user_hook[ul]": None, "net._user_hook[dl]": None,
+               "net.assoc.rlf": False, "radio._blocked": None, "radio.blk_a": None, "radio.obstacle_outputs": False,
+               "radio.white": None, "radio.ch.o2i": False, "radio.ch.soft": False,
+               **{f"net.{lk}.{k}": v for lk in ("ul", "dl") for k, v in (
+                   ("slot_hook", None), ("sinr_hook", None), ("trace", None), ("mimo", False), ("qos", False),
+                   ("_tpc", False), ("_bsr_model", False), ("_lena_mac", False), ("_occ", None))}}
+
+    def _strict_extra_keys(self, sd, used):
+        """strict loading: the state keys of sd that are neither restored (used) nor known to hold no state here,
+        and the host switches that are on."""
+        bad = []
+        for k, v in sd.items():
+            if k in used or k in self._CK_SKIP or k.endswith(".gen"):
+                continue
+            if torch.is_tensor(v) or isinstance(v, np.ndarray):
+                bad.append(k)
+            elif k in self._CK_OFF and v != self._CK_OFF[k] and not (v is None and self._CK_OFF[k] is False):
+                bad.append(f"{k}={v!r}")
+        return bad
+
     def load_state_dict(self, sd, strict=True, T=None, last_g=None):
         """Restore a checkpoint in place: this engine's state_dict(), or the reference engine's (the same keys;
         keys of the reference that hold no state here are skipped: torch generators, trace hooks, statistics, the
@@ -1017,8 +1050,10 @@ class HipNREngine:
         cfg, st, d = self.config, self.st, self.dev
         mine = self.owner_state()
         owner, missing = {}, []
+        used = {"net.rng.env", "net.rng.s0", "T", "net.last_g", "_uniform_epoch"}
         for k, v in mine.items():
             ck = self._ck_key(k)
+            used.add(ck)
             if ck in sd:
                 val = torch.as_tensor(sd[ck])
                 if strict and tuple(val.shape) != tuple(v.shape):
@@ -1034,6 +1069,15 @@ class HipNREngine:
             for k, v in mine.items():
                 owner.setdefault(k, v)
         g = lambda k: torch.as_tensor(sd[k]).to(d)  # noqa: E731
+        for pre, _ in self._field_keys():
+            used.update((pre + ".k", pre + ".phi"))
+        for name in ("ul", "dl"):
+            used.update(f"net.{name}.{k}" for k in ("ntx_hist", "rv_tx", "rv_fail", "prb_used_env"))
+            used.update(f"net.{name}.ctr[{k}]" for k in CTR_NAMES + ("prb_avail",))
+        if strict:
+            bad = self._strict_extra_keys(sd, used)
+            if bad:
+                raise KeyError("load_state_dict: state this engine does not run (strict): " + ", ".join(bad[:12]))
         if "net.rng.env" in sd:
             st["env_id"].copy_(g("net.rng.env").to(torch.int32))
         for pre, fi in self._field_keys():

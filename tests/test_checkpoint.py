@@ -38,8 +38,8 @@ def test_header_and_checks():
         checkpoint.check(eng, other)
     with pytest.warns(UserWarning):
         checkpoint.check(eng, other, strict=False)
-    # fields only the reference's config has are not compared; the seed never is
-    theirs = dict(h, config=dict(h["config"], seed=7, some_reference_only_field=1))
+    # the seed is never compared; a reference-only field at its reference default passes
+    theirs = dict(h, config=dict(h["config"], seed=7, drx_cycle_ms=160.0))
     checkpoint.check(eng, theirs)
 
 
@@ -70,3 +70,33 @@ def test_reference_multicell_checkpoint_holds_the_restored_state():
         assert k in keys, k
     E, R = int(json.loads(bytes(z["host_json"]).decode())["E"]), int(json.loads(bytes(z["host_json"]).decode())["R"])
     assert z["ck/net.h"].shape == (E, R, 3, 13, 2) and z["ck/radio.k"].shape[:2] == (3, E)
+
+
+def test_reference_only_fields_must_hold_their_reference_defaults():
+    """A reference config field that this build does not model (DRX, RLF, TPC, MIMO, ...) passes the check only at
+    its reference default; another value, or a field neither side knows, is refused."""
+    from isaac_net_amd.config import REFERENCE_ONLY_DEFAULTS
+    eng = fake_engine()
+    h = checkpoint.header(eng)
+    ref_cfg = dict(h["config"], **{k: checkpoint._plain(v) for k, v in REFERENCE_ONLY_DEFAULTS.items()})
+    checkpoint.check(eng, dict(h, config=ref_cfg))                # every reference-only field at its default
+    for k, v in (("drx_cycle_ms", 320.0), ("n310", 4), ("ul_mimo", True), ("rach_initial", "idle"),
+                 ("qos_pdb_ms", [20.0, float("inf")])):
+        with pytest.raises(ValueError, match=k):
+            checkpoint.check(eng, dict(h, config=dict(ref_cfg, **{k: v})))
+    with pytest.raises(ValueError, match="not_a_field"):
+        checkpoint.check(eng, dict(h, config=dict(ref_cfg, not_a_field=1)))
+
+
+def test_strict_state_loading_refuses_what_this_engine_does_not_run():
+    """Under strict loading a state tensor the engine neither restores nor knows to skip, or a reference host switch
+    that is on (a traffic model, an access procedure, a hook), is refused; generators, config-derived constants and
+    the reference's per-step caches are skipped."""
+    import torch
+    from isaac_net_amd.engine import HipNREngine as E
+    ok = {"net.ul.sent": torch.zeros(2), "gen": torch.zeros(3), "radio.ch.sf_los.gen": torch.zeros(3),
+          "net.sizes": torch.zeros(2), "access": None, "_extras": False, "net.ul.slot_hook": None, "E": 4}
+    assert E._strict_extra_keys(E, ok, {"net.ul.sent"}) == []
+    assert E._strict_extra_keys(E, dict(ok, **{"net.ul.tag": torch.zeros(2)}), {"net.ul.sent"}) == ["net.ul.tag"]
+    bad = E._strict_extra_keys(E, dict(ok, access={"state": 1}, traffic="poisson"), {"net.ul.sent"})
+    assert len(bad) == 2 and bad[0].startswith("access=")
