@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 5
+#define INET_NR_ABI_VERSION 6
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 128         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two
@@ -183,6 +183,10 @@ typedef struct InetNrDlState {
                                            delivered in the last step, -1 if none (NRNet.dl_newest) */
     int64_t *ctr, *hist;                /* [E][INET_NR_NCTR], [E][3][max_tx + 1]: as InetNrState's, for the DL */
     int64_t *out_newest, *out_queue_len;        /* [E][R] step outputs dl_newest (env clock) and dl_queue_len */
+    float *out_delay;                   /* [E][R][F] or NULL: per frame slot of the queue before compaction, the delivery
+                                           time minus the capture step of a frame delivered in this step (fin - cap,
+                                           control steps), NaN otherwise (the DL frames NRNet._log_dl records,
+                                           nr_engine.py:906-907) */
     const float *cqi_thr;               /* [15] SINR from which CQI k + 1 is reported (cqi_table = "38214"), */
     const int32_t *cqi_mcs;             /* [16] MCS of each CQI; both NULL for cqi_table = "mcs" */
     int64_t *base;                      /* [E][R] the DL byte-stream base, as InetNrState.base for the UL */

@@ -47,7 +47,7 @@ class InetNrDlState(C.Structure):
     _fields_ = [(n, P) for n in (
         "sent", "floor_", "last_tx", "olla", "avg", "enq", "qlen", "csi", "h_meta", "h_lo", "h_hi", "h_ready", "h_tbs",
         "h_comb", "h_lexp", "h_nrb", "q_cap", "q_start", "q_end", "q_fin", "q_meta", "newest", "ctr", "hist",
-        "out_newest", "out_queue_len", "cqi_thr", "cqi_mcs", "base")] + \
+        "out_newest", "out_queue_len", "out_delay", "cqi_thr", "cqi_mcs", "base")] + \
                [("gnb_proc", i32), ("snr_offset", i32), ("ref_off", f32), ("noise_prb", f32), ("snr_off", f32),
                 ("pad", i32)]
 
@@ -115,7 +115,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 WIFI_ABI_VERSION = 2
 _LIB = None
 

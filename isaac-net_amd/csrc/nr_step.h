@@ -1358,8 +1358,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         }
         const int cap_rel = cap >= 0 ? cap - ep0 : -1;
         const int cls = (int)((meta >> 8) & 0xffu);
-        if (DL) {
-            // the DL reports no per-frame outputs (nr_engine.py:866-881)
+        if constexpr (DL) {
+            // the DL's step outputs hold no per-frame keys (nr_engine.py:866-881); its delays go out only when the
+            // caller keeps statistics
+            if (lk.out_delay) sto(lk.out_delay + f, ob * 4u, delay);
         } else if (pm.out_ref) {
             sto(out.delivered + f, ob, (uint8_t)delivered);
             sto(out.timed_out + f, ob, (uint8_t)timed);
@@ -1422,6 +1424,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             }
             sto((uint4*)(out.delay + f), ob * 4u, nans);
         }
+    }
+    if constexpr (DL) {
+        if (act && lk.out_delay)
+            for (int f = qv; f < F; ++f) sto(lk.out_delay + f, ob * 4u, __uint_as_float(0x7fc00000u));
     }
     if (act) {                                         // vacated slots: empty, not completed
         for (int f = kept; f < qlen; ++f) { sto(lk.q_cap + f * R, o_fr, -1); sto(lk.q_fin + f * R, o_fr, (int)FIN_NONE); }

@@ -179,6 +179,9 @@ class HipNREngine:
         self.last_g = None
         self._last_hid = torch.zeros(E, dtype=torch.long, device=dev)
         self._rows = {}
+        self._log_stats, self._feat, self._dl_delay = False, None, None
+        self.log_cap_max = 10 ** 9       # only frames captured at or before this step (global clock) are logged
+        self.clear_stats()
         self.reset(None)
 
     # ------------------------------------------------------------------ buffers
@@ -539,10 +542,14 @@ class HipNREngine:
         self._last_hid = hid.clone()
         acc = torch.empty(self.E, self.R, dtype=torch.bool, device=self.dev)
         cfg = self.config
+        pre = self._stats_pre_submit(T) if self._log_stats else None
         _lib.check(self._lib.inet_nr_submit(
             C.byref(self._cstate), C.byref(self._cparams), T, send.data_ptr(), None if det is None else det.data_ptr(),
             hid.data_ptr(), None, 0, self._sizes.data_ptr(), int(cfg.discard == "pdcp_arrival"),
             cfg.pkt_payload_bytes, cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "submit")
+        if pre is not None:
+            snr = self._last_snr if snr_db is None else snr_db.to(self.dev, torch.float32)
+            self._stats_enqueue(send > 0, *pre, snr if snr.dim() == 2 else snr.mean(-1), acc=acc)
         return acc
 
     def submit_counts(self, counts, t=None):
@@ -553,6 +560,8 @@ class HipNREngine:
         nc = cnt.shape[-1]
         if tuple(cnt.shape[:2]) != (self.E, self.R) or nc > len(self.config.msg_sizes):
             raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        if self._log_stats:
+            self._stats_counts(T, cnt)
         return self._launch_submit_counts(T, cnt)
 
     def _launch_submit_counts(self, T, cnt):
@@ -591,6 +600,8 @@ class HipNREngine:
             C.byref(self._cstate), C.byref(self._cdl), C.byref(self._cparams), T, nb.data_ptr(),
             None if cl is None else cl.data_ptr(), int(cfg.discard == "pdcp_arrival"), cfg.pkt_payload_bytes,
             cfg.pkt_overhead_bytes, acc.data_ptr(), self._stream()), "dl submit")
+        if self._log_stats:                         # every refused DL frame (nr_engine.py:496-497)
+            self.stats["overflow_dl"] = self.stats.get("overflow_dl", 0) + int(((nb > 0) & ~acc).sum())
         return acc
 
     def _alloc_out(self):
@@ -661,7 +672,11 @@ class HipNREngine:
             if not legacy:
                 self._last_hid = torch.zeros_like(self._last_hid)
                 hid = self._last_hid
+        if arr is not None and self._log_stats:
+            self._stats_counts(T, arr)
         o = self._launch_step(T, plan, xin, hid, dl, arrivals=arr)
+        if self._log_stats:
+            self._stats_step(o)
         self._commit(T, plan, o)
         if legacy:
             return o["newest"], o["det_env"]
@@ -718,6 +733,7 @@ class HipNREngine:
             o["dl_queue_len"] = torch.empty(E, R, dtype=torch.int64, device=d)
             cd = self._cdl
             cd.out_newest, cd.out_queue_len = o["dl_newest"].data_ptr(), o["dl_queue_len"].data_ptr()
+            cd.out_delay = None if self._dl_delay is None else self._dl_delay.data_ptr()
             cd.snr_offset = add_off
             self._cparams.input_kind = dkind
             self._cparams.n_data = plan["n_dl"]
@@ -783,6 +799,123 @@ class HipNREngine:
         return GraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     # ------------------------------------------------------------------ statistics
+    FEATS = ("cls", "f_nact", "f_snr", "f_own")
+
+    @property
+    def log_stats(self):
+        """Record per-frame statistics (NRNet.log_stats, nr_engine.py:440-446, 466-497, 885-914): per step the delay,
+        env and features of the UL frames delivered, and of those timed out or dropped, captured at or before
+        log_cap_max; the DL delays; the UL overflow, PDCP-discard, HARQ-drop and late counts, the refused DL
+        frames and refused_env. The queue features f_nact (robots of the env with a queued frame when the frame
+        arrived), f_snr (the SNR given to submit, else the previous step's) and f_own (its queue position) are kept
+        while statistics are on: frames submitted while they were off carry 0."""
+        return self._log_stats
+
+    @log_stats.setter
+    def log_stats(self, on):
+        on = bool(on)
+        if on and self._feat is None:
+            E, R, F, d = self.E, self.R, self.F, self.dev
+            self._feat = {"f_nact": torch.zeros(E, R, F, dtype=torch.long, device=d),
+                          "f_snr": torch.zeros(E, R, F, dtype=torch.float32, device=d),
+                          "f_own": torch.zeros(E, R, F, dtype=torch.long, device=d)}
+            if self.dl:
+                self._dl_delay = torch.empty(E, R, F, dtype=torch.float32, device=d)
+        elif not on:
+            self._feat, self._dl_delay = None, None
+        self._log_stats = on
+
+    def clear_stats(self):
+        """Empty the statistics record and refused_env (NRNet.clear_stats)."""
+        self.stats = {"delay": [], "overflow": 0, "dl_delay": [], "dropped": 0, "late": 0, "discarded": 0,
+                      "d_env": [], "x_env": []}
+        self.refused_env = torch.zeros(self.E, dtype=torch.long, device=self.dev)   # overflow + PDCP discard
+        for f in self.FEATS:
+            self.stats["d_" + f] = []
+            self.stats["x_" + f] = []
+
+    def queued(self):
+        """Queued UL frames per robot [E,R] int64 (NRNet.queued)."""
+        return self.st["qlen"].long()
+
+    def collect(self):
+        """The statistics since the last clear_stats() (NRNet.collect): every per-step list concatenated into one
+        CPU tensor (an empty float32 tensor if nothing was logged), then the counts."""
+        st = self.stats
+        out = {k: (torch.cat(v) if v else torch.zeros(0)) for k, v in st.items() if isinstance(v, list)}
+        out.update({k: v for k, v in st.items() if not isinstance(v, list)})
+        return out
+
+    def _stats_pre_submit(self, T):
+        """(queued frames [E,R], head frame stale under discard="pdcp_arrival" [E,R]) before an enqueue at step T."""
+        count = self.st["qlen"].long()
+        if self.config.discard != "pdcp_arrival":
+            return count, torch.zeros_like(count, dtype=torch.bool)
+        head = self.st["q_cap"][:, 0, :].long()
+        return count, (head >= 0) & ((T - head) >= self.config.timeout_steps)
+
+    def _stats_enqueue(self, want, count, stale, snr, acc=None):
+        """The statistics of one enqueue call (NRNet.add_frames, nr_engine.py:466-487): want [E,R] messages, count /
+        stale as _stats_pre_submit's; acc: the accepted mask the launch returned (None: admission replayed here,
+        PDCP refusal then the full queue). Records the accepted frames' features; returns (acc, queued after)."""
+        st, F = self.stats, self.F
+        adm = want & ~stale
+        full = count >= F
+        if acc is None:
+            acc = adm & ~full
+        st["overflow"] += int((adm & full).sum())
+        st["discarded"] += int((want & ~adm).sum())
+        self.refused_env += (want & ~acc).sum(-1)
+        at = (torch.arange(F, device=self.dev) == count[..., None]) & acc[..., None]
+        ft = self._feat
+        nact = (count > 0).sum(-1)
+        ft["f_nact"] = torch.where(at, nact[:, None, None], ft["f_nact"])
+        ft["f_snr"] = torch.where(at, snr[..., None], ft["f_snr"])
+        ft["f_own"] = torch.where(at, count[..., None], ft["f_own"])
+        return acc, count + acc.long()
+
+    def _stats_counts(self, T, cnt):
+        """The statistics of a counts-form enqueue (submit_counts, or arrivals fused into the step launch): its
+        submit() calls replayed one at a time, class by class and message by message, as the kernel enqueues them."""
+        count, stale0 = self._stats_pre_submit(T)
+        had = count > 0
+        c = cnt.long()
+        for ci in range(c.shape[-1]):
+            for i in range(int(c[..., ci].max())):
+                # the head frame is the one queued before the call, or this step's first (never stale)
+                stale = torch.where(had, stale0, (count > 0) & (self.config.timeout_steps <= 0))
+                _, count = self._stats_enqueue(c[..., ci] > i, count, stale, self._last_snr)
+
+    def _stats_step(self, o):
+        """Log the frames the step resolved (NRNet._log_ul / _log_dl, nr_engine.py:890-907) from its outputs (the
+        queue layout before compaction), then compact the feature record as the queue was (queues.py:105-110)."""
+        st, cfg, E = self.stats, self.config, self.E
+        if "flags" in o:
+            fl = o["flags"]
+            delivered, timed, dropped = (fl & 1) != 0, (fl & 2) != 0, (fl & 4) != 0
+            cap, cls = o["cap32"].long(), o["cls8"].long()
+        else:
+            delivered, timed, dropped, cap, cls = o["delivered"], o["timed_out"], o["dropped"], o["cap"], o["cls"]
+        keep = cap + self.st["epoch"].long()[:, None, None] <= self.log_cap_max     # capture step, global clock
+        dk, tk = delivered & keep, (timed | dropped) & keep
+        delay = o["delay"]
+        st["delay"].append(delay[dk].cpu())
+        eidx = torch.arange(E, device=self.dev)[:, None, None].expand_as(cap)
+        st["d_env"].append(eidx[dk].cpu())
+        st["x_env"].append(eidx[tk].cpu())
+        st["dropped"] += int(dropped.sum())
+        st["late"] += int((dk & (delay >= cfg.timeout_steps)).sum())
+        feats = {"cls": cls, **self._feat}
+        for f in self.FEATS:
+            st["d_" + f].append(feats[f][dk].cpu())
+            st["x_" + f].append(feats[f][tk].cpu())
+        order = torch.argsort((delivered | timed | dropped).to(torch.uint8), dim=-1, stable=True)
+        for k, v in self._feat.items():
+            self._feat[k] = torch.gather(v, -1, order)
+        if self._dl_delay is not None:
+            dd = self._dl_delay
+            st["dl_delay"].append(dd[~torch.isnan(dd)].cpu())
+
     def counters(self):
         """{"ul": {counter: value, ntx_hist, rv_tx, rv_fail}} (and "dl" with the downlink) since the last full reset
         (NRNet.counters)."""
@@ -983,6 +1116,8 @@ class HipNREngine:
         cfg, st, E = self.config, self.st, self.E
         out = {self._ck_key(k): v.clone() for k, v in self.owner_state().items()}
         out["net.rng.env"] = st["env_id"].long().clone()
+        if self._feat is not None:                 # the queued frames' features, kept while log_stats is on
+            out.update({f"net.ul.q.{k}": v.clone() for k, v in self._feat.items()})
         for pre, fi in self._field_keys():
             f = st["field"][:, :, fi].permute(1, 0, 2, 3)          # [C, E, K, 3]
             out[pre + ".k"] = f[..., :2].clone()
@@ -1040,7 +1175,7 @@ class HipNREngine:
     def load_state_dict(self, sd, strict=True, T=None, last_g=None):
         """Restore a checkpoint in place: this engine's state_dict(), or the reference engine's (the same keys;
         keys of the reference that hold no state here are skipped: torch generators, trace hooks, statistics, the
-        queue's f_nact / f_snr / f_own fields, host configuration values). Per-env counters come back as the
+        queue's f_nact / f_snr / f_own fields unless log_stats is on, host configuration values). Per-env counters come back as the
         reference keeps them: totals (on env 0) and per-env PRBs and HARQ histograms. strict: raise if state this
         engine keeps is missing or has another shape. The owner-key form of owner_state() is accepted too (with
         T / last_g as in load_owner_state). Returns self."""
@@ -1117,6 +1252,10 @@ class HipNREngine:
         self.load_owner_state(owner, T=T, last_g=sd.get("net.last_g", last_g))
         if "_uniform_epoch" in sd:
             self._uniform_epoch = sd["_uniform_epoch"]
+        if self._feat is not None:                 # with log_stats on: the queued frames' features
+            for k, v in self._feat.items():
+                if f"net.ul.q.{k}" in sd:
+                    self._feat[k] = g(f"net.ul.q.{k}").to(v.dtype).reshape(v.shape).clone()
         return self
 
 
@@ -1165,6 +1304,8 @@ class GraphStep:
         self.x.copy_(x[..., :2])
         self.counts.copy_(counts)
         eng.st["clock"].fill_(T)
+        if eng._log_stats:
+            eng._stats_counts(T, self.counts)
         self.g_submit.replay()
         eng._last_hid = self.hid
         ev = eng.kernel_events
@@ -1173,6 +1314,8 @@ class GraphStep:
         self.g_step.replay()
         if ev is not None:
             ev.end(torch.cuda.current_stream(eng.dev))
+        if eng._log_stats:
+            eng._stats_step(self.out)
         eng._commit(T, self.plan, self.out)
         return self.out
 

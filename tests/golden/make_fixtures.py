@@ -10,6 +10,7 @@ reference is copied. The vectors pin what no closed form or known answer pins:
   * the processed BLER table and thr_ref (core/phy.py:234-243, 405-482);
   * the plane-wave shadowing draws of the radio (core/radio.py:185-189, core/channels/fields.py:38-64);
   * the eager _finish / compaction output layout (core/nr_engine.py:843-888, core/queues.py:105-110);
+  * the statistics of NRNet with log_stats on (core/nr_engine.py:440-446, 885-914): collect(), queued(), refused_env;
   * level WIFI trajectories (core/wifi/engine.py:100-403 WifiNet on the levels/base.py:43-360 FIFO): the mean-field
     solve per sub-step (core/wifi/meanfield.py:187-209), the Poisson / renewal access counts, the FIFO service and the
     retry-limit loss, with SNR inputs and with poses through the APs' radio.
@@ -120,6 +121,28 @@ CASES = {
                             ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
                             cell_center_m=(60.0, 60.0)),
                    E=3, R=8, steps=40, kind="pose", arena=200.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
+}
+
+
+# Statistics cases (NREngine.log_stats / collect / queued, isaac_net/core/nr_engine.py:440-446, 885-914): the
+# engine runs with log_stats on from construction; every step's queued() and refused_env and the final collect()
+# are recorded. "log_cap_max": set on the reference's NRNet (frames captured later are not logged).
+STATS_CASES = {
+    # UL: HARQ drop (dropped frames), purge timeouts (timed out, late), a small FIFO (overflow), two classes, poses
+    # (frame SNR = the previous step's SNR), partial resets
+    "stats_ul": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="pf", n_harq=4, max_harq_tx=2,
+                              harq_fail="drop", frame_buffer=6, msg_sizes=(3000.0, 600.0), timeout_steps=4,
+                              fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                              cell_positions_m=((60.0, 60.0),), gnb_height_m=10.0),
+                     E=4, R=12, steps=30, kind="pose", arena=260.0, walk=2.0, rates=(1.2, 0.8),
+                     resets={14: [1, 3]}),
+    # UL + DL: PDCP discard on arrival (discarded), small FIFOs (UL and DL overflow), SNR input, RLC UM drop, DL delays,
+    # a log cap
+    "stats_dl": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=2,
+                              harq_fail="drop", frame_buffer=5, msg_sizes=(2500.0,), timeout_steps=5,
+                              discard="pdcp_arrival", dl=True),
+                     E=3, R=8, steps=30, kind="snr", snr=(-6.0, 12.0), rates=(1.4,), dl_sizes=(4000.0,),
+                     dl_rates=(1.1,), resets={10: [0]}, log_cap_max=20),
 }
 
 
@@ -272,6 +295,55 @@ def run_case(name, c):
     out["counters_json"] = np.frombuffer(json.dumps(eng.counters()).encode(), dtype=np.uint8)
     np.savez_compressed(os.path.join(HERE, f"traj_{name}.npz"), **out)
     print(name, "state keys:", len(keys_seen), "arrays:", len(out))
+
+
+def run_stats_case(name, c):
+    """The statistics of NRNet with log_stats on: per step queued() and refused_env, at the end collect() (each list
+    entry as one array, each count as an int64)."""
+    NRConfig, make_engine, state_dict, Requests = _ref()
+    cfg = NRConfig(**c["cfg"], seed=0)
+    E, R, T = c["E"], c["R"], c["steps"]
+    eng = make_engine("L2", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
+    eng.log_stats = True
+    if "log_cap_max" in c:
+        eng.net.log_cap_max = c["log_cap_max"]
+    x, counts, *dl = _inputs(name, c)
+    dl_counts = dl[0] if dl else None
+    out = {"x": x, "counts": counts, "E": np.int64(E), "R": np.int64(R), "steps": np.int64(T),
+           "cfg_json": np.frombuffer(json.dumps(c["cfg"]).encode(), dtype=np.uint8),
+           "kind": np.frombuffer(c["kind"].encode(), dtype=np.uint8),
+           "log_cap_max": np.int64(c.get("log_cap_max", 10 ** 9))}
+    if dl_counts is not None:
+        out["dl_counts"] = dl_counts
+        out["dl_sizes"] = np.asarray(c["dl_sizes"], dtype=np.float32)
+    reset_mask = np.zeros((T, E), dtype=np.bool_)
+    for s, ids in c["resets"].items():
+        reset_mask[s, ids] = True
+    out["reset_mask"] = reset_mask
+    for s in range(T):
+        ids = np.nonzero(reset_mask[s])[0]
+        if len(ids):
+            eng.reset(torch.tensor(ids, dtype=torch.long))
+        for ci in range(counts.shape[-1]):
+            n = torch.from_numpy(counts[s, :, :, ci])
+            for i in range(int(n.max())):
+                eng.submit(None, Requests(send=torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n))))
+        if dl_counts is not None:
+            for ci in range(dl_counts.shape[-1]):
+                n = torch.from_numpy(dl_counts[s, :, :, ci])
+                for i in range(int(n.max())):
+                    nb = torch.where(n > i, torch.full(n.shape, c["dl_sizes"][ci]), torch.zeros(n.shape))
+                    eng.add_dl_frames(None, nb, torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n)))
+        xs = torch.from_numpy(x[s])
+        eng.step(None, xs) if c["kind"] != "snr3" else eng.step(None, snr_db=xs)
+        out[f"s{s:03d}/queued"] = _np(eng.queued())
+        out[f"s{s:03d}/refused_env"] = _np(eng.net.refused_env)
+    col = eng.collect()
+    out["collect_keys"] = np.frombuffer(json.dumps(list(col.keys())).encode(), dtype=np.uint8)
+    for k, v in col.items():
+        out[f"collect/{k}"] = _np(v) if torch.is_tensor(v) else np.int64(v)
+    np.savez_compressed(os.path.join(HERE, f"stats_{name[len('stats_'):]}.npz"), **out)
+    print(name, {k: (tuple(v.shape) if torch.is_tensor(v) else v) for k, v in col.items()})
 
 
 def run_wifi_case(name, c):
@@ -464,7 +536,7 @@ def rng_vectors():
 
 if __name__ == "__main__":
     torch.set_num_threads(1)
-    names = sys.argv[1:] or list(CASES) + list(WIFI_CASES) + ["eventsim"]
+    names = sys.argv[1:] or list(CASES) + list(WIFI_CASES) + list(STATS_CASES) + ["eventsim"]
     if not sys.argv[1:]:
         rng_vectors()
         phy_tables()
@@ -475,5 +547,7 @@ if __name__ == "__main__":
             checkpoint_vectors(n[len("ckpt_"):])
         elif n in WIFI_CASES:
             run_wifi_case(n, WIFI_CASES[n])
+        elif n in STATS_CASES:
+            run_stats_case(n, STATS_CASES[n])
         else:
             run_case(n, CASES[n])
