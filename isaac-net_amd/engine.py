@@ -645,11 +645,7 @@ class HipNREngine:
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
-        if self.R > 64 and kind == 2:
-            raise HipUnsupported("per-subband SNR input with more than 64 robots per env")
-        if self.C > 1 and kind != 0:
-            raise ValueError("several cells: pass poses [E,R,2|3] (the path gain of every robot-cell link comes from "
-                             "the radio)")
+        self._check_kind(kind)
         plan = self._plan(T, kind)
         dl = None
         if self.dl:
@@ -698,6 +694,13 @@ class HipNREngine:
         if tuple(xin.shape) != want:
             raise ValueError(f"input must have shape {want}, got {tuple(xin.shape)}")
         return kind, xin
+
+    def _check_kind(self, kind):
+        if self.R > 64 and kind == 2:
+            raise HipUnsupported("per-subband SNR input with more than 64 robots per env")
+        if self.C > 1 and kind != 0:
+            raise ValueError("several cells: pass poses [E,R,2|3] (the path gain of every robot-cell link comes from "
+                             "the radio)")
 
     def _schedule(self, g0):
         """cfg.schedule(g0), cached by g0 modulo the period of the TDD pattern, SR and CQI occasions."""
@@ -790,12 +793,10 @@ class HipNREngine:
         self._last_snr = o["sinr_db"]
 
     def graph_step(self, n_cls=None):
-        """Record one control step (submit_counts of per-class arrival counts, then step on poses) in a HIP graph.
-        Returns a GraphStep; calling it with (poses [E,R,2|3], counts [E,R,NC]) replays the step. The schedule of
-        every replayed step must match the recorded one (the same TDD / SR / CQI phase and fading slot spacing),
-        which holds when the control step spans whole periods."""
-        if self.dl or self.C > 1:
-            raise HipUnsupported("graph_step with the downlink (dl=True) or several cells: use step()")
+        """The control step (submit_counts of per-class arrival counts, then step) as HIP graph replays: returns a
+        GraphStep, called as g(x, counts) or g(counts=..., snr_db=...) in place of submit_counts + step. A graph is
+        recorded for every new slot schedule (TDD / SR / CQI phase, fading slot spacing) and input kind, then
+        replayed; the downlink and several cells run inside the step graph."""
         return GraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     # ------------------------------------------------------------------ statistics
@@ -1266,42 +1267,65 @@ def state_dict(eng):
 
 
 class GraphStep:
-    """submit_counts + step of a HipNREngine, recorded once as two HIP graphs (torch.cuda.CUDAGraph: the enqueue,
-    then the step kernel) and replayed every control step.
+    """submit_counts + step of a HipNREngine as HIP graphs (torch.cuda.CUDAGraph), recorded on first use and replayed
+    at every control step: one graph for the enqueue, and one step graph per slot schedule (TDD / SR / CQI phase and
+    fading slot spacing) and input kind, as the reference's graph backend keeps one captured step per key
+    (isaac_net/core/nr_fast.py:435-489). The step graph holds the downlink step before the uplink one with
+    NRConfig(dl=True) (DL frames are enqueued eagerly with add_dl_frames, as the reference's fast engine enqueues them
+    outside its graph) and the several-cells step with n_cells > 1.
 
     The recorded launches read the control step from the engine's device clock (InetNrState.clock), which the
-    replay sets to the engine's T; the inputs are copied into the graphs' static buffers; the returned dict is the
-    static output buffers, overwritten by the next replay. The graphs hold kernel nodes only (no memset node)."""
+    replay sets to the engine's T; the inputs are copied into static buffers; the returned dict is the step graph's
+    static output buffers, overwritten by its next replay. The graphs hold kernel nodes only (no memset node).
+    With log_stats on, the statistics of the enqueue and of the resolved frames are taken around the replays."""
 
     def __init__(self, eng, n_cls):
         E, R, dev = eng.E, eng.R, eng.dev
         self.eng = eng
         self.counts = torch.zeros(E, R, n_cls, dtype=torch.uint8, device=dev)
-        self.x = torch.zeros(E, R, 2, dtype=torch.float32, device=dev)
-        self.plan = eng._plan(eng.T, 0)
+        self.inputs = {}                      # input kind -> static input buffer
+        self.steps = {}                       # (schedule key incl. the kind, DL delay buffer) -> (graph, outputs)
         eng.st["clock"].fill_(eng.T)
         torch.cuda.synchronize(dev)
-        self.g_submit, self.g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        ev, eng.kernel_events = eng.kernel_events, None
-        try:
-            with torch.cuda.graph(self.g_submit):
-                eng._launch_submit_counts(-1, self.counts)
-            self.hid = eng._last_hid
-            with torch.cuda.graph(self.g_step):
-                self.out = eng._launch_step(-1, self.plan, self.x, self.hid)
-        finally:
-            eng.kernel_events = ev
+        self.g_submit = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.g_submit):
+            eng._launch_submit_counts(-1, self.counts)
+        self.hid = eng._last_hid              # the submit graph's hazard ids (zeros), read by the step graphs
         torch.cuda.synchronize(dev)
 
-    def __call__(self, x, counts):
+    def _record(self, plan, kind):
+        eng = self.eng
+        x = self.inputs[kind]
+        torch.cuda.synchronize(eng.dev)
+        g = torch.cuda.CUDAGraph()
+        ev, dev_ = eng.kernel_events, eng.dl_kernel_events
+        eng.kernel_events = eng.dl_kernel_events = None
+        try:
+            with torch.cuda.graph(g):
+                out = eng._launch_step(-1, plan, x, self.hid, (kind, x, 1) if eng.dl else None)
+        finally:
+            eng.kernel_events, eng.dl_kernel_events = ev, dev_
+        torch.cuda.synchronize(eng.dev)
+        return g, out
+
+    def __call__(self, x=None, counts=None, *, snr_db=None):
+        """One control step: counts [E,R,NC] uint8 messages per class (as submit_counts), then the step on poses
+        x [E,R,2|3], SNR x [E,R] or snr_db= [E,R,S] (with the downlink: its reference from the same input)."""
         eng = self.eng
         T = eng.T
-        plan = eng._plan(T, 0)
-        if plan["key"] != self.plan["key"]:
-            raise HipUnsupported(f"step {T} has another slot schedule than the recorded step; use step()")
-        if tuple(counts.shape) != tuple(self.counts.shape):
+        kind, xin = eng._input(x, snr_db)
+        eng._check_kind(kind)
+        if counts is None or tuple(counts.shape) != tuple(self.counts.shape):
             raise ValueError(f"counts must be {tuple(self.counts.shape)}")
-        self.x.copy_(x[..., :2])
+        if kind not in self.inputs:
+            self.inputs[kind] = torch.empty_like(xin)
+        self.inputs[kind].copy_(xin)
+        plan = eng._plan(T, kind)
+        key = (plan["key"], 0 if eng._dl_delay is None else eng._dl_delay.data_ptr())
+        hit = self.steps.get(key)
+        if hit is None:
+            hit = self.steps[key] = self._record(plan, kind)
+        g, out = hit
         self.counts.copy_(counts)
         eng.st["clock"].fill_(T)
         if eng._log_stats:
@@ -1311,13 +1335,13 @@ class GraphStep:
         ev = eng.kernel_events
         if ev is not None:
             ev.begin(torch.cuda.current_stream(eng.dev))
-        self.g_step.replay()
+        g.replay()
         if ev is not None:
             ev.end(torch.cuda.current_stream(eng.dev))
         if eng._log_stats:
-            eng._stats_step(self.out)
-        eng._commit(T, self.plan, self.out)
-        return self.out
+            eng._stats_step(out)
+        eng._commit(T, plan, out)
+        return out
 
 
 class KernelTimer:

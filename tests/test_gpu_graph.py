@@ -49,17 +49,28 @@ def test_graph_replay_matches_eager():
     assert a.counters() == b.counters()
 
 
-def test_graph_step_refuses_another_schedule():
+def test_graph_records_one_step_per_schedule():
+    """With 3 slots per control step the TDD phase moves from step to step: the graph step records one graph per
+    schedule key and replays each, bitwise equal to eager launches over two periods of the pattern."""
     P = load_package()
     from isaac_net_amd import scenarios as S
     E, R = 8, 32
-    cfg = S.rl_scale_config(control_step_ms=1.5)        # 3 slots per step: the TDD phase moves from step to step
-    eng = P.make_engine("L2", E, R, "cuda:0", cfg, seed=0)
-    pos = torch.rand(E, R, 2, device="cuda:0") * 100
-    cnt = torch.zeros(E, R, 2, dtype=torch.uint8, device="cuda:0")
-    eng.submit_counts(cnt)
-    eng.step(None, pos)
-    g = eng.graph_step()
-    with pytest.raises(P.HipUnsupported if hasattr(P, "HipUnsupported") else Exception):
-        for _ in range(6):
-            g(pos, cnt)
+    cfg = S.rl_scale_config(control_step_ms=1.5)
+    a = P.make_engine("L2", E, R, "cuda:0", cfg, seed=0)
+    b = P.make_engine("L2", E, R, "cuda:0", cfg, seed=0)
+    g = b.graph_step()
+    gen = torch.Generator().manual_seed(5)
+    for s in range(12):
+        pos = (torch.rand(E, R, 2, generator=gen) * 100).to("cuda:0")
+        cnt = (torch.rand(E, R, 2, generator=gen) < 0.3).to(torch.uint8).to("cuda:0")
+        a.submit_counts(cnt)
+        oa = a.step(None, pos)
+        ob = g(pos, cnt)
+        torch.cuda.synchronize()
+        for k in oa:
+            assert _same(oa[k], ob[k]), (s, k)
+        sa, sb = a.owner_state(), b.owner_state()
+        for k in sa:
+            if torch.is_tensor(sa[k]):
+                assert _same(sa[k], sb[k]), (s, k)
+    assert 1 < len(g.steps) <= 12

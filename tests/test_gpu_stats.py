@@ -114,31 +114,36 @@ def test_clear_stats_and_switching_off():
     assert int(eng.refused_env.sum()) == 0
 
 
-def test_counts_form_and_fused_arrivals_log_as_single_submits():
-    """submit_counts and step(arrivals=) record the statistics of the submit() calls they stand for (class by
-    class, message by message): the same collect() and refused_env as the single form on the stats_ul inputs."""
+def test_counts_form_fused_arrivals_and_graph_log_as_single_submits():
+    """submit_counts, step(arrivals=) and the graph step record the statistics of the submit() calls they stand for
+    (class by class, message by message): the same collect() and refused_env as the single form on the stats_ul
+    inputs."""
     z, cfgd, _ = _load("stats_ul")
     single = _engine(z, cfgd)
     _drive(single, z)
     ref = single.collect()
     T, counts, x, resets = int(z["steps"]), z["counts"], z["x"], z["reset_mask"]
-    for fused in (False, True):
+    for mode in ("counts", "fused", "graph"):
         eng = _engine(z, cfgd)
+        g = eng.graph_step() if mode == "graph" else None
         for s in range(T):
             ids = np.nonzero(resets[s])[0]
             if len(ids):
                 eng.reset(torch.tensor(ids, dtype=torch.long))
             cnt = torch.from_numpy(counts[s]).to(DEV, torch.uint8)
-            if fused:
-                eng.step(None, torch.from_numpy(x[s]).to(DEV), arrivals=cnt)
+            xs = torch.from_numpy(x[s]).to(DEV)
+            if mode == "fused":
+                eng.step(None, xs, arrivals=cnt)
+            elif mode == "graph":
+                g(xs, cnt)
             else:
                 eng.submit_counts(cnt)
-                eng.step(None, torch.from_numpy(x[s]).to(DEV))
+                eng.step(None, xs)
         col = eng.collect()
         assert list(col) == list(ref)
         for k, v in ref.items():
             if torch.is_tensor(v):
-                assert torch.equal(col[k], v), (fused, k)
+                assert torch.equal(col[k], v), (mode, k)
             else:
-                assert col[k] == v, (fused, k)
-        assert torch.equal(eng.refused_env, single.refused_env), fused
+                assert col[k] == v, (mode, k)
+        assert torch.equal(eng.refused_env, single.refused_env), mode
