@@ -6,6 +6,9 @@
     python bench.py --workload mc_interf     (three cells with UL interference, 1024 envs x 64 robots: robot-slots/s)
     python bench.py --workload freq_sel      (16384 envs x 128 robots, 273 PRB in 8 RBGs, K = 20: robot-slots/s)
     python bench.py --summarize-counters DIR KERNEL NAME   (rocprofv3 --pmc CSVs under DIR -> profiles/NAME.json)
+    python bench.py --phase-clocks [...]     (loads libinet_nr_phase.so, built by isaac-net_amd/build.py
+                                              --phase-clocks, and adds the step kernel's per-phase clocks of the last
+                                              launch to the line; its timings are not the product library's)
 
 A step is one control step of every env: this step's message arrivals and step (poses in, the reference's output dict
 out), one launch of the fused step kernel that enqueues the arrivals first (--separate-submit: submit_counts and step,
@@ -412,6 +415,9 @@ def run_mc(args, P, torch):
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
                         "note": "arithmetic-bound kernel: frac is the distance from the HBM bound"}}
+    if args.phase_clocks:
+        rb = 1 << (R - 1).bit_length()                   # robots per segment: the next power of two
+        res["phase_clocks"] = phase_clocks("mc", (E * rb + 63) // 64)
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
@@ -468,11 +474,44 @@ def run_freq_sel(args, P, torch):
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
                         "layout_bytes_per_launch": layout_bytes, "layout_bytes_per_robot_step": layout_per_robot}}
+    if args.phase_clocks:
+        res["phase_clocks"] = phase_clocks("w2", 2 * E)
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, 128), min(args.cpu_steps, 3), 1)
     print(json.dumps(res), flush=True)
+
+
+PHASES = ("prologue", "fading draws", "SR/grants/estimate/MCS/metric", "retx admission", "RBG allocation",
+          "link adaptation", "binding/CSI gains/interference", "decoding", "HARQ/OLLA/PF/counters/RLC pointer",
+          "epilogue frames", "empty-slot outputs/compaction", "stores/env reductions")
+
+
+def phase_clocks(unit, n_waves):
+    """Per-phase shader clocks (s_memtime cycles) of every wavefront of the last step-kernel launch of the phase build
+    (unit: the translation unit that holds the kernel): the mean wave, the slowest wave and the phases' shares."""
+    import ctypes
+    import numpy as np
+    from isaac_net_amd import _lib
+    lib = _lib.load()
+    fn = getattr(lib, f"inet_nr_phase_clocks_{unit}")
+    fn.restype = ctypes.c_int
+    a = np.zeros((n_waves, len(PHASES)), dtype=np.uint64)
+    rc = fn(a.ctypes.data_as(ctypes.c_void_p), ctypes.c_int(n_waves))
+    if rc != 0:
+        raise RuntimeError(f"inet_nr_phase_clocks_{unit}: {rc}")
+    a = a.astype(np.float64)
+    tot = a.sum(1)
+    slow = int(tot.argmax())
+    top = np.argsort(tot)[-max(1, n_waves // 100):]          # the slowest 1% of the waves
+    return {"unit": "cycles (s_memtime)", "waves": n_waves,
+            "wave_total": {"min": float(tot.min()), "median": float(np.median(tot)), "mean": float(tot.mean()),
+                           "max": float(tot.max())},
+            "phases": {name: {"mean": float(a[:, i].mean()), "slowest_wave": float(a[slow, i]),
+                              "slowest_1pct_mean": float(a[top, i].mean()),
+                              "share_mean": float(a[:, i].mean() / tot.mean())}
+                       for i, name in enumerate(PHASES)}}
 
 
 def summarize_counters(d, kernel, name):
@@ -527,6 +566,8 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize-counters":
         load_package()
         return summarize_counters(sys.argv[2], sys.argv[3], sys.argv[4])
+    if "--phase-clocks" in sys.argv:
+        os.environ["INET_NR_LIB"] = os.path.join(ROOT, "isaac-net_amd", "libinet_nr_phase.so")
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -549,6 +590,8 @@ def main():
                     help="enqueue each step's arrivals with submit_counts (its own launch) instead of inside the step")
     ap.add_argument("--cpu-envs", type=int, default=2048)
     ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--phase-clocks", action="store_true",
+                    help="load libinet_nr_phase.so and add the step kernel's per-phase clocks to the line")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB three times (a plain copy kernel of known "
                          "size, the calibration of the HBM byte counters)")
@@ -639,6 +682,8 @@ def main():
                         "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean,
                         "valu_issue_util": valu_util,
                         "counters_src": cs.get("src") if cs else None}}
+    if args.phase_clocks:
+        res["phase_clocks"] = phase_clocks("s13" if eng.S == 13 else "s8", (E * R + 63) // 64)
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)

@@ -6,7 +6,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libinet_nr.so")
+# INET_NR_LIB names another build of the same sources (bench.py --phase-clocks loads libinet_nr_phase.so)
+LIB_PATH = os.environ.get("INET_NR_LIB") or os.path.join(HERE, "libinet_nr.so")
 
 P = C.c_void_p
 i32, i64, f32, u32 = C.c_int32, C.c_int64, C.c_float, C.c_uint32
@@ -127,6 +128,9 @@ def load(path=LIB_PATH):
         return _LIB
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is missing: build it with `python isaac-net_amd/build.py` (hipcc, gfx950)")
+    # torch ships its own HIP runtime: it must be the one this library binds to (loaded first, the library would bind
+    # the system's, and its launches on torch's streams would fail)
+    import torch  # noqa: F401
     lib = C.CDLL(path)
     lib.inet_nr_abi_version.restype = i32
     lib.inet_nr_build_info.restype = C.c_char_p

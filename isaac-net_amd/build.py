@@ -1,6 +1,7 @@
 """Build libinet_nr.so (the C-ABI HIP library) in-tree for gfx950.
 
     python isaac-net_amd/build.py            # or __graft_entry__.build()
+    python isaac-net_amd/build.py --phase-clocks   # libinet_nr_phase.so: the step kernels with per-phase clocks
 
 The step-kernel instantiations are split over translation units (one per subband count) that compile in parallel
 and link into one shared library. Flags: -ffp-contract=off keeps every float multiply and add separately rounded
@@ -16,6 +17,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libinet_nr.so")
+PHASE_LIB = os.path.join(HERE, "libinet_nr_phase.so")
 UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip", "nr_step_mc.hip", "nr_step_w2.hip", "wifi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
@@ -36,14 +38,18 @@ def source_hash():
     return h.hexdigest()[:16]
 
 
-def build(verbose=False, out_dir=None):
-    obj_dir = out_dir or os.path.join(HERE, "_build")
+def build(verbose=False, out_dir=None, phase_clocks=False):
+    """Compile every unit and link the library. phase_clocks: the same sources with INET_PHASE_CLOCKS defined (every
+    step-kernel wavefront records the shader clock spent in each phase of the step), linked as libinet_nr_phase.so
+    for bench.py --phase-clocks; the product library is not touched."""
+    obj_dir = out_dir or os.path.join(HERE, "_build_phase" if phase_clocks else "_build")
     os.makedirs(obj_dir, exist_ok=True)
     src = source_hash()
+    extra = ["-DINET_PHASE_CLOCKS"] if phase_clocks else []
 
     def compile_unit(u):
         obj = os.path.join(obj_dir, u.replace(".hip", ".o"))
-        cmd = [HIPCC, *FLAGS, f'-DINET_SRC_HASH="{src}"', "-c", "-o", obj, os.path.join(CSRC, u)]
+        cmd = [HIPCC, *FLAGS, *extra, f'-DINET_SRC_HASH="{src}"', "-c", "-o", obj, os.path.join(CSRC, u)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
@@ -51,14 +57,15 @@ def build(verbose=False, out_dir=None):
 
     with cf.ThreadPoolExecutor(len(UNITS)) as ex:
         objs = list(ex.map(compile_unit, UNITS))
-    tmp = LIB + ".tmp"
+    lib = PHASE_LIB if phase_clocks else LIB
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, phase_clocks="--phase-clocks" in sys.argv))

@@ -29,6 +29,50 @@
 
 namespace inet {
 
+// Phase clocks (a build option, off in the product library: build.py --phase-clocks writes libinet_nr_phase.so).
+// With INET_PHASE_CLOCKS defined, every wavefront of the step kernel adds the shader clock (s_memtime) spent in each
+// phase of the step to its own row of g_phase_clk [wave][INET_NPH] (vector stores at the end), read back
+// by inet_nr_phase_clocks_<unit> of the translation unit that holds the kernel (each unit has its own array). The
+// marks sit at wave-uniform points, so the counts are wave totals; the work is unchanged.
+constexpr int INET_NPH = 12;
+constexpr int INET_PH_WAVES = 1 << 16;
+#ifdef INET_PHASE_CLOCKS
+static __device__ uint64_t g_phase_clk[INET_PH_WAVES * INET_NPH];
+// the running sums live in one VGPR (lane i holds phase i, a select and an add, no branch) and the
+// last mark in one scalar register (the low 32 bits of the clock), so that the build keeps the product kernel's
+// register allocation as far as possible
+#ifndef INET_PH_MASK
+#define INET_PH_MASK 0xfff
+#endif
+#define INET_PH_DECL                                                                                               \
+    uint32_t ph_v = 0u;                                                                                            \
+    uint32_t ph_t0 = (uint32_t)__builtin_amdgcn_s_memtime();
+#define INET_PH(i)                                                                                                 \
+    if (((INET_PH_MASK) >> (i)) & 1) do {                                                                          \
+        const uint32_t _t = (uint32_t)__builtin_amdgcn_s_memtime();                                                \
+        ph_v += (threadIdx.x & 63) == (i) ? _t - ph_t0 : 0u;                                                       \
+        ph_t0 = _t;                                                                                                \
+    } while (0)
+#define INET_PH_STORE                                                                                              \
+    do {                                                                                                           \
+        const unsigned wv = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);                                    \
+        if ((threadIdx.x & 63) < INET_NPH && wv < (unsigned)INET_PH_WAVES)                                         \
+            g_phase_clk[(size_t)wv * INET_NPH + (threadIdx.x & 63)] = ph_v;                                        \
+    } while (0)
+// copies the first n_waves rows to the host (0, or the HIP error)
+#define INET_PHASE_READER(NAME)                                                                                     \
+    extern "C" int NAME(uint64_t* out, int n_waves) {                                                              \
+        if (n_waves < 0 || n_waves > inet::INET_PH_WAVES) return -1;                                               \
+        return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(inet::g_phase_clk),                                        \
+                                        sizeof(uint64_t) * inet::INET_NPH * n_waves, 0, hipMemcpyDeviceToHost);     \
+    }
+#else
+#define INET_PH_DECL
+#define INET_PH(i) do { } while (0)
+#define INET_PH_STORE do { } while (0)
+#define INET_PHASE_READER(NAME)
+#endif
+
 constexpr int STEP_WAVE = 64;          // one wavefront per workgroup
 constexpr int MAX_UL_ROWS = 64;        // UL data slots per control step
 constexpr int MAX_M = 32;              // MCS table rows
@@ -118,6 +162,22 @@ DEV int seg_first(bool p, int rb, int lane) {
     unsigned long long b = __ballot(p) >> (lane & ~(rb - 1));
     if (rb < 64) b &= (1ull << rb) - 1ull;
     return b ? (int)__builtin_ctzll(b) : rb;
+}
+
+// bit `lane` of a wave-uniform 64-bit mask, as a lane predicate (one v_cndmask on the mask in scalar registers)
+DEV bool lane_bit(unsigned long long m) {
+    int v;
+    asm volatile("v_cndmask_b32_e64 %0, 0, 1, %1" : "=v"(v) : "s"(m));
+    return v != 0;
+}
+// two 32-lane segments per wavefront (envs of 17..32 robots): per segment, the lowest set bit of a wave-uniform mask
+// (scalar ALU), and whether the segment has any bit set, as 64-bit lane masks
+DEV unsigned long long seg32_lowest(unsigned long long b) {
+    const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+    return (unsigned long long)(lo & (0u - lo)) | ((unsigned long long)(hi & (0u - hi)) << 32);
+}
+DEV unsigned long long seg32_any(unsigned long long b) {
+    return ((uint32_t)b ? 0xffffffffull : 0ull) | ((b >> 32) ? 0xffffffff00000000ull : 0ull);
 }
 
 // ---------------------------------------------------------------- ATen-order sums over the RBGs a robot holds
@@ -251,9 +311,10 @@ DEV T sel_of(const T (&v)[N], int idx) {
 // compile-time constants, which removes their tests from the slot loop and the scalar registers that hold them.
 template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC, int FX = 0>
 __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
-    InetNrState st, LS lk, InetNrTables tb_in, InetNrParams pm_in, const InetNrRow* __restrict__ rows, int n_rows,
+    InetNrState st, LS lk_in, InetNrTables tb_in, InetNrParams pm_in, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
+    INET_PH_DECL
     InetNrParams pm = pm_in;
     InetNrTables tb = tb_in;
     if constexpr (FX == 1 || FX == 2) {
@@ -261,6 +322,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
+    // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
+    const LS& lk = [&]() -> const LS& { if constexpr (DL) return lk_in; else return st; }();
     constexpr bool MC = NC > 1;
     static_assert(!(MC && (DL || VREF)), "several cells: the UL with pose input");
     constexpr int W = RBT > STEP_WAVE ? 2 : 1;         // wavefronts per env
@@ -274,7 +337,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ __align__(16) float s_thrs[MAX_M];                // suffix minima of s_thr (the MCS search table)
     __shared__ __align__(16) float s_se[MAX_M];
     __shared__ float s_beta[MAX_M], s_rbeta[MAX_M], s_rate[MAX_M];
-    __shared__ float s_w[S], s_logw[S], s_wdb[S];
+    __shared__ float s_w[S], s_logw[S], s_wdb[S], s_lnw[S + 1];
     __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
     __shared__ int s_ulrel[MAX_UL_ROWS];
     // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
@@ -324,7 +387,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         __syncthreads();
     };
     auto env_any = [&](bool p) -> bool {
-        if constexpr (W == 1) {
+        if constexpr (RBT == 32) {
+            return lane_bit(seg32_any(__ballot(p)));
+        } else if constexpr (W == 1) {
             return seg_any(p, rb, lane);
         } else {
             int a0, a1;
@@ -374,11 +439,22 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     // "the highest m <= mcs_max with x >= thr[m]" is the highest m with x >= min(thr[m..mcs_max]): these suffix
     // minima are non-decreasing, so a binary search over them gives the linear scan's result for any table. Past
     // mcs_max the entries are NaN, which no comparison passes (not even x = +inf).
-    if (lane < MAX_M) {
-        float v = INFINITY;
-        for (int j = tb.mcs_max; j >= lane; --j) v = fminf(v, s_thr[j]);
-        s_thrs[lane] = lane <= tb.mcs_max ? v : __builtin_nanf("");
+    // (a suffix-minimum scan over lanes 0..31, every lane taking part in the lane reads)
+    {
+        float v = (wl < MAX_M && wl <= tb.mcs_max) ? s_thr[wl] : INFINITY;
+#pragma unroll
+        for (int off = 1; off < MAX_M; off <<= 1) {
+            const float o = __shfl_down(v, off, 64);
+            v = wl + off < MAX_M ? fminf(v, o) : v;
+        }
+        if (lane < MAX_M) s_thrs[lane] = lane <= tb.mcs_max ? v : __builtin_nanf("");
     }
+    // log of the held PRB count by count of held RBGs, when every RBG has the same width: the log-sum-exp over the
+    // held RBGs then adds exp(0) = 1 once per RBG, so it depends only on that count (s_lnw[n])
+    if (lane <= S) s_lnw[lane] = lse_logw<S>(s_logw, lane >= 32 ? ~0u : ((1u << lane) - 1u));
+    bool lw_eq = true;
+#pragma unroll
+    for (int s = 1; s < S; ++s) lw_eq = lw_eq && s_logw[s] == s_logw[0];
     __syncthreads();
 
     // ---------------- load per-robot state ----------------
@@ -641,6 +717,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     const int last_ul_row = m_ul ? 63 - __builtin_clzll(m_ul) : -1;
     const int last_h_row = m_h ? 63 - __builtin_clzll(m_h) : -1;
     const bool iid = m_corr == 0ull;
+    INET_PH(0);                                    // prologue: tables, state loads, arrivals, radio
     // ================================================================ slot loop
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
@@ -697,6 +774,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 s_z[(2 * qc) * CW + Lc] = zr;
                 s_z[(2 * qc + 1) * CW + Lc] = zi;
             }
+            INET_PH(1);                            // fading innovations (the robots' own updates follow)
             __syncthreads();
             if (draw) {
 #pragma unroll
@@ -769,7 +847,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 if ((enq - sent) > 0 && bsr <= 0 && sr_t < 0) sr_t = g;
             }
         }
-        if (!(row.flags & 2)) continue;
+        if (!(row.flags & 2)) { INET_PH(2); continue; }
         // ============================ data slot (MacLink.slot) ============================
         // several cells (nr_engine.py:757-766): the UL reference of the serving link per subband against the serving
         // gNB's N+I estimate, the PHR cap from its noise-only SNR, the power-control backoff, this row's cells
@@ -821,6 +899,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 const int m0 = s_xw[0], f0 = s_xw[1], m1 = s_xw[2], f1 = s_xw[3];
                 __syncthreads();
                 return m >= 0 && lane == (m0 >= m1 ? f0 : STEP_WAVE + f1);
+            } else if constexpr (RBT == 32) {
+                // the first lane of each 32-lane segment holding the maximum, found on the scalar unit
+                const int mx = bmax_i(m, 32);
+                return m >= 0 && lane_bit(seg32_lowest(__ballot(m == mx)));
             } else {
                 const int mx = bmax_i(m, rb);
                 const int f = seg_first(m == mx, rb, lane);             // (every lane takes part in the ballot)
@@ -861,70 +943,78 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         int rx_nsb = 0;
 #pragma unroll
         for (int p = 0; p < P; ++p) rx_nsb = p == rx_p ? hm_nsb(hmeta[p]) : rx_nsb;
-        // scheduler estimate with OLLA -> MCS -> rate per RBG (mac_ul.py:154-171, mac.py:256-275)
-        float rate[S];
-        {
-            float eo[S];
-            int mi[S];
-#pragma unroll
-            for (int s = 0; s < S; ++s) {
-                // UL: the PSD over one RBG, at most the power-control PSD (mac_ul.py:154-171); DL: sinr_ref + csi
-                // (mac_dl.py:42-43)
-                const float wd = MC ? (s_wdb[s] > pc ? s_wdb[s] : pc) : s_wdb[s];
-                float est = DL ? REF(s) + csi[s] : (REF(s) - wd) + csi[s];
-                eo[s] = pm.olla ? est + olla : est;
-                mi[s] = 0;
-            }
-            {
-                // highest m <= mcs_max with eo >= thr[m] (0 when none, or NaN): a binary search over the suffix
-                // minima, whose first three levels compare with the same seven values in every lane (broadcast
-                // LDS reads), then a count of the values passed in the last block of four and a branch-free
-                // selection of the spectral efficiency (the S lookups are independent of each other)
-                const float t16 = s_thrs[16], t8 = s_thrs[8], t24 = s_thrs[24];
-                const float t4 = s_thrs[4], t12 = s_thrs[12], t20 = s_thrs[20], t28 = s_thrs[28];
-#pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    const float e = eo[s];
-                    int m = e >= t16 ? 16 : 0;
-                    m += e >= (m ? t24 : t8) ? 8 : 0;
-                    m += e >= (m < 16 ? (m < 8 ? t4 : t12) : (m < 24 ? t20 : t28)) ? 4 : 0;
-                    mi[s] = m;
-                }
-#pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    // the block's search values and spectral efficiencies, read together (the empty asm keeps the
-                    // values in registers, so that the selection below stays branch-free)
-                    float4 q = *reinterpret_cast<const float4*>(&s_thrs[mi[s]]);
-                    float4 g = *reinterpret_cast<const float4*>(&s_se[mi[s]]);
-                    asm("" : "+v"(q.y), "+v"(q.z), "+v"(q.w), "+v"(g.x), "+v"(g.y), "+v"(g.z), "+v"(g.w));
-                    const float e = eo[s];
-                    const int k = (e >= q.y ? 1 : 0) + (e >= q.z ? 1 : 0) + (e >= q.w ? 1 : 0);
-                    float se = g.x;
-                    se = k >= 1 ? g.y : se;
-                    se = k >= 2 ? g.z : se;
-                    se = k >= 3 ? g.w : se;
-                    rate[s] = ((se * row.re_prb) * s_w[s]) / 8.0f;
-                }
-            }
-        }
-        // the scheduler metric per RBG (mac.py:267-275: PF, max C/I, RR) into LDS (rows 0..S-1 of s_x, this lane's
-        // column) for the allocation loop
+        // Scheduler estimate with OLLA -> MCS -> rate -> metric per RBG (mac_ul.py:154-171, mac.py:256-275), for the
+        // robots that can bid in this slot (a retransmission ready or new data with a free process; the others'
+        // rates and metrics are never read). Each such robot writes its estimate row to LDS; the (robot, RBG) pairs
+        // are then dealt round-robin over the wavefront (subband-major, as the fading draws), and each pair's MCS,
+        // rate and metric land in the robot's LDS columns: the metric in rows 0..S-1 of s_x, the rate in s_lin (free
+        // until link adaptation). s_la_slot and s_la_f (the link adaptation work list) hold the list and the PF
+        // average or RR age until then.
         float* const s_met = s_x;
-        if (pm.sched == 0) {
-            const float avg_c = clamp_min(avg, 1e-9f);
-            // (rates in [0, 2^20], the average in [1e-9, 2^40]: DivBy gives the IEEE quotient)
-            const DivBy div_avg(avg_c);
+        float* const s_eo = s_x + S * CW;
+        float* const s_rt = s_lin;
+        {
+            const bool bid0 = has_rx || new_el;
+            if (bid0) {
 #pragma unroll
-            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = div_avg(rate[s]);
-        } else if (pm.sched == 1) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = rate[s];
-        } else {
-            const float age = (float)(g - last_tx);
-#pragma unroll
-            for (int s = 0; s < S; ++s) s_met[s * CW + lane] = age;
+                for (int s = 0; s < S; ++s) {
+                    // UL: the PSD over one RBG, at most the power-control PSD (mac_ul.py:154-171); DL: sinr_ref + csi
+                    // (mac_dl.py:42-43)
+                    const float wd = MC ? (s_wdb[s] > pc ? s_wdb[s] : pc) : s_wdb[s];
+                    const float est = DL ? REF(s) + csi[s] : (REF(s) - wd) + csi[s];
+                    s_eo[s * CW + lane] = pm.olla ? est + olla : est;
+                }
+                s_la_f[lane] = pm.sched == 0 ? clamp_min(avg, 1e-9f) : (float)(g - last_tx);
+            }
+            const unsigned long long bm = __ballot(bid0);
+            const int n_b = __popcll(bm);
+            if (bid0) s_la_slot[wbase + __popcll(bm & ((1ull << wl) - 1ull))] = lane;
+            __syncthreads();
+            // highest m <= mcs_max with eo >= thr[m] (0 when none, or NaN): a binary search over the suffix minima,
+            // whose first three levels compare with seven values held by every lane, then a count of the values
+            // passed in the last block of four and a branch-free selection of the spectral efficiency
+            const float t16 = s_thrs[16], t8 = s_thrs[8], t24 = s_thrs[24];
+            const float t4 = s_thrs[4], t12 = s_thrs[12], t20 = s_thrs[20], t28 = s_thrs[28];
+            const int items = n_b * S;
+            int q = 0, ri = 0, dq = 0, dr = 0;
+            if (n_b > 0) {
+                dq = STEP_WAVE / n_b;
+                dr = STEP_WAVE - dq * n_b;
+                q = wl / n_b;
+                ri = wl - q * n_b;
+            }
+#pragma unroll 1
+            for (int it = wl; it < items; it += STEP_WAVE) {
+                const int L = s_la_slot[wbase + ri], qc = q;
+                q += dq;
+                ri += dr;
+                if (ri >= n_b) { ri -= n_b; ++q; }
+                const float e = s_eo[qc * CW + L];
+                int m = e >= t16 ? 16 : 0;
+                m += e >= (m ? t24 : t8) ? 8 : 0;
+                m += e >= (m < 16 ? (m < 8 ? t4 : t12) : (m < 24 ? t20 : t28)) ? 4 : 0;
+                // the block's search values and spectral efficiencies, read together (the empty asm keeps the
+                // values in registers, so that the selection below stays branch-free)
+                float4 tq = *reinterpret_cast<const float4*>(&s_thrs[m]);
+                float4 gq = *reinterpret_cast<const float4*>(&s_se[m]);
+                asm("" : "+v"(tq.y), "+v"(tq.z), "+v"(tq.w), "+v"(gq.x), "+v"(gq.y), "+v"(gq.z), "+v"(gq.w));
+                const int k = (e >= tq.y ? 1 : 0) + (e >= tq.z ? 1 : 0) + (e >= tq.w ? 1 : 0);
+                float se = gq.x;
+                se = k >= 1 ? gq.y : se;
+                se = k >= 2 ? gq.z : se;
+                se = k >= 3 ? gq.w : se;
+                const float rt = ((se * row.re_prb) * s_w[qc]) / 8.0f;
+                // the metric (mac.py:267-275): PF rate / max(avg, 1e-9) (rates in [0, 2^20], the average in
+                // [1e-9, 2^40]: DivBy gives the IEEE quotient), max C/I the rate, RR the age
+                const float a = s_la_f[L];
+                const float mt = pm.sched == 0 ? DivBy(a)(rt) : (pm.sched == 1 ? rt : a);
+                s_met[qc * CW + L] = mt;
+                s_rt[qc * CW + L] = rt;
+            }
+            __syncthreads();
         }
         auto metric_of = [&](int s) -> float { return s_met[s * CW + lane]; };
+        INET_PH(2);                                // SR / CQI, grants, candidates, estimate, MCS, rate, metric
         // retransmission admission (mac.py:300-313): rank by the metric sum inside each scheduler, admit while the RBG
         // counts fit (the segment's total fitting implies every cell's)
         if (env_any(has_rx)) {
@@ -942,6 +1032,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                     s_rval[lane] = val;
                     __syncthreads();
                 }
+#pragma unroll 1
                 for (int j = 0; j < rb; ++j) {
                     float kj;
                     int vj;
@@ -954,9 +1045,18 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 has_rx = has_rx && cum <= S;
             }
         }
+        INET_PH(3);                                // retransmission admission
         const int want_cnt = has_rx ? rx_nsb : (new_el ? n_max : 0);
+        // RBG-by-RBG allocation (mac.py:322-352); the metric row is read into registers first, so that no bid waits
+        // for its LDS read
         const float prio = pm.retx_prio ? (has_rx ? 1e9f : 0.0f) : 0.0f;
-        // RBG-by-RBG allocation (mac.py:322-352)
+        float mrow[S], rate[S];                         // the bids' values (metric + retransmission priority), rates
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            mrow[s] = metric_of(s) + prio;
+            rate[s] = s_rt[s * CW + lane];
+            asm volatile("" : "+v"(mrow[s]), "+v"(rate[s]));
+        }
         int cnt = 0;
         float left = (float)need;
         uint32_t won = 0;
@@ -967,8 +1067,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             for (int s = 0; s < S; ++s) {
                 const bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
                 // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
-                const float ms = metric_of(s);          // (read by every lane, ahead of the bid)
-                int m = want ? __float_as_int(ms + prio) : -1;
+                int m = want ? __float_as_int(mrow[s]) : -1;
                 if constexpr (RP) {
                     const bool wr = want && has_rx;
                     if (cell_any(wr) && !wr) m = -1;
@@ -997,6 +1096,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 left = left - (sel ? rate[s] : 0.0f);
             }
         }
+        INET_PH(4);                                // RBG-by-RBG allocation
         const int n_sb = __popc(won);
         float n_prb = 0.f;
 #pragma unroll
@@ -1008,7 +1108,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         const float sp0 = 10.0f * log10_clamped(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
         const float sp = MC ? (sp0 > pc ? sp0 : pc) : sp0;
         // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
-        const float lnw = lse_logw<S>(s_logw, won);
+        const float lnw = lw_eq ? s_lnw[__popc(won)] : lse_logw<S>(s_logw, won);
         // ---- link adaptation for new TBs (phy.select_mcs): the highest MCS meeting the BLER target ----
         int mcs_new = 0, tbs_new = 0;
         bool any_new;                                  // (W = 2: both waves enter, the search has barriers)
@@ -1094,6 +1194,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 tbs_new = tb.la_tbs[toff + mcs_new];
             }
         }
+        INET_PH(5);                                // link adaptation (power split, lse of log w, MCS search)
         int cap_b = tbs_new / 8 - pm.tb_oh;
         cap_b = cap_b > 1 ? cap_b : 1;
         const int byt_new = cap_b < unsent ? cap_b : unsent;
@@ -1155,6 +1256,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 if (r == 0 && e < E) ion = ion + aten_row_sum(NCS, [&](int i) { return s_if[i] / cl.noise_mw; });
             }
         }
+        INET_PH(6);                                // binding, actual gains (CSI), interference
         // ---- decoding on the actual channel (mac.py:428-454, mac_ul.py:185-192) ----
         bool ok = false, fail = false, exh = false;
         float comb = comb_p, lexp = lexp_p, nrb = nrb_p;
@@ -1211,6 +1313,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             fail = tx && !ok;
             exh = fail && ntx >= pm.max_tx;
         }
+        INET_PH(7);                                // decoding
         // ---- HARQ state update (mac.py:456-477; UL timing mac_ul.py:218-219, DL mac_dl.py:47-49: decoded TBs wait
         // for their HARQ-ACK at the row's ACK slot, and both outcomes are known gnb_proc slots after it) ----
         int rdy_ok = g, rdy_fail = g + pm.ul_rtt, st_ok = 0;
@@ -1289,6 +1392,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             }
         }
         ++n_ul;
+        INET_PH(8);                                // HARQ / OLLA / PF update, counters, in-order pointer
     }
     const int n_hist = DL ? 0 : (n_ul < n_ul_max ? n_ul : n_ul_max);
 
@@ -1390,6 +1494,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             ++kept;
         }
     }
+    INET_PH(9);                                        // epilogue: frame replay, outputs, compaction
     if constexpr (DL) lost_new += lost_dl;             // marked in the slot loop
     // the slots past the queue get the outputs of an empty slot (not delivered / timed out / dropped, cap -1,
     // class 0, delay NaN): one frame at a time up to a multiple of 4, then 16-byte stores of 4 frames per array
@@ -1447,6 +1552,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         int un = enq - sent;
         bsr = bsr < un ? bsr : un;
     }
+    INET_PH(10);                                       // empty-slot outputs
     const int ack_new = ack_ptr();
     const int qb_end = enq - ack_new;                  // (queue_bytes: a difference of offsets)
     // The byte offsets stay in int32: once the floor reaches rebase_at, every offset of the robot moves down by the
@@ -1546,6 +1652,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         if (r == 0)
             for (int q = rb; q < 3 * HB; ++q) lk.hist[(size_t)e * 3 * HB + q] += my_hist[q];
     }
+    INET_PH(11);                                      // state stores, per-env reductions and counters
+    INET_PH_STORE;
 }
 
 // ---------------------------------------------------------------- launch plumbing

@@ -12,3 +12,5 @@ StepFn pick_step_mc(int S, int C, int P, bool ir, int fx) {
     return nullptr;
 }
 }  // namespace inet
+
+INET_PHASE_READER(inet_nr_phase_clocks_mc)

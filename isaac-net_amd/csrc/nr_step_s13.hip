@@ -6,3 +6,5 @@
 namespace inet {
 StepFn pick_step_s13(int P, bool ir, bool vref, int rb, int fx) { return pick_step_s<13>(P, ir, vref, rb, fx); }
 }  // namespace inet
+
+INET_PHASE_READER(inet_nr_phase_clocks_s13)

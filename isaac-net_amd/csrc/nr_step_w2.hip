@@ -10,3 +10,5 @@ StepFn pick_step_w2(int S, int P, bool ir, int fx) {
     return nullptr;
 }
 }  // namespace inet
+
+INET_PHASE_READER(inet_nr_phase_clocks_w2)
