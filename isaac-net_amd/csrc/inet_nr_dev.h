@@ -60,12 +60,32 @@ DEV float sqrt_pos(float x) {
     r = fmaf(-su, s, x) > 0.0f ? su : r;
     return x == 0.0f ? x : r;
 }
+// cos x for 0 <= x < 2 pi: the steps cosf takes for a finite argument below 2^17 (this build's device library):
+// x reduced by the nearest multiple j of pi / 2 in three parts, then the sine or cosine polynomial of the remainder by
+// the quadrant j mod 4. Without cosf's large-argument reduction and its NaN / infinity test, which never fire here.
+DEV float cos_small(float x) {
+    const float jf = rintf(x * __int_as_float(0x3f22f983));
+    const int j = (int)jf;
+    float r = fmaf(jf, __int_as_float(0xbfc90fda), x);
+    r = fmaf(jf, __int_as_float(0xb3a22168), r);
+    r = fmaf(jf, __int_as_float(0xa7c234c4), r);
+    const float r2 = r * r;
+    float sp = fmaf(r2, __int_as_float(0xb94c1982), __int_as_float(0x3c0881c4));
+    sp = fmaf(r2, sp, __int_as_float(0xbe2aaa9d));
+    const float sn = fmaf(r, r2 * sp, r);
+    float cp = fmaf(r2, __int_as_float(0x37d75334), __int_as_float(0xbab64f3b));
+    cp = fmaf(r2, cp, __int_as_float(0x3d2aabf7));
+    cp = fmaf(r2, cp, __int_as_float(0xbf000004));
+    const float cs = fmaf(r2, cp, 1.0f);
+    const float v = (j & 1) ? -sn : cs;
+    return __uint_as_float(__float_as_uint(v) ^ (((uint32_t)j << 30) & 0x80000000u));
+}
 // Box-Muller, cosine branch, from the hashes of elements 2j and 2j + 1 (u1 in [2^-24, 1], so -2 ln u1 is +-0 or a
-// normal float in [1.2e-7, 33.3])
+// normal float in [1.2e-7, 33.3]; 2 pi u2 in [0, 2 pi))
 DEV float normal_of(uint32_t h1, uint32_t h2) {
     float u1 = (float)((h1 >> 8) + 1u) * INV24;
     float u2 = (float)(h2 >> 8) * INV24;
-    return sqrt_pos(-2.0f * ln_unit(u1)) * cosf((float)6.283185307179586 * u2);
+    return sqrt_pos(-2.0f * ln_unit(u1)) * cos_small((float)6.283185307179586 * u2);
 }
 // element j of a normal draw uses hash elements 2j and 2j + 1
 DEV float normal_at(uint32_t base, uint32_t j) { return normal_of(elem_hash(base, 2u * j), elem_hash(base, 2u * j + 1u)); }

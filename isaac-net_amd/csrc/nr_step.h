@@ -346,8 +346,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ float s_lin[S * CW];                              // per-lane rows: linear RBG SINR
     __shared__ int s_la_i[2 * CW], s_la_slot[CW], s_la_top[CW];  // link adaptation work list
     __shared__ float s_la_f[3 * CW];
-    __shared__ uint8_t s_list[CW];                               // lanes that draw fading innovations this slot
-    __shared__ uint32_t s_bfe[STEP_WAVE];                        // per env of the workgroup: its fading key this slot
+    // robots that draw fading innovations this slot: (lane, hash offset of the robot's first element, env key)
+    __shared__ uint4 s_dlist[CW];
     __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
     __shared__ int s_rval[W > 1 ? CW : 1];
     __shared__ int s_xw[4];                                      // W = 2: the two waves' values of an env collective
@@ -739,38 +739,43 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             const bool draw = act && (full || busy);
             const unsigned long long need = __ballot(draw);              // (per wave: each draws its own robots)
             float* const s_z = s_x;
-            if (r == 0) s_bfe[eloc] = mix32(base0 ^ row.salt_fade);
-            if (draw) s_list[wbase + __builtin_popcountll(need & ((1ull << wl) - 1ull))] = (uint8_t)lane;
+            // the env's key of this slot, and the hash input of the robot's first element (robot r's normals start at
+            // element 2 NC S r, hash element 2 (2 NC S r) = 4 NC S r)
+            const uint32_t bf = mix32(base0 ^ row.salt_fade);
+            if (draw)
+                s_dlist[wbase + __builtin_popcountll(need & ((1ull << wl) - 1ull))] =
+                    make_uint4((uint32_t)lane, bf + (uint32_t)(4 * r * NCS) * GOLD, bf, 0u);
             __syncthreads();
             // pairs in subband-major order: the lanes of one pass write different robots' columns (no LDS bank
             // conflicts between the pairs of one robot)
             const int n_need = __builtin_popcountll(need);
             const int items = n_need * NCS;
-            // envs of 32 robots: the two keys of the wave from lanes 0 and 32; one env per wave or workgroup: its key
-            const uint32_t own_bf = mix32(base0 ^ row.salt_fade);
-            const uint32_t bf_lo = __builtin_amdgcn_readlane(own_bf, 0);
-            const uint32_t bf_hi = __builtin_amdgcn_readlane(own_bf, RBT == 32 ? 32 : 0);
             // item it = q n_need + ri (subband q of the ri-th drawing robot); a lane's items are 64 apart, so (q, ri)
-            // advance by (dq, dr) with one carry, and the next item's robot is read from the list ahead of its use
-            int q = 0, ri = 0, dq = 0, dr = 0, L = 0;
+            // advance by (dq, dr) with one carry, the subband's hash term 4 q GOLD with them, and the next item's
+            // robot is read from the list ahead of its use
+            int q = 0, ri = 0, dq = 0, dr = 0;
+            uint32_t qterm = 0u, dqterm = 0u;
+            uint4 ent = make_uint4(0u, 0u, 0u, 0u);
             if (n_need > 0) {
                 dq = STEP_WAVE / n_need;
                 dr = STEP_WAVE - dq * n_need;
                 q = wl / n_need;
                 ri = wl - q * n_need;
-                L = s_list[wbase + ri];
+                qterm = (uint32_t)(4 * q) * GOLD;
+                dqterm = (uint32_t)(4 * dq) * GOLD;
+                ent = s_dlist[wbase + ri];
             }
 #pragma unroll 1
             for (int it = wl; it < items; it += STEP_WAVE) {
-                const int Lc = L, qc = q;
+                const int Lc = (int)ent.x, qc = q;
+                const uint32_t hin = ent.y + qterm, bfc = ent.z;
                 q += dq;
                 ri += dr;
-                if (ri >= n_need) { ri -= n_need; ++q; }
-                L = s_list[wbase + ri];                       // (ri < n_need: a valid entry, read for the next item)
-                const uint32_t bf = RBT >= 32 ? (Lc < 32 ? bf_lo : bf_hi) : s_bfe[Lc / rb];
-                const uint32_t hin = bf + (uint32_t)(4 * (Lc & (rb - 1)) * NCS + 4 * qc) * GOLD;
-                const float zr = normal_of(mix32(mix32(hin) ^ bf), mix32(mix32(hin + GOLD) ^ bf));
-                const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bf), mix32(mix32(hin + 3u * GOLD) ^ bf));
+                qterm += dqterm;
+                if (ri >= n_need) { ri -= n_need; ++q; qterm += 4u * GOLD; }
+                ent = s_dlist[wbase + ri];                    // (ri < n_need: a valid entry, read for the next item)
+                const float zr = normal_of(mix32(mix32(hin) ^ bfc), mix32(mix32(hin + GOLD) ^ bfc));
+                const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bfc), mix32(mix32(hin + 3u * GOLD) ^ bfc));
                 s_z[(2 * qc) * CW + Lc] = zr;
                 s_z[(2 * qc + 1) * CW + Lc] = zi;
             }
