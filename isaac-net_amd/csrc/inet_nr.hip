@@ -266,7 +266,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
         if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
             return INET_NR_EINVAL;
         if (c.ttt < 0 || c.ho_int < 0 || !(c.noise_mw > 0.0f)) return INET_NR_EINVAL;
-        fn = inet::pick_step_mc(p.S, c.C, p.P, ir, fx);
+        fn = inet::pick_step_mc(p.S, c.C, p.P, ir, fx, rb);
     } else if (rb > inet::STEP_WAVE) {          // 65..128 robots: two wavefronts per env, UL
         if (dl || vref) return INET_NR_EUNSUPPORTED;
         fn = inet::pick_step_w2(p.S, p.P, ir, fx);

@@ -283,12 +283,17 @@ inline size_t step_lds_bytes(int n_ul, int harq_drop, int rb, int max_tx, int nc
                           (nc > 1 ? (cw / rb) * 2 * nc * S : 0));
 }
 
-// v[idx] of a register array indexed by a runtime value (a chain of selects, no scratch memory)
+// v[idx] of a register array indexed by a runtime value (a chain of selects, no scratch memory: the empty asm keeps
+// 32-bit elements in registers, where the compiler would otherwise turn the chain into a stack load)
 template <int N, class T>
 DEV T sel_of(const T (&v)[N], int idx) {
     T r = v[0];
 #pragma unroll
-    for (int i = 1; i < N; ++i) r = idx == i ? v[i] : r;
+    for (int i = 1; i < N; ++i) {
+        T x = v[i];
+        if constexpr (sizeof(T) == 4) asm volatile("" : "+v"(x));
+        r = idx == i ? x : r;
+    }
     return r;
 }
 
@@ -342,7 +347,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ int s_ulrel[MAX_UL_ROWS];
     // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
     // interference terms at every (cell, RBG) during a UL slot
-    __shared__ float s_x[2 * NCS * CW];
+    __shared__ __align__(16) float s_x[2 * NCS * CW];
     __shared__ float s_lin[S * CW];                              // per-lane rows: linear RBG SINR
     __shared__ int s_la_i[2 * CW], s_la_slot[CW], s_la_top[CW];  // link adaptation work list
     __shared__ float s_la_f[3 * CW];
@@ -351,6 +356,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
     __shared__ int s_rval[W > 1 ? CW : 1];
     __shared__ int s_xw[4];                                      // W = 2: the two waves' values of an env collective
+    // several cells: the interference pairs of a UL slot (robot lane | RBG << 8 | serving cell << 16, then the fading
+    // state (re, im) on every cell); at most one holder per (cell, RBG)
+    __shared__ float s_ipair[MC ? NC * S * (1 + 2 * NC) : 1];
+    __shared__ float s_ipsd[MC ? NC * STEP_WAVE : 1];            // several cells: each robot's PSD at every cell
 
     const int lane = threadIdx.x;
     const int wbase = lane & ~(STEP_WAVE - 1), wl = lane - wbase;   // this lane's wavefront (base lane) and lane in it
@@ -1236,15 +1245,47 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             if (cl.use_int) {
                 const bool txing = tx && act;
                 float* const s_t = s_x + S * STEP_WAVE;
+                // (the terms are computed cooperatively: the columns are cleared, every transmitting robot lists
+                // its held RBGs with its fading state on every cell, and the (RBG, other cell) terms of the list
+                // are dealt over the wavefront)
+                {
+                    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                    for (int i = lane; i < NCS * STEP_WAVE / 4; i += STEP_WAVE) reinterpret_cast<float4*>(s_t)[i] = z4;
+                }
+                const int n_h = txing ? __popc(won) : 0;
+                int off = n_h;                          // inclusive prefix sum of the counts over the wavefront
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    const float psd = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
+                for (int d = 1; d < STEP_WAVE; d <<= 1) {
+                    const int o = __shfl_up(off, d, 64);
+                    off += wl >= d ? o : 0;
+                }
+                const int n_pairs = __shfl(off, STEP_WAVE - 1, 64);
+                off -= n_h;
+                // the robot's PSD at every cell: ((pg_c + ue_tx) - ref_db) - split
+                float* const s_psd = s_ipsd;
 #pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        float v = 0.f;
-                        if (txing && c != serv && ((won >> s) & 1u)) v = from_db(psd + gain_cs(c * S + s));
-                        s_t[(c * S + s) * STEP_WAVE + lane] = v;
+                for (int c = 0; c < NC; ++c) s_psd[c * STEP_WAVE + lane] = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    if (txing && ((won >> s) & 1u)) {
+                        float* const ent = s_ipair + off * (1 + 2 * NC);
+                        ent[0] = __int_as_float(lane | (s << 8) | (serv << 16));
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) { ent[1 + 2 * c] = hr[c * S + s]; ent[2 + 2 * c] = hi[c * S + s]; }
+                        ++off;
                     }
+                }
+                __syncthreads();
+#pragma unroll 1
+                for (int it = wl; it < n_pairs * (NC - 1); it += STEP_WAVE) {
+                    const int pi = it / (NC - 1), k = it - pi * (NC - 1);
+                    const float* const ent = s_ipair + pi * (1 + 2 * NC);
+                    const uint32_t w = __float_as_uint(ent[0]);
+                    const int L = (int)(w & 0xffu), sq = (int)((w >> 8) & 0xffu), sv = (int)(w >> 16);
+                    const int c = k < sv ? k : k + 1;            // the k-th cell other than the serving one
+                    const float xr = ent[1 + 2 * c], xi = ent[2 + 2 * c];
+                    const float gc = pm.fading ? 10.0f * log10_pos(clamp_min(xr * xr + xi * xi, 1e-6f)) : 0.0f;
+                    s_t[(c * S + sq) * STEP_WAVE + L] = from_db(s_psd[c * STEP_WAVE + L] + gc);
                 }
                 __syncthreads();
                 if (e < E) {
@@ -1711,10 +1752,10 @@ void launch_step_w2(const StepArgs& a) {
                        a.n_data, a.arr, none);
 }
 
-// the multi-cell step: NC cells, pose input, runtime segment width
-template <int S, int P, bool IR, int NC, int FX = 0>
+// the multi-cell step: NC cells, pose input, runtime segment width (RBT = 0) or one fixed at compile time
+template <int S, int P, bool IR, int NC, int FX = 0, int RBT = 0>
 void launch_step_mc(const StepArgs& a) {
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 0, InetNrState, NC, FX>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, RBT, InetNrState, NC, FX>), dim3(a.grid), dim3(STEP_WAVE), a.lds,
                        a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
                        a.arr, *a.cells);
 }
@@ -1741,16 +1782,16 @@ StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx);    // nr_step_s8
 
 // multi-cell builds (NC = 3): every (P, IR)
 template <int S>
-StepFn pick_step_mc_s(int P, bool ir, int fx) {
-    if constexpr (S == 14)                           // config 3's switches (no Rician phasor), 8 HARQ
-        if (fx == 2 && P == 8 && !ir) return &launch_step_mc<14, 8, false, 3, 2>;
+StepFn pick_step_mc_s(int P, bool ir, int fx, int rb) {
+    if constexpr (S == 14)                           // config 3's switches (no Rician phasor), 8 HARQ, 64-robot envs
+        if (fx == 2 && P == 8 && !ir && rb == 64) return &launch_step_mc<14, 8, false, 3, 2, 64>;
 #define INET_PICK_MC(PP) \
     if (P == PP) return ir ? &launch_step_mc<S, PP, true, 3> : &launch_step_mc<S, PP, false, 3>;
     INET_PICK_MC(2) INET_PICK_MC(4) INET_PICK_MC(8) INET_PICK_MC(16)
 #undef INET_PICK_MC
     return nullptr;
 }
-StepFn pick_step_mc(int S, int C, int P, bool ir, int fx); // nr_step_mc.hip
+StepFn pick_step_mc(int S, int C, int P, bool ir, int fx, int rb); // nr_step_mc.hip
 
 // two-wavefront builds (R = 65..128): every (P, IR)
 template <int S>

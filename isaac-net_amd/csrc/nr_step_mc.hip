@@ -1,14 +1,14 @@
 // Step-kernel instantiations for several cells per env (NRNet.step_cells): 3 cells, 8 / 13 / 14 subbands (RBGs),
 // HARQ processes 2, 4, 8, 16 x (IR combining), pose input, runtime segment width; and config 3's switches fixed at
-// compile time (14 RBGs, 8 HARQ, FX = 2).
+// compile time (14 RBGs, 8 HARQ, FX = 2) for 64-robot envs (segment width fixed at compile time).
 #include "nr_step.h"
 
 namespace inet {
-StepFn pick_step_mc(int S, int C, int P, bool ir, int fx) {
+StepFn pick_step_mc(int S, int C, int P, bool ir, int fx, int rb) {
     if (C != 3) return nullptr;
-    if (S == 8) return pick_step_mc_s<8>(P, ir, fx);
-    if (S == 13) return pick_step_mc_s<13>(P, ir, fx);
-    if (S == 14) return pick_step_mc_s<14>(P, ir, fx);
+    if (S == 8) return pick_step_mc_s<8>(P, ir, fx, rb);
+    if (S == 13) return pick_step_mc_s<13>(P, ir, fx, rb);
+    if (S == 14) return pick_step_mc_s<14>(P, ir, fx, rb);
     return nullptr;
 }
 }  // namespace inet
