@@ -355,7 +355,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ uint4 s_dlist[CW];
     __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
     __shared__ int s_rval[W > 1 ? CW : 1];
-    __shared__ int s_xw[4];                                      // W = 2: the two waves' values of an env collective
+    __shared__ int s_xw[8];                                      // W = 2: the two waves' values of an env collective
     // several cells: the interference pairs of a UL slot (robot lane | RBG << 8 | serving cell << 16, then the fading
     // state (re, im) on every cell); at most one holder per (cell, RBG)
     __shared__ float s_ipair[MC ? NC * S * (1 + 2 * NC) : 1];
@@ -387,13 +387,16 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     float* const s_if = s_ni + NCS;
 
     // ---------------- env-wide collectives: inside the segment (W = 1), or over the two waves of the env (W = 2)
-    // through LDS, between two barriers that both waves reach
+    // through LDS behind one barrier that both waves reach. Successive exchanges alternate between two buffers: a wave
+    // writes a buffer again only two exchanges later, after a barrier that the other wave reaches once it has read it.
+    int xbuf = 0;
     auto xchg2 = [&](int v, int& v0, int& v1) {        // v: uniform in each wave
-        if (wl == 0) s_xw[lane >> 6] = v;
+        int* const b = s_xw + 4 * xbuf;
+        xbuf ^= 1;
+        if (wl == 0) b[lane >> 6] = v;
         __syncthreads();
-        v0 = s_xw[0];
-        v1 = s_xw[1];
-        __syncthreads();
+        v0 = b[0];
+        v1 = b[1];
     };
     auto env_any = [&](bool p) -> bool {
         if constexpr (RBT == 32) {
@@ -416,6 +419,45 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         }
     };
 
+    // ---------------- load per-robot state (issued first: the loads are in flight while the tables are staged) ----
+    int sent = 0, floor_ = 0, bsr = 0, sr_t = -1, last_tx = -1, enq = 0, qlen = 0;
+    float olla = 0.f, avg = 100.f;
+    float csi[S], hr[NCS], hi[NCS];
+    uint32_t hmeta[P];
+    int hlo[P], hhi[P], hrdy[P], htbs[P];
+    float hcomb[P], hlexp[IR ? P : 1], hnrb[IR ? P : 1];
+    const bool read_h = pm.fading && !(n_rows > 0 && (rows[0].flags & 4) && rows[0].rho == 0.0f);
+    // (lanes without a robot read a clamped, valid address and discard the value: the loads are branch-free)
+    sent = ldo(lk.sent, o_r); floor_ = ldo(lk.floor_, o_r);
+    if constexpr (!DL) { bsr = ldo(st.bsr, o_r); sr_t = ldo(st.sr_t, o_r); }
+    last_tx = ldo(lk.last_tx, o_r); enq = ldo(lk.enq, o_r); qlen = ldo(lk.qlen, o_r);
+    olla = ldo(lk.olla, o_r); avg = ldo(lk.avg, o_r);
+    qlen = qlen < 0 ? 0 : (qlen > F ? F : qlen);
+    if (!act) { sent = 0; floor_ = 0; bsr = 0; sr_t = -1; last_tx = -1; enq = 0; qlen = 0; olla = 0.f; avg = 100.f; }
+    const uint32_t o_hr0 = (uint32_t)(ee * NCS * R + rr0) * 4u;   // [E][NC S][R] at q = 0
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        csi[s] = ldo(lk.csi + s * R, o_sr);
+        if (!act) csi[s] = 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < NCS; ++q) {
+        hr[q] = 0.f; hi[q] = 0.f;
+        if (read_h && act) { hr[q] = ldo(st.h_re + q * R, o_hr0); hi[q] = ldo(st.h_im + q * R, o_hr0); }
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int pr = p * R;
+        hmeta[p] = ldo(lk.h_meta + pr, o_pr); hlo[p] = ldo(lk.h_lo + pr, o_pr); hhi[p] = ldo(lk.h_hi + pr, o_pr);
+        hrdy[p] = ldo(lk.h_ready + pr, o_pr); htbs[p] = ldo(lk.h_tbs + pr, o_pr); hcomb[p] = ldo(lk.h_comb + pr, o_pr);
+        if constexpr (IR) { hlexp[p] = ldo(lk.h_lexp + pr, o_pr); hnrb[p] = ldo(lk.h_nrb + pr, o_pr); }
+        if (!act) {
+            hmeta[p] = 0u; hlo[p] = 0; hhi[p] = 0; hrdy[p] = 0; htbs[p] = 0; hcomb[p] = 0.f;
+            if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
+        }
+    }
+    float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
+    if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
     if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
@@ -466,21 +508,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     for (int s = 1; s < S; ++s) lw_eq = lw_eq && s_logw[s] == s_logw[0];
     __syncthreads();
 
-    // ---------------- load per-robot state ----------------
-    int sent = 0, floor_ = 0, bsr = 0, sr_t = -1, last_tx = -1, enq = 0, qlen = 0;
-    float olla = 0.f, avg = 100.f;
-    float csi[S], hr[NCS], hi[NCS];
-    uint32_t hmeta[P];
-    int hlo[P], hhi[P], hrdy[P], htbs[P];
-    float hcomb[P], hlexp[IR ? P : 1], hnrb[IR ? P : 1];
-    const bool read_h = pm.fading && !(n_rows > 0 && (rows[0].flags & 4) && rows[0].rho == 0.0f);
-    // (lanes without a robot read a clamped, valid address and discard the value: the loads are branch-free)
-    sent = ldo(lk.sent, o_r); floor_ = ldo(lk.floor_, o_r);
-    if constexpr (!DL) { bsr = ldo(st.bsr, o_r); sr_t = ldo(st.sr_t, o_r); }
-    last_tx = ldo(lk.last_tx, o_r); enq = ldo(lk.enq, o_r); qlen = ldo(lk.qlen, o_r);
-    olla = ldo(lk.olla, o_r); avg = ldo(lk.avg, o_r);
-    qlen = qlen < 0 ? 0 : (qlen > F ? F : qlen);
-    if (!act) { sent = 0; floor_ = 0; bsr = 0; sr_t = -1; last_tx = -1; enq = 0; qlen = 0; olla = 0.f; avg = 100.f; }
     // the step's arrivals (inet_nr_submit_step): FrameQueue.add / NRNet.add_frames of every message, class by class
     // (queues.py:87-103, nr_engine.py:466-487), at the tail of the FIFO, before the slots
     if constexpr (!DL) {
@@ -509,17 +536,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             if (arr.accepted) sto(arr.accepted, o_r, n_acc);
         }
     }
-    const uint32_t o_hr0 = (uint32_t)(ee * NCS * R + rr0) * 4u;   // [E][NC S][R] at q = 0
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        csi[s] = ldo(lk.csi + s * R, o_sr);
-        if (!act) csi[s] = 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < NCS; ++q) {
-        hr[q] = 0.f; hi[q] = 0.f;
-        if (read_h && act) { hr[q] = ldo(st.h_re + q * R, o_hr0); hi[q] = ldo(st.h_im + q * R, o_hr0); }
-    }
     // several cells: association of this robot, the N+I estimates of its env (LDS), the env's interference statistic
     int serv = 0, a3_cand = -1, a3_cnt = 0, ho_end = 0, n_ho = 0;
     float ion = 0.f;
@@ -535,19 +551,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         }
         __syncthreads();
     }
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int pr = p * R;
-        hmeta[p] = ldo(lk.h_meta + pr, o_pr); hlo[p] = ldo(lk.h_lo + pr, o_pr); hhi[p] = ldo(lk.h_hi + pr, o_pr);
-        hrdy[p] = ldo(lk.h_ready + pr, o_pr); htbs[p] = ldo(lk.h_tbs + pr, o_pr); hcomb[p] = ldo(lk.h_comb + pr, o_pr);
-        if constexpr (IR) { hlexp[p] = ldo(lk.h_lexp + pr, o_pr); hnrb[p] = ldo(lk.h_nrb + pr, o_pr); }
-        if (!act) {
-            hmeta[p] = 0u; hlo[p] = 0; hhi[p] = 0; hrdy[p] = 0; htbs[p] = 0; hcomb[p] = 0.f;
-            if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
-        }
-    }
-    float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
-    if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
     // rician gain coefficients (nr_engine.py:608-611): inv = 1 / (K + 1), sqrt(K inv), sqrt(inv)
     const float kinv = 1.0f / (kk + 1.0f);
     const float ka = sqrtf(kk * kinv), kb = sqrtf(kinv);
@@ -908,10 +911,11 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 // each wave's max and its first lane holding it; the env's winner is wave 0's on ties
                 const int mxw = bmax_i(m, STEP_WAVE);
                 const int fw = (int)__builtin_ctzll(__ballot(m == mxw));
-                if (wl == 0) { s_xw[2 * (lane >> 6)] = mxw; s_xw[2 * (lane >> 6) + 1] = fw; }
+                int* const b = s_xw + 4 * xbuf;           // (alternating buffers, as xchg2)
+                xbuf ^= 1;
+                if (wl == 0) { b[2 * (lane >> 6)] = mxw; b[2 * (lane >> 6) + 1] = fw; }
                 __syncthreads();
-                const int m0 = s_xw[0], f0 = s_xw[1], m1 = s_xw[2], f1 = s_xw[3];
-                __syncthreads();
+                const int m0 = b[0], f0 = b[1], m1 = b[2], f1 = b[3];
                 return m >= 0 && lane == (m0 >= m1 ? f0 : STEP_WAVE + f1);
             } else if constexpr (RBT == 32) {
                 // the first lane of each 32-lane segment holding the maximum, found on the scalar unit
