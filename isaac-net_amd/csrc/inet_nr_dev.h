@@ -372,6 +372,21 @@ DEV void draw_plane_wave(uint32_t s0, uint32_t env, uint32_t ep, int radio_model
     fp[2] = (u2 * 2.0f) * (float)3.141592653589793;
 }
 
+// exclusive prefix sum over the wavefront of a per-lane count 0 <= v < 64 and the wave total: one ballot per bit of
+// v, counted below the lane (mbcnt), no LDS round trip
+DEV int wave_prefix64(int v, int wl, int& total) {
+    const unsigned long long below = wl ? (~0ull >> (64 - wl)) : 0ull;
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+        const unsigned long long m = __ballot((v >> b) & 1);
+        pre += __popcll(m & below) << b;
+        tot += __popcll(m) << b;
+    }
+    total = tot;
+    return pre;
+}
+
 // ---------------------------------------------------------------- segment collectives (RB lanes, power of two)
 DEV unsigned long long seg_bits(int rb, int lane) {
     unsigned long long m = rb >= 64 ? ~0ull : ((1ull << rb) - 1ull);

@@ -356,8 +356,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
     __shared__ int s_rval[W > 1 ? CW : 1];
     __shared__ int s_xw[8];                                      // W = 2: the two waves' values of an env collective
-    // several cells: the interference pairs of a UL slot (robot lane | RBG << 8 | serving cell << 16, then the fading
-    // state (re, im) on every cell); at most one holder per (cell, RBG)
+    // several cells, one env per wavefront: the interference pairs of a UL slot (robot lane | RBG << 8 | serving cell
+    // << 16, then the fading state (re, im) on every cell); at most one holder per (cell, RBG)
     __shared__ float s_ipair[MC ? NC * S * (1 + 2 * NC) : 1];
     __shared__ float s_ipsd[MC ? NC * STEP_WAVE : 1];            // several cells: each robot's PSD at every cell
 
@@ -1127,6 +1127,65 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         const float sp = MC ? (sp0 > pc ? sp0 : pc) : sp0;
         // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
         const float lnw = lw_eq ? s_lnw[__popc(won)] : lse_logw<S>(s_logw, won);
+        // The (robot lane, RBG) pairs of the robots with `who` over the RBGs they hold, in lane order, into this wave's
+        // part of pl ([64 S] entries per wave: lane | RBG << 8); returns this wave's count. Per-RBG work on the held
+        // RBGs (at most S per scheduler, against S per robot) is then dealt over the wavefront.
+        auto build_pairs = [&](bool who, int* pl) -> int {
+            int n;
+            int off = wave_prefix64(who ? __popc(won) : 0, wl, n);
+            int* const wpl = pl + wbase * S;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+                if (who && ((won >> s) & 1u)) wpl[off++] = lane | (s << 8);
+            return n;
+        };
+        // lse_eesm (the EESM log-sum over the held RBGs) of every robot with `who`, for its dB row xv and MCS mc: the
+        // pairs' terms (-lin_s) / beta + log w_s and then exp(term - max) are computed on the pair list; each robot
+        // takes the max and the ATen-order sum over its own RBGs (the RBGs it does not hold add exact zeros), which are
+        // lse_held's steps. Called by every lane (barriers); the result is read in the lanes with `who`. LDS: the dB
+        // rows in s_x rows S..2S-1, the pair list in rows 0..S-1, terms in s_lin, the MCS and max in s_la_i / s_la_f.
+        auto held_lse = [&](bool who, const float (&xv)[S], int mc, bool nanv) -> float {
+            float* const s_dx = s_x + S * CW;
+            int* const s_pl = reinterpret_cast<int*>(s_x);
+            if (who) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) s_dx[s * CW + lane] = xv[s];
+                s_la_i[lane] = mc;
+            }
+            const int n_pairs = build_pairs(who, s_pl);
+            __syncthreads();
+#pragma unroll 1
+            for (int it = wl; it < n_pairs; it += STEP_WAVE) {
+                const int en = s_pl[wbase * S + it], L = en & 0xff, sq = en >> 8;
+                const int m = s_la_i[L];
+                const float lin = from_db_mid(clampf(s_dx[sq * CW + L], -30.0f, 60.0f));
+                s_lin[sq * CW + L] = div_const(-lin, s_beta[m], s_rbeta[m]) + s_logw[sq];
+            }
+            __syncthreads();
+            float mx = -INFINITY;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const float v = ((won >> s) & 1u) ? s_lin[s * CW + lane] : -INFINITY;
+                mx = v > mx ? v : mx;
+            }
+            if (mx == INFINITY || mx == -INFINITY) mx = 0.f;
+            s_la_f[lane] = mx;
+            __syncthreads();
+#pragma unroll 1
+            for (int it = wl; it < n_pairs; it += STEP_WAVE) {
+                const int en = s_pl[wbase * S + it], L = en & 0xff, sq = en >> 8;
+                s_lin[sq * CW + L] = exp_nonpos(s_lin[sq * CW + L] - s_la_f[L]);
+            }
+            __syncthreads();
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const int sq = aten_unrot<S>(i);
+                sum += ((won >> sq) & 1u) ? s_lin[sq * CW + lane] : 0.0f;
+            }
+            const float res = (sum == 0.0f ? -INFINITY : ln_unit(sum)) + mx;
+            return nanv ? NAN : res;
+        };
         // ---- link adaptation for new TBs (phy.select_mcs): the highest MCS meeting the BLER target ----
         int mcs_new = 0, tbs_new = 0;
         bool any_new;                                  // (W = 2: both waves enter, the search has barriers)
@@ -1135,13 +1194,33 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         if (any_new) {
             // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on the held RBGs
             bool nan = false;
-            const uint32_t held = tx_new ? won : 0u;
+            if (pm.eesm) {
+                // the linear values on the pair list of the new TBs' held RBGs (the dB rows in s_x rows S..2S-1, the
+                // list in rows 0..S-1; the search's first round passes a barrier before it reads s_lin)
+                float* const s_ex = s_x + S * CW;
 #pragma unroll
-            for (int s = 0; s < S; ++s) {
-                const float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
-                nan |= x != x;
-                if (!pm.eesm) s_x[s * CW + lane] = x;                    // (the mean-dB row)
-                if ((held >> s) & 1u) s_lin[s * CW + lane] = from_db_mid(clampf(x, -30.0f, 60.0f));
+                for (int s = 0; s < S; ++s) {
+                    const float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];   // DL: the scheduler's estimate
+                    nan |= x != x;
+                    if (tx_new) s_ex[s * CW + lane] = x;
+                }
+                int* const s_pl = reinterpret_cast<int*>(s_x);
+                const int n_pairs = build_pairs(tx_new, s_pl);
+                __syncthreads();
+#pragma unroll 1
+                for (int it = wl; it < n_pairs; it += STEP_WAVE) {
+                    const int en = s_pl[wbase * S + it], L = en & 0xff, sq = en >> 8;
+                    s_lin[sq * CW + L] = from_db_mid(clampf(s_ex[sq * CW + L], -30.0f, 60.0f));
+                }
+            } else {
+                const uint32_t held = tx_new ? won : 0u;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];
+                    nan |= x != x;
+                    s_x[s * CW + lane] = x;                                  // (the mean-dB row)
+                    if ((held >> s) & 1u) s_lin[s * CW + lane] = from_db_mid(clampf(x, -30.0f, 60.0f));
+                }
             }
             const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw) : 0.f;
             const int np = (int)n_prb;
@@ -1249,47 +1328,59 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             if (cl.use_int) {
                 const bool txing = tx && act;
                 float* const s_t = s_x + S * STEP_WAVE;
-                // (the terms are computed cooperatively: the columns are cleared, every transmitting robot lists
-                // its held RBGs with its fading state on every cell, and the (RBG, other cell) terms of the list
-                // are dealt over the wavefront)
-                {
-                    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                    for (int i = lane; i < NCS * STEP_WAVE / 4; i += STEP_WAVE) reinterpret_cast<float4*>(s_t)[i] = z4;
-                }
-                const int n_h = txing ? __popc(won) : 0;
-                int off = n_h;                          // inclusive prefix sum of the counts over the wavefront
-#pragma unroll
-                for (int d = 1; d < STEP_WAVE; d <<= 1) {
-                    const int o = __shfl_up(off, d, 64);
-                    off += wl >= d ? o : 0;
-                }
-                const int n_pairs = __shfl(off, STEP_WAVE - 1, 64);
-                off -= n_h;
-                // the robot's PSD at every cell: ((pg_c + ue_tx) - ref_db) - split
-                float* const s_psd = s_ipsd;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) s_psd[c * STEP_WAVE + lane] = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
-#pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    if (txing && ((won >> s) & 1u)) {
-                        float* const ent = s_ipair + off * (1 + 2 * NC);
-                        ent[0] = __int_as_float(lane | (s << 8) | (serv << 16));
-#pragma unroll
-                        for (int c = 0; c < NC; ++c) { ent[1 + 2 * c] = hr[c * S + s]; ent[2 + 2 * c] = hi[c * S + s]; }
-                        ++off;
+                if (rb == STEP_WAVE) {
+                    // one env per wavefront (at most NC S held (cell, RBG) pairs): the terms are computed
+                    // cooperatively. The columns are cleared, every transmitting robot lists its held RBGs with its
+                    // fading state on every cell, and the (RBG, other cell) terms of the list are dealt over the
+                    // wavefront.
+                    {
+                        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                        for (int i = lane; i < NCS * STEP_WAVE / 4; i += STEP_WAVE)
+                            reinterpret_cast<float4*>(s_t)[i] = z4;
                     }
-                }
-                __syncthreads();
+                    int n_pairs;
+                    int off = wave_prefix64(txing ? __popc(won) : 0, wl, n_pairs);
+                    // the robot's PSD at every cell: ((pg_c + ue_tx) - ref_db) - split
+                    float* const s_psd = s_ipsd;
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) s_psd[c * STEP_WAVE + lane] = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        if (txing && ((won >> s) & 1u)) {
+                            float* const ent = s_ipair + off * (1 + 2 * NC);
+                            ent[0] = __int_as_float(lane | (s << 8) | (serv << 16));
+#pragma unroll
+                            for (int c = 0; c < NC; ++c) {
+                                ent[1 + 2 * c] = hr[c * S + s];
+                                ent[2 + 2 * c] = hi[c * S + s];
+                            }
+                            ++off;
+                        }
+                    }
+                    __syncthreads();
 #pragma unroll 1
-                for (int it = wl; it < n_pairs * (NC - 1); it += STEP_WAVE) {
-                    const int pi = it / (NC - 1), k = it - pi * (NC - 1);
-                    const float* const ent = s_ipair + pi * (1 + 2 * NC);
-                    const uint32_t w = __float_as_uint(ent[0]);
-                    const int L = (int)(w & 0xffu), sq = (int)((w >> 8) & 0xffu), sv = (int)(w >> 16);
-                    const int c = k < sv ? k : k + 1;            // the k-th cell other than the serving one
-                    const float xr = ent[1 + 2 * c], xi = ent[2 + 2 * c];
-                    const float gc = pm.fading ? 10.0f * log10_pos(clamp_min(xr * xr + xi * xi, 1e-6f)) : 0.0f;
-                    s_t[(c * S + sq) * STEP_WAVE + L] = from_db(s_psd[c * STEP_WAVE + L] + gc);
+                    for (int it = wl; it < n_pairs * (NC - 1); it += STEP_WAVE) {
+                        const int pi = it / (NC - 1), k = it - pi * (NC - 1);
+                        const float* const ent = s_ipair + pi * (1 + 2 * NC);
+                        const uint32_t w = __float_as_uint(ent[0]);
+                        const int L = (int)(w & 0xffu), sq = (int)((w >> 8) & 0xffu), sv = (int)(w >> 16);
+                        const int c = k < sv ? k : k + 1;            // the k-th cell other than the serving one
+                        const float xr = ent[1 + 2 * c], xi = ent[2 + 2 * c];
+                        const float gc =
+                            pm.fading ? 10.0f * log10_pos(clamp_min(xr * xr + xi * xi, 1e-6f)) : 0.0f;
+                        s_t[(c * S + sq) * STEP_WAVE + L] = from_db(s_psd[c * STEP_WAVE + L] + gc);
+                    }
+                } else {                                // several envs per wavefront: each lane its own terms
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) {
+                        const float psd = ((pgc[c] + pm.ue_tx) - cl.ref_db) - sp;
+#pragma unroll
+                        for (int s = 0; s < S; ++s) {
+                            float v = 0.f;
+                            if (txing && c != serv && ((won >> s) & 1u)) v = from_db(psd + gain_cs(c * S + s));
+                            s_t[(c * S + s) * STEP_WAVE + lane] = v;
+                        }
+                    }
                 }
                 __syncthreads();
                 if (e < E) {
@@ -1310,7 +1401,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         // ---- decoding on the actual channel (mac.py:428-454, mac_ul.py:185-192) ----
         bool ok = false, fail = false, exh = false;
         float comb = comb_p, lexp = lexp_p, nrb = nrb_p;
-        if (__ballot(tx) != 0ull) {
+        bool any_tx;                                   // (W = 2: both waves enter, the EESM has barriers)
+        if constexpr (W == 1) any_tx = __ballot(tx) != 0ull;
+        else any_tx = env_any(tx);
+        if (any_tx) {
             const float beta = s_beta[mcs], rbeta = s_rbeta[mcs];
             bool nan = false;
             float xs[S];
@@ -1325,12 +1419,12 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 xs[s] = x;
                 if (!pm.eesm) s_x[s * CW + lane] = x;                    // (the mean-dB row)
             }
-            // the linear SINR of RBG s (used where held)
-            auto lin_of = [&](int s) { return from_db_mid(clampf(xs[s], -30.0f, 60.0f)); };
+            // the EESM log-sum of the held RBGs (lse_eesm of the linear SINR per RBG)
+            const float lse_tx = (IR || pm.eesm) ? held_lse(tx, xs, mcs, nan) : 0.0f;
             float eff_used;
             int m_look = mcs;
             if constexpr (IR) {
-                float lse = lse_eesm<S>(lin_of, s_logw, won, beta, rbeta, nan);
+                float lse = lse_tx;
                 // torch.logaddexp: equal infinities stay, else max + log1p(exp(-|a - b|))
                 if (isinf(lexp_p) && lexp_p == lse) lexp = lexp_p;
                 else { float mx = lexp_p > lse ? lexp_p : lse; lexp = mx + log1pf(expf(-fabsf(lexp_p - lse))); }
@@ -1343,7 +1437,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             } else {
                 float eff;
                 if (pm.eesm) {
-                    eff = db_of((-beta) * (lse_eesm<S>(lin_of, s_logw, won, beta, rbeta, nan) - lnw));
+                    eff = db_of((-beta) * (lse_tx - lnw));
                 } else {
                     eff = mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw);
                 }
