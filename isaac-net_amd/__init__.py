@@ -18,7 +18,7 @@ def make_engine(*args, **kwargs):
 
 
 def __getattr__(name):
-    if name in ("HipNREngine", "Requests", "refusals", "HipUnsupported"):
+    if name in ("HipNREngine", "Requests", "refusals", "HipUnsupported", "set_env_offset"):
         from . import engine
         return getattr(engine, name)
     if name in ("HipWifiEngine", "wifi_refusals"):

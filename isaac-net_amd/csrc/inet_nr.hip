@@ -269,10 +269,9 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
         fn = inet::pick_step_mc(p.S, c.C, p.P, ir, fx, rb);
     } else if (rb > inet::STEP_WAVE) {          // 65..128 robots: two wavefronts per env, UL
         if (dl || vref) return INET_NR_EUNSUPPORTED;
-        fn = inet::pick_step_w2(p.S, p.P, ir, fx);
+        fn = inet::pick_step_two_waves(p.S, p.P, ir, fx);
     } else {
-        fn = p.S == 13 ? inet::pick_step_s13(p.P, ir, vref, rb, fx)
-           : p.S == 8 ? inet::pick_step_s8(p.P, ir, vref, rb, fx) : nullptr;
+        fn = inet::pick_step_one_cell(p.S, p.P, ir, vref, rb, fx);
     }
     if (!fn) return INET_NR_EUNSUPPORTED;
     const int envs_pw = rb > inet::STEP_WAVE ? 1 : inet::STEP_WAVE / rb;

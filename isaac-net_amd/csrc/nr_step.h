@@ -1877,19 +1877,29 @@ StepFn pick_step_s(int P, bool ir, bool vref, int rb, int fx) {
 
 StepFn pick_step_s13(int P, bool ir, bool vref, int rb, int fx);   // nr_step_s13.hip
 StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx);    // nr_step_s8.hip
+// the other RBG counts of one cell, each with its two-wavefront builds (nr_step_s<S>.hip): the counts of the standard
+// carriers at 30 kHz (RBG configuration 1: 24, 38/78, 106/217, 133/65, 162, 245, 273 PRB)
+#define INET_STEP_S_EXTRA(X) X(10) X(11) X(12) X(14) X(16) X(17) X(18)
+#define INET_DECL_S(SS)                                                    \
+    StepFn pick_step_s##SS(int P, bool ir, bool vref, int rb, int fx);   \
+    StepFn pick_step_w2_s##SS(int P, bool ir, int fx);
+INET_STEP_S_EXTRA(INET_DECL_S)
+#undef INET_DECL_S
 
-// multi-cell builds (NC = 3): every (P, IR)
-template <int S>
+
+// multi-cell builds (NC cells): every (P, IR)
+template <int S, int NC>
 StepFn pick_step_mc_s(int P, bool ir, int fx, int rb) {
-    if constexpr (S == 14)                           // config 3's switches (no Rician phasor), 8 HARQ, 64-robot envs
+    if constexpr (S == 14 && NC == 3)                // config 3's switches (no Rician phasor), 8 HARQ, 64-robot envs
         if (fx == 2 && P == 8 && !ir && rb == 64) return &launch_step_mc<14, 8, false, 3, 2, 64>;
 #define INET_PICK_MC(PP) \
-    if (P == PP) return ir ? &launch_step_mc<S, PP, true, 3> : &launch_step_mc<S, PP, false, 3>;
+    if (P == PP) return ir ? &launch_step_mc<S, PP, true, NC> : &launch_step_mc<S, PP, false, NC>;
     INET_PICK_MC(2) INET_PICK_MC(4) INET_PICK_MC(8) INET_PICK_MC(16)
 #undef INET_PICK_MC
     return nullptr;
 }
 StepFn pick_step_mc(int S, int C, int P, bool ir, int fx, int rb); // nr_step_mc.hip
+StepFn pick_step_mc2(int S, int P, bool ir, int fx, int rb);       // nr_step_mc2.hip
 
 // two-wavefront builds (R = 65..128): every (P, IR)
 template <int S>
@@ -1903,5 +1913,30 @@ StepFn pick_step_w2_s(int P, bool ir, int fx) {
     return nullptr;
 }
 StepFn pick_step_w2(int S, int P, bool ir, int fx);        // nr_step_w2.hip
+
+// the one-cell step builds for S subbands: envs of up to 64 robots on one wavefront (nullptr: no build)
+inline StepFn pick_step_one_cell(int S, int P, bool ir, bool vref, int rb, int fx) {
+    switch (S) {
+    case 8: return pick_step_s8(P, ir, vref, rb, fx);
+    case 13: return pick_step_s13(P, ir, vref, rb, fx);
+#define INET_CASE_S(SS) \
+    case SS: return pick_step_s##SS(P, ir, vref, rb, fx);
+    INET_STEP_S_EXTRA(INET_CASE_S)
+#undef INET_CASE_S
+    default: return nullptr;
+    }
+}
+// envs of 65..128 robots on two wavefronts
+inline StepFn pick_step_two_waves(int S, int P, bool ir, int fx) {
+    switch (S) {
+    case 8:
+    case 13: return pick_step_w2(S, P, ir, fx);
+#define INET_CASE_S(SS) \
+    case SS: return pick_step_w2_s##SS(P, ir, fx);
+    INET_STEP_S_EXTRA(INET_CASE_S)
+#undef INET_CASE_S
+    default: return nullptr;
+    }
+}
 
 }  // namespace inet

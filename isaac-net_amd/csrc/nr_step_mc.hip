@@ -5,10 +5,11 @@
 
 namespace inet {
 StepFn pick_step_mc(int S, int C, int P, bool ir, int fx, int rb) {
+    if (C == 2) return pick_step_mc2(S, P, ir, fx, rb);
     if (C != 3) return nullptr;
-    if (S == 8) return pick_step_mc_s<8>(P, ir, fx, rb);
-    if (S == 13) return pick_step_mc_s<13>(P, ir, fx, rb);
-    if (S == 14) return pick_step_mc_s<14>(P, ir, fx, rb);
+    if (S == 8) return pick_step_mc_s<8, 3>(P, ir, fx, rb);
+    if (S == 13) return pick_step_mc_s<13, 3>(P, ir, fx, rb);
+    if (S == 14) return pick_step_mc_s<14, 3>(P, ir, fx, rb);
     return nullptr;
 }
 }  // namespace inet

@@ -64,6 +64,11 @@ def seed_key(seed):
     return mix32(mix32(seed & M32) ^ salt((seed >> 32) & M32))
 
 
+# RBG counts of the one-cell step builds (nr_step_s*.hip): 8 (273 PRB in RBGs of 35) and the RBG-configuration-1 counts
+# of the standard carriers at 30 kHz
+ONE_CELL_RBGS = (8, 10, 11, 12, 13, 14, 16, 17, 18)
+
+
 def refusals(cfg: NRConfig):
     """[(feature, why)] of the config's features the HIP step kernel does not implement (empty: it runs)."""
     out = []
@@ -72,7 +77,8 @@ def refusals(cfg: NRConfig):
         if cond:
             out.append((what, why))
     mc = cfg.n_cells > 1
-    no(mc and cfg.n_cells != 3, f"n_cells={cfg.n_cells}", "one or three cells per env in this build")
+    no(mc and cfg.n_cells > 3, f"n_cells={cfg.n_cells}",
+       "one to three cells per env in this build (the fading of every robot-cell link is held in registers)")
     no(mc and cfg.dl, "the downlink with several cells", "the multi-cell step runs the uplink")
     no(cfg.rlf, "radio link failure (rlf=True)", "A3 handover without RLF")
     no(mc and cfg.rician_mode is not None, "Rician fading with several cells", "Rayleigh fading on every link")
@@ -107,8 +113,8 @@ def refusals(cfg: NRConfig):
         no(cfg.tr38901_los not in ("los", "nlos"), "tr38901_los='stochastic'", "a fixed LOS state (los / nlos)")
         no(cfg.tr38901_scenario == "RMa", "the RMa scenario", "UMa, UMi, InH, InF")
         no(cfg.tr38901_scenario.startswith("InF") and cfg.tr38901_los == "nlos", "InF NLOS", "InF LOS")
-    no(cfg.n_subbands not in ((8, 13, 14) if mc else (8, 13)), f"{cfg.n_subbands} subbands",
-       "8 or 13 RBGs (several cells: 8, 13 or 14) in this build")
+    no(cfg.n_subbands not in ((8, 13, 14) if mc else ONE_CELL_RBGS), f"{cfg.n_subbands} subbands",
+       f"{', '.join(map(str, ONE_CELL_RBGS))} RBGs (several cells: 8, 13 or 14) in this build")
     no(cfg.n_harq not in (2, 4, 8, 16), f"n_harq={cfg.n_harq}", "2, 4, 8 or 16 HARQ processes in this build")
     no(cfg.max_harq_tx > 16, "max_harq_tx > 16", "up to 16 transmissions")
     no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
@@ -522,6 +528,21 @@ class HipNREngine:
         mk = mask[:, None]
         self._last_snr = torch.where(mk, torch.zeros_like(self._last_snr), self._last_snr)
         self._last_hid = torch.where(mask, torch.zeros_like(self._last_hid), self._last_hid)
+
+    env_offset = 0
+
+    def set_env_offset(self, offset):
+        """Key env row i by the global env id offset + i (a shard of a larger batch, isaac_net/core/sharded.py:61-78,
+        CounterRNG.set_env_offset, proto/rng.py:103-109): the env ids move in place, the episode counters are rewound
+        by one and every env is reset again, so the envs redraw their initial state under the global ids and stay in
+        their first episode. An env then draws the same numbers whichever shard holds it."""
+        offset = int(offset)
+        if offset == self.env_offset:
+            return
+        self.st["env_id"].add_(offset - self.env_offset)
+        self.env_offset = offset
+        self.st["episode"].sub_(1)
+        self.reset(None)
 
     def _k_lin0(self):
         cfg = self.config
@@ -1258,6 +1279,12 @@ class HipNREngine:
                 if f"net.ul.q.{k}" in sd:
                     self._feat[k] = g(f"net.ul.q.{k}").to(v.dtype).reshape(v.shape).clone()
         return self
+
+
+def set_env_offset(engine, offset):
+    """The engine's env rows keyed by global env id offset + local id (sharded.set_env_offset,
+    isaac_net/core/sharded.py:61-78): HipNREngine / HipWifiEngine.set_env_offset."""
+    engine.set_env_offset(offset)
 
 
 def state_dict(eng):

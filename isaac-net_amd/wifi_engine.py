@@ -244,6 +244,19 @@ class HipWifiEngine:
             m8 = mask.to(torch.uint8).contiguous()
         self._reset_launch(m8)
 
+    env_offset = 0
+
+    def set_env_offset(self, offset):
+        """Key env row i by the global env id offset + i (isaac_net/core/sharded.py:61-78): the env ids move in
+        place, the episode counters are rewound by one and every env is reset again under the global ids."""
+        offset = int(offset)
+        if offset == self.env_offset:
+            return
+        self.st["env_id"].add_(offset - self.env_offset)
+        self.env_offset = offset
+        self.st["episode"].sub_(1)
+        self.reset(None)
+
     def _reset_launch(self, m8):
         _lib.check(self._lib.inet_wifi_reset(C.byref(self._cstate), C.byref(self._cparams),
                                              None if m8 is None else m8.data_ptr(), self._stream()), "wifi reset")
@@ -459,6 +472,19 @@ class HipWifiDcfEngine(HipWifiEngine):
         p.fer = float(np.float32(wc.frame_error_rate))
         self._cdparams = p
         self.dcf_ac = AC_NAMES.index(wc.access_category)
+
+    env_offset = 0
+
+    def set_env_offset(self, offset):
+        """Key env row i by the global env id offset + i (isaac_net/core/sharded.py:61-78): the env ids move in
+        place, the episode counters are rewound by one and every env is reset again under the global ids."""
+        offset = int(offset)
+        if offset == self.env_offset:
+            return
+        self.st["env_id"].add_(offset - self.env_offset)
+        self.env_offset = offset
+        self.st["episode"].sub_(1)
+        self.reset(None)
 
     def _reset_launch(self, m8):
         if not getattr(self, "_dcf_ready", False):

@@ -45,6 +45,7 @@ def pytest_collection_modifyitems(config, items):
             it.add_marker(skip)
 
 
-CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5"]
-DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr"]    # the downlink on (NRConfig(dl=True))
-MC_CASES = ["mc3", "mc3_ho"]                  # several cells (NRConfig(n_cells=3)), uplink
+# one cell; s14 / s18_ir / s10_w2: 14, 18 and 10 RBGs (106, 273 and 78 PRB at the 38.214 RBG sizes)
+CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14", "s18_ir", "s10_w2"]
+DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl"]    # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs
+MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho"]          # several cells (NRConfig(n_cells=3 / 2)), uplink

@@ -121,6 +121,40 @@ CASES = {
                             ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
                             cell_center_m=(60.0, 60.0)),
                    E=3, R=8, steps=40, kind="pose", arena=200.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
+    # one cell at other RBG counts: 106 PRB (14 RBGs of 8), PF, Rician fading, poses, two classes, 16 robots
+    "s14": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=16, msg_sizes=(300.0, 3000.0), fading_rho_per_ms=0.0,
+                         fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi",
+                         tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                E=3, R=16, steps=30, kind="pose", arena=200.0, walk=1.0, rates=(1.0, 0.3), resets={14: [1]}),
+    # 273 PRB at the default RBG size (18 RBGs of 16, the last one of 1 PRB), per-subband SNR, HARQ-IR, max C/I
+    "s18_ir": dict(cfg=dict(mu=1, n_prb=273, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                            harq_combining="ir_lena", frame_buffer=8, msg_sizes=(6000.0,), fading_rho_per_ms=0.3),
+                   E=3, R=8, steps=25, kind="snr3", subbands=18, snr=(-4.0, 14.0), rates=(0.9,), resets={12: [2]}),
+    # 133 PRB (17 RBGs of 8, the last of 5 PRB) with the downlink, SNR input, round robin
+    "s17_dl": dict(cfg=dict(mu=1, n_prb=133, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,
+                            frame_buffer=8, msg_sizes=(2000.0,), fading_rho_per_ms=0.0, dl=True),
+                   E=3, R=8, steps=25, kind="snr", snr=(-2.0, 16.0), rates=(0.8,), dl_sizes=(7000.0,),
+                   dl_rates=(0.7,), resets={9: [0]}),
+    # 78 PRB (10 RBGs of 8, the last of 6 PRB) on envs of 96 robots (two wavefronts), PF, poses
+    "s10_w2": dict(cfg=dict(mu=1, n_prb=78, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                            max_harq_tx=4, frame_buffer=8, msg_sizes=(700.0,), fading_rho_per_ms=0.0,
+                            channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                            cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                   E=2, R=96, steps=10, kind="pose", arena=200.0, walk=1.0, rates=(0.4,), resets={6: [1]}),
+    # two cells per env: 14 RBGs, PF, thermal noise with UL interference, power control, correlated fading
+    "mc2": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2, cell_layout="hex",
+                         cell_isd_m=120.0, noise_model="thermal", a3_offset_db=float("inf"), channel="tr38901",
+                         tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0, fading_rho_per_ms=0.5),
+                E=3, R=16, steps=25, kind="pose", arena=220.0, walk=0.5, rates=(0.7,), resets={12: [1]}),
+    # two cells with A3 handovers, 13 RBGs, max C/I, RLC UM drop, log-distance radio
+    "mc2_ho": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="maxci", n_harq=4,
+                            max_harq_tx=3, harq_fail="drop", frame_buffer=8, msg_sizes=(2500.0, 400.0), n_cells=2,
+                            cell_layout="hex", cell_isd_m=100.0, noise_model="thermal", a3_ttt_ms=10.0,
+                            ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
+                            cell_center_m=(60.0, 60.0)),
+                   E=3, R=8, steps=30, kind="pose", arena=160.0, walk=6.0, rates=(0.5, 1.0), resets={20: [0]}),
 }
 
 
@@ -209,7 +243,7 @@ def _inputs(name, c):
         x = rs.uniform(lo, hi, size=(T, E, R)).astype(np.float32)
     else:
         lo, hi = c["snr"]
-        x = rs.uniform(lo, hi, size=(T, E, R, 1)) + rs.normal(0.0, 2.0, size=(T, E, R, 13))
+        x = rs.uniform(lo, hi, size=(T, E, R, 1)) + rs.normal(0.0, 2.0, size=(T, E, R, c.get("subbands", 13)))
         x = x.astype(np.float32)
     assert counts.shape == (T, E, R, n_cls)
     if "dl_rates" in c:
