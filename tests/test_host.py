@@ -26,7 +26,12 @@ def test_refusals_name_each_unimplemented_feature():
                         (dict(fading_rician=True, rician_k_db=3.0), "Rician fading with several cells"),
                         (dict(ul_tpc=True), "TPC")):
         assert word in " ".join(f for f, _ in EN.refusals(P.NRConfig(**dict(mc, **extra)))), extra
-    assert "subbands" in " ".join(f for f, _ in EN.refusals(P.NRConfig(mu=1, n_prb=106)))   # one cell: 8 or 13
+    # one cell: the 38.214 RBG counts of the standard carriers run (106 PRB: 14 RBGs, 273: 18, 133: 17, 78: 10),
+    # other counts are refused; two cells run
+    for n_prb in (106, 273, 133, 78, 24, 162, 245):
+        assert EN.refusals(P.NRConfig(mu=1, n_prb=n_prb)) == [], n_prb
+    assert "subbands" in " ".join(f for f, _ in EN.refusals(P.NRConfig(mu=1, n_prb=100, rbg_size=4)))   # 25 RBGs
+    assert EN.refusals(P.NRConfig(**dict(mc, n_cells=2))) == []
 
 
 def test_make_engine_refuses_before_building():
