@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 6
+#define INET_NR_ABI_VERSION 7
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 128         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two
@@ -134,11 +134,19 @@ typedef struct InetNrParams {
     int32_t n_cells;                  /* cells per env C (1: the single-cell engine; > 1: inet_nr_step_cells) */
     int32_t rebase_at;                /* floor (bytes) from which a step rebases a robot's byte offsets (InetNrState.base;
                                          2^30; 0: never) */
+    /* 5G-LENA MAC switches (isaac_net/core/mac.py:26-31, 525-554; mac_ul.py:154-180) and UL power control at one cell
+       (nr_engine.py:649-650, 671-675); ABI version 7 */
+    int32_t pf_rbg;                   /* pf_update="rbg": the winner's PF average moves after every RBG grant */
+    int32_t pf_freeze;                /* pf_avg_idle="freeze": only robots with new data to schedule update it */
+    int32_t whole_band;               /* ul_power="whole_band": fixed PSD over the carrier (wb_db), no PHR cap */
+    int32_t pc1_on;                   /* one cell, UL power control from the mean UL reference SINR */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
     float gnb_x, gnb_y, hh2, dbp, pl_a, pl_n1, pl_c20, pl_c2, nl_b1, nl_b0, nl_c, nl_d, sig, amp, pl_const, pl_exp10;
     float proc_off_hi, proc_off_lo;   /* proc_offset_ms / control_step_ms as a double split in two floats */
+    float wb_db;                      /* whole_band: 10 log10(nprb / snr_ref_prbs) */
+    float pc_p0, pc_alpha;            /* pc1_on: P0 (dBm) and alpha of the fractional power control */
 } InetNrParams;
 
 /* One scheduled slot of the control step (host-built per TDD key, device resident). */

@@ -325,6 +325,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     if constexpr (FX == 1 || FX == 2) {
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
+        pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -598,7 +599,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     // PHR cap n_max (mac_ul.py:165-168): ref.mean(-1) -> snr_ref_prbs 10^((ref - phr_min) / 10) / w0 (several cells:
     // from the serving link's noise-only SNR at every UL slot)
     int n_max = S;
-    if (!DL && !MC && pm.phr_cap) {
+    if (!DL && !MC && pm.phr_cap && !pm.whole_band) {
         float rr[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) rr[s] = REF(s);
@@ -608,6 +609,17 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         f = clampf(f, 1.0f, (float)S);
         n_max = (int)f;
     }
+    // UL power control at one cell (nr_engine.py:649-650, 671-675): the backoff from the full power over snr_ref_prbs
+    // PRBs to the PSD P0 + alpha PL, the path loss from the mean UL reference SINR
+    float pc1 = -INFINITY;
+    if (!DL && !MC && pm.pc1_on) {
+        float rr[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) rr[s] = REF(s);
+        const float rx = aten_sum<S>(rr) / (float)S + pm.subband_noise;
+        pc1 = pm.ue_tx - (pm.pc_p0 + pm.pc_alpha * (pm.ue_tx - rx));
+    }
+    const bool use_pc = MC || pm.pc1_on;           // (several cells: cl.pc_on, -inf backoff when off)
 
     // ---------------- counter RNG key of this env and step ----------------
     uint32_t base0 = 0;
@@ -868,7 +880,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         // ============================ data slot (MacLink.slot) ============================
         // several cells (nr_engine.py:757-766): the UL reference of the serving link per subband against the serving
         // gNB's N+I estimate, the PHR cap from its noise-only SNR, the power-control backoff, this row's cells
-        float pc = -INFINITY;
+        float pc = pc1;
         float ni_la[MC ? S : 1];
         unsigned long long mycell = 0ull;
         if constexpr (MC) {
@@ -881,7 +893,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             const float rx_s = pg_s + pm.ue_tx;
             if (cl.pc_on) pc = pm.ue_tx - (cl.pc_p0 + cl.pc_alpha * (pm.ue_tx - rx_s));
             n_max = S;
-            if (pm.phr_cap) {
+            if (pm.phr_cap && !pm.whole_band) {
                 const float phr = rx_s - pm.subband_noise;
                 float f = floorf((pm.snr_ref_prbs * from_db(phr - pm.phr_min)) / pm.w0);
                 n_max = (int)clampf(f, 1.0f, (float)S);
@@ -978,7 +990,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 for (int s = 0; s < S; ++s) {
                     // UL: the PSD over one RBG, at most the power-control PSD (mac_ul.py:154-171); DL: sinr_ref + csi
                     // (mac_dl.py:42-43)
-                    const float wd = MC ? (s_wdb[s] > pc ? s_wdb[s] : pc) : s_wdb[s];
+                    // (ul_power "whole_band": the fixed PSD over the carrier, mac_ul.py:157-160)
+                    const float wdb = pm.whole_band ? pm.wb_db : s_wdb[s];
+                    const float wd = use_pc ? (wdb > pc ? wdb : pc) : wdb;
                     const float est = DL ? REF(s) + csi[s] : (REF(s) - wd) + csi[s];
                     s_eo[s * CW + lane] = pm.olla ? est + olla : est;
                 }
@@ -1078,6 +1092,11 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         int cnt = 0;
         float left = (float)need;
         uint32_t won = 0;
+        // pf_update "rbg" (mac.py:325-329, 526-532): the metric of RBG s is rate_s / max(base + wwin got, 1e-9) with
+        // base = (1 - wwin) avg and got the rate of the RBGs this robot won so far in the slot
+        const float pf_base = pm.pf_a * avg;
+        float got = 0.f;
+        auto rbg_metric = [&](int s) { return DivBy(clamp_min(pf_base + pm.pf_b * got, 1e-9f))(rate[s]); };
         // (one copy of the loop per retx-priority setting, so that the test is not repeated per RBG)
         auto allocate = [&](auto retx_prio) {
             constexpr bool RP = decltype(retx_prio)::value;
@@ -1085,7 +1104,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             for (int s = 0; s < S; ++s) {
                 const bool want = (cnt < want_cnt) && (has_rx || left > 0.0f);
                 // bid key: the bit pattern of the non-negative metric (ordered like the float), -1 for no bid
-                int m = want ? __float_as_int(mrow[s]) : -1;
+                int m = want ? __float_as_int(pm.pf_rbg ? rbg_metric(s) + prio : mrow[s]) : -1;
                 if constexpr (RP) {
                     const bool wr = want && has_rx;
                     if (cell_any(wr) && !wr) m = -1;
@@ -1093,6 +1112,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 // argmax over the robots of the scheduler, first robot on ties (torch argmax); -1: no bid
                 const bool sel = winner(m);
                 if (sel) { won |= 1u << s; ++cnt; }
+                if (pm.pf_rbg && sel) got = got + rate[s];
                 left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
             }
         };
@@ -1107,10 +1127,11 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
             for (int s = 0; s < S; ++s) {
                 bool avs = cell_any((rel_rs >> s) & 1u);
                 bool want = (cnt < want_cnt) && new_el && (left > 0.0f);
-                const float ms = metric_of(s);
+                const float ms = pm.pf_rbg ? rbg_metric(s) : metric_of(s);
                 const int m = want ? __float_as_int(ms) : -1;
                 const bool sel = winner(m) && avs;
                 if (sel) { won |= 1u << s; ++cnt; }
+                if (pm.pf_rbg && sel) got = got + rate[s];
                 left = left - (sel ? rate[s] : 0.0f);
             }
         }
@@ -1123,8 +1144,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         const bool tx_new = new_el && n_sb > 0;
         const bool tx = tx_rx || tx_new;
         // power split (mac_ul.py:173-180): PUSCH power spread over n_prb PRBs, at least the power-control backoff
-        const float sp0 = 10.0f * log10_clamped(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
-        const float sp = MC ? (sp0 > pc ? sp0 : pc) : sp0;
+        const float sp0 = pm.whole_band ? pm.wb_db : 10.0f * log10_clamped(clamp_min(n_prb / pm.snr_ref_prbs, 1e-3f));
+        const float sp = use_pc ? (sp0 > pc ? sp0 : pc) : sp0;
         // log of the held PRB count as torch computes it: logsumexp of log w over the held RBGs
         const float lnw = lw_eq ? s_lnw[__popc(won)] : lse_logw<S>(s_logw, won);
         // The (robot lane, RBG) pairs of the robots with `who` over the RBGs they hold, in lane order, into this wave's
@@ -1491,7 +1512,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                                    -10.0f, 10.0f);
         const int served = ok ? hi_tx - lo_tx : 0;
         if (!DL && tx) bsr = enq - sent;
-        avg = clamp_min(pm.pf_a * avg + pm.pf_b * (float)served, 1e-9f);
+        {
+            // PF average (mac.py:534-554): EWMA of the served bytes; pf_update "rbg": of the granted bytes of a new TB;
+            // pf_avg_idle "freeze": only robots with new data to schedule in this slot move it
+            const float upd = pm.pf_rbg ? (float)(tx_new ? tbs_new / 8 : 0) : (float)served;
+            const float na = clamp_min(pm.pf_a * avg + pm.pf_b * upd, 1e-9f);
+            avg = (pm.pf_freeze && !(need > 0 && !has_rx)) ? avg : na;
+        }
         if (pm.sched == 2 && tx) last_tx = g;
         // ---- counters ----
         c_new += tx_new; c_retx += tx_rx; c_ok += ok; c_fail += fail; c_exh += exh;
@@ -1836,7 +1863,8 @@ void launch_step(const StepArgs& a) {
 
 // the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
 inline int fx_profile(const InetNrParams& p) {
-    const bool common = p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
+    const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
+                        p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;
 }

@@ -90,12 +90,11 @@ def refusals(cfg: NRConfig):
     no(cfg.ul_mini_slot_symbols is not None, "mini-slot grants", "one scheduling occasion per slot")
     no(cfg.scheduler not in ("pf", "maxci", "rr"), f"scheduler={cfg.scheduler!r}", "pf, maxci and rr")
     no(cfg.pf_metric != "subband", "pf_metric='wideband'", "per-RBG PF metric")
-    no(cfg.pf_update != "slot" or cfg.pf_avg_idle != "decay", "pf_update / pf_avg_idle switches", "slot EWMA")
+    no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
+       "the per-RBG PF update of the pf scheduler")
     no(cfg.ul_retx_sched != "ofdma" or cfg.ul_amc_alloc != "current", "ul_retx_sched / ul_amc_alloc switches",
        "OFDMA retransmissions, current-allocation AMC")
-    no((cfg.ul_pc_on and not mc) or cfg.ul_tpc, "UL power control at one cell / closed-loop TPC",
-       "full-power PSD split (open-loop fractional power control with several cells)")
-    no(cfg.ul_power != "allocated", "ul_power='whole_band'", "allocated power split")
+    no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
     no(cfg.rician_mode == "los", "Rician K from the LOS state", "fixed rician_k_db or Rayleigh")
     no(cfg.fading_freq_corr or cfg.fading_doppler != "global", "frequency-correlated / per-robot Doppler fading",
        "i.i.d. subbands, one rho")
@@ -327,6 +326,12 @@ class HipNREngine:
         p.olla_up = cfg.olla_up_db
         p.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
         p.pf_a, p.pf_b = 1 - 1 / cfg.pf_window, 1 / cfg.pf_window
+        # 5G-LENA MAC switches and UL power control at one cell (mac.py:26-31, mac_ul.py:154-180, nr_engine.py:649-675)
+        p.pf_rbg, p.pf_freeze = int(cfg.pf_update == "rbg"), int(cfg.pf_avg_idle == "freeze")
+        p.whole_band = int(cfg.ul_power == "whole_band")
+        p.wb_db = 10 * math.log10(cfg.nprb / cfg.snr_ref_prbs)
+        p.pc1_on = int(cfg.ul_pc_on and cfg.n_cells == 1)
+        p.pc_p0, p.pc_alpha = cfg.ul_pc_p0_dbm, cfg.ul_pc_alpha
         p.target, p.phr_min, p.snr_ref_prbs = cfg.bler_target, cfg.phr_min_db, float(cfg.snr_ref_prbs)
         p.w0 = float(cfg.subband_prbs[0])
         p.ref_off = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs)

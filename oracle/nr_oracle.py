@@ -22,10 +22,12 @@ CPU the oracle is bitwise equal to the reference path (pinned by the golden traj
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
 
 Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state and outputs
-after every step of six uplink, three downlink and two three-cell scenarios) except what those scenarios do not reach:
-the "pf_wideband" / "wideband" PF metric is not implemented here (refused), `whole_band` UL power is not implemented
-(refused), and of the multi-cell options the RSRP admission floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are
-restated but parity unpinned (no trajectory sets them).
+after every step of twelve uplink scenarios (among them 10, 14 and 18 RBGs, two-wavefront envs, the per-RBG and frozen
+PF average, whole-band UL power and UL power control at one cell), five downlink and four multi-cell scenarios with two
+and three cells) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF metric, ul_retx_sched
+"tdma" and ul_amc_alloc "previous" are not implemented here (refused), and of the multi-cell options the RSRP admission
+floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are restated but parity unpinned (no reference trajectory sets them;
+the GPU is checked against this restatement for them).
 """
 from __future__ import annotations
 
@@ -624,10 +626,9 @@ class OracleEngine:
         self.C = C = cfg.n_cells
         assert cfg.ul and cfg.ul_grant_model == "lumped"
         assert C == 1 or not (cfg.dl or cfg.rlf), "several cells: uplink only, no radio link failure"
-        assert C > 1 or not cfg.ul_pc_on, "UL power control at one cell is not restated"
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
-        assert cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay" and cfg.ul_retx_sched == "ofdma"
-        assert cfg.ul_amc_alloc == "current" and not cfg.ul_tpc and cfg.ul_power == "allocated"
+        assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
+        assert cfg.ul_retx_sched == "ofdma" and cfg.ul_amc_alloc == "current" and not cfg.ul_tpc
         assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
@@ -854,6 +855,8 @@ class OracleEngine:
         cfg = self.cfg
         N = cfg.slots_per_step
         g0 = t * N
+        if self.pc_on:           # one cell with UL power control: path loss from the input SNR (nr_engine.py:649-650)
+            self.pc_backoff = self._pc_backoff(ul_ref.mean(-1) + cfg.subband_noise_dbm)
         if self.rician:
             self.k_lin = self.k_in                       # _rician_update with no ramp (nr_engine.py:410-415)
         for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
@@ -994,8 +997,12 @@ class OracleEngine:
         u.sr_t = torch.where(need_sr, torch.full_like(u.sr_t, g), u.sr_t)
 
     def _split(self, n_prb):
-        """UlMac._split (mac_ul.py:173-180): per-PRB backoff from the full power, at least the power-control one."""
-        sp = 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
+        """UlMac._split (mac_ul.py:173-180): per-PRB backoff from the full power (ul_power="whole_band": the fixed PSD
+        over the carrier), at least the power-control one."""
+        if self.cfg.ul_power == "whole_band":
+            sp = torch.full_like(n_prb, 10 * math.log10(self.cfg.nprb / self.cfg.snr_ref_prbs))
+        else:
+            sp = 10 * torch.log10((n_prb / self.cfg.snr_ref_prbs).clamp(min=1e-3))
         return sp if not self.pc_on else torch.maximum(sp, self.pc_backoff)
 
     def _slot(self, L, g, frac, nsym, sinr_ref, gain_now, rel, ack_slot):
@@ -1028,7 +1035,11 @@ class OracleEngine:
             new_el = new_el & self.sched_ok
         pending = (L.h_state == 1).any(-1)
         rx_nsb = L.h_nsb.gather(-1, rx_p[..., None]).squeeze(-1)
-        if ul:                                           # UlMac._sched_estimate (mac_ul.py:154-171)
+        if ul and cfg.ul_power == "whole_band":          # fixed PSD over the carrier, no PHR cap (mac_ul.py:157-160)
+            wb = 10 * math.log10(cfg.nprb / cfg.snr_ref_prbs)
+            est = sinr_ref - (wb if not self.pc_on else self.pc_backoff.clamp(min=wb)[..., None]) + L.csi
+            n_max = torch.full((E, R), S, dtype=torch.long)
+        elif ul:                                         # UlMac._sched_estimate (mac_ul.py:154-171)
             if not self.pc_on:
                 est = sinr_ref - 10 * torch.log10(w / cfg.snr_ref_prbs) + L.csi
             else:
@@ -1082,9 +1093,17 @@ class OracleEngine:
         cnt = torch.zeros(E, R, dtype=torch.long)
         left = need.float()
         cols = []
+        rbg_pf = cfg.pf_update == "rbg"
+        if rbg_pf:       # the winner's average moves after every RBG (mac.py:325-329, _rbg_metric mac.py:526-532)
+            wwin = 1.0 / cfg.pf_window
+            base = (1 - wwin) * L.avg
+            got = torch.zeros(E, R)
+
+        def metric_at(s):
+            return rate_sb[..., s] / (base + wwin * got).clamp(min=1e-9) if rbg_pf else metric_sb[..., s]
         for s in range(S):
             want = (cnt < want_cnt) & (has_rx | (left > 0))
-            m = torch.where(want, metric_sb[..., s] + prio, torch.full_like(left, -1.0))
+            m = torch.where(want, metric_at(s) + prio, torch.full_like(left, -1.0))
             wr = want & has_rx if lex else None
             if M is None:
                 if lex:
@@ -1100,6 +1119,8 @@ class OracleEngine:
                 oh = (onehot(wi, R) & (best >= 0)[..., None]).any(1)
             cols.append(oh)
             cnt = cnt + oh.long()
+            if rbg_pf:
+                got = got + rate_sb[..., s] * oh
             left = left - rate_sb[..., s] * oh * ~has_rx
         won = torch.stack(cols, -1)
         if not lex:                                      # release short retransmissions (mac.py:353-379)
@@ -1110,7 +1131,7 @@ class OracleEngine:
             cols = []
             for s in range(S):
                 want = (cnt < want_cnt) & new_el & (left > 0)
-                m = torch.where(want, metric_sb[..., s], torch.full_like(left, -1.0))
+                m = torch.where(want, metric_at(s), torch.full_like(left, -1.0))
                 if M is None:
                     best, wi = m.max(-1)
                     oh = onehot(wi, R) & ((best >= 0) & rel_rs[..., s].any(-1))[:, None]
@@ -1120,6 +1141,8 @@ class OracleEngine:
                     oh = (onehot(wi, R) & ((best >= 0) & av)[..., None]).any(1)
                 cols.append(oh)
                 cnt = cnt + oh.long()
+                if rbg_pf:
+                    got = got + rate_sb[..., s] * oh
                 left = left - rate_sb[..., s] * oh
             won = won | torch.stack(cols, -1)
         n_sb = won.sum(-1)
@@ -1208,7 +1231,13 @@ class OracleEngine:
         if ul:
             L.bsr = torch.where(tx, L.unsent(), L.bsr)
             L.csi = gain_now
-        L.avg = ((1 - 1 / cfg.pf_window) * L.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
+        if cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay":
+            L.avg = ((1 - 1 / cfg.pf_window) * L.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
+        else:                    # MacLink._pf_update (mac.py:534-554): granted TB bytes, the active list only
+            wwin = 1.0 / cfg.pf_window
+            upd = (tbs_new // 8).float() * tx_new if cfg.pf_update == "rbg" else served.float()
+            new_avg = ((1 - wwin) * L.avg + wwin * upd).clamp(min=AVG_MIN)
+            L.avg = torch.where((need > 0) & ~has_rx, new_avg, L.avg) if cfg.pf_avg_idle == "freeze" else new_avg
         if cfg.scheduler == "rr":
             L.last_tx = torch.where(tx, torch.full_like(L.last_tx, g), L.last_tx)
         c = L.ctr

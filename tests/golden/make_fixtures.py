@@ -155,6 +155,30 @@ CASES = {
                             ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
                             cell_center_m=(60.0, 60.0)),
                    E=3, R=8, steps=30, kind="pose", arena=160.0, walk=6.0, rates=(0.5, 1.0), resets={20: [0]}),
+    # 5G-LENA MAC switches (mac.py:26-31): PF average moved by every RBG grant, only for robots with new data
+    "lena_pf": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                             pf_window=20.0, pf_update="rbg", pf_avg_idle="freeze", n_harq=8, max_harq_tx=4,
+                             frame_buffer=16, msg_sizes=(600.0, 5000.0), fading_rho_per_ms=0.0, fading_rician=True,
+                             rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                             cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                    E=3, R=16, steps=30, kind="pose", arena=240.0, walk=1.0, rates=(1.0, 0.3), resets={15: [2]}),
+    # the same freeze on both links with the downlink on, max C/I (the frozen average is state only), SNR input
+    "lena_dl": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="pf", pf_avg_idle="freeze", n_harq=4,
+                             max_harq_tx=3, frame_buffer=8, msg_sizes=(2500.0,), fading_rho_per_ms=0.5, dl=True),
+                    E=3, R=8, steps=25, kind="snr", snr=(-2.0, 16.0), rates=(0.9,), dl_sizes=(6000.0,),
+                    dl_rates=(0.8,), resets={11: [1]}),
+    # whole-band UL power (fixed PSD over the carrier, no PHR cap) with UL power control at one cell, per-subband SNR,
+    # round robin, HARQ-IR
+    "wb_pc": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,
+                           harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2000.0,), ul_power="whole_band",
+                           ul_pc=True, ul_pc_p0_dbm=-95.0, ul_pc_alpha=0.8, fading_rho_per_ms=0.0),
+                  E=3, R=8, steps=25, kind="snr3", snr=(0.0, 20.0), rates=(1.0,), resets={13: [0]}),
+    # UL power control at one cell with poses (path loss from the UL reference SINR), PF
+    "pc1": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), ul_pc=True, ul_pc_p0_dbm=-90.0,
+                         ul_pc_alpha=0.7, fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMi",
+                         tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                E=3, R=12, steps=25, kind="pose", arena=200.0, walk=1.0, rates=(0.8,), resets={10: [1]}),
 }
 
 
