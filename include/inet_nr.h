@@ -44,8 +44,9 @@ extern "C" {
 #define INET_NR_ABI_VERSION 7
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
-#define INET_NR_MAX_R 128         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two
-                                     wavefronts (65..128: the UL with pose or SNR [E][R] input, one cell) */
+#define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
+                                     wavefronts (65..128 / 129..256: the UL with pose or SNR [E][R] input, one cell;
+                                     four wavefronts with 8 or 13 subbands) */
 #define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
 #define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
 #define INET_NR_MAX_ROWS 64       /* scheduled slots (InetNrRow) per control step */

@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libinet_nr.so")
 PHASE_LIB = os.path.join(HERE, "libinet_nr_phase.so")
 UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip", "nr_step_mc.hip", "nr_step_mc2.hip", "nr_step_w2.hip",
-         "wifi.hip"] + [f"nr_step_s{s}.hip" for s in (10, 11, 12, 14, 16, 17, 18)]
+         "nr_step_w4.hip", "wifi.hip"] + [f"nr_step_s{s}.hip" for s in (10, 11, 12, 14, 16, 17, 18)]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]

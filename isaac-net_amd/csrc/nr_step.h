@@ -306,16 +306,16 @@ DEV T sel_of(const T (&v)[N], int idx) {
 // segment's lanes of one serving cell: ballots masked to the cell, NC interleaved butterflies), fractional power
 // control, and the same-slot interference sum of every gNB and RBG over the other cells' robots (each lane's terms in
 // LDS, summed by one lane per (cell, RBG) in torch's CPU order); cl holds the association state and constants.
-// RBT = 128: envs of 65..128 robots, one env per workgroup of two wavefronts (W = 2); the env-wide collectives then
-// combine the two waves' ballots and butterflies through LDS (xchg), and every cooperative loop runs a number of
-// rounds that both waves agree on, so that every barrier is reached by both.
+// RBT = 128 / 256: envs of 65..128 / 129..256 robots, one env per workgroup of W = 2 / 4 wavefronts; the env-wide
+// collectives then combine the waves' ballots and butterflies through LDS (xchgw), and every cooperative loop runs a
+// number of rounds that all waves agree on, so that every barrier is reached by all.
 //
 // FX = 1 builds the kernel for the common configuration (PF, chase combining, EESM, RLC AM, OLLA, PHR cap, retx
 // priority, a fixed Rician phasor, fading; fx_profile), FX = 2 for the same without the Rician phasor: those
 // switches become
 // compile-time constants, which removes their tests from the slot loop and the scalar registers that hold them.
 template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC, int FX = 0>
-__global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
+__global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
     InetNrState st, LS lk_in, InetNrTables tb_in, InetNrParams pm_in, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
@@ -332,7 +332,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     const LS& lk = [&]() -> const LS& { if constexpr (DL) return lk_in; else return st; }();
     constexpr bool MC = NC > 1;
     static_assert(!(MC && (DL || VREF)), "several cells: the UL with pose input");
-    constexpr int W = RBT > STEP_WAVE ? 2 : 1;         // wavefronts per env
+    constexpr int W = RBT > STEP_WAVE ? RBT / STEP_WAVE : 1;   // wavefronts per env (1, 2 or 4)
+    static_assert(W == 1 || W == 2 || W == 4, "envs of up to 64, 128 or 256 robots");
     constexpr int CW = STEP_WAVE * W;                   // lanes per workgroup (the LDS column stride)
     static_assert(!(MC && W > 1), "several cells: one wavefront per env");
     constexpr int NCS = NC * S;                        // fading links per robot (cell-major, subband-minor)
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     __shared__ uint4 s_dlist[CW];
     __shared__ float s_rkey[W > 1 ? CW : 1];                     // W = 2: retransmission ranking keys and RBG counts
     __shared__ int s_rval[W > 1 ? CW : 1];
-    __shared__ int s_xw[8];                                      // W = 2: the two waves' values of an env collective
+    __shared__ int s_xw[4 * W];                                  // W > 1: the waves' values of an env collective
     // several cells, one env per wavefront: the interference pairs of a UL slot (robot lane | RBG << 8 | serving cell
     // << 16, then the fading state (re, im) on every cell); at most one holder per (cell, RBG)
     __shared__ float s_ipair[MC ? NC * S * (1 + 2 * NC) : 1];
@@ -387,17 +388,17 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
     float* const s_ni = reinterpret_cast<float*>(hist_l + envs_pw * 3 * HB) + eloc * 2 * NCS;
     float* const s_if = s_ni + NCS;
 
-    // ---------------- env-wide collectives: inside the segment (W = 1), or over the two waves of the env (W = 2)
-    // through LDS behind one barrier that both waves reach. Successive exchanges alternate between two buffers: a wave
-    // writes a buffer again only two exchanges later, after a barrier that the other wave reaches once it has read it.
+    // ---------------- env-wide collectives: inside the segment (W = 1), or over the W waves of the env through LDS
+    // behind one barrier that every wave reaches. Successive exchanges alternate between two buffers: a wave writes a
+    // buffer again only two exchanges later, after a barrier that the other waves reach once they have read it.
     int xbuf = 0;
-    auto xchg2 = [&](int v, int& v0, int& v1) {        // v: uniform in each wave
-        int* const b = s_xw + 4 * xbuf;
+    auto xchgw = [&](int v, int (&vals)[W]) {          // v: uniform in each wave; vals: every wave's, in wave order
+        int* const b = s_xw + 2 * W * xbuf;
         xbuf ^= 1;
         if (wl == 0) b[lane >> 6] = v;
         __syncthreads();
-        v0 = b[0];
-        v1 = b[1];
+#pragma unroll
+        for (int w = 0; w < W; ++w) vals[w] = b[w];
     };
     auto env_any = [&](bool p) -> bool {
         if constexpr (RBT == 32) {
@@ -405,18 +406,24 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
         } else if constexpr (W == 1) {
             return seg_any(p, rb, lane);
         } else {
-            int a0, a1;
-            xchg2(__ballot(p) != 0ull ? 1 : 0, a0, a1);
-            return (a0 | a1) != 0;
+            int a[W];
+            xchgw(__ballot(p) != 0ull ? 1 : 0, a);
+            int any = 0;
+#pragma unroll
+            for (int w = 0; w < W; ++w) any |= a[w];
+            return any != 0;
         }
     };
     auto env_sum = [&](int v) -> int {
         if constexpr (W == 1) {
             return bsum(v, rb);
         } else {
-            int a0, a1;
-            xchg2(bsum(v, STEP_WAVE), a0, a1);
-            return a0 + a1;
+            int a[W];
+            xchgw(bsum(v, STEP_WAVE), a);
+            int sum = 0;
+#pragma unroll
+            for (int w = 0; w < W; ++w) sum += a[w];
+            return sum;
         }
     };
 
@@ -920,15 +927,18 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? 2 : 1), NC > 1 ? 1 :
                 const unsigned long long b = (__ballot(m == mx) & mycell) >> (lane & ~(rb - 1));
                 return m >= 0 && b != 0ull && (int)__builtin_ctzll(b) == r;
             } else if constexpr (W > 1) {
-                // each wave's max and its first lane holding it; the env's winner is wave 0's on ties
+                // each wave's max and its first lane holding it; the env's winner is the first wave's on ties
                 const int mxw = bmax_i(m, STEP_WAVE);
                 const int fw = (int)__builtin_ctzll(__ballot(m == mxw));
-                int* const b = s_xw + 4 * xbuf;           // (alternating buffers, as xchg2)
+                int* const b = s_xw + 2 * W * xbuf;       // (alternating buffers, as xchgw)
                 xbuf ^= 1;
                 if (wl == 0) { b[2 * (lane >> 6)] = mxw; b[2 * (lane >> 6) + 1] = fw; }
                 __syncthreads();
-                const int m0 = b[0], f0 = b[1], m1 = b[2], f1 = b[3];
-                return m >= 0 && lane == (m0 >= m1 ? f0 : STEP_WAVE + f1);
+                int best = b[0], at = b[1];
+#pragma unroll
+                for (int w = 1; w < W; ++w)
+                    if (b[2 * w] > best) { best = b[2 * w]; at = STEP_WAVE * w + b[2 * w + 1]; }
+                return m >= 0 && lane == at;
             } else if constexpr (RBT == 32) {
                 // the first lane of each 32-lane segment holding the maximum, found on the scalar unit
                 const int mx = bmax_i(m, 32);
@@ -1869,13 +1879,14 @@ inline int fx_profile(const InetNrParams& p) {
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;
 }
 
-// envs of 65..128 robots: one env per workgroup of two wavefronts (UL, pose or SNR input)
-template <int S, int P, bool IR, int FX = 0>
+// envs of 65..128 (RBT = 128) or 129..256 robots (RBT = 256): one env per workgroup of two or four wavefronts (UL,
+// pose or SNR input)
+template <int S, int P, bool IR, int FX = 0, int RBT = 128>
 void launch_step_w2(const StepArgs& a) {
     const InetNrCells none{};
-    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, 128, InetNrState, 1, FX>), dim3(a.grid), dim3(2 * STEP_WAVE),
-                       a.lds, a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb,
-                       a.n_data, a.arr, none);
+    hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, RBT, InetNrState, 1, FX>), dim3(a.grid), dim3(RBT), a.lds,
+                       a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
+                       a.arr, none);
 }
 
 // the multi-cell step: NC cells, pose input, runtime segment width (RBT = 0) or one fixed at compile time
@@ -1941,6 +1952,16 @@ StepFn pick_step_w2_s(int P, bool ir, int fx) {
     return nullptr;
 }
 StepFn pick_step_w2(int S, int P, bool ir, int fx);        // nr_step_w2.hip
+// four-wavefront builds (R = 129..256), 8 and 13 subbands: every (P, IR)
+template <int S>
+StepFn pick_step_w4_s(int P, bool ir) {
+#define INET_PICK_W4(PP) \
+    if (P == PP) return ir ? &launch_step_w2<S, PP, true, 0, 256> : &launch_step_w2<S, PP, false, 0, 256>;
+    INET_PICK_W4(2) INET_PICK_W4(4) INET_PICK_W4(8) INET_PICK_W4(16)
+#undef INET_PICK_W4
+    return nullptr;
+}
+StepFn pick_step_w4(int S, int P, bool ir);                // nr_step_w4.hip
 
 // the one-cell step builds for S subbands: envs of up to 64 robots on one wavefront (nullptr: no build)
 inline StepFn pick_step_one_cell(int S, int P, bool ir, bool vref, int rb, int fx) {

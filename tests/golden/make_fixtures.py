@@ -155,6 +155,12 @@ CASES = {
                             ho_interruption_ms=5.0, li_alpha=0.5, fading_rho_per_ms=0.0,
                             cell_center_m=(60.0, 60.0)),
                    E=3, R=8, steps=30, kind="pose", arena=160.0, walk=6.0, rates=(0.5, 1.0), resets={20: [0]}),
+    # envs of 200 robots (four wavefronts per env on the GPU): 52 PRB (13 RBGs), PF, poses, 8 HARQ
+    "w4": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                        max_harq_tx=4, frame_buffer=8, msg_sizes=(500.0,), fading_rho_per_ms=0.0, channel="tr38901",
+                        tr38901_scenario="UMi", tr38901_los="los", cell_positions_m=((100.0, 100.0),),
+                        gnb_height_m=10.0),
+               E=2, R=200, steps=8, kind="pose", arena=200.0, walk=1.0, rates=(0.3,), resets={5: [0]}),
     # 5G-LENA MAC switches (mac.py:26-31): PF average moved by every RBG grant, only for robots with new data
     "lena_pf": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
                              pf_window=20.0, pf_update="rbg", pf_avg_idle="freeze", n_harq=8, max_harq_tx=4,
