@@ -807,17 +807,17 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 ent = s_dlist[wbase + ri];                    // (ri < n_need: a valid entry, read for the next item)
                 const float zr = normal_of(mix32(mix32(hin) ^ bfc), mix32(mix32(hin + GOLD) ^ bfc));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bfc), mix32(mix32(hin + 3u * GOLD) ^ bfc));
-                s_z[(2 * qc) * CW + Lc] = zr;
-                s_z[(2 * qc + 1) * CW + Lc] = zi;
+                // the innovation term sqrt(1 - rho^2) z / sqrt(2) of the AR(1) step, ready for the robot's update
+                s_z[(2 * qc) * CW + Lc] = div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                s_z[(2 * qc + 1) * CW + Lc] = div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
             }
             INET_PH(1);                            // fading innovations (the robots' own updates follow)
             __syncthreads();
             if (draw) {
 #pragma unroll
                 for (int q = 0; q < NCS; ++q) {
-                    float zr = s_z[(2 * q) * CW + lane], zi = s_z[(2 * q + 1) * CW + lane];
-                    hr[q] = row.rho * hr[q] + div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
-                    hi[q] = row.rho * hi[q] + div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+                    hr[q] = row.rho * hr[q] + s_z[(2 * q) * CW + lane];
+                    hi[q] = row.rho * hi[q] + s_z[(2 * q + 1) * CW + lane];
                 }
             }
         }
@@ -1126,7 +1126,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 left = left - ((sel && !has_rx) ? rate[s] : 0.0f);
             }
         };
-        if (pm.retx_prio) allocate(std::true_type{});
+        // (the lexicographic mask only acts where some robot of the scheduler has an admitted retransmission)
+        if (pm.retx_prio && (W > 1 || __ballot(has_rx) != 0ull)) allocate(std::true_type{});
         else allocate(std::false_type{});
         if (!pm.retx_prio) {                          // release short retransmissions (mac.py:353-379)
             bool short_ = has_rx && (__popc(won) != rx_nsb);
