@@ -49,9 +49,9 @@ def load_package():
     return mod
 
 
-def survey_bytes_per_robot_step(eng):
-    """The algorithmic bytes of one robot-step in the canonical compact layout (the survey's measurement section):
-    2 B_rw + B_ro + B_in + B_out with B_rw = 12 S + 32 + 32 P + 18 F (fading and CSI, MAC scalars, HARQ processes,
+def canonical_bytes_per_robot_step(eng):
+    """The algorithmic bytes of one robot-step in the canonical compact layout (each state word at its smallest
+    width, the FIFO at 18 B per frame): 2 B_rw + B_ro + B_in + B_out with B_rw = 12 S + 32 + 32 P + 18 F (fading and CSI, MAC scalars, HARQ processes,
     frame FIFO, read and written once), B_ro = 8 (Rician phasor), B_in = 10 (pose and arrivals) and B_out = 9 F + 16.
     2,362 B at S = 13, P = 8, F = 32."""
     S, P, F = eng.S, eng.P, eng.F
@@ -63,11 +63,25 @@ def counter_summary(name):
     equals the hash the loaded library was built from), else None."""
     from isaac_net_amd import _lib
     path = os.path.join(ROOT, "profiles", name + ".json")
-    if not os.path.exists(path):
+    if not name or not os.path.exists(path):
         return None
     d = json.load(open(path))
     built = _lib.load().inet_nr_build_info().decode().rsplit("src=", 1)[-1]
     return d if d.get("src") == built else None
+
+
+def measured_fields(name, k_avg_ms):
+    """roofline fields from the counter summary profiles/<name>.json recorded on the loaded library's sources:
+    traffic (HBM bytes per launch, rocprofv3 FETCH_SIZE + WRITE_SIZE scaled by a copy-kernel calibration),
+    valu_issue_util (a wave64 VALU instruction occupies a 16-lane SIMD for 4 cycles; 1024 SIMDs at 2.4 GHz, over the
+    kernel's measured duration) and the summary's source hash; all null when there is no such summary."""
+    cs = counter_summary(name)
+    if not cs:
+        return {"traffic": None, "valu_issue_util": None, "counters_src": None}
+    valu = cs.get("valu_insts_per_dispatch")
+    return {"traffic": cs.get("bytes_per_launch"),
+            "valu_issue_util": valu * 4 / (1024 * k_avg_ms * 1e-3 * 2.4e9) if valu else None,
+            "counters_src": cs.get("src")}
 
 
 def step_kernel_bytes(eng):
@@ -234,6 +248,17 @@ def run_wifi(args, P, torch):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
+    # At this size the host loop is slower than the GPU, so an event pair recorded in the timed loop also holds the
+    # idle gap before its launch. The kernel durations come from the same launches queued behind a GPU spin: the
+    # spin outlasts the host's enqueueing, and each event pair then brackets its kernel alone.
+    eng.kernel_events = ev = KernelTimer(args.steps, dev)
+    torch.cuda._sleep(int(2e6 + 4e5 * args.steps))
+    for i in range(args.steps):
+        s = args.warmup + i
+        eng.submit_counts(wl.counts[s])
+        eng.step(None, wl.poses[s])
+    torch.cuda.synchronize()
+    eng.kernel_events = None
     k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
     nbytes, per_robot = (dcf_step_bytes if slots else wifi_step_bytes)(eng)
@@ -255,8 +280,12 @@ def run_wifi(args, P, torch):
                       "parallelism": "single GPU", "launch": "eager"},
            "env_steps_per_s": E * args.steps / dt,
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "wifi_step_kernel",
+                        "frac": achieved / PEAK_GBS, "kernel": "wifi_step_kernel",
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
+                        **measured_fields(f"wifi_step_kernel_counters_{args.workload}_epw{args.envs_per_wave}"
+                                          if (E, R) == (2048, 16) else "", k_avg),
+                        "kernel_timing": "HIP events around each launch on the launch stream, the timed loop's "
+                                         "launches repeated behind a GPU spin",
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_station_step": per_robot}}
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
@@ -337,10 +366,19 @@ def run_dl(args, P, torch):
         k = sorted(ev.ms())
         avg = sum(k) / len(k)
         nb, per_robot = fn(eng)
+        extra = {}
+        if fn is step_kernel_bytes:                         # the UL kernel: the canonical bytes, as rl_scale's line
+            extra = {"layout_bytes_per_launch": nb, "layout_bytes_per_robot_step": per_robot}
+            per_robot = canonical_bytes_per_robot_step(eng)
+            nb = E * R * per_robot
         ach = nb / (avg * 1e-3) / 1e9
+        tag = "nr_step_kernel_counters_rl_scale_dl_" + ("ul" if fn is step_kernel_bytes else "dl")
+        meas = measured_fields(tag, avg) if (E, R) == (4096, 32) and args.out_format == "reference" else \
+            measured_fields("", avg)
         ms[name] = {"bound": "hbm", "achieved": ach, "peak": PEAK_GBS, "unit": "GB/s", "frac": ach / PEAK_GBS,
-                    "traffic": None, "kernel": name, "kernel_ms_avg": avg, "kernel_ms_median": k[len(k) // 2],
-                    "algorithmic_bytes_per_launch": nb, "algorithmic_bytes_per_robot_step": per_robot}
+                    "kernel": name, "kernel_ms_avg": avg, "kernel_ms_median": k[len(k) // 2],
+                    "algorithmic_bytes_per_launch": nb, "algorithmic_bytes_per_robot_step": per_robot, **extra,
+                    **meas}
     dom = max(ms.values(), key=lambda r: r["kernel_ms_avg"])
     c = eng.counters()
     res = {"metric": f"robot-slots/sec (UL + DL data slots) @{E} envs×{R} robots K_ul={k_ul} K_dl={k_dl}",
@@ -411,9 +449,11 @@ def run_mc(args, P, torch):
            "env_steps_per_s": E * args.steps / dt,
            "mean_interference_over_thermal_db": float(10 * torch.log10((st["net.ni_ul"] / noise).mean())),
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "nr_step_kernel<cells 3>",
+                        "frac": achieved / PEAK_GBS, "kernel": "nr_step_kernel<cells 3>",
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
+                        **measured_fields("nr_step_kernel_counters_mc_interf" if (E, R) == (1024, 64) and
+                                          args.out_format == "reference" else "", k_avg),
                         "note": "arithmetic-bound kernel: frac is the distance from the HBM bound"}}
     if args.phase_clocks:
         rb = 1 << (R - 1).bit_length()                   # robots per segment: the next power of two
@@ -454,7 +494,7 @@ def run_freq_sel(args, P, torch):
     k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
     layout_bytes, layout_per_robot = step_kernel_bytes(eng)
-    per_robot = survey_bytes_per_robot_step(eng)
+    per_robot = canonical_bytes_per_robot_step(eng)
     nbytes = E * R * per_robot
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     res = {"metric": f"robot-slots/sec @{E} envs×{R} robots K={k_ul}, 273 PRB in 8 RBGs",
@@ -470,10 +510,12 @@ def run_freq_sel(args, P, torch):
                                                                "inside the step kernel)"},
            "env_steps_per_s": E * args.steps / dt,
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                        "frac": achieved / PEAK_GBS, "traffic": None, "kernel": "nr_step_kernel<two waves>",
+                        "frac": achieved / PEAK_GBS, "kernel": "nr_step_kernel<two waves>",
                         "kernel_ms_avg": k_avg, "kernel_ms_median": k_ms[len(k_ms) // 2],
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_robot_step": per_robot,
-                        "layout_bytes_per_launch": layout_bytes, "layout_bytes_per_robot_step": layout_per_robot}}
+                        "layout_bytes_per_launch": layout_bytes, "layout_bytes_per_robot_step": layout_per_robot,
+                        **measured_fields("nr_step_kernel_counters_freq_sel" if (E, R) == (16384, 128) and
+                                          args.out_format == "reference" else "", k_avg)}}
     if args.phase_clocks:
         res["phase_clocks"] = phase_clocks("w2", 2 * E)
     copy_calibration(args, res, torch, dev)
@@ -651,7 +693,7 @@ def main():
     kept_mean = sum(q_post) / max(len(q_post), 1)
     layout_bytes, layout_per_robot = step_kernel_bytes(eng)
     touched = step_kernel_touched_bytes(eng, qlen_mean, kept_mean)
-    per_robot = survey_bytes_per_robot_step(eng)
+    per_robot = canonical_bytes_per_robot_step(eng)
     nbytes = E * R * per_robot
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     value = E * R * k_ul * args.steps / dt
