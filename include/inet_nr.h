@@ -41,14 +41,14 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 7
+#define INET_NR_ABI_VERSION 8
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
                                      wavefronts (65..128 / 129..256: the UL with pose or SNR [E][R] input, one cell;
                                      four wavefronts with 8 or 13 subbands) */
 #define INET_NR_MAX_KF 16         /* plane waves per shadowing field */
-#define INET_NR_NCTR 12           /* per-env counters, see InetNrState.ctr */
+#define INET_NR_NCTR 13           /* per-env counters, see InetNrState.ctr */
 #define INET_NR_MAX_ROWS 64       /* scheduled slots (InetNrRow) per control step */
 #define INET_NR_MAX_C 7           /* cells per env */
 
@@ -87,7 +87,9 @@ typedef struct InetNrState {
        (log_distance) */
     float *field;
     /* per-env counters [E][INET_NR_NCTR] int64: tb_new, tb_retx, tb_ok, tb_fail, exhaust, bytes_ok, bytes_new,
-       lost_frames, new_while_pending, prb_used, reserved, reserved; and per-env HARQ histograms
+       lost_frames, new_while_pending, prb_used, and the 5G-LENA grant accounting tb_bytes, tb_empty, retx_block
+       (mac.py:119-122, 299, 492-493; accumulated always, reported by the engine when a LENA switch is on); and
+       per-env HARQ histograms
        [E][3][max_tx + 1] int64: decoded TBs by transmissions, TBs sent as transmission k, failed as transmission k */
     int64_t *ctr, *hist;
     /* the engine's control-step counter T on the device [1] int64: read by inet_nr_step / inet_nr_submit when
@@ -98,6 +100,9 @@ typedef struct InetNrState {
        robot's floor reaches params.rebase_at at the end of a step, the step moves its offsets down by the floor and
        adds it to base, so the int32 values stay below 2^31 for any run length. */
     int64_t *base;
+    /* per robot [E][R] float: PRBs of the robot's last PUSCH (UlMac.last_nprb, mac_ul.py:51, mac.py:484), read and
+       written only with params.amc_prev (ABI version 8) */
+    float *last_nprb;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -141,6 +146,10 @@ typedef struct InetNrParams {
     int32_t pf_freeze;                /* pf_avg_idle="freeze": only robots with new data to schedule update it */
     int32_t whole_band;               /* ul_power="whole_band": fixed PSD over the carrier (wb_db), no PHR cap */
     int32_t pc1_on;                   /* one cell, UL power control from the mean UL reference SINR */
+    int32_t retx_tdma;                /* ul_retx_sched="tdma" (mac.py:279-299): one UL retransmission per slot and cell,
+                                         the oldest NACK, and no new data in that slot (ABI version 8) */
+    int32_t amc_prev;                 /* ul_amc_alloc="previous" (mac.py:393-401): the UL MCS for the PRBs of the last
+                                         PUSCH (InetNrState.last_nprb), the TB for this allocation (ABI version 8) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */

@@ -25,6 +25,9 @@ NRB_FR1 = {
 }
 # TS 38.214 Table 5.1.2.2.1-1: (largest bandwidth-part size, P for configuration 1, P for configuration 2)
 RBG_ROWS = ((36, 2, 4), (72, 4, 8), (144, 8, 16), (275, 16, 16))
+# the 5G-LENA MAC switches and their default values (isaac_net/core/config.py:121-123)
+LENA_MAC_DEFAULTS = {"pf_update": "slot", "pf_avg_idle": "decay", "ul_retx_sched": "ofdma", "ul_amc_alloc": "current",
+                     "ul_grant_model": "lumped"}
 
 
 def rbg_size_38214(n_prb, config=1):
@@ -366,6 +369,11 @@ class NRConfig:
     @property
     def ul_rtt(self):
         return self.ul_harq_rtt_slots if self.ul_harq_rtt_slots is not None else self.gnb_proc_slots + self.k2
+
+    def lena_mac_switches(self):
+        """The 5G-LENA MAC switches set away from their defaults, {field: value} (config.py:1092-1094): any of them
+        on adds the grant-accounting counters tb_bytes, tb_empty and retx_block to both links."""
+        return {k: getattr(self, k) for k, v in LENA_MAC_DEFAULTS.items() if getattr(self, k) != v}
 
     @property
     def ul_slots_per_step(self):

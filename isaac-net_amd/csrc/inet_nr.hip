@@ -175,6 +175,7 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
         size_t ir = (size_t)e * R + r;
         st.sent[ir] = 0; st.floor_[ir] = 0; st.bsr[ir] = 0; st.sr_t[ir] = -1; st.last_tx[ir] = -1;
         if (st.base) st.base[ir] = 0;
+        if (st.last_nprb) st.last_nprb[ir] = 0.f;
         st.olla[ir] = 0.f; st.avg[ir] = 100.f; st.enq[ir] = 0; st.qlen[ir] = 0;
         for (int s = 0; s < S; ++s) st.csi[((size_t)e * S + s) * R + r] = 0.f;
         for (int p = 0; p < P; ++p) {
@@ -249,6 +250,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.input_kind < 0 || p.input_kind > 2) return INET_NR_EINVAL;
     if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
+    if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);

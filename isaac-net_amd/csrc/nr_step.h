@@ -325,7 +325,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     if constexpr (FX == 1 || FX == 2) {
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
-        pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0;
+        pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -466,6 +466,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     }
     float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
     if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
+    float lnp = 0.f;                                   // PRBs of the last PUSCH (ul_amc_alloc "previous")
+    if (!DL && pm.amc_prev && act) lnp = ldo(st.last_nprb, o_r);
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
     if (lane < MAX_M) s_thr[lane] = lane <= tb.mcs_max ? tb.thr_ref[lane] : INFINITY;
     if (lane < MAX_M) s_se[lane] = lane < tb.M ? tb.se[lane] : 0.0f;
@@ -640,6 +642,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // per-robot counters of this step (summed over the segment at the end)
     int c_new = 0, c_retx = 0, c_ok = 0, c_fail = 0, c_exh = 0, c_new_pend = 0;
     int c_bytes_ok = 0, c_bytes_new = 0, c_prb = 0;
+    int c_tbb = 0, c_tbe = 0, c_blk = 0;               // 5G-LENA grant accounting: TB bytes, empty TBs, TDMA blocks
+    const bool lena = pm.pf_rbg || pm.pf_freeze || pm.retx_tdma || pm.amc_prev;   // (kept with a LENA switch on)
 
     auto ack_ptr = [&]() {
         int a = sent;
@@ -1059,7 +1063,16 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         INET_PH(2);                                // SR / CQI, grants, candidates, estimate, MCS, rate, metric
         // retransmission admission (mac.py:300-313): rank by the metric sum inside each scheduler, admit while the RBG
         // counts fit (the segment's total fitting implies every cell's)
-        if (env_any(has_rx)) {
+        if (!DL && pm.retx_tdma) {
+            // ul_retx_sched "tdma" (mac.py:279-299): one retransmission per scheduler, the oldest NACK (the lowest
+            // ready slot of the robot's ready process, the first robot on ties), alone in its slot: the scheduler
+            // takes no new data. (Ready slots are non-negative, so the bid is too.)
+            const bool adm = winner(has_rx ? 0x7fffffff - best_rdy : -1);
+            const bool blk = cell_any(adm);
+            c_blk += (adm && rx_nsb < S) ? 1 : 0;
+            new_el = new_el && !blk;
+            has_rx = adm;
+        } else if (env_any(has_rx)) {
             int val = has_rx ? rx_nsb : 0;
             int tot = env_sum(val);
             if (tot > S) {
@@ -1162,13 +1175,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         // The (robot lane, RBG) pairs of the robots with `who` over the RBGs they hold, in lane order, into this wave's
         // part of pl ([64 S] entries per wave: lane | RBG << 8); returns this wave's count. Per-RBG work on the held
         // RBGs (at most S per scheduler, against S per robot) is then dealt over the wavefront.
-        auto build_pairs = [&](bool who, int* pl) -> int {
+        auto build_pairs = [&](bool who, uint32_t msk, int* pl) -> int {
             int n;
-            int off = wave_prefix64(who ? __popc(won) : 0, wl, n);
+            int off = wave_prefix64(who ? __popc(msk) : 0, wl, n);
             int* const wpl = pl + wbase * S;
 #pragma unroll
             for (int s = 0; s < S; ++s)
-                if (who && ((won >> s) & 1u)) wpl[off++] = lane | (s << 8);
+                if (who && ((msk >> s) & 1u)) wpl[off++] = lane | (s << 8);
             return n;
         };
         // lse_eesm (the EESM log-sum over the held RBGs) of every robot with `who`, for its dB row xv and MCS mc: the
@@ -1184,7 +1197,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 for (int s = 0; s < S; ++s) s_dx[s * CW + lane] = xv[s];
                 s_la_i[lane] = mc;
             }
-            const int n_pairs = build_pairs(who, s_pl);
+            const int n_pairs = build_pairs(who, won, s_pl);
             __syncthreads();
 #pragma unroll 1
             for (int it = wl; it < n_pairs; it += STEP_WAVE) {
@@ -1224,7 +1237,12 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         if constexpr (W == 1) any_new = __ballot(tx_new) != 0ull;
         else any_new = env_any(tx_new);
         if (any_new) {
-            // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on the held RBGs
+            // the RBGs the MCS is searched over: the held ones; ul_amc_alloc "previous" with whole-band power, every
+            // RBG (mac.py:396)
+            const bool la_all = !DL && pm.amc_prev && pm.whole_band;
+            const uint32_t la_m = la_all ? (1u << S) - 1u : won;
+            const float la_lnw = la_all ? (lw_eq ? s_lnw[S] : lse_logw<S>(s_logw, la_m)) : lnw;
+            // estimated SINR per RBG: x_s = (ref_s - sp) + csi_s in dB, and its linear value on those RBGs
             bool nan = false;
             if (pm.eesm) {
                 // the linear values on the pair list of the new TBs' held RBGs (the dB rows in s_x rows S..2S-1, the
@@ -1237,7 +1255,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     if (tx_new) s_ex[s * CW + lane] = x;
                 }
                 int* const s_pl = reinterpret_cast<int*>(s_x);
-                const int n_pairs = build_pairs(tx_new, s_pl);
+                const int n_pairs = build_pairs(tx_new, la_m, s_pl);
                 __syncthreads();
 #pragma unroll 1
                 for (int it = wl; it < n_pairs; it += STEP_WAVE) {
@@ -1245,7 +1263,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     s_lin[sq * CW + L] = from_db_mid(clampf(s_ex[sq * CW + L], -30.0f, 60.0f));
                 }
             } else {
-                const uint32_t held = tx_new ? won : 0u;
+                const uint32_t held = tx_new ? la_m : 0u;
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     const float x = DL ? REF(s) + csi[s] : (REF(s) - sp) + csi[s];
@@ -1254,9 +1272,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     if ((held >> s) & 1u) s_lin[s * CW + lane] = from_db_mid(clampf(x, -30.0f, 60.0f));
                 }
             }
-            const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, won, lnw) : 0.f;
+            const float eff_md = (!pm.eesm && tx_new) ? mean_db_held<S, CW>(s_x, lane, s_logw, la_m, la_lnw) : 0.f;
             const int np = (int)n_prb;
             const int toff = (row.nsym_idx * (tb.NPRB + 1) + np) * tb.M;
+            // ul_amc_alloc "previous" (mac.py:393-401): the MCS is searched on the table row of the last PUSCH's PRB
+            // count (this allocation's while there was none); the TB of the chosen MCS is this allocation's
+            const int np_sel = (!DL && pm.amc_prev && lnp > 0.0f) ? (int)lnp : np;
+            const int toff_sel = (row.nsym_idx * (tb.NPRB + 1) + np_sel) * tb.M;
             // The search for the highest MCS that meets the target is shared by the whole wavefront: every round,
             // each robot still searching gets 64 / n_searching lanes, which evaluate its next MCS candidates in
             // parallel (top, top - 1, ...); the robot takes the highest candidate that passes or moves its top down.
@@ -1264,9 +1286,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             // divergent tail. A robot's inputs (table row, held RBGs, lnw, OLLA offset, mean_db value) and its
             // linear SINR row are read from LDS by its helpers.
             // (W = 2: each wave searches for its own robots; the rounds go on while either wave has robots left)
-            s_la_i[lane] = toff;
-            s_la_i[CW + lane] = (int)(won | (nan ? 0x80000000u : 0u));
-            s_la_f[lane] = lnw;
+            s_la_i[lane] = toff_sel;
+            s_la_i[CW + lane] = (int)(la_m | (nan ? 0x80000000u : 0u));
+            s_la_f[lane] = la_lnw;
             s_la_f[CW + lane] = pm.olla ? olla : 0.0f;
             s_la_f[2 * CW + lane] = eff_md;
             int top = tb.mcs_max, found_m = -1;
@@ -1523,6 +1545,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                                    -10.0f, 10.0f);
         const int served = ok ? hi_tx - lo_tx : 0;
         if (!DL && tx) bsr = enq - sent;
+        if (!DL && pm.amc_prev && tx) lnp = n_prb;        // UlMac.last_nprb (mac.py:484)
         {
             // PF average (mac.py:534-554): EWMA of the served bytes; pf_update "rbg": of the granted bytes of a new TB;
             // pf_avg_idle "freeze": only robots with new data to schedule in this slot move it
@@ -1535,6 +1558,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         c_new += tx_new; c_retx += tx_rx; c_ok += ok; c_fail += fail; c_exh += exh;
         c_bytes_ok += served; c_bytes_new += tx_new ? byt_new : 0; c_new_pend += (tx_new && pending);
         c_prb += tx ? (int)n_prb : 0;
+        if (lena) { c_tbb += tx_new ? tbs_new / 8 : 0; c_tbe += (tx_new && byt_new == 0) ? 1 : 0; }
         if (tx) {
             int kh = ntx < pm.max_tx ? ntx : pm.max_tx;
             atomicAdd(&my_hist[HB + kh], 1);
@@ -1767,7 +1791,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         asm volatile("" : "+v"(o_r), "+v"(o_sr), "+v"(o_pr));
     if (act) {
         sto(lk.sent, o_r, sent); sto(lk.floor_, o_r, floor_);
-        if constexpr (!DL) { sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t); }
+        if constexpr (!DL) {
+            sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
+            if (pm.amc_prev) sto(st.last_nprb, o_r, lnp);
+        }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
         if (arr.counts || rebased) sto(lk.enq, o_r, enq);
 #pragma unroll
@@ -1812,6 +1839,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     const int v_exh = env_sum(act ? c_exh : 0), v_lost = env_sum(act ? lost_new : 0);
     const int v_pend = env_sum(act ? c_new_pend : 0), v_bok = env_sum(act ? c_bytes_ok : 0);
     const int v_bnew = env_sum(act ? c_bytes_new : 0), v_prb = env_sum(act ? c_prb : 0);
+    int v_tbb = 0, v_tbe = 0, v_blk = 0;
+    if (lena) { v_tbb = env_sum(act ? c_tbb : 0); v_tbe = env_sum(act ? c_tbe : 0); v_blk = env_sum(act ? c_blk : 0); }
     __syncthreads();                                  // histogram atomics of every lane are done
     if constexpr (MC) {
         if (e < E) {
@@ -1828,6 +1857,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         int64_t* c = lk.ctr + (size_t)e * INET_NR_NCTR;
         c[0] += v_new; c[1] += v_retx; c[2] += v_ok; c[3] += v_fail; c[4] += v_exh;
         c[5] += v_bok; c[6] += v_bnew; c[7] += v_lost; c[8] += v_pend; c[9] += v_prb;
+        c[10] += v_tbb; c[11] += v_tbe; c[12] += v_blk;
     }
     if (e < E && r < 3 * HB) lk.hist[(size_t)e * 3 * HB + r] += my_hist[r];
     if (e < E && rb < 3 * HB) {                       // segments narrower than the histogram: robot 0 adds the rest
@@ -1875,6 +1905,7 @@ void launch_step(const StepArgs& a) {
 // the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
+                        p.retx_tdma == 0 && p.amc_prev == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

@@ -26,9 +26,11 @@ from .phy import PhyTables, cqi_tables
 
 BIG_SLOT = 0x7FFFFFFF
 FADING, BLER_UL, BLER_DL = 1, 2, 3
-NCTR = 12
+NCTR = 13
 CTR_NAMES = ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
              "new_while_pending", "prb_used")
+# the 5G-LENA grant accounting (mac.py:119-122), counters 10..12, reported when a LENA MAC switch is on
+LENA_CTR_NAMES = ("tb_bytes", "tb_empty", "retx_block")
 
 
 class HipUnsupported(NotImplementedError, ValueError):
@@ -92,8 +94,6 @@ def refusals(cfg: NRConfig):
     no(cfg.pf_metric != "subband", "pf_metric='wideband'", "per-RBG PF metric")
     no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
        "the per-RBG PF update of the pf scheduler")
-    no(cfg.ul_retx_sched != "ofdma" or cfg.ul_amc_alloc != "current", "ul_retx_sched / ul_amc_alloc switches",
-       "OFDMA retransmissions, current-allocation AMC")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
     no(cfg.rician_mode == "los", "Rician K from the LOS state", "fixed rician_k_db or Rayleigh")
     no(cfg.fading_freq_corr or cfg.fading_doppler != "global", "frequency-correlated / per-robot Doppler fading",
@@ -214,6 +214,7 @@ class HipNREngine:
             "ctr": z(E, NCTR, dt=torch.int64), "hist": z(E, 3, cfg.max_harq_tx + 1, dt=torch.int64),
             "clock": z(1, dt=torch.int64),
             "base": z(E, R, dt=torch.int64),           # byte-stream base of every robot's UL offsets
+            "last_nprb": z(E, R, dt=f32),               # PRBs of the last PUSCH (ul_amc_alloc "previous")
         }
         self._n_fields = nf
         self._last_snr = torch.zeros(E, R, device=d)
@@ -334,6 +335,7 @@ class HipNREngine:
         p.whole_band = int(cfg.ul_power == "whole_band")
         p.wb_db = 10 * math.log10(cfg.nprb / cfg.snr_ref_prbs)
         p.pc1_on = int(cfg.ul_pc_on and cfg.n_cells == 1)
+        p.retx_tdma, p.amc_prev = int(cfg.ul_retx_sched == "tdma"), int(cfg.ul_amc_alloc == "previous")
         p.pc_p0, p.pc_alpha = cfg.ul_pc_p0_dbm, cfg.ul_pc_alpha
         p.target, p.phr_min, p.snr_ref_prbs = cfg.bler_target, cfg.phr_min_db, float(cfg.snr_ref_prbs)
         p.w0 = float(cfg.subband_prbs[0])
@@ -959,6 +961,8 @@ class HipNREngine:
             res["rv_tx"] = h[:, 1].sum(0).double().tolist()
             res["rv_fail"] = h[:, 2].sum(0).double().tolist()
             res["prb_avail"] = float(sum(cfg.subband_prbs)) * self.E * self.C * n_slots
+            if cfg.lena_mac_switches():
+                res.update({k: float(c[10 + i]) for i, k in enumerate(LENA_CTR_NAMES)})
             return res
         out = {"ul": link(self.st, self._ul_slots_run)}
         if self.dl:
@@ -1000,6 +1004,8 @@ class HipNREngine:
         if pre == "ul":
             out.update({"bsr": L(st["bsr"]), "sr_t": L(st["sr_t"]), "q.det": rs((qm & 2) != 0),
                         "q.hid": rs(L(st["q_hid"]))})
+            if cfg.ul_amc_alloc == "previous":        # UlMac AMC_STATE (mac_ul.py:51)
+                out["last_nprb"] = st["last_nprb"]
         else:                                         # the DL link holds no BSR / SR state (constant initial values)
             out.update({"bsr": torch.zeros_like(out["sent"]), "sr_t": torch.full_like(out["sent"], -1)})
         return {f"{pre}.{k}": v for k, v in out.items()}
@@ -1053,6 +1059,8 @@ class HipNREngine:
             pairs += (("bsr", "bsr"), ("sr_t", "sr_t"))
         for a, b in pairs:
             st[a].copy_(I(g(b)))
+        if pre == "ul" and cfg.ul_amc_alloc == "previous" and f"{pre}.last_nprb" in sd:
+            st["last_nprb"].copy_(g("last_nprb").float())
         st["olla"].copy_(g("olla"))
         st["avg"].copy_(g("avg"))
         st["csi"].copy_(rs(g("csi")))
@@ -1157,6 +1165,9 @@ class HipNREngine:
             c = ls["ctr"]
             for i, k in enumerate(CTR_NAMES):
                 out[f"net.{name}.ctr[{k}]"] = c[:, i].sum().float()
+            if cfg.lena_mac_switches():
+                for i, k in enumerate(LENA_CTR_NAMES):
+                    out[f"net.{name}.ctr[{k}]"] = c[:, 10 + i].sum().float()
             out[f"net.{name}.ctr[prb_avail]"] = torch.tensor(float(sum(cfg.subband_prbs)) * E * self.C * n_slots,
                                                              device=self.dev)
             h = ls["hist"].float()
@@ -1179,7 +1190,8 @@ class HipNREngine:
                 "net.dl.q.det", "net.dl.q.hid", "net.dl_newest"}
     # Reference host values that switch on what this engine does not run (traffic models, access procedures, hooks
     # and traces, frequency-correlated or per-robot fading, blockage, O2I, radio link failure, TPC, BSR grants,
-    # MIMO, QoS, the LENA MAC): a checkpoint holding another value was written with that feature on.
+    # MIMO, QoS): a checkpoint holding another value was written with that feature on. (_lena_mac, the LENA grant
+    # counters' switch, must equal this config's: _ck_expected.)
     _CK_OFF = {"_gate": None, "_dl_gate": None, "_los_fn": None, "access": None, "_extras": False, "traffic": None,
                "traffic_dl": None, "per_robot_doppler": False, "net.fc_mode": None, "net.trace_frames": None,
                "net.trace_frames_dl": None, "net._user_hook[ul]": None, "net._user_hook[dl]": None,
@@ -1188,6 +1200,13 @@ class HipNREngine:
                **{f"net.{lk}.{k}": v for lk in ("ul", "dl") for k, v in (
                    ("slot_hook", None), ("sinr_hook", None), ("trace", None), ("mimo", False), ("qos", False),
                    ("_tpc", False), ("_bsr_model", False), ("_lena_mac", False), ("_occ", None))}}
+
+    def _ck_expected(self, k):
+        """The value host switch k must hold in a checkpoint this engine loads."""
+        if k.endswith("._lena_mac"):
+            cfg = getattr(self, "config", None)
+            return bool(cfg.lena_mac_switches()) if cfg is not None else False
+        return self._CK_OFF[k]
 
     def _strict_extra_keys(self, sd, used):
         """strict loading: the state keys of sd that are neither restored (used) nor known to hold no state here,
@@ -1198,8 +1217,10 @@ class HipNREngine:
                 continue
             if torch.is_tensor(v) or isinstance(v, np.ndarray):
                 bad.append(k)
-            elif k in self._CK_OFF and v != self._CK_OFF[k] and not (v is None and self._CK_OFF[k] is False):
-                bad.append(f"{k}={v!r}")
+            elif k in self._CK_OFF:
+                want = HipNREngine._ck_expected(self, k)
+                if v != want and not (v is None and want is False):
+                    bad.append(f"{k}={v!r}")
         return bad
 
     def load_state_dict(self, sd, strict=True, T=None, last_g=None):
@@ -1238,7 +1259,8 @@ class HipNREngine:
             used.update((pre + ".k", pre + ".phi"))
         for name in ("ul", "dl"):
             used.update(f"net.{name}.{k}" for k in ("ntx_hist", "rv_tx", "rv_fail", "prb_used_env"))
-            used.update(f"net.{name}.ctr[{k}]" for k in CTR_NAMES + ("prb_avail",))
+            used.update(f"net.{name}.ctr[{k}]" for k in CTR_NAMES + ("prb_avail",) +
+                        (LENA_CTR_NAMES if cfg.lena_mac_switches() else ()))
         if strict:
             bad = self._strict_extra_keys(sd, used)
             if bad:
@@ -1261,6 +1283,9 @@ class HipNREngine:
             c = torch.zeros_like(ls["ctr"])
             for i, k in enumerate(CTR_NAMES):
                 c[0, i] = int(round(float(sd[f"net.{name}.ctr[{k}]"])))
+            for i, k in enumerate(LENA_CTR_NAMES):
+                if f"net.{name}.ctr[{k}]" in sd:
+                    c[0, 10 + i] = int(round(float(sd[f"net.{name}.ctr[{k}]"])))
             if f"net.{name}.prb_used_env" in sd:
                 c[:, 9] = g(f"net.{name}.prb_used_env").round().long()
             ls["ctr"].copy_(c)

@@ -21,13 +21,14 @@ The element-wise operations, the reduction calls and their order are those of th
 CPU the oracle is bitwise equal to the reference path (pinned by the golden trajectories under tests/golden/).
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
 
-Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state and outputs
-after every step of twelve uplink scenarios (among them 10, 14 and 18 RBGs, two-wavefront envs, the per-RBG and frozen
-PF average, whole-band UL power and UL power control at one cell), five downlink and four multi-cell scenarios with two
-and three cells) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF metric, ul_retx_sched
-"tdma" and ul_amc_alloc "previous" are not implemented here (refused), and of the multi-cell options the RSRP admission
-floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are restated but parity unpinned (no reference trajectory sets them;
-the GPU is checked against this restatement for them).
+Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state, outputs and
+counters after every step of eighteen uplink scenarios (among them 10, 14 and 18 RBGs, envs of 128 and 200 robots,
+the 5G-LENA MAC switches: the per-RBG and frozen PF average, TDMA retransmissions, AMC on the previous PUSCH's PRBs,
+whole-band UL power and UL power control at one cell), five downlink and five multi-cell scenarios with two and three
+cells) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF metric is not implemented here
+(refused), and of the multi-cell options the RSRP admission floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are
+restated but parity unpinned (no reference trajectory sets them; the GPU is checked against this restatement for
+them).
 """
 from __future__ import annotations
 
@@ -432,13 +433,16 @@ class Link:
 
     INIT = {"sent": 0, "floor": 0, "olla": 0.0, "avg": 100.0, "bsr": 0, "sr_t": -1, "csi": 0.0, "h_state": 0,
             "h_lo": 0, "h_hi": 0, "h_ready": 0, "h_ntx": 0, "h_mcs": 0, "h_tbs": 0, "h_nsb": 0, "h_comb": 0.0,
-            "h_lexp": -float("inf"), "h_nrb": 0.0, "last_tx": -1}
+            "h_lexp": -float("inf"), "h_nrb": 0.0, "last_tx": -1, "last_nprb": 0.0}
     INIT_Q = {"cap": -1, "start": 0, "end": 0, "lost": False, "fin": float("inf"), "cls": 0, "det": False, "hid": 0}
     CTR = ("tb_new", "tb_retx", "tb_ok", "tb_fail", "exhaust", "bytes_ok", "bytes_new", "lost_frames",
            "new_while_pending", "prb_used", "prb_avail")
+    LENA_CTR = ("tb_bytes", "tb_empty", "retx_block")       # with the 5G-LENA MAC switches on (mac.py:119-122)
 
-    def __init__(self, d, E, R, S, P, F, phy):
+    def __init__(self, d, E, R, S, P, F, phy, lena=False):
         self.dir, self.phy = d, phy
+        if lena:
+            self.CTR = self.CTR + self.LENA_CTR
         self.F = F
         self.FIELDS_Q = ("cap", "start", "end", "lost", "fin", "cls", "det", "hid") if d == "ul" else \
             ("cap", "start", "end", "lost", "fin", "cls")
@@ -452,6 +456,7 @@ class Link:
         self.h_comb, self.h_nrb = z((E, R, P), 0.0, torch.float32), z((E, R, P), 0.0, torch.float32)
         self.h_lexp = z((E, R, P), -float("inf"), torch.float32)
         self.last_tx = z((E, R), -1, torch.long)
+        self.last_nprb = z((E, R), 0.0, torch.float32)     # PRBs of the last PUSCH (ul_amc_alloc "previous")
         self.q_cap, self.q_start, self.q_end = z((E, R, F), -1, torch.long), z((E, R, F), 0, torch.long), \
             z((E, R, F), 0, torch.long)
         self.q_lost, self.q_fin = z((E, R, F), False, torch.bool), z((E, R, F), float("inf"), torch.float64)
@@ -628,7 +633,7 @@ class OracleEngine:
         assert C == 1 or not (cfg.dl or cfg.rlf), "several cells: uplink only, no radio link failure"
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
-        assert cfg.ul_retx_sched == "ofdma" and cfg.ul_amc_alloc == "current" and not cfg.ul_tpc
+        assert not cfg.ul_tpc
         assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
@@ -649,12 +654,13 @@ class OracleEngine:
         self.last_hid = torch.zeros(E, dtype=torch.long)
         self.last_g = None
         S, P, F = self.S, self.P, self.F
-        self.ul = Link("ul", E, R, S, P, F, self.phy)
+        lena = bool(cfg.lena_mac_switches())
+        self.ul = Link("ul", E, R, S, P, F, self.phy, lena)
         self.dl = None
         if cfg.dl:
             self.tabs_dl = tabs_dl if tabs_dl is not None else PhyTables(cfg.mcs_table, cfg.bler_target, mt,
                                                                          cfg.dl_mcs_max)
-            self.dl = Link("dl", E, R, S, P, F, Phy(self.tabs_dl))
+            self.dl = Link("dl", E, R, S, P, F, Phy(self.tabs_dl), lena)
             self.cqi = None
             if cfg.cqi_table == "38214":
                 thr, cm = cqi_tables(self.tabs_dl, cfg.mcs_table)
@@ -1074,7 +1080,28 @@ class OracleEngine:
             metric_sb = rate_sb / L.avg.clamp(min=AVG_MIN)[..., None]
         # retransmission admission, ranked inside every cell (mac.py:300-313)
         rkey = torch.where(has_rx, metric_sb.sum(-1), torch.full_like(metric_sb[..., 0], -1.0))
-        if M is None:
+        if ul and cfg.ul_retx_sched == "tdma":
+            # one retransmission per slot and cell, the oldest NACK (lowest ready slot, first robot on ties), and no
+            # new data in that cell's slot (mac.py:279-299)
+            rdy = torch.where(has_rx, L.h_ready.gather(-1, rx_p[..., None]).squeeze(-1),
+                              torch.full_like(rx_nsb, BIG))
+            if M is None:
+                adm = onehot(rdy.argmin(-1), R) & has_rx
+                blk = adm.any(-1)
+                n_block = int((blk & (rx_nsb * adm).sum(-1).lt(S)).sum())
+                block = blk[:, None]
+            else:
+                rx_c = has_rx[:, None, :] & M
+                first = torch.where(M, rdy[:, None, :], torch.full_like(M, BIG, dtype=rdy.dtype)).argmin(-1)
+                adm_c = onehot(first, R) & rx_c
+                adm = adm_c.any(1)
+                blk_c = adm_c.any(-1)
+                block = (blk_c[..., None] & M).any(1)
+                n_block = int((blk_c & (rx_nsb[:, None, :] * adm_c).sum(-1).lt(S)).sum())
+            new_el = new_el & ~block
+            L.ctr["retx_block"] += n_block
+            has_rx = adm
+        elif M is None:
             order = rkey.argsort(-1, descending=True)
             cum = (rx_nsb * has_rx).gather(-1, order).cumsum(-1)
             adm_sorted = has_rx.gather(-1, order) & (cum <= S)
@@ -1153,8 +1180,17 @@ class OracleEngine:
         # link adaptation (mac.py:386-405; UL estimate mac_ul.py:182-183, DL the scheduler's)
         est_tx = sinr_ref - self._split(n_prb)[..., None] + L.csi if ul else est
         off = L.olla if cfg.olla else torch.zeros_like(L.olla)
-        mcs_new, tbs_new = phy.select_mcs(est_tx, won, off, n_prb, nsym, cfg.dmrs_re_per_prb,
-                                          cfg.overhead_re_per_prb, cfg.eff_sinr, w, self.dec)
+        amc_prev = ul and cfg.ul_amc_alloc == "previous"
+        if amc_prev:       # the MCS for the PRBs of the previous PUSCH, the TB for this allocation (mac.py:393-401)
+            ref_prb = torch.where(L.last_nprb > 0, L.last_nprb, n_prb)
+            ref_won = torch.ones_like(won) if cfg.ul_power == "whole_band" else won
+            mcs_new, _ = phy.select_mcs(est_tx, ref_won, off, ref_prb, nsym, cfg.dmrs_re_per_prb,
+                                        cfg.overhead_re_per_prb, cfg.eff_sinr, w, self.dec)
+            tbs_new = phy.tbs_all(n_prb, nsym, cfg.dmrs_re_per_prb, cfg.overhead_re_per_prb).gather(
+                -1, mcs_new[..., None]).squeeze(-1)
+        else:
+            mcs_new, tbs_new = phy.select_mcs(est_tx, won, off, n_prb, nsym, cfg.dmrs_re_per_prb,
+                                              cfg.overhead_re_per_prb, cfg.eff_sinr, w, self.dec)
         cap_b = (tbs_new // 8 - cfg.tb_overhead_bytes).clamp(min=1)
         byt_new = torch.minimum(cap_b, unsent)
         # bind TBs to processes (mac.py:407-426)
@@ -1231,6 +1267,8 @@ class OracleEngine:
         if ul:
             L.bsr = torch.where(tx, L.unsent(), L.bsr)
             L.csi = gain_now
+        if amc_prev:
+            L.last_nprb = torch.where(tx, n_prb, L.last_nprb)
         if cfg.pf_update == "slot" and cfg.pf_avg_idle == "decay":
             L.avg = ((1 - 1 / cfg.pf_window) * L.avg + (1 / cfg.pf_window) * served).clamp(min=AVG_MIN)
         else:                    # MacLink._pf_update (mac.py:534-554): granted TB bytes, the active list only
@@ -1246,6 +1284,8 @@ class OracleEngine:
         c["bytes_new"] += int((byt_new * tx_new).sum()); c["new_while_pending"] += int((tx_new & pending).sum())
         c["prb_used"] += float((n_prb * tx).sum()); c["prb_avail"] += float(self.w.sum()) * E * self.C
         c["lost_frames"] += lost_new
+        if "tb_bytes" in c:                              # the 5G-LENA grant accounting (mac.py:492-493)
+            c["tb_bytes"] += int(((tbs_new // 8) * tx_new).sum()); c["tb_empty"] += int((tx_new & (byt_new == 0)).sum())
         # RLC in-order delivery (mac.py:500-503)
         ack = L.ack_ptr()
         done = (L.q_cap >= 0) & (L.q_end <= ack[..., None]) & ~L.q_lost & torch.isinf(L.q_fin)
@@ -1301,6 +1341,8 @@ class OracleEngine:
         items = [(k, self, v) for k, v in self.NET_KEYS.items()]
         for lk in self.links():
             keys = dict(self.LINK_KEYS, **(self.UL_ONLY if lk.dir == "ul" else {}))
+            if lk.dir == "ul" and self.cfg.ul_amc_alloc == "previous":
+                keys["last_nprb"] = "last_nprb"
             items += [(f"{lk.dir}.{k}", lk, v) for k, v in keys.items()]
         if self.dl is not None:
             items.append(("net.dl_newest", self, "dl_newest"))

@@ -48,9 +48,10 @@ def pytest_collection_modifyitems(config, items):
 # one cell; s14 / s18_ir / s10_w2: 14, 18 and 10 RBGs (106, 273 and 78 PRB at the 38.214 RBG sizes); w4: envs of
 # 200 robots (four wavefronts); lena_pf: the PF
 # average moved per RBG grant and frozen outside the active list; wb_pc / pc1: whole-band UL power and UL power control
-# at one cell
+# at one cell; tdma / amc_prev / lena_v2 / wb_amc: TDMA UL retransmissions and the UL MCS on the previous PUSCH's PRBs,
+# alone, with every other switch, and with whole-band power
 CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14", "s18_ir", "s10_w2", "lena_pf",
-         "wb_pc", "pc1", "w4"]
+         "wb_pc", "pc1", "w4", "tdma", "amc_prev", "lena_v2", "wb_amc"]
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl"]
-MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho"]          # several cells (NRConfig(n_cells=3 / 2)), uplink
+MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena"]   # several cells (NRConfig(n_cells=3 / 2)), uplink

@@ -185,6 +185,39 @@ CASES = {
                          ul_pc_alpha=0.7, fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMi",
                          tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
                 E=3, R=12, steps=25, kind="pose", arena=200.0, walk=1.0, rates=(0.8,), resets={10: [1]}),
+    # 5G-LENA UL HARQ in TDMA (mac.py:279-299): one retransmission per slot, the oldest NACK, alone in its slot; PF,
+    # poses at the cell edge (many NACKs), i.i.d. fading
+    "tdma": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                          max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), ul_retx_sched="tdma",
+                          fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                          cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                 E=3, R=16, steps=30, kind="pose", arena=400.0, walk=1.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # 5G-LENA UL AMC on the previous PUSCH's PRBs (mac.py:393-401, 484), SNR input, round robin, chase combining
+    "amc_prev": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,
+                              frame_buffer=8, msg_sizes=(3000.0, 700.0), ul_amc_alloc="previous",
+                              fading_rho_per_ms=0.5),
+                     E=3, R=8, steps=25, kind="snr", snr=(0.0, 18.0), rates=(0.9, 0.6), resets={12: [2]}),
+    # every 5G-LENA MAC switch this engine runs together (LENA_MAC_V2 without the BSR grant pipeline): per-RBG PF
+    # updates frozen while idle, TDMA retransmissions, AMC on the previous PUSCH, 8 B of MAC overhead, HARQ-IR
+    "lena_v2": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                             pf_window=20.0, pf_update="rbg", pf_avg_idle="freeze", ul_retx_sched="tdma",
+                             ul_amc_alloc="previous", tb_overhead_bytes=8, n_harq=8, max_harq_tx=4,
+                             harq_combining="ir_lena", frame_buffer=16, msg_sizes=(600.0, 5000.0),
+                             fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                             cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                    E=3, R=16, steps=30, kind="pose", arena=320.0, walk=1.0, rates=(1.0, 0.3), resets={15: [0]}),
+    # whole-band UL power with AMC on the previous PUSCH (the MCS over every RBG), per-subband SNR, HARQ-IR
+    "wb_amc": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,
+                            harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2000.0,), ul_power="whole_band",
+                            ul_amc_alloc="previous", ul_retx_sched="tdma", fading_rho_per_ms=0.0),
+                   E=3, R=8, steps=25, kind="snr3", snr=(0.0, 20.0), rates=(1.0,), resets={13: [0]}),
+    # two cells with TDMA retransmissions and AMC on the previous PUSCH, per cell (mac.py:286-297), 14 RBGs
+    "mc2_lena": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                              n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2,
+                              cell_layout="hex", cell_isd_m=120.0, noise_model="thermal", a3_offset_db=float("inf"),
+                              channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0,
+                              fading_rho_per_ms=0.0, ul_retx_sched="tdma", ul_amc_alloc="previous"),
+                     E=3, R=16, steps=25, kind="pose", arena=260.0, walk=0.5, rates=(0.8,), resets={12: [1]}),
 }
 
 

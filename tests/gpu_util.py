@@ -92,6 +92,14 @@ def compare(ref, s, out, sd, E, R):
                 b = b + np.abs(np.asarray(r, dtype=np.float64)) * (np.log(10.0) / 10.0) * \
                     np.asarray(BOUND["out.sinr_db"], dtype=np.float64)[..., None]
             BOUND[k] = b
+        if k.endswith(".h_lexp") and "out.sinr_db" in BOUND:
+            # the IR log-sum log sum_tx sum_s exp(-lin_s / beta + log w_s) with poses: every lin_s carries the radio's
+            # rounding (relative ln(10) / 10 of the sinr_db bound), which moves each exponent by lin_s / beta times
+            # that; a log-sum-exp moves by the softmax-weighted mean of its exponents' moves, and the terms that carry
+            # the weight have lin_s / beta within |lse| + log w_s + log(terms) + 1 (the others' weights fall off
+            # exponentially faster than their lin_s / beta grows): at most (|h_lexp| + 8) times the relative rounding
+            BOUND[k] = (np.abs(np.asarray(r, dtype=np.float64)) + 8.0) * (np.log(10.0) / 10.0) * \
+                np.asarray(BOUND["out.sinr_db"], dtype=np.float64)[..., None]
         ok = close(m, r, FLOAT_TOL[k], ABS_FLOOR.get(k, 0.0), k) if k in FLOAT_TOL else (m == r)
         if not ok.all():
             (bad_f if k in FLOAT_TOL else bad_i)[k] = int((~ok).sum())

@@ -97,6 +97,15 @@ def test_strict_state_loading_refuses_what_this_engine_does_not_run():
     ok = {"net.ul.sent": torch.zeros(2), "gen": torch.zeros(3), "radio.ch.sf_los.gen": torch.zeros(3),
           "net.sizes": torch.zeros(2), "access": None, "_extras": False, "net.ul.slot_hook": None, "E": 4}
     assert E._strict_extra_keys(E, ok, {"net.ul.sent"}) == []
+    # the LENA grant counters' switch must equal the config's: on only with a 5G-LENA MAC switch set
+    lena = dict(ok, **{"net.ul._lena_mac": True})
+    assert E._strict_extra_keys(E, lena, {"net.ul.sent"}) == ["net.ul._lena_mac=True"]
+
+    class _Cfg(E):                                    # (the class attributes of the engine, a LENA config)
+        config = P.NRConfig(ul_retx_sched="tdma")
+    assert E._strict_extra_keys(_Cfg, lena, {"net.ul.sent"}) == []
+    assert E._strict_extra_keys(_Cfg, dict(ok, **{"net.ul._lena_mac": False}), {"net.ul.sent"}) == \
+        ["net.ul._lena_mac=False"]
     assert E._strict_extra_keys(E, dict(ok, **{"net.ul.tag": torch.zeros(2)}), {"net.ul.sent"}) == ["net.ul.tag"]
     bad = E._strict_extra_keys(E, dict(ok, access={"state": 1}, traffic="poisson"), {"net.ul.sent"})
     assert len(bad) == 2 and bad[0].startswith("access=")

@@ -1,6 +1,6 @@
 """Checkpoints on the GPU (core/checkpoint.py:103-143 semantics): a checkpoint written by the reference's NR engine
 (tests/golden/ckpt_*.npz, its state_dict() after 10 steps of a golden case: one cell, the downlink, three cells with
-handovers) loads into the hip engine, which then
+handovers, the 5G-LENA MAC switches with their grant counters and the last PUSCH's PRBs) loads into the hip engine, which then
 continues bit for bit along the reference's trajectory (outputs, state and counters as in the free-running parity
 test); and checkpoint.save / load of the hip engine resumes exactly like the uninterrupted run."""
 import json
@@ -28,7 +28,7 @@ def reference_checkpoint(name):
     return sd, int(z["k_steps"])
 
 
-@pytest.mark.parametrize("name", ["c2", "dl_c2", "mc3_ho"])
+@pytest.mark.parametrize("name", ["c2", "dl_c2", "mc3_ho", "lena_v2"])
 def test_reference_checkpoint_resumes_bit_exact(name):
     print(f"reference checkpoint of {name}", flush=True)
     ref, cfgd, kind = load(name)
@@ -59,7 +59,8 @@ def test_reference_checkpoint_resumes_bit_exact(name):
     want = json.loads(bytes(ref["counters_json"]))
     got = eng.counters()
     for lk in (("ul", "dl") if cfg.dl else ("ul",)):
-        for k in ("tb_new", "tb_ok", "tb_fail", "bytes_ok", "prb_used", "prb_avail"):
+        lena = tuple(k for k in ("tb_bytes", "tb_empty", "retx_block") if k in want[lk])   # (5G-LENA switches on)
+        for k in ("tb_new", "tb_ok", "tb_fail", "bytes_ok", "prb_used", "prb_avail") + lena:
             assert got[lk][k] == pytest.approx(want[lk][k], rel=1e-6), (lk, k)
         assert got[lk]["rv_tx"] == pytest.approx(want[lk]["rv_tx"])
 

@@ -38,6 +38,34 @@ def test_oracle_bitwise_vs_reference(name):
 
     replay.run(eng, d, kind, on_step=on_step)
     assert not bad, bad[:10]
+    # the counters of both links, the 5G-LENA grant accounting included (the reference sums them in float32)
+    import json
+    want_all = json.loads(bytes(d["counters_json"]))
+    for lk in eng.links():
+        for k, v in lk.ctr.items():
+            if k != "prb_avail":
+                assert float(v) == pytest.approx(want_all[lk.dir][k], rel=1e-6), (lk.dir, k)
+
+
+@pytest.mark.parametrize("name,field,wrong", [("tdma", "ul_retx_sched", "ofdma"),
+                                              ("amc_prev", "ul_amc_alloc", "current"),
+                                              ("mc2_lena", "ul_retx_sched", "ofdma")])
+def test_lena_switch_trajectories_pin_the_switch(name, field, wrong):
+    """The TDMA retransmission and previous-PUSCH AMC trajectories depend on their switch: the oracle run with the
+    switch at its default diverges from them (so the bitwise comparison above pins the switch's code)."""
+    import dataclasses
+    d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
+    cfg = dataclasses.replace(P.NRConfig(**cfgd, seed=0), **{field: wrong})
+    eng = O.OracleEngine(int(d["E"]), int(d["R"]), cfg, seed=0)
+    diff = []
+
+    def on_step(s, o, acc):
+        for k in ("ul.h_mcs", "ul.sent", "ul.h_state"):
+            if not np.array_equal(d[f"s{s:03d}/{k}"], eng.state()[k].numpy()):
+                diff.append((s, k))
+
+    replay.run(eng, d, kind, steps=12, on_step=on_step)
+    assert diff
 
 
 def test_oracle_catches_a_planted_error():
