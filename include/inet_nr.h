@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 8
+#define INET_NR_ABI_VERSION 9
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -150,6 +150,8 @@ typedef struct InetNrParams {
                                          the oldest NACK, and no new data in that slot (ABI version 8) */
     int32_t amc_prev;                 /* ul_amc_alloc="previous" (mac.py:393-401): the UL MCS for the PRBs of the last
                                          PUSCH (InetNrState.last_nprb), the TB for this allocation (ABI version 8) */
+    int32_t fc_on;                    /* frequency-correlated fading with a fixed delay spread (nr_engine.py:43-48,
+                                         320-368): every fading innovation and reset draw z becomes fc_L z (ABI 9) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -157,6 +159,7 @@ typedef struct InetNrParams {
     float proc_off_hi, proc_off_lo;   /* proc_offset_ms / control_step_ms as a double split in two floats */
     float wb_db;                      /* whole_band: 10 log10(nprb / snr_ref_prbs) */
     float pc_p0, pc_alpha;            /* pc1_on: P0 (dBm) and alpha of the fractional power control */
+    const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
 } InetNrParams;
 
 /* One scheduled slot of the control step (host-built per TDD key, device resident). */

@@ -67,3 +67,28 @@ def breakpoint_m(scn, fc_ghz, h_bs, h_ut):
     if scn in ("UMa", "UMi"):
         return 4 * (h_bs - 1.0) * (h_ut - 1.0) * fc / C_LIGHT
     return math.inf
+
+
+# ------------------------------------------------------------------ frequency-correlated fading
+def subband_fading_sqrt(cfg):
+    """The lower-triangular square root L [S,S] (float32, torch) of the subband correlation of the fading innovations
+    for the fixed rms delay spread cfg.fading_delay_spread_ns, or None (freq_corr_mode is not "fixed").
+
+    The subband centres are the cumulated RBG widths (PRBs x 12 x SCS) less half a width (nr_engine.py:125-129); the
+    correlation of subbands i, j is |1 / (1 + j 2 pi df tau)| = 1 / sqrt(1 + (2 pi df tau)^2) of an exponential
+    power-delay profile (nr_engine.py:132-156); L is its Cholesky factor with rows scaled to unit norm, a diagonal
+    jitter added while the factorization fails (nr_engine.py:159-168), in float64, rounded once to float32."""
+    import torch
+    if cfg.freq_corr_mode != "fixed":
+        return None
+    w = torch.tensor([float(x) for x in cfg.subband_prbs], dtype=torch.float64) * (12 * cfg.scs_khz * 1e3)
+    f = torch.cumsum(w, 0) - w / 2
+    x = 2 * math.pi * (f[:, None] - f[None, :]) * torch.as_tensor(cfg.fading_delay_spread_ns * 1e-9,
+                                                                   dtype=torch.float64)
+    c = 1.0 / torch.sqrt(1.0 + x * x)
+    eye = torch.eye(c.shape[-1], dtype=c.dtype)
+    for eps in (0.0, 1e-12, 1e-10, 1e-8, 1e-6):
+        L, info = torch.linalg.cholesky_ex(c + eps * eye)
+        if not bool((info != 0).any()):
+            return (L / L.norm(dim=-1, keepdim=True)).float().contiguous()
+    raise ValueError("subband correlation matrix is not positive definite")

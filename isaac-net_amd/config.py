@@ -66,7 +66,6 @@ REFERENCE_ONLY_DEFAULTS = {
     'rlc_tail_timer_ms': 10.0,
     'ue_speed_mps': None,
     'doppler_min_speed_mps': 0.0,
-    'fading_delay_spread_ns': None,
     'fading_ds_from_los': True,
     'fading_pdp': 'exponential',
     'fading_ds_grid': (3.0, 3000.0, 16),
@@ -200,6 +199,7 @@ class NRConfig:
     rician_k_from_los: bool = True
     rician_k_ramp_slots: int = 4
     fading_freq_corr: bool = False
+    fading_delay_spread_ns: float | None = None     # fading_freq_corr: one rms delay spread for every link (ns)
     dl_snr_offset_db: float = 10.0
     noise_model: str = "fixed"
     ni_fixed_dbm: float = -90.0
@@ -369,6 +369,14 @@ class NRConfig:
     @property
     def ul_rtt(self):
         return self.ul_harq_rtt_slots if self.ul_harq_rtt_slots is not None else self.gnb_proc_slots + self.k2
+
+    @property
+    def freq_corr_mode(self):
+        """Delay-spread source of the frequency-correlated fading (config.py:948-953): None (fading or
+        fading_freq_corr off), "fixed" (fading_delay_spread_ns for every link) or "los" (a per-link draw by LOS state)."""
+        if not (self.fading and self.fading_freq_corr):
+            return None
+        return "fixed" if self.fading_delay_spread_ns is not None else "los"
 
     def lena_mac_switches(self):
         """The 5G-LENA MAC switches set away from their defaults, {field: value} (config.py:1092-1094): any of them

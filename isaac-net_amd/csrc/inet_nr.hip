@@ -198,6 +198,24 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             st.h_re[is] = div_const(normal_at(bh, j), SQRT2_F, INV_SQRT2_F);
             st.h_im[is] = div_const(normal_at(bh, j + 1u), SQRT2_F, INV_SQRT2_F);
         }
+        if (pm.fc_on) {
+            // frequency-correlated fading: the initial state correlated across the subbands too, h0 <- L h0 per link
+            // (nr_engine.py:264-266), the products accumulated with fused multiply-adds in subband order; rows from
+            // the last down, so each reads the uncorrelated values of the rows above it
+            for (int c = 0; c < NC; ++c) {
+                const size_t i0 = ((size_t)e * CS + c * S) * R + r;
+                for (int i = S - 1; i >= 0; --i) {
+                    float ar = 0.f, ai = 0.f;
+                    for (int jj = 0; jj <= i; ++jj) {
+                        const float l = pm.fc_L[i * S + jj];
+                        ar = fmaf(l, st.h_re[i0 + (size_t)jj * R], ar);
+                        ai = fmaf(l, st.h_im[i0 + (size_t)jj * R], ai);
+                    }
+                    st.h_re[i0 + (size_t)i * R] = ar;
+                    st.h_im[i0 + (size_t)i * R] = ai;
+                }
+            }
+        }
         if (pm.rician) {                                   // phi = 2 pi u (KPHI), nr_engine.py:293-299
             const uint32_t bk = base_key(s0, env, ep, CH_RESET, 0u, SITE_KPHI << 16);
             float phi = (float)6.283185307179586 * uniform_bits(elem_hash(bk, (uint32_t)r));
@@ -251,6 +269,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
+    if (p.fc_on && !p.fc_L) return INET_NR_EINVAL;
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);
@@ -395,7 +414,7 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
     if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
-    if (T < 0 || T > 0x7fffffff) return INET_NR_EINVAL;
+    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L)) return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,
                        dcorr[0], dcorr[1], dcorr[2], spectrum, mask ? 0 : 1);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;

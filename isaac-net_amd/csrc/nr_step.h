@@ -326,6 +326,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
         pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
+        pm.fc_on = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -345,6 +346,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     __shared__ __align__(16) float s_se[MAX_M];
     __shared__ float s_beta[MAX_M], s_rbeta[MAX_M], s_rate[MAX_M];
     __shared__ float s_w[S], s_logw[S], s_wdb[S], s_lnw[S + 1];
+    // frequency-correlated fading: the subband correlation's square root (general build only)
+    __shared__ float s_fcl[FX == 0 ? S * S : 1];
+    const bool fc = FX == 0 && pm.fc_on != 0;
     __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
     __shared__ int s_ulrel[MAX_UL_ROWS];
     // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
@@ -513,6 +517,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // log of the held PRB count by count of held RBGs, when every RBG has the same width: the log-sum-exp over the
     // held RBGs then adds exp(0) = 1 once per RBG, so it depends only on that count (s_lnw[n])
     if (lane <= S) s_lnw[lane] = lse_logw<S>(s_logw, lane >= 32 ? ~0u : ((1u << lane) - 1u));
+    if (fc)
+        for (int i = lane; i < S * S; i += blockDim.x) s_fcl[i] = pm.fc_L[i];
     bool lw_eq = true;
 #pragma unroll
     for (int s = 1; s < S; ++s) lw_eq = lw_eq && s_logw[s] == s_logw[0];
@@ -812,12 +818,33 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 const float zr = normal_of(mix32(mix32(hin) ^ bfc), mix32(mix32(hin + GOLD) ^ bfc));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bfc), mix32(mix32(hin + 3u * GOLD) ^ bfc));
                 // the innovation term sqrt(1 - rho^2) z / sqrt(2) of the AR(1) step, ready for the robot's update
-                s_z[(2 * qc) * CW + Lc] = div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
-                s_z[(2 * qc + 1) * CW + Lc] = div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+                // (frequency-correlated fading: z itself, correlated by the robot first)
+                s_z[(2 * qc) * CW + Lc] = fc ? zr : div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                s_z[(2 * qc + 1) * CW + Lc] = fc ? zi : div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
             }
             INET_PH(1);                            // fading innovations (the robots' own updates follow)
             __syncthreads();
-            if (draw) {
+            if (draw && fc) {
+                // z <- L z over the subbands of every link (L lower-triangular; the products accumulated with fused
+                // multiply-adds in subband order, as a float32 matrix product), then the AR(1) step
+                // (the draws are read from LDS term by term: no register copy of the S draws of a link)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+#pragma unroll
+                    for (int i = 0; i < S; ++i) {
+                        float ar = 0.f, ai = 0.f;
+#pragma unroll 1
+                        for (int j = 0; j <= i; ++j) {
+                            const float l = s_fcl[i * S + j];
+                            ar = fmaf(l, s_z[(2 * (c * S + j)) * CW + lane], ar);
+                            ai = fmaf(l, s_z[(2 * (c * S + j) + 1) * CW + lane], ai);
+                        }
+                        const int q = c * S + i;
+                        hr[q] = row.rho * hr[q] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
+                        hi[q] = row.rho * hi[q] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
+                    }
+                }
+            } else if (draw) {
 #pragma unroll
                 for (int q = 0; q < NCS; ++q) {
                     hr[q] = row.rho * hr[q] + s_z[(2 * q) * CW + lane];
@@ -1905,7 +1932,7 @@ void launch_step(const StepArgs& a) {
 // the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
-                        p.retx_tdma == 0 && p.amc_prev == 0 &&
+                        p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

@@ -21,6 +21,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .channels import subband_fading_sqrt
 from .config import NRConfig
 from .phy import PhyTables, cqi_tables
 
@@ -96,8 +97,9 @@ def refusals(cfg: NRConfig):
        "the per-RBG PF update of the pf scheduler")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
     no(cfg.rician_mode == "los", "Rician K from the LOS state", "fixed rician_k_db or Rayleigh")
-    no(cfg.fading_freq_corr or cfg.fading_doppler != "global", "frequency-correlated / per-robot Doppler fading",
-       "i.i.d. subbands, one rho")
+    no(cfg.freq_corr_mode == "los", "frequency-correlated fading with per-link delay spreads from the LOS state "
+       "(fading_delay_spread_ns=None)", "one fixed delay spread (fading_delay_spread_ns)")
+    no(cfg.fading_doppler != "global", "per-robot Doppler fading", "one rho")
     no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
     no(cfg.rach or cfg.drx, "RACH / DRX access", "always connected")
     no(cfg.tbs_mode != "38214" or cfg.bler_source != "pdsch", "tbs_mode / bler_source", "38.214 TBS, Sionna PDSCH")
@@ -336,6 +338,11 @@ class HipNREngine:
         p.wb_db = 10 * math.log10(cfg.nprb / cfg.snr_ref_prbs)
         p.pc1_on = int(cfg.ul_pc_on and cfg.n_cells == 1)
         p.retx_tdma, p.amc_prev = int(cfg.ul_retx_sched == "tdma"), int(cfg.ul_amc_alloc == "previous")
+        # frequency-correlated fading: the square root of the subband correlation (nr_engine.py:320-330)
+        L = subband_fading_sqrt(cfg)
+        self._fc_L = None if L is None else L.to(self.dev)
+        p.fc_on = int(L is not None)
+        p.fc_L = self._fc_L.data_ptr() if L is not None else None
         p.pc_p0, p.pc_alpha = cfg.ul_pc_p0_dbm, cfg.ul_pc_alpha
         p.target, p.phr_min, p.snr_ref_prbs = cfg.bler_target, cfg.phr_min_db, float(cfg.snr_ref_prbs)
         p.w0 = float(cfg.subband_prbs[0])
@@ -1187,7 +1194,8 @@ class HipNREngine:
                 "net._gain_c", "net._ni_la_ul", "net._pg", "net.ul.member", "net.ul.pc_backoff", "net.ul.phr_snr",
                 "net.ul.sched_ok", "net.ioN[dl]", "net.ni_dl", "net.ul.sb_prb", "net.dl.sb_prb", "net.ul.q.f_nact",
                 "net.ul.q.f_snr", "net.ul.q.f_own", "net.dl.q.f_nact", "net.dl.q.f_snr", "net.dl.q.f_own",
-                "net.dl.q.det", "net.dl.q.hid", "net.dl_newest"}
+                "net.dl.q.det", "net.dl.q.hid", "net.dl_newest",
+                "net.fc_L"}       # (the subband correlation's square root, derived from the config)
     # Reference host values that switch on what this engine does not run (traffic models, access procedures, hooks
     # and traces, frequency-correlated or per-robot fading, blockage, O2I, radio link failure, TPC, BSR grants,
     # MIMO, QoS): a checkpoint holding another value was written with that feature on. (_lena_mac, the LENA grant
@@ -1203,9 +1211,11 @@ class HipNREngine:
 
     def _ck_expected(self, k):
         """The value host switch k must hold in a checkpoint this engine loads."""
+        cfg = getattr(self, "config", None)
         if k.endswith("._lena_mac"):
-            cfg = getattr(self, "config", None)
             return bool(cfg.lena_mac_switches()) if cfg is not None else False
+        if k == "net.fc_mode":
+            return cfg.freq_corr_mode if cfg is not None else None
         return self._CK_OFF[k]
 
     def _strict_extra_keys(self, sd, used):

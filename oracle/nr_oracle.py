@@ -426,6 +426,24 @@ class Radio:
 
 
 # ------------------------------------------------------------------------------------------ the engine
+def fcorr_sqrt(cfg):
+    """L [S,S] float32 with L L^T the subband correlation of the fading innovations for the fixed delay spread
+    (nr_engine.py:125-168, _init_fcorr 320-330): subband centres (cumulated RBG widths less half a width), the
+    correlation 1 / sqrt(1 + (2 pi df tau)^2), its Cholesky factor (diagonal jitter while it fails) with unit-norm
+    rows, in float64, then float32."""
+    w = torch.tensor([float(x) for x in cfg.subband_prbs], dtype=torch.float64) * (12 * cfg.scs_khz * 1e3)
+    f = torch.cumsum(w, 0) - w / 2
+    df = f[:, None] - f[None, :]
+    x = 2 * math.pi * df * torch.as_tensor(cfg.fading_delay_spread_ns * 1e-9, dtype=torch.float64)[..., None, None]
+    c = 1.0 / torch.sqrt(1.0 + x * x)
+    eye = torch.eye(c.shape[-1], dtype=c.dtype)
+    for eps in (0.0, 1e-12, 1e-10, 1e-8, 1e-6):
+        L, info = torch.linalg.cholesky_ex(c + eps * eye)
+        if not bool((info != 0).any()):
+            return (L / L.norm(dim=-1, keepdim=True)).float().contiguous()
+    raise ValueError("subband correlation matrix is not positive definite")
+
+
 class Link:
     """MacLink state (mac.py:67-81) and FrameQueue (queues.py:49-61) of one direction, with the queue helpers.
     The UL queue carries the meta fields cls / det / hid of NRNet (nr_engine.py:191-193); the DL queue cls only
@@ -634,7 +652,8 @@ class OracleEngine:
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
         assert not cfg.ul_tpc
-        assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global" and not cfg.fading_freq_corr
+        assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global"
+        assert cfg.freq_corr_mode in (None, "fixed"), "frequency-correlated fading: a fixed delay spread"
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
         mt = max(cfg.max_harq_tx, 2)
@@ -642,6 +661,7 @@ class OracleEngine:
         self.phy = Phy(self.tabs)
         self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
         self.w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
+        self.fc_L = fcorr_sqrt(cfg) if cfg.freq_corr_mode == "fixed" else None
         self.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
         self.rng = CounterRNG(seed, E)
         self.dec = Decisions()
@@ -696,6 +716,8 @@ class OracleEngine:
         self.rng.reset_mask(mask)
         cd = self.cdim
         h0 = self.rng.reset_normal(H0 << 16, R * math.prod(cd) * S * 2).view(E, R, *cd, S, 2) / math.sqrt(2)
+        if self.fc_L is not None:                        # stationary start, correlated too (nr_engine.py:264-266)
+            h0 = self.fc_L @ h0
         if mask is None:
             self.h = h0
             self.last_g = None
@@ -969,6 +991,8 @@ class OracleEngine:
         dt = 1 if self.last_g is None else g - self.last_g
         if dt > 0:
             z = self.rng.step_normal(FADING, rel, self.h[0].numel()).view(self.h.shape)
+            if self.fc_L is not None:                    # z <- L z across the subbands (nr_engine.py:366-368, 581-582)
+                z = self.fc_L @ z
             rho = self.cfg.fading_rho_per_ms ** (dt * self.cfg.slot_ms)
             self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
         self.last_g = g

@@ -218,6 +218,34 @@ CASES = {
                               channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0,
                               fading_rho_per_ms=0.0, ul_retx_sched="tdma", ul_amc_alloc="previous"),
                      E=3, R=16, steps=25, kind="pose", arena=260.0, walk=0.5, rates=(0.8,), resets={12: [1]}),
+    # frequency-correlated fading (nr_engine.py:43-48, 320-368): the innovations and the initial state correlated
+    # across the 13 RBGs by a fixed 300 ns delay spread; PF, poses, correlated fading in time
+    "fcorr": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                           max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_freq_corr=True,
+                           fading_delay_spread_ns=300.0, fading_rho_per_ms=0.5, channel="tr38901",
+                           tr38901_scenario="UMi", tr38901_los="los", cell_positions_m=((100.0, 100.0),),
+                           gnb_height_m=10.0),
+                  E=3, R=16, steps=30, kind="pose", arena=240.0, walk=1.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # the same on both links (SNR input, i.i.d. in time, 60 ns: strongly correlated subbands), HARQ-IR
+    "fcorr_dl": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                              harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2500.0,), fading_freq_corr=True,
+                              fading_delay_spread_ns=60.0, fading_rho_per_ms=0.0, dl=True),
+                     E=3, R=8, steps=25, kind="snr", snr=(-2.0, 16.0), rates=(0.9,), dl_sizes=(6000.0,),
+                     dl_rates=(0.8,), resets={11: [1]}),
+    # two cells, every robot-cell link correlated across 14 RBGs (1 us delay spread)
+    "fcorr_mc2": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                               max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2, cell_layout="hex",
+                               cell_isd_m=120.0, noise_model="thermal", a3_offset_db=float("inf"), channel="tr38901",
+                               tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0, fading_rho_per_ms=0.5,
+                               fading_freq_corr=True, fading_delay_spread_ns=1000.0),
+                      E=3, R=16, steps=25, kind="pose", arena=220.0, walk=0.5, rates=(0.7,), resets={12: [1]}),
+    # envs of 100 robots on two wavefronts, 273 PRB in 8 RBGs of 35, 100 ns
+    "fcorr_w2": dict(cfg=dict(mu=1, n_prb=273, rbg_size=35, tdd_pattern="DDDSU", control_step_ms=10.0,
+                              scheduler="pf", n_harq=8, max_harq_tx=4, frame_buffer=8, msg_sizes=(800.0,),
+                              fading_freq_corr=True, fading_delay_spread_ns=100.0, fading_rho_per_ms=0.0,
+                              channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                              cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                     E=2, R=100, steps=12, kind="pose", arena=200.0, walk=1.0, rates=(0.3,), resets={7: [0]}),
 }
 
 

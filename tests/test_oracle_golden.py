@@ -49,10 +49,13 @@ def test_oracle_bitwise_vs_reference(name):
 
 @pytest.mark.parametrize("name,field,wrong", [("tdma", "ul_retx_sched", "ofdma"),
                                               ("amc_prev", "ul_amc_alloc", "current"),
-                                              ("mc2_lena", "ul_retx_sched", "ofdma")])
-def test_lena_switch_trajectories_pin_the_switch(name, field, wrong):
-    """The TDMA retransmission and previous-PUSCH AMC trajectories depend on their switch: the oracle run with the
-    switch at its default diverges from them (so the bitwise comparison above pins the switch's code)."""
+                                              ("mc2_lena", "ul_retx_sched", "ofdma"),
+                                              ("fcorr", "fading_delay_spread_ns", 3000.0),
+                                              ("fcorr_mc2", "fading_delay_spread_ns", 300.0)])
+def test_switch_trajectories_pin_the_switch(name, field, wrong):
+    """The TDMA retransmission, previous-PUSCH AMC and frequency-correlated fading trajectories depend on their
+    switch: the oracle run with the switch at another value diverges from them (so the bitwise comparison above pins
+    the switch's code)."""
     import dataclasses
     d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
     cfg = dataclasses.replace(P.NRConfig(**cfgd, seed=0), **{field: wrong})
@@ -60,7 +63,7 @@ def test_lena_switch_trajectories_pin_the_switch(name, field, wrong):
     diff = []
 
     def on_step(s, o, acc):
-        for k in ("ul.h_mcs", "ul.sent", "ul.h_state"):
+        for k in ("ul.h_mcs", "ul.sent", "ul.h_state", "net.h"):
             if not np.array_equal(d[f"s{s:03d}/{k}"], eng.state()[k].numpy()):
                 diff.append((s, k))
 
@@ -108,3 +111,26 @@ def test_oracle_catches_planted_multicell_errors(plant):
 
     replay.run(eng, d, kind, on_step=on_step)
     assert diff
+
+
+def test_subband_correlation_factor_matches_the_restatement():
+    """The engine's square root of the subband correlation (channels.subband_fading_sqrt, uploaded to the kernels) is
+    the oracle's (fcorr_sqrt) for every carrier of the fixtures and a range of delay spreads, and it is one: L L^T
+    has the correlation 1 / sqrt(1 + (2 pi df tau)^2) (within float32 rounding), L is lower-triangular with unit rows."""
+    import math
+    from isaac_net_amd.channels import subband_fading_sqrt
+    for n_prb, rbg, mu in ((52, None, 1), (106, None, 1), (273, 35, 1), (273, None, 1), (25, None, 0)):
+        for tau in (10.0, 60.0, 300.0, 3000.0):
+            kw = dict(n_prb=n_prb, mu=mu, fading_freq_corr=True, fading_delay_spread_ns=tau)
+            if rbg:
+                kw["rbg_size"] = rbg
+            cfg = P.NRConfig(**kw)
+            L = subband_fading_sqrt(cfg)
+            assert torch.equal(L, O.fcorr_sqrt(cfg))
+            S = cfg.n_subbands
+            w = torch.tensor([float(x) for x in cfg.subband_prbs], dtype=torch.float64) * 12 * cfg.scs_khz * 1e3
+            f = torch.cumsum(w, 0) - w / 2
+            c = 1.0 / torch.sqrt(1.0 + (2 * math.pi * (f[:, None] - f[None, :]) * tau * 1e-9) ** 2)
+            Ld = L.double()
+            assert torch.allclose(Ld @ Ld.T, c, atol=1e-5) or tau < 60.0      # (jittered near-singular cases)
+            assert torch.equal(torch.tril(L), L) and torch.allclose(Ld.norm(dim=-1), torch.ones(S, dtype=torch.float64), atol=1e-6)
