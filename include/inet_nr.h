@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 9
+#define INET_NR_ABI_VERSION 10
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -103,6 +103,10 @@ typedef struct InetNrState {
     /* per robot [E][R] float: PRBs of the robot's last PUSCH (UlMac.last_nprb, mac_ul.py:51, mac.py:484), read and
        written only with params.amc_prev (ABI version 8) */
     float *last_nprb;
+    /* per robot [E][R] float: the LOS K draw of Rician fading with K from the LOS state (NRNet.k_los,
+       nr_engine.py:300-303), written by inet_nr_reset with params.k_from_los (ABI version 10); the K the step uses
+       is k_lin, which the caller sets to k_los once the link is reported LOS (NRNet.set_los) */
+    float *k_los;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -152,6 +156,8 @@ typedef struct InetNrParams {
                                          PUSCH (InetNrState.last_nprb), the TB for this allocation (ABI version 8) */
     int32_t fc_on;                    /* frequency-correlated fading with a fixed delay spread (nr_engine.py:43-48,
                                          320-368): every fading innovation and reset draw z becomes fc_L z (ABI 9) */
+    int32_t k_from_los;               /* Rician K from the LOS state: inet_nr_reset draws k_los = 10^((k_mu + k_sigma z)
+                                         / 10), z the link's KFAC normal, and sets k_lin = 0 (ABI 10) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -159,6 +165,7 @@ typedef struct InetNrParams {
     float proc_off_hi, proc_off_lo;   /* proc_offset_ms / control_step_ms as a double split in two floats */
     float wb_db;                      /* whole_band: 10 log10(nprb / snr_ref_prbs) */
     float pc_p0, pc_alpha;            /* pc1_on: P0 (dBm) and alpha of the fractional power control */
+    float k_mu, k_sigma;              /* k_from_los: (mu_K, sigma_K) dB of the scenario, TR 38.901 Table 7.5-6 */
     const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
 } InetNrParams;
 

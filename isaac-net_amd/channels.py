@@ -92,3 +92,9 @@ def subband_fading_sqrt(cfg):
         if not bool((info != 0).any()):
             return (L / L.norm(dim=-1, keepdim=True)).float().contiguous()
     raise ValueError("subband correlation matrix is not positive definite")
+
+
+# Rician K-factor of LOS links, (mu_K, sigma_K) in dB per scenario: TR 38.901 V17.0.0 Table 7.5-6 (UMi-Street Canyon
+# 9 / 5, UMa 9 / 3.5, RMa 7 / 4, Indoor-Office 7 / 4, InF 7 / 8; K is defined for LOS links only)
+RICIAN_K_DB = {"UMi": (9.0, 5.0), "UMa": (9.0, 3.5), "RMa": (7.0, 4.0), "InH": (7.0, 4.0),
+               "InF-SL": (7.0, 8.0), "InF-DL": (7.0, 8.0), "InF-SH": (7.0, 8.0), "InF-DH": (7.0, 8.0)}

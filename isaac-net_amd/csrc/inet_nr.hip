@@ -17,7 +17,7 @@ using namespace inet;
 namespace {
 
 constexpr uint32_t CH_RESET = 3;
-constexpr uint32_t SITE_H0 = 4, SITE_KPHI = 6;
+constexpr uint32_t SITE_H0 = 4, SITE_KFAC = 5, SITE_KPHI = 6;
 
 }  // namespace
 
@@ -222,6 +222,14 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             st.spec_re[ir] = cosf(phi);
             st.spec_im[ir] = sinf(phi);
             st.k_lin[ir] = k_lin0;
+            if (pm.k_from_los) {
+                // K from the LOS state (nr_engine.py:300-303): k_los = 10^((mu_K + sigma_K z) / 10), z the link's
+                // KFAC normal (element r); K = 0 until the link is reported LOS. 10^x in double, rounded once.
+                const uint32_t bz = base_key(s0, env, ep, CH_RESET, 0u, SITE_KFAC << 16);
+                const float x = (pm.k_mu + pm.k_sigma * normal_at(bz, (uint32_t)r)) / 10.0f;
+                st.k_los[ir] = (float)exp10((double)x);
+                st.k_lin[ir] = 0.0f;
+            }
         }
     }
     // env-level: radio fields (draw_plane_waves) of the new episode, one per cell: wave kk of cell c is element
@@ -414,7 +422,8 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
     if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
-    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L)) return INET_NR_EINVAL;
+    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L) || (p.k_from_los && (!st->k_los || !p.rician)))
+        return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,
                        dcorr[0], dcorr[1], dcorr[2], spectrum, mask ? 0 : 1);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;

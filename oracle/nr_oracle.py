@@ -45,6 +45,9 @@ GOLD = 0x9E3779B9
 INV24 = 1.0 / 16777216.0
 SUBMIT, STEP, RESET = 1, 2, 3
 FADING, BLER_UL, BLER_DL, H0, KFAC, KPHI, DSPR = 1, 2, 3, 4, 5, 6, 7
+# Rician K of LOS links, (mu_K, sigma_K) dB per TR 38.901 scenario (Table 7.5-6, nr_engine.py:67-72)
+RICIAN_K_DB = {"UMi": (9.0, 5.0), "UMa": (9.0, 3.5), "RMa": (7.0, 4.0), "InH": (7.0, 4.0),
+               "InF-SL": (7.0, 8.0), "InF-DL": (7.0, 8.0), "InF-SH": (7.0, 8.0), "InF-DH": (7.0, 8.0)}
 LOG_DISTANCE_STREAM = 10
 RADIO_STREAM = 0x52 << 16
 TR38901_STREAM = RADIO_STREAM + 16
@@ -652,7 +655,9 @@ class OracleEngine:
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
         assert not cfg.ul_tpc
-        assert cfg.rician_mode in (None, "fixed") and cfg.fading_doppler == "global"
+        assert cfg.fading_doppler == "global"
+        assert cfg.rician_mode in (None, "fixed") or (cfg.rician_mode == "los" and C == 1), \
+            "Rician K: fixed, or from the LOS state at one cell"
         assert cfg.freq_corr_mode in (None, "fixed"), "frequency-correlated fading: a fixed delay spread"
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
@@ -666,6 +671,10 @@ class OracleEngine:
         self.rng = CounterRNG(seed, E)
         self.dec = Decisions()
         self.rician = cfg.rician_mode
+        self.k_ramp = cfg.rician_k_ramp_slots if self.rician == "los" else 0
+        if self.rician == "los":
+            from isaac_net_amd.channels import scenario_name
+            self.scn = scenario_name(cfg.tr38901_scenario)
         self.radio = None
         self.T = 0
         self.epoch = torch.zeros(E, dtype=torch.long)
@@ -727,19 +736,28 @@ class OracleEngine:
             n = R * math.prod(cd)
             u = self.rng.reset_uniform(KPHI << 16, n)
             self.rng.reset_normal(KFAC << 16, n)
+            z = self.rng.reset_normal(KFAC << 16, n)
             phi = (2 * math.pi) * u.view(E, R, *cd)
             spec = torch.stack((torch.cos(phi), torch.sin(phi)), -1)
-            k_los = torch.full((E, R, *cd), 10 ** (self.cfg.rician_k_db / 10))
+            if self.rician == "fixed":
+                k_los = torch.full((E, R, *cd), 10 ** (self.cfg.rician_k_db / 10))
+                k0 = k_los
+            else:                    # a log-normal K per link; K = 0 until the LOS state arrives (nr_engine.py:300-303)
+                mu, sigma = RICIAN_K_DB[self.scn]
+                k_los = 10 ** ((mu + sigma * z.view(E, R, *cd)) / 10)
+                k0 = torch.zeros_like(k_los)
             if mask is None:
                 self.spec, self.k_los = spec, k_los
-                self.k_in, self.k_lin, self.k_from = k_los.clone(), k_los.clone(), k_los.clone()
+                self.k_in, self.k_lin, self.k_from = k0.clone(), k0.clone(), k0.clone()
                 self.k_g0 = torch.zeros((E, R, *cd), dtype=torch.long)
+                self.k_fresh = torch.ones(E, dtype=torch.bool)
             else:
                 self.spec = where_env(m, spec, self.spec)
                 self.k_los = where_env(m, k_los, self.k_los)
                 for n in ("k_in", "k_lin", "k_from"):
-                    setattr(self, n, where_env(m, k_los, getattr(self, n)))
+                    setattr(self, n, where_env(m, k0, getattr(self, n)))
                 self.k_g0 = where_env(m, 0, self.k_g0)
+                self.k_fresh = self.k_fresh | m
         if self.C > 1:                                   # NRNet._reset_cells (nr_engine.py:424-438)
             self.assoc.reset(m)
             if mask is None:
@@ -844,6 +862,8 @@ class OracleEngine:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
+            if self.rician == "los" and cfg.channel == "tr38901":
+                self._set_los(torch.full((self.E, self.R), cfg.tr38901_los == "los"))
             pgs = pg[..., None].expand(-1, -1, self.S)
             n_ul = torch.full_like(pgs, cfg.noise_dbm_per_prb("gnb"))
             ul_ref = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs) + pgs - n_ul
@@ -886,11 +906,11 @@ class OracleEngine:
         if self.pc_on:           # one cell with UL power control: path loss from the input SNR (nr_engine.py:649-650)
             self.pc_backoff = self._pc_backoff(ul_ref.mean(-1) + cfg.subband_noise_dbm)
         if self.rician:
-            self.k_lin = self.k_in                       # _rician_update with no ramp (nr_engine.py:410-415)
+            self._rician_update(g0)
         for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
             g = g0 + rel
             self._evolve(g, rel)
-            gain = self._gain()
+            gain = self._gain(g)
             if cqi:
                 self._cqi_report(dl_ref, gain)
             if dls:
@@ -997,13 +1017,41 @@ class OracleEngine:
             self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
         self.last_g = g
 
-    def _gain(self):
+    def _set_los(self, los):
+        """NRNet.set_los (nr_engine.py:370-392) for the K factor: the target is the link's LOS draw where LOS, else 0;
+        right after a reset it applies at once."""
+        k = torch.where(los, self.k_los, torch.zeros_like(self.k_los))
+        fr = self.k_fresh[:, None]
+        self.k_in = k
+        self.k_lin = torch.where(fr, k, self.k_lin)
+        self.k_from = torch.where(fr, k, self.k_from)
+        self.k_fresh = torch.zeros_like(self.k_fresh)
+
+    def _k_at(self, gv):
+        """K of every link in slot gv (nr_engine.py:402-408): the target, or on the ramp from k_from."""
+        if self.k_ramp == 0 or gv is None:
+            return self.k_lin
+        n = gv - self.k_g0 + 1
+        return torch.where(n >= self.k_ramp, self.k_lin,
+                           self.k_from + (self.k_lin - self.k_from) * (n * (1.0 / self.k_ramp)))
+
+    def _rician_update(self, g0):
+        """Start of a control step (nr_engine.py:410-419): links whose input K changed start a ramp."""
+        if self.k_ramp == 0:
+            self.k_lin = self.k_in
+            return
+        ch = self.k_in != self.k_lin
+        self.k_from = torch.where(ch, self._k_at(g0 - 1), self.k_from)
+        self.k_g0 = torch.where(ch, torch.full_like(self.k_g0, g0), self.k_g0)
+        self.k_lin = self.k_in
+
+    def _gain(self, gv=None):
         """Fading gain dB [E,R,S] (nr_engine.py:602-611)."""
         if not self.cfg.fading:
             return torch.zeros(self.h.shape[:-1])
         if not self.rician:
             return 10 * torch.log10((self.h ** 2).sum(-1).clamp(min=1e-6))
-        k = self.k_lin[..., None, None]
+        k = self._k_at(gv)[..., None, None]
         inv = 1 / (k + 1)
         x = torch.sqrt(k * inv) * self.spec[..., None, :] + torch.sqrt(inv) * self.h
         return 10 * torch.log10((x ** 2).sum(-1).clamp(min=1e-6))
@@ -1372,6 +1420,8 @@ class OracleEngine:
             items.append(("net.dl_newest", self, "dl_newest"))
         if self.rician:
             items += [(k, self, v) for k, v in self.RICIAN_MAP.items()]
+            if self.rician == "los":
+                items.append(("net.k_fresh", self, "k_fresh"))
         if self.C > 1:
             items += [(k, self, v) for k, v in self.CELL_KEYS.items()]
             items += [("assoc." + n, self.assoc, n) for n in (*Association.INIT, "pending")]

@@ -246,6 +246,24 @@ CASES = {
                               channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
                               cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
                      E=2, R=100, steps=12, kind="pose", arena=200.0, walk=1.0, rates=(0.3,), resets={7: [0]}),
+    # Rician fading with K from the LOS state (rician_k_db None: a log-normal K per link, TR 38.901 Table 7.5-6, that
+    # applies once the radio reports the link LOS, nr_engine.py:282-419): UMi LOS, PF, correlated fading, a reset
+    "rice_los": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                              max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_rician=True,
+                              fading_rho_per_ms=0.5, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                              cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                     E=3, R=16, steps=30, kind="pose", arena=240.0, walk=1.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # the same with the downlink, UMa
+    "rice_los_dl": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                 n_harq=8, max_harq_tx=4, frame_buffer=8, msg_sizes=(2000.0,), fading_rician=True,
+                                 fading_rho_per_ms=0.0, channel="tr38901", tr38901_scenario="UMa", tr38901_los="los",
+                                 cell_positions_m=((100.0, 100.0),), gnb_height_m=25.0, dl=True),
+                        E=3, R=8, steps=25, kind="pose", arena=260.0, walk=1.0, rates=(0.8,), dl_sizes=(4000.0,),
+                        dl_rates=(0.6,), resets={11: [2]}),
+    # SNR input: the radio reports no LOS state, so K stays 0 (Rayleigh) however long the run
+    "rice_snr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                              frame_buffer=8, msg_sizes=(2500.0,), fading_rician=True, fading_rho_per_ms=0.5),
+                     E=3, R=8, steps=20, kind="snr", snr=(-2.0, 16.0), rates=(0.9,), resets={9: [0]}),
 }
 
 

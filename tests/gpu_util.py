@@ -12,8 +12,11 @@ from oracle import replay
 # log-sum) 1e-5 relative, h_comb with the derived bound comb_bound below plus, with poses, the radio's rounding of the
 # reference SINR; the OLLA offset and PF average are pure arithmetic on the decisions and must be bitwise equal.
 FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1e-5, "ul.h_comb": 1e-5,
-             "ul.h_lexp": 1e-5, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0, "net.k_los": 0.0,
-             "net.k_in": 0.0, "net.k_lin": 0.0, "net.k_from": 0.0,
+             "ul.h_lexp": 1e-5, "ul.h_nrb": 0.0, "ul.olla": 0.0, "ul.avg": 0.0, "ul.q.fin": 0.0,
+             # the K factor: exact with a fixed K; from the LOS state 10^((mu + sigma z) / 10) of a Box-Muller normal z
+             # (the device's and the CPU's normals are within an ulp or two, as for the fading state h, and the CPU's
+             # float32 power is within an ulp of the device's correctly rounded one): 1e-5 relative, as net.h
+             "net.k_los": 1e-5, "net.k_in": 1e-5, "net.k_lin": 1e-5, "net.k_from": 1e-5,
              # the DL link: its CSI is an MCS threshold minus the reference SINR (exact once the reported MCS agrees)
              "dl.csi": 1e-5, "dl.h_comb": 1e-5, "dl.h_lexp": 1e-5, "dl.h_nrb": 0.0, "dl.olla": 0.0, "dl.avg": 0.0,
              "dl.q.fin": 0.0,
