@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 10
+#define INET_NR_ABI_VERSION 11
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -158,6 +158,10 @@ typedef struct InetNrParams {
                                          320-368): every fading innovation and reset draw z becomes fc_L z (ABI 9) */
     int32_t k_from_los;               /* Rician K from the LOS state: inet_nr_reset draws k_los = 10^((k_mu + k_sigma z)
                                          / 10), z the link's KFAC normal, and sets k_lin = 0 (ABI 10) */
+    int32_t los_sto;                  /* TR 38.901 stochastic LOS state (models.py:121-167): LOS where u(x) < Pr_LOS(d_2D),
+                                         u the LOS-state field (field 2) through los_cdf; NLOS path loss and sig_nlos
+                                         elsewhere (ABI 11) */
+    int32_t plos_scn;                 /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -166,7 +170,9 @@ typedef struct InetNrParams {
     float wb_db;                      /* whole_band: 10 log10(nprb / snr_ref_prbs) */
     float pc_p0, pc_alpha;            /* pc1_on: P0 (dBm) and alpha of the fractional power control */
     float k_mu, k_sigma;              /* k_from_los: (mu_K, sigma_K) dB of the scenario, TR 38.901 Table 7.5-6 */
+    float sig_nlos;                   /* los_sto: NLOS shadow-fading sigma (dB); sig is the LOS one */
     const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
+    const float *los_cdf;             /* los_sto: [65536] sorted samples of a unit sum of cosines (fields.py:94-106) */
 } InetNrParams;
 
 /* One scheduled slot of the control step (host-built per TDD key, device resident). */

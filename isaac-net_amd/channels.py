@@ -98,3 +98,13 @@ def subband_fading_sqrt(cfg):
 # 9 / 5, UMa 9 / 3.5, RMa 7 / 4, Indoor-Office 7 / 4, InF 7 / 8; K is defined for LOS links only)
 RICIAN_K_DB = {"UMi": (9.0, 5.0), "UMa": (9.0, 3.5), "RMa": (7.0, 4.0), "InH": (7.0, 4.0),
                "InF-SL": (7.0, 8.0), "InF-DL": (7.0, 8.0), "InF-SH": (7.0, 8.0), "InF-DH": (7.0, 8.0)}
+
+
+def sum_of_cosines_cdf_table(K, n=1 << 16, seed=0):
+    """Sorted samples [n] (float32, torch) of sqrt(2/K) sum_k cos(U_k), U_k ~ U(0, 2 pi) drawn from a CPU generator
+    seeded with seed, in float64 (fields.py:94-100): the empirical marginal of a unit plane-wave field, through which
+    the LOS-state field becomes a U(0, 1) value (the kernels search it as torch.searchsorted does)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    z = math.sqrt(2 / K) * torch.cos(torch.rand(n, K, generator=g, dtype=torch.float64) * 2 * math.pi).sum(-1)
+    return z.sort().values.float()

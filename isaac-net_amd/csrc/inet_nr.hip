@@ -278,6 +278,8 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
     if (p.fc_on && !p.fc_L) return INET_NR_EINVAL;
+    if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
+        return INET_NR_EINVAL;
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
     const int rb = next_pow2(p.R);

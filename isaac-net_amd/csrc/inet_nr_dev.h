@@ -295,19 +295,79 @@ DEV float aten_row_sum(int n, X x) {
 // PM: a parameter struct with the radio fields of InetNrParams (hh2 ... pl_exp10, ue_tx, radio_model, n_modes);
 // fld_env: the cell's fields of the env [n_fields][n_modes][3] (kx, ky, phase). The transcendental functions are evaluated in
 // double precision and rounded once (the field arguments k . x reach 1e4 rad).
+// the plane-wave field fld [n_modes][3] (kx, ky, phase) at (px, py): amp times the ATen-order row sum of the cosines
+DEV float field_at(float px, float py, const float* fld, int n_modes, float amp) {
+    float cs[16];
+    for (int k = 0; k < n_modes; ++k) {
+        float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
+        cs[k] = (float)cos((double)arg);
+    }
+    // runtime-length ATen row sum (n_modes <= 16)
+    float field;
+    if (n_modes >= 8) {
+        field = 0.f;
+        for (int k = 8; k < n_modes; ++k) field += cs[k];
+        for (int l = 0; l < 8; ++l) field += cs[l];
+    } else {
+        float q[4] = {0.f, 0.f, 0.f, 0.f};
+        const int si = n_modes / 4;
+        for (int i = 0; i < si; ++i)
+            for (int k = 0; k < 4; ++k) q[k] += cs[i * 4 + k];
+        for (int i = si * 4; i < n_modes; ++i) q[0] += cs[i];
+        field = ((q[0] + q[1]) + q[2]) + q[3];
+    }
+    return amp * field;
+}
+
+// The TR 38.901 stochastic LOS state (models.py:121-135, tr38901.py:228-242): the LOS-state field value z through the
+// empirical CDF of a unit sum of cosines (cdf: 65536 sorted samples), u = (index of the first sample >= z + 0.5) /
+// 65537 as torch.searchsorted and float32 arithmetic give it, against Pr_LOS(d_2D) of the scenario (scn 0 UMi, 1 UMa
+// with h_UT <= 13 m, 2 InH); true: LOS.
+struct StoLos {
+    const float* cdf;
+    int scn;
+    float sig_nlos;
+};
+DEV bool los_draw(const StoLos& sl, float z, float d2) {
+    int lo = 0, hi = 1 << 16;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sl.cdf[mid] < z) lo = mid + 1;
+        else hi = mid;
+    }
+    const float u = ((float)lo + 0.5f) / 65537.0f;
+    float p;
+    if (sl.scn <= 1) {
+        const float d = d2 > 18.0f ? d2 : 18.0f;
+        const float e = expf(-d / (sl.scn == 0 ? 36.0f : 63.0f));
+        p = d2 <= 18.0f ? 1.0f : 18.0f / d + e * (1.0f - 18.0f / d);
+    } else {
+        p = d2 <= 1.2f ? 1.0f : (d2 < 6.5f ? expf(-(d2 - 1.2f) / 4.7f) : expf(-(d2 - 6.5f) / 32.6f) * 0.32f);
+    }
+    return u < p;
+}
+
 template <class PM>
-DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, const float* fld_env) {
+DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, const float* fld_env,
+                       const StoLos* sto = nullptr) {
     float dx = px - gx, dy = py - gy;
     float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
     int fi = 0;
-    float pl;
-    if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203), deterministic LOS state
+    float pl, sig = 0.f;
+    if (pm.radio_model == 1) {                 // TR 38.901 (tr38901.py:162-203)
         float d3 = sqrtf(d2 * d2 + pm.hh2);
         float lg = (float)log10((double)d3);
         float pl1 = (pm.pl_a + pm.pl_n1 * lg) + pm.pl_c20;
         float pl2 = ((pm.pl_a + 40.0f * lg) + pm.pl_c20) - pm.pl_c2;
         pl = d2 <= pm.dbp ? pl1 : pl2;
-        if (pm.nl_b1 != 0.0f) {                // NLOS: max(PL_LOS, PL'_NLOS)
+        sig = pm.sig;
+        // NLOS: the fixed NLOS state, or the stochastic state's draw (the LOS-state field is field 2)
+        bool nlos = pm.nl_b1 != 0.0f;
+        if (sto) {
+            nlos = !los_draw(*sto, field_at(px, py, fld_env + 2 * pm.n_modes * 3, pm.n_modes, pm.amp), d2);
+            if (nlos) sig = sto->sig_nlos;
+        }
+        if (nlos) {                            // NLOS: max(PL_LOS, PL'_NLOS)
             float pn = ((pm.nl_b1 * lg + pm.nl_b0) + pm.nl_c) - pm.nl_d;
             pl = pn > pl ? pn : pl;
             fi = 1;
@@ -315,29 +375,9 @@ DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, con
     } else {
         pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
     }
-    const float* fld = fld_env + fi * pm.n_modes * 3;
-    float cs[16];
-    for (int k = 0; k < pm.n_modes; ++k) {
-        float arg = (px * fld[k * 3 + 0] + py * fld[k * 3 + 1]) + fld[k * 3 + 2];
-        cs[k] = (float)cos((double)arg);
-    }
-    // runtime-length ATen row sum (n_modes <= 16)
-    float field;
-    if (pm.n_modes >= 8) {
-        field = 0.f;
-        for (int k = 8; k < pm.n_modes; ++k) field += cs[k];
-        for (int l = 0; l < 8; ++l) field += cs[l];
-    } else {
-        float q[4] = {0.f, 0.f, 0.f, 0.f};
-        const int si = pm.n_modes / 4;
-        for (int i = 0; i < si; ++i)
-            for (int k = 0; k < 4; ++k) q[k] += cs[i * 4 + k];
-        for (int i = si * 4; i < pm.n_modes; ++i) q[0] += cs[i];
-        field = ((q[0] + q[1]) + q[2]) + q[3];
-    }
-    field = pm.amp * field;
+    const float field = field_at(px, py, fld_env + fi * pm.n_modes * 3, pm.n_modes, pm.amp);
     if (pm.radio_model == 1) {
-        float loss = pl + pm.sig * field;
+        float loss = pl + sig * field;
         return pm.ue_tx + (-loss);
     }
     return (pm.ue_tx - pl) - field;

@@ -326,7 +326,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
         pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
-        pm.fc_on = 0;
+        pm.fc_on = 0; pm.los_sto = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -578,6 +578,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     float ref[(VREF || MC) ? S : 1];
     float snr_out = 0.f;
     float pgc[NC];                                 // several cells: path gain to every cell (dB)
+    // the stochastic LOS state of TR 38.901 (general build only)
+    const StoLos sto_los{pm.los_cdf, pm.plos_scn, pm.sig_nlos};
+    const StoLos* const sto_p = (FX == 0 && pm.los_sto) ? &sto_los : nullptr;
     if constexpr (MC) {
         // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
         float px = 0.f, py = 0.f;
@@ -585,7 +588,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
-            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc) - pm.ue_tx;
+            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_p) - pm.ue_tx;
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) ref[s] = 0.f;
@@ -604,7 +607,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         float px = 0.f, py = 0.f;
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
         const float rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y,
-                                      st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3);
+                                      st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3, sto_p);
         const float pg = rx - pm.ue_tx;
         if constexpr (DL) ref[0] = (pg + lk.ref_off) - lk.noise_prb;
         else ref[0] = (pg + pm.ref_off) - pm.noise_prb;
@@ -1932,7 +1935,7 @@ void launch_step(const StepArgs& a) {
 // the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
-                        p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 &&
+                        p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 && p.los_sto == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

@@ -325,6 +325,14 @@ def plane_waves(rand, spectrum, dcorr):
     return k.permute(1, 0, 2, 3).contiguous(), phi.permute(1, 0, 2).contiguous()
 
 
+def sum_of_cosines_cdf(K, n=1 << 16, seed=0):
+    """Sorted samples [n] (float32) of sqrt(2/K) sum_k cos(U_k), U_k ~ U(0, 2 pi) from a CPU generator seeded with
+    seed, in float64 (fields.py:94-100): the empirical marginal of a unit field."""
+    g = torch.Generator().manual_seed(seed)
+    z = math.sqrt(2 / K) * torch.cos(torch.rand(n, K, generator=g, dtype=torch.float64) * 2 * math.pi).sum(-1)
+    return z.sort().values.float()
+
+
 def eval_plane_waves(pos, k, phi, amp):
     arg = torch.einsum("erx,cekx->cerk", pos, k) + phi[:, :, None, :]
     return (amp * torch.cos(arg).sum(-1)).permute(1, 2, 0)
@@ -346,7 +354,8 @@ class Radio:
         if self.model == "log_distance":
             self.amp = cfg.shadow_sigma_db * math.sqrt(2 / K)
         else:
-            assert cfg.tr38901_los in ("los", "nlos") and cfg.o2i_indoor_frac == 0
+            assert cfg.o2i_indoor_frac == 0
+            assert cfg.tr38901_los in ("los", "nlos") or cfg.tr38901_scenario in ("UMi", "UMa", "InH")
             sc = SCENARIOS[cfg.tr38901_scenario]
             self.scn = cfg.tr38901_scenario
             self.h_bs = float(cfg.gnb_height_m) if cfg.gnb_height_m is not None else sc.h_bs
@@ -356,6 +365,8 @@ class Radio:
             self.sig = SIGMA_SF[self.scn]
             self.amp = 1.0 * math.sqrt(2 / K)
             self.dcorr = (sc.sf_corr_los_m, sc.sf_corr_nlos_m, sc.los_corr_m)
+            if cfg.tr38901_los == "stochastic":
+                self.cdf = sum_of_cosines_cdf(K)
         self.fields = self.draw()
 
     def draw(self):
@@ -392,6 +403,19 @@ class Radio:
             return cfg.ue_tx_dbm - pl - sh
         d2 = (pos[:, :, None, :] - self.gnb).norm(dim=-1).clamp(min=1.0)
         d3 = torch.sqrt(d2 * d2 + (self.h_bs - self.h_ut) ** 2)
+        if cfg.tr38901_los == "stochastic":
+            # the LOS state (models.py:121-135): u(x) from the LOS-state field through the empirical CDF of a unit
+            # sum of cosines (fields.py:94-106), LOS where u < Pr_LOS(d_2D) (tr38901.py:228-242)
+            z = eval_plane_waves(pos, *self.fields[2], self.amp)
+            n = self.cdf.numel()
+            u = (torch.searchsorted(self.cdf, z.contiguous()).float() + 0.5) / (n + 1)
+            los = u < self._p_los(d2)
+            pl_l = self._pl_los(d2, d3)
+            pl = torch.where(los, pl_l, self._pl_nlos(d3, pl_l))
+            sf = torch.where(los, self.sig[0] * eval_plane_waves(pos, *self.fields[0], self.amp),
+                             self.sig[1] * eval_plane_waves(pos, *self.fields[1], self.amp))
+            self.los = los
+            return cfg.ue_tx_dbm + (-(pl + sf))
         los = cfg.tr38901_los == "los"
         pl_l = self._pl_los(d2, d3)
         pl = pl_l if los else self._pl_nlos(d3, pl_l)
@@ -414,6 +438,17 @@ class Radio:
         if scn.startswith("InF"):
             return 31.84 + 21.50 * lg + 19.00 * math.log10(fc)
         raise NotImplementedError(scn)
+
+    def _p_los(self, d2):
+        """LOS probability, Table 7.4.2-1 (tr38901.py:228-242), UMi / UMa (h_UT <= 13 m) / InH."""
+        if self.scn in ("UMi", "UMa"):
+            d = torch.clamp(d2, min=18.0)
+            dd = 36.0 if self.scn == "UMi" else 63.0
+            p = 18.0 / d + torch.exp(-d / dd) * (1 - 18.0 / d)
+            assert self.scn == "UMi" or self.h_ut <= 13.0
+            return torch.where(d2 <= 18.0, torch.ones_like(p), p)
+        return torch.where(d2 <= 1.2, torch.ones_like(d2), torch.where(d2 < 6.5, torch.exp(-(d2 - 1.2) / 4.7),
+                                                                        torch.exp(-(d2 - 6.5) / 32.6) * 0.32))
 
     def _pl_nlos(self, d3, los):
         scn, fc = self.scn, self.fc

@@ -264,6 +264,27 @@ CASES = {
     "rice_snr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
                               frame_buffer=8, msg_sizes=(2500.0,), fading_rician=True, fading_rho_per_ms=0.5),
                      E=3, R=8, steps=20, kind="snr", snr=(-2.0, 16.0), rates=(0.9,), resets={9: [0]}),
+    # the TR 38.901 stochastic LOS state (the reference's default): LOS where the LOS-state field's uniform is below
+    # Pr_LOS(d_2D) (models.py:121-167): UMi at distances where both states occur, fast motion, a reset
+    "los_sto": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                             max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_rho_per_ms=0.5,
+                             channel="tr38901", tr38901_scenario="UMi", tr38901_los="stochastic",
+                             cell_positions_m=((150.0, 150.0),), gnb_height_m=10.0),
+                    E=3, R=16, steps=30, kind="pose", arena=300.0, walk=4.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # three cells on UMa with the stochastic LOS state of every robot-cell link, interference
+    "los_sto_mc": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                                max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3, cell_layout="hex",
+                                cell_isd_m=200.0, noise_model="thermal", a3_offset_db=float("inf"), channel="tr38901",
+                                tr38901_scenario="UMa", tr38901_los="stochastic", gnb_height_m=25.0,
+                                fading_rho_per_ms=0.5),
+                       E=2, R=16, steps=25, kind="pose", arena=300.0, walk=3.0, rates=(0.7,), resets={12: [1]}),
+    # indoor hotspot with the downlink
+    "los_sto_dl": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                n_harq=4, max_harq_tx=3, frame_buffer=8, msg_sizes=(2000.0,), fading_rho_per_ms=0.0,
+                                channel="tr38901", tr38901_scenario="InH", tr38901_los="stochastic",
+                                cell_positions_m=((30.0, 30.0),), gnb_height_m=3.0, dl=True),
+                       E=3, R=8, steps=25, kind="pose", arena=60.0, walk=1.0, rates=(0.8,), dl_sizes=(4000.0,),
+                       dl_rates=(0.6,), resets={11: [2]}),
 }
 
 

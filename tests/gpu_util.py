@@ -131,11 +131,19 @@ def set_radio_bound(ref, s, cfg, eng, kind):
     key = next((k for k in (f"s{s:03d}/radio.k", f"s{s:03d}/radio.sf_los.k") if k in ref), None)
     if key is None:
         return
-    n = "radio" if key.endswith("radio.k") else "radio." + ("sf_los", "sf_nlos")[fi]
-    k_, phi = ref[f"s{s:03d}/{n}.k"], ref[f"s{s:03d}/{n}.phi"]             # [C, E, K, 2], [C, E, K]
-    # the field of each robot's serving cell (cell 0 with one cell)
-    b = np.stack([sinr_bound(ref["x"][s], np.concatenate([k_[c], phi[c][..., None]], -1), sig, amp,
-                             ref[f"s{s:03d}/out.sinr_db"]) for c in range(k_.shape[0])], -1)
+    fields = [("radio", sig)] if key.endswith("radio.k") else [("radio." + ("sf_los", "sf_nlos")[fi], sig)]
+    if not key.endswith("radio.k") and cfg.tr38901_los == "stochastic":
+        # the stochastic LOS state: each link follows the LOS or the NLOS field (the larger bound of the two)
+        from isaac_net_amd.channels import SIGMA_SF, scenario_name
+        sl, sn = SIGMA_SF[scenario_name(cfg.tr38901_scenario)]
+        fields = [("radio.sf_los", sl), ("radio.sf_nlos", sn)]
+    b = None
+    for n, sg in fields:
+        k_, phi = ref[f"s{s:03d}/{n}.k"], ref[f"s{s:03d}/{n}.phi"]             # [C, E, K, 2], [C, E, K]
+        # the field of each robot's serving cell (cell 0 with one cell)
+        bn = np.stack([sinr_bound(ref["x"][s], np.concatenate([k_[c], phi[c][..., None]], -1), sg, amp,
+                                  ref[f"s{s:03d}/out.sinr_db"]) for c in range(k_.shape[0])], -1)
+        b = bn if b is None else np.maximum(b, bn)
     serv = ref[f"s{s:03d}/out.serving_cell"]
     b = np.take_along_axis(b, serv[..., None], -1)[..., 0]
     BOUND["out.sinr_db"] = b
