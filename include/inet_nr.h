@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 11
+#define INET_NR_ABI_VERSION 12
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -107,6 +107,12 @@ typedef struct InetNrState {
        nr_engine.py:300-303), written by inet_nr_reset with params.k_from_los (ABI version 10); the K the step uses
        is k_lin, which the caller sets to k_los once the link is reported LOS (NRNet.set_los) */
     float *k_los;
+    /* Rician K from the LOS state, the ramp (nr_engine.py:402-419; ABI 12): per robot [E][R] the ramp start k_from and
+       its slot k_g0 (k_lin is the target), per env [E] k_fresh (no LOS state seen since the reset). The step kernels
+       apply NRNet.set_los with the radio's LOS state of a pose step (K target = k_los where LOS, else 0; a fresh env
+       takes it at once), start a ramp of k_ramp slots where the target changed, and evaluate K in every slot. */
+    float *k_from;
+    int32_t *k_g0, *k_fresh;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -162,6 +168,7 @@ typedef struct InetNrParams {
                                          u the LOS-state field (field 2) through los_cdf; NLOS path loss and sig_nlos
                                          elsewhere (ABI 11) */
     int32_t plos_scn;                 /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
+    int32_t k_ramp;                   /* k_from_los: rician_k_ramp_slots (0: a new target applies at once) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -171,6 +178,7 @@ typedef struct InetNrParams {
     float pc_p0, pc_alpha;            /* pc1_on: P0 (dBm) and alpha of the fractional power control */
     float k_mu, k_sigma;              /* k_from_los: (mu_K, sigma_K) dB of the scenario, TR 38.901 Table 7.5-6 */
     float sig_nlos;                   /* los_sto: NLOS shadow-fading sigma (dB); sig is the LOS one */
+    float k_rinv;                     /* k_from_los: 1 / k_ramp as float32 (the ramp's step per slot) */
     const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
     const float *los_cdf;             /* los_sto: [65536] sorted samples of a unit sum of cosines (fields.py:94-106) */
 } InetNrParams;

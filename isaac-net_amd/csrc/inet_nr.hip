@@ -168,7 +168,10 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
     const int R = pm.R, S = pm.S, P = pm.P, F = pm.F;
     const int NC = pm.n_cells > 1 ? pm.n_cells : 1;
     __shared__ int ep_new;
-    if (threadIdx.x == 0) ep_new = st.episode[e] + 1;
+    if (threadIdx.x == 0) {
+        ep_new = st.episode[e] + 1;
+        if (pm.rician && pm.k_from_los) st.k_fresh[e] = 1;      // waiting for the env's first LOS state
+    }
     __syncthreads();
     const uint32_t s0 = (uint32_t)pm.seed_key, env = (uint32_t)st.env_id[e], ep = (uint32_t)ep_new;
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
@@ -229,6 +232,8 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
                 const float x = (pm.k_mu + pm.k_sigma * normal_at(bz, (uint32_t)r)) / 10.0f;
                 st.k_los[ir] = (float)exp10((double)x);
                 st.k_lin[ir] = 0.0f;
+                st.k_from[ir] = 0.0f;
+                st.k_g0[ir] = 0;
             }
         }
     }
@@ -278,6 +283,9 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
     if (p.fc_on && !p.fc_L) return INET_NR_EINVAL;
+    if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0 ||
+                         p.n_cells > 1))
+        return INET_NR_EINVAL;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_NR_EINVAL;
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
@@ -424,7 +432,8 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
     if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
-    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L) || (p.k_from_los && (!st->k_los || !p.rician)))
+    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L) ||
+        (p.k_from_los && (!st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || !p.rician)))
         return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,
                        dcorr[0], dcorr[1], dcorr[2], spectrum, mask ? 0 : 1);

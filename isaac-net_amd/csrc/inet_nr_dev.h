@@ -322,11 +322,12 @@ DEV float field_at(float px, float py, const float* fld, int n_modes, float amp)
 // The TR 38.901 stochastic LOS state (models.py:121-135, tr38901.py:228-242): the LOS-state field value z through the
 // empirical CDF of a unit sum of cosines (cdf: 65536 sorted samples), u = (index of the first sample >= z + 0.5) /
 // 65537 as torch.searchsorted and float32 arithmetic give it, against Pr_LOS(d_2D) of the scenario (scn 0 UMi, 1 UMa
-// with h_UT <= 13 m, 2 InH); true: LOS.
+// with h_UT <= 13 m, 2 InH); true: LOS. on = false: the fixed LOS state of the parameters.
 struct StoLos {
     const float* cdf;
     int scn;
     float sig_nlos;
+    bool on;
 };
 DEV bool los_draw(const StoLos& sl, float z, float d2) {
     int lo = 0, hi = 1 << 16;
@@ -349,7 +350,7 @@ DEV bool los_draw(const StoLos& sl, float z, float d2) {
 
 template <class PM>
 DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, const float* fld_env,
-                       const StoLos* sto = nullptr) {
+                       const StoLos& sto = StoLos{nullptr, 0, 0.f, false}, bool* los_out = nullptr) {
     float dx = px - gx, dy = py - gy;
     float d2 = clamp_min(sqrtf(dx * dx + dy * dy), 1.0f);
     int fi = 0;
@@ -363,15 +364,16 @@ DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, con
         sig = pm.sig;
         // NLOS: the fixed NLOS state, or the stochastic state's draw (the LOS-state field is field 2)
         bool nlos = pm.nl_b1 != 0.0f;
-        if (sto) {
-            nlos = !los_draw(*sto, field_at(px, py, fld_env + 2 * pm.n_modes * 3, pm.n_modes, pm.amp), d2);
-            if (nlos) sig = sto->sig_nlos;
+        if (sto.on) {
+            nlos = !los_draw(sto, field_at(px, py, fld_env + 2 * pm.n_modes * 3, pm.n_modes, pm.amp), d2);
+            if (nlos) sig = sto.sig_nlos;
         }
         if (nlos) {                            // NLOS: max(PL_LOS, PL'_NLOS)
             float pn = ((pm.nl_b1 * lg + pm.nl_b0) + pm.nl_c) - pm.nl_d;
             pl = pn > pl ? pn : pl;
             fi = 1;
         }
+        if (los_out) *los_out = !nlos;         // the link's LOS state (Radio.los_state)
     } else {
         pl = pm.pl_const + pm.pl_exp10 * (float)log10((double)d2);
     }

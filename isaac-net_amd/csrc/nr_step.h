@@ -326,7 +326,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
         pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
-        pm.fc_on = 0; pm.los_sto = 0;
+        pm.fc_on = 0; pm.los_sto = 0; pm.k_from_los = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -470,6 +470,11 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     }
     float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
     if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
+    // K from the LOS state (general build): kk is the target, kf the ramp start, kg its slot
+    const bool kl = FX == 0 && pm.k_from_los != 0;
+    float kf = 0.f;
+    int kg = 0;
+    if (kl && act) { kf = ldo(st.k_from, o_r); kg = ldo(st.k_g0, o_r); }
     float lnp = 0.f;                                   // PRBs of the last PUSCH (ul_amc_alloc "previous")
     if (!DL && pm.amc_prev && act) lnp = ldo(st.last_nprb, o_r);
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
@@ -567,9 +572,6 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         }
         __syncthreads();
     }
-    // rician gain coefficients (nr_engine.py:608-611): inv = 1 / (K + 1), sqrt(K inv), sqrt(inv)
-    const float kinv = 1.0f / (kk + 1.0f);
-    const float ka = sqrtf(kk * kinv), kb = sqrtf(kinv);
 
     // ---------------- inputs: SINR reference per subband and the reported SNR ----------------
     // the DL reference SINR per PRB (NRNet.step_rx / step, nr_engine.py:624-631, 651-653): with poses the gNB PSD
@@ -579,8 +581,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     float snr_out = 0.f;
     float pgc[NC];                                 // several cells: path gain to every cell (dB)
     // the stochastic LOS state of TR 38.901 (general build only)
-    const StoLos sto_los{pm.los_cdf, pm.plos_scn, pm.sig_nlos};
-    const StoLos* const sto_p = (FX == 0 && pm.los_sto) ? &sto_los : nullptr;
+    const StoLos sto_los{pm.los_cdf, pm.plos_scn, pm.sig_nlos, FX == 0 && pm.los_sto != 0};
+    bool los_now = false, los_rep = false;         // this step's LOS state of the link (TR 38.901 with poses)
     if constexpr (MC) {
         // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
         float px = 0.f, py = 0.f;
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
-            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_p) - pm.ue_tx;
+            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los) - pm.ue_tx;
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) ref[s] = 0.f;
@@ -607,7 +609,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         float px = 0.f, py = 0.f;
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
         const float rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y,
-                                      st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3, sto_p);
+                                      st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3, sto_los, &los_now);
+        los_rep = pm.radio_model == 1;
         const float pg = rx - pm.ue_tx;
         if constexpr (DL) ref[0] = (pg + lk.ref_off) - lk.noise_prb;
         else ref[0] = (pg + pm.ref_off) - pm.noise_prb;
@@ -668,6 +671,30 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     int n_ul = 0;
     int nf = 0, lost_dl = 0;                      // DL: first frame not yet resolved, frames lost under RLC UM
     const int g0 = (int)(T * (int64_t)N);
+
+    // ---------------- Rician K of the link (nr_engine.py:370-419, 602-611) ----------------
+    // K of slot g on the ramp: the target once k_ramp slots have begun since kg, else k_from + (target - k_from) n / k_ramp
+    auto k_at = [&](int g) -> float {
+        const int n = g - kg + 1;
+        return n >= pm.k_ramp ? kk : kf + (kk - kf) * ((float)n * pm.k_rinv);
+    };
+    // NRNet.set_los with this step's LOS state (target k_los where LOS, else 0; an env's first state since its reset
+    // applies at once), then _rician_update at g0 (a changed target starts a ramp from the K of slot g0 - 1)
+    if (kl && los_rep) {
+        const float kt = (act && los_now) ? ldo(st.k_los, o_r) : 0.f;
+        if (act && st.k_fresh[ee] != 0) { kk = kt; kf = kt; }
+        else if (pm.k_ramp == 0) kk = kt;
+        else if (kt != kk) { kf = k_at(g0 - 1); kg = g0; kk = kt; }
+    }
+    // gain coefficients inv = 1 / (K + 1), sqrt(K inv), sqrt(inv); while a ramp runs, set again in every slot
+    float ka = 0.f, kb = 1.f;
+    auto set_k = [&](float k) {
+        const float kinv = 1.0f / (k + 1.0f);
+        ka = sqrtf(k * kinv);
+        kb = sqrtf(kinv);
+    };
+    set_k(kk);
+    const bool k_ramps = kl && pm.k_ramp > 0;
 
     // ---------------- several cells: association and the A3 plan of this step (CellAssociation, radio.py:410-437) ----
     // rx = path gain + ue_tx (RSRP up to a constant); a pending env attaches every robot to its max-rx cell; the A3
@@ -766,6 +793,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
         const int g = g0 + row.rel;
+        if (k_ramps) set_k(k_at(g));
         if constexpr (MC) {                        // A3 handovers due by this slot (nr_engine.py:740-754)
             if (act && !fired && k_ho >= 0 && k_ho <= row.rel) handover(g0 + k_ho);
         }
@@ -1824,6 +1852,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         if constexpr (!DL) {
             sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
             if (pm.amc_prev) sto(st.last_nprb, o_r, lnp);
+            if (kl) { sto(st.k_lin, o_r, kk); sto(st.k_from, o_r, kf); sto(st.k_g0, o_r, kg); }
         }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
         if (arr.counts || rebased) sto(lk.enq, o_r, enq);
@@ -1883,6 +1912,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             out.det_env[e] = det_any;
             out.t[e] = (int64_t)t - (int64_t)st.epoch[e];
             st.ctr_step[e] = st.ctr_step[e] + 1;      // rng.tick_step (nr_engine.py:847-848)
+            if (kl && los_rep) st.k_fresh[e] = 0;      // the env's LOS state has arrived
         }
         int64_t* c = lk.ctr + (size_t)e * INET_NR_NCTR;
         c[0] += v_new; c[1] += v_retx; c[2] += v_ok; c[3] += v_fail; c[4] += v_exh;
@@ -1935,7 +1965,7 @@ void launch_step(const StepArgs& a) {
 // the build that fixes these parameters at compile time: 1 (with the Rician phasor) or 2 (without), 0 for none
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
-                        p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 && p.los_sto == 0 &&
+                        p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 && p.los_sto == 0 && p.k_from_los == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

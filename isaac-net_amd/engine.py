@@ -96,8 +96,6 @@ def refusals(cfg: NRConfig):
     no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
        "the per-RBG PF update of the pf scheduler")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
-    no(cfg.rician_mode == "los" and cfg.channel == "tr38901" and cfg.tr38901_los == "stochastic",
-       "Rician K from a stochastic LOS state", "K from a fixed LOS state (tr38901_los 'los' / 'nlos')")
     no(cfg.freq_corr_mode == "los", "frequency-correlated fading with per-link delay spreads from the LOS state "
        "(fading_delay_spread_ns=None)", "one fixed delay spread (fading_delay_spread_ns)")
     no(cfg.fading_doppler != "global", "per-robot Doppler fading", "one rho")
@@ -215,6 +213,7 @@ class HipNREngine:
             "q_meta": z(E, F, R), "q_hid": z(E, F, R),
             "spec_re": z(E, R, dt=f32), "spec_im": z(E, R, dt=f32), "k_lin": z(E, R, dt=f32),
             "k_los": z(E, R, dt=f32),                  # the LOS K draw (Rician K from the LOS state)
+            "k_from": z(E, R, dt=f32), "k_g0": z(E, R), "k_fresh": z(E),   # its ramp start, slot and fresh envs
             "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
             "ctr_submit": z(E), "epoch": z(E),
             "field": z(E, self.C, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
@@ -328,6 +327,8 @@ class HipNREngine:
         p.k_from_los = int(cfg.rician_mode == "los")
         if p.k_from_los:                              # (mu_K, sigma_K) of the scenario (nr_engine.py:67-77)
             p.k_mu, p.k_sigma = RICIAN_K_DB[scenario_name(cfg.tr38901_scenario)]
+            p.k_ramp = int(cfg.rician_k_ramp_slots)   # K ramps to a new target over k_ramp slots
+            p.k_rinv = 1.0 / p.k_ramp if p.k_ramp else 0.0
         p.purge = int(cfg.discard == "purge")
         p.out_ref = int(self.out_format == "reference")
         p.max_tx, p.sr_delay, p.ul_rtt, p.rlc_retx = cfg.max_harq_tx, cfg.sr_delay, cfg.ul_rtt, cfg.rlc_retx_slots
@@ -532,7 +533,6 @@ class HipNREngine:
             if self.dl:
                 _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), None, self._stream()),
                            "dl reset")
-            self._k_mark_fresh(None)
             return
         if isinstance(env_ids, torch.Tensor) and env_ids.dtype == torch.bool:
             mask = env_ids.to(self.dev)
@@ -556,7 +556,6 @@ class HipNREngine:
             _lib.check(lib.inet_nr_dl_reset(C.byref(self._cdl), C.byref(self._cparams), m8.data_ptr(),
                                             self._stream()), "dl reset")
 
-        self._k_mark_fresh(mask)
         self._uniform_epoch = None
         mk = mask[:, None]
         self._last_snr = torch.where(mk, torch.zeros_like(self._last_snr), self._last_snr)
@@ -580,32 +579,6 @@ class HipNREngine:
     def _k_lin0(self):
         cfg = self.config
         return float(10 ** (cfg.rician_k_db / 10)) if cfg.rician_mode == "fixed" else 0.0
-
-    # Rician K from the LOS state (NRNet.set_los, nr_engine.py:370-392): after a reset an env's K is 0 until a step
-    # with poses reports its links' LOS state, which then applies at once; a fixed LOS state never changes after that
-    # (so no K ramp starts). _k_fresh [E]: envs waiting for their first LOS state; _k_pending: any such env (host).
-    _k_fresh = None
-    _k_pending = False
-
-    def _k_mark_fresh(self, mask):
-        if self.config.rician_mode != "los":
-            return
-        if self._k_fresh is None or mask is None:
-            self._k_fresh = torch.ones(self.E, dtype=torch.bool, device=self.dev)
-        else:
-            self._k_fresh |= mask
-        self._k_pending = True
-
-    def _k_set_los(self, x):
-        """Before a step with poses x [E,R,2|3]: the radio's LOS state sets the K of the envs waiting for it."""
-        cfg = self.config
-        if not self._k_pending or x is None or x.dim() != 3 or cfg.channel != "tr38901":
-            return
-        st = self.st
-        k = st["k_los"] if cfg.tr38901_los == "los" else torch.zeros_like(st["k_los"])
-        st["k_lin"].copy_(torch.where(self._k_fresh[:, None], k, st["k_lin"]))
-        self._k_fresh.zero_()
-        self._k_pending = False
 
     def submit(self, t, requests, snr_db=None, *, tag=None, priority=None, deadline_ms=None):
         """Enqueue one message per robot (Requests or send [E,R]); returns accepted [E,R] bool (engine.py:796-819)."""
@@ -726,8 +699,6 @@ class HipNREngine:
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
         self._check_kind(kind)
-        if kind == 0:
-            self._k_set_los(x)
         plan = self._plan(T, kind)
         dl = None
         if self.dl:
@@ -1086,15 +1057,15 @@ class HipNREngine:
             out["net.ni_ul"] = c["ni_ul"]
             out["net.ioN[ul]"] = c["ion"]
         if cfg.rician_mode in ("fixed", "los"):
-            # (a fixed LOS state never starts a K ramp: input, target and ramp start are the K in use, k_g0 0)
+            # (between steps the input K is the target; a fixed K never ramps: ramp start = target, k_g0 0)
             k = st["k_lin"]
-            out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1),
-                        "net.k_los": k if cfg.rician_mode == "fixed" else st["k_los"], "net.k_in": k,
-                        "net.k_lin": k, "net.k_from": k, "net.k_g0": torch.zeros_like(L(st["epoch"]))[:, None]
-                        .expand(-1, self.R)})
+            out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1), "net.k_in": k, "net.k_lin": k})
             if cfg.rician_mode == "los":
-                out["net.k_fresh"] = self._k_fresh.clone() if self._k_fresh is not None else \
-                    torch.zeros(self.E, dtype=torch.bool, device=self.dev)
+                out.update({"net.k_los": st["k_los"], "net.k_from": st["k_from"], "net.k_g0": L(st["k_g0"]),
+                            "net.k_fresh": st["k_fresh"] != 0})
+            else:
+                out.update({"net.k_los": k, "net.k_from": k,
+                            "net.k_g0": torch.zeros_like(L(st["epoch"]))[:, None].expand(-1, self.R)})
         return out
 
     def _link_load(self, pre, st, sd):
@@ -1179,10 +1150,10 @@ class HipNREngine:
             st["k_lin"].copy_(g("net.k_lin"))
             if cfg.rician_mode == "los":
                 st["k_los"].copy_(g("net.k_los"))
+                st["k_from"].copy_(g("net.k_from"))
+                st["k_g0"].copy_(I(g("net.k_g0")))
                 fr = sd.get("net.k_fresh")
-                self._k_fresh = (torch.as_tensor(fr).to(self.dev).bool().clone() if fr is not None else
-                                 torch.zeros(self.E, dtype=torch.bool, device=self.dev))
-                self._k_pending = bool(self._k_fresh.any())
+                st["k_fresh"].copy_(I(torch.as_tensor(fr).to(self.dev)) if fr is not None else 0)
         self._last_snr = g("eng._last_snr").float().clone()
         self._last_hid = g("eng._last_hid").long().clone()
         if T is not None:
@@ -1440,8 +1411,6 @@ class GraphStep:
         T = eng.T
         kind, xin = eng._input(x, snr_db)
         eng._check_kind(kind)
-        if kind == 0:
-            eng._k_set_los(x)                 # (eager, before the replay: the K of envs waiting for their LOS state)
         if counts is None or tuple(counts.shape) != tuple(self.counts.shape):
             raise ValueError(f"counts must be {tuple(self.counts.shape)}")
         if kind not in self.inputs:

@@ -898,7 +898,9 @@ class OracleEngine:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
             if self.rician == "los" and cfg.channel == "tr38901":
-                self._set_los(torch.full((self.E, self.R), cfg.tr38901_los == "los"))
+                # the radio's LOS state (Radio.los_state, engine.py:853-861): fixed, or the stochastic draw
+                self._set_los(self.radio.los[..., 0] if cfg.tr38901_los == "stochastic"
+                              else torch.full((self.E, self.R), cfg.tr38901_los == "los"))
             pgs = pg[..., None].expand(-1, -1, self.S)
             n_ul = torch.full_like(pgs, cfg.noise_dbm_per_prb("gnb"))
             ul_ref = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs) + pgs - n_ul

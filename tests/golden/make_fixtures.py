@@ -285,6 +285,29 @@ CASES = {
                                 cell_positions_m=((30.0, 30.0),), gnb_height_m=3.0, dl=True),
                        E=3, R=8, steps=25, kind="pose", arena=60.0, walk=1.0, rates=(0.8,), dl_sizes=(4000.0,),
                        dl_rates=(0.6,), resets={11: [2]}),
+    # Rician K from the stochastic LOS state (the reference's defaults: fading_rician, K from LOS, a 4-slot ramp):
+    # links flip between LOS and NLOS as the robots move, and K ramps to each new target (nr_engine.py:370-419)
+    "rice_sto": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                              max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_rician=True,
+                              fading_rho_per_ms=0.5, channel="tr38901", tr38901_scenario="UMi",
+                              tr38901_los="stochastic", cell_positions_m=((150.0, 150.0),), gnb_height_m=10.0),
+                     E=3, R=16, steps=30, kind="pose", arena=300.0, walk=4.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # the same on InH with the downlink and no ramp (a new target applies at once)
+    "rice_sto_dl": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                 n_harq=4, max_harq_tx=3, frame_buffer=8, msg_sizes=(2000.0,), fading_rician=True,
+                                 fading_rho_per_ms=0.5, rician_k_ramp_slots=0, channel="tr38901",
+                                 tr38901_scenario="InH", tr38901_los="stochastic", cell_positions_m=((30.0, 30.0),),
+                                 gnb_height_m=3.0, dl=True),
+                        E=3, R=8, steps=25, kind="pose", arena=60.0, walk=2.0, rates=(0.8,), dl_sizes=(4000.0,),
+                        dl_rates=(0.6,), resets={11: [2]}),
+    # UMa with a ramp longer than two control steps (50 slots against 20 per step): ramps carry over steps, restart
+    # from a K on the way, and a checkpoint is taken mid-ramp
+    "rice_sto_slow": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                   n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), fading_rician=True,
+                                   fading_rho_per_ms=0.0, rician_k_ramp_slots=50, channel="tr38901",
+                                   tr38901_scenario="UMa", tr38901_los="stochastic",
+                                   cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
+                          E=3, R=16, steps=30, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={17: [0]}),
 }
 
 

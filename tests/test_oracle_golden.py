@@ -51,10 +51,11 @@ def test_oracle_bitwise_vs_reference(name):
                                               ("amc_prev", "ul_amc_alloc", "current"),
                                               ("mc2_lena", "ul_retx_sched", "ofdma"),
                                               ("fcorr", "fading_delay_spread_ns", 3000.0),
-                                              ("fcorr_mc2", "fading_delay_spread_ns", 300.0)])
+                                              ("fcorr_mc2", "fading_delay_spread_ns", 300.0),
+                                              ("rice_sto_slow", "rician_k_ramp_slots", 4)])
 def test_switch_trajectories_pin_the_switch(name, field, wrong):
-    """The TDMA retransmission, previous-PUSCH AMC and frequency-correlated fading trajectories depend on their
-    switch: the oracle run with the switch at another value diverges from them (so the bitwise comparison above pins
+    """The TDMA retransmission, previous-PUSCH AMC, frequency-correlated fading and K-ramp trajectories depend on
+    their switch: the oracle run with the switch at another value diverges from them (so the bitwise comparison above pins
     the switch's code)."""
     import dataclasses
     d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
@@ -63,7 +64,7 @@ def test_switch_trajectories_pin_the_switch(name, field, wrong):
     diff = []
 
     def on_step(s, o, acc):
-        for k in ("ul.h_mcs", "ul.sent", "ul.h_state", "net.h"):
+        for k in ("ul.h_mcs", "ul.sent", "ul.h_state", "net.h", "ul.csi"):
             if not np.array_equal(d[f"s{s:03d}/{k}"], eng.state()[k].numpy()):
                 diff.append((s, k))
 
