@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 12
+#define INET_NR_ABI_VERSION 13
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -113,6 +113,10 @@ typedef struct InetNrState {
        takes it at once), start a ramp of k_ramp slots where the target changed, and evaluate K in every slot. */
     float *k_from;
     int32_t *k_g0, *k_fresh;
+    /* Per-link delay spreads (fc_on = 2, nr_engine.py:341-381; ABI 13): per robot [E][R] the grid index of fc_tab in
+       use (fc_idx) and those of the link's LOS and NLOS draws (fc_idl, fc_idn), drawn at reset; a pose step on TR 38.901
+       selects the LOS or NLOS one by the radio's LOS state (NLOS until one is reported). */
+    int32_t *fc_idx, *fc_idl, *fc_idn;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -160,8 +164,9 @@ typedef struct InetNrParams {
                                          the oldest NACK, and no new data in that slot (ABI version 8) */
     int32_t amc_prev;                 /* ul_amc_alloc="previous" (mac.py:393-401): the UL MCS for the PRBs of the last
                                          PUSCH (InetNrState.last_nprb), the TB for this allocation (ABI version 8) */
-    int32_t fc_on;                    /* frequency-correlated fading with a fixed delay spread (nr_engine.py:43-48,
-                                         320-368): every fading innovation and reset draw z becomes fc_L z (ABI 9) */
+    int32_t fc_on;                    /* frequency-correlated fading (nr_engine.py:43-48, 320-368): every fading
+                                         innovation and reset draw z becomes L z; 1: L = fc_L, one fixed delay spread
+                                         (ABI 9); 2: L = fc_tab[fc_idx] per link, per-link delay spreads (ABI 13) */
     int32_t k_from_los;               /* Rician K from the LOS state: inet_nr_reset draws k_los = 10^((k_mu + k_sigma z)
                                          / 10), z the link's KFAC normal, and sets k_lin = 0 (ABI 10) */
     int32_t los_sto;                  /* TR 38.901 stochastic LOS state (models.py:121-167): LOS where u(x) < Pr_LOS(d_2D),
@@ -169,6 +174,7 @@ typedef struct InetNrParams {
                                          elsewhere (ABI 11) */
     int32_t plos_scn;                 /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
     int32_t k_ramp;                   /* k_from_los: rician_k_ramp_slots (0: a new target applies at once) */
+    int32_t fc_G;                     /* fc_on 2: grid points of fc_tab (fading_ds_grid) */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -179,8 +185,12 @@ typedef struct InetNrParams {
     float k_mu, k_sigma;              /* k_from_los: (mu_K, sigma_K) dB of the scenario, TR 38.901 Table 7.5-6 */
     float sig_nlos;                   /* los_sto: NLOS shadow-fading sigma (dB); sig is the LOS one */
     float k_rinv;                     /* k_from_los: 1 / k_ramp as float32 (the ramp's step per slot) */
+    /* fc_on 2: lgDS = mu + sigma z (float32) of the NLOS and the LOS state (TR 38.901 Table 7.5-6), its grid index
+       round((lgDS + 9 - ds_c1) ds_c2) clamped to [0, fc_G - 1], ds_c1 = log10(min ns), ds_c2 = (G - 1) / log10(max/min) */
+    float ds_mu_n, ds_sig_n, ds_mu_l, ds_sig_l, ds_c1, ds_c2;
     const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
     const float *los_cdf;             /* los_sto: [65536] sorted samples of a unit sum of cosines (fields.py:94-106) */
+    const float *fc_tab;              /* fc_on 2: [fc_G][S][S] square roots of the subband correlation on the grid */
 } InetNrParams;
 
 /* One scheduled slot of the control step (host-built per TDD key, device resident). */

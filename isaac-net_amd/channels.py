@@ -70,21 +70,16 @@ def breakpoint_m(scn, fc_ghz, h_bs, h_ut):
 
 
 # ------------------------------------------------------------------ frequency-correlated fading
-def subband_fading_sqrt(cfg):
-    """The lower-triangular square root L [S,S] (float32, torch) of the subband correlation of the fading innovations
-    for the fixed rms delay spread cfg.fading_delay_spread_ns, or None (freq_corr_mode is not "fixed").
-
-    The subband centres are the cumulated RBG widths (PRBs x 12 x SCS) less half a width (nr_engine.py:125-129); the
-    correlation of subbands i, j is |1 / (1 + j 2 pi df tau)| = 1 / sqrt(1 + (2 pi df tau)^2) of an exponential
-    power-delay profile (nr_engine.py:132-156); L is its Cholesky factor with rows scaled to unit norm, a diagonal
-    jitter added while the factorization fails (nr_engine.py:159-168), in float64, rounded once to float32."""
+def _corr_sqrt(cfg, tau_ns):
+    """L [..., S, S] (float32, torch) for rms delay spreads tau_ns [...] (ns, float64): the subband centres are the
+    cumulated RBG widths (PRBs x 12 x SCS) less half a width (nr_engine.py:125-129); the correlation of subbands i, j
+    is |1 / (1 + j 2 pi df tau)| = 1 / sqrt(1 + (2 pi df tau)^2) of an exponential power-delay profile
+    (nr_engine.py:132-156); L is its Cholesky factor with rows scaled to unit norm, one diagonal jitter for the whole
+    batch while any factorization fails (nr_engine.py:159-168), in float64, rounded once to float32."""
     import torch
-    if cfg.freq_corr_mode != "fixed":
-        return None
     w = torch.tensor([float(x) for x in cfg.subband_prbs], dtype=torch.float64) * (12 * cfg.scs_khz * 1e3)
     f = torch.cumsum(w, 0) - w / 2
-    x = 2 * math.pi * (f[:, None] - f[None, :]) * torch.as_tensor(cfg.fading_delay_spread_ns * 1e-9,
-                                                                   dtype=torch.float64)
+    x = 2 * math.pi * (f[:, None] - f[None, :]) * (torch.as_tensor(tau_ns, dtype=torch.float64) * 1e-9)[..., None, None]
     c = 1.0 / torch.sqrt(1.0 + x * x)
     eye = torch.eye(c.shape[-1], dtype=c.dtype)
     for eps in (0.0, 1e-12, 1e-10, 1e-8, 1e-6):
@@ -92,6 +87,40 @@ def subband_fading_sqrt(cfg):
         if not bool((info != 0).any()):
             return (L / L.norm(dim=-1, keepdim=True)).float().contiguous()
     raise ValueError("subband correlation matrix is not positive definite")
+
+
+def subband_fading_sqrt(cfg):
+    """The lower-triangular square root L [S,S] (float32, torch) of the subband correlation of the fading innovations
+    for the fixed rms delay spread cfg.fading_delay_spread_ns, or None (freq_corr_mode is not "fixed")."""
+    if cfg.freq_corr_mode != "fixed":
+        return None
+    return _corr_sqrt(cfg, cfg.fading_delay_spread_ns)
+
+
+def delay_spread_grid(cfg):
+    """Per-link delay spreads (freq_corr_mode "los", nr_engine.py:320-340): the log grid of fading_ds_grid
+    (lo ns, hi ns, G points; torch.logspace in float64) and its square roots L [G,S,S] float32."""
+    import torch
+    lo, hi, G = cfg.fading_ds_grid
+    grid = torch.logspace(math.log10(lo), math.log10(hi), int(G), dtype=torch.float64)
+    return grid, _corr_sqrt(cfg, grid)
+
+
+# mean and spread of lgDS = log10(DS / 1 s), TR 38.901 V17.0.0 Table 7.5-6 (fc in GHz; the tables' frequency floors,
+# 2 GHz for UMi, 6 GHz for UMa and InH), as (LOS, NLOS) pairs of (mu, sigma)
+def lg_ds_params(scn, fc_ghz, los):
+    """(mu_lgDS, sigma_lgDS) of scenario scn in the LOS or NLOS state (nr_engine.py:92-113), Python floats."""
+    lg = math.log10
+    if scn == "UMi":
+        f = lg(1 + max(fc_ghz, 2.0))
+        return (-0.24 * f - 7.14, 0.38) if los else (-0.24 * f - 6.83, 0.16 * f + 0.28)
+    if scn == "UMa":
+        f = lg(max(fc_ghz, 6.0))
+        return (-6.955 - 0.0963 * f, 0.66) if los else (-6.28 - 0.204 * f, 0.39)
+    if scn == "InH":
+        f = lg(1 + max(fc_ghz, 6.0))
+        return (-0.01 * f - 7.692, 0.18) if los else (-0.28 * f - 7.173, 0.10 * f + 0.055)
+    raise ValueError(f"per-link delay spreads: no lgDS table for scenario {scn}")
 
 
 # Rician K-factor of LOS links, (mu_K, sigma_K) in dB per scenario: TR 38.901 V17.0.0 Table 7.5-6 (UMi-Street Canyon

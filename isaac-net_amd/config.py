@@ -68,7 +68,6 @@ REFERENCE_ONLY_DEFAULTS = {
     'doppler_min_speed_mps': 0.0,
     'fading_ds_from_los': True,
     'fading_pdp': 'exponential',
-    'fading_ds_grid': (3.0, 3000.0, 16),
     'inf_hall_volume_m3': None,
     'inf_hall_surface_m2': None,
     'inf_lg_ds': None,
@@ -200,6 +199,7 @@ class NRConfig:
     rician_k_ramp_slots: int = 4
     fading_freq_corr: bool = False
     fading_delay_spread_ns: float | None = None     # fading_freq_corr: one rms delay spread for every link (ns)
+    fading_ds_grid: tuple = (3.0, 3000.0, 16)       # per-link delay spreads: (min ns, max ns, points) of the L grid
     dl_snr_offset_db: float = 10.0
     noise_model: str = "fixed"
     ni_fixed_dbm: float = -90.0
@@ -269,6 +269,10 @@ class NRConfig:
 
     def __post_init__(self):
         assert self.mu in (0, 1, 2), "mu must be 0, 1 or 2 (FR1)"
+        self.fading_ds_grid = tuple(self.fading_ds_grid)
+        assert len(self.fading_ds_grid) == 3 and 0 < self.fading_ds_grid[0] < self.fading_ds_grid[1] and \
+            int(self.fading_ds_grid[2]) == self.fading_ds_grid[2] and self.fading_ds_grid[2] >= 2, \
+            "fading_ds_grid: (min ns, max ns, points >= 2)"
         assert set(self.tdd_pattern) <= set("DSU") and self.tdd_pattern
         assert self.harq_combining in ("cc", "ir_lena", "none") and self.harq_fail in ("rlc_am", "drop")
         assert self.eff_sinr in ("eesm", "mean_db") and self.pf_metric in ("subband", "wideband")

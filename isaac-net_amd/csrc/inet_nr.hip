@@ -17,7 +17,7 @@ using namespace inet;
 namespace {
 
 constexpr uint32_t CH_RESET = 3;
-constexpr uint32_t SITE_H0 = 4, SITE_KFAC = 5, SITE_KPHI = 6;
+constexpr uint32_t SITE_H0 = 4, SITE_KFAC = 5, SITE_KPHI = 6, SITE_DSPR = 7;
 
 }  // namespace
 
@@ -203,16 +203,31 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
         }
         if (pm.fc_on) {
             // frequency-correlated fading: the initial state correlated across the subbands too, h0 <- L h0 per link
-            // (nr_engine.py:264-266), the products accumulated with fused multiply-adds in subband order; rows from
-            // the last down, so each reads the uncorrelated values of the rows above it
+            // (nr_engine.py:264-266), the products accumulated in subband order; rows from the last down, so each
+            // reads the uncorrelated values of the rows above it. One delay spread: L = fc_L, fused multiply-adds (a
+            // float32 matrix product). Per-link delay spreads: the link's NLOS and LOS grid indices from two normals
+            // of reset site DSPR (elements 2 r, 2 r + 1; nr_engine.py:341-363), L = fc_tab[NLOS index], and the
+            // batched product's order: separate multiplies and adds while S S 2 < 400, fused above
+            const float* L = pm.fc_L;
+            bool seq = false;
+            if (pm.fc_on == 2) {
+                const uint32_t bd = base_key(s0, env, ep, CH_RESET, 0u, SITE_DSPR << 16);
+                const int idn = ds_index(pm.ds_mu_n, pm.ds_sig_n, normal_at(bd, 2u * r), pm.ds_c1, pm.ds_c2, pm.fc_G);
+                const int idl = ds_index(pm.ds_mu_l, pm.ds_sig_l, normal_at(bd, 2u * r + 1u), pm.ds_c1, pm.ds_c2,
+                                         pm.fc_G);
+                st.fc_idn[ir] = idn; st.fc_idl[ir] = idl; st.fc_idx[ir] = idn;
+                L = pm.fc_tab + (size_t)idn * S * S;
+                seq = S * S * 2 < 400;
+            }
             for (int c = 0; c < NC; ++c) {
                 const size_t i0 = ((size_t)e * CS + c * S) * R + r;
                 for (int i = S - 1; i >= 0; --i) {
                     float ar = 0.f, ai = 0.f;
                     for (int jj = 0; jj <= i; ++jj) {
-                        const float l = pm.fc_L[i * S + jj];
-                        ar = fmaf(l, st.h_re[i0 + (size_t)jj * R], ar);
-                        ai = fmaf(l, st.h_im[i0 + (size_t)jj * R], ai);
+                        const float l = L[i * S + jj];
+                        const float xr = st.h_re[i0 + (size_t)jj * R], xi = st.h_im[i0 + (size_t)jj * R];
+                        if (seq) { ar = ar + l * xr; ai = ai + l * xi; }
+                        else { ar = fmaf(l, xr, ar); ai = fmaf(l, xi, ai); }
                     }
                     st.h_re[i0 + (size_t)i * R] = ar;
                     st.h_im[i0 + (size_t)i * R] = ai;
@@ -282,7 +297,9 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
-    if (p.fc_on && !p.fc_L) return INET_NR_EINVAL;
+    if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L)) return INET_NR_EINVAL;
+    if (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn))
+        return INET_NR_EINVAL;
     if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0 ||
                          p.n_cells > 1))
         return INET_NR_EINVAL;
@@ -432,7 +449,10 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
     if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
-    if (T < 0 || T > 0x7fffffff || (p.fc_on && !p.fc_L) ||
+    if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L) ||
+        (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn)))
+        return INET_NR_EINVAL;
+    if (T < 0 || T > 0x7fffffff ||
         (p.k_from_los && (!st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || !p.rician)))
         return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,

@@ -348,6 +348,16 @@ DEV bool los_draw(const StoLos& sl, float z, float d2) {
     return u < p;
 }
 
+// Grid index of a link's delay spread (nr_engine.py:335-340, 352-356): lgDS = mu + sigma z, then
+// round((lgDS + 9 - c1) c2) (half to even) clamped to [0, G - 1], every step a float32 operation as in torch
+DEV int ds_index(float mu, float sig, float z, float c1, float c2, int G) {
+    const float lg = mu + sig * z;
+    float r = rintf(((lg + 9.0f) - c1) * c2);
+    r = r > 0.0f ? r : 0.0f;
+    r = r < (float)(G - 1) ? r : (float)(G - 1);
+    return (int)r;
+}
+
 template <class PM>
 DEV float radio_rx_dbm(const PM& pm, float px, float py, float gx, float gy, const float* fld_env,
                        const StoLos& sto = StoLos{nullptr, 0, 0.f, false}, bool* los_out = nullptr) {

@@ -349,6 +349,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // frequency-correlated fading: the subband correlation's square root (general build only)
     __shared__ float s_fcl[FX == 0 ? S * S : 1];
     const bool fc = FX == 0 && pm.fc_on != 0;
+    const bool fc2 = FX == 0 && pm.fc_on == 2;         // per-link delay spreads: L = fc_tab[the robot's grid index]
+    // the batched product of the reference accumulates separately rounded products while S S 2 < 400, fused above
+    constexpr bool FC_SEQ = S * S * 2 < 400;
     __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
     __shared__ int s_ulrel[MAX_UL_ROWS];
     // per-lane rows: fading normals (2 NC S), RBG SINR in dB (S); several cells: rows S .. S + NC S hold each lane's
@@ -475,6 +478,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     float kf = 0.f;
     int kg = 0;
     if (kl && act) { kf = ldo(st.k_from, o_r); kg = ldo(st.k_g0, o_r); }
+    int fci = 0;                                       // per-link delay spreads: the grid index in use
+    if (fc2 && act) fci = ldo(st.fc_idx, o_r);
     float lnp = 0.f;                                   // PRBs of the last PUSCH (ul_amc_alloc "previous")
     if (!DL && pm.amc_prev && act) lnp = ldo(st.last_nprb, o_r);
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
@@ -522,7 +527,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // log of the held PRB count by count of held RBGs, when every RBG has the same width: the log-sum-exp over the
     // held RBGs then adds exp(0) = 1 once per RBG, so it depends only on that count (s_lnw[n])
     if (lane <= S) s_lnw[lane] = lse_logw<S>(s_logw, lane >= 32 ? ~0u : ((1u << lane) - 1u));
-    if (fc)
+    if (fc && !fc2)
         for (int i = lane; i < S * S; i += blockDim.x) s_fcl[i] = pm.fc_L[i];
     bool lw_eq = true;
 #pragma unroll
@@ -680,6 +685,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     };
     // NRNet.set_los with this step's LOS state (target k_los where LOS, else 0; an env's first state since its reset
     // applies at once), then _rician_update at g0 (a changed target starts a ramp from the K of slot g0 - 1)
+    // NRNet.set_los for the delay spread (nr_engine.py:377-381): the link's LOS or NLOS grid index
+    if (fc2 && los_rep && act) fci = los_now ? ldo(st.fc_idl, o_r) : ldo(st.fc_idn, o_r);
+    fci = fci < 0 ? 0 : (fci < pm.fc_G ? fci : pm.fc_G - 1);
     if (kl && los_rep) {
         const float kt = (act && los_now) ? ldo(st.k_los, o_r) : 0.f;
         if (act && st.k_fresh[ee] != 0) { kk = kt; kf = kt; }
@@ -855,7 +863,26 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             }
             INET_PH(1);                            // fading innovations (the robots' own updates follow)
             __syncthreads();
-            if (draw && fc) {
+            if (draw && fc2) {
+                // per-link delay spreads: L = fc_tab[the link's grid index] (nr_engine.py:365-368), read from global
+                // memory (the table is a few KB, cached); the reference's batched product accumulates separately
+                // rounded products while S S 2 < 400 and fused ones above
+                uint32_t lo0 = (uint32_t)fci * (uint32_t)(S * S * 4);         // byte offset of the link's L
+                asm volatile("" : "+v"(lo0));          // (recomputed here: no per-row offsets kept across the slots)
+#pragma unroll
+                for (int i = 0; i < S; ++i) {
+                    float ar = 0.f, ai = 0.f;
+#pragma unroll 1
+                    for (int j = 0; j <= i; ++j) {
+                        const float l = ldo(pm.fc_tab, lo0 + (uint32_t)((i * S + j) * 4));
+                        const float zr = s_z[(2 * j) * CW + lane], zi = s_z[(2 * j + 1) * CW + lane];
+                        if constexpr (FC_SEQ) { ar = ar + l * zr; ai = ai + l * zi; }
+                        else { ar = fmaf(l, zr, ar); ai = fmaf(l, zi, ai); }
+                    }
+                    hr[i] = row.rho * hr[i] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
+                    hi[i] = row.rho * hi[i] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
+                }
+            } else if (draw && fc) {
                 // z <- L z over the subbands of every link (L lower-triangular; the products accumulated with fused
                 // multiply-adds in subband order, as a float32 matrix product), then the AR(1) step
                 // (the draws are read from LDS term by term: no register copy of the S draws of a link)
@@ -1853,6 +1880,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
             if (pm.amc_prev) sto(st.last_nprb, o_r, lnp);
             if (kl) { sto(st.k_lin, o_r, kk); sto(st.k_from, o_r, kf); sto(st.k_g0, o_r, kg); }
+            if (fc2) sto(st.fc_idx, o_r, fci);
         }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
         if (arr.counts || rebased) sto(lk.enq, o_r, enq);

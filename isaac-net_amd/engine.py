@@ -21,7 +21,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .channels import RICIAN_K_DB, scenario_name, subband_fading_sqrt, sum_of_cosines_cdf_table
+from .channels import (RICIAN_K_DB, delay_spread_grid, lg_ds_params, scenario_name, subband_fading_sqrt,
+                       sum_of_cosines_cdf_table)
 from .config import NRConfig
 from .phy import PhyTables, cqi_tables
 
@@ -96,8 +97,10 @@ def refusals(cfg: NRConfig):
     no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
        "the per-RBG PF update of the pf scheduler")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
-    no(cfg.freq_corr_mode == "los", "frequency-correlated fading with per-link delay spreads from the LOS state "
-       "(fading_delay_spread_ns=None)", "one fixed delay spread (fading_delay_spread_ns)")
+    no(cfg.freq_corr_mode == "los" and (mc or cfg.channel != "tr38901" or
+                                        scenario_name(cfg.tr38901_scenario) not in ("UMi", "UMa", "InH")),
+       "per-link delay spreads (fading_delay_spread_ns=None) with several cells, outside TR 38.901 or on RMa / InF",
+       "per-link delay spreads at one cell on UMi, UMa and InH, or one fixed delay spread")
     no(cfg.fading_doppler != "global", "per-robot Doppler fading", "one rho")
     no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
     no(cfg.rach or cfg.drx, "RACH / DRX access", "always connected")
@@ -214,6 +217,7 @@ class HipNREngine:
             "spec_re": z(E, R, dt=f32), "spec_im": z(E, R, dt=f32), "k_lin": z(E, R, dt=f32),
             "k_los": z(E, R, dt=f32),                  # the LOS K draw (Rician K from the LOS state)
             "k_from": z(E, R, dt=f32), "k_g0": z(E, R), "k_fresh": z(E),   # its ramp start, slot and fresh envs
+            "fc_idx": z(E, R), "fc_idl": z(E, R), "fc_idn": z(E, R),   # per-link delay spreads: grid indices
             "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
             "ctr_submit": z(E), "epoch": z(E),
             "field": z(E, self.C, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
@@ -352,6 +356,16 @@ class HipNREngine:
         self._fc_L = None if L is None else L.to(self.dev)
         p.fc_on = int(L is not None)
         p.fc_L = self._fc_L.data_ptr() if L is not None else None
+        if cfg.freq_corr_mode == "los":    # per-link delay spreads: L on the log grid, lgDS per state (:330-340)
+            _, tab = delay_spread_grid(cfg)
+            self._fc_tab = tab.to(self.dev).contiguous()
+            lo, hi, G = cfg.fading_ds_grid
+            scn = scenario_name(cfg.tr38901_scenario)
+            p.fc_on, p.fc_G, p.fc_tab = 2, int(G), self._fc_tab.data_ptr()
+            (p.ds_mu_n, p.ds_sig_n), (p.ds_mu_l, p.ds_sig_l) = (lg_ds_params(scn, cfg.carrier_ghz, los)
+                                                                for los in (False, True))
+            p.ds_c1 = math.log10(lo)
+            p.ds_c2 = (int(G) - 1) / (math.log10(hi) - math.log10(lo))
         p.pc_p0, p.pc_alpha = cfg.ul_pc_p0_dbm, cfg.ul_pc_alpha
         p.target, p.phr_min, p.snr_ref_prbs = cfg.bler_target, cfg.phr_min_db, float(cfg.snr_ref_prbs)
         p.w0 = float(cfg.subband_prbs[0])
@@ -1066,6 +1080,9 @@ class HipNREngine:
             else:
                 out.update({"net.k_los": k, "net.k_from": k,
                             "net.k_g0": torch.zeros_like(L(st["epoch"]))[:, None].expand(-1, self.R)})
+        if cfg.freq_corr_mode == "los":
+            out.update({"net.fc_idx": L(st["fc_idx"]), "net.fc_idx_los": L(st["fc_idl"]),
+                        "net.fc_idx_nlos": L(st["fc_idn"])})
         return out
 
     def _link_load(self, pre, st, sd):
@@ -1154,6 +1171,13 @@ class HipNREngine:
                 st["k_g0"].copy_(I(g("net.k_g0")))
                 fr = sd.get("net.k_fresh")
                 st["k_fresh"].copy_(I(torch.as_tensor(fr).to(self.dev)) if fr is not None else 0)
+        if cfg.freq_corr_mode == "los":
+            G = int(cfg.fading_ds_grid[2])
+            for n, k in (("fc_idx", "net.fc_idx"), ("fc_idl", "net.fc_idx_los"), ("fc_idn", "net.fc_idx_nlos")):
+                v = g(k)
+                if bool(((v < 0) | (v >= G)).any()):
+                    raise ValueError(f"{k}: grid indices outside [0, {G})")
+                st[n].copy_(I(v))
         self._last_snr = g("eng._last_snr").float().clone()
         self._last_hid = g("eng._last_hid").long().clone()
         if T is not None:
@@ -1221,7 +1245,7 @@ class HipNREngine:
                 "net.ul.sched_ok", "net.ioN[dl]", "net.ni_dl", "net.ul.sb_prb", "net.dl.sb_prb", "net.ul.q.f_nact",
                 "net.ul.q.f_snr", "net.ul.q.f_own", "net.dl.q.f_nact", "net.dl.q.f_snr", "net.dl.q.f_own",
                 "net.dl.q.det", "net.dl.q.hid", "net.dl_newest",
-                "net.fc_L"}       # (the subband correlation's square root, derived from the config)
+                "net.fc_L", "net.fc_tab", "net.fc_grid_ns"}   # (the subband correlations' square roots: config)
     # Reference host values that switch on what this engine does not run (traffic models, access procedures, hooks
     # and traces, frequency-correlated or per-robot fading, blockage, O2I, radio link failure, TPC, BSR grants,
     # MIMO, QoS): a checkpoint holding another value was written with that feature on. (_lena_mac, the LENA grant

@@ -464,15 +464,17 @@ class Radio:
 
 
 # ------------------------------------------------------------------------------------------ the engine
-def fcorr_sqrt(cfg):
+def fcorr_sqrt(cfg, tau_ns=None):
     """L [S,S] float32 with L L^T the subband correlation of the fading innovations for the fixed delay spread
     (nr_engine.py:125-168, _init_fcorr 320-330): subband centres (cumulated RBG widths less half a width), the
     correlation 1 / sqrt(1 + (2 pi df tau)^2), its Cholesky factor (diagonal jitter while it fails) with unit-norm
-    rows, in float64, then float32."""
+    rows, in float64, then float32. tau_ns [G] (float64): the batch [G,S,S] of those delay spreads, one jitter for
+    the whole batch."""
     w = torch.tensor([float(x) for x in cfg.subband_prbs], dtype=torch.float64) * (12 * cfg.scs_khz * 1e3)
     f = torch.cumsum(w, 0) - w / 2
     df = f[:, None] - f[None, :]
-    x = 2 * math.pi * df * torch.as_tensor(cfg.fading_delay_spread_ns * 1e-9, dtype=torch.float64)[..., None, None]
+    tau = cfg.fading_delay_spread_ns if tau_ns is None else tau_ns
+    x = 2 * math.pi * df * torch.as_tensor(tau * 1e-9, dtype=torch.float64)[..., None, None]
     c = 1.0 / torch.sqrt(1.0 + x * x)
     eye = torch.eye(c.shape[-1], dtype=c.dtype)
     for eps in (0.0, 1e-12, 1e-10, 1e-8, 1e-6):
@@ -480,6 +482,23 @@ def fcorr_sqrt(cfg):
         if not bool((info != 0).any()):
             return (L / L.norm(dim=-1, keepdim=True)).float().contiguous()
     raise ValueError("subband correlation matrix is not positive definite")
+
+
+def lg_ds(cfg, los):
+    """(mu, sigma) of lgDS = log10(DS / 1 s) for the scenario in the LOS or NLOS state at the carrier
+    (nr_engine.py:92-113, TR 38.901 Table 7.5-6; UMi, UMa, InH)."""
+    from isaac_net_amd.channels import scenario_name
+    sc, fc = scenario_name(cfg.tr38901_scenario), cfg.carrier_ghz
+    lg = math.log10
+    if sc == "UMi":
+        return (-0.24 * lg(1 + max(fc, 2.0)) - 7.14, 0.38) if los else \
+            (-0.24 * lg(1 + max(fc, 2.0)) - 6.83, 0.16 * lg(1 + max(fc, 2.0)) + 0.28)
+    if sc == "UMa":
+        return (-6.955 - 0.0963 * lg(max(fc, 6.0)), 0.66) if los else (-6.28 - 0.204 * lg(max(fc, 6.0)), 0.39)
+    if sc == "InH":
+        return (-0.01 * lg(1 + max(fc, 6.0)) - 7.692, 0.18) if los else \
+            (-0.28 * lg(1 + max(fc, 6.0)) - 7.173, 0.10 * lg(1 + max(fc, 6.0)) + 0.055)
+    raise ValueError(sc)
 
 
 class Link:
@@ -693,7 +712,8 @@ class OracleEngine:
         assert cfg.fading_doppler == "global"
         assert cfg.rician_mode in (None, "fixed") or (cfg.rician_mode == "los" and C == 1), \
             "Rician K: fixed, or from the LOS state at one cell"
-        assert cfg.freq_corr_mode in (None, "fixed"), "frequency-correlated fading: a fixed delay spread"
+        assert cfg.freq_corr_mode in (None, "fixed") or (cfg.freq_corr_mode == "los" and C == 1), \
+            "frequency-correlated fading: a fixed delay spread, or per-link delay spreads at one cell"
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
         mt = max(cfg.max_harq_tx, 2)
@@ -702,6 +722,11 @@ class OracleEngine:
         self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
         self.w = torch.tensor(cfg.subband_prbs, dtype=torch.float32)
         self.fc_L = fcorr_sqrt(cfg) if cfg.freq_corr_mode == "fixed" else None
+        self.fc_los = cfg.freq_corr_mode == "los"
+        if self.fc_los:                  # per-link delay spreads on a log grid of L (nr_engine.py:330-333)
+            lo, hi, G = cfg.fading_ds_grid
+            self.fc_tab = fcorr_sqrt(cfg, torch.logspace(math.log10(lo), math.log10(hi), int(G), dtype=torch.float64))
+            self.fc_lgds = (lg_ds(cfg, False), lg_ds(cfg, True))
         self.olla_dn = cfg.olla_up_db * (1 - cfg.bler_target) / cfg.bler_target
         self.rng = CounterRNG(seed, E)
         self.dec = Decisions()
@@ -760,8 +785,10 @@ class OracleEngine:
         self.rng.reset_mask(mask)
         cd = self.cdim
         h0 = self.rng.reset_normal(H0 << 16, R * math.prod(cd) * S * 2).view(E, R, *cd, S, 2) / math.sqrt(2)
-        if self.fc_L is not None:                        # stationary start, correlated too (nr_engine.py:264-266)
-            h0 = self.fc_L @ h0
+        if self.fc_los:
+            self._reset_fcorr(m, mask is None)
+        if self.fc_L is not None or self.fc_los:         # stationary start, correlated too (nr_engine.py:264-266)
+            h0 = self._fc_mat() @ h0
         if mask is None:
             self.h = h0
             self.last_g = None
@@ -897,10 +924,14 @@ class OracleEngine:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
-            if self.rician == "los" and cfg.channel == "tr38901":
+            if (self.rician == "los" or self.fc_los) and cfg.channel == "tr38901":
                 # the radio's LOS state (Radio.los_state, engine.py:853-861): fixed, or the stochastic draw
-                self._set_los(self.radio.los[..., 0] if cfg.tr38901_los == "stochastic"
-                              else torch.full((self.E, self.R), cfg.tr38901_los == "los"))
+                los = self.radio.los[..., 0] if cfg.tr38901_los == "stochastic" else \
+                    torch.full((self.E, self.R), cfg.tr38901_los == "los")
+                if self.fc_los:
+                    self._set_fc_los(los)
+                if self.rician == "los":
+                    self._set_los(los)
             pgs = pg[..., None].expand(-1, -1, self.S)
             n_ul = torch.full_like(pgs, cfg.noise_dbm_per_prb("gnb"))
             ul_ref = cfg.ue_tx_dbm - 10 * math.log10(cfg.snr_ref_prbs) + pgs - n_ul
@@ -1048,11 +1079,39 @@ class OracleEngine:
         dt = 1 if self.last_g is None else g - self.last_g
         if dt > 0:
             z = self.rng.step_normal(FADING, rel, self.h[0].numel()).view(self.h.shape)
-            if self.fc_L is not None:                    # z <- L z across the subbands (nr_engine.py:366-368, 581-582)
-                z = self.fc_L @ z
+            if self.fc_L is not None or self.fc_los:     # z <- L z across the subbands (nr_engine.py:366-368, 581-582)
+                z = self._fc_mat() @ z
             rho = self.cfg.fading_rho_per_ms ** (dt * self.cfg.slot_ms)
             self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
         self.last_g = g
+
+    def _fc_mat(self):
+        """L of the fixed delay spread, or of every link's grid index [E,R,(C),S,S] (nr_engine.py:365-368)."""
+        return self.fc_L if self.fc_L is not None else self.fc_tab[self.fc_idx]
+
+    def _ds_index(self, lg):
+        """Nearest grid point in log tau of lgDS values, clamped to the grid (nr_engine.py:335-340)."""
+        lo, hi, G = self.cfg.fading_ds_grid
+        u = (lg + 9.0 - math.log10(lo)) * ((int(G) - 1) / (math.log10(hi) - math.log10(lo)))
+        return torch.round(u).clamp(0, int(G) - 1).long()
+
+    def _reset_fcorr(self, m, full):
+        """Per-link delay spreads of the reset envs (nr_engine.py:341-363): two normals per link (reset site DSPR),
+        lgDS = mu + sigma z in the NLOS and the LOS state as grid indices; the live index starts at the NLOS one."""
+        E, R, cd = self.E, self.R, self.cdim
+        z = self.rng.reset_normal(DSPR << 16, R * math.prod(cd) * 2).view(E, R, *cd, 2)
+        (mn, sn), (ml, sl) = self.fc_lgds
+        i_n, i_l = self._ds_index(mn + sn * z[..., 0]), self._ds_index(ml + sl * z[..., 1])
+        if full:
+            self.fc_idx_nlos, self.fc_idx_los, self.fc_idx = i_n, i_l, i_n.clone()
+            return
+        self.fc_idx_nlos = where_env(m, i_n, self.fc_idx_nlos)
+        self.fc_idx_los = where_env(m, i_l, self.fc_idx_los)
+        self.fc_idx = where_env(m, i_n, self.fc_idx)
+
+    def _set_fc_los(self, los):
+        """NRNet.set_los (nr_engine.py:377-381) for the delay spread: every link's LOS or NLOS grid index."""
+        self.fc_idx = torch.where(los, self.fc_idx_los, self.fc_idx_nlos)
 
     def _set_los(self, los):
         """NRNet.set_los (nr_engine.py:370-392) for the K factor: the target is the link's LOS draw where LOS, else 0;
@@ -1455,6 +1514,8 @@ class OracleEngine:
             items += [(f"{lk.dir}.{k}", lk, v) for k, v in keys.items()]
         if self.dl is not None:
             items.append(("net.dl_newest", self, "dl_newest"))
+        if self.fc_los:
+            items += [(k, self, k[4:]) for k in ("net.fc_idx", "net.fc_idx_los", "net.fc_idx_nlos")]
         if self.rician:
             items += [(k, self, v) for k, v in self.RICIAN_MAP.items()]
             if self.rician == "los":

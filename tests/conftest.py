@@ -52,11 +52,13 @@ def pytest_collection_modifyitems(config, items):
 # alone, with every other switch, and with whole-band power; fcorr / fcorr_w2: frequency-correlated fading (fixed delay
 # spread), 13 RBGs and 8 RBGs on two-wavefront envs; rice_los / rice_snr: Rician K from the LOS state (poses: the
 # link's LOS draw; SNR input: no LOS state, K = 0); los_sto (and _dl, _mc): the TR 38.901 stochastic LOS state;
-# rice_sto (and _dl, _slow): Rician K from the stochastic LOS state, ramps of 4, 0 and 50 slots
+# rice_sto (and _dl, _slow): Rician K from the stochastic LOS state, ramps of 4, 0 and 50 slots; fcorr_los (and _dl,
+# _rice): per-link delay spreads from the LOS state (13, 14 and 18 RBGs)
 CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14", "s18_ir", "s10_w2", "lena_pf",
          "wb_pc", "pc1", "w4", "tdma", "amc_prev", "lena_v2", "wb_amc", "fcorr", "fcorr_w2",
-         "rice_los", "rice_snr", "los_sto", "rice_sto", "rice_sto_slow"]
+         "rice_los", "rice_snr", "los_sto", "rice_sto", "rice_sto_slow",
+         "fcorr_los", "fcorr_los_rice"]
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl", "fcorr_dl", "rice_los_dl", "los_sto_dl",
-            "rice_sto_dl"]
+            "rice_sto_dl", "fcorr_los_dl"]
 MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc"]   # several cells (NRConfig(n_cells=3 / 2)), uplink

@@ -308,6 +308,29 @@ CASES = {
                                    tr38901_scenario="UMa", tr38901_los="stochastic",
                                    cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
                           E=3, R=16, steps=30, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={17: [0]}),
+    # frequency-correlated fading with per-link delay spreads (fading_delay_spread_ns None, the reference's default
+    # with fading_freq_corr): a TR 38.901 lgDS draw per link and LOS state on the log grid of fading_ds_grid, the LOS
+    # or NLOS one by the radio's state (nr_engine.py:320-381): UMi with the stochastic LOS state and fast motion
+    "fcorr_los": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                               max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_rho_per_ms=0.5,
+                               fading_freq_corr=True, channel="tr38901", tr38901_scenario="UMi",
+                               tr38901_los="stochastic", cell_positions_m=((150.0, 150.0),), gnb_height_m=10.0),
+                      E=3, R=16, steps=30, kind="pose", arena=300.0, walk=4.0, rates=(0.8, 0.5), resets={14: [1]}),
+    # InH in a fixed LOS state with the downlink, 106 PRB (14 RBGs), a grid of 8 points
+    "fcorr_los_dl": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                  n_harq=4, max_harq_tx=3, frame_buffer=8, msg_sizes=(2000.0,), fading_rho_per_ms=0.5,
+                                  fading_freq_corr=True, fading_ds_grid=(5.0, 500.0, 8), channel="tr38901",
+                                  tr38901_scenario="InH", tr38901_los="los", cell_positions_m=((30.0, 30.0),),
+                                  gnb_height_m=3.0, dl=True),
+                         E=3, R=8, steps=25, kind="pose", arena=60.0, walk=2.0, rates=(0.8,), dl_sizes=(4000.0,),
+                         dl_rates=(0.6,), resets={11: [2]}),
+    # UMa with Rician K and the delay spread both from the stochastic LOS state, 273 PRB (18 RBGs)
+    "fcorr_los_rice": dict(cfg=dict(mu=1, n_prb=273, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                    n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(3000.0,),
+                                    fading_rho_per_ms=0.3, fading_freq_corr=True, fading_rician=True,
+                                    channel="tr38901", tr38901_scenario="UMa", tr38901_los="stochastic",
+                                    cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
+                           E=3, R=16, steps=25, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={12: [0]}),
 }
 
 

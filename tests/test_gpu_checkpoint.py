@@ -29,7 +29,7 @@ def reference_checkpoint(name):
 
 
 @pytest.mark.parametrize("name", ["c2", "dl_c2", "mc3_ho", "lena_v2", "fcorr", "rice_los",
-                                  "rice_sto_slow"])
+                                  "rice_sto_slow", "fcorr_los"])
 def test_reference_checkpoint_resumes_bit_exact(name):
     print(f"reference checkpoint of {name}", flush=True)
     ref, cfgd, kind = load(name)
