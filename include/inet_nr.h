@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 13
+#define INET_NR_ABI_VERSION 14
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -77,7 +77,8 @@ typedef struct InetNrState {
     int32_t *q_cap, *q_start, *q_end, *q_fin;
     uint32_t *q_meta;
     int32_t *q_hid;
-    /* Rician specular phasor and K (linear) per robot [E][R] (rician_k_db mode) */
+    /* Rician specular phasor and K (linear) per robot-cell link [E][C][R] (C = n_cells, 1 with one cell; several
+       cells since ABI 14) */
     float *spec_re, *spec_im, *k_lin;
     /* counter RNG per env [E]: env id (global), episode, step and submit call counters */
     int32_t *env_id, *episode, *ctr_step, *ctr_submit;
@@ -103,11 +104,10 @@ typedef struct InetNrState {
     /* per robot [E][R] float: PRBs of the robot's last PUSCH (UlMac.last_nprb, mac_ul.py:51, mac.py:484), read and
        written only with params.amc_prev (ABI version 8) */
     float *last_nprb;
-    /* per robot [E][R] float: the LOS K draw of Rician fading with K from the LOS state (NRNet.k_los,
-       nr_engine.py:300-303), written by inet_nr_reset with params.k_from_los (ABI version 10); the K the step uses
-       is k_lin, which the caller sets to k_los once the link is reported LOS (NRNet.set_los) */
+    /* per link [E][C][R] float: the LOS K draw of Rician fading with K from the LOS state (NRNet.k_los,
+       nr_engine.py:300-303), written by inet_nr_reset with params.k_from_los (ABI version 10) */
     float *k_los;
-    /* Rician K from the LOS state, the ramp (nr_engine.py:402-419; ABI 12): per robot [E][R] the ramp start k_from and
+    /* Rician K from the LOS state, the ramp (nr_engine.py:402-419; ABI 12): per link [E][C][R] the ramp start k_from and
        its slot k_g0 (k_lin is the target), per env [E] k_fresh (no LOS state seen since the reset). The step kernels
        apply NRNet.set_los with the radio's LOS state of a pose step (K target = k_los where LOS, else 0; a fresh env
        takes it at once), start a ramp of k_ramp slots where the target changed, and evaluate K in every slot. */

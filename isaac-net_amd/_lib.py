@@ -119,7 +119,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 WIFI_ABI_VERSION = 2
 _LIB = None
 

@@ -235,20 +235,25 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             }
         }
         if (pm.rician) {                                   // phi = 2 pi u (KPHI), nr_engine.py:293-299
+            // every robot-cell link c: element j = r NC + c of the per-env draws, state [E][NC][R]
             const uint32_t bk = base_key(s0, env, ep, CH_RESET, 0u, SITE_KPHI << 16);
-            float phi = (float)6.283185307179586 * uniform_bits(elem_hash(bk, (uint32_t)r));
-            st.spec_re[ir] = cosf(phi);
-            st.spec_im[ir] = sinf(phi);
-            st.k_lin[ir] = k_lin0;
-            if (pm.k_from_los) {
-                // K from the LOS state (nr_engine.py:300-303): k_los = 10^((mu_K + sigma_K z) / 10), z the link's
-                // KFAC normal (element r); K = 0 until the link is reported LOS. 10^x in double, rounded once.
-                const uint32_t bz = base_key(s0, env, ep, CH_RESET, 0u, SITE_KFAC << 16);
-                const float x = (pm.k_mu + pm.k_sigma * normal_at(bz, (uint32_t)r)) / 10.0f;
-                st.k_los[ir] = (float)exp10((double)x);
-                st.k_lin[ir] = 0.0f;
-                st.k_from[ir] = 0.0f;
-                st.k_g0[ir] = 0;
+            const uint32_t bz = base_key(s0, env, ep, CH_RESET, 0u, SITE_KFAC << 16);
+            for (int c = 0; c < NC; ++c) {
+                const uint32_t j = (uint32_t)(r * NC + c);
+                const size_t ic = ((size_t)e * NC + c) * R + r;
+                float phi = (float)6.283185307179586 * uniform_bits(elem_hash(bk, j));
+                st.spec_re[ic] = cosf(phi);
+                st.spec_im[ic] = sinf(phi);
+                st.k_lin[ic] = k_lin0;
+                if (pm.k_from_los) {
+                    // K from the LOS state (nr_engine.py:300-303): k_los = 10^((mu_K + sigma_K z) / 10), z the link's
+                    // KFAC normal; K = 0 until the link is reported LOS. 10^x in double, rounded once.
+                    const float x = (pm.k_mu + pm.k_sigma * normal_at(bz, j)) / 10.0f;
+                    st.k_los[ic] = (float)exp10((double)x);
+                    st.k_lin[ic] = 0.0f;
+                    st.k_from[ic] = 0.0f;
+                    st.k_g0[ic] = 0;
+                }
             }
         }
     }
@@ -300,8 +305,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L)) return INET_NR_EINVAL;
     if (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn))
         return INET_NR_EINVAL;
-    if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0 ||
-                         p.n_cells > 1))
+    if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0))
         return INET_NR_EINVAL;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_NR_EINVAL;
@@ -317,7 +321,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     const int fx = (gen && gen[0] == '1') ? 0 : inet::fx_profile(p);
     if (cells) {
         const InetNrCells& c = *cells;
-        if (c.C != p.n_cells || c.C > INET_NR_MAX_C || p.input_kind != 0 || p.rician || p.F > 64 || dl)
+        if (c.C != p.n_cells || c.C > INET_NR_MAX_C || p.input_kind != 0 || p.F > 64 || dl)
             return INET_NR_EINVAL;
         if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
             return INET_NR_EINVAL;
@@ -448,7 +452,7 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     if (!st || !prm || !dcorr) return INET_NR_EINVAL;
     const InetNrParams& p = *prm;
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
-    if (p.n_cells > INET_NR_MAX_C || (p.n_cells > 1 && p.rician)) return INET_NR_EINVAL;
+    if (p.n_cells > INET_NR_MAX_C) return INET_NR_EINVAL;
     if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L) ||
         (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn)))
         return INET_NR_EINVAL;

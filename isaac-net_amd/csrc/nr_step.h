@@ -471,13 +471,22 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             if constexpr (IR) { hlexp[p] = -INFINITY; hnrb[p] = 0.f; }
         }
     }
-    float sp_re = 0.f, sp_im = 0.f, kk = 0.f;
-    if (pm.rician && act) { sp_re = ldo(st.spec_re, o_r); sp_im = ldo(st.spec_im, o_r); kk = ldo(st.k_lin, o_r); }
-    // K from the LOS state (general build): kk is the target, kf the ramp start, kg its slot
+    // Rician state of every robot-cell link c ([E][NC][R]): specular phasor, K target kk, ramp start kf and slot kg
+    float sp_re[NC], sp_im[NC], kk[NC], kf[NC];
+    int kg[NC];
+    auto o_rc = [&](int c) -> uint32_t { return (uint32_t)((ee * NC + c) * R + rr0) * 4u; };
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        sp_re[c] = 0.f; sp_im[c] = 0.f; kk[c] = 0.f; kf[c] = 0.f; kg[c] = 0;
+        if (pm.rician && act) {
+            sp_re[c] = ldo(st.spec_re, o_rc(c)); sp_im[c] = ldo(st.spec_im, o_rc(c)); kk[c] = ldo(st.k_lin, o_rc(c));
+        }
+    }
+    // K from the LOS state (general build)
     const bool kl = FX == 0 && pm.k_from_los != 0;
-    float kf = 0.f;
-    int kg = 0;
-    if (kl && act) { kf = ldo(st.k_from, o_r); kg = ldo(st.k_g0, o_r); }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        if (kl && act) { kf[c] = ldo(st.k_from, o_rc(c)); kg[c] = ldo(st.k_g0, o_rc(c)); }
     int fci = 0;                                       // per-link delay spreads: the grid index in use
     if (fc2 && act) fci = ldo(st.fc_idx, o_r);
     float lnp = 0.f;                                   // PRBs of the last PUSCH (ul_amc_alloc "previous")
@@ -588,6 +597,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // the stochastic LOS state of TR 38.901 (general build only)
     const StoLos sto_los{pm.los_cdf, pm.plos_scn, pm.sig_nlos, FX == 0 && pm.los_sto != 0};
     bool los_now = false, los_rep = false;         // this step's LOS state of the link (TR 38.901 with poses)
+    bool los_c[NC];                                // several cells: that of every robot-cell link
+#pragma unroll
+    for (int c = 0; c < NC; ++c) los_c[c] = false;
     if constexpr (MC) {
         // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
         float px = 0.f, py = 0.f;
@@ -595,8 +607,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
-            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los) - pm.ue_tx;
+            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los, &los_c[c]) -
+                     pm.ue_tx;
         }
+        los_rep = pm.radio_model == 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) ref[s] = 0.f;
     } else if constexpr (VREF) {
@@ -679,9 +693,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 
     // ---------------- Rician K of the link (nr_engine.py:370-419, 602-611) ----------------
     // K of slot g on the ramp: the target once k_ramp slots have begun since kg, else k_from + (target - k_from) n / k_ramp
-    auto k_at = [&](int g) -> float {
-        const int n = g - kg + 1;
-        return n >= pm.k_ramp ? kk : kf + (kk - kf) * ((float)n * pm.k_rinv);
+    auto k_at = [&](int c, int g) -> float {
+        const int n = g - kg[c] + 1;
+        return n >= pm.k_ramp ? kk[c] : kf[c] + (kk[c] - kf[c]) * ((float)n * pm.k_rinv);
     };
     // NRNet.set_los with this step's LOS state (target k_los where LOS, else 0; an env's first state since its reset
     // applies at once), then _rician_update at g0 (a changed target starts a ramp from the K of slot g0 - 1)
@@ -689,19 +703,25 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     if (fc2 && los_rep && act) fci = los_now ? ldo(st.fc_idl, o_r) : ldo(st.fc_idn, o_r);
     fci = fci < 0 ? 0 : (fci < pm.fc_G ? fci : pm.fc_G - 1);
     if (kl && los_rep) {
-        const float kt = (act && los_now) ? ldo(st.k_los, o_r) : 0.f;
-        if (act && st.k_fresh[ee] != 0) { kk = kt; kf = kt; }
-        else if (pm.k_ramp == 0) kk = kt;
-        else if (kt != kk) { kf = k_at(g0 - 1); kg = g0; kk = kt; }
+        const bool fresh = act && st.k_fresh[ee] != 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const bool lc = MC ? los_c[c] : los_now;
+            const float kt = (act && lc) ? ldo(st.k_los, o_rc(c)) : 0.f;
+            if (fresh) { kk[c] = kt; kf[c] = kt; }
+            else if (pm.k_ramp == 0) kk[c] = kt;
+            else if (kt != kk[c]) { kf[c] = k_at(c, g0 - 1); kg[c] = g0; kk[c] = kt; }
+        }
     }
     // gain coefficients inv = 1 / (K + 1), sqrt(K inv), sqrt(inv); while a ramp runs, set again in every slot
-    float ka = 0.f, kb = 1.f;
-    auto set_k = [&](float k) {
+    float ka[NC], kb[NC];
+    auto set_k = [&](int c, float k) {
         const float kinv = 1.0f / (k + 1.0f);
-        ka = sqrtf(k * kinv);
-        kb = sqrtf(kinv);
+        ka[c] = sqrtf(k * kinv);
+        kb[c] = sqrtf(kinv);
     };
-    set_k(kk);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) set_k(c, kk[c]);
     const bool k_ramps = kl && pm.k_ramp > 0;
 
     // ---------------- several cells: association and the A3 plan of this step (CellAssociation, radio.py:410-437) ----
@@ -801,7 +821,10 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     for (int k = 0; k < n_rows; ++k) {
         const InetNrRow row = rows[k];
         const int g = g0 + row.rel;
-        if (k_ramps) set_k(k_at(g));
+        if (k_ramps) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) set_k(c, k_at(c, g));
+        }
         if constexpr (MC) {                        // A3 handovers due by this slot (nr_engine.py:740-754)
             if (act && !fired && k_ho >= 0 && k_ho <= row.rel) handover(g0 + k_ho);
         }
@@ -913,19 +936,27 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         // fading gain (dB) of subband s of the serving link in this slot (nr_engine.py:602-611; several cells: the
         // serving cell's, pick(gain_c, serv)), and of link (c, s) (gain_cs)
         // (the powers are finite and clamped to at least 1e-6, where log10_pos is log10f)
+        // power of link q = c S + s: |sqrt(K inv) e^{j phi} + sqrt(inv) h|^2 with Rician fading, else |h|^2
+        auto power_cs = [&](int q, bool rician) -> float {
+            const int c = q / S;
+            if (rician) {
+                const float xr = ka[c] * sp_re[c] + kb[c] * hr[q];
+                const float xi = ka[c] * sp_im[c] + kb[c] * hi[q];
+                return xr * xr + xi * xi;
+            }
+            return hr[q] * hr[q] + hi[q] * hi[q];
+        };
         auto power_of = [&](int s, bool rician) -> float {
             if constexpr (MC) {
-                float p = hr[s] * hr[s] + hi[s] * hi[s];
+                float p = power_cs(s, rician);
 #pragma unroll
                 for (int c = 1; c < NC; ++c) {
-                    const float pc_ = hr[c * S + s] * hr[c * S + s] + hi[c * S + s] * hi[c * S + s];
+                    const float pc_ = power_cs(c * S + s, rician);
                     p = serv == c ? pc_ : p;
                 }
                 return p;
             } else if (rician) {
-                const float xr = ka * sp_re + kb * hr[s];
-                const float xi = ka * sp_im + kb * hi[s];
-                return xr * xr + xi * xi;
+                return power_cs(s, true);
             } else {
                 return hr[s] * hr[s] + hi[s] * hi[s];
             }
@@ -938,7 +969,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             if (!pm.fading) {
 #pragma unroll
                 for (int s = 0; s < S; ++s) gv[s] = 0.0f;
-            } else if (!MC && pm.rician) {
+            } else if (pm.rician) {
 #pragma unroll
                 for (int s = 0; s < S; ++s) gv[s] = 10.0f * log10_pos(clamp_min(power_of(s, true), 1e-6f));
             } else {
@@ -947,7 +978,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             }
         };
         auto gain_cs = [&](int q) -> float {
-            return pm.fading ? 10.0f * log10_pos(clamp_min(hr[q] * hr[q] + hi[q] * hi[q], 1e-6f)) : 0.0f;
+            return pm.fading ? 10.0f * log10_pos(clamp_min(power_cs(q, pm.rician), 1e-6f)) : 0.0f;
         };
         if constexpr (DL) {
             if (row.flags & 1) {                   // CQI report (DlMac.cqi_report, mac_dl.py:30-40)
@@ -1879,7 +1910,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         if constexpr (!DL) {
             sto(st.bsr, o_r, bsr); sto(st.sr_t, o_r, sr_t);
             if (pm.amc_prev) sto(st.last_nprb, o_r, lnp);
-            if (kl) { sto(st.k_lin, o_r, kk); sto(st.k_from, o_r, kf); sto(st.k_g0, o_r, kg); }
+            if (kl) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const uint32_t oc = (uint32_t)((ee * NC + c) * R + rr0) * 4u;
+                    sto(st.k_lin, oc, kk[c]); sto(st.k_from, oc, kf[c]); sto(st.k_g0, oc, kg[c]);
+                }
+            }
             if (fc2) sto(st.fc_idx, o_r, fci);
         }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);

@@ -85,7 +85,6 @@ def refusals(cfg: NRConfig):
        "one to three cells per env in this build (the fading of every robot-cell link is held in registers)")
     no(mc and cfg.dl, "the downlink with several cells", "the multi-cell step runs the uplink")
     no(cfg.rlf, "radio link failure (rlf=True)", "A3 handover without RLF")
-    no(mc and cfg.rician_mode is not None, "Rician fading with several cells", "Rayleigh fading on every link")
     no(mc and cfg.frame_buffer > 64, "frame_buffer > 64 with several cells", "a 64-bit handover loss mask")
     no(not cfg.ul, "ul=False (a downlink-only engine)", "the UL link runs every step")
     no(cfg.dl and cfg.duplex != "tdd", "the FDD downlink carrier", "TDD (one carrier)")
@@ -214,9 +213,11 @@ class HipNREngine:
             "h_comb": z(E, P, R, dt=f32), "h_lexp": z(E, P, R, dt=f32, v=-math.inf), "h_nrb": z(E, P, R, dt=f32),
             "q_cap": z(E, F, R, v=-1), "q_start": z(E, F, R), "q_end": z(E, F, R), "q_fin": z(E, F, R, v=BIG_SLOT),
             "q_meta": z(E, F, R), "q_hid": z(E, F, R),
-            "spec_re": z(E, R, dt=f32), "spec_im": z(E, R, dt=f32), "k_lin": z(E, R, dt=f32),
-            "k_los": z(E, R, dt=f32),                  # the LOS K draw (Rician K from the LOS state)
-            "k_from": z(E, R, dt=f32), "k_g0": z(E, R), "k_fresh": z(E),   # its ramp start, slot and fresh envs
+            # Rician state per robot-cell link [E][C][R]: phasor, K target, the LOS K draw (K from the LOS state),
+            # its ramp start and slot; per env: waiting for the first LOS state
+            "spec_re": z(E, self.C, R, dt=f32), "spec_im": z(E, self.C, R, dt=f32), "k_lin": z(E, self.C, R, dt=f32),
+            "k_los": z(E, self.C, R, dt=f32), "k_from": z(E, self.C, R, dt=f32), "k_g0": z(E, self.C, R),
+            "k_fresh": z(E),
             "fc_idx": z(E, R), "fc_idl": z(E, R), "fc_idn": z(E, R),   # per-link delay spreads: grid indices
             "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
             "ctr_submit": z(E), "epoch": z(E),
@@ -1072,14 +1073,15 @@ class HipNREngine:
             out["net.ioN[ul]"] = c["ion"]
         if cfg.rician_mode in ("fixed", "los"):
             # (between steps the input K is the target; a fixed K never ramps: ramp start = target, k_g0 0)
-            k = st["k_lin"]
-            out.update({"net.spec": torch.stack([st["spec_re"], st["spec_im"]], -1), "net.k_in": k, "net.k_lin": k})
+            rv = (lambda x: x[:, 0]) if self.C == 1 else (lambda x: x.permute(0, 2, 1))   # [E,R] / [E,R,C]
+            k = rv(st["k_lin"])
+            out.update({"net.spec": torch.stack([rv(st["spec_re"]), rv(st["spec_im"])], -1), "net.k_in": k,
+                        "net.k_lin": k})
             if cfg.rician_mode == "los":
-                out.update({"net.k_los": st["k_los"], "net.k_from": st["k_from"], "net.k_g0": L(st["k_g0"]),
+                out.update({"net.k_los": rv(st["k_los"]), "net.k_from": rv(st["k_from"]), "net.k_g0": L(rv(st["k_g0"])),
                             "net.k_fresh": st["k_fresh"] != 0})
             else:
-                out.update({"net.k_los": k, "net.k_from": k,
-                            "net.k_g0": torch.zeros_like(L(st["epoch"]))[:, None].expand(-1, self.R)})
+                out.update({"net.k_los": k, "net.k_from": k, "net.k_g0": torch.zeros_like(L(k))})
         if cfg.freq_corr_mode == "los":
             out.update({"net.fc_idx": L(st["fc_idx"]), "net.fc_idx_los": L(st["fc_idl"]),
                         "net.fc_idx_nlos": L(st["fc_idn"])})
@@ -1162,13 +1164,14 @@ class HipNREngine:
         st["ctr_step"].copy_(I(g("rng.ctr[2]")))
         if cfg.rician_mode in ("fixed", "los"):
             sp = g("net.spec")
-            st["spec_re"].copy_(sp[..., 0])
-            st["spec_im"].copy_(sp[..., 1])
-            st["k_lin"].copy_(g("net.k_lin"))
+            lv = (lambda v: v[:, None]) if self.C == 1 else (lambda v: v.permute(0, 2, 1))   # -> [E,C,R]
+            st["spec_re"].copy_(lv(sp[..., 0]))
+            st["spec_im"].copy_(lv(sp[..., 1]))
+            st["k_lin"].copy_(lv(g("net.k_lin")))
             if cfg.rician_mode == "los":
-                st["k_los"].copy_(g("net.k_los"))
-                st["k_from"].copy_(g("net.k_from"))
-                st["k_g0"].copy_(I(g("net.k_g0")))
+                st["k_los"].copy_(lv(g("net.k_los")))
+                st["k_from"].copy_(lv(g("net.k_from")))
+                st["k_g0"].copy_(lv(I(g("net.k_g0"))))
                 fr = sd.get("net.k_fresh")
                 st["k_fresh"].copy_(I(torch.as_tensor(fr).to(self.dev)) if fr is not None else 0)
         if cfg.freq_corr_mode == "los":

@@ -710,8 +710,7 @@ class OracleEngine:
         assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
         assert not cfg.ul_tpc
         assert cfg.fading_doppler == "global"
-        assert cfg.rician_mode in (None, "fixed") or (cfg.rician_mode == "los" and C == 1), \
-            "Rician K: fixed, or from the LOS state at one cell"
+        assert cfg.rician_mode in (None, "fixed", "los")
         assert cfg.freq_corr_mode in (None, "fixed") or (cfg.freq_corr_mode == "los" and C == 1), \
             "frequency-correlated fading: a fixed delay spread, or per-link delay spreads at one cell"
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
@@ -918,7 +917,11 @@ class OracleEngine:
             assert snr_db is None and x is not None and x.dim() == 3, "several cells: pass poses [E,R,2]"
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
-            out = self._net_step_cells(T, self.radio.pathgain(x), hid)
+            pg = self.radio.pathgain(x)
+            if self.rician == "los" and cfg.channel == "tr38901":       # every robot-cell link's LOS state
+                self._set_los(self.radio.los if cfg.tr38901_los == "stochastic" else
+                              torch.full((self.E, self.R, self.C), cfg.tr38901_los == "los"))
+            out = self._net_step_cells(T, pg, hid)
             snr = self.serving_sinr_db()
         elif snr_db is None and x is not None and x.dim() == 3:
             if self.radio is None:
@@ -1005,15 +1008,15 @@ class OracleEngine:
         k_ho, tgt = asc.plan(rx, self.dec)
         g_ho = g0 + k_ho
         fired = torch.zeros(self.E, self.R, dtype=torch.bool)
-        if self.rician:
-            self.k_lin = self.k_in
+        if self.rician:                                  # (nr_engine.py:740-741, 752)
+            self._rician_update(g0)
         for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
             g = g0 + rel
             ho = (k_ho >= 0) & (k_ho <= rel) & ~fired
             self._handover(ho, tgt, g_ho)
             fired = fired | ho
             self._evolve(g, rel)
-            gain_c = self._gain()
+            gain_c = self._gain(g)
             self._gain_c = gain_c
             serv = asc.serv
             gain = pick(gain_c, serv)
@@ -1117,7 +1120,7 @@ class OracleEngine:
         """NRNet.set_los (nr_engine.py:370-392) for the K factor: the target is the link's LOS draw where LOS, else 0;
         right after a reset it applies at once."""
         k = torch.where(los, self.k_los, torch.zeros_like(self.k_los))
-        fr = self.k_fresh[:, None]
+        fr = self.k_fresh.view(-1, *([1] * (k.dim() - 1)))
         self.k_in = k
         self.k_lin = torch.where(fr, k, self.k_lin)
         self.k_from = torch.where(fr, k, self.k_from)

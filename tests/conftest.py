@@ -61,4 +61,5 @@ CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl", "fcorr_dl", "rice_los_dl", "los_sto_dl",
             "rice_sto_dl", "fcorr_los_dl"]
-MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc"]   # several cells (NRConfig(n_cells=3 / 2)), uplink
+MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc", "mc2_rice",
+            "mc3_rice_sto"]   # several cells (NRConfig(n_cells=3 / 2)), uplink

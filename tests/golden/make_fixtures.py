@@ -308,6 +308,20 @@ CASES = {
                                    tr38901_scenario="UMa", tr38901_los="stochastic",
                                    cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
                           E=3, R=16, steps=30, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={17: [0]}),
+    # Rician fading on every robot-cell link (nr_engine.py:282-319, 602-611, 740-752): two cells with a fixed K of
+    # 6 dB, UMi LOS; three cells with K from the stochastic LOS state of each link (4-slot ramp), UMa
+    "mc2_rice": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                              max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2, cell_layout="hex",
+                              cell_isd_m=150.0, noise_model="thermal", channel="tr38901", tr38901_scenario="UMi",
+                              tr38901_los="los", gnb_height_m=10.0, fading_rho_per_ms=0.5, fading_rician=True,
+                              rician_k_db=6.0),
+                     E=2, R=16, steps=25, kind="pose", arena=250.0, walk=3.0, rates=(0.7,), resets={12: [1]}),
+    "mc3_rice_sto": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                  n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3,
+                                  cell_layout="hex", cell_isd_m=200.0, noise_model="thermal", channel="tr38901",
+                                  tr38901_scenario="UMa", tr38901_los="stochastic", gnb_height_m=25.0,
+                                  fading_rho_per_ms=0.5, fading_rician=True, rician_k_ramp_slots=30),
+                         E=2, R=16, steps=25, kind="pose", arena=300.0, walk=5.0, rates=(0.7,), resets={12: [1]}),
     # frequency-correlated fading with per-link delay spreads (fading_delay_spread_ns None, the reference's default
     # with fading_freq_corr): a TR 38.901 lgDS draw per link and LOS state on the log grid of fading_ds_grid, the LOS
     # or NLOS one by the radio's state (nr_engine.py:320-381): UMi with the stochastic LOS state and fast motion

@@ -23,7 +23,6 @@ def test_refusals_name_each_unimplemented_feature():
     assert EN.refusals(P.NRConfig(**mc, a3_offset_db=float("inf"), harq_fail="drop", ho_rlc="flush")) == []
     for extra, word in ((dict(n_cells=7), "n_cells=7"), (dict(dl=True), "downlink with several cells"),
                         (dict(rlf=True), "radio link failure"), (dict(frame_buffer=65), "frame_buffer > 64"),
-                        (dict(fading_rician=True, rician_k_db=3.0), "Rician fading with several cells"),
                         (dict(ul_tpc=True), "TPC")):
         assert word in " ".join(f for f, _ in EN.refusals(P.NRConfig(**dict(mc, **extra)))), extra
     # one cell: the 38.214 RBG counts of the standard carriers run (106 PRB: 14 RBGs, 273: 18, 133: 17, 78: 10),
@@ -32,6 +31,7 @@ def test_refusals_name_each_unimplemented_feature():
         assert EN.refusals(P.NRConfig(mu=1, n_prb=n_prb)) == [], n_prb
     assert "subbands" in " ".join(f for f, _ in EN.refusals(P.NRConfig(mu=1, n_prb=100, rbg_size=4)))   # 25 RBGs
     assert EN.refusals(P.NRConfig(**dict(mc, n_cells=2))) == []
+    assert EN.refusals(P.NRConfig(**mc, fading_rician=True, rician_k_db=3.0)) == []    # Rician on every link
 
 
 def test_make_engine_refuses_before_building():
