@@ -711,8 +711,7 @@ class OracleEngine:
         assert not cfg.ul_tpc
         assert cfg.fading_doppler == "global"
         assert cfg.rician_mode in (None, "fixed", "los")
-        assert cfg.freq_corr_mode in (None, "fixed") or (cfg.freq_corr_mode == "los" and C == 1), \
-            "frequency-correlated fading: a fixed delay spread, or per-link delay spreads at one cell"
+        assert cfg.freq_corr_mode in (None, "fixed", "los")
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
         assert cfg.duplex == "tdd"
         mt = max(cfg.max_harq_tx, 2)
@@ -918,9 +917,13 @@ class OracleEngine:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
-            if self.rician == "los" and cfg.channel == "tr38901":       # every robot-cell link's LOS state
-                self._set_los(self.radio.los if cfg.tr38901_los == "stochastic" else
-                              torch.full((self.E, self.R, self.C), cfg.tr38901_los == "los"))
+            if (self.rician == "los" or self.fc_los) and cfg.channel == "tr38901":   # every link's LOS state
+                los = self.radio.los if cfg.tr38901_los == "stochastic" else \
+                    torch.full((self.E, self.R, self.C), cfg.tr38901_los == "los")
+                if self.fc_los:
+                    self._set_fc_los(los)
+                if self.rician == "los":
+                    self._set_los(los)
             out = self._net_step_cells(T, pg, hid)
             snr = self.serving_sinr_db()
         elif snr_db is None and x is not None and x.dim() == 3:

@@ -135,6 +135,8 @@ def test_per_link_delay_spread_and_k_from_los_refusals():
         assert EN.refusals(cfg) == [], scn
     mc = P.NRConfig(**dict(one, n_prb=106), n_cells=3, cell_layout="hex", cell_isd_m=150.0, tr38901_scenario="UMi")
     assert "per-link delay spreads" in " ".join(f for f, _ in EN.refusals(mc))
+    inf = P.NRConfig(**one, tr38901_scenario="InF-SL", tr38901_los="los")
+    assert "per-link delay spreads" in " ".join(f for f, _ in EN.refusals(inf))
     assert EN.refusals(P.NRConfig(**dict(one, n_prb=106), n_cells=3, cell_layout="hex", cell_isd_m=150.0,
                                   tr38901_scenario="UMi", fading_delay_spread_ns=300.0)) == []
 
