@@ -208,18 +208,21 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
             // float32 matrix product). Per-link delay spreads: the link's NLOS and LOS grid indices from two normals
             // of reset site DSPR (elements 2 r, 2 r + 1; nr_engine.py:341-363), L = fc_tab[NLOS index], and the
             // batched product's order: separate multiplies and adds while S S 2 < 400, fused above
+            // (several cells: every robot-cell link c has its own two normals, elements 2 (r NC + c) + {0, 1}, and
+            // its own indices, state [E][NC][R])
             const float* L = pm.fc_L;
-            bool seq = false;
-            if (pm.fc_on == 2) {
-                const uint32_t bd = base_key(s0, env, ep, CH_RESET, 0u, SITE_DSPR << 16);
-                const int idn = ds_index(pm.ds_mu_n, pm.ds_sig_n, normal_at(bd, 2u * r), pm.ds_c1, pm.ds_c2, pm.fc_G);
-                const int idl = ds_index(pm.ds_mu_l, pm.ds_sig_l, normal_at(bd, 2u * r + 1u), pm.ds_c1, pm.ds_c2,
-                                         pm.fc_G);
-                st.fc_idn[ir] = idn; st.fc_idl[ir] = idl; st.fc_idx[ir] = idn;
-                L = pm.fc_tab + (size_t)idn * S * S;
-                seq = S * S * 2 < 400;
-            }
+            const bool seq = pm.fc_on == 2 && S * S * 2 < 400;
+            const uint32_t bd = base_key(s0, env, ep, CH_RESET, 0u, SITE_DSPR << 16);
             for (int c = 0; c < NC; ++c) {
+                if (pm.fc_on == 2) {
+                    const uint32_t j = 2u * (uint32_t)(r * NC + c);
+                    const size_t ic = ((size_t)e * NC + c) * R + r;
+                    const int idn = ds_index(pm.ds_mu_n, pm.ds_sig_n, normal_at(bd, j), pm.ds_c1, pm.ds_c2, pm.fc_G);
+                    const int idl = ds_index(pm.ds_mu_l, pm.ds_sig_l, normal_at(bd, j + 1u), pm.ds_c1, pm.ds_c2,
+                                             pm.fc_G);
+                    st.fc_idn[ic] = idn; st.fc_idl[ic] = idl; st.fc_idx[ic] = idn;
+                    L = pm.fc_tab + (size_t)idn * S * S;
+                }
                 const size_t i0 = ((size_t)e * CS + c * S) * R + r;
                 for (int i = S - 1; i >= 0; --i) {
                     float ar = 0.f, ai = 0.f;
@@ -303,7 +306,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
     if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L)) return INET_NR_EINVAL;
-    if (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn))
+    if (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn))
         return INET_NR_EINVAL;
     if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0))
         return INET_NR_EINVAL;
@@ -360,9 +363,10 @@ int32_t inet_nr_abi_version(void) { return INET_NR_ABI_VERSION; }
 // "<description>; src=<sha256 of the sources the library was built from>" (build.py passes the hash; the loader
 // refuses a library whose hash is not the tree's)
 const char* inet_nr_build_info(void) {
-    return "inet_nr gfx950: step<S in {8,13}, P in {2,4,8,16}, IR, per-subband SNR>, two-wave step (R <= 128), "
-           "multi-cell step<C = 3, S in {8,13,14}, P, IR>, common-configuration step<13, 8>, DPP segment reductions, "
-           "ATen-order sums; src=" INET_SRC_HASH;
+    return "inet_nr gfx950: one-cell step<S in {8,10,11,12,13,14,16,17,18}, P in {2,4,8,16}, IR, per-subband SNR> "
+           "for envs of up to 64 robots (UL and DL), two-wave step (R <= 128, every S), four-wave step (R <= 256, "
+           "S in {8,13}), multi-cell step<C in {2,3}, S in {8,13,14}, P, IR>, common-configuration builds (FX 1, 2), "
+           "DPP segment reductions, ATen-order sums; Wi-Fi mean-field and DCF steps; src=" INET_SRC_HASH;
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,
@@ -454,7 +458,7 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     if (p.E <= 0 || p.R <= 0 || p.n_fields < 0 || p.n_fields > 3 || p.n_modes > INET_NR_MAX_KF) return INET_NR_EINVAL;
     if (p.n_cells > INET_NR_MAX_C) return INET_NR_EINVAL;
     if (p.fc_on < 0 || p.fc_on > 2 || (p.fc_on == 1 && !p.fc_L) ||
-        (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || p.n_cells > 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn)))
+        (p.fc_on == 2 && (!p.fc_tab || p.fc_G < 1 || !st->fc_idx || !st->fc_idl || !st->fc_idn)))
         return INET_NR_EINVAL;
     if (T < 0 || T > 0x7fffffff ||
         (p.k_from_los && (!st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || !p.rician)))

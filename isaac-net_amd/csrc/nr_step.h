@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "../../include/inet_nr.h"
+#include "aten_sort.h"
 #include "inet_nr_dev.h"
 
 namespace inet {
@@ -487,8 +488,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 #pragma unroll
     for (int c = 0; c < NC; ++c)
         if (kl && act) { kf[c] = ldo(st.k_from, o_rc(c)); kg[c] = ldo(st.k_g0, o_rc(c)); }
-    int fci = 0;                                       // per-link delay spreads: the grid index in use
-    if (fc2 && act) fci = ldo(st.fc_idx, o_r);
+    int fci[NC];                                       // per-link delay spreads: each link's grid index in use
+#pragma unroll
+    for (int c = 0; c < NC; ++c) fci[c] = (fc2 && act) ? ldo(st.fc_idx, o_rc(c)) : 0;
     float lnp = 0.f;                                   // PRBs of the last PUSCH (ul_amc_alloc "previous")
     if (!DL && pm.amc_prev && act) lnp = ldo(st.last_nprb, o_r);
     // ---------------- stage the per-MCS and per-RBG tables in LDS ----------------
@@ -700,8 +702,12 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // NRNet.set_los with this step's LOS state (target k_los where LOS, else 0; an env's first state since its reset
     // applies at once), then _rician_update at g0 (a changed target starts a ramp from the K of slot g0 - 1)
     // NRNet.set_los for the delay spread (nr_engine.py:377-381): the link's LOS or NLOS grid index
-    if (fc2 && los_rep && act) fci = los_now ? ldo(st.fc_idl, o_r) : ldo(st.fc_idn, o_r);
-    fci = fci < 0 ? 0 : (fci < pm.fc_G ? fci : pm.fc_G - 1);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const bool lc = MC ? los_c[c] : los_now;
+        if (fc2 && los_rep && act) fci[c] = lc ? ldo(st.fc_idl, o_rc(c)) : ldo(st.fc_idn, o_rc(c));
+        fci[c] = fci[c] < 0 ? 0 : (fci[c] < pm.fc_G ? fci[c] : pm.fc_G - 1);
+    }
     if (kl && los_rep) {
         const bool fresh = act && st.k_fresh[ee] != 0;
 #pragma unroll
@@ -890,20 +896,25 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 // per-link delay spreads: L = fc_tab[the link's grid index] (nr_engine.py:365-368), read from global
                 // memory (the table is a few KB, cached); the reference's batched product accumulates separately
                 // rounded products while S S 2 < 400 and fused ones above
-                uint32_t lo0 = (uint32_t)fci * (uint32_t)(S * S * 4);         // byte offset of the link's L
-                asm volatile("" : "+v"(lo0));          // (recomputed here: no per-row offsets kept across the slots)
 #pragma unroll
-                for (int i = 0; i < S; ++i) {
-                    float ar = 0.f, ai = 0.f;
+                for (int c = 0; c < NC; ++c) {
+                    uint32_t lo0 = (uint32_t)fci[c] * (uint32_t)(S * S * 4);   // byte offset of the link's L
+                    asm volatile("" : "+v"(lo0));      // (recomputed here: no per-row offsets kept across the slots)
+#pragma unroll
+                    for (int i = 0; i < S; ++i) {
+                        float ar = 0.f, ai = 0.f;
 #pragma unroll 1
-                    for (int j = 0; j <= i; ++j) {
-                        const float l = ldo(pm.fc_tab, lo0 + (uint32_t)((i * S + j) * 4));
-                        const float zr = s_z[(2 * j) * CW + lane], zi = s_z[(2 * j + 1) * CW + lane];
-                        if constexpr (FC_SEQ) { ar = ar + l * zr; ai = ai + l * zi; }
-                        else { ar = fmaf(l, zr, ar); ai = fmaf(l, zi, ai); }
+                        for (int j = 0; j <= i; ++j) {
+                            const float l = ldo(pm.fc_tab, lo0 + (uint32_t)((i * S + j) * 4));
+                            const float zr = s_z[(2 * (c * S + j)) * CW + lane];
+                            const float zi = s_z[(2 * (c * S + j) + 1) * CW + lane];
+                            if constexpr (FC_SEQ) { ar = ar + l * zr; ai = ai + l * zi; }
+                            else { ar = fmaf(l, zr, ar); ai = fmaf(l, zi, ai); }
+                        }
+                        const int q = c * S + i;
+                        hr[q] = row.rho * hr[q] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
+                        hi[q] = row.rho * hi[q] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
                     }
-                    hr[i] = row.rho * hr[i] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
-                    hi[i] = row.rho * hi[i] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
                 }
             } else if (draw && fc) {
                 // z <- L z over the subbands of every link (L lower-triangular; the products accumulated with fused
@@ -1188,32 +1199,80 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             c_blk += (adm && rx_nsb < S) ? 1 : 0;
             new_el = new_el && !blk;
             has_rx = adm;
-        } else if (env_any(has_rx)) {
-            int val = has_rx ? rx_nsb : 0;
-            int tot = env_sum(val);
-            if (tot > S) {
-                float mt[S];
+        } else {
+            // Ranked by the metric sum, descending (rkey = -1 for the robots that are not candidates of the
+            // scheduler), the candidates taken while their RBG counts fit. The order is torch's argsort: ATen's
+            // comparator (a NaN key first, then the larger), and for keys it holds equal the order std::sort leaves
+            // them in. Up to 16 robots that is the index order (insertion sort); above, a scheduler whose candidates
+            // hold equal keys takes the sort's own steps (aten_sort.h, rank_exact below).
+            const bool cand = has_rx;
+            bool tie = false, ranked = false;
+            float rkey = -1.0f;
+            if (env_any(has_rx)) {
+                int val = has_rx ? rx_nsb : 0;
+                int tot = env_sum(val);
+                if (tot > S) {
+                    ranked = true;
+                    float mt[S];
 #pragma unroll
-                for (int s = 0; s < S; ++s) mt[s] = metric_of(s);
-                float rkey = has_rx ? aten_sum<S>(mt) : -1.0f;
-                int cum = 0;
-                const int sb = lane & ~(rb - 1);
-                if constexpr (W > 1) {             // the env's keys and counts through LDS
-                    s_rkey[lane] = rkey;
-                    s_rval[lane] = val;
-                    __syncthreads();
-                }
+                    for (int s = 0; s < S; ++s) mt[s] = metric_of(s);
+                    rkey = has_rx ? aten_sum<S>(mt) : -1.0f;
+                    int cum = 0;
+                    const int sb = lane & ~(rb - 1);
+                    if constexpr (W > 1) {             // the env's keys and counts through LDS
+                        s_rkey[lane] = rkey;
+                        s_rval[lane] = val;
+                        __syncthreads();
+                    }
 #pragma unroll 1
-                for (int j = 0; j < rb; ++j) {
-                    float kj;
-                    int vj;
-                    if constexpr (W > 1) { kj = s_rkey[j]; vj = s_rval[j]; }
-                    else { kj = __shfl(rkey, sb + j, 64); vj = __shfl(val, sb + j, 64); }
-                    bool before = (kj > rkey) || (kj == rkey && j <= r);
-                    if constexpr (MC) before = before && __shfl(serv, sb + j, 64) == serv;
-                    cum += before ? vj : 0;
+                    for (int j = 0; j < rb; ++j) {
+                        float kj;
+                        int vj;
+                        if constexpr (W > 1) { kj = s_rkey[j]; vj = s_rval[j]; }
+                        else { kj = __shfl(rkey, sb + j, 64); vj = __shfl(val, sb + j, 64); }
+                        bool same = true;
+                        if constexpr (MC) same = __shfl(serv, sb + j, 64) == serv;
+                        const bool fwd = AtenSortDesc::comp(kj, rkey), bwd = AtenSortDesc::comp(rkey, kj);
+                        cum += (same && (fwd || (!bwd && j <= r))) ? vj : 0;
+                        tie |= same && has_rx && vj > 0 && j != r && !fwd && !bwd;
+                    }
+                    has_rx = has_rx && cum <= S;
                 }
-                has_rx = has_rx && cum <= S;
+            }
+            // rank_exact: one lane per (env, scheduler) sorts the env's keys with std::sort's steps (the reference's
+            // tensor: the keys of the scheduler's candidates, -1 elsewhere, robots 0..R-1) in LDS (rows S.. of s_x,
+            // free between the estimate and the allocation), walks the sorted order and marks the candidates whose
+            // running RBG count fits. (Wave-uniform: every env of the wavefront takes part when any env needs it.)
+            bool exact = false;
+            if constexpr (W == 1) exact = rb > 16 && __ballot(tie) != 0ull;
+            else if (ranked) exact = env_any(tie);          // (W > 1: one env per workgroup, `ranked` is uniform)
+            if (exact) {
+                const int XS = NC * 3 * rb + rb + NC * 64;   // ints per env: NC (keys, indices, counts), marks, stacks
+                int* const xs = reinterpret_cast<int*>(s_x + S * CW) + eloc * XS;
+                int* const mark = xs + NC * 3 * rb;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const bool in_c = cand && (!MC || serv == c);
+                    reinterpret_cast<float*>(xs)[c * 3 * rb + r] = in_c ? rkey : -1.0f;
+                    xs[c * 3 * rb + rb + r] = r;
+                    xs[c * 3 * rb + 2 * rb + r] = in_c ? rx_nsb : 0;
+                }
+                mark[r] = 0;
+                __syncthreads();
+                if (r < NC && e < E && ranked) {
+                    int* const kc = xs + r * 3 * rb;
+                    AtenSortDesc srt{reinterpret_cast<float*>(kc), kc + rb};
+                    srt.sort(R, mark + rb + r * 64);
+                    int run = 0;
+                    for (int i = 0; i < R; ++i) {
+                        const int j = kc[rb + i];
+                        const int v = kc[2 * rb + j];
+                        run += v;
+                        if (v > 0) mark[j] = run <= S ? 1 : 0;
+                    }
+                }
+                __syncthreads();
+                if (ranked) has_rx = cand && mark[r] != 0;
             }
         }
         INET_PH(3);                                // retransmission admission
@@ -1519,10 +1578,13 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                         if (txing && ((won >> s) & 1u)) {
                             float* const ent = s_ipair + off * (1 + 2 * NC);
                             ent[0] = __int_as_float(lane | (s << 8) | (serv << 16));
+                            // the link's complex gain whose power power_cs takes: with Rician fading the specular
+                            // phasor and the scattered part at this slot's K (ka, kb), else the fading state
 #pragma unroll
                             for (int c = 0; c < NC; ++c) {
-                                ent[1 + 2 * c] = hr[c * S + s];
-                                ent[2 + 2 * c] = hi[c * S + s];
+                                const int q = c * S + s;
+                                ent[1 + 2 * c] = pm.rician ? ka[c] * sp_re[c] + kb[c] * hr[q] : hr[q];
+                                ent[2 + 2 * c] = pm.rician ? ka[c] * sp_im[c] + kb[c] * hi[q] : hi[q];
                             }
                             ++off;
                         }
@@ -1917,7 +1979,9 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     sto(st.k_lin, oc, kk[c]); sto(st.k_from, oc, kf[c]); sto(st.k_g0, oc, kg[c]);
                 }
             }
-            if (fc2) sto(st.fc_idx, o_r, fci);
+            if (fc2)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) sto(st.fc_idx, o_rc(c), fci[c]);
         }
         sto(lk.last_tx, o_r, last_tx); sto(lk.qlen, o_r, kept); sto(lk.olla, o_r, olla); sto(lk.avg, o_r, avg);
         if (arr.counts || rebased) sto(lk.enq, o_r, enq);

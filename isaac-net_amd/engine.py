@@ -96,10 +96,10 @@ def refusals(cfg: NRConfig):
     no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
        "the per-RBG PF update of the pf scheduler")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
-    no(cfg.freq_corr_mode == "los" and (mc or cfg.channel != "tr38901" or
+    no(cfg.freq_corr_mode == "los" and (cfg.channel != "tr38901" or
                                         scenario_name(cfg.tr38901_scenario) not in ("UMi", "UMa", "InH")),
-       "per-link delay spreads (fading_delay_spread_ns=None) with several cells, outside TR 38.901 or on RMa / InF",
-       "per-link delay spreads at one cell on UMi, UMa and InH, or one fixed delay spread")
+       "per-link delay spreads (fading_delay_spread_ns=None) outside TR 38.901 or on RMa / InF",
+       "per-link delay spreads on UMi, UMa and InH, or one fixed delay spread")
     no(cfg.fading_doppler != "global", "per-robot Doppler fading", "one rho")
     no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
     no(cfg.rach or cfg.drx, "RACH / DRX access", "always connected")
@@ -218,7 +218,8 @@ class HipNREngine:
             "spec_re": z(E, self.C, R, dt=f32), "spec_im": z(E, self.C, R, dt=f32), "k_lin": z(E, self.C, R, dt=f32),
             "k_los": z(E, self.C, R, dt=f32), "k_from": z(E, self.C, R, dt=f32), "k_g0": z(E, self.C, R),
             "k_fresh": z(E),
-            "fc_idx": z(E, R), "fc_idl": z(E, R), "fc_idn": z(E, R),   # per-link delay spreads: grid indices
+            # per-link delay spreads: grid indices of every robot-cell link [E][C][R]
+            "fc_idx": z(E, self.C, R), "fc_idl": z(E, self.C, R), "fc_idn": z(E, self.C, R),
             "env_id": torch.arange(E, dtype=i32, device=d), "episode": z(E, v=-1), "ctr_step": z(E),
             "ctr_submit": z(E), "epoch": z(E),
             "field": z(E, self.C, max(nf, 1), max(cfg.shadow_modes, 1), 3, dt=f32),
@@ -1083,8 +1084,9 @@ class HipNREngine:
             else:
                 out.update({"net.k_los": k, "net.k_from": k, "net.k_g0": torch.zeros_like(L(k))})
         if cfg.freq_corr_mode == "los":
-            out.update({"net.fc_idx": L(st["fc_idx"]), "net.fc_idx_los": L(st["fc_idl"]),
-                        "net.fc_idx_nlos": L(st["fc_idn"])})
+            rv = (lambda x: x[:, 0]) if self.C == 1 else (lambda x: x.permute(0, 2, 1))   # [E,R] / [E,R,C]
+            out.update({"net.fc_idx": L(rv(st["fc_idx"])), "net.fc_idx_los": L(rv(st["fc_idl"])),
+                        "net.fc_idx_nlos": L(rv(st["fc_idn"]))})
         return out
 
     def _link_load(self, pre, st, sd):
@@ -1176,11 +1178,12 @@ class HipNREngine:
                 st["k_fresh"].copy_(I(torch.as_tensor(fr).to(self.dev)) if fr is not None else 0)
         if cfg.freq_corr_mode == "los":
             G = int(cfg.fading_ds_grid[2])
+            lv = (lambda v: v[:, None]) if self.C == 1 else (lambda v: v.permute(0, 2, 1))   # -> [E,C,R]
             for n, k in (("fc_idx", "net.fc_idx"), ("fc_idl", "net.fc_idx_los"), ("fc_idn", "net.fc_idx_nlos")):
                 v = g(k)
                 if bool(((v < 0) | (v >= G)).any()):
                     raise ValueError(f"{k}: grid indices outside [0, {G})")
-                st[n].copy_(I(v))
+                st[n].copy_(lv(I(v)))
         self._last_snr = g("eng._last_snr").float().clone()
         self._last_hid = g("eng._last_hid").long().clone()
         if T is not None:

@@ -22,13 +22,13 @@ CPU the oracle is bitwise equal to the reference path (pinned by the golden traj
 The PHY tables come from isaac_net_amd.phy (pinned separately against the reference's processed tables).
 
 Parity status of each part: every function here is pinned by the golden trajectories (bitwise, state, outputs and
-counters after every step of eighteen uplink scenarios (among them 10, 14 and 18 RBGs, envs of 128 and 200 robots,
-the 5G-LENA MAC switches: the per-RBG and frozen PF average, TDMA retransmissions, AMC on the previous PUSCH's PRBs,
-whole-band UL power and UL power control at one cell), five downlink and five multi-cell scenarios with two and three
-cells) except what those scenarios do not reach: the "pf_wideband" / "wideband" PF metric is not implemented here
-(refused), and of the multi-cell options the RSRP admission floor (a3_min_target_rsrp_dbm) and ho_rlc="flush" are
-restated but parity unpinned (no reference trajectory sets them; the GPU is checked against this restatement for
-them).
+counters after every step) of the uplink scenarios (among them 10, 14 and 18 RBGs, envs of 64, 100, 128 and 200
+robots, the 5G-LENA MAC switches: the per-RBG and frozen PF average, TDMA retransmissions, AMC on the previous PUSCH's
+PRBs, whole-band UL power and UL power control at one cell; the stochastic LOS state, Rician K from it and per-link
+delay spreads), the downlink scenarios and the scenarios with two and three cells (A3 handovers with RLC carry and
+flush, the A3 admission floor a3_min_target_rsrp_dbm, Rician links, per-link delay spreads on every robot-cell link),
+each also with planted mistakes that the comparison catches. Not implemented here (refused): the "pf_wideband" /
+"wideband" PF metric.
 """
 from __future__ import annotations
 

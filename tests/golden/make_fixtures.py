@@ -345,6 +345,84 @@ CASES = {
                                     channel="tr38901", tr38901_scenario="UMa", tr38901_los="stochastic",
                                     cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
                            E=3, R=16, steps=25, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={12: [0]}),
+    # several cells with A3 handovers under ho_rlc="flush" (every queued frame of a robot dropped at its switch,
+    # mac.py:557-581): fast motion, HARQ-IR, round robin, an N+I EWMA, a reset
+    "mc3_flush": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=4,
+                               max_harq_tx=3, harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2500.0, 400.0),
+                               n_cells=3, cell_layout="hex", cell_isd_m=120.0, cell_center_m=(60.0, 60.0),
+                               noise_model="thermal", a3_ttt_ms=10.0, ho_interruption_ms=2.5, ho_rlc="flush",
+                               li_alpha=0.3, fading_rho_per_ms=0.5),
+                      E=3, R=16, steps=30, kind="pose", arena=200.0, walk=8.0, rates=(0.5, 1.0), resets={12: [1]}),
+    # the A3 target admission floor (a3_min_target_rsrp_dbm, radio.py:311-361: a neighbour whose RSRP is below it
+    # never satisfies A3): three cells far apart, fast motion, so that some targets at the cell edge are refused
+    "mc3_a3floor": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="maxci",
+                                 n_harq=4, max_harq_tx=3, harq_fail="drop", frame_buffer=8,
+                                 msg_sizes=(2500.0, 400.0), n_cells=3, cell_layout="hex", cell_isd_m=200.0,
+                                 noise_model="thermal", a3_ttt_ms=20.0, ho_interruption_ms=5.0, li_alpha=0.5,
+                                 fading_rho_per_ms=0.0, cell_center_m=(100.0, 100.0), channel="tr38901",
+                                 tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0,
+                                 a3_min_target_rsrp_dbm=-68.0),
+                        E=3, R=16, steps=40, kind="pose", arena=300.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
+    # two cells with per-link delay spreads (fading_delay_spread_ns None): each robot-cell link's own lgDS draws, the
+    # LOS or NLOS grid index by that link's stochastic LOS state (nr_engine.py:320-381), UMi, 13 RBGs
+    "mc2_fcorr_los": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                   n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2,
+                                   cell_layout="hex", cell_isd_m=150.0, noise_model="thermal",
+                                   a3_offset_db=float("inf"), channel="tr38901", tr38901_scenario="UMi",
+                                   tr38901_los="stochastic", gnb_height_m=10.0, fading_rho_per_ms=0.5,
+                                   fading_freq_corr=True),
+                          E=2, R=16, steps=25, kind="pose", arena=250.0, walk=4.0, rates=(0.7,), resets={12: [1]}),
+    # three cells at 64 robots per env (one env per wavefront on the GPU: the cooperative interference list) with
+    # Rician fading on every link, K from each link's stochastic LOS state with a 6-slot ramp, UMa, 14 RBGs
+    "mc3_rice64": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1200.0,), n_cells=3,
+                                cell_layout="hex", cell_isd_m=200.0, noise_model="thermal",
+                                a3_offset_db=float("inf"), channel="tr38901", tr38901_scenario="UMa",
+                                tr38901_los="stochastic", gnb_height_m=25.0, fading_rho_per_ms=0.5,
+                                fading_rician=True, rician_k_ramp_slots=6),
+                       E=2, R=64, steps=14, kind="pose", arena=300.0, walk=5.0, rates=(0.4,), resets={8: [1]}),
+    # the same three cells at 48 robots per env with a fixed K of 6 dB and the A3 handover on (UMi LOS)
+    "mc3_rice48": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3,
+                                cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", a3_ttt_ms=10.0,
+                                ho_interruption_ms=2.5, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                                gnb_height_m=10.0, fading_rho_per_ms=0.0, fading_rician=True, rician_k_db=6.0),
+                       E=2, R=48, steps=16, kind="pose", arena=260.0, walk=6.0, rates=(0.5,), resets={9: [0]}),
+    # the same without Rician fading (A3 handovers and i.i.d. fading on 48-robot envs), with correlated fading in time,
+    # and on 32-robot envs (two envs per wavefront)
+    "mc3_ho48": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                              n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3,
+                              cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", a3_ttt_ms=10.0,
+                              ho_interruption_ms=2.5, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                              gnb_height_m=10.0, fading_rho_per_ms=0.0),
+                     E=2, R=48, steps=16, kind="pose", arena=260.0, walk=6.0, rates=(0.5,), resets={9: [0]}),
+    "mc3_rice48c": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                 n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3,
+                                 cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", a3_ttt_ms=10.0,
+                                 ho_interruption_ms=2.5, channel="tr38901", tr38901_scenario="UMi",
+                                 tr38901_los="los", gnb_height_m=10.0, fading_rho_per_ms=0.5, fading_rician=True,
+                                 rician_k_db=6.0),
+                        E=2, R=48, steps=16, kind="pose", arena=260.0, walk=6.0, rates=(0.5,), resets={9: [0]}),
+    "mc3_rice32": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3,
+                                cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", a3_ttt_ms=10.0,
+                                ho_interruption_ms=2.5, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                                gnb_height_m=10.0, fading_rho_per_ms=0.0, fading_rician=True, rician_k_db=6.0),
+                       E=2, R=32, steps=16, kind="pose", arena=260.0, walk=6.0, rates=(0.5,), resets={9: [0]}),
+    # one cell at 64 robots per env (one env per wavefront) with the per-link features of TR 38.901: the stochastic
+    # LOS state, Rician K from it with the default ramp, per-link delay spreads, UMi, 13 RBGs
+    "sto64": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                           max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_rho_per_ms=0.5,
+                           fading_rician=True, fading_freq_corr=True, channel="tr38901", tr38901_scenario="UMi",
+                           tr38901_los="stochastic", cell_positions_m=((150.0, 150.0),), gnb_height_m=10.0),
+                  E=2, R=64, steps=16, kind="pose", arena=300.0, walk=4.0, rates=(0.5, 0.3), resets={9: [1]}),
+    # the same on envs of 100 robots (two wavefronts per env), UMa, 8 RBGs of 35 PRB, a 10-slot ramp
+    "sto100": dict(cfg=dict(mu=1, n_prb=273, rbg_size=35, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                            n_harq=8, max_harq_tx=4, frame_buffer=8, msg_sizes=(900.0,), fading_rho_per_ms=0.3,
+                            fading_rician=True, rician_k_ramp_slots=10, fading_freq_corr=True, channel="tr38901",
+                            tr38901_scenario="UMa", tr38901_los="stochastic", cell_positions_m=((150.0, 150.0),),
+                            gnb_height_m=25.0),
+                   E=2, R=100, steps=10, kind="pose", arena=300.0, walk=5.0, rates=(0.3,), resets={6: [0]}),
 }
 
 

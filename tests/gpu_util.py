@@ -28,6 +28,8 @@ OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
 # The reported SINR is (pg + ue_tx) - noise with |pg| ~ 100-150 dB: one float32 ulp there is 7.6e-6 .. 1.5e-5 dB,
 # so near 0 dB a relative bound is meaningless; the absolute floor is 4 ulp of that magnitude.
 ABS_FLOOR = {"sinr_db": 6.1e-5, "eng._last_snr": 6.1e-5}
+# compared relative to their own magnitude (no unit floor): the N+I estimates are mW per PRB, about 1e-12
+RELATIVE = ("net.ni_ul",)
 MAX_DEV = {}
 BOUND = {}     # key -> per-element absolute bound (numpy) for the current comparison, from oracle.tolerance
 
@@ -58,7 +60,8 @@ def close(m, r, tol, floor=0.0, key=None):
         dev = np.where(same, 0.0, np.abs(m - r))
     if key is not None and dev.size:
         MAX_DEV[key] = max(MAX_DEV.get(key, 0.0), float(np.nanmax(dev)))
-    lim = np.maximum(tol * np.maximum(np.maximum(np.abs(m), np.abs(r)), 1.0), floor)
+    unit = 0.0 if key in RELATIVE else 1.0
+    lim = np.maximum(tol * np.maximum(np.maximum(np.abs(m), np.abs(r)), unit), floor)
     if key in BOUND:
         lim = np.maximum(lim, BOUND[key])
     return same | (dev <= lim)
@@ -146,8 +149,29 @@ def set_radio_bound(ref, s, cfg, eng, kind):
         b = bn if b is None else np.maximum(b, bn)
     serv = ref[f"s{s:03d}/out.serving_cell"]
     b = np.take_along_axis(b, serv[..., None], -1)[..., 0]
+    if k_.shape[0] > 1:
+        # several cells: the reported SINR subtracts 10 log10 of the serving gNB's N+I estimate, whose interference
+        # terms carry the path-gain rounding of the interferers' links (oracle.tolerance.ni_rel_bound); the estimate
+        # is an EWMA, a convex combination of the steps since the reset, so its relative bound is the largest of theirs
+        nib = ni_rel_bound_upto(ref, s, fields, amp)                                   # [E, C]
+        b = b + (10.0 / np.log(10.0)) * np.take_along_axis(nib, serv, 1)
+        BOUND["net.ni_ul"] = np.abs(ref[f"s{s:03d}/net.ni_ul"].astype(np.float64)) * nib[..., None]
     BOUND["out.sinr_db"] = b
     BOUND["eng._last_snr"] = b
+
+
+def ni_rel_bound_upto(ref, s, fields, amp):
+    """Largest oracle.tolerance.ni_rel_bound [E, C] over steps 0..s of a several-cell trajectory (with the stochastic
+    LOS state, of the LOS and the NLOS fields)."""
+    from oracle.tolerance import ni_rel_bound
+    out = None
+    for t in range(s + 1):
+        for n, sg in fields:
+            k_, phi = ref[f"s{t:03d}/{n}.k"], ref[f"s{t:03d}/{n}.phi"]
+            f = [np.concatenate([k_[c], phi[c][..., None]], -1) for c in range(k_.shape[0])]
+            v = ni_rel_bound(ref["x"][t], f, sg, amp)
+            out = v if out is None else np.maximum(out, v)
+    return out
 
 
 def teacher_forced(P, name, dev="cuda:0"):

@@ -135,3 +135,44 @@ def test_subband_correlation_factor_matches_the_restatement():
             Ld = L.double()
             assert torch.allclose(Ld @ Ld.T, c, atol=1e-5) or tau < 60.0      # (jittered near-singular cases)
             assert torch.equal(torch.tril(L), L) and torch.allclose(Ld.norm(dim=-1), torch.ones(S, dtype=torch.float64), atol=1e-6)
+
+
+@pytest.mark.parametrize("plant", ["flush_as_carry", "floor_epre_per_prb", "ds_index_of_cell0"])
+def test_oracle_catches_planted_handover_and_link_errors(plant):
+    """The reference trajectories of the handover RLC flush, the A3 admission floor and the per-link delay spreads
+    with several cells pin those branches of the oracle: a plausible mistake in each fails its comparison.
+    flush_as_carry: ho_rlc="flush" read as "carry" (no frame dropped at the switch, mac.py:557-581);
+    floor_epre_per_prb: the floor converted with the EPRE over nprb PRBs instead of 12 nprb subcarriers
+    (radio.py:337-340); ds_index_of_cell0: every robot-cell link's delay-spread index taken from the LOS state of the
+    link to cell 0 instead of its own (nr_engine.py:377-381)."""
+    import dataclasses
+    import math
+    name, keys = {"flush_as_carry": ("mc3_flush", ("ul.q.lost", "ul.q.cap", "ul.sent")),
+                  "floor_epre_per_prb": ("mc3_a3floor", ("assoc.serv", "assoc.n_ho", "assoc.a3_cand")),
+                  "ds_index_of_cell0": ("mc2_fcorr_los", ("net.h", "net.fc_idx"))}[plant]
+    d, cfgd, kind = replay.load_case(os.path.join(GOLDEN, f"traj_{name}.npz"))
+    cfg = P.NRConfig(**cfgd, seed=0)
+    if plant == "flush_as_carry":
+        cfg = dataclasses.replace(cfg, ho_rlc="carry")
+    eng = O.OracleEngine(int(d["E"]), int(d["R"]), cfg, seed=0)
+    if plant == "floor_epre_per_prb":
+        eng.assoc.floor_rx = cfg.a3_min_target_rsrp_dbm - (cfg.gnb_tx_dbm - 10 * math.log10(cfg.nprb) - cfg.ue_tx_dbm)
+    elif plant == "ds_index_of_cell0":
+        def set_fc_los(los, e=eng):
+            los0 = los[:, :, :1].expand_as(los) if los.dim() == 3 else los
+            e.fc_idx = torch.where(los0, e.fc_idx_los, e.fc_idx_nlos)
+        eng._set_fc_los = set_fc_los
+    diff = []
+
+    def on_step(s, o, acc):
+        st = eng.state()
+        for k in keys:
+            ref, mine = d[f"s{s:03d}/{k}"], st[k].numpy()
+            if k.startswith("ul.q.") and k != "ul.q.enq":
+                v = d[f"s{s:03d}/ul.q.cap"] >= 0
+                ref, mine = np.where(v, ref, 0), np.where(v, mine, 0)
+            if not np.array_equal(ref, mine):
+                diff.append((s, k))
+
+    replay.run(eng, d, kind, on_step=on_step)
+    assert diff
