@@ -289,6 +289,47 @@ DEV float aten_row_sum(int n, X x) {
     return fin;
 }
 
+// aten_row_sum for a runtime n <= NMAX whose elements are LDS reads: every read is issued before the first add (a
+// loop with a runtime bound waits for each read in turn), then the same additions in the same order. Elements past n
+// read as +0.0 and are added where the loops above would not add anything: x + (+0.0) == x for every partial sum here
+// (each starts at +0.0, so none is -0.0), so the result has the same bits.
+template <int NMAX, class X>
+DEV float aten_row_sum_u(int n, X x) {
+    float v[NMAX];
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) v[i] = i < n ? x(i) : 0.0f;
+    if (n < 8) {
+        const int si = n >> 2;
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < (NMAX < 8 ? NMAX : 8); ++i) {
+            if (i < 4) a[i] += si > 0 ? v[i] : 0.0f;
+            a[0] += (i >= si * 4 && i < n) ? v[i] : 0.0f;
+        }
+        return ((a[0] + a[1]) + a[2]) + a[3];
+    }
+    const int nv = n >> 3, ni = nv >> 2;
+    float fin = 0.f;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) fin += (i >= nv * 8 && i < n) ? v[i] : 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NMAX / 32; ++i) {
+            const bool in = i < ni;
+            a0 += in ? v[(i * 4) * 8 + l] : 0.0f;
+            a1 += in ? v[(i * 4 + 1) * 8 + l] : 0.0f;
+            a2 += in ? v[(i * 4 + 2) * 8 + l] : 0.0f;
+            a3 += in ? v[(i * 4 + 3) * 8 + l] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < NMAX / 8; ++i) a0 += (i >= ni * 4 && i < nv) ? v[i * 8 + l] : 0.0f;
+        fin += ((a0 + a1) + a2) + a3;
+    }
+    return fin;
+}
+
 // ---------------------------------------------------------------- radio (RadioMC.rx_dbm at one cell / AP)
 // Received power (dBm) of a robot at (px, py) from the cell at (gx, gy): path loss and plane-wave shadowing
 // (isaac_net/core/radio.py:238-272, channels/models.py:137-167, channels/tr38901.py:162-203 with a fixed LOS state).

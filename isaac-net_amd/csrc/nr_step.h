@@ -1466,7 +1466,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             s_la_f[lane] = la_lnw;
             s_la_f[CW + lane] = pm.olla ? olla : 0.0f;
             s_la_f[2 * CW + lane] = eff_md;
-            int top = tb.mcs_max, found_m = -1;
+            int top = tb.mcs_max, found_m = -1, tbs_found = 0;
             bool mine = tx_new;
             unsigned long long searching = __ballot(mine);
             auto more = [&]() -> bool {
@@ -1481,6 +1481,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 __syncthreads();
                 const int slot = wl / chunk, j = wl - slot * chunk;
                 bool pass = false;
+                int tbs_c = 0;                             // this candidate's TBS (the winner's is the TB's)
                 const int rl = slot < n_s ? s_la_slot[wbase + slot] : 0;
                 const int m = slot < n_s ? s_la_top[rl] - j : -1;
                 if (m >= 0) {
@@ -1488,6 +1489,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     const int ti = s_la_i[rl] + m;
                     const int tbs_m = tb.la_tbs[ti], ci0 = tb.la_ci0[ti];
                     const float cwi = tb.la_cwi[ti], ncb = tb.la_ncb[ti];
+                    tbs_c = tbs_m;
                     float eff;
                     if (pm.eesm) {
                         const uint32_t wr = (uint32_t)s_la_i[CW + rl];
@@ -1506,10 +1508,12 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     }
                 }
                 const unsigned long long pb = __ballot(pass);
+                const unsigned long long cm =
+                    mine ? (pb >> (rank * chunk)) & (chunk >= STEP_WAVE ? ~0ull : ((1ull << chunk) - 1ull)) : 0ull;
+                // the passing candidate's TBS from the lane that evaluated it (every lane takes part in the read)
+                const int tw = __shfl(tbs_c, wbase + rank * chunk + (cm ? (int)__builtin_ctzll(cm) : 0), 64);
                 if (mine) {
-                    const unsigned long long cm =
-                        (pb >> (rank * chunk)) & (chunk >= STEP_WAVE ? ~0ull : ((1ull << chunk) - 1ull));
-                    if (cm) { found_m = top - (int)__builtin_ctzll(cm); mine = false; }
+                    if (cm) { found_m = top - (int)__builtin_ctzll(cm); tbs_found = tw; mine = false; }
                     else { top -= chunk; mine = top >= 0; }
                 }
                 searching = __ballot(mine);
@@ -1517,7 +1521,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             }
             if (tx_new) {
                 mcs_new = found_m >= 0 ? found_m : 0;
-                tbs_new = tb.la_tbs[toff + mcs_new];
+                // (searched on this allocation's table row: the TBS the search read; else the row's entry)
+                tbs_new = (found_m >= 0 && toff_sel == toff) ? tbs_found : tb.la_tbs[toff + mcs_new];
             }
         }
         INET_PH(5);                                // link adaptation (power split, lse of log w, MCS search)

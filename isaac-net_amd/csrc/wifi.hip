@@ -41,7 +41,7 @@ DEV float pow_int_torch(float x, int n) {
     if (n == 1) return x;
     if (n == 2) return x * x;
     if (n == 3) return (x * x) * x;
-    return pow_r(x, (float)n);
+    return pow_count(x, (float)n);
 }
 // p ** k of tau(p) (torch pow of two float tensors) for an integer k >= 0: double-precision binary powering,
 // rounded once
@@ -72,22 +72,45 @@ DEV void access_times(const InetWifiParams& pm, float B, float rate, float aifsn
 // both sums in torch's CPU order. p^k is the double-precision running product rounded once (the correctly rounded
 // power unless p^k lies within ~k 2^-53 relative of a float rounding boundary). Under 8 stages the CPU order adds
 // stages 0..3 into four partial sums and the later stages into the first, so one pass over k in order suffices.
-DEV float tau_of_p(float p, float W0, float Wm, int L) {
+// the stage weights (W_k + 1) / 2, W_k = min(2^k W0, Wmax), of the first 7 stages (2^k W0 by doubling, exact)
+struct TauW {
+    float c[7];
+};
+DEV TauW tau_weights(float W0, float Wm) {
+    TauW t;
+    float wk = W0;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        t.c[k] = (fminn(wk, Wm) + 1.0f) * 0.5f;
+        wk = wk * 2.0f;
+    }
+    return t;
+}
+DEV float tau_of_p(float p, float W0, float Wm, int L, const TauW& tw) {
     if (L < 8) {
-        float n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f, d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+        // (unrolled to the 7-stage bound; the stage terms are the running product's, and the four partial sums take
+        // stages 0..3 one each and the later ones into the first when L >= 4, every stage into the first below 4)
         const double pd = (double)p;
+        float pk[7], tk[7];
         double pw = 1.0;
-        float wk = W0;
-        for (int k = 0; k < L; ++k) {
-            const float pk = (float)pw;
+#pragma unroll
+        for (int k = 0; k < 7; ++k) {
+            pk[k] = (float)pw;
             pw *= pd;
-            const float t = pk * ((fminn(wk, Wm) + 1.0f) * 0.5f);
-            wk = wk * 2.0f;
-            const int slot = L >= 4 && k < 4 ? k : 0;
-            if (slot == 0) { n0 += pk; d0 += t; }
-            else if (slot == 1) { n1 += pk; d1 += t; }
-            else if (slot == 2) { n2 += pk; d2 += t; }
-            else { n3 += pk; d3 += t; }
+            tk[k] = pk[k] * tw.c[k];
+        }
+        float n0, n1 = 0.f, n2 = 0.f, n3 = 0.f, d0, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+        if (L >= 4) {
+            n0 = pk[0]; n1 = pk[1]; n2 = pk[2]; n3 = pk[3];
+            d0 = tk[0]; d1 = tk[1]; d2 = tk[2]; d3 = tk[3];
+#pragma unroll
+            for (int k = 4; k < 7; ++k)
+                if (k < L) { n0 += pk[k]; d0 += tk[k]; }
+        } else {
+            n0 = pk[0]; d0 = tk[0];
+#pragma unroll
+            for (int k = 1; k < 3; ++k)
+                if (k < L) { n0 += pk[k]; d0 += tk[k]; }
         }
         return (((n0 + n1) + n2) + n3) / (((d0 + d1) + d2) + d3);
     }
@@ -128,6 +151,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                                                          int rb, InetDcfState ds, InetDcfParams dp) {
     extern __shared__ float dyn[];
     __shared__ float s_red[WAVE];
+    __shared__ float s_red4[DCF ? 1 : 3 * WAVE];          // three more rows of station values (dom_sum4)
     const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
     float* s_rem = dyn;                                   // [F][64] bytes left of every frame slot
     float* s_fin = dyn + F * WAVE;                        // [F][64] finish time, then the compaction staging row
@@ -187,12 +211,25 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     int ac = pm.cls_ac[1];
     float capB = cap_bytes(pm, rate, pm.ac_txop[ac]);
     float o_acc = NAN, o_pf = NAN, o_busy = 0.0f;       // wifi_access_ms, wifi_p_fail, wifi_busy
+    // (the row sums read LDS: aten_row_sum_u issues every read before the first add)
     auto fifo_sum = [&]() -> float {
-        return aten_row_sum(F, [&](int f) { return s_rem[f * WAVE + lane]; });
+        auto xf = [&](int f) { return s_rem[f * WAVE + lane]; };
+        if (F == 16) return aten_row_sum_u<16>(16, xf);
+#ifdef INET_EXP_R16
+        return 0.f;
+#endif
+        if (F <= 16) return aten_row_sum_u<16>(F, xf);
+        if (F <= 32) return aten_row_sum_u<32>(F, xf);
+        if (F <= 64) return aten_row_sum_u<64>(F, xf);
+        return aten_row_sum(F, xf);
     };
     if constexpr (!DCF) {
-    float tau = rob ? st.tau[(size_t)ec * (R + 1) + rc] : pm.tau0;
-    float tau_b = env_ok ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0;
+    // The AP's background station is station R of the domain. With a lane to spare in the segment (rb > R) it runs in
+    // lane R like a robot (its own tau, window, times and weight; nothing else), else every lane evaluates it too.
+    const bool bgl = rb > R;
+    const bool is_bg = bgl && env_ok && r == R;
+    float tau = rob ? st.tau[(size_t)ec * (R + 1) + rc] : (is_bg ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0);
+    float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
     float att_n = rob ? st.att_n[ir] : 0.f, att_logp = rob ? st.att_logp[ir] : 0.f;
     float credit = rob ? st.credit[ir] : 0.f;
@@ -204,6 +241,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     access_times(pm, pm.bg_B, pm.bg_rate, pm.ac_aifsn[pm.bg_ac], tsb, tcb);
     const float wb = pm.bg_w;
     const bool act_b = wb > 0.f;
+    const TauW twb = tau_weights(W0b, Wmb);
 
     // sum over the stations of the env (robots in lane order, then the background station), torch's CPU order
     auto dom_sum = [&](float v, float vb) -> float {
@@ -211,7 +249,41 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         s_red[lane] = v;
         __syncthreads();
         const float* row = s_red + gseg * rb;
-        return aten_row_sum(R + 1, [&](int i) { return i < R ? row[i] : vb; });
+        auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
+        if (R == 16) return aten_row_sum_u<17>(17, xr);
+#ifdef INET_EXP_R16
+        return 0.f;
+#endif
+        if (R < 8) return aten_row_sum_u<8>(R + 1, xr);
+        if (R < 16) return aten_row_sum_u<16>(R + 1, xr);
+        if (R < 17) return aten_row_sum_u<17>(R + 1, xr);
+        if (R < 33) return aten_row_sum_u<33>(R + 1, xr);
+        return aten_row_sum_u<65>(R + 1, xr);
+    };
+
+    // four such sums at once (one LDS round trip): rows s_red and s_red4[0..2]
+    auto dom_sum4 = [&](float v0, float b0, float v1, float b1, float v2, float b2, float v3, float b3, float& o0,
+                        float& o1, float& o2, float& o3) {
+        __syncthreads();
+        s_red[lane] = v0; s_red4[lane] = v1; s_red4[WAVE + lane] = v2; s_red4[2 * WAVE + lane] = v3;
+        __syncthreads();
+        auto sum_row = [&](const float* base, float vb) -> float {
+            const float* row = base + gseg * rb;
+            auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
+            if (R == 16) return aten_row_sum_u<17>(17, xr);
+#ifdef INET_EXP_R16
+            return 0.f;
+#endif
+            if (R < 8) return aten_row_sum_u<8>(R + 1, xr);
+            if (R < 16) return aten_row_sum_u<16>(R + 1, xr);
+            if (R < 17) return aten_row_sum_u<17>(R + 1, xr);
+            if (R < 33) return aten_row_sum_u<33>(R + 1, xr);
+            return aten_row_sum_u<65>(R + 1, xr);
+        };
+        o0 = sum_row(s_red, b0);
+        o1 = sum_row(s_red4, b1);
+        o2 = sum_row(s_red4 + WAVE, b2);
+        o3 = sum_row(s_red4 + 2 * WAVE, b3);
     };
 
     float acc_sum = 0.f, acc_n = 0.f, p_sum = 0.f, busy_sum = 0.f;
@@ -231,35 +303,50 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         const float w = act ? 1.0f : 0.0f;
         float ts, tc;
         access_times(pm, B, rate, aifsn, ts, tc);
+        // this lane's station in the solve: the robot's, or in lane R the background station's
+        const float ws = is_bg ? wb : w, tss = is_bg ? tsb : ts, tcs = is_bg ? tcb : tc;
+        const float W0s = is_bg ? W0b : W0, Wms = is_bg ? Wmb : Wm;
+        const bool acts = is_bg ? act_b : act;
+        const TauW tw = tau_weights(W0s, Wms);
 
         // ---- mean-field fixed point (meanfield.solve, one domain, one AIFS zone)
         float p = 0.f, ok = 0.f, pb = 0.f, S = 0.f;
+        // (the iterations' log1p and exp in float32, the device library's, within 2 ulp: the fixed point carries
+        // last-bit differences from the CPU's float routines either way, and the tests bound them at 2e-5 relative)
         auto fail = [&]() {
-            const float lt = log1p_r(-tau), ltb = log1p_r(-tau_b);
-            S = dom_sum(w * lt, wb * ltb);
-            const float own = act ? lt : 0.0f, ownb = act_b ? ltb : 0.0f;
-            ok = exp_r(S - own) * pm.fer1;
-            const float okb = exp_r(S - ownb) * pm.fer1;
+            const float lt = log1pf(-tau), ltb = bgl ? 0.0f : log1pf(-tau_b);
+            S = dom_sum(ws * lt, wb * ltb);
+            const float own = acts ? lt : 0.0f;
+            ok = expf(S - own) * pm.fer1;
             p = 1.0f - ok;
-            pb = 1.0f - okb;
+            if (!bgl) {
+                const float ownb = act_b ? ltb : 0.0f;
+                pb = 1.0f - expf(S - ownb) * pm.fer1;
+            }
         };
         for (int it = 0; it < pm.fp_iters; ++it) {
             tau = clampf(tau, 1e-7f, 0.999f);
-            tau_b = clampf(tau_b, 1e-7f, 0.999f);
+            if (!bgl) tau_b = clampf(tau_b, 1e-7f, 0.999f);
             fail();
-            tau = tau + pm.damp * (tau_of_p(p, W0, Wm, L) - tau);
-            tau_b = tau_b + pm.damp * (tau_of_p(pb, W0b, Wmb, L) - tau_b);
+            tau = tau + pm.damp * (tau_of_p(p, W0s, Wms, L, tw) - tau);
+            if (!bgl) tau_b = tau_b + pm.damp * (tau_of_p(pb, W0b, Wmb, L, twb) - tau_b);
         }
         tau = clampf(tau, 1e-7f, 0.999f);
-        tau_b = clampf(tau_b, 1e-7f, 0.999f);
+        if (!bgl) tau_b = clampf(tau_b, 1e-7f, 0.999f);
         fail();
-        const float r_o = (w * tau) / (1.0f - tau), r_b = (wb * tau_b) / (1.0f - tau_b);
-        const float wt_o = w * tau, wt_b = wb * tau_b;
+        const float r_o = (ws * tau) / (1.0f - tau), r_b = bgl ? 0.0f : (wb * tau_b) / (1.0f - tau_b);
+        const float wt_o = ws * tau, wt_b = wb * tau_b;
+        // ---- retry-limit loss inputs (wifi/engine.py:375-381; they need only this sub-step's p, so they are
+        // evaluated here, where their latency overlaps the sums below)
+        const bool back = q > 0.f;
+        att_n = back ? att_n + w : 0.0f;
+        const float lp = act ? log_r(clamp_min(p, 1e-12f)) : 0.0f;
+        att_logp = back ? att_logp + lp : 0.0f;
+        const float p_bar = att_n > 0.f ? exp_r(att_logp / clamp_min(att_n, 1e-12f)) : p;
+        const float pbl = pow_int_torch(p_bar, L);
         const float idle = exp_r(S);
-        const float a0 = dom_sum(r_o, r_b);
-        const float a1 = dom_sum(r_o * ts, r_b * tsb);
-        const float gd = dom_sum(wt_o, wt_b);
-        const float gg = dom_sum(wt_o * tc, wt_b * tcb);
+        float a0, a1, gd, gg;
+        dom_sum4(r_o, r_b, r_o * tss, r_b * tsb, wt_o, wt_b, wt_o * tcs, wt_b * tcb, a0, a1, gd, gg);
         const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
         const float tcav = gg / clamp_min(gd, 1e-12f);
         const float tslot = 0.0f + ((pm.slot_us * idle + idle * a1) + p_coll * tcav);
@@ -287,20 +374,11 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         }
         const float served = fminn(q, n_acc * B) * w;
 
-        // ---- retry-limit loss inputs (wifi/engine.py:375-381)
-        const bool back = q > 0.f;
-        att_n = back ? att_n + w : 0.0f;
-        const float lp = act ? log_r(clamp_min(p, 1e-12f)) : 0.0f;
-        att_logp = back ? att_logp + lp : 0.0f;
-        const float p_bar = att_n > 0.f ? exp_r(att_logp / clamp_min(att_n, 1e-12f)) : p;
-        const float pbl = pow_int_torch(p_bar, L);
-
         // ---- FIFO service, finish times, loss (serve_fifo, wifi/engine.py:361-383)
         double cacc = 0.0;
         float prev_nc = 0.0f;
-        for (int f = 0; f < qlen; ++f) {
+        auto serve = [&](int f, float rm, int c) {
             const int o = f * WAVE + lane;
-            const float rm = s_rem[o];
             cacc += (double)rm;
             const float cum = (float)cacc;
             const float nc = clamp_min(cum - served, 0.0f);
@@ -313,12 +391,25 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                 float frac = pm.access_noise == 0 ? j / (n_acc + 1.0f) : (j - credit) / clamp_min(lam, 1e-9f);
                 frac = clampf(frac, 0.0f, 1.0f);
                 const float tfin = fminn(tf + ((float)k + frac) / (float)K, (tf + 1.0f) - 1e-6f);
-                const int c = s_cls[o];
                 const float size = pm.sizes[(c > 1 ? (c < pm.n_cls ? c : pm.n_cls) : 1) - 1];
                 const float n_frame = clamp_min(ceilf(size / B), 1.0f);
-                const float p_lost = 1.0f - pow_r(1.0f - pbl, n_frame);
+                const float p_lost = 1.0f - pow_count(1.0f - pbl, n_frame);
                 const float u = uniform_bits(elem_hash(key_loss, (uint32_t)(rc * F + f)));
                 if (!(u < p_lost)) s_fin[o] = tfin;
+            }
+        };
+        {
+            // (the next frame's bytes and class are read before this frame is served)
+            float rm_n = qlen > 0 ? s_rem[lane] : 0.0f;
+            int cl_n = qlen > 0 ? (int)s_cls[lane] : 0;
+            for (int f = 0; f < qlen; ++f) {
+                const float rm = rm_n;
+                const int c = cl_n;
+                if (f + 1 < qlen) {
+                    rm_n = s_rem[(f + 1) * WAVE + lane];
+                    cl_n = (int)s_cls[(f + 1) * WAVE + lane];
+                }
+                serve(f, rm, c);
             }
         }
         if (pm.access_noise == 1 && act) credit = fifo_sum() > 0.f ? c1 - n_acc : 0.0f;
@@ -333,12 +424,13 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const bool keep = fifo_sum() > 0.f;
     if (rob) {
         st.tau[(size_t)ec * (R + 1) + rc] = tau;
-        if (r == 0) st.tau[(size_t)ec * (R + 1) + R] = tau_b;
+        if (r == 0 && !bgl) st.tau[(size_t)ec * (R + 1) + R] = tau_b;
         st.roam_left[ir] = roam;
         st.credit[ir] = keep ? credit : 0.0f;
         st.att_n[ir] = keep ? att_n : 0.0f;
         st.att_logp[ir] = keep ? att_logp : 0.0f;
     }
+    if (is_bg) st.tau[(size_t)ec * (R + 1) + R] = tau;
     o_acc = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
     o_pf = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
     o_busy = busy_sum / (float)K;
@@ -721,11 +813,15 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     if (rc) return rc;
     if (input_kind < 0 || input_kind > 2) return INET_WIFI_EINVAL;
     if (input_kind == 0 && p.n_fields < 1) return INET_WIFI_EINVAL;
-    const int rb = next_pow2(p.R);
-    const int G = p.envs_per_wave;
+    // segments of next_pow2(R + 1) lanes, lane R for the background station of the mean-field solve (R < 64); as
+    // many envs per wave as the submit kernel's segments hold, at most what fits
+    const int rb = p.R < WAVE ? next_pow2(p.R + 1) : WAVE;
+    InetWifiParams pm = p;
+    pm.envs_per_wave = p.envs_per_wave * next_pow2(p.R) / rb > 0 ? p.envs_per_wave * next_pow2(p.R) / rb : 1;
+    const int G = pm.envs_per_wave;
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    hipLaunchKernelGGL(wifi_step_kernel<false>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t,
+    hipLaunchKernelGGL(wifi_step_kernel<false>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm, t,
                        input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
