@@ -628,6 +628,11 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="replay submit and step from HIP graphs recorded after the warm-up instead of launching them "
                          "from Python every step (on this stack the eager launches are the faster of the two)")
+    ap.add_argument("--no-graph-window", action="store_true",
+                    help="skip the graph-replay window timed after the eager one (rl_scale)")
+    ap.add_argument("--steady", type=int, default=0, metavar="N",
+                    help="instead of the bench line: run N steps of rl_scale from a fresh engine and print the step "
+                         "kernel's mean duration and queue occupancy per 50-step window")
     ap.add_argument("--separate-submit", action="store_true",
                     help="enqueue each step's arrivals with submit_counts (its own launch) instead of inside the step")
     ap.add_argument("--cpu-envs", type=int, default=2048)
@@ -658,12 +663,18 @@ def main():
     dev = "cuda:0"
     E = args.envs if args.envs_set else 4096
     R = args.robots if args.robots_set else 32
-    total = args.warmup + args.steps
+    # (after the timed window: the same number of steps as HIP graph replays, reported beside the eager figure)
+    n_graph = 0 if (args.graph or args.no_graph_window) else args.steps
+    total = args.warmup + args.steps + (n_graph + 2 if n_graph else 0)
+    if args.steady:
+        total = max(total, args.steady)
     print(f"# workload rl_scale {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
     wl = S.Workload(E, R, total, seed=0, device=dev)
     cfg = wl.cfg
     eng = P.make_engine("L2", E, R, dev, cfg, seed=0, out_format=args.out_format)
     k_ul = sum(1 for x in cfg.schedule(0) if x[2])
+    if args.steady:
+        return steady_state(eng, wl, args, torch, dev, k_ul)
     q_pre, q_post = [], []
     for s in range(args.warmup):
         eng.submit_counts(wl.counts[s])
@@ -724,6 +735,21 @@ def main():
                         "touched_bytes_per_launch": touched, "queue_frames_per_robot": qlen_mean,
                         "valu_issue_util": valu_util,
                         "counters_src": cs.get("src") if cs else None}}
+    if n_graph:
+        # the next n_graph steps as replays of the recorded step graph (counts-form enqueue + step); the first two
+        # replays (recording) are not timed
+        g = eng.graph_step()
+        base = args.warmup + args.steps
+        for s in range(base, base + 2):
+            g(wl.poses[s], wl.counts[s])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for s in range(base + 2, base + 2 + n_graph):
+            g(wl.poses[s], wl.counts[s])
+        torch.cuda.synchronize()
+        res["graph_replay"] = {"ms_per_step": 1e3 * (time.perf_counter() - t1) / n_graph, "steps": n_graph,
+                               "launch": "HIP graph replay of submit_counts + step, the inputs copied into the "
+                                         "graph's buffers first"}
     if args.phase_clocks:
         res["phase_clocks"] = phase_clocks("s13" if eng.S == 13 else "s8", (E * R + 63) // 64)
     copy_calibration(args, res, torch, dev)
@@ -731,6 +757,29 @@ def main():
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(P, wl, cfg, min(args.cpu_envs, E), args.cpu_steps, 1)
     print(json.dumps(res), flush=True)
+
+
+def steady_state(eng, wl, args, torch, dev, k_ul):
+    """The whole run of the workload (args.steady steps, from a fresh engine): the step kernel's mean duration (HIP
+    events) and the mean queue length per window of 50 steps, to show whether a short window after a few warm-up
+    steps measures the steady state."""
+    from isaac_net_amd.engine import KernelTimer
+    n = args.steady
+    eng.kernel_events = ev = KernelTimer(n, dev)
+    q = []
+    for s in range(n):
+        eng.step(None, wl.poses[s], arrivals=wl.counts[s])
+        if s % 10 == 9:
+            q.append((s, float(eng.st["qlen"].float().mean())))
+    torch.cuda.synchronize()
+    ms = ev.ms()
+    win = []
+    for a in range(0, n, 50):
+        w = ms[a:a + 50]
+        qq = [v for (s, v) in q if a <= s < a + 50]
+        win.append({"steps": f"{a}..{a + len(w) - 1}", "kernel_ms_avg": sum(w) / len(w),
+                    "queue_frames_per_robot": sum(qq) / max(len(qq), 1)})
+    print(json.dumps({"workload": "rl_scale steady-state check", "steps": n, "windows": win}), flush=True)
 
 
 if __name__ == "__main__":
