@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 2
+#define INET_WIFI_ABI_VERSION 3
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -95,7 +95,11 @@ typedef struct InetWifiParams {
     /* radio of the AP (same meaning as in InetNrParams) */
     float gnb_x, gnb_y, hh2, dbp, pl_a, pl_n1, pl_c20, pl_c2, nl_b1, nl_b0, nl_c, nl_d, sig, amp, pl_const, pl_exp10,
           ue_tx;
+    int32_t los_sto;                 /* TR 38.901 stochastic LOS state of every robot-AP link (as InetNrParams) */
+    int32_t plos_scn;                /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
+    float sig_nlos;                  /* los_sto: NLOS shadow-fading sigma (dB); sig is the LOS one */
     int32_t pad1;
+    const float *los_cdf;            /* los_sto: [65536] sorted samples of a unit sum of cosines */
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */

@@ -96,7 +96,8 @@ class InetWifiParams(C.Structure):
                 ("lgamma", f32 * WIFI_MAX_NACC)] + \
                [(n, f32) for n in (
         "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1", "nl_b0", "nl_c", "nl_d", "sig",
-        "amp", "pl_const", "pl_exp10", "ue_tx")] + [("pad1", i32)]
+        "amp", "pl_const", "pl_exp10", "ue_tx")] + \
+               [("los_sto", i32), ("plos_scn", i32), ("sig_nlos", f32), ("pad1", i32), ("los_cdf", P)]
 
 
 class InetWifiOutputs(C.Structure):
@@ -120,7 +121,7 @@ ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configurati
           -3: "HIP launch failed"}
 
 ABI_VERSION = 14
-WIFI_ABI_VERSION = 2
+WIFI_ABI_VERSION = 3
 _LIB = None
 
 

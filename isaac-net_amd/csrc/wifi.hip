@@ -175,7 +175,9 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     if (rob) {
         if (input_kind == 0) {
             float px = xin[ir * 2], py = xin[ir * 2 + 1];
-            rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3);
+            const StoLos sto{pm.los_cdf, pm.plos_scn, pm.sig_nlos, pm.los_sto != 0};
+            rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3,
+                              sto);
         } else if (input_kind == 1) {
             rx = xin[ir] + pm.noise_dbm;
         } else {
@@ -793,6 +795,8 @@ int check_params(const InetWifiParams& p) {
         return INET_WIFI_EINVAL;
     if (p.n_fields < 0 || p.n_fields > 3 || p.n_modes < 0 || p.n_modes > INET_WIFI_MAX_KF) return INET_WIFI_EINVAL;
     if (p.bg_ac < 0 || p.bg_ac > 4) return INET_WIFI_EINVAL;
+    if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
+        return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
     const int rb = next_pow2(p.R);
     if (p.envs_per_wave < 1 || p.envs_per_wave * rb > WAVE) return INET_WIFI_EINVAL;

@@ -54,7 +54,10 @@ def wifi_refusals(cfg: NRConfig):
        "plain path loss + plane-wave shadowing")
     no(cfg.channel not in ("log_distance", "tr38901"), f"channel={cfg.channel!r}", "log_distance and tr38901")
     if cfg.channel == "tr38901":
-        no(cfg.tr38901_los not in ("los", "nlos"), "tr38901_los='stochastic'", "a fixed LOS state (los / nlos)")
+        no(cfg.tr38901_los == "stochastic" and (cfg.tr38901_scenario.startswith("InF") or
+                                                (cfg.tr38901_scenario == "UMa" and cfg.ue_height_m > 13.0)),
+           "the stochastic LOS state of InF or of UMa above 13 m", "the stochastic LOS state of UMi, UMa and InH")
+        no(cfg.los_soft, "the soft LOS state (los_soft)", "a hard LOS state")
         no(cfg.tr38901_scenario == "RMa", "the RMa scenario", "UMa, UMi, InH, InF")
         no(cfg.tr38901_scenario.startswith("InF") and cfg.tr38901_los == "nlos", "InF NLOS", "InF LOS")
     no(cfg.shadow_modes > 16, "shadow_modes > 16", "up to 16 plane waves")
@@ -122,7 +125,7 @@ class HipWifiEngine:
         self._cstate = s
 
     def _build_params(self):
-        from .channels import SCENARIOS, SIGMA_SF, breakpoint_m
+        from .channels import SCENARIOS, SIGMA_SF, breakpoint_m, sum_of_cosines_cdf_table
         cfg, wc, dd = self.config, self.wc, self.d
         p = _lib.InetWifiParams()
         p.E, p.R, p.F, p.K, p.M, p.L = self.E, self.R, self.F, dd.K, len(dd.rates), wc.max_tx
@@ -178,14 +181,20 @@ class HipWifiEngine:
                 p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 32.4, 17.3, 20 * math.log10(fc), 0.0
             else:
                 p.pl_a, p.pl_n1, p.pl_c20, p.pl_c2 = 31.84, 21.50, 19.00 * math.log10(fc), 0.0
-            if rc.tr38901_los != "los":
+            los = rc.tr38901_los == "los"
+            if rc.tr38901_los == "stochastic":   # LOS and NLOS parameters, the CDF of the LOS-state field
+                self._los_cdf = sum_of_cosines_cdf_table(K).to(self.dev)
+                p.los_sto, p.los_cdf = 1, self._los_cdf.data_ptr()
+                p.plos_scn = {"UMi": 0, "UMa": 1, "InH": 2}[scn]
+                p.sig_nlos = SIGMA_SF[scn][1]
+            if not los:
                 if scn == "UMi":
                     p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 35.3, 22.4, 21.3 * math.log10(fc), 0.3 * (h_ut - 1.5)
                 elif scn == "UMa":
                     p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 39.08, 13.54, 20 * math.log10(fc), 0.6 * (h_ut - 1.5)
                 else:
                     p.nl_b1, p.nl_b0, p.nl_c, p.nl_d = 38.3, 17.30, 24.9 * math.log10(fc), 0.0
-            p.sig = SIGMA_SF[scn][0 if rc.tr38901_los == "los" else 1]
+            p.sig = SIGMA_SF[scn][0 if rc.tr38901_los in ("los", "stochastic") else 1]
             p.amp = 1.0 * math.sqrt(2 / K)
             p.spectrum = 1
             dc = (sc.sf_corr_los_m, sc.sf_corr_nlos_m, sc.los_corr_m)

@@ -473,6 +473,13 @@ WIFI_CASES = {
                  wifi=dict(class_ac=("VO", "VI"), bandwidth_mhz=80, n_ss=2, gi_us=1.6, substep_ms=2.0,
                            ap_height_m=6.0),
                  E=3, R=8, steps=25, kind="pose", arena=150.0, walk=2.0, rates=(1.5, 0.5), resets={15: [2]}),
+    # poses through TR 38.901 UMi with the stochastic LOS state (the reference's default), the AP in the middle of a
+    # 300 m arena so that links cross the LOS / NLOS boundary as the robots move
+    "w_sto": dict(cfg=dict(control_step_ms=10.0, frame_buffer=10, msg_sizes=(600.0, 1500.0), timeout_steps=5,
+                           channel="tr38901", tr38901_scenario="UMi", tr38901_los="stochastic",
+                           cell_positions_m=((150.0, 150.0),)),
+                  wifi=dict(ap_height_m=6.0),
+                  E=3, R=16, steps=30, kind="pose", arena=300.0, walk=4.0, rates=(1.5, 0.5), resets={14: [0]}),
     # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
     # AP, 1500 B messages, 20 sub-steps per control step
     "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),

@@ -141,6 +141,19 @@ def test_per_link_delay_spread_and_k_from_los_refusals():
                                   tr38901_scenario="UMi", fading_delay_spread_ns=300.0)) == []
 
 
+def test_wifi_stochastic_los_refusals():
+    """Level WIFI runs the stochastic LOS state (the reference's default) on UMi, UMa up to 13 m and InH; InF and UMa
+    above 13 m are refused, as at the NR levels."""
+    from isaac_net_amd.wifi_config import WifiConfig
+    from isaac_net_amd.wifi_engine import wifi_refusals
+    one = dict(channel="tr38901", tr38901_los="stochastic", cell_positions_m=((0.0, 0.0),), wifi=WifiConfig())
+    for scn in ("UMi", "UMa", "InH"):
+        assert wifi_refusals(P.NRConfig(**one, tr38901_scenario=scn)) == [], scn
+    for cfg in (P.NRConfig(**one, tr38901_scenario="InF-SL"), P.NRConfig(**one, tr38901_scenario="UMa",
+                                                                           ue_height_m=20.0)):
+        assert "stochastic LOS" in " ".join(f for f, _ in wifi_refusals(cfg))
+
+
 @pytest.mark.parametrize("name", ["fcorr_los", "fcorr_los_dl", "fcorr_los_rice", "mc2_fcorr_los"])
 def test_delay_spread_grid_matches_the_reference_table(name):
     """The square roots on the delay-spread grid (channels.delay_spread_grid) equal the reference engine's own
