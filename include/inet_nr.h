@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define INET_NR_ABI_VERSION 14
+#define INET_NR_ABI_VERSION 15
 #define INET_NR_MAX_S 32          /* subbands (RBGs) */
 #define INET_NR_MAX_P 16          /* HARQ processes */
 #define INET_NR_MAX_R 256         /* robots per env: a segment of one 64-wide wavefront (up to 64), or two / four
@@ -117,6 +117,16 @@ typedef struct InetNrState {
        use (fc_idx) and those of the link's LOS and NLOS draws (fc_idl, fc_idn), drawn at reset; a pose step on TR 38.901
        selects the LOS or NLOS one by the radio's LOS state (NLOS until one is reported). */
     int32_t *fc_idx, *fc_idl, *fc_idn;
+    /* Per-robot Doppler (fading_doppler = "per_robot": engine.py:862-864, radio.py:285-300, channels/doppler.py:23-29;
+       ABI 15): per robot [E][R] the last pose (x, y) ([E][R][2]), whether it is set (0 after a reset), and the AR(1)
+       correlation per ms (NRNet.fading_rho_ms; the caller sets it to fading_rho_per_ms at creation). A pose step sets
+       the speed from params.vel or |pose - last pose| / control step, floored at dop_floor, and from it the
+       correlation J0(dop_kx v dop_kf)^(1 / 2.5) (0 from the first zero of J0 on); every fading row then evolves with
+       rho = rho_ms^(row.rho) (row.rho holds the exponent dt slot_ms) and sqrt(1 - rho^2). The DL step reads them,
+       the UL step writes them. */
+    float *prev_pos;
+    int32_t *has_prev;
+    float *rho_ms;
 } InetNrState;
 
 /* Device tables (PHY) and the host constants that go with them. */
@@ -175,6 +185,8 @@ typedef struct InetNrParams {
     int32_t plos_scn;                 /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
     int32_t k_ramp;                   /* k_from_los: rician_k_ramp_slots (0: a new target applies at once) */
     int32_t fc_G;                     /* fc_on 2: grid points of fc_tab (fading_ds_grid) */
+    int32_t doppler;                  /* per-robot Doppler (InetNrState.rho_ms; ABI 15) */
+    int32_t pad_d;
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */
@@ -188,9 +200,13 @@ typedef struct InetNrParams {
     /* fc_on 2: lgDS = mu + sigma z (float32) of the NLOS and the LOS state (TR 38.901 Table 7.5-6), its grid index
        round((lgDS + 9 - ds_c1) ds_c2) clamped to [0, fc_G - 1], ds_c1 = log10(min ns), ds_c2 = (G - 1) / log10(max/min) */
     float ds_mu_n, ds_sig_n, ds_mu_l, ds_sig_l, ds_c1, ds_c2;
+    /* doppler: speed floor (m/s), f_c / c (float32 of carrier_ghz 1e9 / c), 2 pi 2.5 ms (float32), control step (s) */
+    float dop_floor, dop_kf, dop_kx, dop_dt;
     const float *fc_L;                /* fc_on: [S][S] lower-triangular square root of the subband correlation */
     const float *los_cdf;             /* los_sto: [65536] sorted samples of a unit sum of cosines (fields.py:94-106) */
     const float *fc_tab;              /* fc_on 2: [fc_G][S][S] square roots of the subband correlation on the grid */
+    const float *vel;                 /* doppler, this call only: the velocity input [E][R][2] (m/s) of a pose step, or
+                                         NULL (the speed from consecutive poses) */
 } InetNrParams;
 
 /* One scheduled slot of the control step (host-built per TDD key, device resident). */
@@ -199,7 +215,8 @@ typedef struct InetNrRow {
     int32_t nsym_idx;     /* index into the LA tables (-1: no UL data symbols) */
     int32_t flags;        /* 1 SR opportunity, 2 UL data, 4 fading evolves, 8 fading state needed, 16 proactive grant */
     float re_prb;         /* data REs per PRB of the UL slot */
-    float rho, c1;        /* AR(1) coefficients rho^(dt slot_ms) and sqrt(1 - rho^2), as float32 */
+    float rho, c1;        /* AR(1) coefficients rho^(dt slot_ms) and sqrt(1 - rho^2), as float32 (params.doppler:
+                             rho = the exponent dt slot_ms, c1 unused) */
     uint32_t salt_fade;   /* salt((FADING << 16) | rel) */
     uint32_t salt_bler;   /* salt((BLER_UL << 16) | rel) */
 } InetNrRow;

@@ -18,7 +18,8 @@ class InetNrState(C.Structure):
         "sent", "floor_", "bsr", "sr_t", "last_tx", "olla", "avg", "enq", "qlen", "csi", "h_re", "h_im",
         "h_meta", "h_lo", "h_hi", "h_ready", "h_tbs", "h_comb", "h_lexp", "h_nrb",
         "q_cap", "q_start", "q_end", "q_fin", "q_meta", "q_hid", "spec_re", "spec_im", "k_lin",
-        "env_id", "episode", "ctr_step", "ctr_submit", "epoch", "field", "ctr", "hist", "clock", "base", "last_nprb", "k_los", "k_from", "k_g0", "k_fresh", "fc_idx", "fc_idl", "fc_idn")]
+        "env_id", "episode", "ctr_step", "ctr_submit", "epoch", "field", "ctr", "hist", "clock", "base", "last_nprb", "k_los", "k_from", "k_g0", "k_fresh", "fc_idx", "fc_idl", "fc_idn",
+        "prev_pos", "has_prev", "rho_ms")]
 
 
 class InetNrTables(C.Structure):
@@ -33,13 +34,14 @@ class InetNrParams(C.Structure):
         "E", "R", "S", "P", "F", "N", "sched", "comb", "eesm", "harq_drop", "olla", "phr_cap", "retx_prio", "rician",
         "fading", "purge", "input_kind", "radio_model", "out_ref", "max_tx", "sr_delay", "ul_rtt", "rlc_retx",
         "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "n_data", "n_cells", "rebase_at", "pf_rbg", "pf_freeze",
-        "whole_band", "pc1_on", "retx_tdma", "amc_prev", "fc_on", "k_from_los", "los_sto", "plos_scn", "k_ramp", "fc_G")] + \
+        "whole_band", "pc1_on", "retx_tdma", "amc_prev", "fc_on", "k_from_los", "los_sto", "plos_scn", "k_ramp", "fc_G",
+        "doppler", "pad_d")] + \
                [(n, f32) for n in (
         "olla_up", "olla_dn", "pf_a", "pf_b", "target", "phr_min", "snr_ref_prbs", "w0", "ref_off", "noise_prb",
         "ue_tx", "subband_noise", "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1",
         "nl_b0", "nl_c", "nl_d", "sig", "amp", "pl_const", "pl_exp10", "proc_off_hi", "proc_off_lo", "wb_db", "pc_p0",
         "pc_alpha", "k_mu", "k_sigma", "sig_nlos", "k_rinv", "ds_mu_n", "ds_sig_n", "ds_mu_l", "ds_sig_l", "ds_c1",
-        "ds_c2")] + [("fc_L", P), ("los_cdf", P), ("fc_tab", P)]
+        "ds_c2", "dop_floor", "dop_kf", "dop_kx", "dop_dt")] + [("fc_L", P), ("los_cdf", P), ("fc_tab", P), ("vel", P)]
 
 
 class InetNrOutputs(C.Structure):
@@ -120,7 +122,7 @@ ROW_DTYPE_FIELDS = ("rel", "nsym_idx", "flags", "re_prb", "rho", "c1", "salt_fad
 ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configuration for this build",
           -3: "HIP launch failed"}
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 WIFI_ABI_VERSION = 3
 _LIB = None
 

@@ -39,9 +39,9 @@ def rbg_size_38214(n_prb, config=1):
 
 
 # The reference NRConfig's fields that this build does not model, with their reference defaults (isaac_net/core/
-# config.py:477-786): FDD DL carrier, DL mini-slots, LENA TBS, rank / MIMO, QoS, the BSR grant pipeline, Doppler and
-# delay-spread fading, InF / O2I details, radio maps, blockage, sector antennas, closed-loop TPC, radio link failure,
-# RACH, DRX and the prototype levels. A reference config (a checkpoint's) that sets one of them to anything else
+# config.py:477-786): FDD DL carrier, DL mini-slots, LENA TBS, rank / MIMO, QoS, the BSR grant pipeline, the
+# speed-derived global rho, delay-spread details, InF / O2I details, radio maps, blockage, sector antennas,
+# closed-loop TPC, radio link failure, RACH, DRX and the prototype levels. A reference config (a checkpoint's) that sets one of them to anything else
 # needs a feature this engine does not run (checkpoint.check refuses it).
 REFERENCE_ONLY_DEFAULTS = {
     'dl_n_prb': None,
@@ -65,7 +65,6 @@ REFERENCE_ONLY_DEFAULTS = {
     'rlc_tail_bytes': 16,
     'rlc_tail_timer_ms': 10.0,
     'ue_speed_mps': None,
-    'doppler_min_speed_mps': 0.0,
     'fading_ds_from_los': True,
     'fading_pdp': 'exponential',
     'inf_hall_volume_m3': None,
@@ -191,7 +190,8 @@ class NRConfig:
     phr_min_db: float = 3.0
     fading: bool = True
     fading_rho_per_ms: float = 0.93 ** (1 / 2.5)
-    fading_doppler: str = "global"
+    fading_doppler: str = "global"       # "per_robot": each robot's AR(1) correlation from its own speed
+    doppler_min_speed_mps: float = 0.0   # per_robot: speed floor (0: a still robot's fading is frozen)
     carrier_ghz: float = 3.5
     fading_rician: bool = False
     rician_k_db: float | None = None
@@ -269,6 +269,7 @@ class NRConfig:
 
     def __post_init__(self):
         assert self.mu in (0, 1, 2), "mu must be 0, 1 or 2 (FR1)"
+        assert self.fading_doppler in ("global", "per_robot") and self.doppler_min_speed_mps >= 0
         self.fading_ds_grid = tuple(self.fading_ds_grid)
         assert len(self.fading_ds_grid) == 3 and 0 < self.fading_ds_grid[0] < self.fading_ds_grid[1] and \
             int(self.fading_ds_grid[2]) == self.fading_ds_grid[2] and self.fading_ds_grid[2] >= 2, \

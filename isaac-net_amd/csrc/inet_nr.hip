@@ -179,6 +179,7 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
         st.sent[ir] = 0; st.floor_[ir] = 0; st.bsr[ir] = 0; st.sr_t[ir] = -1; st.last_tx[ir] = -1;
         if (st.base) st.base[ir] = 0;
         if (st.last_nprb) st.last_nprb[ir] = 0.f;
+        if (pm.doppler) st.has_prev[ir] = 0;          // (radio.py:218: no last pose; rho_ms is kept)
         st.olla[ir] = 0.f; st.avg[ir] = 100.f; st.enq[ir] = 0; st.qlen[ir] = 0;
         for (int s = 0; s < S; ++s) st.csi[((size_t)e * S + s) * R + r] = 0.f;
         for (int p = 0; p < P; ++p) {
@@ -311,6 +312,8 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (p.k_from_los && (!p.rician || !st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || p.k_ramp < 0))
         return INET_NR_EINVAL;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
+        return INET_NR_EINVAL;
+    if (p.doppler && (!st->prev_pos || !st->has_prev || !st->rho_ms || !(p.dop_dt > 0.0f)))
         return INET_NR_EINVAL;
     const int n_data = p.n_data > 0 ? p.n_data : n_rows;
     const bool ir = p.comb == 2, vref = p.input_kind == 2;
@@ -463,6 +466,7 @@ int32_t inet_nr_reset(const InetNrState* st, const InetNrParams* prm, const uint
     if (T < 0 || T > 0x7fffffff ||
         (p.k_from_los && (!st->k_los || !st->k_from || !st->k_g0 || !st->k_fresh || !p.rician)))
         return INET_NR_EINVAL;
+    if (p.doppler && !st->has_prev) return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, *st, p, mask, (int)T, k_lin0,
                        dcorr[0], dcorr[1], dcorr[2], spectrum, mask ? 0 : 1);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;

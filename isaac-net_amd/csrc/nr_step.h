@@ -26,6 +26,7 @@
 
 #include "../../include/inet_nr.h"
 #include "aten_sort.h"
+#include "doppler.h"
 #include "inet_nr_dev.h"
 
 namespace inet {
@@ -327,7 +328,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
         pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
-        pm.fc_on = 0; pm.los_sto = 0; pm.k_from_los = 0;
+        pm.fc_on = 0; pm.los_sto = 0; pm.k_from_los = 0; pm.doppler = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -351,6 +352,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     __shared__ float s_fcl[FX == 0 ? S * S : 1];
     const bool fc = FX == 0 && pm.fc_on != 0;
     const bool fc2 = FX == 0 && pm.fc_on == 2;         // per-link delay spreads: L = fc_tab[the robot's grid index]
+    const bool dop = FX == 0 && pm.doppler != 0;       // per-robot Doppler: rho = rho_ms^(row.rho) per robot
     // the batched product of the reference accumulates separately rounded products while S S 2 < 400, fused above
     constexpr bool FC_SEQ = S * S * 2 < 400;
     __shared__ int s_eq[IR ? MAX_M * MAX_EQW : 1];              // HARQ-IR equivalent MCS (IR builds only)
@@ -602,6 +604,31 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     bool los_c[NC];                                // several cells: that of every robot-cell link
 #pragma unroll
     for (int c = 0; c < NC; ++c) los_c[c] = false;
+    // per-robot Doppler (engine.py:862-864, radio.py:285-300): the robot's AR(1) correlation per ms, set anew by a pose
+    // step from its speed (|vel|, else |pose - last pose| / control step, 0 right after a reset; floored); the DL step
+    // derives the same value from the state the UL step then updates
+    float rho_ms = 0.f;
+    if (dop && act) rho_ms = ldo(st.rho_ms, o_r);
+    auto observe_motion = [&](float px, float py) {
+        if (!dop || !act) return;
+        float v;
+        if (pm.vel) {
+            const float vx = ldo(pm.vel, o_r * 2u), vy = ldo(pm.vel + 1, o_r * 2u);
+            v = sqrtf(fmaf(vy, vy, vx * vx));          // (torch's norm over the last two: x x, then fused y y +)
+        } else {
+            const float dx = px - ldo(st.prev_pos, o_r * 2u), dy = py - ldo(st.prev_pos + 1, o_r * 2u);
+            v = sqrtf(fmaf(dy, dy, dx * dx)) / pm.dop_dt;
+            if (ldo(st.has_prev, o_r) == 0) v = 0.f;
+        }
+        v = v < pm.dop_floor ? pm.dop_floor : v;    // (clamp(min): NaN stays NaN)
+        rho_ms = inet::doppler_rho_ms(v, pm.dop_kf, pm.dop_kx);
+        if constexpr (!DL) {
+            sto(st.rho_ms, o_r, rho_ms);
+            sto(st.prev_pos, o_r * 2u, px);
+            sto(st.prev_pos + 1, o_r * 2u, py);
+            sto(st.has_prev, o_r, 1);
+        }
+    };
     if constexpr (MC) {
         // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
         float px = 0.f, py = 0.f;
@@ -612,6 +639,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los, &los_c[c]) -
                      pm.ue_tx;
         }
+        observe_motion(px, py);
         los_rep = pm.radio_model == 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) ref[s] = 0.f;
@@ -631,6 +659,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
         const float rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y,
                                       st.field + (size_t)ee * pm.n_fields * pm.n_modes * 3, sto_los, &los_now);
+        observe_motion(px, py);
         los_rep = pm.radio_model == 1;
         const float pg = rx - pm.ue_tx;
         if constexpr (DL) ref[0] = (pg + lk.ref_off) - lk.noise_prb;
@@ -886,11 +915,19 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 const float zr = normal_of(mix32(mix32(hin) ^ bfc), mix32(mix32(hin + GOLD) ^ bfc));
                 const float zi = normal_of(mix32(mix32(hin + 2u * GOLD) ^ bfc), mix32(mix32(hin + 3u * GOLD) ^ bfc));
                 // the innovation term sqrt(1 - rho^2) z / sqrt(2) of the AR(1) step, ready for the robot's update
-                // (frequency-correlated fading: z itself, correlated by the robot first)
-                s_z[(2 * qc) * CW + Lc] = fc ? zr : div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
-                s_z[(2 * qc + 1) * CW + Lc] = fc ? zi : div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
+                // (frequency-correlated fading: z itself, correlated by the robot first; per-robot Doppler: z, scaled
+                // by the robot's own coefficient)
+                s_z[(2 * qc) * CW + Lc] = (fc || dop) ? zr : div_const(row.c1 * zr, SQRT2_F, INV_SQRT2_F);
+                s_z[(2 * qc + 1) * CW + Lc] = (fc || dop) ? zi : div_const(row.c1 * zi, SQRT2_F, INV_SQRT2_F);
             }
             INET_PH(1);                            // fading innovations (the robots' own updates follow)
+            // the AR(1) coefficients: the row's, or with per-robot Doppler rho = rho_ms^(dt slot_ms) and
+            // sqrt(1 - rho^2) of the robot (nr_engine.py:586-589)
+            float rho_k = row.rho, c1_k = row.c1;
+            if (dop) {
+                rho_k = inet::pow_scalar_f32(rho_ms, row.rho);
+                c1_k = sqrtf(1.0f - rho_k * rho_k);
+            }
             __syncthreads();
             if (draw && fc2) {
                 // per-link delay spreads: L = fc_tab[the link's grid index] (nr_engine.py:365-368), read from global
@@ -912,8 +949,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                             else { ar = fmaf(l, zr, ar); ai = fmaf(l, zi, ai); }
                         }
                         const int q = c * S + i;
-                        hr[q] = row.rho * hr[q] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
-                        hi[q] = row.rho * hi[q] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
+                        hr[q] = rho_k * hr[q] + div_const(c1_k * ar, SQRT2_F, INV_SQRT2_F);
+                        hi[q] = rho_k * hi[q] + div_const(c1_k * ai, SQRT2_F, INV_SQRT2_F);
                     }
                 }
             } else if (draw && fc) {
@@ -932,9 +969,15 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                             ai = fmaf(l, s_z[(2 * (c * S + j) + 1) * CW + lane], ai);
                         }
                         const int q = c * S + i;
-                        hr[q] = row.rho * hr[q] + div_const(row.c1 * ar, SQRT2_F, INV_SQRT2_F);
-                        hi[q] = row.rho * hi[q] + div_const(row.c1 * ai, SQRT2_F, INV_SQRT2_F);
+                        hr[q] = rho_k * hr[q] + div_const(c1_k * ar, SQRT2_F, INV_SQRT2_F);
+                        hi[q] = rho_k * hi[q] + div_const(c1_k * ai, SQRT2_F, INV_SQRT2_F);
                     }
+                }
+            } else if (draw && dop) {
+#pragma unroll
+                for (int q = 0; q < NCS; ++q) {
+                    hr[q] = rho_k * hr[q] + div_const(c1_k * s_z[(2 * q) * CW + lane], SQRT2_F, INV_SQRT2_F);
+                    hi[q] = rho_k * hi[q] + div_const(c1_k * s_z[(2 * q + 1) * CW + lane], SQRT2_F, INV_SQRT2_F);
                 }
             } else if (draw) {
 #pragma unroll
@@ -2100,6 +2143,7 @@ void launch_step(const StepArgs& a) {
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
                         p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 && p.los_sto == 0 && p.k_from_los == 0 &&
+                        p.doppler == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

@@ -100,7 +100,6 @@ def refusals(cfg: NRConfig):
                                         scenario_name(cfg.tr38901_scenario) not in ("UMi", "UMa", "InH")),
        "per-link delay spreads (fading_delay_spread_ns=None) outside TR 38.901 or on RMa / InF",
        "per-link delay spreads on UMi, UMa and InH, or one fixed delay spread")
-    no(cfg.fading_doppler != "global", "per-robot Doppler fading", "one rho")
     no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
     no(cfg.rach or cfg.drx, "RACH / DRX access", "always connected")
     no(cfg.tbs_mode != "38214" or cfg.bler_source != "pdsch", "tbs_mode / bler_source", "38.214 TBS, Sionna PDSCH")
@@ -227,6 +226,10 @@ class HipNREngine:
             "clock": z(1, dt=torch.int64),
             "base": z(E, R, dt=torch.int64),           # byte-stream base of every robot's UL offsets
             "last_nprb": z(E, R, dt=f32),               # PRBs of the last PUSCH (ul_amc_alloc "previous")
+            # per-robot Doppler: the last pose, whether it is set, the AR(1) correlation per ms (the global one
+            # until a pose step sets it: channels/doppler.py:32-37)
+            "prev_pos": z(E, R, 2, dt=f32), "has_prev": z(E, R),
+            "rho_ms": z(E, R, dt=f32, v=float(cfg.fading_rho_per_ms)),
         }
         self._n_fields = nf
         self._last_snr = torch.zeros(E, R, device=d)
@@ -336,6 +339,13 @@ class HipNREngine:
             p.k_ramp = int(cfg.rician_k_ramp_slots)   # K ramps to a new target over k_ramp slots
             p.k_rinv = 1.0 / p.k_ramp if p.k_ramp else 0.0
         p.purge = int(cfg.discard == "purge")
+        # per-robot Doppler (engine.py:862-864, channels/doppler.py:23-29): the float32 scalars of the reference's
+        # tensor-scalar operations (f_c / c, 2 pi 2.5 ms evaluated left to right in double, the control step in s)
+        p.doppler = int(cfg.fading_doppler == "per_robot")
+        p.dop_floor = cfg.doppler_min_speed_mps
+        p.dop_kf = cfg.carrier_ghz * 1e9 / 299_792_458.0
+        p.dop_kx = 2 * math.pi * 2.5 * 1e-3
+        p.dop_dt = cfg.control_step_ms * 1e-3
         p.out_ref = int(self.out_format == "reference")
         p.max_tx, p.sr_delay, p.ul_rtt, p.rlc_retx = cfg.max_harq_tx, cfg.sr_delay, cfg.ul_rtt, cfg.rlc_retx_slots
         p.timeout, p.tb_oh = cfg.timeout_steps, cfg.tb_overhead_bytes
@@ -437,14 +447,13 @@ class HipNREngine:
         for rel, _dls, uls, sr, _cqi, _ack in sched:
             dt = dt0 if prev is None else rel - prev
             prev = rel
-            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
+            rho = self._row_rho(dt)[0]
             evol.append(cfg.fading and dt > 0)
             rhos.append(float(np.float32(rho)))
         n = len(sched)
         for k, (rel, _dls, uls, sr, _cqi, _ack) in enumerate(sched):
             dt = dt0 if k == 0 else rel - sched[k - 1][0]
-            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
-            c1 = math.sqrt(1 - rho ** 2)
+            rho, c1 = self._row_rho(dt)
             need_h = evol[k] and (uls > 0 or k == n - 1 or not (evol[k + 1] and rhos[k + 1] == 0.0))
             pg = cfg.proactive_grant == "every_ul_slot" or (cfg.proactive_grant == "per_period"
                                                             and (g0 + rel) % P_ == pg_pos)
@@ -461,6 +470,16 @@ class HipNREngine:
         self._rows[key] = res
         return res
 
+    def _row_rho(self, dt):
+        """(rho, c1) of a fading row dt slots after the previous one: rho^(dt slot_ms) and sqrt(1 - rho^2) of the
+        global rho (nr_engine.py:583-585); with per-robot Doppler the exponent dt slot_ms (the kernels raise each
+        robot's rho_ms to it, nr_engine.py:586-589) and 0."""
+        cfg = self.config
+        if cfg.fading_doppler == "per_robot":
+            return (dt * cfg.slot_ms if dt > 0 else 1.0), 0.0
+        rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
+        return rho, math.sqrt(1 - rho ** 2)
+
     def _dl_rows(self, sched, evol, rhos, dt0):
         """The DL rows of a step (the rows of the UL kernel with the DL meaning): flags 1 CQI report, 2 DL data slot,
         4 / 8 fading evolves / its gain is needed (at DL data and CQI rows, and wherever a later row's evolution
@@ -470,8 +489,7 @@ class HipNREngine:
         rows = []
         for k, (rel, dls, _uls, _sr, cqi, ack) in enumerate(sched):
             dt = dt0 if k == 0 else rel - sched[k - 1][0]
-            rho = cfg.fading_rho_per_ms ** (dt * cfg.slot_ms) if dt > 0 else 1.0
-            c1 = math.sqrt(1 - rho ** 2)
+            rho, c1 = self._row_rho(dt)
             need_h = evol[k] and (dls > 0 or cqi or (k < n - 1 and not (evol[k + 1] and rhos[k + 1] == 0.0)))
             if not 0 <= ack < 1 << 16:
                 raise HipUnsupported("a HARQ-ACK slot more than 65535 slots after the step start")
@@ -705,16 +723,17 @@ class HipNREngine:
         Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env).
         arrivals= (extension): counts [E,R,NC] uint8 of this step's messages, enqueued inside the step's launch as
         submit_counts(counts) would do before it; the dict then also holds arrivals_accepted [E,R] int32."""
-        if (dl_snr_db is not None and not self.dl) or pathgain_db is not None or vel is not None or \
+        if (dl_snr_db is not None and not self.dl) or pathgain_db is not None or \
                 triggers is not None or blockers is not None:
-            raise HipUnsupported("dl_snr_db (without dl=True) / pathgain_db / vel / triggers / blockers need features "
-                                 "the hip backend does not implement (several cells, per-robot Doppler, traffic "
+            raise HipUnsupported("dl_snr_db (without dl=True) / pathgain_db / triggers / blockers need features "
+                                 "the hip backend does not implement (the path gain input with several cells, traffic "
                                  "models, blockage)")
         T = self._now(t)
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
         kind, xin = self._input(x, snr_db)
         self._check_kind(kind)
+        vin = self._vel_input(vel, kind)
         plan = self._plan(T, kind)
         dl = None
         if self.dl:
@@ -739,7 +758,11 @@ class HipNREngine:
                 hid = self._last_hid
         if arr is not None and self._log_stats:
             self._stats_counts(T, arr)
-        o = self._launch_step(T, plan, xin, hid, dl, arrivals=arr)
+        self._cparams.vel = None if vin is None else vin.data_ptr()
+        try:
+            o = self._launch_step(T, plan, xin, hid, dl, arrivals=arr)
+        finally:
+            self._cparams.vel = None
         if self._log_stats:
             self._stats_step(o)
         self._commit(T, plan, o)
@@ -763,6 +786,17 @@ class HipNREngine:
         if tuple(xin.shape) != want:
             raise ValueError(f"input must have shape {want}, got {tuple(xin.shape)}")
         return kind, xin
+
+    def _vel_input(self, vel, kind):
+        """The velocity input [E,R,2|3] (m/s) of a pose step with per-robot Doppler as a contiguous [E,R,2] float32
+        device tensor (the speed is |vel[..., :2]|, radio.py:292-293); None without one. Like the reference it is
+        ignored with SNR input or without per-robot Doppler."""
+        if vel is None or kind != 0 or self.config.fading_doppler != "per_robot":
+            return None
+        v = vel[..., :2].to(self.dev, torch.float32).contiguous()
+        if tuple(v.shape) != (self.E, self.R, 2):
+            raise ValueError(f"vel must be [E,R,2|3], got {tuple(vel.shape)}")
+        return v
 
     def _check_kind(self, kind):
         if self.R > 64 and kind == 2:
@@ -1087,6 +1121,8 @@ class HipNREngine:
             rv = (lambda x: x[:, 0]) if self.C == 1 else (lambda x: x.permute(0, 2, 1))   # [E,R] / [E,R,C]
             out.update({"net.fc_idx": L(rv(st["fc_idx"])), "net.fc_idx_los": L(rv(st["fc_idl"])),
                         "net.fc_idx_nlos": L(rv(st["fc_idn"]))})
+        if cfg.fading_doppler == "per_robot":
+            out["net.fading_rho_ms"] = st["rho_ms"]
         return out
 
     def _link_load(self, pre, st, sd):
@@ -1184,6 +1220,8 @@ class HipNREngine:
                 if bool(((v < 0) | (v >= G)).any()):
                     raise ValueError(f"{k}: grid indices outside [0, {G})")
                 st[n].copy_(lv(I(v)))
+        if cfg.fading_doppler == "per_robot" and "net.fading_rho_ms" in sd:
+            st["rho_ms"].copy_(g("net.fading_rho_ms").float())
         self._last_snr = g("eng._last_snr").float().clone()
         self._last_hid = g("eng._last_hid").long().clone()
         if T is not None:
@@ -1238,6 +1276,10 @@ class HipNREngine:
             out[f"net.{name}.rv_tx"] = h[:, 1].clone()
             out[f"net.{name}.rv_fail"] = h[:, 2].clone()
             out[f"net.{name}.prb_used_env"] = c[:, 9].float()
+        if cfg.fading_doppler == "per_robot":          # the radio's last poses (radio.py:194-195)
+            out["radio.prev_pos"] = st["prev_pos"].clone()
+            out["radio.has_prev"] = st["has_prev"] != 0
+            out["per_robot_doppler"] = True
         out.update({"T": int(self.T), "net.last_g": self.last_g, "_uniform_epoch": self._uniform_epoch,
                     "E": E, "R": self.R, "F": self.F, "seed": self.seed,
                     "net.rng.s0": int(self._cparams.seed_key) & M32})
@@ -1272,6 +1314,8 @@ class HipNREngine:
             return bool(cfg.lena_mac_switches()) if cfg is not None else False
         if k == "net.fc_mode":
             return cfg.freq_corr_mode if cfg is not None else None
+        if k == "per_robot_doppler":
+            return cfg is not None and cfg.fading_doppler == "per_robot"
         return self._CK_OFF[k]
 
     def _strict_extra_keys(self, sd, used):
@@ -1333,6 +1377,9 @@ class HipNREngine:
                 raise KeyError("load_state_dict: state this engine does not run (strict): " + ", ".join(bad[:12]))
         if "net.rng.env" in sd:
             st["env_id"].copy_(g("net.rng.env").to(torch.int32))
+        if cfg.fading_doppler == "per_robot" and "radio.prev_pos" in sd and "radio.has_prev" in sd:
+            st["prev_pos"].copy_(g("radio.prev_pos").float())
+            st["has_prev"].copy_(g("radio.has_prev").to(torch.int32))
         for pre, fi in self._field_keys():
             if pre + ".k" in sd:
                 st["field"][:, :, fi, :, :2].copy_(g(pre + ".k").permute(1, 0, 2, 3))
@@ -1410,7 +1457,8 @@ class GraphStep:
         self.eng = eng
         self.counts = torch.zeros(E, R, n_cls, dtype=torch.uint8, device=dev)
         self.inputs = {}                      # input kind -> static input buffer
-        self.steps = {}                       # (schedule key incl. the kind, DL delay buffer) -> (graph, outputs)
+        self.vel = None                       # per-robot Doppler: the static velocity input [E,R,2]
+        self.steps = {}                       # (schedule key incl. the kind, DL delay buffer, vel) -> (graph, outputs)
         eng.st["clock"].fill_(eng.T)
         torch.cuda.synchronize(dev)
         self.g_submit = torch.cuda.CUDAGraph()
@@ -1419,38 +1467,46 @@ class GraphStep:
         self.hid = eng._last_hid              # the submit graph's hazard ids (zeros), read by the step graphs
         torch.cuda.synchronize(dev)
 
-    def _record(self, plan, kind):
+    def _record(self, plan, kind, use_vel):
         eng = self.eng
         x = self.inputs[kind]
         torch.cuda.synchronize(eng.dev)
         g = torch.cuda.CUDAGraph()
         ev, dev_ = eng.kernel_events, eng.dl_kernel_events
         eng.kernel_events = eng.dl_kernel_events = None
+        eng._cparams.vel = self.vel.data_ptr() if use_vel else None
         try:
             with torch.cuda.graph(g):
                 out = eng._launch_step(-1, plan, x, self.hid, (kind, x, 1) if eng.dl else None)
         finally:
             eng.kernel_events, eng.dl_kernel_events = ev, dev_
+            eng._cparams.vel = None
         torch.cuda.synchronize(eng.dev)
         return g, out
 
-    def __call__(self, x=None, counts=None, *, snr_db=None):
+    def __call__(self, x=None, counts=None, *, snr_db=None, vel=None):
         """One control step: counts [E,R,NC] uint8 messages per class (as submit_counts), then the step on poses
-        x [E,R,2|3], SNR x [E,R] or snr_db= [E,R,S] (with the downlink: its reference from the same input)."""
+        x [E,R,2|3], SNR x [E,R] or snr_db= [E,R,S] (with the downlink: its reference from the same input); vel=
+        [E,R,2|3] the velocity input of per-robot Doppler (as step)."""
         eng = self.eng
         T = eng.T
         kind, xin = eng._input(x, snr_db)
         eng._check_kind(kind)
+        vin = eng._vel_input(vel, kind)
+        if vin is not None:
+            if self.vel is None:
+                self.vel = torch.empty_like(vin)
+            self.vel.copy_(vin)
         if counts is None or tuple(counts.shape) != tuple(self.counts.shape):
             raise ValueError(f"counts must be {tuple(self.counts.shape)}")
         if kind not in self.inputs:
             self.inputs[kind] = torch.empty_like(xin)
         self.inputs[kind].copy_(xin)
         plan = eng._plan(T, kind)
-        key = (plan["key"], 0 if eng._dl_delay is None else eng._dl_delay.data_ptr())
+        key = (plan["key"], 0 if eng._dl_delay is None else eng._dl_delay.data_ptr(), vin is not None)
         hit = self.steps.get(key)
         if hit is None:
-            hit = self.steps[key] = self._record(plan, kind)
+            hit = self.steps[key] = self._record(plan, kind, vin is not None)
         g, out = hit
         self.counts.copy_(counts)
         eng.st["clock"].fill_(T)

@@ -27,7 +27,8 @@ robots, the 5G-LENA MAC switches: the per-RBG and frozen PF average, TDMA retran
 PRBs, whole-band UL power and UL power control at one cell; the stochastic LOS state, Rician K from it and per-link
 delay spreads), the downlink scenarios and the scenarios with two and three cells (A3 handovers with RLC carry and
 flush, the A3 admission floor a3_min_target_rsrp_dbm, Rician links, per-link delay spreads on every robot-cell link),
-each also with planted mistakes that the comparison catches. Not implemented here (refused): the "pf_wideband" /
+per-robot Doppler fading (speeds from poses or the velocity input, at one and two cells, with the downlink), each also
+with planted mistakes that the comparison catches. Not implemented here (refused): the "pf_wideband" /
 "wideband" PF metric.
 """
 from __future__ import annotations
@@ -368,6 +369,25 @@ class Radio:
             if cfg.tr38901_los == "stochastic":
                 self.cdf = sum_of_cosines_cdf(K)
         self.fields = self.draw()
+        self.prev_pos = self.has_prev = self.speed = None
+
+    def observe_motion(self, pos, vel=None):
+        """Per-robot speed [E,R] m/s (radio.py:285-300): |vel|, else |pos - previous pos| / control step (0 right
+        after a reset), floored at doppler_min_speed_mps; remembers the poses."""
+        pos = pos[..., :2]
+        if self.prev_pos is None:                    # RadioMC._alloc (radio.py:190-196)
+            self.prev_pos = torch.zeros(self.E, pos.shape[1], 2)
+            self.has_prev = torch.zeros(self.E, pos.shape[1], dtype=torch.bool)
+        floor = self.cfg.doppler_min_speed_mps
+        if vel is not None:
+            v = vel[..., :2].norm(dim=-1)
+        else:
+            v = (pos - self.prev_pos).norm(dim=-1) / (self.cfg.control_step_ms * 1e-3)
+            v = torch.where(self.has_prev, v, torch.zeros_like(v))
+        self.speed = v.clamp(min=floor)
+        self.prev_pos = pos.clone()
+        self.has_prev = torch.ones_like(self.has_prev)
+        return self.speed
 
     def draw(self):
         cfg, K, C = self.cfg, self.cfg.shadow_modes, self.C
@@ -385,6 +405,10 @@ class Radio:
         new = self.draw()
         self.fields = [(torch.where(m.view(1, -1, 1, 1), k2, k1), torch.where(m.view(1, -1, 1), p2, p1))
                        for (k1, p1), (k2, p2) in zip(self.fields, new)]
+        if self.has_prev is not None:                # radio.py:216-219
+            self.has_prev = self.has_prev & ~m[:, None]
+            self.speed = torch.where(m[:, None], torch.full_like(self.speed, self.cfg.doppler_min_speed_mps),
+                                     self.speed)
 
     def pathgain(self, pos):
         """Large-scale gain dB of the poses (radio.py:275-277): rx_dbm - ue_tx_dbm, [E,R] at one cell, [E,R,C]
@@ -709,7 +733,6 @@ class OracleEngine:
         assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
         assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
         assert not cfg.ul_tpc
-        assert cfg.fading_doppler == "global"
         assert cfg.rician_mode in (None, "fixed", "los")
         assert cfg.freq_corr_mode in (None, "fixed", "los")
         assert cfg.n_layers_max == 1 and cfg.ul_mini_slot_symbols is None and cfg.traffic is None
@@ -734,6 +757,8 @@ class OracleEngine:
             from isaac_net_amd.channels import scenario_name
             self.scn = scenario_name(cfg.tr38901_scenario)
         self.radio = None
+        # per-robot Doppler: net.fading_rho_ms [E,R], the global rho until a pose step sets it (doppler.py:32-37)
+        self.rho_ms = torch.full((E, R), float(cfg.fading_rho_per_ms)) if cfg.fading_doppler == "per_robot" else None
         self.T = 0
         self.epoch = torch.zeros(E, dtype=torch.long)
         self.uniform_epoch = 0
@@ -906,7 +931,7 @@ class OracleEngine:
         return acc
 
     # ---------------- step (engine.py:867-960, nr_engine.py:613-668) ----------------
-    def step(self, t=None, x=None, snr_db=None, dl_snr_db=None):
+    def step(self, t=None, x=None, snr_db=None, dl_snr_db=None, vel=None):
         cfg = self.cfg
         T = self.T
         self.dec.begin()
@@ -917,6 +942,7 @@ class OracleEngine:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
+            self._observe_motion(x, vel)
             if (self.rician == "los" or self.fc_los) and cfg.channel == "tr38901":   # every link's LOS state
                 los = self.radio.los if cfg.tr38901_los == "stochastic" else \
                     torch.full((self.E, self.R, self.C), cfg.tr38901_los == "los")
@@ -930,6 +956,7 @@ class OracleEngine:
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
             pg = self.radio.pathgain(x)
+            self._observe_motion(x, vel)
             if (self.rician == "los" or self.fc_los) and cfg.channel == "tr38901":
                 # the radio's LOS state (Radio.los_state, engine.py:853-861): fixed, or the stochastic draw
                 los = self.radio.los[..., 0] if cfg.tr38901_los == "stochastic" else \
@@ -965,6 +992,17 @@ class OracleEngine:
             out["serving_cell"] = torch.zeros(self.E, self.R, dtype=torch.long)
         out["t"] = (T - self.epoch).clone()
         return out
+
+    def _observe_motion(self, x, vel):
+        """Per-robot Doppler of a pose step (engine.py:862-864): rho_ms = J0(2 pi 2.5 ms f_D)^(1 / 2.5) with
+        f_D = v f_c / c, 0 from the first zero of J0 on (channels/doppler.py:23-29)."""
+        if self.rho_ms is None:
+            return
+        speed = self.radio.observe_motion(x, vel)
+        fd = speed * (self.cfg.carrier_ghz * 1e9 / 299_792_458.0)
+        xj = 2 * math.pi * 2.5 * 1e-3 * fd
+        j0 = torch.where(xj >= 2.404825557695773, torch.zeros_like(xj), torch.special.bessel_j0(xj))
+        self.rho_ms = j0.clamp(0.0, 1.0) ** (1 / 2.5)
 
     def _rel(self, x):
         shape = (-1,) + (1,) * (x.dim() - 1)
@@ -1087,8 +1125,13 @@ class OracleEngine:
             z = self.rng.step_normal(FADING, rel, self.h[0].numel()).view(self.h.shape)
             if self.fc_L is not None or self.fc_los:     # z <- L z across the subbands (nr_engine.py:366-368, 581-582)
                 z = self._fc_mat() @ z
-            rho = self.cfg.fading_rho_per_ms ** (dt * self.cfg.slot_ms)
-            self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
+            if self.rho_ms is None:
+                rho = self.cfg.fading_rho_per_ms ** (dt * self.cfg.slot_ms)
+                self.h = rho * self.h + math.sqrt(1 - rho ** 2) * z / math.sqrt(2)
+            else:                                        # per-robot Doppler (nr_engine.py:586-589)
+                r = self.rho_ms
+                rho = (r ** (dt * self.cfg.slot_ms)).reshape(*r.shape, *([1] * (self.h.dim() - 2)))
+                self.h = rho * self.h + torch.sqrt(1 - rho ** 2) * z / math.sqrt(2)
         self.last_g = g
 
     def _fc_mat(self):
@@ -1520,6 +1563,8 @@ class OracleEngine:
             items += [(f"{lk.dir}.{k}", lk, v) for k, v in keys.items()]
         if self.dl is not None:
             items.append(("net.dl_newest", self, "dl_newest"))
+        if self.rho_ms is not None:
+            items.append(("net.fading_rho_ms", self, "rho_ms"))
         if self.fc_los:
             items += [(k, self, k[4:]) for k in ("net.fc_idx", "net.fc_idx_los", "net.fc_idx_nlos")]
         if self.rician:

@@ -365,6 +365,26 @@ CASES = {
                         E=3, R=16, steps=40, kind="pose", arena=300.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
     # two cells with per-link delay spreads (fading_delay_spread_ns None): each robot-cell link's own lgDS draws, the
     # LOS or NLOS grid index by that link's stochastic LOS state (nr_engine.py:320-381), UMi, 13 RBGs
+    # per-robot Doppler (fading_doppler="per_robot": engine.py:862-864, radio.py:285-300, channels/doppler.py:23-29,
+    # nr_engine.py:583-589): speeds from consecutive poses, 0 .. 25 m/s (J0 reaches its first zero near 13 m/s at
+    # 3.5 GHz, rho 0 from there), a 0.5 m/s floor
+    "dop": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0, 300.0), fading_doppler="per_robot",
+                         doppler_min_speed_mps=0.5, cell_positions_m=((100.0, 100.0),)),
+                E=3, R=16, steps=30, kind="pose", arena=200.0, walk_max=0.25, rates=(0.8, 0.5), resets={14: [1]}),
+    # the velocity input (vel=, |v| of normal components with sigma 8 m/s) with the downlink and Rician K on UMi LOS
+    "dop_vel_dl": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=4,
+                                max_harq_tx=3, frame_buffer=8, msg_sizes=(2000.0,), fading_doppler="per_robot",
+                                fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi",
+                                tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0, dl=True),
+                       E=3, R=8, steps=25, kind="pose", arena=200.0, walk=1.0, vel=8.0, rates=(0.8,),
+                       dl_sizes=(4000.0,), dl_rates=(0.6,), resets={11: [2]}),
+    # two cells, every robot-cell link with the robot's correlation, a 1 m/s floor
+    "mc2_dop": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                             max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2, cell_layout="hex",
+                             cell_isd_m=150.0, noise_model="thermal", fading_doppler="per_robot",
+                             doppler_min_speed_mps=1.0),
+                    E=2, R=16, steps=25, kind="pose", arena=300.0, walk_max=0.3, rates=(0.7,), resets={12: [1]}),
     "mc2_fcorr_los": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
                                    n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2,
                                    cell_layout="hex", cell_isd_m=150.0, noise_model="thermal",
@@ -511,7 +531,9 @@ def _inputs(name, c):
         for _ in range(T):
             xs.append(p.copy())
             ang = rs.uniform(0.0, 2 * math.pi, size=(E, R))
-            p = np.clip(p + c["walk"] * np.stack([np.cos(ang), np.sin(ang)], -1), 0.0, a)
+            # walk_max: a step length per robot and step, uniform in [0, walk_max] (robots of different speeds)
+            w = c["walk"] if "walk_max" not in c else rs.uniform(0.0, c["walk_max"], size=(E, R))[..., None]
+            p = np.clip(p + w * np.stack([np.cos(ang), np.sin(ang)], -1), 0.0, a)
         x = np.stack(xs).astype(np.float32)
     elif c["kind"] == "snr":
         lo, hi = c["snr"]
@@ -527,6 +549,14 @@ def _inputs(name, c):
     return x, counts
 
 
+def _vel(name, c):
+    """The velocity input [T,E,R,2] float32 (m/s, normal with sigma c["vel"] per axis) of a case with one, else None."""
+    if "vel" not in c:
+        return None
+    rs = np.random.default_rng(int.from_bytes(hashlib.sha256((name + ":vel").encode()).digest()[:4], "little"))
+    return rs.normal(0.0, c["vel"], size=(c["steps"], c["E"], c["R"], 2)).astype(np.float32)
+
+
 def _np(v):
     """A copy (the reference updates some state tensors in place: rng counters, episode, epoch)."""
     return np.array(v.detach().cpu().numpy(), copy=True)
@@ -539,12 +569,15 @@ def run_case(name, c):
     eng = make_engine("L2", E, R, "cpu", cfg, backend="reference", seed=0, strict=None)
     x, counts, *dl = _inputs(name, c)
     dl_counts = dl[0] if dl else None
+    vel = _vel(name, c)
     out = {"x": x, "counts": counts, "E": np.int64(E), "R": np.int64(R), "steps": np.int64(T),
            "cfg_json": np.frombuffer(json.dumps(c["cfg"]).encode(), dtype=np.uint8),
            "kind": np.frombuffer(c["kind"].encode(), dtype=np.uint8)}
     if dl_counts is not None:
         out["dl_counts"] = dl_counts
         out["dl_sizes"] = np.asarray(c["dl_sizes"], dtype=np.float32)
+    if vel is not None:
+        out["vel"] = vel
     reset_mask = np.zeros((T, E), dtype=np.bool_)
     for s, ids in c["resets"].items():
         reset_mask[s, ids] = True
@@ -593,7 +626,7 @@ def run_case(name, c):
                     eng.add_dl_frames(None, nb, torch.where(n > i, torch.full_like(n, ci + 1), torch.zeros_like(n)))
         xs = torch.from_numpy(x[s])
         if c["kind"] == "pose":
-            o = eng.step(None, xs)
+            o = eng.step(None, xs, vel=None if vel is None else torch.from_numpy(vel[s]))
         elif c["kind"] == "snr":
             o = eng.step(None, xs)
         else:

@@ -23,7 +23,10 @@ FLOAT_TOL = {"ul.csi": 1e-5, "net.h": 1e-5, "net.spec": 1e-5, "eng._last_snr": 1
              # several cells: each gNB's N+I estimate and its I/N statistic. The interference terms are
              # 10^(x / 10) of dB sums x = psd + gain around -100 dB, where one float32 ulp of x (7.6e-6 dB) is
              # 1.75e-6 relative in mW; x carries a few ulp from the path gain, the power split and the fading gain
-             "net.ni_ul": 5e-5, "net.ioN[ul]": 5e-5}
+             "net.ni_ul": 5e-5, "net.ioN[ul]": 5e-5,
+             # per-robot Doppler: the correlation per ms J0(...)^0.4 in [0, 1], where torch's CPU pow (SLEEF's) is
+             # within an ulp of the device's correctly rounded one (tests/test_doppler.py): 1e-6 absolute
+             "net.fading_rho_ms": 1e-6}
 OUT_TOL = {"sinr_db": 1e-5, "delay": 0.0, "queue_bytes": 0.0}
 # The reported SINR is (pg + ue_tx) - noise with |pg| ~ 100-150 dB: one float32 ulp there is 7.6e-6 .. 1.5e-5 dB,
 # so near 0 dB a relative bound is meaningless; the absolute floor is 4 ulp of that magnitude.
@@ -197,7 +200,8 @@ def teacher_forced(P, name, dev="cuda:0"):
         for nb, cls in replay.dl_frames(ref, s):
             eng.add_dl_frames(None, to(nb), to(cls))
         x = to(ref["x"][s])
-        o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x)
+        vel = to(ref["vel"][s]) if "vel" in ref.files else None
+        o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x, vel=vel)
         set_radio_bound(ref, s, cfg, eng, kind)
         bi, bf, robots = compare(ref, s, o, eng.owner_state(), E, R)
         n_bad += int(robots.sum())

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     lib.inet_nr_abi_version.restype = ctypes.c_int32
-    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 14
+    assert lib.inet_nr_abi_version() == _lib.ABI_VERSION == 15
     lib.inet_nr_build_info.restype = ctypes.c_char_p
     assert b"gfx950" in lib.inet_nr_build_info()
     wifi = declared_functions(WIFI_HEADER, "inet_wifi_")

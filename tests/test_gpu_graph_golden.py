@@ -34,7 +34,8 @@ def test_graph_replay_matches_reference(name):
             eng.add_dl_frames(None, to(nb), to(cls))
         cnt = to(ref["counts"][s].astype(np.uint8))
         x = to(ref["x"][s])
-        o = g(counts=cnt, snr_db=x) if kind == "snr3" else g(x, cnt)
+        vel = to(ref["vel"][s]) if "vel" in ref.files else None
+        o = g(counts=cnt, snr_db=x) if kind == "snr3" else g(x, cnt, vel=vel)
         torch.cuda.synchronize()
         set_radio_bound(ref, s, cfg, eng, kind)
         bi, bf, _ = compare(ref, s, o, eng.owner_state(), E, R)

@@ -52,7 +52,10 @@ def test_oracle_bitwise_vs_reference(name):
                                               ("mc2_lena", "ul_retx_sched", "ofdma"),
                                               ("fcorr", "fading_delay_spread_ns", 3000.0),
                                               ("fcorr_mc2", "fading_delay_spread_ns", 300.0),
-                                              ("rice_sto_slow", "rician_k_ramp_slots", 4)])
+                                              ("rice_sto_slow", "rician_k_ramp_slots", 4),
+                                              ("dop", "fading_doppler", "global"),
+                                              ("dop", "doppler_min_speed_mps", 0.0),
+                                              ("mc2_dop", "carrier_ghz", 3.6)])
 def test_switch_trajectories_pin_the_switch(name, field, wrong):
     """The TDMA retransmission, previous-PUSCH AMC, frequency-correlated fading and K-ramp trajectories depend on
     their switch: the oracle run with the switch at another value diverges from them (so the bitwise comparison above pins
