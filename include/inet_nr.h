@@ -186,7 +186,9 @@ typedef struct InetNrParams {
     int32_t k_ramp;                   /* k_from_los: rician_k_ramp_slots (0: a new target applies at once) */
     int32_t fc_G;                     /* fc_on 2: grid points of fc_tab (fading_ds_grid) */
     int32_t doppler;                  /* per-robot Doppler (InetNrState.rho_ms; ABI 15) */
-    int32_t pad_d;
+    int32_t pf_wb;                    /* the wideband rate in the scheduler's metric (pf_metric "wideband", scheduler
+                                         "pf_wideband"; mac.py:259-264; ABI 15): every RBG gets the rate of the highest
+                                         MCS whose effective SINR over all RBGs reaches its threshold */
     float olla_up, olla_dn, pf_a, pf_b, target, phr_min, snr_ref_prbs, w0;
     float ref_off, noise_prb, ue_tx, subband_noise;   /* ul_ref = (pg + ref_off) - noise_prb; snr = (pg + ue_tx) - subband_noise */
     /* radio constants (float32 values of the reference's Python doubles) */

@@ -35,7 +35,7 @@ class InetNrParams(C.Structure):
         "fading", "purge", "input_kind", "radio_model", "out_ref", "max_tx", "sr_delay", "ul_rtt", "rlc_retx",
         "timeout", "tb_oh", "n_fields", "n_modes", "seed_key", "n_data", "n_cells", "rebase_at", "pf_rbg", "pf_freeze",
         "whole_band", "pc1_on", "retx_tdma", "amc_prev", "fc_on", "k_from_los", "los_sto", "plos_scn", "k_ramp", "fc_G",
-        "doppler", "pad_d")] + \
+        "doppler", "pf_wb")] + \
                [(n, f32) for n in (
         "olla_up", "olla_dn", "pf_a", "pf_b", "target", "phr_min", "snr_ref_prbs", "w0", "ref_off", "noise_prb",
         "ue_tx", "subband_noise", "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1",

@@ -328,7 +328,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         pm.sched = 0; pm.comb = 1; pm.eesm = 1; pm.harq_drop = 0; pm.olla = 1; pm.phr_cap = 1; pm.retx_prio = 1;
         pm.rician = FX == 1 ? 1 : 0; pm.fading = 1;
         pm.pf_rbg = 0; pm.pf_freeze = 0; pm.whole_band = 0; pm.pc1_on = 0; pm.retx_tdma = 0; pm.amc_prev = 0;
-        pm.fc_on = 0; pm.los_sto = 0; pm.k_from_los = 0; pm.doppler = 0;
+        pm.fc_on = 0; pm.los_sto = 0; pm.k_from_los = 0; pm.doppler = 0; pm.pf_wb = 0;
     }
     constexpr bool DL = !std::is_same<LS, InetNrState>::value;
     // the link whose MAC state the kernel runs: the UL link is the shared state itself (one set of pointers)
@@ -1185,12 +1185,58 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             const unsigned long long bm = __ballot(bid0);
             const int n_b = __popcll(bm);
             if (bid0) s_la_slot[wbase + __popcll(bm & ((1ull << wl) - 1ull))] = lane;
-            __syncthreads();
             // highest m <= mcs_max with eo >= thr[m] (0 when none, or NaN): a binary search over the suffix minima,
             // whose first three levels compare with seven values held by every lane, then a count of the values
-            // passed in the last block of four and a branch-free selection of the spectral efficiency
+            // passed in the last block of four
             const float t16 = s_thrs[16], t8 = s_thrs[8], t24 = s_thrs[24];
             const float t4 = s_thrs[4], t12 = s_thrs[12], t20 = s_thrs[20], t28 = s_thrs[28];
+            auto mcs_search = [&](float e) -> int {
+                int m = e >= t16 ? 16 : 0;
+                m += e >= (m ? t24 : t8) ? 8 : 0;
+                m += e >= (m < 16 ? (m < 8 ? t4 : t12) : (m < 24 ? t20 : t28)) ? 4 : 0;
+                return m + (e >= s_thrs[m + 1] ? 1 : 0) + (e >= s_thrs[m + 2] ? 1 : 0) + (e >= s_thrs[m + 3] ? 1 : 0);
+            };
+            // the wideband rate (mac.py:259-264): the MCS of every bidding robot from its effective SINR over every
+            // RBG (general build only), into s_la_top (free until link adaptation)
+            const bool wbr = FX == 0 && pm.pf_wb != 0;
+            if (wbr) {
+                const uint32_t all = (1u << S) - 1u;
+                const float lnw_all = lw_eq ? s_lnw[S] : lse_logw<S>(s_logw, all);
+                if (!pm.eesm) {
+                    // mean_db: the PRB-weighted mean of the estimate over every RBG, then the highest MCS it reaches
+                    if (bid0) s_la_top[lane] = mcs_search(mean_db_held<S, CW>(s_eo, lane, s_logw, all, lnw_all));
+                } else {
+                    // EESM: for every MCS m <= mcs_max, -beta_m (lse_s((-lin_s) / beta_m + log w_s) - lnw) in dB
+                    // against thr_ref[m]; the (robot, MCS) items are dealt over the wavefront and each passing item
+                    // sets its bit in the robot's mask (an LDS atomic OR); the robot takes the highest bit (0: none)
+                    bool nanr = false;
+                    if (bid0) {
+#pragma unroll
+                        for (int s2 = 0; s2 < S; ++s2) {
+                            const float x = s_eo[s2 * CW + lane];
+                            nanr |= x != x;
+                            s_lin[s2 * CW + lane] = from_db_mid(clampf(x, -30.0f, 60.0f));
+                        }
+                    }
+                    s_la_top[lane] = 0;
+                    s_la_i[lane] = nanr ? 1 : 0;
+                    __syncthreads();
+                    const int nm = tb.mcs_max + 1;
+#pragma unroll 1
+                    for (int it = wl; it < n_b * nm; it += STEP_WAVE) {
+                        const int mi = it / n_b, L = s_la_slot[wbase + (it - mi * n_b)];
+                        const float beta = s_beta[mi];
+                        const float eff = db_of((-beta) * (lse_eesm<S>([&](int s2) { return s_lin[s2 * CW + L]; },
+                                                                         s_logw, all, beta, s_rbeta[mi],
+                                                                         s_la_i[L] != 0) - lnw_all));
+                        if (eff >= s_thr[mi]) atomicOr(&s_la_top[L], 1 << mi);
+                    }
+                    __syncthreads();
+                    const int mk = s_la_top[lane];
+                    if (bid0) s_la_top[lane] = mk ? 31 - __builtin_clz((uint32_t)mk) : 0;
+                }
+            }
+            __syncthreads();
             const int items = n_b * S;
             int q = 0, ri = 0, dq = 0, dr = 0;
             if (n_b > 0) {
@@ -1206,6 +1252,14 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                 ri += dr;
                 if (ri >= n_b) { ri -= n_b; ++q; }
                 const float e = s_eo[qc * CW + L];
+                if (wbr) {
+                    // the wideband rate: (se[m] re_prb / 8) w_s, in the reference's order
+                    const float rt = ((s_se[s_la_top[L]] * row.re_prb) / 8.0f) * s_w[qc];
+                    const float a = s_la_f[L];
+                    s_met[qc * CW + L] = pm.sched == 0 ? DivBy(a)(rt) : (pm.sched == 1 ? rt : a);
+                    s_rt[qc * CW + L] = rt;
+                    continue;
+                }
                 int m = e >= t16 ? 16 : 0;
                 m += e >= (m ? t24 : t8) ? 8 : 0;
                 m += e >= (m < 16 ? (m < 8 ? t4 : t12) : (m < 24 ? t20 : t28)) ? 4 : 0;
@@ -2143,7 +2197,7 @@ void launch_step(const StepArgs& a) {
 inline int fx_profile(const InetNrParams& p) {
     const bool common = p.pf_rbg == 0 && p.pf_freeze == 0 && p.whole_band == 0 && p.pc1_on == 0 &&
                         p.retx_tdma == 0 && p.amc_prev == 0 && p.fc_on == 0 && p.los_sto == 0 && p.k_from_los == 0 &&
-                        p.doppler == 0 &&
+                        p.doppler == 0 && p.pf_wb == 0 &&
                         p.sched == 0 && p.comb == 1 && p.eesm == 1 && p.harq_drop == 0 && p.olla == 1 &&
                         p.phr_cap == 1 && p.retx_prio == 1 && p.fading == 1;
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;

@@ -91,10 +91,10 @@ def refusals(cfg: NRConfig):
     no(cfg.ul_grant_model != "lumped", "ul_grant_model='bsr'", "lumped SR grants only")
     no(cfg.n_layers_max != 1, "rank-2 MIMO", "single-layer TBs")
     no(cfg.ul_mini_slot_symbols is not None, "mini-slot grants", "one scheduling occasion per slot")
-    no(cfg.scheduler not in ("pf", "maxci", "rr"), f"scheduler={cfg.scheduler!r}", "pf, maxci and rr")
-    no(cfg.pf_metric != "subband", "pf_metric='wideband'", "per-RBG PF metric")
-    no(cfg.pf_update == "rbg" and cfg.scheduler != "pf", "pf_update='rbg' without the PF scheduler",
-       "the per-RBG PF update of the pf scheduler")
+    no(cfg.scheduler not in ("pf", "pf_wideband", "maxci", "rr"), f"scheduler={cfg.scheduler!r}",
+       "pf, pf_wideband, maxci and rr")
+    no(cfg.pf_update == "rbg" and cfg.scheduler not in ("pf", "pf_wideband"),
+       "pf_update='rbg' without a PF scheduler", "the per-RBG PF update of the pf schedulers")
     no(cfg.ul_tpc, "closed-loop TPC (ul_tpc)", "open-loop fractional power control")
     no(cfg.freq_corr_mode == "los" and (cfg.channel != "tr38901" or
                                         scenario_name(cfg.tr38901_scenario) not in ("UMi", "UMa", "InH")),
@@ -327,7 +327,8 @@ class HipNREngine:
         cfg = self.config
         p = _lib.InetNrParams()
         p.E, p.R, p.S, p.P, p.F, p.N = self.E, self.R, self.S, self.P, self.F, self.N
-        p.sched = {"pf": 0, "maxci": 1, "rr": 2}[cfg.scheduler]
+        p.sched = {"pf": 0, "pf_wideband": 0, "maxci": 1, "rr": 2}[cfg.scheduler]
+        p.pf_wb = int(cfg.pf_metric == "wideband" or cfg.scheduler == "pf_wideband")   # (mac.py:259)
         p.comb = {"none": 0, "cc": 1, "ir_lena": 2}[cfg.harq_combining]
         p.eesm = int(cfg.eff_sinr == "eesm")
         p.harq_drop = int(cfg.harq_fail == "drop")

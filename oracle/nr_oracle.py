@@ -27,9 +27,9 @@ robots, the 5G-LENA MAC switches: the per-RBG and frozen PF average, TDMA retran
 PRBs, whole-band UL power and UL power control at one cell; the stochastic LOS state, Rician K from it and per-link
 delay spreads), the downlink scenarios and the scenarios with two and three cells (A3 handovers with RLC carry and
 flush, the A3 admission floor a3_min_target_rsrp_dbm, Rician links, per-link delay spreads on every robot-cell link),
-per-robot Doppler fading (speeds from poses or the velocity input, at one and two cells, with the downlink), each also
-with planted mistakes that the comparison catches. Not implemented here (refused): the "pf_wideband" /
-"wideband" PF metric.
+per-robot Doppler fading (speeds from poses or the velocity input, at one and two cells, with the downlink) and the
+wideband rate of the PF metric (pf_metric="wideband", scheduler="pf_wideband"), each also with planted mistakes that
+the comparison catches.
 """
 from __future__ import annotations
 
@@ -730,8 +730,8 @@ class OracleEngine:
         self.C = C = cfg.n_cells
         assert cfg.ul and cfg.ul_grant_model == "lumped"
         assert C == 1 or not (cfg.dl or cfg.rlf), "several cells: uplink only, no radio link failure"
-        assert cfg.scheduler in ("pf", "maxci", "rr") and cfg.pf_metric == "subband"
-        assert cfg.pf_update == "slot" or cfg.scheduler == "pf", "pf_update='rbg' needs the PF scheduler"
+        assert cfg.scheduler in ("pf", "pf_wideband", "maxci", "rr")
+        assert cfg.pf_update == "slot" or cfg.scheduler in ("pf", "pf_wideband"), "pf_update='rbg' needs a PF scheduler"
         assert not cfg.ul_tpc
         assert cfg.rician_mode in (None, "fixed", "los")
         assert cfg.freq_corr_mode in (None, "fixed", "los")
@@ -1288,7 +1288,16 @@ class OracleEngine:
             n_max = torch.full((E, R), S, dtype=torch.long)
         est_o = est + (L.olla[..., None] if cfg.olla else 0.0)
         re_prb = float(min(12 * nsym - cfg.dmrs_re_per_prb - cfg.overhead_re_per_prb, 156))
-        rate_sb = phy.se[phy.mcs_at(est_o, self.dec)] * re_prb * w / 8
+        if cfg.pf_metric == "wideband" or cfg.scheduler == "pf_wideband":
+            # the wideband rate (mac.py:259-264): the highest MCS whose effective SINR over every RBG reaches its
+            # threshold, its rate spread over the RBGs by their PRBs
+            wb = phy.eff_sinr_all(est_o, torch.ones(E, R, S, dtype=torch.bool), cfg.eff_sinr, w)
+            ge = (lambda a, b: self.dec.cmp("wb", a, b)) if self.dec is not None else _ge
+            ok = ge(wb, phy.thr_ref) & (torch.arange(phy.M) <= phy.mcs_max)
+            m = (ok.long() * torch.arange(1, phy.M + 1)).max(-1).values.clamp(min=1) - 1
+            rate_sb = (phy.se[m] * re_prb / 8)[..., None] * w
+        else:
+            rate_sb = phy.se[phy.mcs_at(est_o, self.dec)] * re_prb * w / 8
         if cfg.scheduler == "maxci":
             metric_sb = rate_sb
         elif cfg.scheduler == "rr":

@@ -58,12 +58,12 @@ def pytest_collection_modifyitems(config, items):
 CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14", "s18_ir", "s10_w2", "lena_pf",
          "wb_pc", "pc1", "w4", "tdma", "amc_prev", "lena_v2", "wb_amc", "fcorr", "fcorr_w2",
          "rice_los", "rice_snr", "los_sto", "rice_sto", "rice_sto_slow",
-         "fcorr_los", "fcorr_los_rice", "sto64", "sto100", "dop"]
+         "fcorr_los", "fcorr_los_rice", "sto64", "sto100", "dop", "wb_pf", "wb_maxci_md"]
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl", "fcorr_dl", "rice_los_dl", "los_sto_dl",
-            "rice_sto_dl", "fcorr_los_dl", "dop_vel_dl"]
+            "rice_sto_dl", "fcorr_los_dl", "dop_vel_dl", "pfwb_dl"]
 MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc", "mc2_rice",
             "mc3_rice_sto", "mc3_flush", "mc3_a3floor", "mc2_fcorr_los", "mc3_rice64", "mc3_rice48",
-            "mc3_ho48", "mc3_rice48c", "mc3_rice32", "mc2_dop"]
+            "mc3_ho48", "mc3_rice48c", "mc3_rice32", "mc2_dop", "mc2_wb"]
 # several cells (NRConfig(n_cells=3 / 2)), uplink; mc3_flush: ho_rlc="flush"; mc3_a3floor: the A3 admission floor;
 # mc2_fcorr_los: per-link delay spreads; mc3_rice64 / mc3_rice48: Rician links on 64- and 48-robot envs

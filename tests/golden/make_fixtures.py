@@ -365,6 +365,29 @@ CASES = {
                         E=3, R=16, steps=40, kind="pose", arena=300.0, walk=6.0, rates=(0.5, 1.0), resets={25: [0]}),
     # two cells with per-link delay spreads (fading_delay_spread_ns None): each robot-cell link's own lgDS draws, the
     # LOS or NLOS grid index by that link's stochastic LOS state (nr_engine.py:320-381), UMi, 13 RBGs
+    # the wideband rate in the PF metric (mac.py:259-264): pf_metric="wideband" on per-subband SNR (RBGs of different
+    # SINR, so the wideband MCS differs from the per-RBG ones), the per-RBG PF update, 16 robots
+    "wb_pf": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="pf", pf_metric="wideband",
+                           pf_update="rbg", n_harq=4, max_harq_tx=3, frame_buffer=8, msg_sizes=(2500.0, 400.0),
+                           fading_rho_per_ms=0.7),
+                  E=3, R=16, steps=30, kind="snr3", snr=(-4.0, 18.0), rates=(0.8, 0.6), resets={15: [2]}),
+    # scheduler="pf_wideband" with the downlink, poses on UMi LOS, Rician K
+    "pfwb_dl": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf_wideband",
+                             n_harq=4, max_harq_tx=3, frame_buffer=8, msg_sizes=(2000.0,), fading_rician=True,
+                             rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                             cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0, dl=True),
+                    E=3, R=8, steps=25, kind="pose", arena=200.0, walk=1.0, rates=(0.8,), dl_sizes=(4000.0,),
+                    dl_rates=(0.6,), resets={11: [2]}),
+    # the wideband rate under max C/I with the mean-dB effective SINR, log-distance radio
+    "wb_maxci_md": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", pf_metric="wideband",
+                                 eff_sinr="mean_db", n_harq=4, max_harq_tx=4, frame_buffer=10, msg_sizes=(1500.0,),
+                                 cell_positions_m=((60.0, 60.0),), fading_rho_per_ms=0.5),
+                        E=3, R=8, steps=25, kind="pose", arena=150.0, walk=1.0, rates=(1.0,), resets={12: [0]}),
+    # two cells, pf_wideband: one wideband PF scheduler per cell
+    "mc2_wb": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf_wideband",
+                            n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2,
+                            cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", fading_rho_per_ms=0.5),
+                   E=2, R=16, steps=25, kind="pose", arena=300.0, walk=1.0, rates=(0.7,), resets={12: [1]}),
     # per-robot Doppler (fading_doppler="per_robot": engine.py:862-864, radio.py:285-300, channels/doppler.py:23-29,
     # nr_engine.py:583-589): speeds from consecutive poses, 0 .. 25 m/s (J0 reaches its first zero near 13 m/s at
     # 3.5 GHz, rho 0 from there), a 0.5 m/s floor

@@ -55,7 +55,9 @@ def test_oracle_bitwise_vs_reference(name):
                                               ("rice_sto_slow", "rician_k_ramp_slots", 4),
                                               ("dop", "fading_doppler", "global"),
                                               ("dop", "doppler_min_speed_mps", 0.0),
-                                              ("mc2_dop", "carrier_ghz", 3.6)])
+                                              ("mc2_dop", "carrier_ghz", 3.6),
+                                              ("wb_pf", "pf_metric", "subband"),
+                                              ("mc2_wb", "scheduler", "pf")])
 def test_switch_trajectories_pin_the_switch(name, field, wrong):
     """The TDMA retransmission, previous-PUSCH AMC, frequency-correlated fading and K-ramp trajectories depend on
     their switch: the oracle run with the switch at another value diverges from them (so the bitwise comparison above pins
