@@ -296,6 +296,24 @@ typedef struct InetNrCells {
     float ref_db;                       /* 10 log10(snr_ref_prbs) */
     float li_a, li_b;                   /* N+I EWMA: li_a * now + li_b * estimate (li_b = 0: the measurement) */
     float pc_p0, pc_alpha;              /* power control: backoff = ue_tx - (p0 + alpha (ue_tx - rx_serving)) */
+    /* Radio link failure (cfg.rlf; CellAssociation, radio.py:456-531, NRNet._rlf_events / _rlf_links,
+       nr_engine.py:684-707; ABI 15). Per robot [E][R]: in RLF, out-of-sync / in-sync counts, the slots at which
+       T310, T311 and the re-establishment end (-1: not running), the re-establishment cell, RLFs since the reset.
+       Once per step, at its first slot, before the A3 plan: T311 expiry (the robot goes idle: its queue is flushed),
+       the cell search of the robots in RLF, the indications of the connected ones (serving SINR < qout:
+       out-of-sync, > qin: in-sync) and T310 start (n310 out-of-sync in a row) / stop (n311 in-sync). At every
+       scheduled slot and after the last one: T310 expiries (RLF: unschedulable, T311 starts, the search runs, the
+       link's MAC restarts as at a handover, flushed with rlf_flush) unless a handover precedes them, then the
+       re-establishments due (the robot attaches to the selected cell, the MAC restarts unflushed). A handover stops
+       T310. The search takes the max-RSRP cell with SINR estimate >= qin (and RSRP above the floor when set); the
+       re-establishment completes reest slots later. Counters [E][5] int64 (rlf, reest, rlf_idle, t310_start,
+       t310_stop), cleared by a full reset only; out_rlf [E][R] uint8: in RLF after the step (the "rlf" output). */
+    int32_t *rlf_active, *oos_cnt, *is_cnt, *t310_end, *t311_end, *reest_end, *reest_cell, *n_rlf;
+    int64_t *rlf_ctr;
+    uint8_t *out_rlf;
+    int32_t rlf, rlf_flush, n310, n311, t310, t311, reest;
+    float qout, qin;
+    int32_t pad_r;
 } InetNrCells;
 
 /* Library version (INET_NR_ABI_VERSION) and a short build string. */
@@ -358,7 +376,8 @@ int32_t inet_nr_dl_submit(const InetNrState *st, const InetNrDlState *dl, const 
 int32_t inet_nr_dl_reset(const InetNrDlState *dl, const InetNrParams *prm, const uint8_t *mask, void *stream);
 
 /* One control step T with several cells (NRNet.step_cells, nr_engine.py:718-788, uplink): per robot the path gain to
-   every cell from its pose (x: poses [E][R][2]), the max-RSRP association of the envs flagged pending, the A3 plan of
+   every cell from its pose (input_kind 0, x: poses [E][R][2]) or as given (input_kind 3, x: path gain [E][R][C] dB,
+   step(pathgain_db=), engine.py:909-915: no radio, so no LOS state and no motion), the max-RSRP association of the envs flagged pending, the A3 plan of
    the step (the slot at which a handover fires); per scheduled slot the handovers due by that slot (CellAssociation
    switch, UlMac.handover: mac_ul.py:238-247, mac.py:557-581), AR(1) fading on every robot-cell link, one scheduler
    per cell over the same RBGs (mac.py:278-379 with member masks), the robots in a handover interruption left out,
@@ -367,7 +386,7 @@ int32_t inet_nr_dl_reset(const InetNrDlState *dl, const InetNrParams *prm, const
    then the handovers due after the last slot and the end of step as inet_nr_step. sinr_db is the serving link's
    full-power SINR against the serving gNB's estimate (serving_sinr_db, nr_engine.py:709-713); serving_cell the
    serving cell. arr: this step's arrivals as inet_nr_submit_step, or NULL. Needs prm->n_cells == cells->C > 1,
-   poses input (input_kind 0), no Rician fading and F <= 64. No counterpart in the reference's triton backend, which
+   input_kind 0 or 3 and F <= 64. No counterpart in the reference's triton backend, which
    runs one cell (nr_fast.py:538-554 refuses n_cells > 1); the reference path is the eager NRNet.step_cells. */
 int32_t inet_nr_step_cells(const InetNrState *st, const InetNrCells *cells, const InetNrTables *tab,
                            const InetNrParams *prm, const InetNrRow *rows, int32_t n_rows, int64_t T, const float *x,

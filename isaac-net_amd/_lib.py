@@ -66,7 +66,11 @@ class InetNrCells(C.Structure):
                [("gnb_xy", f32 * (2 * MAX_C))] + \
                [(n, i32) for n in ("C", "ttt", "ho_int", "ho_flush", "use_int", "pc_on", "has_floor")] + \
                [(n, f32) for n in ("a3_off", "a3_hyst", "floor_rx", "noise_mw", "ref_db", "li_a", "li_b", "pc_p0",
-                                   "pc_alpha")]
+                                   "pc_alpha")] + \
+               [(n, P) for n in ("rlf_active", "oos_cnt", "is_cnt", "t310_end", "t311_end", "reest_end", "reest_cell",
+                                 "n_rlf", "rlf_ctr", "out_rlf")] + \
+               [(n, i32) for n in ("rlf", "rlf_flush", "n310", "n311", "t310", "t311", "reest")] + \
+               [("qout", f32), ("qin", f32), ("pad_r", i32)]
 
 
 class InetNrArrivals(C.Structure):

@@ -92,14 +92,6 @@ REFERENCE_ONLY_DEFAULTS = {
     'ul_tpc_steps_db': None,
     'ul_tpc_delay_slots': None,
     'ul_tpc_range_db': 20.0,
-    'rlf_qout_db': -8.0,
-    'rlf_qin_db': -6.0,
-    'n310': 1,
-    'n311': 1,
-    't310_ms': 1000.0,
-    't311_ms': 3000.0,
-    'reest_delay_ms': 40.0,
-    'rlf_rlc': None,
     'rach_occasion_slots': 20,
     'rach_preambles': 64,
     'rach_rar_window_slots': 10,
@@ -248,7 +240,18 @@ class NRConfig:
     ho_interruption_ms: float = 40.0  # a robot is not scheduled for this long after its handover
     ho_rlc: str = "carry"             # "carry": queued frames continue at the target; "flush": they are dropped
     a3_min_target_rsrp_dbm: float | None = None
+    # radio link failure (config.py:718-731): the serving-link SINR against Qout / Qin once per control step; n310
+    # out-of-sync in a row start T310, n311 in-sync in a row stop it; at T310 expiry the robot is in RLF and
+    # re-establishes reest_delay_ms after the strongest suitable cell is found, or goes idle when T311 expires first
     rlf: bool = False
+    rlf_qout_db: float = -8.0
+    rlf_qin_db: float = -6.0
+    n310: int = 1
+    n311: int = 1
+    t310_ms: float = 1000.0
+    t311_ms: float = 3000.0
+    reest_delay_ms: float = 40.0
+    rlf_rlc: str | None = None        # on RLF: "carry" or "flush"; None: as ho_rlc
     rach: bool = False
     drx: bool = False
     # ---- application (config.py:755-786)
@@ -391,6 +394,11 @@ class NRConfig:
     @property
     def ul_slots_per_step(self):
         return sum(1 for g in range(self.slots_per_step) if self.slot_symbols(g)[1] > 0)
+
+    @property
+    def rlf_flush(self):
+        """Whether a radio link failure drops the robot's queued frames: rlf_rlc, or ho_rlc when it is None."""
+        return (self.ho_rlc if self.rlf_rlc is None else self.rlf_rlc) == "flush"
 
     @property
     def ul_pc_on(self):

@@ -138,8 +138,9 @@ __global__ void nr_dl_reset_kernel(InetNrDlState dl, InetNrParams pm, const uint
 
 // ======================================================================================= cells reset kernel
 // CellAssociation.reset and NRNet._reset_cells (radio.py:402-408, nr_engine.py:424-438) of the envs of the mask: serving
-// cell 0 until the next step's association, no A3 candidate, no interruption, no handovers; every gNB's N+I estimate
-// back to the noise; a full reset (mask NULL) also clears the interference statistic.
+// cell 0 until the next step's association, no A3 candidate, no interruption, no handovers, no radio link failure
+// state; every gNB's N+I estimate back to the noise; a full reset (mask NULL) also clears the interference statistic
+// and the RLF counters.
 __global__ void nr_cells_reset_kernel(InetNrCells cl, int E, int R, int S, const uint8_t* __restrict__ mask, int full) {
     const int e = blockIdx.x;
     if (e >= E) return;
@@ -147,11 +148,17 @@ __global__ void nr_cells_reset_kernel(InetNrCells cl, int E, int R, int S, const
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
         size_t ir = (size_t)e * R + r;
         cl.serv[ir] = 0; cl.a3_cand[ir] = -1; cl.a3_cnt[ir] = 0; cl.ho_end[ir] = 0; cl.n_ho[ir] = 0;
+        if (cl.rlf) {
+            cl.rlf_active[ir] = 0; cl.oos_cnt[ir] = 0; cl.is_cnt[ir] = 0; cl.t310_end[ir] = -1; cl.t311_end[ir] = -1;
+            cl.reest_end[ir] = -1; cl.reest_cell[ir] = 0; cl.n_rlf[ir] = 0;
+        }
     }
     for (int q = threadIdx.x; q < cl.C * S; q += blockDim.x) cl.ni_ul[(size_t)e * cl.C * S + q] = cl.noise_mw;
     if (threadIdx.x == 0) {
         cl.pending[e] = 1;
         if (full) cl.ion[e] = 0.f;
+        if (full && cl.rlf)
+            for (int k = 0; k < 5; ++k) cl.rlf_ctr[(size_t)e * 5 + k] = 0;
     }
 }
 
@@ -287,6 +294,13 @@ __global__ void nr_reset_kernel(InetNrState st, InetNrParams pm, const uint8_t* 
 // ======================================================================================= C ABI
 namespace {
 
+// the radio link failure state and constants of a cells struct with rlf set (step: with the rlf output)
+bool rlf_ok(const InetNrCells& c, bool step) {
+    return c.rlf_active && c.oos_cnt && c.is_cnt && c.t310_end && c.t311_end && c.reest_end && c.reest_cell && c.n_rlf &&
+           c.rlf_ctr && (c.out_rlf || !step) && c.n310 >= 1 && c.n311 >= 1 && c.t310 >= 0 && c.t311 >= 0 &&
+           c.reest >= 0;
+}
+
 int next_pow2(int v) { int p = 1; while (p < v) p <<= 1; return p; }
 
 // the argument checks and the launch of one step kernel (UL: dl NULL)
@@ -302,7 +316,7 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     if (n_rows < 0 || n_rows > INET_NR_MAX_ROWS || (n_rows > 0 && !rows) || p.n_modes > INET_NR_MAX_KF)
         return INET_NR_EINVAL;
     if (t.M <= 0 || t.M > inet::MAX_M || t.EQW <= 0 || t.EQW > inet::MAX_EQW || t.mcs_max >= t.M) return INET_NR_EINVAL;
-    if (p.input_kind < 0 || p.input_kind > 2) return INET_NR_EINVAL;
+    if (p.input_kind < 0 || p.input_kind > 3 || (p.input_kind == 3 && !cells)) return INET_NR_EINVAL;
     if ((T < 0 && !st->clock) || T * (int64_t)p.N > (int64_t)0x3fffffff) return INET_NR_EINVAL;
     if (p.n_data < 0 || p.n_data > n_rows) return INET_NR_EINVAL;
     if (p.amc_prev && !st->last_nprb) return INET_NR_EINVAL;     // (the UL link's last PUSCH PRBs are state)
@@ -327,11 +341,12 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
     const int fx = (gen && gen[0] == '1') ? 0 : inet::fx_profile(p);
     if (cells) {
         const InetNrCells& c = *cells;
-        if (c.C != p.n_cells || c.C > INET_NR_MAX_C || p.input_kind != 0 || p.F > 64 || dl)
+        if (c.C != p.n_cells || c.C > INET_NR_MAX_C || (p.input_kind != 0 && p.input_kind != 3) || p.F > 64 || dl)
             return INET_NR_EINVAL;
         if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
             return INET_NR_EINVAL;
         if (c.ttt < 0 || c.ho_int < 0 || !(c.noise_mw > 0.0f)) return INET_NR_EINVAL;
+        if (c.rlf && !rlf_ok(c, true)) return INET_NR_EINVAL;
         fn = inet::pick_step_mc(p.S, c.C, p.P, ir, fx, rb);
     } else if (rb > inet::STEP_WAVE) {          // 65..128 / 129..256 robots: two / four wavefronts per env, UL
         if (dl || vref) return INET_NR_EUNSUPPORTED;
@@ -401,6 +416,7 @@ int32_t inet_nr_cells_reset(const InetNrCells* cells, const InetNrParams* prm, c
         return INET_NR_EINVAL;
     if (!c.serv || !c.a3_cand || !c.a3_cnt || !c.ho_end || !c.n_ho || !c.pending || !c.ni_ul || !c.ion)
         return INET_NR_EINVAL;
+    if (c.rlf && !rlf_ok(c, false)) return INET_NR_EINVAL;
     hipLaunchKernelGGL(nr_cells_reset_kernel, dim3(p.E), dim3(64), 0, (hipStream_t)stream, c, p.E, p.R, p.S, mask,
                        mask ? 0 : 1);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;

@@ -578,11 +578,22 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // several cells: association of this robot, the N+I estimates of its env (LDS), the env's interference statistic
     int serv = 0, a3_cand = -1, a3_cnt = 0, ho_end = 0, n_ho = 0;
     float ion = 0.f;
+    // radio link failure (cl.rlf): the robot's RLF state machine (CellAssociation, radio.py:456-531) and its counts
+    // of this step (rlf, reest, rlf_idle, t310_start, t310_stop)
+    bool rlf_on = false;
+    int oos_cnt = 0, is_cnt = 0, t310_end = -1, t311_end = -1, reest_end = -1, reest_cell = 0, n_rlf = 0;
+    int c_rl[5] = {0, 0, 0, 0, 0};
     if constexpr (MC) {
         if (act) {
             serv = ldo(cl.serv, o_r); a3_cand = ldo(cl.a3_cand, o_r); a3_cnt = ldo(cl.a3_cnt, o_r);
             ho_end = ldo(cl.ho_end, o_r); n_ho = ldo(cl.n_ho, o_r);
             serv = serv < 0 ? 0 : (serv >= NC ? NC - 1 : serv);   // (indexes LDS rows: kept in range)
+            if (cl.rlf) {
+                rlf_on = ldo(cl.rlf_active, o_r) != 0; oos_cnt = ldo(cl.oos_cnt, o_r); is_cnt = ldo(cl.is_cnt, o_r);
+                t310_end = ldo(cl.t310_end, o_r); t311_end = ldo(cl.t311_end, o_r); reest_end = ldo(cl.reest_end, o_r);
+                reest_cell = ldo(cl.reest_cell, o_r); n_rlf = ldo(cl.n_rlf, o_r);
+                reest_cell = reest_cell < 0 ? 0 : (reest_cell >= NC ? NC - 1 : reest_cell);
+            }
         }
         if (e < E) {
             for (int q = r; q < NCS; q += rb) s_ni[q] = cl.ni_ul[(size_t)ee * NCS + q];
@@ -630,17 +641,24 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         }
     };
     if constexpr (MC) {
-        // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
-        float px = 0.f, py = 0.f;
-        if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
+        if (pm.input_kind == 3) {
+            // the path gain of every robot-cell link as given, [E][R][NC] dB (step(pathgain_db=), engine.py:909-915):
+            // no radio, so no LOS state and no motion
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
-            pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los, &los_c[c]) -
-                     pm.ue_tx;
+            for (int c = 0; c < NC; ++c) pgc[c] = act ? ldo(xin + c, o_r * (uint32_t)NC) : 0.f;
+        } else {
+            // RadioMC.pathgain_db of every robot-cell link (radio.py:238-277); the UL reference is set per UL slot
+            float px = 0.f, py = 0.f;
+            if (act) { px = ldo(xin, o_r * 2u); py = ldo(xin + 1, o_r * 2u); }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float* fc = st.field + ((size_t)ee * NC + c) * pm.n_fields * pm.n_modes * 3;
+                pgc[c] = radio_rx_dbm(pm, px, py, cl.gnb_xy[2 * c], cl.gnb_xy[2 * c + 1], fc, sto_los, &los_c[c]) -
+                         pm.ue_tx;
+            }
+            observe_motion(px, py);
+            los_rep = pm.radio_model == 1;
         }
-        observe_motion(px, py);
-        los_rep = pm.radio_model == 1;
 #pragma unroll
         for (int s = 0; s < S; ++s) ref[s] = 0.f;
     } else if constexpr (VREF) {
@@ -763,55 +781,26 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     // rx = path gain + ue_tx (RSRP up to a constant); a pending env attaches every robot to its max-rx cell; the A3
     // condition (best other cell > (serving + offset) + hysteresis, and above the admission floor) held toward the same
     // target for ttt slots fires at slot k_ho = ttt - cnt - 1 of this step when that is inside the step
-    int k_ho = -1, tgt = 0, ho_j = -1;
+    int k_ho = -1, tgt = 0;
     bool fired = false;
-    unsigned long long ho_mask = 0ull;                 // frames a handover drops (replayed at UL slot ho_j)
-    if constexpr (MC) {
-        float rxc[NC];
+    // frames that handovers and radio link failures drop in this step: a mask over the robot's FIFO and the UL slot
+    // (0 .. n_ul) before which it applies, replayed in order by the epilogue so that frames completed earlier keep
+    // their completion (at most three per step: a handover; or T311's idling or an RLF, then a re-establishment)
+    constexpr int ND = MC ? 3 : 1;
+    unsigned long long drop_m[ND];
+    int drop_j[ND];
+    int n_drop = 0;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) rxc[c] = pgc[c] + pm.ue_tx;
-        if (act && cl.pending[ee] != 0) {
-            int b = 0;
-            float bv = rxc[0];
-#pragma unroll
-            for (int c = 1; c < NC; ++c) if (rxc[c] > bv) { bv = rxc[c]; b = c; }
-            serv = b;
-        }
-        if (act) {
-            const float rs = sel_of(rxc, serv);
-            float best = 0.f;
-            int bc = 0;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float v = c == serv ? -INFINITY : rxc[c];
-                if (c == 0 || v > best) { best = v; bc = c; }
-            }
-            bool cond = best > ((rs + cl.a3_off) + cl.a3_hyst);
-            if (cl.has_floor) cond = cond && best >= cl.floor_rx;
-            const int cnt = (cond && bc == a3_cand) ? a3_cnt : 0;
-            int kf = cl.ttt - cnt - 1;
-            kf = kf > 0 ? kf : 0;
-            const bool fire = cond && kf < N;
-            a3_cnt = (cond && !fire) ? cnt + N : 0;
-            a3_cand = (cond && !fire) ? bc : -1;
-            k_ho = fire ? kf : -1;
-            tgt = bc;
-        }
-    }
-    // NRNet._handover at slot g_sw (nr_engine.py:677-682): the switch (radio.py:439-448), then UlMac.handover
-    // (mac_ul.py:238-247, mac.py:557-581): under RLC UM or ho_rlc "flush" the frames overlapping the undecoded HARQ
-    // bytes (flush: every queued frame) are lost, marked when the epilogue replays the UL slots (before UL slot ho_j)
-    // so that frames completed earlier keep their completion, and those processes are freed; otherwise they restart
-    // their combining at the target. OLLA, the PF average and the CSI start afresh; the BSR reaches the target, a
-    // pending SR is dropped.
-    auto handover = [&](int g_sw) {
-        serv = tgt;
-        ho_end = g_sw + cl.ho_int;
-        ++n_ho;
-        fired = true;
-        if (pm.harq_drop || cl.ho_flush) {
+    for (int i = 0; i < ND; ++i) { drop_m[i] = 0ull; drop_j[i] = 0; }
+    // The MAC side of a handover (UlMac.handover, mac_ul.py:238-247, mac.py:557-581; also of an RLF, a
+    // re-establishment and idling, NRNet._rlf_links, nr_engine.py:684-689): under RLC UM or with flush the frames
+    // overlapping the undecoded HARQ bytes (flush: every queued frame) are lost, marked when the epilogue replays the
+    // UL slots, and those processes are freed; otherwise they restart their combining at the target. OLLA, the PF
+    // average and the CSI start afresh; the BSR reaches the target, a pending SR is dropped.
+    auto link_handover = [&](bool flush) {
+        if (pm.harq_drop || flush) {
             unsigned long long mk = 0ull;
-            if (cl.ho_flush) {
+            if (flush) {
                 mk = qlen >= 64 ? ~0ull : ((1ull << qlen) - 1ull);
             } else {
                 for (int f = 0; f < qlen; ++f) {
@@ -822,9 +811,14 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
                     if (ov) mk |= 1ull << f;
                 }
             }
-            ho_mask = mk;
-            ho_j = n_ul;
-            if (cl.ho_flush) sent = enq;
+#pragma unroll
+            for (int i = 0; i < ND; ++i)
+                if (i == n_drop || (i == ND - 1 && n_drop >= ND)) {
+                    drop_m[i] |= mk;                   // (a fourth event would join the third: never reached)
+                    if (i == n_drop) drop_j[i] = n_ul;
+                }
+            n_drop = n_drop < ND ? n_drop + 1 : ND;
+            if (flush) sent = enq;
 #pragma unroll
             for (int p = 0; p < P; ++p)
                 if (hm_state(hmeta[p]) == 1) hmeta[p] = hm_pack(0, hm_ntx(hmeta[p]), hm_mcs(hmeta[p]), hm_nsb(hmeta[p]));
@@ -844,6 +838,135 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         for (int s = 0; s < S; ++s) csi[s] = 0.f;
         if constexpr (!DL) { sr_t = -1; bsr = enq - sent; }
     };
+    // NRNet._handover at slot g_sw (nr_engine.py:677-682): the switch (radio.py:439-448; with RLF it stops T310 and
+    // the indication counts), then the MAC side with ho_rlc's flush
+    auto handover = [&](int g_sw) {
+        serv = tgt;
+        ho_end = g_sw + cl.ho_int;
+        ++n_ho;
+        fired = true;
+        if (cl.rlf) {
+            c_rl[4] += t310_end >= 0 ? 1 : 0;
+            t310_end = -1;
+            oos_cnt = 0;
+            is_cnt = 0;
+        }
+        link_handover(cl.ho_flush != 0);
+    };
+    // radio link failure: the SINR estimate toward every cell at the step start (nr_engine.py:704-707), the cell search
+    // (radio.py:503-519: the max-RSRP cell whose estimate reaches qin and whose RSRP the floor, re-establishment reest
+    // slots after slot g), and the events due by slot g (NRNet._rlf_events, nr_engine.py:691-702: T310 expiries not
+    // preceded by a handover declare RLF, then the re-establishments due complete); returns the handover due by g
+    float sinr_c[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) sinr_c[c] = 0.f;
+    auto rlf_search = [&](int g, bool mask) {
+        bool any = false;
+        int bc = 0;
+        float bv = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float rxv = pgc[c] + pm.ue_tx;
+            const bool ok = sinr_c[c] >= cl.qin && (!cl.has_floor || rxv >= cl.floor_rx);
+            any |= ok;
+            const float v = ok ? rxv : -INFINITY;
+            if (c == 0 || v > bv) { bv = v; bc = c; }
+        }
+        if (mask && rlf_on && reest_end < 0 && any) { reest_end = g + cl.reest; reest_cell = bc; }
+    };
+    auto rlf_events = [&](int g) -> bool {
+        if (!act) return false;
+        const int g_ho = g0 + k_ho;
+        const bool ho = !fired && k_ho >= 0 && g_ho <= g;
+        const bool ex = t310_end >= 0 && t310_end <= g && !rlf_on && !(ho && g_ho <= t310_end);
+        if (ex) {                                      // CellAssociation.declare (radio.py:486-501)
+            const int g_rlf = t310_end;
+            rlf_on = true;
+            t311_end = g_rlf + cl.t311;
+            t310_end = -1;
+            reest_end = -1;
+            oos_cnt = 0;
+            is_cnt = 0;
+            a3_cnt = 0;
+            a3_cand = -1;
+            ++n_rlf;
+            ++c_rl[0];
+            rlf_search(g_rlf, true);
+            link_handover(cl.rlf_flush != 0);
+            fired = true;
+        }
+        if (rlf_on && reest_end >= 0 && reest_end <= g) {   // CellAssociation.complete (radio.py:521-531)
+            serv = reest_cell;
+            rlf_on = false;
+            t311_end = -1;
+            reest_end = -1;
+            ++c_rl[1];
+            link_handover(false);
+        }
+        return ho && !rlf_on && !ex;
+    };
+    if constexpr (MC) {
+        float rxc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) rxc[c] = pgc[c] + pm.ue_tx;
+        if (act && cl.pending[ee] != 0) {
+            int b = 0;
+            float bv = rxc[0];
+#pragma unroll
+            for (int c = 1; c < NC; ++c) if (rxc[c] > bv) { bv = rxc[c]; b = c; }
+            serv = b;
+        }
+        if (cl.rlf && act) {
+            // radio link monitoring at the step's first slot (nr_engine.py:733-736, radio.py:456-480): the SINR
+            // estimate toward every cell against its gNB's latest wideband N+I estimate (the serving one is the
+            // serving link's), ((pg + ue_tx) - ref_db) - 10 log10(mean_s ni)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                float nrow[S];
+#pragma unroll
+                for (int s2 = 0; s2 < S; ++s2) nrow[s2] = s_ni[c * S + s2];
+                sinr_c[c] = ((pgc[c] + pm.ue_tx) - cl.ref_db) - 10.0f * log10f(aten_sum<S>(nrow) / (float)S);
+            }
+            const float sinr_s = sel_of(sinr_c, serv);
+            const bool idle = rlf_on && reest_end < 0 && t311_end >= 0 && t311_end <= g0;
+            if (idle) { t311_end = -1; ++c_rl[2]; }
+            rlf_search(g0, rlf_on);
+            const bool conn = !rlf_on;
+            const bool oos = conn && cl.qout > sinr_s, ins = conn && sinr_s > cl.qin;
+            const bool run = t310_end >= 0;
+            const int oc = ins ? 0 : oos_cnt + (oos ? 1 : 0);
+            const bool start = conn && !run && oc >= cl.n310;
+            const int ic = oos ? 0 : is_cnt + (ins ? 1 : 0);
+            const bool stop = run && ic >= cl.n311;
+            oos_cnt = (run || start || !conn) ? 0 : oc;
+            is_cnt = (run && !stop) ? ic : 0;
+            t310_end = start ? g0 + cl.t310 : (stop ? -1 : t310_end);
+            c_rl[3] += start ? 1 : 0;
+            c_rl[4] += stop ? 1 : 0;
+            if (idle) link_handover(true);             // the idle robot's queue is dropped (nr_engine.py:736)
+        }
+        if (act) {
+            const float rs = sel_of(rxc, serv);
+            float best = 0.f;
+            int bc = 0;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float v = c == serv ? -INFINITY : rxc[c];
+                if (c == 0 || v > best) { best = v; bc = c; }
+            }
+            bool cond = best > ((rs + cl.a3_off) + cl.a3_hyst);
+            if (cl.has_floor) cond = cond && best >= cl.floor_rx;
+            if (cl.rlf) cond = cond && !rlf_on;       // no measurement reporting while in RLF
+            const int cnt = (cond && bc == a3_cand) ? a3_cnt : 0;
+            int kf = cl.ttt - cnt - 1;
+            kf = kf > 0 ? kf : 0;
+            const bool fire = cond && kf < N;
+            a3_cnt = (cond && !fire) ? cnt + N : 0;
+            a3_cand = (cond && !fire) ? bc : -1;
+            k_ho = fire ? kf : -1;
+            tgt = bc;
+        }
+    }
     // i.i.d. fading (rho = 0 at every evolving row): a robot's fading state and CSI are then pure functions of the
     // latest draw, so a robot with nothing to send and no HARQ process pending (it takes part in no decision for the
     // rest of the step) skips the draws until the last row that fixes the stored state (the last UL slot for the CSI,
@@ -861,7 +984,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             for (int c = 0; c < NC; ++c) set_k(c, k_at(c, g));
         }
         if constexpr (MC) {                        // A3 handovers due by this slot (nr_engine.py:740-754)
-            if (act && !fired && k_ho >= 0 && k_ho <= row.rel) handover(g0 + k_ho);
+            const bool ho_now = cl.rlf ? rlf_events(g) : (act && !fired && k_ho >= 0 && k_ho <= row.rel);
+            if (ho_now) handover(g0 + k_ho);
         }
         if ((row.flags & 4) && (row.flags & 8)) {  // AR(1) fading innovation of this slot (nr_engine.py:575-589)
             // The 2 NC S normals of every robot that needs them are drawn cooperatively by the whole wavefront: the
@@ -1150,7 +1274,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         bool new_el = any_free && need > 0 && !has_rx && act;
         has_rx = has_rx && act;
         if constexpr (MC) {                        // handover interruption (mac.py:249-251, radio.py:450-453)
-            const bool ok_ = g >= ho_end;
+            const bool ok_ = g >= ho_end && !rlf_on;
             has_rx = has_rx && ok_;
             new_el = new_el && ok_;
         }
@@ -1884,7 +2008,8 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
 
     // ================================================================ end of step (NRNet._finish)
     if constexpr (MC) {                            // A3 triggers after the step's last active slot (nr_engine.py:780)
-        if (act && !fired && k_ho >= 0) handover(g0 + k_ho);
+        const bool late = cl.rlf ? rlf_events(g0 + N - 1) : (act && !fired && k_ho >= 0);
+        if (late) handover(g0 + k_ho);
         // the reported SINR (serving_sinr_db, nr_engine.py:709-713): full power over snr_ref_prbs PRBs against the
         // serving gNB's wideband N+I estimate, ((pg + ue_tx) - ref_db) - 10 log10(mean_s ni)
         float nrow[S];
@@ -1910,14 +2035,23 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         int fin = ldo(lk.q_fin + fr, o_fr);
         const uint32_t meta = ldo(lk.q_meta + fr, o_fr);
         bool lost = meta & 1u;
-        // a handover's loss, at its place among the slots: frames not completed and not lost by then
-        const bool ho_hit = MC && ((ho_mask >> (f & 63)) & 1ull) != 0ull;
+        // the losses of handovers and radio link failures, each at its place among the slots: frames not completed and
+        // not lost by then
+        auto drop_at = [&](int j, bool after) {
+            if constexpr (MC) {
+#pragma unroll
+                for (int i = 0; i < ND; ++i) {
+                    const bool at = after ? drop_j[i] >= n_hist : drop_j[i] == j;
+                    if (i < n_drop && at && ((drop_m[i] >> (f & 63)) & 1ull) != 0ull && fin == FIN_NONE) {
+                        if (!lost) ++lost_new;
+                        lost = true;
+                    }
+                }
+            }
+        };
         // replay the slots: lost marking (handover, RLC UM) first, then in-order completion (mac.py:474-477, 500-503)
         for (int j = 0; j < n_hist; ++j) {
-            if (ho_hit && j == ho_j && fin == FIN_NONE) {
-                if (!lost) ++lost_new;
-                lost = true;
-            }
+            drop_at(j, false);
             if (pm.harq_drop) {
                 int xl = exlo_l[j * CW + lane], xh = exhi_l[j * CW + lane];
                 if (xh > xl && qs < xh && qe > xl) {
@@ -1927,10 +2061,7 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
             }
             if (fin == FIN_NONE && !lost && qe <= ack_l[j * CW + lane]) fin = g0 + s_ulrel[j];
         }
-        if (ho_hit && ho_j >= n_hist && fin == FIN_NONE) {
-            if (!lost) ++lost_new;
-            lost = true;
-        }
+        drop_at(0, true);
         double fin_d = INFINITY;
         if (fin != FIN_NONE) {
             int tf = fin / N, rel = fin - tf * N;
@@ -2100,6 +2231,12 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
         if constexpr (MC) {
             sto(cl.serv, o_r, serv); sto(cl.a3_cand, o_r, a3_cand); sto(cl.a3_cnt, o_r, a3_cnt);
             sto(cl.ho_end, o_r, ho_end); sto(cl.n_ho, o_r, n_ho);
+            if (cl.rlf) {
+                sto(cl.rlf_active, o_r, rlf_on ? 1 : 0); sto(cl.oos_cnt, o_r, oos_cnt); sto(cl.is_cnt, o_r, is_cnt);
+                sto(cl.t310_end, o_r, t310_end); sto(cl.t311_end, o_r, t311_end); sto(cl.reest_end, o_r, reest_end);
+                sto(cl.reest_cell, o_r, reest_cell); sto(cl.n_rlf, o_r, n_rlf);
+                sto(cl.out_rlf, o_r >> 2, (uint8_t)(rlf_on ? 1 : 0));
+            }
         }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -2133,9 +2270,18 @@ __global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1)
     if (lena) { v_tbb = env_sum(act ? c_tbb : 0); v_tbe = env_sum(act ? c_tbe : 0); v_blk = env_sum(act ? c_blk : 0); }
     __syncthreads();                                  // histogram atomics of every lane are done
     if constexpr (MC) {
+        int v_rl[5] = {0, 0, 0, 0, 0};
+        if (cl.rlf) {
+#pragma unroll
+            for (int k = 0; k < 5; ++k) v_rl[k] = env_sum(act ? c_rl[k] : 0);
+        }
         if (e < E) {
             for (int q = r; q < NCS; q += rb) cl.ni_ul[(size_t)e * NCS + q] = s_ni[q];
             if (r == 0) { cl.pending[e] = 0; cl.ion[e] = ion; }
+            if (cl.rlf && r == 0) {
+#pragma unroll
+                for (int k = 0; k < 5; ++k) cl.rlf_ctr[(size_t)e * 5 + k] += v_rl[k];
+            }
         }
     }
     if (r == 0 && e < E) {

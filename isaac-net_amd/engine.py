@@ -84,7 +84,7 @@ def refusals(cfg: NRConfig):
     no(mc and cfg.n_cells > 3, f"n_cells={cfg.n_cells}",
        "one to three cells per env in this build (the fading of every robot-cell link is held in registers)")
     no(mc and cfg.dl, "the downlink with several cells", "the multi-cell step runs the uplink")
-    no(cfg.rlf, "radio link failure (rlf=True)", "A3 handover without RLF")
+    no(cfg.rlf and cfg.rach, "re-establishment through RACH (rlf with rach)", "a fixed re-establishment delay")
     no(mc and cfg.frame_buffer > 64, "frame_buffer > 64 with several cells", "a 64-bit handover loss mask")
     no(not cfg.ul, "ul=False (a downlink-only engine)", "the UL link runs every step")
     no(cfg.dl and cfg.duplex != "tdd", "the FDD downlink carrier", "TDD (one carrier)")
@@ -242,9 +242,19 @@ class HipNREngine:
             C_ = self.C
             self.cst = {"serv": z(E, R), "a3_cand": z(E, R, v=-1), "a3_cnt": z(E, R), "ho_end": z(E, R),
                         "n_ho": z(E, R), "pending": z(E, v=1), "ni_ul": z(E, C_, S, dt=f32), "ion": z(E, dt=f32)}
+            if cfg.rlf:                      # radio link failure (CellAssociation.RLF_INIT, radio.py:340-342)
+                self.cst.update({"rlf_active": z(E, R), "oos_cnt": z(E, R), "is_cnt": z(E, R),
+                                 "t310_end": z(E, R, v=-1), "t311_end": z(E, R, v=-1), "reest_end": z(E, R, v=-1),
+                                 "reest_cell": z(E, R), "n_rlf": z(E, R), "rlf_ctr": z(E, 5, dt=torch.int64)})
             c = _lib.InetNrCells()
             for name, t_ in self.cst.items():
                 setattr(c, name, t_.data_ptr())
+            if cfg.rlf:
+                ms = lambda v: int(round(v / cfg.slot_ms))  # noqa: E731
+                c.rlf, c.rlf_flush = 1, int(cfg.rlf_flush)
+                c.n310, c.n311 = cfg.n310, cfg.n311
+                c.t310, c.t311, c.reest = ms(cfg.t310_ms), ms(cfg.t311_ms), ms(cfg.reest_delay_ms)
+                c.qout, c.qin = cfg.rlf_qout_db, cfg.rlf_qin_db
             xy = [v for p_ in cfg.gnb_xy() for v in p_]
             c.gnb_xy[:len(xy)] = xy
             c.C = C_
@@ -716,6 +726,9 @@ class HipNREngine:
         c.cap32, c.cls8, c.delay = ptr("cap32"), ptr("cls8"), ptr("delay")
         c.newest, c.queue_len, c.serving_cell = ptr("newest"), ptr("queue_len"), ptr("serving_cell")
         c.queue_bytes, c.sinr_db, c.det_env, c.t = ptr("queue_bytes"), ptr("sinr_db"), ptr("det_env"), ptr("t")
+        if self._ccells is not None and self.config.rlf:      # robots in radio link failure after the step
+            o["rlf"] = e(E, R, dt=torch.bool)
+            self._ccells.out_rlf = o["rlf"].data_ptr()
         return o, c
 
     def step(self, t=None, x=None, cur_hid=None, *, snr_db=None, dl_snr_db=None, pathgain_db=None, vel=None,
@@ -724,15 +737,15 @@ class HipNREngine:
         Returns the reference's output dict; with cur_hid (legacy form) returns (newest, det_env).
         arrivals= (extension): counts [E,R,NC] uint8 of this step's messages, enqueued inside the step's launch as
         submit_counts(counts) would do before it; the dict then also holds arrivals_accepted [E,R] int32."""
-        if (dl_snr_db is not None and not self.dl) or pathgain_db is not None or \
-                triggers is not None or blockers is not None:
-            raise HipUnsupported("dl_snr_db (without dl=True) / pathgain_db / triggers / blockers need features "
-                                 "the hip backend does not implement (the path gain input with several cells, traffic "
-                                 "models, blockage)")
+        if pathgain_db is not None and self.C == 1:
+            raise ValueError("pathgain_db= needs config.n_cells > 1; use x (poses or SNR) with one cell")
+        if (dl_snr_db is not None and not self.dl) or triggers is not None or blockers is not None:
+            raise HipUnsupported("dl_snr_db (without dl=True) / triggers / blockers need features the hip backend "
+                                 "does not implement (traffic models, blockage)")
         T = self._now(t)
         legacy = cur_hid is not None
         hid = (cur_hid if legacy else self._last_hid).to(self.dev, torch.long).contiguous()
-        kind, xin = self._input(x, snr_db)
+        kind, xin = self._input(x, snr_db, pathgain_db)
         self._check_kind(kind)
         vin = self._vel_input(vel, kind)
         plan = self._plan(T, kind)
@@ -771,8 +784,13 @@ class HipNREngine:
             return o["newest"], o["det_env"]
         return o
 
-    def _input(self, x, snr_db):
+    def _input(self, x, snr_db, pathgain_db=None):
         E, R, S = self.E, self.R, self.S
+        if pathgain_db is not None:                  # several cells: the path gain of every link as given (kind 3)
+            xin = pathgain_db.to(self.dev, torch.float32).contiguous()
+            if tuple(xin.shape) != (E, R, self.C):
+                raise ValueError(f"pathgain_db must be [E,R,C] = {(E, R, self.C)}, got {tuple(xin.shape)}")
+            return 3, xin
         if snr_db is None:
             if x is None:
                 raise ValueError("step needs poses [E,R,2|3] or an SNR [E,R]")
@@ -802,9 +820,8 @@ class HipNREngine:
     def _check_kind(self, kind):
         if self.R > 64 and kind == 2:
             raise HipUnsupported("per-subband SNR input with more than 64 robots per env")
-        if self.C > 1 and kind != 0:
-            raise ValueError("several cells: pass poses [E,R,2|3] (the path gain of every robot-cell link comes from "
-                             "the radio)")
+        if self.C > 1 and kind not in (0, 3):
+            raise ValueError("several cells: pass poses [E,R,2|3] or pathgain_db=[E,R,C]")
 
     def _schedule(self, g0):
         """cfg.schedule(g0), cached by g0 modulo the period of the TDD pattern, SR and CQI occasions."""
@@ -1105,6 +1122,10 @@ class HipNREngine:
             c = self.cst
             out.update({"assoc." + n: L(c[n]) for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho")})
             out["assoc.pending"] = c["pending"] != 0
+            if cfg.rlf:
+                out.update({"assoc." + n: L(c[n]) for n in RLF_KEYS})
+                out["assoc.rlf_active"] = c["rlf_active"] != 0
+                out.update({f"assoc.ctr[{k}]": c["rlf_ctr"][:, i].sum() for i, k in enumerate(RLF_CTR)})
             out["net.ni_ul"] = c["ni_ul"]
             out["net.ioN[ul]"] = c["ion"]
         if cfg.rician_mode in ("fixed", "los"):
@@ -1192,8 +1213,14 @@ class HipNREngine:
         st["h_im"].copy_(rs(h[..., 1]))
         if self.C > 1:
             c = self.cst
-            for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho"):
+            for n in ("serv", "a3_cand", "a3_cnt", "ho_end", "n_ho") + (("rlf_active",) + RLF_KEYS if cfg.rlf else ()):
                 c[n].copy_(I(g("assoc." + n)))
+            if cfg.rlf:                               # the counters: totals on env 0
+                rc = torch.zeros_like(c["rlf_ctr"])
+                for i, k in enumerate(RLF_CTR):
+                    if f"assoc.ctr[{k}]" in sd:
+                        rc[0, i] = int(torch.as_tensor(sd[f"assoc.ctr[{k}]"]))
+                c["rlf_ctr"].copy_(rc)
             c["pending"].copy_(I(g("assoc.pending")))
             c["ni_ul"].copy_(g("net.ni_ul").float())
             c["ion"].copy_(g("net.ioN[ul]").float())
@@ -1317,6 +1344,8 @@ class HipNREngine:
             return cfg.freq_corr_mode if cfg is not None else None
         if k == "per_robot_doppler":
             return cfg is not None and cfg.fading_doppler == "per_robot"
+        if k == "net.assoc.rlf":
+            return cfg is not None and bool(cfg.rlf) and cfg.n_cells > 1
         return self._CK_OFF[k]
 
     def _strict_extra_keys(self, sd, used):
@@ -1440,6 +1469,12 @@ def state_dict(eng):
     return eng.owner_state()
 
 
+# the radio link failure state of CellAssociation kept per robot (radio.py:340-342; rlf_active is a bool) and its
+# counters (radio.py:342)
+RLF_KEYS = ("oos_cnt", "is_cnt", "t310_end", "t311_end", "reest_end", "reest_cell", "n_rlf")
+RLF_CTR = ("rlf", "reest", "rlf_idle", "t310_start", "t310_stop")
+
+
 class GraphStep:
     """submit_counts + step of a HipNREngine as HIP graphs (torch.cuda.CUDAGraph), recorded on first use and replayed
     at every control step: one graph for the enqueue, and one step graph per slot schedule (TDD / SR / CQI phase and
@@ -1485,13 +1520,15 @@ class GraphStep:
         torch.cuda.synchronize(eng.dev)
         return g, out
 
-    def __call__(self, x=None, counts=None, *, snr_db=None, vel=None):
+    def __call__(self, x=None, counts=None, *, snr_db=None, vel=None, pathgain_db=None):
         """One control step: counts [E,R,NC] uint8 messages per class (as submit_counts), then the step on poses
-        x [E,R,2|3], SNR x [E,R] or snr_db= [E,R,S] (with the downlink: its reference from the same input); vel=
-        [E,R,2|3] the velocity input of per-robot Doppler (as step)."""
+        x [E,R,2|3], SNR x [E,R] or snr_db= [E,R,S] (with the downlink: its reference from the same input), or with
+        several cells pathgain_db= [E,R,C]; vel= [E,R,2|3] the velocity input of per-robot Doppler (as step)."""
         eng = self.eng
         T = eng.T
-        kind, xin = eng._input(x, snr_db)
+        if pathgain_db is not None and eng.C == 1:
+            raise ValueError("pathgain_db= needs config.n_cells > 1")
+        kind, xin = eng._input(x, snr_db, pathgain_db)
         eng._check_kind(kind)
         vin = eng._vel_input(vel, kind)
         if vin is not None:

@@ -667,11 +667,17 @@ def pick(x, idx):
 
 
 class Association:
-    """CellAssociation without radio link failure (radio.py:303-453): max-RSRP attach after a reset (associate), the
-    A3 condition evaluated once per control step with the exact slot at which the handover fires (plan), the switch
-    and the handover interruption (schedulable). RSRP here is rx = path gain + ue_tx_dbm [E,R,C]."""
+    """CellAssociation (radio.py:303-531): max-RSRP attach after a reset (associate), the A3 condition evaluated once
+    per control step with the exact slot at which the handover fires (plan), the switch and the handover interruption
+    (schedulable); with cfg.rlf radio link failure: radio link monitoring once per step (rlm: out-of-sync / in-sync
+    counts, T310 start and stop, T311 expiry to idle), T310 expiry (declare) with the cell search (search) and the
+    re-establishment at the selected cell (complete). RSRP here is rx = path gain + ue_tx_dbm [E,R,C]. Slot numbers
+    of timers; -1 = not running."""
 
     INIT = {"serv": 0, "a3_cand": -1, "a3_cnt": 0, "ho_end": 0, "n_ho": 0}
+    RLF_INIT = {"rlf_active": False, "oos_cnt": 0, "is_cnt": 0, "t310_end": -1, "t311_end": -1, "reest_end": -1,
+                "reest_cell": 0, "n_rlf": 0}
+    RLF_CTR = ("rlf", "reest", "rlf_idle", "t310_start", "t310_stop")
 
     def __init__(self, cfg, E, R, C):
         self.cfg, self.C, self.K = cfg, C, cfg.slots_per_step
@@ -680,14 +686,23 @@ class Association:
         floor = cfg.a3_min_target_rsrp_dbm
         self.floor_rx = None if floor is None else floor - (cfg.gnb_tx_dbm - 10 * math.log10(12 * cfg.nprb)
                                                             - cfg.ue_tx_dbm)
-        for n, v in self.INIT.items():
-            setattr(self, n, torch.full((E, R), v, dtype=torch.long))
+        self._init = dict(self.INIT)
+        self.rlf = bool(cfg.rlf)
+        if self.rlf:                                     # (radio.py:369-375)
+            ms = lambda v: int(round(v / cfg.slot_ms))  # noqa: E731
+            self.t310, self.t311, self.reest = ms(cfg.t310_ms), ms(cfg.t311_ms), ms(cfg.reest_delay_ms)
+            self._init.update(self.RLF_INIT)
+            self.ctr = {k: 0 for k in self.RLF_CTR}
+        for n, v in self._init.items():
+            setattr(self, n, torch.full((E, R), v, dtype=torch.bool if isinstance(v, bool) else torch.long))
         self.pending = torch.ones(E, dtype=torch.bool)
 
     def reset(self, m):
-        for n, v in self.INIT.items():
+        for n, v in self._init.items():
             setattr(self, n, where_env(m, v, getattr(self, n)))
         self.pending = torch.where(m, torch.ones_like(self.pending), self.pending)
+        if self.rlf and bool(m.all()):                   # global counters: cleared by a full reset only
+            self.ctr = {k: 0 for k in self.RLF_CTR}
 
     def associate(self, rx):
         self.serv = torch.where(self.pending[:, None], rx.argmax(-1), self.serv)
@@ -703,6 +718,8 @@ class Association:
         cond = cmp("a3", best, rs + cfg.a3_offset_db + cfg.a3_hyst_db, "gt")
         if self.floor_rx is not None:
             cond = cond & cmp("a3_floor", best, torch.tensor(self.floor_rx, dtype=best.dtype))
+        if self.rlf:                                     # no measurement reporting while in RLF
+            cond = cond & ~self.rlf_active
         cnt = torch.where(cond & (bc == self.a3_cand), self.a3_cnt, torch.zeros_like(self.a3_cnt))
         k_fire = (self.ttt - cnt - 1).clamp(min=0)
         fire = cond & (k_fire < self.K)
@@ -714,9 +731,80 @@ class Association:
         self.serv = torch.where(ho, target, self.serv)
         self.ho_end = torch.where(ho, g + self.ho_int, self.ho_end)
         self.n_ho = self.n_ho + ho.long()
+        if self.rlf:                                     # the handover command stops T310 and the counts
+            self.ctr["t310_stop"] += int((ho & (self.t310_end >= 0)).sum())
+            self.t310_end = torch.where(ho, -1, self.t310_end)
+            self.oos_cnt = torch.where(ho, 0, self.oos_cnt)
+            self.is_cnt = torch.where(ho, 0, self.is_cnt)
 
     def schedulable(self, g):
+        if self.rlf:
+            return (g >= self.ho_end) & ~self.rlf_active
         return g >= self.ho_end
+
+    # ---- radio link failure (radio.py:456-531) ----
+    def rlm(self, sinr_db, rx, sinr_c, g, dec=None):
+        """Evaluation at the step's first slot g: T311 expiry (idle), the cell search of the robots in RLF, the
+        out-of-sync / in-sync indications of the connected robots, T310 start / stop. Returns the robots gone idle."""
+        cfg = self.cfg
+        cmp = dec.cmp if dec is not None else (lambda _site, a, b, op="ge": _ge(a, b, op))
+        idle = self.rlf_active & (self.reest_end < 0) & (self.t311_end >= 0) & (self.t311_end <= g)
+        self.t311_end = torch.where(idle, -1, self.t311_end)
+        self.ctr["rlf_idle"] += int(idle.sum())
+        self.search(rx, sinr_c, g, self.rlf_active, dec)
+        conn = ~self.rlf_active
+        oos = conn & cmp("qout", torch.tensor(cfg.rlf_qout_db, dtype=sinr_db.dtype), sinr_db, "gt")
+        ins = conn & cmp("qin", sinr_db, torch.tensor(cfg.rlf_qin_db, dtype=sinr_db.dtype), "gt")
+        run = self.t310_end >= 0
+        oc = torch.where(ins, 0, self.oos_cnt + oos.long())
+        start = conn & ~run & (oc >= cfg.n310)
+        ic = torch.where(oos, 0, self.is_cnt + ins.long())
+        stop = run & (ic >= cfg.n311)
+        self.oos_cnt = torch.where(run | start | ~conn, 0, oc)
+        self.is_cnt = torch.where(run & ~stop, ic, 0)
+        self.t310_end = torch.where(start, g + self.t310, torch.where(stop, -1, self.t310_end))
+        self.ctr["t310_start"] += int(start.sum())
+        self.ctr["t310_stop"] += int(stop.sum())
+        return idle
+
+    def expired(self, g):
+        return (self.t310_end >= 0) & (self.t310_end <= g) & ~self.rlf_active
+
+    def declare(self, new, rx, sinr_c, dec=None):
+        g_rlf = self.t310_end
+        self.rlf_active = self.rlf_active | new
+        self.t311_end = torch.where(new, g_rlf + self.t311, self.t311_end)
+        self.t310_end = torch.where(new, -1, self.t310_end)
+        self.reest_end = torch.where(new, -1, self.reest_end)
+        self.oos_cnt = torch.where(new, 0, self.oos_cnt)
+        self.is_cnt = torch.where(new, 0, self.is_cnt)
+        self.a3_cnt = torch.where(new, 0, self.a3_cnt)
+        self.a3_cand = torch.where(new, -1, self.a3_cand)
+        self.n_rlf = self.n_rlf + new.long()
+        self.ctr["rlf"] += int(new.sum())
+        self.search(rx, sinr_c, g_rlf, new, dec)
+        return g_rlf
+
+    def search(self, rx, sinr_c, g, mask, dec=None):
+        """The max-RSRP suitable cell (SINR estimate >= Qin, RSRP >= the admission floor when set) of the robots in
+        RLF without a target, selected at slot g; re-establishment reest_delay later."""
+        cmp = dec.cmp if dec is not None else (lambda _site, a, b, op="ge": _ge(a, b, op))
+        ok = cmp("search", sinr_c, torch.tensor(self.cfg.rlf_qin_db, dtype=sinr_c.dtype))
+        if self.floor_rx is not None:
+            ok = ok & cmp("search_floor", rx, torch.tensor(self.floor_rx, dtype=rx.dtype))
+        best, bc = rx.masked_fill(~ok, -float("inf")).max(-1)
+        cand = mask & self.rlf_active & (self.reest_end < 0) & ok.any(-1)
+        self.reest_end = torch.where(cand, g + self.reest, self.reest_end)
+        self.reest_cell = torch.where(cand, bc, self.reest_cell)
+
+    def complete(self, g):
+        done = self.rlf_active & (self.reest_end >= 0) & (self.reest_end <= g)
+        self.serv = torch.where(done, self.reest_cell, self.serv)
+        self.rlf_active = self.rlf_active & ~done
+        self.t311_end = torch.where(done, -1, self.t311_end)
+        self.reest_end = torch.where(done, -1, self.reest_end)
+        self.ctr["reest"] += int(done.sum())
+        return done
 
 
 class OracleEngine:
@@ -729,7 +817,7 @@ class OracleEngine:
         self.S, self.P, self.F = cfg.n_subbands, cfg.n_harq, cfg.frame_buffer
         self.C = C = cfg.n_cells
         assert cfg.ul and cfg.ul_grant_model == "lumped"
-        assert C == 1 or not (cfg.dl or cfg.rlf), "several cells: uplink only, no radio link failure"
+        assert C == 1 or not cfg.dl, "several cells: uplink only"
         assert cfg.scheduler in ("pf", "pf_wideband", "maxci", "rr")
         assert cfg.pf_update == "slot" or cfg.scheduler in ("pf", "pf_wideband"), "pf_update='rbg' needs a PF scheduler"
         assert not cfg.ul_tpc
@@ -931,13 +1019,17 @@ class OracleEngine:
         return acc
 
     # ---------------- step (engine.py:867-960, nr_engine.py:613-668) ----------------
-    def step(self, t=None, x=None, snr_db=None, dl_snr_db=None, vel=None):
+    def step(self, t=None, x=None, snr_db=None, dl_snr_db=None, vel=None, pathgain_db=None):
         cfg = self.cfg
         T = self.T
         self.dec.begin()
         hid = self.last_hid
         dl_ref = None
-        if self.C > 1:                                   # engine.py:918-924 with NRNet.step_cells
+        if self.C > 1 and pathgain_db is not None:       # engine.py:909-915: the path gain as given, no radio
+            pg = pathgain_db
+            out = self._net_step_cells(T, pg, hid)
+            snr = self.serving_sinr_db()
+        elif self.C > 1:                                 # engine.py:918-924 with NRNet.step_cells
             assert snr_db is None and x is not None and x.dim() == 3, "several cells: pass poses [E,R,2]"
             if self.radio is None:
                 self.radio = Radio(cfg, self.E, self.rng)
@@ -1046,6 +1138,11 @@ class OracleEngine:
         rx = pg + cfg.ue_tx_dbm
         asc = self.assoc
         asc.associate(rx)
+        rlf = asc.rlf
+        sinr_c = None
+        if rlf:                                          # radio link monitoring once per step (nr_engine.py:733-736)
+            sinr_c = self._cells_sinr_db()
+            self._rlf_links(asc.rlm(self.serving_sinr_db(), rx, sinr_c, g0, self.dec), True)
         k_ho, tgt = asc.plan(rx, self.dec)
         g_ho = g0 + k_ho
         fired = torch.zeros(self.E, self.R, dtype=torch.bool)
@@ -1053,7 +1150,11 @@ class OracleEngine:
             self._rician_update(g0)
         for rel, dls, uls, sr, cqi, ack in self.schedule(g0):
             g = g0 + rel
-            ho = (k_ho >= 0) & (k_ho <= rel) & ~fired
+            if rlf:
+                ho, failed = self._rlf_events(g, k_ho, fired, g_ho, rx, sinr_c)
+                fired = fired | failed
+            else:
+                ho = (k_ho >= 0) & (k_ho <= rel) & ~fired
             self._handover(ho, tgt, g_ho)
             fired = fired | ho
             self._evolve(g, rel)
@@ -1074,11 +1175,37 @@ class OracleEngine:
                 if self.pc_on:
                     self.pc_backoff = self._pc_backoff(rx_s)
                 self._slot(self.ul, g, t + (rel + 1) / N, uls, ul_ref, gain, rel, 0)
-        late = (k_ho >= 0) & ~fired                      # triggers after the last active slot of the step
+        if rlf:
+            late = self._rlf_events(g0 + N - 1, k_ho, fired, g_ho, rx, sinr_c)[0]
+        else:
+            late = (k_ho >= 0) & ~fired                  # triggers after the last active slot of the step
         self._handover(late, tgt, g_ho)
         out = self._finish(t, hid)
         out["serving_cell"] = asc.serv.clone()
+        if rlf:
+            out["rlf"] = asc.rlf_active.clone()
         return out
+
+    def _rlf_events(self, g, k_ho, fired, g_ho, rx, sinr_c):
+        """NRNet._rlf_events (nr_engine.py:691-702): T310 expiries due by slot g (cancelled by a handover that precedes
+        or ties them), the re-establishments that complete by g; returns (the handovers due without the robots in
+        RLF, the robots declared now)."""
+        asc = self.assoc
+        ho = (k_ho >= 0) & (g_ho <= g) & ~fired
+        exp = asc.expired(g) & ~(ho & (g_ho <= asc.t310_end))
+        asc.declare(exp, rx, sinr_c, self.dec)
+        self._rlf_links(exp, self.cfg.rlf_flush)
+        self._rlf_links(asc.complete(g), False)
+        return ho & ~asc.rlf_active & ~exp, exp
+
+    def _cells_sinr_db(self):
+        """nr_engine.py:704-707: the SINR estimate toward every cell [E,R,C] against each gNB's N+I estimate."""
+        ni = 10 * torch.log10(self.ni_ul.mean(-1))[:, None, :]
+        return self._pg + self.cfg.ue_tx_dbm - self.ref_db - ni
+
+    def _rlf_links(self, m, flush):
+        """NRNet._rlf_links (nr_engine.py:684-689): the MAC side of a handover for the robots m."""
+        self._link_handover(m, flush)
 
     def _pc_backoff(self, rx_serv):
         """Fractional UL power control (nr_engine.py:671-675): backoff from the full power over snr_ref_prbs PRBs
@@ -1089,10 +1216,14 @@ class OracleEngine:
     def _handover(self, ho, target, g):
         """NRNet._handover (nr_engine.py:677-682): switch, then UlMac.handover (mac_ul.py:238-247)."""
         self.assoc.switch(ho, target, g)
+        self._link_handover(ho, self.cfg.ho_rlc == "flush")
+
+    def _link_handover(self, m, flush):
+        """UlMac.handover (mac_ul.py:238-247) of the robots m."""
         u = self.ul
-        u.ctr["lost_frames"] += u.handover(ho, self.cfg.ho_rlc == "flush", self.cfg.harq_fail == "drop")
-        u.sr_t = torch.where(ho, torch.full_like(u.sr_t, -1), u.sr_t)
-        u.bsr = torch.where(ho, u.unsent(), u.bsr)
+        u.ctr["lost_frames"] += u.handover(m, flush, self.cfg.harq_fail == "drop")
+        u.sr_t = torch.where(m, torch.full_like(u.sr_t, -1), u.sr_t)
+        u.bsr = torch.where(m, u.unsent(), u.bsr)
 
     def serving_sinr_db(self):
         """nr_engine.py:709-713: full-power SINR over snr_ref_prbs PRBs against the serving gNB's N+I estimate."""
@@ -1582,11 +1713,13 @@ class OracleEngine:
                 items.append(("net.k_fresh", self, "k_fresh"))
         if self.C > 1:
             items += [(k, self, v) for k, v in self.CELL_KEYS.items()]
-            items += [("assoc." + n, self.assoc, n) for n in (*Association.INIT, "pending")]
+            items += [("assoc." + n, self.assoc, n) for n in (*self.assoc._init, "pending")]
         return items
 
     def state(self):
         out = {k: getattr(o, v) for k, o, v in self._state_items() if getattr(o, v) is not None}
+        if self.C > 1 and self.assoc.rlf:                # the RLF counters (radio.py:342, 375)
+            out.update({f"assoc.ctr[{k}]": torch.tensor(v) for k, v in self.assoc.ctr.items()})
         out["rng.episode"] = self.rng.episode
         out["rng.ctr[1]"] = self.rng.ctr[SUBMIT]
         out["rng.ctr[2]"] = self.rng.ctr[STEP]

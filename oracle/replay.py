@@ -54,6 +54,8 @@ def run(eng, d, kind, steps=None, on_step=None, to=lambda a: torch.from_numpy(a)
         x = to(d["x"][s])
         if kind == "snr3":
             o = eng.step(None, snr_db=x)
+        elif kind == "pg":
+            o = eng.step(None, pathgain_db=x)
         elif "vel" in d.files:
             o = eng.step(None, x, vel=to(d["vel"][s]))
         else:

@@ -388,6 +388,32 @@ CASES = {
                             n_harq=8, max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2,
                             cell_layout="hex", cell_isd_m=150.0, noise_model="thermal", fading_rho_per_ms=0.5),
                    E=2, R=16, steps=25, kind="pose", arena=300.0, walk=1.0, rates=(0.7,), resets={12: [1]}),
+    # several cells with the path gain given (step(pathgain_db=[E,R,C]), engine.py:909-915): three cells, A3
+    # handovers as the per-link gains drift, Rician K fixed, interference and power control
+    "mc3_pg": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                            max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3, cell_layout="hex",
+                            cell_isd_m=200.0, noise_model="thermal", a3_offset_db=1.0, a3_ttt_ms=2.0,
+                            fading_rician=True, rician_k_db=6.0, rician_k_from_los=False, fading_rho_per_ms=0.5),
+                   E=3, R=16, steps=25, kind="pg", pg=(-125.0, -75.0), pg_walk=2.5, rates=(0.7,), resets={12: [1]}),
+    # radio link failure (nr_engine.py:691-707, 733-736, 778-787; radio.py:456-531) on the path gain input: the
+    # serving SINR crosses Qout / Qin as the per-link gains drift, T310 of 30 ms, re-establishment after 20 ms at the
+    # strongest suitable cell, T311 of 60 ms to idle; A3 handovers that stop T310
+    "mc3_rlf": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                             max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=3, cell_layout="hex",
+                             cell_isd_m=200.0, noise_model="thermal", a3_offset_db=2.0, a3_ttt_ms=5.0,
+                             fading_rho_per_ms=0.5, rlf=True, n310=1, n311=2, t310_ms=30.0, t311_ms=60.0,
+                             reest_delay_ms=20.0),
+                    E=3, R=16, steps=30, kind="pg", pg=(-150.0, -100.0), pg_walk=5.0, rates=(0.7,),
+                    resets={15: [1]}),
+    # radio link failure with poses, the RLC flushed at RLF, the A3 floor (also the cell search's), no handovers
+    "mc2_rlf_flush": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf",
+                                   n_harq=4, max_harq_tx=3, frame_buffer=10, msg_sizes=(1500.0,), n_cells=2,
+                                   cell_layout="hex", cell_isd_m=500.0, noise_model="thermal",
+                                   a3_offset_db=float("inf"), a3_min_target_rsrp_dbm=-112.0, channel="tr38901",
+                                   tr38901_scenario="UMa", tr38901_los="nlos", gnb_height_m=25.0, rlf=True,
+                                   rlf_rlc="flush", n310=2, n311=1, t310_ms=20.0, t311_ms=50.0, reest_delay_ms=10.0,
+                                   fading_rho_per_ms=0.5),
+                          E=3, R=16, steps=30, kind="pose", arena=900.0, walk=25.0, rates=(0.8,), resets={14: [2]}),
     # per-robot Doppler (fading_doppler="per_robot": engine.py:862-864, radio.py:285-300, channels/doppler.py:23-29,
     # nr_engine.py:583-589): speeds from consecutive poses, 0 .. 25 m/s (J0 reaches its first zero near 13 m/s at
     # 3.5 GHz, rho 0 from there), a 0.5 m/s floor
@@ -561,6 +587,15 @@ def _inputs(name, c):
     elif c["kind"] == "snr":
         lo, hi = c["snr"]
         x = rs.uniform(lo, hi, size=(T, E, R)).astype(np.float32)
+    elif c["kind"] == "pg":
+        # the path gain of every robot-cell link [T,E,R,C] (dB): a per-link level plus a slow random walk
+        lo, hi = c["pg"]
+        p = rs.uniform(lo, hi, size=(E, R, c["cfg"]["n_cells"]))
+        xs = []
+        for _ in range(T):
+            xs.append(p.copy())
+            p = np.clip(p + rs.normal(0.0, c["pg_walk"], size=p.shape), lo, hi)
+        x = np.stack(xs).astype(np.float32)
     else:
         lo, hi = c["snr"]
         x = rs.uniform(lo, hi, size=(T, E, R, 1)) + rs.normal(0.0, 2.0, size=(T, E, R, c.get("subbands", 13)))
@@ -652,6 +687,8 @@ def run_case(name, c):
             o = eng.step(None, xs, vel=None if vel is None else torch.from_numpy(vel[s]))
         elif c["kind"] == "snr":
             o = eng.step(None, xs)
+        elif c["kind"] == "pg":
+            o = eng.step(None, pathgain_db=xs)
         else:
             o = eng.step(None, snr_db=xs)
         for k, v in o.items():

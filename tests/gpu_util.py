@@ -201,7 +201,12 @@ def teacher_forced(P, name, dev="cuda:0"):
             eng.add_dl_frames(None, to(nb), to(cls))
         x = to(ref["x"][s])
         vel = to(ref["vel"][s]) if "vel" in ref.files else None
-        o = eng.step(None, snr_db=x) if kind == "snr3" else eng.step(None, x, vel=vel)
+        if kind == "snr3":
+            o = eng.step(None, snr_db=x)
+        elif kind == "pg":
+            o = eng.step(None, pathgain_db=x)
+        else:
+            o = eng.step(None, x, vel=vel)
         set_radio_bound(ref, s, cfg, eng, kind)
         bi, bf, robots = compare(ref, s, o, eng.owner_state(), E, R)
         n_bad += int(robots.sum())

@@ -35,7 +35,12 @@ def test_graph_replay_matches_reference(name):
         cnt = to(ref["counts"][s].astype(np.uint8))
         x = to(ref["x"][s])
         vel = to(ref["vel"][s]) if "vel" in ref.files else None
-        o = g(counts=cnt, snr_db=x) if kind == "snr3" else g(x, cnt, vel=vel)
+        if kind == "snr3":
+            o = g(counts=cnt, snr_db=x)
+        elif kind == "pg":
+            o = g(counts=cnt, pathgain_db=x)
+        else:
+            o = g(x, cnt, vel=vel)
         torch.cuda.synchronize()
         set_radio_bound(ref, s, cfg, eng, kind)
         bi, bf, _ = compare(ref, s, o, eng.owner_state(), E, R)

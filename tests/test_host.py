@@ -21,8 +21,9 @@ def test_refusals_name_each_unimplemented_feature():
     mc = dict(mu=1, n_prb=106, n_cells=3, cell_layout="hex", cell_isd_m=150.0, noise_model="thermal")
     assert EN.refusals(P.NRConfig(**mc)) == []
     assert EN.refusals(P.NRConfig(**mc, a3_offset_db=float("inf"), harq_fail="drop", ho_rlc="flush")) == []
+    assert EN.refusals(P.NRConfig(**mc, rlf=True, rlf_rlc="flush")) == []
     for extra, word in ((dict(n_cells=7), "n_cells=7"), (dict(dl=True), "downlink with several cells"),
-                        (dict(rlf=True), "radio link failure"), (dict(frame_buffer=65), "frame_buffer > 64"),
+                        (dict(rlf=True, rach=True), "RACH"), (dict(frame_buffer=65), "frame_buffer > 64"),
                         (dict(ul_tpc=True), "TPC")):
         assert word in " ".join(f for f, _ in EN.refusals(P.NRConfig(**dict(mc, **extra)))), extra
     # one cell: the 38.214 RBG counts of the standard carriers run (106 PRB: 14 RBGs, 273: 18, 133: 17, 78: 10),
