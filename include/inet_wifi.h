@@ -43,6 +43,7 @@ extern "C" {
 #define INET_WIFI_MAX_CLS 16      /* message classes */
 #define INET_WIFI_MAX_NACC 128    /* support of the Poisson access count */
 #define INET_WIFI_MAX_KF 16       /* plane waves per shadowing field */
+#define INET_WIFI_MAX_A 8         /* access points per env (on one channel: one collision domain) */
 
 #define INET_WIFI_OK 0
 #define INET_WIFI_EINVAL (-1)
@@ -66,13 +67,13 @@ typedef struct InetWifiState {
     float *last_snr;
     int32_t *roam_left, *serv;
     float *att_n, *att_logp, *credit;
-    /* mean-field attempt probability [E][R + 1]: the robots, then the AP's background station */
+    /* mean-field attempt probability [E][R + A]: the robots, then one background station per AP */
     float *tau;
     /* per env [E]: clock, hazard id of the last submit, association pending, counter-RNG key and call counters */
     int64_t *clock, *last_hid;
     uint8_t *pending;
     int32_t *env_id, *episode, *ctr_step, *ctr_submit;
-    /* radio plane waves [E][n_fields][n_modes][3] = (kx, ky, phase) */
+    /* radio plane waves [E][A][n_fields][n_modes][3] = (kx, ky, phase), one set per AP */
     float *field;
 } InetWifiState;
 
@@ -98,8 +99,11 @@ typedef struct InetWifiParams {
     int32_t los_sto;                 /* TR 38.901 stochastic LOS state of every robot-AP link (as InetNrParams) */
     int32_t plos_scn;                /* los_sto: the Pr_LOS formula, 0 UMi, 1 UMa (h_UT <= 13 m), 2 InH */
     float sig_nlos;                  /* los_sto: NLOS shadow-fading sigma (dB); sig is the LOS one */
-    int32_t pad1;
+    int32_t A;                       /* access points (1 .. INET_WIFI_MAX_A), all on one channel: the robots associate to
+                                        the strongest after a reset and roam to an AP stronger by roam_hyst dB, with
+                                        roam_sub sub-steps without channel access (wifi/engine.py:245-257) */
     const float *los_cdf;            /* los_sto: [65536] sorted samples of a unit sum of cosines */
+    float ap_xy[2 * INET_WIFI_MAX_A]; /* AP positions (x, y); gnb_x, gnb_y repeat AP 0 */
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */

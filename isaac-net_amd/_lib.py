@@ -85,7 +85,7 @@ class InetWifiState(C.Structure):
         "ctr_submit", "field")]
 
 
-WIFI_MAX_M, WIFI_MAX_CLS, WIFI_MAX_NACC = 16, 16, 128
+WIFI_MAX_M, WIFI_MAX_CLS, WIFI_MAX_NACC, WIFI_MAX_A = 16, 16, 128, 8
 
 
 class InetWifiParams(C.Structure):
@@ -103,7 +103,8 @@ class InetWifiParams(C.Structure):
                [(n, f32) for n in (
         "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1", "nl_b0", "nl_c", "nl_d", "sig",
         "amp", "pl_const", "pl_exp10", "ue_tx")] + \
-               [("los_sto", i32), ("plos_scn", i32), ("sig_nlos", f32), ("pad1", i32), ("los_cdf", P)]
+               [("los_sto", i32), ("plos_scn", i32), ("sig_nlos", f32), ("A", i32), ("los_cdf", P),
+                ("ap_xy", f32 * (2 * WIFI_MAX_A))]
 
 
 class InetWifiOutputs(C.Structure):

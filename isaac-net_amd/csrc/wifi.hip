@@ -171,20 +171,38 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
 
     // ---------------- inputs, association, MCS (wifi/engine.py:227-259, 295-299) ----------------
     const int64_t t = env_ok ? (tin ? tin[ec] : st.clock[ec]) : 0;
+    // the received power at every AP (poses through the APs' radio, the SNR to the one AP, or rx_dbm [E][R][A]); the
+    // strongest AP after a reset, else a roam to an AP stronger than the serving one by roam_hyst (the first of equal
+    // maxima), which starts the roaming interruption
+    const int A = pm.A;
     float rx = 0.f;
+    int sv = 0;
+    bool roamed = false;
     if (rob) {
-        if (input_kind == 0) {
-            float px = xin[ir * 2], py = xin[ir * 2 + 1];
-            const StoLos sto{pm.los_cdf, pm.plos_scn, pm.sig_nlos, pm.los_sto != 0};
-            rx = radio_rx_dbm(pm, px, py, pm.gnb_x, pm.gnb_y, st.field + (size_t)ec * pm.n_fields * pm.n_modes * 3,
-                              sto);
-        } else if (input_kind == 1) {
-            rx = xin[ir] + pm.noise_dbm;
-        } else {
-            rx = xin[ir];
+        const int s0 = st.serv[ir];
+        const bool pend = st.pending[ec] != 0;
+        float bv = 0.f, cur = 0.f;
+        int best = 0;
+        const float px = input_kind == 0 ? xin[ir * 2] : 0.f, py = input_kind == 0 ? xin[ir * 2 + 1] : 0.f;
+        const StoLos sto{pm.los_cdf, pm.plos_scn, pm.sig_nlos, pm.los_sto != 0};
+        for (int c = 0; c < A; ++c) {
+            float v;
+            if (input_kind == 0)
+                v = radio_rx_dbm(pm, px, py, pm.ap_xy[2 * c], pm.ap_xy[2 * c + 1],
+                                 st.field + ((size_t)ec * A + c) * pm.n_fields * pm.n_modes * 3, sto);
+            else if (input_kind == 1)
+                v = xin[ir] + pm.noise_dbm;
+            else
+                v = xin[ir * A + c];
+            if (c == 0 || v > bv) { bv = v; best = c; }
+            if (c == s0) cur = v;
         }
+        const bool better = bv > cur + pm.roam_hyst;
+        roamed = better && !pend && best != s0;
+        sv = (pend || roamed) ? best : s0;
+        rx = sv == s0 ? cur : bv;
     }
-    const float snr = rx - pm.noise_dbm;     // one AP: the association keeps AP 0 (no roaming between APs)
+    const float snr = rx - pm.noise_dbm;
     int nm = 0;
     for (int m = 0; m < pm.M; ++m) nm += snr >= pm.thr[m] ? 1 : 0;
     const bool link = nm > 0;
@@ -217,9 +235,6 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     auto fifo_sum = [&]() -> float {
         auto xf = [&](int f) { return s_rem[f * WAVE + lane]; };
         if (F == 16) return aten_row_sum_u<16>(16, xf);
-#ifdef INET_EXP_R16
-        return 0.f;
-#endif
         if (F <= 16) return aten_row_sum_u<16>(F, xf);
         if (F <= 32) return aten_row_sum_u<32>(F, xf);
         if (F <= 64) return aten_row_sum_u<64>(F, xf);
@@ -230,9 +245,11 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     // lane R like a robot (its own tau, window, times and weight; nothing else), else every lane evaluates it too.
     const bool bgl = rb > R;
     const bool is_bg = bgl && env_ok && r == R;
-    float tau = rob ? st.tau[(size_t)ec * (R + 1) + rc] : (is_bg ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0);
-    float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * (R + 1) + R] : pm.tau0;
+    const int NS = R + A;                                  // stations of the domain: robots, one per AP
+    float tau = rob ? st.tau[(size_t)ec * NS + rc] : (is_bg ? st.tau[(size_t)ec * NS + R] : pm.tau0);
+    float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * NS + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
+    if (roamed && pm.roam_sub > 0) roam = pm.roam_sub;
     float att_n = rob ? st.att_n[ir] : 0.f, att_logp = rob ? st.att_logp[ir] : 0.f;
     float credit = rob ? st.credit[ir] : 0.f;
 
@@ -245,22 +262,23 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const bool act_b = wb > 0.f;
     const TauW twb = tau_weights(W0b, Wmb);
 
-    // sum over the stations of the env (robots in lane order, then the background station), torch's CPU order
+    // sum over the R + A stations of the env (robots in lane order, then the APs' background stations, which all hold
+    // the same values: lane R's, or vb without a spare lane), torch's CPU order
+    auto sum_row = [&](const float* base, float vb) -> float {
+        const float* row = base + gseg * rb;
+        auto xr = [&](int i) { return i < R ? row[i] : (bgl ? row[R] : vb); };
+        if (NS == 17) return aten_row_sum_u<17>(17, xr);
+        if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
+        if (NS <= 16) return aten_row_sum_u<16>(NS, xr);
+        if (NS <= 33) return aten_row_sum_u<33>(NS, xr);
+        if (NS <= 65) return aten_row_sum_u<65>(NS, xr);
+        return aten_row_sum(NS, xr);
+    };
     auto dom_sum = [&](float v, float vb) -> float {
         __syncthreads();
         s_red[lane] = v;
         __syncthreads();
-        const float* row = s_red + gseg * rb;
-        auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
-        if (R == 16) return aten_row_sum_u<17>(17, xr);
-#ifdef INET_EXP_R16
-        return 0.f;
-#endif
-        if (R < 8) return aten_row_sum_u<8>(R + 1, xr);
-        if (R < 16) return aten_row_sum_u<16>(R + 1, xr);
-        if (R < 17) return aten_row_sum_u<17>(R + 1, xr);
-        if (R < 33) return aten_row_sum_u<33>(R + 1, xr);
-        return aten_row_sum_u<65>(R + 1, xr);
+        return sum_row(s_red, vb);
     };
 
     // four such sums at once (one LDS round trip): rows s_red and s_red4[0..2]
@@ -269,19 +287,6 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         __syncthreads();
         s_red[lane] = v0; s_red4[lane] = v1; s_red4[WAVE + lane] = v2; s_red4[2 * WAVE + lane] = v3;
         __syncthreads();
-        auto sum_row = [&](const float* base, float vb) -> float {
-            const float* row = base + gseg * rb;
-            auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
-            if (R == 16) return aten_row_sum_u<17>(17, xr);
-#ifdef INET_EXP_R16
-            return 0.f;
-#endif
-            if (R < 8) return aten_row_sum_u<8>(R + 1, xr);
-            if (R < 16) return aten_row_sum_u<16>(R + 1, xr);
-            if (R < 17) return aten_row_sum_u<17>(R + 1, xr);
-            if (R < 33) return aten_row_sum_u<33>(R + 1, xr);
-            return aten_row_sum_u<65>(R + 1, xr);
-        };
         o0 = sum_row(s_red, b0);
         o1 = sum_row(s_red4, b1);
         o2 = sum_row(s_red4 + WAVE, b2);
@@ -425,14 +430,16 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     // ---------------- per-robot state and outputs of _serve ----------------
     const bool keep = fifo_sum() > 0.f;
     if (rob) {
-        st.tau[(size_t)ec * (R + 1) + rc] = tau;
-        if (r == 0 && !bgl) st.tau[(size_t)ec * (R + 1) + R] = tau_b;
+        st.tau[(size_t)ec * NS + rc] = tau;
+        if (r == 0 && !bgl)
+            for (int a = 0; a < A; ++a) st.tau[(size_t)ec * NS + R + a] = tau_b;
         st.roam_left[ir] = roam;
         st.credit[ir] = keep ? credit : 0.0f;
         st.att_n[ir] = keep ? att_n : 0.0f;
         st.att_logp[ir] = keep ? att_logp : 0.0f;
     }
-    if (is_bg) st.tau[(size_t)ec * (R + 1) + R] = tau;
+    if (is_bg)
+        for (int a = 0; a < A; ++a) st.tau[(size_t)ec * NS + R + a] = tau;
     o_acc = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
     o_pf = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
     o_busy = busy_sum / (float)K;
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     o_busy = (float)((double)busy_ns / (double)Tn);
     }
     if (rob) {
-        st.serv[ir] = 0;
+        st.serv[ir] = sv;
         st.last_snr[ir] = snr;
         out.access_ms[ir] = o_acc;
         out.p_fail[ir] = o_pf;
@@ -552,7 +559,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         out.mcs[ir] = link ? pm.mcs_ids[mcs] : -1;
         out.rate_mbps[ir] = link ? rate : 0.0f;
         out.sinr_db[ir] = snr;
-        out.serving_cell[ir] = 0;
+        out.serving_cell[ir] = sv;
     }
 
     // ---------------- end of step: finish_body ----------------
@@ -748,12 +755,15 @@ __global__ void wifi_reset_kernel(InetWifiState st, InetWifiParams pm, const uin
         st.qlen[ir] = 0; st.last_snr[ir] = 0.f; st.roam_left[ir] = 0; st.serv[ir] = 0;
         st.att_n[ir] = 0.f; st.att_logp[ir] = 0.f; st.credit[ir] = 0.f;
     }
-    for (int r = threadIdx.x; r <= R; r += blockDim.x) st.tau[(size_t)e * (R + 1) + r] = pm.tau0;
-    const int Kf = pm.n_modes;
-    for (int q = threadIdx.x; q < pm.n_fields * Kf; q += blockDim.x) {
-        const int fi = q / Kf, kk = q - fi * Kf;
-        draw_plane_wave((uint32_t)pm.seed_key, (uint32_t)st.env_id[e], (uint32_t)ep_new, pm.radio_model, fi, kk,
-                        pm.dcorr[fi], pm.spectrum, st.field + (((size_t)e * pm.n_fields + fi) * Kf + kk) * 3);
+    for (int r = threadIdx.x; r < R + pm.A; r += blockDim.x) st.tau[(size_t)e * (R + pm.A) + r] = pm.tau0;
+    // the fields of every AP: wave kk of AP c is element c K + kk of the field's draws (as the cells of RadioMC)
+    const int Kf = pm.n_modes, A = pm.A;
+    for (int q = threadIdx.x; q < A * pm.n_fields * Kf; q += blockDim.x) {
+        const int c = q / (pm.n_fields * Kf), rem = q - c * pm.n_fields * Kf;
+        const int fi = rem / Kf, kk = rem - fi * Kf;
+        draw_plane_wave((uint32_t)pm.seed_key, (uint32_t)st.env_id[e], (uint32_t)ep_new, pm.radio_model, fi,
+                        c * Kf + kk, pm.dcorr[fi], pm.spectrum,
+                        st.field + ((((size_t)e * A + c) * pm.n_fields + fi) * Kf + kk) * 3);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -794,7 +804,7 @@ int check_params(const InetWifiParams& p) {
         p.n_cls > INET_WIFI_MAX_CLS || p.n_acc_max <= 0 || p.n_acc_max > INET_WIFI_MAX_NACC || p.fp_iters < 1)
         return INET_WIFI_EINVAL;
     if (p.n_fields < 0 || p.n_fields > 3 || p.n_modes < 0 || p.n_modes > INET_WIFI_MAX_KF) return INET_WIFI_EINVAL;
-    if (p.bg_ac < 0 || p.bg_ac > 4) return INET_WIFI_EINVAL;
+    if (p.bg_ac < 0 || p.bg_ac > 4 || p.A < 1 || p.A > INET_WIFI_MAX_A) return INET_WIFI_EINVAL;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
@@ -815,7 +825,7 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     const InetWifiParams& p = *prm;
     int rc = check_params(p);
     if (rc) return rc;
-    if (input_kind < 0 || input_kind > 2) return INET_WIFI_EINVAL;
+    if (input_kind < 0 || input_kind > 2 || (input_kind == 1 && p.A != 1)) return INET_WIFI_EINVAL;
     if (input_kind == 0 && p.n_fields < 1) return INET_WIFI_EINVAL;
     // segments of next_pow2(R + 1) lanes, lane R for the background station of the mean-field solve (R < 64); as
     // many envs per wave as the submit kernel's segments hold, at most what fits
@@ -858,7 +868,7 @@ int check_dcf(const InetWifiParams& p, const InetDcfParams& d) {
     for (int m = 0; m < p.M; ++m) if (d.ndbps[m] <= 0) return INET_WIFI_EINVAL;
     // whole-byte sizes stay exact in the float32 FIFO
     for (int c = 0; c < p.n_cls; ++c) if (!(p.sizes[c] >= 0.0f && p.sizes[c] <= 16777216.0f)) return INET_WIFI_EINVAL;
-    if (p.per_class_ac || p.bg_w != 0.0f) return INET_WIFI_EUNSUPPORTED;
+    if (p.per_class_ac || p.bg_w != 0.0f || p.A != 1) return INET_WIFI_EUNSUPPORTED;
     return INET_WIFI_OK;
 }
 }  // namespace

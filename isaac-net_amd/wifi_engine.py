@@ -1,13 +1,13 @@
-"""HipWifiEngine: level "WIFI" (the mean-field 802.11 uplink at one access point) over the HIP kernels of
-libinet_nr.so (include/inet_wifi.h).
+"""HipWifiEngine: level "WIFI" (the mean-field 802.11 uplink at one or several access points on one channel) over the
+HIP kernels of libinet_nr.so (include/inet_wifi.h).
 
 Mirrors isaac_net/core/wifi/engine.py (WifiNet, :100-403) on the LevelNet contract (isaac_net/core/levels/base.py:43-360):
 reset(env_ids) / submit(t, requests, snr_db) / step(t, poses_or_snr, cur_hid, *, rx_dbm) -> dict / clock /
 state_dict, with the same inputs, output keys, dtypes and shapes and the same per-env clock rules (t=None uses the
 engine clock; an int or an [E] tensor sets each env's step). What the kernels do not implement is refused at
-construction with HipUnsupported: several access points (and with them roaming and several channels), hidden nodes,
-AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio features the NR engine
-refuses.
+construction with HipUnsupported: access points on different channels (several collision domains), more than 8
+APs, hidden nodes, AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio features
+the NR engine refuses. Several APs on one channel run with association and roaming.
 
 All state lives in device tensors that torch allocates; every call hands the library plain pointers.
 """
@@ -38,7 +38,9 @@ def wifi_refusals(cfg: NRConfig):
         if cond:
             out.append((what, why))
     n_ap = len(wc.ap_xy(cfg))
-    no(n_ap != 1, f"{n_ap} access points", "one AP per env (one collision domain, no roaming)")
+    no(n_ap > 8, f"{n_ap} access points", "up to 8 APs per env")
+    no(len(set(wc.channels(n_ap))) > 1, "APs on different channels (several collision domains)",
+       "APs on one channel (one collision domain)")
     no(wc.hidden_nodes, "hidden_nodes=True", "every robot senses every other one")
     d = derive(cfg, wc)
     no(d.Z > 1, "access categories with different AIFSN in one env (AIFS zones)", "one AIFS zone")
@@ -93,6 +95,7 @@ class HipWifiEngine:
         self.d = derive(cfg, self.wc)
         self.K = self.Ksub = self.d.K
         self.n_acc_max = self.d.n_acc_max
+        self.A = len(self.wc.ap_xy(cfg))                 # access points, one background station each
         rb = 1 << max(0, (R - 1).bit_length())
         self.envs_per_wave = int(envs_per_wave) if envs_per_wave is not None else 1
         if self.envs_per_wave < 1 or self.envs_per_wave * rb > 64:
@@ -114,10 +117,10 @@ class HipWifiEngine:
             "rem": z(E, F, R, dt=f32), "f_nact": z(E, F, R), "f_snr": z(E, F, R, dt=f32), "f_own": z(E, F, R),
             "qlen": z(E, R), "last_snr": z(E, R, dt=f32), "roam_left": z(E, R), "serv": z(E, R),
             "att_n": z(E, R, dt=f32), "att_logp": z(E, R, dt=f32), "credit": z(E, R, dt=f32),
-            "tau": z(E, R + 1, dt=f32), "clock": z(E, dt=torch.int64), "last_hid": z(E, dt=torch.int64),
+            "tau": z(E, R + self.A, dt=f32), "clock": z(E, dt=torch.int64), "last_hid": z(E, dt=torch.int64),
             "pending": z(E, dt=torch.uint8, v=1), "env_id": torch.arange(E, dtype=i32, device=d),
             "episode": z(E, v=-1), "ctr_step": z(E), "ctr_submit": z(E),
-            "field": z(E, nf, max(cfg.shadow_modes, 1), 3, dt=f32),
+            "field": z(E, self.A, nf, max(cfg.shadow_modes, 1), 3, dt=f32),
         }
         s = _lib.InetWifiState()
         for name, _ in _lib.InetWifiState._fields_:
@@ -160,8 +163,12 @@ class HipWifiEngine:
         rc = radio_config(cfg, wc)
         K = rc.shadow_modes
         p.n_fields, p.n_modes = self._n_fields, K
-        gx, gy = rc.gnb_xy()[0]
+        xy = rc.gnb_xy()
+        gx, gy = xy[0]
         p.gnb_x, p.gnb_y, p.ue_tx = gx, gy, rc.ue_tx_dbm
+        p.A = len(xy)
+        for a, (x_, y_) in enumerate(xy):
+            p.ap_xy[2 * a], p.ap_xy[2 * a + 1] = x_, y_
         dc = (rc.shadow_dcorr_m, 0.0, 0.0)
         p.spectrum = 0 if rc.shadow_acf == "sos" else 1
         if rc.channel == "tr38901":
@@ -335,13 +342,15 @@ class HipWifiEngine:
             raise ValueError("pass poses, an SNR [E,R] or rx_dbm=[E,R,A]")
         E, R = self.E, self.R
         if rx_dbm is not None:
-            xin = rx_dbm.to(self.dev, torch.float32)
-            if tuple(xin.shape) != (E, R, 1):
-                raise ValueError(f"rx_dbm must be [E,R,A] = {(E, R, 1)}")
-            xin, kind = xin[..., 0].contiguous(), 2
+            xin = rx_dbm.to(self.dev, torch.float32).contiguous()
+            if tuple(xin.shape) != (E, R, self.A):
+                raise ValueError(f"rx_dbm must be [E,R,A] = {(E, R, self.A)}")
+            kind = 2
         elif x.dim() == 3:
             xin, kind = x[..., :2].to(self.dev, torch.float32).contiguous(), 0
         else:
+            if self.A != 1:
+                raise ValueError(f"{self.A} APs: pass poses [E,R,2|3] or rx_dbm=[E,R,A], not an SNR")
             xin, kind = x.to(self.dev, torch.float32).contiguous(), 1
             if tuple(xin.shape) != (E, R):
                 raise ValueError(f"SNR must be [E,R] = {(E, R)}")
@@ -380,14 +389,14 @@ class HipWifiEngine:
                "roam_left": L(st["roam_left"]), "att_n": st["att_n"], "att_logp": st["att_logp"],
                "credit": st["credit"], "serv": L(st["serv"]), "pending": st["pending"] != 0,
                "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"])}
-        f = st["field"]
+        f = st["field"].permute(1, 0, 2, 3, 4)                     # [A, E, NF, K, 3]: the cells of RadioMC
         if self.config.channel == "tr38901":
             for j, n in enumerate(("sf_los", "sf_nlos", "los_field")):
-                out[f"radio.ch.{n}.k"] = f[None, :, j, :, :2]
-                out[f"radio.ch.{n}.phi"] = f[None, :, j, :, 2]
+                out[f"radio.ch.{n}.k"] = f[:, :, j, :, :2]
+                out[f"radio.ch.{n}.phi"] = f[:, :, j, :, 2]
         else:
-            out["radio.k"] = f[None, :, 0, :, :2]
-            out["radio.phi"] = f[None, :, 0, :, 2]
+            out["radio.k"] = f[:, :, 0, :, :2]
+            out["radio.phi"] = f[:, :, 0, :, 2]
         return out
 
     def load_state_dict(self, sd):
@@ -416,14 +425,15 @@ class HipWifiEngine:
         st["ctr_submit"].copy_(I(g("rng.ctr[1]")))
         st["ctr_step"].copy_(I(g("rng.ctr[2]")))
         names = (("sf_los", 0), ("sf_nlos", 1), ("los_field", 2)) if self.config.channel == "tr38901" else ()
+        fv = st["field"].permute(1, 0, 2, 3, 4)                    # [A, E, NF, K, 3] view of the buffer
         if names:
             for n, j in names:
                 if f"radio.ch.{n}.k" in sd:
-                    st["field"][:, j, :, :2].copy_(g(f"radio.ch.{n}.k")[0])
-                    st["field"][:, j, :, 2].copy_(g(f"radio.ch.{n}.phi")[0])
+                    fv[:, :, j, :, :2] = g(f"radio.ch.{n}.k")
+                    fv[:, :, j, :, 2] = g(f"radio.ch.{n}.phi")
         elif "radio.k" in sd:
-            st["field"][:, 0, :, :2].copy_(g("radio.k")[0])
-            st["field"][:, 0, :, 2].copy_(g("radio.phi")[0])
+            fv[:, :, 0, :, :2] = g("radio.k")
+            fv[:, :, 0, :, 2] = g("radio.phi")
 
 
 class HipWifiDcfEngine(HipWifiEngine):
@@ -437,8 +447,9 @@ class HipWifiDcfEngine(HipWifiEngine):
     def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, envs_per_wave=None):
         cfg = cfg if cfg is not None else NRConfig()
         wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
-        if wc.bg_stations > 0 or wc.class_ac is not None:
-            raise HipUnsupported("level WIFI_DCF: one access category for every robot and no background stations")
+        if wc.bg_stations > 0 or wc.class_ac is not None or len(wc.ap_xy(cfg)) != 1:
+            raise HipUnsupported("level WIFI_DCF: one AP, one access category for every robot and no background "
+                                 "stations")
         self._dcf_ready = False
         super().__init__(E, R, device, cfg, seed=seed, envs_per_wave=envs_per_wave)
         self._build_dcf()

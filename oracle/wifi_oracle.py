@@ -3,8 +3,8 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
 checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
 
-A from-scratch torch-CPU restatement of isaac-net's WifiNet with one access point, for the configs the HIP backend
-implements (one AP, so one collision domain; no hidden nodes; one AIFS zone):
+A from-scratch torch-CPU restatement of isaac-net's WifiNet for the configs the HIP backend implements (one collision
+domain: one AP, or several APs on one channel with association and roaming; no hidden nodes; one AIFS zone):
   LevelNet         core/levels/base.py:43-360 (clock, reset, submit, step, the regions' order)
   add_body         core/proto/netsim_fast.py:136-160 (enqueue into FIFO slot count)
   finish_body      core/proto/netsim_fast.py:185-206 (delivered / timed out, newest, det_env, stable compaction)
@@ -20,10 +20,11 @@ The element-wise operations, the reduction calls and their order are those of th
 the oracle is bitwise equal to the reference (pinned by tests/golden/traj_w_*.npz, every state tensor and output
 after every step). The constants come from isaac_net_amd.wifi_config (pinned by the same fixtures' static tensors).
 
-Parity status: every function here is pinned by the five golden Wi-Fi trajectories, including both access-noise
-modes, RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background
-stations, both radio models and partial resets. Not implemented (refused, as by the HIP backend): several APs,
-hidden nodes, AIFS zones (Z > 1), roaming interruptions with several APs.
+Parity status: every function here is pinned by the golden Wi-Fi trajectories, including both access-noise modes,
+RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background stations,
+both radio models, the stochastic LOS state, several APs on one channel with roaming and its interruption, and partial
+resets. Not implemented (refused, as by the HIP backend): APs on different channels (several collision domains),
+hidden nodes, AIFS zones (Z > 1).
 """
 from __future__ import annotations
 
@@ -45,7 +46,8 @@ class WifiOracle:
     def __init__(self, E, R, cfg, seed=0):
         from isaac_net_amd.wifi_config import WifiConfig, derive, radio_config
         wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
-        assert len(wc.ap_xy(cfg)) == 1 and not wc.hidden_nodes, "one AP, no hidden nodes"
+        A = len(wc.ap_xy(cfg))
+        assert len(set(wc.channels(A))) == 1 and not wc.hidden_nodes, "one channel (one domain), no hidden nodes"
         d = derive(cfg, wc)
         assert d.Z == 1, "one AIFS zone"
         self.cfg, self.wc, self.d, self.E, self.R = cfg, wc, d, E, R
@@ -57,10 +59,11 @@ class WifiOracle:
         self.ac_W0, self.ac_Wmax = torch.from_numpy(d.ac_W0), torch.from_numpy(d.ac_Wmax)
         self.ac_aifsn, self.ac_txop = torch.from_numpy(d.ac_aifsn), torch.from_numpy(d.ac_txop)
         self.cls_ac = torch.from_numpy(d.cls_ac)
-        self.bg_w = torch.full((E, 1), float(wc.bg_stations))
-        self.bg_rate = torch.full((E, 1), d.bg_rate, dtype=f)
-        self.bg_B = torch.full((E, 1), float(wc.bg_frame_bytes))
-        self.bg_ac = torch.full((E, 1), d.bg_ac, dtype=torch.long)
+        self.A = A                                       # one saturated background station per AP (engine.py:147-151)
+        self.bg_w = torch.full((E, A), float(wc.bg_stations))
+        self.bg_rate = torch.full((E, A), d.bg_rate, dtype=f)
+        self.bg_B = torch.full((E, A), float(wc.bg_frame_bytes))
+        self.bg_ac = torch.full((E, A), d.bg_ac, dtype=torch.long)
         self.lgamma = torch.from_numpy(d.lgamma)
         self.rng = CounterRNG(seed, E)
         self.radio_cfg = radio_config(cfg, wc)
@@ -72,7 +75,7 @@ class WifiOracle:
         self.clock = z((E,), 0, torch.long)
         self.last_snr = z((E, R), 0.0, f)
         self.last_hid = z((E,), 0, torch.long)
-        self.tau = z((E, R + 1), d.tau0, f)
+        self.tau = z((E, R + A), d.tau0, f)
         self.roam_left = z((E, R), 0, torch.long)
         self.att_n, self.att_logp, self.credit = z((E, R), 0.0, f), z((E, R), 0.0, f), z((E, R), 0.0, f)
         self.serv = z((E, R), 0, torch.long)

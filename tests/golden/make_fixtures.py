@@ -549,6 +549,13 @@ WIFI_CASES = {
                            cell_positions_m=((150.0, 150.0),)),
                   wifi=dict(ap_height_m=6.0),
                   E=3, R=16, steps=30, kind="pose", arena=300.0, walk=4.0, rates=(1.5, 0.5), resets={14: [0]}),
+    # three APs on one channel (one collision domain, the reference's default n_channels=1): max-RSSI association,
+    # roaming with a 3 dB hysteresis and a 2-sub-step interruption, one background station per AP, robots crossing a
+    # 240 m arena
+    "w_multi": dict(cfg=dict(control_step_ms=10.0, frame_buffer=10, msg_sizes=(800.0, 2000.0), timeout_steps=5),
+                    wifi=dict(ap_positions_m=((40.0, 40.0), (200.0, 60.0), (120.0, 200.0)), roam_hyst_db=3.0,
+                              roam_ms=2.0, bg_stations=1),
+                    E=3, R=16, steps=30, kind="pose", arena=240.0, walk=6.0, rates=(1.0, 0.4), resets={14: [1]}),
     # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
     # AP, 1500 B messages, 20 sub-steps per control step
     "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),

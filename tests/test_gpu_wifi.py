@@ -22,7 +22,7 @@ import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig
 
 pytestmark = pytest.mark.gpu
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_dcf"]
 
 # relative tolerance, absolute floor
 FLOAT_TOL = {"tau": (2e-5, 1e-9), "att_logp": (2e-5, 1e-6), "credit": (2e-5, 1e-5), "_last_snr": (1e-5, 6.1e-5),

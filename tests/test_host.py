@@ -142,6 +142,19 @@ def test_per_link_delay_spread_and_k_from_los_refusals():
                                   tr38901_scenario="UMi", fading_delay_spread_ns=300.0)) == []
 
 
+def test_wifi_several_aps_refusals():
+    """Several APs run on one channel (one collision domain, the default n_channels=1); APs on different channels
+    (several collision domains) and more than 8 APs are refused, and level WIFI_DCF keeps one AP."""
+    from isaac_net_amd.wifi_config import WifiConfig
+    from isaac_net_amd.wifi_engine import wifi_refusals
+    aps = ((0.0, 0.0), (100.0, 0.0), (50.0, 80.0))
+    assert wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=aps, roam_ms=2.0))) == []
+    names = " ".join(f for f, _ in wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=aps, n_channels=3))))
+    assert "different channels" in names
+    many = tuple((10.0 * i, 0.0) for i in range(9))
+    assert "9 access points" in " ".join(f for f, _ in wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=many))))
+
+
 def test_wifi_stochastic_los_refusals():
     """Level WIFI runs the stochastic LOS state (the reference's default) on UMi, UMa up to 13 m and InH; InF and UMa
     above 13 m are refused, as at the NR levels."""

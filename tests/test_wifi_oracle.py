@@ -14,7 +14,7 @@ from oracle.wifi_oracle import WifiOracle
 import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig, derive, mcs_table
 
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_dcf"]
 
 
 def load(name):
