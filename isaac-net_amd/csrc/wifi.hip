@@ -142,8 +142,10 @@ DEV void dcf_busy(const InetWifiParams& pm, const InetDcfParams& dp, int B, int 
 }  // namespace
 
 // ======================================================================================= step kernel
-// DCF = false: the mean-field level (WifiNet._serve); true: the per-slot CSMA/CA level (integer backoff counters)
-template <bool DCF>
+// DCF = false: the mean-field level (WifiNet._serve); true: the per-slot CSMA/CA level (integer backoff counters).
+// MA: several APs (pm.A > 1); the one-AP build fixes A = 1, which keeps the station count R + 1 a compile-time
+// offset of R (measured: the general count costs a fifth of the one-AP step through register allocation)
+template <bool DCF, bool MA = false>
 __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetWifiParams pm,
                                                          const int64_t* __restrict__ tin, int input_kind,
                                                          const float* __restrict__ xin,
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     // the received power at every AP (poses through the APs' radio, the SNR to the one AP, or rx_dbm [E][R][A]); the
     // strongest AP after a reset, else a roam to an AP stronger than the serving one by roam_hyst (the first of equal
     // maxima), which starts the roaming interruption
-    const int A = pm.A;
+    const int A = MA ? pm.A : 1;
     float rx = 0.f;
     int sv = 0;
     bool roamed = false;
@@ -241,12 +243,13 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         return aten_row_sum(F, xf);
     };
     if constexpr (!DCF) {
-    // The AP's background station is station R of the domain. With a lane to spare in the segment (rb > R) it runs in
-    // lane R like a robot (its own tau, window, times and weight; nothing else), else every lane evaluates it too.
-    const bool bgl = rb > R;
-    const bool is_bg = bgl && env_ok && r == R;
+    // The APs' background stations are stations R .. R + A - 1 of the domain (identical: the same weight, window,
+    // times and start, so the same tau). With lanes to spare in the segment (rb >= R + A) each runs in its lane like
+    // a robot (nothing else), else every lane evaluates one and the sums count it A times.
     const int NS = R + A;                                  // stations of the domain: robots, one per AP
-    float tau = rob ? st.tau[(size_t)ec * NS + rc] : (is_bg ? st.tau[(size_t)ec * NS + R] : pm.tau0);
+    const bool bgl = rb >= NS;
+    const bool is_bg = bgl && env_ok && r >= R && r < NS;
+    float tau = rob ? st.tau[(size_t)ec * NS + rc] : (is_bg ? st.tau[(size_t)ec * NS + r] : pm.tau0);
     float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * NS + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
     if (roamed && pm.roam_sub > 0) roam = pm.roam_sub;
@@ -263,22 +266,19 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const TauW twb = tau_weights(W0b, Wmb);
 
     // sum over the R + A stations of the env (robots in lane order, then the APs' background stations, which all hold
-    // the same values: lane R's, or vb without a spare lane), torch's CPU order
-    auto sum_row = [&](const float* base, float vb) -> float {
-        const float* row = base + gseg * rb;
-        auto xr = [&](int i) { return i < R ? row[i] : (bgl ? row[R] : vb); };
-        if (NS == 17) return aten_row_sum_u<17>(17, xr);
-        if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
-        if (NS <= 16) return aten_row_sum_u<16>(NS, xr);
-        if (NS <= 33) return aten_row_sum_u<33>(NS, xr);
-        if (NS <= 65) return aten_row_sum_u<65>(NS, xr);
-        return aten_row_sum(NS, xr);
-    };
+    // the same values: lane R's, or vb without a spare lane), torch's CPU order. (dom_sum and dom_sum4 each keep
+    // their own copy of the row sum: one shared helper made the compiler spill to scratch.)
     auto dom_sum = [&](float v, float vb) -> float {
         __syncthreads();
         s_red[lane] = v;
         __syncthreads();
-        return sum_row(s_red, vb);
+        const float* row = s_red + gseg * rb;
+        auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
+        if (NS == 17) return aten_row_sum_u<17>(17, xr);
+        if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
+        if (NS <= 16) return aten_row_sum_u<16>(NS, xr);
+        if (NS <= 33) return aten_row_sum_u<33>(NS, xr);
+        return aten_row_sum_u<65>(NS, xr);                  // (R + A <= 65: checked by the entry points)
     };
 
     // four such sums at once (one LDS round trip): rows s_red and s_red4[0..2]
@@ -287,6 +287,15 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         __syncthreads();
         s_red[lane] = v0; s_red4[lane] = v1; s_red4[WAVE + lane] = v2; s_red4[2 * WAVE + lane] = v3;
         __syncthreads();
+        auto sum_row = [&](const float* base, float vb) -> float {
+            const float* row = base + gseg * rb;
+            auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
+            if (NS == 17) return aten_row_sum_u<17>(17, xr);
+            if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
+            if (NS <= 16) return aten_row_sum_u<16>(NS, xr);
+            if (NS <= 33) return aten_row_sum_u<33>(NS, xr);
+            return aten_row_sum_u<65>(NS, xr);
+        };
         o0 = sum_row(s_red, b0);
         o1 = sum_row(s_red4, b1);
         o2 = sum_row(s_red4 + WAVE, b2);
@@ -438,8 +447,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         st.att_n[ir] = keep ? att_n : 0.0f;
         st.att_logp[ir] = keep ? att_logp : 0.0f;
     }
-    if (is_bg)
-        for (int a = 0; a < A; ++a) st.tau[(size_t)ec * NS + R + a] = tau;
+    if (is_bg) st.tau[(size_t)ec * NS + r] = tau;
     o_acc = acc_n > 0.f ? (acc_sum / clamp_min(acc_n, 1.0f)) / 1000.0f : NAN;
     o_pf = acc_n > 0.f ? p_sum / clamp_min(acc_n, 1.0f) : NAN;
     o_busy = busy_sum / (float)K;
@@ -804,7 +812,7 @@ int check_params(const InetWifiParams& p) {
         p.n_cls > INET_WIFI_MAX_CLS || p.n_acc_max <= 0 || p.n_acc_max > INET_WIFI_MAX_NACC || p.fp_iters < 1)
         return INET_WIFI_EINVAL;
     if (p.n_fields < 0 || p.n_fields > 3 || p.n_modes < 0 || p.n_modes > INET_WIFI_MAX_KF) return INET_WIFI_EINVAL;
-    if (p.bg_ac < 0 || p.bg_ac > 4 || p.A < 1 || p.A > INET_WIFI_MAX_A) return INET_WIFI_EINVAL;
+    if (p.bg_ac < 0 || p.bg_ac > 4 || p.A < 1 || p.A > INET_WIFI_MAX_A || p.R + p.A > 65) return INET_WIFI_EINVAL;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
@@ -827,16 +835,20 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     if (rc) return rc;
     if (input_kind < 0 || input_kind > 2 || (input_kind == 1 && p.A != 1)) return INET_WIFI_EINVAL;
     if (input_kind == 0 && p.n_fields < 1) return INET_WIFI_EINVAL;
-    // segments of next_pow2(R + 1) lanes, lane R for the background station of the mean-field solve (R < 64); as
-    // many envs per wave as the submit kernel's segments hold, at most what fits
-    const int rb = p.R < WAVE ? next_pow2(p.R + 1) : WAVE;
+    // segments of next_pow2(R + A) lanes, lanes R .. R + A - 1 for the APs' background stations of the mean-field
+    // solve (R + A <= 64); as many envs per wave as the submit kernel's segments hold, at most what fits
+    const int rb = p.R + p.A <= WAVE ? next_pow2(p.R + p.A) : WAVE;
     InetWifiParams pm = p;
     pm.envs_per_wave = p.envs_per_wave * next_pow2(p.R) / rb > 0 ? p.envs_per_wave * next_pow2(p.R) / rb : 1;
     const int G = pm.envs_per_wave;
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    hipLaunchKernelGGL(wifi_step_kernel<false>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm, t,
-                       input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
+    if (p.A > 1)
+        hipLaunchKernelGGL((wifi_step_kernel<false, true>), dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm,
+                           t, input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
+    else
+        hipLaunchKernelGGL((wifi_step_kernel<false, false>), dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm,
+                           t, input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 
