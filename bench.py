@@ -156,29 +156,31 @@ def copy_calibration(args, res, torch, dev):
         res["copy_calibration_bytes"] = 2 * src.numel()
 
 
-def wifi_step_bytes(eng):
+def wifi_step_bytes(eng, n_cls):
     """Algorithmic HBM bytes of one Wi-Fi step-kernel launch: per station-step the frame FIFO (F slots of cap, cls,
     det, hid, rem, f_nact, f_snr, f_own = 29 B) and the per-station words (queue length, last SNR, roaming, serving AP,
     contention count, log-failure sum, credit, tau = 32 B) read and written once, the pose (8 B), the [E,R,F] outputs
     (delivered, timed out, cap, cls, delay = 22 B per slot) and the per-station outputs (4 int64 + 6 float32 = 56 B);
-    per env the background station's tau, clock, hazard id, RNG key and counters and the shadowing field."""
+    per env the background station's tau, clock, hazard id, RNG key and counters and the shadowing field. The step's
+    enqueue adds the arrival counts (n_cls B) and accepted messages (4 B) per station and the env's submit counter."""
     p = eng._cparams
     F = eng.F
-    per_robot = 2 * (F * 29 + 32) + 8 + F * 22 + 56
-    per_env = 2 * (4 + 8 + 8 + 1 + 4 * 4) + p.n_fields * p.n_modes * 3 * 4
+    per_robot = 2 * (F * 29 + 32) + 8 + F * 22 + 56 + n_cls + 4
+    per_env = 2 * (4 + 8 + 8 + 1 + 4 * 4) + p.n_fields * p.n_modes * 3 * 4 + 2 * 4
     return eng.E * eng.R * per_robot + eng.E * per_env, per_robot
 
 
-def dcf_step_bytes(eng):
+def dcf_step_bytes(eng, n_cls):
     """Algorithmic HBM bytes of one WIFI_DCF step-kernel launch: per station-step the frame FIFO (29 B per slot) read
     and written once, the queue length (read and written), last SNR and serving AP (written), the backoff counter,
     retry stage and contention flag (9 B, read and written), the pose (8 B), the [E,R,F] outputs (22 B per slot) and
     the per-station outputs (56 B); per env the clock, step counter and idle anchor (read and written), the hazard id,
-    RNG key, episode, pending flag, det_env and t, and the shadowing field."""
+    RNG key, episode, pending flag, det_env and t, and the shadowing field. The step's enqueue adds the arrival counts
+    (n_cls B) and accepted messages (4 B) per station and the env's submit counter."""
     p = eng._cparams
     F = eng.F
-    per_robot = 2 * F * 29 + 8 + 4 + 4 + 2 * 9 + 8 + F * 22 + 56
-    per_env = 2 * (8 + 4 + 4) + 8 + 4 + 4 + 1 + 1 + 8 + p.n_fields * p.n_modes * 3 * 4
+    per_robot = 2 * F * 29 + 8 + 4 + 4 + 2 * 9 + 8 + F * 22 + 56 + n_cls + 4
+    per_env = 2 * (8 + 4 + 4) + 8 + 4 + 4 + 1 + 1 + 8 + p.n_fields * p.n_modes * 3 * 4 + 2 * 4
     return eng.E * eng.R * per_robot + eng.E * per_env, per_robot
 
 
@@ -226,7 +228,8 @@ def run_wifi(args, P, torch):
     dev = "cuda:0"
     E = args.envs if args.envs_set else 2048
     R = args.robots if args.robots_set else 16
-    total = args.warmup + args.steps
+    n_graph = 0 if args.no_graph_window else args.steps
+    total = args.warmup + args.steps + (n_graph + 2 if n_graph else 0)
     print(f"# workload {args.workload} {E}x{R}, {total} steps of inputs", file=sys.stderr, flush=True)
     wl = S.Workload(E, R, total, seed=0, device=dev, name=args.workload)
     cfg = wl.cfg
@@ -234,17 +237,17 @@ def run_wifi(args, P, torch):
     from isaac_net_amd.wifi_engine import HipWifiDcfEngine, HipWifiEngine
     eng = (HipWifiDcfEngine if slots else HipWifiEngine)(E, R, dev, cfg, seed=0, envs_per_wave=args.envs_per_wave)
     K = eng.K
+    # one launch per control step: the step enqueues the step's arrival counts itself (step(counts=), the same state
+    # as submit_counts + step)
     for s in range(args.warmup):
-        eng.submit_counts(wl.counts[s])
-        eng.step(None, wl.poses[s])
+        eng.step(None, wl.poses[s], counts=wl.counts[s])
     torch.cuda.synchronize()
     eng.kernel_events = ev = KernelTimer(args.steps, dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         s = args.warmup + i
-        eng.submit_counts(wl.counts[s])
-        eng.step(None, wl.poses[s])
+        eng.step(None, wl.poses[s], counts=wl.counts[s])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     eng.kernel_events = None
@@ -255,13 +258,12 @@ def run_wifi(args, P, torch):
     torch.cuda._sleep(int(2e6 + 4e5 * args.steps))
     for i in range(args.steps):
         s = args.warmup + i
-        eng.submit_counts(wl.counts[s])
-        eng.step(None, wl.poses[s])
+        eng.step(None, wl.poses[s], counts=wl.counts[s])
     torch.cuda.synchronize()
     eng.kernel_events = None
     k_ms = sorted(ev.ms())
     k_avg = sum(k_ms) / len(k_ms)
-    nbytes, per_robot = (dcf_step_bytes if slots else wifi_step_bytes)(eng)
+    nbytes, per_robot = (dcf_step_bytes if slots else wifi_step_bytes)(eng, wl.counts.shape[-1])
     achieved = nbytes / (k_avg * 1e-3) / 1e9
     if slots:
         metric, value, unit = (f"station-steps/sec @{E} envs×{R} stations (level WIFI_DCF, per-slot CSMA/CA)",
@@ -277,7 +279,8 @@ def run_wifi(args, P, torch):
                                   + ("per-slot CSMA/CA over the 20 ms step" if slots else f"K={K} sub-steps of 1 ms")
                                   + ", 1500 B @0.4 per station-step, FIFO 16, 50 m disc, log-distance + shadowing",
                       "envs": E, "stations": R, "substeps_per_step": K, "envs_per_wave": args.envs_per_wave,
-                      "parallelism": "single GPU", "launch": "eager"},
+                      "parallelism": "single GPU",
+                      "launch": "eager, one launch per step (the enqueue in the step kernel)"},
            "env_steps_per_s": E * args.steps / dt,
            "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                         "frac": achieved / PEAK_GBS, "kernel": "wifi_step_kernel",
@@ -287,6 +290,30 @@ def run_wifi(args, P, torch):
                         "kernel_timing": "HIP events around each launch on the launch stream, the timed loop's "
                                          "launches repeated behind a GPU spin",
                         "algorithmic_bytes_per_launch": nbytes, "algorithmic_bytes_per_station_step": per_robot}}
+    if n_graph:
+        # the next n_graph steps as replays of the recorded graph (counts-form enqueue + step), after the timed eager
+        # steps and the spin-timed repeat of their launches; the first two replays (recording) are not timed
+        g = eng.graph_step()
+        base = args.warmup + args.steps
+        for s in range(base, base + 2):
+            g(wl.poses[s], wl.counts[s])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for s in range(base + 2, base + 2 + n_graph):
+            g(wl.poses[s], wl.counts[s])
+        torch.cuda.synchronize()
+        gms = 1e3 * (time.perf_counter() - t1) / n_graph
+        # the same replays with the inputs left in the graph's buffers (a producer writing them in place)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(n_graph):
+            g.replay(0)
+        torch.cuda.synchronize()
+        bms = 1e3 * (time.perf_counter() - t1) / n_graph
+        res["graph_replay"] = {"ms_per_step": gms, "steps": n_graph, "wall_over_kernel": gms / k_avg,
+                               "launch": "HIP graph replay of the step with its enqueue (one kernel node), the inputs "
+                                         "copied into the graph's buffers first (one launch)",
+                               "in_place_ms_per_step": bms, "in_place_wall_over_kernel": bms / k_avg}
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:
         print("# cpu baseline (oracle)", file=sys.stderr, flush=True)

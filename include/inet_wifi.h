@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 3
+#define INET_WIFI_ABI_VERSION 4
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -75,6 +75,9 @@ typedef struct InetWifiState {
     int32_t *env_id, *episode, *ctr_step, *ctr_submit;
     /* radio plane waves [E][A][n_fields][n_modes][3] = (kx, ky, phase), one set per AP */
     float *field;
+    /* [1]: the counts form's global submit calls (each advances every env's SUBMIT counter alike): env e's counter
+       is ctr_submit[e] + calls[0]; a reset sets ctr_submit[e] = -calls[0] */
+    int32_t *calls;
 } InetWifiState;
 
 /* Config constants (derived on the host from NRConfig + WifiConfig; float32 values of the reference's tensors). */
@@ -104,6 +107,14 @@ typedef struct InetWifiParams {
                                         roam_sub sub-steps without channel access (wifi/engine.py:245-257) */
     const float *los_cdf;            /* los_sto: [65536] sorted samples of a unit sum of cosines */
     float ap_xy[2 * INET_WIFI_MAX_A]; /* AP positions (x, y); gnb_x, gnb_y repeat AP 0 */
+    /* The control step's enqueue in the step launch (inet_wifi_step, inet_wifi_dcf_step; NULL elsewhere): with
+       step_counts set, the step first enqueues step_counts [E][R][step_n_cls] uint8 (device) exactly as
+       inet_wifi_submit's counts form does (the same FIFO entries, submit counters and last hazard ids) and writes the
+       messages accepted per robot to step_accepted [E][R] int32 (device, or NULL). One launch in place of three. */
+    const uint8_t *step_counts;
+    int32_t *step_accepted;
+    int32_t step_n_cls;
+    int32_t pad1;
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */
@@ -140,9 +151,11 @@ typedef struct InetDcfParams {
 int32_t inet_wifi_abi_version(void);
 
 /* One control step. t: [E] int64 step of each env (device) or NULL for st->clock. input_kind: 0 poses [E][R][2],
-   1 SNR [E][R] dB, 2 received power [E][R] dBm (float32, device). cur_hid: [E] int64 or NULL for st->last_hid.
+   1 SNR [E][R] dB, 2 received power [E][R][A] dBm (float32, device). cur_hid: [E] int64 or NULL for st->last_hid.
    Replaces the step region of LevelNet.step (levels/base.py:252-316) with WifiNet._snr_from / _serve
-   (wifi/engine.py:227-403). */
+   (wifi/engine.py:227-403), and with prm->step_counts set also the enqueue region before it (the harness's
+   per-class LevelNet.submit calls, base.py:290-299): the env's own FIFO entries in the env's wavefront (a call
+   changes nothing of an env in which no robot sends), the global call count in one extra workgroup. */
 int32_t inet_wifi_step(const InetWifiState *st, const InetWifiParams *prm, const int64_t *t, int32_t input_kind,
                        const float *x, const int64_t *cur_hid, const InetWifiOutputs *out, void *stream);
 
@@ -152,7 +165,7 @@ int32_t inet_wifi_step(const InetWifiState *st, const InetWifiParams *prm, const
    hid [E] int64 or NULL; accepted [E][R] uint8. Counts form (send == NULL): counts [E][R][n_cls] uint8, the calls of
    class 1 first, one call per message index up to the class's largest count over every env (a call is global, as
    LevelNet.submit is); accepted [E][R] int32 = messages accepted; every env's submit counter advances by the number
-   of calls and its last hazard id becomes 0 (a second, one-workgroup launch reduces the counts). */
+   of calls (st->calls[0]) and its last hazard id becomes 0 (a second, one-workgroup launch reduces the counts). */
 int32_t inet_wifi_submit(const InetWifiState *st, const InetWifiParams *prm, const int64_t *t, const int64_t *send,
                          const uint8_t *det, const int64_t *hid, const float *snr, const uint8_t *counts,
                          int32_t n_cls, void *accepted, void *stream);

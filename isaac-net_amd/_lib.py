@@ -82,7 +82,7 @@ class InetWifiState(C.Structure):
     _fields_ = [(n, P) for n in (
         "cap", "cls", "det", "hid", "rem", "f_nact", "f_snr", "f_own", "qlen", "last_snr", "roam_left", "serv",
         "att_n", "att_logp", "credit", "tau", "clock", "last_hid", "pending", "env_id", "episode", "ctr_step",
-        "ctr_submit", "field")]
+        "ctr_submit", "field", "calls")]
 
 
 WIFI_MAX_M, WIFI_MAX_CLS, WIFI_MAX_NACC, WIFI_MAX_A = 16, 16, 128, 8
@@ -104,7 +104,8 @@ class InetWifiParams(C.Structure):
         "gnb_x", "gnb_y", "hh2", "dbp", "pl_a", "pl_n1", "pl_c20", "pl_c2", "nl_b1", "nl_b0", "nl_c", "nl_d", "sig",
         "amp", "pl_const", "pl_exp10", "ue_tx")] + \
                [("los_sto", i32), ("plos_scn", i32), ("sig_nlos", f32), ("A", i32), ("los_cdf", P),
-                ("ap_xy", f32 * (2 * WIFI_MAX_A))]
+                ("ap_xy", f32 * (2 * WIFI_MAX_A)), ("step_counts", P), ("step_accepted", P),
+                ("step_n_cls", i32), ("pad1", i32)]
 
 
 class InetWifiOutputs(C.Structure):
@@ -128,7 +129,7 @@ ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configurati
           -3: "HIP launch failed"}
 
 ABI_VERSION = 15
-WIFI_ABI_VERSION = 3
+WIFI_ABI_VERSION = 4
 _LIB = None
 
 

@@ -139,13 +139,126 @@ DEV void dcf_busy(const InetWifiParams& pm, const InetDcfParams& dp, int B, int 
     }
 }
 
+// One submit call of class cls (0: none) by each robot lane (add_body, proto/netsim_fast.py:136-160): the message
+// takes FIFO slot qlen unless the FIFO is full; f_nact records how many robots of the env hold a message after the
+// call. Convergent over the env's segment (a ballot).
+DEV bool fifo_call(const InetWifiState& st, const InetWifiParams& pm, bool rob, int cls, int& qlen, size_t fo,
+                   int64_t t, bool dt, int64_t hid, float snr, int rb, int lane) {
+    const bool nw = rob && cls > 0 && qlen < pm.F;
+    const int nact = __builtin_popcountll(__ballot(rob && (qlen + (nw ? 1 : 0)) > 0) & seg_bits(rb, lane));
+    if (nw) {
+        const size_t o = fo + (size_t)qlen * pm.R;
+        const int c = cls < pm.n_cls ? cls : pm.n_cls;
+        st.cap[o] = (int32_t)t;
+        st.cls[o] = cls;
+        st.det[o] = dt;
+        st.hid[o] = (int32_t)hid;
+        st.rem[o] = pm.sizes[c - 1];
+        st.f_nact[o] = nact;
+        st.f_snr[o] = snr;
+        st.f_own[o] = qlen;
+        ++qlen;
+    }
+    return nw;
+}
+
+// The counts form's calls as seen by the env of this lane's segment: class 1 first, one call per message index up to
+// the env's largest count of the class (the later calls change nothing of the env). Returns the messages accepted for
+// this robot; calls = the env's number of calls (segment-uniform).
+DEV int fifo_counts(const InetWifiState& st, const InetWifiParams& pm, const uint8_t* __restrict__ counts, int n_cls,
+                    bool rob, size_t ir, int& qlen, size_t fo, int64_t t, bool dt, int64_t hid, float snr, int rb,
+                    int lane, int& calls) {
+    int n_acc = 0;
+    calls = 0;
+    for (int c = 0; c < n_cls; ++c) {
+        const int mine = rob ? counts[ir * n_cls + c] : 0;
+        const int most = seg_max_i(mine, rb);
+        for (int i = 0; i < most; ++i)
+            n_acc += fifo_call(st, pm, rob, mine > i ? c + 1 : 0, qlen, fo, t, dt, hid, snr, rb, lane) ? 1 : 0;
+        calls += most;
+    }
+    return n_acc;
+}
+
+// bytewise maximum of two words of four uint8
+DEV uint32_t max_u8x4(uint32_t a, uint32_t b) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const uint32_t x = (a >> k) & 0xffu, y = (b >> k) & 0xffu;
+        m |= (x > y ? x : y) << k;
+    }
+    return m;
+}
+
+// The global part of the counts form, run by one workgroup: the calls of every class number its largest count over
+// every env and robot, and each call advances every env's SUBMIT call counter (the global word st.calls) and, with
+// set_hid, sets its last hazard id to 0. s_max: n_cls ints of LDS. 16-byte loads, sixteen in flight per lane; with
+// n_cls dividing 16 each byte position of a load holds one class, so every lane keeps a running maximum per byte
+// position; at the end each class's maximum is reduced over the lane's positions and over the wave (shuffles), and
+// lane 0 takes one LDS maximum per class (LDS atomics of every lane on one word serialize).
+DEV void submit_calls(const InetWifiState& st, int E, const uint8_t* __restrict__ counts, size_t n, int n_cls,
+                      int* s_max, bool set_hid) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (tid < n_cls) s_max[tid] = 0;
+    __syncthreads();
+    const bool vec = ((uintptr_t)counts & 15u) == 0u && 16 % n_cls == 0;
+    const size_t n16 = vec ? n / 16 : 0;
+    const uint4* c4 = reinterpret_cast<const uint4*>(counts);
+    uint32_t m0 = 0, m1 = 0, m2 = 0, m3 = 0;
+    constexpr int U = 16;
+    size_t j = tid;
+    for (; j + (size_t)(U - 1) * nt < n16; j += (size_t)U * nt) {
+        uint4 w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) w[u] = c4[j + (size_t)u * nt];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            m0 = max_u8x4(m0, w[u].x); m1 = max_u8x4(m1, w[u].y); m2 = max_u8x4(m2, w[u].z); m3 = max_u8x4(m3, w[u].w);
+        }
+    }
+    for (; j < n16; j += nt) {
+        const uint4 w = c4[j];
+        m0 = max_u8x4(m0, w.x); m1 = max_u8x4(m1, w.y); m2 = max_u8x4(m2, w.z); m3 = max_u8x4(m3, w.w);
+    }
+    if (n16) {
+        const uint32_t ws[4] = {m0, m1, m2, m3};
+        for (int c = 0; c < n_cls; ++c) {
+            int v = 0;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int x = (int)((ws[b >> 2] >> (8 * (b & 3))) & 0xffu);
+                v = (b % n_cls == c && x > v) ? x : v;
+            }
+#pragma unroll
+            for (int o = WAVE / 2; o > 0; o >>= 1) {
+                const int w = __shfl_xor(v, o, WAVE);
+                v = w > v ? w : v;
+            }
+            if ((tid & (WAVE - 1)) == 0 && v > 0) atomicMax(&s_max[c], v);
+        }
+    }
+    for (size_t i = 16 * n16 + tid; i < n; i += nt) {
+        const int v = counts[i];
+        if (v > 0) atomicMax(&s_max[i % (size_t)n_cls], v);
+    }
+    __syncthreads();
+    int tot = 0;
+    for (int c = 0; c < n_cls; ++c) tot += s_max[c];
+    if (tot > 0 && tid == 0) st.calls[0] += tot;
+    if (tot > 0 && set_hid)
+        for (int e = tid; e < E; e += nt) st.last_hid[e] = 0;
+}
+
 }  // namespace
 
 // ======================================================================================= step kernel
 // DCF = false: the mean-field level (WifiNet._serve); true: the per-slot CSMA/CA level (integer backoff counters).
 // MA: several APs (pm.A > 1); the one-AP build fixes A = 1, which keeps the station count R + 1 a compile-time
-// offset of R (measured: the general count costs a fifth of the one-AP step through register allocation)
-template <bool DCF, bool MA = false>
+// offset of R (measured: the general count costs a fifth of the one-AP step through register allocation).
+// CNT: the launch enqueues pm.step_counts first (a build of its own, so that the step without it keeps its register
+// allocation).
+template <bool DCF, bool MA = false, bool CNT = false>
 __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetWifiParams pm,
                                                          const int64_t* __restrict__ tin, int input_kind,
                                                          const float* __restrict__ xin,
@@ -154,6 +267,8 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     extern __shared__ float dyn[];
     __shared__ float s_red[WAVE];
     __shared__ float s_red4[DCF ? 1 : 3 * WAVE];          // three more rows of station values (dom_sum4)
+    __shared__ uint8_t s_hid0[CNT ? WAVE : 1];            // per env: the enqueue's calls clear the last hazard id
+    __shared__ int s_cmax[CNT ? INET_WIFI_MAX_CLS : 1];   // the largest count of every class (workgroup 0)
     const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
     float* s_rem = dyn;                                   // [F][64] bytes left of every frame slot
     float* s_fin = dyn + F * WAVE;                        // [F][64] finish time, then the compaction staging row
@@ -171,8 +286,29 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const size_t ir = (size_t)ec * R + rc;                 // [E][R]
     const size_t fo = (size_t)ec * F * R + rc;             // [E][F][R] slot f at fo + f R
 
-    // ---------------- inputs, association, MCS (wifi/engine.py:227-259, 295-299) ----------------
     const int64_t t = env_ok ? (tin ? tin[ec] : st.clock[ec]) : 0;
+    // ---------------- the control step's enqueue (the counts form of submit, before anything else is live) ----------
+    if constexpr (CNT) {
+        int qlen = rob ? st.qlen[ir] : 0, calls;
+        const int na = fifo_counts(st, pm, pm.step_counts, pm.step_n_cls, rob, ir, qlen, fo, t, false, 0,
+                                   rob ? st.last_snr[ir] : 0.f, rb, lane, calls);
+        if (rob) {
+            st.qlen[ir] = qlen;
+            if (pm.step_accepted) pm.step_accepted[ir] = na;
+        }
+        // the calls clear every env's last hazard id: known from the env's own calls, else (an env with a hazard id
+        // and nothing to send) from a scan of every count for any message
+        bool any = calls > 0;
+        if (!any && env_ok && st.last_hid[ec] != 0) {
+            const size_t n = (size_t)pm.E * R * pm.step_n_cls;
+            bool mine = false;
+            for (size_t j = r; j < n && !mine; j += rb) mine = pm.step_counts[j] != 0;
+            any = seg_any(mine, rb, lane);
+        }
+        if (env_ok && r == 0) s_hid0[gseg] = any;
+    }
+
+    // ---------------- inputs, association, MCS (wifi/engine.py:227-259, 295-299) ----------------
     // the received power at every AP (poses through the APs' radio, the SNR to the one AP, or rx_dbm [E][R][A]); the
     // strongest AP after a reset, else a roam to an AP stronger than the serving one by roam_hyst (the first of equal
     // maxima), which starts the roaming interruption
@@ -571,7 +707,12 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     }
 
     // ---------------- end of step: finish_body ----------------
-    const int64_t chid = env_ok ? (hid_in ? hid_in[ec] : st.last_hid[ec]) : 0;
+    int64_t lhid = env_ok ? st.last_hid[ec] : 0;
+    if (CNT && env_ok && s_hid0[gseg] && lhid != 0) {     // (the enqueue's calls clear it)
+        lhid = 0;
+        if (r == 0) st.last_hid[ec] = 0;
+    }
+    const int64_t chid = env_ok ? (hid_in ? hid_in[ec] : lhid) : 0;
     int newest = -1;
     bool det_hit = false;
     uint64_t vmask = 0, dmask = 0;                         // slots still queued after the step; their det flags
@@ -650,6 +791,9 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         st.ctr_step[ec] = ctr;
         st.pending[ec] = 0;
     }
+    // the enqueue's global calls, counted by workgroup 0 at its end (a one-wave pass over every count)
+    if (CNT && blockIdx.x == 0)
+        submit_calls(st, pm.E, pm.step_counts, (size_t)pm.E * R * pm.step_n_cls, pm.step_n_cls, s_cmax, false);
 }
 
 // ======================================================================================= submit kernel
@@ -677,38 +821,14 @@ __global__ __launch_bounds__(WAVE) void wifi_submit_kernel(InetWifiState st, Ine
     int qlen = rob ? st.qlen[ir] : 0;
     const float snr_in = rob ? (snr ? snr[ir] : st.last_snr[ir]) : 0.f;
     const bool dt = rob && det ? det[ir] != 0 : false;
-    int n_calls = 0, n_acc = 0;
-
-    auto call = [&](int cls) {     // one submit of class cls (0 = none) by this lane
-        const bool nw = rob && cls > 0 && qlen < F;
-        const int nact = __builtin_popcountll(__ballot(rob && (qlen + (nw ? 1 : 0)) > 0) & seg_bits(rb, lane));
-        if (nw) {
-            const size_t o = fo + (size_t)qlen * R;
-            const int c = cls < pm.n_cls ? cls : pm.n_cls;
-            st.cap[o] = (int32_t)t;
-            st.cls[o] = cls;
-            st.det[o] = dt;
-            st.hid[o] = (int32_t)hid_e;
-            st.rem[o] = pm.sizes[c - 1];
-            st.f_nact[o] = nact;
-            st.f_snr[o] = snr_in;
-            st.f_own[o] = qlen;
-            ++qlen;
-            ++n_acc;
-        }
-        return nw;
-    };
+    int n_calls = 0;
     if (!counts) {
-        const bool nw = call(rob ? (int)send[ir] : 0);
+        const bool nw = fifo_call(st, pm, rob, rob ? (int)send[ir] : 0, qlen, fo, t, dt, hid_e, snr_in, rb, lane);
         if (rob) ((uint8_t*)accepted)[ir] = nw;
         n_calls = 1;
     } else {
-        for (int c = 0; c < n_cls; ++c) {
-            const int mine = rob ? counts[ir * n_cls + c] : 0;
-            const int most = seg_max_i(mine, rb);
-            for (int i = 0; i < most; ++i) call(mine > i ? c + 1 : 0);
-            n_calls += most;
-        }
+        const int n_acc = fifo_counts(st, pm, counts, n_cls, rob, ir, qlen, fo, t, dt, hid_e, snr_in, rb, lane,
+                                      n_calls);
         if (rob) ((int32_t*)accepted)[ir] = n_acc;
     }
     if (rob) st.qlen[ir] = qlen;
@@ -721,27 +841,11 @@ __global__ __launch_bounds__(WAVE) void wifi_submit_kernel(InetWifiState st, Ine
 
 // The counts form stands for a sequence of global submit calls (class 1 first, one call per message index up to the
 // largest count of the class over every env): each call advances every env's SUBMIT call counter and sets its last
-// hazard id (0: no hid in this form), including envs with nothing to send. One workgroup: the per-class maxima over
-// all [E][R] counts (LDS atomics), then the counters.
+// hazard id (0: no hid in this form), including envs with nothing to send. One workgroup.
 __global__ __launch_bounds__(1024) void wifi_submit_calls_kernel(InetWifiState st, int E, int R,
                                                                  const uint8_t* __restrict__ counts, int n_cls) {
     __shared__ int s_max[INET_WIFI_MAX_CLS];
-    if ((int)threadIdx.x < n_cls) s_max[threadIdx.x] = 0;
-    __syncthreads();
-    const size_t n = (size_t)E * R;
-    for (int c = 0; c < n_cls; ++c) {
-        int m = 0;
-        for (size_t i = threadIdx.x; i < n; i += blockDim.x) m = max(m, (int)counts[i * n_cls + c]);
-        if (m > 0) atomicMax(&s_max[c], m);
-    }
-    __syncthreads();
-    int tot = 0;
-    for (int c = 0; c < n_cls; ++c) tot += s_max[c];
-    if (tot > 0)
-        for (int e = threadIdx.x; e < E; e += blockDim.x) {
-            st.ctr_submit[e] += tot;
-            st.last_hid[e] = 0;
-        }
+    submit_calls(st, E, counts, (size_t)E * R * n_cls, n_cls, s_max, true);
 }
 
 // ======================================================================================= reset kernel
@@ -777,7 +881,7 @@ __global__ void wifi_reset_kernel(InetWifiState st, InetWifiParams pm, const uin
     if (threadIdx.x == 0) {
         st.episode[e] = ep_new;
         st.ctr_step[e] = 0;
-        st.ctr_submit[e] = 0;
+        st.ctr_submit[e] = -st.calls[0];
         st.clock[e] = 0;
         st.last_hid[e] = 0;
         st.pending[e] = 1;
@@ -821,6 +925,12 @@ int check_params(const InetWifiParams& p) {
     return INET_WIFI_OK;
 }
 
+// the step's enqueue (step_counts): its class count
+int check_step_counts(const InetWifiParams& p) {
+    if (p.step_counts && (p.step_n_cls <= 0 || p.step_n_cls > p.n_cls)) return INET_WIFI_EINVAL;
+    return INET_WIFI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -842,13 +952,12 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     pm.envs_per_wave = p.envs_per_wave * next_pow2(p.R) / rb > 0 ? p.envs_per_wave * next_pow2(p.R) / rb : 1;
     const int G = pm.envs_per_wave;
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
+    if ((rc = check_step_counts(p))) return rc;
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    if (p.A > 1)
-        hipLaunchKernelGGL((wifi_step_kernel<false, true>), dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm,
-                           t, input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
-    else
-        hipLaunchKernelGGL((wifi_step_kernel<false, false>), dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm,
-                           t, input_kind, x, cur_hid, *out, rb, InetDcfState{}, InetDcfParams{});
+    auto k = p.A > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true> : wifi_step_kernel<false, true, false>)
+                     : (p.step_counts ? wifi_step_kernel<false, false, true> : wifi_step_kernel<false, false, false>);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm, t, input_kind, x, cur_hid, *out,
+                       rb, InetDcfState{}, InetDcfParams{});
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 
@@ -898,9 +1007,11 @@ int32_t inet_wifi_dcf_step(const InetWifiState* st, const InetDcfState* ds, cons
     const int rb = next_pow2(p.R);
     const int G = p.envs_per_wave;
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
+    if ((rc = check_step_counts(p))) return rc;
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    hipLaunchKernelGGL(wifi_step_kernel<true>, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t,
-                       input_kind, x, cur_hid, *out, rb, *ds, *dp);
+    auto k = p.step_counts ? wifi_step_kernel<true, false, true> : wifi_step_kernel<true, false, false>;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, p, t, input_kind, x, cur_hid, *out,
+                       rb, *ds, *dp);
     return hipGetLastError() == hipSuccess ? INET_WIFI_OK : INET_WIFI_ELAUNCH;
 }
 

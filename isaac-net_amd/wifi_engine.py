@@ -120,7 +120,7 @@ class HipWifiEngine:
             "tau": z(E, R + self.A, dt=f32), "clock": z(E, dt=torch.int64), "last_hid": z(E, dt=torch.int64),
             "pending": z(E, dt=torch.uint8, v=1), "env_id": torch.arange(E, dtype=i32, device=d),
             "episode": z(E, v=-1), "ctr_step": z(E), "ctr_submit": z(E),
-            "field": z(E, self.A, nf, max(cfg.shadow_modes, 1), 3, dt=f32),
+            "field": z(E, self.A, nf, max(cfg.shadow_modes, 1), 3, dt=f32), "calls": z(1),
         }
         s = _lib.InetWifiState()
         for name, _ in _lib.InetWifiState._fields_:
@@ -295,13 +295,18 @@ class HipWifiEngine:
             None, 0, acc.data_ptr(), self._stream()), "wifi submit")
         return acc
 
+    def _counts(self, counts):
+        cnt = counts.to(self.dev, torch.uint8).contiguous()
+        if cnt.dim() != 3 or tuple(cnt.shape[:2]) != (self.E, self.R) or not 0 < cnt.shape[-1] <= len(
+                self.config.msg_sizes):
+            raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        return cnt
+
     def submit_counts(self, counts, t=None):
         """Enqueue counts [E,R,NC] messages per class in one launch: the submit() calls of class 1 first, one call per
         message index. Returns accepted messages [E,R] int32."""
         tv = self._tvec(t)
-        cnt = counts.to(self.dev, torch.uint8).contiguous()
-        if tuple(cnt.shape[:2]) != (self.E, self.R) or cnt.shape[-1] > len(self.config.msg_sizes):
-            raise ValueError("counts must be [E,R,n_classes] with n_classes <= len(msg_sizes)")
+        cnt = self._counts(counts)
         acc = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
         _lib.check(self._lib.inet_wifi_submit(
             C.byref(self._cstate), C.byref(self._cparams), None if tv is None else tv.data_ptr(), None, None, None,
@@ -332,12 +337,24 @@ class HipWifiEngine:
             setattr(c, a, o[k].data_ptr())
         return o, c
 
-    def step(self, t=None, x=None, cur_hid=None, *, rx_dbm=None, sense=None):
-        """Advance [t, t+1). x: poses [E,R,2|3] (through the AP's radio) or the SNR [E,R] in dB; rx_dbm= [E,R,1]
-        gives the received power (dBm) instead (wifi/engine.py:207-225). Returns the reference's dict, or
-        (newest, det_env) in the legacy form with cur_hid."""
+    def step(self, t=None, x=None, cur_hid=None, *, rx_dbm=None, sense=None, counts=None):
+        """Advance [t, t+1). x: poses [E,R,2|3] (through the APs' radio) or the SNR [E,R] in dB; rx_dbm= [E,R,A]
+        gives the received power (dBm) instead (wifi/engine.py:207-225). counts= [E,R,NC] enqueues first, as
+        submit_counts(counts, t) would, in the step's own launch; the dict then also holds "accepted" [E,R] int32.
+        Returns the reference's dict, or (newest, det_env) in the legacy form with cur_hid."""
         if sense is not None:
             raise ValueError("sense= needs WifiConfig(hidden_nodes=True)")
+        kind, xin = self._input(x, rx_dbm)
+        tv = self._tvec(t)
+        hid = None if cur_hid is None else torch.as_tensor(cur_hid).to(self.dev, torch.long).contiguous()
+        o = self._run(tv, kind, xin, hid, None if counts is None else self._counts(counts))
+        if cur_hid is not None:
+            return o["newest"], o["det_env"]
+        return o
+
+    def _input(self, x, rx_dbm):
+        """(input kind, contiguous float32 device tensor) of the step's input: 0 poses [E,R,2], 1 SNR [E,R], 2 received
+        power [E,R,A]."""
         if x is None and rx_dbm is None:
             raise ValueError("pass poses, an SNR [E,R] or rx_dbm=[E,R,A]")
         E, R = self.E, self.R
@@ -354,18 +371,33 @@ class HipWifiEngine:
             xin, kind = x.to(self.dev, torch.float32).contiguous(), 1
             if tuple(xin.shape) != (E, R):
                 raise ValueError(f"SNR must be [E,R] = {(E, R)}")
-        tv = self._tvec(t)
-        hid = None if cur_hid is None else torch.as_tensor(cur_hid).to(self.dev, torch.long).contiguous()
+        return kind, xin
+
+    def _run(self, tv, kind, xin, hid, cnt=None):
+        """Allocate the step's outputs and launch the step kernel (timed by kernel_events when set); with cnt
+        [E,R,NC] uint8 the launch enqueues them first."""
         o, c = self._alloc_out()
+        p = self._cparams
+        if cnt is not None:
+            o["accepted"] = torch.empty(self.E, self.R, dtype=torch.int32, device=self.dev)
+            p.step_counts, p.step_accepted, p.step_n_cls = cnt.data_ptr(), o["accepted"].data_ptr(), cnt.shape[-1]
         ev = self.kernel_events
-        if ev is not None:
-            ev.begin(torch.cuda.current_stream(self.dev))
-        _lib.check(self._launch(tv, kind, xin, hid, c), "wifi step")
-        if ev is not None:
-            ev.end(torch.cuda.current_stream(self.dev))
-        if cur_hid is not None:
-            return o["newest"], o["det_env"]
+        try:
+            if ev is not None:
+                ev.begin(torch.cuda.current_stream(self.dev))
+            _lib.check(self._launch(tv, kind, xin, hid, c), "wifi step")
+            if ev is not None:
+                ev.end(torch.cuda.current_stream(self.dev))
+        finally:
+            p.step_counts, p.step_accepted, p.step_n_cls = None, None, 0
         return o
+
+    def graph_step(self, n_cls=None):
+        """The control step (the enqueue of per-class arrival counts, then the step: one launch) as HIP graph replays:
+        returns a WifiGraphStep, called as g(x, counts) or g(counts=..., rx_dbm=...) in place of submit_counts + step.
+        A graph is recorded for every input kind and replayed; it reads the control step from the engine's device
+        clock."""
+        return WifiGraphStep(self, len(self.config.msg_sizes) if n_cls is None else n_cls)
 
     def _launch(self, tv, kind, xin, hid, c):
         return self._lib.inet_wifi_step(
@@ -388,7 +420,8 @@ class HipWifiEngine:
                "_last_snr": st["last_snr"], "_last_hid": st["last_hid"], "tau": st["tau"],
                "roam_left": L(st["roam_left"]), "att_n": st["att_n"], "att_logp": st["att_logp"],
                "credit": st["credit"], "serv": L(st["serv"]), "pending": st["pending"] != 0,
-               "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]), "rng.ctr[2]": L(st["ctr_step"])}
+               "rng.episode": L(st["episode"]), "rng.ctr[1]": L(st["ctr_submit"]) + L(st["calls"]),
+               "rng.ctr[2]": L(st["ctr_step"])}
         f = st["field"].permute(1, 0, 2, 3, 4)                     # [A, E, NF, K, 3]: the cells of RadioMC
         if self.config.channel == "tr38901":
             for j, n in enumerate(("sf_los", "sf_nlos", "los_field")):
@@ -422,6 +455,7 @@ class HipWifiEngine:
             st[k].copy_(g(k).float())
         st["pending"].copy_(g("pending").to(torch.uint8))
         st["episode"].copy_(I(g("rng.episode")))
+        st["calls"].zero_()
         st["ctr_submit"].copy_(I(g("rng.ctr[1]")))
         st["ctr_step"].copy_(I(g("rng.ctr[2]")))
         names = (("sf_los", 0), ("sf_nlos", 1), ("los_field", 2)) if self.config.channel == "tr38901" else ()
@@ -434,6 +468,51 @@ class HipWifiEngine:
         elif "radio.k" in sd:
             fv[:, :, 0, :, :2] = g("radio.k")
             fv[:, :, 0, :, 2] = g("radio.phi")
+
+
+class WifiGraphStep:
+    """step(x, counts=) of a HipWifiEngine (level WIFI or WIFI_DCF) as HIP graphs (torch.cuda.CUDAGraph): one per
+    input kind, recorded on first use and replayed at every control step. The inputs are copied into static buffers
+    (a producer may also write g.counts and g.inputs[kind] itself and call g.replay(kind)); the returned dict is the
+    graph's static output buffers, overwritten by its next replay. Each graph is one kernel node (the step launch with
+    its enqueue)."""
+
+    def __init__(self, eng, n_cls):
+        self.eng = eng
+        self.counts = torch.zeros(eng.E, eng.R, n_cls, dtype=torch.uint8, device=eng.dev)
+        self.inputs = {}
+        self.graphs = {}
+
+    def __call__(self, x=None, counts=None, *, rx_dbm=None):
+        eng = self.eng
+        kind, xin = eng._input(x, rx_dbm)
+        if counts is None or tuple(counts.shape) != tuple(self.counts.shape):
+            raise ValueError(f"counts must be {tuple(self.counts.shape)}")
+        if kind not in self.inputs:
+            self.inputs[kind] = torch.empty_like(xin)
+        cnt = counts.to(eng.dev, torch.uint8)
+        torch._foreach_copy_([self.inputs[kind], self.counts], [xin, cnt])      # (one launch for both)
+        return self.replay(kind)
+
+    def replay(self, kind):
+        """Replay the graph of input kind (0 poses, 1 SNR, 2 received power) on the current contents of g.counts and
+        g.inputs[kind], recording it first if needed; returns the static outputs."""
+        eng = self.eng
+        hit = self.graphs.get(kind)
+        if hit is None:
+            torch.cuda.synchronize(eng.dev)
+            g = torch.cuda.CUDAGraph()
+            ev, eng.kernel_events = eng.kernel_events, None
+            try:
+                with torch.cuda.graph(g):
+                    out = eng._run(None, kind, self.inputs[kind], None, self.counts)
+            finally:
+                eng.kernel_events = ev
+            torch.cuda.synchronize(eng.dev)
+            hit = self.graphs[kind] = (g, out)
+        g, out = hit
+        g.replay()
+        return out
 
 
 class HipWifiDcfEngine(HipWifiEngine):

@@ -188,3 +188,85 @@ def test_wifi_larger_free_run_vs_oracle():
     print(f"64x16 free run: max |deviation| { {k: f'{v:.2e}' for k, v in MAX_DEV.items()} }", flush=True)
     MAX_DEV.clear()
     assert not bad, bad[:5]
+
+
+@pytest.mark.parametrize("level,name", [("WIFI", "w_snr"), ("WIFI", "w_multi"), ("WIFI_DCF", "w_dcf")])
+def test_wifi_graph_replay_matches_eager(level, name):
+    """graph_step(): the recorded counts-form enqueue + step, replayed at every step with resets done eagerly between
+    the replays, gives the eager engine's outputs and state bit for bit on both levels."""
+    ref, cfg, kind = load(name)
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    a = P.make_engine(level, E, R, "cuda:0", cfg, seed=0)
+    b = P.make_engine(level, E, R, "cuda:0", cfg, seed=0)
+    g = b.graph_step(ref["counts"].shape[-1])
+    to = lambda v: torch.from_numpy(np.asarray(v)).to("cuda:0")  # noqa: E731
+    bad = []
+    for s in range(T):
+        ids = np.nonzero(ref["reset_mask"][s])[0]
+        if len(ids):
+            a.reset(ids.tolist())
+            b.reset(ids.tolist())
+        cnt = to(ref["counts"][s].astype(np.uint8))
+        x = to(ref["x"][s])
+        a.submit_counts(cnt)
+        oa = a.step(None, x)
+        ob = g(x, cnt)
+        torch.cuda.synchronize()
+        for k, v in oa.items():
+            if not torch.equal(torch.nan_to_num(v.float(), nan=-7.0), torch.nan_to_num(ob[k].float(), nan=-7.0)):
+                bad.append((s, "out." + k))
+        sa, sb = a.state_dict(), b.state_dict()
+        for k, v in sa.items():
+            if torch.is_tensor(v) and not torch.equal(v, sb[k]):
+                bad.append((s, k))
+    assert len(g.graphs) == 1
+    assert not bad, bad[:8]
+
+
+@pytest.mark.parametrize("level,name", [("WIFI", "w_mean"), ("WIFI", "w_multi"), ("WIFI_DCF", "w_dcf")])
+def test_wifi_step_with_counts_equals_submit_then_step(level, name):
+    """step(x, counts=) (the enqueue in the step's own launch) against submit_counts + step: outputs, accepted
+    messages and the whole state bit for bit, including the submit counters and the last hazard ids. Envs start with
+    a hazard id from a send-form submit (det and hid given), and the counts leave some envs with nothing to send and
+    one step with no message at all, so that an env learns of other envs' calls from the counts alone."""
+    ref, cfg, kind = load(name)
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    a = P.make_engine(level, E, R, "cuda:0", cfg, seed=0)
+    b = P.make_engine(level, E, R, "cuda:0", cfg, seed=0)
+    to = lambda v: torch.from_numpy(np.asarray(v)).to("cuda:0")  # noqa: E731
+    assert E >= 2 and T >= 3
+    rs = np.random.default_rng(5)
+    send = to(rs.integers(0, 2, size=(E, R)))
+    det = to(rs.integers(0, 2, size=(E, R)).astype(bool))
+    hid = to(np.arange(1, E + 1))
+    bad = []
+    for s in range(T):
+        if s < 3:
+            for eng in (a, b):                    # every env's last hazard id becomes its hid
+                eng.submit(None, P.Requests(send, det, hid))
+        cnt = ref["counts"][s].astype(np.uint8).copy()
+        cnt[: E // 2] = 0                         # half the envs send nothing
+        if s == 1:
+            cnt[:] = 0                            # no call at all
+        if s == 2:
+            cnt[:] = 0
+            cnt[E - 1, 0, 0] = 1                  # one message in the whole fleet
+        cnt = to(cnt)
+        x = to(ref["x"][s])
+        acc_a = a.submit_counts(cnt)
+        oa = a.step(None, x)
+        ob = b.step(None, x, counts=cnt)
+        if not torch.equal(acc_a, ob["accepted"]):
+            bad.append((s, "accepted"))
+        for k, v in oa.items():
+            if not torch.equal(torch.nan_to_num(v.float(), nan=-7.0), torch.nan_to_num(ob[k].float(), nan=-7.0)):
+                bad.append((s, "out." + k))
+        sa, sb = a.state_dict(), b.state_dict()
+        for k, v in sa.items():
+            if torch.is_tensor(v) and not torch.equal(v, sb[k]):
+                bad.append((s, k))
+        if s == 1:
+            assert torch.equal(sb["_last_hid"], hid.long()), "no call: the hazard ids stay"
+        if s == 2:
+            assert int(sb["_last_hid"].abs().sum()) == 0, "one call anywhere clears every env's hazard id"
+    assert not bad, bad[:8]
