@@ -312,7 +312,7 @@ def run_wifi(args, P, torch):
         bms = 1e3 * (time.perf_counter() - t1) / n_graph
         res["graph_replay"] = {"ms_per_step": gms, "steps": n_graph, "wall_over_kernel": gms / k_avg,
                                "launch": "HIP graph replay of the step with its enqueue (one kernel node), the inputs "
-                                         "copied into the graph's buffers first (one launch)",
+                                         "copied into the graph's buffers first",
                                "in_place_ms_per_step": bms, "in_place_wall_over_kernel": bms / k_avg}
     copy_calibration(args, res, torch, dev)
     if not args.no_cpu:

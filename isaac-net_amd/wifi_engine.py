@@ -490,8 +490,8 @@ class WifiGraphStep:
             raise ValueError(f"counts must be {tuple(self.counts.shape)}")
         if kind not in self.inputs:
             self.inputs[kind] = torch.empty_like(xin)
-        cnt = counts.to(eng.dev, torch.uint8)
-        torch._foreach_copy_([self.inputs[kind], self.counts], [xin, cnt])      # (one launch for both)
+        self.inputs[kind].copy_(xin)
+        self.counts.copy_(counts)
         return self.replay(kind)
 
     def replay(self, kind):
