@@ -384,7 +384,9 @@ const char* inet_nr_build_info(void) {
     return "inet_nr gfx950: one-cell step<S in {8,10,11,12,13,14,16,17,18}, P in {2,4,8,16}, IR, per-subband SNR> "
            "for envs of up to 64 robots (UL and DL), two-wave step (R <= 128, every S), four-wave step (R <= 256, "
            "S in {8,13}), multi-cell step<C in {2,3}, S in {8,13,14}, P, IR>, common-configuration builds (FX 1, 2), "
-           "DPP segment reductions, ATen-order sums; Wi-Fi mean-field and DCF steps; src=" INET_SRC_HASH;
+           "radio link failure, per-robot Doppler, wideband PF, DPP segment reductions, ATen-order sums; Wi-Fi "
+           "mean-field (one AP or up to 8 on one channel) and DCF steps, each with or without the enqueue in the "
+           "step launch; src=" INET_SRC_HASH;
 }
 
 int32_t inet_nr_step(const InetNrState* st, const InetNrTables* tab, const InetNrParams* prm, const InetNrRow* rows,
