@@ -314,10 +314,14 @@ DEV T sel_of(const T (&v)[N], int idx) {
 //
 // FX = 1 builds the kernel for the common configuration (PF, chase combining, EESM, RLC AM, OLLA, PHR cap, retx
 // priority, a fixed Rician phasor, fading; fx_profile), FX = 2 for the same without the Rician phasor: those
-// switches become
-// compile-time constants, which removes their tests from the slot loop and the scalar registers that hold them.
+// switches become compile-time constants, which removes their tests from the slot loop and the scalar registers that
+// hold them.
+// Minimum waves per SIMD (the register budget): 2, and 3 for the two-wave FX = 2 build (envs of 65..128 robots at the
+// common configuration: 168 VGPRs with 104 B per lane of spills, measured 7% faster than 193 VGPRs at 2 waves on
+// 16384 x 128; 4 waves, at 128 VGPRs, spill enough to be 30% slower); 1 with several cells.
 template <int S, int P, bool IR, bool VREF, int RBT, class LS, int NC, int FX = 0>
-__global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1), NC > 1 ? 1 : 2) void nr_step_kernel(
+__global__ __launch_bounds__(STEP_WAVE * (RBT > STEP_WAVE ? RBT / STEP_WAVE : 1),
+                             NC > 1 ? 1 : ((RBT == 128 && FX == 2) ? 3 : 2)) void nr_step_kernel(
     InetNrState st, LS lk_in, InetNrTables tb_in, InetNrParams pm_in, const InetNrRow* __restrict__ rows, int n_rows,
     int64_t T_arg, const float* __restrict__ xin, const int64_t* __restrict__ cur_hid, InetNrOutputs out, int rb_arg,
     int n_ul_max, InetNrArrivals arr, InetNrCells cl) {
