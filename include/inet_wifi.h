@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 4
+#define INET_WIFI_ABI_VERSION 5
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -114,7 +114,12 @@ typedef struct InetWifiParams {
     const uint8_t *step_counts;
     int32_t *step_accepted;
     int32_t step_n_cls;
-    int32_t pad1;
+    /* APs on several channels (wifi/engine.py:117-166, 300-305): n_dom collision domains, one per distinct channel,
+       and each AP's domain (the index of its channel among the sorted distinct channels). A robot contends in its
+       serving AP's domain, an AP's background station in the AP's. n_dom = 1: one domain. n_dom > 1 needs
+       R + A <= 64 and (R + A) n_dom < 400 (else INET_WIFI_EUNSUPPORTED). */
+    int32_t n_dom;
+    int32_t ap_dom[INET_WIFI_MAX_A];
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */

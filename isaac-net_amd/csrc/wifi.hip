@@ -180,6 +180,16 @@ DEV int fifo_counts(const InetWifiState& st, const InetWifiParams& pm, const uin
     return n_acc;
 }
 
+// The sum over the stations of one collision domain as the reference's DomainView.sum forms it
+// (wifi/meanfield.py:76-89: onehot^T x, then onehot times that, two batched products small enough for ATen's CPU
+// kernel, which accumulates products in index order): the members' values added in station order. (Each product is
+// 1 x or 0 x, exact, and adding a zero leaves a non-zero sum unchanged.)
+DEV float dom_seq_sum(const float* row, const uint8_t* dom, int n, int d) {
+    float acc = 0.f;
+    for (int i = 0; i < n; ++i) acc = dom[i] == d ? acc + row[i] : acc;
+    return acc;
+}
+
 // bytewise maximum of two words of four uint8
 DEV uint32_t max_u8x4(uint32_t a, uint32_t b) {
     uint32_t m = 0;
@@ -269,6 +279,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     __shared__ float s_red4[DCF ? 1 : 3 * WAVE];          // three more rows of station values (dom_sum4)
     __shared__ uint8_t s_hid0[CNT ? WAVE : 1];            // per env: the enqueue's calls clear the last hazard id
     __shared__ int s_cmax[CNT ? INET_WIFI_MAX_CLS : 1];   // the largest count of every class (workgroup 0)
+    __shared__ uint8_t s_dom[MA ? WAVE : 1];              // APs on several channels: each station's domain
     const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
     float* s_rem = dyn;                                   // [F][64] bytes left of every frame slot
     float* s_fin = dyn + F * WAVE;                        // [F][64] finish time, then the compaction staging row
@@ -385,6 +396,14 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const int NS = R + A;                                  // stations of the domain: robots, one per AP
     const bool bgl = rb >= NS;
     const bool is_bg = bgl && env_ok && r >= R && r < NS;
+    // APs on several channels (MA builds): one collision domain per channel. A robot is in its serving AP's channel,
+    // an AP's background station in the AP's (each has its own lane: R + A <= 64, checked by the entry points).
+    const bool doms = MA && pm.n_dom > 1;
+    if (doms) {
+        if (env_ok && r < NS) s_dom[lane] = (uint8_t)(r < R ? pm.ap_dom[sv] : pm.ap_dom[r - R]);
+        __syncthreads();
+    }
+    const int mydom = doms && env_ok && r < NS ? s_dom[lane] : 0;
     float tau = rob ? st.tau[(size_t)ec * NS + rc] : (is_bg ? st.tau[(size_t)ec * NS + r] : pm.tau0);
     float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * NS + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
@@ -409,6 +428,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         s_red[lane] = v;
         __syncthreads();
         const float* row = s_red + gseg * rb;
+        if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
         auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
         if (NS == 17) return aten_row_sum_u<17>(17, xr);
         if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
@@ -425,6 +445,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         __syncthreads();
         auto sum_row = [&](const float* base, float vb) -> float {
             const float* row = base + gseg * rb;
+            if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
             auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
             if (NS == 17) return aten_row_sum_u<17>(17, xr);
             if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
@@ -917,6 +938,11 @@ int check_params(const InetWifiParams& p) {
         return INET_WIFI_EINVAL;
     if (p.n_fields < 0 || p.n_fields > 3 || p.n_modes < 0 || p.n_modes > INET_WIFI_MAX_KF) return INET_WIFI_EINVAL;
     if (p.bg_ac < 0 || p.bg_ac > 4 || p.A < 1 || p.A > INET_WIFI_MAX_A || p.R + p.A > 65) return INET_WIFI_EINVAL;
+    // several channels: every AP's domain index below n_dom, every station in a lane of its own (R + A <= 64), and
+    // (R + A) n_dom < 400 (the size up to which the reference's batched product adds in index order)
+    if (p.n_dom < 1 || p.n_dom > p.A) return INET_WIFI_EINVAL;
+    for (int a = 0; a < p.A; ++a) if (p.ap_dom[a] < 0 || p.ap_dom[a] >= p.n_dom) return INET_WIFI_EINVAL;
+    if (p.n_dom > 1 && (p.R + p.A > 64 || (p.R + p.A) * p.n_dom >= 400)) return INET_WIFI_EUNSUPPORTED;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;

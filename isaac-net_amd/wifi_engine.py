@@ -5,9 +5,10 @@ Mirrors isaac_net/core/wifi/engine.py (WifiNet, :100-403) on the LevelNet contra
 reset(env_ids) / submit(t, requests, snr_db) / step(t, poses_or_snr, cur_hid, *, rx_dbm) -> dict / clock /
 state_dict, with the same inputs, output keys, dtypes and shapes and the same per-env clock rules (t=None uses the
 engine clock; an int or an [E] tensor sets each env's step). What the kernels do not implement is refused at
-construction with HipUnsupported: access points on different channels (several collision domains), more than 8
-APs, hidden nodes, AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio features
-the NR engine refuses. Several APs on one channel run with association and roaming.
+construction with HipUnsupported: more than 8 APs, APs on several channels when R + A > 64 or (R + A) x channels
+>= 400, hidden nodes, AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio
+features the NR engine refuses. Several APs run with association and roaming, on one channel or several (one
+collision domain per channel).
 
 All state lives in device tensors that torch allocates; every call hands the library plain pointers.
 """
@@ -39,8 +40,6 @@ def wifi_refusals(cfg: NRConfig):
             out.append((what, why))
     n_ap = len(wc.ap_xy(cfg))
     no(n_ap > 8, f"{n_ap} access points", "up to 8 APs per env")
-    no(len(set(wc.channels(n_ap))) > 1, "APs on different channels (several collision domains)",
-       "APs on one channel (one collision domain)")
     no(wc.hidden_nodes, "hidden_nodes=True", "every robot senses every other one")
     d = derive(cfg, wc)
     no(d.Z > 1, "access categories with different AIFSN in one env (AIFS zones)", "one AIFS zone")
@@ -96,6 +95,13 @@ class HipWifiEngine:
         self.K = self.Ksub = self.d.K
         self.n_acc_max = self.d.n_acc_max
         self.A = len(self.wc.ap_xy(cfg))                 # access points, one background station each
+        chans = self.wc.channels(self.A)
+        uniq = sorted(set(chans))
+        self._ap_dom = [uniq.index(c) for c in chans]     # each AP's collision domain (wifi/engine.py:119-122)
+        self.D = len(uniq)
+        if self.D > 1 and (R + self.A > 64 or (R + self.A) * self.D >= 400):
+            raise HipUnsupported(f"APs on {self.D} channels with R + A = {R + self.A}: several collision domains "
+                                 "need R + A <= 64 and (R + A) x channels < 400")
         rb = 1 << max(0, (R - 1).bit_length())
         self.envs_per_wave = int(envs_per_wave) if envs_per_wave is not None else 1
         if self.envs_per_wave < 1 or self.envs_per_wave * rb > 64:
@@ -169,6 +175,9 @@ class HipWifiEngine:
         p.A = len(xy)
         for a, (x_, y_) in enumerate(xy):
             p.ap_xy[2 * a], p.ap_xy[2 * a + 1] = x_, y_
+        p.n_dom = self.D
+        for a, dom in enumerate(self._ap_dom):
+            p.ap_dom[a] = dom
         dc = (rc.shadow_dcorr_m, 0.0, 0.0)
         p.spectrum = 0 if rc.shadow_acf == "sos" else 1
         if rc.channel == "tr38901":

@@ -3,8 +3,9 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
 checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
 
-A from-scratch torch-CPU restatement of isaac-net's WifiNet for the configs the HIP backend implements (one collision
-domain: one AP, or several APs on one channel with association and roaming; no hidden nodes; one AIFS zone):
+A from-scratch torch-CPU restatement of isaac-net's WifiNet for the configs the HIP backend implements (one AP, or
+several APs with association and roaming, on one channel or several: one collision domain per channel; no hidden
+nodes; one AIFS zone):
   LevelNet         core/levels/base.py:43-360 (clock, reset, submit, step, the regions' order)
   add_body         core/proto/netsim_fast.py:136-160 (enqueue into FIFO slot count)
   finish_body      core/proto/netsim_fast.py:185-206 (delivered / timed out, newest, det_env, stable compaction)
@@ -12,7 +13,8 @@ domain: one AP, or several APs on one channel with association and roaming; no h
   WifiNet          core/wifi/engine.py:100-403 (association, _serve: K sub-steps of mean-field solve, Poisson or
                    renewal access counts, FIFO service, finish times, retry-limit loss, the extra outputs)
   poisson_icdf     core/wifi/engine.py:57-63
-  meanfield.solve  core/wifi/meanfield.py:48-62 (stage factors, tau(p)), :65-73 (one domain), :106-209 (Z = 1)
+  meanfield.solve  core/wifi/meanfield.py:48-62 (stage factors, tau(p)), :65-73 (one domain), :76-89 (a domain per
+                   channel: the channel one-hot's two batched products), :106-209 (Z = 1)
   AccessTiming     core/wifi/phy.py:107-155 (cap_bytes, times)
   CounterRNG       core/proto/rng.py (STEP draws uniform(STEP, 0, K, R) and uniform(STEP, 1, R, F))
   RadioMC          through oracle.nr_oracle.Radio on the APs' NRConfig (core/wifi/engine.py:82-97, 189-197)
@@ -22,9 +24,8 @@ after every step). The constants come from isaac_net_amd.wifi_config (pinned by 
 
 Parity status: every function here is pinned by the golden Wi-Fi trajectories, including both access-noise modes,
 RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background stations,
-both radio models, the stochastic LOS state, several APs on one channel with roaming and its interruption, and partial
-resets. Not implemented (refused, as by the HIP backend): APs on different channels (several collision domains),
-hidden nodes, AIFS zones (Z > 1).
+both radio models, the stochastic LOS state, several APs on one channel with roaming and its interruption, APs on two
+channels, and partial resets. Not implemented (refused, as by the HIP backend): hidden nodes, AIFS zones (Z > 1).
 """
 from __future__ import annotations
 
@@ -47,7 +48,7 @@ class WifiOracle:
         from isaac_net_amd.wifi_config import WifiConfig, derive, radio_config
         wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
         A = len(wc.ap_xy(cfg))
-        assert len(set(wc.channels(A))) == 1 and not wc.hidden_nodes, "one channel (one domain), no hidden nodes"
+        assert not wc.hidden_nodes, "no hidden nodes"
         d = derive(cfg, wc)
         assert d.Z == 1, "one AIFS zone"
         self.cfg, self.wc, self.d, self.E, self.R = cfg, wc, d, E, R
@@ -80,6 +81,15 @@ class WifiOracle:
         self.att_n, self.att_logp, self.credit = z((E, R), 0.0, f), z((E, R), 0.0, f), z((E, R), 0.0, f)
         self.serv = z((E, R), 0, torch.long)
         self.pending = z((E,), True, torch.bool)
+        # collision domains, one per distinct channel (wifi/engine.py:119-122, 163-166): the one-hot of every station's
+        # domain, the robots' rows set by each association (:254-256), the background stations' by their AP
+        chans = wc.channels(A)
+        uniq = sorted(set(chans))
+        self.D = len(uniq)
+        self.ap_ch = torch.tensor([uniq.index(c) for c in chans], dtype=torch.long)
+        self.chan_oh = torch.zeros(E, R + A, self.D)
+        self.chan_oh[:, R:] = (self.ap_ch[:, None] == torch.arange(self.D)).to(f)
+        self.chan_oh[:, :R, 0] = 1.0
         self.reset(None)
 
     # ------------------------------------------------------------------ reset / clock (levels/base.py:142-157)
@@ -164,6 +174,8 @@ class WifiOracle:
         if self.roam_sub > 0:
             self.roam_left = torch.where(roam, torch.full_like(self.roam_left, self.roam_sub), self.roam_left)
         self.serv_out = new.clone()
+        ch = self.ap_ch[new]
+        self.chan_oh[:, :R] = (ch[..., None] == torch.arange(self.D)).float()
         return rx.gather(-1, new[..., None])[..., 0] - self.d.noise_dbm
 
     # ------------------------------------------------------------------ PHY timing (wifi/phy.py:130-155)
@@ -190,10 +202,13 @@ class WifiOracle:
         return ts, tc
 
     # ------------------------------------------------------------------ mean field, one domain, Z = 1
-    @staticmethod
-    def _dom_sum(x):
-        """Sum over the stations of the env (one collision domain), broadcast back."""
-        return x.sum(-1, keepdim=True).expand_as(x)
+    def _dom_sum(self, x):
+        """Sum over the stations of each station's collision domain: the env (one channel, SingleView.sum,
+        meanfield.py:68-69), or its channel's stations (DomainView.sum, :83-84)."""
+        if self.D == 1:
+            return x.sum(-1, keepdim=True).expand_as(x)
+        M = self.chan_oh
+        return (M @ (M.transpose(-1, -2) @ x[..., None]))[..., 0]
 
     @staticmethod
     def _stage_factors(W0, Wm, L):

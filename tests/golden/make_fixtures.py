@@ -556,6 +556,18 @@ WIFI_CASES = {
                     wifi=dict(ap_positions_m=((40.0, 40.0), (200.0, 60.0), (120.0, 200.0)), roam_hyst_db=3.0,
                               roam_ms=2.0, bg_stations=1),
                     E=3, R=16, steps=30, kind="pose", arena=240.0, walk=6.0, rates=(1.0, 0.4), resets={14: [1]}),
+    # APs on two channels (two collision domains): APs 0 and 2 share channel 1, AP 1 is on channel 6; robots roam
+    # between the domains
+    "w_chan": dict(cfg=dict(control_step_ms=10.0, frame_buffer=10, msg_sizes=(800.0, 2000.0), timeout_steps=5),
+                   wifi=dict(ap_positions_m=((40.0, 40.0), (200.0, 60.0), (120.0, 200.0)), ap_channels=(1, 6, 1),
+                             roam_hyst_db=3.0, roam_ms=2.0, bg_stations=2),
+                   E=3, R=16, steps=30, kind="pose", arena=240.0, walk=6.0, rates=(1.2, 0.4), resets={17: [2]}),
+    # four APs spread round robin over three channels (n_channels), the log-distance radio
+    "w_chan3": dict(cfg=dict(control_step_ms=10.0, frame_buffer=8, msg_sizes=(1200.0,), timeout_steps=4,
+                             channel="log_distance"),
+                    wifi=dict(ap_positions_m=((0.0, 0.0), (120.0, 0.0), (0.0, 120.0), (120.0, 120.0)), n_channels=3,
+                              roam_hyst_db=2.0, bg_stations=1),
+                    E=2, R=12, steps=25, kind="pose", arena=130.0, walk=8.0, rates=(1.5,), resets={}),
     # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
     # AP, 1500 B messages, 20 sub-steps per control step
     "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),

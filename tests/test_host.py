@@ -143,14 +143,14 @@ def test_per_link_delay_spread_and_k_from_los_refusals():
 
 
 def test_wifi_several_aps_refusals():
-    """Several APs run on one channel (one collision domain, the default n_channels=1); APs on different channels
-    (several collision domains) and more than 8 APs are refused, and level WIFI_DCF keeps one AP."""
+    """Several APs run on one channel or several (one collision domain per channel); more than 8 APs are refused, and
+    level WIFI_DCF keeps one AP. (Several channels with R + A > 64 or (R + A) x channels >= 400 are refused when the
+    engine is made, where R is known: the GPU tests cover the accepted sizes.)"""
     from isaac_net_amd.wifi_config import WifiConfig
     from isaac_net_amd.wifi_engine import wifi_refusals
     aps = ((0.0, 0.0), (100.0, 0.0), (50.0, 80.0))
     assert wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=aps, roam_ms=2.0))) == []
-    names = " ".join(f for f, _ in wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=aps, n_channels=3))))
-    assert "different channels" in names
+    assert wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=aps, n_channels=3))) == []
     many = tuple((10.0 * i, 0.0) for i in range(9))
     assert "9 access points" in " ".join(f for f, _ in wifi_refusals(P.NRConfig(wifi=WifiConfig(ap_positions_m=many))))
 

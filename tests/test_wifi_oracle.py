@@ -14,7 +14,7 @@ from oracle.wifi_oracle import WifiOracle
 import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig, derive, mcs_table
 
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_dcf"]
 
 
 def load(name):
@@ -60,6 +60,24 @@ def test_wifi_oracle_catches_a_planted_error():
     def plant(o):
         o.wc = o.wc.with_(fp_damping=0.5)
     assert run_oracle("w_snr", plant=plant, steps=3)
+
+
+@pytest.mark.parametrize("plant_name", ["one_domain", "robots_stay_in_domain_0", "sorted_row_sum"])
+def test_wifi_oracle_domains_are_pinned(plant_name):
+    """Several channels: summing over every station of the env (one domain), leaving the robots in the first domain
+    after association, or summing a domain in ATen's vectorized order instead of the batched product's index order
+    must each fail the w_chan trajectory."""
+    def plant(o):
+        if plant_name == "one_domain":
+            o.D = 1
+        elif plant_name == "robots_stay_in_domain_0":
+            o.ap_ch = torch.zeros_like(o.ap_ch)
+        else:
+            def dom_sum(x, o=o):
+                per = (o.chan_oh.transpose(-1, -2) * x[:, None, :]).contiguous().sum(-1)       # [E, D]
+                return (o.chan_oh * per[:, None, :]).sum(-1)
+            o._dom_sum = dom_sum
+    assert run_oracle("w_chan", plant=plant, steps=12)
 
 
 def test_wifi_constants_match_reference_tables():
