@@ -4,8 +4,8 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import 
 checker (or as the timed CPU baseline). The product (isaac-net_amd/) never imports it.
 
 A from-scratch torch-CPU restatement of isaac-net's WifiNet for the configs the HIP backend implements (one AP, or
-several APs with association and roaming, on one channel or several: one collision domain per channel; no hidden
-nodes; one AIFS zone):
+several APs with association and roaming, on one channel or several: one collision domain per channel; AIFS zones;
+no hidden nodes):
   LevelNet         core/levels/base.py:43-360 (clock, reset, submit, step, the regions' order)
   add_body         core/proto/netsim_fast.py:136-160 (enqueue into FIFO slot count)
   finish_body      core/proto/netsim_fast.py:185-206 (delivered / timed out, newest, det_env, stable compaction)
@@ -14,7 +14,7 @@ nodes; one AIFS zone):
                    renewal access counts, FIFO service, finish times, retry-limit loss, the extra outputs)
   poisson_icdf     core/wifi/engine.py:57-63
   meanfield.solve  core/wifi/meanfield.py:48-62 (stage factors, tau(p)), :65-73 (one domain), :76-89 (a domain per
-                   channel: the channel one-hot's two batched products), :106-209 (Z = 1)
+                   channel: the channel one-hot's two batched products), :106-209 (AIFS zones, no hidden nodes)
   AccessTiming     core/wifi/phy.py:107-155 (cap_bytes, times)
   CounterRNG       core/proto/rng.py (STEP draws uniform(STEP, 0, K, R) and uniform(STEP, 1, R, F))
   RadioMC          through oracle.nr_oracle.Radio on the APs' NRConfig (core/wifi/engine.py:82-97, 189-197)
@@ -25,7 +25,7 @@ after every step). The constants come from isaac_net_amd.wifi_config (pinned by 
 Parity status: every function here is pinned by the golden Wi-Fi trajectories, including both access-noise modes,
 RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background stations,
 both radio models, the stochastic LOS state, several APs on one channel with roaming and its interruption, APs on two
-channels, and partial resets. Not implemented (refused, as by the HIP backend): hidden nodes, AIFS zones (Z > 1).
+channels, AIFS zones, and partial resets. Not implemented (refused, as by the HIP backend): hidden nodes.
 """
 from __future__ import annotations
 
@@ -50,7 +50,6 @@ class WifiOracle:
         A = len(wc.ap_xy(cfg))
         assert not wc.hidden_nodes, "no hidden nodes"
         d = derive(cfg, wc)
-        assert d.Z == 1, "one AIFS zone"
         self.cfg, self.wc, self.d, self.E, self.R = cfg, wc, d, E, R
         self.K, self.F, self.timeout = d.K, cfg.frame_buffer, cfg.timeout_steps
         self.sizes = torch.tensor(cfg.msg_sizes, dtype=torch.float32)
@@ -216,36 +215,81 @@ class WifiOracle:
         Wk = torch.minimum(W0[..., None] * torch.exp2(k.clamp(max=60)), Wm[..., None])
         return (Wk + 1.0) * 0.5
 
-    def _fail(self, w, tau, active):
-        """(p, success probability, S = sum_j w_j log(1 - tau_j)) of every station."""
-        lt = torch.log1p(-tau)
-        S = self._dom_sum(w * lt)
-        own = torch.where(active, lt, torch.zeros_like(lt))
-        ok = torch.exp(S - own) * 1.0 * (1.0 - self.wc.frame_error_rate)
-        num = torch.zeros_like(tau) + torch.ones_like(tau) * ok
-        O = torch.zeros_like(tau) + torch.ones_like(tau)
-        return 1.0 - num / O.clamp(min=1e-12), num, S
+    def _dom_min(self, x, mask):
+        """The smallest x over the masked stations of each station's domain (SingleView.min / DomainView.min,
+        meanfield.py:71-73, 86-89; BIG = 1e9 where a domain has none)."""
+        v = torch.where(mask, x, torch.full_like(x, 1e9))
+        if self.D == 1:
+            return v.amin(-1, keepdim=True).expand_as(x)
+        M = self.chan_oh
+        agg = (v[..., :, None] + (1.0 - M) * 1e9).amin(-2)
+        return (M * agg[..., None, :]).sum(-1)
 
-    def _solve(self, w, Ts, Tc, tau, Wfac):
-        wc = self.wc
+    def _zones(self, w, tau, dz, active):
+        """meanfield._zones (meanfield.py:106-131): per AIFS zone z the domain sum S_z of w log(1 - tau) over the
+        stations with offset <= z, the own term, and the stationary zone distribution pi_z."""
+        Z = self.d.Z
+        lt = torch.log1p(-tau)
+        wl = w * lt
+        if Z == 1:
+            return [self._dom_sum(wl)], [torch.where(active, lt, torch.zeros_like(lt))], [torch.ones_like(tau)]
+        S, own = [], []
+        for z in range(Z):
+            m = dz <= z
+            S.append(self._dom_sum(torch.where(m, wl, torch.zeros_like(wl))))
+            own.append(torch.where(active & m, lt, torch.zeros_like(lt)))
+        g = torch.ones_like(tau)
+        raw = []
+        for z in range(Z):
+            idle = torch.exp(S[z])
+            raw.append(g if z < Z - 1 else g / (1.0 - idle).clamp(min=1e-12))
+            g = g * idle
+        tot = sum(raw)
+        return S, own, [r / tot for r in raw]
+
+    def _fail(self, w, tau, dz, active):
+        """meanfield._fail (meanfield.py:161-178) without hidden nodes: (p, successes, zones)."""
+        Z = self.d.Z
+        zones = self._zones(w, tau, dz, active)
+        S, own, pi = zones
+        num = torch.zeros_like(tau)
+        O = torch.zeros_like(tau)
+        for z in range(Z):
+            ok = torch.exp(S[z] - own[z]) * 1.0 * (1.0 - self.wc.frame_error_rate)
+            wz = pi[z] if Z == 1 else torch.where(dz <= z, pi[z], torch.zeros_like(pi[z]))
+            num = num + wz * ok
+            O = O + wz
+        return 1.0 - num / O.clamp(min=1e-12), num, zones
+
+    def _solve(self, w, Ts, Tc, tau, Wfac, dz=None):
+        wc, Z = self.wc, self.d.Z
         active = w > 0
         k = torch.arange(Wfac.shape[-1], dtype=torch.float32)
         for _ in range(int(wc.fp_iters)):
             tau = tau.clamp(1e-7, 0.999)
-            p, _, _ = self._fail(w, tau, active)
+            p, _, _ = self._fail(w, tau, dz, active)
             pk = p[..., None] ** k
             tau = tau + wc.fp_damping * (pk.sum(-1) / (pk * Wfac).sum(-1) - tau)
         tau = tau.clamp(1e-7, 0.999)
-        p, succ, S = self._fail(w, tau, active)
+        p, succ, (S, _, pi) = self._fail(w, tau, dz, active)
+        # slot_time (meanfield.py:134-158)
         r = w * tau / (1.0 - tau)
         wt = w * tau
-        idle = torch.exp(S)
-        a0, a1 = self._dom_sum(r), self._dom_sum(r * Ts)
-        gd, g = self._dom_sum(wt), self._dom_sum(wt * Tc)
-        p_coll = (1.0 - idle - idle * a0).clamp(min=0.0)
-        tc = g / gd.clamp(min=1e-12)
-        tslot = torch.zeros_like(tau) + torch.ones_like(tau) * (wc.slot_us * idle + idle * a1 + p_coll * tc)
-        p_idle = torch.zeros_like(tau) + torch.ones_like(tau) * idle
+        tslot = torch.zeros_like(tau)
+        p_idle = torch.zeros_like(tau)
+        for z in range(Z):
+            if Z == 1:
+                rz, wtz = r, wt
+            else:
+                m = dz <= z
+                rz, wtz = torch.where(m, r, torch.zeros_like(r)), torch.where(m, wt, torch.zeros_like(wt))
+            idle = torch.exp(S[z])
+            a0, a1 = self._dom_sum(rz), self._dom_sum(rz * Ts)
+            gd, g = self._dom_sum(wtz), self._dom_sum(wtz * Tc)
+            p_coll = (1.0 - idle - idle * a0).clamp(min=0.0)
+            tc = g / gd.clamp(min=1e-12)
+            tslot = tslot + pi[z] * (wc.slot_us * idle + idle * a1 + p_coll * tc)
+            p_idle = p_idle + pi[z] * idle
         mu = torch.where(active, tau * succ / tslot, torch.zeros_like(tau))
         return tau, p, mu, p_idle
 
@@ -266,7 +310,7 @@ class WifiOracle:
 
     # ------------------------------------------------------------------ the control step
     def _serve(self, t, snr):
-        """WifiNet._serve (wifi/engine.py:292-403) for one domain and Z = 1: finish times [E,R,F]."""
+        """WifiNet._serve (wifi/engine.py:292-403): finish times [E,R,F]."""
         wc, d, E, R, K, F = self.wc, self.d, self.E, self.R, self.K, self.F
         u_acc = self.rng._draw(self.rng.ctr[STEP], STEP, 0, K * R, False).view(E, K, R)
         u_loss = self.rng._draw(self.rng.ctr[STEP], STEP, 1, R * F, False).view(E, R, F)
@@ -302,8 +346,13 @@ class WifiOracle:
             B = torch.where(act, torch.minimum(q, cap), cap)
             BN = torch.cat([B, self.bg_B], -1)
             w = torch.cat([act.to(torch.float32), self.bg_w], -1)
-            Ts, Tc = self._times(BN, rateN, aifsn)
-            tau, p, mu, p_idle = self._solve(w, Ts, Tc, tau, Wfac)
+            if d.Z > 1:          # AIFS zones: offsets from the smallest AIFSN among the domain's active stations
+                aif_min = torch.minimum(self._dom_min(aifsn, torch.cat([act, self.bg_w > 0], -1)), aifsn)
+                dz = aifsn - aif_min
+            else:
+                aif_min, dz = aifsn, None
+            Ts, Tc = self._times(BN, rateN, aif_min)
+            tau, p, mu, p_idle = self._solve(w, Ts, Tc, tau, Wfac, dz)
             mu, p = mu[:, :R], p[:, :R]
             lam = mu * d.dt_us
             if wc.access_noise == "poisson":

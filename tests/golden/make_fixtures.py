@@ -568,6 +568,15 @@ WIFI_CASES = {
                     wifi=dict(ap_positions_m=((0.0, 0.0), (120.0, 0.0), (0.0, 120.0), (120.0, 120.0)), n_channels=3,
                               roam_hyst_db=2.0, bg_stations=1),
                     E=2, R=12, steps=25, kind="pose", arena=130.0, walk=8.0, rates=(1.5,), resets={}),
+    # AIFS zones: the robots in AC_VI (AIFSN 2) beside background stations in AC_BE (AIFSN 3): two zones
+    "w_aifs": dict(cfg=dict(control_step_ms=10.0, frame_buffer=8, msg_sizes=(1000.0,), timeout_steps=4),
+                   wifi=dict(access_category="VI", bg_stations=3, bg_ac="BE"),
+                   E=3, R=12, steps=25, kind="disc", radius=40.0, walk=1.0, rates=(1.6,), resets={11: [0]}),
+    # six AIFS zones (per-class ACs VO and BK, background stations in BE) on two APs on two channels
+    "w_aifs_cls": dict(cfg=dict(control_step_ms=10.0, frame_buffer=10, msg_sizes=(600.0, 3000.0), timeout_steps=5),
+                       wifi=dict(class_ac=("VO", "BK"), bg_stations=2, bg_ac="BE",
+                                 ap_positions_m=((30.0, 30.0), (150.0, 60.0)), ap_channels=(1, 6), roam_hyst_db=2.0),
+                       E=2, R=14, steps=25, kind="pose", arena=180.0, walk=7.0, rates=(0.9, 0.5), resets={13: [1]}),
     # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
     # AP, 1500 B messages, 20 sub-steps per control step
     "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),

@@ -14,7 +14,7 @@ from oracle.wifi_oracle import WifiOracle
 import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig, derive, mcs_table
 
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls", "w_dcf"]
 
 
 def load(name):
@@ -78,6 +78,28 @@ def test_wifi_oracle_domains_are_pinned(plant_name):
                 return (o.chan_oh * per[:, None, :]).sum(-1)
             o._dom_sum = dom_sum
     assert run_oracle("w_chan", plant=plant, steps=12)
+
+
+@pytest.mark.parametrize("plant_name", ["one_zone", "min_over_all_stations", "no_last_zone_factor"])
+def test_wifi_oracle_zones_are_pinned(plant_name):
+    """AIFS zones: one zone for all, the smallest AIFSN taken over every station instead of the contending ones, or
+    the last zone's stationary weight without its 1 / (1 - idle) geometric sum must each fail the w_aifs_cls
+    trajectory (six zones)."""
+    def plant(o):
+        if plant_name == "one_zone":
+            o.d.Z = 1
+        elif plant_name == "min_over_all_stations":
+            o._dom_min = lambda x, mask, o=o: WifiOracle._dom_min(o, x, torch.ones_like(mask))
+        else:
+            def zones(w, tau, dz, active, o=o):
+                S, own, pi = WifiOracle._zones(o, w, tau, dz, active)
+                raw = [torch.ones_like(tau)]
+                for z in range(1, len(S)):
+                    raw.append(raw[-1] * torch.exp(S[z - 1]))
+                tot = sum(raw)
+                return S, own, [r / tot for r in raw]
+            o._zones = zones
+    assert run_oracle("w_aifs_cls", plant=plant, steps=12)
 
 
 def test_wifi_constants_match_reference_tables():
