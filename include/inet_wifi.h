@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 5
+#define INET_WIFI_ABI_VERSION 6
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -43,7 +43,8 @@ extern "C" {
 #define INET_WIFI_MAX_CLS 16      /* message classes */
 #define INET_WIFI_MAX_NACC 128    /* support of the Poisson access count */
 #define INET_WIFI_MAX_KF 16       /* plane waves per shadowing field */
-#define INET_WIFI_MAX_A 8         /* access points per env (on one channel: one collision domain) */
+#define INET_WIFI_MAX_A 8
+#define INET_WIFI_MAX_Z 6         /* AIFS zones (AIFSN 2 .. 7) */         /* access points per env (on one channel: one collision domain) */
 
 #define INET_WIFI_OK 0
 #define INET_WIFI_EINVAL (-1)
@@ -120,6 +121,11 @@ typedef struct InetWifiParams {
        R + A <= 64 and (R + A) n_dom < 400 (else INET_WIFI_EUNSUPPORTED). */
     int32_t n_dom;
     int32_t ap_dom[INET_WIFI_MAX_A];
+    /* AIFS zones (wifi/meanfield.py:106-209, wifi/engine.py:344-348): 1 + the largest AIFSN difference among the
+       access categories in use (robots' and background stations'), 1 .. INET_WIFI_MAX_Z. Z > 1: each station's
+       offset from the smallest AIFSN among the contending stations of its domain, per-zone sums and the stationary
+       zone distribution; needs R + A <= 64 (else INET_WIFI_EUNSUPPORTED); level WIFI_DCF needs Z = 1. */
+    int32_t Z;
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */

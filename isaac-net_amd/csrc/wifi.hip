@@ -267,8 +267,8 @@ DEV void submit_calls(const InetWifiState& st, int E, const uint8_t* __restrict_
 // MA: several APs (pm.A > 1); the one-AP build fixes A = 1, which keeps the station count R + 1 a compile-time
 // offset of R (measured: the general count costs a fifth of the one-AP step through register allocation).
 // CNT: the launch enqueues pm.step_counts first (a build of its own, so that the step without it keeps its register
-// allocation).
-template <bool DCF, bool MA = false, bool CNT = false>
+// allocation). ZN: AIFS zones (pm.Z > 1; with MA, every station in a lane of its own).
+template <bool DCF, bool MA = false, bool CNT = false, bool ZN = false>
 __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetWifiParams pm,
                                                          const int64_t* __restrict__ tin, int input_kind,
                                                          const float* __restrict__ xin,
@@ -459,6 +459,19 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         o3 = sum_row(s_red4 + 2 * WAVE, b3);
     };
 
+    // the smallest value over the stations of this lane's domain (SingleView.min / DomainView.min, meanfield.py:71-73,
+    // 86-89: 1e9 stands for excluded stations; exact in any order)
+    auto dom_min = [&](float v) -> float {
+        __syncthreads();
+        s_red[lane] = v;
+        __syncthreads();
+        const float* row = s_red + gseg * rb;
+        float m = 1e9f;
+        for (int i = 0; i < NS; ++i)
+            if (!doms || s_dom[gseg * rb + i] == mydom) m = fminn(m, row[i]);
+        return m;
+    };
+
     float acc_sum = 0.f, acc_n = 0.f, p_sum = 0.f, busy_sum = 0.f;
     const float tf = (float)t;
     for (int k = 0; k < K; ++k) {
@@ -475,9 +488,19 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         const float B = act ? fminn(q, capB) : capB;
         const float w = act ? 1.0f : 0.0f;
         float ts, tc;
-        access_times(pm, B, rate, aifsn, ts, tc);
+        // AIFS zones (wifi/engine.py:344-348): each station's offset from the smallest AIFSN among the contending
+        // stations of its domain, whose AIFS the channel times then use
+        float aif_t = aifsn, d_s = 0.0f, tsbz = tsb, tcbz = tcb;
+        if constexpr (ZN) {
+            const float aif_s = is_bg ? pm.ac_aifsn[pm.bg_ac] : aifsn;
+            const bool on = is_bg ? act_b : act;
+            aif_t = fminn(dom_min(on ? aif_s : 1e9f), aif_s);
+            d_s = aif_s - aif_t;
+            if (is_bg) access_times(pm, pm.bg_B, pm.bg_rate, aif_t, tsbz, tcbz);
+        }
+        access_times(pm, B, rate, aif_t, ts, tc);
         // this lane's station in the solve: the robot's, or in lane R the background station's
-        const float ws = is_bg ? wb : w, tss = is_bg ? tsb : ts, tcs = is_bg ? tcb : tc;
+        const float ws = is_bg ? wb : w, tss = is_bg ? tsbz : ts, tcs = is_bg ? tcbz : tc;
         const float W0s = is_bg ? W0b : W0, Wms = is_bg ? Wmb : Wm;
         const bool acts = is_bg ? act_b : act;
         const TauW tw = tau_weights(W0s, Wms);
@@ -497,16 +520,50 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                 pb = 1.0f - expf(S - ownb) * pm.fer1;
             }
         };
+        // zones (meanfield._zones / _fail, meanfield.py:106-131, 161-178): per zone z the domain sum of w log(1 - tau)
+        // over the stations with offset <= z, the stationary zone distribution, and the success and failure
+        // probabilities weighted by the zones the station counts down in
+        constexpr int ZX = ZN ? INET_WIFI_MAX_Z : 1;
+        float Sz[ZX], piz[ZX], num = 0.0f;
+        auto failz = [&]() {
+            const float lt = log1pf(-tau), wl = ws * lt;
+#pragma unroll
+            for (int z = 0; z < ZX; ++z)
+                if (z < pm.Z) Sz[z] = dom_sum(d_s <= (float)z ? wl : 0.0f, 0.0f);
+            float g = 1.0f, raw[ZX], tot = 0.0f;
+#pragma unroll
+            for (int z = 0; z < ZX; ++z)
+                if (z < pm.Z) {
+                    const float idle = expf(Sz[z]);
+                    raw[z] = z < pm.Z - 1 ? g : g / clamp_min(1.0f - idle, 1e-12f);
+                    g = g * idle;
+                }
+#pragma unroll
+            for (int z = 0; z < ZX; ++z) if (z < pm.Z) tot = tot + raw[z];
+            float O = 0.0f;
+            num = 0.0f;
+#pragma unroll
+            for (int z = 0; z < ZX; ++z)
+                if (z < pm.Z) {
+                    piz[z] = raw[z] / tot;
+                    const bool in = d_s <= (float)z;
+                    const float okz = expf(Sz[z] - ((acts && in) ? lt : 0.0f)) * pm.fer1;
+                    const float wz = in ? piz[z] : 0.0f;
+                    num = num + wz * okz;
+                    O = O + wz;
+                }
+            p = 1.0f - num / clamp_min(O, 1e-12f);
+        };
         for (int it = 0; it < pm.fp_iters; ++it) {
             tau = clampf(tau, 1e-7f, 0.999f);
             if (!bgl) tau_b = clampf(tau_b, 1e-7f, 0.999f);
-            fail();
+            if constexpr (ZN) failz(); else fail();
             tau = tau + pm.damp * (tau_of_p(p, W0s, Wms, L, tw) - tau);
             if (!bgl) tau_b = tau_b + pm.damp * (tau_of_p(pb, W0b, Wmb, L, twb) - tau_b);
         }
         tau = clampf(tau, 1e-7f, 0.999f);
         if (!bgl) tau_b = clampf(tau_b, 1e-7f, 0.999f);
-        fail();
+        if constexpr (ZN) failz(); else fail();
         const float r_o = (ws * tau) / (1.0f - tau), r_b = bgl ? 0.0f : (wb * tau_b) / (1.0f - tau_b);
         const float wt_o = ws * tau, wt_b = wb * tau_b;
         // ---- retry-limit loss inputs (wifi/engine.py:375-381; they need only this sub-step's p, so they are
@@ -517,14 +574,33 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         att_logp = back ? att_logp + lp : 0.0f;
         const float p_bar = att_n > 0.f ? exp_r(att_logp / clamp_min(att_n, 1e-12f)) : p;
         const float pbl = pow_int_torch(p_bar, L);
-        const float idle = exp_r(S);
-        float a0, a1, gd, gg;
-        dom_sum4(r_o, r_b, r_o * tss, r_b * tsb, wt_o, wt_b, wt_o * tcs, wt_b * tcb, a0, a1, gd, gg);
-        const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
-        const float tcav = gg / clamp_min(gd, 1e-12f);
-        const float tslot = 0.0f + ((pm.slot_us * idle + idle * a1) + p_coll * tcav);
-        const float p_idle = 0.0f + idle;
-        const float mu = act ? (tau * ok) / tslot : 0.0f;
+        float tslot = 0.0f, p_idle = 0.0f, succ = ok;
+        if constexpr (ZN) {
+            // slot_time (meanfield.py:134-158): the four sums and the idle share of every zone, weighted by pi
+            succ = num;
+#pragma unroll
+            for (int z = 0; z < ZX; ++z)
+                if (z < pm.Z) {
+                    const bool in = d_s <= (float)z;
+                    const float rz = in ? r_o : 0.0f, wtz = in ? wt_o : 0.0f;
+                    const float idle = exp_r(Sz[z]);
+                    float a0, a1, gd, gg;
+                    dom_sum4(rz, 0.0f, rz * tss, 0.0f, wtz, 0.0f, wtz * tcs, 0.0f, a0, a1, gd, gg);
+                    const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
+                    const float tcav = gg / clamp_min(gd, 1e-12f);
+                    tslot = tslot + piz[z] * ((pm.slot_us * idle + idle * a1) + p_coll * tcav);
+                    p_idle = p_idle + piz[z] * idle;
+                }
+        } else {
+            const float idle = exp_r(S);
+            float a0, a1, gd, gg;
+            dom_sum4(r_o, r_b, r_o * tss, r_b * tsb, wt_o, wt_b, wt_o * tcs, wt_b * tcb, a0, a1, gd, gg);
+            const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
+            const float tcav = gg / clamp_min(gd, 1e-12f);
+            tslot = 0.0f + ((pm.slot_us * idle + idle * a1) + p_coll * tcav);
+            p_idle = 0.0f + idle;
+        }
+        const float mu = act ? (tau * succ) / tslot : 0.0f;
 
         // ---- access count (wifi/engine.py:355-360)
         const float lam = mu * pm.dt_us;
@@ -943,6 +1019,9 @@ int check_params(const InetWifiParams& p) {
     if (p.n_dom < 1 || p.n_dom > p.A) return INET_WIFI_EINVAL;
     for (int a = 0; a < p.A; ++a) if (p.ap_dom[a] < 0 || p.ap_dom[a] >= p.n_dom) return INET_WIFI_EINVAL;
     if (p.n_dom > 1 && (p.R + p.A > 64 || (p.R + p.A) * p.n_dom >= 400)) return INET_WIFI_EUNSUPPORTED;
+    // AIFS zones: 1 .. INET_WIFI_MAX_Z, every station in a lane of its own
+    if (p.Z < 1 || p.Z > INET_WIFI_MAX_Z) return INET_WIFI_EINVAL;
+    if (p.Z > 1 && p.R + p.A > 64) return INET_WIFI_EUNSUPPORTED;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
@@ -980,7 +1059,9 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
     if ((rc = check_step_counts(p))) return rc;
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    auto k = p.A > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true> : wifi_step_kernel<false, true, false>)
+    auto k = p.Z > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true, true>
+                                      : wifi_step_kernel<false, true, false, true>)
+           : p.A > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true> : wifi_step_kernel<false, true, false>)
                      : (p.step_counts ? wifi_step_kernel<false, false, true> : wifi_step_kernel<false, false, false>);
     hipLaunchKernelGGL(k, dim3(grid), dim3(WAVE), lds, (hipStream_t)stream, *st, pm, t, input_kind, x, cur_hid, *out,
                        rb, InetDcfState{}, InetDcfParams{});
@@ -1007,6 +1088,7 @@ int32_t inet_wifi_submit(const InetWifiState* st, const InetWifiParams* prm, con
 
 namespace {
 int check_dcf(const InetWifiParams& p, const InetDcfParams& d) {
+    if (p.Z != 1) return INET_WIFI_EUNSUPPORTED;
     // every exchange lasts at least one symbol or one control frame, so the event loop ends within the step
     if (d.T <= 0 || d.T > (1 << 30) || d.slot <= 0 || d.sifs < 0 || d.tsym <= 0 || d.pre < 0 || d.t_ack < 0 ||
         d.t_rts <= 0 || d.t_cts <= 0 || d.W0 < 1 || d.Wmax < d.W0 || d.Wmax > 65536 || d.aifsn < 0 ||

@@ -6,9 +6,9 @@ reset(env_ids) / submit(t, requests, snr_db) / step(t, poses_or_snr, cur_hid, *,
 state_dict, with the same inputs, output keys, dtypes and shapes and the same per-env clock rules (t=None uses the
 engine clock; an int or an [E] tensor sets each env's step). What the kernels do not implement is refused at
 construction with HipUnsupported: more than 8 APs, APs on several channels when R + A > 64 or (R + A) x channels
->= 400, hidden nodes, AIFS zones (access categories of different AIFSN in one env), rng="global", and the radio
-features the NR engine refuses. Several APs run with association and roaming, on one channel or several (one
-collision domain per channel).
+>= 400, AIFS zones (access categories of different AIFSN in one env) when R + A > 64, hidden nodes, rng="global",
+and the radio features the NR engine refuses. Several APs run with association and roaming, on one channel or
+several (one collision domain per channel), with or without AIFS zones.
 
 All state lives in device tensors that torch allocates; every call hands the library plain pointers.
 """
@@ -42,7 +42,7 @@ def wifi_refusals(cfg: NRConfig):
     no(n_ap > 8, f"{n_ap} access points", "up to 8 APs per env")
     no(wc.hidden_nodes, "hidden_nodes=True", "every robot senses every other one")
     d = derive(cfg, wc)
-    no(d.Z > 1, "access categories with different AIFSN in one env (AIFS zones)", "one AIFS zone")
+    no(d.Z > 6, f"{d.Z} AIFS zones", "AIFSN differences up to 5 (six zones)")
     no(cfg.rng != "engine", "rng='global'", "counter-based engine RNG")
     no(cfg.traffic is not None, "traffic models (NRConfig.traffic)", "messages through submit()")
     no(cfg.frame_buffer > 64, "frame_buffer > 64", "FIFO columns of up to 64 slots in LDS")
@@ -102,6 +102,9 @@ class HipWifiEngine:
         if self.D > 1 and (R + self.A > 64 or (R + self.A) * self.D >= 400):
             raise HipUnsupported(f"APs on {self.D} channels with R + A = {R + self.A}: several collision domains "
                                  "need R + A <= 64 and (R + A) x channels < 400")
+        if self.d.Z > 1 and R + self.A > 64:
+            raise HipUnsupported(f"AIFS zones with R + A = {R + self.A}: every station needs a lane of its own "
+                                 "(R + A <= 64)")
         rb = 1 << max(0, (R - 1).bit_length())
         self.envs_per_wave = int(envs_per_wave) if envs_per_wave is not None else 1
         if self.envs_per_wave < 1 or self.envs_per_wave * rb > 64:
@@ -178,6 +181,7 @@ class HipWifiEngine:
         p.n_dom = self.D
         for a, dom in enumerate(self._ap_dom):
             p.ap_dom[a] = dom
+        p.Z = dd.Z
         dc = (rc.shadow_dcorr_m, 0.0, 0.0)
         p.spectrum = 0 if rc.shadow_acf == "sos" else 1
         if rc.channel == "tr38901":

@@ -22,7 +22,7 @@ import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig
 
 pytestmark = pytest.mark.gpu
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls", "w_dcf"]
 
 # relative tolerance, absolute floor
 FLOAT_TOL = {"tau": (2e-5, 1e-9), "att_logp": (2e-5, 1e-6), "credit": (2e-5, 1e-5), "_last_snr": (1e-5, 6.1e-5),
@@ -223,7 +223,8 @@ def test_wifi_graph_replay_matches_eager(level, name):
     assert not bad, bad[:8]
 
 
-@pytest.mark.parametrize("level,name", [("WIFI", "w_mean"), ("WIFI", "w_multi"), ("WIFI", "w_chan"), ("WIFI_DCF", "w_dcf")])
+@pytest.mark.parametrize("level,name", [("WIFI", "w_mean"), ("WIFI", "w_multi"), ("WIFI", "w_chan"),
+                                        ("WIFI", "w_aifs_cls"), ("WIFI_DCF", "w_dcf")])
 def test_wifi_step_with_counts_equals_submit_then_step(level, name):
     """step(x, counts=) (the enqueue in the step's own launch) against submit_counts + step: outputs, accepted
     messages and the whole state bit for bit, including the submit counters and the last hazard ids. Envs start with
