@@ -129,6 +129,12 @@ class WifiConfig:
             return list(self.ap_channels)
         return [a % self.n_channels for a in range(n_ap)]
 
+    def sta_pl_1m(self):
+        """Robot-robot path loss at 1 m (dB): sta_pl_1m_db, else free space at the carrier (wifi/config.py:182-185)."""
+        if self.sta_pl_1m_db is not None:
+            return float(self.sta_pl_1m_db)
+        return 20 * math.log10(4 * math.pi * self.carrier_ghz * 1e9 / 299_792_458.0)
+
     def substeps(self, control_step_ms):
         n = control_step_ms / self.substep_ms
         if abs(n - round(n)) > 1e-9 or round(n) < 1:

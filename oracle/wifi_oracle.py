@@ -5,7 +5,7 @@ checker (or as the timed CPU baseline). The product (isaac-net_amd/) never impor
 
 A from-scratch torch-CPU restatement of isaac-net's WifiNet for the configs the HIP backend implements (one AP, or
 several APs with association and roaming, on one channel or several: one collision domain per channel; AIFS zones;
-no hidden nodes):
+hidden nodes):
   LevelNet         core/levels/base.py:43-360 (clock, reset, submit, step, the regions' order)
   add_body         core/proto/netsim_fast.py:136-160 (enqueue into FIFO slot count)
   finish_body      core/proto/netsim_fast.py:185-206 (delivered / timed out, newest, det_env, stable compaction)
@@ -14,7 +14,9 @@ no hidden nodes):
                    renewal access counts, FIFO service, finish times, retry-limit loss, the extra outputs)
   poisson_icdf     core/wifi/engine.py:57-63
   meanfield.solve  core/wifi/meanfield.py:48-62 (stage factors, tau(p)), :65-73 (one domain), :76-89 (a domain per
-                   channel: the channel one-hot's two batched products), :106-209 (AIFS zones, no hidden nodes)
+                   channel: the channel one-hot's two batched products), :92-103 (the sensing matrix's product),
+                   :106-209 (AIFS zones, the hidden-node term)
+  _sensing         core/wifi/engine.py:260-282 (sensing and hidden matrices from the robot-robot path loss)
   AccessTiming     core/wifi/phy.py:107-155 (cap_bytes, times)
   CounterRNG       core/proto/rng.py (STEP draws uniform(STEP, 0, K, R) and uniform(STEP, 1, R, F))
   RadioMC          through oracle.nr_oracle.Radio on the APs' NRConfig (core/wifi/engine.py:82-97, 189-197)
@@ -25,7 +27,7 @@ after every step). The constants come from isaac_net_amd.wifi_config (pinned by 
 Parity status: every function here is pinned by the golden Wi-Fi trajectories, including both access-noise modes,
 RTS/CTS, both collision times, no aggregation, a TXOP limit, FER, per-class access categories, background stations,
 both radio models, the stochastic LOS state, several APs on one channel with roaming and its interruption, APs on two
-channels, AIFS zones, and partial resets. Not implemented (refused, as by the HIP backend): hidden nodes.
+channels, AIFS zones, hidden nodes, and partial resets.
 """
 from __future__ import annotations
 
@@ -48,7 +50,6 @@ class WifiOracle:
         from isaac_net_amd.wifi_config import WifiConfig, derive, radio_config
         wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
         A = len(wc.ap_xy(cfg))
-        assert not wc.hidden_nodes, "no hidden nodes"
         d = derive(cfg, wc)
         self.cfg, self.wc, self.d, self.E, self.R = cfg, wc, d, E, R
         self.K, self.F, self.timeout = d.K, cfg.frame_buffer, cfg.timeout_steps
@@ -89,6 +90,10 @@ class WifiOracle:
         self.chan_oh = torch.zeros(E, R + A, self.D)
         self.chan_oh[:, R:] = (self.ap_ch[:, None] == torch.arange(self.D)).to(f)
         self.chan_oh[:, :R, 0] = 1.0
+        self.hidden = bool(wc.hidden_nodes)
+        if self.hidden:             # sensing (V) and hidden (H) matrices over robots + background stations
+            self.V = torch.ones(E, R + A, R + A)
+            self.H = torch.zeros(E, R + A, R + A)
         self.reset(None)
 
     # ------------------------------------------------------------------ reset / clock (levels/base.py:142-157)
@@ -154,12 +159,14 @@ class WifiOracle:
         return new
 
     # ------------------------------------------------------------------ association (wifi/engine.py:227-259)
-    def _snr_from(self, x):
+    def _snr_from(self, x, sense=None):
         E, R = self.E, self.R
+        pos = None
         if x.dim() == 3:
             if self.radio is None:
                 self.radio = Radio(self.radio_cfg, E, self.rng)
-            rx = self.radio.rx_dbm(x[..., :2].to(torch.float32))
+            pos = x[..., :2].to(torch.float32)
+            rx = self.radio.rx_dbm(pos)
         else:
             rx = (x.to(torch.float32) + self.d.noise_dbm)[..., None]
         best = rx.argmax(-1)
@@ -175,7 +182,34 @@ class WifiOracle:
         self.serv_out = new.clone()
         ch = self.ap_ch[new]
         self.chan_oh[:, :R] = (ch[..., None] == torch.arange(self.D)).float()
+        if self.hidden:
+            self._sensing(rx, ch, new, pos, sense)
         return rx.gather(-1, new[..., None])[..., 0] - self.d.noise_dbm
+
+    def _sensing(self, rx, ch, serv, pos, sense):
+        """WifiNet._sensing (wifi/engine.py:260-282): V (senses: same channel, and for two robots the robot-robot
+        path loss above the CCA threshold, self included) and H (same channel, not sensed, heard at i's AP)."""
+        E, R, A, wc = self.E, self.R, self.A, self.wc
+        chN = torch.cat([ch, self.ap_ch.expand(E, A)], -1)
+        same = chN[:, :, None] == chN[:, None, :]
+        eye = torch.eye(R, dtype=torch.bool)
+        if sense is not None:
+            sensed = sense.to(torch.bool)
+        elif pos is not None:
+            dist = (pos[:, :, None, :] - pos[:, None, :, :]).norm(dim=-1).clamp(min=1.0)
+            prx = wc.sta_tx_dbm - wc.sta_pl_1m() - 10 * wc.sta_pl_exp * torch.log10(dist)
+            sensed = prx >= wc.cca_dbm
+        else:
+            sensed = torch.ones(E, R, R, dtype=torch.bool)
+        sensed = sensed | eye
+        at_ap = rx.transpose(1, 2).gather(1, serv[:, :, None].expand(E, R, R))
+        s_rr = same[:, :R, :R]
+        V = same.clone()
+        V[:, :R, :R] = s_rr & sensed
+        H = torch.zeros_like(same)
+        H[:, :R, :R] = s_rr & ~sensed & (at_ap >= wc.cca_dbm)
+        self.V = V.float()
+        self.H = H.float()
 
     # ------------------------------------------------------------------ PHY timing (wifi/phy.py:130-155)
     def _cap_bytes(self, rate, txop):
@@ -195,15 +229,19 @@ class WifiOracle:
             hs = d.t_rts + wc.sifs_us + d.t_cts + wc.sifs_us
             ts = aifs + hs + tdata + wc.sifs_us + d.t_ack
             tc = aifs + d.t_rts + wc.sifs_us + d.t_cts
+            tv = tdata * 0.0 + d.t_rts                 # the vulnerable period of a hidden-node collision
         else:
             ts = aifs + tdata + wc.sifs_us + d.t_ack
             tc = ts if wc.collision_time == "ack" else aifs + tdata
-        return ts, tc
+            tv = tdata
+        return ts, tc, tv
 
     # ------------------------------------------------------------------ mean field, one domain, Z = 1
     def _dom_sum(self, x):
         """Sum over the stations of each station's collision domain: the env (one channel, SingleView.sum,
         meanfield.py:68-69), or its channel's stations (DomainView.sum, :83-84)."""
+        if self.hidden:                                         # MatrixView.sum (meanfield.py:98-99)
+            return (self.V @ x[..., None])[..., 0]
         if self.D == 1:
             return x.sum(-1, keepdim=True).expand_as(x)
         M = self.chan_oh
@@ -219,6 +257,8 @@ class WifiOracle:
         """The smallest x over the masked stations of each station's domain (SingleView.min / DomainView.min,
         meanfield.py:71-73, 86-89; BIG = 1e9 where a domain has none)."""
         v = torch.where(mask, x, torch.full_like(x, 1e9))
+        if self.hidden:                                         # MatrixView.min (meanfield.py:101-103)
+            return (v[..., None, :] + (1.0 - self.V) * 1e9).amin(-1)
         if self.D == 1:
             return v.amin(-1, keepdim=True).expand_as(x)
         M = self.chan_oh
@@ -247,32 +287,46 @@ class WifiOracle:
         tot = sum(raw)
         return S, own, [r / tot for r in raw]
 
-    def _fail(self, w, tau, dz, active):
-        """meanfield._fail (meanfield.py:161-178) without hidden nodes: (p, successes, zones)."""
+    def _fail(self, w, tau, dz, active, Ts, Tc, Tv):
+        """meanfield._fail (meanfield.py:161-178): (p, successes, zones)."""
         Z = self.d.Z
         zones = self._zones(w, tau, dz, active)
         S, own, pi = zones
+        hid = 1.0
+        if self.hidden:
+            Tslot, _ = self._slot_time(w, tau, dz, Ts, Tc, zones)
+            opn = pi[0] if Z == 1 else sum(torch.where(dz <= z, pi[z], torch.zeros_like(pi[z])) for z in range(Z))
+            rate = w * tau * opn / Tslot
+            H = self.H
+            hid = torch.exp(-(Tv * (H @ rate[..., None])[..., 0] + (H @ (rate * Tv)[..., None])[..., 0]))
         num = torch.zeros_like(tau)
         O = torch.zeros_like(tau)
         for z in range(Z):
-            ok = torch.exp(S[z] - own[z]) * 1.0 * (1.0 - self.wc.frame_error_rate)
+            ok = torch.exp(S[z] - own[z]) * hid * (1.0 - self.wc.frame_error_rate)
             wz = pi[z] if Z == 1 else torch.where(dz <= z, pi[z], torch.zeros_like(pi[z]))
             num = num + wz * ok
             O = O + wz
         return 1.0 - num / O.clamp(min=1e-12), num, zones
 
-    def _solve(self, w, Ts, Tc, tau, Wfac, dz=None):
-        wc, Z = self.wc, self.d.Z
+    def _solve(self, w, Ts, Tc, tau, Wfac, dz=None, Tv=None):
+        wc = self.wc
         active = w > 0
         k = torch.arange(Wfac.shape[-1], dtype=torch.float32)
         for _ in range(int(wc.fp_iters)):
             tau = tau.clamp(1e-7, 0.999)
-            p, _, _ = self._fail(w, tau, dz, active)
+            p, _, _ = self._fail(w, tau, dz, active, Ts, Tc, Tv)
             pk = p[..., None] ** k
             tau = tau + wc.fp_damping * (pk.sum(-1) / (pk * Wfac).sum(-1) - tau)
         tau = tau.clamp(1e-7, 0.999)
-        p, succ, (S, _, pi) = self._fail(w, tau, dz, active)
-        # slot_time (meanfield.py:134-158)
+        p, succ, zones = self._fail(w, tau, dz, active, Ts, Tc, Tv)
+        tslot, p_idle = self._slot_time(w, tau, dz, Ts, Tc, zones)
+        mu = torch.where(active, tau * succ / tslot, torch.zeros_like(tau))
+        return tau, p, mu, p_idle
+
+    def _slot_time(self, w, tau, dz, Ts, Tc, zones):
+        """slot_time (meanfield.py:134-158): (Tslot, P_idle) averaged over the AIFS zones."""
+        wc, Z = self.wc, self.d.Z
+        S, _, pi = zones
         r = w * tau / (1.0 - tau)
         wt = w * tau
         tslot = torch.zeros_like(tau)
@@ -290,8 +344,7 @@ class WifiOracle:
             tc = g / gd.clamp(min=1e-12)
             tslot = tslot + pi[z] * (wc.slot_us * idle + idle * a1 + p_coll * tc)
             p_idle = p_idle + pi[z] * idle
-        mu = torch.where(active, tau * succ / tslot, torch.zeros_like(tau))
-        return tau, p, mu, p_idle
+        return tslot, p_idle
 
     def _poisson(self, lam, u):
         """poisson_icdf (wifi/engine.py:57-63) with the lgamma(k + 1) table of the derived constants."""
@@ -351,8 +404,8 @@ class WifiOracle:
                 dz = aifsn - aif_min
             else:
                 aif_min, dz = aifsn, None
-            Ts, Tc = self._times(BN, rateN, aif_min)
-            tau, p, mu, p_idle = self._solve(w, Ts, Tc, tau, Wfac, dz)
+            Ts, Tc, Tv = self._times(BN, rateN, aif_min)
+            tau, p, mu, p_idle = self._solve(w, Ts, Tc, tau, Wfac, dz, Tv)
             mu, p = mu[:, :R], p[:, :R]
             lam = mu * d.dt_us
             if wc.access_noise == "poisson":
@@ -422,10 +475,11 @@ class WifiOracle:
             setattr(self, n, torch.empty_like(vals[n]).scatter_(-1, dest, vals[n]))
         return newest, det_env, delivered, timed, delay, cap_out, cls_out
 
-    def step(self, t, x):
-        """Advance [t, t+1): x = SNR [E,R] dB (one AP) or poses [E,R,2|3]. The reference's step dict."""
+    def step(self, t, x, sense=None):
+        """Advance [t, t+1): x = SNR [E,R] dB (one AP) or poses [E,R,2|3]; sense [E,R,R] bool (hidden nodes: robot i
+        senses robot j, in place of the robot-robot path loss). The reference's step dict."""
         t = self._tvec(t)
-        snr = self._snr_from(x)
+        snr = self._snr_from(x, sense)
         self.last_snr = snr.clone()
         cur_hid = self.last_hid.clone()
         self.rng.ctr[STEP] += 1

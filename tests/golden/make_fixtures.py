@@ -577,6 +577,16 @@ WIFI_CASES = {
                        wifi=dict(class_ac=("VO", "BK"), bg_stations=2, bg_ac="BE",
                                  ap_positions_m=((30.0, 30.0), (150.0, 60.0)), ap_channels=(1, 6), roam_hyst_db=2.0),
                        E=2, R=14, steps=25, kind="pose", arena=180.0, walk=7.0, rates=(0.9, 0.5), resets={13: [1]}),
+    # hidden nodes: robots in a 110 m disc around one AP, out of each other's carrier sense beyond ~120 m
+    "w_hidden": dict(cfg=dict(control_step_ms=10.0, frame_buffer=8, msg_sizes=(1500.0,), timeout_steps=4,
+                              cell_positions_m=((0.0, 0.0),)),
+                     wifi=dict(hidden_nodes=True),
+                     E=3, R=12, steps=25, kind="disc", radius=110.0, walk=3.0, rates=(1.5,), resets={12: [2]}),
+    # hidden nodes with RTS/CTS on two APs on two channels, background stations
+    "w_hidden_rts": dict(cfg=dict(control_step_ms=10.0, frame_buffer=8, msg_sizes=(800.0, 2400.0), timeout_steps=5),
+                         wifi=dict(hidden_nodes=True, rts_cts=True, ap_positions_m=((0.0, 0.0), (90.0, 0.0)),
+                                   ap_channels=(1, 6), bg_stations=1, roam_hyst_db=2.0),
+                         E=2, R=12, steps=25, kind="pose", arena=160.0, walk=6.0, rates=(0.8, 0.5), resets={}),
     # the DCF workload: legacy DCF parameters (CWmin 15, CWmax 1023), 16 stations uniform in a 50 m disc around the
     # AP, 1500 B messages, 20 sub-steps per control step
     "w_dcf": dict(cfg=dict(control_step_ms=20.0, frame_buffer=16, msg_sizes=(1500.0,),

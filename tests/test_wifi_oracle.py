@@ -14,7 +14,8 @@ from oracle.wifi_oracle import WifiOracle
 import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig, derive, mcs_table
 
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls",
+              "w_hidden", "w_hidden_rts", "w_dcf"]
 
 
 def load(name):
@@ -100,6 +101,28 @@ def test_wifi_oracle_zones_are_pinned(plant_name):
                 return S, own, [r / tot for r in raw]
             o._zones = zones
     assert run_oracle("w_aifs_cls", plant=plant, steps=12)
+
+
+@pytest.mark.parametrize("plant_name", ["no_hidden_term", "cca_off_by_1db", "tv_of_data_with_rts"])
+def test_wifi_oracle_hidden_nodes_are_pinned(plant_name):
+    """Hidden nodes: dropping the hidden-collision term, a CCA threshold 1 dB off, or the data time as the
+    vulnerable period under RTS/CTS must each fail its trajectory."""
+    def plant(o):
+        if plant_name == "no_hidden_term":
+            def sensing(*a, o=o):
+                WifiOracle._sensing(o, *a)
+                o.H = torch.zeros_like(o.H)
+            o._sensing = sensing
+        elif plant_name == "cca_off_by_1db":
+            import dataclasses
+            o.wc = dataclasses.replace(o.wc, cca_dbm=o.wc.cca_dbm - 1.0)
+        else:
+            def times(B, rate, aifsn, o=o):
+                ts, tc, tv = WifiOracle._times(o, B, rate, aifsn)
+                nsym = torch.ceil((22.0 + 8.0 * (B * o.d.ovh1)) / (rate * o.d.tsym))
+                return ts, tc, o.d.pre + o.d.tsym * nsym
+            o._times = times
+    assert run_oracle("w_hidden_rts" if plant_name == "tv_of_data_with_rts" else "w_hidden", plant=plant, steps=10)
 
 
 def test_wifi_constants_match_reference_tables():
