@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define INET_WIFI_ABI_VERSION 6
+#define INET_WIFI_ABI_VERSION 7
 #define INET_WIFI_MAX_R 64        /* robots per env (one wavefront segment) */
 #define INET_WIFI_MAX_F 64        /* frame buffer */
 #define INET_WIFI_MAX_M 16        /* MCS table entries */
@@ -126,6 +126,15 @@ typedef struct InetWifiParams {
        offset from the smallest AIFSN among the contending stations of its domain, per-zone sums and the stationary
        zone distribution; needs R + A <= 64 (else INET_WIFI_EUNSUPPORTED); level WIFI_DCF needs Z = 1. */
     int32_t Z;
+    /* Hidden nodes (wifi/engine.py:260-282, wifi/meanfield.py:92-103, 161-178): each station senses the stations of
+       its domain, and a robot the robots whose power at it reaches cca_dbm (sta_c0 - sta_c1 log10(max(d, 1 m)):
+       sta_c0 = sta_tx_dbm - PL(1 m), sta_c1 = 10 n as float32; or sense[E][R][R] uint8, robot i senses robot j,
+       device, per call; or every robot with an SNR or received-power input). An unsensed robot of the domain whose
+       power at the robot's AP reaches cca_dbm is hidden; the failure probability gains the hidden-collision term.
+       Needs (R + A)^2 < 400 (else INET_WIFI_EUNSUPPORTED); level WIFI_DCF refuses it. */
+    int32_t hidden;
+    float cca_dbm, sta_c0, sta_c1;
+    const uint8_t *sense;
 } InetWifiParams;
 
 /* Step outputs, the reference's keys, layouts and dtypes (bool as uint8). */

@@ -105,7 +105,8 @@ class InetWifiParams(C.Structure):
         "amp", "pl_const", "pl_exp10", "ue_tx")] + \
                [("los_sto", i32), ("plos_scn", i32), ("sig_nlos", f32), ("A", i32), ("los_cdf", P),
                 ("ap_xy", f32 * (2 * WIFI_MAX_A)), ("step_counts", P), ("step_accepted", P),
-                ("step_n_cls", i32), ("n_dom", i32), ("ap_dom", i32 * WIFI_MAX_A), ("Z", i32)]
+                ("step_n_cls", i32), ("n_dom", i32), ("ap_dom", i32 * WIFI_MAX_A), ("Z", i32),
+                ("hidden", i32), ("cca_dbm", f32), ("sta_c0", f32), ("sta_c1", f32), ("sense", P)]
 
 
 class InetWifiOutputs(C.Structure):
@@ -129,7 +130,7 @@ ERRORS = {-1: "invalid argument (size or pointer)", -2: "unsupported configurati
           -3: "HIP launch failed"}
 
 ABI_VERSION = 15
-WIFI_ABI_VERSION = 6
+WIFI_ABI_VERSION = 7
 _LIB = None
 
 

@@ -68,6 +68,12 @@ DEV void access_times(const InetWifiParams& pm, float B, float rate, float aifsn
         tc = pm.coll_ack ? ts : aifs + tdata;
     }
 }
+// the vulnerable period Tv of a hidden-node collision (wifi/phy.py:150, 154): the RTS, or the data PPDU
+DEV float vuln_time(const InetWifiParams& pm, float B, float rate) {
+    if (pm.rts_cts) return pm.t_rts;
+    const float nsym = ceilf(((B * pm.ovh1) * 8.0f + 22.0f) / (rate * pm.tsym));
+    return pm.tsym * nsym + pm.pre;
+}
 // tau(p) of meanfield.tau_from_p: sum_k p^k / sum_k p^k (W_k + 1) / 2 over the L stages, W_k = min(2^k W0, Wmax),
 // both sums in torch's CPU order. p^k is the double-precision running product rounded once (the correctly rounded
 // power unless p^k lies within ~k 2^-53 relative of a float rounding boundary). Under 8 stages the CPU order adds
@@ -190,6 +196,14 @@ DEV float dom_seq_sum(const float* row, const uint8_t* dom, int n, int d) {
     return acc;
 }
 
+// the sum over the stations of a mask (MatrixView.sum, meanfield.py:98-99: V @ x with V of 0 / 1, added in index
+// order by ATen's CPU product kernel at (R + A)^2 < 400)
+DEV float mask_seq_sum(const float* row, uint64_t mask, int n) {
+    float acc = 0.f;
+    for (int i = 0; i < n; ++i) acc = ((mask >> i) & 1ull) ? acc + row[i] : acc;
+    return acc;
+}
+
 // bytewise maximum of two words of four uint8
 DEV uint32_t max_u8x4(uint32_t a, uint32_t b) {
     uint32_t m = 0;
@@ -280,6 +294,8 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     __shared__ uint8_t s_hid0[CNT ? WAVE : 1];            // per env: the enqueue's calls clear the last hazard id
     __shared__ int s_cmax[CNT ? INET_WIFI_MAX_CLS : 1];   // the largest count of every class (workgroup 0)
     __shared__ uint8_t s_dom[MA ? WAVE : 1];              // APs on several channels: each station's domain
+    __shared__ float s_rxa[ZN ? WAVE * INET_WIFI_MAX_A : 1];   // hidden nodes: every robot's power at every AP
+    __shared__ float s_pos[ZN ? 2 * WAVE : 1];                  // hidden nodes: every robot's position
     const int R = pm.R, F = pm.F, K = pm.K, L = pm.L, G = pm.envs_per_wave;
     float* s_rem = dyn;                                   // [F][64] bytes left of every frame slot
     float* s_fin = dyn + F * WAVE;                        // [F][64] finish time, then the compaction staging row
@@ -333,6 +349,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         float bv = 0.f, cur = 0.f;
         int best = 0;
         const float px = input_kind == 0 ? xin[ir * 2] : 0.f, py = input_kind == 0 ? xin[ir * 2 + 1] : 0.f;
+        if constexpr (ZN) { s_pos[2 * lane] = px; s_pos[2 * lane + 1] = py; }
         const StoLos sto{pm.los_cdf, pm.plos_scn, pm.sig_nlos, pm.los_sto != 0};
         for (int c = 0; c < A; ++c) {
             float v;
@@ -345,6 +362,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                 v = xin[ir * A + c];
             if (c == 0 || v > bv) { bv = v; best = c; }
             if (c == s0) cur = v;
+            if constexpr (ZN) s_rxa[lane * INET_WIFI_MAX_A + c] = v;
         }
         const bool better = bv > cur + pm.roam_hyst;
         roamed = better && !pend && best != s0;
@@ -398,12 +416,37 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
     const bool is_bg = bgl && env_ok && r >= R && r < NS;
     // APs on several channels (MA builds): one collision domain per channel. A robot is in its serving AP's channel,
     // an AP's background station in the AP's (each has its own lane: R + A <= 64, checked by the entry points).
-    const bool doms = MA && pm.n_dom > 1;
+    const bool hid = ZN && pm.hidden != 0;
+    const bool doms = MA && (pm.n_dom > 1 || hid);
     if (doms) {
         if (env_ok && r < NS) s_dom[lane] = (uint8_t)(r < R ? pm.ap_dom[sv] : pm.ap_dom[r - R]);
         __syncthreads();
     }
     const int mydom = doms && env_ok && r < NS ? s_dom[lane] : 0;
+    // hidden nodes (WifiNet._sensing, wifi/engine.py:260-282): this station's row of V (the stations it senses: its
+    // domain's, and among robots those whose power at it, robot-robot path loss, reaches the CCA threshold, or
+    // pm.sense) and of H (robots of its domain it does not sense whose power at its AP reaches the threshold)
+    uint64_t vmask = 0ull, hmask = 0ull;
+    if (hid && env_ok && r < NS) {
+        const int sb = gseg * rb;
+        for (int j = 0; j < NS; ++j) {
+            const bool same = s_dom[sb + j] == mydom;
+            bool sensed = true;
+            if (r < R && j < R && j != r) {
+                if (pm.sense) {
+                    sensed = pm.sense[((size_t)ec * R + r) * R + j] != 0;
+                } else if (input_kind == 0) {
+                    const float dx = s_pos[2 * lane] - s_pos[2 * (sb + j)];
+                    const float dy = s_pos[2 * lane + 1] - s_pos[2 * (sb + j) + 1];
+                    const float dist = fmaxf(sqrtf(fmaf(dy, dy, dx * dx)), 1.0f);        // (torch's norm of two)
+                    const float prx = pm.sta_c0 - pm.sta_c1 * (float)log10((double)dist);
+                    sensed = prx >= pm.cca_dbm;
+                }
+                if (same && !sensed && s_rxa[(sb + j) * INET_WIFI_MAX_A + sv] >= pm.cca_dbm) hmask |= 1ull << j;
+            }
+            if (same && (r >= R || j >= R || sensed)) vmask |= 1ull << j;
+        }
+    }
     float tau = rob ? st.tau[(size_t)ec * NS + rc] : (is_bg ? st.tau[(size_t)ec * NS + r] : pm.tau0);
     float tau_b = (!bgl && env_ok) ? st.tau[(size_t)ec * NS + R] : pm.tau0;
     int roam = rob ? st.roam_left[ir] : 0;
@@ -428,6 +471,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         s_red[lane] = v;
         __syncthreads();
         const float* row = s_red + gseg * rb;
+        if (hid) return mask_seq_sum(row, vmask, NS);
         if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
         auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
         if (NS == 17) return aten_row_sum_u<17>(17, xr);
@@ -445,6 +489,7 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         __syncthreads();
         auto sum_row = [&](const float* base, float vb) -> float {
             const float* row = base + gseg * rb;
+            if (hid) return mask_seq_sum(row, vmask, NS);
             if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
             auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
             if (NS == 17) return aten_row_sum_u<17>(17, xr);
@@ -468,8 +513,17 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         const float* row = s_red + gseg * rb;
         float m = 1e9f;
         for (int i = 0; i < NS; ++i)
-            if (!doms || s_dom[gseg * rb + i] == mydom) m = fminn(m, row[i]);
+            if (hid ? ((vmask >> i) & 1ull) != 0ull : (!doms || s_dom[gseg * rb + i] == mydom)) m = fminn(m, row[i]);
         return m;
+    };
+    // two sums over this station's hidden set (H @ x, meanfield.py:170; rows s_red and s_red4)
+    auto hid_sum2 = [&](float v0, float v1, float& o0, float& o1) {
+        __syncthreads();
+        s_red[lane] = v0;
+        s_red4[lane] = v1;
+        __syncthreads();
+        o0 = mask_seq_sum(s_red + gseg * rb, hmask, NS);
+        o1 = mask_seq_sum(s_red4 + gseg * rb, hmask, NS);
     };
 
     float acc_sum = 0.f, acc_n = 0.f, p_sum = 0.f, busy_sum = 0.f;
@@ -491,12 +545,14 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         // AIFS zones (wifi/engine.py:344-348): each station's offset from the smallest AIFSN among the contending
         // stations of its domain, whose AIFS the channel times then use
         float aif_t = aifsn, d_s = 0.0f, tsbz = tsb, tcbz = tcb;
+        float tv_s = 0.0f;
         if constexpr (ZN) {
             const float aif_s = is_bg ? pm.ac_aifsn[pm.bg_ac] : aifsn;
             const bool on = is_bg ? act_b : act;
             aif_t = fminn(dom_min(on ? aif_s : 1e9f), aif_s);
             d_s = aif_s - aif_t;
             if (is_bg) access_times(pm, pm.bg_B, pm.bg_rate, aif_t, tsbz, tcbz);
+            if (hid) tv_s = is_bg ? vuln_time(pm, pm.bg_B, pm.bg_rate) : vuln_time(pm, B, rate);
         }
         access_times(pm, B, rate, aif_t, ts, tc);
         // this lane's station in the solve: the robot's, or in lane R the background station's
@@ -540,14 +596,37 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                 }
 #pragma unroll
             for (int z = 0; z < ZX; ++z) if (z < pm.Z) tot = tot + raw[z];
+#pragma unroll
+            for (int z = 0; z < ZX; ++z) if (z < pm.Z) piz[z] = raw[z] / tot;
+            // hidden nodes: exp(-(Tv_i sum_H rate + sum_H rate Tv)), rate = w tau open / Tslot (meanfield.py:167-170)
+            float hf = 1.0f;
+            if (hid) {
+                const float r_h = (ws * tau) / (1.0f - tau), wt_h = ws * tau;
+                float tsl = 0.0f, opn = 0.0f;
+#pragma unroll
+                for (int z = 0; z < ZX; ++z)
+                    if (z < pm.Z) {
+                        const bool in = d_s <= (float)z;
+                        const float rz = in ? r_h : 0.0f, wtz = in ? wt_h : 0.0f;
+                        const float idle = expf(Sz[z]);
+                        float a0, a1, gd, gg;
+                        dom_sum4(rz, 0.0f, rz * tss, 0.0f, wtz, 0.0f, wtz * tcs, 0.0f, a0, a1, gd, gg);
+                        const float p_coll = clamp_min((1.0f - idle) - idle * a0, 0.0f);
+                        tsl = tsl + piz[z] * ((pm.slot_us * idle + idle * a1) + p_coll * (gg / clamp_min(gd, 1e-12f)));
+                        opn = opn + (in ? piz[z] : 0.0f);
+                    }
+                const float rate_h = ((ws * tau) * opn) / tsl;
+                float h0, h1;
+                hid_sum2(rate_h, rate_h * tv_s, h0, h1);
+                hf = expf(-(tv_s * h0 + h1));
+            }
             float O = 0.0f;
             num = 0.0f;
 #pragma unroll
             for (int z = 0; z < ZX; ++z)
                 if (z < pm.Z) {
-                    piz[z] = raw[z] / tot;
                     const bool in = d_s <= (float)z;
-                    const float okz = expf(Sz[z] - ((acts && in) ? lt : 0.0f)) * pm.fer1;
+                    const float okz = (expf(Sz[z] - ((acts && in) ? lt : 0.0f)) * hf) * pm.fer1;
                     const float wz = in ? piz[z] : 0.0f;
                     num = num + wz * okz;
                     O = O + wz;
@@ -1022,6 +1101,8 @@ int check_params(const InetWifiParams& p) {
     // AIFS zones: 1 .. INET_WIFI_MAX_Z, every station in a lane of its own
     if (p.Z < 1 || p.Z > INET_WIFI_MAX_Z) return INET_WIFI_EINVAL;
     if (p.Z > 1 && p.R + p.A > 64) return INET_WIFI_EUNSUPPORTED;
+    // hidden nodes: (R + A)^2 < 400 (the size up to which the reference's products add in index order)
+    if (p.hidden && (p.R + p.A) * (p.R + p.A) >= 400) return INET_WIFI_EUNSUPPORTED;
     if (p.los_sto && (!p.los_cdf || p.radio_model != 1 || p.n_fields != 3 || p.plos_scn < 0 || p.plos_scn > 2))
         return INET_WIFI_EINVAL;
     for (int c = 0; c <= p.n_cls; ++c) if (p.cls_ac[c] < 0 || p.cls_ac[c] > 4) return INET_WIFI_EINVAL;
@@ -1059,7 +1140,7 @@ int32_t inet_wifi_step(const InetWifiState* st, const InetWifiParams* prm, const
     const unsigned grid = (unsigned)((p.E + G - 1) / G);
     if ((rc = check_step_counts(p))) return rc;
     const size_t lds = (size_t)p.F * WAVE * (4 + 4 + 1 + 1);
-    auto k = p.Z > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true, true>
+    auto k = (p.Z > 1 || p.hidden) ? (p.step_counts ? wifi_step_kernel<false, true, true, true>
                                       : wifi_step_kernel<false, true, false, true>)
            : p.A > 1 ? (p.step_counts ? wifi_step_kernel<false, true, true> : wifi_step_kernel<false, true, false>)
                      : (p.step_counts ? wifi_step_kernel<false, false, true> : wifi_step_kernel<false, false, false>);
@@ -1088,7 +1169,7 @@ int32_t inet_wifi_submit(const InetWifiState* st, const InetWifiParams* prm, con
 
 namespace {
 int check_dcf(const InetWifiParams& p, const InetDcfParams& d) {
-    if (p.Z != 1) return INET_WIFI_EUNSUPPORTED;
+    if (p.Z != 1 || p.hidden) return INET_WIFI_EUNSUPPORTED;
     // every exchange lasts at least one symbol or one control frame, so the event loop ends within the step
     if (d.T <= 0 || d.T > (1 << 30) || d.slot <= 0 || d.sifs < 0 || d.tsym <= 0 || d.pre < 0 || d.t_ack < 0 ||
         d.t_rts <= 0 || d.t_cts <= 0 || d.W0 < 1 || d.Wmax < d.W0 || d.Wmax > 65536 || d.aifsn < 0 ||

@@ -6,9 +6,10 @@ reset(env_ids) / submit(t, requests, snr_db) / step(t, poses_or_snr, cur_hid, *,
 state_dict, with the same inputs, output keys, dtypes and shapes and the same per-env clock rules (t=None uses the
 engine clock; an int or an [E] tensor sets each env's step). What the kernels do not implement is refused at
 construction with HipUnsupported: more than 8 APs, APs on several channels when R + A > 64 or (R + A) x channels
->= 400, AIFS zones (access categories of different AIFSN in one env) when R + A > 64, hidden nodes, rng="global",
-and the radio features the NR engine refuses. Several APs run with association and roaming, on one channel or
-several (one collision domain per channel), with or without AIFS zones.
+>= 400, AIFS zones (access categories of different AIFSN in one env) when R + A > 64, hidden nodes when
+(R + A)^2 >= 400, rng="global", and the radio features the NR engine refuses. Several APs run with association and
+roaming, on one channel or several (one collision domain per channel), with or without AIFS zones and hidden
+nodes.
 
 All state lives in device tensors that torch allocates; every call hands the library plain pointers.
 """
@@ -40,7 +41,6 @@ def wifi_refusals(cfg: NRConfig):
             out.append((what, why))
     n_ap = len(wc.ap_xy(cfg))
     no(n_ap > 8, f"{n_ap} access points", "up to 8 APs per env")
-    no(wc.hidden_nodes, "hidden_nodes=True", "every robot senses every other one")
     d = derive(cfg, wc)
     no(d.Z > 6, f"{d.Z} AIFS zones", "AIFSN differences up to 5 (six zones)")
     no(cfg.rng != "engine", "rng='global'", "counter-based engine RNG")
@@ -105,6 +105,9 @@ class HipWifiEngine:
         if self.d.Z > 1 and R + self.A > 64:
             raise HipUnsupported(f"AIFS zones with R + A = {R + self.A}: every station needs a lane of its own "
                                  "(R + A <= 64)")
+        if self.wc.hidden_nodes and (R + self.A) ** 2 >= 400:
+            raise HipUnsupported(f"hidden nodes with R + A = {R + self.A}: (R + A)^2 < 400, the size up to which the "
+                                 "reference's sensing-matrix products add in index order")
         rb = 1 << max(0, (R - 1).bit_length())
         self.envs_per_wave = int(envs_per_wave) if envs_per_wave is not None else 1
         if self.envs_per_wave < 1 or self.envs_per_wave * rb > 64:
@@ -182,6 +185,11 @@ class HipWifiEngine:
         for a, dom in enumerate(self._ap_dom):
             p.ap_dom[a] = dom
         p.Z = dd.Z
+        # hidden nodes: the robot-robot power sta_c0 - sta_c1 log10(d) against the CCA threshold (wifi/engine.py:268-271)
+        p.hidden = int(bool(wc.hidden_nodes))
+        p.cca_dbm = wc.cca_dbm
+        p.sta_c0 = float(np.float32(wc.sta_tx_dbm - wc.sta_pl_1m()))
+        p.sta_c1 = float(np.float32(10 * wc.sta_pl_exp))
         dc = (rc.shadow_dcorr_m, 0.0, 0.0)
         p.spectrum = 0 if rc.shadow_acf == "sos" else 1
         if rc.channel == "tr38901":
@@ -352,15 +360,25 @@ class HipWifiEngine:
 
     def step(self, t=None, x=None, cur_hid=None, *, rx_dbm=None, sense=None, counts=None):
         """Advance [t, t+1). x: poses [E,R,2|3] (through the APs' radio) or the SNR [E,R] in dB; rx_dbm= [E,R,A]
-        gives the received power (dBm) instead (wifi/engine.py:207-225). counts= [E,R,NC] enqueues first, as
+        gives the received power (dBm) instead (wifi/engine.py:207-225); sense= [E,R,R] bool (hidden nodes): robot i
+        senses robot j, in place of the robot-robot path loss. counts= [E,R,NC] enqueues first, as
         submit_counts(counts, t) would, in the step's own launch; the dict then also holds "accepted" [E,R] int32.
         Returns the reference's dict, or (newest, det_env) in the legacy form with cur_hid."""
-        if sense is not None:
+        if sense is not None and not self.wc.hidden_nodes:
             raise ValueError("sense= needs WifiConfig(hidden_nodes=True)")
         kind, xin = self._input(x, rx_dbm)
         tv = self._tvec(t)
         hid = None if cur_hid is None else torch.as_tensor(cur_hid).to(self.dev, torch.long).contiguous()
-        o = self._run(tv, kind, xin, hid, None if counts is None else self._counts(counts))
+        sn = None
+        if sense is not None:
+            sn = sense.to(self.dev, torch.uint8).contiguous()
+            if tuple(sn.shape) != (self.E, self.R, self.R):
+                raise ValueError(f"sense must be [E,R,R] = {(self.E, self.R, self.R)}")
+        self._cparams.sense = None if sn is None else sn.data_ptr()
+        try:
+            o = self._run(tv, kind, xin, hid, None if counts is None else self._counts(counts))
+        finally:
+            self._cparams.sense = None
         if cur_hid is not None:
             return o["newest"], o["det_env"]
         return o
@@ -539,9 +557,9 @@ class HipWifiDcfEngine(HipWifiEngine):
     def __init__(self, E, R, device="cuda", cfg: NRConfig | None = None, seed=None, envs_per_wave=None):
         cfg = cfg if cfg is not None else NRConfig()
         wc = cfg.wifi if cfg.wifi is not None else WifiConfig()
-        if wc.bg_stations > 0 or wc.class_ac is not None or len(wc.ap_xy(cfg)) != 1:
-            raise HipUnsupported("level WIFI_DCF: one AP, one access category for every robot and no background "
-                                 "stations")
+        if wc.bg_stations > 0 or wc.class_ac is not None or len(wc.ap_xy(cfg)) != 1 or wc.hidden_nodes:
+            raise HipUnsupported("level WIFI_DCF: one AP, one access category for every robot, no background "
+                                 "stations and no hidden nodes")
         self._dcf_ready = False
         super().__init__(E, R, device, cfg, seed=seed, envs_per_wave=envs_per_wave)
         self._build_dcf()

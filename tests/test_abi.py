@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol():
     for n in wifi:
         assert hasattr(lib, n), n
     lib.inet_wifi_abi_version.restype = ctypes.c_int32
-    assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 6
+    assert lib.inet_wifi_abi_version() == _lib.WIFI_ABI_VERSION == 7
 
 
 STRUCTS = ("InetNrState", "InetNrTables", "InetNrParams", "InetNrOutputs", "InetNrRow", "InetNrDlState",

@@ -22,7 +22,8 @@ import isaac_net_amd as P
 from isaac_net_amd.wifi_config import WifiConfig
 
 pytestmark = pytest.mark.gpu
-WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls", "w_dcf"]
+WIFI_CASES = ["w_snr", "w_mean", "w_logd", "w_tr", "w_sto", "w_multi", "w_chan", "w_chan3", "w_aifs", "w_aifs_cls",
+              "w_hidden", "w_hidden_rts", "w_dcf"]
 
 # relative tolerance, absolute floor
 FLOAT_TOL = {"tau": (2e-5, 1e-9), "att_logp": (2e-5, 1e-6), "credit": (2e-5, 1e-5), "_last_snr": (1e-5, 6.1e-5),
@@ -271,3 +272,36 @@ def test_wifi_step_with_counts_equals_submit_then_step(level, name):
         if s == 2:
             assert int(sb["_last_hid"].abs().sum()) == 0, "one call anywhere clears every env's hazard id"
     assert not bad, bad[:8]
+
+
+def _wcfg(**kw):
+    nr = {k: kw.pop(k) for k in list(kw) if k in P.NRConfig.__dataclass_fields__}
+    return P.NRConfig(wifi=WifiConfig(**kw), **nr)
+
+
+def test_wifi_hidden_nodes_two_robots():
+    """The reference's own hidden-node check (tests/test_wifi.py:343-360) on the HIP engine, each run also against the
+    oracle: two robots on opposite sides of the AP, out of each other's carrier sense, fail more than three times as
+    often as when they sense each other; RTS/CTS lowers it; sense= all-true gives the sensed result."""
+    pos = torch.tensor([[[-60.0, 0.0], [60.0, 0.0]]])
+    kw = dict(ap_positions_m=((0.0, 0.0),), msg_sizes=(30000.0,), shadow_sigma_db=0.0, access_noise="mean",
+              pl_const_db=30.0, pathloss_exp=2.5)
+    p = {}
+
+    def run(c, sense=None):
+        eng = P.make_engine("WIFI", 1, 2, "cuda:0", c, seed=0)
+        orc = WifiOracle(1, 2, c, seed=0)
+        send = torch.ones(1, 2, dtype=torch.long)
+        eng.submit(None, send.to("cuda:0"))
+        orc.submit(None, send)
+        og = eng.step(None, pos.to("cuda:0"), sense=None if sense is None else sense.to("cuda:0"))
+        oo = orc.step(None, pos, sense=sense)
+        g, o = float(og["wifi_p_fail"][0, 0]), float(oo["wifi_p_fail"][0, 0])
+        assert g == pytest.approx(o, rel=2e-5, abs=1e-7), (g, o)
+        return g
+    for name, extra in (("sensed", dict(hidden_nodes=False)), ("hidden", dict(hidden_nodes=True)),
+                        ("hidden_rts", dict(hidden_nodes=True, rts_cts=True))):
+        p[name] = run(_wcfg(**kw, **extra))
+    assert p["hidden"] > 3 * p["sensed"] and p["hidden_rts"] < p["hidden"], p
+    p_sense = run(_wcfg(**kw, hidden_nodes=True), sense=torch.ones(1, 2, 2, dtype=torch.bool))
+    assert p_sense == pytest.approx(p["sensed"], rel=1e-5), (p_sense, p)
