@@ -348,8 +348,8 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
         if (c.ttt < 0 || c.ho_int < 0 || !(c.noise_mw > 0.0f)) return INET_NR_EINVAL;
         if (c.rlf && !rlf_ok(c, true)) return INET_NR_EINVAL;
         fn = inet::pick_step_mc(p.S, c.C, p.P, ir, fx, rb);
-    } else if (rb > inet::STEP_WAVE) {          // 65..128 / 129..256 robots: two / four wavefronts per env, UL
-        if (dl || vref) return INET_NR_EUNSUPPORTED;
+    } else if (rb > inet::STEP_WAVE) {          // 65..128 / 129..256 robots: two / four wavefronts per env (the DL: two)
+        if (vref || (dl && rb > 2 * inet::STEP_WAVE)) return INET_NR_EUNSUPPORTED;
         fn = rb == 2 * inet::STEP_WAVE ? inet::pick_step_two_waves(p.S, p.P, ir, fx) : inet::pick_step_w4(p.S, p.P, ir);
     } else {
         fn = inet::pick_step_one_cell(p.S, p.P, ir, vref, rb, fx);

@@ -2353,11 +2353,18 @@ inline int fx_profile(const InetNrParams& p) {
     return common ? (p.rician == 1 ? 1 : (p.rician == 0 ? 2 : 0)) : 0;
 }
 
-// envs of 65..128 (RBT = 128) or 129..256 robots (RBT = 256): one env per workgroup of two or four wavefronts (UL,
-// pose or SNR input)
+// envs of 65..128 (RBT = 128) or 129..256 robots (RBT = 256): one env per workgroup of two or four wavefronts (pose
+// or SNR input; the UL, and with RBT = 128 the DL too)
 template <int S, int P, bool IR, int FX = 0, int RBT = 128>
 void launch_step_w2(const StepArgs& a) {
     const InetNrCells none{};
+    if constexpr (RBT == 128)
+        if (a.dl) {
+            hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, RBT, InetNrDlState, 1, FX>), dim3(a.grid), dim3(RBT),
+                               a.lds, a.stream, a.st, *a.dl, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out,
+                               a.rb, a.n_data, a.arr, none);
+            return;
+        }
     hipLaunchKernelGGL((nr_step_kernel<S, P, IR, false, RBT, InetNrState, 1, FX>), dim3(a.grid), dim3(RBT), a.lds,
                        a.stream, a.st, a.st, a.tb, a.pm, a.rows, a.n_rows, a.T, a.x, a.hid, a.out, a.rb, a.n_data,
                        a.arr, none);

@@ -167,9 +167,11 @@ class HipNREngine:
         if R > 128 and cfg.n_subbands not in (8, 13):
             raise HipUnsupported(f"R={R} with {cfg.n_subbands} subbands: envs of 129..256 robots (four wavefronts) "
                                  "run 8 or 13 RBGs in this build")
-        if R > 64 and (cfg.dl or cfg.n_cells > 1):
-            raise HipUnsupported(f"R={R} with the downlink or several cells: envs of more than 64 robots (two "
-                                 "wavefronts) run the single-cell uplink")
+        if R > 64 and cfg.n_cells > 1:
+            raise HipUnsupported(f"R={R} with several cells: envs of more than 64 robots (two or four wavefronts) run "
+                                 "one cell")
+        if R > 128 and cfg.dl:
+            raise HipUnsupported(f"R={R} with the downlink: envs of up to 128 robots (two wavefronts) run the DL")
         self._lib = _lib.load()
         self.E, self.R, self.dev, self.config = E, R, dev, cfg
         if seed is None:

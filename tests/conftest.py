@@ -61,7 +61,7 @@ CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14
          "fcorr_los", "fcorr_los_rice", "sto64", "sto100", "dop", "wb_pf", "wb_maxci_md"]
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links
 DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl", "fcorr_dl", "rice_los_dl", "los_sto_dl",
-            "rice_sto_dl", "fcorr_los_dl", "dop_vel_dl", "pfwb_dl"]
+            "rice_sto_dl", "fcorr_los_dl", "dop_vel_dl", "pfwb_dl", "dl_w2", "dl_w2_snr"]
 MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc", "mc2_rice",
             "mc3_rice_sto", "mc3_flush", "mc3_a3floor", "mc2_fcorr_los", "mc3_rice64", "mc3_rice48",
             "mc3_ho48", "mc3_rice48c", "mc3_rice32", "mc2_dop", "mc2_wb", "mc3_pg", "mc3_rlf", "mc2_rlf_flush"]

@@ -92,6 +92,19 @@ CASES = {
                             dl_mcs_max=20, dl_snr_offset_db=6.0),
                    E=3, R=8, steps=30, kind="snr", snr=(-4.0, 14.0), rates=(0.8,), dl_sizes=(9000.0, 1500.0),
                    dl_rates=(0.9, 0.8), resets={17: [1]}),
+    # the downlink with envs of 72 and 100 robots (two wavefronts per env): dl_c2's link on poses, dl_snr's on SNR
+    "dl_w2": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=25.0, scheduler="pf", pf_window=100.0,
+                           n_harq=8, max_harq_tx=5, frame_buffer=16, msg_sizes=(200.0, 4000.0), fading_rho_per_ms=0.0,
+                           fading_rician=True, rician_k_db=3.0, channel="tr38901", tr38901_scenario="UMi",
+                           tr38901_los="los", cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0, dl=True),
+                  E=2, R=72, steps=20, kind="pose", arena=200.0, walk=0.025, rates=(0.5, 0.1),
+                  dl_sizes=(6000.0, 30000.0), dl_rates=(0.4, 0.1), resets={11: [1]}),
+    "dl_w2_snr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                               harq_fail="drop", frame_buffer=6, msg_sizes=(3000.0,), timeout_steps=6,
+                               fading_rho_per_ms=0.9, dl=True, cqi_table="38214", cqi_period_slots=5, k1=3,
+                               dl_mcs_max=20, dl_snr_offset_db=6.0),
+                      E=2, R=100, steps=20, kind="snr", snr=(-4.0, 14.0), rates=(0.5,), dl_sizes=(9000.0, 1500.0),
+                      dl_rates=(0.5, 0.4), resets={9: [0]}),
     # downlink with per-subband SNR: IR combining, no retransmission priority, round robin, PDCP discard, gNB
     # processing 2 slots
     "dl_ir_rr": dict(cfg=dict(mu=1, n_prb=52, control_step_ms=10.0, scheduler="rr", n_harq=4, max_harq_tx=3,

@@ -101,6 +101,10 @@ def compare(ref, s, out, sd, E, R):
                 b = b + np.abs(np.asarray(r, dtype=np.float64)) * (np.log(10.0) / 10.0) * \
                     np.asarray(BOUND["out.sinr_db"], dtype=np.float64)[..., None]
             BOUND[k] = b
+        if k == "dl.csi" and "out.sinr_db" in BOUND:
+            # the DL CSI is an MCS threshold minus the reference SINR, whose path gain from the poses carries the
+            # radio's rounding (the sinr_db bound, dB, the same for every subband of the robot)
+            BOUND[k] = np.asarray(BOUND["out.sinr_db"], dtype=np.float64)[..., None]
         if k.endswith(".h_lexp") and "out.sinr_db" in BOUND:
             # the IR log-sum log sum_tx sum_s exp(-lin_s / beta + log w_s) with poses: every lin_s carries the radio's
             # rounding (relative ln(10) / 10 of the sinr_db bound), which moves each exponent by lin_s / beta times
