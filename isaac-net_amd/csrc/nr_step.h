@@ -2402,7 +2402,8 @@ StepFn pick_step_s8(int P, bool ir, bool vref, int rb, int fx);    // nr_step_s8
 #define INET_STEP_S_EXTRA(X) X(10) X(11) X(12) X(14) X(16) X(17) X(18)
 #define INET_DECL_S(SS)                                                    \
     StepFn pick_step_s##SS(int P, bool ir, bool vref, int rb, int fx);   \
-    StepFn pick_step_w2_s##SS(int P, bool ir, int fx);
+    StepFn pick_step_w2_s##SS(int P, bool ir, int fx);                   \
+    StepFn pick_step_w4_s##SS(int P, bool ir);
 INET_STEP_S_EXTRA(INET_DECL_S)
 #undef INET_DECL_S
 
@@ -2433,7 +2434,7 @@ StepFn pick_step_w2_s(int P, bool ir, int fx) {
     return nullptr;
 }
 StepFn pick_step_w2(int S, int P, bool ir, int fx);        // nr_step_w2.hip
-// four-wavefront builds (R = 129..256), 8 and 13 subbands: every (P, IR)
+// four-wavefront builds (R = 129..256): every (P, IR)
 template <int S>
 StepFn pick_step_w4_s(int P, bool ir) {
 #define INET_PICK_W4(PP) \

@@ -164,9 +164,6 @@ class HipNREngine:
         if not 1 <= R <= 256:
             raise HipUnsupported(f"R={R}: the hip backend holds one env's robots in one 64-lane wavefront segment, "
                                  "or in two or four wavefronts (1 <= R <= 256)")
-        if R > 128 and cfg.n_subbands not in (8, 13):
-            raise HipUnsupported(f"R={R} with {cfg.n_subbands} subbands: envs of 129..256 robots (four wavefronts) "
-                                 "run 8 or 13 RBGs in this build")
         if R > 64 and cfg.n_cells > 1:
             raise HipUnsupported(f"R={R} with several cells: envs of more than 64 robots (two or four wavefronts) run "
                                  "one cell")

@@ -56,7 +56,7 @@ def pytest_collection_modifyitems(config, items):
 # _rice): per-link delay spreads from the LOS state (13, 14 and 18 RBGs); sto64 / sto100: the stochastic LOS state,
 # Rician K from it and per-link delay spreads on 64-robot envs (one wavefront) and 100-robot envs (two wavefronts)
 CASES = ["c1", "c2", "c2heavy", "snr_drop", "snr3_ir", "logd_meandb", "c5", "s14", "s18_ir", "s10_w2", "lena_pf",
-         "wb_pc", "pc1", "w4", "tdma", "amc_prev", "lena_v2", "wb_amc", "fcorr", "fcorr_w2",
+         "wb_pc", "pc1", "w4", "s14_w4", "s18_w4", "tdma", "amc_prev", "lena_v2", "wb_amc", "fcorr", "fcorr_w2",
          "rice_los", "rice_snr", "los_sto", "rice_sto", "rice_sto_slow",
          "fcorr_los", "fcorr_los_rice", "sto64", "sto100", "dop", "wb_pf", "wb_maxci_md"]
 # the downlink on (NRConfig(dl=True)); s17_dl: 17 RBGs; lena_dl: the frozen PF average on both links

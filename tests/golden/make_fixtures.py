@@ -155,6 +155,15 @@ CASES = {
                             channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
                             cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
                    E=2, R=96, steps=10, kind="pose", arena=200.0, walk=1.0, rates=(0.4,), resets={6: [1]}),
+    # 106 PRB (14 RBGs of 8) and 273 PRB (18 RBGs of 16) on envs of 160 and 144 robots (four wavefronts)
+    "s14_w4": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                            max_harq_tx=4, frame_buffer=8, msg_sizes=(600.0,), fading_rho_per_ms=0.5,
+                            channel="tr38901", tr38901_scenario="UMi", tr38901_los="los",
+                            cell_positions_m=((100.0, 100.0),), gnb_height_m=10.0),
+                   E=2, R=160, steps=8, kind="pose", arena=200.0, walk=1.0, rates=(0.3,), resets={5: [1]}),
+    "s18_w4": dict(cfg=dict(mu=1, n_prb=273, control_step_ms=10.0, scheduler="maxci", n_harq=4, max_harq_tx=3,
+                            harq_combining="ir_lena", frame_buffer=8, msg_sizes=(4000.0,), fading_rho_per_ms=0.3),
+                   E=2, R=144, steps=8, kind="snr", snr=(-4.0, 14.0), rates=(0.4,), resets={4: [0]}),
     # two cells per env: 14 RBGs, PF, thermal noise with UL interference, power control, correlated fading
     "mc2": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
                          max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=2, cell_layout="hex",
