@@ -289,8 +289,8 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
                                                          const int64_t* __restrict__ hid_in, InetWifiOutputs out,
                                                          int rb, InetDcfState ds, InetDcfParams dp) {
     extern __shared__ float dyn[];
-    __shared__ float s_red[WAVE];
-    __shared__ float s_red4[DCF ? 1 : 3 * WAVE];          // three more rows of station values (dom_sum4)
+    __shared__ __align__(16) float s_red[WAVE];
+    __shared__ __align__(16) float s_red4[DCF ? 1 : 3 * WAVE];          // three more rows of station values (dom_sum4)
     __shared__ uint8_t s_hid0[CNT ? WAVE : 1];            // per env: the enqueue's calls clear the last hazard id
     __shared__ int s_cmax[CNT ? INET_WIFI_MAX_CLS : 1];   // the largest count of every class (workgroup 0)
     __shared__ uint8_t s_dom[MA ? WAVE : 1];              // APs on several channels: each station's domain
@@ -473,6 +473,17 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
         const float* row = s_red + gseg * rb;
         if (hid) return mask_seq_sum(row, vmask, NS);
         if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
+        if (NS == 17 && bgl) {          // (a 32-lane segment: the row is 128-byte aligned, read 16 bytes at a time)
+            float v[17];
+            const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 q = r4[k];
+                v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
+            }
+            v[16] = row[16];
+            return aten_row_sum_u<17>(17, [&](int i) { return v[i]; });
+        }
         auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
         if (NS == 17) return aten_row_sum_u<17>(17, xr);
         if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
@@ -491,6 +502,17 @@ __global__ __launch_bounds__(WAVE) void wifi_step_kernel(InetWifiState st, InetW
             const float* row = base + gseg * rb;
             if (hid) return mask_seq_sum(row, vmask, NS);
             if (doms) return dom_seq_sum(row, s_dom + gseg * rb, NS, mydom);
+            if (NS == 17 && bgl) {          // (a 32-lane segment: the row is 128-byte aligned, read 16 bytes at a time)
+                float v[17];
+                const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 q = r4[k];
+                    v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
+                }
+                v[16] = row[16];
+                return aten_row_sum_u<17>(17, [&](int i) { return v[i]; });
+            }
             auto xr = [&](int i) { return (i < R || bgl) ? row[i] : vb; };
             if (NS == 17) return aten_row_sum_u<17>(17, xr);
             if (NS <= 8) return aten_row_sum_u<8>(NS, xr);
