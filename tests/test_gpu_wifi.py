@@ -305,3 +305,28 @@ def test_wifi_hidden_nodes_two_robots():
     assert p["hidden"] > 3 * p["sensed"] and p["hidden_rts"] < p["hidden"], p
     p_sense = run(_wcfg(**kw, hidden_nodes=True), sense=torch.ones(1, 2, 2, dtype=torch.bool))
     assert p_sense == pytest.approx(p["sensed"], rel=1e-5), (p_sense, p)
+
+
+def test_wifi_static_outputs_match_fresh_ones():
+    """static_outputs: every step writes the same tensors (the reference graph backend's output semantics) with the
+    values fresh outputs get, with and without the enqueue in the step."""
+    ref, cfg, kind = load("w_mean")
+    E, R, T = int(ref["E"]), int(ref["R"]), int(ref["steps"])
+    a = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    b = P.make_engine("WIFI", E, R, "cuda:0", cfg, seed=0)
+    b.static_outputs = True
+    to = lambda v: torch.from_numpy(np.asarray(v)).to("cuda:0")  # noqa: E731
+    first = None
+    for s in range(T):
+        cnt = to(ref["counts"][s].astype(np.uint8))
+        x = to(ref["x"][s])
+        if s % 2:
+            a.submit_counts(cnt)
+            b.submit_counts(cnt)
+            oa, ob = a.step(None, x), b.step(None, x)
+        else:
+            oa, ob = a.step(None, x, counts=cnt), b.step(None, x, counts=cnt)
+        first = ob["newest"] if first is None else first
+        assert ob["newest"] is first
+        for k, v in oa.items():
+            assert torch.equal(torch.nan_to_num(v.float(), nan=-7.0), torch.nan_to_num(ob[k].float(), nan=-7.0)), (s, k)
