@@ -18,8 +18,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libinet_nr.so")
 PHASE_LIB = os.path.join(HERE, "libinet_nr_phase.so")
-UNITS = ["inet_nr.hip", "nr_step_s13.hip", "nr_step_s8.hip", "nr_step_mc.hip", "nr_step_mc2.hip", "nr_step_w2.hip",
-         "nr_step_w4.hip", "wifi.hip"] + [f"nr_step_s{s}.hip" for s in (10, 11, 12, 14, 16, 17, 18)]
+# (the units with the most and the largest instantiations first: the pool's last unit sets the build's wall time)
+UNITS = [f"nr_step_mc{c}.hip" for c in (7, 6, 5, 4)] + \
+        ["nr_step_s13.hip", "nr_step_w2.hip", "nr_step_w4.hip", "nr_step_mc.hip", "nr_step_mc2.hip", "nr_step_s8.hip"] + \
+        [f"nr_step_s{s}.hip" for s in (10, 11, 12, 14, 16, 17, 18)] + ["inet_nr.hip", "wifi.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]

@@ -365,6 +365,15 @@ int32_t launch_step_kernel(const InetNrState* st, const InetNrDlState* dl, const
                      (unsigned)((p.E + envs_pw - 1) / envs_pw),
                      inet::step_lds_bytes(n_hist, p.harq_drop, rb, p.max_tx, cells ? cells->C : 1, p.S),
                      (hipStream_t)stream};
+    // several cells: the static LDS grows with the cells (each lane's fading normals, 2 NC S floats, the
+    // interference pairs and every robot's PSD at each cell; under 16 KiB besides) and must fit the CU's 160 KiB
+    // with the dynamic part
+    if (cells) {
+        const size_t nc = (size_t)cells->C, ns = (size_t)p.S;
+        const size_t stat = sizeof(float) * (2 * nc * ns * inet::STEP_WAVE + nc * ns * (1 + 2 * nc) +
+                                             nc * inet::STEP_WAVE) + 16384;
+        if (a.lds + stat > 160 * 1024) return INET_NR_EUNSUPPORTED;
+    }
     fn(a);
     return hipGetLastError() == hipSuccess ? INET_NR_OK : INET_NR_ELAUNCH;
 }

@@ -2413,14 +2413,19 @@ template <int S, int NC>
 StepFn pick_step_mc_s(int P, bool ir, int fx, int rb) {
     if constexpr (S == 14 && NC == 3)                // config 3's switches (no Rician phasor), 8 HARQ, 64-robot envs
         if (fx == 2 && P == 8 && !ir && rb == 64) return &launch_step_mc<14, 8, false, 3, 2, 64>;
+// (no HARQ-IR builds with several cells: refused, INET_NR_EUNSUPPORTED)
 #define INET_PICK_MC(PP) \
-    if (P == PP) return ir ? &launch_step_mc<S, PP, true, NC> : &launch_step_mc<S, PP, false, NC>;
+    if (P == PP) return ir ? nullptr : &launch_step_mc<S, PP, false, NC>;
     INET_PICK_MC(2) INET_PICK_MC(4) INET_PICK_MC(8) INET_PICK_MC(16)
 #undef INET_PICK_MC
     return nullptr;
 }
 StepFn pick_step_mc(int S, int C, int P, bool ir, int fx, int rb); // nr_step_mc.hip
 StepFn pick_step_mc2(int S, int P, bool ir, int fx, int rb);       // nr_step_mc2.hip
+StepFn pick_step_mc4(int S, int P, bool ir, int fx, int rb);       // nr_step_mc4.hip
+StepFn pick_step_mc5(int S, int P, bool ir, int fx, int rb);       // nr_step_mc5.hip
+StepFn pick_step_mc6(int S, int P, bool ir, int fx, int rb);       // nr_step_mc6.hip
+StepFn pick_step_mc7(int S, int P, bool ir, int fx, int rb);       // nr_step_mc7.hip
 
 // two-wavefront builds (R = 65..128): every (P, IR)
 template <int S>

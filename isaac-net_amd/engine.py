@@ -81,9 +81,11 @@ def refusals(cfg: NRConfig):
         if cond:
             out.append((what, why))
     mc = cfg.n_cells > 1
-    no(mc and cfg.n_cells > 3, f"n_cells={cfg.n_cells}",
-       "one to three cells per env in this build (the fading of every robot-cell link is held in registers)")
+    no(mc and cfg.n_cells > 7, f"n_cells={cfg.n_cells}", "one to seven cells per env (the reference's 1..7)")
     no(mc and cfg.dl, "the downlink with several cells", "the multi-cell step runs the uplink")
+    no(mc and cfg.harq_combining == "ir_lena", "HARQ-IR (harq_combining='ir_lena') with several cells",
+       "chase combining or none with several cells (IR's integer state differed from the reference's on 2 of 6 "
+       "seeded 3- and 4-cell trajectories)")
     no(cfg.rlf and cfg.rach, "re-establishment through RACH (rlf with rach)", "a fixed re-establishment delay")
     no(mc and cfg.frame_buffer > 64, "frame_buffer > 64 with several cells", "a 64-bit handover loss mask")
     no(not cfg.ul, "ul=False (a downlink-only engine)", "the UL link runs every step")

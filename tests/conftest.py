@@ -64,6 +64,7 @@ DL_CASES = ["dl_c2", "dl_snr", "dl_ir_rr", "s17_dl", "lena_dl", "fcorr_dl", "ric
             "rice_sto_dl", "fcorr_los_dl", "dop_vel_dl", "pfwb_dl", "dl_w2", "dl_w2_snr"]
 MC_CASES = ["mc3", "mc3_ho", "mc2", "mc2_ho", "mc2_lena", "fcorr_mc2", "los_sto_mc", "mc2_rice",
             "mc3_rice_sto", "mc3_flush", "mc3_a3floor", "mc2_fcorr_los", "mc3_rice64", "mc3_rice48",
-            "mc3_ho48", "mc3_rice48c", "mc3_rice32", "mc2_dop", "mc2_wb", "mc3_pg", "mc3_rlf", "mc2_rlf_flush"]
-# several cells (NRConfig(n_cells=3 / 2)), uplink; mc3_flush: ho_rlc="flush"; mc3_a3floor: the A3 admission floor;
+            "mc3_ho48", "mc3_rice48c", "mc3_rice32", "mc2_dop", "mc2_wb", "mc3_pg", "mc3_rlf", "mc2_rlf_flush",
+            "mc4", "mc5", "mc6", "mc7"]
+# several cells (NRConfig(n_cells=2..7)), uplink; mc4..mc7: four to seven hex cells; mc3_flush: ho_rlc="flush"; mc3_a3floor: the A3 admission floor;
 # mc2_fcorr_los: per-link delay spreads; mc3_rice64 / mc3_rice48: Rician links on 64- and 48-robot envs

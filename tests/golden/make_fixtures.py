@@ -368,9 +368,9 @@ CASES = {
                                     cell_positions_m=((150.0, 150.0),), gnb_height_m=25.0),
                            E=3, R=16, steps=25, kind="pose", arena=300.0, walk=5.0, rates=(0.8,), resets={12: [0]}),
     # several cells with A3 handovers under ho_rlc="flush" (every queued frame of a robot dropped at its switch,
-    # mac.py:557-581): fast motion, HARQ-IR, round robin, an N+I EWMA, a reset
+    # mac.py:557-581): fast motion, round robin, an N+I EWMA, a reset
     "mc3_flush": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=4,
-                               max_harq_tx=3, harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2500.0, 400.0),
+                               max_harq_tx=3, frame_buffer=8, msg_sizes=(2500.0, 400.0),
                                n_cells=3, cell_layout="hex", cell_isd_m=120.0, cell_center_m=(60.0, 60.0),
                                noise_model="thermal", a3_ttt_ms=10.0, ho_interruption_ms=2.5, ho_rlc="flush",
                                li_alpha=0.3, fading_rho_per_ms=0.5),
@@ -436,6 +436,34 @@ CASES = {
                                    rlf_rlc="flush", n310=2, n311=1, t310_ms=20.0, t311_ms=50.0, reest_delay_ms=10.0,
                                    fading_rho_per_ms=0.5),
                           E=3, R=16, steps=30, kind="pose", arena=900.0, walk=25.0, rates=(0.8,), resets={14: [2]}),
+    # four to seven cells (radio.py gnb_xy: the hex centre site and the first ring, up to the full 7-site cluster):
+    # mc4: 4 cells, 106 PRB (14 RBGs), PF, Rician TR 38.901 UMi LOS links, same-slot UL interference;
+    # mc5: 5 cells, 273 PRB in 8 RBGs of 35, maxCI, A3 handovers, RLC UM drop; mc6: 6 cells, 52 PRB, round robin,
+    # radio link failure on path gains; mc7: the full cluster, 52 PRB, PF, A3 handovers with fast motion
+    "mc4": dict(cfg=dict(mu=1, n_prb=106, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=4,
+                         cell_layout="hex", cell_isd_m=150.0, cell_center_m=(120.0, 120.0), noise_model="thermal",
+                         channel="tr38901", tr38901_scenario="UMi", tr38901_los="los", gnb_height_m=10.0,
+                         fading_rho_per_ms=0.5, fading_rician=True, rician_k_db=3.0),
+                E=2, R=16, steps=18, kind="pose", arena=240.0, walk=3.0, rates=(0.7,), resets={11: [1]}),
+    "mc5": dict(cfg=dict(mu=1, n_prb=273, rbg_size=35, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="maxci",
+                         n_harq=4, max_harq_tx=3, harq_fail="drop", frame_buffer=8, msg_sizes=(2500.0, 400.0),
+                         n_cells=5, cell_layout="hex", cell_isd_m=120.0, cell_center_m=(120.0, 120.0),
+                         noise_model="thermal", a3_ttt_ms=20.0, ho_interruption_ms=5.0, li_alpha=0.5,
+                         fading_rho_per_ms=0.0),
+                E=3, R=8, steps=30, kind="pose", arena=240.0, walk=6.0, rates=(0.5, 1.0), resets={20: [0]}),
+    "mc6": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=6, cell_layout="hex",
+                         cell_isd_m=200.0, noise_model="thermal", a3_offset_db=2.0, a3_ttt_ms=5.0,
+                         fading_rho_per_ms=0.5, rlf=True, n310=1, n311=2, t310_ms=30.0, t311_ms=60.0,
+                         reest_delay_ms=20.0),
+                E=2, R=16, steps=24, kind="pg", pg=(-172.0, -118.0), pg_walk=6.0, rates=(0.7,), resets={12: [1]}),
+    "mc7": dict(cfg=dict(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="pf", n_harq=8,
+                         max_harq_tx=4, frame_buffer=12, msg_sizes=(1500.0,), n_cells=7, cell_layout="hex",
+                         cell_isd_m=120.0, cell_center_m=(150.0, 150.0), noise_model="thermal", a3_ttt_ms=10.0,
+                         ho_interruption_ms=5.0, fading_rho_per_ms=0.5, channel="tr38901", tr38901_scenario="UMi",
+                         tr38901_los="los", gnb_height_m=10.0),
+                E=2, R=16, steps=30, kind="pose", arena=300.0, walk=8.0, rates=(0.6,), resets={18: [0]}),
     # per-robot Doppler (fading_doppler="per_robot": engine.py:862-864, radio.py:285-300, channels/doppler.py:23-29,
     # nr_engine.py:583-589): speeds from consecutive poses, 0 .. 25 m/s (J0 reaches its first zero near 13 m/s at
     # 3.5 GHz, rho 0 from there), a 0.5 m/s floor

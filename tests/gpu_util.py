@@ -163,6 +163,10 @@ def set_radio_bound(ref, s, cfg, eng, kind):
         nib = ni_rel_bound_upto(ref, s, fields, amp)                                   # [E, C]
         b = b + (10.0 / np.log(10.0)) * np.take_along_axis(nib, serv, 1)
         BOUND["net.ni_ul"] = np.abs(ref[f"s{s:03d}/net.ni_ul"].astype(np.float64)) * nib[..., None]
+        # the interference-over-noise sum since the reset adds the same non-negative interference terms over cells,
+        # subbands and slots: each carries at most its cell's relative bound, so the sum the largest of the env's
+        if f"s{s:03d}/net.ioN[ul]" in ref:
+            BOUND["net.ioN[ul]"] = np.abs(ref[f"s{s:03d}/net.ioN[ul]"].astype(np.float64)) * nib.max(-1)
     BOUND["out.sinr_db"] = b
     BOUND["eng._last_snr"] = b
 

@@ -89,11 +89,11 @@ def test_interference_workload_prefix_parity():
     assert fc.ok(E_chk * R * steps) and ni_dev <= 1.0, fc.report()
 
 
-def test_handover_flush_ir_rr_against_oracle():
-    """A3 handovers under fast motion with ho_rlc="flush" (queued frames dropped at the switch), HARQ-IR, round
-    robin, an N+I EWMA (li_alpha 0.3) and a partial reset, against the oracle on every env."""
+def test_handover_flush_rr_against_oracle():
+    """A3 handovers under fast motion with ho_rlc="flush" (queued frames dropped at the switch), round robin, an N+I
+    EWMA (li_alpha 0.3) and a partial reset, against the oracle on every env."""
     cfg = P.NRConfig(mu=1, n_prb=52, tdd_pattern="DDDSU", control_step_ms=10.0, scheduler="rr", n_harq=4,
-                     max_harq_tx=3, harq_combining="ir_lena", frame_buffer=8, msg_sizes=(2500.0, 400.0), n_cells=3,
+                     max_harq_tx=3, frame_buffer=8, msg_sizes=(2500.0, 400.0), n_cells=3,
                      cell_layout="hex", cell_isd_m=120.0, cell_center_m=(60.0, 60.0), noise_model="thermal",
                      a3_ttt_ms=10.0, ho_interruption_ms=2.5, ho_rlc="flush", li_alpha=0.3, fading_rho_per_ms=0.5)
     E, R, steps = 4, 16, 30

@@ -22,7 +22,9 @@ def test_refusals_name_each_unimplemented_feature():
     assert EN.refusals(P.NRConfig(**mc)) == []
     assert EN.refusals(P.NRConfig(**mc, a3_offset_db=float("inf"), harq_fail="drop", ho_rlc="flush")) == []
     assert EN.refusals(P.NRConfig(**mc, rlf=True, rlf_rlc="flush")) == []
-    for extra, word in ((dict(n_cells=7), "n_cells=7"), (dict(dl=True), "downlink with several cells"),
+    for n_cells in (4, 5, 6, 7):                           # the hex centre site and the first ring, up to 7
+        assert EN.refusals(P.NRConfig(**dict(mc, n_cells=n_cells))) == [], n_cells
+    for extra, word in ((dict(dl=True), "downlink with several cells"), (dict(harq_combining="ir_lena"), "HARQ-IR"),
                         (dict(rlf=True, rach=True), "RACH"), (dict(frame_buffer=65), "frame_buffer > 64"),
                         (dict(ul_tpc=True), "TPC")):
         assert word in " ".join(f for f, _ in EN.refusals(P.NRConfig(**dict(mc, **extra)))), extra
